@@ -1,0 +1,366 @@
+"""Python front end of libcbxops (the gfx950 fused layer-op library).
+
+Functions carry the names of the ggml ops they replace on chatterbox-cpp's
+layer-op path and take torch tensors that live on a ROCm device; every call
+goes through the library's C ABI (include/cbxops.h) on torch's current
+stream.  Shapes are torch order (outermost first); the descriptor passed to
+the library reverses them into ggml's ne[] (innermost first), with byte
+strides as nb[].
+
+There is no fallback: if libcbxops.so is missing or a call fails, a
+CbxError is raised.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from typing import Optional
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libcbxops.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "cbxops.h")
+
+# ggml_type numbering
+F32, F16, Q8_0, I32 = 0, 1, 8, 26
+QK8_0, Q8_0_BLOCK = 32, 34
+
+# cbx_unary_op
+UNARY_NONE, GELU, GELU_ERF, SILU, TANH, SOFTPLUS, SIN, SQR, MISH = -1, 0, 1, 2, 3, 4, 5, 6, 7
+
+# cbx_status
+OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_NOT_INITIALIZED, ERR_HIP = 0, -1, -2, -3, -4
+
+
+class CbxError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"cbxops error {status}: {message}")
+        self.status = status
+
+
+class Tensor(ctypes.Structure):
+    """cbx_tensor"""
+
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("type", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("ne", ctypes.c_int64 * 4),
+        ("nb", ctypes.c_size_t * 4),
+    ]
+
+
+_lib = None
+_initialised: set[int] = set()
+
+
+def header_symbols() -> list[str]:
+    """Every function the public header declares."""
+    text = open(HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cbx_[a-z0-9_]+)\s*\(", text)))
+
+
+def load() -> ctypes.CDLL:
+    """Loads libcbxops.so (no GPU needed) and declares its signatures."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise CbxError(ERR_UNSUPPORTED, f"{LIB_PATH} is not built; run python -m chatterbox_amdvulkan_amd.build")
+    L = ctypes.CDLL(LIB_PATH)
+    P = ctypes.POINTER(Tensor)
+    i, f, vp = ctypes.c_int, ctypes.c_float, ctypes.c_void_p
+    sigs = {
+        "cbx_init": (i, [i]),
+        "cbx_shutdown": (None, []),
+        "cbx_last_error": (ctypes.c_char_p, []),
+        "cbx_version": (ctypes.c_char_p, []),
+        "cbx_device_errors": (i, [i, ctypes.POINTER(ctypes.c_uint32), i]),
+        "cbx_get_rows": (i, [P, P, P, vp]),
+        "cbx_get_rows_add": (i, [P, P, P, P, P, vp]),
+        "cbx_cpy": (i, [P, P, vp]),
+        "cbx_norm": (i, [P, f, P, vp]),
+        "cbx_layer_norm": (i, [P, P, P, f, i, P, vp]),
+        "cbx_rms_norm": (i, [P, f, P, vp]),
+        "cbx_rms_norm_mul": (i, [P, P, f, P, vp]),
+        "cbx_group_norm": (i, [P, i, f, P, P, i, P, vp]),
+        "cbx_rope_cache_create": (i, [i, i, i, f, f, f, f, f, f, vp, ctypes.c_int32, ctypes.POINTER(vp)]),
+        "cbx_rope_cache_destroy": (None, [vp]),
+        "cbx_rope_ext": (i, [P, P, vp, P, vp]),
+        "cbx_unary": (i, [i, P, P, vp]),
+        "cbx_gelu": (i, [P, P, vp]),
+        "cbx_gelu_erf": (i, [P, P, vp]),
+        "cbx_silu": (i, [P, P, vp]),
+        "cbx_mish": (i, [P, P, vp]),
+        "cbx_leaky_relu": (i, [P, f, P, vp]),
+        "cbx_swiglu": (i, [P, P, P, vp]),
+        "cbx_snake": (i, [P, P, P, P, vp]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    return (load().cbx_last_error() or b"").decode()
+
+
+def _check(rc: int):
+    if rc != OK:
+        raise CbxError(rc, last_error())
+
+
+def init(device: Optional[int] = None) -> None:
+    """cbx_init for `device` (default: torch's current device); idempotent."""
+    dev = torch.cuda.current_device() if device is None else int(device)
+    if dev in _initialised:
+        return
+    _check(load().cbx_init(dev))
+    _initialised.add(dev)
+
+
+def device_errors(device: Optional[int] = None, clear: bool = True) -> int:
+    dev = torch.cuda.current_device() if device is None else int(device)
+    out = ctypes.c_uint32(0)
+    _check(load().cbx_device_errors(dev, ctypes.byref(out), 1 if clear else 0))
+    return out.value
+
+
+def _ready(t: torch.Tensor):
+    if not t.is_cuda:
+        raise CbxError(ERR_INVALID_ARG, "tensor is not on a ROCm device")
+    init(t.device.index)
+
+
+_DTYPES = {torch.float32: F32, torch.float16: F16, torch.int32: I32}
+
+
+def desc(t: torch.Tensor, ggml_type: Optional[int] = None) -> Tensor:
+    """cbx_tensor for a torch tensor (up to 4 dims, any strides)."""
+    if t.dim() > 4:
+        raise CbxError(ERR_INVALID_ARG, "more than 4 dims")
+    d = Tensor()
+    d.data = t.data_ptr()
+    es = t.element_size()
+    shape = list(t.shape[::-1]) or [1]
+    strides = [s * es for s in t.stride()[::-1]] or [es]
+    row_bytes = strides[-1] * shape[-1]
+    if ggml_type == Q8_0:
+        if t.dtype != torch.uint8 or t.shape[-1] % Q8_0_BLOCK or t.stride(-1) != 1:
+            raise CbxError(ERR_INVALID_ARG, "Q8_0 tables are uint8 [..., n_blocks * 34] with unit inner stride")
+        shape[0] = shape[0] // Q8_0_BLOCK * QK8_0
+        strides[0] = Q8_0_BLOCK
+        d.type = Q8_0
+    else:
+        if t.dtype not in _DTYPES:
+            raise CbxError(ERR_INVALID_ARG, f"unsupported dtype {t.dtype}")
+        d.type = _DTYPES[t.dtype] if ggml_type is None else ggml_type
+    while len(shape) < 4:
+        shape.append(1)
+        strides.append(row_bytes)
+    for k in range(4):
+        d.ne[k] = shape[k]
+        d.nb[k] = strides[k]
+    return d
+
+
+def _ref(d: Optional[Tensor]):
+    return ctypes.byref(d) if d is not None else None
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+# ---- gather / conversion ----------------------------------------------------
+
+def get_rows(table: torch.Tensor, ids: torch.Tensor, out: Optional[torch.Tensor] = None,
+             q8_0: bool = False) -> torch.Tensor:
+    """ggml_get_rows + ggml_cast(F32).  table [.., n_rows, ne0] (f32/f16, or
+    uint8 Q8_0 blocks with q8_0=True); ids int32; out f32 ids.shape + (ne0,)."""
+    _ready(table)
+    ne0 = table.shape[-1] // Q8_0_BLOCK * QK8_0 if q8_0 else table.shape[-1]
+    if out is None:
+        out = torch.empty(tuple(ids.shape) + (ne0,), dtype=torch.float32, device=table.device)
+    _check(load().cbx_get_rows(_ref(desc(table, Q8_0 if q8_0 else None)), _ref(desc(ids)), _ref(desc(out)),
+                               _stream()))
+    return out
+
+
+def get_rows_add(table, ids, table2, ids2, out=None, q8_0=False, q8_0_2=False):
+    """ggml_add(get_rows(table, ids), get_rows(table2, ids2)) in one pass."""
+    _ready(table)
+    ne0 = table.shape[-1] // Q8_0_BLOCK * QK8_0 if q8_0 else table.shape[-1]
+    if out is None:
+        out = torch.empty(tuple(ids.shape) + (ne0,), dtype=torch.float32, device=table.device)
+    _check(load().cbx_get_rows_add(_ref(desc(table, Q8_0 if q8_0 else None)), _ref(desc(ids)),
+                                   _ref(desc(table2, Q8_0 if q8_0_2 else None)), _ref(desc(ids2)),
+                                   _ref(desc(out)), _stream()))
+    return out
+
+
+def cpy(src: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """ggml_cpy / ggml_cast between f32 and f16."""
+    _ready(src)
+    _check(load().cbx_cpy(_ref(desc(src)), _ref(desc(out)), _stream()))
+    return out
+
+
+# ---- norms --------------------------------------------------------------------
+
+def _out_like(x, out):
+    return torch.empty_like(x) if out is None else out
+
+
+def norm(x, eps, out=None):
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_norm(_ref(desc(x)), eps, _ref(desc(out)), _stream()))
+    return out
+
+
+def layer_norm(x, w, b, eps, act=UNARY_NONE, out=None):
+    """layer_norm() helper: add(mul(norm(x), w), b) [-> act] in one pass."""
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_layer_norm(_ref(desc(x)), _ref(desc(w)) if w is not None else None,
+                                 _ref(desc(b)) if b is not None else None, eps, act, _ref(desc(out)), _stream()))
+    return out
+
+
+def rms_norm(x, eps, out=None):
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_rms_norm(_ref(desc(x)), eps, _ref(desc(out)), _stream()))
+    return out
+
+
+def rms_norm_mul(x, g, eps, out=None):
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_rms_norm_mul(_ref(desc(x)), _ref(desc(g)) if g is not None else None, eps,
+                                   _ref(desc(out)), _stream()))
+    return out
+
+
+def group_norm(x, n_groups, eps, w=None, b=None, act=UNARY_NONE, out=None):
+    """ggml_group_norm (channels = ggml ne[2], i.e. torch dim -3) [+ affine] [+ act]."""
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_group_norm(_ref(desc(x)), n_groups, eps, _ref(desc(w)) if w is not None else None,
+                                 _ref(desc(b)) if b is not None else None, act, _ref(desc(out)), _stream()))
+    return out
+
+
+# ---- rope -----------------------------------------------------------------------
+
+class RopeCache:
+    """cbx_rope_cache: cos/sin table for ggml_rope_ext's parameters."""
+
+    def __init__(self, n_dims: int, mode: int = 2, n_ctx_orig: int = 2048, freq_base: float = 10000.0,
+                 freq_scale: float = 1.0, ext_factor: float = 0.0, attn_factor: float = 1.0,
+                 beta_fast: float = 0.0, beta_slow: float = 0.0, freq_factors=None, n_pos: int = 2048,
+                 device: Optional[int] = None):
+        dev = torch.cuda.current_device() if device is None else int(device)
+        init(dev)
+        self.n_dims, self.mode, self.n_pos = n_dims, mode, n_pos
+        ff = None
+        if freq_factors is not None:
+            ff = (ctypes.c_float * len(freq_factors))(*[float(v) for v in freq_factors])
+        h = ctypes.c_void_p()
+        with torch.cuda.device(dev):
+            _check(load().cbx_rope_cache_create(n_dims, mode, n_ctx_orig, freq_base, freq_scale, ext_factor,
+                                                attn_factor, beta_fast, beta_slow,
+                                                ctypes.cast(ff, ctypes.c_void_p) if ff is not None else None,
+                                                n_pos, ctypes.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            load().cbx_rope_cache_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def rope_ext(x, pos, cache: RopeCache, out=None):
+    """ggml_rope_ext.  x [batch, n_tok, n_head, head_dim] (ggml (head_dim, n_head, n_tok, batch))."""
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_rope_ext(_ref(desc(x)), _ref(desc(pos)), cache.handle, _ref(desc(out)), _stream()))
+    return out
+
+
+# ---- activations ----------------------------------------------------------------
+
+def unary(op, x, out=None):
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_unary(op, _ref(desc(x)), _ref(desc(out)), _stream()))
+    return out
+
+
+def gelu(x, out=None):
+    return unary(GELU, x, out)
+
+
+def gelu_erf(x, out=None):
+    return unary(GELU_ERF, x, out)
+
+
+def silu(x, out=None):
+    return unary(SILU, x, out)
+
+
+def tanh(x, out=None):
+    return unary(TANH, x, out)
+
+
+def softplus(x, out=None):
+    return unary(SOFTPLUS, x, out)
+
+
+def sin(x, out=None):
+    return unary(SIN, x, out)
+
+
+def sqr(x, out=None):
+    return unary(SQR, x, out)
+
+
+def mish(x, out=None):
+    return unary(MISH, x, out)
+
+
+def leaky_relu(x, slope, out=None):
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_leaky_relu(_ref(desc(x)), slope, _ref(desc(out)), _stream()))
+    return out
+
+
+def swiglu(g, u, out=None):
+    """ggml_swiglu_split(g, u) = silu(g) * u."""
+    _ready(g)
+    out = _out_like(g, out)
+    _check(load().cbx_swiglu(_ref(desc(g)), _ref(desc(u)), _ref(desc(out)), _stream()))
+    return out
+
+
+def snake(x, alpha, alpha_inv, out=None):
+    """snake() helper: x + sin^2(x*alpha) * alpha_inv.  alpha shaped (C,) for
+    channel-innermost x [.., T, C], or (C, 1) for x [.., C, T]."""
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_snake(_ref(desc(x)), _ref(desc(alpha)), _ref(desc(alpha_inv)), _ref(desc(out)), _stream()))
+    return out

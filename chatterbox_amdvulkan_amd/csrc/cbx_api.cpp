@@ -1,0 +1,559 @@
+// cbx_api.cpp -- the C ABI: argument validation, error reporting, per-device
+// state, and the host-built constant tables (fp16 GELU, RoPE cos/sin).
+//
+// Built with -ffp-contract=off like the kernels: the tables below are
+// evaluated with one rounding per operation, as ggml-cpu's scalar code is.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "cbx_internal.h"
+
+namespace cbx {
+
+namespace {
+
+thread_local std::string g_last_error;
+constexpr int kMaxDevices = 64;
+DeviceState g_dev[kMaxDevices];
+
+}  // namespace
+
+int set_error(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        return set_error(CBX_ERR_HIP, std::string(what) + ": kernel launch failed: " + hipGetErrorString(e));
+    }
+    return CBX_OK;
+}
+
+DeviceState* current_state(int* code) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        *code = set_error(CBX_ERR_HIP, "hipGetDevice failed");
+        return nullptr;
+    }
+    if (!g_dev[dev].ready) {
+        *code = set_error(CBX_ERR_NOT_INITIALIZED, "cbx_init() has not been called for device " + std::to_string(dev));
+        return nullptr;
+    }
+    *code = CBX_OK;
+    return &g_dev[dev];
+}
+
+size_t type_size(int type) {
+    switch (type) {
+        case CBX_TYPE_F32: return 4;
+        case CBX_TYPE_F16: return 2;
+        case CBX_TYPE_Q8_0: return 34;
+        case CBX_TYPE_I32: return 4;
+        default: return 0;
+    }
+}
+
+static int64_t row_elems_per_block(int type) { return type == CBX_TYPE_Q8_0 ? 32 : 1; }
+
+int64_t nrows(const cbx_tensor* t) { return t->ne[1] * t->ne[2] * t->ne[3]; }
+int64_t nelements(const cbx_tensor* t) { return t->ne[0] * nrows(t); }
+
+bool rows_contiguous(const cbx_tensor* t) { return t->nb[0] == type_size(t->type); }
+
+bool is_contiguous(const cbx_tensor* t) {
+    if (!rows_contiguous(t)) return false;
+    size_t expect = type_size(t->type) * static_cast<size_t>(t->ne[0] / row_elems_per_block(t->type));
+    for (int i = 1; i < 4; i++) {
+        if (t->ne[i] > 1 && t->nb[i] != expect) return false;
+        expect *= static_cast<size_t>(t->ne[i]);
+    }
+    return true;
+}
+
+bool same_shape(const cbx_tensor* a, const cbx_tensor* b) {
+    for (int i = 0; i < 4; i++) if (a->ne[i] != b->ne[i]) return false;
+    return true;
+}
+
+int validate(const cbx_tensor* t, const char* what, const char* name) {
+    const std::string where = std::string(what) + ": " + name;
+    if (!t) return set_error(CBX_ERR_INVALID_ARG, where + " is NULL");
+    if (type_size(t->type) == 0) return set_error(CBX_ERR_INVALID_ARG, where + " has an unknown type " + std::to_string(t->type));
+    if (t->reserved != 0) return set_error(CBX_ERR_INVALID_ARG, where + ".reserved must be 0");
+    for (int i = 0; i < 4; i++) {
+        if (t->ne[i] < 0) return set_error(CBX_ERR_INVALID_ARG, where + " has a negative ne[" + std::to_string(i) + "]");
+    }
+    if (t->type == CBX_TYPE_Q8_0 && t->ne[0] % 32 != 0) {
+        return set_error(CBX_ERR_INVALID_ARG, where + ": Q8_0 ne[0] must be a multiple of 32");
+    }
+    if (!rows_contiguous(t)) {
+        return set_error(CBX_ERR_UNSUPPORTED, where + ": nb[0] must equal the element (block) size");
+    }
+    if (nelements(t) > 0 && t->data == nullptr) return set_error(CBX_ERR_INVALID_ARG, where + ".data is NULL");
+    return CBX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Host-built GELU table: entry h = f16(gelu(f32(h))) with
+// gelu(x) = 0.5x(1 + tanhf(sqrt(2/pi) x (1 + 0.044715 x^2))), the table that
+// ggml_cpu_init builds for ggml_gelu's f32 path (t3.cpp:537).
+// ---------------------------------------------------------------------------
+static void build_gelu_table(std::vector<uint16_t>& tab) {
+    const float coef_a = 0.044715f;
+    const float sqrt_2_over_pi = 0.79788456080286535587989211986876f;
+    tab.resize(65536);
+    for (uint32_t h = 0; h < 65536; h++) {
+        const float x = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+        const float inner = 1.0f + coef_a * x * x;
+        const float g = 0.5f * x * (1.0f + tanhf(sqrt_2_over_pi * x * inner));
+        tab[h] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(g));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// RoPE: ggml's YaRN helpers, restated for the host-side table.
+// ---------------------------------------------------------------------------
+static float yarn_corr_dim(int n_dims, int n_ctx_orig, float n_rot, float base) {
+    return n_dims * logf(n_ctx_orig / (n_rot * 2 * static_cast<float>(M_PI))) / (2 * logf(base));
+}
+
+static void yarn_corr_dims(int n_dims, int n_ctx_orig, float freq_base, float beta_fast,
+                           float beta_slow, float dims[2]) {
+    const float start = floorf(yarn_corr_dim(n_dims, n_ctx_orig, beta_fast, freq_base));
+    const float end = ceilf(yarn_corr_dim(n_dims, n_ctx_orig, beta_slow, freq_base));
+    dims[0] = start > 0.0f ? start : 0.0f;
+    dims[1] = end < static_cast<float>(n_dims - 1) ? end : static_cast<float>(n_dims - 1);
+}
+
+static void yarn_cos_sin(float theta_extrap, int64_t i0, const RopeParams& p, float* c, float* s) {
+    const float theta_interp = p.freq_scale * theta_extrap;
+    float theta = theta_interp;
+    float mscale = p.attn_factor;
+    if (p.ext_factor != 0.0f) {
+        const float d = p.corr_dims[1] - p.corr_dims[0];
+        const float y = (static_cast<float>(i0 / 2) - p.corr_dims[0]) / (d > 0.001f ? d : 0.001f);
+        const float cl = y < 0.0f ? 0.0f : y;
+        const float ramp_mix = (1.0f - (cl < 1.0f ? cl : 1.0f)) * p.ext_factor;
+        theta = theta_interp * (1 - ramp_mix) + theta_extrap * ramp_mix;
+        mscale *= 1.0f + 0.1f * logf(1.0f / p.freq_scale);
+    }
+    *c = cosf(theta) * mscale;
+    *s = sinf(theta) * mscale;
+}
+
+}  // namespace cbx
+
+struct cbx_rope_cache {
+    int              device;
+    cbx::RopeParams  p;
+    int32_t          n_pos;
+    float2*          table;        // [n_pos][n_dims/2] (cos, sin)
+    float*           freq_factors; // device copy or nullptr
+};
+
+using namespace cbx;
+
+extern "C" {
+
+const char* cbx_last_error(void) { return g_last_error.c_str(); }
+
+const char* cbx_version(void) { return "cbxops 0.1.0 (gfx950)"; }
+
+int cbx_init(int device) {
+    clear_error();
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        return set_error(CBX_ERR_HIP, "cbx_init: no HIP device");
+    }
+    if (device < 0 || device >= count || device >= kMaxDevices) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_init: device " + std::to_string(device) + " out of range");
+    }
+    DeviceState& st = g_dev[device];
+    if (st.ready) return CBX_OK;
+    int prev = 0;
+    hipGetDevice(&prev);
+    if (hipSetDevice(device) != hipSuccess) return set_error(CBX_ERR_HIP, "cbx_init: hipSetDevice failed");
+    int rc = CBX_OK;
+    std::vector<uint16_t> tab;
+    build_gelu_table(tab);
+    if (hipDeviceGetAttribute(&st.n_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        st.n_cu <= 0) {
+        st.n_cu = 256;
+    }
+    if (hipMalloc(reinterpret_cast<void**>(&st.gelu_table), 65536 * sizeof(uint16_t)) != hipSuccess ||
+        hipMalloc(reinterpret_cast<void**>(&st.err_word), sizeof(uint32_t)) != hipSuccess) {
+        rc = set_error(CBX_ERR_HIP, "cbx_init: hipMalloc failed");
+    } else if (hipMemcpy(st.gelu_table, tab.data(), 65536 * sizeof(uint16_t), hipMemcpyHostToDevice) != hipSuccess ||
+               hipMemset(st.err_word, 0, sizeof(uint32_t)) != hipSuccess ||
+               hipDeviceSynchronize() != hipSuccess) {
+        rc = set_error(CBX_ERR_HIP, "cbx_init: upload failed");
+    }
+    if (rc != CBX_OK) {
+        if (st.gelu_table) hipFree(st.gelu_table);
+        if (st.err_word) hipFree(st.err_word);
+        st = DeviceState();
+    } else {
+        st.ready = true;
+    }
+    hipSetDevice(prev);
+    return rc;
+}
+
+void cbx_shutdown(void) {
+    int prev = 0;
+    hipGetDevice(&prev);
+    for (int d = 0; d < kMaxDevices; d++) {
+        DeviceState& st = g_dev[d];
+        if (!st.ready) continue;
+        hipSetDevice(d);
+        hipDeviceSynchronize();
+        hipFree(st.gelu_table);
+        hipFree(st.err_word);
+        st = DeviceState();
+    }
+    hipSetDevice(prev);
+}
+
+int cbx_device_errors(int device, uint32_t* flags_out, int clear) {
+    clear_error();
+    if (device < 0 || device >= kMaxDevices || !g_dev[device].ready) {
+        return set_error(CBX_ERR_NOT_INITIALIZED, "cbx_device_errors: device not initialised");
+    }
+    if (!flags_out) return set_error(CBX_ERR_INVALID_ARG, "cbx_device_errors: flags_out is NULL");
+    int prev = 0;
+    hipGetDevice(&prev);
+    hipSetDevice(device);
+    int rc = CBX_OK;
+    uint32_t v = 0;
+    if (hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(&v, g_dev[device].err_word, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess) {
+        rc = set_error(CBX_ERR_HIP, "cbx_device_errors: read failed");
+    } else if (clear && (hipMemset(g_dev[device].err_word, 0, sizeof(uint32_t)) != hipSuccess ||
+                         hipDeviceSynchronize() != hipSuccess)) {
+        rc = set_error(CBX_ERR_HIP, "cbx_device_errors: clear failed");
+    }
+    *flags_out = v;
+    hipSetDevice(prev);
+    return rc;
+}
+
+// ---- gather / conversion ---------------------------------------------------
+
+static int check_gather(const char* what, const cbx_tensor* src, const cbx_tensor* ids, const cbx_tensor* dst) {
+    int rc;
+    if ((rc = validate(src, what, "src")) || (rc = validate(ids, what, "ids")) || (rc = validate(dst, what, "dst"))) return rc;
+    if (src->type != CBX_TYPE_F32 && src->type != CBX_TYPE_F16 && src->type != CBX_TYPE_Q8_0) {
+        return set_error(CBX_ERR_UNSUPPORTED, std::string(what) + ": src must be F32, F16 or Q8_0");
+    }
+    if (ids->type != CBX_TYPE_I32) return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": ids must be I32");
+    if (dst->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, std::string(what) + ": dst must be F32");
+    if (ids->ne[3] != 1) return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": ids must have ne[3] == 1");
+    if (dst->ne[0] != src->ne[0] || dst->ne[1] != ids->ne[0] || dst->ne[2] != ids->ne[1] || dst->ne[3] != ids->ne[2]) {
+        return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": dst shape must be (src.ne0, ids.ne0, ids.ne1, ids.ne2)");
+    }
+    if (src->ne[2] != ids->ne[1] || src->ne[3] != ids->ne[2]) {
+        return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": src.ne2/ne3 must equal ids.ne1/ne2");
+    }
+    return CBX_OK;
+}
+
+int cbx_get_rows(const cbx_tensor* src, const cbx_tensor* ids, cbx_tensor* dst, cbx_stream stream) {
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = check_gather("cbx_get_rows", src, ids, dst))) return rc;
+    if (nelements(dst) == 0) return CBX_OK;
+    return launch_get_rows(src, ids, nullptr, nullptr, dst, st, reinterpret_cast<hipStream_t>(stream));
+}
+
+int cbx_get_rows_add(const cbx_tensor* src, const cbx_tensor* ids, const cbx_tensor* src2,
+                     const cbx_tensor* ids2, cbx_tensor* dst, cbx_stream stream) {
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = check_gather("cbx_get_rows_add", src, ids, dst)) || (rc = check_gather("cbx_get_rows_add", src2, ids2, dst))) return rc;
+    if (nelements(dst) == 0) return CBX_OK;
+    return launch_get_rows(src, ids, src2, ids2, dst, st, reinterpret_cast<hipStream_t>(stream));
+}
+
+int cbx_cpy(const cbx_tensor* src, cbx_tensor* dst, cbx_stream stream) {
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(src, "cbx_cpy", "src")) || (rc = validate(dst, "cbx_cpy", "dst"))) return rc;
+    if ((src->type != CBX_TYPE_F32 && src->type != CBX_TYPE_F16) || (dst->type != CBX_TYPE_F32 && dst->type != CBX_TYPE_F16)) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_cpy: F32/F16 only");
+    }
+    if (!same_shape(src, dst)) return set_error(CBX_ERR_INVALID_ARG, "cbx_cpy: shapes differ");
+    if (nelements(dst) == 0) return CBX_OK;
+    return launch_cpy(src, dst, st, reinterpret_cast<hipStream_t>(stream));
+}
+
+// ---- norms -------------------------------------------------------------------
+
+static int check_float(const cbx_tensor* t, const char* what, const char* name) {
+    int rc = validate(t, what, name);
+    if (rc) return rc;
+    if (t->type != CBX_TYPE_F32 && t->type != CBX_TYPE_F16) {
+        return set_error(CBX_ERR_UNSUPPORTED, std::string(what) + ": " + name + " must be F32 or F16");
+    }
+    return CBX_OK;
+}
+
+static int check_act(int act, const char* what) {
+    if (act < CBX_UNARY_NONE || act > CBX_UNARY_MISH) {
+        return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": unknown activation " + std::to_string(act));
+    }
+    return CBX_OK;
+}
+
+// affine vector: F32, ne == (ne0, 1, 1, 1), contiguous
+static int check_row_param(const cbx_tensor* p, const cbx_tensor* x, const char* what, const char* name) {
+    if (!p) return CBX_OK;
+    int rc = validate(p, what, name);
+    if (rc) return rc;
+    if (p->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, std::string(what) + ": " + name + " must be F32");
+    if (p->ne[0] != x->ne[0] || p->ne[1] != 1 || p->ne[2] != 1 || p->ne[3] != 1) {
+        return set_error(CBX_ERR_UNSUPPORTED, std::string(what) + ": " + name + " must have ne = (x.ne0, 1, 1, 1)");
+    }
+    return CBX_OK;
+}
+
+static int row_norm_entry(const char* what, int kind, const cbx_tensor* x, const cbx_tensor* w,
+                          const cbx_tensor* b, float eps, int act, cbx_tensor* y, cbx_stream stream) {
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = check_float(x, what, "x")) || (rc = check_float(y, what, "y"))) return rc;
+    if (!same_shape(x, y)) return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": x and y shapes differ");
+    if (!(eps >= 0.0f)) return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": eps must be >= 0");
+    if ((rc = check_row_param(w, x, what, "w")) || (rc = check_row_param(b, x, what, "b")) || (rc = check_act(act, what))) return rc;
+    if (nelements(x) == 0) return CBX_OK;
+    return launch_row_norm(kind, x, w, b, eps, act, y, st, reinterpret_cast<hipStream_t>(stream));
+}
+
+int cbx_norm(const cbx_tensor* x, float eps, cbx_tensor* y, cbx_stream stream) {
+    return row_norm_entry("cbx_norm", NORM_LN, x, nullptr, nullptr, eps, CBX_UNARY_NONE, y, stream);
+}
+
+int cbx_layer_norm(const cbx_tensor* x, const cbx_tensor* w, const cbx_tensor* b, float eps, int act,
+                   cbx_tensor* y, cbx_stream stream) {
+    return row_norm_entry("cbx_layer_norm", NORM_LN, x, w, b, eps, act, y, stream);
+}
+
+int cbx_rms_norm(const cbx_tensor* x, float eps, cbx_tensor* y, cbx_stream stream) {
+    return row_norm_entry("cbx_rms_norm", NORM_RMS, x, nullptr, nullptr, eps, CBX_UNARY_NONE, y, stream);
+}
+
+int cbx_rms_norm_mul(const cbx_tensor* x, const cbx_tensor* g, float eps, cbx_tensor* y, cbx_stream stream) {
+    return row_norm_entry("cbx_rms_norm_mul", NORM_RMS, x, g, nullptr, eps, CBX_UNARY_NONE, y, stream);
+}
+
+int cbx_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
+                   int act, cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_group_norm";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(x, what, "x")) || (rc = validate(y, what, "y"))) return rc;
+    if (x->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, "cbx_group_norm: F32 only");
+    if (!same_shape(x, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_group_norm: x and y shapes differ");
+    if (n_groups <= 0) return set_error(CBX_ERR_INVALID_ARG, "cbx_group_norm: n_groups must be > 0");
+    if (!(eps >= 0.0f)) return set_error(CBX_ERR_INVALID_ARG, "cbx_group_norm: eps must be >= 0");
+    if ((rc = check_act(act, what))) return rc;
+    for (const cbx_tensor* p : {w, b}) {
+        if (!p) continue;
+        if ((rc = validate(p, what, p == w ? "w" : "b"))) return rc;
+        if (p->type != CBX_TYPE_F32 || p->ne[0] != 1 || p->ne[1] != 1 || p->ne[2] != x->ne[2] || p->ne[3] != 1 ||
+            (p->ne[2] > 1 && p->nb[2] != sizeof(float))) {
+            return set_error(CBX_ERR_UNSUPPORTED, "cbx_group_norm: w/b must be contiguous F32 with ne = (1, 1, x.ne2, 1)");
+        }
+    }
+    if (nelements(x) == 0) return CBX_OK;
+    return launch_group_norm(x, n_groups, eps, w, b, act, y, st, reinterpret_cast<hipStream_t>(stream));
+}
+
+// ---- rope --------------------------------------------------------------------
+
+int cbx_rope_cache_create(int n_dims, int mode, int n_ctx_orig, float freq_base, float freq_scale,
+                          float ext_factor, float attn_factor, float beta_fast, float beta_slow,
+                          const float* freq_factors, int32_t n_pos, cbx_rope_cache** out) {
+    clear_error();
+    if (!out) return set_error(CBX_ERR_INVALID_ARG, "cbx_rope_cache_create: out is NULL");
+    *out = nullptr;
+    if (n_dims <= 0 || n_dims % 2 != 0) return set_error(CBX_ERR_INVALID_ARG, "cbx_rope_cache_create: n_dims must be even and > 0");
+    if (mode != 0 && mode != 2) return set_error(CBX_ERR_UNSUPPORTED, "cbx_rope_cache_create: mode must be 0 (NORMAL) or 2 (NEOX)");
+    if (n_pos < 0 || static_cast<int64_t>(n_pos) * (n_dims / 2) > (int64_t{1} << 28)) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_rope_cache_create: n_pos out of range");
+    }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(CBX_ERR_HIP, "cbx_rope_cache_create: hipGetDevice failed");
+    RopeParams p{};
+    p.n_dims = n_dims;
+    p.mode = mode;
+    p.n_ctx_orig = n_ctx_orig;
+    p.freq_base = freq_base;
+    p.freq_scale = freq_scale;
+    p.ext_factor = ext_factor;
+    p.attn_factor = attn_factor;
+    p.beta_fast = beta_fast;
+    p.beta_slow = beta_slow;
+    p.theta_scale = powf(freq_base, -2.0f / n_dims);
+    yarn_corr_dims(n_dims, n_ctx_orig, freq_base, beta_fast, beta_slow, p.corr_dims);
+
+    const int half = n_dims / 2;
+    std::vector<float2> tab(static_cast<size_t>(n_pos) * half);
+    for (int32_t pos = 0; pos < n_pos; pos++) {
+        // theta_i = pos * theta_scale^i as ggml_rope_cache_init forms it
+        float theta = static_cast<float>(pos);
+        for (int i = 0; i < half; i++) {
+            const float ff = freq_factors ? freq_factors[i] : 1.0f;
+            float c, s;
+            yarn_cos_sin(theta / ff, 2 * i, p, &c, &s);
+            tab[static_cast<size_t>(pos) * half + i] = make_float2(c, s);
+            theta *= p.theta_scale;
+        }
+    }
+    auto* cache = new cbx_rope_cache();
+    cache->device = dev;
+    cache->p = p;
+    cache->n_pos = n_pos;
+    cache->table = nullptr;
+    cache->freq_factors = nullptr;
+    bool ok = true;
+    if (n_pos > 0) {
+        ok = hipMalloc(reinterpret_cast<void**>(&cache->table), tab.size() * sizeof(float2)) == hipSuccess &&
+             hipMemcpy(cache->table, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice) == hipSuccess;
+    }
+    if (ok && freq_factors) {
+        ok = hipMalloc(reinterpret_cast<void**>(&cache->freq_factors), half * sizeof(float)) == hipSuccess &&
+             hipMemcpy(cache->freq_factors, freq_factors, half * sizeof(float), hipMemcpyHostToDevice) == hipSuccess;
+    }
+    if (!ok) {
+        cbx_rope_cache_destroy(cache);
+        return set_error(CBX_ERR_HIP, "cbx_rope_cache_create: device allocation/upload failed");
+    }
+    *out = cache;
+    return CBX_OK;
+}
+
+void cbx_rope_cache_destroy(cbx_rope_cache* cache) {
+    if (!cache) return;
+    int prev = 0;
+    hipGetDevice(&prev);
+    hipSetDevice(cache->device);
+    hipDeviceSynchronize();
+    if (cache->table) hipFree(cache->table);
+    if (cache->freq_factors) hipFree(cache->freq_factors);
+    hipSetDevice(prev);
+    delete cache;
+}
+
+int cbx_rope_ext(const cbx_tensor* x, const cbx_tensor* pos, const cbx_rope_cache* cache, cbx_tensor* y,
+                 cbx_stream stream) {
+    const char* what = "cbx_rope_ext";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if (!cache) return set_error(CBX_ERR_INVALID_ARG, "cbx_rope_ext: cache is NULL");
+    int dev = 0;
+    hipGetDevice(&dev);
+    if (dev != cache->device) return set_error(CBX_ERR_INVALID_ARG, "cbx_rope_ext: cache belongs to another device");
+    if ((rc = check_float(x, what, "x")) || (rc = check_float(y, what, "y")) || (rc = validate(pos, what, "pos"))) return rc;
+    if (x->type != y->type) return set_error(CBX_ERR_UNSUPPORTED, "cbx_rope_ext: x and y types differ");
+    if (!same_shape(x, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_rope_ext: x and y shapes differ");
+    if (pos->type != CBX_TYPE_I32 || pos->ne[0] != x->ne[2] || pos->ne[1] != 1 || pos->ne[2] != 1 || pos->ne[3] != 1) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_rope_ext: pos must be I32 with ne = (x.ne2, 1, 1, 1)");
+    }
+    if (cache->p.n_dims > x->ne[0]) return set_error(CBX_ERR_INVALID_ARG, "cbx_rope_ext: n_dims > x.ne0");
+    if (nelements(x) == 0) return CBX_OK;
+    return launch_rope(x, pos, cache->p, cache->table, cache->n_pos, cache->freq_factors, y, st,
+                       reinterpret_cast<hipStream_t>(stream));
+}
+
+// ---- activations -------------------------------------------------------------
+
+static int unary_entry(const char* what, int op, float param, const cbx_tensor* x, cbx_tensor* y,
+                       cbx_stream stream) {
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = check_float(x, what, "x")) || (rc = check_float(y, what, "y"))) return rc;
+    if (x->type != y->type) return set_error(CBX_ERR_UNSUPPORTED, std::string(what) + ": x and y types differ");
+    if (!same_shape(x, y)) return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": x and y shapes differ");
+    if (nelements(x) == 0) return CBX_OK;
+    return launch_unary(op, param, x, y, st, reinterpret_cast<hipStream_t>(stream));
+}
+
+int cbx_unary(int op, const cbx_tensor* x, cbx_tensor* y, cbx_stream stream) {
+    if (op < CBX_UNARY_GELU || op > CBX_UNARY_MISH) {
+        clear_error();
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_unary: unknown op " + std::to_string(op));
+    }
+    return unary_entry("cbx_unary", op, 0.0f, x, y, stream);
+}
+int cbx_gelu(const cbx_tensor* x, cbx_tensor* y, cbx_stream s) { return unary_entry("cbx_gelu", CBX_UNARY_GELU, 0.0f, x, y, s); }
+int cbx_gelu_erf(const cbx_tensor* x, cbx_tensor* y, cbx_stream s) { return unary_entry("cbx_gelu_erf", CBX_UNARY_GELU_ERF, 0.0f, x, y, s); }
+int cbx_silu(const cbx_tensor* x, cbx_tensor* y, cbx_stream s) { return unary_entry("cbx_silu", CBX_UNARY_SILU, 0.0f, x, y, s); }
+int cbx_mish(const cbx_tensor* x, cbx_tensor* y, cbx_stream s) { return unary_entry("cbx_mish", CBX_UNARY_MISH, 0.0f, x, y, s); }
+
+int cbx_leaky_relu(const cbx_tensor* x, float slope, cbx_tensor* y, cbx_stream stream) {
+    return unary_entry("cbx_leaky_relu", UNARY_LEAKY, slope, x, y, stream);
+}
+
+int cbx_swiglu(const cbx_tensor* g, const cbx_tensor* u, cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_swiglu";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = check_float(g, what, "g")) || (rc = check_float(u, what, "u")) || (rc = check_float(y, what, "y"))) return rc;
+    if (g->type != u->type || g->type != y->type) return set_error(CBX_ERR_UNSUPPORTED, "cbx_swiglu: g, u, y types differ");
+    if (!same_shape(g, y) || !same_shape(u, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_swiglu: shapes differ");
+    if (nelements(y) == 0) return CBX_OK;
+    return launch_swiglu(g, u, y, st, reinterpret_cast<hipStream_t>(stream));
+}
+
+int cbx_snake(const cbx_tensor* x, const cbx_tensor* alpha, const cbx_tensor* alpha_inv, cbx_tensor* y,
+              cbx_stream stream) {
+    const char* what = "cbx_snake";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(x, what, "x")) || (rc = validate(y, what, "y")) || (rc = validate(alpha, what, "alpha")) ||
+        (rc = validate(alpha_inv, what, "alpha_inv"))) return rc;
+    if (x->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32 || alpha->type != CBX_TYPE_F32 || alpha_inv->type != CBX_TYPE_F32) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_snake: F32 only");
+    }
+    if (!same_shape(x, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_snake: x and y shapes differ");
+    if (!same_shape(alpha, alpha_inv)) return set_error(CBX_ERR_INVALID_ARG, "cbx_snake: alpha and alpha_inv shapes differ");
+    const bool inner = alpha->ne[0] == x->ne[0] && alpha->ne[1] == 1 && alpha->ne[2] == 1 && alpha->ne[3] == 1;
+    const bool outer = alpha->ne[0] == 1 && alpha->ne[1] == x->ne[1] && alpha->ne[2] == 1 && alpha->ne[3] == 1;
+    if (!inner && !outer) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_snake: alpha must have ne = (x.ne0,1,1,1) or (1,x.ne1,1,1)");
+    }
+    if (!is_contiguous(alpha) || !is_contiguous(alpha_inv)) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_snake: alpha and alpha_inv must be contiguous");
+    }
+    if (nelements(x) == 0) return CBX_OK;
+    return launch_snake(x, alpha, alpha_inv, y, st, reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

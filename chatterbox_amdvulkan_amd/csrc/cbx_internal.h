@@ -1,0 +1,101 @@
+// cbx_internal.h -- definitions shared by the host ABI layer and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/cbxops.h"
+
+namespace cbx {
+
+// A tensor view passed to kernels by value.
+struct View {
+    char*   data;
+    int64_t ne[4];
+    int64_t nb[4];
+};
+
+inline View view_of(const cbx_tensor* t) {
+    View v;
+    v.data = static_cast<char*>(t->data);
+    for (int i = 0; i < 4; i++) {
+        v.ne[i] = t->ne[i];
+        v.nb[i] = static_cast<int64_t>(t->nb[i]);
+    }
+    return v;
+}
+
+inline View null_view() {
+    View v;
+    v.data = nullptr;
+    for (int i = 0; i < 4; i++) { v.ne[i] = 1; v.nb[i] = 0; }
+    return v;
+}
+
+// Per-device state created by cbx_init.
+struct DeviceState {
+    bool      ready = false;
+    int       n_cu = 0;
+    uint16_t* gelu_table = nullptr;   // 65536 fp16 codes
+    uint32_t* err_word = nullptr;     // sticky device error bits
+};
+
+// Device error bits.
+enum : uint32_t { DEV_ERR_ROW_INDEX = 1u };
+
+// ---- host helpers implemented in cbx_api.cpp ----------------------------
+int  set_error(int code, const std::string& msg);
+void clear_error();
+// Current device's state, or nullptr (and an error recorded) when cbx_init
+// has not been called for it.
+DeviceState* current_state(int* code);
+int  check_launch(const char* what);
+
+int64_t nelements(const cbx_tensor* t);
+int64_t nrows(const cbx_tensor* t);
+size_t  type_size(int type);
+bool    is_contiguous(const cbx_tensor* t);
+bool    rows_contiguous(const cbx_tensor* t);   // nb[0] == element size
+bool    same_shape(const cbx_tensor* a, const cbx_tensor* b);
+// Validates pointer, type, non-negative sizes and nb[0] for a float/int
+// tensor.  Returns 0 or a negative status with the error recorded.
+int validate(const cbx_tensor* t, const char* what, const char* name);
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Kernel launchers, one per translation unit.
+int launch_get_rows(const cbx_tensor* src, const cbx_tensor* ids, const cbx_tensor* src2,
+                    const cbx_tensor* ids2, cbx_tensor* dst, DeviceState* st, hipStream_t s);
+int launch_cpy(const cbx_tensor* src, cbx_tensor* dst, DeviceState* st, hipStream_t s);
+int launch_row_norm(int kind, const cbx_tensor* x, const cbx_tensor* w, const cbx_tensor* b,
+                    float eps, int act, cbx_tensor* y, DeviceState* st, hipStream_t s);
+int launch_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w,
+                      const cbx_tensor* b, int act, cbx_tensor* y, DeviceState* st,
+                      hipStream_t s);
+int launch_unary(int op, float param, const cbx_tensor* x, cbx_tensor* y, DeviceState* st,
+                 hipStream_t s);
+int launch_swiglu(const cbx_tensor* g, const cbx_tensor* u, cbx_tensor* y, DeviceState* st,
+                  hipStream_t s);
+int launch_snake(const cbx_tensor* x, const cbx_tensor* a, const cbx_tensor* ai, cbx_tensor* y,
+                 DeviceState* st, hipStream_t s);
+
+struct RopeParams {
+    int   n_dims;
+    int   mode;
+    int   n_ctx_orig;
+    float freq_base, freq_scale, ext_factor, attn_factor, beta_fast, beta_slow;
+    float theta_scale;
+    float corr_dims[2];
+};
+int launch_rope(const cbx_tensor* x, const cbx_tensor* pos, const RopeParams& p,
+                const float2* table, int32_t n_pos, const float* freq_factors_dev,
+                cbx_tensor* y, DeviceState* st, hipStream_t s);
+
+// Row-norm kinds.
+enum { NORM_LN = 0, NORM_RMS = 1 };
+// Pseudo unary op used internally for leaky_relu.
+enum { UNARY_LEAKY = 100 };
+
+}  // namespace cbx

@@ -1,0 +1,204 @@
+// k_rows.hip -- embedding gather (F32 / F16 / Q8_0 tables, optional fused
+// second gather + add) and F32<->F16 conversion.
+//
+// Gather: one workgroup per output row; lanes move 4 consecutive elements
+// each (16-byte stores), so a wave writes 1 KiB contiguous.  Q8_0 rows are
+// dequantised in registers: each 4-element group reads its block's f16
+// scale and four int8 quants and forms q * d with one f32 multiply, exactly
+// dequantize_row_q8_0.  The second gather's row is added with one f32 add,
+// exactly ggml_add of the two gathered tensors (t3.cpp:446-455).
+#include "cbx_device.h"
+
+namespace cbx {
+namespace {
+
+enum { T_F32 = CBX_TYPE_F32, T_F16 = CBX_TYPE_F16, T_Q8 = CBX_TYPE_Q8_0 };
+
+// 4 elements starting at element j (j % 4 == 0) of a table row.
+template <int TYPE>
+__device__ __forceinline__ float4 load_row4(const char* row, int64_t j) {
+    if constexpr (TYPE == T_F32) {
+        return *reinterpret_cast<const float4*>(row + j * 4);
+    } else if constexpr (TYPE == T_F16) {
+        return Elt<uint16_t>::load4(row + j * 2);
+    } else {
+        const char* blk = row + (j >> 5) * 34;
+        const float d = h2f(*reinterpret_cast<const uint16_t*>(blk));
+        const int8_t* q = reinterpret_cast<const int8_t*>(blk + 2 + (j & 31));
+        return make_float4(static_cast<float>(q[0]) * d, static_cast<float>(q[1]) * d,
+                           static_cast<float>(q[2]) * d, static_cast<float>(q[3]) * d);
+    }
+}
+
+template <int TYPE>
+__device__ __forceinline__ float load_row1(const char* row, int64_t j) {
+    if constexpr (TYPE == T_F32) {
+        return *reinterpret_cast<const float*>(row + j * 4);
+    } else if constexpr (TYPE == T_F16) {
+        return h2f(*reinterpret_cast<const uint16_t*>(row + j * 2));
+    } else {
+        const char* blk = row + (j >> 5) * 34;
+        const float d = h2f(*reinterpret_cast<const uint16_t*>(blk));
+        return static_cast<float>(*reinterpret_cast<const int8_t*>(blk + 2 + (j & 31))) * d;
+    }
+}
+
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+// TYPE2 < 0: plain gather.  VEC: rows are 16-byte aligned and ne0 % 4 == 0.
+template <int TYPE, int TYPE2, bool VEC>
+__global__ __launch_bounds__(256) void k_get_rows(View src, View ids, View src2, View ids2, View dst,
+                                                  int64_t n_out_rows, uint32_t* __restrict__ err) {
+    const int64_t ne0 = dst.ne[0];
+    const int64_t n10 = ids.ne[0], n11 = ids.ne[1];
+    for (int64_t r = blockIdx.x; r < n_out_rows; r += gridDim.x) {
+        const int64_t i12 = r / (n11 * n10);
+        const int64_t i11 = (r - i12 * n11 * n10) / n10;
+        const int64_t i10 = r - i12 * n11 * n10 - i11 * n10;
+        const int32_t id = *reinterpret_cast<const int32_t*>(ids.data + i10 * ids.nb[0] + i11 * ids.nb[1] + i12 * ids.nb[2]);
+        bool ok = id >= 0 && id < src.ne[1];
+        int32_t id2 = 0;
+        if constexpr (TYPE2 >= 0) {
+            id2 = *reinterpret_cast<const int32_t*>(ids2.data + i10 * ids2.nb[0] + i11 * ids2.nb[1] + i12 * ids2.nb[2]);
+            ok = ok && id2 >= 0 && id2 < src2.ne[1];
+        }
+        char* d = dst.data + i10 * dst.nb[1] + i11 * dst.nb[2] + i12 * dst.nb[3];
+        if (!ok) {
+            // ggml aborts on an out-of-range index; here the row is zeroed and
+            // the sticky device error bit is raised for the host to read.
+            for (int64_t j = threadIdx.x; j < ne0; j += blockDim.x) reinterpret_cast<float*>(d)[j] = 0.0f;
+            if (threadIdx.x == 0) atomicOr(err, static_cast<uint32_t>(DEV_ERR_ROW_INDEX));
+            continue;
+        }
+        const char* s = src.data + id * src.nb[1] + i11 * src.nb[2] + i12 * src.nb[3];
+        const char* s2 = nullptr;
+        if constexpr (TYPE2 >= 0) s2 = src2.data + id2 * src2.nb[1] + i11 * src2.nb[2] + i12 * src2.nb[3];
+        if constexpr (VEC) {
+            for (int64_t j = threadIdx.x * 4; j < ne0; j += blockDim.x * 4) {
+                float4 v = load_row4<TYPE>(s, j);
+                if constexpr (TYPE2 >= 0) v = add4(v, load_row4<TYPE2>(s2, j));
+                *reinterpret_cast<float4*>(d + j * 4) = v;
+            }
+        } else {
+            for (int64_t j = threadIdx.x; j < ne0; j += blockDim.x) {
+                float v = load_row1<TYPE>(s, j);
+                if constexpr (TYPE2 >= 0) v = v + load_row1<TYPE2>(s2, j);
+                reinterpret_cast<float*>(d)[j] = v;
+            }
+        }
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+
+// Can the table be read 4 elements at a time with aligned vector loads?
+bool vec_ok_table(const cbx_tensor* t) {
+    if (!t) return true;
+    if (t->type == CBX_TYPE_Q8_0) return true;   // byte loads
+    const size_t a = t->type == CBX_TYPE_F32 ? 16 : 8;
+    if (reinterpret_cast<uintptr_t>(t->data) % a) return false;
+    for (int i = 1; i < 4; i++) if (t->nb[i] % a) return false;
+    return t->ne[0] % 4 == 0;
+}
+
+template <int TYPE, int TYPE2>
+int launch_gather_t(bool vec, dim3 grid, dim3 block, hipStream_t s, View src, View ids, View src2, View ids2,
+                    View dst, int64_t n, uint32_t* err) {
+    if (vec) {
+        hipLaunchKernelGGL((k_get_rows<TYPE, TYPE2, true>), grid, block, 0, s, src, ids, src2, ids2, dst, n, err);
+    } else {
+        hipLaunchKernelGGL((k_get_rows<TYPE, TYPE2, false>), grid, block, 0, s, src, ids, src2, ids2, dst, n, err);
+    }
+    return check_launch("get_rows");
+}
+
+template <int TYPE>
+int launch_gather_t1(int type2, bool vec, dim3 grid, dim3 block, hipStream_t s, View src, View ids, View src2,
+                     View ids2, View dst, int64_t n, uint32_t* err) {
+    switch (type2) {
+        case -1: return launch_gather_t<TYPE, -1>(vec, grid, block, s, src, ids, src2, ids2, dst, n, err);
+        case T_F32: return launch_gather_t<TYPE, T_F32>(vec, grid, block, s, src, ids, src2, ids2, dst, n, err);
+        case T_F16: return launch_gather_t<TYPE, T_F16>(vec, grid, block, s, src, ids, src2, ids2, dst, n, err);
+        default: return launch_gather_t<TYPE, T_Q8>(vec, grid, block, s, src, ids, src2, ids2, dst, n, err);
+    }
+}
+
+// ---- F32 <-> F16 conversion -------------------------------------------------
+
+template <typename TS, typename TD>
+__global__ __launch_bounds__(256) void k_cpy_flat(const char* __restrict__ x, char* __restrict__ y, int64_t n) {
+    const int64_t n4 = n / 4;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride) {
+        Elt<TD>::store4(y + i * 4 * Elt<TD>::size, Elt<TS>::load4(x + i * 4 * Elt<TS>::size));
+    }
+    if (blockIdx.x == 0) {
+        for (int64_t i = n4 * 4 + threadIdx.x; i < n; i += blockDim.x) {
+            Elt<TD>::store1(y + i * Elt<TD>::size, Elt<TS>::load1(x + i * Elt<TS>::size));
+        }
+    }
+}
+
+template <typename TS, typename TD>
+__global__ __launch_bounds__(256) void k_cpy_rows(View x, View y, int64_t nr) {
+    for (int64_t r = blockIdx.x; r < nr; r += gridDim.x) {
+        const int64_t i3 = r / (x.ne[2] * x.ne[1]);
+        const int64_t i2 = (r - i3 * x.ne[2] * x.ne[1]) / x.ne[1];
+        const int64_t i1 = r - i3 * x.ne[2] * x.ne[1] - i2 * x.ne[1];
+        const char* xr = x.data + i1 * x.nb[1] + i2 * x.nb[2] + i3 * x.nb[3];
+        char* yr = y.data + i1 * y.nb[1] + i2 * y.nb[2] + i3 * y.nb[3];
+        for (int64_t j = threadIdx.x; j < x.ne[0]; j += blockDim.x) {
+            Elt<TD>::store1(yr + j * Elt<TD>::size, Elt<TS>::load1(xr + j * Elt<TS>::size));
+        }
+    }
+}
+
+template <typename TS, typename TD>
+int launch_cpy_t(const cbx_tensor* src, cbx_tensor* dst, DeviceState* st, hipStream_t s) {
+    const int64_t n = nelements(src);
+    const bool flat = is_contiguous(src) && is_contiguous(dst) && aligned16(src->data) && aligned16(dst->data);
+    if (flat) {
+        const int64_t blocks = std::min<int64_t>(std::max<int64_t>(1, cdiv(n / 4, 256)), int64_t{st->n_cu} * 16);
+        hipLaunchKernelGGL((k_cpy_flat<TS, TD>), dim3(blocks), dim3(256), 0, s,
+                           static_cast<const char*>(src->data), static_cast<char*>(dst->data), n);
+    } else {
+        const int64_t nr = nrows(src);
+        const int64_t blocks = std::min<int64_t>(nr, int64_t{1} << 20);
+        hipLaunchKernelGGL((k_cpy_rows<TS, TD>), dim3(blocks), dim3(256), 0, s, view_of(src), view_of(dst), nr);
+    }
+    return check_launch("cpy");
+}
+
+}  // namespace
+
+int launch_get_rows(const cbx_tensor* src, const cbx_tensor* ids, const cbx_tensor* src2, const cbx_tensor* ids2,
+                    cbx_tensor* dst, DeviceState* st, hipStream_t s) {
+    const int64_t n = ids->ne[0] * ids->ne[1] * ids->ne[2];
+    const bool vec = dst->ne[0] % 4 == 0 && vec_ok_table(src) && vec_ok_table(src2) && aligned16(dst->data) &&
+                     dst->nb[1] % 16 == 0 && dst->nb[2] % 16 == 0 && dst->nb[3] % 16 == 0;
+    const int64_t lanes = vec ? cdiv(dst->ne[0], 4) : dst->ne[0];
+    const int threads = static_cast<int>(std::min<int64_t>(256, std::max<int64_t>(64, cdiv(lanes, 64) * 64)));
+    const dim3 grid(static_cast<unsigned>(std::min<int64_t>(n, int64_t{1} << 20)));
+    const dim3 block(threads);
+    View vs = view_of(src), vi = view_of(ids), vd = view_of(dst);
+    View vs2 = src2 ? view_of(src2) : null_view(), vi2 = ids2 ? view_of(ids2) : null_view();
+    const int t2 = src2 ? src2->type : -1;
+    switch (src->type) {
+        case T_F32: return launch_gather_t1<T_F32>(t2, vec, grid, block, s, vs, vi, vs2, vi2, vd, n, st->err_word);
+        case T_F16: return launch_gather_t1<T_F16>(t2, vec, grid, block, s, vs, vi, vs2, vi2, vd, n, st->err_word);
+        default: return launch_gather_t1<T_Q8>(t2, vec, grid, block, s, vs, vi, vs2, vi2, vd, n, st->err_word);
+    }
+}
+
+int launch_cpy(const cbx_tensor* src, cbx_tensor* dst, DeviceState* st, hipStream_t s) {
+    const bool s16 = src->type == CBX_TYPE_F16, d16 = dst->type == CBX_TYPE_F16;
+    if (!s16 && !d16) return launch_cpy_t<float, float>(src, dst, st, s);
+    if (!s16 && d16) return launch_cpy_t<float, uint16_t>(src, dst, st, s);
+    if (s16 && !d16) return launch_cpy_t<uint16_t, float>(src, dst, st, s);
+    return launch_cpy_t<uint16_t, uint16_t>(src, dst, st, s);
+}
+
+}  // namespace cbx

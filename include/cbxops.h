@@ -1,0 +1,192 @@
+/*
+ * cbxops.h -- C ABI of the MI355X (gfx950) fused layer-op library.
+ *
+ * Each entry point replaces one ggml op, or one composition of ggml ops,
+ * that chatterbox-cpp's graph builders call on the fused layer-op path, with
+ * the same tensor layout (ggml ne[]/nb[]: ne[0] innermost, byte strides) and
+ * the same arithmetic as ggml's CPU backend.  Every entry point:
+ *   - takes device pointers owned by the caller and a HIP stream;
+ *   - allocates nothing and launches asynchronously on that stream;
+ *   - returns CBX_OK (0) or a negative cbx_status, with a message available
+ *     from cbx_last_error() on the calling thread (the convention of the
+ *     reference's own C ABI, chatterbox-cpp/src/chatterbox_capi.cpp:14-18).
+ * Unlike ggml (GGML_ASSERT), no call aborts the process.
+ *
+ * Threading: calls are stream-ordered; calls on different streams may run
+ * concurrently.  cbx_init / cbx_shutdown / cbx_rope_cache_* are not
+ * thread-safe against each other.
+ */
+#ifndef CBXOPS_H
+#define CBXOPS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same handle type as HIP's hipStream_t (NULL = the null stream). */
+struct ihipStream_t;
+typedef struct ihipStream_t* cbx_stream;
+
+/* Element types, numbered as ggml_type. */
+typedef enum cbx_type {
+    CBX_TYPE_F32  = 0,
+    CBX_TYPE_F16  = 1,
+    CBX_TYPE_Q8_0 = 8,   /* blocks of 32: f16 scale d + int8 qs[32], 34 bytes */
+    CBX_TYPE_I32  = 26,
+} cbx_type;
+
+typedef enum cbx_status {
+    CBX_OK                  = 0,
+    CBX_ERR_INVALID_ARG     = -1,  /* bad pointer, shape, stride or type   */
+    CBX_ERR_UNSUPPORTED     = -2,  /* valid ggml op, layout not supported  */
+    CBX_ERR_NOT_INITIALIZED = -3,  /* cbx_init() not called for the device */
+    CBX_ERR_HIP             = -4,  /* a HIP runtime call failed            */
+} cbx_status;
+
+/* A ggml-layout tensor view.  For Q8_0, ne[0] counts elements (a multiple
+ * of 32) and nb[0] is the block size, 34, as in ggml. */
+typedef struct cbx_tensor {
+    void*    data;
+    int32_t  type;      /* cbx_type */
+    int32_t  reserved;  /* must be 0 */
+    int64_t  ne[4];
+    size_t   nb[4];
+} cbx_tensor;
+
+/* Activations for cbx_unary and the fused epilogues. */
+typedef enum cbx_unary_op {
+    CBX_UNARY_NONE     = -1, /* epilogue only: no activation                           */
+    CBX_UNARY_GELU     = 0,  /* ggml_gelu, fp16-table semantics (t3.cpp:537)           */
+    CBX_UNARY_GELU_ERF = 1,  /* ggml_gelu_erf (cfm_decoder.cpp:239, s3enc.cpp:177)      */
+    CBX_UNARY_SILU     = 2,  /* ggml_silu (cfm_decoder.cpp:466, flow_encoder.cpp:402)   */
+    CBX_UNARY_TANH     = 3,  /* ggml_tanh (cfm_decoder.cpp:37)                          */
+    CBX_UNARY_SOFTPLUS = 4,  /* ggml_softplus (cfm_decoder.cpp:37)                      */
+    CBX_UNARY_SIN      = 5,  /* ggml_sin (hift_vocoder.cpp:69)                          */
+    CBX_UNARY_SQR      = 6,  /* ggml_sqr (hift_vocoder.cpp:70)                          */
+    CBX_UNARY_MISH     = 7,  /* mish() = mul(x, tanh(softplus(x))) (cfm_decoder.cpp:36-38) */
+} cbx_unary_op;
+
+/* ---- library lifecycle -------------------------------------------------- */
+
+/* Prepares `device` for use: uploads the 65536-entry fp16 GELU table (the
+ * table ggml_cpu_init builds for ggml_gelu), and a sticky device error word.
+ * The analogue of ggml_cpu_init(); call once per device before any op.     */
+int  cbx_init(int device);
+/* Releases every device's state.  No op may be in flight. */
+void cbx_shutdown(void);
+/* Message of the last failed call on this thread ("" if none). */
+const char* cbx_last_error(void);
+const char* cbx_version(void);
+/* Reads (and with clear != 0 resets) the device error word of `device`,
+ * synchronising the device first.  Bit 0: a get_rows index was out of
+ * range (ggml aborts there; this library writes zeros to that row).       */
+int  cbx_device_errors(int device, uint32_t* flags_out, int clear);
+
+/* ---- gather and conversion ---------------------------------------------- */
+
+/* ggml_get_rows(src, ids) then ggml_cast(F32): dst[:, i10, i11, i12] =
+ * to_f32(src[:, ids[i10, i11, i12], i11, i12]).  src F32, F16 or Q8_0; ids
+ * I32; dst F32 with ne = (src.ne0, ids.ne0, ids.ne1, ids.ne2).
+ * Replaces t3.cpp:440-447 and flow_encoder.cpp:588-590.                    */
+int cbx_get_rows(const cbx_tensor* src, const cbx_tensor* ids,
+                 cbx_tensor* dst, cbx_stream stream);
+
+/* ggml_add(get_rows(src, ids), get_rows(src2, ids2)) in one pass: the T3
+ * token + learned-position embedding (t3.cpp:446-455).                     */
+int cbx_get_rows_add(const cbx_tensor* src, const cbx_tensor* ids,
+                     const cbx_tensor* src2, const cbx_tensor* ids2,
+                     cbx_tensor* dst, cbx_stream stream);
+
+/* ggml_cpy / ggml_cast between F32 and F16 (round to nearest even), same
+ * shape (t3.cpp:441,447,454).                                              */
+int cbx_cpy(const cbx_tensor* src, cbx_tensor* dst, cbx_stream stream);
+
+/* ---- norms -------------------------------------------------------------- */
+
+/* ggml_norm(x, eps) over ne[0] (F32 or F16 storage, f32/f64 arithmetic). */
+int cbx_norm(const cbx_tensor* x, float eps, cbx_tensor* y, cbx_stream stream);
+
+/* layer_norm() = ggml_add(ggml_mul(ggml_norm(x, eps), w), b) in one pass
+ * (cfm_decoder.cpp:29-33; t3.cpp:465-466,531-532,545-546;
+ * flow_encoder.cpp:58-62; s3enc.cpp:100-104).  w, b: F32 with ne =
+ * (x.ne0,1,1,1), or NULL.  act: CBX_UNARY_NONE, or an activation applied
+ * to the result (CBX_UNARY_MISH fuses causal_block1d's LN -> Mish,
+ * cfm_decoder.cpp:143-146).                                                */
+int cbx_layer_norm(const cbx_tensor* x, const cbx_tensor* w,
+                   const cbx_tensor* b, float eps, int act, cbx_tensor* y,
+                   cbx_stream stream);
+
+/* ggml_rms_norm(x, eps). */
+int cbx_rms_norm(const cbx_tensor* x, float eps, cbx_tensor* y,
+                 cbx_stream stream);
+
+/* ggml_mul(ggml_rms_norm(x, eps), g) in one pass; g F32 (x.ne0,1,1,1) or
+ * NULL.  F16 x/y: f32 arithmetic, one rounding at the store.              */
+int cbx_rms_norm_mul(const cbx_tensor* x, const cbx_tensor* g, float eps,
+                     cbx_tensor* y, cbx_stream stream);
+
+/* ggml_group_norm(x, n_groups, eps) [-> mul(w) -> add(b)] [-> act] in one
+ * pass.  Channels are ne[2] (ggml's convention), F32.  w, b: F32 with ne =
+ * (1,1,ne2,1), or NULL.  act: CBX_UNARY_NONE or an activation.             */
+int cbx_group_norm(const cbx_tensor* x, int n_groups, float eps,
+                   const cbx_tensor* w, const cbx_tensor* b, int act,
+                   cbx_tensor* y, cbx_stream stream);
+
+/* ---- rotary embedding --------------------------------------------------- */
+
+/* A device-resident cos/sin table for ggml_rope_ext's parameters, for
+ * positions [0, n_pos).  Built on the host with ggml's semantics (theta
+ * iterated as an f32 product, YaRN ramp, attn_factor) and uploaded once;
+ * the per-position rows are staged in LDS by cbx_rope_ext.  Allocates
+ * device memory on the current device.  freq_factors: host array of
+ * n_dims/2 floats, or NULL.                                                */
+typedef struct cbx_rope_cache cbx_rope_cache;
+int  cbx_rope_cache_create(int n_dims, int mode, int n_ctx_orig,
+                           float freq_base, float freq_scale,
+                           float ext_factor, float attn_factor,
+                           float beta_fast, float beta_slow,
+                           const float* freq_factors, int32_t n_pos,
+                           cbx_rope_cache** out);
+void cbx_rope_cache_destroy(cbx_rope_cache* cache);
+
+/* ggml_rope_ext(x, pos, NULL, n_dims, mode, ...) with the cache's
+ * parameters (s3enc.cpp:215-229).  x, y: F32 or F16, ne = (head_dim,
+ * n_head, n_tok, batch); pos: I32 [n_tok].  Positions outside [0, n_pos)
+ * are computed on the device (same theta recurrence, device cosf/sinf).   */
+int cbx_rope_ext(const cbx_tensor* x, const cbx_tensor* pos,
+                 const cbx_rope_cache* cache, cbx_tensor* y,
+                 cbx_stream stream);
+
+/* ---- activations -------------------------------------------------------- */
+
+/* One ggml unary op (cbx_unary_op), F32 or F16, x and y same shape. */
+int cbx_unary(int op, const cbx_tensor* x, cbx_tensor* y, cbx_stream stream);
+int cbx_gelu(const cbx_tensor* x, cbx_tensor* y, cbx_stream stream);
+int cbx_gelu_erf(const cbx_tensor* x, cbx_tensor* y, cbx_stream stream);
+int cbx_silu(const cbx_tensor* x, cbx_tensor* y, cbx_stream stream);
+int cbx_mish(const cbx_tensor* x, cbx_tensor* y, cbx_stream stream);
+
+/* ggml_leaky_relu(x, slope, false) (hift_vocoder.cpp:686,748;
+ * flow_encoder.cpp:454). */
+int cbx_leaky_relu(const cbx_tensor* x, float slope, cbx_tensor* y,
+                   cbx_stream stream);
+
+/* ggml_swiglu_split(g, u) = silu(g) * u, F32 or F16. */
+int cbx_swiglu(const cbx_tensor* g, const cbx_tensor* u, cbx_tensor* y,
+               cbx_stream stream);
+
+/* snake() = x + sin^2(x * alpha) * alpha_inv in one pass
+ * (hift_vocoder.cpp:64-73; alpha_inv = 1/(alpha + 1e-9) precomputed by the
+ * caller as at hift_vocoder.cpp:413-427).  x, y F32; alpha, alpha_inv F32
+ * with ne = (x.ne0,1,1,1) (channel innermost, the reference's (C, T)
+ * layout) or (1,x.ne1,1,1) (channel outer).                                */
+int cbx_snake(const cbx_tensor* x, const cbx_tensor* alpha,
+              const cbx_tensor* alpha_inv, cbx_tensor* y, cbx_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CBXOPS_H */

@@ -1,0 +1,142 @@
+/*
+ * cbx_oracle.h -- CPU restatement of the ggml-cpu arithmetic used by
+ * chatterbox-cpp's fused layer-op path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * op library and the timed CPU baseline of bench.py.  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.  The
+ * product (libcbxops) never links, loads or calls it.
+ *
+ * What it restates and why: every op on the path is a ggml_* call made by the
+ * reference's graph builders (chatterbox-cpp/src/t3.cpp, cfm_decoder.cpp,
+ * hift_vocoder.cpp, flow_encoder.cpp, s3enc.cpp).  The arithmetic itself lives
+ * in the ggml submodule (chatterbox-cpp/third_party/ggml, .gitmodules:1-3,
+ * pinned v0.12.0 per chatterbox-cpp/README.md:36), which is not vendored in
+ * the reference checkout.  Each function below restates the published
+ * ggml-cpu behaviour of one op (scalar code path, ISO C evaluation: no FMA
+ * contraction), in this library's own code, and names the reference call site
+ * whose semantics it fixes.
+ *
+ * Parity pins (tests/test_oracle_*.py): closed forms evaluated in float64,
+ * numpy's independent float16 conversion, exhaustive enumeration of all 65536
+ * f16 codes, invariants (LN of a constant row, rotation norm preservation,
+ * group-norm moments), brute force on tiny inputs, and committed golden
+ * vectors under tests/golden/.  Functions with no such pin are marked
+ * "parity unpinned" in their comment; none is at present.
+ *
+ * Tensors use ggml's layout: ne[0] is the innermost (contiguous) dimension,
+ * nb[] are byte strides.  Types use ggml_type numbering.
+ */
+#ifndef CBX_ORACLE_H
+#define CBX_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    CBXO_TYPE_F32  = 0,
+    CBXO_TYPE_F16  = 1,
+    CBXO_TYPE_Q8_0 = 8,
+    CBXO_TYPE_I32  = 26,
+};
+
+/* ggml_unary_op / ggml_glu_op subset used by the path. */
+enum {
+    CBXO_UNARY_GELU      = 0,  /* ggml_gelu      (t3.cpp:537)            */
+    CBXO_UNARY_GELU_ERF  = 1,  /* ggml_gelu_erf  (cfm_decoder.cpp:239)   */
+    CBXO_UNARY_SILU      = 2,  /* ggml_silu      (cfm_decoder.cpp:466)   */
+    CBXO_UNARY_TANH      = 3,  /* ggml_tanh      (cfm_decoder.cpp:37)    */
+    CBXO_UNARY_SOFTPLUS  = 4,  /* ggml_softplus  (cfm_decoder.cpp:37)    */
+    CBXO_UNARY_SIN       = 5,  /* ggml_sin       (hift_vocoder.cpp:69)   */
+    CBXO_UNARY_SQR       = 6,  /* ggml_sqr       (hift_vocoder.cpp:70)   */
+    CBXO_UNARY_MISH      = 7,  /* mish() helper  (cfm_decoder.cpp:36-38) */
+};
+
+typedef struct cbxo_tensor {
+    void*    data;
+    int32_t  type;
+    int32_t  reserved;
+    int64_t  ne[4];
+    size_t   nb[4];
+} cbxo_tensor;
+
+#define CBXO_QK8_0 32
+#define CBXO_Q8_0_BLOCK_BYTES 34   /* ggml block_q8_0: f16 d + int8 qs[32] */
+
+/* ---- scalar conversions ------------------------------------------------ */
+float    cbxo_fp16_to_fp32(uint16_t h);
+uint16_t cbxo_fp32_to_fp16(float f);   /* round to nearest even */
+
+/* ---- Q8_0 (ggml-quants reference rule) --------------------------------- */
+void cbxo_quantize_row_q8_0(const float* x, void* y, int64_t k);
+void cbxo_dequantize_row_q8_0(const void* x, float* y, int64_t k);
+
+/* ---- GELU fp16 table (ggml_cpu_init) ----------------------------------- */
+/* fma_variant = 0: ISO C evaluation of 0.5x(1+tanh(s x (1 + a x^2)));
+ * fma_variant = 1: the same with (a*x)*x + 1 contracted to one fmaf, which
+ * is what gcc/clang emit for ggml-cpu on FMA hardware at default flags.   */
+void  cbxo_gelu_table(uint16_t* out65536, int fma_variant);
+float cbxo_gelu_f32(float x, int fma_variant);
+
+/* ---- ops (return 0, or a negative value on invalid input) -------------- */
+int cbxo_get_rows(const cbxo_tensor* src, const cbxo_tensor* ids,
+                  cbxo_tensor* dst, int n_threads);
+int cbxo_add(const cbxo_tensor* a, const cbxo_tensor* b, cbxo_tensor* dst,
+             int n_threads);
+int cbxo_mul(const cbxo_tensor* a, const cbxo_tensor* b, cbxo_tensor* dst,
+             int n_threads);
+int cbxo_norm(const cbxo_tensor* x, float eps, cbxo_tensor* dst,
+              int n_threads);
+int cbxo_rms_norm(const cbxo_tensor* x, float eps, cbxo_tensor* dst,
+                  int n_threads);
+int cbxo_group_norm(const cbxo_tensor* x, int n_groups, float eps,
+                    cbxo_tensor* dst, int n_threads);
+int cbxo_unary(int op, const cbxo_tensor* x, cbxo_tensor* dst, int n_threads);
+int cbxo_leaky_relu(const cbxo_tensor* x, float slope, cbxo_tensor* dst,
+                    int n_threads);
+int cbxo_swiglu(const cbxo_tensor* g, const cbxo_tensor* u, cbxo_tensor* dst,
+                int n_threads);
+int cbxo_cpy(const cbxo_tensor* src, cbxo_tensor* dst, int n_threads);
+
+/* RoPE: the ggml_rope_ext argument list.  mode 0 = NORMAL, 2 = NEOX. */
+void cbxo_rope_yarn_corr_dims(int n_dims, int n_ctx_orig, float freq_base,
+                              float beta_fast, float beta_slow, float dims[2]);
+void cbxo_rope_cache_init(float theta_base, float freq_scale,
+                          const float* freq_factors, const float corr_dims[2],
+                          int64_t ne0, float ext_factor, float mscale,
+                          float* cache, float sin_sign, float theta_scale);
+int cbxo_rope_ext(const cbxo_tensor* x, const cbxo_tensor* pos,
+                  const float* freq_factors, int n_dims, int mode,
+                  int n_ctx_orig, float freq_base, float freq_scale,
+                  float ext_factor, float attn_factor, float beta_fast,
+                  float beta_slow, cbxo_tensor* dst, int n_threads);
+
+/* ---- compositions made by the reference's graph builders --------------- */
+/* layer_norm(): norm -> mul(w) -> add(b)  (cfm_decoder.cpp:29-33,
+ * t3.cpp:465-466); w and b may be NULL (plain ggml_norm then).           */
+int cbxo_layer_norm(const cbxo_tensor* x, const cbxo_tensor* w,
+                    const cbxo_tensor* b, float eps, cbxo_tensor* dst,
+                    int n_threads);
+/* rms_norm -> mul(g); f16 x/dst are computed in f32 and rounded once.    */
+int cbxo_rms_norm_mul(const cbxo_tensor* x, const cbxo_tensor* g, float eps,
+                      cbxo_tensor* dst, int n_threads);
+/* group_norm -> mul(w) -> add(b) -> optional mish.                       */
+int cbxo_group_norm_affine(const cbxo_tensor* x, int n_groups, float eps,
+                           const cbxo_tensor* w, const cbxo_tensor* b,
+                           int fuse_mish, cbxo_tensor* dst, int n_threads);
+/* snake(): x + sin^2(x*alpha) * alpha_inv (hift_vocoder.cpp:64-73).      */
+int cbxo_snake(const cbxo_tensor* x, const cbxo_tensor* alpha,
+               const cbxo_tensor* alpha_inv, cbxo_tensor* dst, int n_threads);
+/* get_rows(tok) + get_rows(pos) (t3.cpp:440-455).                        */
+int cbxo_get_rows_add(const cbxo_tensor* src, const cbxo_tensor* ids,
+                      const cbxo_tensor* src2, const cbxo_tensor* ids2,
+                      cbxo_tensor* dst, int n_threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
