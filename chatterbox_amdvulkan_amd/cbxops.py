@@ -149,6 +149,8 @@ def desc(t: torch.Tensor, ggml_type: Optional[int] = None) -> Tensor:
     d.data = t.data_ptr()
     es = t.element_size()
     shape = list(t.shape[::-1]) or [1]
+    if t.numel() == 0:
+        t = t.contiguous()
     strides = [s * es for s in t.stride()[::-1]] or [es]
     row_bytes = strides[-1] * shape[-1]
     if ggml_type == Q8_0:

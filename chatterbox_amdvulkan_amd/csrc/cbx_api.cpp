@@ -95,6 +95,7 @@ int validate(const cbx_tensor* t, const char* what, const char* name) {
     if (t->type == CBX_TYPE_Q8_0 && t->ne[0] % 32 != 0) {
         return set_error(CBX_ERR_INVALID_ARG, where + ": Q8_0 ne[0] must be a multiple of 32");
     }
+    if (nelements(t) == 0) return CBX_OK;   // nothing is read or written
     if (!rows_contiguous(t)) {
         return set_error(CBX_ERR_UNSUPPORTED, where + ": nb[0] must equal the element (block) size");
     }
