@@ -79,10 +79,21 @@ class PrefillSet:
         r = self.r
         return self.L.cbx_layer_norm(r["h"], r["ln_w"], r["ln_b"], 1e-5, -1, r["ln"], s)
 
+    def embed_layer_norm(self, s):
+        r = self.r
+        return self.L.cbx_get_rows_add_layer_norm(r["table"], r["ids"], r["pos_table"], r["pos_ids"], r["ln_w"],
+                                                  r["ln_b"], 1e-5, r["h"], r["ln"], s)
+
     def gelu(self, s):
         return self.L.cbx_gelu(self.r["ffn"], self.r["g"], s)
 
     def step(self, s):
+        """Fused chain: token+position gather with LayerNorm, then GELU."""
+        rc = self.embed_layer_norm(s) | self.gelu(s)
+        if rc:
+            raise self.C.CbxError(rc, self.C.last_error())
+
+    def step_unfused(self, s):
         rc = self.gather(s) | self.layer_norm(s) | self.gelu(s)
         if rc:
             raise self.C.CbxError(rc, self.C.last_error())
@@ -118,36 +129,44 @@ def time_graph_steps(torch, graphs_all, graphs_one, n_sets, steps):
 
 
 def per_launch_ms(torch, fns, reps):
-    """Mean duration of single launches, each bracketed by its own events on
-    the launch stream; launches rotate over `fns`."""
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    s = cur_stream(torch)
+    """Average duration of one launch of a kernel in a back-to-back stream of
+    its launches: one HIP graph holds a launch per buffer set (rotating
+    inputs); it is replayed until `reps` launches have run, with events on
+    the launch stream around the whole batch.  (An event pair around a
+    single launch adds several microseconds of its own.)"""
+    g = capture(torch, lambda s: [fn(s) for fn in fns])
+    n_rep = max(1, reps // len(fns))
+    g.replay()
     torch.cuda.synchronize()
-    for i in range(reps):
-        evs[i][0].record()
-        fns[i % len(fns)](s)
-        evs[i][1].record()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n_rep):
+        g.replay()
+    e1.record()
     torch.cuda.synchronize()
-    return float(np.mean([a.elapsed_time(b) for a, b in evs]))
+    ms = e0.elapsed_time(e1) / (n_rep * len(fns))
+    del g
+    return ms
 
 
 # --------------------------------------------------------------------------- #
 # workloads
 # --------------------------------------------------------------------------- #
 
-def bench_prefill(C, W, torch, steps, warmup, f16_table=False):
+def bench_prefill(C, W, torch, steps, warmup, f16_table=False, fused=True):
     inp = W.prefill_inputs(f16_table=False)
-    nbytes = W.prefill_bytes(f16_table)
+    nbytes = W.prefill_bytes(f16_table, fused)
     per_step = sum(nbytes.values())
     n_sets = max(2, math.ceil(MALL_DEFEAT_BYTES / per_step))
-    log(f"prefill{' f16' if f16_table else ''}: {per_step} B/step, {n_sets} buffer sets")
+    log(f"prefill{' f16' if f16_table else ''}{'' if fused else ' unfused'}: {per_step} B/step, {n_sets} buffer sets")
     sets = [PrefillSet(C, W, torch, inp, f16_table) for _ in range(n_sets)]
+    step = (lambda st: st.step) if fused else (lambda st: st.step_unfused)
 
     # eager pass + parity of set 0 against the oracle (the product path is the HIP library)
     from oracle import oracle as O
 
     for st in sets:
-        st.step(cur_stream(torch))
+        step(st)(cur_stream(torch))
     torch.cuda.synchronize()
     tab = inp["table"].astype(np.float16) if f16_table else inp["table"]
     h_ref = O.get_rows_add(tab, inp["ids"], inp["pos_table"], inp["pos_ids"], nth=8)
@@ -158,8 +177,8 @@ def bench_prefill(C, W, torch, steps, warmup, f16_table=False):
         if not np.array_equal(got.view(np.uint32), ref.view(np.uint32)):
             raise SystemExit(f"bench: {name} differs from the oracle")
 
-    g_all = capture(torch, lambda s: [st.step(s) for st in sets])
-    g_one = [capture(torch, st.step) for st in sets]
+    g_all = capture(torch, lambda s: [step(st)(s) for st in sets])
+    g_one = [capture(torch, step(st)) for st in sets]
     time_graph_steps(torch, g_all, g_one, n_sets, warmup)
     ms = time_graph_steps(torch, g_all, g_one, n_sets, steps)
     # replays must reproduce the eager result
@@ -168,11 +187,13 @@ def bench_prefill(C, W, torch, steps, warmup, f16_table=False):
         raise SystemExit("bench: graph replay result differs")
 
     reps = 400
-    k_ms = {
-        "gather_pos": per_launch_ms(torch, [st.gather for st in sets], reps),
-        "layer_norm": per_launch_ms(torch, [st.layer_norm for st in sets], reps),
-        "gelu": per_launch_ms(torch, [st.gelu for st in sets], reps),
-    }
+    if fused:
+        k_ms = {"embed_layer_norm": per_launch_ms(torch, [st.embed_layer_norm for st in sets], reps),
+                "gelu": per_launch_ms(torch, [st.gelu for st in sets], reps)}
+    else:
+        k_ms = {"gather_pos": per_launch_ms(torch, [st.gather for st in sets], reps),
+                "layer_norm": per_launch_ms(torch, [st.layer_norm for st in sets], reps),
+                "gelu": per_launch_ms(torch, [st.gelu for st in sets], reps)}
     del g_all, g_one, sets
     return {"ms_per_step": ms / steps, "bytes_per_step": per_step, "n_sets": n_sets,
             "kernel_ms": k_ms, "kernel_bytes": nbytes}
@@ -273,11 +294,15 @@ def main():
     torch.cuda.set_device(0)
     C.init(0)
     res = bench_prefill(C, W, torch, a.steps, a.warmup)
-    details = {"prefill_f32": {k: v for k, v in res.items()}}
+    details = {"prefill_f32_fused": {k: v for k, v in res.items()}}
     if not a.quick:
+        def gbps(r):
+            return r["bytes_per_step"] / (r["ms_per_step"] * 1e-3) / 1e9
+
+        ru = bench_prefill(C, W, torch, max(200, a.steps // 4), 20, fused=False)
+        details["prefill_f32_unfused"] = dict(ru, GBps=gbps(ru))
         r16 = bench_prefill(C, W, torch, max(200, a.steps // 4), 20, f16_table=True)
-        details["prefill_f16_table"] = {"ms_per_step": r16["ms_per_step"], "bytes_per_step": r16["bytes_per_step"],
-                                        "gather_pos_ms": r16["kernel_ms"]["gather_pos"]}
+        details["prefill_f16_table_fused"] = dict(r16, GBps=gbps(r16))
         details["t3_decode"] = bench_decode(C, W, torch)
         details["hift_snake_16x64x120000"] = bench_snake(C, W, torch)
     k_ms = res["kernel_ms"]["gelu"]
@@ -297,8 +322,10 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "t3_prefill_op_chain", "gather": "512 ids of [8194,1024] f32 + pos rows 0..511",
-                   "layer_norm": "[512,1024] eps 1e-5 affine", "gelu": "[512,4096] tanh (fp16 table)",
+        "config": {"workload": "t3_prefill_op_chain",
+                   "embed_layer_norm": "512 ids of [8194,1024] f32 + pos rows 0..511, then LayerNorm eps 1e-5 "
+                                       "affine, one kernel writing h and LN(h)",
+                   "gelu": "[512,4096] tanh (fp16-table semantics)",
                    "hbm_pct_of_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
                    "buffer_sets": res["n_sets"]},
         "roofline": {"bound": "hbm", "kernel": "gelu [512,4096] f32", "achieved": round(achieved, 2),

@@ -81,6 +81,7 @@ def load() -> ctypes.CDLL:
         "cbx_device_errors": (i, [i, ctypes.POINTER(ctypes.c_uint32), i]),
         "cbx_get_rows": (i, [P, P, P, vp]),
         "cbx_get_rows_add": (i, [P, P, P, P, P, vp]),
+        "cbx_get_rows_add_layer_norm": (i, [P, P, P, P, P, P, f, P, P, vp]),
         "cbx_cpy": (i, [P, P, vp]),
         "cbx_norm": (i, [P, f, P, vp]),
         "cbx_layer_norm": (i, [P, P, P, f, i, P, vp]),
@@ -205,6 +206,24 @@ def get_rows_add(table, ids, table2, ids2, out=None, q8_0=False, q8_0_2=False):
                                    _ref(desc(table2, Q8_0 if q8_0_2 else None)), _ref(desc(ids2)),
                                    _ref(desc(out)), _stream()))
     return out
+
+
+def get_rows_add_layer_norm(table, ids, table2, ids2, w, b, eps, h=None, out=None, q8_0=False, q8_0_2=False,
+                            store_h=True):
+    """T3 embedding + first LayerNorm in one pass; returns (h, y) (h None when
+    store_h is False and no h buffer is given)."""
+    _ready(table)
+    ne0 = table.shape[-1] // Q8_0_BLOCK * QK8_0 if q8_0 else table.shape[-1]
+    shape = tuple(ids.shape) + (ne0,)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.float32, device=table.device)
+    if h is None and store_h:
+        h = torch.empty(shape, dtype=torch.float32, device=table.device)
+    _check(load().cbx_get_rows_add_layer_norm(
+        _ref(desc(table, Q8_0 if q8_0 else None)), _ref(desc(ids)), _ref(desc(table2, Q8_0 if q8_0_2 else None)),
+        _ref(desc(ids2)), _ref(desc(w)) if w is not None else None, _ref(desc(b)) if b is not None else None, eps,
+        _ref(desc(h)) if h is not None else None, _ref(desc(out)), _stream()))
+    return h, out
 
 
 def cpy(src: torch.Tensor, out: torch.Tensor) -> torch.Tensor:

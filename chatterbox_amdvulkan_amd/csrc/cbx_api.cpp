@@ -288,6 +288,29 @@ int cbx_get_rows_add(const cbx_tensor* src, const cbx_tensor* ids, const cbx_ten
     return launch_get_rows(src, ids, src2, ids2, dst, st, reinterpret_cast<hipStream_t>(stream));
 }
 
+static int check_row_param(const cbx_tensor* p, const cbx_tensor* x, const char* what, const char* name);
+
+int cbx_get_rows_add_layer_norm(const cbx_tensor* src, const cbx_tensor* ids, const cbx_tensor* src2,
+                                const cbx_tensor* ids2, const cbx_tensor* w, const cbx_tensor* b, float eps,
+                                cbx_tensor* h, cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_get_rows_add_layer_norm";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = check_gather(what, src, ids, y)) || (rc = check_gather(what, src2, ids2, y))) return rc;
+    if (h) {
+        if ((rc = validate(h, what, "h"))) return rc;
+        if (h->type != CBX_TYPE_F32 || !same_shape(h, y)) {
+            return set_error(CBX_ERR_INVALID_ARG, "cbx_get_rows_add_layer_norm: h must be F32 with y's shape");
+        }
+    }
+    if (!(eps >= 0.0f)) return set_error(CBX_ERR_INVALID_ARG, "cbx_get_rows_add_layer_norm: eps must be >= 0");
+    if ((rc = check_row_param(w, y, what, "w")) || (rc = check_row_param(b, y, what, "b"))) return rc;
+    if (nelements(y) == 0) return CBX_OK;
+    return launch_embed_norm(src, ids, src2, ids2, w, b, eps, h, y, st, reinterpret_cast<hipStream_t>(stream));
+}
+
 int cbx_cpy(const cbx_tensor* src, cbx_tensor* dst, cbx_stream stream) {
     clear_error();
     int rc;

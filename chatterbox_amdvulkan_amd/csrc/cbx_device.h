@@ -63,6 +63,35 @@ template <> struct Elt<uint16_t> {   // fp16 storage
     static constexpr int size = 2;
 };
 
+// Streaming (nontemporal) 4-element loads/stores: data touched once is not
+// kept in the caches.
+typedef float cbx_f4v __attribute__((ext_vector_type(4)));
+typedef unsigned int cbx_u2v __attribute__((ext_vector_type(2)));
+
+template <typename T> struct Stream;
+template <> struct Stream<float> {
+    static __device__ __forceinline__ float4 load4(const char* p) {
+        const cbx_f4v t = __builtin_nontemporal_load(reinterpret_cast<const cbx_f4v*>(p));
+        return make_float4(t.x, t.y, t.z, t.w);
+    }
+    static __device__ __forceinline__ void store4(char* p, float4 v) {
+        const cbx_f4v t = {v.x, v.y, v.z, v.w};
+        __builtin_nontemporal_store(t, reinterpret_cast<cbx_f4v*>(p));
+    }
+};
+template <> struct Stream<uint16_t> {
+    static __device__ __forceinline__ float4 load4(const char* p) {
+        const cbx_u2v u = __builtin_nontemporal_load(reinterpret_cast<const cbx_u2v*>(p));
+        return make_float4(h2f(u.x & 0xffffu), h2f(u.x >> 16), h2f(u.y & 0xffffu), h2f(u.y >> 16));
+    }
+    static __device__ __forceinline__ void store4(char* p, float4 v) {
+        cbx_u2v u;
+        u.x = static_cast<uint32_t>(f2h(v.x)) | (static_cast<uint32_t>(f2h(v.y)) << 16);
+        u.y = static_cast<uint32_t>(f2h(v.z)) | (static_cast<uint32_t>(f2h(v.w)) << 16);
+        __builtin_nontemporal_store(u, reinterpret_cast<cbx_u2v*>(p));
+    }
+};
+
 __device__ __forceinline__ float get(const float4& v, int k) {
     return k == 0 ? v.x : (k == 1 ? v.y : (k == 2 ? v.z : v.w));
 }
@@ -71,10 +100,36 @@ __device__ __forceinline__ void set(float4& v, int k, float x) {
 }
 
 // ---- reductions ----------------------------------------------------------
+// DPP move of a double (two 32-bit halves) inside each 16-lane row.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const int lo = __builtin_amdgcn_mov_dpp(static_cast<int>(u & 0xffffffffu), CTRL, 0xf, 0xf, true);
+    const int hi = __builtin_amdgcn_mov_dpp(static_cast<int>(u >> 32), CTRL, 0xf, 0xf, true);
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                          static_cast<uint32_t>(lo));
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(u & 0xffffffffu), lane);
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(u >> 32), lane);
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Sum over the 64 lanes of a wave, identical in every lane: a butterfly
+// inside each 16-lane row with DPP (quad_perm [1,0,3,2], quad_perm
+// [2,3,0,1], row_half_mirror, row_mirror -- each pairs lanes so both
+// partners add the same two values), then the four row sums read from
+// lanes 0/16/32/48 and added in a fixed order.  All 64 lanes must be active.
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int off = WAVE / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
-    return v;
+    v += dpp_f64<0xB1>(v);
+    v += dpp_f64<0x4E>(v);
+    v += dpp_f64<0x141>(v);
+    v += dpp_f64<0x140>(v);
+    const double r0 = readlane_f64(v, 0), r1 = readlane_f64(v, 16);
+    const double r2 = readlane_f64(v, 32), r3 = readlane_f64(v, 48);
+    return (r0 + r1) + (r2 + r3);
 }
 
 // Sum over the block in a fixed order (lanes in a butterfly, waves in index
@@ -108,10 +163,60 @@ __device__ __forceinline__ float act_mish(float x) {
 __device__ __forceinline__ float act_gelu_erf(float x) {
     return 0.5f * x * (1.0f + erff(x * CBX_SQRT_2_INV));
 }
+// ggml_gelu (f32): x <= -10 -> 0, x >= 10 -> x, else the fp16 table entry
+// of h = f16(x) (the table cbx_init uploads).  This form reads the table
+// in global memory; the streaming GELU kernel stages it in LDS instead.
 __device__ __forceinline__ float act_gelu_tab(const uint16_t* __restrict__ tab, float x) {
     if (x <= -10.0f) return 0.0f;
     if (x >= 10.0f) return x;
     return h2f(tab[f2h(x)]);
+}
+
+// The same function without a gather per element.  For |x| < 10 the
+// result is a function of h = f16(x) alone; it is evaluated here with the
+// table's f32 formula but a fast tanh (1 - 2/(2^(2a log2 e) + 1) with the
+// hardware exp2 and reciprocal), and the f16 rounding of that value is kept
+// when it lies more than a margin of 32/(1 + t) + 8 ulps from an f16
+// rounding midpoint -- the fast tanh is within ~20 ulps of 1 of the exact
+// one, which moves g by at most ~20/(1 + t) ulps.  Otherwise (1 + t < 1/64,
+// f16-subnormal g, or too close to a midpoint) the exact table entry is
+// used; lanes that do not need it all read entry 0, so the load touches a
+// single cache line in the common case.  Because the result depends on h
+// only, running every f16 code through this function checks it for every
+// input.
+#define CBX_GELU_COEF_A 0.044715f
+#define CBX_SQRT_2_OVER_PI 0.79788456080286535587989211986876f
+
+__device__ __forceinline__ float act_gelu_fast(const uint16_t* __restrict__ tab, float x) {
+    const uint32_t h = f2h(x);
+    const float xf = h2f(static_cast<uint16_t>(h));
+    const float inner = 1.0f + CBX_GELU_COEF_A * xf * xf;
+    const float a = CBX_SQRT_2_OVER_PI * xf * inner;
+    const float e = __builtin_amdgcn_exp2f(a * 2.8853900817779268f);
+    const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+    const float opt = 1.0f + t;
+    const float g = 0.5f * xf * opt;
+    const uint32_t gb = __builtin_bit_cast(uint32_t, g) & 0x7fffffffu;
+    const float dist = __builtin_fabsf(static_cast<float>(static_cast<int32_t>(gb & 0x1fffu) - 0x1000));
+    // dist > 32/opt + 8  <=>  (dist - 8) * opt > 32   (opt > 0)
+    const bool sure = opt >= 0.015625f && gb >= 0x38800000u && (dist - 8.0f) * opt > 32.0f;
+    const uint16_t tv = tab[sure ? 0u : h];
+    float r = sure ? h2f(f2h(g)) : h2f(tv);
+    r = x <= -10.0f ? 0.0f : r;
+    return x >= 10.0f ? x : r;
+}
+
+// ---- row addressing --------------------------------------------------------
+// Byte offset of row r (rows enumerate ne[1], ne[2], ne[3] in that order).
+// `flat` means the row strides are uniform (nb2 = nb1*ne1, nb3 = nb2*ne2, or
+// the dimension is 1), so no division is needed; otherwise r is split.
+__device__ __forceinline__ int64_t row_offset(const View& t, int64_t r, bool flat) {
+    if (flat) return r * t.nb[1];
+    const int64_t i3 = r / (t.ne[2] * t.ne[1]);
+    const int64_t rem = r - i3 * t.ne[2] * t.ne[1];
+    const int64_t i2 = rem / t.ne[1];
+    const int64_t i1 = rem - i2 * t.ne[1];
+    return i1 * t.nb[1] + i2 * t.nb[2] + i3 * t.nb[3];
 }
 __device__ __forceinline__ float act_leaky(float x, float ns) {
     return ((x > 0.f) ? x : 0.f) + ns * ((x < 0.0f) ? x : 0.f);

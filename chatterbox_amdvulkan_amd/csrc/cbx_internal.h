@@ -27,6 +27,17 @@ inline View view_of(const cbx_tensor* t) {
     return v;
 }
 
+// Rows of t (ne[1..3]) sit at uniform byte steps of nb[1].
+// (Each dimension k >= 2 with ne[k] > 1 has nb[k] = nb[1] * ne[1] * ... * ne[k-1].)
+inline bool flat_rows(const cbx_tensor* t) {
+    size_t step = t->nb[1] * static_cast<size_t>(t->ne[1]);
+    for (int k = 2; k < 4; k++) {
+        if (t->ne[k] > 1 && t->nb[k] != step) return false;
+        step *= static_cast<size_t>(t->ne[k]);
+    }
+    return true;
+}
+
 inline View null_view() {
     View v;
     v.data = nullptr;
@@ -71,6 +82,9 @@ int launch_get_rows(const cbx_tensor* src, const cbx_tensor* ids, const cbx_tens
 int launch_cpy(const cbx_tensor* src, cbx_tensor* dst, DeviceState* st, hipStream_t s);
 int launch_row_norm(int kind, const cbx_tensor* x, const cbx_tensor* w, const cbx_tensor* b,
                     float eps, int act, cbx_tensor* y, DeviceState* st, hipStream_t s);
+int launch_embed_norm(const cbx_tensor* src, const cbx_tensor* ids, const cbx_tensor* src2, const cbx_tensor* ids2,
+                      const cbx_tensor* w, const cbx_tensor* b, float eps, cbx_tensor* h, cbx_tensor* y,
+                      DeviceState* st, hipStream_t s);
 int launch_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w,
                       const cbx_tensor* b, int act, cbx_tensor* y, DeviceState* st,
                       hipStream_t s);

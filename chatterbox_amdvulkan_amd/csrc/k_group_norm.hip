@@ -50,27 +50,40 @@ __global__ __launch_bounds__(kThreads) void k_group_norm(GnArgs a) {
     if (c0 >= c1) return;   // uniform across the workgroup
     const int64_t count = a.x.ne[0] * a.x.ne[1] * (c1 - c0);
 
+    // VEC: the group is one contiguous run of count floats (x and y), read
+    // with unconditional 16-byte loads (clamped addresses) so all NV are in
+    // flight together; per_ch floats per channel.
+    const char* xg = a.x.data + c0 * a.x.nb[2] + i3 * a.x.nb[3];
+    char* yg = a.y.data + c0 * a.y.nb[2] + i3 * a.y.nb[3];
+    const uint32_t per_ch = static_cast<uint32_t>(a.x.ne[0] * a.x.ne[1]);
     float4 v[NV];
-    int64_t off[NV], ch[NV];
+    int64_t ch[NV];
     double s = 0.0;
 #pragma unroll
     for (int k = 0; k < NV; k++) {
         const int64_t e = (threadIdx.x + static_cast<int64_t>(k) * blockDim.x) * 4;
-        if (e < count) {
-            off[k] = gn_offset(a.x, e, c0, i3, &ch[k]);
-            if constexpr (VEC) {
-                v[k] = *reinterpret_cast<const float4*>(a.x.data + off[k]);
-            } else {
+        if constexpr (VEC) {
+            v[k] = *reinterpret_cast<const float4*>(xg + 4 * (e < count ? e : 0));
+        } else {
+            if (e < count) {
                 for (int q = 0; q < 4; q++) {
                     int64_t chq;
                     const int64_t oq = gn_offset(a.x, e + q, c0, i3, &chq);
                     set(v[k], q, e + q < count ? *reinterpret_cast<const float*>(a.x.data + oq) : 0.0f);
                 }
+            } else {
+                v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t e = (threadIdx.x + static_cast<int64_t>(k) * blockDim.x) * 4;
+        if constexpr (VEC) {
+            if (e >= count) v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+            ch[k] = c0 + static_cast<uint32_t>(e < count ? e : 0) / per_ch;
         } else {
-            off[k] = 0;
             ch[k] = 0;
-            v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
         for (int q = 0; q < 4; q++) s += static_cast<double>(get(v[k], q));
@@ -111,8 +124,7 @@ __global__ __launch_bounds__(kThreads) void k_group_norm(GnArgs a) {
             set(o, q, t);
         }
         if constexpr (VEC) {
-            int64_t cy;
-            *reinterpret_cast<float4*>(a.y.data + gn_offset(a.y, e, c0, i3, &cy)) = o;
+            *reinterpret_cast<float4*>(yg + 4 * e) = o;
         } else {
             for (int q = 0; q < 4; q++) {
                 if (e + q < count) {
@@ -187,11 +199,14 @@ int launch_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_te
     a.eps = eps;
     a.act = act;
     a.tab = st->gelu_table;
-    // 4-wide vectors stay inside one ne[0] row when ne[0] % 4 == 0.
+    // VEC: every group is a contiguous run of floats (ne0, ne1 dense within a
+    // channel, channels adjacent), 16-byte aligned, ne0 % 4 == 0.
     bool vec = x->ne[0] % 4 == 0;
     for (const cbx_tensor* t : {x, static_cast<const cbx_tensor*>(y)}) {
-        if (reinterpret_cast<uintptr_t>(t->data) % 16) vec = false;
-        for (int i = 1; i < 4; i++) if (t->nb[i] % 16) vec = false;
+        const size_t row = 4 * static_cast<size_t>(t->ne[0]);
+        if (t->ne[1] > 1 && t->nb[1] != row) vec = false;
+        if (t->ne[2] > 1 && t->nb[2] != row * static_cast<size_t>(t->ne[1])) vec = false;
+        if (reinterpret_cast<uintptr_t>(t->data) % 16 || t->nb[2] % 16 || t->nb[3] % 16) vec = false;
     }
     const int64_t count = x->ne[0] * x->ne[1] * std::min<int64_t>(a.cpg, x->ne[2]);
     const int64_t need = cdiv(count, int64_t{kThreads} * 4);

@@ -1,20 +1,22 @@
 // k_norm.hip -- LayerNorm / RMSNorm over ne[0] with the affine multiply/add
 // and an optional activation fused into the same pass: one HBM read of x,
-// one write of y, per row.
+// one write of y, per row.  Also the T3 embedding chain: token row + learned
+// position row, then the first LayerNorm, in one pass.
 //
 // Arithmetic follows ggml-cpu exactly:
 //   LN : mean = (float)(sum_f64 x) / n;  v = x - mean;
 //        var = (float)(sum_f64 (v*v) / n);  y = v * (1/sqrtf(var + eps))
 //   RMS: ms = (float)(sum_f64 (x*x) / n);   y = x * (1/sqrtf(ms + eps))
 //   then y*w, then +b, each rounded to f32 (ggml_mul, ggml_add).
-// The f64 sums use a fixed butterfly + per-wave order rather than ggml's
-// sequential order; the f32 values derived from them agree unless an f64
-// sum falls within ~2^-29 relative of an f32 rounding boundary.
+// The f64 sums use a fixed butterfly order rather than ggml's sequential
+// order; the f32 values derived from them agree unless an f64 sum falls
+// within ~2^-29 relative of an f32 rounding boundary.
 //
-// One workgroup per row; each lane keeps its share of the row in registers
-// (NV 4-element vectors), so x is read from HBM once.  Rows longer than
-// 8 * 4 * 256 = 8192 elements use a three-pass loop instead.
-// x and y share one storage type (F32, or F16 with f32 arithmetic).
+// Rows of up to 4096 elements (ne0 % 4 == 0, 16-byte aligned) take one
+// wave per row: each lane holds NV 4-element vectors in registers and the
+// two reductions are wave-local (DPP), with no LDS or barrier.  Other rows
+// take one workgroup per row (LDS combine), and rows past 8192 elements a
+// three-pass loop.
 #include "cbx_device.h"
 
 namespace cbx {
@@ -22,18 +24,219 @@ namespace {
 
 constexpr int kMaxThreads = 256;
 
+// ---------------------------------------------------------------------------
+// wave-per-row building blocks
+// ---------------------------------------------------------------------------
+
+// Normalisation scale of the row held in v (lane owns elements
+// (lane + 64k)*4 .. +3); for LN, v is replaced by v - mean.
+template <int NV, int KIND>
+__device__ __forceinline__ float wave_row_scale(float4 (&v)[NV], int lane, int64_t ne0, float eps) {
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float t = get(v[k], e);
+            if constexpr (KIND == NORM_LN) s += static_cast<double>(t);
+            else s += static_cast<double>(t * t);
+        }
+    }
+    s = wave_sum(s);
+    if constexpr (KIND == NORM_LN) {
+        const float mean = static_cast<float>(s) / static_cast<float>(ne0);
+        double s2 = 0.0;
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            if ((lane + 64 * k) * 4 < ne0) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float d = get(v[k], e) - mean;
+                    set(v[k], e, d);
+                    s2 += static_cast<double>(d * d);
+                }
+            }
+        }
+        s2 = wave_sum(s2);
+        const float var = static_cast<float>(s2 / static_cast<double>(ne0));
+        return 1.0f / sqrtf(var + eps);
+    } else {
+        const float ms = static_cast<float>(s / static_cast<double>(ne0));
+        return 1.0f / sqrtf(ms + eps);
+    }
+}
+
+// Affine vectors for the lane's elements, loaded up front (uniform branches:
+// the loads overlap the row loads instead of stalling the epilogue).
+template <int NV>
+struct Affine {
+    float4 w[NV], b[NV];
+    __device__ __forceinline__ void load(const float* __restrict__ wp, const float* __restrict__ bp, int lane,
+                                         int64_t ne0) {
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int64_t j = (lane + 64 * k) * 4;
+            const int64_t jc = j < ne0 ? j : 0;
+            if (wp) w[k] = *reinterpret_cast<const float4*>(wp + jc);
+            if (bp) b[k] = *reinterpret_cast<const float4*>(bp + jc);
+        }
+    }
+};
+
+template <typename TO, int NV, bool ACT>
+__device__ __forceinline__ void wave_row_store(const float4 (&v)[NV], int lane, int64_t ne0, float scale,
+                                               const Affine<NV>& af, bool hw, bool hb, int act,
+                                               const uint16_t* __restrict__ tab, char* yr) {
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t j = (lane + 64 * k) * 4;
+        if (j < ne0) {
+            float4 o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float t = get(v[k], e) * scale;
+                if (hw) t = t * get(af.w[k], e);
+                if (hb) t = t + get(af.b[k], e);
+                if constexpr (ACT) t = apply_act(act, t, tab, 0.0f);
+                set(o, e, t);
+            }
+            Elt<TO>::store4(yr + j * Elt<TO>::size, o);
+        }
+    }
+}
+
+template <typename T, int NV, int KIND, bool ACT>
+__global__ __launch_bounds__(kMaxThreads) void k_row_norm_wave(View x, View y, const float* __restrict__ w,
+                                                                const float* __restrict__ b, float eps, int act,
+                                                                const uint16_t* __restrict__ tab, int64_t nr,
+                                                                bool fx, bool fy) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) +
+                      __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (r >= nr) return;   // uniform per wave
+    const int64_t ne0 = x.ne[0];
+    const char* xr = x.data + row_offset(x, r, fx);
+    char* yr = y.data + row_offset(y, r, fy);
+    // affine vectors first (L2-resident), then the row: loads are
+    // unconditional (clamped address), so all are in flight at once; lanes
+    // past the row end zero their values afterwards
+    Affine<NV> af;
+    af.load(w, b, lane, ne0);
+    float4 v[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t j = (lane + 64 * k) * 4;
+        v[k] = Elt<T>::load4(xr + (j < ne0 ? j : 0) * Elt<T>::size);
+    }
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        if ((lane + 64 * k) * 4 >= ne0) v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const float scale = wave_row_scale<NV, KIND>(v, lane, ne0, eps);
+    wave_row_store<T, NV, ACT>(v, lane, ne0, scale, af, w != nullptr, b != nullptr, act, tab, yr);
+}
+
+// ---------------------------------------------------------------------------
+// T3 embedding chain: h = f32(table[ids]) + f32(pos_table[pos_ids]) (one f32
+// add, t3.cpp:446-455), optionally stored, then y = LN(h)*w + b
+// (t3.cpp:465-466) -- one wave per token.
+// ---------------------------------------------------------------------------
+
+template <int TYPE>
+__device__ __forceinline__ float4 load_table4(const char* row, int64_t j) {
+    if constexpr (TYPE == CBX_TYPE_F32) {
+        return *reinterpret_cast<const float4*>(row + j * 4);
+    } else if constexpr (TYPE == CBX_TYPE_F16) {
+        return Elt<uint16_t>::load4(row + j * 2);
+    } else {
+        const char* blk = row + (j >> 5) * 34;
+        const float d = h2f(*reinterpret_cast<const uint16_t*>(blk));
+        const int8_t* q = reinterpret_cast<const int8_t*>(blk + 2 + (j & 31));
+        return make_float4(static_cast<float>(q[0]) * d, static_cast<float>(q[1]) * d,
+                           static_cast<float>(q[2]) * d, static_cast<float>(q[3]) * d);
+    }
+}
+
+struct EmbedArgs {
+    View src, ids, src2, ids2, h, y;
+    const float* w;
+    const float* b;
+    float eps;
+    int64_t n_tok;
+    uint32_t* err;
+};
+
+template <int TYPE, int TYPE2, int NV>
+__global__ __launch_bounds__(kMaxThreads) void k_embed_norm(EmbedArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) +
+                      __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (t >= a.n_tok) return;   // uniform per wave
+    const int64_t ne0 = a.y.ne[0];
+    int64_t i10 = t, i11 = 0, i12 = 0;
+    if (a.ids.ne[1] * a.ids.ne[2] > 1) {
+        const int64_t n10 = a.ids.ne[0], n11 = a.ids.ne[1];
+        i12 = t / (n11 * n10);
+        i11 = (t - i12 * n11 * n10) / n10;
+        i10 = t - i12 * n11 * n10 - i11 * n10;
+    }
+    const int32_t id = __builtin_amdgcn_readfirstlane(
+        *reinterpret_cast<const int32_t*>(a.ids.data + i10 * a.ids.nb[0] + i11 * a.ids.nb[1] + i12 * a.ids.nb[2]));
+    const int32_t id2 = __builtin_amdgcn_readfirstlane(
+        *reinterpret_cast<const int32_t*>(a.ids2.data + i10 * a.ids2.nb[0] + i11 * a.ids2.nb[1] + i12 * a.ids2.nb[2]));
+    char* yr = a.y.data + i10 * a.y.nb[1] + i11 * a.y.nb[2] + i12 * a.y.nb[3];
+    char* hr = a.h.data ? a.h.data + i10 * a.h.nb[1] + i11 * a.h.nb[2] + i12 * a.h.nb[3] : nullptr;
+    if (id < 0 || id >= a.src.ne[1] || id2 < 0 || id2 >= a.src2.ne[1]) {
+        // ggml aborts on an out-of-range index; here the outputs are zeroed
+        // and the sticky device error bit is raised.
+        for (int64_t j = lane; j < ne0; j += 64) {
+            reinterpret_cast<float*>(yr)[j] = 0.0f;
+            if (hr) reinterpret_cast<float*>(hr)[j] = 0.0f;
+        }
+        if (lane == 0) atomicOr(a.err, static_cast<uint32_t>(DEV_ERR_ROW_INDEX));
+        return;
+    }
+    const char* s1 = a.src.data + id * a.src.nb[1] + i11 * a.src.nb[2] + i12 * a.src.nb[3];
+    const char* s2 = a.src2.data + id2 * a.src2.nb[1] + i11 * a.src2.nb[2] + i12 * a.src2.nb[3];
+    Affine<NV> af;
+    af.load(a.w, a.b, lane, ne0);
+    float4 p[NV], q[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {   // unconditional loads, clamped addresses
+        const int64_t j = (lane + 64 * k) * 4;
+        p[k] = load_table4<TYPE>(s1, j < ne0 ? j : 0);
+        q[k] = load_table4<TYPE2>(s2, j < ne0 ? j : 0);
+    }
+    float4 v[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t j = (lane + 64 * k) * 4;
+        if (j < ne0) {
+            v[k] = make_float4(p[k].x + q[k].x, p[k].y + q[k].y, p[k].z + q[k].z, p[k].w + q[k].w);
+            if (hr) *reinterpret_cast<float4*>(hr + j * 4) = v[k];
+        } else {
+            v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    const float scale = wave_row_scale<NV, NORM_LN>(v, lane, ne0, a.eps);
+    wave_row_store<float, NV, false>(v, lane, ne0, scale, af, a.w != nullptr, a.b != nullptr, CBX_UNARY_NONE,
+                                     nullptr, yr);
+}
+
+// ---------------------------------------------------------------------------
+// workgroup-per-row fallback (ragged or unaligned rows, up to 8192 elements)
+// ---------------------------------------------------------------------------
+
 template <typename T, int NV, int KIND, bool ACT, bool VEC>
 __global__ __launch_bounds__(kMaxThreads) void k_row_norm(View x, View y, const float* __restrict__ w,
                                                            const float* __restrict__ b, float eps, int act,
-                                                           const uint16_t* __restrict__ tab, int64_t nr) {
+                                                           const uint16_t* __restrict__ tab, int64_t nr, bool fx,
+                                                           bool fy) {
     __shared__ double red[kMaxThreads / WAVE];
     const int64_t ne0 = x.ne[0];
     for (int64_t r = blockIdx.x; r < nr; r += gridDim.x) {
-        const int64_t i3 = r / (x.ne[2] * x.ne[1]);
-        const int64_t i2 = (r - i3 * x.ne[2] * x.ne[1]) / x.ne[1];
-        const int64_t i1 = r - i3 * x.ne[2] * x.ne[1] - i2 * x.ne[1];
-        const char* xr = x.data + i1 * x.nb[1] + i2 * x.nb[2] + i3 * x.nb[3];
-        char* yr = y.data + i1 * y.nb[1] + i2 * y.nb[2] + i3 * y.nb[3];
+        const char* xr = x.data + row_offset(x, r, fx);
+        char* yr = y.data + row_offset(y, r, fy);
 
         // element index of component e of vector k held by this lane
         auto idx = [&](int k, int e) -> int64_t {
@@ -47,7 +250,8 @@ __global__ __launch_bounds__(kMaxThreads) void k_row_norm(View x, View y, const 
         for (int k = 0; k < NV; k++) {
             if constexpr (VEC) {
                 const int64_t j = idx(k, 0);
-                v[k] = j < ne0 ? Elt<T>::load4(xr + j * Elt<T>::size) : make_float4(0.f, 0.f, 0.f, 0.f);
+                v[k] = Elt<T>::load4(xr + (j < ne0 ? j : 0) * Elt<T>::size);
+                if (j >= ne0) v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
@@ -117,15 +321,13 @@ __global__ __launch_bounds__(kMaxThreads) void k_row_norm(View x, View y, const 
 template <typename T, int KIND, bool ACT>
 __global__ __launch_bounds__(kMaxThreads) void k_row_norm_loop(View x, View y, const float* __restrict__ w,
                                                                 const float* __restrict__ b, float eps, int act,
-                                                                const uint16_t* __restrict__ tab, int64_t nr) {
+                                                                const uint16_t* __restrict__ tab, int64_t nr,
+                                                                bool fx, bool fy) {
     __shared__ double red[kMaxThreads / WAVE];
     const int64_t ne0 = x.ne[0];
     for (int64_t r = blockIdx.x; r < nr; r += gridDim.x) {
-        const int64_t i3 = r / (x.ne[2] * x.ne[1]);
-        const int64_t i2 = (r - i3 * x.ne[2] * x.ne[1]) / x.ne[1];
-        const int64_t i1 = r - i3 * x.ne[2] * x.ne[1] - i2 * x.ne[1];
-        const char* xr = x.data + i1 * x.nb[1] + i2 * x.nb[2] + i3 * x.nb[3];
-        char* yr = y.data + i1 * y.nb[1] + i2 * y.nb[2] + i3 * y.nb[3];
+        const char* xr = x.data + row_offset(x, r, fx);
+        char* yr = y.data + row_offset(y, r, fy);
         double s = 0.0;
         for (int64_t j = threadIdx.x; j < ne0; j += blockDim.x) {
             const float t = Elt<T>::load1(xr + j * Elt<T>::size);
@@ -158,6 +360,10 @@ __global__ __launch_bounds__(kMaxThreads) void k_row_norm_loop(View x, View y, c
     }
 }
 
+// ---------------------------------------------------------------------------
+// launch selection
+// ---------------------------------------------------------------------------
+
 struct NormLaunch {
     View x, y;
     const float* w;
@@ -166,16 +372,34 @@ struct NormLaunch {
     int act;
     const uint16_t* tab;
     int64_t nr;
+    bool fx, fy;
     dim3 grid, block;
     hipStream_t s;
 };
 
+template <typename T, int KIND, bool ACT>
+void go_wave(const NormLaunch& L, int nv) {
+#define CBX_WAVE_CASE(N)                                                                                     \
+    case N:                                                                                                 \
+        hipLaunchKernelGGL((k_row_norm_wave<T, N, KIND, ACT>), L.grid, L.block, 0, L.s, L.x, L.y, L.w, L.b, \
+                           L.eps, L.act, L.tab, L.nr, L.fx, L.fy);                                          \
+        break;
+    switch (nv) {
+        CBX_WAVE_CASE(1)
+        CBX_WAVE_CASE(2)
+        CBX_WAVE_CASE(4)
+        CBX_WAVE_CASE(8)
+        CBX_WAVE_CASE(16)
+    }
+#undef CBX_WAVE_CASE
+}
+
 template <typename T, int KIND, bool ACT, bool VEC>
-void go_nv(const NormLaunch& L, int nv) {
+void go_block(const NormLaunch& L, int nv) {
 #define CBX_NORM_CASE(N)                                                                                         \
     case N:                                                                                                     \
         hipLaunchKernelGGL((k_row_norm<T, N, KIND, ACT, VEC>), L.grid, L.block, 0, L.s, L.x, L.y, L.w, L.b,     \
-                           L.eps, L.act, L.tab, L.nr);                                                          \
+                           L.eps, L.act, L.tab, L.nr, L.fx, L.fy);                                              \
         break;
     switch (nv) {
         CBX_NORM_CASE(1)
@@ -184,20 +408,23 @@ void go_nv(const NormLaunch& L, int nv) {
         CBX_NORM_CASE(8)
         default:
             hipLaunchKernelGGL((k_row_norm_loop<T, KIND, ACT>), L.grid, L.block, 0, L.s, L.x, L.y, L.w, L.b, L.eps,
-                               L.act, L.tab, L.nr);
+                               L.act, L.tab, L.nr, L.fx, L.fy);
     }
 #undef CBX_NORM_CASE
 }
 
 template <typename T, int KIND>
-void go(const NormLaunch& L, int nv, bool vec) {
+void go(const NormLaunch& L, int nv, bool vec, bool wave) {
     const bool act = L.act != CBX_UNARY_NONE;
-    if (act) {
-        if (vec) go_nv<T, KIND, true, true>(L, nv);
-        else go_nv<T, KIND, true, false>(L, nv);
+    if (wave) {
+        if (act) go_wave<T, KIND, true>(L, nv);
+        else go_wave<T, KIND, false>(L, nv);
+    } else if (act) {
+        if (vec) go_block<T, KIND, true, true>(L, nv);
+        else go_block<T, KIND, true, false>(L, nv);
     } else {
-        if (vec) go_nv<T, KIND, false, true>(L, nv);
-        else go_nv<T, KIND, false, false>(L, nv);
+        if (vec) go_block<T, KIND, false, true>(L, nv);
+        else go_block<T, KIND, false, false>(L, nv);
     }
 }
 
@@ -206,6 +433,14 @@ bool rows_aligned(const cbx_tensor* t, size_t a) {
     for (int i = 1; i < 4; i++) if (t->nb[i] % a) return false;
     return true;
 }
+
+int pow2_nv(int64_t need) { return need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : need <= 16 ? 16 : 0; }
+
+// Waves per workgroup for wave-per-row kernels: small row counts get one
+// wave per workgroup so they spread over more CUs.
+int waves_per_block(int64_t rows, const DeviceState* st) { return rows >= int64_t{8} * st->n_cu ? 4 : 1; }
+
+constexpr int64_t kWaveMaxRow = 64 * 4 * 16;   // 4096 elements
 
 }  // namespace
 
@@ -216,10 +451,8 @@ int launch_row_norm(int kind, const cbx_tensor* x, const cbx_tensor* w, const cb
     const int64_t nr = nrows(x);
     const size_t a = x->type == CBX_TYPE_F32 ? 16 : 8;
     const bool vec = ne0 % 4 == 0 && rows_aligned(x, a) && rows_aligned(y, a);
-    const int64_t quads = cdiv(ne0, 4);
-    const int threads = static_cast<int>(std::min<int64_t>(kMaxThreads, std::max<int64_t>(WAVE, cdiv(quads, WAVE) * WAVE)));
-    const int64_t need = cdiv(quads, threads);
-    const int nv = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : 0;
+    const bool wave = vec && ne0 <= kWaveMaxRow && (!w || reinterpret_cast<uintptr_t>(w->data) % 16 == 0) &&
+                      (!b || reinterpret_cast<uintptr_t>(b->data) % 16 == 0);
     NormLaunch L;
     L.x = view_of(x);
     L.y = view_of(y);
@@ -229,17 +462,93 @@ int launch_row_norm(int kind, const cbx_tensor* x, const cbx_tensor* w, const cb
     L.act = act;
     L.tab = st->gelu_table;
     L.nr = nr;
-    L.grid = dim3(static_cast<unsigned>(std::min<int64_t>(nr, int64_t{1} << 20)));
-    L.block = dim3(threads);
+    L.fx = flat_rows(x);
+    L.fy = flat_rows(y);
     L.s = s;
-    if (x->type == CBX_TYPE_F32) {
-        if (kind == NORM_LN) go<float, NORM_LN>(L, nv, vec);
-        else go<float, NORM_RMS>(L, nv, vec);
+    int nv;
+    if (wave) {
+        nv = pow2_nv(cdiv(ne0, 256));
+        const int wpb = waves_per_block(nr, st);
+        L.block = dim3(64 * wpb);
+        L.grid = dim3(static_cast<unsigned>(cdiv(nr, wpb)));
+        if (cdiv(nr, wpb) > 0x7fffffff) return set_error(CBX_ERR_UNSUPPORTED, "norm: too many rows");
     } else {
-        if (kind == NORM_LN) go<uint16_t, NORM_LN>(L, nv, vec);
-        else go<uint16_t, NORM_RMS>(L, nv, vec);
+        const int64_t quads = cdiv(ne0, 4);
+        const int threads = static_cast<int>(std::min<int64_t>(kMaxThreads, std::max<int64_t>(WAVE, cdiv(quads, WAVE) * WAVE)));
+        nv = pow2_nv(cdiv(quads, threads));
+        if (nv == 16) nv = 0;   // past the block kernel's register budget
+        L.block = dim3(threads);
+        L.grid = dim3(static_cast<unsigned>(std::min<int64_t>(nr, int64_t{1} << 20)));
+    }
+    if (x->type == CBX_TYPE_F32) {
+        if (kind == NORM_LN) go<float, NORM_LN>(L, nv, vec, wave);
+        else go<float, NORM_RMS>(L, nv, vec, wave);
+    } else {
+        if (kind == NORM_LN) go<uint16_t, NORM_LN>(L, nv, vec, wave);
+        else go<uint16_t, NORM_RMS>(L, nv, vec, wave);
     }
     return check_launch(kind == NORM_LN ? "layer_norm" : "rms_norm");
+}
+
+namespace {
+
+template <int TYPE, int TYPE2>
+void embed_nv(const EmbedArgs& a, int nv, dim3 grid, dim3 block, hipStream_t s) {
+    switch (nv) {
+        case 1: hipLaunchKernelGGL((k_embed_norm<TYPE, TYPE2, 1>), grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL((k_embed_norm<TYPE, TYPE2, 2>), grid, block, 0, s, a); break;
+        case 4: hipLaunchKernelGGL((k_embed_norm<TYPE, TYPE2, 4>), grid, block, 0, s, a); break;
+        case 8: hipLaunchKernelGGL((k_embed_norm<TYPE, TYPE2, 8>), grid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL((k_embed_norm<TYPE, TYPE2, 16>), grid, block, 0, s, a); break;
+    }
+}
+
+template <int TYPE>
+void embed_t2(int t2, const EmbedArgs& a, int nv, dim3 grid, dim3 block, hipStream_t s) {
+    if (t2 == CBX_TYPE_F32) embed_nv<TYPE, CBX_TYPE_F32>(a, nv, grid, block, s);
+    else if (t2 == CBX_TYPE_F16) embed_nv<TYPE, CBX_TYPE_F16>(a, nv, grid, block, s);
+    else embed_nv<TYPE, CBX_TYPE_Q8_0>(a, nv, grid, block, s);
+}
+
+bool table_vec_ok(const cbx_tensor* t) {
+    if (t->type == CBX_TYPE_Q8_0) return true;
+    const size_t al = t->type == CBX_TYPE_F32 ? 16 : 8;
+    return rows_aligned(t, al);
+}
+
+}  // namespace
+
+int launch_embed_norm(const cbx_tensor* src, const cbx_tensor* ids, const cbx_tensor* src2, const cbx_tensor* ids2,
+                      const cbx_tensor* w, const cbx_tensor* b, float eps, cbx_tensor* h, cbx_tensor* y,
+                      DeviceState* st, hipStream_t s) {
+    const int64_t ne0 = y->ne[0];
+    if (ne0 % 4 != 0 || ne0 > kWaveMaxRow || !table_vec_ok(src) || !table_vec_ok(src2) || !rows_aligned(y, 16) ||
+        (h && !rows_aligned(h, 16)) || (w && reinterpret_cast<uintptr_t>(w->data) % 16) ||
+        (b && reinterpret_cast<uintptr_t>(b->data) % 16)) {
+        return set_error(CBX_ERR_UNSUPPORTED,
+                         "get_rows_add_layer_norm: needs ne0 % 4 == 0, ne0 <= 4096 and 16-byte aligned rows, w, b");
+    }
+    EmbedArgs a;
+    a.src = view_of(src);
+    a.ids = view_of(ids);
+    a.src2 = view_of(src2);
+    a.ids2 = view_of(ids2);
+    a.h = h ? view_of(h) : null_view();
+    a.y = view_of(y);
+    a.w = w ? static_cast<const float*>(w->data) : nullptr;
+    a.b = b ? static_cast<const float*>(b->data) : nullptr;
+    a.eps = eps;
+    a.n_tok = ids->ne[0] * ids->ne[1] * ids->ne[2];
+    a.err = st->err_word;
+    const int nv = pow2_nv(cdiv(ne0, 256));
+    const int wpb = waves_per_block(a.n_tok, st);
+    const dim3 block(64 * wpb), grid(static_cast<unsigned>(cdiv(a.n_tok, wpb)));
+    switch (src->type) {
+        case CBX_TYPE_F32: embed_t2<CBX_TYPE_F32>(src2->type, a, nv, grid, block, s); break;
+        case CBX_TYPE_F16: embed_t2<CBX_TYPE_F16>(src2->type, a, nv, grid, block, s); break;
+        default: embed_t2<CBX_TYPE_Q8_0>(src2->type, a, nv, grid, block, s); break;
+    }
+    return check_launch("get_rows_add_layer_norm");
 }
 
 }  // namespace cbx

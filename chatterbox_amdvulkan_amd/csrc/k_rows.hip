@@ -54,9 +54,12 @@ __global__ __launch_bounds__(256) void k_get_rows(View src, View ids, View src2,
     const int64_t ne0 = dst.ne[0];
     const int64_t n10 = ids.ne[0], n11 = ids.ne[1];
     for (int64_t r = blockIdx.x; r < n_out_rows; r += gridDim.x) {
-        const int64_t i12 = r / (n11 * n10);
-        const int64_t i11 = (r - i12 * n11 * n10) / n10;
-        const int64_t i10 = r - i12 * n11 * n10 - i11 * n10;
+        int64_t i10 = r, i11 = 0, i12 = 0;
+        if (ids.ne[1] * ids.ne[2] > 1) {
+            i12 = r / (n11 * n10);
+            i11 = (r - i12 * n11 * n10) / n10;
+            i10 = r - i12 * n11 * n10 - i11 * n10;
+        }
         const int32_t id = *reinterpret_cast<const int32_t*>(ids.data + i10 * ids.nb[0] + i11 * ids.nb[1] + i12 * ids.nb[2]);
         bool ok = id >= 0 && id < src.ne[1];
         int32_t id2 = 0;
@@ -130,26 +133,20 @@ int launch_gather_t1(int type2, bool vec, dim3 grid, dim3 block, hipStream_t s, 
 
 template <typename TS, typename TD>
 __global__ __launch_bounds__(256) void k_cpy_flat(const char* __restrict__ x, char* __restrict__ y, int64_t n) {
-    const int64_t n4 = n / 4;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride) {
-        Elt<TD>::store4(y + i * 4 * Elt<TD>::size, Elt<TS>::load4(x + i * 4 * Elt<TS>::size));
-    }
-    if (blockIdx.x == 0) {
-        for (int64_t i = n4 * 4 + threadIdx.x; i < n; i += blockDim.x) {
-            Elt<TD>::store1(y + i * Elt<TD>::size, Elt<TS>::load1(x + i * Elt<TS>::size));
-        }
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t n4 = n >> 2;
+    if (i < n4) {
+        Stream<TD>::store4(y + i * 4 * Elt<TD>::size, Stream<TS>::load4(x + i * 4 * Elt<TS>::size));
+    } else if (i == n4) {
+        for (int64_t j = n4 * 4; j < n; j++) Elt<TD>::store1(y + j * Elt<TD>::size, Elt<TS>::load1(x + j * Elt<TS>::size));
     }
 }
 
 template <typename TS, typename TD>
-__global__ __launch_bounds__(256) void k_cpy_rows(View x, View y, int64_t nr) {
+__global__ __launch_bounds__(256) void k_cpy_rows(View x, View y, int64_t nr, bool fx, bool fy) {
     for (int64_t r = blockIdx.x; r < nr; r += gridDim.x) {
-        const int64_t i3 = r / (x.ne[2] * x.ne[1]);
-        const int64_t i2 = (r - i3 * x.ne[2] * x.ne[1]) / x.ne[1];
-        const int64_t i1 = r - i3 * x.ne[2] * x.ne[1] - i2 * x.ne[1];
-        const char* xr = x.data + i1 * x.nb[1] + i2 * x.nb[2] + i3 * x.nb[3];
-        char* yr = y.data + i1 * y.nb[1] + i2 * y.nb[2] + i3 * y.nb[3];
+        const char* xr = x.data + row_offset(x, r, fx);
+        char* yr = y.data + row_offset(y, r, fy);
         for (int64_t j = threadIdx.x; j < x.ne[0]; j += blockDim.x) {
             Elt<TD>::store1(yr + j * Elt<TD>::size, Elt<TS>::load1(xr + j * Elt<TS>::size));
         }
@@ -159,15 +156,17 @@ __global__ __launch_bounds__(256) void k_cpy_rows(View x, View y, int64_t nr) {
 template <typename TS, typename TD>
 int launch_cpy_t(const cbx_tensor* src, cbx_tensor* dst, DeviceState* st, hipStream_t s) {
     const int64_t n = nelements(src);
-    const bool flat = is_contiguous(src) && is_contiguous(dst) && aligned16(src->data) && aligned16(dst->data);
+    const bool flat = is_contiguous(src) && is_contiguous(dst) && aligned16(src->data) && aligned16(dst->data) &&
+                      (n >> 2) + 1 < (int64_t{1} << 39);
     if (flat) {
-        const int64_t blocks = std::min<int64_t>(std::max<int64_t>(1, cdiv(n / 4, 256)), int64_t{st->n_cu} * 16);
-        hipLaunchKernelGGL((k_cpy_flat<TS, TD>), dim3(blocks), dim3(256), 0, s,
+        const int64_t blocks = cdiv((n >> 2) + 1, 256);
+        hipLaunchKernelGGL((k_cpy_flat<TS, TD>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s,
                            static_cast<const char*>(src->data), static_cast<char*>(dst->data), n);
     } else {
         const int64_t nr = nrows(src);
         const int64_t blocks = std::min<int64_t>(nr, int64_t{1} << 20);
-        hipLaunchKernelGGL((k_cpy_rows<TS, TD>), dim3(blocks), dim3(256), 0, s, view_of(src), view_of(dst), nr);
+        hipLaunchKernelGGL((k_cpy_rows<TS, TD>), dim3(blocks), dim3(256), 0, s, view_of(src), view_of(dst), nr,
+                           flat_rows(src), flat_rows(dst));
     }
     return check_launch("cpy");
 }

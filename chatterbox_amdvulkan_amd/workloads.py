@@ -95,11 +95,17 @@ def prefill_inputs(f16_table: bool = False) -> dict:
     }
 
 
-def prefill_bytes(f16_table: bool = False) -> dict:
-    """Algorithmic bytes: each input read once, each output written once."""
+def prefill_bytes(f16_table: bool = False, fused: bool = True) -> dict:
+    """Algorithmic bytes of one prefill step: each input read once, each
+    output written once.  fused: token+position gather and LayerNorm are one
+    kernel that writes both h (the residual stream) and LN(h); unfused: the
+    gather writes h and the LayerNorm reads it back."""
     es = 2 if f16_table else 4
     row = D_MODEL * es
-    gather = N_PREFILL * (row + 4 * D_MODEL) + N_PREFILL * 4 * 2 + N_PREFILL * 4 * D_MODEL
-    ln = 2 * N_PREFILL * D_MODEL * 4 + 2 * D_MODEL * 4
+    rows_in = N_PREFILL * (row + 4 * D_MODEL) + N_PREFILL * 4 * 2      # table + pos rows, both id vectors
+    act = N_PREFILL * D_MODEL * 4                                        # one [512,1024] f32 tensor
+    affine = 2 * D_MODEL * 4
     gelu = 2 * N_PREFILL * D_FF * 4
-    return {"gather_pos": gather, "layer_norm": ln, "gelu": gelu}
+    if fused:
+        return {"embed_layer_norm": rows_in + affine + 2 * act, "gelu": gelu}
+    return {"gather_pos": rows_in + act, "layer_norm": 2 * act + affine, "gelu": gelu}

@@ -100,6 +100,17 @@ int cbx_get_rows_add(const cbx_tensor* src, const cbx_tensor* ids,
                      const cbx_tensor* src2, const cbx_tensor* ids2,
                      cbx_tensor* dst, cbx_stream stream);
 
+/* The T3 input embedding and the first LayerNorm it feeds, in one pass:
+ * h = ggml_add(get_rows(src, ids), get_rows(src2, ids2)) (t3.cpp:446-455),
+ * y = layer_norm(h, w, b, eps) (t3.cpp:465-466).  h (F32, y's shape) is
+ * stored when non-NULL -- it is the residual stream.  Needs ne0 % 4 == 0,
+ * ne0 <= 4096 and 16-byte aligned rows.                                    */
+int cbx_get_rows_add_layer_norm(const cbx_tensor* src, const cbx_tensor* ids,
+                                const cbx_tensor* src2, const cbx_tensor* ids2,
+                                const cbx_tensor* w, const cbx_tensor* b,
+                                float eps, cbx_tensor* h, cbx_tensor* y,
+                                cbx_stream stream);
+
 /* ggml_cpy / ggml_cast between F32 and F16 (round to nearest even), same
  * shape (t3.cpp:441,447,454).                                              */
 int cbx_cpy(const cbx_tensor* src, cbx_tensor* dst, cbx_stream stream);

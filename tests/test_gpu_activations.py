@@ -40,6 +40,20 @@ def test_gelu_all_codes_and_edges(cbx, oracle):
     assert_bitexact(host(cbx.gelu(dev(x))), oracle.unary(oracle.GELU, x), "gelu f32 edges")
 
 
+def test_gelu_lds_path_all_codes(cbx, oracle):
+    """Tensors of >= 2^18 elements take the LDS-staged table: every f16 code
+    as an f32 input, shuffled, plus the clamps, in a ragged length."""
+    codes = np.arange(65536, dtype=np.uint16).view(np.float16).astype(np.float32)
+    codes = codes[~np.isnan(codes)]
+    rng = np.random.default_rng(7)
+    x = np.concatenate([rng.permutation(np.tile(codes, 5)),
+                        np.array([-10.0, 10.0, np.nextafter(-10, 0), np.nextafter(10, 0), 9.9995, -9.9995, np.nan],
+                                 dtype=np.float32),
+                        W.normal(57, (1003,), 0.0, 6.0)])
+    got = host(cbx.gelu(dev(x)))
+    assert_bitexact(got, oracle.unary(oracle.GELU, x, nth=8), "gelu lds path")
+
+
 OPS = ["GELU_ERF", "SILU", "TANH", "SOFTPLUS", "SIN", "MISH"]
 
 

@@ -103,6 +103,29 @@ def test_layer_norm_f16_storage(cbx, oracle):
     assert_bitexact(got, oracle.layer_norm(x, w, b, 1e-5), "ln f16")
 
 
+@pytest.mark.parametrize("table", ["f32", "f16", "q8_0"])
+def test_embed_then_layer_norm_fused(cbx, oracle, table):
+    """T3 prefill: token + position rows, then LN-1 of layer 0, in one kernel;
+    h (the residual stream) and y both bit-exact vs the unfused oracle chain."""
+    inp = W.prefill_inputs()
+    tab = inp["table"]
+    q8 = table == "q8_0"
+    if table == "f16":
+        tab = tab.astype(np.float16)
+    elif q8:
+        tab = oracle.quantize_q8_0(tab)
+    h_ref = oracle.get_rows_add(tab, inp["ids"], inp["pos_table"], inp["pos_ids"], q8_0=q8, nth=8)
+    y_ref = oracle.layer_norm(h_ref, inp["ln_w"], inp["ln_b"], 1e-5, nth=8)
+    h, y = cbx.get_rows_add_layer_norm(dev(tab), dev(inp["ids"]), dev(inp["pos_table"]), dev(inp["pos_ids"]),
+                                       dev(inp["ln_w"]), dev(inp["ln_b"]), 1e-5, q8_0=q8)
+    assert_bitexact(host(h), h_ref, "h")
+    assert_bitexact(host(y), y_ref, "y")
+    _, y2 = cbx.get_rows_add_layer_norm(dev(tab), dev(inp["ids"][:7]), dev(inp["pos_table"]),
+                                        dev(inp["pos_ids"][:7]), dev(inp["ln_w"]), None, 1e-5, q8_0=q8,
+                                        store_h=False)
+    assert_bitexact(host(y2), oracle.layer_norm(h_ref[:7], inp["ln_w"], None, 1e-5), "no h, no bias")
+
+
 def test_norm_rejects_bad_args(cbx):
     x = dev(W.normal(34, (4, 64)))
     with pytest.raises(cbx.CbxError):
