@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="skip the secondary workloads")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only run the launches used by the FETCH_SIZE/WRITE_SIZE counter runs")
     return ap.parse_args()
 
 
@@ -257,6 +259,51 @@ def bench_snake(C, W, torch):
     return {"ms": ms, "bytes": nbytes, "GBps": nbytes / ms / 1e6}
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gelu_512x4096_and_embed_ln_traffic.md")
+
+
+def recorded_traffic(key):
+    """HBM bytes per launch of a kernel as last measured with rocprofv3 --pmc
+    FETCH_SIZE and WRITE_SIZE (copy-calibrated), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith(f"traffic_bytes_per_launch {key}:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def traffic_probe(C, W, torch):
+    """A few launches for counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE):
+    a plain f32 copy of 64 MiB (the calibration kernel of known size), then
+    GELU [512,4096] and the fused embedding + LayerNorm on rotating buffer
+    sets.  Prints the expected bytes of each."""
+    x = torch.empty(16 << 20, dtype=torch.float32, device="cuda").uniform_()
+    ys = [torch.empty_like(x) for _ in range(4)]
+    L = C.load()
+    s = cur_stream(torch)
+    dx = C.ctypes.byref(C.desc(x))
+    for y in ys:
+        rc = L.cbx_cpy(dx, C.ctypes.byref(C.desc(y)), s)
+        if rc:
+            raise C.CbxError(rc, C.last_error())
+    torch.cuda.synchronize()
+    inp = W.prefill_inputs()
+    sets = [PrefillSet(C, W, torch, inp) for _ in range(8)]
+    for st in sets:
+        st.gelu(s)
+    torch.cuda.synchronize()
+    for st in sets:
+        st.embed_layer_norm(s)
+    torch.cuda.synchronize()
+    nb = W.prefill_bytes()
+    print(json.dumps({"copy_bytes_read": x.numel() * 4, "copy_bytes_written": x.numel() * 4,
+                      "gelu_bytes_read": nb["gelu"] // 2, "gelu_bytes_written": nb["gelu"] // 2,
+                      "embed_layer_norm_bytes": nb["embed_layer_norm"]}), flush=True)
+
+
 def cpu_baseline(W, seconds):
     """The oracle runs the same prefill chain on the host cores."""
     from oracle import oracle as O
@@ -293,6 +340,9 @@ def main():
 
     torch.cuda.set_device(0)
     C.init(0)
+    if a.traffic_probe:
+        traffic_probe(C, W, torch)
+        return 0
     res = bench_prefill(C, W, torch, a.steps, a.warmup)
     details = {"prefill_f32_fused": {k: v for k, v in res.items()}}
     if not a.quick:
@@ -330,7 +380,9 @@ def main():
                    "buffer_sets": res["n_sets"]},
         "roofline": {"bound": "hbm", "kernel": "gelu [512,4096] f32", "achieved": round(achieved, 2),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                     "traffic": None, "launch_ms": k_ms, "algorithmic_bytes": k_bytes},
+                     "traffic": recorded_traffic("gelu_512x4096"),
+                     "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT),
+                     "launch_ms": k_ms, "algorithmic_bytes": k_bytes},
     }
     if "t3_decode" in details:
         out["t3_decode_us_per_step_chain"] = round(details["t3_decode"]["us_per_step_chain"], 3)
