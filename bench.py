@@ -100,6 +100,19 @@ class PrefillSet:
         if rc:
             raise self.C.CbxError(rc, self.C.last_error())
 
+    def step_one_launch(self, s):
+        """The same two ops as one cbx_run_ops launch (their inputs are
+        independent in this synthetic chain)."""
+        if not hasattr(self, "batch"):
+            C, t = self.C, self.t
+            self.batch = C.OpBatch([
+                C.Op(C.OP_GET_ROWS_ADD_LAYER_NORM, [t["table"], t["ids"], t["pos_table"], t["pos_ids"], t["ln_w"],
+                                                    t["ln_b"]], [t["h"], t["ln"]], eps=1e-5),
+                C.Op(C.OP_UNARY, [t["ffn"]], [t["g"]], act=C.GELU)])
+        rc = self.L.cbx_run_ops(self.batch.arr, self.batch.n, s)
+        if rc:
+            raise self.C.CbxError(rc, self.C.last_error())
+
 
 def cur_stream(torch):
     import ctypes
@@ -155,41 +168,46 @@ def per_launch_ms(torch, fns, reps):
 # workloads
 # --------------------------------------------------------------------------- #
 
-def bench_prefill(C, W, torch, steps, warmup, f16_table=False, fused=True):
+def same_bits(a, b):
+    return np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8))
+
+
+def bench_prefill(C, W, torch, steps, warmup, f16_table=False, fused=True, one_launch=False):
     inp = W.prefill_inputs(f16_table=False)
     nbytes = W.prefill_bytes(f16_table, fused)
     per_step = sum(nbytes.values())
     n_sets = max(2, math.ceil(MALL_DEFEAT_BYTES / per_step))
-    log(f"prefill{' f16' if f16_table else ''}{'' if fused else ' unfused'}: {per_step} B/step, {n_sets} buffer sets")
+    log(f"prefill{' f16' if f16_table else ''}{'' if fused else ' unfused'}{' one-launch' if one_launch else ''}: "
+        f"{per_step} B/step, {n_sets} buffer sets")
     sets = [PrefillSet(C, W, torch, inp, f16_table) for _ in range(n_sets)]
-    step = (lambda st: st.step) if fused else (lambda st: st.step_unfused)
+    if one_launch:
+        step = lambda st: st.step_one_launch  # noqa: E731
+    else:
+        step = (lambda st: st.step) if fused else (lambda st: st.step_unfused)
 
-    # eager pass + parity of set 0 against the oracle (the product path is the HIP library)
-    from oracle import oracle as O
-
+    # eager pass; the graph replays below must reproduce its results bit for
+    # bit (parity with the CPU restatement is the test suite's job)
     for st in sets:
         step(st)(cur_stream(torch))
     torch.cuda.synchronize()
-    tab = inp["table"].astype(np.float16) if f16_table else inp["table"]
-    h_ref = O.get_rows_add(tab, inp["ids"], inp["pos_table"], inp["pos_ids"], nth=8)
-    ln_ref = O.layer_norm(h_ref, inp["ln_w"], inp["ln_b"], 1e-5, nth=8)
-    g_ref = O.unary(O.GELU, inp["ffn"], nth=8)
-    for name, ref in (("h", h_ref), ("ln", ln_ref), ("g", g_ref)):
-        got = sets[-1].t[name].cpu().numpy()
-        if not np.array_equal(got.view(np.uint32), ref.view(np.uint32)):
-            raise SystemExit(f"bench: {name} differs from the oracle")
+    eager = {k: sets[0].t[k].cpu().numpy() for k in ("h", "ln", "g")}
+    for st in sets:
+        for k in ("h", "ln", "g"):
+            st.t[k].zero_()
 
     g_all = capture(torch, lambda s: [step(st)(s) for st in sets])
     g_one = [capture(torch, step(st)) for st in sets]
     time_graph_steps(torch, g_all, g_one, n_sets, warmup)
     ms = time_graph_steps(torch, g_all, g_one, n_sets, steps)
-    # replays must reproduce the eager result
     torch.cuda.synchronize()
-    if not np.array_equal(sets[0].t["g"].cpu().numpy().view(np.uint32), g_ref.view(np.uint32)):
-        raise SystemExit("bench: graph replay result differs")
+    for k, v in eager.items():
+        if not same_bits(sets[0].t[k].cpu().numpy(), v):
+            raise SystemExit(f"bench: graph replay result {k} differs from the eager launch")
 
     reps = 400
-    if fused:
+    if one_launch:
+        k_ms = {"run_ops": per_launch_ms(torch, [st.step_one_launch for st in sets], reps)}
+    elif fused:
         k_ms = {"embed_layer_norm": per_launch_ms(torch, [st.embed_layer_norm for st in sets], reps),
                 "gelu": per_launch_ms(torch, [st.gelu for st in sets], reps)}
     else:
@@ -201,35 +219,14 @@ def bench_prefill(C, W, torch, steps, warmup, f16_table=False, fused=True):
             "kernel_ms": k_ms, "kernel_bytes": nbytes}
 
 
-def bench_decode(C, W, torch, reps=200):
-    """T3 decode step: RMSNorm+gamma [1,1024], RoPE q,k [1,16,64] at positions
-    0..29, SiLU(gate)*up [1,4096]; 30 steps captured as one graph."""
-    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
-    L = C.load()
-    cache = C.RopeCache(64, mode=2, n_ctx_orig=2048, n_pos=2048)
-    steps = []
-    for s in range(30):
-        t = {"x": d(W.normal(W.seed_of(1, 0) + s, (1, 1024))), "g": d(W.normal(W.seed_of(1, 1), (1024,), 1.0, 0.02)),
-             "q": d(W.normal(W.seed_of(1, 2) + 97 * s, (1, 16, 64))),
-             "k": d(W.normal(W.seed_of(1, 3) + 97 * s, (1, 16, 64))),
-             "pos": d(np.array([s], dtype=np.int32)),
-             "gate": d(W.normal(W.seed_of(1, 5) + s, (1, 4096))), "up": d(W.normal(W.seed_of(1, 6) + s, (1, 4096)))}
-        t["y"] = torch.empty_like(t["x"])
-        t["qo"], t["ko"], t["h"] = torch.empty_like(t["q"]), torch.empty_like(t["k"]), torch.empty_like(t["gate"])
-        r = {k: C.ctypes.byref(C.desc(v)) for k, v in t.items()}
-        steps.append((t, r))
+def dev_of(torch):
+    return lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
-    def run(s):
-        for _, r in steps:
-            rc = (L.cbx_rms_norm_mul(r["x"], r["g"], 1e-5, r["y"], s) |
-                  L.cbx_rope_ext(r["q"], r["pos"], cache.handle, r["qo"], s) |
-                  L.cbx_rope_ext(r["k"], r["pos"], cache.handle, r["ko"], s) |
-                  L.cbx_swiglu(r["gate"], r["up"], r["h"], s))
-            if rc:
-                raise C.CbxError(rc, C.last_error())
 
-    run(cur_stream(torch))
-    g = capture(torch, run)
+def time_steps_us(torch, fn, n_steps, reps=200):
+    """Microseconds per step of fn(stream) (which runs n_steps steps),
+    captured once as a HIP graph and replayed `reps` times."""
+    g = capture(torch, fn)
     for _ in range(10):
         g.replay()
     torch.cuda.synchronize()
@@ -239,24 +236,253 @@ def bench_decode(C, W, torch, reps=200):
         g.replay()
     e1.record()
     torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / (reps * 30)
-    cache.close()
-    return {"us_per_step_chain": us, "bytes_per_step": 77824 + 4}
+    us = e0.elapsed_time(e1) * 1000.0 / (reps * n_steps)
+    del g
+    return us
 
 
-def bench_snake(C, W, torch):
-    """HiFT Snake on [16,64,120000] (ggml (C=64, T) channel innermost): 983 MB."""
-    x = torch.empty((16, 120000, 64), dtype=torch.float32, device="cuda").normal_()
-    y = torch.empty_like(x)
-    a = torch.empty(64, device="cuda").uniform_(0.5, 1.5)
-    ai = 1.0 / (a + 1e-9)
+def check_rc(C, rc):
+    if rc:
+        raise C.CbxError(rc, C.last_error())
+
+
+def bench_decode(C, W, torch):
+    """T3 decode step (f32): RMSNorm+gamma [1,1024], RoPE q,k [1,16,64] at
+    positions 0..29, SiLU(gate)*up [1,4096]; the 30 steps run from one HIP
+    graph.  Three launch plans: one kernel per op (4 per step); q and k
+    rotated by one launch (3 per step: the ops a real step can merge, since
+    q and k come out of the same projection); all four in one launch."""
+    d = dev_of(torch)
     L = C.load()
-    r = [C.ctypes.byref(C.desc(v)) for v in (x, a, ai, y)]
-    fn = lambda s: L.cbx_snake(r[0], r[1], r[2], r[3], s)  # noqa: E731
-    fn(cur_stream(torch))
-    ms = per_launch_ms(torch, [fn], 20)
-    nbytes = 2 * x.numel() * 4 + 2 * 64 * 4
-    return {"ms": ms, "bytes": nbytes, "GBps": nbytes / ms / 1e6}
+    cache = C.RopeCache(W.HEAD_DIM, mode=2, n_ctx_orig=2048, n_pos=2048)
+    steps = []
+    for s in range(W.DECODE_STEPS):
+        t = {k: d(v) for k, v in W.decode_inputs(s).items()}
+        t["y"] = torch.empty_like(t["x"])
+        t["qo"], t["ko"], t["h"] = torch.empty_like(t["q"]), torch.empty_like(t["k"]), torch.empty_like(t["gate"])
+        r = {k: C.ctypes.byref(C.desc(v)) for k, v in t.items()}
+        qk = C.OpBatch([C.Op(C.OP_ROPE, [t["q"], t["pos"]], [t["qo"]], rope=cache),
+                        C.Op(C.OP_ROPE, [t["k"], t["pos"]], [t["ko"]], rope=cache)])
+        one = C.OpBatch([C.Op(C.OP_RMS_NORM, [t["x"], t["g"]], [t["y"]], eps=1e-5),
+                         C.Op(C.OP_ROPE, [t["q"], t["pos"]], [t["qo"]], rope=cache),
+                         C.Op(C.OP_ROPE, [t["k"], t["pos"]], [t["ko"]], rope=cache),
+                         C.Op(C.OP_SWIGLU, [t["gate"], t["up"]], [t["h"]])])
+        steps.append((t, r, qk, one))
+
+    def per_op(s):
+        for _, r, _, _ in steps:
+            check_rc(C, L.cbx_rms_norm_mul(r["x"], r["g"], 1e-5, r["y"], s) |
+                     L.cbx_rope_ext(r["q"], r["pos"], cache.handle, r["qo"], s) |
+                     L.cbx_rope_ext(r["k"], r["pos"], cache.handle, r["ko"], s) |
+                     L.cbx_swiglu(r["gate"], r["up"], r["h"], s))
+
+    def qk_merged(s):
+        for _, r, qk, _ in steps:
+            check_rc(C, L.cbx_rms_norm_mul(r["x"], r["g"], 1e-5, r["y"], s) |
+                     L.cbx_run_ops(qk.arr, qk.n, s) |
+                     L.cbx_swiglu(r["gate"], r["up"], r["h"], s))
+
+    def one_launch(s):
+        for _, _, _, one in steps:
+            check_rc(C, L.cbx_run_ops(one.arr, one.n, s))
+
+    out = {}
+    ref = None
+    for name, fn in (("per_op_4_launches", per_op), ("qk_merged_3_launches", qk_merged),
+                     ("one_launch", one_launch)):
+        for t, *_ in steps:
+            for k in ("y", "qo", "ko", "h"):
+                t[k].zero_()
+        fn(cur_stream(torch))
+        torch.cuda.synchronize()
+        got = [steps[-1][0][k].cpu().numpy() for k in ("y", "qo", "ko", "h")]
+        if ref is None:
+            ref = got
+        elif not all(same_bits(a, b) for a, b in zip(got, ref)):
+            raise SystemExit(f"bench: decode plan {name} differs from one kernel per op")
+        out[name] = {"us_per_step": time_steps_us(torch, fn, W.DECODE_STEPS)}
+    cache.close()
+    nb = sum(W.decode_bytes().values())
+    for v in out.values():
+        v["GBps"] = nb / (v["us_per_step"] * 1e-6) / 1e9
+    return dict(out, bytes_per_step=nb, note="30 steps' buffers stay cache resident (77,824 B per step)")
+
+
+def bench_serving(C, W, torch, reps=400):
+    """64-stream decode step, f16 storage: RMSNorm+gamma [64,1024], RoPE q,k
+    [64,16,64] at per-stream positions, SiLU-gate [64,4096], Q8_0 gather of
+    64 rows of [8194,1024] -- per op (5 launches) and as one launch, over
+    rotating buffer sets larger than the Infinity Cache."""
+    d = dev_of(torch)
+    L = C.load()
+    cache = C.RopeCache(W.HEAD_DIM, mode=2, n_ctx_orig=2048, n_pos=2048)
+    base = {k: d(v) for k, v in W.serving_inputs().items()}
+    nb = W.serving_bytes()
+    per_step = sum(nb.values())
+    n_sets = max(2, math.ceil(MALL_DEFEAT_BYTES / per_step))
+    sets = []
+    for _ in range(n_sets):
+        t = {k: v.clone() for k, v in base.items()}
+        t["y"], t["qo"], t["ko"] = torch.empty_like(t["x"]), torch.empty_like(t["q"]), torch.empty_like(t["k"])
+        t["h"] = torch.empty_like(t["gate"])
+        t["emb"] = torch.empty((W.N_STREAMS, W.D_MODEL), dtype=torch.float32, device="cuda")
+        r = {k: C.ctypes.byref(C.desc(v, C.Q8_0 if k == "tab" else None)) for k, v in t.items()}
+        one = C.OpBatch([C.Op(C.OP_RMS_NORM, [t["x"], t["g"]], [t["y"]], eps=1e-5),
+                         C.Op(C.OP_ROPE, [t["q"], t["pos"]], [t["qo"]], rope=cache),
+                         C.Op(C.OP_ROPE, [t["k"], t["pos"]], [t["ko"]], rope=cache),
+                         C.Op(C.OP_SWIGLU, [t["gate"], t["up"]], [t["h"]]),
+                         C.Op(C.OP_GET_ROWS, [t["tab"], t["ids"]], [t["emb"]], q8=[0])])
+        sets.append((t, r, one))
+
+    def per_op(st):
+        _, r, _ = st
+        return lambda s: check_rc(C, L.cbx_rms_norm_mul(r["x"], r["g"], 1e-5, r["y"], s) |
+                                  L.cbx_rope_ext(r["q"], r["pos"], cache.handle, r["qo"], s) |
+                                  L.cbx_rope_ext(r["k"], r["pos"], cache.handle, r["ko"], s) |
+                                  L.cbx_swiglu(r["gate"], r["up"], r["h"], s) |
+                                  L.cbx_get_rows(r["tab"], r["ids"], r["emb"], s))
+
+    def one_launch(st):
+        one = st[2]
+        return lambda s: check_rc(C, L.cbx_run_ops(one.arr, one.n, s))
+
+    out = {}
+    ref = None
+    for name, mk in (("per_op_5_launches", per_op), ("one_launch", one_launch)):
+        fns = [mk(st) for st in sets]
+        fns[0](cur_stream(torch))
+        torch.cuda.synchronize()
+        got = [sets[0][0][k].cpu().numpy() for k in ("y", "qo", "ko", "h", "emb")]
+        if ref is None:
+            ref = got
+        elif not all(same_bits(a, b) for a, b in zip(got, ref)):
+            raise SystemExit(f"bench: serving plan {name} differs from one kernel per op")
+        us = per_launch_ms(torch, fns, reps) * 1000.0
+        out[name] = {"us_per_step": us, "GBps": per_step / (us * 1e-6) / 1e9}
+    cache.close()
+    return dict(out, bytes_per_step=per_step, bytes=nb, buffer_sets=n_sets)
+
+
+def bench_cfm(C, W, torch, reps=400):
+    """CFM estimator ops of one flow step: GroupNorm(8)+affine+Mish on
+    [2,256,500] and [2,512,500], LayerNorm+affine then NEOX RoPE (positions
+    0..499) on [2,500,8x64]; rotating buffer sets."""
+    d = dev_of(torch)
+    L = C.load()
+    cache = C.RopeCache(W.HEAD_DIM, mode=2, n_ctx_orig=2048, n_pos=2048)
+    base = {k: d(v) for k, v in W.cfm_inputs().items()}
+    nb = W.cfm_bytes()
+    per_step = sum(nb.values())
+    n_sets = max(2, math.ceil(MALL_DEFEAT_BYTES / per_step))
+    sets = []
+    for _ in range(n_sets):
+        t = {k: v.clone() for k, v in base.items()}
+        for k in ("x256", "x512", "xa"):
+            t["y" + k[1:]] = torch.empty_like(t[k])
+        t["ya_rope"] = torch.empty_like(t["xa"])
+        r = {k: C.ctypes.byref(C.desc(v)) for k, v in t.items()}
+        ra = C.ctypes.byref(C.desc(t["ya"].view(2, W.CFM_T, W.CFM_HEADS, W.HEAD_DIM)))
+        ro = C.ctypes.byref(C.desc(t["ya_rope"].view(2, W.CFM_T, W.CFM_HEADS, W.HEAD_DIM)))
+        sets.append((t, r, ra, ro))
+
+    def gn(key):
+        return lambda st: (lambda s: check_rc(C, L.cbx_group_norm(st[1]["x" + key], W.CFM_GROUPS, 1e-5,
+                                                                  st[1]["w" + key], st[1]["b" + key], C.MISH,
+                                                                  st[1]["y" + key], s)))
+
+    def ln(st):
+        r = st[1]
+        return lambda s: check_rc(C, L.cbx_layer_norm(r["xa"], r["wa"], r["ba"], 1e-5, -1, r["ya"], s))
+
+    def rope(st):
+        return lambda s: check_rc(C, L.cbx_rope_ext(st[2], st[1]["pos"], cache.handle, st[3], s))
+
+    out = {}
+    for name, mk in (("group_norm_mish_256", gn("256")), ("group_norm_mish_512", gn("512")),
+                     ("layer_norm_1024x512", ln), ("rope_2x500x8x64", rope)):
+        fns = [mk(st) for st in sets]
+        for f in fns:
+            f(cur_stream(torch))
+        out[name] = {"us": per_launch_ms(torch, fns, reps) * 1000.0}
+    step = lambda st: (lambda s: [mk(st)(s) for mk in (gn("256"), gn("512"), ln, rope)])  # noqa: E731
+    out["flow_step"] = {"us": per_launch_ms(torch, [step(st) for st in sets], reps) * 1000.0}
+    for k, key in (("group_norm_mish_256", "group_norm_mish_256"), ("group_norm_mish_512", "group_norm_mish_512")):
+        out[k]["GBps"] = nb[key] / (out[k]["us"] * 1e-6) / 1e9
+    lr = out["layer_norm_1024x512"]["us"] + out["rope_2x500x8x64"]["us"]
+    out["layer_norm_rope_GBps_vs_fused_bytes"] = nb["layer_norm_rope"] / (lr * 1e-6) / 1e9
+    out["flow_step"]["GBps"] = per_step / (out["flow_step"]["us"] * 1e-6) / 1e9
+    cache.close()
+    return dict(out, bytes_per_flow_step=per_step, bytes=nb, buffer_sets=n_sets)
+
+
+def bench_hift(C, W, torch, quick=False):
+    """HiFT vocoder activations: Snake (channel innermost as the reference
+    lays it out, and time innermost) and LeakyReLU(0.1) on every upsample
+    stage shape; buffer sets rotate past the Infinity Cache.  x ~ N(0,1)
+    from torch's seeded device generator (the tensors reach 123M elements)."""
+    L = C.load()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(W.seed_of(4, 0))
+    out = {}
+    shapes = W.HIFT_SHAPES[-1:] if quick else W.HIFT_SHAPES
+    for (B, Ch, T) in shapes:
+        n = B * Ch * T
+        a_np, ai_np = W.snake_alpha(Ch)
+        a, ai = torch.from_numpy(a_np).cuda(), torch.from_numpy(ai_np).cuda()
+        per = 8 * n
+        n_sets = max(2, math.ceil(MALL_DEFEAT_BYTES / per))
+        xs = [torch.empty((B, T, Ch), dtype=torch.float32, device="cuda").normal_(generator=gen) for _ in range(n_sets)]
+        ys = [torch.empty_like(x) for x in xs]
+        ra, rai = C.ctypes.byref(C.desc(a)), C.ctypes.byref(C.desc(ai))
+        a_o, ai_o = a.view(Ch, 1), ai.view(Ch, 1)
+        rao, raio = C.ctypes.byref(C.desc(a_o)), C.ctypes.byref(C.desc(ai_o))
+        rx = [C.ctypes.byref(C.desc(x)) for x in xs]
+        ry = [C.ctypes.byref(C.desc(y)) for y in ys]
+        rxo = [C.ctypes.byref(C.desc(x.view(B, Ch, T))) for x in xs]
+        ryo = [C.ctypes.byref(C.desc(y.view(B, Ch, T))) for y in ys]
+        plans = {
+            "snake_channel_inner": [(lambda i: lambda s: check_rc(C, L.cbx_snake(rx[i], ra, rai, ry[i], s)))(i)
+                                    for i in range(n_sets)],
+            "snake_time_inner": [(lambda i: lambda s: check_rc(C, L.cbx_snake(rxo[i], rao, raio, ryo[i], s)))(i)
+                                 for i in range(n_sets)],
+            "leaky_relu_0.1": [(lambda i: lambda s: check_rc(C, L.cbx_leaky_relu(rx[i], 0.1, ry[i], s)))(i)
+                               for i in range(n_sets)],
+        }
+        key = f"{B}x{Ch}x{T}"
+        out[key] = {"bytes": per + (8 * Ch), "buffer_sets": n_sets}
+        reps = max(n_sets, min(200, int(2e10 / per)))
+        for name, fns in plans.items():
+            for f in fns:
+                f(cur_stream(torch))
+            ms = per_launch_ms(torch, fns, reps)
+            nbytes = per + (8 * Ch if name.startswith("snake") else 0)
+            out[key][name] = {"us": ms * 1000.0, "GBps": nbytes / (ms * 1e-3) / 1e9}
+        del xs, ys
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_copy_ceiling(C, torch, sizes, reps=400):
+    """A plain f32 device copy (cbx_cpy: one read, one write, nothing else)
+    of each byte count, over rotating buffers: the best rate a launch moving
+    that many bytes reaches on this GPU, the practical ceiling of a kernel
+    of the same size."""
+    L = C.load()
+    out = {}
+    for name, nbytes in sizes.items():
+        n = nbytes // 8
+        n_sets = max(2, math.ceil(MALL_DEFEAT_BYTES / (2 * 4 * n)))
+        xs = [torch.empty(n, dtype=torch.float32, device="cuda").uniform_() for _ in range(n_sets)]
+        ys = [torch.empty_like(x) for x in xs]
+        rx = [C.ctypes.byref(C.desc(x)) for x in xs]
+        ry = [C.ctypes.byref(C.desc(y)) for y in ys]
+        fns = [(lambda i: lambda s: check_rc(C, L.cbx_cpy(rx[i], ry[i], s)))(i) for i in range(n_sets)]
+        for f in fns:
+            f(cur_stream(torch))
+        ms = per_launch_ms(torch, fns, reps)
+        out[name] = {"bytes": 8 * n, "us": ms * 1000.0, "GBps": 8 * n / (ms * 1e-3) / 1e9}
+        del xs, ys
+    return out
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gelu_512x4096_and_embed_ln_traffic.md")
@@ -321,9 +547,16 @@ def cpu_baseline(W, seconds):
         el = time.perf_counter() - t0
         if el >= seconds or reps >= 100000:
             break
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
     return {"value": per_step * reps / el / 1e9, "unit": "GB/s", "cores": nth, "kind": "port",
             "sample": f"{reps} steps of the T3 prefill op chain (gather+pos f32, LayerNorm, GELU), "
-                      f"{el:.1f} s, OpenMP row split as ggml-cpu"}
+                      f"{el:.1f} s, OpenMP row split as ggml-cpu",
+            "nproc": os.cpu_count(), "cpu_model": model}
 
 
 def main():
@@ -353,8 +586,20 @@ def main():
         details["prefill_f32_unfused"] = dict(ru, GBps=gbps(ru))
         r16 = bench_prefill(C, W, torch, max(200, a.steps // 4), 20, f16_table=True)
         details["prefill_f16_table_fused"] = dict(r16, GBps=gbps(r16))
+        r1 = bench_prefill(C, W, torch, max(200, a.steps // 4), 20, one_launch=True)
+        details["prefill_f32_one_launch"] = dict(r1, GBps=gbps(r1))
+        nb = W.prefill_bytes()
+        details["copy_ceiling"] = bench_copy_ceiling(C, torch, {"gelu_bytes": nb["gelu"],
+                                                                "embed_layer_norm_bytes": nb["embed_layer_norm"],
+                                                                "chain_bytes": sum(nb.values())})
+        log("decode")
         details["t3_decode"] = bench_decode(C, W, torch)
-        details["hift_snake_16x64x120000"] = bench_snake(C, W, torch)
+        log("serving")
+        details["serving_64_streams_f16"] = bench_serving(C, W, torch)
+        log("cfm")
+        details["cfm_flow_step"] = bench_cfm(C, W, torch)
+        log("hift")
+        details["hift_activations"] = bench_hift(C, W, torch)
     k_ms = res["kernel_ms"]["gelu"]
     k_bytes = res["kernel_bytes"]["gelu"]
     achieved = k_bytes / (k_ms * 1e-3) / 1e9
@@ -385,7 +630,9 @@ def main():
                      "launch_ms": k_ms, "algorithmic_bytes": k_bytes},
     }
     if "t3_decode" in details:
-        out["t3_decode_us_per_step_chain"] = round(details["t3_decode"]["us_per_step_chain"], 3)
+        dd = details["t3_decode"]
+        out["t3_decode_us_per_step_chain"] = {k: round(dd[k]["us_per_step"], 3)
+                                              for k in ("per_op_4_launches", "qk_merged_3_launches", "one_launch")}
     out["details"] = details
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(W, a.cpu_seconds)

@@ -31,8 +31,9 @@ SOURCES = [
     "k_group_norm.hip",
     "k_rope.hip",
     "k_eltwise.hip",
+    "k_batch.hip",
 ]
-HEADERS = ["cbx_internal.h", "cbx_device.h", os.path.join("..", "..", "include", "cbxops.h")]
+HEADERS = ["cbx_internal.h", "cbx_device.h", "cbx_rowops.h", os.path.join("..", "..", "include", "cbxops.h")]
 
 ARCH = "gfx950"
 COMMON = [

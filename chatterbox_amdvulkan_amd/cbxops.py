@@ -52,6 +52,25 @@ class Tensor(ctypes.Structure):
     ]
 
 
+class OpStruct(ctypes.Structure):
+    """cbx_op"""
+
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("act", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("param", ctypes.c_float),
+        ("src", ctypes.POINTER(Tensor) * 6),
+        ("dst", ctypes.POINTER(Tensor) * 2),
+        ("rope", ctypes.c_void_p),
+    ]
+
+
+# cbx_op_kind
+OP_LAYER_NORM, OP_RMS_NORM, OP_UNARY, OP_LEAKY_RELU, OP_SWIGLU, OP_ROPE, OP_GET_ROWS, \
+    OP_GET_ROWS_ADD_LAYER_NORM, OP_SNAKE = range(1, 10)
+MAX_OPS = 12
+
 _lib = None
 _initialised: set[int] = set()
 
@@ -99,6 +118,7 @@ def load() -> ctypes.CDLL:
         "cbx_leaky_relu": (i, [P, f, P, vp]),
         "cbx_swiglu": (i, [P, P, P, vp]),
         "cbx_snake": (i, [P, P, P, P, vp]),
+        "cbx_run_ops": (i, [ctypes.POINTER(OpStruct), i, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -385,3 +405,58 @@ def snake(x, alpha, alpha_inv, out=None):
     out = _out_like(x, out)
     _check(load().cbx_snake(_ref(desc(x)), _ref(desc(alpha)), _ref(desc(alpha_inv)), _ref(desc(out)), _stream()))
     return out
+
+
+# ---- one launch for several independent ops -----------------------------------
+
+class Op:
+    """One entry of run_ops: kind (OP_*), source and destination tensors
+    (None for absent optional operands), activation, eps, param, rope table.
+    q8 lists the source indices that are Q8_0 tables (uint8 blocks)."""
+
+    def __init__(self, kind, src=(), dst=(), act=UNARY_NONE, eps=0.0, param=0.0, rope: Optional[RopeCache] = None,
+                 q8=()):
+        self.kind, self.act, self.eps, self.param, self.rope = kind, act, eps, param, rope
+        self.src = list(src) + [None] * (6 - len(src))
+        self.dst = list(dst) + [None] * (2 - len(dst))
+        self.q8 = set(q8)
+
+    def struct(self, keep: list) -> OpStruct:
+        o = OpStruct()
+        o.kind, o.act, o.eps, o.param = self.kind, self.act, self.eps, self.param
+        for k, t in enumerate(self.src):
+            if t is not None:
+                d = desc(t, Q8_0 if k in self.q8 else None)
+                keep.append(d)
+                o.src[k] = ctypes.pointer(d)
+        for k, t in enumerate(self.dst):
+            if t is not None:
+                d = desc(t)
+                keep.append(d)
+                o.dst[k] = ctypes.pointer(d)
+        o.rope = self.rope.handle.value if self.rope is not None else None
+        return o
+
+
+class OpBatch:
+    """Prebuilt argument array for cbx_run_ops (build once, launch often)."""
+
+    def __init__(self, ops):
+        if not ops or len(ops) > MAX_OPS:
+            raise CbxError(ERR_INVALID_ARG, f"1..{MAX_OPS} ops per launch")
+        self._keep: list = []
+        self.n = len(ops)
+        self.arr = (OpStruct * self.n)(*[op.struct(self._keep) for op in ops])
+
+    def launch(self, stream=None) -> None:
+        _check(load().cbx_run_ops(self.arr, self.n, stream if stream is not None else _stream()))
+
+
+def run_ops(ops) -> None:
+    """Runs independent ops in one kernel launch (cbx_run_ops)."""
+    for op in ops:
+        for t in op.src + op.dst:
+            if t is not None:
+                _ready(t)
+                break
+    OpBatch(ops).launch()

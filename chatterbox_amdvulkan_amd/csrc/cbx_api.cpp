@@ -581,3 +581,265 @@ int cbx_snake(const cbx_tensor* x, const cbx_tensor* alpha, const cbx_tensor* al
 }
 
 }  // extern "C"
+
+// ---- one launch for several independent ops --------------------------------
+
+namespace {
+
+// [lo, hi) bytes a tensor spans (empty tensors span nothing)
+bool byte_range(const cbx_tensor* t, uintptr_t* lo, uintptr_t* hi) {
+    if (!t || nelements(t) == 0) return false;
+    const size_t row = t->type == CBX_TYPE_Q8_0 ? static_cast<size_t>(t->ne[0] / 32) * 34
+                                                 : static_cast<size_t>(t->ne[0]) * type_size(t->type);
+    size_t span = row;
+    for (int k = 1; k < 4; k++) span += static_cast<size_t>(t->ne[k] - 1) * t->nb[k];
+    *lo = reinterpret_cast<uintptr_t>(t->data);
+    *hi = *lo + span;
+    return true;
+}
+
+bool rows_aligned_to(const cbx_tensor* t, size_t a) {
+    if (reinterpret_cast<uintptr_t>(t->data) % a) return false;
+    for (int k = 1; k < 4; k++) if (t->ne[k] > 1 && t->nb[k] % a) return false;
+    return true;
+}
+
+BTen bten(const cbx_tensor* t, int64_t step) {
+    BTen b;
+    b.p = t ? static_cast<char*>(t->data) : nullptr;
+    b.nb1 = step;
+    return b;
+}
+
+int batch_fail(int i, int code, const std::string& msg) {
+    return set_error(code, "cbx_run_ops: op " + std::to_string(i) + ": " + msg);
+}
+
+// Fills b from o (validated) and returns the op's workgroup count in *nblk.
+int build_op(int i, const cbx_op& o, BOp& b, DeviceState* st, int64_t* nblk) {
+    const char* what = "cbx_run_ops";
+    int rc;
+    b.kind = o.kind;
+    b.act = o.act;
+    b.eps = o.eps;
+    b.param = o.param;
+    b.table = st->gelu_table;
+    b.ff = nullptr;
+    b.n_pos = 0;
+    b.nv = 1;
+    for (auto& t : b.t) t = bten(nullptr, 0);
+    *nblk = 0;
+    switch (o.kind) {
+        case CBX_OP_LAYER_NORM:
+        case CBX_OP_RMS_NORM: {
+            const cbx_tensor *x = o.src[0], *w = o.src[1], *bb = o.kind == CBX_OP_LAYER_NORM ? o.src[2] : nullptr;
+            const cbx_tensor* y = o.dst[0];
+            if ((rc = check_float(x, what, "x")) || (rc = check_float(y, what, "y"))) return rc;
+            if (x->type != y->type || !same_shape(x, y)) return batch_fail(i, CBX_ERR_INVALID_ARG, "x and y differ in type or shape");
+            if (!(o.eps >= 0.0f)) return batch_fail(i, CBX_ERR_INVALID_ARG, "eps must be >= 0");
+            if ((rc = check_row_param(w, x, what, "w")) || (rc = check_row_param(bb, x, what, "b")) || (rc = check_act(o.act, what))) return rc;
+            if (o.kind == CBX_OP_RMS_NORM && o.act != CBX_UNARY_NONE) return batch_fail(i, CBX_ERR_UNSUPPORTED, "RMS norm takes no activation");
+            const size_t al = x->type == CBX_TYPE_F32 ? 16 : 8;
+            if (x->ne[0] % 4 || x->ne[0] > 1024 || !flat_rows(x) || !flat_rows(y) || !rows_aligned_to(x, al) ||
+                !rows_aligned_to(y, al) || (w && reinterpret_cast<uintptr_t>(w->data) % 16) ||
+                (bb && reinterpret_cast<uintptr_t>(bb->data) % 16)) {
+                return batch_fail(i, CBX_ERR_UNSUPPORTED, "norm rows must be <= 1024 elements, ne0 % 4 == 0, uniformly strided and aligned");
+            }
+            b.t_x = x->type;
+            b.ne0 = x->ne[0];
+            b.rows = nrows(x);
+            b.nv = x->ne[0] <= 256 ? 1 : x->ne[0] <= 512 ? 2 : 4;
+            b.t[0] = bten(x, static_cast<int64_t>(x->nb[1]));
+            b.t[1] = bten(w, 0);
+            b.t[2] = bten(bb, 0);
+            b.t[6] = bten(y, static_cast<int64_t>(y->nb[1]));
+            *nblk = cdiv(b.rows, 4);
+            return CBX_OK;
+        }
+        case CBX_OP_UNARY:
+        case CBX_OP_LEAKY_RELU:
+        case CBX_OP_SWIGLU: {
+            const bool glu = o.kind == CBX_OP_SWIGLU;
+            const cbx_tensor *x = o.src[0], *u = glu ? o.src[1] : nullptr, *y = o.dst[0];
+            if ((rc = check_float(x, what, "x")) || (rc = check_float(y, what, "y")) || (glu && (rc = check_float(u, what, "u")))) return rc;
+            if (x->type != y->type || !same_shape(x, y) || (glu && (u->type != x->type || !same_shape(u, x)))) {
+                return batch_fail(i, CBX_ERR_INVALID_ARG, "operands differ in type or shape");
+            }
+            if (o.kind == CBX_OP_UNARY && (o.act < CBX_UNARY_GELU || o.act > CBX_UNARY_MISH)) {
+                return batch_fail(i, CBX_ERR_INVALID_ARG, "unknown unary op " + std::to_string(o.act));
+            }
+            const size_t al = x->type == CBX_TYPE_F32 ? 16 : 8;
+            for (const cbx_tensor* t : {x, u, static_cast<const cbx_tensor*>(y)}) {
+                if (t && (!is_contiguous(t) || reinterpret_cast<uintptr_t>(t->data) % al)) {
+                    return batch_fail(i, CBX_ERR_UNSUPPORTED, "element-wise operands must be contiguous and aligned");
+                }
+            }
+            b.t_x = x->type;
+            b.rows = nelements(x);
+            b.t[0] = bten(x, 0);
+            b.t[1] = bten(u, 0);
+            b.t[6] = bten(y, 0);
+            *nblk = b.rows ? cdiv(b.rows / 4 + 1, 256) : 0;
+            return CBX_OK;
+        }
+        case CBX_OP_ROPE: {
+            const cbx_tensor *x = o.src[0], *pos = o.src[1], *y = o.dst[0];
+            const cbx_rope_cache* c = o.rope;
+            if (!c) return batch_fail(i, CBX_ERR_INVALID_ARG, "rope is NULL");
+            int dev = 0;
+            hipGetDevice(&dev);
+            if (dev != c->device) return batch_fail(i, CBX_ERR_INVALID_ARG, "rope table belongs to another device");
+            if ((rc = check_float(x, what, "x")) || (rc = check_float(y, what, "y")) || (rc = validate(pos, what, "pos"))) return rc;
+            if (x->type != y->type || !same_shape(x, y)) return batch_fail(i, CBX_ERR_INVALID_ARG, "x and y differ in type or shape");
+            if (pos->type != CBX_TYPE_I32 || pos->ne[0] != x->ne[2] || nelements(pos) != pos->ne[0]) {
+                return batch_fail(i, CBX_ERR_INVALID_ARG, "pos must be I32 with ne = (x.ne2, 1, 1, 1)");
+            }
+            if (c->p.n_dims > x->ne[0]) return batch_fail(i, CBX_ERR_INVALID_ARG, "n_dims > x.ne0");
+            if (c->p.n_dims / 2 > 256 || !flat_rows(x) || !flat_rows(y)) {
+                return batch_fail(i, CBX_ERR_UNSUPPORTED, "rope needs n_dims <= 512 and uniformly strided rows");
+            }
+            b.t_x = x->type;
+            b.ne0 = x->ne[0];
+            b.rows = x->ne[2] * x->ne[3];
+            b.aux = x->ne[1];
+            b.aux2 = x->ne[2];
+            b.t[0] = bten(x, static_cast<int64_t>(x->nb[1]));
+            b.t[1] = bten(pos, static_cast<int64_t>(pos->nb[0]));
+            b.t[6] = bten(y, static_cast<int64_t>(y->nb[1]));
+            b.table = c->table;
+            b.ff = c->freq_factors;
+            b.n_pos = c->n_pos;
+            b.rp = c->p;
+            *nblk = nelements(x) ? b.rows : 0;
+            return CBX_OK;
+        }
+        case CBX_OP_GET_ROWS:
+        case CBX_OP_GET_ROWS_ADD_LAYER_NORM: {
+            const bool ln = o.kind == CBX_OP_GET_ROWS_ADD_LAYER_NORM;
+            const cbx_tensor *src = o.src[0], *ids = o.src[1], *src2 = o.src[2], *ids2 = o.src[3];
+            cbx_tensor* y = ln ? o.dst[1] : o.dst[0];
+            cbx_tensor* h = ln ? o.dst[0] : nullptr;
+            if ((rc = check_gather(what, src, ids, y))) return rc;
+            if ((src2 || ids2 || ln) && (rc = check_gather(what, src2, ids2, y))) return rc;
+            if (h && ((rc = validate(h, what, "h")) || h->type != CBX_TYPE_F32 || !same_shape(h, y))) {
+                return rc ? rc : batch_fail(i, CBX_ERR_INVALID_ARG, "h must be F32 with y's shape");
+            }
+            if (ln) {
+                if (!(o.eps >= 0.0f)) return batch_fail(i, CBX_ERR_INVALID_ARG, "eps must be >= 0");
+                if ((rc = check_row_param(o.src[4], y, what, "w")) || (rc = check_row_param(o.src[5], y, what, "b"))) return rc;
+            }
+            auto table_ok = [](const cbx_tensor* t) {
+                if (!t) return true;
+                if (t->ne[2] != 1 || t->ne[3] != 1) return false;
+                return t->type == CBX_TYPE_Q8_0 || rows_aligned_to(t, t->type == CBX_TYPE_F32 ? 16 : 8);
+            };
+            if (ids->ne[1] != 1 || ids->ne[2] != 1 || y->ne[0] % 4 || !table_ok(src) || !table_ok(src2) ||
+                !flat_rows(y) || !rows_aligned_to(y, 16) || (h && (!flat_rows(h) || !rows_aligned_to(h, 16))) ||
+                (ln && (y->ne[0] > 1024 || (o.src[4] && reinterpret_cast<uintptr_t>(o.src[4]->data) % 16) ||
+                        (o.src[5] && reinterpret_cast<uintptr_t>(o.src[5]->data) % 16)))) {
+                return batch_fail(i, CBX_ERR_UNSUPPORTED,
+                                  "gathers need 1-D ids, 2-D tables, ne0 % 4 == 0 (<= 1024 with LayerNorm) and aligned rows");
+            }
+            b.t_x = src->type;
+            b.t_x2 = src2 ? src2->type : -1;
+            b.ne0 = y->ne[0];
+            b.rows = ids->ne[0];
+            b.aux = src->ne[1];
+            b.aux2 = src2 ? src2->ne[1] : 0;
+            b.t[0] = bten(src, static_cast<int64_t>(src->nb[1]));
+            b.t[1] = bten(ids, static_cast<int64_t>(ids->nb[0]));
+            b.t[2] = bten(src2, src2 ? static_cast<int64_t>(src2->nb[1]) : 0);
+            b.t[3] = bten(ids2, ids2 ? static_cast<int64_t>(ids2->nb[0]) : 0);
+            if (ln) {
+                b.t[4] = bten(o.src[4], 0);
+                b.t[5] = bten(o.src[5], 0);
+                b.t[6] = bten(h, h ? static_cast<int64_t>(h->nb[1]) : 0);
+                b.t[7] = bten(y, static_cast<int64_t>(y->nb[1]));
+                b.nv = y->ne[0] <= 256 ? 1 : y->ne[0] <= 512 ? 2 : 4;
+                *nblk = cdiv(b.rows, 4);
+            } else {
+                b.t[6] = bten(y, static_cast<int64_t>(y->nb[1]));
+                *nblk = b.rows;
+            }
+            if (nelements(y) == 0) *nblk = 0;
+            return CBX_OK;
+        }
+        case CBX_OP_SNAKE: {
+            const cbx_tensor *x = o.src[0], *a = o.src[1], *ai = o.src[2], *y = o.dst[0];
+            if ((rc = validate(x, what, "x")) || (rc = validate(y, what, "y")) || (rc = validate(a, what, "alpha")) ||
+                (rc = validate(ai, what, "alpha_inv"))) return rc;
+            if (x->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32 || a->type != CBX_TYPE_F32 || ai->type != CBX_TYPE_F32) {
+                return batch_fail(i, CBX_ERR_UNSUPPORTED, "snake is F32 only");
+            }
+            if (!same_shape(x, y) || !same_shape(a, ai)) return batch_fail(i, CBX_ERR_INVALID_ARG, "shapes differ");
+            const bool inner = a->ne[0] == x->ne[0] && a->ne[1] == 1 && a->ne[2] == 1 && a->ne[3] == 1 && x->ne[0] > 1;
+            const bool outer = a->ne[0] == 1 && a->ne[1] == x->ne[1] && a->ne[2] == 1 && a->ne[3] == 1;
+            if (!inner && !outer) return batch_fail(i, CBX_ERR_UNSUPPORTED, "alpha must be (x.ne0,1,1,1) or (1,x.ne1,1,1)");
+            const int64_t n = nelements(x);
+            if (!is_contiguous(x) || !is_contiguous(y) || !is_contiguous(a) || !is_contiguous(ai) || x->ne[0] % 4 ||
+                n >= (int64_t{1} << 32) || reinterpret_cast<uintptr_t>(x->data) % 16 ||
+                reinterpret_cast<uintptr_t>(y->data) % 16 || reinterpret_cast<uintptr_t>(a->data) % 16 ||
+                reinterpret_cast<uintptr_t>(ai->data) % 16) {
+                return batch_fail(i, CBX_ERR_UNSUPPORTED, "snake needs contiguous aligned tensors, ne0 % 4 == 0");
+            }
+            const int64_t C = inner ? x->ne[0] : x->ne[1];
+            b.act = inner ? 1 : 0;
+            b.rows = n;
+            b.aux = C;
+            b.aux2 = (C & (C - 1)) == 0 ? C - 1 : 0;
+            b.aux3 = x->ne[0] / 4;
+            b.t[0] = bten(x, 0);
+            b.t[1] = bten(a, 0);
+            b.t[2] = bten(ai, 0);
+            b.t[6] = bten(y, 0);
+            *nblk = cdiv(n / 4, 256);
+            return CBX_OK;
+        }
+        default:
+            return batch_fail(i, CBX_ERR_INVALID_ARG, "unknown op kind " + std::to_string(o.kind));
+    }
+}
+
+}  // namespace
+
+extern "C" int cbx_run_ops(const cbx_op* ops, int n_ops, cbx_stream stream) {
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if (!ops || n_ops <= 0 || n_ops > CBX_MAX_OPS) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_run_ops: n_ops must be in 1.." + std::to_string(CBX_MAX_OPS));
+    }
+    BatchArgs a{};
+    a.n = n_ops;
+    a.err = st->err_word;
+    int64_t total = 0;
+    for (int i = 0; i < n_ops; i++) {
+        int64_t nb = 0;
+        a.op[i].blk0 = static_cast<uint32_t>(total);
+        if ((rc = build_op(i, ops[i], a.op[i], st, &nb))) return rc;
+        total += nb;
+        if (total >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "cbx_run_ops: too many workgroups");
+    }
+    // independence: no op writes what another op reads or writes
+    for (int i = 0; i < n_ops; i++) {
+        for (const cbx_tensor* d : ops[i].dst) {
+            uintptr_t dl, dh;
+            if (!byte_range(d, &dl, &dh)) continue;
+            for (int j = 0; j < n_ops; j++) {
+                if (j == i) continue;
+                const cbx_tensor* other[8] = {ops[j].src[0], ops[j].src[1], ops[j].src[2], ops[j].src[3],
+                                              ops[j].src[4], ops[j].src[5], ops[j].dst[0], ops[j].dst[1]};
+                for (const cbx_tensor* t : other) {
+                    uintptr_t tl, th;
+                    if (byte_range(t, &tl, &th) && dl < th && tl < dh) {
+                        return set_error(CBX_ERR_INVALID_ARG, "cbx_run_ops: op " + std::to_string(i) +
+                                                                  " writes memory that op " + std::to_string(j) + " uses");
+                    }
+                }
+            }
+        }
+    }
+    if (total == 0) return CBX_OK;
+    return launch_batch(a, static_cast<uint32_t>(total), reinterpret_cast<hipStream_t>(stream));
+}

@@ -107,6 +107,48 @@ int launch_rope(const cbx_tensor* x, const cbx_tensor* pos, const RopeParams& p,
                 const float2* table, int32_t n_pos, const float* freq_factors_dev,
                 cbx_tensor* y, DeviceState* st, hipStream_t s);
 
+// ---- one-launch op batch --------------------------------------------------
+// A tensor of a batched op: base pointer and the byte step between rows
+// (for id vectors: between elements).
+struct BTen {
+    char*   p;
+    int64_t nb1;
+};
+
+// One op of a batch, in kernel-argument memory.  Field use by kind:
+//   norms:     t0 x, t1 w, t2 b, t6 y; ne0, rows; nv vectors per lane; t_x type
+//   unary/leaky/swiglu: t0 (t1) -> t6; n elements in `rows`; t_x type
+//   rope:      t0 x, t1 pos, t6 y; ne0 head_dim, aux heads, aux2 ne2, rows tokens
+//   get_rows(+add)(+LN): t0 table, t1 ids, t2 table2, t3 ids2, t4 w, t5 b,
+//              t6 dst (h), t7 y; t_x/t_x2 table types; aux/aux2 table rows
+//   snake:     t0 x, t1 a, t2 ai, t6 y; act 1 = alpha along ne0; aux C,
+//              aux2 cmask, aux3 ne0/4
+struct BOp {
+    int32_t     kind;
+    int32_t     act;
+    int32_t     nv;
+    int32_t     t_x, t_x2;
+    float       eps, param;
+    uint32_t    blk0;        // first workgroup of this op
+    int64_t     ne0, rows, aux, aux2, aux3;
+    BTen        t[8];
+    const void* table;       // rope cos/sin table or the GELU table
+    const float* ff;         // rope freq factors (device) or nullptr
+    int32_t     n_pos;
+    RopeParams  rp;
+};
+
+constexpr int kBatchMaxOps = CBX_MAX_OPS;
+
+struct BatchArgs {
+    int32_t   n;
+    uint32_t* err;
+    BOp       op[kBatchMaxOps];
+};
+static_assert(sizeof(BatchArgs) <= 4096, "batch arguments must fit the kernel argument segment");
+
+int launch_batch(const BatchArgs& a, uint32_t total_blocks, hipStream_t s);
+
 // Row-norm kinds.
 enum { NORM_LN = 0, NORM_RMS = 1 };
 // Pseudo unary op used internally for leaky_relu.

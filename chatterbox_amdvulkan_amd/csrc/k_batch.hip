@@ -1,0 +1,377 @@
+// k_batch.hip -- several independent ops in one kernel launch.
+//
+// Every workgroup (256 lanes) finds its op by scanning the ops' first-block
+// offsets (scalar, in kernel-argument memory) and runs that op's body on
+// its local block index.  The bodies are the standalone kernels' bodies
+// (same arithmetic, bit-identical results): wave-per-row norms (4 rows per
+// workgroup), full-grid element-wise ops (256 vectors per workgroup), RoPE
+// with the token's cos/sin row in LDS (one token per workgroup), row gathers
+// (one row per workgroup) and the fused embedding + LayerNorm (4 tokens per
+// workgroup).  Launching them together pays the fixed dispatch cost once.
+#include "cbx_rowops.h"
+
+namespace cbx {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRopeMaxHalf = 256;
+
+// ---- norms: wave per row ----------------------------------------------------
+template <typename T, int NV, int KIND>
+__device__ __forceinline__ void b_norm_row(const BOp& op, int64_t row, int lane, const uint16_t* tab) {
+    const int64_t ne0 = op.ne0;
+    const char* xr = op.t[0].p + row * op.t[0].nb1;
+    char* yr = op.t[6].p + row * op.t[6].nb1;
+    const float* w = reinterpret_cast<const float*>(op.t[1].p);
+    const float* b = reinterpret_cast<const float*>(op.t[2].p);
+    Affine<NV> af;
+    af.load(w, b, lane, ne0);
+    float4 v[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t j = (lane + 64 * k) * 4;
+        v[k] = Elt<T>::load4(xr + (j < ne0 ? j : 0) * Elt<T>::size);
+    }
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        if ((lane + 64 * k) * 4 >= ne0) v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const float scale = wave_row_scale<NV, KIND>(v, lane, ne0, op.eps);
+    if (op.act != CBX_UNARY_NONE) {
+        wave_row_store<T, NV, true>(v, lane, ne0, scale, af, w != nullptr, b != nullptr, op.act, tab, yr);
+    } else {
+        wave_row_store<T, NV, false>(v, lane, ne0, scale, af, w != nullptr, b != nullptr, op.act, tab, yr);
+    }
+}
+
+template <typename T, int KIND>
+__device__ __forceinline__ void b_norm_nv(const BOp& op, int64_t row, int lane, const uint16_t* tab) {
+    switch (op.nv) {
+        case 1: b_norm_row<T, 1, KIND>(op, row, lane, tab); break;
+        case 2: b_norm_row<T, 2, KIND>(op, row, lane, tab); break;
+        default: b_norm_row<T, 4, KIND>(op, row, lane, tab); break;
+    }
+}
+
+__device__ __forceinline__ void b_norm(const BOp& op, uint32_t lb, const uint16_t* tab) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(lb) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (row >= op.rows) return;   // uniform per wave
+    const bool f16 = op.t_x == CBX_TYPE_F16;
+    if (op.kind == CBX_OP_LAYER_NORM) {
+        if (f16) b_norm_nv<uint16_t, NORM_LN>(op, row, lane, tab);
+        else b_norm_nv<float, NORM_LN>(op, row, lane, tab);
+    } else {
+        if (f16) b_norm_nv<uint16_t, NORM_RMS>(op, row, lane, tab);
+        else b_norm_nv<float, NORM_RMS>(op, row, lane, tab);
+    }
+}
+
+// ---- element-wise: one 4-vector per lane --------------------------------------
+__device__ __forceinline__ float b_unary1(int op, float x, const uint16_t* tab, float param) {
+    if (op == CBX_UNARY_GELU) return act_gelu_fast(tab, x);
+    return apply_act(op, x, tab, param);
+}
+
+template <typename T>
+__device__ __forceinline__ void b_unary_t(const BOp& op, uint32_t lb, const uint16_t* tab) {
+    const int64_t i = static_cast<int64_t>(lb) * kThreads + threadIdx.x;
+    const int64_t n = op.rows, n4 = n >> 2;
+    const int fn = op.kind == CBX_OP_LEAKY_RELU ? UNARY_LEAKY : op.act;
+    const char* x = op.t[0].p;
+    char* y = op.t[6].p;
+    constexpr int es = Elt<T>::size;
+    if (i < n4) {
+        if (std::is_same<T, uint16_t>::value && fn == CBX_UNARY_GELU) {
+            const cbx_u2v raw = __builtin_nontemporal_load(reinterpret_cast<const cbx_u2v*>(x + i * 8));
+            cbx_u2v o;
+            o.x = tab[raw.x & 0xffffu] | (static_cast<uint32_t>(tab[raw.x >> 16]) << 16);
+            o.y = tab[raw.y & 0xffffu] | (static_cast<uint32_t>(tab[raw.y >> 16]) << 16);
+            __builtin_nontemporal_store(o, reinterpret_cast<cbx_u2v*>(y + i * 8));
+        } else {
+            const float4 v = Stream<T>::load4(x + i * 4 * es);
+            float4 o;
+            o.x = b_unary1(fn, v.x, tab, op.param);
+            o.y = b_unary1(fn, v.y, tab, op.param);
+            o.z = b_unary1(fn, v.z, tab, op.param);
+            o.w = b_unary1(fn, v.w, tab, op.param);
+            Stream<T>::store4(y + i * 4 * es, o);
+        }
+    } else if (i == n4) {
+        for (int64_t j = n4 * 4; j < n; j++) {
+            if (std::is_same<T, uint16_t>::value && fn == CBX_UNARY_GELU) {
+                *reinterpret_cast<uint16_t*>(y + j * 2) = tab[*reinterpret_cast<const uint16_t*>(x + j * 2)];
+            } else {
+                Elt<T>::store1(y + j * es, b_unary1(fn, Elt<T>::load1(x + j * es), tab, op.param));
+            }
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void b_swiglu_t(const BOp& op, uint32_t lb) {
+    const int64_t i = static_cast<int64_t>(lb) * kThreads + threadIdx.x;
+    const int64_t n = op.rows, n4 = n >> 2;
+    const char* g = op.t[0].p;
+    const char* u = op.t[1].p;
+    char* y = op.t[6].p;
+    constexpr int es = Elt<T>::size;
+    if (i < n4) {
+        const float4 vg = Stream<T>::load4(g + i * 4 * es);
+        const float4 vu = Stream<T>::load4(u + i * 4 * es);
+        float4 o;
+        o.x = act_silu(vg.x) * vu.x;
+        o.y = act_silu(vg.y) * vu.y;
+        o.z = act_silu(vg.z) * vu.z;
+        o.w = act_silu(vg.w) * vu.w;
+        Stream<T>::store4(y + i * 4 * es, o);
+    } else if (i == n4) {
+        for (int64_t j = n4 * 4; j < n; j++) {
+            Elt<T>::store1(y + j * es, act_silu(Elt<T>::load1(g + j * es)) * Elt<T>::load1(u + j * es));
+        }
+    }
+}
+
+__device__ __forceinline__ float b_snake1(float xv, float a, float ai) {
+    const float xa = xv * a;
+    const float sn = sinf(xa);
+    const float s2 = sn * sn;
+    const float m = s2 * ai;
+    return xv + m;
+}
+
+__device__ __forceinline__ void b_snake(const BOp& op, uint32_t lb) {
+    const uint32_t i = lb * kThreads + threadIdx.x;
+    const uint32_t n4 = static_cast<uint32_t>(op.rows >> 2);
+    if (i >= n4) return;
+    const uint32_t C = static_cast<uint32_t>(op.aux), cmask = static_cast<uint32_t>(op.aux2);
+    const float* a = reinterpret_cast<const float*>(op.t[1].p);
+    const float* ai = reinterpret_cast<const float*>(op.t[2].p);
+    const float4 v = Stream<float>::load4(op.t[0].p + 16ull * i);
+    float4 o;
+    if (op.act) {   // alpha along ne0
+        const uint32_t c = cmask ? (4u * i) & cmask : (4u * i) % C;
+        const float4 av = *reinterpret_cast<const float4*>(a + c);
+        const float4 iv = *reinterpret_cast<const float4*>(ai + c);
+        o.x = b_snake1(v.x, av.x, iv.x);
+        o.y = b_snake1(v.y, av.y, iv.y);
+        o.z = b_snake1(v.z, av.z, iv.z);
+        o.w = b_snake1(v.w, av.w, iv.w);
+    } else {        // alpha per row
+        const uint32_t row = i / static_cast<uint32_t>(op.aux3);
+        const uint32_t c = cmask ? row & cmask : row % C;
+        const float av = a[c], iv = ai[c];
+        o.x = b_snake1(v.x, av, iv);
+        o.y = b_snake1(v.y, av, iv);
+        o.z = b_snake1(v.z, av, iv);
+        o.w = b_snake1(v.w, av, iv);
+    }
+    Stream<float>::store4(op.t[6].p + 16ull * i, o);
+}
+
+// ---- rope: one token per workgroup ------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void b_rope_t(const BOp& op, uint32_t lb, float2* cs) {
+    const int64_t t = lb;                         // token index over ne2 * ne3
+    const int half = op.rp.n_dims / 2;
+    const int64_t heads = op.aux, ne2 = op.aux2, ne0 = op.ne0;
+    const int32_t p = *reinterpret_cast<const int32_t*>(op.t[1].p + (t % ne2) * op.t[1].nb1);
+    const float2* table = reinterpret_cast<const float2*>(op.table);
+    for (int k = threadIdx.x; k < half; k += kThreads) {
+        if (p >= 0 && p < op.n_pos) {
+            cs[k] = table[static_cast<int64_t>(p) * half + k];
+        } else {
+            float c, s;
+            rope_cos_sin_dev(p, k, op.rp, op.ff, &c, &s);
+            cs[k] = make_float2(c, s);
+        }
+    }
+    __syncthreads();
+    constexpr int es = Elt<T>::size;
+    for (int64_t q = threadIdx.x; q < heads * half; q += kThreads) {
+        const int64_t h = q / half;
+        const int k = static_cast<int>(q - h * half);
+        const char* xr = op.t[0].p + (t * heads + h) * op.t[0].nb1;
+        char* yr = op.t[6].p + (t * heads + h) * op.t[6].nb1;
+        const int64_t ia = op.rp.mode == 2 ? k : 2 * k;
+        const int64_t ib = op.rp.mode == 2 ? k + half : 2 * k + 1;
+        const float x0 = Elt<T>::load1(xr + ia * es);
+        const float x1 = Elt<T>::load1(xr + ib * es);
+        const float2 c = cs[k];
+        Elt<T>::store1(yr + ia * es, x0 * c.x - x1 * c.y);
+        Elt<T>::store1(yr + ib * es, x0 * c.y + x1 * c.x);
+    }
+    const int64_t n_tail = ne0 - op.rp.n_dims;
+    for (int64_t q = threadIdx.x; q < heads * n_tail; q += kThreads) {
+        const int64_t h = q / n_tail;
+        const int64_t j = op.rp.n_dims + (q - h * n_tail);
+        *reinterpret_cast<T*>(op.t[6].p + (t * heads + h) * op.t[6].nb1 + j * es) =
+            *reinterpret_cast<const T*>(op.t[0].p + (t * heads + h) * op.t[0].nb1 + j * es);
+    }
+}
+
+// ---- gathers -------------------------------------------------------------------------
+template <int TYPE>
+__device__ __forceinline__ float4 b_load_row4(const BOp& op, const char* row, int64_t j) {
+    return load_table4<TYPE>(row, j);
+}
+
+template <int TYPE, int TYPE2>
+__device__ __forceinline__ void b_gather_t(const BOp& op, uint32_t lb, uint32_t* err) {
+    const int64_t r = lb;
+    const int32_t id = *reinterpret_cast<const int32_t*>(op.t[1].p + r * op.t[1].nb1);
+    int32_t id2 = 0;
+    bool ok = id >= 0 && id < op.aux;
+    if constexpr (TYPE2 >= 0) {
+        id2 = *reinterpret_cast<const int32_t*>(op.t[3].p + r * op.t[3].nb1);
+        ok = ok && id2 >= 0 && id2 < op.aux2;
+    }
+    float* d = reinterpret_cast<float*>(op.t[6].p + r * op.t[6].nb1);
+    if (!ok) {
+        for (int64_t j = threadIdx.x; j < op.ne0; j += kThreads) d[j] = 0.0f;
+        if (threadIdx.x == 0) atomicOr(err, static_cast<uint32_t>(DEV_ERR_ROW_INDEX));
+        return;
+    }
+    const char* s1 = op.t[0].p + id * op.t[0].nb1;
+    const char* s2 = TYPE2 >= 0 ? op.t[2].p + id2 * op.t[2].nb1 : nullptr;
+    for (int64_t j = threadIdx.x * 4; j < op.ne0; j += kThreads * 4) {
+        float4 v = load_table4<TYPE>(s1, j);
+        if constexpr (TYPE2 >= 0) {
+            const float4 q = load_table4<TYPE2>(s2, j);
+            v = make_float4(v.x + q.x, v.y + q.y, v.z + q.z, v.w + q.w);
+        }
+        *reinterpret_cast<float4*>(d + j) = v;
+    }
+}
+
+template <int TYPE, int TYPE2, int NV>
+__device__ __forceinline__ void b_embed_ln_t(const BOp& op, uint32_t lb, uint32_t* err) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = static_cast<int64_t>(lb) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (t >= op.rows) return;   // uniform per wave
+    const int64_t ne0 = op.ne0;
+    const int32_t id = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const int32_t*>(op.t[1].p + t * op.t[1].nb1));
+    const int32_t id2 = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const int32_t*>(op.t[3].p + t * op.t[3].nb1));
+    char* yr = op.t[7].p + t * op.t[7].nb1;
+    char* hr = op.t[6].p ? op.t[6].p + t * op.t[6].nb1 : nullptr;
+    if (id < 0 || id >= op.aux || id2 < 0 || id2 >= op.aux2) {
+        for (int64_t j = lane; j < ne0; j += 64) {
+            reinterpret_cast<float*>(yr)[j] = 0.0f;
+            if (hr) reinterpret_cast<float*>(hr)[j] = 0.0f;
+        }
+        if (lane == 0) atomicOr(err, static_cast<uint32_t>(DEV_ERR_ROW_INDEX));
+        return;
+    }
+    const char* s1 = op.t[0].p + id * op.t[0].nb1;
+    const char* s2 = op.t[2].p + id2 * op.t[2].nb1;
+    const float* w = reinterpret_cast<const float*>(op.t[4].p);
+    const float* b = reinterpret_cast<const float*>(op.t[5].p);
+    Affine<NV> af;
+    af.load(w, b, lane, ne0);
+    float4 p[NV], q[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t j = (lane + 64 * k) * 4;
+        p[k] = load_table4<TYPE>(s1, j < ne0 ? j : 0);
+        q[k] = load_table4<TYPE2>(s2, j < ne0 ? j : 0);
+    }
+    float4 v[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t j = (lane + 64 * k) * 4;
+        if (j < ne0) {
+            v[k] = make_float4(p[k].x + q[k].x, p[k].y + q[k].y, p[k].z + q[k].z, p[k].w + q[k].w);
+            if (hr) *reinterpret_cast<float4*>(hr + j * 4) = v[k];
+        } else {
+            v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    const float scale = wave_row_scale<NV, NORM_LN>(v, lane, ne0, op.eps);
+    wave_row_store<float, NV, false>(v, lane, ne0, scale, af, w != nullptr, b != nullptr, CBX_UNARY_NONE, nullptr,
+                                     yr);
+}
+
+template <int TYPE>
+__device__ __forceinline__ void b_gather_1(const BOp& op, uint32_t lb, uint32_t* err) {
+    if (op.t[2].p == nullptr) b_gather_t<TYPE, -1>(op, lb, err);
+    else if (op.t_x2 == CBX_TYPE_F32) b_gather_t<TYPE, CBX_TYPE_F32>(op, lb, err);
+    else if (op.t_x2 == CBX_TYPE_F16) b_gather_t<TYPE, CBX_TYPE_F16>(op, lb, err);
+    else b_gather_t<TYPE, CBX_TYPE_Q8_0>(op, lb, err);
+}
+
+template <int TYPE, int TYPE2>
+__device__ __forceinline__ void b_embed_nv(const BOp& op, uint32_t lb, uint32_t* err) {
+    switch (op.nv) {
+        case 1: b_embed_ln_t<TYPE, TYPE2, 1>(op, lb, err); break;
+        case 2: b_embed_ln_t<TYPE, TYPE2, 2>(op, lb, err); break;
+        default: b_embed_ln_t<TYPE, TYPE2, 4>(op, lb, err); break;
+    }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void b_embed_1(const BOp& op, uint32_t lb, uint32_t* err) {
+    if (op.t_x2 == CBX_TYPE_F32) b_embed_nv<TYPE, CBX_TYPE_F32>(op, lb, err);
+    else if (op.t_x2 == CBX_TYPE_F16) b_embed_nv<TYPE, CBX_TYPE_F16>(op, lb, err);
+    else b_embed_nv<TYPE, CBX_TYPE_Q8_0>(op, lb, err);
+}
+
+// ---- the batch kernel ------------------------------------------------------------------
+// The op list is read in place from the kernel-argument segment (the
+// pointer's origin lets the compiler use scalar constant loads); indexing the
+// by-value parameter with a run-time index would copy all of it to scratch.
+__global__ __launch_bounds__(kThreads) void k_batch(BatchArgs args) {
+    (void)args;
+    __shared__ float2 cs[kRopeMaxHalf];
+    const BatchArgs* a = (const BatchArgs*)(const void*)__builtin_amdgcn_kernarg_segment_ptr();
+    const uint32_t b = blockIdx.x;
+    const int n = a->n;
+    int i = 0;
+    while (i + 1 < n && b >= a->op[i + 1].blk0) i++;
+    const BOp& op = a->op[i];
+    const uint32_t lb = b - op.blk0;
+    uint32_t* err = a->err;
+    const uint16_t* tab = reinterpret_cast<const uint16_t*>(op.table);
+    switch (op.kind) {
+        case CBX_OP_LAYER_NORM:
+        case CBX_OP_RMS_NORM:
+            b_norm(op, lb, tab);
+            break;
+        case CBX_OP_UNARY:
+        case CBX_OP_LEAKY_RELU:
+            if (op.t_x == CBX_TYPE_F16) b_unary_t<uint16_t>(op, lb, tab);
+            else b_unary_t<float>(op, lb, tab);
+            break;
+        case CBX_OP_SWIGLU:
+            if (op.t_x == CBX_TYPE_F16) b_swiglu_t<uint16_t>(op, lb);
+            else b_swiglu_t<float>(op, lb);
+            break;
+        case CBX_OP_ROPE:
+            if (op.t_x == CBX_TYPE_F16) b_rope_t<uint16_t>(op, lb, cs);
+            else b_rope_t<float>(op, lb, cs);
+            break;
+        case CBX_OP_GET_ROWS:
+            if (op.t_x == CBX_TYPE_F32) b_gather_1<CBX_TYPE_F32>(op, lb, err);
+            else if (op.t_x == CBX_TYPE_F16) b_gather_1<CBX_TYPE_F16>(op, lb, err);
+            else b_gather_1<CBX_TYPE_Q8_0>(op, lb, err);
+            break;
+        case CBX_OP_GET_ROWS_ADD_LAYER_NORM:
+            if (op.t_x == CBX_TYPE_F32) b_embed_1<CBX_TYPE_F32>(op, lb, err);
+            else if (op.t_x == CBX_TYPE_F16) b_embed_1<CBX_TYPE_F16>(op, lb, err);
+            else b_embed_1<CBX_TYPE_Q8_0>(op, lb, err);
+            break;
+        case CBX_OP_SNAKE:
+            b_snake(op, lb);
+            break;
+        default:
+            break;
+    }
+}
+
+}  // namespace
+
+int launch_batch(const BatchArgs& a, uint32_t total_blocks, hipStream_t s) {
+    hipLaunchKernelGGL(k_batch, dim3(total_blocks), dim3(kThreads), 0, s, a);
+    return check_launch("run_ops");
+}
+
+}  // namespace cbx

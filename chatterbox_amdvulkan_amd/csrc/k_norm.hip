@@ -17,93 +17,12 @@
 // two reductions are wave-local (DPP), with no LDS or barrier.  Other rows
 // take one workgroup per row (LDS combine), and rows past 8192 elements a
 // three-pass loop.
-#include "cbx_device.h"
+#include "cbx_rowops.h"
 
 namespace cbx {
 namespace {
 
 constexpr int kMaxThreads = 256;
-
-// ---------------------------------------------------------------------------
-// wave-per-row building blocks
-// ---------------------------------------------------------------------------
-
-// Normalisation scale of the row held in v (lane owns elements
-// (lane + 64k)*4 .. +3); for LN, v is replaced by v - mean.
-template <int NV, int KIND>
-__device__ __forceinline__ float wave_row_scale(float4 (&v)[NV], int lane, int64_t ne0, float eps) {
-    double s = 0.0;
-#pragma unroll
-    for (int k = 0; k < NV; k++) {
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float t = get(v[k], e);
-            if constexpr (KIND == NORM_LN) s += static_cast<double>(t);
-            else s += static_cast<double>(t * t);
-        }
-    }
-    s = wave_sum(s);
-    if constexpr (KIND == NORM_LN) {
-        const float mean = static_cast<float>(s) / static_cast<float>(ne0);
-        double s2 = 0.0;
-#pragma unroll
-        for (int k = 0; k < NV; k++) {
-            if ((lane + 64 * k) * 4 < ne0) {
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float d = get(v[k], e) - mean;
-                    set(v[k], e, d);
-                    s2 += static_cast<double>(d * d);
-                }
-            }
-        }
-        s2 = wave_sum(s2);
-        const float var = static_cast<float>(s2 / static_cast<double>(ne0));
-        return 1.0f / sqrtf(var + eps);
-    } else {
-        const float ms = static_cast<float>(s / static_cast<double>(ne0));
-        return 1.0f / sqrtf(ms + eps);
-    }
-}
-
-// Affine vectors for the lane's elements, loaded up front (uniform branches:
-// the loads overlap the row loads instead of stalling the epilogue).
-template <int NV>
-struct Affine {
-    float4 w[NV], b[NV];
-    __device__ __forceinline__ void load(const float* __restrict__ wp, const float* __restrict__ bp, int lane,
-                                         int64_t ne0) {
-#pragma unroll
-        for (int k = 0; k < NV; k++) {
-            const int64_t j = (lane + 64 * k) * 4;
-            const int64_t jc = j < ne0 ? j : 0;
-            if (wp) w[k] = *reinterpret_cast<const float4*>(wp + jc);
-            if (bp) b[k] = *reinterpret_cast<const float4*>(bp + jc);
-        }
-    }
-};
-
-template <typename TO, int NV, bool ACT>
-__device__ __forceinline__ void wave_row_store(const float4 (&v)[NV], int lane, int64_t ne0, float scale,
-                                               const Affine<NV>& af, bool hw, bool hb, int act,
-                                               const uint16_t* __restrict__ tab, char* yr) {
-#pragma unroll
-    for (int k = 0; k < NV; k++) {
-        const int64_t j = (lane + 64 * k) * 4;
-        if (j < ne0) {
-            float4 o;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float t = get(v[k], e) * scale;
-                if (hw) t = t * get(af.w[k], e);
-                if (hb) t = t + get(af.b[k], e);
-                if constexpr (ACT) t = apply_act(act, t, tab, 0.0f);
-                set(o, e, t);
-            }
-            Elt<TO>::store4(yr + j * Elt<TO>::size, o);
-        }
-    }
-}
 
 template <typename T, int NV, int KIND, bool ACT>
 __global__ __launch_bounds__(kMaxThreads) void k_row_norm_wave(View x, View y, const float* __restrict__ w,
@@ -141,21 +60,6 @@ __global__ __launch_bounds__(kMaxThreads) void k_row_norm_wave(View x, View y, c
 // add, t3.cpp:446-455), optionally stored, then y = LN(h)*w + b
 // (t3.cpp:465-466) -- one wave per token.
 // ---------------------------------------------------------------------------
-
-template <int TYPE>
-__device__ __forceinline__ float4 load_table4(const char* row, int64_t j) {
-    if constexpr (TYPE == CBX_TYPE_F32) {
-        return *reinterpret_cast<const float4*>(row + j * 4);
-    } else if constexpr (TYPE == CBX_TYPE_F16) {
-        return Elt<uint16_t>::load4(row + j * 2);
-    } else {
-        const char* blk = row + (j >> 5) * 34;
-        const float d = h2f(*reinterpret_cast<const uint16_t*>(blk));
-        const int8_t* q = reinterpret_cast<const int8_t*>(blk + 2 + (j & 31));
-        return make_float4(static_cast<float>(q[0]) * d, static_cast<float>(q[1]) * d,
-                           static_cast<float>(q[2]) * d, static_cast<float>(q[3]) * d);
-    }
-}
 
 struct EmbedArgs {
     View src, ids, src2, ids2, h, y;

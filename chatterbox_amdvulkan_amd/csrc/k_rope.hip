@@ -11,30 +11,10 @@
 // A position outside the table's range is computed on the device with the
 // same recurrence (theta <- theta * theta_scale, one f32 multiply per pair)
 // and the device's cosf/sinf.
-#include "cbx_device.h"
+#include "cbx_rowops.h"
 
 namespace cbx {
 namespace {
-
-__device__ void rope_cos_sin_dev(int32_t p, int k, const RopeParams& rp, const float* __restrict__ ff, float* c,
-                                 float* s) {
-    float theta = static_cast<float>(p);
-    for (int i = 0; i < k; i++) theta = theta * rp.theta_scale;
-    const float theta_extrap = ff ? theta / ff[k] : theta;
-    const float theta_interp = rp.freq_scale * theta_extrap;
-    float th = theta_interp;
-    float mscale = rp.attn_factor;
-    if (rp.ext_factor != 0.0f) {
-        const float d = rp.corr_dims[1] - rp.corr_dims[0];
-        const float y = (static_cast<float>(k) - rp.corr_dims[0]) / (d > 0.001f ? d : 0.001f);
-        const float cl = y < 0.0f ? 0.0f : y;
-        const float ramp_mix = (1.0f - (cl < 1.0f ? cl : 1.0f)) * rp.ext_factor;
-        th = theta_interp * (1 - ramp_mix) + theta_extrap * ramp_mix;
-        mscale = mscale * (1.0f + 0.1f * logf(1.0f / rp.freq_scale));
-    }
-    *c = cosf(th) * mscale;
-    *s = sinf(th) * mscale;
-}
 
 template <typename T, int MODE>
 __global__ __launch_bounds__(256) void k_rope(View x, View y, const char* __restrict__ pos, int64_t pos_nb0,

@@ -109,3 +109,114 @@ def prefill_bytes(f16_table: bool = False, fused: bool = True) -> dict:
     if fused:
         return {"embed_layer_norm": rows_in + affine + 2 * act, "gelu": gelu}
     return {"gather_pos": rows_in + act, "layer_norm": 2 * act + affine, "gelu": gelu}
+
+
+QK8_0, Q8_0_BLOCK = 32, 34
+
+
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    """float32 [rows, k] -> uint8 [rows, k/32*34] Q8_0 blocks (f16 scale
+    d = amax/127, then q = round(x/d) half away from zero).  Builds synthetic
+    tables only; what the kernels must reproduce exactly is the dequant."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    b = x.reshape(rows, k // QK8_0, QK8_0)
+    d = (np.abs(b).max(axis=2) / np.float32(127.0)).astype(np.float32)
+    inv = np.divide(np.float32(1.0), d, out=np.zeros_like(d), where=d != 0)
+    v = b * inv[:, :, None]
+    q = np.clip(np.trunc(v + np.copysign(np.float32(0.5), v)), -128, 127).astype(np.int8)
+    out = np.empty((rows, k // QK8_0, Q8_0_BLOCK), dtype=np.uint8)
+    out[:, :, :2] = d.astype(np.float16).view(np.uint8).reshape(rows, k // QK8_0, 2)
+    out[:, :, 2:] = q.view(np.uint8)
+    return out.reshape(rows, k // QK8_0 * Q8_0_BLOCK)
+
+
+# ---- workload 1: T3 decode step ------------------------------------------------
+
+DECODE_STEPS, N_HEAD, HEAD_DIM = 30, 16, 64
+
+
+def decode_inputs(step: int) -> dict:
+    """Inputs of decode step `step` (RoPE position = step)."""
+    w = 1
+    return {
+        "x": normal(seed_of(w, 0) + step, (1, D_MODEL)),
+        "g": normal(seed_of(w, 1), (D_MODEL,), 1.0, 0.02),
+        "q": normal(seed_of(w, 2) + 97 * step, (1, N_HEAD, HEAD_DIM)),
+        "k": normal(seed_of(w, 3) + 97 * step, (1, N_HEAD, HEAD_DIM)),
+        "pos": np.array([step], dtype=np.int32),
+        "gate": normal(seed_of(w, 5) + step, (1, D_FF)),
+        "up": normal(seed_of(w, 6) + step, (1, D_FF)),
+    }
+
+
+def decode_bytes() -> dict:
+    return {"rms_norm_mul": 3 * D_MODEL * 4, "rope_qk": 4 * N_HEAD * HEAD_DIM * 4, "swiglu": 3 * D_FF * 4}
+
+
+# ---- workload 5: 64-stream decode, f16 storage -------------------------------
+
+N_STREAMS = 64
+
+
+def serving_inputs() -> dict:
+    w = 5
+    return {
+        "tab": quantize_q8_0(normal(seed_of(w, 0), (VOCAB, D_MODEL), 0.0, 0.02)),
+        "ids": randint(seed_of(w, 1), (N_STREAMS,), 0, VOCAB),
+        "x": normal(seed_of(w, 2), (N_STREAMS, D_MODEL)).astype(np.float16),
+        "g": normal(seed_of(w, 3), (D_MODEL,), 1.0, 0.02),
+        "q": normal(seed_of(w, 4), (N_STREAMS, N_HEAD, HEAD_DIM)).astype(np.float16),
+        "pos": randint(seed_of(w, 5), (N_STREAMS,), 0, 2048),
+        "k": normal(seed_of(w, 6), (N_STREAMS, N_HEAD, HEAD_DIM)).astype(np.float16),
+        "gate": normal(seed_of(w, 7), (N_STREAMS, D_FF)).astype(np.float16),
+        "up": normal(seed_of(w, 8), (N_STREAMS, D_FF)).astype(np.float16),
+    }
+
+
+def serving_bytes() -> dict:
+    act = N_STREAMS * D_MODEL * 2
+    qk = N_STREAMS * N_HEAD * HEAD_DIM * 2
+    return {"rms_norm_mul": 2 * act + D_MODEL * 4,
+            "rope_qk": 4 * qk + N_STREAMS * 4,
+            "swiglu": 3 * N_STREAMS * D_FF * 2,
+            "get_rows_q8_0": N_STREAMS * (D_MODEL // QK8_0 * Q8_0_BLOCK) + N_STREAMS * 4 + N_STREAMS * D_MODEL * 4}
+
+
+# ---- workload 3: CFM estimator ops ----------------------------------------------
+
+CFM_GROUPS, CFM_T, CFM_HEADS = 8, 500, 8
+
+
+def cfm_inputs() -> dict:
+    """GroupNorm inputs in torch order [2, C, 1, T] (ggml ne (T, 1, C, 2)):
+    the group statistics run over C/8 channels x T frames of one batch item."""
+    w = 3
+    return {
+        "x256": normal(seed_of(w, 0), (2, 256, 1, CFM_T)),
+        "w256": normal(seed_of(w, 1), (1, 256, 1, 1), 1.0, 0.02),
+        "b256": normal(seed_of(w, 2), (1, 256, 1, 1), 0.0, 0.02),
+        "x512": normal(seed_of(w, 3), (2, 512, 1, CFM_T)),
+        "w512": normal(seed_of(w, 4), (1, 512, 1, 1), 1.0, 0.02),
+        "b512": normal(seed_of(w, 5), (1, 512, 1, 1), 0.0, 0.02),
+        "xa": normal(seed_of(w, 6), (2, CFM_T, CFM_HEADS * HEAD_DIM)),
+        "wa": normal(seed_of(w, 7), (CFM_HEADS * HEAD_DIM,), 1.0, 0.02),
+        "ba": normal(seed_of(w, 8), (CFM_HEADS * HEAD_DIM,), 0.0, 0.02),
+        "pos": np.arange(CFM_T, dtype=np.int32),
+    }
+
+
+def cfm_bytes() -> dict:
+    return {"group_norm_mish_256": 2 * 2 * 256 * CFM_T * 4 + 2 * 256 * 4,
+            "group_norm_mish_512": 2 * 2 * 512 * CFM_T * 4 + 2 * 512 * 4,
+            "layer_norm_rope": 2 * 2 * CFM_T * CFM_HEADS * HEAD_DIM * 4 + 2 * CFM_HEADS * HEAD_DIM * 4}
+
+
+# ---- workload 4: HiFT activations -----------------------------------------------
+
+HIFT_SHAPES = ((1, 256, 6000), (1, 128, 48000), (1, 64, 120000), (16, 64, 120000))   # (B, C, T)
+
+
+def snake_alpha(C: int, tensor: int = 1):
+    a = uniform_range(seed_of(4, tensor), (C,), 0.5, 1.5)
+    return a, (np.float32(1.0) / (a + np.float32(1e-9))).astype(np.float32)

@@ -197,6 +197,55 @@ int cbx_swiglu(const cbx_tensor* g, const cbx_tensor* u, cbx_tensor* y,
 int cbx_snake(const cbx_tensor* x, const cbx_tensor* alpha,
               const cbx_tensor* alpha_inv, cbx_tensor* y, cbx_stream stream);
 
+/* ---- one launch for several independent ops ------------------------------ */
+
+/* A ggml graph step often holds several small ops that do not depend on
+ * each other (RoPE on q and on k, s3enc.cpp:217-226; a decode step's norm,
+ * rotary and gate ops); each as its own kernel pays a fixed launch cost
+ * larger than its work.  cbx_run_ops runs up to CBX_MAX_OPS of them in one
+ * kernel launch, workgroup ranges mapped to ops, with the same results as
+ * the single-op entry points.  No counterpart in ggml's API: it is the
+ * launch-level analogue of the scheduler running several graph nodes.     */
+typedef enum cbx_op_kind {
+    CBX_OP_LAYER_NORM              = 1, /* src0 x, src1 w|NULL, src2 b|NULL -> dst0 y; eps, act           */
+    CBX_OP_RMS_NORM                = 2, /* src0 x, src1 g|NULL -> dst0 y; eps                            */
+    CBX_OP_UNARY                   = 3, /* src0 x -> dst0 y; act = the cbx_unary_op                      */
+    CBX_OP_LEAKY_RELU              = 4, /* src0 x -> dst0 y; param = negative slope                      */
+    CBX_OP_SWIGLU                  = 5, /* src0 g, src1 u -> dst0 y                                       */
+    CBX_OP_ROPE                    = 6, /* src0 x, src1 pos -> dst0 y; rope = table                       */
+    CBX_OP_GET_ROWS                = 7, /* src0 table, src1 ids [, src2 table2, src3 ids2: added] -> dst0 */
+    CBX_OP_GET_ROWS_ADD_LAYER_NORM = 8, /* src0..3 as GET_ROWS, src4 w, src5 b -> dst0 h|NULL, dst1 y; eps */
+    CBX_OP_SNAKE                   = 9, /* src0 x, src1 alpha, src2 alpha_inv -> dst0 y                   */
+} cbx_op_kind;
+
+typedef struct cbx_op {
+    int32_t               kind;    /* cbx_op_kind */
+    int32_t               act;     /* cbx_unary_op (CBX_OP_UNARY, CBX_OP_LAYER_NORM epilogue) */
+    float                 eps;
+    float                 param;
+    const cbx_tensor*     src[6];
+    cbx_tensor*           dst[2];
+    const cbx_rope_cache* rope;
+} cbx_op;
+
+#define CBX_MAX_OPS 12
+
+/* Runs ops[0..n_ops) in one kernel launch on `stream`.  The ops must be
+ * independent: no op may write memory that another op of the call reads
+ * or writes (checked on the host; an op's dst may be its own src for the
+ * norms, RoPE and the element-wise ops).  Operands follow the single-op
+ * rules, restricted to the layouts the one-launch kernel handles (anything
+ * else returns CBX_ERR_UNSUPPORTED and launches nothing):
+ *   - rows at one uniform byte stride, nb[0] = element size;
+ *   - norms: ne0 % 4 == 0 and ne0 <= 1024, rows and w/b 16-byte (F32) or
+ *     8-byte (F16) aligned;
+ *   - UNARY / LEAKY_RELU / SWIGLU: contiguous, same alignment, any length;
+ *   - ROPE: n_dims <= 512 (columns n_dims..ne0 are copied, as ggml does);
+ *   - gathers: 1-D ids, 2-D tables, ne0 % 4 == 0 (<= 1024 with LayerNorm),
+ *     F32 destination rows 16-byte aligned;
+ *   - SNAKE: F32, contiguous, 16-byte aligned, ne0 % 4 == 0.              */
+int cbx_run_ops(const cbx_op* ops, int n_ops, cbx_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -44,6 +44,17 @@ def test_ops_before_init_fail_cleanly():
     rc = L.cbx_unary(99, ctypes.byref(t), ctypes.byref(t), None)
     assert rc == C.ERR_INVALID_ARG
     assert "unknown op" in C.last_error()
+    ops = (C.OpStruct * 1)()
+    assert L.cbx_run_ops(ops, 1, None) in (C.ERR_NOT_INITIALIZED, C.ERR_HIP)
+    assert C.last_error()
+
+
+def test_op_struct_layout_matches_header():
+    # struct cbx_op { int32 kind, act; float eps, param; cbx_tensor* src[6], dst[2]; void* rope; }
+    assert C.OpStruct.src.offset == 16 and C.OpStruct.dst.offset == 64 and C.OpStruct.rope.offset == 80
+    assert ctypes.sizeof(C.OpStruct) == 88
+    with pytest.raises(C.CbxError):
+        C.OpBatch([C.Op(C.OP_UNARY)] * (C.MAX_OPS + 1))
 
 
 def test_init_without_gpu_reports_hip_error():

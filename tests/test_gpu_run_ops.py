@@ -1,0 +1,160 @@
+"""cbx_run_ops: several independent ops in one launch must give exactly what
+the single-op entry points give (and hence the oracle's results)."""
+import numpy as np
+import pytest
+import torch
+
+from chatterbox_amdvulkan_amd import workloads as W
+from tests._util import assert_bitexact, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+@pytest.fixture(scope="module")
+def rope64(cbx):
+    c = cbx.RopeCache(64, mode=2, n_ctx_orig=2048, n_pos=2048)
+    yield c
+    c.close()
+
+
+def test_decode_step_one_launch(cbx, oracle, rope64):
+    """T3 decode step: RMSNorm+gamma, RoPE q, RoPE k, SiLU-gate in one launch."""
+    x = W.normal(W.seed_of(1, 0), (1, 1024))
+    g = W.normal(W.seed_of(1, 1), (1024,), 1.0, 0.02)
+    q = W.normal(W.seed_of(1, 2), (1, 16, 64))
+    k = W.normal(W.seed_of(1, 3), (1, 16, 64))
+    pos = np.array([17], dtype=np.int32)
+    gate = W.normal(W.seed_of(1, 5), (1, 4096))
+    up = W.normal(W.seed_of(1, 6), (1, 4096))
+    t = {n: dev(a) for n, a in dict(x=x, g=g, q=q, k=k, pos=pos, gate=gate, up=up).items()}
+    y, qo, ko, h = (torch.empty_like(t["x"]), torch.empty_like(t["q"]), torch.empty_like(t["k"]),
+                    torch.empty_like(t["gate"]))
+    cbx.run_ops([
+        cbx.Op(cbx.OP_RMS_NORM, [t["x"], t["g"]], [y], eps=1e-5),
+        cbx.Op(cbx.OP_ROPE, [t["q"], t["pos"]], [qo], rope=rope64),
+        cbx.Op(cbx.OP_ROPE, [t["k"], t["pos"]], [ko], rope=rope64),
+        cbx.Op(cbx.OP_SWIGLU, [t["gate"], t["up"]], [h]),
+    ])
+    assert_bitexact(host(y), oracle.rms_norm_mul(x, g, 1e-5), "rms")
+    assert_bitexact(host(qo), oracle.rope_ext(q, pos, 64), "rope q")
+    assert_bitexact(host(ko), oracle.rope_ext(k, pos, 64), "rope k")
+    assert_bitexact(host(h), host(cbx.swiglu(t["gate"], t["up"])), "swiglu = single op")
+    assert_close(host(h), oracle.swiglu(gate, up), what="swiglu")
+
+
+def test_serving_step_f16_and_q8(cbx, oracle, rope64):
+    """64 streams, f16 storage: RMSNorm, RoPE q/k at per-stream positions,
+    SiLU-gate, and a Q8_0 embedding gather, in one launch."""
+    x = W.normal(W.seed_of(5, 2), (64, 1024)).astype(np.float16)
+    g = W.normal(W.seed_of(5, 3), (1024,), 1.0, 0.02)
+    q = W.normal(W.seed_of(5, 4), (64, 16, 64)).astype(np.float16)
+    k = W.normal(W.seed_of(5, 6), (64, 16, 64)).astype(np.float16)
+    pos = W.randint(W.seed_of(5, 5), (64,), 0, 2048)
+    gate = W.normal(W.seed_of(5, 7), (64, 4096)).astype(np.float16)
+    up = W.normal(W.seed_of(5, 8), (64, 4096)).astype(np.float16)
+    tab = oracle.quantize_q8_0(W.normal(W.seed_of(5, 0), (W.VOCAB, 1024), 0.0, 0.02))
+    ids = W.randint(W.seed_of(5, 1), (64,), 0, W.VOCAB)
+    t = {n: dev(a) for n, a in dict(x=x, g=g, q=q, k=k, pos=pos, gate=gate, up=up, tab=tab, ids=ids).items()}
+    y, qo, ko, h = (torch.empty_like(t["x"]), torch.empty_like(t["q"]), torch.empty_like(t["k"]),
+                    torch.empty_like(t["gate"]))
+    emb = torch.empty((64, 1024), dtype=torch.float32, device="cuda")
+    cbx.run_ops([
+        cbx.Op(cbx.OP_RMS_NORM, [t["x"], t["g"]], [y], eps=1e-5),
+        cbx.Op(cbx.OP_ROPE, [t["q"], t["pos"]], [qo], rope=rope64),
+        cbx.Op(cbx.OP_ROPE, [t["k"], t["pos"]], [ko], rope=rope64),
+        cbx.Op(cbx.OP_SWIGLU, [t["gate"], t["up"]], [h]),
+        cbx.Op(cbx.OP_GET_ROWS, [t["tab"], t["ids"]], [emb], q8=[0]),
+    ])
+    assert_bitexact(host(y), oracle.rms_norm_mul(x, g, 1e-5), "rms f16")
+    assert_bitexact(host(qo), oracle.rope_ext(q, pos, 64), "rope q f16")
+    assert_bitexact(host(ko), oracle.rope_ext(k, pos, 64), "rope k f16")
+    assert_bitexact(host(h), host(cbx.swiglu(t["gate"], t["up"])), "swiglu f16 = single op")
+    assert_bitexact(host(emb), oracle.get_rows(tab, ids, q8_0=True), "q8 gather")
+
+
+def test_prefill_chain_one_launch(cbx, oracle):
+    inp = W.prefill_inputs()
+    t = {n: dev(inp[n]) for n in ("table", "ids", "pos_table", "pos_ids", "ln_w", "ln_b", "ffn")}
+    h = torch.empty((512, 1024), dtype=torch.float32, device="cuda")
+    y = torch.empty_like(h)
+    g = torch.empty_like(t["ffn"])
+    cbx.run_ops([
+        cbx.Op(cbx.OP_GET_ROWS_ADD_LAYER_NORM, [t["table"], t["ids"], t["pos_table"], t["pos_ids"], t["ln_w"],
+                                                t["ln_b"]], [h, y], eps=1e-5),
+        cbx.Op(cbx.OP_UNARY, [t["ffn"]], [g], act=cbx.GELU),
+    ])
+    h_ref = oracle.get_rows_add(inp["table"], inp["ids"], inp["pos_table"], inp["pos_ids"], nth=8)
+    assert_bitexact(host(h), h_ref, "h")
+    assert_bitexact(host(y), oracle.layer_norm(h_ref, inp["ln_w"], inp["ln_b"], 1e-5, nth=8), "ln")
+    assert_bitexact(host(g), oracle.unary(oracle.GELU, inp["ffn"], nth=8), "gelu")
+
+
+def test_vocoder_ops_and_tails(cbx, oracle):
+    """Snake (both alpha layouts), LeakyReLU, LayerNorm+Mish, unary with a
+    ragged length, gather + add -- together."""
+    xs = W.normal(71, (300, 64))
+    a = W.uniform_range(72, (64,), 0.5, 1.5)
+    ai = (1.0 / (a + np.float32(1e-9))).astype(np.float32)
+    xo = W.normal(73, (48, 1000))
+    ao = W.uniform_range(74, (48, 1), 0.5, 1.5)
+    aio = (1.0 / (ao + np.float32(1e-9))).astype(np.float32)
+    xl = W.normal(75, (3, 1001))
+    xn = W.normal(76, (40, 256))
+    wn = W.normal(77, (256,), 1.0, 0.02)
+    bn = W.normal(78, (256,), 0.0, 0.02)
+    xu = W.normal(79, (1027,), 0.0, 3.0)
+    tb = W.normal(80, (20, 32))
+    tb2 = W.normal(81, (20, 32))
+    ids = np.array([3, 19, 0], dtype=np.int32)
+    ids2 = np.array([1, 2, 3], dtype=np.int32)
+    T = {n: dev(v) for n, v in dict(xs=xs, a=a, ai=ai, xo=xo, ao=ao, aio=aio, xl=xl, xn=xn, wn=wn, bn=bn, xu=xu,
+                                     tb=tb, tb2=tb2, ids=ids, ids2=ids2).items()}
+    out = {n: torch.empty_like(T[s]) for n, s in (("s", "xs"), ("so", "xo"), ("l", "xl"), ("n", "xn"), ("u", "xu"))}
+    out["g"] = torch.empty((3, 32), dtype=torch.float32, device="cuda")
+    cbx.run_ops([
+        cbx.Op(cbx.OP_SNAKE, [T["xs"], T["a"], T["ai"]], [out["s"]]),
+        cbx.Op(cbx.OP_SNAKE, [T["xo"], T["ao"], T["aio"]], [out["so"]]),
+        cbx.Op(cbx.OP_LEAKY_RELU, [T["xl"]], [out["l"]], param=0.1),
+        cbx.Op(cbx.OP_LAYER_NORM, [T["xn"], T["wn"], T["bn"]], [out["n"]], eps=1e-5, act=cbx.MISH),
+        cbx.Op(cbx.OP_UNARY, [T["xu"]], [out["u"]], act=cbx.SILU),
+        cbx.Op(cbx.OP_GET_ROWS, [T["tb"], T["ids"], T["tb2"], T["ids2"]], [out["g"]]),
+    ])
+    assert_bitexact(host(out["s"]), host(cbx.snake(T["xs"], T["a"], T["ai"])), "snake inner = single op")
+    assert_bitexact(host(out["so"]), host(cbx.snake(T["xo"], T["ao"], T["aio"])), "snake outer = single op")
+    assert_close(host(out["s"]), oracle.snake(xs, a, ai), x=xs, what="snake")
+    assert_bitexact(host(out["l"]), oracle.leaky_relu(xl, 0.1), "leaky")
+    ln = oracle.layer_norm(xn, wn, bn, 1e-5)
+    assert_bitexact(host(out["n"]), host(cbx.layer_norm(T["xn"], T["wn"], T["bn"], 1e-5, act=cbx.MISH)), "ln mish")
+    assert_close(host(out["n"]), oracle.unary(oracle.MISH, ln), x=ln, what="ln mish")
+    assert_bitexact(host(out["u"]), host(cbx.silu(T["xu"])), "silu = single op")
+    assert_bitexact(host(out["g"]), oracle.get_rows_add(tb, ids, tb2, ids2), "gather add")
+
+
+def test_rejects_dependent_or_bad_ops(cbx):
+    x = dev(W.normal(82, (4, 256)))
+    y = torch.empty_like(x)
+    z = torch.empty_like(x)
+    with pytest.raises(cbx.CbxError, match="writes memory"):
+        cbx.run_ops([cbx.Op(cbx.OP_UNARY, [x], [y], act=cbx.SILU),
+                     cbx.Op(cbx.OP_UNARY, [y], [z], act=cbx.SILU)])      # second reads what the first writes
+    with pytest.raises(cbx.CbxError):
+        cbx.run_ops([cbx.Op(cbx.OP_UNARY, [x], [y], act=42)])
+    with pytest.raises(cbx.CbxError):
+        cbx.run_ops([cbx.Op(99, [x], [y])])
+    big = dev(W.normal(83, (2, 2048)))
+    with pytest.raises(cbx.CbxError, match="1024"):
+        cbx.run_ops([cbx.Op(cbx.OP_LAYER_NORM, [big], [torch.empty_like(big)], eps=1e-5)])
+    # in place within one element-wise op is allowed
+    x2 = dev(W.normal(84, (1000,)))
+    ref = host(cbx.silu(x2))
+    cbx.run_ops([cbx.Op(cbx.OP_UNARY, [x2], [x2], act=cbx.SILU)])
+    assert_bitexact(host(x2), ref, "in place")
