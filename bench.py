@@ -365,8 +365,9 @@ def bench_serving(C, W, torch, reps=400):
 
 def bench_cfm(C, W, torch, reps=400):
     """CFM estimator ops of one flow step: GroupNorm(8)+affine+Mish on
-    [2,256,500] and [2,512,500], LayerNorm+affine then NEOX RoPE (positions
-    0..499) on [2,500,8x64]; rotating buffer sets."""
+    [2,256,500] and [2,512,500], LayerNorm+affine+NEOX RoPE (positions
+    0..499) on [2,500,8x64] as one fused kernel (also timed as LayerNorm
+    then RoPE); rotating buffer sets."""
     d = dev_of(torch)
     L = C.load()
     cache = C.RopeCache(W.HEAD_DIM, mode=2, n_ctx_orig=2048, n_pos=2048)
@@ -397,19 +398,35 @@ def bench_cfm(C, W, torch, reps=400):
     def rope(st):
         return lambda s: check_rc(C, L.cbx_rope_ext(st[2], st[1]["pos"], cache.handle, st[3], s))
 
+    def ln_rope(st):
+        r = st[1]
+        return lambda s: check_rc(C, L.cbx_layer_norm_rope(r["xa"], r["wa"], r["ba"], 1e-5, W.HEAD_DIM, r["pos"],
+                                                           cache.handle, r["ya_rope"], s))
+
     out = {}
     for name, mk in (("group_norm_mish_256", gn("256")), ("group_norm_mish_512", gn("512")),
-                     ("layer_norm_1024x512", ln), ("rope_2x500x8x64", rope)):
+                     ("layer_norm_1024x512", ln), ("rope_2x500x8x64", rope), ("layer_norm_rope_fused", ln_rope)):
         fns = [mk(st) for st in sets]
         for f in fns:
             f(cur_stream(torch))
         out[name] = {"us": per_launch_ms(torch, fns, reps) * 1000.0}
-    step = lambda st: (lambda s: [mk(st)(s) for mk in (gn("256"), gn("512"), ln, rope)])  # noqa: E731
-    out["flow_step"] = {"us": per_launch_ms(torch, [step(st) for st in sets], reps) * 1000.0}
-    for k, key in (("group_norm_mish_256", "group_norm_mish_256"), ("group_norm_mish_512", "group_norm_mish_512")):
-        out[k]["GBps"] = nb[key] / (out[k]["us"] * 1e-6) / 1e9
+    # the fused kernel must reproduce layer_norm then rope_ext bit for bit
+    torch.cuda.synchronize()
+    fused = sets[0][0]["ya_rope"].cpu().numpy()
+    for f in (ln(sets[0]), rope(sets[0])):
+        f(cur_stream(torch))
+    torch.cuda.synchronize()
+    if not same_bits(fused, sets[0][0]["ya_rope"].cpu().numpy()):
+        raise SystemExit("bench: fused LayerNorm+RoPE differs from LayerNorm then RoPE")
+    step = lambda st: (lambda s: [mk(st)(s) for mk in (gn("256"), gn("512"), ln_rope)])  # noqa: E731
+    out["flow_step"] = {"us": per_launch_ms(torch, [step(st) for st in sets], reps) * 1000.0,
+                        "launches": "group_norm+mish [2,256,500], group_norm+mish [2,512,500], "
+                                    "layer_norm_rope [2,500,512]"}
+    for k in ("group_norm_mish_256", "group_norm_mish_512"):
+        out[k]["GBps"] = nb[k] / (out[k]["us"] * 1e-6) / 1e9
+    out["layer_norm_rope_fused"]["GBps"] = nb["layer_norm_rope"] / (out["layer_norm_rope_fused"]["us"] * 1e-6) / 1e9
     lr = out["layer_norm_1024x512"]["us"] + out["rope_2x500x8x64"]["us"]
-    out["layer_norm_rope_GBps_vs_fused_bytes"] = nb["layer_norm_rope"] / (lr * 1e-6) / 1e9
+    out["layer_norm_then_rope_GBps_vs_fused_bytes"] = nb["layer_norm_rope"] / (lr * 1e-6) / 1e9
     out["flow_step"]["GBps"] = per_step / (out["flow_step"]["us"] * 1e-6) / 1e9
     cache.close()
     return dict(out, bytes_per_flow_step=per_step, bytes=nb, buffer_sets=n_sets)
@@ -504,30 +521,48 @@ def recorded_traffic(key):
 def traffic_probe(C, W, torch):
     """A few launches for counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE):
     a plain f32 copy of 64 MiB (the calibration kernel of known size), then
-    GELU [512,4096] and the fused embedding + LayerNorm on rotating buffer
-    sets.  Prints the expected bytes of each."""
+    GELU [512,4096], the fused embedding + LayerNorm, GroupNorm+Mish
+    [2,512,500] and LayerNorm+RoPE [2,500,512], each on 8 rotating buffer
+    sets.  Prints the algorithmic bytes of each."""
     x = torch.empty(16 << 20, dtype=torch.float32, device="cuda").uniform_()
     ys = [torch.empty_like(x) for _ in range(4)]
     L = C.load()
     s = cur_stream(torch)
     dx = C.ctypes.byref(C.desc(x))
     for y in ys:
-        rc = L.cbx_cpy(dx, C.ctypes.byref(C.desc(y)), s)
-        if rc:
-            raise C.CbxError(rc, C.last_error())
+        check_rc(C, L.cbx_cpy(dx, C.ctypes.byref(C.desc(y)), s))
     torch.cuda.synchronize()
     inp = W.prefill_inputs()
     sets = [PrefillSet(C, W, torch, inp) for _ in range(8)]
     for st in sets:
-        st.gelu(s)
+        check_rc(C, st.gelu(s))
     torch.cuda.synchronize()
     for st in sets:
-        st.embed_layer_norm(s)
+        check_rc(C, st.embed_layer_norm(s))
     torch.cuda.synchronize()
+    d = dev_of(torch)
+    cfm = W.cfm_inputs()
+    cache = C.RopeCache(W.HEAD_DIM, mode=2, n_ctx_orig=2048, n_pos=2048)
+    cfm_sets = []
+    for _ in range(8):
+        t = {k: d(v) for k, v in cfm.items()}
+        t["y512"], t["ya"] = torch.empty_like(t["x512"]), torch.empty_like(t["xa"])
+        cfm_sets.append((t, {k: C.ctypes.byref(C.desc(v)) for k, v in t.items()}))
+    for _, r in cfm_sets:
+        check_rc(C, L.cbx_group_norm(r["x512"], W.CFM_GROUPS, 1e-5, r["w512"], r["b512"], C.MISH, r["y512"], s))
+    torch.cuda.synchronize()
+    for _, r in cfm_sets:
+        check_rc(C, L.cbx_layer_norm_rope(r["xa"], r["wa"], r["ba"], 1e-5, W.HEAD_DIM, r["pos"], cache.handle,
+                                          r["ya"], s))
+    torch.cuda.synchronize()
+    cache.close()
     nb = W.prefill_bytes()
+    cb = W.cfm_bytes()
     print(json.dumps({"copy_bytes_read": x.numel() * 4, "copy_bytes_written": x.numel() * 4,
                       "gelu_bytes_read": nb["gelu"] // 2, "gelu_bytes_written": nb["gelu"] // 2,
-                      "embed_layer_norm_bytes": nb["embed_layer_norm"]}), flush=True)
+                      "embed_layer_norm_bytes": nb["embed_layer_norm"],
+                      "group_norm_mish_512_bytes": cb["group_norm_mish_512"],
+                      "layer_norm_rope_bytes": cb["layer_norm_rope"]}), flush=True)
 
 
 def cpu_baseline(W, seconds):

@@ -30,6 +30,7 @@ SOURCES = [
     "k_norm.hip",
     "k_group_norm.hip",
     "k_rope.hip",
+    "k_norm_rope.hip",
     "k_eltwise.hip",
     "k_batch.hip",
 ]

@@ -110,6 +110,7 @@ def load() -> ctypes.CDLL:
         "cbx_rope_cache_create": (i, [i, i, i, f, f, f, f, f, f, vp, ctypes.c_int32, ctypes.POINTER(vp)]),
         "cbx_rope_cache_destroy": (None, [vp]),
         "cbx_rope_ext": (i, [P, P, vp, P, vp]),
+        "cbx_layer_norm_rope": (i, [P, P, P, f, ctypes.c_int64, P, vp, P, vp]),
         "cbx_unary": (i, [i, P, P, vp]),
         "cbx_gelu": (i, [P, P, vp]),
         "cbx_gelu_erf": (i, [P, P, vp]),
@@ -339,6 +340,17 @@ def rope_ext(x, pos, cache: RopeCache, out=None):
     _ready(x)
     out = _out_like(x, out)
     _check(load().cbx_rope_ext(_ref(desc(x)), _ref(desc(pos)), cache.handle, _ref(desc(out)), _stream()))
+    return out
+
+
+def layer_norm_rope(x, w, b, eps, head_dim, pos, cache: RopeCache, out=None):
+    """LayerNorm+affine of each row of x [batch, n_tok, C], then RoPE of the
+    row viewed as [C/head_dim, head_dim] heads at position pos[token]."""
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_layer_norm_rope(_ref(desc(x)), _ref(desc(w)) if w is not None else None,
+                                      _ref(desc(b)) if b is not None else None, eps, head_dim, _ref(desc(pos)),
+                                      cache.handle, _ref(desc(out)), _stream()))
     return out
 
 

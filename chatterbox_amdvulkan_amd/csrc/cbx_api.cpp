@@ -496,8 +496,9 @@ int cbx_rope_ext(const cbx_tensor* x, const cbx_tensor* pos, const cbx_rope_cach
     if (!st) return rc;
     if (!cache) return set_error(CBX_ERR_INVALID_ARG, "cbx_rope_ext: cache is NULL");
     int dev = 0;
-    hipGetDevice(&dev);
-    if (dev != cache->device) return set_error(CBX_ERR_INVALID_ARG, "cbx_rope_ext: cache belongs to another device");
+    if (hipGetDevice(&dev) != hipSuccess || dev != cache->device) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_rope_ext: cache belongs to another device");
+    }
     if ((rc = check_float(x, what, "x")) || (rc = check_float(y, what, "y")) || (rc = validate(pos, what, "pos"))) return rc;
     if (x->type != y->type) return set_error(CBX_ERR_UNSUPPORTED, "cbx_rope_ext: x and y types differ");
     if (!same_shape(x, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_rope_ext: x and y shapes differ");
@@ -508,6 +509,48 @@ int cbx_rope_ext(const cbx_tensor* x, const cbx_tensor* pos, const cbx_rope_cach
     if (nelements(x) == 0) return CBX_OK;
     return launch_rope(x, pos, cache->p, cache->table, cache->n_pos, cache->freq_factors, y, st,
                        reinterpret_cast<hipStream_t>(stream));
+}
+
+int cbx_layer_norm_rope(const cbx_tensor* x, const cbx_tensor* w, const cbx_tensor* b, float eps, int64_t head_dim,
+                        const cbx_tensor* pos, const cbx_rope_cache* cache, cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_layer_norm_rope";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if (!cache) return set_error(CBX_ERR_INVALID_ARG, "cbx_layer_norm_rope: cache is NULL");
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev != cache->device) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_layer_norm_rope: cache belongs to another device");
+    }
+    if ((rc = validate(x, what, "x")) || (rc = validate(y, what, "y")) || (rc = validate(pos, what, "pos"))) return rc;
+    if (x->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, "cbx_layer_norm_rope: F32 only");
+    if (!same_shape(x, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_layer_norm_rope: x and y shapes differ");
+    if (!(eps >= 0.0f)) return set_error(CBX_ERR_INVALID_ARG, "cbx_layer_norm_rope: eps must be >= 0");
+    if ((rc = check_row_param(w, x, what, "w")) || (rc = check_row_param(b, x, what, "b"))) return rc;
+    if (head_dim <= 0 || head_dim % 4 || x->ne[0] % head_dim) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_layer_norm_rope: head_dim must divide x.ne0 and be a multiple of 4");
+    }
+    if (cache->p.n_dims > head_dim) return set_error(CBX_ERR_INVALID_ARG, "cbx_layer_norm_rope: n_dims > head_dim");
+    if (x->ne[3] != 1) return set_error(CBX_ERR_INVALID_ARG, "cbx_layer_norm_rope: x must be at most 3-D (C, n_tok, batch)");
+    if (pos->type != CBX_TYPE_I32 || pos->ne[0] != x->ne[1] || pos->ne[1] != 1 || pos->ne[2] != 1 || pos->ne[3] != 1) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_layer_norm_rope: pos must be I32 with ne = (x.ne1, 1, 1, 1)");
+    }
+    if (x->ne[0] > 1024 || cache->p.n_dims / 2 > 256 || reinterpret_cast<uintptr_t>(x->data) % 16 ||
+        reinterpret_cast<uintptr_t>(y->data) % 16 || (w && reinterpret_cast<uintptr_t>(w->data) % 16) ||
+        (b && reinterpret_cast<uintptr_t>(b->data) % 16)) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_layer_norm_rope: rows of at most 1024 elements, 16-byte aligned");
+    }
+    for (const cbx_tensor* t : {x, static_cast<const cbx_tensor*>(y)}) {
+        for (int k = 1; k < 4; k++) {
+            if (t->ne[k] > 1 && t->nb[k] % 16) {
+                return set_error(CBX_ERR_UNSUPPORTED, "cbx_layer_norm_rope: row strides must be multiples of 16 bytes");
+            }
+        }
+    }
+    if (nelements(x) == 0) return CBX_OK;
+    return launch_layer_norm_rope(x, w, b, eps, head_dim, pos, cache->p, cache->table, cache->n_pos,
+                                  cache->freq_factors, y, st, reinterpret_cast<hipStream_t>(stream));
 }
 
 // ---- activations -------------------------------------------------------------
@@ -687,8 +730,9 @@ int build_op(int i, const cbx_op& o, BOp& b, DeviceState* st, int64_t* nblk) {
             const cbx_rope_cache* c = o.rope;
             if (!c) return batch_fail(i, CBX_ERR_INVALID_ARG, "rope is NULL");
             int dev = 0;
-            hipGetDevice(&dev);
-            if (dev != c->device) return batch_fail(i, CBX_ERR_INVALID_ARG, "rope table belongs to another device");
+            if (hipGetDevice(&dev) != hipSuccess || dev != c->device) {
+                return batch_fail(i, CBX_ERR_INVALID_ARG, "rope table belongs to another device");
+            }
             if ((rc = check_float(x, what, "x")) || (rc = check_float(y, what, "y")) || (rc = validate(pos, what, "pos"))) return rc;
             if (x->type != y->type || !same_shape(x, y)) return batch_fail(i, CBX_ERR_INVALID_ARG, "x and y differ in type or shape");
             if (pos->type != CBX_TYPE_I32 || pos->ne[0] != x->ne[2] || nelements(pos) != pos->ne[0]) {

@@ -164,46 +164,66 @@ __device__ __forceinline__ float act_gelu_erf(float x) {
     return 0.5f * x * (1.0f + erff(x * CBX_SQRT_2_INV));
 }
 // ggml_gelu (f32): x <= -10 -> 0, x >= 10 -> x, else the fp16 table entry
-// of h = f16(x) (the table cbx_init uploads).  This form reads the table
-// in global memory; the streaming GELU kernel stages it in LDS instead.
+// of h = f16(x) (the table cbx_init uploads), read from global memory.
 __device__ __forceinline__ float act_gelu_tab(const uint16_t* __restrict__ tab, float x) {
     if (x <= -10.0f) return 0.0f;
     if (x >= 10.0f) return x;
     return h2f(tab[f2h(x)]);
 }
 
-// The same function without a gather per element.  For |x| < 10 the
-// result is a function of h = f16(x) alone; it is evaluated here with the
-// table's f32 formula but a fast tanh (1 - 2/(2^(2a log2 e) + 1) with the
-// hardware exp2 and reciprocal), and the f16 rounding of that value is kept
-// when it lies more than a margin of 32/(1 + t) + 8 ulps from an f16
-// rounding midpoint -- the fast tanh is within ~20 ulps of 1 of the exact
-// one, which moves g by at most ~20/(1 + t) ulps.  Otherwise (1 + t < 1/64,
-// f16-subnormal g, or too close to a midpoint) the exact table entry is
-// used; lanes that do not need it all read entry 0, so the load touches a
-// single cache line in the common case.  Because the result depends on h
-// only, running every f16 code through this function checks it for every
-// input.
-#define CBX_GELU_COEF_A 0.044715f
-#define CBX_SQRT_2_OVER_PI 0.79788456080286535587989211986876f
+// The same function with the table read only where it is needed.  For
+// |x| < 10 the result is a function of h = f16(x) alone.  With
+// E = 2^(xf (K1 + K2 xf^2)) = e^(2a), a = sqrt(2/pi) xf (1 + 0.044715 xf^2),
+// the table's 0.5 xf (1 + tanh a) equals xf (1 - 1/(E + 1)); that is
+// evaluated with the hardware exp2 and reciprocal (q = 1 - r is within
+// ~2 ulps of 1 absolute, i.e. ~2/q ulps of g relative, plus ~8 ulps from
+// the rounding of the exponent), and the f16 rounding of g is kept when g
+// lies more than 8 + 16/q f32 ulps from an f16 rounding midpoint.  Otherwise
+// (q < 1/128, f16-subnormal g, or too close to a midpoint) the exact table
+// entry is used; lanes that do not need it all read entry 0, so the load
+// touches a single cache line in the common case.  Because the result
+// depends on h only, running every f16 code through this function checks it
+// for every input.
+#define CBX_GELU_K1 2.3022081983f          // 2 sqrt(2/pi) log2(e)
+#define CBX_GELU_K2 0.10294324967f         // K1 * 0.044715
 
-__device__ __forceinline__ float act_gelu_fast(const uint16_t* __restrict__ tab, float x) {
+struct GeluPart {
+    uint32_t idx;   // table entry to read: h, or 0 when g's rounding is sure
+    float    g;     // (idx 0 also stands for "sure": for h = 0 both are +0)
+};
+
+__device__ __forceinline__ GeluPart gelu_part(float x) {
     const uint32_t h = f2h(x);
     const float xf = h2f(static_cast<uint16_t>(h));
-    const float inner = 1.0f + CBX_GELU_COEF_A * xf * xf;
-    const float a = CBX_SQRT_2_OVER_PI * xf * inner;
-    const float e = __builtin_amdgcn_exp2f(a * 2.8853900817779268f);
-    const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-    const float opt = 1.0f + t;
-    const float g = 0.5f * xf * opt;
+    const float w = xf * (CBX_GELU_K2 * (xf * xf) + CBX_GELU_K1);
+    const float r = __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(w) + 1.0f);
+    const float q = 1.0f - r;
+    const float g = xf * q;
     const uint32_t gb = __builtin_bit_cast(uint32_t, g) & 0x7fffffffu;
     const float dist = __builtin_fabsf(static_cast<float>(static_cast<int32_t>(gb & 0x1fffu) - 0x1000));
-    // dist > 32/opt + 8  <=>  (dist - 8) * opt > 32   (opt > 0)
-    const bool sure = opt >= 0.015625f && gb >= 0x38800000u && (dist - 8.0f) * opt > 32.0f;
-    const uint16_t tv = tab[sure ? 0u : h];
-    float r = sure ? h2f(f2h(g)) : h2f(tv);
+    // bitwise & keeps this branch-free, so the table loads of several
+    // elements issue together
+    const bool sure = (q >= 0.0078125f) & (gb >= 0x38800000u) & ((dist - 8.0f) * q > 16.0f);
+    return GeluPart{sure ? 0u : h, g};
+}
+
+__device__ __forceinline__ float gelu_finish(float x, const GeluPart& p, uint16_t tv) {
+    float r = p.idx == 0u ? h2f(f2h(p.g)) : h2f(tv);
     r = x <= -10.0f ? 0.0f : r;
     return x >= 10.0f ? x : r;
+}
+
+__device__ __forceinline__ float act_gelu_fast(const uint16_t* __restrict__ tab, float x) {
+    const GeluPart p = gelu_part(x);
+    return gelu_finish(x, p, tab[p.idx]);
+}
+
+// Four elements: the arithmetic first, then the four table reads together.
+__device__ __forceinline__ float4 act_gelu_fast4(const uint16_t* __restrict__ tab, float4 x) {
+    const GeluPart p0 = gelu_part(x.x), p1 = gelu_part(x.y), p2 = gelu_part(x.z), p3 = gelu_part(x.w);
+    const uint16_t t0 = tab[p0.idx], t1 = tab[p1.idx], t2 = tab[p2.idx], t3 = tab[p3.idx];
+    return make_float4(gelu_finish(x.x, p0, t0), gelu_finish(x.y, p1, t1), gelu_finish(x.z, p2, t2),
+                       gelu_finish(x.w, p3, t3));
 }
 
 // ---- row addressing --------------------------------------------------------

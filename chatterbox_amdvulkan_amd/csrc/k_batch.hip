@@ -91,10 +91,14 @@ __device__ __forceinline__ void b_unary_t(const BOp& op, uint32_t lb, const uint
         } else {
             const float4 v = Stream<T>::load4(x + i * 4 * es);
             float4 o;
-            o.x = b_unary1(fn, v.x, tab, op.param);
-            o.y = b_unary1(fn, v.y, tab, op.param);
-            o.z = b_unary1(fn, v.z, tab, op.param);
-            o.w = b_unary1(fn, v.w, tab, op.param);
+            if (fn == CBX_UNARY_GELU) {
+                o = act_gelu_fast4(tab, v);
+            } else {
+                o.x = b_unary1(fn, v.x, tab, op.param);
+                o.y = b_unary1(fn, v.y, tab, op.param);
+                o.z = b_unary1(fn, v.z, tab, op.param);
+                o.w = b_unary1(fn, v.w, tab, op.param);
+            }
             Stream<T>::store4(y + i * 4 * es, o);
         }
     } else if (i == n4) {

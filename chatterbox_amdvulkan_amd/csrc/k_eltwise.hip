@@ -64,10 +64,14 @@ __global__ __launch_bounds__(kThreads) void k_unary(const char* __restrict__ x, 
         } else {
             const float4 v = Stream<T>::load4(x + i * 4 * Elt<T>::size);
             float4 o;
-            o.x = unary_op<OP>(v.x, tab, param);
-            o.y = unary_op<OP>(v.y, tab, param);
-            o.z = unary_op<OP>(v.z, tab, param);
-            o.w = unary_op<OP>(v.w, tab, param);
+            if constexpr (OP == CBX_UNARY_GELU) {
+                o = act_gelu_fast4(tab, v);
+            } else {
+                o.x = unary_op<OP>(v.x, tab, param);
+                o.y = unary_op<OP>(v.y, tab, param);
+                o.z = unary_op<OP>(v.z, tab, param);
+                o.w = unary_op<OP>(v.w, tab, param);
+            }
             Stream<T>::store4(y + i * 4 * Elt<T>::size, o);
         }
     } else if (i == n4) {

@@ -8,14 +8,17 @@
 //   var = (float)(sum_f64 (v*v) / count); y = v * (1/sqrtf(var + eps)),
 // then y*w[c], +b[c], activation -- each rounded to f32.
 //
-// One 1024-lane workgroup per (batch, group); the group (up to 64K
-// elements) stays in registers between the two reductions and the store.
+// Groups of up to 64K elements stay in registers between the two
+// reductions; larger ones take three passes over memory.
+#include <algorithm>
+
 #include "cbx_device.h"
 
 namespace cbx {
 namespace {
 
 constexpr int kThreads = 1024;
+constexpr uint32_t kXcds = 8;   // gfx950: workgroups go to XCD (index % 8)
 
 struct GnArgs {
     View x, y;
@@ -39,7 +42,8 @@ __device__ __forceinline__ int64_t gn_offset(const View& t, int64_t e, int64_t c
     return i0 * 4 + i1 * t.nb[1] + (c0 + c) * t.nb[2] + i3 * t.nb[3];
 }
 
-template <int NV, bool ACT, bool VEC>
+// Strided layouts: each lane gathers its 4 elements one by one.
+template <int NV, bool ACT>
 __global__ __launch_bounds__(kThreads) void k_group_norm(GnArgs a) {
     __shared__ double red[kThreads / WAVE];
     const int64_t C = a.x.ne[2];
@@ -50,41 +54,22 @@ __global__ __launch_bounds__(kThreads) void k_group_norm(GnArgs a) {
     if (c0 >= c1) return;   // uniform across the workgroup
     const int64_t count = a.x.ne[0] * a.x.ne[1] * (c1 - c0);
 
-    // VEC: the group is one contiguous run of count floats (x and y), read
-    // with unconditional 16-byte loads (clamped addresses) so all NV are in
-    // flight together; per_ch floats per channel.
-    const char* xg = a.x.data + c0 * a.x.nb[2] + i3 * a.x.nb[3];
-    char* yg = a.y.data + c0 * a.y.nb[2] + i3 * a.y.nb[3];
-    const uint32_t per_ch = static_cast<uint32_t>(a.x.ne[0] * a.x.ne[1]);
     float4 v[NV];
-    int64_t ch[NV];
     double s = 0.0;
 #pragma unroll
     for (int k = 0; k < NV; k++) {
         const int64_t e = (threadIdx.x + static_cast<int64_t>(k) * blockDim.x) * 4;
-        if constexpr (VEC) {
-            v[k] = *reinterpret_cast<const float4*>(xg + 4 * (e < count ? e : 0));
-        } else {
-            if (e < count) {
-                for (int q = 0; q < 4; q++) {
-                    int64_t chq;
-                    const int64_t oq = gn_offset(a.x, e + q, c0, i3, &chq);
-                    set(v[k], q, e + q < count ? *reinterpret_cast<const float*>(a.x.data + oq) : 0.0f);
-                }
-            } else {
-                v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (e < count) {
+            for (int q = 0; q < 4; q++) {
+                int64_t chq;
+                const int64_t oq = gn_offset(a.x, e + q, c0, i3, &chq);
+                set(v[k], q, e + q < count ? *reinterpret_cast<const float*>(a.x.data + oq) : 0.0f);
             }
         }
     }
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        const int64_t e = (threadIdx.x + static_cast<int64_t>(k) * blockDim.x) * 4;
-        if constexpr (VEC) {
-            if (e >= count) v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-            ch[k] = c0 + static_cast<uint32_t>(e < count ? e : 0) / per_ch;
-        } else {
-            ch[k] = 0;
-        }
 #pragma unroll
         for (int q = 0; q < 4; q++) s += static_cast<double>(get(v[k], q));
     }
@@ -111,28 +96,118 @@ __global__ __launch_bounds__(kThreads) void k_group_norm(GnArgs a) {
     for (int k = 0; k < NV; k++) {
         const int64_t e = (threadIdx.x + static_cast<int64_t>(k) * blockDim.x) * 4;
         if (e >= count) continue;
-        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            if (e + q >= count) continue;   // scalar tail of the last vector
-            int64_t c = ch[k];
-            if constexpr (!VEC) gn_offset(a.y, e + q, c0, i3, &c);
+            if (e + q >= count) continue;
+            int64_t c;
+            const int64_t oy = gn_offset(a.y, e + q, c0, i3, &c);
             float t = get(v[k], q) * scale;
             if (a.w) t = t * a.w[c];
             if (a.b) t = t + a.b[c];
             if constexpr (ACT) t = apply_act(a.act, t, a.tab, 0.0f);
-            set(o, q, t);
+            *reinterpret_cast<float*>(a.y.data + oy) = t;
         }
-        if constexpr (VEC) {
-            *reinterpret_cast<float4*>(yg + 4 * e) = o;
-        } else {
-            for (int q = 0; q < 4; q++) {
-                if (e + q < count) {
-                    int64_t cy;
-                    *reinterpret_cast<float*>(a.y.data + gn_offset(a.y, e + q, c0, i3, &cy)) = get(o, q);
-                }
-            }
+    }
+}
+
+// y of 4 elements of channel c, given d = x - mean.
+template <bool ACT>
+__device__ __forceinline__ float4 gn_apply4(const GnArgs& a, float4 d, float scale, int64_t c) {
+    float4 o;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        float t = get(d, q) * scale;
+        if (a.w) t = t * a.w[c];
+        if (a.b) t = t + a.b[c];
+        if constexpr (ACT) t = apply_act(a.act, t, a.tab, 0.0f);
+        set(o, q, t);
+    }
+    return o;
+}
+
+// Contiguous groups (ne0 % 4 == 0, ne0 x ne1 dense per channel, channels
+// adjacent, 16-byte aligned), split over n_chunks workgroups per group so a
+// few large groups still fill the chip.  Every workgroup of a group reads
+// the whole group into registers and computes the same statistics (same
+// lanes, same order: bit-identical mean and scale), then writes only its
+// chunk.  Workgroups are dealt to the 8 XCDs round-robin by index, so the
+// chunks of one group are given indices that land on one XCD: its L2 serves
+// the repeated reads of the group and HBM sees it once.  With one chunk the
+// output comes straight from registers.
+template <int NV, bool ACT>
+__global__ __launch_bounds__(kThreads) void k_group_norm_vec(GnArgs a, uint32_t n_chunks, uint32_t n_gi) {
+    __shared__ double red[kThreads / WAVE];
+    const uint32_t b = blockIdx.x;
+    const uint32_t j = b / kXcds;
+    const uint32_t m = j / n_chunks;
+    const uint32_t ci = j - m * n_chunks;
+    const uint32_t gi = b % kXcds + kXcds * m;
+    if (gi >= n_gi) return;   // uniform across the workgroup
+    const int64_t C = a.x.ne[2];
+    const int64_t g = gi % a.n_groups;
+    const int64_t i3 = gi / a.n_groups;
+    const int64_t c0 = g * a.cpg;
+    const int64_t c1 = c0 + a.cpg < C ? c0 + a.cpg : C;
+    if (c0 >= c1) return;
+    const int64_t count = a.x.ne[0] * a.x.ne[1] * (c1 - c0);
+    const char* xg = a.x.data + c0 * a.x.nb[2] + i3 * a.x.nb[3];
+    char* yg = a.y.data + c0 * a.y.nb[2] + i3 * a.y.nb[3];
+    const uint32_t per_ch = static_cast<uint32_t>(a.x.ne[0] * a.x.ne[1]);
+
+    // unconditional 16-byte loads (clamped addresses) keep all NV in flight
+    float4 v[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t e = (threadIdx.x + static_cast<int64_t>(k) * kThreads) * 4;
+        v[k] = *reinterpret_cast<const float4*>(xg + 4 * (e < count ? e : 0));
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t e = (threadIdx.x + static_cast<int64_t>(k) * kThreads) * 4;
+        if (e >= count) v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int q = 0; q < 4; q++) s += static_cast<double>(get(v[k], q));
+    }
+    s = block_sum(s, red);
+    const float mean = static_cast<float>(s / static_cast<double>(count));
+    double s2 = 0.0;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t e = (threadIdx.x + static_cast<int64_t>(k) * kThreads) * 4;
+        if (e < count) {   // count % 4 == 0: a vector is all in or all out
+            const float4 d = make_float4(v[k].x - mean, v[k].y - mean, v[k].z - mean, v[k].w - mean);
+            v[k] = d;
+            s2 += static_cast<double>(d.x * d.x);
+            s2 += static_cast<double>(d.y * d.y);
+            s2 += static_cast<double>(d.z * d.z);
+            s2 += static_cast<double>(d.w * d.w);
         }
+    }
+    s2 = block_sum(s2, red);
+    const float var = static_cast<float>(s2 / static_cast<double>(count));
+    const float scale = 1.0f / sqrtf(var + a.eps);
+
+    if (n_chunks == 1) {
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int64_t e = (threadIdx.x + static_cast<int64_t>(k) * kThreads) * 4;
+            if (e >= count) continue;
+            const int64_t c = c0 + static_cast<uint32_t>(e) / per_ch;
+            *reinterpret_cast<float4*>(yg + 4 * e) = gn_apply4<ACT>(a, v[k], scale, c);
+        }
+        return;
+    }
+    // this workgroup's chunk, re-read from L2 with one vector per lane
+    const int64_t n4 = count / 4;
+    const int64_t per = (n4 + n_chunks - 1) / n_chunks;
+    const int64_t q0 = ci * per;
+    const int64_t q1 = q0 + per < n4 ? q0 + per : n4;
+    for (int64_t q = q0 + threadIdx.x; q < q1; q += kThreads) {
+        const float4 xv = *reinterpret_cast<const float4*>(xg + 16 * q);
+        const float4 d = make_float4(xv.x - mean, xv.y - mean, xv.z - mean, xv.w - mean);
+        const int64_t c = c0 + static_cast<uint32_t>(4 * q) / per_ch;
+        Stream<float>::store4(yg + 16 * q, gn_apply4<ACT>(a, d, scale, c));
     }
 }
 
@@ -173,15 +248,27 @@ __global__ __launch_bounds__(kThreads) void k_group_norm_loop(GnArgs a) {
     }
 }
 
-template <bool ACT, bool VEC>
+template <bool ACT>
 void gn_nv(const GnArgs& a, int nv, dim3 grid, hipStream_t s) {
     switch (nv) {
-        case 1: hipLaunchKernelGGL((k_group_norm<1, ACT, VEC>), grid, dim3(kThreads), 0, s, a); break;
-        case 2: hipLaunchKernelGGL((k_group_norm<2, ACT, VEC>), grid, dim3(kThreads), 0, s, a); break;
-        case 4: hipLaunchKernelGGL((k_group_norm<4, ACT, VEC>), grid, dim3(kThreads), 0, s, a); break;
-        case 8: hipLaunchKernelGGL((k_group_norm<8, ACT, VEC>), grid, dim3(kThreads), 0, s, a); break;
-        case 16: hipLaunchKernelGGL((k_group_norm<16, ACT, VEC>), grid, dim3(kThreads), 0, s, a); break;
+        case 1: hipLaunchKernelGGL((k_group_norm<1, ACT>), grid, dim3(kThreads), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((k_group_norm<2, ACT>), grid, dim3(kThreads), 0, s, a); break;
+        case 4: hipLaunchKernelGGL((k_group_norm<4, ACT>), grid, dim3(kThreads), 0, s, a); break;
+        case 8: hipLaunchKernelGGL((k_group_norm<8, ACT>), grid, dim3(kThreads), 0, s, a); break;
+        case 16: hipLaunchKernelGGL((k_group_norm<16, ACT>), grid, dim3(kThreads), 0, s, a); break;
         default: hipLaunchKernelGGL((k_group_norm_loop<ACT>), grid, dim3(kThreads), 0, s, a); break;
+    }
+}
+
+template <bool ACT>
+void gn_vec(const GnArgs& a, int nv, uint32_t n_chunks, uint32_t n_gi, hipStream_t s) {
+    const dim3 grid(kXcds * ((n_gi + kXcds - 1) / kXcds) * n_chunks);
+    switch (nv) {
+        case 1: hipLaunchKernelGGL((k_group_norm_vec<1, ACT>), grid, dim3(kThreads), 0, s, a, n_chunks, n_gi); break;
+        case 2: hipLaunchKernelGGL((k_group_norm_vec<2, ACT>), grid, dim3(kThreads), 0, s, a, n_chunks, n_gi); break;
+        case 4: hipLaunchKernelGGL((k_group_norm_vec<4, ACT>), grid, dim3(kThreads), 0, s, a, n_chunks, n_gi); break;
+        case 8: hipLaunchKernelGGL((k_group_norm_vec<8, ACT>), grid, dim3(kThreads), 0, s, a, n_chunks, n_gi); break;
+        default: hipLaunchKernelGGL((k_group_norm_vec<16, ACT>), grid, dim3(kThreads), 0, s, a, n_chunks, n_gi); break;
     }
 }
 
@@ -213,12 +300,24 @@ int launch_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_te
     const int nv = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : need <= 16 ? 16 : 0;
     const int64_t nblocks = int64_t{n_groups} * x->ne[3];
     if (nblocks > (int64_t{1} << 30)) return set_error(CBX_ERR_UNSUPPORTED, "group_norm: too many groups");
-    const dim3 grid(static_cast<unsigned>(nblocks));
     const bool act_on = a.act != CBX_UNARY_NONE;
-    if (act_on && vec) gn_nv<true, true>(a, nv, grid, s);
-    else if (act_on) gn_nv<true, false>(a, nv, grid, s);
-    else if (vec) gn_nv<false, true>(a, nv, grid, s);
-    else gn_nv<false, false>(a, nv, grid, s);
+    if (vec && nv != 0) {
+        // chunks per group: about two workgroups per CU in all, each chunk
+        // at least 1024 elements, at most 16 (each chunk re-reads the
+        // group).  In place, one chunk: a group is read whole before any of
+        // it is written only when one workgroup owns it.
+        const int64_t want = cdiv(int64_t{2} * st->n_cu, nblocks);
+        int64_t n_chunks = std::max<int64_t>(1, std::min<int64_t>({want, cdiv(count, 1024), int64_t{16}}));
+        const uintptr_t xl = reinterpret_cast<uintptr_t>(x->data), yl = reinterpret_cast<uintptr_t>(y->data);
+        const size_t span = static_cast<size_t>(x->ne[3]) * x->nb[3];
+        if (xl < yl + span && yl < xl + span) n_chunks = 1;
+        if (act_on) gn_vec<true>(a, nv, static_cast<uint32_t>(n_chunks), static_cast<uint32_t>(nblocks), s);
+        else gn_vec<false>(a, nv, static_cast<uint32_t>(n_chunks), static_cast<uint32_t>(nblocks), s);
+        return check_launch("group_norm");
+    }
+    const dim3 grid(static_cast<unsigned>(nblocks));
+    if (act_on) gn_nv<true>(a, nv, grid, s);
+    else gn_nv<false>(a, nv, grid, s);
     return check_launch("group_norm");
 }
 

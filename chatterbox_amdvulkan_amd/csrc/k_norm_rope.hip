@@ -1,0 +1,196 @@
+// k_norm_rope.hip -- LayerNorm (+ affine) of each token row followed by
+// RoPE of the row viewed as heads, in one read and one write:
+//
+//   t = ggml_add(ggml_mul(ggml_norm(x, eps), w), b)          x ne = (C, T, B)
+//   y = ggml_rope_ext(ggml_reshape_4d(t, hd, C/hd, T, B), pos, ...)
+//
+// the norm -> attention-input chain of a CFM/S3 transformer block when the
+// rotary embedding is applied to the normalised stream (ggml composition of
+// cfm_decoder.cpp:29-33 and s3enc.cpp:215-229).
+//
+// One wave per token row (C <= 1024): the row is normalised in registers
+// exactly as the standalone LayerNorm does (same lanes, same f64 wave
+// reductions, same rounding order), the normalised row goes to LDS, and
+// each lane then rotates its own 4-element vectors, reading the partner
+// elements from there and the cos/sin of its elements from the table row of
+// the token's position.  Rotation arithmetic is the standalone RoPE's.
+#include "cbx_rowops.h"
+
+namespace cbx {
+namespace {
+
+constexpr int kRowMax = 1024;
+
+struct NormRopeArgs {
+    View x, y;
+    const float* w;
+    const float* b;
+    float eps;
+    int64_t hd;            // head size (rotation row length)
+    const char* pos;
+    int64_t pos_nb0;
+    RopeParams rp;
+    const float2* table;
+    int32_t n_pos;
+    const float* ff;
+    bool fx, fy;           // uniform row strides
+};
+
+// Table slot (pair index) of head-local element i, or -1 past n_dims.
+template <int MODE>
+__device__ __forceinline__ int pair_of(int i, int nd, int half) {
+    if (i >= nd) return -1;
+    if constexpr (MODE == 2) return i < half ? i : i - half;
+    return i >> 1;
+}
+
+template <int NV, int MODE>
+__global__ __launch_bounds__(64) void k_layer_norm_rope(NormRopeArgs a) {
+    __shared__ float row[kRowMax];
+    const int lane = threadIdx.x;
+    const int64_t r = blockIdx.x;                 // token row over ne1 * ne2
+    const int64_t ne0 = a.x.ne[0];
+    const char* xr = a.x.data + row_offset(a.x, r, a.fx);
+    char* yr = a.y.data + row_offset(a.y, r, a.fy);
+    const int nd = a.rp.n_dims, half = nd / 2;
+
+    // position of the token (ne1 index of x); the row and affine loads go
+    // out first, then the cos/sin of each of the lane's elements (table rows
+    // are L2-resident), so the table latency hides under the row loads
+    const int64_t tok = r % a.x.ne[1];
+    const int32_t p = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const int32_t*>(a.pos + tok * a.pos_nb0));
+    Affine<NV> af;
+    af.load(a.w, a.b, lane, ne0);
+    float4 v[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t j = (lane + 64 * k) * 4;
+        v[k] = Elt<float>::load4(xr + (j < ne0 ? j : 0) * 4);
+    }
+    float2 cs[NV][4];
+    int i0[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t j = (lane + 64 * k) * 4;
+        const int64_t jc = j < ne0 ? j : 0;
+        // hd % 4 == 0: the vector sits in one head (32-bit: jc < 1024)
+        i0[k] = static_cast<int>(static_cast<uint32_t>(jc) % static_cast<uint32_t>(a.hd));
+    }
+    if (p >= 0 && p < a.n_pos) {   // uniform
+        const float2* tr = a.table + static_cast<int64_t>(p) * half;
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = pair_of<MODE>(i0[k] + e, nd, half);
+                cs[k][e] = m >= 0 ? tr[m] : make_float2(0.f, 0.f);
+            }
+        }
+    } else {   // positions past the table: the device recurrence
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = pair_of<MODE>(i0[k] + e, nd, half);
+                cs[k][e] = make_float2(0.f, 0.f);
+                if (m >= 0) rope_cos_sin_dev(p, m, a.rp, a.ff, &cs[k][e].x, &cs[k][e].y);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        if ((lane + 64 * k) * 4 >= ne0) v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const float scale = wave_row_scale<NV, NORM_LN>(v, lane, ne0, a.eps);
+    const bool hw = a.w != nullptr, hb = a.b != nullptr;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t j = (lane + 64 * k) * 4;
+        if (j < ne0) {
+            float4 o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float t = get(v[k], e) * scale;
+                if (hw) t = t * get(af.w[k], e);
+                if (hb) t = t + get(af.b[k], e);
+                set(o, e, t);
+            }
+            v[k] = o;
+            *reinterpret_cast<float4*>(&row[j]) = o;
+        }
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t j = (lane + 64 * k) * 4;
+        if (j >= ne0) continue;
+        const int64_t h0 = j - i0[k];             // first element of the head
+        float4 o = v[k];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int i = i0[k] + e;
+            if (i >= nd) continue;                // past n_dims: copied
+            const float2 c = cs[k][e];
+            if constexpr (MODE == 2) {
+                if (i < half) {
+                    const float x0 = get(v[k], e), x1 = row[h0 + i + half];
+                    set(o, e, x0 * c.x - x1 * c.y);
+                } else {
+                    const float x0 = row[h0 + i - half], x1 = get(v[k], e);
+                    set(o, e, x0 * c.y + x1 * c.x);
+                }
+            } else {
+                if ((i & 1) == 0) {
+                    const float x0 = get(v[k], e), x1 = row[h0 + i + 1];
+                    set(o, e, x0 * c.x - x1 * c.y);
+                } else {
+                    const float x0 = row[h0 + i - 1], x1 = get(v[k], e);
+                    set(o, e, x0 * c.y + x1 * c.x);
+                }
+            }
+        }
+        Elt<float>::store4(yr + j * 4, o);
+    }
+}
+
+template <int MODE>
+void go(const NormRopeArgs& a, int nv, dim3 grid, hipStream_t s) {
+    switch (nv) {
+        case 1: hipLaunchKernelGGL((k_layer_norm_rope<1, MODE>), grid, dim3(64), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((k_layer_norm_rope<2, MODE>), grid, dim3(64), 0, s, a); break;
+        default: hipLaunchKernelGGL((k_layer_norm_rope<4, MODE>), grid, dim3(64), 0, s, a); break;
+    }
+}
+
+}  // namespace
+
+int launch_layer_norm_rope(const cbx_tensor* x, const cbx_tensor* w, const cbx_tensor* b, float eps, int64_t head_dim,
+                           const cbx_tensor* pos, const RopeParams& p, const float2* table, int32_t n_pos,
+                           const float* ff, cbx_tensor* y, DeviceState* st, hipStream_t s) {
+    (void)st;
+    NormRopeArgs a;
+    a.x = view_of(x);
+    a.y = view_of(y);
+    a.w = w ? static_cast<const float*>(w->data) : nullptr;
+    a.b = b ? static_cast<const float*>(b->data) : nullptr;
+    a.eps = eps;
+    a.hd = head_dim;
+    a.pos = static_cast<const char*>(pos->data);
+    a.pos_nb0 = static_cast<int64_t>(pos->nb[0]);
+    a.rp = p;
+    a.table = table;
+    a.n_pos = n_pos;
+    a.ff = ff;
+    a.fx = flat_rows(x);
+    a.fy = flat_rows(y);
+    const int64_t rows = x->ne[1] * x->ne[2] * x->ne[3];
+    if (rows >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "layer_norm_rope: too many rows");
+    const int nv = x->ne[0] <= 256 ? 1 : x->ne[0] <= 512 ? 2 : 4;
+    const dim3 grid(static_cast<unsigned>(rows));
+    if (p.mode == 2) go<2>(a, nv, grid, s);
+    else go<0>(a, nv, grid, s);
+    return check_launch("layer_norm_rope");
+}
+
+}  // namespace cbx

@@ -171,6 +171,19 @@ int cbx_rope_ext(const cbx_tensor* x, const cbx_tensor* pos,
                  const cbx_rope_cache* cache, cbx_tensor* y,
                  cbx_stream stream);
 
+/* LayerNorm + affine of each token row, then RoPE of the row viewed as
+ * heads, in one pass:
+ *   ggml_rope_ext(ggml_reshape_4d(layer_norm(x, w, b, eps), head_dim,
+ *                 x.ne0/head_dim, x.ne1, x.ne2), pos, NULL, ...cache...)
+ * (layer_norm as cfm_decoder.cpp:29-33, rope as s3enc.cpp:215-229).
+ * x, y: F32, ne = (C, n_tok, batch, 1) with C <= 1024, C % head_dim == 0,
+ * head_dim % 4 == 0, n_dims <= head_dim; pos: I32 [n_tok]; w, b as for
+ * cbx_layer_norm.  Same results as cbx_layer_norm then cbx_rope_ext.       */
+int cbx_layer_norm_rope(const cbx_tensor* x, const cbx_tensor* w,
+                        const cbx_tensor* b, float eps, int64_t head_dim,
+                        const cbx_tensor* pos, const cbx_rope_cache* cache,
+                        cbx_tensor* y, cbx_stream stream);
+
 /* ---- activations -------------------------------------------------------- */
 
 /* One ggml unary op (cbx_unary_op), F32 or F16, x and y same shape. */

@@ -40,9 +40,9 @@ def test_gelu_all_codes_and_edges(cbx, oracle):
     assert_bitexact(host(cbx.gelu(dev(x))), oracle.unary(oracle.GELU, x), "gelu f32 edges")
 
 
-def test_gelu_lds_path_all_codes(cbx, oracle):
-    """Tensors of >= 2^18 elements take the LDS-staged table: every f16 code
-    as an f32 input, shuffled, plus the clamps, in a ragged length."""
+def test_gelu_large_all_codes(cbx, oracle):
+    """A large tensor (full grid of workgroups): every f16 code as an f32
+    input, shuffled, plus the clamps, in a ragged length."""
     codes = np.arange(65536, dtype=np.uint16).view(np.float16).astype(np.float32)
     codes = codes[~np.isnan(codes)]
     rng = np.random.default_rng(7)

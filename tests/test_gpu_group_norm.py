@@ -51,3 +51,29 @@ def test_one_group_equals_layer_norm(cbx, oracle):
     got = host(cbx.group_norm(dev(x), 1, 1e-5)).reshape(3, -1)
     ln = oracle.norm(x.reshape(3, -1), 1e-5)
     assert_close(got, ln, what="gn(1) vs ln")
+
+
+@pytest.mark.parametrize("shape,groups", [((2, 10, 1, 2048), 3), ((1, 6, 1, 1024), 4), ((3, 48, 2, 256), 2),
+                                          ((1, 8, 1, 8192), 8), ((16, 64, 1, 100), 8)])
+def test_group_norm_split_over_workgroups(cbx, oracle, shape, groups):
+    """Contiguous groups few enough to be split over several workgroups:
+    ragged last groups, an empty trailing group, batches, and the
+    many-groups case that keeps one workgroup per group.  Affine + Mish."""
+    x = W.normal(63 + shape[1] + shape[-1], shape, 0.5, 2.0)
+    C = shape[1]
+    w = W.normal(64, (1, C, 1, 1), 1.0, 0.1)
+    b = W.normal(65, (1, C, 1, 1), 0.0, 0.1)
+    gn = oracle.group_norm_affine(x, groups, 1e-5, w, b, False, nth=8)
+    assert_bitexact(host(cbx.group_norm(dev(x), groups, 1e-5, dev(w), dev(b))), gn, f"gn {shape}/{groups}")
+    got = host(cbx.group_norm(dev(x), groups, 1e-5, dev(w), dev(b), act=cbx.MISH))
+    assert_close(got, oracle.group_norm_affine(x, groups, 1e-5, w, b, True, nth=8), x=gn, what="gn+mish")
+
+
+def test_group_norm_in_place(cbx, oracle):
+    """y == x: every group is read whole before any of it is written."""
+    x = W.normal(W.seed_of(3, 0) + 512, (2, 512, 1, 500))
+    w = W.normal(W.seed_of(3, 1) + 512, (1, 512, 1, 1), 1.0, 0.02)
+    b = W.normal(W.seed_of(3, 2) + 512, (1, 512, 1, 1), 0.0, 0.02)
+    t = dev(x)
+    cbx.group_norm(t, 8, 1e-5, dev(w), dev(b), out=t)
+    assert_bitexact(host(t), oracle.group_norm_affine(x, 8, 1e-5, w, b, False, nth=8), "in place")

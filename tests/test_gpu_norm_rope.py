@@ -1,0 +1,83 @@
+"""cbx_layer_norm_rope (LayerNorm+affine, then RoPE of the row viewed as
+heads) vs the oracle's layer_norm followed by its rope_ext, and vs the two
+standalone entry points."""
+import numpy as np
+import pytest
+import torch
+
+from chatterbox_amdvulkan_amd import workloads as W
+from tests._util import assert_bitexact, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def test_cfm_shape(cbx, oracle):
+    """[2, 500, 8 heads x 64], positions 0..499, NEOX, theta 10000."""
+    inp = W.cfm_inputs()
+    x, w, b, pos = inp["xa"], inp["wa"], inp["ba"], inp["pos"]
+    cache = cbx.RopeCache(64, mode=2, n_ctx_orig=2048, n_pos=2048)
+    got = host(cbx.layer_norm_rope(dev(x), dev(w), dev(b), 1e-5, 64, dev(pos), cache))
+    ln = oracle.layer_norm(x, w, b, 1e-5, nth=8)
+    exp = oracle.rope_ext(ln.reshape(2, W.CFM_T, 8, 64), pos, 64, mode=2, nth=8).reshape(x.shape)
+    assert_bitexact(got, exp, "ln+rope")
+    two = cbx.rope_ext(cbx.layer_norm(dev(x), dev(w), dev(b), 1e-5).view(2, W.CFM_T, 8, 64), dev(pos), cache)
+    assert_bitexact(got, host(two).reshape(x.shape), "= layer_norm then rope_ext")
+    cache.close()
+
+
+@pytest.mark.parametrize("C,hd,n_dims,mode", [(256, 64, 64, 2), (1024, 128, 96, 2), (512, 64, 32, 0),
+                                              (192, 64, 64, 0), (64, 32, 16, 2), (1000, 40, 40, 2)])
+def test_shapes_modes_partial_dims(cbx, oracle, C, hd, n_dims, mode):
+    """Row widths for every vector count, NORMAL and NEOX pairs, rotation of
+    only the first n_dims of each head (the rest copied), ragged C."""
+    T, B = 37, 2
+    x = W.normal(90 + C, (B, T, C), 0.3, 2.0)
+    w = W.normal(91, (C,), 1.0, 0.05)
+    b = W.normal(92, (C,), 0.0, 0.05)
+    pos = W.randint(93, (T,), 0, 4096)
+    cache = cbx.RopeCache(n_dims, mode=mode, n_ctx_orig=4096, freq_base=10000.0, n_pos=4096)
+    got = host(cbx.layer_norm_rope(dev(x), dev(w), dev(b), 1e-5, hd, dev(pos), cache))
+    ln = oracle.layer_norm(x, w, b, 1e-5)
+    exp = oracle.rope_ext(ln.reshape(B, T, C // hd, hd), pos, n_dims, mode=mode, n_ctx_orig=4096).reshape(x.shape)
+    assert_bitexact(got, exp, f"ln+rope C={C} hd={hd} n_dims={n_dims} mode={mode}")
+    cache.close()
+
+
+def test_no_affine_in_place_and_positions_past_table(cbx, oracle):
+    """w = b = NULL; y == x; positions beyond the table's rows use the device
+    recurrence exactly as cbx_rope_ext does."""
+    x = W.normal(94, (3, 20, 256))
+    pos = np.arange(50, 70, dtype=np.int32)
+    cache = cbx.RopeCache(64, mode=2, n_ctx_orig=2048, n_pos=60)
+    t = dev(x)
+    cbx.layer_norm_rope(t, None, None, 1e-12, 64, dev(pos), cache, out=t)
+    two = cbx.rope_ext(cbx.layer_norm(dev(x), None, None, 1e-12).view(3, 20, 4, 64), dev(pos), cache)
+    assert_bitexact(host(t), host(two).reshape(x.shape), "in place, fallback positions")
+    ln = oracle.layer_norm(x, None, None, 1e-12)
+    exp = oracle.rope_ext(ln.reshape(3, 20, 4, 64), pos, 64, mode=2).reshape(x.shape)
+    assert_close(host(t), exp, x=ln, what="vs oracle")
+    cache.close()
+
+
+def test_rejects_bad_shapes(cbx):
+    x = dev(W.normal(95, (2, 8, 256)))
+    pos = dev(np.arange(8, dtype=np.int32))
+    cache = cbx.RopeCache(64, mode=2, n_pos=64)
+    with pytest.raises(cbx.CbxError, match="head_dim"):
+        cbx.layer_norm_rope(x, None, None, 1e-5, 48, pos, cache)          # does not divide 256
+    big = cbx.RopeCache(128, mode=2, n_pos=64)
+    with pytest.raises(cbx.CbxError, match="n_dims"):
+        cbx.layer_norm_rope(x, None, None, 1e-5, 64, pos, big)
+    with pytest.raises(cbx.CbxError, match="pos"):
+        cbx.layer_norm_rope(x, None, None, 1e-5, 64, dev(np.arange(7, dtype=np.int32)), cache)
+    cache.close()
+    big.close()

@@ -158,3 +158,16 @@ def test_rejects_dependent_or_bad_ops(cbx):
     ref = host(cbx.silu(x2))
     cbx.run_ops([cbx.Op(cbx.OP_UNARY, [x2], [x2], act=cbx.SILU)])
     assert_bitexact(host(x2), ref, "in place")
+
+
+def test_gelu_all_codes_in_batch(cbx, oracle):
+    """The batched GELU (f32 and f16) at every f16 code and the clamps."""
+    codes = np.arange(65536, dtype=np.uint16).view(np.float16)
+    x32 = codes.astype(np.float32)
+    x32 = np.concatenate([x32[~np.isnan(x32)], np.array([-10.0, 10.0, np.nextafter(-10, 0), np.nextafter(10, 0)],
+                                                        dtype=np.float32)])
+    a, b = dev(x32), dev(codes)
+    ya, yb = torch.empty_like(a), torch.empty_like(b)
+    cbx.run_ops([cbx.Op(cbx.OP_UNARY, [a], [ya], act=cbx.GELU), cbx.Op(cbx.OP_UNARY, [b], [yb], act=cbx.GELU)])
+    assert_bitexact(host(ya), oracle.unary(oracle.GELU, x32), "batched gelu f32")
+    assert_bitexact(host(yb), oracle.unary(oracle.GELU, codes), "batched gelu f16")
