@@ -502,7 +502,7 @@ def bench_copy_ceiling(C, torch, sizes, reps=400):
     return out
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gelu_512x4096_and_embed_ln_traffic.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_gelu_embedln_groupnorm_lnrope.md")
 
 
 def recorded_traffic(key):
