@@ -432,6 +432,34 @@ def bench_cfm(C, W, torch, reps=400):
     return dict(out, bytes_per_flow_step=per_step, bytes=nb, buffer_sets=n_sets)
 
 
+def bench_softmax(C, W, torch, reps=200):
+    """Attention-score epilogue (scale -> diag_mask_inf -> soft_max, one
+    kernel): T3 prefill scores [16 heads, 512, 512] with the causal mask, and
+    CFM scores [2, 8 heads, 500, 500] without; rotating buffer sets."""
+    L = C.load()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(W.seed_of(6, 0))
+    out = {}
+    for name, shape, sc, n_past in (("t3_prefill_causal_16x512x512", (16, 512, 512), 0.125, 0),
+                                    ("cfm_2x8x500x500", (2, 8, 500, 500), 0.125, -1)):
+        n = int(np.prod(shape))
+        per = 8 * n
+        n_sets = max(2, math.ceil(MALL_DEFEAT_BYTES / per))
+        xs = [torch.empty(shape, dtype=torch.float32, device="cuda").normal_(0.0, 4.0, generator=gen)
+              for _ in range(n_sets)]
+        ys = [torch.empty_like(x) for x in xs]
+        rx = [C.ctypes.byref(C.desc(x)) for x in xs]
+        ry = [C.ctypes.byref(C.desc(y)) for y in ys]
+        fns = [(lambda i: lambda s: check_rc(C, L.cbx_scale_diag_mask_soft_max(rx[i], sc, n_past, ry[i], s)))(i)
+               for i in range(n_sets)]
+        for f in fns:
+            f(cur_stream(torch))
+        ms = per_launch_ms(torch, fns, reps)
+        out[name] = {"us": ms * 1000.0, "bytes": per, "GBps": per / (ms * 1e-3) / 1e9, "buffer_sets": n_sets}
+        del xs, ys
+    return out
+
+
 def bench_hift(C, W, torch, quick=False):
     """HiFT vocoder activations: Snake (channel innermost as the reference
     lays it out, and time innermost) and LeakyReLU(0.1) on every upsample
@@ -635,6 +663,8 @@ def main():
         details["cfm_flow_step"] = bench_cfm(C, W, torch)
         log("hift")
         details["hift_activations"] = bench_hift(C, W, torch)
+        log("softmax")
+        details["attention_softmax"] = bench_softmax(C, W, torch)
     k_ms = res["kernel_ms"]["gelu"]
     k_bytes = res["kernel_bytes"]["gelu"]
     achieved = k_bytes / (k_ms * 1e-3) / 1e9

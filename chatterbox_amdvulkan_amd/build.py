@@ -31,6 +31,7 @@ SOURCES = [
     "k_group_norm.hip",
     "k_rope.hip",
     "k_norm_rope.hip",
+    "k_softmax.hip",
     "k_eltwise.hip",
     "k_batch.hip",
 ]

@@ -111,6 +111,7 @@ def load() -> ctypes.CDLL:
         "cbx_rope_cache_destroy": (None, [vp]),
         "cbx_rope_ext": (i, [P, P, vp, P, vp]),
         "cbx_layer_norm_rope": (i, [P, P, P, f, ctypes.c_int64, P, vp, P, vp]),
+        "cbx_scale_diag_mask_soft_max": (i, [P, f, ctypes.c_int32, P, vp]),
         "cbx_unary": (i, [i, P, P, vp]),
         "cbx_gelu": (i, [P, P, vp]),
         "cbx_gelu_erf": (i, [P, P, vp]),
@@ -351,6 +352,17 @@ def layer_norm_rope(x, w, b, eps, head_dim, pos, cache: RopeCache, out=None):
     _check(load().cbx_layer_norm_rope(_ref(desc(x)), _ref(desc(w)) if w is not None else None,
                                       _ref(desc(b)) if b is not None else None, eps, head_dim, _ref(desc(pos)),
                                       cache.handle, _ref(desc(out)), _stream()))
+    return out
+
+
+# ---- attention-score epilogue ---------------------------------------------------
+
+def scale_diag_mask_soft_max(x, scale=1.0, n_past=-1, out=None):
+    """soft_max(diag_mask_inf(scale(x), n_past)) over the last dim of x
+    [.., n_queries, n_keys]; n_past < 0: no mask."""
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_scale_diag_mask_soft_max(_ref(desc(x)), scale, n_past, _ref(desc(out)), _stream()))
     return out
 
 

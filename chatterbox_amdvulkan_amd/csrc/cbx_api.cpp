@@ -553,6 +553,24 @@ int cbx_layer_norm_rope(const cbx_tensor* x, const cbx_tensor* w, const cbx_tens
                                   cache->freq_factors, y, st, reinterpret_cast<hipStream_t>(stream));
 }
 
+// ---- attention-score epilogue ---------------------------------------------------
+
+int cbx_scale_diag_mask_soft_max(const cbx_tensor* x, float scale, int32_t n_past, cbx_tensor* y,
+                                 cbx_stream stream) {
+    const char* what = "cbx_scale_diag_mask_soft_max";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(x, what, "x")) || (rc = validate(y, what, "y"))) return rc;
+    if (x->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_scale_diag_mask_soft_max: F32 only");
+    }
+    if (!same_shape(x, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_scale_diag_mask_soft_max: x and y shapes differ");
+    if (nelements(x) == 0) return CBX_OK;
+    return launch_soft_max(x, scale, n_past, y, st, reinterpret_cast<hipStream_t>(stream));
+}
+
 // ---- activations -------------------------------------------------------------
 
 static int unary_entry(const char* what, int op, float param, const cbx_tensor* x, cbx_tensor* y,

@@ -1,0 +1,141 @@
+// k_softmax.hip -- the attention-score epilogue in one pass:
+//
+//   y = ggml_soft_max(ggml_diag_mask_inf(ggml_scale(x, s), n_past))
+//
+// (t3.cpp:513-518; without the mask, n_past < 0: cfm_decoder.cpp:218-220,
+// flow_encoder.cpp:371-372, s3enc.cpp:260-262).  Per row of ne0 scores:
+// t = x*s (one f32 multiply), t = -inf where column i > n_past + j (j = the
+// row's ne1 index), m = max t, e = expf(t - m), sum of e in f64,
+// y = e * (float)(1.0 / sum) -- ggml-cpu's scalar order of operations.
+//
+// Rows up to 4096 with ne0 % 4 == 0: one wave per row, the row in
+// registers (one read, one write), the max by a butterfly of lane shuffles
+// (exact in any order), the sum by the f64 DPP butterfly.  Other rows: a
+// workgroup per row, three passes.
+#include "cbx_rowops.h"
+
+namespace cbx {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaveMaxRow = 4096;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// score after scale and mask; columns past the row end read as -inf
+__device__ __forceinline__ float masked(float x, float s, int64_t col, int64_t limit) {
+    return col > limit ? -INFINITY : x * s;
+}
+
+template <int NV>
+__global__ __launch_bounds__(kThreads) void k_soft_max_wave(View x, View y, float s, int64_t n_past, int64_t nr,
+                                                            bool fx, bool fy) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) +
+                      __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (r >= nr) return;   // uniform per wave
+    const int64_t ne0 = x.ne[0];
+    const char* xr = x.data + row_offset(x, r, fx);
+    char* yr = y.data + row_offset(y, r, fy);
+    // last unmasked column of this row
+    const int64_t j = r % x.ne[1];
+    const int64_t lim = n_past >= 0 ? (n_past + j < ne0 - 1 ? n_past + j : ne0 - 1) : ne0 - 1;
+    float4 v[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t c = (lane + 64 * k) * 4;
+        v[k] = Elt<float>::load4(xr + (c < ne0 ? c : 0) * 4);
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t c = (lane + 64 * k) * 4;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float t = masked(get(v[k], e), s, c + e, lim);
+            set(v[k], e, t);
+            m = fmaxf(m, t);
+        }
+    }
+    m = wave_max(m);
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float ev = expf(get(v[k], e) - m);
+            set(v[k], e, ev);
+            sum += static_cast<double>(ev);
+        }
+    }
+    sum = wave_sum(sum);
+    const float inv = static_cast<float>(1.0 / sum);
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t c = (lane + 64 * k) * 4;
+        if (c < ne0) {   // ne0 % 4 == 0: whole vectors
+            Elt<float>::store4(yr + c * 4, make_float4(v[k].x * inv, v[k].y * inv, v[k].z * inv, v[k].w * inv));
+        }
+    }
+}
+
+// Any row length: max, then the f64 sum of exponentials, then the output,
+// each pass over the row (the exponentials are recomputed identically).
+__global__ __launch_bounds__(kThreads) void k_soft_max_loop(View x, View y, float s, int64_t n_past, bool fx,
+                                                            bool fy) {
+    __shared__ double red[kThreads / WAVE];
+    __shared__ float redf[kThreads / WAVE];
+    const int64_t r = blockIdx.x;
+    const int64_t ne0 = x.ne[0];
+    const float* xr = reinterpret_cast<const float*>(x.data + row_offset(x, r, fx));
+    float* yr = reinterpret_cast<float*>(y.data + row_offset(y, r, fy));
+    const int64_t j = r % x.ne[1];
+    const int64_t lim = n_past >= 0 ? (n_past + j < ne0 - 1 ? n_past + j : ne0 - 1) : ne0 - 1;
+    float m = -INFINITY;
+    for (int64_t c = threadIdx.x; c < ne0; c += kThreads) m = fmaxf(m, masked(xr[c], s, c, lim));
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) redf[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = -INFINITY;
+    for (int w = 0; w < kThreads / WAVE; w++) m = fmaxf(m, redf[w]);
+    double sum = 0.0;
+    for (int64_t c = threadIdx.x; c < ne0; c += kThreads) sum += static_cast<double>(expf(masked(xr[c], s, c, lim) - m));
+    sum = block_sum(sum, red);
+    const float inv = static_cast<float>(1.0 / sum);
+    for (int64_t c = threadIdx.x; c < ne0; c += kThreads) yr[c] = expf(masked(xr[c], s, c, lim) - m) * inv;
+}
+
+int waves_for(int64_t rows, const DeviceState* st) { return rows >= int64_t{8} * st->n_cu ? 4 : 1; }
+
+}  // namespace
+
+int launch_soft_max(const cbx_tensor* x, float s, int64_t n_past, cbx_tensor* y, DeviceState* st, hipStream_t strm) {
+    const View vx = view_of(x), vy = view_of(y);
+    const bool fx = flat_rows(x), fy = flat_rows(y);
+    const int64_t nr = nrows(x), ne0 = x->ne[0];
+    const bool vec = ne0 <= kWaveMaxRow && ne0 % 4 == 0 && reinterpret_cast<uintptr_t>(x->data) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(y->data) % 16 == 0 && x->nb[1] % 16 == 0 && y->nb[1] % 16 == 0 &&
+                     (x->ne[2] <= 1 || x->nb[2] % 16 == 0) && (x->ne[3] <= 1 || x->nb[3] % 16 == 0) &&
+                     (y->ne[2] <= 1 || y->nb[2] % 16 == 0) && (y->ne[3] <= 1 || y->nb[3] % 16 == 0);
+    if (nr >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "soft_max: too many rows");
+    if (vec) {
+        const int wpb = waves_for(nr, st);
+        const dim3 grid(static_cast<unsigned>(cdiv(nr, wpb))), block(64 * wpb);
+        const int64_t need = cdiv(ne0, 256);
+        if (need <= 1) hipLaunchKernelGGL((k_soft_max_wave<1>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy);
+        else if (need <= 2) hipLaunchKernelGGL((k_soft_max_wave<2>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy);
+        else if (need <= 4) hipLaunchKernelGGL((k_soft_max_wave<4>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy);
+        else if (need <= 8) hipLaunchKernelGGL((k_soft_max_wave<8>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy);
+        else hipLaunchKernelGGL((k_soft_max_wave<16>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy);
+    } else {
+        hipLaunchKernelGGL(k_soft_max_loop, dim3(static_cast<unsigned>(nr)), dim3(kThreads), 0, strm, vx, vy, s, n_past,
+                           fx, fy);
+    }
+    return check_launch("soft_max");
+}
+
+}  // namespace cbx

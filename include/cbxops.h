@@ -184,6 +184,19 @@ int cbx_layer_norm_rope(const cbx_tensor* x, const cbx_tensor* w,
                         const cbx_tensor* pos, const cbx_rope_cache* cache,
                         cbx_tensor* y, cbx_stream stream);
 
+/* ---- attention-score epilogue ------------------------------------------ */
+
+/* ggml_soft_max(ggml_diag_mask_inf(ggml_scale(x, scale), n_past)) over ne0
+ * in one pass (t3.cpp:513-518: scale 1/sqrt(Hd), causal mask shifted by the
+ * cached positions).  n_past < 0 leaves out the mask:
+ * ggml_soft_max(ggml_scale(x, scale)) (cfm_decoder.cpp:218-220,
+ * flow_encoder.cpp:371-372, s3enc.cpp:260-262).  x, y: F32 with the same
+ * shape, ne = (n_keys, n_queries, n_head, batch); the mask hides key i from
+ * query j (ne1 index) when i > n_past + j.  y may be x.                     */
+int cbx_scale_diag_mask_soft_max(const cbx_tensor* x, float scale,
+                                 int32_t n_past, cbx_tensor* y,
+                                 cbx_stream stream);
+
 /* ---- activations -------------------------------------------------------- */
 
 /* One ggml unary op (cbx_unary_op), F32 or F16, x and y same shape. */

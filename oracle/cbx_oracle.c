@@ -782,3 +782,72 @@ int cbxo_get_rows_add(const cbxo_tensor* src, const cbxo_tensor* ids,
     free_tmp(&b);
     return rc;
 }
+
+/* ggml: ggml_compute_forward_scale_f32 (bias 0) -- copy, then y[i] *= s. */
+int cbxo_scale(const cbxo_tensor* x, float sc, cbxo_tensor* dst, int nth) {
+    if (!same_shape(x, dst) || x->type != CBXO_TYPE_F32 || dst->type != CBXO_TYPE_F32) return -1;
+    const int64_t nr = nrows(x), n = x->ne[0];
+#pragma omp parallel for num_threads(nth) schedule(static, 1)
+    for (int64_t ir = 0; ir < nr; ir++) {
+        int64_t i1, i2, i3;
+        split_row(x, ir, &i1, &i2, &i3);
+        const float* rx = (const float*)row_ptr(x, i1, i2, i3);
+        float* rd = (float*)row_ptr(dst, i1, i2, i3);
+        for (int64_t i = 0; i < n; i++) rd[i] = rx[i] * sc;
+    }
+    return 0;
+}
+
+/* ggml: ggml_compute_forward_diag_mask_f32 with value -INFINITY -- column i
+ * of row j is masked when i > n_past + j (t3.cpp:514-517 relies on this
+ * shift for incremental attention). */
+int cbxo_diag_mask_inf(const cbxo_tensor* x, int n_past, cbxo_tensor* dst, int nth) {
+    if (!same_shape(x, dst) || x->type != CBXO_TYPE_F32 || dst->type != CBXO_TYPE_F32) return -1;
+    if (n_past < 0) return -1;
+    const int64_t nr = nrows(x), n = x->ne[0];
+#pragma omp parallel for num_threads(nth) schedule(static, 1)
+    for (int64_t ir = 0; ir < nr; ir++) {
+        int64_t i1, i2, i3;
+        split_row(x, ir, &i1, &i2, &i3);
+        const float* rx = (const float*)row_ptr(x, i1, i2, i3);
+        float* rd = (float*)row_ptr(dst, i1, i2, i3);
+        for (int64_t i = 0; i < n; i++) rd[i] = i > (int64_t)n_past + i1 ? -INFINITY : rx[i];
+    }
+    return 0;
+}
+
+/* ggml: ggml_compute_forward_soft_max_f32 (scale 1, no mask, no ALiBi) with
+ * the scalar ggml_vec_soft_max_f32: max over the row, e_i = expf(x_i - max)
+ * summed in f64, then every e_i times (float)(1.0 / sum). */
+int cbxo_soft_max(const cbxo_tensor* x, cbxo_tensor* dst, int nth) {
+    if (!same_shape(x, dst) || x->type != CBXO_TYPE_F32 || dst->type != CBXO_TYPE_F32) return -1;
+    const int64_t nr = nrows(x), n = x->ne[0];
+#pragma omp parallel for num_threads(nth) schedule(static, 1)
+    for (int64_t ir = 0; ir < nr; ir++) {
+        int64_t i1, i2, i3;
+        split_row(x, ir, &i1, &i2, &i3);
+        const float* rx = (const float*)row_ptr(x, i1, i2, i3);
+        float* rd = (float*)row_ptr(dst, i1, i2, i3);
+        float mx = -INFINITY;
+        for (int64_t i = 0; i < n; i++) mx = mx > rx[i] ? mx : rx[i];   /* ggml's MAX(max, x) */
+        double sum = 0.0;
+        for (int64_t i = 0; i < n; i++) {
+            const float e = expf(rx[i] - mx);
+            sum += (double)e;
+            rd[i] = e;
+        }
+        const float inv = (float)(1.0 / sum);
+        for (int64_t i = 0; i < n; i++) rd[i] *= inv;
+    }
+    return 0;
+}
+
+int cbxo_scale_diag_mask_soft_max(const cbxo_tensor* x, float sc, int n_past, cbxo_tensor* dst, int nth) {
+    if (!same_shape(x, dst) || x->type != CBXO_TYPE_F32 || dst->type != CBXO_TYPE_F32) return -1;
+    cbxo_tensor t = make_tmp_f32(x);
+    int rc = cbxo_scale(x, sc, &t, nth);
+    if (!rc && n_past >= 0) rc = cbxo_diag_mask_inf(&t, n_past, &t, nth);
+    if (!rc) rc = cbxo_soft_max(&t, dst, nth);
+    free_tmp(&t);
+    return rc;
+}

@@ -115,6 +115,15 @@ int cbxo_rope_ext(const cbxo_tensor* x, const cbxo_tensor* pos,
                   float ext_factor, float attn_factor, float beta_fast,
                   float beta_slow, cbxo_tensor* dst, int n_threads);
 
+/* ggml_scale(x, s): y = x * s, one f32 multiply per element.             */
+int cbxo_scale(const cbxo_tensor* x, float s, cbxo_tensor* dst, int n_threads);
+/* ggml_diag_mask_inf(x, n_past): element i of row j (j = ne1 index) is set
+ * to -INFINITY when i > n_past + j, in every ne2 x ne3 slice.            */
+int cbxo_diag_mask_inf(const cbxo_tensor* x, int n_past, cbxo_tensor* dst, int n_threads);
+/* ggml_soft_max(x) over ne0: m = max, e = expf(x - m), sum in f64,
+ * y = e * (float)(1.0 / sum).                                            */
+int cbxo_soft_max(const cbxo_tensor* x, cbxo_tensor* dst, int n_threads);
+
 /* ---- compositions made by the reference's graph builders --------------- */
 /* layer_norm(): norm -> mul(w) -> add(b)  (cfm_decoder.cpp:29-33,
  * t3.cpp:465-466); w and b may be NULL (plain ggml_norm then).           */
@@ -131,6 +140,11 @@ int cbxo_group_norm_affine(const cbxo_tensor* x, int n_groups, float eps,
 /* snake(): x + sin^2(x*alpha) * alpha_inv (hift_vocoder.cpp:64-73).      */
 int cbxo_snake(const cbxo_tensor* x, const cbxo_tensor* alpha,
                const cbxo_tensor* alpha_inv, cbxo_tensor* dst, int n_threads);
+/* attention scores: soft_max(diag_mask_inf(scale(x, s), n_past))
+ * (t3.cpp:513-518); n_past < 0 leaves out the mask, as the encoders do
+ * (cfm_decoder.cpp:218-220, flow_encoder.cpp:371-372, s3enc.cpp:260-262). */
+int cbxo_scale_diag_mask_soft_max(const cbxo_tensor* x, float s, int n_past,
+                                  cbxo_tensor* dst, int n_threads);
 /* get_rows(tok) + get_rows(pos) (t3.cpp:440-455).                        */
 int cbxo_get_rows_add(const cbxo_tensor* src, const cbxo_tensor* ids,
                       const cbxo_tensor* src2, const cbxo_tensor* ids2,

@@ -72,6 +72,10 @@ def lib():
             "cbxo_group_norm_affine": (i, [P, i, f, P, P, i, P, i]),
             "cbxo_snake": (i, [P, P, P, P, i]),
             "cbxo_get_rows_add": (i, [P, P, P, P, P, i]),
+            "cbxo_scale": (i, [P, f, P, i]),
+            "cbxo_diag_mask_inf": (i, [P, i, P, i]),
+            "cbxo_soft_max": (i, [P, P, i]),
+            "cbxo_scale_diag_mask_soft_max": (i, [P, f, i, P, i]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -304,6 +308,32 @@ def group_norm_affine(x, n_groups, eps, w, b, fuse_mish, nth=1):
                                         _ref(desc(w)) if w is not None else None,
                                         _ref(desc(b)) if b is not None else None,
                                         1 if fuse_mish else 0, _ref(desc(out)), nth), "group_norm_affine")
+    return out
+
+
+def scale(x, s, nth=1):
+    out = np.empty_like(x)
+    _check(lib().cbxo_scale(_ref(desc(x)), s, _ref(desc(out)), nth), "scale")
+    return out
+
+
+def diag_mask_inf(x, n_past, nth=1):
+    out = np.empty_like(x)
+    _check(lib().cbxo_diag_mask_inf(_ref(desc(x)), n_past, _ref(desc(out)), nth), "diag_mask_inf")
+    return out
+
+
+def soft_max(x, nth=1):
+    out = np.empty_like(x)
+    _check(lib().cbxo_soft_max(_ref(desc(x)), _ref(desc(out)), nth), "soft_max")
+    return out
+
+
+def scale_diag_mask_soft_max(x, s, n_past=-1, nth=1):
+    """soft_max(diag_mask_inf(scale(x, s), n_past)); n_past < 0: no mask."""
+    out = np.empty_like(x)
+    _check(lib().cbxo_scale_diag_mask_soft_max(_ref(desc(x)), s, n_past, _ref(desc(out)), nth),
+           "scale_diag_mask_soft_max")
     return out
 
 

@@ -1,0 +1,83 @@
+"""cbx_scale_diag_mask_soft_max (scale -> diag_mask_inf -> soft_max over the
+key axis) vs the oracle.  The exponentials come from the device libm, so
+the bar is the f32 one (|d| <= 1e-5 |e|, plus a 1e-37 floor for outputs in
+the f32 subnormal range); masked scores must come out exactly 0."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from chatterbox_amdvulkan_amd import workloads as W
+from tests._util import assert_bitexact
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def mask_of(shape, n_past):
+    """True where diag_mask_inf hides key i from query j: i > n_past + j."""
+    n_q, n_k = shape[-2], shape[-1]
+    m = np.arange(n_k)[None, :] > n_past + np.arange(n_q)[:, None]
+    return np.broadcast_to(m, shape) if n_past >= 0 else np.zeros(shape, dtype=bool)
+
+
+def check(got, exp, what, masked=None):
+    d = np.abs(got.astype(np.float64) - exp.astype(np.float64))
+    bad = d > 1e-5 * np.abs(exp.astype(np.float64)) + 1e-37
+    assert not bad.any(), f"{what}: {int(bad.sum())} of {got.size} off, max |d| {d.max():.3g}"
+    if masked is not None:
+        assert_bitexact(got[masked], np.zeros(int(masked.sum()), dtype=np.float32), f"{what}: masked")
+
+
+def test_t3_prefill_causal(cbx, oracle):
+    """[16 heads, 512 queries, 512 keys], scale 1/sqrt(64), causal (n_past 0)."""
+    x = W.normal(130, (1, 16, 512, 512), 0.0, 8.0)
+    got = host(cbx.scale_diag_mask_soft_max(dev(x), 1.0 / math.sqrt(64), 0))
+    exp = oracle.scale_diag_mask_soft_max(x, 1.0 / math.sqrt(64), 0, nth=8)
+    check(got, exp, "t3 prefill", mask_of(x.shape, 0))
+
+
+@pytest.mark.parametrize("n_new,n_total", [(1, 777), (3, 100), (5, 4096), (2, 4097), (4, 9000)])
+def test_t3_incremental(cbx, oracle, n_new, n_total):
+    """New queries after n_past = n_total - n_new cached keys (t3.cpp:514-517)."""
+    x = W.normal(131 + n_total, (16, n_new, n_total), 0.0, 6.0)
+    n_past = n_total - n_new
+    got = host(cbx.scale_diag_mask_soft_max(dev(x), 0.125, n_past))
+    check(got, oracle.scale_diag_mask_soft_max(x, 0.125, n_past), f"t3 {n_new}x{n_total}",
+          mask_of(x.shape, n_past))
+
+
+def test_cfm_attention_no_mask(cbx, oracle):
+    """CFM scores [2 (CFG pair), 8 heads, 500, 500], scale 1/8, no mask."""
+    x = W.normal(132, (2, 8, 500, 500), 0.0, 4.0)
+    got = host(cbx.scale_diag_mask_soft_max(dev(x), 0.125, -1))
+    check(got, oracle.scale_diag_mask_soft_max(x, 0.125, -1, nth=8), "cfm")
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 63, 64, 257, 1000, 4096])
+def test_row_lengths_in_place_and_constant_rows(cbx, oracle, n):
+    x = W.normal(133 + n, (7, n), 0.0, 10.0)
+    x[0] = 1.5                     # constant row: exactly (float)(1/n)
+    t = dev(x)
+    cbx.scale_diag_mask_soft_max(t, 1.0, -1, out=t)
+    got = host(t)
+    check(got, oracle.scale_diag_mask_soft_max(x, 1.0, -1), f"n={n}")
+    assert_bitexact(got[0], np.full(n, np.float32(1.0 / n)), "constant row")
+
+
+def test_strided_rows_and_extremes(cbx, oracle):
+    """A column-sliced view (rows at a stride, loop path) and large score gaps."""
+    base = W.normal(134, (6, 300), 0.0, 30.0)
+    v = dev(base)[:, 10:266]
+    got = host(cbx.scale_diag_mask_soft_max(v, 2.0, 3))
+    check(got, oracle.scale_diag_mask_soft_max(np.ascontiguousarray(base[:, 10:266]), 2.0, 3), "strided",
+          mask_of((6, 256), 3))

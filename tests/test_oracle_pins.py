@@ -416,3 +416,53 @@ def test_thread_count_does_not_change_results(oracle):
     x = W.normal(34, (37, 513))
     for fn in (lambda n: oracle.norm(x, 1e-5, nth=n), lambda n: oracle.unary(oracle.SILU, x, nth=n)):
         assert_bitexact(fn(1), fn(7), "threads")
+
+
+# --------------------------------------------------------------------------- #
+# attention epilogue: scale -> diag_mask_inf -> soft_max
+# --------------------------------------------------------------------------- #
+
+def _softmax64(x):
+    """The reference's NumPy text (scripts/reference_t3_forward.py:87-89) in float64."""
+    x = x.astype(np.float64)
+    m = x.max(-1, keepdims=True)
+    e = np.exp(x - m)
+    return e / e.sum(-1, keepdims=True)
+
+
+def test_scale_and_diag_mask_exact(oracle):
+    x = W.normal(120, (2, 3, 5, 7))
+    assert_bitexact(oracle.scale(x, 0.125), (x * np.float32(0.125)).astype(np.float32), "scale")
+    m = oracle.diag_mask_inf(x, 2)
+    i = np.arange(7)[None, :]
+    j = np.arange(5)[:, None]
+    masked = np.broadcast_to(i > 2 + j, x.shape)
+    assert np.all(np.isneginf(m[masked])) and np.array_equal(m[~masked], x[~masked])
+
+
+@pytest.mark.parametrize("n", [1, 2, 33, 500, 4097])
+def test_soft_max_float64_and_invariants(oracle, n):
+    x = W.normal(121 + n, (6, n), 0.0, 3.0)
+    y = oracle.soft_max(x)
+    assert np.max(np.abs(y - _softmax64(x))) < 4e-7
+    assert np.allclose(y.astype(np.float64).sum(-1), 1.0, atol=2e-6)
+    # a constant row gives exactly (float)(1.0 / n)
+    c = np.full((3, n), 2.5, dtype=np.float32)
+    assert_bitexact(oracle.soft_max(c), np.full((3, n), np.float32(1.0 / n)), "constant row")
+
+
+def test_causal_attention_matches_reference_text(oracle):
+    """scores/sqrt(Hd), triu(k=1) masked to -inf, softmax (reference_t3_forward.py:113-120)
+    equals scale -> diag_mask_inf(n_past=0) -> soft_max; masked entries are exactly 0."""
+    H, L, Hd = 4, 37, 64
+    s = W.normal(122, (H, L, L), 0.0, 8.0)
+    y = oracle.scale_diag_mask_soft_max(s, 1.0 / math.sqrt(Hd), 0)
+    causal = np.triu(np.ones((L, L), dtype=bool), k=1)
+    ref = _softmax64(np.where(causal[None], -np.inf, s.astype(np.float64) / math.sqrt(Hd)))
+    assert np.max(np.abs(y - ref)) < 4e-7
+    assert not y[:, causal].any()
+    # incremental decode: one new query row after n_past cached keys sees every key
+    q = W.normal(123, (H, 1, 50))
+    y1 = oracle.scale_diag_mask_soft_max(q, 0.125, 49)
+    assert_bitexact(y1, oracle.scale_diag_mask_soft_max(q, 0.125, -1), "n_past masks nothing")
+    assert np.max(np.abs(y1 - _softmax64(q * np.float32(0.125)))) < 4e-7
