@@ -103,6 +103,44 @@ __device__ __forceinline__ float4 load_table4(const char* row, int64_t j) {
     }
 }
 
+// The T3 embedding row: h = f32(table row) + f32(position row), stored when
+// hr is non-null, then y = LN(h)*w + b.  Row loads are unconditional
+// (clamped addresses) so all 2*NV are in flight together.
+template <int TYPE, int TYPE2, int NV>
+__device__ __forceinline__ void embed_ln_row(const char* s1, const char* s2, const Affine<NV>& af, bool hw, bool hb,
+                                             char* hr, char* yr, int64_t ne0, float eps, int lane) {
+    float4 p[NV], q[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t j = (lane + 64 * k) * 4;
+        p[k] = load_table4<TYPE>(s1, j < ne0 ? j : 0);
+        q[k] = load_table4<TYPE2>(s2, j < ne0 ? j : 0);
+    }
+    float4 v[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t j = (lane + 64 * k) * 4;
+        if (j < ne0) {
+            v[k] = make_float4(p[k].x + q[k].x, p[k].y + q[k].y, p[k].z + q[k].z, p[k].w + q[k].w);
+            if (hr) *reinterpret_cast<float4*>(hr + j * 4) = v[k];
+        } else {
+            v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    const float scale = wave_row_scale<NV, NORM_LN>(v, lane, ne0, eps);
+    wave_row_store<float, NV, false>(v, lane, ne0, scale, af, hw, hb, CBX_UNARY_NONE, nullptr, yr);
+}
+
+// An out-of-range id: ggml aborts; here the row's outputs are zeroed and
+// the sticky device error bit is raised.
+__device__ __forceinline__ void embed_bad_row(char* hr, char* yr, int64_t ne0, int lane, uint32_t* err) {
+    for (int64_t j = lane; j < ne0; j += 64) {
+        reinterpret_cast<float*>(yr)[j] = 0.0f;
+        if (hr) reinterpret_cast<float*>(hr)[j] = 0.0f;
+    }
+    if (lane == 0) atomicOr(err, static_cast<uint32_t>(DEV_ERR_ROW_INDEX));
+}
+
 // cos/sin of pair k for position p: theta = p * theta_scale^k as an iterated
 // f32 product (ggml's rope cache), then ggml's YaRN correction.
 __device__ inline void rope_cos_sin_dev(int32_t p, int k, const RopeParams& rp, const float* __restrict__ ff, float* c,

@@ -258,41 +258,16 @@ __device__ __forceinline__ void b_embed_ln_t(const BOp& op, uint32_t lb, uint32_
     const int32_t id2 = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const int32_t*>(op.t[3].p + t * op.t[3].nb1));
     char* yr = op.t[7].p + t * op.t[7].nb1;
     char* hr = op.t[6].p ? op.t[6].p + t * op.t[6].nb1 : nullptr;
-    if (id < 0 || id >= op.aux || id2 < 0 || id2 >= op.aux2) {
-        for (int64_t j = lane; j < ne0; j += 64) {
-            reinterpret_cast<float*>(yr)[j] = 0.0f;
-            if (hr) reinterpret_cast<float*>(hr)[j] = 0.0f;
-        }
-        if (lane == 0) atomicOr(err, static_cast<uint32_t>(DEV_ERR_ROW_INDEX));
-        return;
-    }
-    const char* s1 = op.t[0].p + id * op.t[0].nb1;
-    const char* s2 = op.t[2].p + id2 * op.t[2].nb1;
     const float* w = reinterpret_cast<const float*>(op.t[4].p);
     const float* b = reinterpret_cast<const float*>(op.t[5].p);
     Affine<NV> af;
     af.load(w, b, lane, ne0);
-    float4 p[NV], q[NV];
-#pragma unroll
-    for (int k = 0; k < NV; k++) {
-        const int64_t j = (lane + 64 * k) * 4;
-        p[k] = load_table4<TYPE>(s1, j < ne0 ? j : 0);
-        q[k] = load_table4<TYPE2>(s2, j < ne0 ? j : 0);
+    if (id < 0 || id >= op.aux || id2 < 0 || id2 >= op.aux2) {
+        embed_bad_row(hr, yr, ne0, lane, err);
+        return;
     }
-    float4 v[NV];
-#pragma unroll
-    for (int k = 0; k < NV; k++) {
-        const int64_t j = (lane + 64 * k) * 4;
-        if (j < ne0) {
-            v[k] = make_float4(p[k].x + q[k].x, p[k].y + q[k].y, p[k].z + q[k].z, p[k].w + q[k].w);
-            if (hr) *reinterpret_cast<float4*>(hr + j * 4) = v[k];
-        } else {
-            v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    }
-    const float scale = wave_row_scale<NV, NORM_LN>(v, lane, ne0, op.eps);
-    wave_row_store<float, NV, false>(v, lane, ne0, scale, af, w != nullptr, b != nullptr, CBX_UNARY_NONE, nullptr,
-                                     yr);
+    embed_ln_row<TYPE, TYPE2, NV>(op.t[0].p + id * op.t[0].nb1, op.t[2].p + id2 * op.t[2].nb1, af, w != nullptr,
+                                  b != nullptr, hr, yr, ne0, op.eps, lane);
 }
 
 template <int TYPE>

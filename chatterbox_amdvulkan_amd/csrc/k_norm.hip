@@ -24,15 +24,20 @@ namespace {
 
 constexpr int kMaxThreads = 256;
 
-template <typename T, int NV, int KIND, bool ACT>
-__global__ __launch_bounds__(kMaxThreads) void k_row_norm_wave(View x, View y, const float* __restrict__ w,
-                                                                const float* __restrict__ b, float eps, int act,
-                                                                const uint16_t* __restrict__ tab, int64_t nr,
-                                                                bool fx, bool fy) {
+// WPB waves (rows) per workgroup.  With WPB == 1 the grid has exactly one
+// workgroup per row, so there is no bounds check and no read of the block
+// size: nothing waits before the argument and row loads are issued.
+template <typename T, int NV, int KIND, bool ACT, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_row_norm_wave(View x, View y, const float* __restrict__ w,
+                                                            const float* __restrict__ b, float eps, int act,
+                                                            const uint16_t* __restrict__ tab, int64_t nr,
+                                                            bool fx, bool fy) {
     const int lane = threadIdx.x & 63;
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) +
-                      __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (r >= nr) return;   // uniform per wave
+    int64_t r = blockIdx.x;
+    if constexpr (WPB > 1) {
+        r = r * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        if (r >= nr) return;   // uniform per wave
+    }
     const int64_t ne0 = x.ne[0];
     const char* xr = x.data + row_offset(x, r, fx);
     char* yr = y.data + row_offset(y, r, fy);
@@ -90,41 +95,57 @@ __global__ __launch_bounds__(kMaxThreads) void k_embed_norm(EmbedArgs a) {
         *reinterpret_cast<const int32_t*>(a.ids2.data + i10 * a.ids2.nb[0] + i11 * a.ids2.nb[1] + i12 * a.ids2.nb[2]));
     char* yr = a.y.data + i10 * a.y.nb[1] + i11 * a.y.nb[2] + i12 * a.y.nb[3];
     char* hr = a.h.data ? a.h.data + i10 * a.h.nb[1] + i11 * a.h.nb[2] + i12 * a.h.nb[3] : nullptr;
+    Affine<NV> af;
+    af.load(a.w, a.b, lane, ne0);
     if (id < 0 || id >= a.src.ne[1] || id2 < 0 || id2 >= a.src2.ne[1]) {
-        // ggml aborts on an out-of-range index; here the outputs are zeroed
-        // and the sticky device error bit is raised.
-        for (int64_t j = lane; j < ne0; j += 64) {
-            reinterpret_cast<float*>(yr)[j] = 0.0f;
-            if (hr) reinterpret_cast<float*>(hr)[j] = 0.0f;
-        }
-        if (lane == 0) atomicOr(a.err, static_cast<uint32_t>(DEV_ERR_ROW_INDEX));
+        embed_bad_row(hr, yr, ne0, lane, a.err);
         return;
     }
     const char* s1 = a.src.data + id * a.src.nb[1] + i11 * a.src.nb[2] + i12 * a.src.nb[3];
     const char* s2 = a.src2.data + id2 * a.src2.nb[1] + i11 * a.src2.nb[2] + i12 * a.src2.nb[3];
+    embed_ln_row<TYPE, TYPE2, NV>(s1, s2, af, a.w != nullptr, a.b != nullptr, hr, yr, ne0, a.eps, lane);
+}
+
+// The common layout -- 1-D contiguous ids, 2-D tables, uniformly strided
+// output rows, ne0 <= 1024 -- with a compact argument block: every field is
+// read by one batch of scalar loads at entry, so the id loads issue
+// immediately (the general kernel's View-based arguments took a second
+// dependent round of argument loads).
+struct EmbedFlat {
+    const char* src;
+    const char* src2;
+    const int32_t* ids;
+    const int32_t* ids2;
+    const float* w;
+    const float* b;
+    char* h;
+    char* y;
+    int64_t src_nb1, src2_nb1, h_nb1, y_nb1;
+    int32_t src_rows, src2_rows, n_tok, ne0;
+    float eps;
+    uint32_t* err;
+};
+
+// One wave per workgroup and exactly n_tok workgroups: no bounds check and
+// no read of the launch's block size, so nothing waits before the argument
+// loads and the id loads are issued.
+template <int TYPE, int TYPE2, int NV>
+__global__ __launch_bounds__(64) void k_embed_norm_flat(EmbedFlat a) {
+    const int lane = threadIdx.x;
+    const int t = static_cast<int>(blockIdx.x);
+    const int32_t id = __builtin_amdgcn_readfirstlane(a.ids[t]);
+    const int32_t id2 = __builtin_amdgcn_readfirstlane(a.ids2[t]);
+    const int64_t ne0 = a.ne0;
     Affine<NV> af;
     af.load(a.w, a.b, lane, ne0);
-    float4 p[NV], q[NV];
-#pragma unroll
-    for (int k = 0; k < NV; k++) {   // unconditional loads, clamped addresses
-        const int64_t j = (lane + 64 * k) * 4;
-        p[k] = load_table4<TYPE>(s1, j < ne0 ? j : 0);
-        q[k] = load_table4<TYPE2>(s2, j < ne0 ? j : 0);
+    char* yr = a.y + t * a.y_nb1;
+    char* hr = a.h ? a.h + t * a.h_nb1 : nullptr;
+    if (id < 0 || id >= a.src_rows || id2 < 0 || id2 >= a.src2_rows) {
+        embed_bad_row(hr, yr, ne0, lane, a.err);
+        return;
     }
-    float4 v[NV];
-#pragma unroll
-    for (int k = 0; k < NV; k++) {
-        const int64_t j = (lane + 64 * k) * 4;
-        if (j < ne0) {
-            v[k] = make_float4(p[k].x + q[k].x, p[k].y + q[k].y, p[k].z + q[k].z, p[k].w + q[k].w);
-            if (hr) *reinterpret_cast<float4*>(hr + j * 4) = v[k];
-        } else {
-            v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    }
-    const float scale = wave_row_scale<NV, NORM_LN>(v, lane, ne0, a.eps);
-    wave_row_store<float, NV, false>(v, lane, ne0, scale, af, a.w != nullptr, a.b != nullptr, CBX_UNARY_NONE,
-                                     nullptr, yr);
+    embed_ln_row<TYPE, TYPE2, NV>(a.src + id * a.src_nb1, a.src2 + id2 * a.src2_nb1, af, a.w != nullptr,
+                                  a.b != nullptr, hr, yr, ne0, a.eps, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -281,12 +302,12 @@ struct NormLaunch {
     hipStream_t s;
 };
 
-template <typename T, int KIND, bool ACT>
-void go_wave(const NormLaunch& L, int nv) {
-#define CBX_WAVE_CASE(N)                                                                                     \
-    case N:                                                                                                 \
-        hipLaunchKernelGGL((k_row_norm_wave<T, N, KIND, ACT>), L.grid, L.block, 0, L.s, L.x, L.y, L.w, L.b, \
-                           L.eps, L.act, L.tab, L.nr, L.fx, L.fy);                                          \
+template <typename T, int KIND, bool ACT, int WPB>
+void go_wave_w(const NormLaunch& L, int nv) {
+#define CBX_WAVE_CASE(N)                                                                                          \
+    case N:                                                                                                      \
+        hipLaunchKernelGGL((k_row_norm_wave<T, N, KIND, ACT, WPB>), L.grid, L.block, 0, L.s, L.x, L.y, L.w, L.b, \
+                           L.eps, L.act, L.tab, L.nr, L.fx, L.fy);                                               \
         break;
     switch (nv) {
         CBX_WAVE_CASE(1)
@@ -296,6 +317,12 @@ void go_wave(const NormLaunch& L, int nv) {
         CBX_WAVE_CASE(16)
     }
 #undef CBX_WAVE_CASE
+}
+
+template <typename T, int KIND, bool ACT>
+void go_wave(const NormLaunch& L, int nv) {
+    if (L.block.x == 64) go_wave_w<T, KIND, ACT, 1>(L, nv);
+    else go_wave_w<T, KIND, ACT, 4>(L, nv);
 }
 
 template <typename T, int KIND, bool ACT, bool VEC>
@@ -407,6 +434,23 @@ void embed_nv(const EmbedArgs& a, int nv, dim3 grid, dim3 block, hipStream_t s) 
     }
 }
 
+template <int TYPE, int TYPE2>
+void embed_flat_nv(const EmbedFlat& a, int nv, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(a.n_tok)), block(64);
+    switch (nv) {
+        case 1: hipLaunchKernelGGL((k_embed_norm_flat<TYPE, TYPE2, 1>), grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL((k_embed_norm_flat<TYPE, TYPE2, 2>), grid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL((k_embed_norm_flat<TYPE, TYPE2, 4>), grid, block, 0, s, a); break;
+    }
+}
+
+template <int TYPE>
+void embed_flat_t2(int t2, const EmbedFlat& a, int nv, hipStream_t s) {
+    if (t2 == CBX_TYPE_F32) embed_flat_nv<TYPE, CBX_TYPE_F32>(a, nv, s);
+    else if (t2 == CBX_TYPE_F16) embed_flat_nv<TYPE, CBX_TYPE_F16>(a, nv, s);
+    else embed_flat_nv<TYPE, CBX_TYPE_Q8_0>(a, nv, s);
+}
+
 template <int TYPE>
 void embed_t2(int t2, const EmbedArgs& a, int nv, dim3 grid, dim3 block, hipStream_t s) {
     if (t2 == CBX_TYPE_F32) embed_nv<TYPE, CBX_TYPE_F32>(a, nv, grid, block, s);
@@ -432,6 +476,42 @@ int launch_embed_norm(const cbx_tensor* src, const cbx_tensor* ids, const cbx_te
         return set_error(CBX_ERR_UNSUPPORTED,
                          "get_rows_add_layer_norm: needs ne0 % 4 == 0, ne0 <= 4096 and 16-byte aligned rows, w, b");
     }
+    const int64_t n_tok = ids->ne[0] * ids->ne[1] * ids->ne[2];
+    const int nv = pow2_nv(cdiv(ne0, 256));
+    const int wpb = waves_per_block(n_tok, st);
+    const dim3 block(64 * wpb), grid(static_cast<unsigned>(cdiv(n_tok, wpb)));
+    auto one_d = [](const cbx_tensor* i) {
+        return i->ne[1] == 1 && i->ne[2] == 1 && (i->ne[0] <= 1 || i->nb[0] == sizeof(int32_t));
+    };
+    auto table_2d = [](const cbx_tensor* t) { return t->ne[2] == 1 && t->ne[3] == 1 && t->ne[1] < (int64_t{1} << 31); };
+    if (nv <= 4 && one_d(ids) && one_d(ids2) && table_2d(src) && table_2d(src2) && flat_rows(y) &&
+        (!h || flat_rows(h)) && n_tok < (int64_t{1} << 31)) {
+        EmbedFlat f;
+        f.src = static_cast<const char*>(src->data);
+        f.src2 = static_cast<const char*>(src2->data);
+        f.ids = static_cast<const int32_t*>(ids->data);
+        f.ids2 = static_cast<const int32_t*>(ids2->data);
+        f.w = w ? static_cast<const float*>(w->data) : nullptr;
+        f.b = b ? static_cast<const float*>(b->data) : nullptr;
+        f.h = h ? static_cast<char*>(h->data) : nullptr;
+        f.y = static_cast<char*>(y->data);
+        f.src_nb1 = static_cast<int64_t>(src->nb[1]);
+        f.src2_nb1 = static_cast<int64_t>(src2->nb[1]);
+        f.h_nb1 = h ? static_cast<int64_t>(h->nb[1]) : 0;
+        f.y_nb1 = static_cast<int64_t>(y->nb[1]);
+        f.src_rows = static_cast<int32_t>(src->ne[1]);
+        f.src2_rows = static_cast<int32_t>(src2->ne[1]);
+        f.n_tok = static_cast<int32_t>(n_tok);
+        f.ne0 = static_cast<int32_t>(ne0);
+        f.eps = eps;
+        f.err = st->err_word;
+        switch (src->type) {
+            case CBX_TYPE_F32: embed_flat_t2<CBX_TYPE_F32>(src2->type, f, nv, s); break;
+            case CBX_TYPE_F16: embed_flat_t2<CBX_TYPE_F16>(src2->type, f, nv, s); break;
+            default: embed_flat_t2<CBX_TYPE_Q8_0>(src2->type, f, nv, s); break;
+        }
+        return check_launch("get_rows_add_layer_norm");
+    }
     EmbedArgs a;
     a.src = view_of(src);
     a.ids = view_of(ids);
@@ -442,11 +522,8 @@ int launch_embed_norm(const cbx_tensor* src, const cbx_tensor* ids, const cbx_te
     a.w = w ? static_cast<const float*>(w->data) : nullptr;
     a.b = b ? static_cast<const float*>(b->data) : nullptr;
     a.eps = eps;
-    a.n_tok = ids->ne[0] * ids->ne[1] * ids->ne[2];
+    a.n_tok = n_tok;
     a.err = st->err_word;
-    const int nv = pow2_nv(cdiv(ne0, 256));
-    const int wpb = waves_per_block(a.n_tok, st);
-    const dim3 block(64 * wpb), grid(static_cast<unsigned>(cdiv(a.n_tok, wpb)));
     switch (src->type) {
         case CBX_TYPE_F32: embed_t2<CBX_TYPE_F32>(src2->type, a, nv, grid, block, s); break;
         case CBX_TYPE_F16: embed_t2<CBX_TYPE_F16>(src2->type, a, nv, grid, block, s); break;

@@ -31,13 +31,17 @@ __device__ __forceinline__ float masked(float x, float s, int64_t col, int64_t l
     return col > limit ? -INFINITY : x * s;
 }
 
-template <int NV>
-__global__ __launch_bounds__(kThreads) void k_soft_max_wave(View x, View y, float s, int64_t n_past, int64_t nr,
+// WPB rows per workgroup; with one, the grid is exactly one workgroup per
+// row and nothing waits (bounds check, block size) before the loads issue.
+template <int NV, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(View x, View y, float s, int64_t n_past, int64_t nr,
                                                             bool fx, bool fy) {
     const int lane = threadIdx.x & 63;
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) +
-                      __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (r >= nr) return;   // uniform per wave
+    int64_t r = blockIdx.x;
+    if constexpr (WPB > 1) {
+        r = r * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        if (r >= nr) return;   // uniform per wave
+    }
     const int64_t ne0 = x.ne[0];
     const char* xr = x.data + row_offset(x, r, fx);
     char* yr = y.data + row_offset(y, r, fy);
@@ -111,6 +115,19 @@ __global__ __launch_bounds__(kThreads) void k_soft_max_loop(View x, View y, floa
 
 int waves_for(int64_t rows, const DeviceState* st) { return rows >= int64_t{8} * st->n_cu ? 4 : 1; }
 
+template <int WPB>
+void sm_wave(int nv, const View& vx, const View& vy, float s, int64_t n_past, int64_t nr, bool fx, bool fy,
+             hipStream_t strm) {
+    const dim3 grid(static_cast<unsigned>(cdiv(nr, WPB))), block(64 * WPB);
+    switch (nv) {
+        case 1: hipLaunchKernelGGL((k_soft_max_wave<1, WPB>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy); break;
+        case 2: hipLaunchKernelGGL((k_soft_max_wave<2, WPB>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy); break;
+        case 4: hipLaunchKernelGGL((k_soft_max_wave<4, WPB>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy); break;
+        case 8: hipLaunchKernelGGL((k_soft_max_wave<8, WPB>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy); break;
+        default: hipLaunchKernelGGL((k_soft_max_wave<16, WPB>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy); break;
+    }
+}
+
 }  // namespace
 
 int launch_soft_max(const cbx_tensor* x, float s, int64_t n_past, cbx_tensor* y, DeviceState* st, hipStream_t strm) {
@@ -123,14 +140,10 @@ int launch_soft_max(const cbx_tensor* x, float s, int64_t n_past, cbx_tensor* y,
                      (y->ne[2] <= 1 || y->nb[2] % 16 == 0) && (y->ne[3] <= 1 || y->nb[3] % 16 == 0);
     if (nr >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "soft_max: too many rows");
     if (vec) {
-        const int wpb = waves_for(nr, st);
-        const dim3 grid(static_cast<unsigned>(cdiv(nr, wpb))), block(64 * wpb);
         const int64_t need = cdiv(ne0, 256);
-        if (need <= 1) hipLaunchKernelGGL((k_soft_max_wave<1>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy);
-        else if (need <= 2) hipLaunchKernelGGL((k_soft_max_wave<2>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy);
-        else if (need <= 4) hipLaunchKernelGGL((k_soft_max_wave<4>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy);
-        else if (need <= 8) hipLaunchKernelGGL((k_soft_max_wave<8>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy);
-        else hipLaunchKernelGGL((k_soft_max_wave<16>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy);
+        const int nv = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : 16;
+        if (waves_for(nr, st) == 1) sm_wave<1>(nv, vx, vy, s, n_past, nr, fx, fy, strm);
+        else sm_wave<4>(nv, vx, vy, s, n_past, nr, fx, fy, strm);
     } else {
         hipLaunchKernelGGL(k_soft_max_loop, dim3(static_cast<unsigned>(nr)), dim3(kThreads), 0, strm, vx, vy, s, n_past,
                            fx, fy);
