@@ -757,7 +757,7 @@ int build_op(int i, const cbx_op& o, BOp& b, DeviceState* st, int64_t* nblk) {
                 return batch_fail(i, CBX_ERR_INVALID_ARG, "pos must be I32 with ne = (x.ne2, 1, 1, 1)");
             }
             if (c->p.n_dims > x->ne[0]) return batch_fail(i, CBX_ERR_INVALID_ARG, "n_dims > x.ne0");
-            if (c->p.n_dims / 2 > 256 || !flat_rows(x) || !flat_rows(y)) {
+            if (c->p.n_dims / 2 > 256 || !flat_rows(x) || !flat_rows(y) || x->ne[1] * x->ne[0] >= (int64_t{1} << 31)) {
                 return batch_fail(i, CBX_ERR_UNSUPPORTED, "rope needs n_dims <= 512 and uniformly strided rows");
             }
             b.t_x = x->type;
@@ -878,7 +878,7 @@ extern "C" int cbx_run_ops(const cbx_op* ops, int n_ops, cbx_stream stream) {
     int64_t total = 0;
     for (int i = 0; i < n_ops; i++) {
         int64_t nb = 0;
-        a.op[i].blk0 = static_cast<uint32_t>(total);
+        a.blk0[i] = static_cast<uint32_t>(total);
         if ((rc = build_op(i, ops[i], a.op[i], st, &nb))) return rc;
         total += nb;
         if (total >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "cbx_run_ops: too many workgroups");

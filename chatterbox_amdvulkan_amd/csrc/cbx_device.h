@@ -173,7 +173,8 @@ __device__ __forceinline__ float act_gelu_tab(const uint16_t* __restrict__ tab, 
 
 // The same function with the table read only where it is needed.  For
 // |x| < 10 the result is a function of h = f16(x) alone.  With
-// E = 2^(xf (K1 + K2 xf^2)) = e^(2a), a = sqrt(2/pi) xf (1 + 0.044715 xf^2),
+// E = 2^(xf (K1 + K2 xf^2)) = e^(2a), a = sqrt(2/pi) xf (1 + 0.044715 xf^2)
+// (the inner polynomial with one fused multiply-add),
 // the table's 0.5 xf (1 + tanh a) equals xf (1 - 1/(E + 1)); that is
 // evaluated with the hardware exp2 and reciprocal (q = 1 - r is within
 // ~2 ulps of 1 absolute, i.e. ~2/q ulps of g relative, plus ~8 ulps from
@@ -189,13 +190,14 @@ __device__ __forceinline__ float act_gelu_tab(const uint16_t* __restrict__ tab, 
 
 struct GeluPart {
     uint32_t idx;   // table entry to read: h, or 0 when g's rounding is sure
-    float    g;     // (idx 0 also stands for "sure": for h = 0 both are +0)
+    float    g;
+    bool     sure;
 };
 
 __device__ __forceinline__ GeluPart gelu_part(float x) {
     const uint32_t h = f2h(x);
     const float xf = h2f(static_cast<uint16_t>(h));
-    const float w = xf * (CBX_GELU_K2 * (xf * xf) + CBX_GELU_K1);
+    const float w = xf * __builtin_fmaf(CBX_GELU_K2, xf * xf, CBX_GELU_K1);
     const float r = __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(w) + 1.0f);
     const float q = 1.0f - r;
     const float g = xf * q;
@@ -204,11 +206,11 @@ __device__ __forceinline__ GeluPart gelu_part(float x) {
     // bitwise & keeps this branch-free, so the table loads of several
     // elements issue together
     const bool sure = (q >= 0.0078125f) & (gb >= 0x38800000u) & ((dist - 8.0f) * q > 16.0f);
-    return GeluPart{sure ? 0u : h, g};
+    return GeluPart{sure ? 0u : h, g, sure};
 }
 
 __device__ __forceinline__ float gelu_finish(float x, const GeluPart& p, uint16_t tv) {
-    float r = p.idx == 0u ? h2f(f2h(p.g)) : h2f(tv);
+    float r = h2f(p.sure ? static_cast<uint16_t>(f2h(p.g)) : tv);
     r = x <= -10.0f ? 0.0f : r;
     return x >= 10.0f ? x : r;
 }

@@ -133,7 +133,6 @@ struct BOp {
     int32_t     nv;
     int32_t     t_x, t_x2;
     float       eps, param;
-    uint32_t    blk0;        // first workgroup of this op
     int64_t     ne0, rows, aux, aux2, aux3;
     BTen        t[8];
     const void* table;       // rope cos/sin table or the GELU table
@@ -146,6 +145,7 @@ constexpr int kBatchMaxOps = CBX_MAX_OPS;
 
 struct BatchArgs {
     int32_t   n;
+    uint32_t  blk0[kBatchMaxOps];   // first workgroup of each op, contiguous for one scalar load batch
     uint32_t* err;
     BOp       op[kBatchMaxOps];
 };

@@ -176,41 +176,42 @@ __device__ __forceinline__ void b_snake(const BOp& op, uint32_t lb) {
 // ---- rope: one token per workgroup ------------------------------------------------
 template <typename T>
 __device__ __forceinline__ void b_rope_t(const BOp& op, uint32_t lb, float2* cs) {
-    const int64_t t = lb;                         // token index over ne2 * ne3
-    const int half = op.rp.n_dims / 2;
-    const int64_t heads = op.aux, ne2 = op.aux2, ne0 = op.ne0;
+    const uint32_t t = lb;                        // token index over ne2 * ne3
+    const uint32_t half = static_cast<uint32_t>(op.rp.n_dims / 2);
+    const uint32_t heads = static_cast<uint32_t>(op.aux), ne2 = static_cast<uint32_t>(op.aux2);
+    const uint32_t n_tail = static_cast<uint32_t>(op.ne0 - op.rp.n_dims);
     const int32_t p = *reinterpret_cast<const int32_t*>(op.t[1].p + (t % ne2) * op.t[1].nb1);
     const float2* table = reinterpret_cast<const float2*>(op.table);
-    for (int k = threadIdx.x; k < half; k += kThreads) {
+    for (uint32_t k = threadIdx.x; k < half; k += kThreads) {
         if (p >= 0 && p < op.n_pos) {
             cs[k] = table[static_cast<int64_t>(p) * half + k];
         } else {
             float c, s;
-            rope_cos_sin_dev(p, k, op.rp, op.ff, &c, &s);
+            rope_cos_sin_dev(p, static_cast<int>(k), op.rp, op.ff, &c, &s);
             cs[k] = make_float2(c, s);
         }
     }
     __syncthreads();
     constexpr int es = Elt<T>::size;
-    for (int64_t q = threadIdx.x; q < heads * half; q += kThreads) {
-        const int64_t h = q / half;
-        const int k = static_cast<int>(q - h * half);
-        const char* xr = op.t[0].p + (t * heads + h) * op.t[0].nb1;
-        char* yr = op.t[6].p + (t * heads + h) * op.t[6].nb1;
-        const int64_t ia = op.rp.mode == 2 ? k : 2 * k;
-        const int64_t ib = op.rp.mode == 2 ? k + half : 2 * k + 1;
+    const char* xt = op.t[0].p + static_cast<int64_t>(t) * heads * op.t[0].nb1;
+    char* yt = op.t[6].p + static_cast<int64_t>(t) * heads * op.t[6].nb1;
+    for (uint32_t q = threadIdx.x; q < heads * half; q += kThreads) {
+        const uint32_t h = q / half;
+        const uint32_t k = q - h * half;
+        const char* xr = xt + h * op.t[0].nb1;
+        char* yr = yt + h * op.t[6].nb1;
+        const uint32_t ia = op.rp.mode == 2 ? k : 2 * k;
+        const uint32_t ib = op.rp.mode == 2 ? k + half : 2 * k + 1;
         const float x0 = Elt<T>::load1(xr + ia * es);
         const float x1 = Elt<T>::load1(xr + ib * es);
         const float2 c = cs[k];
         Elt<T>::store1(yr + ia * es, x0 * c.x - x1 * c.y);
         Elt<T>::store1(yr + ib * es, x0 * c.y + x1 * c.x);
     }
-    const int64_t n_tail = ne0 - op.rp.n_dims;
-    for (int64_t q = threadIdx.x; q < heads * n_tail; q += kThreads) {
-        const int64_t h = q / n_tail;
-        const int64_t j = op.rp.n_dims + (q - h * n_tail);
-        *reinterpret_cast<T*>(op.t[6].p + (t * heads + h) * op.t[6].nb1 + j * es) =
-            *reinterpret_cast<const T*>(op.t[0].p + (t * heads + h) * op.t[0].nb1 + j * es);
+    for (uint32_t q = threadIdx.x; q < heads * n_tail; q += kThreads) {
+        const uint32_t h = q / n_tail;
+        const uint32_t j = static_cast<uint32_t>(op.rp.n_dims) + (q - h * n_tail);
+        *reinterpret_cast<T*>(yt + h * op.t[6].nb1 + j * es) = *reinterpret_cast<const T*>(xt + h * op.t[0].nb1 + j * es);
     }
 }
 
@@ -304,10 +305,19 @@ __global__ __launch_bounds__(kThreads) void k_batch(BatchArgs args) {
     const BatchArgs* a = (const BatchArgs*)(const void*)__builtin_amdgcn_kernarg_segment_ptr();
     const uint32_t b = blockIdx.x;
     const int n = a->n;
+    // the op owning this workgroup: all first-block offsets are read at once
+    // (independent scalar loads), not one dependent load per op
     int i = 0;
-    while (i + 1 < n && b >= a->op[i + 1].blk0) i++;
+    uint32_t base = 0;   // blk0[0] == 0
+#pragma unroll
+    for (int k = 1; k < kBatchMaxOps; k++) {
+        if (k < n && b >= a->blk0[k]) {
+            i = k;
+            base = a->blk0[k];
+        }
+    }
     const BOp& op = a->op[i];
-    const uint32_t lb = b - op.blk0;
+    const uint32_t lb = b - base;
     uint32_t* err = a->err;
     const uint16_t* tab = reinterpret_cast<const uint16_t*>(op.table);
     switch (op.kind) {
