@@ -26,6 +26,7 @@ LIB = os.path.join(PKG, "libcbxops.so")
 
 SOURCES = [
     "cbx_api.cpp",
+    "cbx_gguf.cpp",
     "k_rows.hip",
     "k_norm.hip",
     "k_group_norm.hip",

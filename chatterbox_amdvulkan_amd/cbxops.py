@@ -66,6 +66,19 @@ class OpStruct(ctypes.Structure):
     ]
 
 
+class GgufTensorInfo(ctypes.Structure):
+    """cbx_gguf_tensor_info"""
+
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("type", ctypes.c_int32),
+        ("n_dims", ctypes.c_int32),
+        ("ne", ctypes.c_int64 * 4),
+        ("nbytes", ctypes.c_size_t),
+        ("file_offset", ctypes.c_size_t),
+    ]
+
+
 # cbx_op_kind
 OP_LAYER_NORM, OP_RMS_NORM, OP_UNARY, OP_LEAKY_RELU, OP_SWIGLU, OP_ROPE, OP_GET_ROWS, \
     OP_GET_ROWS_ADD_LAYER_NORM, OP_SNAKE = range(1, 10)
@@ -121,6 +134,14 @@ def load() -> ctypes.CDLL:
         "cbx_swiglu": (i, [P, P, P, vp]),
         "cbx_snake": (i, [P, P, P, P, vp]),
         "cbx_run_ops": (i, [ctypes.POINTER(OpStruct), i, vp]),
+        "cbx_gguf_open": (i, [ctypes.c_char_p, ctypes.POINTER(vp)]),
+        "cbx_gguf_close": (None, [vp]),
+        "cbx_gguf_n_tensors": (ctypes.c_int64, [vp]),
+        "cbx_gguf_find_tensor": (ctypes.c_int64, [vp, ctypes.c_char_p]),
+        "cbx_gguf_get_str": (ctypes.c_char_p, [vp, ctypes.c_char_p]),
+        "cbx_gguf_tensor": (i, [vp, ctypes.c_int64, ctypes.POINTER(GgufTensorInfo)]),
+        "cbx_gguf_describe": (i, [vp, ctypes.c_int64, vp, P]),
+        "cbx_gguf_upload": (i, [vp, ctypes.c_int64, vp, ctypes.c_size_t, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -131,7 +152,8 @@ def load() -> ctypes.CDLL:
 
 
 def last_error() -> str:
-    return (load().cbx_last_error() or b"").decode()
+    # messages can quote names read from files: never fail on their bytes
+    return (load().cbx_last_error() or b"").decode("utf-8", errors="replace")
 
 
 def _check(rc: int):
@@ -484,3 +506,66 @@ def run_ops(ops) -> None:
                 _ready(t)
                 break
     OpBatch(ops).launch()
+
+
+# ---- GGUF tables ------------------------------------------------------------------
+
+class Gguf:
+    """cbx_gguf: a GGUF file's directory; tensors upload into torch device tensors."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        _check(load().cbx_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            load().cbx_gguf_close(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __len__(self) -> int:
+        return int(load().cbx_gguf_n_tensors(self.handle))
+
+    def find(self, name: str) -> int:
+        return int(load().cbx_gguf_find_tensor(self.handle, name.encode()))
+
+    def get_str(self, key: str) -> Optional[str]:
+        v = load().cbx_gguf_get_str(self.handle, key.encode())
+        return v.decode() if v is not None else None
+
+    def info(self, index: int) -> GgufTensorInfo:
+        out = GgufTensorInfo()
+        _check(load().cbx_gguf_tensor(self.handle, index, ctypes.byref(out)))
+        return out
+
+    def upload(self, index: int, device: Optional[int] = None) -> torch.Tensor:
+        """The tensor's bytes as a uint8 device tensor (viewed as float32 /
+        float16 / int32 for those types, Q8_0 blocks stay uint8 [rows, n*34])."""
+        inf = self.info(index)
+        dev = torch.cuda.current_device() if device is None else int(device)
+        raw = torch.empty(inf.nbytes, dtype=torch.uint8, device=f"cuda:{dev}")
+        with torch.cuda.device(dev):
+            _check(load().cbx_gguf_upload(self.handle, index, ctypes.c_void_p(raw.data_ptr()), inf.nbytes,
+                                          _stream()))
+        ne = [inf.ne[k] for k in range(inf.n_dims)][::-1]
+        if inf.type == Q8_0:
+            return raw.view(*ne[:-1], ne[-1] // QK8_0 * Q8_0_BLOCK)
+        dt = {F32: torch.float32, F16: torch.float16, I32: torch.int32}.get(inf.type)
+        return raw.view(dt).view(*ne) if dt is not None else raw
+
+    def describe(self, index: int, data: torch.Tensor) -> Tensor:
+        d = Tensor()
+        _check(load().cbx_gguf_describe(self.handle, index, ctypes.c_void_p(data.data_ptr()), ctypes.byref(d)))
+        return d
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -223,6 +223,49 @@ int cbx_swiglu(const cbx_tensor* g, const cbx_tensor* u, cbx_tensor* y,
 int cbx_snake(const cbx_tensor* x, const cbx_tensor* alpha,
               const cbx_tensor* alpha_inv, cbx_tensor* y, cbx_stream stream);
 
+/* ---- model tables from a GGUF file ---------------------------------------- */
+
+/* The reference reads its weights with ggml's gguf reader: the header,
+ * key/values and tensor directory first, then each tensor's bytes from
+ * data_offset + offset, uploaded to the backend (chatterbox-cpp/src/
+ * model.cpp:41-121).  These entry points do the same for device memory the
+ * caller owns, so the token/position tables of a GGUF (F32, F16 or Q8_0,
+ * e.g. token_embd.text.weight, position_embd.weight) feed cbx_get_rows*
+ * directly.  Host code; only cbx_gguf_upload touches the device.          */
+typedef struct cbx_gguf cbx_gguf;
+
+typedef struct cbx_gguf_tensor_info {
+    const char* name;         /* valid until cbx_gguf_close               */
+    int32_t     type;         /* ggml_type numbering                       */
+    int32_t     n_dims;
+    int64_t     ne[4];        /* unused dimensions are 1                   */
+    size_t      nbytes;       /* bytes of the tensor's data                */
+    size_t      file_offset;  /* absolute offset of the data in the file  */
+} cbx_gguf_tensor_info;
+
+/* Parses a GGUF v2/v3 file (gguf_init_from_file with no_alloc,
+ * model.cpp:46-57): checks the magic, version, every key's encoding, the
+ * alignment, each tensor's type, shape and that its data lies inside the
+ * file.  Keeps string-valued keys (general.architecture, ...).            */
+int         cbx_gguf_open(const char* path, cbx_gguf** out);
+void        cbx_gguf_close(cbx_gguf* gguf);
+int64_t     cbx_gguf_n_tensors(const cbx_gguf* gguf);
+/* Index of the tensor named `name`, or -1.                                 */
+int64_t     cbx_gguf_find_tensor(const cbx_gguf* gguf, const char* name);
+/* Value of a string key, or NULL (model.cpp:32-36).                        */
+const char* cbx_gguf_get_str(const cbx_gguf* gguf, const char* key);
+int         cbx_gguf_tensor(const cbx_gguf* gguf, int64_t index,
+                            cbx_gguf_tensor_info* out);
+/* A contiguous descriptor of tensor `index` whose data sits at `data`
+ * (F32, F16, Q8_0 or I32; ggml strides, nb[0] = block size).              */
+int         cbx_gguf_describe(const cbx_gguf* gguf, int64_t index, void* data,
+                              cbx_tensor* out);
+/* Copies tensor `index`'s bytes from the file to device memory `dst`
+ * (at least nbytes) on `stream`, staged through host memory; returns when
+ * the copy has completed (model.cpp:97-121).                               */
+int         cbx_gguf_upload(const cbx_gguf* gguf, int64_t index, void* dst,
+                            size_t dst_bytes, cbx_stream stream);
+
 /* ---- one launch for several independent ops ------------------------------ */
 
 /* A ggml graph step often holds several small ops that do not depend on
