@@ -793,7 +793,8 @@ int build_op(int i, const cbx_op& o, BOp& b, DeviceState* st, int64_t* nblk) {
             auto table_ok = [](const cbx_tensor* t) {
                 if (!t) return true;
                 if (t->ne[2] != 1 || t->ne[3] != 1) return false;
-                return t->type == CBX_TYPE_Q8_0 || rows_aligned_to(t, t->type == CBX_TYPE_F32 ? 16 : 8);
+                if (t->type == CBX_TYPE_Q8_0) return (reinterpret_cast<uintptr_t>(t->data) & 1u) == 0;
+                return rows_aligned_to(t, t->type == CBX_TYPE_F32 ? 16 : 8);
             };
             if (ids->ne[1] != 1 || ids->ne[2] != 1 || y->ne[0] % 4 || !table_ok(src) || !table_ok(src2) ||
                 !flat_rows(y) || !rows_aligned_to(y, 16) || (h && (!flat_rows(h) || !rows_aligned_to(h, 16))) ||

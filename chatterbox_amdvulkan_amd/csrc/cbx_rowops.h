@@ -95,11 +95,16 @@ __device__ __forceinline__ float4 load_table4(const char* row, int64_t j) {
     } else if constexpr (TYPE == CBX_TYPE_F16) {
         return Elt<uint16_t>::load4(row + j * 2);
     } else {
+        // block: f16 scale d, then 32 int8 quants; the 4 quants of a
+        // 4-aligned j sit at an even offset, read as two 16-bit words
         const char* blk = row + (j >> 5) * 34;
         const float d = h2f(*reinterpret_cast<const uint16_t*>(blk));
-        const int8_t* q = reinterpret_cast<const int8_t*>(blk + 2 + (j & 31));
-        return make_float4(static_cast<float>(q[0]) * d, static_cast<float>(q[1]) * d,
-                           static_cast<float>(q[2]) * d, static_cast<float>(q[3]) * d);
+        const uint16_t* q = reinterpret_cast<const uint16_t*>(blk + 2 + (j & 31));
+        const uint32_t q01 = q[0], q23 = q[1];
+        return make_float4(static_cast<float>(static_cast<int8_t>(q01 & 0xffu)) * d,
+                           static_cast<float>(static_cast<int8_t>(q01 >> 8)) * d,
+                           static_cast<float>(static_cast<int8_t>(q23 & 0xffu)) * d,
+                           static_cast<float>(static_cast<int8_t>(q23 >> 8)) * d);
     }
 }
 

@@ -459,7 +459,7 @@ void embed_t2(int t2, const EmbedArgs& a, int nv, dim3 grid, dim3 block, hipStre
 }
 
 bool table_vec_ok(const cbx_tensor* t) {
-    if (t->type == CBX_TYPE_Q8_0) return true;
+    if (t->type == CBX_TYPE_Q8_0) return (reinterpret_cast<uintptr_t>(t->data) & 1u) == 0;   // 16-bit quant loads
     const size_t al = t->type == CBX_TYPE_F32 ? 16 : 8;
     return rows_aligned(t, al);
 }
@@ -474,7 +474,8 @@ int launch_embed_norm(const cbx_tensor* src, const cbx_tensor* ids, const cbx_te
         (h && !rows_aligned(h, 16)) || (w && reinterpret_cast<uintptr_t>(w->data) % 16) ||
         (b && reinterpret_cast<uintptr_t>(b->data) % 16)) {
         return set_error(CBX_ERR_UNSUPPORTED,
-                         "get_rows_add_layer_norm: needs ne0 % 4 == 0, ne0 <= 4096 and 16-byte aligned rows, w, b");
+                         "get_rows_add_layer_norm: needs ne0 % 4 == 0, ne0 <= 4096, 16-byte aligned rows, w, b "
+                         "(Q8_0 tables: an even address)");
     }
     const int64_t n_tok = ids->ne[0] * ids->ne[1] * ids->ne[2];
     const int nv = pow2_nv(cdiv(ne0, 256));

@@ -7,7 +7,7 @@
 // scale and four int8 quants and forms q * d with one f32 multiply, exactly
 // dequantize_row_q8_0.  The second gather's row is added with one f32 add,
 // exactly ggml_add of the two gathered tensors (t3.cpp:446-455).
-#include "cbx_device.h"
+#include "cbx_rowops.h"
 
 namespace cbx {
 namespace {
@@ -17,17 +17,7 @@ enum { T_F32 = CBX_TYPE_F32, T_F16 = CBX_TYPE_F16, T_Q8 = CBX_TYPE_Q8_0 };
 // 4 elements starting at element j (j % 4 == 0) of a table row.
 template <int TYPE>
 __device__ __forceinline__ float4 load_row4(const char* row, int64_t j) {
-    if constexpr (TYPE == T_F32) {
-        return *reinterpret_cast<const float4*>(row + j * 4);
-    } else if constexpr (TYPE == T_F16) {
-        return Elt<uint16_t>::load4(row + j * 2);
-    } else {
-        const char* blk = row + (j >> 5) * 34;
-        const float d = h2f(*reinterpret_cast<const uint16_t*>(blk));
-        const int8_t* q = reinterpret_cast<const int8_t*>(blk + 2 + (j & 31));
-        return make_float4(static_cast<float>(q[0]) * d, static_cast<float>(q[1]) * d,
-                           static_cast<float>(q[2]) * d, static_cast<float>(q[3]) * d);
-    }
+    return load_table4<TYPE>(row, j);
 }
 
 template <int TYPE>
@@ -47,13 +37,18 @@ __device__ __forceinline__ float4 add4(float4 a, float4 b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 
+constexpr int kGatherThreads = 256;
+
 // TYPE2 < 0: plain gather.  VEC: rows are 16-byte aligned and ne0 % 4 == 0.
+// Exactly one workgroup per output row, of a fixed size: no loop bound or
+// block size to wait for before the id load.
 template <int TYPE, int TYPE2, bool VEC>
-__global__ __launch_bounds__(256) void k_get_rows(View src, View ids, View src2, View ids2, View dst,
-                                                  int64_t n_out_rows, uint32_t* __restrict__ err) {
+__global__ __launch_bounds__(kGatherThreads) void k_get_rows(View src, View ids, View src2, View ids2, View dst,
+                                                             uint32_t* __restrict__ err) {
     const int64_t ne0 = dst.ne[0];
     const int64_t n10 = ids.ne[0], n11 = ids.ne[1];
-    for (int64_t r = blockIdx.x; r < n_out_rows; r += gridDim.x) {
+    {
+        const int64_t r = blockIdx.x;
         int64_t i10 = r, i11 = 0, i12 = 0;
         if (ids.ne[1] * ids.ne[2] > 1) {
             i12 = r / (n11 * n10);
@@ -71,21 +66,21 @@ __global__ __launch_bounds__(256) void k_get_rows(View src, View ids, View src2,
         if (!ok) {
             // ggml aborts on an out-of-range index; here the row is zeroed and
             // the sticky device error bit is raised for the host to read.
-            for (int64_t j = threadIdx.x; j < ne0; j += blockDim.x) reinterpret_cast<float*>(d)[j] = 0.0f;
+            for (int64_t j = threadIdx.x; j < ne0; j += kGatherThreads) reinterpret_cast<float*>(d)[j] = 0.0f;
             if (threadIdx.x == 0) atomicOr(err, static_cast<uint32_t>(DEV_ERR_ROW_INDEX));
-            continue;
+            return;
         }
         const char* s = src.data + id * src.nb[1] + i11 * src.nb[2] + i12 * src.nb[3];
         const char* s2 = nullptr;
         if constexpr (TYPE2 >= 0) s2 = src2.data + id2 * src2.nb[1] + i11 * src2.nb[2] + i12 * src2.nb[3];
         if constexpr (VEC) {
-            for (int64_t j = threadIdx.x * 4; j < ne0; j += blockDim.x * 4) {
+            for (int64_t j = threadIdx.x * 4; j < ne0; j += kGatherThreads * 4) {
                 float4 v = load_row4<TYPE>(s, j);
                 if constexpr (TYPE2 >= 0) v = add4(v, load_row4<TYPE2>(s2, j));
                 *reinterpret_cast<float4*>(d + j * 4) = v;
             }
         } else {
-            for (int64_t j = threadIdx.x; j < ne0; j += blockDim.x) {
+            for (int64_t j = threadIdx.x; j < ne0; j += kGatherThreads) {
                 float v = load_row1<TYPE>(s, j);
                 if constexpr (TYPE2 >= 0) v = v + load_row1<TYPE2>(s2, j);
                 reinterpret_cast<float*>(d)[j] = v;
@@ -100,7 +95,7 @@ bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0
 // Can the table be read 4 elements at a time with aligned vector loads?
 bool vec_ok_table(const cbx_tensor* t) {
     if (!t) return true;
-    if (t->type == CBX_TYPE_Q8_0) return true;   // byte loads
+    if (t->type == CBX_TYPE_Q8_0) return (reinterpret_cast<uintptr_t>(t->data) & 1u) == 0;   // 16-bit quant loads
     const size_t a = t->type == CBX_TYPE_F32 ? 16 : 8;
     if (reinterpret_cast<uintptr_t>(t->data) % a) return false;
     for (int i = 1; i < 4; i++) if (t->nb[i] % a) return false;
@@ -110,10 +105,11 @@ bool vec_ok_table(const cbx_tensor* t) {
 template <int TYPE, int TYPE2>
 int launch_gather_t(bool vec, dim3 grid, dim3 block, hipStream_t s, View src, View ids, View src2, View ids2,
                     View dst, int64_t n, uint32_t* err) {
+    (void)n;
     if (vec) {
-        hipLaunchKernelGGL((k_get_rows<TYPE, TYPE2, true>), grid, block, 0, s, src, ids, src2, ids2, dst, n, err);
+        hipLaunchKernelGGL((k_get_rows<TYPE, TYPE2, true>), grid, block, 0, s, src, ids, src2, ids2, dst, err);
     } else {
-        hipLaunchKernelGGL((k_get_rows<TYPE, TYPE2, false>), grid, block, 0, s, src, ids, src2, ids2, dst, n, err);
+        hipLaunchKernelGGL((k_get_rows<TYPE, TYPE2, false>), grid, block, 0, s, src, ids, src2, ids2, dst, err);
     }
     return check_launch("get_rows");
 }
@@ -178,10 +174,8 @@ int launch_get_rows(const cbx_tensor* src, const cbx_tensor* ids, const cbx_tens
     const int64_t n = ids->ne[0] * ids->ne[1] * ids->ne[2];
     const bool vec = dst->ne[0] % 4 == 0 && vec_ok_table(src) && vec_ok_table(src2) && aligned16(dst->data) &&
                      dst->nb[1] % 16 == 0 && dst->nb[2] % 16 == 0 && dst->nb[3] % 16 == 0;
-    const int64_t lanes = vec ? cdiv(dst->ne[0], 4) : dst->ne[0];
-    const int threads = static_cast<int>(std::min<int64_t>(256, std::max<int64_t>(64, cdiv(lanes, 64) * 64)));
-    const dim3 grid(static_cast<unsigned>(std::min<int64_t>(n, int64_t{1} << 20)));
-    const dim3 block(threads);
+    if (n >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "get_rows: too many rows");
+    const dim3 grid(static_cast<unsigned>(n)), block(kGatherThreads);
     View vs = view_of(src), vi = view_of(ids), vd = view_of(dst);
     View vs2 = src2 ? view_of(src2) : null_view(), vi2 = ids2 ? view_of(ids2) : null_view();
     const int t2 = src2 ? src2->type : -1;

@@ -58,6 +58,23 @@ def test_q8_0_special_scales(cbx, oracle):
     assert_bitexact(host(got), exp, "q8_0 special")
 
 
+def test_q8_0_odd_address_and_added_q8_table(cbx, oracle):
+    """A Q8_0 table at an odd byte address (read byte by byte) and a second
+    Q8_0 table added in (16-bit quant loads): both as the oracle."""
+    q = oracle.quantize_q8_0(W.normal(230, (40, 128), 0.0, 0.05))
+    q2 = oracle.quantize_q8_0(W.normal(231, (40, 128), 0.0, 0.05))
+    ids = W.randint(232, (33,), 0, 40)
+    ids2 = W.randint(233, (33,), 0, 40)
+    buf = torch.zeros(q.size + 1, dtype=torch.uint8, device="cuda")
+    odd = buf[1:].view(q.shape)
+    odd.copy_(dev(q))
+    assert odd.data_ptr() % 2 == 1
+    assert_bitexact(host(cbx.get_rows(odd, dev(ids), q8_0=True)), oracle.get_rows(q, ids, q8_0=True), "odd q8")
+    got = cbx.get_rows_add(dev(q), dev(ids), dev(q2), dev(ids2), q8_0=True, q8_0_2=True)
+    exp = oracle.add(oracle.get_rows(q, ids, q8_0=True), oracle.get_rows(q2, ids2, q8_0=True))
+    assert_bitexact(host(got), exp, "q8 + q8")
+
+
 def test_f16_table_all_codes(cbx, oracle):
     """All 65536 f16 codes as one table row each: widening is exact."""
     codes = np.arange(65536, dtype=np.uint16).view(np.float16).reshape(4096, 16)
