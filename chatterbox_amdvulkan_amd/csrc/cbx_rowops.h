@@ -8,6 +8,36 @@
 namespace cbx {
 
 // ---------------------------------------------------------------------------
+// argument and row addressing for the row kernels
+// ---------------------------------------------------------------------------
+
+// Byte offset of row r of a tensor whose rows enumerate ne1, ne2, ne3
+// (fewer than 2^31 rows), with 32-bit index arithmetic.
+struct RowMap {
+    int64_t nb1, nb2, nb3;
+    uint32_t ne1, ne2;
+    uint32_t flat;   // rows at one uniform step nb1: no index split
+};
+
+inline RowMap row_map(const cbx_tensor* t) {
+    RowMap m;
+    m.flat = flat_rows(t) ? 1u : 0u;
+    m.nb1 = static_cast<int64_t>(t->nb[1]);
+    m.nb2 = static_cast<int64_t>(t->nb[2]);
+    m.nb3 = static_cast<int64_t>(t->nb[3]);
+    m.ne1 = static_cast<uint32_t>(t->ne[1] > 0 ? t->ne[1] : 1);
+    m.ne2 = static_cast<uint32_t>(t->ne[2] > 0 ? t->ne[2] : 1);
+    return m;
+}
+
+__device__ __forceinline__ int64_t row_at(const RowMap& m, uint32_t r) {
+    if (m.flat) return r * m.nb1;
+    const uint32_t i1 = r % m.ne1, q = r / m.ne1;
+    const uint32_t i2 = q % m.ne2, i3 = q / m.ne2;
+    return i1 * m.nb1 + i2 * m.nb2 + i3 * m.nb3;
+}
+
+// ---------------------------------------------------------------------------
 // wave-per-row building blocks
 // ---------------------------------------------------------------------------
 

@@ -24,28 +24,39 @@ namespace {
 
 constexpr int kMaxThreads = 256;
 
+// Compact arguments of the wave-per-row norm (a small argument block: its
+// loads are on the path to the first row load).
+struct WaveNormArgs {
+    const char* x;
+    char* y;
+    const float* w;
+    const float* b;
+    const uint16_t* tab;
+    RowMap mx, my;
+    int32_t ne0, nr;
+    float eps;
+    int32_t act;
+};
+
 // WPB waves (rows) per workgroup.  With WPB == 1 the grid has exactly one
 // workgroup per row, so there is no bounds check and no read of the block
-// size: nothing waits before the argument and row loads are issued.
+// size before the loads.
 template <typename T, int NV, int KIND, bool ACT, int WPB>
-__global__ __launch_bounds__(64 * WPB) void k_row_norm_wave(View x, View y, const float* __restrict__ w,
-                                                            const float* __restrict__ b, float eps, int act,
-                                                            const uint16_t* __restrict__ tab, int64_t nr,
-                                                            bool fx, bool fy) {
+__global__ __launch_bounds__(64 * WPB) void k_row_norm_wave(WaveNormArgs a) {
     const int lane = threadIdx.x & 63;
-    int64_t r = blockIdx.x;
+    uint32_t r = blockIdx.x;
     if constexpr (WPB > 1) {
         r = r * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-        if (r >= nr) return;   // uniform per wave
+        if (r >= static_cast<uint32_t>(a.nr)) return;   // uniform per wave
     }
-    const int64_t ne0 = x.ne[0];
-    const char* xr = x.data + row_offset(x, r, fx);
-    char* yr = y.data + row_offset(y, r, fy);
+    const int64_t ne0 = a.ne0;
+    const char* xr = a.x + row_at(a.mx, r);
+    char* yr = a.y + row_at(a.my, r);
     // affine vectors first (L2-resident), then the row: loads are
     // unconditional (clamped address), so all are in flight at once; lanes
     // past the row end zero their values afterwards
     Affine<NV> af;
-    af.load(w, b, lane, ne0);
+    af.load(a.w, a.b, lane, ne0);
     float4 v[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
@@ -56,8 +67,8 @@ __global__ __launch_bounds__(64 * WPB) void k_row_norm_wave(View x, View y, cons
     for (int k = 0; k < NV; k++) {
         if ((lane + 64 * k) * 4 >= ne0) v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    const float scale = wave_row_scale<NV, KIND>(v, lane, ne0, eps);
-    wave_row_store<T, NV, ACT>(v, lane, ne0, scale, af, w != nullptr, b != nullptr, act, tab, yr);
+    const float scale = wave_row_scale<NV, KIND>(v, lane, ne0, a.eps);
+    wave_row_store<T, NV, ACT>(v, lane, ne0, scale, af, a.w != nullptr, a.b != nullptr, a.act, a.tab, yr);
 }
 
 // ---------------------------------------------------------------------------
@@ -291,6 +302,7 @@ __global__ __launch_bounds__(kMaxThreads) void k_row_norm_loop(View x, View y, c
 
 struct NormLaunch {
     View x, y;
+    RowMap mx, my;
     const float* w;
     const float* b;
     float eps;
@@ -304,10 +316,21 @@ struct NormLaunch {
 
 template <typename T, int KIND, bool ACT, int WPB>
 void go_wave_w(const NormLaunch& L, int nv) {
-#define CBX_WAVE_CASE(N)                                                                                          \
-    case N:                                                                                                      \
-        hipLaunchKernelGGL((k_row_norm_wave<T, N, KIND, ACT, WPB>), L.grid, L.block, 0, L.s, L.x, L.y, L.w, L.b, \
-                           L.eps, L.act, L.tab, L.nr, L.fx, L.fy);                                               \
+    WaveNormArgs a;
+    a.x = L.x.data;
+    a.y = L.y.data;
+    a.w = L.w;
+    a.b = L.b;
+    a.tab = L.tab;
+    a.mx = L.mx;
+    a.my = L.my;
+    a.ne0 = static_cast<int32_t>(L.x.ne[0]);
+    a.nr = static_cast<int32_t>(L.nr);
+    a.eps = L.eps;
+    a.act = L.act;
+#define CBX_WAVE_CASE(N)                                                                       \
+    case N:                                                                                   \
+        hipLaunchKernelGGL((k_row_norm_wave<T, N, KIND, ACT, WPB>), L.grid, L.block, 0, L.s, a); \
         break;
     switch (nv) {
         CBX_WAVE_CASE(1)
@@ -395,6 +418,8 @@ int launch_row_norm(int kind, const cbx_tensor* x, const cbx_tensor* w, const cb
     L.nr = nr;
     L.fx = flat_rows(x);
     L.fy = flat_rows(y);
+    L.mx = row_map(x);
+    L.my = row_map(y);
     L.s = s;
     int nv;
     if (wave) {
@@ -402,7 +427,7 @@ int launch_row_norm(int kind, const cbx_tensor* x, const cbx_tensor* w, const cb
         const int wpb = waves_per_block(nr, st);
         L.block = dim3(64 * wpb);
         L.grid = dim3(static_cast<unsigned>(cdiv(nr, wpb)));
-        if (cdiv(nr, wpb) > 0x7fffffff) return set_error(CBX_ERR_UNSUPPORTED, "norm: too many rows");
+        if (nr >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "norm: too many rows");
     } else {
         const int64_t quads = cdiv(ne0, 4);
         const int threads = static_cast<int>(std::min<int64_t>(kMaxThreads, std::max<int64_t>(WAVE, cdiv(quads, WAVE) * WAVE)));
