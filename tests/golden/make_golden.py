@@ -111,6 +111,29 @@ def main():
     close64(gn, ref, rtol=3e-6, what="gn")
     f.update(gn_x=xg, gn_w=wg, gn_b=bg, gn_out=gn, gn_mish=O.group_norm_affine(xg, 4, 1e-5, wg, bg, True))
 
+    # attention-score epilogue: scale -> diag_mask_inf(n_past) -> soft_max
+    xs = W.normal(117, (3, 5, 40), 0.0, 6.0)
+    sm = O.scale_diag_mask_soft_max(xs, 0.125, 2)
+    t = xs.astype(np.float64) * 0.125
+    t = np.where(np.arange(40)[None, None, :] > 2 + np.arange(5)[None, :, None], -np.inf, t)
+    e = np.exp(t - t.max(-1, keepdims=True))
+    close64(sm, e / e.sum(-1, keepdims=True), rtol=1e-6, what="softmax")
+    f.update(sm_x=xs, sm_out=sm)
+
+    # LayerNorm + affine, then NEOX RoPE of the normalised row viewed as heads
+    xl = W.normal(118, (2, 6, 128), 0.2, 1.5)
+    wl = W.normal(119, (128,), 1.0, 0.05)
+    bl = W.normal(120, (128,), 0.0, 0.05)
+    pl = np.array([0, 1, 2, 3, 5, 8], dtype=np.int32)
+    lr = O.rope_ext(O.layer_norm(xl, wl, bl, 1e-5).reshape(2, 6, 2, 64), pl, 64, mode=2).reshape(xl.shape)
+    xd = xl.astype(np.float64)
+    n64 = ((xd - xd.mean(-1, keepdims=True)) / np.sqrt(xd.var(-1, keepdims=True) + 1e-5) * wl + bl).reshape(2, 6, 2, 64)
+    th = pl[None, :, None, None].astype(np.float64) * 10000.0 ** (-np.arange(32) / 32.0)
+    a0, a1 = n64[..., :32], n64[..., 32:]
+    ref = np.concatenate([a0 * np.cos(th) - a1 * np.sin(th), a0 * np.sin(th) + a1 * np.cos(th)], -1).reshape(xl.shape)
+    close64(lr, ref, rtol=3e-6, what="ln+rope")
+    f.update(lnr_x=xl, lnr_w=wl, lnr_b=bl, lnr_pos=pl, lnr_out=lr)
+
     np.savez_compressed(OUT, **f)
     print(f"wrote {OUT}: {len(f)} arrays, {os.path.getsize(OUT)} bytes")
 

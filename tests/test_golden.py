@@ -40,6 +40,10 @@ def test_oracle_reproduces_golden(oracle, G):
     assert_bitexact(oracle.snake(G["snake_x"], G["snake_a"], G["snake_ai"]), G["snake_out"], "snake")
     assert_bitexact(oracle.group_norm_affine(G["gn_x"], 4, 1e-5, G["gn_w"], G["gn_b"], False), G["gn_out"], "gn")
     assert_bitexact(oracle.group_norm_affine(G["gn_x"], 4, 1e-5, G["gn_w"], G["gn_b"], True), G["gn_mish"], "gn mish")
+    assert_bitexact(oracle.scale_diag_mask_soft_max(G["sm_x"], 0.125, 2), G["sm_out"], "softmax")
+    ln = oracle.layer_norm(G["lnr_x"], G["lnr_w"], G["lnr_b"], 1e-5)
+    assert_bitexact(oracle.rope_ext(ln.reshape(2, 6, 2, 64), G["lnr_pos"], 64, mode=2).reshape(ln.shape),
+                    G["lnr_out"], "ln+rope")
 
 
 @pytest.mark.gpu
@@ -77,3 +81,10 @@ def test_hip_matches_golden(cbx, G):
     assert_bitexact(host(cbx.group_norm(dev(G["gn_x"]), 4, 1e-5, dev(G["gn_w"]), dev(G["gn_b"]))), G["gn_out"], "gn")
     assert_close(host(cbx.group_norm(dev(G["gn_x"]), 4, 1e-5, dev(G["gn_w"]), dev(G["gn_b"]), act=cbx.MISH)),
                  G["gn_mish"], x=G["gn_out"], what="gn mish")
+    sm = host(cbx.scale_diag_mask_soft_max(dev(G["sm_x"]), 0.125, 2))
+    assert np.all(np.abs(sm - G["sm_out"]) <= 1e-5 * np.abs(G["sm_out"]) + 1e-37), "softmax"
+    assert_bitexact(sm[G["sm_out"] == 0], G["sm_out"][G["sm_out"] == 0], "softmax masked")
+    c = cbx.RopeCache(64, mode=2, n_pos=2048)
+    got = host(cbx.layer_norm_rope(dev(G["lnr_x"]), dev(G["lnr_w"]), dev(G["lnr_b"]), 1e-5, 64, dev(G["lnr_pos"]), c))
+    c.close()
+    assert_bitexact(got, G["lnr_out"], "ln+rope")

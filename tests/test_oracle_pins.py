@@ -69,6 +69,13 @@ def test_q8_0_dequant_closed_form(oracle):
     assert_bitexact(got, ref, "dequant")
 
 
+def test_workload_q8_0_tables_match_the_oracle_quantizer(oracle):
+    """The synthetic Q8_0 tables of the workloads come from the same rule."""
+    x = W.normal(W.seed_of(5, 0), (300, 1024), 0.0, 0.02)
+    x[0, :32] = 0.0                     # an all-zero block: d = 0
+    assert np.array_equal(W.quantize_q8_0(x), oracle.quantize_q8_0(x))
+
+
 def test_q8_0_quantize_rule_and_roundtrip(oracle):
     x = W.normal(3, (16, 1024), 0.0, 0.02)
     x[0, :32] = 0.0
