@@ -22,18 +22,20 @@ namespace {
 constexpr int kRowMax = 1024;
 
 struct NormRopeArgs {
-    View x, y;
+    const char* x;
+    char* y;
     const float* w;
     const float* b;
-    float eps;
-    int64_t hd;            // head size (rotation row length)
     const char* pos;
-    int64_t pos_nb0;
-    RopeParams rp;
     const float2* table;
-    int32_t n_pos;
     const float* ff;
-    bool fx, fy;           // uniform row strides
+    RowMap mx, my;
+    int64_t pos_nb0;
+    int32_t ne0, hd;       // row length, head size (rotation row length)
+    uint32_t n_tok;        // x.ne1: tokens per batch item (the position index)
+    int32_t n_pos;
+    float eps;
+    RopeParams rp;
 };
 
 // Table slot (pair index) of head-local element i, or -1 past n_dims.
@@ -48,16 +50,16 @@ template <int NV, int MODE>
 __global__ __launch_bounds__(64) void k_layer_norm_rope(NormRopeArgs a) {
     __shared__ float row[kRowMax];
     const int lane = threadIdx.x;
-    const int64_t r = blockIdx.x;                 // token row over ne1 * ne2
-    const int64_t ne0 = a.x.ne[0];
-    const char* xr = a.x.data + row_offset(a.x, r, a.fx);
-    char* yr = a.y.data + row_offset(a.y, r, a.fy);
+    const uint32_t r = blockIdx.x;                // token row over ne1 * ne2
+    const int64_t ne0 = a.ne0;
+    const char* xr = a.x + row_at(a.mx, r);
+    char* yr = a.y + row_at(a.my, r);
     const int nd = a.rp.n_dims, half = nd / 2;
 
     // position of the token (ne1 index of x); the row and affine loads go
     // out first, then the cos/sin of each of the lane's elements (table rows
     // are L2-resident), so the table latency hides under the row loads
-    const int64_t tok = r % a.x.ne[1];
+    const uint32_t tok = r % a.n_tok;
     const int32_t p = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const int32_t*>(a.pos + tok * a.pos_nb0));
     Affine<NV> af;
     af.load(a.w, a.b, lane, ne0);
@@ -170,20 +172,22 @@ int launch_layer_norm_rope(const cbx_tensor* x, const cbx_tensor* w, const cbx_t
                            const float* ff, cbx_tensor* y, DeviceState* st, hipStream_t s) {
     (void)st;
     NormRopeArgs a;
-    a.x = view_of(x);
-    a.y = view_of(y);
+    a.x = static_cast<const char*>(x->data);
+    a.y = static_cast<char*>(y->data);
     a.w = w ? static_cast<const float*>(w->data) : nullptr;
     a.b = b ? static_cast<const float*>(b->data) : nullptr;
-    a.eps = eps;
-    a.hd = head_dim;
     a.pos = static_cast<const char*>(pos->data);
-    a.pos_nb0 = static_cast<int64_t>(pos->nb[0]);
-    a.rp = p;
     a.table = table;
-    a.n_pos = n_pos;
     a.ff = ff;
-    a.fx = flat_rows(x);
-    a.fy = flat_rows(y);
+    a.mx = row_map(x);
+    a.my = row_map(y);
+    a.pos_nb0 = static_cast<int64_t>(pos->nb[0]);
+    a.ne0 = static_cast<int32_t>(x->ne[0]);
+    a.hd = static_cast<int32_t>(head_dim);
+    a.n_tok = static_cast<uint32_t>(x->ne[1]);
+    a.n_pos = n_pos;
+    a.eps = eps;
+    a.rp = p;
     const int64_t rows = x->ne[1] * x->ne[2] * x->ne[3];
     if (rows >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "layer_norm_rope: too many rows");
     const int nv = x->ne[0] <= 256 ? 1 : x->ne[0] <= 512 ? 2 : 4;

@@ -31,22 +31,33 @@ __device__ __forceinline__ float masked(float x, float s, int64_t col, int64_t l
     return col > limit ? -INFINITY : x * s;
 }
 
+struct SoftMaxArgs {
+    const char* x;
+    char* y;
+    RowMap mx, my;
+    int64_t n_past;
+    int32_t ne0, nr;
+    uint32_t n_q;          // x.ne1: the query index of a row is r % n_q
+    float s;
+};
+
 // WPB rows per workgroup; with one, the grid is exactly one workgroup per
 // row and nothing waits (bounds check, block size) before the loads issue.
 template <int NV, int WPB>
-__global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(View x, View y, float s, int64_t n_past, int64_t nr,
-                                                            bool fx, bool fy) {
+__global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
     const int lane = threadIdx.x & 63;
-    int64_t r = blockIdx.x;
+    uint32_t r = blockIdx.x;
     if constexpr (WPB > 1) {
         r = r * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-        if (r >= nr) return;   // uniform per wave
+        if (r >= static_cast<uint32_t>(a.nr)) return;   // uniform per wave
     }
-    const int64_t ne0 = x.ne[0];
-    const char* xr = x.data + row_offset(x, r, fx);
-    char* yr = y.data + row_offset(y, r, fy);
+    const int64_t ne0 = a.ne0;
+    const float s = a.s;
+    const int64_t n_past = a.n_past;
+    const char* xr = a.x + row_at(a.mx, r);
+    char* yr = a.y + row_at(a.my, r);
     // last unmasked column of this row
-    const int64_t j = r % x.ne[1];
+    const int64_t j = r % a.n_q;
     const int64_t lim = n_past >= 0 ? (n_past + j < ne0 - 1 ? n_past + j : ne0 - 1) : ne0 - 1;
     float4 v[NV];
 #pragma unroll
@@ -116,15 +127,14 @@ __global__ __launch_bounds__(kThreads) void k_soft_max_loop(View x, View y, floa
 int waves_for(int64_t rows, const DeviceState* st) { return rows >= int64_t{8} * st->n_cu ? 4 : 1; }
 
 template <int WPB>
-void sm_wave(int nv, const View& vx, const View& vy, float s, int64_t n_past, int64_t nr, bool fx, bool fy,
-             hipStream_t strm) {
-    const dim3 grid(static_cast<unsigned>(cdiv(nr, WPB))), block(64 * WPB);
+void sm_wave(int nv, const SoftMaxArgs& a, hipStream_t strm) {
+    const dim3 grid(static_cast<unsigned>(cdiv(a.nr, WPB))), block(64 * WPB);
     switch (nv) {
-        case 1: hipLaunchKernelGGL((k_soft_max_wave<1, WPB>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy); break;
-        case 2: hipLaunchKernelGGL((k_soft_max_wave<2, WPB>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy); break;
-        case 4: hipLaunchKernelGGL((k_soft_max_wave<4, WPB>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy); break;
-        case 8: hipLaunchKernelGGL((k_soft_max_wave<8, WPB>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy); break;
-        default: hipLaunchKernelGGL((k_soft_max_wave<16, WPB>), grid, block, 0, strm, vx, vy, s, n_past, nr, fx, fy); break;
+        case 1: hipLaunchKernelGGL((k_soft_max_wave<1, WPB>), grid, block, 0, strm, a); break;
+        case 2: hipLaunchKernelGGL((k_soft_max_wave<2, WPB>), grid, block, 0, strm, a); break;
+        case 4: hipLaunchKernelGGL((k_soft_max_wave<4, WPB>), grid, block, 0, strm, a); break;
+        case 8: hipLaunchKernelGGL((k_soft_max_wave<8, WPB>), grid, block, 0, strm, a); break;
+        default: hipLaunchKernelGGL((k_soft_max_wave<16, WPB>), grid, block, 0, strm, a); break;
     }
 }
 
@@ -142,8 +152,18 @@ int launch_soft_max(const cbx_tensor* x, float s, int64_t n_past, cbx_tensor* y,
     if (vec) {
         const int64_t need = cdiv(ne0, 256);
         const int nv = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : 16;
-        if (waves_for(nr, st) == 1) sm_wave<1>(nv, vx, vy, s, n_past, nr, fx, fy, strm);
-        else sm_wave<4>(nv, vx, vy, s, n_past, nr, fx, fy, strm);
+        SoftMaxArgs a;
+        a.x = static_cast<const char*>(x->data);
+        a.y = static_cast<char*>(y->data);
+        a.mx = row_map(x);
+        a.my = row_map(y);
+        a.n_past = n_past;
+        a.ne0 = static_cast<int32_t>(ne0);
+        a.nr = static_cast<int32_t>(nr);
+        a.n_q = static_cast<uint32_t>(x->ne[1]);
+        a.s = s;
+        if (waves_for(nr, st) == 1) sm_wave<1>(nv, a, strm);
+        else sm_wave<4>(nv, a, strm);
     } else {
         hipLaunchKernelGGL(k_soft_max_loop, dim3(static_cast<unsigned>(nr)), dim3(kThreads), 0, strm, vx, vy, s, n_past,
                            fx, fy);
