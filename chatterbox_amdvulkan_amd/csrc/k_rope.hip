@@ -20,34 +20,47 @@ constexpr int kRopeThreads = 256;
 
 // One workgroup per token (exactly ne2*ne3 workgroups of a fixed size: no
 // grid-stride loop bound or block-size read to wait for before the loads).
+struct RopeArgs {
+    const char* x;
+    char* y;
+    const char* pos;
+    const float2* table;
+    const float* ff;
+    int64_t xnb1, xnb2, xnb3, ynb1, ynb2, ynb3, pos_nb0;
+    uint32_t ne1, ne2, n_tail;
+    int32_t n_pos;
+    RopeParams rp;
+};
+
 template <typename T, int MODE>
-__global__ __launch_bounds__(kRopeThreads) void k_rope(View x, View y, const char* __restrict__ pos, int64_t pos_nb0,
-                                                       RopeParams rp, const float2* __restrict__ table, int32_t n_pos,
-                                                       const float* __restrict__ ff) {
+__global__ __launch_bounds__(kRopeThreads) void k_rope(RopeArgs a) {
     extern __shared__ float2 cs[];
-    const uint32_t ne1 = static_cast<uint32_t>(x.ne[1]), ne2 = static_cast<uint32_t>(x.ne[2]);
+    const RopeParams& rp = a.rp;
+    const float2* __restrict__ table = a.table;
+    const uint32_t ne1 = a.ne1, ne2 = a.ne2;
     const uint32_t half = static_cast<uint32_t>(rp.n_dims / 2);
-    const uint32_t n_tail = static_cast<uint32_t>(x.ne[0] - rp.n_dims);
+    const uint32_t n_tail = a.n_tail;
+    const int32_t n_pos = a.n_pos;
     const uint32_t t = blockIdx.x;
     const uint32_t i2 = t % ne2, i3 = t / ne2;
-    const int32_t p = *reinterpret_cast<const int32_t*>(pos + i2 * pos_nb0);
+    const int32_t p = *reinterpret_cast<const int32_t*>(a.pos + i2 * a.pos_nb0);
     for (uint32_t k = threadIdx.x; k < half; k += kRopeThreads) {
         if (p >= 0 && p < n_pos) {
             cs[k] = table[static_cast<int64_t>(p) * half + k];
         } else {
             float c, s;
-            rope_cos_sin_dev(p, static_cast<int>(k), rp, ff, &c, &s);
+            rope_cos_sin_dev(p, static_cast<int>(k), rp, a.ff, &c, &s);
             cs[k] = make_float2(c, s);
         }
     }
     __syncthreads();
-    const char* xt = x.data + i2 * x.nb[2] + i3 * x.nb[3];
-    char* yt = y.data + i2 * y.nb[2] + i3 * y.nb[3];
+    const char* xt = a.x + i2 * a.xnb2 + i3 * a.xnb3;
+    char* yt = a.y + i2 * a.ynb2 + i3 * a.ynb3;
     for (uint32_t q = threadIdx.x; q < ne1 * half; q += kRopeThreads) {
         const uint32_t h = q / half;
         const uint32_t k = q - h * half;
-        const char* xr = xt + h * x.nb[1];
-        char* yr = yt + h * y.nb[1];
+        const char* xr = xt + h * a.xnb1;
+        char* yr = yt + h * a.ynb1;
         const uint32_t ia = MODE == 2 ? k : 2 * k;
         const uint32_t ib = MODE == 2 ? k + half : 2 * k + 1;
         const float x0 = Elt<T>::load1(xr + ia * Elt<T>::size);
@@ -59,8 +72,8 @@ __global__ __launch_bounds__(kRopeThreads) void k_rope(View x, View y, const cha
     for (uint32_t q = threadIdx.x; q < ne1 * n_tail; q += kRopeThreads) {
         const uint32_t h = q / n_tail;
         const uint32_t j = static_cast<uint32_t>(rp.n_dims) + (q - h * n_tail);
-        *reinterpret_cast<T*>(yt + h * y.nb[1] + j * Elt<T>::size) =
-            *reinterpret_cast<const T*>(xt + h * x.nb[1] + j * Elt<T>::size);
+        *reinterpret_cast<T*>(yt + h * a.ynb1 + j * Elt<T>::size) =
+            *reinterpret_cast<const T*>(xt + h * a.xnb1 + j * Elt<T>::size);
     }
 }
 
@@ -75,14 +88,30 @@ int launch_rope(const cbx_tensor* x, const cbx_tensor* pos, const RopeParams& p,
     }
     const dim3 grid(static_cast<unsigned>(ntok)), block(kRopeThreads);
     const size_t lds = static_cast<size_t>(p.n_dims / 2) * sizeof(float2);
-    const char* pp = static_cast<const char*>(pos->data);
-    const int64_t pnb = static_cast<int64_t>(pos->nb[0]);
+    RopeArgs a;
+    a.x = static_cast<const char*>(x->data);
+    a.y = static_cast<char*>(y->data);
+    a.pos = static_cast<const char*>(pos->data);
+    a.table = table;
+    a.ff = ff;
+    a.xnb1 = static_cast<int64_t>(x->nb[1]);
+    a.xnb2 = static_cast<int64_t>(x->nb[2]);
+    a.xnb3 = static_cast<int64_t>(x->nb[3]);
+    a.ynb1 = static_cast<int64_t>(y->nb[1]);
+    a.ynb2 = static_cast<int64_t>(y->nb[2]);
+    a.ynb3 = static_cast<int64_t>(y->nb[3]);
+    a.pos_nb0 = static_cast<int64_t>(pos->nb[0]);
+    a.ne1 = static_cast<uint32_t>(x->ne[1]);
+    a.ne2 = static_cast<uint32_t>(x->ne[2]);
+    a.n_tail = static_cast<uint32_t>(x->ne[0] - p.n_dims);
+    a.n_pos = n_pos;
+    a.rp = p;
     if (x->type == CBX_TYPE_F32) {
-        if (p.mode == 2) hipLaunchKernelGGL((k_rope<float, 2>), grid, block, lds, s, view_of(x), view_of(y), pp, pnb, p, table, n_pos, ff);
-        else hipLaunchKernelGGL((k_rope<float, 0>), grid, block, lds, s, view_of(x), view_of(y), pp, pnb, p, table, n_pos, ff);
+        if (p.mode == 2) hipLaunchKernelGGL((k_rope<float, 2>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((k_rope<float, 0>), grid, block, lds, s, a);
     } else {
-        if (p.mode == 2) hipLaunchKernelGGL((k_rope<uint16_t, 2>), grid, block, lds, s, view_of(x), view_of(y), pp, pnb, p, table, n_pos, ff);
-        else hipLaunchKernelGGL((k_rope<uint16_t, 0>), grid, block, lds, s, view_of(x), view_of(y), pp, pnb, p, table, n_pos, ff);
+        if (p.mode == 2) hipLaunchKernelGGL((k_rope<uint16_t, 2>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((k_rope<uint16_t, 0>), grid, block, lds, s, a);
     }
     return check_launch("rope_ext");
 }

@@ -42,51 +42,85 @@ constexpr int kGatherThreads = 256;
 // TYPE2 < 0: plain gather.  VEC: rows are 16-byte aligned and ne0 % 4 == 0.
 // Exactly one workgroup per output row, of a fixed size: no loop bound or
 // block size to wait for before the id load.
+// A table operand: base, strides of its rows and of dims 2 and 3, row count.
+struct GTable {
+    const char* p;
+    int64_t nb1, nb2, nb3;
+    int64_t rows;
+};
+
+// An id operand (int32): base and the byte strides of its three dims.
+struct GIds {
+    const char* p;
+    int64_t nb0, nb1, nb2;
+};
+
+struct GatherArgs {
+    GTable src, src2;
+    GIds ids, ids2;
+    char* dst;
+    int64_t dnb1, dnb2, dnb3;
+    uint32_t n10, n11;     // ids ne0, ne1: output row r is (r % n10, (r / n10) % n11, r / (n10 * n11))
+    int32_t ne0;
+    uint32_t* err;
+};
+
 template <int TYPE, int TYPE2, bool VEC>
-__global__ __launch_bounds__(kGatherThreads) void k_get_rows(View src, View ids, View src2, View ids2, View dst,
-                                                             uint32_t* __restrict__ err) {
-    const int64_t ne0 = dst.ne[0];
-    const int64_t n10 = ids.ne[0], n11 = ids.ne[1];
-    {
-        const int64_t r = blockIdx.x;
-        int64_t i10 = r, i11 = 0, i12 = 0;
-        if (ids.ne[1] * ids.ne[2] > 1) {
-            i12 = r / (n11 * n10);
-            i11 = (r - i12 * n11 * n10) / n10;
-            i10 = r - i12 * n11 * n10 - i11 * n10;
+__global__ __launch_bounds__(kGatherThreads) void k_get_rows(GatherArgs a) {
+    const int64_t ne0 = a.ne0;
+    const uint32_t r = blockIdx.x;
+    const uint32_t i10 = r % a.n10, q = r / a.n10;
+    const uint32_t i11 = q % a.n11, i12 = q / a.n11;
+    const int32_t id = *reinterpret_cast<const int32_t*>(a.ids.p + i10 * a.ids.nb0 + i11 * a.ids.nb1 + i12 * a.ids.nb2);
+    bool ok = id >= 0 && id < a.src.rows;
+    int32_t id2 = 0;
+    if constexpr (TYPE2 >= 0) {
+        id2 = *reinterpret_cast<const int32_t*>(a.ids2.p + i10 * a.ids2.nb0 + i11 * a.ids2.nb1 + i12 * a.ids2.nb2);
+        ok = ok && id2 >= 0 && id2 < a.src2.rows;
+    }
+    char* d = a.dst + i10 * a.dnb1 + i11 * a.dnb2 + i12 * a.dnb3;
+    if (!ok) {
+        // ggml aborts on an out-of-range index; here the row is zeroed and
+        // the sticky device error bit is raised for the host to read.
+        for (int64_t j = threadIdx.x; j < ne0; j += kGatherThreads) reinterpret_cast<float*>(d)[j] = 0.0f;
+        if (threadIdx.x == 0) atomicOr(a.err, static_cast<uint32_t>(DEV_ERR_ROW_INDEX));
+        return;
+    }
+    const char* s = a.src.p + id * a.src.nb1 + i11 * a.src.nb2 + i12 * a.src.nb3;
+    const char* s2 = nullptr;
+    if constexpr (TYPE2 >= 0) s2 = a.src2.p + id2 * a.src2.nb1 + i11 * a.src2.nb2 + i12 * a.src2.nb3;
+    if constexpr (VEC) {
+        for (int64_t j = threadIdx.x * 4; j < ne0; j += kGatherThreads * 4) {
+            float4 v = load_row4<TYPE>(s, j);
+            if constexpr (TYPE2 >= 0) v = add4(v, load_row4<TYPE2>(s2, j));
+            *reinterpret_cast<float4*>(d + j * 4) = v;
         }
-        const int32_t id = *reinterpret_cast<const int32_t*>(ids.data + i10 * ids.nb[0] + i11 * ids.nb[1] + i12 * ids.nb[2]);
-        bool ok = id >= 0 && id < src.ne[1];
-        int32_t id2 = 0;
-        if constexpr (TYPE2 >= 0) {
-            id2 = *reinterpret_cast<const int32_t*>(ids2.data + i10 * ids2.nb[0] + i11 * ids2.nb[1] + i12 * ids2.nb[2]);
-            ok = ok && id2 >= 0 && id2 < src2.ne[1];
-        }
-        char* d = dst.data + i10 * dst.nb[1] + i11 * dst.nb[2] + i12 * dst.nb[3];
-        if (!ok) {
-            // ggml aborts on an out-of-range index; here the row is zeroed and
-            // the sticky device error bit is raised for the host to read.
-            for (int64_t j = threadIdx.x; j < ne0; j += kGatherThreads) reinterpret_cast<float*>(d)[j] = 0.0f;
-            if (threadIdx.x == 0) atomicOr(err, static_cast<uint32_t>(DEV_ERR_ROW_INDEX));
-            return;
-        }
-        const char* s = src.data + id * src.nb[1] + i11 * src.nb[2] + i12 * src.nb[3];
-        const char* s2 = nullptr;
-        if constexpr (TYPE2 >= 0) s2 = src2.data + id2 * src2.nb[1] + i11 * src2.nb[2] + i12 * src2.nb[3];
-        if constexpr (VEC) {
-            for (int64_t j = threadIdx.x * 4; j < ne0; j += kGatherThreads * 4) {
-                float4 v = load_row4<TYPE>(s, j);
-                if constexpr (TYPE2 >= 0) v = add4(v, load_row4<TYPE2>(s2, j));
-                *reinterpret_cast<float4*>(d + j * 4) = v;
-            }
-        } else {
-            for (int64_t j = threadIdx.x; j < ne0; j += kGatherThreads) {
-                float v = load_row1<TYPE>(s, j);
-                if constexpr (TYPE2 >= 0) v = v + load_row1<TYPE2>(s2, j);
-                reinterpret_cast<float*>(d)[j] = v;
-            }
+    } else {
+        for (int64_t j = threadIdx.x; j < ne0; j += kGatherThreads) {
+            float v = load_row1<TYPE>(s, j);
+            if constexpr (TYPE2 >= 0) v = v + load_row1<TYPE2>(s2, j);
+            reinterpret_cast<float*>(d)[j] = v;
         }
     }
+}
+
+GTable gtable(const cbx_tensor* t) {
+    GTable g;
+    g.p = t ? static_cast<const char*>(t->data) : nullptr;
+    g.nb1 = t ? static_cast<int64_t>(t->nb[1]) : 0;
+    g.nb2 = t ? static_cast<int64_t>(t->nb[2]) : 0;
+    g.nb3 = t ? static_cast<int64_t>(t->nb[3]) : 0;
+    g.rows = t ? t->ne[1] : 0;
+    return g;
+}
+
+GIds gids(const cbx_tensor* t) {
+    GIds g;
+    g.p = t ? static_cast<const char*>(t->data) : nullptr;
+    g.nb0 = t ? static_cast<int64_t>(t->nb[0]) : 0;
+    g.nb1 = t ? static_cast<int64_t>(t->nb[1]) : 0;
+    g.nb2 = t ? static_cast<int64_t>(t->nb[2]) : 0;
+    return g;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -103,25 +137,22 @@ bool vec_ok_table(const cbx_tensor* t) {
 }
 
 template <int TYPE, int TYPE2>
-int launch_gather_t(bool vec, dim3 grid, dim3 block, hipStream_t s, View src, View ids, View src2, View ids2,
-                    View dst, int64_t n, uint32_t* err) {
-    (void)n;
+int launch_gather_t(bool vec, dim3 grid, dim3 block, hipStream_t s, const GatherArgs& a) {
     if (vec) {
-        hipLaunchKernelGGL((k_get_rows<TYPE, TYPE2, true>), grid, block, 0, s, src, ids, src2, ids2, dst, err);
+        hipLaunchKernelGGL((k_get_rows<TYPE, TYPE2, true>), grid, block, 0, s, a);
     } else {
-        hipLaunchKernelGGL((k_get_rows<TYPE, TYPE2, false>), grid, block, 0, s, src, ids, src2, ids2, dst, err);
+        hipLaunchKernelGGL((k_get_rows<TYPE, TYPE2, false>), grid, block, 0, s, a);
     }
     return check_launch("get_rows");
 }
 
 template <int TYPE>
-int launch_gather_t1(int type2, bool vec, dim3 grid, dim3 block, hipStream_t s, View src, View ids, View src2,
-                     View ids2, View dst, int64_t n, uint32_t* err) {
+int launch_gather_t1(int type2, bool vec, dim3 grid, dim3 block, hipStream_t s, const GatherArgs& a) {
     switch (type2) {
-        case -1: return launch_gather_t<TYPE, -1>(vec, grid, block, s, src, ids, src2, ids2, dst, n, err);
-        case T_F32: return launch_gather_t<TYPE, T_F32>(vec, grid, block, s, src, ids, src2, ids2, dst, n, err);
-        case T_F16: return launch_gather_t<TYPE, T_F16>(vec, grid, block, s, src, ids, src2, ids2, dst, n, err);
-        default: return launch_gather_t<TYPE, T_Q8>(vec, grid, block, s, src, ids, src2, ids2, dst, n, err);
+        case -1: return launch_gather_t<TYPE, -1>(vec, grid, block, s, a);
+        case T_F32: return launch_gather_t<TYPE, T_F32>(vec, grid, block, s, a);
+        case T_F16: return launch_gather_t<TYPE, T_F16>(vec, grid, block, s, a);
+        default: return launch_gather_t<TYPE, T_Q8>(vec, grid, block, s, a);
     }
 }
 
@@ -174,15 +205,28 @@ int launch_get_rows(const cbx_tensor* src, const cbx_tensor* ids, const cbx_tens
     const int64_t n = ids->ne[0] * ids->ne[1] * ids->ne[2];
     const bool vec = dst->ne[0] % 4 == 0 && vec_ok_table(src) && vec_ok_table(src2) && aligned16(dst->data) &&
                      dst->nb[1] % 16 == 0 && dst->nb[2] % 16 == 0 && dst->nb[3] % 16 == 0;
-    if (n >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "get_rows: too many rows");
+    if (n >= (int64_t{1} << 31) || dst->ne[0] >= (int64_t{1} << 31)) {
+        return set_error(CBX_ERR_UNSUPPORTED, "get_rows: too many rows or columns");
+    }
     const dim3 grid(static_cast<unsigned>(n)), block(kGatherThreads);
-    View vs = view_of(src), vi = view_of(ids), vd = view_of(dst);
-    View vs2 = src2 ? view_of(src2) : null_view(), vi2 = ids2 ? view_of(ids2) : null_view();
+    GatherArgs a;
+    a.src = gtable(src);
+    a.src2 = gtable(src2);
+    a.ids = gids(ids);
+    a.ids2 = gids(ids2);
+    a.dst = static_cast<char*>(dst->data);
+    a.dnb1 = static_cast<int64_t>(dst->nb[1]);
+    a.dnb2 = static_cast<int64_t>(dst->nb[2]);
+    a.dnb3 = static_cast<int64_t>(dst->nb[3]);
+    a.n10 = static_cast<uint32_t>(ids->ne[0]);
+    a.n11 = static_cast<uint32_t>(ids->ne[1]);
+    a.ne0 = static_cast<int32_t>(dst->ne[0]);
+    a.err = st->err_word;
     const int t2 = src2 ? src2->type : -1;
     switch (src->type) {
-        case T_F32: return launch_gather_t1<T_F32>(t2, vec, grid, block, s, vs, vi, vs2, vi2, vd, n, st->err_word);
-        case T_F16: return launch_gather_t1<T_F16>(t2, vec, grid, block, s, vs, vi, vs2, vi2, vd, n, st->err_word);
-        default: return launch_gather_t1<T_Q8>(t2, vec, grid, block, s, vs, vi, vs2, vi2, vd, n, st->err_word);
+        case T_F32: return launch_gather_t1<T_F32>(t2, vec, grid, block, s, a);
+        case T_F16: return launch_gather_t1<T_F16>(t2, vec, grid, block, s, a);
+        default: return launch_gather_t1<T_Q8>(t2, vec, grid, block, s, a);
     }
 }
 
