@@ -172,14 +172,20 @@ def same_bits(a, b):
     return np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8))
 
 
-def bench_prefill(C, W, torch, steps, warmup, f16_table=False, fused=True, one_launch=False):
+def bench_prefill(C, W, torch, steps, warmup, f16_table=False, fused=True, one_launch=False, resident=False):
     inp = W.prefill_inputs(f16_table=False)
     nbytes = W.prefill_bytes(f16_table, fused)
     per_step = sum(nbytes.values())
-    n_sets = max(2, math.ceil(MALL_DEFEAT_BYTES / per_step))
-    log(f"prefill{' f16' if f16_table else ''}{'' if fused else ' unfused'}{' one-launch' if one_launch else ''}: "
+    # resident: every step reuses one buffer set (32 steps per graph), so the
+    # bytes come from the Infinity Cache after the first step
+    n_sets = 32 if resident else max(2, math.ceil(MALL_DEFEAT_BYTES / per_step))
+    log(f"prefill{' f16' if f16_table else ''}{'' if fused else ' unfused'}{' one-launch' if one_launch else ''}"
+        f"{' cache-resident' if resident else ''}: "
         f"{per_step} B/step, {n_sets} buffer sets")
-    sets = [PrefillSet(C, W, torch, inp, f16_table) for _ in range(n_sets)]
+    if resident:
+        sets = [PrefillSet(C, W, torch, inp, f16_table)] * n_sets
+    else:
+        sets = [PrefillSet(C, W, torch, inp, f16_table) for _ in range(n_sets)]
     if one_launch:
         step = lambda st: st.step_one_launch  # noqa: E731
     else:
@@ -610,6 +616,7 @@ def cpu_baseline(W, seconds):
         el = time.perf_counter() - t0
         if el >= seconds or reps >= 100000:
             break
+    details = cpu_other_workloads(W, O, nth, max(1.0, seconds / 5.0))
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -619,7 +626,64 @@ def cpu_baseline(W, seconds):
     return {"value": per_step * reps / el / 1e9, "unit": "GB/s", "cores": nth, "kind": "port",
             "sample": f"{reps} steps of the T3 prefill op chain (gather+pos f32, LayerNorm, GELU), "
                       f"{el:.1f} s, OpenMP row split as ggml-cpu",
-            "nproc": os.cpu_count(), "cpu_model": model}
+            "nproc": os.cpu_count(), "cpu_model": model, "details": details}
+
+
+def _timed(fn, seconds):
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 100000:
+            return reps, el
+
+
+def cpu_other_workloads(W, O, nth, seconds):
+    """The oracle on the other workloads' shapes (same inputs as the GPU
+    legs), a bounded sample each: decode step chain (us per step), the
+    64-stream f16 step, a CFM flow step, two HiFT stages."""
+    out = {}
+    steps = [W.decode_inputs(t) for t in range(W.DECODE_STEPS)]
+
+    def decode():
+        for d in steps:
+            O.rms_norm_mul(d["x"], d["g"], 1e-5, nth=nth)
+            O.rope_ext(d["q"], d["pos"], W.HEAD_DIM, mode=2, nth=nth)
+            O.rope_ext(d["k"], d["pos"], W.HEAD_DIM, mode=2, nth=nth)
+            O.swiglu(d["gate"], d["up"], nth=nth)
+    reps, el = _timed(decode, seconds)
+    out["t3_decode_us_per_step"] = el / (reps * W.DECODE_STEPS) * 1e6
+
+    sv = W.serving_inputs()
+
+    def serving():
+        O.rms_norm_mul(sv["x"], sv["g"], 1e-5, nth=nth)
+        O.rope_ext(sv["q"], sv["pos"], W.HEAD_DIM, mode=2, nth=nth)
+        O.rope_ext(sv["k"], sv["pos"], W.HEAD_DIM, mode=2, nth=nth)
+        O.swiglu(sv["gate"], sv["up"], nth=nth)
+        O.get_rows(sv["tab"], sv["ids"], q8_0=True, nth=nth)
+    reps, el = _timed(serving, seconds)
+    out["serving_64_streams_f16_GBps"] = sum(W.serving_bytes().values()) * reps / el / 1e9
+
+    cf = W.cfm_inputs()
+
+    def flow():
+        O.group_norm_affine(cf["x256"], W.CFM_GROUPS, 1e-5, cf["w256"], cf["b256"], True, nth=nth)
+        O.group_norm_affine(cf["x512"], W.CFM_GROUPS, 1e-5, cf["w512"], cf["b512"], True, nth=nth)
+        ln = O.layer_norm(cf["xa"], cf["wa"], cf["ba"], 1e-5, nth=nth)
+        O.rope_ext(ln.reshape(2, W.CFM_T, W.CFM_HEADS, W.HEAD_DIM), cf["pos"], W.HEAD_DIM, mode=2, nth=nth)
+    reps, el = _timed(flow, seconds)
+    out["cfm_flow_step_GBps"] = sum(W.cfm_bytes().values()) * reps / el / 1e9
+
+    for (B, Ch, T) in W.HIFT_SHAPES[:3:2]:
+        x = W.normal(W.seed_of(4, 2), (B, T, Ch))
+        a, ai = W.snake_alpha(Ch)
+        reps, el = _timed(lambda: O.snake(x, a, ai, nth=nth), seconds)
+        out[f"hift_snake_{B}x{Ch}x{T}_GBps"] = (8 * x.size + 8 * Ch) * reps / el / 1e9
+        reps, el = _timed(lambda: O.leaky_relu(x, 0.1, nth=nth), seconds)
+        out[f"hift_leaky_{B}x{Ch}x{T}_GBps"] = 8 * x.size * reps / el / 1e9
+    return out
 
 
 def main():
@@ -651,6 +715,8 @@ def main():
         details["prefill_f16_table_fused"] = dict(r16, GBps=gbps(r16))
         r1 = bench_prefill(C, W, torch, max(200, a.steps // 4), 20, one_launch=True)
         details["prefill_f32_one_launch"] = dict(r1, GBps=gbps(r1))
+        rr = bench_prefill(C, W, torch, max(200, a.steps // 4), 20, resident=True)
+        details["prefill_f32_fused_cache_resident"] = dict(rr, GBps=gbps(rr))
         nb = W.prefill_bytes()
         details["copy_ceiling"] = bench_copy_ceiling(C, torch, {"gelu_bytes": nb["gelu"],
                                                                 "embed_layer_norm_bytes": nb["embed_layer_norm"],
