@@ -27,12 +27,14 @@ LIB = os.path.join(PKG, "libcbxops.so")
 SOURCES = [
     "cbx_api.cpp",
     "cbx_gguf.cpp",
+    "cbx_graph.cpp",
     "k_rows.hip",
     "k_norm.hip",
     "k_group_norm.hip",
     "k_rope.hip",
     "k_norm_rope.hip",
     "k_softmax.hip",
+    "k_norm_ext.hip",
     "k_eltwise.hip",
     "k_batch.hip",
 ]

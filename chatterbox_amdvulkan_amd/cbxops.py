@@ -79,6 +79,38 @@ class GgufTensorInfo(ctypes.Structure):
     ]
 
 
+class GNode(ctypes.Structure):
+    """cbx_gnode"""
+
+    _fields_ = [
+        ("op", ctypes.c_int32),
+        ("dst", ctypes.c_int32),
+        ("src", ctypes.c_int32 * 2),
+        ("iparam", ctypes.c_int32),
+        ("fparam", ctypes.c_float),
+        ("rope", ctypes.c_void_p),
+    ]
+
+
+class GLaunch(ctypes.Structure):
+    """cbx_glaunch"""
+
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("first_node", ctypes.c_int32),
+        ("n_nodes", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+    ]
+
+
+# cbx_gop
+GOP_VIEW, GOP_GET_ROWS, GOP_ADD, GOP_MUL, GOP_SCALE, GOP_NORM, GOP_RMS_NORM, GOP_GROUP_NORM, GOP_ROPE, \
+    GOP_SOFT_MAX, GOP_DIAG_MASK_INF, GOP_UNARY, GOP_LEAKY_RELU, GOP_CPY = range(14)
+# cbx_glaunch_kind
+GL_UNSUPPORTED, GL_VIEW, GL_GET_ROWS, GL_GET_ROWS_ADD, GL_GET_ROWS_ADD_LAYER_NORM, GL_NORM, GL_LAYER_NORM, \
+    GL_LAYER_NORM_ROPE, GL_RMS_NORM, GL_GROUP_NORM, GL_SOFT_MAX, GL_SNAKE, GL_UNARY, GL_SWIGLU, GL_LEAKY_RELU, \
+    GL_ROPE, GL_CPY, GL_ADD_LAYER_NORM, GL_LAYER_NORM_MASK, GL_BIAS_ACT = range(20)
+
 # cbx_op_kind
 OP_LAYER_NORM, OP_RMS_NORM, OP_UNARY, OP_LEAKY_RELU, OP_SWIGLU, OP_ROPE, OP_GET_ROWS, \
     OP_GET_ROWS_ADD_LAYER_NORM, OP_SNAKE = range(1, 10)
@@ -133,6 +165,9 @@ def load() -> ctypes.CDLL:
         "cbx_leaky_relu": (i, [P, f, P, vp]),
         "cbx_swiglu": (i, [P, P, P, vp]),
         "cbx_snake": (i, [P, P, P, P, vp]),
+        "cbx_add_layer_norm": (i, [P, P, P, P, P, f, i, P, P, vp]),
+        "cbx_layer_norm_mask": (i, [P, P, P, f, i, P, P, vp]),
+        "cbx_bias_act": (i, [i, P, P, P, vp]),
         "cbx_run_ops": (i, [ctypes.POINTER(OpStruct), i, vp]),
         "cbx_gguf_open": (i, [ctypes.c_char_p, ctypes.POINTER(vp)]),
         "cbx_gguf_close": (None, [vp]),
@@ -142,6 +177,14 @@ def load() -> ctypes.CDLL:
         "cbx_gguf_tensor": (i, [vp, ctypes.c_int64, ctypes.POINTER(GgufTensorInfo)]),
         "cbx_gguf_describe": (i, [vp, ctypes.c_int64, vp, P]),
         "cbx_gguf_upload": (i, [vp, ctypes.c_int64, vp, ctypes.c_size_t, vp]),
+        "cbx_graph_plan": (i, [P, ctypes.c_int32, ctypes.POINTER(GNode), ctypes.c_int32,
+                               ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, ctypes.POINTER(GLaunch),
+                               ctypes.c_int32, ctypes.POINTER(ctypes.c_int32)]),
+        "cbx_graph_launch": (i, [P, ctypes.c_int32, ctypes.POINTER(GNode), ctypes.c_int32,
+                                 ctypes.POINTER(GLaunch), vp]),
+        "cbx_graph_compute": (i, [P, ctypes.c_int32, ctypes.POINTER(GNode), ctypes.c_int32,
+                                  ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, vp,
+                                  ctypes.POINTER(ctypes.c_int32)]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -444,6 +487,40 @@ def swiglu(g, u, out=None):
     return out
 
 
+def add_layer_norm(a, r, w, b, eps, a_bias=None, act=UNARY_NONE, s=None, out=None, store_sum=True):
+    """Residual join + LayerNorm: s = (a [+ a_bias]) + r, y = act(LN(s)*w + b).
+    Returns (s, y); s is None when store_sum is False."""
+    _ready(a)
+    out = _out_like(a, out)
+    if store_sum and s is None:
+        s = torch.empty_like(a)
+    if not store_sum:
+        s = None
+    _check(load().cbx_add_layer_norm(_ref(desc(a)), _ref(desc(a_bias) if a_bias is not None else None),
+                                     _ref(desc(r)), _ref(desc(w) if w is not None else None),
+                                     _ref(desc(b) if b is not None else None), eps, act,
+                                     _ref(desc(s) if s is not None else None), _ref(desc(out)), _stream()))
+    return s, out
+
+
+def layer_norm_mask(x, w, b, eps, mask, act=UNARY_NONE, out=None):
+    """act(LN(x)*w + b) * mask, mask with one value per row index i1."""
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_layer_norm_mask(_ref(desc(x)), _ref(desc(w) if w is not None else None),
+                                      _ref(desc(b) if b is not None else None), eps, act, _ref(desc(mask)),
+                                      _ref(desc(out)), _stream()))
+    return out
+
+
+def bias_act(act, x, bias, out=None):
+    """act(x + bias); bias shaped (C,) along the last dim, or (C, 1) per row."""
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_bias_act(act, _ref(desc(x)), _ref(desc(bias)), _ref(desc(out)), _stream()))
+    return out
+
+
 def snake(x, alpha, alpha_inv, out=None):
     """snake() helper: x + sin^2(x*alpha) * alpha_inv.  alpha shaped (C,) for
     channel-innermost x [.., T, C], or (C, 1) for x [.., C, T]."""
@@ -569,3 +646,61 @@ class Gguf:
             self.close()
         except Exception:
             pass
+
+
+# ---- ggml-style node lists -------------------------------------------------------
+
+class Graph:
+    """A node list for cbx_graph_*: tensors are registered once (torch
+    tensors, device or host -- planning reads only shapes, types and
+    addresses) and nodes name them by index, as a ggml graph names its
+    tensors.  plan() shows how the nodes group into launches; compute() runs
+    them on torch's current stream."""
+
+    def __init__(self):
+        self._descs: list = []
+        self._torch: list = []
+        self.nodes: list = []
+
+    def tensor(self, t: torch.Tensor, ggml_type: Optional[int] = None) -> int:
+        self._descs.append(desc(t, ggml_type))
+        self._torch.append(t)
+        return len(self._descs) - 1
+
+    def node(self, op: int, dst: int, src=(), iparam: int = 0, fparam: float = 0.0,
+             rope: Optional[RopeCache] = None) -> int:
+        s = list(src) + [-1] * (2 - len(src))
+        n = GNode()
+        n.op, n.dst, n.iparam, n.fparam = op, dst, iparam, fparam
+        n.src[0], n.src[1] = s[0], s[1]
+        n.rope = rope.handle.value if rope is not None else None
+        self.nodes.append(n)
+        return dst
+
+    def _arrays(self, keep):
+        T = (Tensor * max(1, len(self._descs)))(*self._descs)
+        N = (GNode * max(1, len(self.nodes)))(*self.nodes)
+        K = (ctypes.c_int32 * max(1, len(keep)))(*keep)
+        return T, N, K
+
+    def plan(self, keep=()) -> list:
+        """[(kind, first_node, n_nodes, flags)] from cbx_graph_plan."""
+        T, N, K = self._arrays(keep)
+        cap = max(1, len(self.nodes))
+        out = (GLaunch * cap)()
+        n = ctypes.c_int32(0)
+        _check(load().cbx_graph_plan(T, len(self._descs), N, len(self.nodes), K, len(keep), out, cap,
+                                     ctypes.byref(n)))
+        return [(out[k].kind, out[k].first_node, out[k].n_nodes, out[k].flags) for k in range(n.value)]
+
+    def compute(self, keep=()) -> int:
+        """Runs the nodes (cbx_graph_compute); returns the number of launches."""
+        for t in self._torch:
+            if t.is_cuda:
+                _ready(t)
+                break
+        T, N, K = self._arrays(keep)
+        n = ctypes.c_int32(0)
+        _check(load().cbx_graph_compute(T, len(self._descs), N, len(self.nodes), K, len(keep), _stream(),
+                                        ctypes.byref(n)))
+        return n.value

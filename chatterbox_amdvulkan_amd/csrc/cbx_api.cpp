@@ -386,6 +386,68 @@ int cbx_rms_norm_mul(const cbx_tensor* x, const cbx_tensor* g, float eps, cbx_te
     return row_norm_entry("cbx_rms_norm_mul", NORM_RMS, x, g, nullptr, eps, CBX_UNARY_NONE, y, stream);
 }
 
+// F32 operand of a fused LayerNorm with x's shape.
+static int check_f32_like(const cbx_tensor* t, const cbx_tensor* x, const char* what, const char* name) {
+    int rc = validate(t, what, name);
+    if (rc) return rc;
+    if (t->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, std::string(what) + ": " + name + " must be F32");
+    if (!same_shape(t, x)) return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": " + name + " must have x's shape");
+    return CBX_OK;
+}
+
+// Byte ranges of two tensors' rows overlap.
+static bool overlaps(const cbx_tensor* a, const cbx_tensor* b) {
+    auto span = [](const cbx_tensor* t) {
+        size_t hi = type_size(t->type);
+        for (int i = 0; i < 4; i++) hi += static_cast<size_t>(t->ne[i] > 0 ? t->ne[i] - 1 : 0) * t->nb[i];
+        return hi;
+    };
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a->data), b0 = reinterpret_cast<uintptr_t>(b->data);
+    return a0 < b0 + span(b) && b0 < a0 + span(a);
+}
+
+int cbx_add_layer_norm(const cbx_tensor* a, const cbx_tensor* a_bias, const cbx_tensor* r, const cbx_tensor* w,
+                       const cbx_tensor* b, float eps, int act, cbx_tensor* s, cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_add_layer_norm";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(a, what, "a"))) return rc;
+    if (a->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, "cbx_add_layer_norm: a must be F32");
+    if ((rc = check_f32_like(r, a, what, "r")) || (rc = check_f32_like(y, a, what, "y")) ||
+        (s && (rc = check_f32_like(s, a, what, "s")))) return rc;
+    if ((rc = check_row_param(a_bias, a, what, "a_bias")) || (rc = check_row_param(w, a, what, "w")) ||
+        (rc = check_row_param(b, a, what, "b")) || (rc = check_act(act, what))) return rc;
+    if (!(eps >= 0.0f)) return set_error(CBX_ERR_INVALID_ARG, "cbx_add_layer_norm: eps must be >= 0");
+    if (nelements(a) == 0) return CBX_OK;
+    if (s && overlaps(s, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_add_layer_norm: s and y overlap");
+    return launch_layer_norm_ext(a, a_bias, r, w, b, nullptr, eps, act, s, y, st, reinterpret_cast<hipStream_t>(stream),
+                                 what);
+}
+
+int cbx_layer_norm_mask(const cbx_tensor* x, const cbx_tensor* w, const cbx_tensor* b, float eps, int act,
+                        const cbx_tensor* mask, cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_layer_norm_mask";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(x, what, "x"))) return rc;
+    if (x->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, "cbx_layer_norm_mask: x must be F32");
+    if ((rc = check_f32_like(y, x, what, "y"))) return rc;
+    if ((rc = check_row_param(w, x, what, "w")) || (rc = check_row_param(b, x, what, "b")) ||
+        (rc = check_act(act, what)) || (rc = validate(mask, what, "mask"))) return rc;
+    if (mask->type != CBX_TYPE_F32 || mask->ne[0] != 1 || mask->ne[1] != x->ne[1] || mask->ne[2] != 1 ||
+        mask->ne[3] != 1 || (mask->ne[1] > 1 && mask->nb[1] != sizeof(float))) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_layer_norm_mask: mask must be contiguous F32 with ne = (1, x.ne1, 1, 1)");
+    }
+    if (!(eps >= 0.0f)) return set_error(CBX_ERR_INVALID_ARG, "cbx_layer_norm_mask: eps must be >= 0");
+    if (nelements(x) == 0) return CBX_OK;
+    return launch_layer_norm_ext(x, nullptr, nullptr, w, b, mask, eps, act, nullptr, y, st,
+                                 reinterpret_cast<hipStream_t>(stream), what);
+}
+
 int cbx_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
                    int act, cbx_tensor* y, cbx_stream stream) {
     const char* what = "cbx_group_norm";
@@ -613,6 +675,28 @@ int cbx_swiglu(const cbx_tensor* g, const cbx_tensor* u, cbx_tensor* y, cbx_stre
     if (!same_shape(g, y) || !same_shape(u, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_swiglu: shapes differ");
     if (nelements(y) == 0) return CBX_OK;
     return launch_swiglu(g, u, y, st, reinterpret_cast<hipStream_t>(stream));
+}
+
+int cbx_bias_act(int act, const cbx_tensor* x, const cbx_tensor* bias, cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_bias_act";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(x, what, "x")) || (rc = validate(y, what, "y")) || (rc = validate(bias, what, "bias")) ||
+        (rc = check_act(act, what))) return rc;
+    if (x->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32 || bias->type != CBX_TYPE_F32) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_bias_act: F32 only");
+    }
+    if (!same_shape(x, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_bias_act: x and y shapes differ");
+    const bool inner = bias->ne[0] == x->ne[0] && bias->ne[1] == 1 && bias->ne[2] == 1 && bias->ne[3] == 1;
+    const bool outer = bias->ne[0] == 1 && bias->ne[1] == x->ne[1] && bias->ne[2] == 1 && bias->ne[3] == 1;
+    if (!inner && !outer) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_bias_act: bias must have ne = (x.ne0,1,1,1) or (1,x.ne1,1,1)");
+    }
+    if (!is_contiguous(bias)) return set_error(CBX_ERR_UNSUPPORTED, "cbx_bias_act: bias must be contiguous");
+    if (nelements(x) == 0) return CBX_OK;
+    return launch_bias_act(act, x, bias, y, st, reinterpret_cast<hipStream_t>(stream));
 }
 
 int cbx_snake(const cbx_tensor* x, const cbx_tensor* alpha, const cbx_tensor* alpha_inv, cbx_tensor* y,

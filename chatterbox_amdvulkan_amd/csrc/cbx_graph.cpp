@@ -1,0 +1,530 @@
+// cbx_graph.cpp -- runs a list of ggml-style op nodes by mapping the
+// reference's op compositions onto the fused entry points.
+//
+// The reference reaches its layer ops through ggml graphs that the backend
+// scheduler runs node by node (chatterbox-cpp/src/backend.cpp:108-122); its
+// helpers emit the same short node chains every time: layer_norm() is
+// norm -> mul -> add (cfm_decoder.cpp:29-33), mish() is softplus -> tanh ->
+// mul (cfm_decoder.cpp:36-38) and follows a layer_norm in causal_block1d
+// (cfm_decoder.cpp:143-146), snake() is mul -> sin -> sqr -> mul -> add
+// (hift_vocoder.cpp:64-73), the T3 input is get_rows -> cast -> get_rows ->
+// cast -> add -> norm -> mul -> add (t3.cpp:446-466), attention scores are
+// scale -> diag_mask_inf -> soft_max (t3.cpp:513-518), a block's residual
+// join is add(add(mul_mat, bias), h) -> layer_norm (t3.cpp:528-532), its
+// feed-forward input add(mul_mat, bias) -> gelu (t3.cpp:535-537), and
+// causal_block1d ends layer_norm -> mish -> mul(mask) (cfm_decoder.cpp:
+// 143-148).  The planner walks
+// the nodes in order and, at each node, takes the longest such chain whose
+// intermediate results no other node reads and the caller does not keep;
+// the chain then runs as one library call.  Because a chain is a run of
+// consecutive nodes of a topologically ordered list, every value it reads
+// from outside is ready when its first node's turn comes.  Host code only:
+// every launch goes through the public entry points, which check operand
+// layouts as they do for any caller.
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <vector>
+
+#include "cbx_internal.h"
+
+using namespace cbx;
+
+namespace {
+
+struct Planner {
+    const cbx_tensor* t;
+    int32_t n_t;
+    const cbx_gnode* nd;
+    int32_t n;
+    std::vector<int32_t> uses;   // how many node operands name each tensor
+    std::vector<char> keep;
+
+    bool valid_t(int32_t i) const { return i >= 0 && i < n_t; }
+    bool is(int32_t i, int op) const { return i < n && nd[i].op == op; }
+    bool is_unary(int32_t i, int u) const { return is(i, CBX_GOP_UNARY) && nd[i].iparam == u; }
+    // An intermediate may stay unstored: the caller does not keep it and the
+    // `inside` operands that read it within the chain are all its readers.
+    bool internal(int32_t tensor, int inside) const {
+        return valid_t(tensor) && !keep[static_cast<size_t>(tensor)] && uses[static_cast<size_t>(tensor)] == inside;
+    }
+    bool dims(int32_t p, int64_t a, int64_t b, int64_t c, int64_t d) const {
+        return valid_t(p) && t[p].ne[0] == a && t[p].ne[1] == b && t[p].ne[2] == c && t[p].ne[3] == d;
+    }
+    bool row_vec(int32_t p, int32_t x) const { return valid_t(x) && dims(p, t[x].ne[0], 1, 1, 1); }
+    bool chan_vec(int32_t p, int32_t x) const { return valid_t(x) && dims(p, 1, 1, t[x].ne[2], 1); }
+    bool same_dims(int32_t a, int32_t b) const {
+        return valid_t(a) && valid_t(b) && dims(a, t[b].ne[0], t[b].ne[1], t[b].ne[2], t[b].ne[3]);
+    }
+
+    // mish(x) = mul(x, tanh(softplus(x))) at node i
+    bool mish_at(int32_t i, int32_t x) const {
+        return is_unary(i, CBX_UNARY_SOFTPLUS) && nd[i].src[0] == x && is_unary(i + 1, CBX_UNARY_TANH) &&
+               nd[i + 1].src[0] == nd[i].dst && is(i + 2, CBX_GOP_MUL) && nd[i + 2].src[0] == x &&
+               nd[i + 2].src[1] == nd[i + 1].dst && internal(nd[i].dst, 1) && internal(nd[i + 1].dst, 1);
+    }
+
+    // layer_norm(x) = add(mul(norm(x), w), b) at node i, w and b (x.ne0)
+    bool layer_norm_at(int32_t i) const {
+        if (!is(i, CBX_GOP_NORM)) return false;
+        const int32_t x = nd[i].src[0];
+        return is(i + 1, CBX_GOP_MUL) && nd[i + 1].src[0] == nd[i].dst && row_vec(nd[i + 1].src[1], x) &&
+               is(i + 2, CBX_GOP_ADD) && nd[i + 2].src[0] == nd[i + 1].dst && row_vec(nd[i + 2].src[1], x) &&
+               internal(nd[i].dst, 1) && internal(nd[i + 1].dst, 1);
+    }
+
+    // a cast right after a gather takes over its result: 1 node, or 0
+    int32_t cast_after(int32_t i, int32_t* value) const {
+        if (is(i, CBX_GOP_CPY) && nd[i].src[0] == *value && internal(*value, 1) && valid_t(nd[i].dst) &&
+            t[nd[i].dst].type == CBX_TYPE_F32) {
+            *value = nd[i].dst;
+            return 1;
+        }
+        return 0;
+    }
+
+    bool col_vec(int32_t p, int32_t x) const { return valid_t(x) && dims(p, 1, t[x].ne[1], 1, 1); }
+
+    // layer_norm at node i reading `in`, optionally followed by a mish
+    // chain: the node count (3 or 6), or 0
+    int32_t layer_norm_mish_at(int32_t i, int32_t in) const {
+        if (!layer_norm_at(i) || nd[i].src[0] != in) return 0;
+        const int32_t y = nd[i + 2].dst;
+        return mish_at(i + 3, y) && internal(y, 2) ? 6 : 3;
+    }
+
+    // norm -> mul -> add -> view -> rope, the view splitting rows into heads
+    bool layer_norm_rope_at(int32_t i) const {
+        if (!layer_norm_at(i) || !is(i + 3, CBX_GOP_VIEW) || !is(i + 4, CBX_GOP_ROPE)) return false;
+        const int32_t x = nd[i].src[0], y = nd[i + 2].dst, v = nd[i + 3].dst, r = nd[i + 4].dst;
+        if (nd[i + 3].src[0] != y || nd[i + 4].src[0] != v || !internal(y, 1) || !internal(v, 1) || !valid_t(x)) {
+            return false;
+        }
+        const cbx_tensor &X = t[x], &Y = t[y], &V = t[v], &R = t[r];
+        return X.ne[3] == 1 && V.ne[0] > 0 && V.ne[0] * V.ne[1] == X.ne[0] && V.ne[2] == X.ne[1] &&
+               V.ne[3] == X.ne[2] && V.data == Y.data && V.type == CBX_TYPE_F32 && R.type == CBX_TYPE_F32 &&
+               is_contiguous(&Y) && is_contiguous(&V) && is_contiguous(&R) && same_dims(r, v);
+    }
+
+    // The longest chain at node i: its kind, *len nodes, *flags.
+    int32_t match(int32_t i, int32_t* len, int32_t* flags) const {
+        const cbx_gnode& a = nd[i];
+        *len = 1;
+        *flags = 0;
+        switch (a.op) {
+            case CBX_GOP_VIEW:
+                return CBX_GL_VIEW;
+            case CBX_GOP_GET_ROWS: {
+                int32_t g1 = a.dst;
+                const int32_t j = i + 1 + cast_after(i + 1, &g1);
+                if (is(j, CBX_GOP_GET_ROWS)) {
+                    int32_t g2 = nd[j].dst;
+                    const int32_t k = j + 1 + cast_after(j + 1, &g2);
+                    if (is(k, CBX_GOP_ADD) && nd[k].src[0] == g1 && nd[k].src[1] == g2 && same_dims(g1, g2) &&
+                        internal(g1, 1) && internal(g2, 1)) {
+                        const int32_t h = nd[k].dst;
+                        if (layer_norm_at(k + 1) && nd[k + 1].src[0] == h) {
+                            // h is the residual stream: stored unless only the norm reads it
+                            if (internal(h, 1)) *flags = 1;
+                            *len = k + 4 - i;
+                            return CBX_GL_GET_ROWS_ADD_LAYER_NORM;
+                        }
+                        *len = k + 1 - i;
+                        return CBX_GL_GET_ROWS_ADD;
+                    }
+                }
+                *len = j - i;
+                return CBX_GL_GET_ROWS;
+            }
+            case CBX_GOP_NORM: {
+                if (layer_norm_rope_at(i)) {
+                    *len = 5;
+                    return CBX_GL_LAYER_NORM_ROPE;
+                }
+                const int32_t l = layer_norm_mish_at(i, a.src[0]);
+                if (!l) return CBX_GL_NORM;
+                *len = l;
+                // causal_block1d's post-mask: mul(., mask) with one value per frame
+                const int32_t z = nd[i + l - 1].dst;
+                if (is(i + l, CBX_GOP_MUL) && nd[i + l].src[0] == z && internal(z, 1) &&
+                    col_vec(nd[i + l].src[1], a.src[0])) {
+                    *len = l + 1;
+                    return CBX_GL_LAYER_NORM_MASK;
+                }
+                return CBX_GL_LAYER_NORM;
+            }
+            case CBX_GOP_ADD: {
+                const int32_t x = a.src[0], t1 = a.dst;
+                const bool bias = row_vec(a.src[1], x);
+                // bias add -> residual add -> layer_norm [-> mish]
+                if (bias && is(i + 1, CBX_GOP_ADD) && internal(t1, 1)) {
+                    const cbx_gnode& r = nd[i + 1];
+                    const int32_t other = r.src[0] == t1 ? r.src[1] : r.src[1] == t1 ? r.src[0] : -1;
+                    const int32_t l = same_dims(other, x) ? layer_norm_mish_at(i + 2, r.dst) : 0;
+                    if (l) {
+                        if (internal(r.dst, 1)) *flags = 1;
+                        *len = 2 + l;
+                        return CBX_GL_ADD_LAYER_NORM;
+                    }
+                }
+                // residual add -> layer_norm [-> mish]
+                if (same_dims(a.src[1], x)) {
+                    const int32_t l = layer_norm_mish_at(i + 1, t1);
+                    if (l) {
+                        if (internal(t1, 1)) *flags = 1;
+                        *len = 1 + l;
+                        return CBX_GL_ADD_LAYER_NORM;
+                    }
+                    if (!bias) return CBX_GL_UNSUPPORTED;   // (a one-row x is also a bias add)
+                }
+                // bias add [-> activation]
+                if (!bias && !col_vec(a.src[1], x)) return CBX_GL_UNSUPPORTED;
+                if (is_unary(i + 1, CBX_UNARY_SOFTPLUS) && mish_at(i + 1, t1) && internal(t1, 2)) {
+                    *len = 4;
+                } else if (is(i + 1, CBX_GOP_UNARY) && nd[i + 1].src[0] == t1 && internal(t1, 1) &&
+                           nd[i + 1].iparam >= CBX_UNARY_GELU && nd[i + 1].iparam <= CBX_UNARY_MISH) {
+                    *len = 2;
+                }
+                return CBX_GL_BIAS_ACT;
+            }
+            case CBX_GOP_RMS_NORM:
+                if (is(i + 1, CBX_GOP_MUL) && nd[i + 1].src[0] == a.dst && row_vec(nd[i + 1].src[1], a.src[0]) &&
+                    internal(a.dst, 1)) {
+                    *len = 2;
+                }
+                return CBX_GL_RMS_NORM;
+            case CBX_GOP_GROUP_NORM: {
+                int32_t y = a.dst;
+                if (is(i + 1, CBX_GOP_MUL) && nd[i + 1].src[0] == a.dst && chan_vec(nd[i + 1].src[1], a.src[0]) &&
+                    is(i + 2, CBX_GOP_ADD) && nd[i + 2].src[0] == nd[i + 1].dst &&
+                    chan_vec(nd[i + 2].src[1], a.src[0]) && internal(a.dst, 1) && internal(nd[i + 1].dst, 1)) {
+                    y = nd[i + 2].dst;
+                    *len = 3;
+                }
+                if (mish_at(i + *len, y) && internal(y, 2)) *len += 3;
+                return CBX_GL_GROUP_NORM;
+            }
+            case CBX_GOP_SCALE:
+            case CBX_GOP_DIAG_MASK_INF: {
+                // scale and the mask only fuse into a plain soft_max: a
+                // soft_max with its own scale would round twice
+                int32_t j = i, prev = a.src[0];
+                if (is(j, CBX_GOP_SCALE)) prev = nd[j++].dst;
+                if (is(j, CBX_GOP_DIAG_MASK_INF) && (j == i || (nd[j].src[0] == prev && internal(prev, 1)))) {
+                    if (nd[j].iparam < 0) return CBX_GL_UNSUPPORTED;
+                    prev = nd[j++].dst;
+                }
+                if (is(j, CBX_GOP_SOFT_MAX) && nd[j].src[0] == prev && internal(prev, 1) && nd[j].src[1] < 0 &&
+                    nd[j].fparam == 1.0f) {
+                    *len = j + 1 - i;
+                    return CBX_GL_SOFT_MAX;
+                }
+                return CBX_GL_UNSUPPORTED;
+            }
+            case CBX_GOP_SOFT_MAX:
+                return a.src[1] < 0 ? CBX_GL_SOFT_MAX : CBX_GL_UNSUPPORTED;
+            case CBX_GOP_MUL: {
+                const int32_t x = a.src[0], al = a.src[1];
+                const bool bcast = row_vec(al, x) || (valid_t(x) && dims(al, 1, t[x].ne[1], 1, 1));
+                if (bcast && is_unary(i + 1, CBX_UNARY_SIN) && nd[i + 1].src[0] == a.dst &&
+                    is_unary(i + 2, CBX_UNARY_SQR) && nd[i + 2].src[0] == nd[i + 1].dst && is(i + 3, CBX_GOP_MUL) &&
+                    nd[i + 3].src[0] == nd[i + 2].dst && same_dims(nd[i + 3].src[1], al) && is(i + 4, CBX_GOP_ADD) &&
+                    nd[i + 4].src[0] == x && nd[i + 4].src[1] == nd[i + 3].dst && internal(a.dst, 1) &&
+                    internal(nd[i + 1].dst, 1) && internal(nd[i + 2].dst, 1) && internal(nd[i + 3].dst, 1)) {
+                    *len = 5;
+                    return CBX_GL_SNAKE;
+                }
+                return CBX_GL_UNSUPPORTED;
+            }
+            case CBX_GOP_UNARY: {
+                const int32_t x = a.src[0];
+                if (a.iparam == CBX_UNARY_SOFTPLUS && mish_at(i, x)) {
+                    *len = 3;
+                    return CBX_GL_UNARY;
+                }
+                if (a.iparam == CBX_UNARY_SILU && is(i + 1, CBX_GOP_MUL) && nd[i + 1].src[0] == a.dst &&
+                    same_dims(nd[i + 1].src[1], x) && internal(a.dst, 1)) {
+                    *len = 2;
+                    return CBX_GL_SWIGLU;
+                }
+                return a.iparam >= CBX_UNARY_GELU && a.iparam <= CBX_UNARY_MISH ? CBX_GL_UNARY : CBX_GL_UNSUPPORTED;
+            }
+            case CBX_GOP_LEAKY_RELU:
+                return CBX_GL_LEAKY_RELU;
+            case CBX_GOP_ROPE:
+                return CBX_GL_ROPE;
+            case CBX_GOP_CPY:
+                return CBX_GL_CPY;
+            default:
+                return CBX_GL_UNSUPPORTED;
+        }
+    }
+};
+
+const char* op_name(int op) {
+    switch (op) {
+        case CBX_GOP_VIEW: return "VIEW";
+        case CBX_GOP_GET_ROWS: return "GET_ROWS";
+        case CBX_GOP_ADD: return "ADD";
+        case CBX_GOP_MUL: return "MUL";
+        case CBX_GOP_SCALE: return "SCALE";
+        case CBX_GOP_NORM: return "NORM";
+        case CBX_GOP_RMS_NORM: return "RMS_NORM";
+        case CBX_GOP_GROUP_NORM: return "GROUP_NORM";
+        case CBX_GOP_ROPE: return "ROPE";
+        case CBX_GOP_SOFT_MAX: return "SOFT_MAX";
+        case CBX_GOP_DIAG_MASK_INF: return "DIAG_MASK_INF";
+        case CBX_GOP_UNARY: return "UNARY";
+        case CBX_GOP_LEAKY_RELU: return "LEAKY_RELU";
+        case CBX_GOP_CPY: return "CPY";
+        default: return "unknown op";
+    }
+}
+
+int check_lists(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes,
+                const char* what) {
+    if ((!tensors && n_tensors) || n_tensors < 0 || (!nodes && n_nodes) || n_nodes < 0) {
+        return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": bad tensor or node array");
+    }
+    for (int32_t i = 0; i < n_nodes; i++) {
+        bool ok = nodes[i].dst >= 0 && nodes[i].dst < n_tensors;
+        for (int32_t s : nodes[i].src) ok = ok && s >= -1 && s < n_tensors;
+        if (!ok) {
+            return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": node " + std::to_string(i) +
+                                                      " names a tensor index out of range");
+        }
+    }
+    return CBX_OK;
+}
+
+int plan(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes, const int32_t* keep,
+         int32_t n_keep, std::vector<cbx_glaunch>* out, const char* what) {
+    int rc = check_lists(tensors, n_tensors, nodes, n_nodes, what);
+    if (rc) return rc;
+    if ((!keep && n_keep) || n_keep < 0) return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": bad keep array");
+    Planner p{tensors, n_tensors, nodes, n_nodes, std::vector<int32_t>(static_cast<size_t>(n_tensors), 0),
+              std::vector<char>(static_cast<size_t>(n_tensors), 0)};
+    for (int32_t k = 0; k < n_keep; k++) {
+        if (!p.valid_t(keep[k])) return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": keep index out of range");
+        p.keep[static_cast<size_t>(keep[k])] = 1;
+    }
+    for (int32_t i = 0; i < n_nodes; i++) {
+        for (int32_t s : nodes[i].src) {
+            if (s >= 0) p.uses[static_cast<size_t>(s)]++;
+        }
+    }
+    for (int32_t i = 0; i < n_nodes;) {
+        int32_t len = 1, flags = 0;
+        const int32_t kind = p.match(i, &len, &flags);
+        out->push_back(cbx_glaunch{kind, i, kind == CBX_GL_UNSUPPORTED ? 1 : len, flags});
+        i += out->back().n_nodes;
+    }
+    return CBX_OK;
+}
+
+const cbx_tensor* T(const cbx_tensor* t, int32_t i) { return i >= 0 ? &t[i] : nullptr; }
+
+// Node counts a launch of each kind may span.
+constexpr int32_t kSpan[][2] = {
+    {1, 1},  // UNSUPPORTED
+    {1, 1},  // VIEW
+    {1, 2},  // GET_ROWS [cast]
+    {3, 5},  // GET_ROWS_ADD
+    {6, 8},  // GET_ROWS_ADD_LAYER_NORM
+    {1, 1},  // NORM
+    {3, 6},  // LAYER_NORM [mish]
+    {5, 5},  // LAYER_NORM_ROPE
+    {1, 2},  // RMS_NORM [mul]
+    {1, 6},  // GROUP_NORM [affine] [mish]
+    {1, 3},  // SOFT_MAX [scale] [mask]
+    {5, 5},  // SNAKE
+    {1, 3},  // UNARY / mish
+    {2, 2},  // SWIGLU
+    {1, 1},  // LEAKY_RELU
+    {1, 1},  // ROPE
+    {1, 1},  // CPY
+    {4, 8},  // ADD_LAYER_NORM [bias] [mish]
+    {4, 7},  // LAYER_NORM_MASK [mish]
+    {1, 4},  // BIAS_ACT [act | mish]
+};
+constexpr int32_t kLastKind = CBX_GL_BIAS_ACT;
+static_assert(sizeof(kSpan) / sizeof(kSpan[0]) == kLastKind + 1, "one span per launch kind");
+
+// Issues the entry point a launch maps to.  A launch is only read within
+// the node list, so one not made by the planner cannot read past it.
+int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_glaunch& l, cbx_stream s) {
+    if (l.kind < CBX_GL_UNSUPPORTED || l.kind > kLastKind || l.first_node < 0 || l.n_nodes < kSpan[l.kind][0] ||
+        l.n_nodes > kSpan[l.kind][1] || l.first_node > n_nodes - l.n_nodes) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_graph_launch: launch does not fit the node list");
+    }
+    const int32_t f = l.first_node;
+    const cbx_gnode& a = nd[f];
+    cbx_tensor* y = const_cast<cbx_tensor*>(&t[nd[f + l.n_nodes - 1].dst]);
+    switch (l.kind) {
+        case CBX_GL_UNSUPPORTED:
+            return set_error(CBX_ERR_UNSUPPORTED, std::string("cbx_graph_launch: node ") + std::to_string(f) + " (" +
+                                                      op_name(a.op) + ") starts no chain the library runs");
+        case CBX_GL_VIEW:
+            return CBX_OK;
+        case CBX_GL_GET_ROWS:
+            return cbx_get_rows(T(t, a.src[0]), T(t, a.src[1]), y, s);
+        case CBX_GL_GET_ROWS_ADD:
+        case CBX_GL_GET_ROWS_ADD_LAYER_NORM: {
+            const int32_t k_add = l.kind == CBX_GL_GET_ROWS_ADD ? f + l.n_nodes - 1 : f + l.n_nodes - 4;
+            const int32_t j = nd[f + 1].op == CBX_GOP_CPY ? f + 2 : f + 1;   // the second gather
+            const cbx_gnode& b = nd[j];
+            if (l.kind == CBX_GL_GET_ROWS_ADD) {
+                return cbx_get_rows_add(T(t, a.src[0]), T(t, a.src[1]), T(t, b.src[0]), T(t, b.src[1]), y, s);
+            }
+            cbx_tensor* h = (l.flags & 1) ? nullptr : const_cast<cbx_tensor*>(&t[nd[k_add].dst]);
+            return cbx_get_rows_add_layer_norm(T(t, a.src[0]), T(t, a.src[1]), T(t, b.src[0]), T(t, b.src[1]),
+                                               T(t, nd[k_add + 2].src[1]), T(t, nd[k_add + 3].src[1]),
+                                               nd[k_add + 1].fparam, h, y, s);
+        }
+        case CBX_GL_NORM:
+            return cbx_norm(T(t, a.src[0]), a.fparam, y, s);
+        case CBX_GL_LAYER_NORM:
+            if (l.n_nodes != 3 && l.n_nodes != 6) break;
+            return cbx_layer_norm(T(t, a.src[0]), T(t, nd[f + 1].src[1]), T(t, nd[f + 2].src[1]), a.fparam,
+                                  l.n_nodes == 6 ? CBX_UNARY_MISH : CBX_UNARY_NONE, y, s);
+        case CBX_GL_LAYER_NORM_ROPE: {
+            const cbx_tensor* x = T(t, a.src[0]);
+            if (!x) break;
+            // the rope output re-described with the rows' shape (C, n_tok, batch)
+            cbx_tensor out = *y;
+            out.ne[0] = x->ne[0];
+            out.ne[1] = x->ne[1];
+            out.ne[2] = x->ne[2];
+            out.ne[3] = 1;
+            out.nb[0] = sizeof(float);
+            for (int k = 1; k < 4; k++) out.nb[k] = out.nb[k - 1] * static_cast<size_t>(out.ne[k - 1]);
+            const cbx_gnode& r = nd[f + 4];
+            return cbx_layer_norm_rope(x, T(t, nd[f + 1].src[1]), T(t, nd[f + 2].src[1]), a.fparam,
+                                       t[nd[f + 3].dst].ne[0], T(t, r.src[1]), r.rope, &out, s);
+        }
+        case CBX_GL_RMS_NORM:
+            if (l.n_nodes == 2) return cbx_rms_norm_mul(T(t, a.src[0]), T(t, nd[f + 1].src[1]), a.fparam, y, s);
+            return cbx_rms_norm(T(t, a.src[0]), a.fparam, y, s);
+        case CBX_GL_GROUP_NORM: {
+            if (l.n_nodes == 2 || l.n_nodes == 5) break;
+            const bool affine = l.n_nodes == 3 || l.n_nodes == 6;
+            const bool mish = l.n_nodes == 4 || l.n_nodes == 6;
+            return cbx_group_norm(T(t, a.src[0]), a.iparam, a.fparam, affine ? T(t, nd[f + 1].src[1]) : nullptr,
+                                  affine ? T(t, nd[f + 2].src[1]) : nullptr, mish ? CBX_UNARY_MISH : CBX_UNARY_NONE, y,
+                                  s);
+        }
+        case CBX_GL_SOFT_MAX: {
+            if (l.n_nodes == 1) return cbx_scale_diag_mask_soft_max(T(t, a.src[0]), a.fparam, -1, y, s);
+            float scale = 1.0f;
+            int32_t n_past = -1;
+            for (int32_t k = f; k < f + l.n_nodes - 1; k++) {
+                if (nd[k].op == CBX_GOP_SCALE) scale = nd[k].fparam;
+                if (nd[k].op == CBX_GOP_DIAG_MASK_INF) {
+                    if (nd[k].iparam < 0) {
+                        return set_error(CBX_ERR_INVALID_ARG, "cbx_graph_launch: DIAG_MASK_INF needs n_past >= 0");
+                    }
+                    n_past = nd[k].iparam;
+                }
+            }
+            return cbx_scale_diag_mask_soft_max(T(t, a.src[0]), scale, n_past, y, s);
+        }
+        case CBX_GL_SNAKE:
+            return cbx_snake(T(t, a.src[0]), T(t, a.src[1]), T(t, nd[f + 3].src[1]), y, s);
+        case CBX_GL_UNARY:
+            if (l.n_nodes == 3) return cbx_unary(CBX_UNARY_MISH, T(t, a.src[0]), y, s);
+            if (l.n_nodes != 1) break;
+            return cbx_unary(a.iparam, T(t, a.src[0]), y, s);
+        case CBX_GL_SWIGLU:
+            return cbx_swiglu(T(t, a.src[0]), T(t, nd[f + 1].src[1]), y, s);
+        case CBX_GL_LEAKY_RELU:
+            return cbx_leaky_relu(T(t, a.src[0]), a.fparam, y, s);
+        case CBX_GL_ROPE:
+            return cbx_rope_ext(T(t, a.src[0]), T(t, a.src[1]), a.rope, y, s);
+        case CBX_GL_CPY:
+            return cbx_cpy(T(t, a.src[0]), y, s);
+        case CBX_GL_ADD_LAYER_NORM: {
+            if (l.n_nodes == 6) break;
+            const bool bias = l.n_nodes == 5 || l.n_nodes == 8;
+            const int32_t k = bias ? f + 1 : f;        // the residual add
+            const int32_t ln = k + 1;                  // the norm
+            const cbx_gnode& r = nd[k];
+            const int32_t other = !bias ? r.src[1] : r.src[0] == a.dst ? r.src[1] : r.src[0];
+            cbx_tensor* sum = (l.flags & 1) ? nullptr : const_cast<cbx_tensor*>(&t[r.dst]);
+            return cbx_add_layer_norm(T(t, a.src[0]), bias ? T(t, a.src[1]) : nullptr, T(t, other),
+                                      T(t, nd[ln + 1].src[1]), T(t, nd[ln + 2].src[1]), nd[ln].fparam,
+                                      l.n_nodes >= 7 ? CBX_UNARY_MISH : CBX_UNARY_NONE, sum, y, s);
+        }
+        case CBX_GL_LAYER_NORM_MASK:
+            if (l.n_nodes != 4 && l.n_nodes != 7) break;
+            return cbx_layer_norm_mask(T(t, a.src[0]), T(t, nd[f + 1].src[1]), T(t, nd[f + 2].src[1]), a.fparam,
+                                       l.n_nodes == 7 ? CBX_UNARY_MISH : CBX_UNARY_NONE,
+                                       T(t, nd[f + l.n_nodes - 1].src[1]), y, s);
+        case CBX_GL_BIAS_ACT: {
+            if (l.n_nodes == 3) break;
+            const int act = l.n_nodes == 1 ? CBX_UNARY_NONE : l.n_nodes == 4 ? CBX_UNARY_MISH : nd[f + 1].iparam;
+            return cbx_bias_act(act, T(t, a.src[0]), T(t, a.src[1]), y, s);
+        }
+        default:
+            break;
+    }
+    return set_error(CBX_ERR_INVALID_ARG, "cbx_graph_launch: launch does not fit the node list");
+}
+
+}  // namespace
+
+extern "C" {
+
+int cbx_graph_plan(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes,
+                   const int32_t* keep, int32_t n_keep, cbx_glaunch* launches, int32_t max_launches,
+                   int32_t* n_launches) {
+    clear_error();
+    std::vector<cbx_glaunch> ls;
+    const int rc = plan(tensors, n_tensors, nodes, n_nodes, keep, n_keep, &ls, "cbx_graph_plan");
+    if (n_launches) *n_launches = static_cast<int32_t>(ls.size());
+    if (rc) return rc;
+    if (static_cast<int64_t>(ls.size()) > max_launches || (!launches && !ls.empty())) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_graph_plan: " + std::to_string(ls.size()) +
+                                                  " launches do not fit max_launches");
+    }
+    for (size_t k = 0; k < ls.size(); k++) launches[k] = ls[k];
+    return CBX_OK;
+}
+
+int cbx_graph_launch(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes,
+                     const cbx_glaunch* launch, cbx_stream stream) {
+    clear_error();
+    int rc = check_lists(tensors, n_tensors, nodes, n_nodes, "cbx_graph_launch");
+    if (rc) return rc;
+    if (!launch) return set_error(CBX_ERR_INVALID_ARG, "cbx_graph_launch: launch is NULL");
+    return run(tensors, nodes, n_nodes, *launch, stream);
+}
+
+int cbx_graph_compute(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes,
+                      const int32_t* keep, int32_t n_keep, cbx_stream stream, int32_t* n_launches) {
+    clear_error();
+    if (n_launches) *n_launches = 0;
+    std::vector<cbx_glaunch> ls;
+    int rc = plan(tensors, n_tensors, nodes, n_nodes, keep, n_keep, &ls, "cbx_graph_compute");
+    if (rc) return rc;
+    for (const cbx_glaunch& l : ls) {
+        if (l.kind == CBX_GL_UNSUPPORTED) {
+            return set_error(CBX_ERR_UNSUPPORTED, "cbx_graph_compute: node " + std::to_string(l.first_node) + " (" +
+                                                      op_name(nodes[l.first_node].op) +
+                                                      ") starts no chain the library runs");
+        }
+    }
+    int32_t issued = 0;
+    for (const cbx_glaunch& l : ls) {
+        rc = run(tensors, nodes, n_nodes, l, stream);
+        if (rc) {
+            const std::string inner = cbx_last_error();
+            return set_error(rc, "cbx_graph_compute: nodes " + std::to_string(l.first_node) + ".." +
+                                     std::to_string(l.first_node + l.n_nodes - 1) + ": " + inner);
+        }
+        if (l.kind != CBX_GL_VIEW) issued++;
+        if (n_launches) *n_launches = issued;
+    }
+    return CBX_OK;
+}
+
+}  // extern "C"

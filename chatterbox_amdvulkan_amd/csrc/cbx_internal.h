@@ -92,6 +92,13 @@ int launch_unary(int op, float param, const cbx_tensor* x, cbx_tensor* y, Device
                  hipStream_t s);
 int launch_swiglu(const cbx_tensor* g, const cbx_tensor* u, cbx_tensor* y, DeviceState* st,
                   hipStream_t s);
+int launch_bias_act(int op, const cbx_tensor* x, const cbx_tensor* bias, cbx_tensor* y, DeviceState* st,
+                    hipStream_t s);
+// LayerNorm with a residual-join prologue (r, optional a_bias; s stored
+// when non-null) or a per-row mask epilogue (mask non-null, r null).
+int launch_layer_norm_ext(const cbx_tensor* a, const cbx_tensor* a_bias, const cbx_tensor* r, const cbx_tensor* w,
+                          const cbx_tensor* b, const cbx_tensor* mask, float eps, int act, cbx_tensor* s,
+                          cbx_tensor* y, DeviceState* st, hipStream_t strm, const char* what);
 int launch_snake(const cbx_tensor* x, const cbx_tensor* a, const cbx_tensor* ai, cbx_tensor* y,
                  DeviceState* st, hipStream_t s);
 

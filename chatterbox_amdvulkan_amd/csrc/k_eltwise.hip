@@ -1,5 +1,5 @@
 // k_eltwise.hip -- element-wise activations: the ggml unary ops, leaky_relu,
-// swiglu (silu(g) * u) and the fused Snake chain.
+// swiglu (silu(g) * u), bias add + activation and the fused Snake chain.
 //
 // Contiguous tensors take the streaming path: one 4-element vector per lane
 // over a grid that covers the tensor once (no grid-stride loop), with
@@ -198,6 +198,62 @@ __global__ __launch_bounds__(kThreads) void k_snake_rows(View x, View y, const f
     }
 }
 
+// ---- bias add + activation -------------------------------------------------------
+// y = act(x + bias): the ggml_add of a bias vector rounded to f32, then the
+// activation node reading it (t3.cpp:535-537, cfm_decoder.cpp:237-239,
+// flow_encoder.cpp:401-402, s3enc.cpp:176-177).  INNER: the bias runs along
+// ne[0] (ne0 % 4 == 0), element c = element % ne0; otherwise one bias value
+// per row index i1 (the (1, C) bias of a time-major tensor,
+// s3enc.cpp:117-120), c = (element / ne0) % ne1.
+
+template <int OP>
+__device__ __forceinline__ float4 act4(float4 t, const uint16_t* __restrict__ tab) {
+    if constexpr (OP == CBX_UNARY_NONE) {
+        return t;
+    } else if constexpr (OP == CBX_UNARY_GELU) {
+        return act_gelu_fast4(tab, t);
+    } else {
+        return make_float4(unary_op<OP>(t.x, tab, 0.0f), unary_op<OP>(t.y, tab, 0.0f), unary_op<OP>(t.z, tab, 0.0f),
+                           unary_op<OP>(t.w, tab, 0.0f));
+    }
+}
+
+template <int OP, bool INNER>
+__global__ __launch_bounds__(kThreads) void k_bias_act(const float* __restrict__ x, float* __restrict__ y,
+                                                       const float* __restrict__ bias, uint32_t n4, uint32_t C,
+                                                       uint32_t cmask, uint32_t ne0_4, const uint16_t* __restrict__ tab) {
+    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n4) return;
+    float4 bv;
+    if constexpr (INNER) {
+        const uint32_t c = cmask ? (4u * i) & cmask : (4u * i) % C;
+        bv = *reinterpret_cast<const float4*>(bias + c);
+    } else {
+        const uint32_t row = i / ne0_4;
+        const float bb = bias[cmask ? row & cmask : row % C];
+        bv = make_float4(bb, bb, bb, bb);
+    }
+    const float4 v = Stream<float>::load4(reinterpret_cast<const char*>(x + 4ull * i));
+    const float4 t = make_float4(v.x + bv.x, v.y + bv.y, v.z + bv.z, v.w + bv.w);
+    Stream<float>::store4(reinterpret_cast<char*>(y + 4ull * i), act4<OP>(t, tab));
+}
+
+template <int OP>
+__global__ __launch_bounds__(kThreads) void k_bias_act_rows(View x, View y, const float* __restrict__ bias, int64_t nr,
+                                                            bool inner, bool fx, bool fy,
+                                                            const uint16_t* __restrict__ tab) {
+    for (int64_t r = blockIdx.x; r < nr; r += gridDim.x) {
+        const float* xr = reinterpret_cast<const float*>(x.data + row_offset(x, r, fx));
+        float* yr = reinterpret_cast<float*>(y.data + row_offset(y, r, fy));
+        const float br = inner ? 0.0f : bias[r % x.ne[1]];
+        for (int64_t j = threadIdx.x; j < x.ne[0]; j += kThreads) {
+            const float t = xr[j] + (inner ? bias[j] : br);
+            if constexpr (OP == CBX_UNARY_NONE) yr[j] = t;
+            else yr[j] = unary_op<OP>(t, tab, 0.0f);
+        }
+    }
+}
+
 // ---- launch helpers -------------------------------------------------------------
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
@@ -234,7 +290,54 @@ void unary_dispatch(int op, const cbx_tensor* x, cbx_tensor* y, float param, Dev
     }
 }
 
+template <int OP>
+void bias_act_go(const cbx_tensor* x, const cbx_tensor* bias, bool inner, cbx_tensor* y, DeviceState* st,
+                 hipStream_t s) {
+    const int64_t n = nelements(x);
+    const int64_t C = inner ? x->ne[0] : x->ne[1];
+    const bool flat = is_contiguous(x) && is_contiguous(y) && aligned(x->data, 16) && aligned(y->data, 16) &&
+                      aligned(bias->data, 16) && x->ne[0] % 4 == 0 && n / 4 < (int64_t{1} << 32);
+    if (flat) {
+        const uint32_t n4 = static_cast<uint32_t>(n / 4);
+        const uint32_t cmask = (C & (C - 1)) == 0 ? static_cast<uint32_t>(C - 1) : 0u;
+        const uint32_t ne0_4 = static_cast<uint32_t>(x->ne[0] / 4);
+        const dim3 grid(static_cast<unsigned>(cdiv(n4, kThreads)));
+        const float* xp = static_cast<const float*>(x->data);
+        float* yp = static_cast<float*>(y->data);
+        const float* bp = static_cast<const float*>(bias->data);
+        if (inner) {
+            hipLaunchKernelGGL((k_bias_act<OP, true>), grid, dim3(kThreads), 0, s, xp, yp, bp, n4,
+                               static_cast<uint32_t>(C), cmask, ne0_4, st->gelu_table);
+        } else {
+            hipLaunchKernelGGL((k_bias_act<OP, false>), grid, dim3(kThreads), 0, s, xp, yp, bp, n4,
+                               static_cast<uint32_t>(C), cmask, ne0_4, st->gelu_table);
+        }
+    } else {
+        const int64_t nr = nrows(x);
+        hipLaunchKernelGGL((k_bias_act_rows<OP>), dim3(static_cast<unsigned>(std::min<int64_t>(nr, int64_t{1} << 20))),
+                           dim3(kThreads), 0, s, view_of(x), view_of(y), static_cast<const float*>(bias->data), nr,
+                           inner, flat_rows(x), flat_rows(y), st->gelu_table);
+    }
+}
+
 }  // namespace
+
+int launch_bias_act(int op, const cbx_tensor* x, const cbx_tensor* bias, cbx_tensor* y, DeviceState* st,
+                    hipStream_t s) {
+    const bool inner = bias->ne[0] == x->ne[0] && bias->ne[1] == 1;
+    switch (op) {
+        case CBX_UNARY_NONE: bias_act_go<CBX_UNARY_NONE>(x, bias, inner, y, st, s); break;
+        case CBX_UNARY_GELU: bias_act_go<CBX_UNARY_GELU>(x, bias, inner, y, st, s); break;
+        case CBX_UNARY_GELU_ERF: bias_act_go<CBX_UNARY_GELU_ERF>(x, bias, inner, y, st, s); break;
+        case CBX_UNARY_SILU: bias_act_go<CBX_UNARY_SILU>(x, bias, inner, y, st, s); break;
+        case CBX_UNARY_TANH: bias_act_go<CBX_UNARY_TANH>(x, bias, inner, y, st, s); break;
+        case CBX_UNARY_SOFTPLUS: bias_act_go<CBX_UNARY_SOFTPLUS>(x, bias, inner, y, st, s); break;
+        case CBX_UNARY_SIN: bias_act_go<CBX_UNARY_SIN>(x, bias, inner, y, st, s); break;
+        case CBX_UNARY_SQR: bias_act_go<CBX_UNARY_SQR>(x, bias, inner, y, st, s); break;
+        default: bias_act_go<CBX_UNARY_MISH>(x, bias, inner, y, st, s); break;
+    }
+    return check_launch("bias_act");
+}
 
 int launch_unary(int op, float param, const cbx_tensor* x, cbx_tensor* y, DeviceState* st, hipStream_t s) {
     const size_t a = x->type == CBX_TYPE_F32 ? 16 : 8;

@@ -1,0 +1,191 @@
+// k_norm_ext.hip -- LayerNorm with the element-wise nodes that the
+// reference's graph builders put right before or after it, in one pass:
+//
+//   residual join + LayerNorm (t3.cpp:528-532, 539-546; s3enc.cpp:273-276;
+//   flow_encoder.cpp:395-399):
+//       s = (a + a_bias) + r      (two ggml_add nodes; a_bias optional)
+//       y = act(LN(s) * w + b)    (s stored: it is the residual stream)
+//   causal_block1d's tail (cfm_decoder.cpp:143-148):
+//       y = act(LN(x) * w + b) * mask[row]      (mask (1, T): one per frame)
+//
+// One wave per row, as the plain LayerNorm kernel: each lane holds NV
+// 4-element vectors of the row in registers, the two reductions are
+// wave-local f64 butterflies, every f32 operation rounds once in the order
+// of the ggml nodes it replaces.  HBM traffic per row: the residual join
+// reads two rows and writes two (s, y) where the ggml nodes read and write
+// nine; the masked form reads one and writes one.
+#include "cbx_rowops.h"
+
+namespace cbx {
+namespace {
+
+enum { PRO_NONE = 0, PRO_RESID = 1, PRO_BIAS_RESID = 2 };
+
+struct LnExtArgs {
+    const char* a;
+    const char* r;
+    const float* ab;     // a_bias (PRO_BIAS_RESID)
+    const float* w;
+    const float* b;
+    const float* mask;   // one scale per ne1 index (MASK)
+    const uint16_t* tab;
+    char* s;             // the sum, or nullptr
+    char* y;
+    RowMap ma, mr, ms, my;
+    int32_t ne0, nr;
+    float eps;
+    int32_t act;
+};
+
+template <int NV, bool ACT, int PRO, bool MASK, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_ln_ext(LnExtArgs p) {
+    const int lane = threadIdx.x & 63;
+    uint32_t row = blockIdx.x;
+    if constexpr (WPB > 1) {
+        row = row * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        if (row >= static_cast<uint32_t>(p.nr)) return;   // uniform per wave
+    }
+    const int64_t ne0 = p.ne0;
+    const char* ar = p.a + row_at(p.ma, row);
+    char* yr = p.y + row_at(p.my, row);
+    Affine<NV> af;
+    af.load(p.w, p.b, lane, ne0);
+    float m = 1.0f;
+    if constexpr (MASK) m = p.mask[row % p.ma.ne1];
+    // every load is unconditional (clamped address) so all are in flight
+    // together; lanes past the row end zero their values afterwards
+    float4 v[NV], q[NV], c[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t j = (lane + 64 * k) * 4;
+        const int64_t jc = j < ne0 ? j : 0;
+        v[k] = *reinterpret_cast<const float4*>(ar + jc * 4);
+        if constexpr (PRO == PRO_BIAS_RESID) c[k] = *reinterpret_cast<const float4*>(p.ab + jc);
+    }
+    if constexpr (PRO != PRO_NONE) {
+        const char* rr = p.r + row_at(p.mr, row);
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int64_t j = (lane + 64 * k) * 4;
+            q[k] = *reinterpret_cast<const float4*>(rr + (j < ne0 ? j : 0) * 4);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        if ((lane + 64 * k) * 4 >= ne0) {
+            v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+            continue;
+        }
+        if constexpr (PRO == PRO_BIAS_RESID) {
+            v[k] = make_float4(v[k].x + c[k].x, v[k].y + c[k].y, v[k].z + c[k].z, v[k].w + c[k].w);
+        }
+        if constexpr (PRO != PRO_NONE) {
+            v[k] = make_float4(v[k].x + q[k].x, v[k].y + q[k].y, v[k].z + q[k].z, v[k].w + q[k].w);
+        }
+    }
+    if constexpr (PRO != PRO_NONE) {
+        if (p.s) {
+            char* sr = p.s + row_at(p.ms, row);
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                const int64_t j = (lane + 64 * k) * 4;
+                if (j < ne0) *reinterpret_cast<float4*>(sr + j * 4) = v[k];
+            }
+        }
+    }
+    const float scale = wave_row_scale<NV, NORM_LN>(v, lane, ne0, p.eps);
+    const bool hw = p.w != nullptr, hb = p.b != nullptr;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t j = (lane + 64 * k) * 4;
+        if (j < ne0) {
+            float4 o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float t = get(v[k], e) * scale;
+                if (hw) t = t * get(af.w[k], e);
+                if (hb) t = t + get(af.b[k], e);
+                if constexpr (ACT) t = apply_act(p.act, t, p.tab, 0.0f);
+                if constexpr (MASK) t = t * m;
+                set(o, e, t);
+            }
+            *reinterpret_cast<float4*>(yr + j * 4) = o;
+        }
+    }
+}
+
+template <bool ACT, int PRO, bool MASK, int WPB>
+void go_nv(const LnExtArgs& a, int nv, dim3 grid, hipStream_t s) {
+    const dim3 block(64 * WPB);
+    switch (nv) {
+        case 1: hipLaunchKernelGGL((k_ln_ext<1, ACT, PRO, MASK, WPB>), grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL((k_ln_ext<2, ACT, PRO, MASK, WPB>), grid, block, 0, s, a); break;
+        case 4: hipLaunchKernelGGL((k_ln_ext<4, ACT, PRO, MASK, WPB>), grid, block, 0, s, a); break;
+        case 8: hipLaunchKernelGGL((k_ln_ext<8, ACT, PRO, MASK, WPB>), grid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL((k_ln_ext<16, ACT, PRO, MASK, WPB>), grid, block, 0, s, a); break;
+    }
+}
+
+template <int PRO, bool MASK>
+void go_pro(const LnExtArgs& a, bool act, int nv, int wpb, int64_t nr, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(cdiv(nr, wpb)));
+    if (wpb == 1) {
+        if (act) go_nv<true, PRO, MASK, 1>(a, nv, grid, s);
+        else go_nv<false, PRO, MASK, 1>(a, nv, grid, s);
+    } else {
+        if (act) go_nv<true, PRO, MASK, 4>(a, nv, grid, s);
+        else go_nv<false, PRO, MASK, 4>(a, nv, grid, s);
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool rows16(const cbx_tensor* t) {
+    if (!aligned16(t->data)) return false;
+    for (int i = 1; i < 4; i++) if (t->nb[i] % 16) return false;
+    return true;
+}
+
+}  // namespace
+
+int launch_layer_norm_ext(const cbx_tensor* a, const cbx_tensor* a_bias, const cbx_tensor* r, const cbx_tensor* w,
+                          const cbx_tensor* b, const cbx_tensor* mask, float eps, int act, cbx_tensor* s,
+                          cbx_tensor* y, DeviceState* st, hipStream_t strm, const char* what) {
+    const int64_t ne0 = a->ne[0];
+    const int64_t nr = nrows(a);
+    bool ok = ne0 % 4 == 0 && ne0 <= 4096 && nr < (int64_t{1} << 31) && rows16(a) && rows16(y) &&
+              (!r || rows16(r)) && (!s || rows16(s));
+    for (const cbx_tensor* v : {a_bias, w, b}) ok = ok && (!v || aligned16(v->data));
+    if (!ok) {
+        return set_error(CBX_ERR_UNSUPPORTED, std::string(what) +
+                                                  ": needs ne0 % 4 == 0, ne0 <= 4096, fewer than 2^31 rows, and "
+                                                  "16-byte aligned rows and vectors");
+    }
+    LnExtArgs p;
+    p.a = static_cast<const char*>(a->data);
+    p.r = r ? static_cast<const char*>(r->data) : nullptr;
+    p.ab = a_bias ? static_cast<const float*>(a_bias->data) : nullptr;
+    p.w = w ? static_cast<const float*>(w->data) : nullptr;
+    p.b = b ? static_cast<const float*>(b->data) : nullptr;
+    p.mask = mask ? static_cast<const float*>(mask->data) : nullptr;
+    p.tab = st->gelu_table;
+    p.s = s ? static_cast<char*>(s->data) : nullptr;
+    p.y = static_cast<char*>(y->data);
+    p.ma = row_map(a);
+    p.mr = r ? row_map(r) : p.ma;
+    p.ms = s ? row_map(s) : p.ma;
+    p.my = row_map(y);
+    p.ne0 = static_cast<int32_t>(ne0);
+    p.nr = static_cast<int32_t>(nr);
+    p.eps = eps;
+    p.act = act;
+    const int nv = ne0 <= 256 ? 1 : ne0 <= 512 ? 2 : ne0 <= 1024 ? 4 : ne0 <= 2048 ? 8 : 16;
+    const int wpb = nr >= int64_t{8} * st->n_cu ? 4 : 1;
+    const bool has_act = act != CBX_UNARY_NONE;
+    if (mask) go_pro<PRO_NONE, true>(p, has_act, nv, wpb, nr, strm);
+    else if (a_bias) go_pro<PRO_BIAS_RESID, false>(p, has_act, nv, wpb, nr, strm);
+    else go_pro<PRO_RESID, false>(p, has_act, nv, wpb, nr, strm);
+    return check_launch(what);
+}
+
+}  // namespace cbx

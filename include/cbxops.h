@@ -146,6 +146,31 @@ int cbx_group_norm(const cbx_tensor* x, int n_groups, float eps,
                    const cbx_tensor* w, const cbx_tensor* b, int act,
                    cbx_tensor* y, cbx_stream stream);
 
+/* The residual join and the LayerNorm that reads it, in one pass:
+ *   s = ggml_add(ggml_add(a, a_bias), r)     (a_bias NULL: ggml_add(a, r))
+ *   y = act(layer_norm(s, w, b, eps))
+ * (t3.cpp:528-532: attn_residual = add(add(mul_mat, out_b), h), then the
+ * pre-FFN LayerNorm; t3.cpp:539-541 with the next block's :465-466 or the
+ * final LayerNorm :545-546; s3enc.cpp:273-276; flow_encoder.cpp:395-399).
+ * a, r, s, y: F32, one shape, ne0 % 4 == 0, ne0 <= 4096, 16-byte aligned
+ * rows; a_bias, w, b: F32 (x.ne0,1,1,1), 16-byte aligned, or NULL.  s (the
+ * residual stream) is stored when non-NULL; it may be a or r but must not
+ * overlap y.  act: CBX_UNARY_NONE or an activation.                        */
+int cbx_add_layer_norm(const cbx_tensor* a, const cbx_tensor* a_bias,
+                       const cbx_tensor* r, const cbx_tensor* w,
+                       const cbx_tensor* b, float eps, int act, cbx_tensor* s,
+                       cbx_tensor* y, cbx_stream stream);
+
+/* causal_block1d's tail in one pass (cfm_decoder.cpp:143-148): LayerNorm,
+ * the activation (Mish there), then the frame mask:
+ *   y = ggml_mul(act(layer_norm(x, w, b, eps)), mask)
+ * mask: contiguous F32 with ne = (1, x.ne1, 1, 1), the reference's (1, T).
+ * Layouts as cbx_add_layer_norm; y may be x.                               */
+int cbx_layer_norm_mask(const cbx_tensor* x, const cbx_tensor* w,
+                        const cbx_tensor* b, float eps, int act,
+                        const cbx_tensor* mask, cbx_tensor* y,
+                        cbx_stream stream);
+
 /* ---- rotary embedding --------------------------------------------------- */
 
 /* A device-resident cos/sin table for ggml_rope_ext's parameters, for
@@ -210,6 +235,16 @@ int cbx_mish(const cbx_tensor* x, cbx_tensor* y, cbx_stream stream);
  * flow_encoder.cpp:454). */
 int cbx_leaky_relu(const cbx_tensor* x, float slope, cbx_tensor* y,
                    cbx_stream stream);
+
+/* A bias add and the activation reading it: y = act(ggml_add(x, bias))
+ * (t3.cpp:535-537 fc bias -> ggml_gelu; cfm_decoder.cpp:237-239 and
+ * s3enc.cpp:176-177,279-280 -> ggml_gelu_erf; flow_encoder.cpp:401-402 and
+ * cfm_decoder.cpp:464-466 -> ggml_silu).  x, y: F32 same shape; bias:
+ * contiguous F32 with ne = (x.ne0,1,1,1), or (1,x.ne1,1,1) for the (1, C)
+ * bias of a time-major tensor (s3enc.cpp:117-120).  act CBX_UNARY_NONE
+ * leaves the bias add alone.                                               */
+int cbx_bias_act(int act, const cbx_tensor* x, const cbx_tensor* bias,
+                 cbx_tensor* y, cbx_stream stream);
 
 /* ggml_swiglu_split(g, u) = silu(g) * u, F32 or F16. */
 int cbx_swiglu(const cbx_tensor* g, const cbx_tensor* u, cbx_tensor* y,
@@ -314,6 +349,108 @@ typedef struct cbx_op {
  *     F32 destination rows 16-byte aligned;
  *   - SNAKE: F32, contiguous, 16-byte aligned, ne0 % 4 == 0.              */
 int cbx_run_ops(const cbx_op* ops, int n_ops, cbx_stream stream);
+
+/* ---- ggml-style node lists ------------------------------------------------ */
+
+/* The reference's graph builders emit the ops of this library as short node
+ * chains that its backend scheduler then runs one node at a time
+ * (ggml_backend_sched_graph_compute, chatterbox-cpp/src/backend.cpp:108-122;
+ * the chains: layer_norm cfm_decoder.cpp:29-33, mish cfm_decoder.cpp:36-38,
+ * snake hift_vocoder.cpp:64-73, T3 input t3.cpp:446-466, attention scores
+ * t3.cpp:513-518).  A backend's graph_compute can pass its nodes here in
+ * graph order: the planner takes, at each node, the longest known chain
+ * whose intermediate results no other node reads and the caller does not
+ * keep, and runs it as one fused call; everything else runs as the
+ * single-node entry points, or is reported as not supported.
+ *
+ * Tensors are given once, in an array; nodes refer to them by index.  A
+ * node reads src[] (-1 = none) and writes dst, ggml's broadcast rules
+ * apply to ADD/MUL operands, and a VIEW node only re-describes its
+ * source's memory (ggml's VIEW, RESHAPE, PERMUTE, TRANSPOSE: no launch).  */
+typedef enum cbx_gop {
+    CBX_GOP_VIEW          = 0,  /* dst describes src0's memory                       */
+    CBX_GOP_GET_ROWS      = 1,  /* src0 table, src1 ids I32                           */
+    CBX_GOP_ADD           = 2,  /* src0 + src1 (a bias add, or inside a chain)        */
+    CBX_GOP_MUL           = 3,  /* src0 * src1 (only inside a chain)                  */
+    CBX_GOP_SCALE         = 4,  /* src0 * fparam (only before SOFT_MAX)               */
+    CBX_GOP_NORM          = 5,  /* fparam = eps                                       */
+    CBX_GOP_RMS_NORM      = 6,  /* fparam = eps                                       */
+    CBX_GOP_GROUP_NORM    = 7,  /* iparam = n_groups, fparam = eps                    */
+    CBX_GOP_ROPE          = 8,  /* src0 x, src1 pos I32; rope = the parameters' cache */
+    CBX_GOP_SOFT_MAX      = 9,  /* fparam = scale (ggml_soft_max: 1.0); no mask src  */
+    CBX_GOP_DIAG_MASK_INF = 10, /* iparam = n_past (only before SOFT_MAX)             */
+    CBX_GOP_UNARY         = 11, /* iparam = cbx_unary_op (GELU .. SQR)                */
+    CBX_GOP_LEAKY_RELU    = 12, /* fparam = negative slope                            */
+    CBX_GOP_CPY           = 13, /* ggml_cpy / ggml_cast to dst's type (F32, F16)      */
+} cbx_gop;
+
+typedef struct cbx_gnode {
+    int32_t               op;      /* cbx_gop                                  */
+    int32_t               dst;     /* tensor index                             */
+    int32_t               src[2];  /* tensor indices, -1 = none                */
+    int32_t               iparam;
+    float                 fparam;
+    const cbx_rope_cache* rope;    /* CBX_GOP_ROPE                             */
+} cbx_gnode;
+
+/* What one planned launch runs: nodes [first_node, first_node + n_nodes). */
+typedef enum cbx_glaunch_kind {
+    CBX_GL_UNSUPPORTED = 0,   /* one node the library does not run              */
+    CBX_GL_VIEW,              /* one VIEW node: nothing to launch               */
+    CBX_GL_GET_ROWS,          /* get_rows [-> cast]                             */
+    CBX_GL_GET_ROWS_ADD,      /* get_rows [-> cast] -> get_rows [-> cast] -> add */
+    CBX_GL_GET_ROWS_ADD_LAYER_NORM, /* ... -> add -> norm -> mul -> add         */
+    CBX_GL_NORM,              /* norm                                           */
+    CBX_GL_LAYER_NORM,        /* norm -> mul -> add [-> softplus -> tanh -> mul] */
+    CBX_GL_LAYER_NORM_ROPE,   /* norm -> mul -> add -> view -> rope             */
+    CBX_GL_RMS_NORM,          /* rms_norm [-> mul]                              */
+    CBX_GL_GROUP_NORM,        /* group_norm [-> mul -> add] [-> mish chain]     */
+    CBX_GL_SOFT_MAX,          /* [scale ->] [diag_mask_inf ->] soft_max         */
+    CBX_GL_SNAKE,             /* mul -> sin -> sqr -> mul -> add                */
+    CBX_GL_UNARY,             /* one unary op, or softplus -> tanh -> mul (mish) */
+    CBX_GL_SWIGLU,            /* silu -> mul                                    */
+    CBX_GL_LEAKY_RELU,
+    CBX_GL_ROPE,
+    CBX_GL_CPY,
+    CBX_GL_ADD_LAYER_NORM,    /* [add(x, bias) ->] add(., r) -> norm -> mul -> add [-> mish chain] */
+    CBX_GL_LAYER_NORM_MASK,   /* norm -> mul -> add [-> mish chain] -> mul(., mask (1, ne1)) */
+    CBX_GL_BIAS_ACT,          /* add(x, bias) [-> unary op | -> mish chain]     */
+} cbx_glaunch_kind;
+
+typedef struct cbx_glaunch {
+    int32_t kind;         /* cbx_glaunch_kind                                   */
+    int32_t first_node;
+    int32_t n_nodes;
+    int32_t flags;        /* bit 0: an intermediate the fused kernel may skip
+                             storing (the embedding sum h nobody reads)         */
+} cbx_glaunch;
+
+/* Splits nodes[0..n_nodes) into launches, in order, covering every node
+ * (CBX_GL_UNSUPPORTED for a node that starts no chain the library runs).
+ * keep[0..n_keep): tensor indices read after the node list (graph outputs,
+ * inputs of another backend's nodes): never left unstored.  Chains are
+ * matched on op structure, operand roles and broadcast shapes; the entry
+ * point a launch maps to checks the rest of the layout when it runs.
+ * Host only.  *n_launches gets the count even when max_launches is short. */
+int cbx_graph_plan(const cbx_tensor* tensors, int32_t n_tensors,
+                   const cbx_gnode* nodes, int32_t n_nodes,
+                   const int32_t* keep, int32_t n_keep,
+                   cbx_glaunch* launches, int32_t max_launches,
+                   int32_t* n_launches);
+
+/* Runs one planned launch on `stream` (CBX_GL_UNSUPPORTED: returns
+ * CBX_ERR_UNSUPPORTED and launches nothing).                               */
+int cbx_graph_launch(const cbx_tensor* tensors, int32_t n_tensors,
+                     const cbx_gnode* nodes, int32_t n_nodes,
+                     const cbx_glaunch* launch, cbx_stream stream);
+
+/* Plans and runs the whole node list on `stream`.  If any node is
+ * unsupported, returns CBX_ERR_UNSUPPORTED naming it and launches nothing.
+ * *n_launches (may be NULL) gets the number of kernel launches issued.    */
+int cbx_graph_compute(const cbx_tensor* tensors, int32_t n_tensors,
+                      const cbx_gnode* nodes, int32_t n_nodes,
+                      const int32_t* keep, int32_t n_keep,
+                      cbx_stream stream, int32_t* n_launches);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,257 @@
+"""cbx_graph_compute on the reference's ggml node chains, checked against
+the oracle evaluating the same nodes one at a time (ggml-cpu's order of
+operations): T3 input embedding + first LayerNorm (t3.cpp:446-466),
+causal_block1d's LayerNorm -> Mish (cfm_decoder.cpp:143-146), snake
+(hift_vocoder.cpp:64-73), attention scores (t3.cpp:513-518), LayerNorm ->
+view -> RoPE, GroupNorm + affine + Mish, and a list of single ops.  Also
+checks how many kernel launches each list took."""
+import numpy as np
+import pytest
+import torch
+
+from chatterbox_amdvulkan_amd import workloads as W
+from tests._util import assert_bitexact, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def empty(*shape, dtype=torch.float32):
+    return torch.full(shape, float("nan"), dtype=dtype, device="cuda")
+
+
+@pytest.mark.parametrize("keep_h", [True, False])
+def test_t3_input_embedding(cbx, oracle, keep_h):
+    n, D = 150, 1024
+    tok_q = W.quantize_q8_0(W.normal(W.seed_of(7, 0), (704, D), 0.0, 0.02))
+    pos_t = W.normal(W.seed_of(7, 1), (600, D), 0.0, 0.02)
+    ids = W.randint(W.seed_of(7, 2), (n,), 0, 704)
+    pids = np.arange(3, 3 + n, dtype=np.int32)
+    w = W.normal(W.seed_of(7, 3), (D,), 1.0, 0.02)
+    b = W.normal(W.seed_of(7, 4), (D,), 0.0, 0.02)
+
+    g = cbx.Graph()
+    tok = g.tensor(dev(tok_q), cbx.Q8_0)
+    pos = g.tensor(dev(pos_t))
+    ti, tp = g.tensor(dev(ids)), g.tensor(dev(pids))
+    tw, tb = g.tensor(dev(w)), g.tensor(dev(b))
+    buf = [empty(n, D) for _ in range(8)]
+    t = [g.tensor(x) for x in buf]
+    g.node(cbx.GOP_GET_ROWS, t[0], (tok, ti))
+    g.node(cbx.GOP_CPY, t[1], (t[0],))
+    g.node(cbx.GOP_GET_ROWS, t[2], (pos, tp))
+    g.node(cbx.GOP_CPY, t[3], (t[2],))
+    g.node(cbx.GOP_ADD, t[4], (t[1], t[3]))
+    g.node(cbx.GOP_NORM, t[5], (t[4],), fparam=1e-5)
+    g.node(cbx.GOP_MUL, t[6], (t[5], tw))
+    g.node(cbx.GOP_ADD, t[7], (t[6], tb))
+    keep = [t[4]] if keep_h else []
+    assert g.compute(keep) == 1
+
+    h = oracle.add(oracle.cpy(oracle.get_rows(tok_q, ids, q8_0=True), np.float32),
+                   oracle.cpy(oracle.get_rows(pos_t, pids), np.float32))
+    y = oracle.add(oracle.mul(oracle.norm(h, 1e-5), w), b)
+    assert_bitexact(host(buf[7]), y, "LN(tok + pos)")
+    if keep_h:
+        assert_bitexact(host(buf[4]), h, "h kept")
+    else:
+        assert np.isnan(host(buf[4])).all(), "h was not asked for and stays unwritten"
+
+
+def test_causal_block_layer_norm_mish(cbx, oracle):
+    T, Ch = 300, 256
+    x = W.normal(W.seed_of(8, 0), (T, Ch), 0.1, 1.5)
+    w = W.normal(W.seed_of(8, 1), (Ch,), 1.0, 0.05)
+    b = W.normal(W.seed_of(8, 2), (Ch,), 0.0, 0.05)
+    g = cbx.Graph()
+    tx, tw, tb = g.tensor(dev(x)), g.tensor(dev(w)), g.tensor(dev(b))
+    buf = [empty(T, Ch) for _ in range(6)]
+    t = [g.tensor(v) for v in buf]
+    g.node(cbx.GOP_NORM, t[0], (tx,), fparam=1e-5)
+    g.node(cbx.GOP_MUL, t[1], (t[0], tw))
+    g.node(cbx.GOP_ADD, t[2], (t[1], tb))
+    g.node(cbx.GOP_UNARY, t[3], (t[2],), iparam=cbx.SOFTPLUS)
+    g.node(cbx.GOP_UNARY, t[4], (t[3],), iparam=cbx.TANH)
+    g.node(cbx.GOP_MUL, t[5], (t[2], t[4]))
+    assert g.compute() == 1
+    ln = oracle.add(oracle.mul(oracle.norm(x, 1e-5), w), b)
+    exp = oracle.mul(ln, oracle.unary(oracle.TANH, oracle.unary(oracle.SOFTPLUS, ln)))
+    assert_close(host(buf[5]), exp, x=ln, what="layer_norm -> mish nodes")
+
+
+def test_snake_nodes(cbx, oracle):
+    T, Ch = 2000, 128
+    x = W.normal(W.seed_of(9, 0), (T, Ch), 0.0, 2.0)
+    alpha = np.abs(W.normal(W.seed_of(9, 1), (Ch,), 1.0, 0.3)).astype(np.float32)
+    alpha_inv = (1.0 / (alpha + np.float32(1e-9))).astype(np.float32)
+    g = cbx.Graph()
+    tx, ta, tai = g.tensor(dev(x)), g.tensor(dev(alpha)), g.tensor(dev(alpha_inv))
+    buf = [empty(T, Ch) for _ in range(5)]
+    t = [g.tensor(v) for v in buf]
+    g.node(cbx.GOP_MUL, t[0], (tx, ta))
+    g.node(cbx.GOP_UNARY, t[1], (t[0],), iparam=cbx.SIN)
+    g.node(cbx.GOP_UNARY, t[2], (t[1],), iparam=cbx.SQR)
+    g.node(cbx.GOP_MUL, t[3], (t[2], tai))
+    g.node(cbx.GOP_ADD, t[4], (tx, t[3]))
+    assert g.compute() == 1
+    xa = oracle.mul(x, alpha)
+    exp = oracle.add(x, oracle.mul(oracle.unary(oracle.SQR, oracle.unary(oracle.SIN, xa)), alpha_inv))
+    assert_close(host(buf[4]), exp, x=x, what="snake nodes")
+
+
+@pytest.mark.parametrize("n_past", [-1, 0, 37])
+def test_attention_score_nodes(cbx, oracle, n_past):
+    H, nq = 8, 40
+    nk = n_past + nq if n_past >= 0 else 40
+    kq = W.normal(W.seed_of(10, n_past + 2), (H, nq, nk), 0.0, 3.0)
+    s = np.float32(1.0 / np.sqrt(64.0))
+    g = cbx.Graph()
+    tkq = g.tensor(dev(kq))
+    buf = [empty(H, nq, nk) for _ in range(3)]
+    t = [g.tensor(v) for v in buf]
+    g.node(cbx.GOP_SCALE, t[0], (tkq,), fparam=float(s))
+    src = t[0]
+    if n_past >= 0:
+        g.node(cbx.GOP_DIAG_MASK_INF, t[1], (t[0],), iparam=n_past)
+        src = t[1]
+    g.node(cbx.GOP_SOFT_MAX, t[2], (src,), fparam=1.0)
+    assert g.compute() == 1
+    z = oracle.scale(kq, float(s))
+    if n_past >= 0:
+        z = oracle.diag_mask_inf(z, n_past)
+    assert_close(host(buf[2]), oracle.soft_max(z), what=f"scores n_past={n_past}")
+
+
+def test_layer_norm_view_rope(cbx, oracle):
+    B, T, H, hd = 2, 100, 8, 64
+    x = W.normal(W.seed_of(11, 0), (B, T, H * hd), 0.2, 1.0)
+    w = W.normal(W.seed_of(11, 1), (H * hd,), 1.0, 0.02)
+    b = W.normal(W.seed_of(11, 2), (H * hd,), 0.0, 0.02)
+    pos = np.arange(T, dtype=np.int32)
+    cache = cbx.RopeCache(hd, mode=2, n_ctx_orig=2048, n_pos=2048)
+    g = cbx.Graph()
+    tx, tw, tb, tp = g.tensor(dev(x)), g.tensor(dev(w)), g.tensor(dev(b)), g.tensor(dev(pos))
+    n_, m_, y_ = (g.tensor(empty(B, T, H * hd)) for _ in range(3))
+    y_buf = g._torch[y_]
+    v_ = g.tensor(y_buf.view(B, T, H, hd))
+    out = empty(B, T, H, hd)
+    r_ = g.tensor(out)
+    g.node(cbx.GOP_NORM, n_, (tx,), fparam=1e-5)
+    g.node(cbx.GOP_MUL, m_, (n_, tw))
+    g.node(cbx.GOP_ADD, y_, (m_, tb))
+    g.node(cbx.GOP_VIEW, v_, (y_,))
+    g.node(cbx.GOP_ROPE, r_, (v_, tp), rope=cache)
+    assert g.compute() == 1
+    ln = oracle.add(oracle.mul(oracle.norm(x, 1e-5), w), b)
+    exp = oracle.rope_ext(ln.reshape(B, T, H, hd), pos, hd, mode=2)
+    assert_bitexact(host(out), exp, "layer_norm -> view -> rope")
+    cache.close()
+
+
+def test_group_norm_affine_mish_nodes(cbx, oracle):
+    inp = W.cfm_inputs()
+    x, w, b = inp["x256"], inp["w256"], inp["b256"]
+    g = cbx.Graph()
+    tx, tw, tb = g.tensor(dev(x)), g.tensor(dev(w)), g.tensor(dev(b))
+    buf = [empty(*x.shape) for _ in range(6)]
+    t = [g.tensor(v) for v in buf]
+    g.node(cbx.GOP_GROUP_NORM, t[0], (tx,), iparam=8, fparam=1e-5)
+    g.node(cbx.GOP_MUL, t[1], (t[0], tw))
+    g.node(cbx.GOP_ADD, t[2], (t[1], tb))
+    g.node(cbx.GOP_UNARY, t[3], (t[2],), iparam=cbx.SOFTPLUS)
+    g.node(cbx.GOP_UNARY, t[4], (t[3],), iparam=cbx.TANH)
+    g.node(cbx.GOP_MUL, t[5], (t[2], t[4]))
+    assert g.compute() == 1
+    gn = oracle.add(oracle.mul(oracle.group_norm(x, 8, 1e-5, nth=8), w), b)
+    exp = oracle.mul(gn, oracle.unary(oracle.TANH, oracle.unary(oracle.SOFTPLUS, gn)))
+    assert_close(host(buf[5]), exp, x=gn, what="group_norm -> mul -> add -> mish nodes")
+
+
+def test_single_ops_and_views(cbx, oracle):
+    R, Cc = 64, 1024
+    a = W.normal(W.seed_of(12, 0), (R, Cc), 0.0, 3.0)
+    u = W.normal(W.seed_of(12, 1), (R, Cc), 0.0, 1.0)
+    gain = W.normal(W.seed_of(12, 2), (Cc,), 1.0, 0.1)
+    g = cbx.Graph()
+    ta, tu, tg = g.tensor(dev(a)), g.tensor(dev(u)), g.tensor(dev(gain))
+    bufs = {k: empty(R, Cc) for k in ("s", "sw", "ge", "lr", "rn", "rm")}
+    h16 = empty(R, Cc, dtype=torch.float16)
+    t = {k: g.tensor(v) for k, v in bufs.items()}
+    t16 = g.tensor(h16)
+    sw_view = g.tensor(bufs["sw"].view(R * 4, Cc // 4))
+    g.node(cbx.GOP_UNARY, t["s"], (ta,), iparam=cbx.SILU)
+    g.node(cbx.GOP_MUL, t["sw"], (t["s"], tu))
+    g.node(cbx.GOP_VIEW, sw_view, (t["sw"],))
+    g.node(cbx.GOP_UNARY, t["ge"], (t["sw"],), iparam=cbx.GELU)
+    g.node(cbx.GOP_LEAKY_RELU, t["lr"], (t["ge"],), fparam=0.1)
+    g.node(cbx.GOP_RMS_NORM, t["rn"], (t["lr"],), fparam=1e-6)
+    g.node(cbx.GOP_MUL, t["rm"], (t["rn"], tg))
+    g.node(cbx.GOP_CPY, t16, (t["rm"],))
+    assert g.compute() == 5            # swiglu, gelu, leaky_relu, rms_norm*g, cast
+    sw = oracle.mul(oracle.unary(oracle.SILU, a), u)
+    got_sw = host(bufs["sw"])
+    assert_close(got_sw, sw, x=a, what="silu -> mul")
+    # the remaining nodes are exact ops: feed them the device's own swiglu result
+    ge = oracle.unary(oracle.GELU, got_sw)
+    assert_bitexact(host(bufs["ge"]), ge, "gelu")
+    lr = oracle.leaky_relu(ge, 0.1)
+    assert_bitexact(host(bufs["lr"]), lr, "leaky_relu")
+    rm = oracle.mul(oracle.rms_norm(lr, 1e-6), gain)
+    assert_bitexact(host(bufs["rm"]), rm, "rms_norm -> mul")
+    assert_bitexact(host(h16), oracle.cpy(rm, np.float16), "cast f16")
+    assert np.isnan(host(bufs["rn"])).all(), "rms_norm's own output is fused away"
+
+
+def test_plan_then_launch_one_by_one(cbx, oracle):
+    """cbx_graph_plan + cbx_graph_launch, as a scheduler that interleaves
+    its own kernels would use them: same results as compute."""
+    import ctypes
+
+    T, Ch = 64, 256
+    x = W.normal(W.seed_of(13, 0), (T, Ch))
+    w = W.normal(W.seed_of(13, 1), (Ch,), 1.0, 0.05)
+    b = W.normal(W.seed_of(13, 2), (Ch,), 0.0, 0.05)
+    g = cbx.Graph()
+    tx, tw, tb = g.tensor(dev(x)), g.tensor(dev(w)), g.tensor(dev(b))
+    buf = [empty(T, Ch) for _ in range(4)]
+    t = [g.tensor(v) for v in buf]
+    g.node(cbx.GOP_NORM, t[0], (tx,), fparam=1e-5)
+    g.node(cbx.GOP_MUL, t[1], (t[0], tw))
+    g.node(cbx.GOP_ADD, t[2], (t[1], tb))
+    g.node(cbx.GOP_UNARY, t[3], (t[2],), iparam=cbx.GELU)
+    plan = g.plan()
+    assert [p[0] for p in plan] == [cbx.GL_LAYER_NORM, cbx.GL_UNARY]
+    T_, N_, _ = g._arrays([])
+    L = cbx.load()
+    for kind, first, n, flags in plan:
+        rc = L.cbx_graph_launch(T_, len(g._descs), N_, len(g.nodes), ctypes.byref(cbx.GLaunch(kind, first, n, flags)),
+                                cbx._stream())
+        assert rc == cbx.OK, cbx.last_error()
+    ln = oracle.add(oracle.mul(oracle.norm(x, 1e-5), w), b)
+    assert_bitexact(host(buf[2]), ln, "planned layer_norm")
+    assert_bitexact(host(buf[3]), oracle.unary(oracle.GELU, ln), "planned gelu")
+
+
+def test_layout_error_names_the_nodes(cbx):
+    """A chain that matches on structure but not on layout (a strided gain)
+    fails in the entry point; the message names the node range."""
+    g = cbx.Graph()
+    x = g.tensor(empty(4, 2048))
+    w_full = empty(2048 * 2)
+    w = g.tensor(w_full[::2])                      # (2048,) with an 8-byte stride
+    b = g.tensor(empty(2048))
+    t = [g.tensor(empty(4, 2048)) for _ in range(3)]
+    g.node(cbx.GOP_NORM, t[0], (x,), fparam=1e-5)
+    g.node(cbx.GOP_MUL, t[1], (t[0], w))
+    g.node(cbx.GOP_ADD, t[2], (t[1], b))
+    with pytest.raises(cbx.CbxError) as e:
+        g.compute()
+    assert "nodes 0..2" in str(e.value)

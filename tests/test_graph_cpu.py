@@ -1,0 +1,378 @@
+"""The node-list planner (cbx_graph_plan) on the host: which of the
+reference's ggml op chains become one fused launch, when an intermediate
+that someone else reads blocks the fusion, and how bad lists are refused.
+Planning reads only shapes, types and addresses, so host tensors stand in
+for device memory; nothing here launches a kernel."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from chatterbox_amdvulkan_amd import cbxops as C
+
+
+def f32(*shape):
+    return torch.zeros(shape, dtype=torch.float32)
+
+
+def t3_input(g: C.Graph, n_tok=6, D=64, residual_read=True):
+    """t3.cpp:446-466: get_rows -> cast -> get_rows -> cast -> add -> norm -> mul -> add
+    (+ the residual add that reads h again when residual_read)."""
+    tok = g.tensor(f32(50, D))
+    ids = g.tensor(torch.zeros(n_tok, dtype=torch.int32))
+    pos = g.tensor(f32(40, D))
+    pids = g.tensor(torch.zeros(n_tok, dtype=torch.int32))
+    w, b = g.tensor(f32(D)), g.tensor(f32(D))
+    t = [g.tensor(f32(n_tok, D)) for _ in range(9)]
+    g.node(C.GOP_GET_ROWS, t[0], (tok, ids))
+    g.node(C.GOP_CPY, t[1], (t[0],))
+    g.node(C.GOP_GET_ROWS, t[2], (pos, pids))
+    g.node(C.GOP_CPY, t[3], (t[2],))
+    g.node(C.GOP_ADD, t[4], (t[1], t[3]))          # h
+    g.node(C.GOP_NORM, t[5], (t[4],), fparam=1e-5)
+    g.node(C.GOP_MUL, t[6], (t[5], w))
+    g.node(C.GOP_ADD, t[7], (t[6], b))
+    if residual_read:
+        g.node(C.GOP_ADD, t[8], (t[7], t[4]))     # stands for attn_residual = add(cur, h)
+    return t
+
+
+def test_t3_input_chain_is_one_launch():
+    g = C.Graph()
+    t3_input(g)
+    plan = g.plan()
+    assert plan[0] == (C.GL_GET_ROWS_ADD_LAYER_NORM, 0, 8, 0)   # h is read again: stored
+    assert plan[1] == (C.GL_UNSUPPORTED, 8, 1, 0)               # a plain residual add is not this library's
+
+
+def test_t3_input_unread_sum_is_not_stored():
+    g = C.Graph()
+    t3_input(g, residual_read=False)
+    assert g.plan() == [(C.GL_GET_ROWS_ADD_LAYER_NORM, 0, 8, 1)]
+
+
+def test_kept_intermediate_blocks_fusion():
+    g = C.Graph()
+    t = t3_input(g, residual_read=False)
+    # the caller needs the position rows themselves: the gathers split
+    plan = g.plan(keep=[t[3]])
+    assert plan[0] == (C.GL_GET_ROWS, 0, 2, 0)
+    assert plan[1] == (C.GL_GET_ROWS, 2, 2, 0)
+    # the sum and its LayerNorm still fuse, as a residual join
+    assert plan[2] == (C.GL_ADD_LAYER_NORM, 4, 4, 1)
+
+
+def causal_block_tail(g: C.Graph, C_=32, T=20, extra_reader=False):
+    """cfm_decoder.cpp:143-148: layer_norm -> mish -> mul(mask)."""
+    x = g.tensor(f32(T, C_))
+    w, b = g.tensor(f32(C_)), g.tensor(f32(C_))
+    mask = g.tensor(f32(T, 1))
+    t = [g.tensor(f32(T, C_)) for _ in range(7)]
+    g.node(C.GOP_NORM, t[0], (x,), fparam=1e-5)
+    g.node(C.GOP_MUL, t[1], (t[0], w))
+    g.node(C.GOP_ADD, t[2], (t[1], b))
+    g.node(C.GOP_UNARY, t[3], (t[2],), iparam=C.SOFTPLUS)
+    g.node(C.GOP_UNARY, t[4], (t[3],), iparam=C.TANH)
+    g.node(C.GOP_MUL, t[5], (t[2], t[4]))
+    g.node(C.GOP_MUL, t[6], (t[5], mask))
+    if extra_reader:
+        g.node(C.GOP_UNARY, g.tensor(f32(T, C_)), (t[2],), iparam=C.GELU)
+    return t
+
+
+def test_layer_norm_mish_mask():
+    g = C.Graph()
+    causal_block_tail(g)
+    assert g.plan() == [(C.GL_LAYER_NORM_MASK, 0, 7, 0)]
+    # a mask that is not one value per frame is a plain multiply: not this library's
+    g2 = C.Graph()
+    t = causal_block_tail(g2)
+    g2._descs[3] = C.desc(f32(20, 32))
+    assert g2.plan() == [(C.GL_LAYER_NORM, 0, 6, 0), (C.GL_UNSUPPORTED, 6, 1, 0)]
+
+
+def t3_block_tail(g: C.Graph, N=5, D=64, F=256):
+    """t3.cpp:526-541 around the matmuls (stood in by op 99, which the
+    library does not run): bias add -> residual add -> layer_norm, bias add
+    -> gelu, bias add -> residual add."""
+    MM = 99
+    attn_mm, h = g.tensor(f32(N, D)), g.tensor(f32(N, D))
+    out_b, ln_w, ln_b = g.tensor(f32(D)), g.tensor(f32(D)), g.tensor(f32(D))
+    fc_b, proj_b = g.tensor(f32(F)), g.tensor(f32(D))
+    wd = [g.tensor(f32(N, D)) for _ in range(5)]
+    wf = [g.tensor(f32(N, F)) for _ in range(3)]
+    wp = [g.tensor(f32(N, D)) for _ in range(3)]
+    g.node(C.GOP_ADD, wd[0], (attn_mm, out_b))      # cur = add(mm, out_b)
+    g.node(C.GOP_ADD, wd[1], (wd[0], h))            # attn_residual = add(cur, h)
+    g.node(C.GOP_NORM, wd[2], (wd[1],), fparam=1e-5)
+    g.node(C.GOP_MUL, wd[3], (wd[2], ln_w))
+    g.node(C.GOP_ADD, wd[4], (wd[3], ln_b))
+    g.node(MM, wf[0], (wd[4],))                     # fc mul_mat
+    g.node(C.GOP_ADD, wf[1], (wf[0], fc_b))
+    g.node(C.GOP_UNARY, wf[2], (wf[1],), iparam=C.GELU)
+    g.node(MM, wp[0], (wf[2],))                     # proj mul_mat
+    g.node(C.GOP_ADD, wp[1], (wp[0], proj_b))
+    g.node(C.GOP_ADD, wp[2], (wp[1], wd[1]))        # h = add(cur, attn_residual)
+    return wd, wf, wp
+
+
+def test_t3_block_tail():
+    g = C.Graph()
+    t3_block_tail(g)
+    assert g.plan() == [(C.GL_ADD_LAYER_NORM, 0, 5, 0),   # attn_residual is read again: stored
+                        (C.GL_UNSUPPORTED, 5, 1, 0),
+                        (C.GL_BIAS_ACT, 6, 2, 0),
+                        (C.GL_UNSUPPORTED, 8, 1, 0),
+                        (C.GL_BIAS_ACT, 9, 1, 0),         # proj bias add alone
+                        (C.GL_UNSUPPORTED, 10, 1, 0)]     # a residual add with no norm after it
+
+
+def test_residual_join_without_bias_and_unread_sum():
+    g = C.Graph()
+    a, r, w, b = g.tensor(f32(3, 32)), g.tensor(f32(3, 32)), g.tensor(f32(32)), g.tensor(f32(32))
+    s = g.node(C.GOP_ADD, g.tensor(f32(3, 32)), (a, r))
+    n = g.node(C.GOP_NORM, g.tensor(f32(3, 32)), (s,), fparam=1e-5)
+    m = g.node(C.GOP_MUL, g.tensor(f32(3, 32)), (n, w))
+    g.node(C.GOP_ADD, g.tensor(f32(3, 32)), (m, b))
+    assert g.plan() == [(C.GL_ADD_LAYER_NORM, 0, 4, 1)]
+    assert g.plan(keep=[s]) == [(C.GL_ADD_LAYER_NORM, 0, 4, 0)]
+
+
+def test_bias_add_forms():
+    """(C,) bias along ne0, (1, C) bias per row (s3enc.cpp:117-120), a mish
+    chain after the bias, and a one-row tensor whose bias has its shape."""
+    g = C.Graph()
+    x = g.tensor(f32(6, 40))
+    inner, outer = g.tensor(f32(40)), g.tensor(f32(6, 1))
+    y1 = g.node(C.GOP_ADD, g.tensor(f32(6, 40)), (x, outer))
+    g.node(C.GOP_UNARY, g.tensor(f32(6, 40)), (y1,), iparam=C.GELU_ERF)
+    y2 = g.node(C.GOP_ADD, g.tensor(f32(6, 40)), (x, inner))
+    sp = g.node(C.GOP_UNARY, g.tensor(f32(6, 40)), (y2,), iparam=C.SOFTPLUS)
+    th = g.node(C.GOP_UNARY, g.tensor(f32(6, 40)), (sp,), iparam=C.TANH)
+    g.node(C.GOP_MUL, g.tensor(f32(6, 40)), (y2, th))
+    v, vb = g.tensor(f32(40)), g.tensor(f32(40))
+    y3 = g.node(C.GOP_ADD, g.tensor(f32(40)), (v, vb))
+    g.node(C.GOP_UNARY, g.tensor(f32(40)), (y3,), iparam=C.SILU)
+    full = g.tensor(f32(6, 40))
+    g.node(C.GOP_ADD, g.tensor(f32(6, 40)), (x, full))
+    assert g.plan() == [(C.GL_BIAS_ACT, 0, 2, 0), (C.GL_BIAS_ACT, 2, 4, 0), (C.GL_BIAS_ACT, 6, 2, 0),
+                        (C.GL_UNSUPPORTED, 8, 1, 0)]
+
+
+def test_layer_norm_output_read_elsewhere_keeps_mish_separate():
+    g = C.Graph()
+    causal_block_tail(g, extra_reader=True)
+    assert g.plan() == [(C.GL_LAYER_NORM, 0, 3, 0), (C.GL_UNARY, 3, 3, 0), (C.GL_UNSUPPORTED, 6, 1, 0),
+                        (C.GL_UNARY, 7, 1, 0)]
+
+
+def test_shape_mismatch_is_not_a_layer_norm():
+    g = C.Graph()
+    x = g.tensor(f32(4, 32))
+    w = g.tensor(f32(4, 32))          # full-shape gain: not ggml's (ne0) broadcast of layer_norm
+    b = g.tensor(f32(32))
+    n, m, y = (g.tensor(f32(4, 32)) for _ in range(3))
+    g.node(C.GOP_NORM, n, (x,), fparam=1e-5)
+    g.node(C.GOP_MUL, m, (n, w))
+    g.node(C.GOP_ADD, y, (m, b))
+    # the norm alone, the full-shape multiply not this library's, the bias add alone
+    assert [p[0] for p in g.plan()] == [C.GL_NORM, C.GL_UNSUPPORTED, C.GL_BIAS_ACT]
+
+
+def test_snake_chain():
+    """hift_vocoder.cpp:64-73."""
+    g = C.Graph()
+    x = g.tensor(f32(30, 16))
+    a, ai = g.tensor(f32(16)), g.tensor(f32(16))
+    t = [g.tensor(f32(30, 16)) for _ in range(5)]
+    g.node(C.GOP_MUL, t[0], (x, a))
+    g.node(C.GOP_UNARY, t[1], (t[0],), iparam=C.SIN)
+    g.node(C.GOP_UNARY, t[2], (t[1],), iparam=C.SQR)
+    g.node(C.GOP_MUL, t[3], (t[2], ai))
+    g.node(C.GOP_ADD, t[4], (x, t[3]))
+    assert g.plan() == [(C.GL_SNAKE, 0, 5, 0)]
+    # the same nodes with the sin result kept: five separate nodes, two of them not runnable alone
+    assert [p[0] for p in g.plan(keep=[t[1]])] == [C.GL_UNSUPPORTED, C.GL_UNARY, C.GL_UNARY, C.GL_UNSUPPORTED,
+                                                    C.GL_UNSUPPORTED]
+
+
+@pytest.mark.parametrize("with_mask", [True, False])
+def test_attention_scores(with_mask):
+    """t3.cpp:513-518 (scale -> diag_mask_inf -> soft_max) and the unmasked
+    form of cfm_decoder.cpp:218-220."""
+    g = C.Graph()
+    kq = g.tensor(f32(4, 7, 9))
+    t = [g.tensor(f32(4, 7, 9)) for _ in range(3)]
+    g.node(C.GOP_SCALE, t[0], (kq,), fparam=0.125)
+    src = t[0]
+    if with_mask:
+        g.node(C.GOP_DIAG_MASK_INF, t[1], (t[0],), iparam=2)
+        src = t[1]
+    g.node(C.GOP_SOFT_MAX, t[2], (src,), fparam=1.0)
+    assert g.plan() == [(C.GL_SOFT_MAX, 0, 3 if with_mask else 2, 0)]
+
+
+def test_soft_max_with_own_scale_does_not_absorb_scale():
+    g = C.Graph()
+    kq = g.tensor(f32(4, 8))
+    s, y = g.tensor(f32(4, 8)), g.tensor(f32(4, 8))
+    g.node(C.GOP_SCALE, s, (kq,), fparam=0.5)
+    g.node(C.GOP_SOFT_MAX, y, (s,), fparam=2.0)
+    assert g.plan() == [(C.GL_UNSUPPORTED, 0, 1, 0), (C.GL_SOFT_MAX, 1, 1, 0)]
+
+
+def test_soft_max_with_mask_operand_is_unsupported():
+    g = C.Graph()
+    kq, m, y = g.tensor(f32(4, 8)), g.tensor(f32(4, 8)), g.tensor(f32(4, 8))
+    g.node(C.GOP_SOFT_MAX, y, (kq, m), fparam=1.0)
+    assert g.plan() == [(C.GL_UNSUPPORTED, 0, 1, 0)]
+
+
+def test_layer_norm_view_rope():
+    g = C.Graph()
+    n_tok, H, hd = 10, 4, 16
+    x = g.tensor(f32(n_tok, H * hd))
+    w, b = g.tensor(f32(H * hd)), g.tensor(f32(H * hd))
+    pos = g.tensor(torch.zeros(n_tok, dtype=torch.int32))
+    n, m = g.tensor(f32(n_tok, H * hd)), g.tensor(f32(n_tok, H * hd))
+    y_t = f32(n_tok, H * hd)
+    y = g.tensor(y_t)
+    v = g.tensor(y_t.view(n_tok, H, hd))
+    r = g.tensor(f32(n_tok, H, hd))
+    g.node(C.GOP_NORM, n, (x,), fparam=1e-5)
+    g.node(C.GOP_MUL, m, (n, w))
+    g.node(C.GOP_ADD, y, (m, b))
+    g.node(C.GOP_VIEW, v, (y,))
+    g.node(C.GOP_ROPE, r, (v, pos))
+    assert g.plan() == [(C.GL_LAYER_NORM_ROPE, 0, 5, 0)]
+    # a view of other memory is a different tensor: no fusion
+    g.tensor(f32(n_tok, H, hd))
+    g.nodes[3].dst = len(g._descs) - 1
+    g.nodes[4].src[0] = len(g._descs) - 1
+    assert [p[0] for p in g.plan()] == [C.GL_LAYER_NORM, C.GL_VIEW, C.GL_ROPE]
+
+
+@pytest.mark.parametrize("affine,mish,want", [(True, True, 6), (True, False, 3), (False, True, 4), (False, False, 1)])
+def test_group_norm_chains(affine, mish, want):
+    g = C.Graph()
+    Ch = 8
+    x = g.tensor(f32(2, Ch, 5, 3))            # ggml ne = (3, 5, C, 2): channels on ne2
+    w, b = g.tensor(f32(1, Ch, 1, 1)), g.tensor(f32(1, Ch, 1, 1))
+    y = g.node(C.GOP_GROUP_NORM, g.tensor(f32(2, Ch, 5, 3)), (x,), iparam=4, fparam=1e-5)
+    if affine:
+        y = g.node(C.GOP_MUL, g.tensor(f32(2, Ch, 5, 3)), (y, w))
+        y = g.node(C.GOP_ADD, g.tensor(f32(2, Ch, 5, 3)), (y, b))
+    if mish:
+        sp = g.node(C.GOP_UNARY, g.tensor(f32(2, Ch, 5, 3)), (y,), iparam=C.SOFTPLUS)
+        th = g.node(C.GOP_UNARY, g.tensor(f32(2, Ch, 5, 3)), (sp,), iparam=C.TANH)
+        g.node(C.GOP_MUL, g.tensor(f32(2, Ch, 5, 3)), (y, th))
+    assert g.plan() == [(C.GL_GROUP_NORM, 0, want, 0)]
+
+
+def test_silu_gate_and_singles():
+    g = C.Graph()
+    a, u = g.tensor(f32(3, 40)), g.tensor(f32(3, 40))
+    s = g.node(C.GOP_UNARY, g.tensor(f32(3, 40)), (a,), iparam=C.SILU)
+    y = g.node(C.GOP_MUL, g.tensor(f32(3, 40)), (s, u))
+    g.node(C.GOP_UNARY, g.tensor(f32(3, 40)), (y,), iparam=C.GELU)
+    g.node(C.GOP_LEAKY_RELU, g.tensor(f32(3, 40)), (y,), fparam=0.1)
+    g.node(C.GOP_RMS_NORM, g.tensor(f32(3, 40)), (y,), fparam=1e-6)
+    g.node(C.GOP_CPY, g.tensor(torch.zeros(3, 40, dtype=torch.float16)), (y,))
+    g.node(C.GOP_UNARY, g.tensor(f32(3, 40)), (y,), iparam=42)   # no such activation
+    assert [p[:3] for p in g.plan()] == [(C.GL_SWIGLU, 0, 2), (C.GL_UNARY, 2, 1), (C.GL_LEAKY_RELU, 3, 1),
+                                         (C.GL_RMS_NORM, 4, 1), (C.GL_CPY, 5, 1), (C.GL_UNSUPPORTED, 6, 1)]
+
+
+def _raw(g: C.Graph, keep=()):
+    T, N, K = g._arrays(list(keep))
+    return T, N, K
+
+
+def test_bad_lists_are_refused():
+    L = C.load()
+    g = C.Graph()
+    x, y = g.tensor(f32(2, 8)), g.tensor(f32(2, 8))
+    g.node(C.GOP_NORM, y, (x,), fparam=1e-5)
+    T, N, K = _raw(g)
+    out = (C.GLaunch * 4)()
+    n = ctypes.c_int32(-1)
+    assert L.cbx_graph_plan(T, 2, N, 1, K, 0, out, 4, ctypes.byref(n)) == C.OK and n.value == 1
+    # too little room: the count is still reported
+    assert L.cbx_graph_plan(T, 2, N, 1, K, 0, out, 0, ctypes.byref(n)) == C.ERR_INVALID_ARG and n.value == 1
+    # a node naming a tensor past the array
+    g.nodes[0].src[0] = 7
+    T, N, K = _raw(g)
+    assert L.cbx_graph_plan(T, 2, N, 1, K, 0, out, 4, ctypes.byref(n)) == C.ERR_INVALID_ARG
+    assert "out of range" in C.last_error()
+    g.nodes[0].src[0] = x
+    g.nodes[0].dst = -1
+    T, N, K = _raw(g)
+    assert L.cbx_graph_plan(T, 2, N, 1, K, 0, out, 4, ctypes.byref(n)) == C.ERR_INVALID_ARG
+    g.nodes[0].dst = y
+    # a keep index past the array
+    T, N, K = _raw(g, keep=[5])
+    assert L.cbx_graph_plan(T, 2, N, 1, K, 1, out, 4, ctypes.byref(n)) == C.ERR_INVALID_ARG
+    # empty list: no launches
+    assert L.cbx_graph_plan(None, 0, None, 0, None, 0, None, 0, ctypes.byref(n)) == C.OK and n.value == 0
+
+
+def test_compute_refuses_unsupported_before_any_launch():
+    """The whole list is planned first: an unsupported node anywhere stops
+    the call before the device is touched (this runs without a GPU)."""
+    L = C.load()
+    g = C.Graph()
+    t3_input(g)
+    T, N, K = _raw(g)
+    n = ctypes.c_int32(-1)
+    rc = L.cbx_graph_compute(T, len(g._descs), N, len(g.nodes), K, 0, None, ctypes.byref(n))
+    assert rc == C.ERR_UNSUPPORTED and n.value == 0
+    assert "node 8 (ADD)" in C.last_error()
+
+
+def test_hand_made_launches_stay_inside_the_list():
+    L = C.load()
+    g = C.Graph()
+    x, y = g.tensor(f32(2, 8)), g.tensor(f32(2, 8))
+    g.node(C.GOP_NORM, y, (x,), fparam=1e-5)
+    g.node(C.GOP_VIEW, x, (y,))
+    T, N, _ = _raw(g)
+    bad = [C.GLaunch(C.GL_SNAKE, 0, 5, 0),         # runs past the two nodes
+           C.GLaunch(C.GL_NORM, -1, 1, 0),
+           C.GLaunch(C.GL_LAYER_NORM, 0, 4, 0),     # not a length a layer_norm chain has
+           C.GLaunch(99, 0, 1, 0)]
+    for l in bad:
+        assert L.cbx_graph_launch(T, 2, N, 2, ctypes.byref(l), None) == C.ERR_INVALID_ARG, (l.kind, l.n_nodes)
+    assert L.cbx_graph_launch(T, 2, N, 2, ctypes.byref(C.GLaunch(C.GL_UNSUPPORTED, 0, 1, 0)), None) == \
+        C.ERR_UNSUPPORTED
+    assert L.cbx_graph_launch(T, 2, N, 2, ctypes.byref(C.GLaunch(C.GL_VIEW, 1, 1, 0)), None) == C.OK
+
+
+def test_random_lists_plan_into_an_exact_cover():
+    """Random node lists over random operands: the plan covers every node
+    exactly once, in order, each launch within its kind's span."""
+    rng = np.random.default_rng(5)
+    spans = {C.GL_UNSUPPORTED: {1}, C.GL_VIEW: {1}, C.GL_GET_ROWS: {1, 2}, C.GL_GET_ROWS_ADD: {3, 4, 5},
+             C.GL_GET_ROWS_ADD_LAYER_NORM: {6, 7, 8}, C.GL_NORM: {1}, C.GL_LAYER_NORM: {3, 6},
+             C.GL_LAYER_NORM_ROPE: {5}, C.GL_RMS_NORM: {1, 2}, C.GL_GROUP_NORM: {1, 3, 4, 6},
+             C.GL_SOFT_MAX: {1, 2, 3}, C.GL_SNAKE: {5}, C.GL_UNARY: {1, 3}, C.GL_SWIGLU: {2},
+             C.GL_LEAKY_RELU: {1}, C.GL_ROPE: {1}, C.GL_CPY: {1}, C.GL_ADD_LAYER_NORM: {4, 5, 7, 8},
+             C.GL_LAYER_NORM_MASK: {4, 7}, C.GL_BIAS_ACT: {1, 2, 4}}
+    shapes = [(4, 8), (8,), (1, 8, 1, 1), (4, 8), (4, 1)]
+    for trial in range(200):
+        g = C.Graph()
+        n_t = int(rng.integers(3, 12))
+        for k in range(n_t):
+            g.tensor(f32(*shapes[int(rng.integers(0, len(shapes)))]))
+        for k in range(int(rng.integers(1, 25))):
+            op = int(rng.integers(0, 14))
+            src = [int(rng.integers(-1, n_t)) for _ in range(2)]
+            g.node(op, int(rng.integers(0, n_t)), src, iparam=int(rng.integers(-1, 9)),
+                   fparam=float(rng.choice([1.0, 0.5, 1e-5])))
+        keep = [int(v) for v in rng.integers(0, n_t, size=int(rng.integers(0, 3)))]
+        plan = g.plan(keep)
+        at = 0
+        for kind, first, n, flags in plan:
+            assert first == at and n in spans[kind], (trial, kind, n)
+            at += n
+        assert at == len(g.nodes)
