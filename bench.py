@@ -466,6 +466,89 @@ def bench_softmax(C, W, torch, reps=200):
     return out
 
 
+def bench_t3_block(C, W, torch, reps=300):
+    """One T3 block's element-wise nodes at prefill size [512,1024] /
+    [512,4096] (t3.cpp:526-546; the matmul outputs given): the residual join
+    + pre-FFN LayerNorm, fc bias + GELU, and the projection's residual join +
+    the next block's LayerNorm -- three launches planned from the ggml node
+    list by cbx_graph_plan, then issued with cbx_graph_launch over rotating
+    buffer sets.  Also the host cost of cbx_graph_compute on that list."""
+    d = dev_of(torch)
+    L = C.load()
+    base = {k: d(v) for k, v in W.t3_block_inputs().items()}
+    nb = W.t3_block_bytes()
+    per_step = nb["residual_ln2"] + nb["fc_bias_gelu"] + nb["residual_next_ln1"]
+    n_sets = max(2, math.ceil(MALL_DEFEAT_BYTES / per_step))
+    N, D, F = W.N_PREFILL, W.D_MODEL, W.D_FF
+
+    def graph_of(t):
+        g = C.Graph()
+        T = {k: g.tensor(v) for k, v in t.items()}
+        g.node(C.GOP_ADD, T["cur"], (T["attn_mm"], T["out_b"]))
+        g.node(C.GOP_ADD, T["res"], (T["cur"], T["h"]))
+        g.node(C.GOP_NORM, T["n"], (T["res"],), fparam=1e-5)
+        g.node(C.GOP_MUL, T["m"], (T["n"], T["ln2_w"]))
+        g.node(C.GOP_ADD, T["ln2"], (T["m"], T["ln2_b"]))
+        g.node(C.GOP_ADD, T["fcb"], (T["fc_mm"], T["fc_b"]))
+        g.node(C.GOP_UNARY, T["gelu"], (T["fcb"],), iparam=C.GELU)
+        g.node(C.GOP_ADD, T["pcur"], (T["proj_mm"], T["proj_b"]))
+        g.node(C.GOP_ADD, T["h2"], (T["pcur"], T["res"]))
+        g.node(C.GOP_NORM, T["n2"], (T["h2"],), fparam=1e-5)
+        g.node(C.GOP_MUL, T["m2"], (T["n2"], T["ln1_w"]))
+        g.node(C.GOP_ADD, T["ln1"], (T["m2"], T["ln1_b"]))
+        keep = [T["ln2"], T["gelu"], T["h2"], T["ln1"]]
+        plan = g.plan(keep)
+        arrs = g._arrays(keep)
+        return g, plan, arrs, keep
+
+    sets = []
+    for _ in range(n_sets):
+        t = {k: v.clone() for k, v in base.items()}
+        for k in ("cur", "res", "n", "m", "ln2", "pcur", "h2", "n2", "m2", "ln1"):
+            t[k] = torch.empty((N, D), dtype=torch.float32, device="cuda")
+        for k in ("fcb", "gelu"):
+            t[k] = torch.empty((N, F), dtype=torch.float32, device="cuda")
+        g, plan, arrs, keep = graph_of(t)
+        launches = [C.GLaunch(*p) for p in plan]
+        sets.append((t, g, plan, arrs, launches, keep))
+    kinds = [p[0] for p in sets[0][2]]
+    if kinds != [C.GL_ADD_LAYER_NORM, C.GL_BIAS_ACT, C.GL_ADD_LAYER_NORM]:
+        raise SystemExit(f"bench: unexpected T3 block plan {kinds}")
+
+    def one(st, k):
+        _, g, _, (Tn, Nn, _), launches, _ = st
+        nt, nn = len(g._descs), len(g.nodes)
+        lr = C.ctypes.byref(launches[k])
+        return lambda s: check_rc(C, L.cbx_graph_launch(Tn, nt, Nn, nn, lr, s))
+
+    out = {}
+    for name, k in (("residual_ln2", 0), ("fc_bias_gelu", 1), ("residual_next_ln1", 2)):
+        fns = [one(st, k) for st in sets]
+        for f in fns:
+            f(cur_stream(torch))
+        us = per_launch_ms(torch, fns, reps) * 1000.0
+        out[name] = {"us": us, "bytes": nb[name], "GBps": nb[name] / (us * 1e-6) / 1e9}
+    block = [(lambda st: lambda s: [one(st, k)(s) for k in range(3)])(st) for st in sets]
+    us = per_launch_ms(torch, block, reps) * 1000.0
+    out["block"] = {"us": us, "launches": 3, "bytes": per_step, "GBps": per_step / (us * 1e-6) / 1e9,
+                    "ggml_node_bytes": nb["ggml_nodes"],
+                    "ggml_node_bytes_ratio": nb["ggml_nodes"] / per_step}
+    # host cost of planning + issuing the whole list (no GPU sync inside)
+    t0 = sets[0]
+    Tn, Nn, Kn = t0[3]
+    n = C.ctypes.c_int32(0)
+    s = cur_stream(torch)
+    torch.cuda.synchronize()
+    tm = time.perf_counter()
+    for _ in range(200):
+        check_rc(C, L.cbx_graph_compute(Tn, len(t0[1]._descs), Nn, len(t0[1].nodes), Kn, len(t0[5]), s,
+                                        C.ctypes.byref(n)))
+    host_us = (time.perf_counter() - tm) / 200 * 1e6
+    torch.cuda.synchronize()
+    out["graph_compute_host_us_per_call"] = host_us
+    return dict(out, buffer_sets=n_sets)
+
+
 def bench_hift(C, W, torch, quick=False):
     """HiFT vocoder activations: Snake (channel innermost as the reference
     lays it out, and time innermost) and LeakyReLU(0.1) on every upsample
@@ -536,7 +619,7 @@ def bench_copy_ceiling(C, torch, sizes, reps=400):
     return out
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_gelu_embedln_groupnorm_lnrope.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_fused_layer_ops.md")
 
 
 def recorded_traffic(key):
@@ -556,8 +639,9 @@ def traffic_probe(C, W, torch):
     """A few launches for counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE):
     a plain f32 copy of 64 MiB (the calibration kernel of known size), then
     GELU [512,4096], the fused embedding + LayerNorm, GroupNorm+Mish
-    [2,512,500] and LayerNorm+RoPE [2,500,512], each on 8 rotating buffer
-    sets.  Prints the algorithmic bytes of each."""
+    [2,512,500], LayerNorm+RoPE [2,500,512], the residual join + LayerNorm
+    [512,1024] and bias + GELU [512,4096], each on 8 rotating buffer sets.
+    Prints the algorithmic bytes of each."""
     x = torch.empty(16 << 20, dtype=torch.float32, device="cuda").uniform_()
     ys = [torch.empty_like(x) for _ in range(4)]
     L = C.load()
@@ -590,13 +674,31 @@ def traffic_probe(C, W, torch):
                                           r["ya"], s))
     torch.cuda.synchronize()
     cache.close()
+    blk = W.t3_block_inputs()
+    N, D, F = W.N_PREFILL, W.D_MODEL, W.D_FF
+    blk_sets = []
+    for _ in range(8):
+        t = {k: d(blk[k]) for k in ("attn_mm", "h", "out_b", "ln2_w", "ln2_b", "fc_mm", "fc_b")}
+        t["res"], t["ln2"] = torch.empty((N, D), device="cuda"), torch.empty((N, D), device="cuda")
+        t["gelu"] = torch.empty((N, F), device="cuda")
+        blk_sets.append({k: C.ctypes.byref(C.desc(v)) for k, v in t.items()})
+    for r in blk_sets:
+        check_rc(C, L.cbx_add_layer_norm(r["attn_mm"], r["out_b"], r["h"], r["ln2_w"], r["ln2_b"], 1e-5, -1,
+                                         r["res"], r["ln2"], s))
+    torch.cuda.synchronize()
+    for r in blk_sets:
+        check_rc(C, L.cbx_bias_act(C.GELU, r["fc_mm"], r["fc_b"], r["gelu"], s))
+    torch.cuda.synchronize()
     nb = W.prefill_bytes()
     cb = W.cfm_bytes()
+    bb = W.t3_block_bytes()
     print(json.dumps({"copy_bytes_read": x.numel() * 4, "copy_bytes_written": x.numel() * 4,
                       "gelu_bytes_read": nb["gelu"] // 2, "gelu_bytes_written": nb["gelu"] // 2,
                       "embed_layer_norm_bytes": nb["embed_layer_norm"],
                       "group_norm_mish_512_bytes": cb["group_norm_mish_512"],
-                      "layer_norm_rope_bytes": cb["layer_norm_rope"]}), flush=True)
+                      "layer_norm_rope_bytes": cb["layer_norm_rope"],
+                      "residual_join_layer_norm_bytes": bb["residual_ln2"],
+                      "bias_gelu_bytes": bb["fc_bias_gelu"]}), flush=True)
 
 
 def cpu_baseline(W, seconds):
@@ -731,6 +833,8 @@ def main():
         details["hift_activations"] = bench_hift(C, W, torch)
         log("softmax")
         details["attention_softmax"] = bench_softmax(C, W, torch)
+        log("t3 block")
+        details["t3_block_elementwise"] = bench_t3_block(C, W, torch)
     k_ms = res["kernel_ms"]["gelu"]
     k_bytes = res["kernel_bytes"]["gelu"]
     achieved = k_bytes / (k_ms * 1e-3) / 1e9

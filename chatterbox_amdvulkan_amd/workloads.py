@@ -220,3 +220,36 @@ HIFT_SHAPES = ((1, 256, 6000), (1, 128, 48000), (1, 64, 120000), (16, 64, 120000
 def snake_alpha(C: int, tensor: int = 1):
     a = uniform_range(seed_of(4, tensor), (C,), 0.5, 1.5)
     return a, (np.float32(1.0) / (a + np.float32(1e-9))).astype(np.float32)
+
+
+# ---- workload 5: one T3 block's element-wise nodes around its matmuls --------------
+
+def t3_block_inputs() -> dict:
+    """The matmul outputs and parameters of one T3 block at prefill size
+    (t3.cpp:526-546): attention output projection [512,1024] + out_b, the
+    residual h, LN2 w/b, fc output [512,4096] + fc_b, projection output
+    [512,1024] + proj_b, the next block's LN1 w/b."""
+    w = 7
+    N, D, F = N_PREFILL, D_MODEL, D_FF
+    return {
+        "attn_mm": normal(seed_of(w, 0), (N, D)), "h": normal(seed_of(w, 1), (N, D)),
+        "out_b": normal(seed_of(w, 2), (D,), 0.0, 0.02),
+        "ln2_w": normal(seed_of(w, 3), (D,), 1.0, 0.02), "ln2_b": normal(seed_of(w, 4), (D,), 0.0, 0.02),
+        "fc_mm": normal(seed_of(w, 5), (N, F)), "fc_b": normal(seed_of(w, 6), (F,), 0.0, 0.02),
+        "proj_mm": normal(seed_of(w, 7), (N, D)), "proj_b": normal(seed_of(w, 8), (D,), 0.0, 0.02),
+        "ln1_w": normal(seed_of(w, 9), (D,), 1.0, 0.02), "ln1_b": normal(seed_of(w, 10), (D,), 0.0, 0.02),
+    }
+
+
+def t3_block_bytes() -> dict:
+    """Algorithmic bytes of the three fused launches (each input read once,
+    each output written once), and what the ggml nodes they replace move
+    when each node reads its inputs and writes its output (vectors aside):
+    add-bias, add-residual, norm, mul, add = 11 [N,D] rows per residual
+    join; add-bias, gelu = 4 [N,F] rows."""
+    N, D, F = N_PREFILL, D_MODEL, D_FF
+    act = N * D * 4
+    join = 4 * act + 3 * D * 4                 # read a, r; write s, y; out_b/proj_b, w, b
+    bias_gelu = 2 * N * F * 4 + F * 4
+    return {"residual_ln2": join, "fc_bias_gelu": bias_gelu, "residual_next_ln1": join,
+            "ggml_nodes": 2 * 11 * act + 4 * N * F * 4}
