@@ -744,7 +744,8 @@ def _timed(fn, seconds):
 def cpu_other_workloads(W, O, nth, seconds):
     """The oracle on the other workloads' shapes (same inputs as the GPU
     legs), a bounded sample each: decode step chain (us per step), the
-    64-stream f16 step, a CFM flow step, two HiFT stages."""
+    64-stream f16 step, a CFM flow step, a T3 block's element-wise nodes,
+    two HiFT stages."""
     out = {}
     steps = [W.decode_inputs(t) for t in range(W.DECODE_STEPS)]
 
@@ -777,6 +778,18 @@ def cpu_other_workloads(W, O, nth, seconds):
         O.rope_ext(ln.reshape(2, W.CFM_T, W.CFM_HEADS, W.HEAD_DIM), cf["pos"], W.HEAD_DIM, mode=2, nth=nth)
     reps, el = _timed(flow, seconds)
     out["cfm_flow_step_GBps"] = sum(W.cfm_bytes().values()) * reps / el / 1e9
+
+    blk = W.t3_block_inputs()
+
+    def t3_block():
+        res = O.add(O.add(blk["attn_mm"], blk["out_b"], nth=nth), blk["h"], nth=nth)
+        O.layer_norm(res, blk["ln2_w"], blk["ln2_b"], 1e-5, nth=nth)
+        O.unary(O.GELU, O.add(blk["fc_mm"], blk["fc_b"], nth=nth), nth=nth)
+        h2 = O.add(O.add(blk["proj_mm"], blk["proj_b"], nth=nth), res, nth=nth)
+        O.layer_norm(h2, blk["ln1_w"], blk["ln1_b"], 1e-5, nth=nth)
+    reps, el = _timed(t3_block, seconds)
+    bb = W.t3_block_bytes()
+    out["t3_block_elementwise_GBps"] = (bb["residual_ln2"] + bb["fc_bias_gelu"] + bb["residual_next_ln1"]) * reps / el / 1e9
 
     for (B, Ch, T) in W.HIFT_SHAPES[:3:2]:
         x = W.normal(W.seed_of(4, 2), (B, T, Ch))
