@@ -264,6 +264,11 @@ static int check_gather(const char* what, const cbx_tensor* src, const cbx_tenso
     if (src->ne[2] != ids->ne[1] || src->ne[3] != ids->ne[2]) {
         return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": src.ne2/ne3 must equal ids.ne1/ne2");
     }
+    // every id would be out of range (ggml aborts); the kernels read row 0
+    // in place of a bad id, so a table without rows is refused here
+    if (src->ne[1] == 0 && nelements(dst) > 0) {
+        return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": src has no rows to gather from");
+    }
     return CBX_OK;
 }
 

@@ -99,6 +99,15 @@ __device__ __forceinline__ void set(float4& v, int k, float x) {
     if (k == 0) v.x = x; else if (k == 1) v.y = x; else if (k == 2) v.z = x; else v.w = x;
 }
 
+// ---- kernel arguments --------------------------------------------------------
+// The compiler loads a kernel argument where it is first used, and sinks
+// that load into a conditional block when only the block uses it (a store
+// guarded by a bounds test, say): the block then waits for a second round
+// of argument loads.  Naming the values here, at the top of the kernel,
+// makes them part of the first round.
+__device__ __forceinline__ void arg_now(const void* p) { asm volatile("" ::"s"(p)); }
+__device__ __forceinline__ void arg_now(uint32_t v) { asm volatile("" ::"s"(v)); }
+
 // ---- reductions ----------------------------------------------------------
 // DPP move of a double (two 32-bit halves) inside each 16-lane row.
 template <int CTRL>

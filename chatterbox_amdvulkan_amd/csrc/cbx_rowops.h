@@ -84,6 +84,23 @@ __device__ __forceinline__ float wave_row_scale(float4 (&v)[NV], int lane, int64
 template <int NV>
 struct Affine {
     float4 w[NV], b[NV];
+    // Branch-free form: a null wp/bp reads its vectors from `safe` (a
+    // 16-byte aligned address of at least ne0 floats) instead, and the
+    // caller ignores them.  A pointer select rather than a branch, so the
+    // compiler has no conditional block to sink argument loads into: every
+    // argument arrives in the kernel's first round of scalar loads.
+    __device__ __forceinline__ void load_sel(const float* wp, const float* bp, const float* safe, int lane,
+                                             int64_t ne0) {
+        const float* wq = wp ? wp : safe;
+        const float* bq = bp ? bp : safe;
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int64_t j = (lane + 64 * k) * 4;
+            const int64_t jc = j < ne0 ? j : 0;
+            w[k] = *reinterpret_cast<const float4*>(wq + jc);
+            b[k] = *reinterpret_cast<const float4*>(bq + jc);
+        }
+    }
     __device__ __forceinline__ void load(const float* __restrict__ wp, const float* __restrict__ bp, int lane,
                                          int64_t ne0) {
 #pragma unroll
@@ -138,18 +155,36 @@ __device__ __forceinline__ float4 load_table4(const char* row, int64_t j) {
     }
 }
 
+// An out-of-range id: ggml aborts; here the row's outputs are zeroed and
+// the sticky device error bit is raised.
+__device__ __forceinline__ void embed_bad_row(char* hr, char* yr, int64_t ne0, int lane, uint32_t* err) {
+    for (int64_t j = lane; j < ne0; j += 64) {
+        reinterpret_cast<float*>(yr)[j] = 0.0f;
+        if (hr) reinterpret_cast<float*>(hr)[j] = 0.0f;
+    }
+    if (lane == 0) atomicOr(err, static_cast<uint32_t>(DEV_ERR_ROW_INDEX));
+}
+
 // The T3 embedding row: h = f32(table row) + f32(position row), stored when
 // hr is non-null, then y = LN(h)*w + b.  Row loads are unconditional
-// (clamped addresses) so all 2*NV are in flight together.
+// (clamped addresses) so all 2*NV are in flight together.  `bad` (uniform):
+// an id was out of range -- the caller passed row 0 in its place, and the
+// row's outputs are zeroed instead, after the loads, so no branch precedes
+// them.
 template <int TYPE, int TYPE2, int NV>
 __device__ __forceinline__ void embed_ln_row(const char* s1, const char* s2, const Affine<NV>& af, bool hw, bool hb,
-                                             char* hr, char* yr, int64_t ne0, float eps, int lane) {
+                                             char* hr, char* yr, int64_t ne0, float eps, int lane, bool bad,
+                                             uint32_t* err) {
     float4 p[NV], q[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
         const int64_t j = (lane + 64 * k) * 4;
         p[k] = load_table4<TYPE>(s1, j < ne0 ? j : 0);
         q[k] = load_table4<TYPE2>(s2, j < ne0 ? j : 0);
+    }
+    if (bad) {
+        embed_bad_row(hr, yr, ne0, lane, err);
+        return;
     }
     float4 v[NV];
 #pragma unroll
@@ -164,16 +199,6 @@ __device__ __forceinline__ void embed_ln_row(const char* s1, const char* s2, con
     }
     const float scale = wave_row_scale<NV, NORM_LN>(v, lane, ne0, eps);
     wave_row_store<float, NV, false>(v, lane, ne0, scale, af, hw, hb, CBX_UNARY_NONE, nullptr, yr);
-}
-
-// An out-of-range id: ggml aborts; here the row's outputs are zeroed and
-// the sticky device error bit is raised.
-__device__ __forceinline__ void embed_bad_row(char* hr, char* yr, int64_t ne0, int lane, uint32_t* err) {
-    for (int64_t j = lane; j < ne0; j += 64) {
-        reinterpret_cast<float*>(yr)[j] = 0.0f;
-        if (hr) reinterpret_cast<float*>(hr)[j] = 0.0f;
-    }
-    if (lane == 0) atomicOr(err, static_cast<uint32_t>(DEV_ERR_ROW_INDEX));
 }
 
 // cos/sin of pair k for position p: theta = p * theta_scale^k as an iterated

@@ -263,12 +263,10 @@ __device__ __forceinline__ void b_embed_ln_t(const BOp& op, uint32_t lb, uint32_
     const float* b = reinterpret_cast<const float*>(op.t[5].p);
     Affine<NV> af;
     af.load(w, b, lane, ne0);
-    if (id < 0 || id >= op.aux || id2 < 0 || id2 >= op.aux2) {
-        embed_bad_row(hr, yr, ne0, lane, err);
-        return;
-    }
-    embed_ln_row<TYPE, TYPE2, NV>(op.t[0].p + id * op.t[0].nb1, op.t[2].p + id2 * op.t[2].nb1, af, w != nullptr,
-                                  b != nullptr, hr, yr, ne0, op.eps, lane);
+    const bool bad = id < 0 || id >= op.aux || id2 < 0 || id2 >= op.aux2;
+    const int64_t r1 = bad ? 0 : id, r2 = bad ? 0 : id2;
+    embed_ln_row<TYPE, TYPE2, NV>(op.t[0].p + r1 * op.t[0].nb1, op.t[2].p + r2 * op.t[2].nb1, af, w != nullptr,
+                                  b != nullptr, hr, yr, ne0, op.eps, lane, bad, err);
 }
 
 template <int TYPE>

@@ -147,8 +147,14 @@ template <bool INNER>
 __global__ __launch_bounds__(kThreads) void k_snake(const float* __restrict__ x, float* __restrict__ y,
                                                     const float* __restrict__ a, const float* __restrict__ ai,
                                                     uint32_t n4, uint32_t C, uint32_t cmask, uint32_t ne0_4) {
-    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n4) return;
+    // lanes past the end load the last vector and store nothing: no early
+    // exit stands before the loads (n4 >= 1)
+    arg_now(x);
+    arg_now(y);
+    arg_now(a);
+    arg_now(ai);
+    const uint32_t iu = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t i = iu < n4 ? iu : n4 - 1;
     uint32_t c;
     if constexpr (INNER) {
         c = cmask ? (4u * i) & cmask : (4u * i) % C;
@@ -172,7 +178,7 @@ __global__ __launch_bounds__(kThreads) void k_snake(const float* __restrict__ x,
         o.z = snake1(v.z, av, iv);
         o.w = snake1(v.w, av, iv);
     }
-    Stream<float>::store4(reinterpret_cast<char*>(y + 4ull * i), o);
+    if (iu < n4) Stream<float>::store4(reinterpret_cast<char*>(y + 4ull * i), o);
 }
 
 // General rows: alpha either per element of ne[0] (inner) or per row i1 (outer).
@@ -222,8 +228,12 @@ template <int OP, bool INNER>
 __global__ __launch_bounds__(kThreads) void k_bias_act(const float* __restrict__ x, float* __restrict__ y,
                                                        const float* __restrict__ bias, uint32_t n4, uint32_t C,
                                                        uint32_t cmask, uint32_t ne0_4, const uint16_t* __restrict__ tab) {
-    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n4) return;
+    // lanes past the end load the last vector and store nothing (n4 >= 1)
+    arg_now(x);
+    arg_now(y);
+    arg_now(bias);
+    const uint32_t iu = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t i = iu < n4 ? iu : n4 - 1;
     float4 bv;
     if constexpr (INNER) {
         const uint32_t c = cmask ? (4u * i) & cmask : (4u * i) % C;
@@ -235,7 +245,8 @@ __global__ __launch_bounds__(kThreads) void k_bias_act(const float* __restrict__
     }
     const float4 v = Stream<float>::load4(reinterpret_cast<const char*>(x + 4ull * i));
     const float4 t = make_float4(v.x + bv.x, v.y + bv.y, v.z + bv.z, v.w + bv.w);
-    Stream<float>::store4(reinterpret_cast<char*>(y + 4ull * i), act4<OP>(t, tab));
+    const float4 o = act4<OP>(t, tab);
+    if (iu < n4) Stream<float>::store4(reinterpret_cast<char*>(y + 4ull * i), o);
 }
 
 template <int OP>

@@ -142,13 +142,15 @@ __global__ __launch_bounds__(kThreads) void k_group_norm_vec(GnArgs a, uint32_t 
     const uint32_t m = j / n_chunks;
     const uint32_t ci = j - m * n_chunks;
     const uint32_t gi = b % kXcds + kXcds * m;
-    if (gi >= n_gi) return;   // uniform across the workgroup
     const int64_t C = a.x.ne[2];
-    const int64_t g = gi % a.n_groups;
-    const int64_t i3 = gi / a.n_groups;
-    const int64_t c0 = g * a.cpg;
+    int64_t g = gi % a.n_groups;
+    int64_t i3 = gi / a.n_groups;
+    int64_t c0 = g * a.cpg;
+    // a workgroup past the last group, or of an empty group (past C), reads
+    // group 0 and stores nothing: no early exit stands before the loads
+    const bool live = gi < n_gi && c0 < C;
+    if (!live) g = i3 = c0 = 0;
     const int64_t c1 = c0 + a.cpg < C ? c0 + a.cpg : C;
-    if (c0 >= c1) return;
     const int64_t count = a.x.ne[0] * a.x.ne[1] * (c1 - c0);
     const char* xg = a.x.data + c0 * a.x.nb[2] + i3 * a.x.nb[3];
     char* yg = a.y.data + c0 * a.y.nb[2] + i3 * a.y.nb[3];
@@ -187,6 +189,7 @@ __global__ __launch_bounds__(kThreads) void k_group_norm_vec(GnArgs a, uint32_t 
     s2 = block_sum(s2, red);
     const float var = static_cast<float>(s2 / static_cast<double>(count));
     const float scale = 1.0f / sqrtf(var + a.eps);
+    if (!live) return;   // uniform across the workgroup
 
     if (n_chunks == 1) {
 #pragma unroll

@@ -41,7 +41,9 @@ struct WaveNormArgs {
 // WPB waves (rows) per workgroup.  With WPB == 1 the grid has exactly one
 // workgroup per row, so there is no bounds check and no read of the block
 // size before the loads.
-template <typename T, int NV, int KIND, bool ACT, int WPB>
+// FLAT: x and y rows at one stride each, so a row's address is one multiply
+// and nothing tests an argument before the loads are issued.
+template <typename T, int NV, int KIND, bool ACT, int WPB, bool FLAT>
 __global__ __launch_bounds__(64 * WPB) void k_row_norm_wave(WaveNormArgs a) {
     const int lane = threadIdx.x & 63;
     uint32_t r = blockIdx.x;
@@ -50,13 +52,14 @@ __global__ __launch_bounds__(64 * WPB) void k_row_norm_wave(WaveNormArgs a) {
         if (r >= static_cast<uint32_t>(a.nr)) return;   // uniform per wave
     }
     const int64_t ne0 = a.ne0;
-    const char* xr = a.x + row_at(a.mx, r);
-    char* yr = a.y + row_at(a.my, r);
+    const char* xr = a.x + (FLAT ? static_cast<int64_t>(r) * a.mx.nb1 : row_at(a.mx, r));
+    char* yr = a.y + (FLAT ? static_cast<int64_t>(r) * a.my.nb1 : row_at(a.my, r));
     // affine vectors first (L2-resident), then the row: loads are
-    // unconditional (clamped address), so all are in flight at once; lanes
-    // past the row end zero their values afterwards
+    // unconditional (clamped address; a missing w or b reads the GELU table
+    // instead), so all are in flight at once; lanes past the row end zero
+    // their values afterwards
     Affine<NV> af;
-    af.load(a.w, a.b, lane, ne0);
+    af.load_sel(a.w, a.b, reinterpret_cast<const float*>(a.tab), lane, ne0);
     float4 v[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
@@ -107,14 +110,12 @@ __global__ __launch_bounds__(kMaxThreads) void k_embed_norm(EmbedArgs a) {
     char* yr = a.y.data + i10 * a.y.nb[1] + i11 * a.y.nb[2] + i12 * a.y.nb[3];
     char* hr = a.h.data ? a.h.data + i10 * a.h.nb[1] + i11 * a.h.nb[2] + i12 * a.h.nb[3] : nullptr;
     Affine<NV> af;
-    af.load(a.w, a.b, lane, ne0);
-    if (id < 0 || id >= a.src.ne[1] || id2 < 0 || id2 >= a.src2.ne[1]) {
-        embed_bad_row(hr, yr, ne0, lane, a.err);
-        return;
-    }
-    const char* s1 = a.src.data + id * a.src.nb[1] + i11 * a.src.nb[2] + i12 * a.src.nb[3];
-    const char* s2 = a.src2.data + id2 * a.src2.nb[1] + i11 * a.src2.nb[2] + i12 * a.src2.nb[3];
-    embed_ln_row<TYPE, TYPE2, NV>(s1, s2, af, a.w != nullptr, a.b != nullptr, hr, yr, ne0, a.eps, lane);
+    af.load_sel(a.w, a.b, reinterpret_cast<const float*>(yr), lane, ne0);
+    const bool bad = id < 0 || id >= a.src.ne[1] || id2 < 0 || id2 >= a.src2.ne[1];
+    const int64_t r1 = bad ? 0 : id, r2 = bad ? 0 : id2;
+    const char* s1 = a.src.data + r1 * a.src.nb[1] + i11 * a.src.nb[2] + i12 * a.src.nb[3];
+    const char* s2 = a.src2.data + r2 * a.src2.nb[1] + i11 * a.src2.nb[2] + i12 * a.src2.nb[3];
+    embed_ln_row<TYPE, TYPE2, NV>(s1, s2, af, a.w != nullptr, a.b != nullptr, hr, yr, ne0, a.eps, lane, bad, a.err);
 }
 
 // The common layout -- 1-D contiguous ids, 2-D tables, uniformly strided
@@ -147,16 +148,15 @@ __global__ __launch_bounds__(64) void k_embed_norm_flat(EmbedFlat a) {
     const int32_t id = __builtin_amdgcn_readfirstlane(a.ids[t]);
     const int32_t id2 = __builtin_amdgcn_readfirstlane(a.ids2[t]);
     const int64_t ne0 = a.ne0;
-    Affine<NV> af;
-    af.load(a.w, a.b, lane, ne0);
     char* yr = a.y + t * a.y_nb1;
     char* hr = a.h ? a.h + t * a.h_nb1 : nullptr;
-    if (id < 0 || id >= a.src_rows || id2 < 0 || id2 >= a.src2_rows) {
-        embed_bad_row(hr, yr, ne0, lane, a.err);
-        return;
-    }
-    embed_ln_row<TYPE, TYPE2, NV>(a.src + id * a.src_nb1, a.src2 + id2 * a.src2_nb1, af, a.w != nullptr,
-                                  a.b != nullptr, hr, yr, ne0, a.eps, lane);
+    Affine<NV> af;
+    af.load_sel(a.w, a.b, reinterpret_cast<const float*>(yr), lane, ne0);
+    // an out-of-range id reads row 0 and zeroes the outputs after the loads
+    const bool bad = id < 0 || id >= a.src_rows || id2 < 0 || id2 >= a.src2_rows;
+    const int64_t r1 = bad ? 0 : id, r2 = bad ? 0 : id2;
+    embed_ln_row<TYPE, TYPE2, NV>(a.src + r1 * a.src_nb1, a.src2 + r2 * a.src2_nb1, af, a.w != nullptr,
+                                  a.b != nullptr, hr, yr, ne0, a.eps, lane, bad, a.err);
 }
 
 // ---------------------------------------------------------------------------
@@ -314,7 +314,7 @@ struct NormLaunch {
     hipStream_t s;
 };
 
-template <typename T, int KIND, bool ACT, int WPB>
+template <typename T, int KIND, bool ACT, int WPB, bool FLAT>
 void go_wave_w(const NormLaunch& L, int nv) {
     WaveNormArgs a;
     a.x = L.x.data;
@@ -330,7 +330,7 @@ void go_wave_w(const NormLaunch& L, int nv) {
     a.act = L.act;
 #define CBX_WAVE_CASE(N)                                                                       \
     case N:                                                                                   \
-        hipLaunchKernelGGL((k_row_norm_wave<T, N, KIND, ACT, WPB>), L.grid, L.block, 0, L.s, a); \
+        hipLaunchKernelGGL((k_row_norm_wave<T, N, KIND, ACT, WPB, FLAT>), L.grid, L.block, 0, L.s, a); \
         break;
     switch (nv) {
         CBX_WAVE_CASE(1)
@@ -342,10 +342,12 @@ void go_wave_w(const NormLaunch& L, int nv) {
 #undef CBX_WAVE_CASE
 }
 
+// Strided-plane layouts (not FLAT) take one row per workgroup.
 template <typename T, int KIND, bool ACT>
 void go_wave(const NormLaunch& L, int nv) {
-    if (L.block.x == 64) go_wave_w<T, KIND, ACT, 1>(L, nv);
-    else go_wave_w<T, KIND, ACT, 4>(L, nv);
+    if (!(L.mx.flat && L.my.flat)) go_wave_w<T, KIND, ACT, 1, false>(L, nv);
+    else if (L.block.x == 64) go_wave_w<T, KIND, ACT, 1, true>(L, nv);
+    else go_wave_w<T, KIND, ACT, 4, true>(L, nv);
 }
 
 template <typename T, int KIND, bool ACT, bool VEC>
@@ -424,7 +426,7 @@ int launch_row_norm(int kind, const cbx_tensor* x, const cbx_tensor* w, const cb
     int nv;
     if (wave) {
         nv = pow2_nv(cdiv(ne0, 256));
-        const int wpb = waves_per_block(nr, st);
+        const int wpb = L.mx.flat && L.my.flat ? waves_per_block(nr, st) : 1;
         L.block = dim3(64 * wpb);
         L.grid = dim3(static_cast<unsigned>(cdiv(nr, wpb)));
         if (nr >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "norm: too many rows");

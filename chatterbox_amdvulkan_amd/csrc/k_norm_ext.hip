@@ -37,7 +37,15 @@ struct LnExtArgs {
     int32_t act;
 };
 
-template <int NV, bool ACT, int PRO, bool MASK, int WPB>
+// Byte offset of row r: FLAT rows sit at one stride (no index split and no
+// test of the map's flag, so nothing waits on an argument before the loads).
+template <bool FLAT>
+__device__ __forceinline__ int64_t row_off(const RowMap& m, uint32_t r) {
+    if constexpr (FLAT) return static_cast<int64_t>(r) * m.nb1;
+    else return row_at(m, r);
+}
+
+template <int NV, bool ACT, int PRO, bool MASK, int WPB, bool FLAT>
 __global__ __launch_bounds__(64 * WPB) void k_ln_ext(LnExtArgs p) {
     const int lane = threadIdx.x & 63;
     uint32_t row = blockIdx.x;
@@ -46,10 +54,11 @@ __global__ __launch_bounds__(64 * WPB) void k_ln_ext(LnExtArgs p) {
         if (row >= static_cast<uint32_t>(p.nr)) return;   // uniform per wave
     }
     const int64_t ne0 = p.ne0;
-    const char* ar = p.a + row_at(p.ma, row);
-    char* yr = p.y + row_at(p.my, row);
+    const char* ar = p.a + row_off<FLAT>(p.ma, row);
+    char* yr = p.y + row_off<FLAT>(p.my, row);
+    char* sr = p.s + row_off<FLAT>(p.ms, row);   // only stored through when p.s is set
     Affine<NV> af;
-    af.load(p.w, p.b, lane, ne0);
+    af.load_sel(p.w, p.b, reinterpret_cast<const float*>(p.tab), lane, ne0);
     float m = 1.0f;
     if constexpr (MASK) m = p.mask[row % p.ma.ne1];
     // every load is unconditional (clamped address) so all are in flight
@@ -63,7 +72,7 @@ __global__ __launch_bounds__(64 * WPB) void k_ln_ext(LnExtArgs p) {
         if constexpr (PRO == PRO_BIAS_RESID) c[k] = *reinterpret_cast<const float4*>(p.ab + jc);
     }
     if constexpr (PRO != PRO_NONE) {
-        const char* rr = p.r + row_at(p.mr, row);
+        const char* rr = p.r + row_off<FLAT>(p.mr, row);
 #pragma unroll
         for (int k = 0; k < NV; k++) {
             const int64_t j = (lane + 64 * k) * 4;
@@ -85,7 +94,6 @@ __global__ __launch_bounds__(64 * WPB) void k_ln_ext(LnExtArgs p) {
     }
     if constexpr (PRO != PRO_NONE) {
         if (p.s) {
-            char* sr = p.s + row_at(p.ms, row);
 #pragma unroll
             for (int k = 0; k < NV; k++) {
                 const int64_t j = (lane + 64 * k) * 4;
@@ -114,27 +122,35 @@ __global__ __launch_bounds__(64 * WPB) void k_ln_ext(LnExtArgs p) {
     }
 }
 
-template <bool ACT, int PRO, bool MASK, int WPB>
+template <bool ACT, int PRO, bool MASK, int WPB, bool FLAT>
 void go_nv(const LnExtArgs& a, int nv, dim3 grid, hipStream_t s) {
     const dim3 block(64 * WPB);
     switch (nv) {
-        case 1: hipLaunchKernelGGL((k_ln_ext<1, ACT, PRO, MASK, WPB>), grid, block, 0, s, a); break;
-        case 2: hipLaunchKernelGGL((k_ln_ext<2, ACT, PRO, MASK, WPB>), grid, block, 0, s, a); break;
-        case 4: hipLaunchKernelGGL((k_ln_ext<4, ACT, PRO, MASK, WPB>), grid, block, 0, s, a); break;
-        case 8: hipLaunchKernelGGL((k_ln_ext<8, ACT, PRO, MASK, WPB>), grid, block, 0, s, a); break;
-        default: hipLaunchKernelGGL((k_ln_ext<16, ACT, PRO, MASK, WPB>), grid, block, 0, s, a); break;
+        case 1: hipLaunchKernelGGL((k_ln_ext<1, ACT, PRO, MASK, WPB, FLAT>), grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL((k_ln_ext<2, ACT, PRO, MASK, WPB, FLAT>), grid, block, 0, s, a); break;
+        case 4: hipLaunchKernelGGL((k_ln_ext<4, ACT, PRO, MASK, WPB, FLAT>), grid, block, 0, s, a); break;
+        case 8: hipLaunchKernelGGL((k_ln_ext<8, ACT, PRO, MASK, WPB, FLAT>), grid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL((k_ln_ext<16, ACT, PRO, MASK, WPB, FLAT>), grid, block, 0, s, a); break;
     }
 }
 
+// Uniformly strided tensors take the FLAT kernels (four rows per workgroup
+// past 2048 rows); any other layout the general row map, one row each.
 template <int PRO, bool MASK>
-void go_pro(const LnExtArgs& a, bool act, int nv, int wpb, int64_t nr, hipStream_t s) {
+void go_pro(const LnExtArgs& a, bool act, int nv, int wpb, bool flat, int64_t nr, hipStream_t s) {
+    if (!flat) {
+        const dim3 grid(static_cast<unsigned>(nr));
+        if (act) go_nv<true, PRO, MASK, 1, false>(a, nv, grid, s);
+        else go_nv<false, PRO, MASK, 1, false>(a, nv, grid, s);
+        return;
+    }
     const dim3 grid(static_cast<unsigned>(cdiv(nr, wpb)));
     if (wpb == 1) {
-        if (act) go_nv<true, PRO, MASK, 1>(a, nv, grid, s);
-        else go_nv<false, PRO, MASK, 1>(a, nv, grid, s);
+        if (act) go_nv<true, PRO, MASK, 1, true>(a, nv, grid, s);
+        else go_nv<false, PRO, MASK, 1, true>(a, nv, grid, s);
     } else {
-        if (act) go_nv<true, PRO, MASK, 4>(a, nv, grid, s);
-        else go_nv<false, PRO, MASK, 4>(a, nv, grid, s);
+        if (act) go_nv<true, PRO, MASK, 4, true>(a, nv, grid, s);
+        else go_nv<false, PRO, MASK, 4, true>(a, nv, grid, s);
     }
 }
 
@@ -182,9 +198,10 @@ int launch_layer_norm_ext(const cbx_tensor* a, const cbx_tensor* a_bias, const c
     const int nv = ne0 <= 256 ? 1 : ne0 <= 512 ? 2 : ne0 <= 1024 ? 4 : ne0 <= 2048 ? 8 : 16;
     const int wpb = nr >= int64_t{8} * st->n_cu ? 4 : 1;
     const bool has_act = act != CBX_UNARY_NONE;
-    if (mask) go_pro<PRO_NONE, true>(p, has_act, nv, wpb, nr, strm);
-    else if (a_bias) go_pro<PRO_BIAS_RESID, false>(p, has_act, nv, wpb, nr, strm);
-    else go_pro<PRO_RESID, false>(p, has_act, nv, wpb, nr, strm);
+    const bool flat = p.ma.flat && p.my.flat && (!r || p.mr.flat) && (!s || p.ms.flat);
+    if (mask) go_pro<PRO_NONE, true>(p, has_act, nv, wpb, flat, nr, strm);
+    else if (a_bias) go_pro<PRO_BIAS_RESID, false>(p, has_act, nv, wpb, flat, nr, strm);
+    else go_pro<PRO_RESID, false>(p, has_act, nv, wpb, flat, nr, strm);
     return check_launch(what);
 }
 

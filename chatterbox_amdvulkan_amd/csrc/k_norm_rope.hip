@@ -46,14 +46,16 @@ __device__ __forceinline__ int pair_of(int i, int nd, int half) {
     return i >> 1;
 }
 
-template <int NV, int MODE>
+// FLAT: x and y rows at one stride each (no test of the row map before the
+// loads are issued).
+template <int NV, int MODE, bool FLAT>
 __global__ __launch_bounds__(64) void k_layer_norm_rope(NormRopeArgs a) {
     __shared__ float row[kRowMax];
     const int lane = threadIdx.x;
     const uint32_t r = blockIdx.x;                // token row over ne1 * ne2
     const int64_t ne0 = a.ne0;
-    const char* xr = a.x + row_at(a.mx, r);
-    char* yr = a.y + row_at(a.my, r);
+    const char* xr = a.x + (FLAT ? static_cast<int64_t>(r) * a.mx.nb1 : row_at(a.mx, r));
+    char* yr = a.y + (FLAT ? static_cast<int64_t>(r) * a.my.nb1 : row_at(a.my, r));
     const int nd = a.rp.n_dims, half = nd / 2;
 
     // position of the token (ne1 index of x); the row and affine loads go
@@ -62,7 +64,7 @@ __global__ __launch_bounds__(64) void k_layer_norm_rope(NormRopeArgs a) {
     const uint32_t tok = r % a.n_tok;
     const int32_t p = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const int32_t*>(a.pos + tok * a.pos_nb0));
     Affine<NV> af;
-    af.load(a.w, a.b, lane, ne0);
+    af.load_sel(a.w, a.b, reinterpret_cast<const float*>(yr), lane, ne0);
     float4 v[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
@@ -156,12 +158,12 @@ __global__ __launch_bounds__(64) void k_layer_norm_rope(NormRopeArgs a) {
     }
 }
 
-template <int MODE>
+template <int MODE, bool FLAT>
 void go(const NormRopeArgs& a, int nv, dim3 grid, hipStream_t s) {
     switch (nv) {
-        case 1: hipLaunchKernelGGL((k_layer_norm_rope<1, MODE>), grid, dim3(64), 0, s, a); break;
-        case 2: hipLaunchKernelGGL((k_layer_norm_rope<2, MODE>), grid, dim3(64), 0, s, a); break;
-        default: hipLaunchKernelGGL((k_layer_norm_rope<4, MODE>), grid, dim3(64), 0, s, a); break;
+        case 1: hipLaunchKernelGGL((k_layer_norm_rope<1, MODE, FLAT>), grid, dim3(64), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((k_layer_norm_rope<2, MODE, FLAT>), grid, dim3(64), 0, s, a); break;
+        default: hipLaunchKernelGGL((k_layer_norm_rope<4, MODE, FLAT>), grid, dim3(64), 0, s, a); break;
     }
 }
 
@@ -192,8 +194,14 @@ int launch_layer_norm_rope(const cbx_tensor* x, const cbx_tensor* w, const cbx_t
     if (rows >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "layer_norm_rope: too many rows");
     const int nv = x->ne[0] <= 256 ? 1 : x->ne[0] <= 512 ? 2 : 4;
     const dim3 grid(static_cast<unsigned>(rows));
-    if (p.mode == 2) go<2>(a, nv, grid, s);
-    else go<0>(a, nv, grid, s);
+    const bool flat = a.mx.flat && a.my.flat;
+    if (p.mode == 2) {
+        if (flat) go<2, true>(a, nv, grid, s);
+        else go<2, false>(a, nv, grid, s);
+    } else {
+        if (flat) go<0, true>(a, nv, grid, s);
+        else go<0, false>(a, nv, grid, s);
+    }
     return check_launch("layer_norm_rope");
 }
 

@@ -79,29 +79,28 @@ __global__ __launch_bounds__(kGatherThreads) void k_get_rows(GatherArgs a) {
         ok = ok && id2 >= 0 && id2 < a.src2.rows;
     }
     char* d = a.dst + i10 * a.dnb1 + i11 * a.dnb2 + i12 * a.dnb3;
-    if (!ok) {
-        // ggml aborts on an out-of-range index; here the row is zeroed and
-        // the sticky device error bit is raised for the host to read.
-        for (int64_t j = threadIdx.x; j < ne0; j += kGatherThreads) reinterpret_cast<float*>(d)[j] = 0.0f;
-        if (threadIdx.x == 0) atomicOr(a.err, static_cast<uint32_t>(DEV_ERR_ROW_INDEX));
-        return;
-    }
-    const char* s = a.src.p + id * a.src.nb1 + i11 * a.src.nb2 + i12 * a.src.nb3;
+    // ggml aborts on an out-of-range index; here the row is zeroed and the
+    // sticky device error bit is raised for the host to read.  A bad id
+    // reads row 0 (the table has rows) and the values are replaced by zeros,
+    // so no branch stands between the id and the row loads.
+    const int64_t r1 = ok ? id : 0, r2 = ok ? id2 : 0;
+    const char* s = a.src.p + r1 * a.src.nb1 + i11 * a.src.nb2 + i12 * a.src.nb3;
     const char* s2 = nullptr;
-    if constexpr (TYPE2 >= 0) s2 = a.src2.p + id2 * a.src2.nb1 + i11 * a.src2.nb2 + i12 * a.src2.nb3;
+    if constexpr (TYPE2 >= 0) s2 = a.src2.p + r2 * a.src2.nb1 + i11 * a.src2.nb2 + i12 * a.src2.nb3;
     if constexpr (VEC) {
         for (int64_t j = threadIdx.x * 4; j < ne0; j += kGatherThreads * 4) {
             float4 v = load_row4<TYPE>(s, j);
             if constexpr (TYPE2 >= 0) v = add4(v, load_row4<TYPE2>(s2, j));
-            *reinterpret_cast<float4*>(d + j * 4) = v;
+            *reinterpret_cast<float4*>(d + j * 4) = ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     } else {
         for (int64_t j = threadIdx.x; j < ne0; j += kGatherThreads) {
             float v = load_row1<TYPE>(s, j);
             if constexpr (TYPE2 >= 0) v = v + load_row1<TYPE2>(s2, j);
-            reinterpret_cast<float*>(d)[j] = v;
+            reinterpret_cast<float*>(d)[j] = ok ? v : 0.0f;
         }
     }
+    if (!ok && threadIdx.x == 0) atomicOr(a.err, static_cast<uint32_t>(DEV_ERR_ROW_INDEX));
 }
 
 GTable gtable(const cbx_tensor* t) {

@@ -43,7 +43,8 @@ struct SoftMaxArgs {
 
 // WPB rows per workgroup; with one, the grid is exactly one workgroup per
 // row and nothing waits (bounds check, block size) before the loads issue.
-template <int NV, int WPB>
+// FLAT: rows at one stride each, so the row map's flag is not tested either.
+template <int NV, int WPB, bool FLAT>
 __global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
     const int lane = threadIdx.x & 63;
     uint32_t r = blockIdx.x;
@@ -54,8 +55,8 @@ __global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
     const int64_t ne0 = a.ne0;
     const float s = a.s;
     const int64_t n_past = a.n_past;
-    const char* xr = a.x + row_at(a.mx, r);
-    char* yr = a.y + row_at(a.my, r);
+    const char* xr = a.x + (FLAT ? static_cast<int64_t>(r) * a.mx.nb1 : row_at(a.mx, r));
+    char* yr = a.y + (FLAT ? static_cast<int64_t>(r) * a.my.nb1 : row_at(a.my, r));
     // last unmasked column of this row
     const int64_t j = r % a.n_q;
     const int64_t lim = n_past >= 0 ? (n_past + j < ne0 - 1 ? n_past + j : ne0 - 1) : ne0 - 1;
@@ -126,15 +127,15 @@ __global__ __launch_bounds__(kThreads) void k_soft_max_loop(View x, View y, floa
 
 int waves_for(int64_t rows, const DeviceState* st) { return rows >= int64_t{8} * st->n_cu ? 4 : 1; }
 
-template <int WPB>
+template <int WPB, bool FLAT>
 void sm_wave(int nv, const SoftMaxArgs& a, hipStream_t strm) {
     const dim3 grid(static_cast<unsigned>(cdiv(a.nr, WPB))), block(64 * WPB);
     switch (nv) {
-        case 1: hipLaunchKernelGGL((k_soft_max_wave<1, WPB>), grid, block, 0, strm, a); break;
-        case 2: hipLaunchKernelGGL((k_soft_max_wave<2, WPB>), grid, block, 0, strm, a); break;
-        case 4: hipLaunchKernelGGL((k_soft_max_wave<4, WPB>), grid, block, 0, strm, a); break;
-        case 8: hipLaunchKernelGGL((k_soft_max_wave<8, WPB>), grid, block, 0, strm, a); break;
-        default: hipLaunchKernelGGL((k_soft_max_wave<16, WPB>), grid, block, 0, strm, a); break;
+        case 1: hipLaunchKernelGGL((k_soft_max_wave<1, WPB, FLAT>), grid, block, 0, strm, a); break;
+        case 2: hipLaunchKernelGGL((k_soft_max_wave<2, WPB, FLAT>), grid, block, 0, strm, a); break;
+        case 4: hipLaunchKernelGGL((k_soft_max_wave<4, WPB, FLAT>), grid, block, 0, strm, a); break;
+        case 8: hipLaunchKernelGGL((k_soft_max_wave<8, WPB, FLAT>), grid, block, 0, strm, a); break;
+        default: hipLaunchKernelGGL((k_soft_max_wave<16, WPB, FLAT>), grid, block, 0, strm, a); break;
     }
 }
 
@@ -162,8 +163,10 @@ int launch_soft_max(const cbx_tensor* x, float s, int64_t n_past, cbx_tensor* y,
         a.nr = static_cast<int32_t>(nr);
         a.n_q = static_cast<uint32_t>(x->ne[1]);
         a.s = s;
-        if (waves_for(nr, st) == 1) sm_wave<1>(nv, a, strm);
-        else sm_wave<4>(nv, a, strm);
+        // strided-plane layouts take one row per workgroup through the row map
+        if (!(a.mx.flat && a.my.flat)) sm_wave<1, false>(nv, a, strm);
+        else if (waves_for(nr, st) == 1) sm_wave<1, true>(nv, a, strm);
+        else sm_wave<4, true>(nv, a, strm);
     } else {
         hipLaunchKernelGGL(k_soft_max_loop, dim3(static_cast<unsigned>(nr)), dim3(kThreads), 0, strm, vx, vy, s, n_past,
                            fx, fy);
