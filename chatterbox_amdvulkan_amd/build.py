@@ -35,6 +35,7 @@ SOURCES = [
     "k_norm_rope.hip",
     "k_softmax.hip",
     "k_norm_ext.hip",
+    "k_conv1d.hip",
     "k_eltwise.hip",
     "k_batch.hip",
 ]

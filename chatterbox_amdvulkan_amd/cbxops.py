@@ -168,6 +168,9 @@ def load() -> ctypes.CDLL:
         "cbx_add_layer_norm": (i, [P, P, P, P, P, f, i, P, P, vp]),
         "cbx_layer_norm_mask": (i, [P, P, P, f, i, P, P, vp]),
         "cbx_bias_act": (i, [i, P, P, P, vp]),
+        "cbx_conv1d_weights_create": (i, [P, vp, ctypes.POINTER(vp)]),
+        "cbx_conv1d_weights_destroy": (None, [vp]),
+        "cbx_conv1d": (i, [P, vp, i, i, i, i, P, P, f, P, P, P, vp]),
         "cbx_run_ops": (i, [ctypes.POINTER(OpStruct), i, vp]),
         "cbx_gguf_open": (i, [ctypes.c_char_p, ctypes.POINTER(vp)]),
         "cbx_gguf_close": (None, [vp]),
@@ -518,6 +521,48 @@ def bias_act(act, x, bias, out=None):
     _ready(x)
     out = _out_like(x, out)
     _check(load().cbx_bias_act(act, _ref(desc(x)), _ref(desc(bias)), _ref(desc(out)), _stream()))
+    return out
+
+
+# cbx_conv_prologue
+CONV_PRO_NONE, CONV_PRO_SNAKE, CONV_PRO_LEAKY_RELU = 0, 1, 2
+
+
+class Conv1dWeights:
+    """cbx_conv1d_weights: the f16 copy of a conv1d weight, torch [C_out,
+    C_in, K] (ggml ne (K, C_in, C_out)), F32 or F16."""
+
+    def __init__(self, w: torch.Tensor):
+        _ready(w)
+        h = ctypes.c_void_p()
+        _check(load().cbx_conv1d_weights_create(_ref(desc(w)), _stream(), ctypes.byref(h)))
+        self.handle = h
+        self.c_out, self.c_in, self.k = w.shape
+
+    def close(self):
+        if self.handle:
+            load().cbx_conv1d_weights_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def conv1d(x, weights: Conv1dWeights, stride=1, pad=0, dilation=1, prologue=CONV_PRO_NONE, alpha=None,
+           alpha_inv=None, slope=0.0, bias=None, res=None, out=None):
+    """conv1d_CT(pro(x)) (+ bias) (+ res): x torch [B, T_in, C_in] or [T_in,
+    C_in] (channel innermost, the reference's (C, T)); returns [.., T_out, C_out]."""
+    _ready(x)
+    t_in = x.shape[-2]
+    t_out = (t_in + 2 * pad - dilation * (weights.k - 1) - 1) // stride + 1
+    if out is None:
+        out = torch.empty(tuple(x.shape[:-2]) + (t_out, weights.c_out), dtype=torch.float32, device=x.device)
+    opt = lambda t: _ref(desc(t)) if t is not None else None  # noqa: E731
+    _check(load().cbx_conv1d(_ref(desc(x)), weights.handle, stride, pad, dilation, prologue, opt(alpha),
+                             opt(alpha_inv), slope, opt(bias), opt(res), _ref(desc(out)), _stream()))
     return out
 
 

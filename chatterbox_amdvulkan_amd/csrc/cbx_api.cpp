@@ -153,6 +153,12 @@ static void yarn_cos_sin(float theta_extrap, int64_t i0, const RopeParams& p, fl
 
 }  // namespace cbx
 
+struct cbx_conv1d_weights {
+    int       device;
+    int64_t   k, c_in, c_out, c_in_pad, c_out_pad;
+    _Float16* data;   // [c_out_pad][k][c_in_pad]
+};
+
 struct cbx_rope_cache {
     int              device;
     cbx::RopeParams  p;
@@ -702,6 +708,125 @@ int cbx_bias_act(int act, const cbx_tensor* x, const cbx_tensor* bias, cbx_tenso
     if (!is_contiguous(bias)) return set_error(CBX_ERR_UNSUPPORTED, "cbx_bias_act: bias must be contiguous");
     if (nelements(x) == 0) return CBX_OK;
     return launch_bias_act(act, x, bias, y, st, reinterpret_cast<hipStream_t>(stream));
+}
+
+// ---- conv1d -------------------------------------------------------------------
+
+int cbx_conv1d_weights_create(const cbx_tensor* w, cbx_stream stream, cbx_conv1d_weights** out) {
+    const char* what = "cbx_conv1d_weights_create";
+    clear_error();
+    if (!out) return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d_weights_create: out is NULL");
+    *out = nullptr;
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(w, what, "w"))) return rc;
+    if (w->type != CBX_TYPE_F32 && w->type != CBX_TYPE_F16) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_conv1d_weights_create: w must be F32 or F16");
+    }
+    if (w->ne[0] < 1 || w->ne[0] > 64 || w->ne[1] < 1 || w->ne[1] > 8192 || w->ne[2] < 1 || w->ne[2] > 8192 ||
+        w->ne[3] != 1) {
+        return set_error(CBX_ERR_INVALID_ARG,
+                         "cbx_conv1d_weights_create: w must be (K <= 64, C_in <= 8192, C_out <= 8192, 1)");
+    }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(CBX_ERR_HIP, "cbx_conv1d_weights_create: hipGetDevice failed");
+    auto* cw = new cbx_conv1d_weights();
+    cw->device = dev;
+    cw->k = w->ne[0];
+    cw->c_in = w->ne[1];
+    cw->c_out = w->ne[2];
+    conv1d_weights_layout(cw->c_in, cw->c_out, &cw->c_in_pad, &cw->c_out_pad);
+    const size_t bytes = static_cast<size_t>(cw->c_out_pad * cw->k * cw->c_in_pad) * sizeof(_Float16);
+    if (hipMalloc(reinterpret_cast<void**>(&cw->data), bytes) != hipSuccess) {
+        delete cw;
+        return set_error(CBX_ERR_HIP, "cbx_conv1d_weights_create: hipMalloc failed");
+    }
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    rc = launch_conv1d_weights(w, cw->data, cw->c_in_pad, cw->c_out_pad, s);
+    if (!rc && hipStreamSynchronize(s) != hipSuccess) {
+        rc = set_error(CBX_ERR_HIP, "cbx_conv1d_weights_create: stream synchronisation failed");
+    }
+    if (rc) {
+        hipFree(cw->data);
+        delete cw;
+        return rc;
+    }
+    *out = cw;
+    return CBX_OK;
+}
+
+void cbx_conv1d_weights_destroy(cbx_conv1d_weights* w) {
+    if (!w) return;
+    int prev = 0;
+    hipGetDevice(&prev);
+    hipSetDevice(w->device);
+    hipDeviceSynchronize();
+    hipFree(w->data);
+    hipSetDevice(prev);
+    delete w;
+}
+
+int cbx_conv1d(const cbx_tensor* x, const cbx_conv1d_weights* w, int stride, int pad, int dilation, int prologue,
+               const cbx_tensor* alpha, const cbx_tensor* alpha_inv, float slope, const cbx_tensor* bias,
+               const cbx_tensor* res, cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_conv1d";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if (!w) return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: weights are NULL");
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev != w->device) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: the weights belong to another device");
+    }
+    if ((rc = validate(x, what, "x")) || (rc = validate(y, what, "y"))) return rc;
+    if (x->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, "cbx_conv1d: F32 only");
+    if (stride < 1 || pad < 0 || dilation < 1 || stride > 64 || pad > (1 << 20) || dilation > 1024) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: stride must be 1..64, pad >= 0, dilation 1..1024");
+    }
+    if (prologue < CBX_CONV_PRO_NONE || prologue > CBX_CONV_PRO_LEAKY_RELU) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: unknown prologue");
+    }
+    if (x->ne[0] != w->c_in || x->ne[3] != 1) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: x must be (C_in, T_in, B, 1) with the weights' C_in");
+    }
+    const int64_t t_in = x->ne[1], batch = x->ne[2];
+    const int64_t span = dilation * (w->k - 1) + 1;
+    const int64_t t_out = t_in + 2 * pad >= span ? (t_in + 2 * pad - span) / stride + 1 : 0;
+    if (y->ne[0] != w->c_out || y->ne[1] != t_out || y->ne[2] != batch || y->ne[3] != 1) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: y must be (C_out, T_out, B, 1), T_out = (T_in + 2 pad - "
+                                              "dilation (K - 1) - 1) / stride + 1");
+    }
+    if (t_in >= (int64_t{1} << 30) || t_out >= (int64_t{1} << 30) || batch >= 65536) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_conv1d: T must be below 2^30 and B below 65536");
+    }
+    if (bias) {
+        if ((rc = validate(bias, what, "bias"))) return rc;
+        if (bias->type != CBX_TYPE_F32 || nelements(bias) != w->c_out || !is_contiguous(bias)) {
+            return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: bias must be contiguous F32 with C_out elements");
+        }
+    }
+    if (res) {
+        if ((rc = validate(res, what, "res"))) return rc;
+        if (res->type != CBX_TYPE_F32 || !same_shape(res, y)) {
+            return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: res must be F32 with y's shape");
+        }
+    }
+    if (prologue == CBX_CONV_PRO_SNAKE) {
+        for (const cbx_tensor* p : {alpha, alpha_inv}) {
+            if ((rc = validate(p, what, p == alpha ? "alpha" : "alpha_inv"))) return rc;
+            if (p->type != CBX_TYPE_F32 || nelements(p) != w->c_in || !is_contiguous(p)) {
+                return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: alpha and alpha_inv must be contiguous F32 with C_in elements");
+            }
+        }
+    }
+    if (nelements(y) == 0) return CBX_OK;
+    if (overlaps(x, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: y must not overlap x");
+    return launch_conv1d(x, w->data, w->k, w->c_in_pad, w->c_out, stride, pad, dilation, prologue,
+                         prologue == CBX_CONV_PRO_SNAKE ? alpha : nullptr,
+                         prologue == CBX_CONV_PRO_SNAKE ? alpha_inv : nullptr, slope, bias, res, y, st,
+                         reinterpret_cast<hipStream_t>(stream));
 }
 
 int cbx_snake(const cbx_tensor* x, const cbx_tensor* alpha, const cbx_tensor* alpha_inv, cbx_tensor* y,

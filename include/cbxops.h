@@ -258,6 +258,43 @@ int cbx_swiglu(const cbx_tensor* g, const cbx_tensor* u, cbx_tensor* y,
 int cbx_snake(const cbx_tensor* x, const cbx_tensor* alpha,
               const cbx_tensor* alpha_inv, cbx_tensor* y, cbx_stream stream);
 
+/* ---- HiFT convolutions -------------------------------------------------- */
+
+/* Weights of one conv1d, prepared once for the matrix cores: an f16 copy of
+ * a ggml (K, C_in, C_out) F32/F16 weight (the reference's ConvW.w,
+ * hift_vocoder.cpp:77-93; PyTorch (C_out, C_in, K) order), rounded as the
+ * reference's mul_mat rounds its F32 operand to F16.  Allocates device
+ * memory on the current device; returns when the copy is complete (the
+ * source may then be freed).  K <= 64, C_in and C_out <= 8192.            */
+typedef struct cbx_conv1d_weights cbx_conv1d_weights;
+int  cbx_conv1d_weights_create(const cbx_tensor* w, cbx_stream stream,
+                               cbx_conv1d_weights** out);
+void cbx_conv1d_weights_destroy(cbx_conv1d_weights* w);
+
+typedef enum cbx_conv_prologue {
+    CBX_CONV_PRO_NONE       = 0,
+    CBX_CONV_PRO_SNAKE      = 1,  /* snake(x) = x + sin^2(x*alpha)*alpha_inv  */
+    CBX_CONV_PRO_LEAKY_RELU = 2,  /* leaky_relu(x, slope)                     */
+} cbx_conv_prologue;
+
+/* conv1d_CT(pro(x)) (+ bias) (+ res) in one kernel, on the reference's
+ * (C, T) layout, channel innermost (hift_vocoder.cpp:46-59,77-93):
+ *   y[t][co] = res[t][co] + (bias[co] + sum_{ci,k} f16(w[co][ci][k]) *
+ *              f16(pro(x)[t*stride + k*dilation - pad][ci]))
+ * with zero padding outside [0, T_in): the ResBlock sublayer's snake ->
+ * conv and snake -> conv -> + x (hift_vocoder.cpp:119-138) are two calls;
+ * leaky_relu -> conv_post (:748-749) one.  Products are summed in f32 on
+ * the matrix cores, as the reference's im2col (F16) + mul_mat (PREC_F32)
+ * sums them (order differs).  x: F32 (C_in, T_in, B, 1), rows of C_in
+ * contiguous floats; y, res: F32 (C_out, T_out, B, 1), T_out = (T_in +
+ * 2 pad - dilation (K - 1) - 1) / stride + 1; bias: F32 C_out or NULL;
+ * alpha, alpha_inv: F32 C_in (snake only).  y may be res, not x.           */
+int cbx_conv1d(const cbx_tensor* x, const cbx_conv1d_weights* w, int stride,
+               int pad, int dilation, int prologue, const cbx_tensor* alpha,
+               const cbx_tensor* alpha_inv, float slope,
+               const cbx_tensor* bias, const cbx_tensor* res, cbx_tensor* y,
+               cbx_stream stream);
+
 /* ---- model tables from a GGUF file ---------------------------------------- */
 
 /* The reference reads its weights with ggml's gguf reader: the header,

@@ -851,3 +851,87 @@ int cbxo_scale_diag_mask_soft_max(const cbxo_tensor* x, float sc, int n_past, cb
     free_tmp(&t);
     return rc;
 }
+
+/* ------------------------------------------------------------------------ */
+/* conv1d_CT with a fused prologue (hift_vocoder.cpp:46-59,77-93,119-138)   */
+/* ------------------------------------------------------------------------ */
+
+/* ggml: conv_1d_f32 = im2col(w, x, s, 0, p, 0, d, 0, false, F16) then
+ * mul_mat(im2col, w_2d) with F32 precision: element (ic*K + k, ol) of the
+ * im2col matrix is f16(x[ic][ol*s + k*d - p]), 0 outside [0, T_in); mul_mat
+ * converts w to F16 (its F16 operand's dot type) and sums the products.
+ * Then ggml_add of the (1, C_out) bias, the transposes, and the ResBlock's
+ * residual ggml_add(x, h).  Prologues: snake() (hift_vocoder.cpp:64-73) as
+ * five f32 ops; leaky_relu as ggml_vec_leaky_relu_f32. */
+int cbxo_conv1d(const cbxo_tensor* x, const cbxo_tensor* w, int stride, int pad, int dilation, int prologue,
+                const cbxo_tensor* alpha, const cbxo_tensor* alpha_inv, float slope, const cbxo_tensor* bias,
+                const cbxo_tensor* res, cbxo_tensor* y, int nth) {
+    if (x->type != CBXO_TYPE_F32 || y->type != CBXO_TYPE_F32) return -1;
+    if (w->type != CBXO_TYPE_F32 && w->type != CBXO_TYPE_F16) return -1;
+    if (stride < 1 || pad < 0 || dilation < 1 || x->ne[3] != 1) return -1;
+    const int64_t C_in = x->ne[0], T_in = x->ne[1], B = x->ne[2];
+    const int64_t K = w->ne[0], C_out = w->ne[2];
+    if (w->ne[1] != C_in || w->ne[3] != 1) return -1;
+    const int64_t T_out = (T_in + 2 * pad - dilation * (K - 1) - 1) / stride + 1;
+    if (T_out < 1 || y->ne[0] != C_out || y->ne[1] != T_out || y->ne[2] != B || y->ne[3] != 1) return -1;
+    if (bias && (bias->type != CBXO_TYPE_F32 || bias->ne[0] != C_out)) return -1;
+    if (res && (res->type != CBXO_TYPE_F32 || !same_shape(res, y))) return -1;
+    if (prologue == 1 && (!alpha || !alpha_inv || alpha->ne[0] != C_in || alpha_inv->ne[0] != C_in)) return -1;
+    if (prologue < 0 || prologue > 2) return -1;
+    /* the f16 im2col source: pro(x) rounded to f16, per (b, t, ic) */
+    float* h = (float*)malloc(sizeof(float) * (size_t)(C_in * T_in * B));
+    float* wf = (float*)malloc(sizeof(float) * (size_t)(C_out * K * C_in));   /* [oc][k][ic] */
+    if (!h || !wf) { free(h); free(wf); return -1; }
+    for (int64_t b = 0; b < B; b++) {
+        for (int64_t t = 0; t < T_in; t++) {
+            const float* rx = (const float*)row_ptr(x, t, b, 0);
+            for (int64_t ic = 0; ic < C_in; ic++) {
+                float v = rx[ic];
+                if (prologue == 1) {
+                    const float a = ((const float*)alpha->data)[ic];
+                    const float ai = ((const float*)alpha_inv->data)[ic];
+                    const float xa = v * a;
+                    const float sn = sinf(xa);
+                    const float s2 = sn * sn;
+                    const float m = s2 * ai;
+                    v = v + m;
+                } else if (prologue == 2) {
+                    v = op_leaky(v, slope);
+                }
+                h[(b * T_in + t) * C_in + ic] = cbxo_fp16_to_fp32(cbxo_fp32_to_fp16(v));
+            }
+        }
+    }
+    for (int64_t oc = 0; oc < C_out; oc++) {
+        for (int64_t ic = 0; ic < C_in; ic++) {
+            const char* rw = row_ptr(w, ic, oc, 0);
+            for (int64_t k = 0; k < K; k++) {
+                const float v = load_elem(w, rw, k);
+                wf[(oc * K + k) * C_in + ic] = cbxo_fp16_to_fp32(cbxo_fp32_to_fp16(v));
+            }
+        }
+    }
+#pragma omp parallel for num_threads(nth) schedule(static)
+    for (int64_t bt = 0; bt < B * T_out; bt++) {
+        const int64_t b = bt / T_out, t = bt % T_out;
+        float* ry = (float*)row_ptr(y, t, b, 0);
+        const float* rr = res ? (const float*)row_ptr(res, t, b, 0) : NULL;
+        for (int64_t oc = 0; oc < C_out; oc++) {
+            double acc = 0.0;
+            for (int64_t k = 0; k < K; k++) {
+                const int64_t ti = t * stride + k * dilation - pad;
+                if (ti < 0 || ti >= T_in) continue;
+                const float* hr = h + (b * T_in + ti) * C_in;
+                const float* wr = wf + (oc * K + k) * C_in;
+                for (int64_t ic = 0; ic < C_in; ic++) acc += (double)hr[ic] * (double)wr[ic];
+            }
+            float v = (float)acc;
+            if (bias) v = v + ((const float*)bias->data)[oc];
+            if (rr) v = rr[oc] + v;
+            ry[oc] = v;
+        }
+    }
+    free(h);
+    free(wf);
+    return 0;
+}

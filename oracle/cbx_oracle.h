@@ -149,6 +149,19 @@ int cbxo_scale_diag_mask_soft_max(const cbxo_tensor* x, float s, int n_past,
 int cbxo_get_rows_add(const cbxo_tensor* src, const cbxo_tensor* ids,
                       const cbxo_tensor* src2, const cbxo_tensor* ids2,
                       cbxo_tensor* dst, int n_threads);
+/* conv1d_CT(pro(x)) [+ bias] [+ res] on the reference's (C, T) layout
+ * (hift_vocoder.cpp:46-59,77-93,119-138): im2col to F16, the weights
+ * converted to F16 by mul_mat, products summed, the f32 result plus the
+ * bias, then plus res.  x (C_in, T_in, B) F32; w (K, C_in, C_out) F32/F16;
+ * bias (C_out) or NULL; res (C_out, T_out, B) or NULL; y (C_out, T_out, B).
+ * prologue 0: none, 1: snake (alpha, alpha_inv (C_in)), 2: leaky_relu.
+ * The sum is accumulated in f64 (the reference's f32 SIMD accumulation
+ * order depends on the host ISA).                                         */
+int cbxo_conv1d(const cbxo_tensor* x, const cbxo_tensor* w, int stride,
+                int pad, int dilation, int prologue,
+                const cbxo_tensor* alpha, const cbxo_tensor* alpha_inv,
+                float slope, const cbxo_tensor* bias, const cbxo_tensor* res,
+                cbxo_tensor* y, int n_threads);
 
 #ifdef __cplusplus
 }

@@ -76,6 +76,7 @@ def lib():
             "cbxo_diag_mask_inf": (i, [P, i, P, i]),
             "cbxo_soft_max": (i, [P, P, i]),
             "cbxo_scale_diag_mask_soft_max": (i, [P, f, i, P, i]),
+            "cbxo_conv1d": (i, [P, P, i, i, i, i, P, P, f, P, P, P, i]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -341,4 +342,25 @@ def snake(x, alpha, alpha_inv, nth=1):
     out = np.empty_like(x)
     _check(lib().cbxo_snake(_ref(desc(x)), _ref(desc(alpha)), _ref(desc(alpha_inv)), _ref(desc(out)), nth),
            "snake")
+    return out
+
+
+CONV_PRO_NONE, CONV_PRO_SNAKE, CONV_PRO_LEAKY = 0, 1, 2
+
+
+def conv1d(x, w, stride=1, pad=0, dilation=1, prologue=0, alpha=None, alpha_inv=None, slope=0.0, bias=None,
+           res=None, nth=1):
+    """conv1d_CT(pro(x)) (+ bias) (+ res).  x: numpy [B, T_in, C_in] or
+    [T_in, C_in] (ggml ne = (C_in, T_in, B)); w: [C_out, C_in, K] (ggml ne =
+    (K, C_in, C_out), the PyTorch layout); returns [.., T_out, C_out]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    C_out, C_in, K = w.shape
+    T_in = x.shape[-2]
+    T_out = (T_in + 2 * pad - dilation * (K - 1) - 1) // stride + 1
+    out = np.empty(x.shape[:-2] + (T_out, C_out), dtype=np.float32)
+    opt = lambda a: _ref(desc(np.ascontiguousarray(a, dtype=np.float32))) if a is not None else None  # noqa: E731
+    keep = [np.ascontiguousarray(a, dtype=np.float32) if a is not None else None for a in (alpha, alpha_inv, bias, res)]
+    _check(lib().cbxo_conv1d(_ref(desc(x)), _ref(desc(np.ascontiguousarray(w))), stride, pad, dilation, prologue,
+                             opt(keep[0]), opt(keep[1]), slope, opt(keep[2]), opt(keep[3]), _ref(desc(out)), nth),
+           "conv1d")
     return out

@@ -1,0 +1,176 @@
+"""cbx_conv1d (HiFT conv1d with the Snake / LeakyReLU prologue, bias and
+residual fused) against the oracle's conv1d_CT restatement on the same
+inputs: ResBlock convs at each stage's channel count, kernel size and
+dilation (hift_vocoder.cpp:119-138), conv_pre, conv_post and the strided
+source convs (:673, :713, :749).
+
+Tolerance: both sides round the conv input and the weights to f16 and sum
+exact products, the oracle in f64, the matrix cores in f32 in their own
+order, so per output |got - ref| <= 2^-13 * sum_k |a_k b_k| (the sum of the
+absolute products, computed by the oracle on |a|, |b|).  A Snake prologue
+computed with the device's sinf can land on the other side of an f16
+rounding boundary than glibc's for a few inputs; each such term moves by
+2^-11 |a_k b_k|, inside the same bound."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from chatterbox_amdvulkan_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def check(oracle, got, x, w, stride, pad, dil, pro, alpha, alpha_inv, slope, bias, res, what):
+    ref = oracle.conv1d(x, w, stride, pad, dil, pro, alpha, alpha_inv, slope, bias, res, nth=8)
+    if pro == oracle.CONV_PRO_SNAKE:
+        h = oracle.snake(x, alpha, alpha_inv)
+    elif pro == oracle.CONV_PRO_LEAKY:
+        h = oracle.leaky_relu(x, slope)
+    else:
+        h = x
+    mag = oracle.conv1d(np.abs(h), np.abs(w), stride, pad, dil, nth=8).astype(np.float64)
+    d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    bound = 2.0 ** -13 * mag + 2.0 ** -22 * np.abs(ref)
+    bad = d > bound
+    assert got.shape == ref.shape, what
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {got.size} outside the bound; worst excess "
+                           f"{float((d - bound).max()):.3g} (d {float(d.max()):.3g})")
+
+
+def case(oracle, C, T, C_out, K, stride, pad, dil, pro, with_bias=True, with_res=False, B=None, seed=0, w_f16=False,
+         slope=0.1):
+    sd = W.seed_of(11, seed)
+    shape = (T, C) if B is None else (B, T, C)
+    x = W.normal(sd, shape, 0.0, 1.0)
+    w = W.normal(sd + 1, (C_out, C, K), 0.0, 1.0 / np.sqrt(C * K))
+    if w_f16:
+        w = w.astype(np.float16)
+    alpha, alpha_inv = W.snake_alpha(C, seed + 2) if pro == oracle.CONV_PRO_SNAKE else (None, None)
+    bias = W.normal(sd + 3, (C_out,), 0.0, 0.1) if with_bias else None
+    T_out = (T + 2 * pad - dil * (K - 1) - 1) // stride + 1
+    res = W.normal(sd + 4, shape[:-2] + (T_out, C_out), 0.0, 1.0) if with_res else None
+    return x, w, alpha, alpha_inv, bias, res, slope
+
+
+def run(cbx, x, w, stride, pad, dil, pro, alpha, alpha_inv, slope, bias, res, out=None):
+    wts = cbx.Conv1dWeights(dev(w))
+    opt = lambda a: dev(a) if a is not None else None  # noqa: E731
+    y = cbx.conv1d(dev(x), wts, stride, pad, dil, pro, opt(alpha), opt(alpha_inv), slope, opt(bias), opt(res),
+                   out=out)
+    got = host(y)
+    wts.close()
+    return got
+
+
+RESBLOCK = [  # (C, T, K, dilation): the three stages' channels with each kernel size
+    (256, 300, 3, 1), (256, 301, 11, 5), (128, 800, 7, 3), (128, 777, 11, 1), (64, 2000, 11, 5), (64, 1500, 3, 3)]
+
+
+@pytest.mark.parametrize("C,T,K,dil", RESBLOCK)
+def test_resblock_snake_conv(cbx, oracle, C, T, K, dil):
+    """snake -> conv (K, dilation, 'same' padding) + bias: a ResBlock's first conv."""
+    pad = (K - 1) // 2 * dil
+    x, w, al, ai, b, r, sl = case(oracle, C, T, C, K, 1, pad, dil, oracle.CONV_PRO_SNAKE, seed=C + K + dil)
+    got = run(cbx, x, w, 1, pad, dil, cbx.CONV_PRO_SNAKE, al, ai, sl, b, r)
+    check(oracle, got, x, w, 1, pad, dil, oracle.CONV_PRO_SNAKE, al, ai, sl, b, r, f"C{C} T{T} K{K} d{dil}")
+
+
+@pytest.mark.parametrize("C,T,K", [(256, 400, 11), (128, 640, 7), (64, 1000, 3)])
+def test_resblock_second_conv_with_residual(cbx, oracle, C, T, K):
+    """snake -> conv (K, dilation 1) + bias, then + x: the sublayer's output."""
+    pad = (K - 1) // 2
+    x, w, al, ai, b, r, sl = case(oracle, C, T, C, K, 1, pad, 1, oracle.CONV_PRO_SNAKE, with_res=True, seed=7 * K)
+    got = run(cbx, x, w, 1, pad, 1, cbx.CONV_PRO_SNAKE, al, ai, sl, b, r)
+    check(oracle, got, x, w, 1, pad, 1, oracle.CONV_PRO_SNAKE, al, ai, sl, b, r, f"res C{C} K{K}")
+
+
+def test_conv_pre_and_post(cbx, oracle):
+    """conv_pre 80 -> 512 (k 7, p 3) and leaky_relu(0.01) -> conv_post 64 -> 18
+    (hift_vocoder.cpp:673, :748-749): channel counts that are not multiples
+    of the tiles."""
+    x, w, al, ai, b, r, sl = case(oracle, 80, 250, 512, 7, 1, 3, 1, oracle.CONV_PRO_NONE, seed=31)
+    got = run(cbx, x, w, 1, 3, 1, cbx.CONV_PRO_NONE, al, ai, sl, b, r)
+    check(oracle, got, x, w, 1, 3, 1, oracle.CONV_PRO_NONE, al, ai, sl, b, r, "conv_pre")
+    x, w, al, ai, b, r, sl = case(oracle, 64, 3000, 18, 7, 1, 3, 1, oracle.CONV_PRO_LEAKY, seed=32, slope=0.01)
+    got = run(cbx, x, w, 1, 3, 1, cbx.CONV_PRO_LEAKY_RELU, al, ai, 0.01, b, r)
+    check(oracle, got, x, w, 1, 3, 1, oracle.CONV_PRO_LEAKY, al, ai, 0.01, b, r, "conv_post")
+
+
+@pytest.mark.parametrize("stride,K,C_out", [(15, 7, 256), (3, 7, 128), (1, 11, 64)])
+def test_source_down_convs(cbx, oracle, stride, K, C_out):
+    """source_downs: 18 -> C_out with stride 15 / 3 / 1 (hift_vocoder.cpp:712-714)."""
+    pad = 0 if stride == 1 else stride // 2
+    x, w, al, ai, b, r, sl = case(oracle, 18, 1200, C_out, K, stride, pad, 1, oracle.CONV_PRO_NONE, seed=stride)
+    got = run(cbx, x, w, stride, pad, 1, cbx.CONV_PRO_NONE, al, ai, sl, b, r)
+    check(oracle, got, x, w, stride, pad, 1, oracle.CONV_PRO_NONE, al, ai, sl, b, r, f"src s{stride}")
+
+
+def test_batch_f16_weights_no_bias_and_in_place_residual(cbx, oracle):
+    x, w, al, ai, b, r, sl = case(oracle, 128, 333, 128, 7, 1, 9, 3, oracle.CONV_PRO_SNAKE, with_bias=False,
+                                  with_res=True, B=3, seed=40, w_f16=True)
+    wts = cbx.Conv1dWeights(dev(w))
+    rd = dev(r)
+    y = cbx.conv1d(dev(x), wts, 1, 9, 3, cbx.CONV_PRO_SNAKE, dev(al), dev(ai), sl, None, rd, out=rd)
+    assert y is rd
+    check(oracle, host(rd), x, w, 1, 9, 3, oracle.CONV_PRO_SNAKE, al, ai, sl, None, r, "batch 3, y == res")
+    wts.close()
+
+
+@pytest.mark.parametrize("C", [36, 34])
+def test_strided_input_rows(cbx, oracle, C):
+    """x rows read through a view with a larger row stride; 34 channels are
+    not a multiple of 4, so the input is staged element by element."""
+    big = W.normal(50, (400, 40))
+    x = np.ascontiguousarray(big[:, :C])
+    w = W.normal(51, (64, C, 3), 0.0, 0.1)
+    b = W.normal(52, (64,), 0.0, 0.1)
+    wts = cbx.Conv1dWeights(dev(w))
+    y = cbx.conv1d(dev(big)[:, :C], wts, 1, 1, 1, cbx.CONV_PRO_LEAKY_RELU, None, None, 0.1, dev(b))
+    check(oracle, host(y), x, w, 1, 1, 1, oracle.CONV_PRO_LEAKY, None, None, 0.1, b, None, f"strided rows C{C}")
+    wts.close()
+
+
+def test_hift_stage_shape(cbx, oracle):
+    """A stage-2 ResBlock conv at full length: 64 channels, 24000 frames,
+    K 11, dilation 5 (the oracle takes a few seconds)."""
+    x, w, al, ai, b, r, sl = case(oracle, 64, 24000, 64, 11, 1, 25, 5, oracle.CONV_PRO_SNAKE, seed=60)
+    got = run(cbx, x, w, 1, 25, 5, cbx.CONV_PRO_SNAKE, al, ai, sl, b, r)
+    check(oracle, got, x, w, 1, 25, 5, oracle.CONV_PRO_SNAKE, al, ai, sl, b, r, "64x24000 K11 d5")
+
+
+def test_errors(cbx):
+    L = cbx.load()
+    w = torch.zeros((16, 32, 3), device="cuda")
+    wts = cbx.Conv1dWeights(w)
+    d = lambda t: ctypes.byref(cbx.desc(t))  # noqa: E731
+    x = torch.zeros((100, 32), device="cuda")
+    y = torch.zeros((100, 16), device="cuda")
+    ok = L.cbx_conv1d(d(x), wts.handle, 1, 1, 1, 0, None, None, 0.0, None, None, d(y), None)
+    assert ok == cbx.OK, cbx.last_error()
+    bad_y = torch.zeros((99, 16), device="cuda")
+    assert L.cbx_conv1d(d(x), wts.handle, 1, 1, 1, 0, None, None, 0.0, None, None, d(bad_y), None) == \
+        cbx.ERR_INVALID_ARG
+    assert L.cbx_conv1d(d(x), wts.handle, 1, 1, 1, cbx.CONV_PRO_SNAKE, None, None, 0.0, None, None, d(y), None) == \
+        cbx.ERR_INVALID_ARG
+    x16 = torch.zeros((100, 16), device="cuda")
+    assert L.cbx_conv1d(d(x16), wts.handle, 1, 1, 1, 0, None, None, 0.0, None, None, d(y), None) == \
+        cbx.ERR_INVALID_ARG
+    # y overlapping x
+    xy = torch.zeros((100, 32), device="cuda")
+    assert L.cbx_conv1d(d(xy), wts.handle, 1, 1, 1, 0, None, None, 0.0, None, None, d(xy[:, :16]), None) == \
+        cbx.ERR_INVALID_ARG
+    assert L.cbx_conv1d(d(x), None, 1, 1, 1, 0, None, None, 0.0, None, None, d(y), None) == cbx.ERR_INVALID_ARG
+    assert L.cbx_conv1d(d(x), wts.handle, 0, 1, 1, 0, None, None, 0.0, None, None, d(y), None) == \
+        cbx.ERR_INVALID_ARG
+    wts.close()

@@ -473,3 +473,62 @@ def test_causal_attention_matches_reference_text(oracle):
     y1 = oracle.scale_diag_mask_soft_max(q, 0.125, 49)
     assert_bitexact(y1, oracle.scale_diag_mask_soft_max(q, 0.125, -1), "n_past masks nothing")
     assert np.max(np.abs(y1 - _softmax64(q * np.float32(0.125)))) < 4e-7
+
+
+# ---- conv1d (HiFT conv_1d_f32 with the fused prologue) ---------------------------
+
+def _conv_brute(xh, wh, stride, pad, dil):
+    """float64 brute force over f16-rounded operands: x [B, T, C], w [Co, C, K]."""
+    B, T, C = xh.shape
+    Co, _, K = wh.shape
+    T_out = (T + 2 * pad - dil * (K - 1) - 1) // stride + 1
+    out = np.zeros((B, T_out, Co))
+    for t in range(T_out):
+        for k in range(K):
+            ti = t * stride + k * dil - pad
+            if 0 <= ti < T:
+                out[:, t, :] += xh[:, ti, :] @ wh[:, :, k].T
+    return out
+
+
+@pytest.mark.parametrize("stride,pad,dil", [(1, 2, 1), (1, 10, 5), (2, 3, 1), (15, 7, 1), (3, 0, 2)])
+def test_conv1d_matches_brute_force(oracle, stride, pad, dil):
+    """im2col semantics (tap k reads time t*stride + k*dil - pad, zero
+    outside), f16 operands, exact products: against float64 brute force."""
+    rng = np.random.default_rng(stride * 10 + dil)
+    x = rng.standard_normal((2, 61, 12)).astype(np.float32)
+    w = rng.standard_normal((8, 12, 5)).astype(np.float32)
+    b = rng.standard_normal(8).astype(np.float32)
+    got = oracle.conv1d(x, w, stride, pad, dil, bias=b)
+    ref = _conv_brute(x.astype(np.float16).astype(np.float64), w.astype(np.float16).astype(np.float64), stride, pad,
+                      dil)
+    assert got.shape == ref.shape
+    assert np.array_equal(got, (ref.astype(np.float32) + b).astype(np.float32))
+
+
+def test_conv1d_identity_and_prologues(oracle):
+    """K = 1 with the identity weight returns f16(pro(x)) exactly; the snake
+    and leaky prologues equal the oracle's own snake / leaky_relu ops; the
+    residual is added last (ggml_add(x, h))."""
+    rng = np.random.default_rng(3)
+    C = 16
+    x = (rng.standard_normal((1, 40, C)) * 3).astype(np.float32)
+    eye = np.eye(C, dtype=np.float32)[:, :, None]
+    f16 = lambda a: a.astype(np.float16).astype(np.float32)  # noqa: E731
+    assert np.array_equal(oracle.conv1d(x, eye), f16(x))
+    a = rng.uniform(0.5, 1.5, C).astype(np.float32)
+    ai = (np.float32(1) / (a + np.float32(1e-9))).astype(np.float32)
+    assert np.array_equal(oracle.conv1d(x, eye, prologue=oracle.CONV_PRO_SNAKE, alpha=a, alpha_inv=ai),
+                          f16(oracle.snake(x, a, ai)))
+    assert np.array_equal(oracle.conv1d(x, eye, prologue=oracle.CONV_PRO_LEAKY, slope=0.1),
+                          f16(oracle.leaky_relu(x, 0.1)))
+    r = rng.standard_normal((1, 40, C)).astype(np.float32)
+    bias = rng.standard_normal(C).astype(np.float32)
+    assert np.array_equal(oracle.conv1d(x, eye, bias=bias, res=r), (r + (f16(x) + bias)).astype(np.float32))
+
+
+def test_conv1d_f16_weights_equal_rounded_f32(oracle):
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((30, 8)).astype(np.float32)
+    w = rng.standard_normal((4, 8, 3)).astype(np.float32)
+    assert np.array_equal(oracle.conv1d(x, w, pad=1), oracle.conv1d(x, w.astype(np.float16), pad=1))
