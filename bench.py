@@ -549,6 +549,56 @@ def bench_t3_block(C, W, torch, reps=300):
     return dict(out, buffer_sets=n_sets)
 
 
+PEAK_MFMA_F16_TFLOPS = 2500.0
+
+
+def bench_hift_conv(C, W, torch, reps=60):
+    """HiFT ResBlock convs (hift_vocoder.cpp:119-138) at the vocoder stage
+    shapes [1,256,6000], [1,128,48000], [1,64,120000]: snake -> conv1d
+    (K 11, dilation 5) + bias, snake -> conv1d (K 3, dilation 1) + bias + x,
+    and one whole sublayer (snake -> conv K 11 d 5 -> snake -> conv K 11 d 1
+    -> + x, two launches).  f16 operands, f32 accumulation on the matrix
+    cores; algorithmic FLOPs 2*C_in*C_out*K*T_out per conv."""
+    d = dev_of(torch)
+    L = C.load()
+    out = {}
+    for (Ch, T) in ((256, 6000), (128, 48000), (64, 120000)):
+        x = d(W.normal(W.seed_of(8, Ch), (T, Ch)))
+        a, ai = (d(v) for v in W.snake_alpha(Ch, 3))
+        bias = d(W.normal(W.seed_of(8, Ch + 1), (Ch,), 0.0, 0.1))
+        ws = {K: C.Conv1dWeights(d(W.normal(W.seed_of(8, Ch + K), (Ch, Ch, K), 0.0, 1.0 / np.sqrt(Ch * K))))
+              for K in (3, 11)}
+        h = torch.empty_like(x)
+        y = torch.empty_like(x)
+        R = {k: C.ctypes.byref(C.desc(v)) for k, v in dict(x=x, a=a, ai=ai, b=bias, h=h, y=y).items()}
+        res = {}
+
+        def conv(K, dil, src, dst, residual):
+            pad = (K - 1) // 2 * dil
+            return lambda s: check_rc(C, L.cbx_conv1d(R[src], ws[K].handle, 1, pad, dil, C.CONV_PRO_SNAKE, R["a"],
+                                                      R["ai"], 0.0, R["b"], R["x"] if residual else None, R[dst], s))
+        for name, K, dil, residual in (("k11_d5", 11, 5, False), ("k3_d1_residual", 3, 1, True)):
+            fn = conv(K, dil, "x", "y", residual)
+            fn(cur_stream(torch))
+            us = per_launch_ms(torch, [fn], reps) * 1000.0
+            flops = 2.0 * Ch * Ch * K * T
+            nbytes = 4 * T * Ch * (3 if residual else 2)
+            res[name] = {"us": us, "TFLOPs": flops / (us * 1e-6) / 1e12,
+                         "pct_of_mfma_f16_peak": 100.0 * flops / (us * 1e-6) / 1e12 / PEAK_MFMA_F16_TFLOPS,
+                         "GBps": nbytes / (us * 1e-6) / 1e9}
+        c1, c2 = conv(11, 5, "x", "h", False), conv(11, 1, "h", "y", True)
+        sub = lambda s: (c1(s), c2(s))  # noqa: E731
+        sub(cur_stream(torch))
+        us = per_launch_ms(torch, [sub], reps) * 1000.0
+        flops = 2 * 2.0 * Ch * Ch * 11 * T
+        res["sublayer_k11_d5"] = {"us": us, "TFLOPs": flops / (us * 1e-6) / 1e12, "launches": 2}
+        for wt in ws.values():
+            wt.close()
+        out[f"{Ch}x{T}"] = res
+        del x, h, y
+    return out
+
+
 def bench_hift(C, W, torch, quick=False):
     """HiFT vocoder activations: Snake (channel innermost as the reference
     lays it out, and time innermost) and LeakyReLU(0.1) on every upsample
@@ -674,6 +724,12 @@ def traffic_probe(C, W, torch):
                                           r["ya"], s))
     torch.cuda.synchronize()
     cache.close()
+    xc = W.normal(W.seed_of(8, 64), (2000, 64))
+    wc = W.normal(W.seed_of(8, 75), (64, 64, 11), 0.0, 0.04)
+    ac, aic = W.snake_alpha(64, 3)
+    reps, el = _timed(lambda: O.conv1d(xc, wc, 1, 25, 5, O.CONV_PRO_SNAKE, ac, aic, nth=nth), seconds)
+    out["hift_conv_64x2000_k11_d5_GFLOPs"] = 2.0 * 64 * 64 * 11 * 2000 * reps / el / 1e9
+
     blk = W.t3_block_inputs()
     N, D, F = W.N_PREFILL, W.D_MODEL, W.D_FF
     blk_sets = []
@@ -848,6 +904,8 @@ def main():
         details["attention_softmax"] = bench_softmax(C, W, torch)
         log("t3 block")
         details["t3_block_elementwise"] = bench_t3_block(C, W, torch)
+        log("hift conv")
+        details["hift_resblock_conv"] = bench_hift_conv(C, W, torch)
     k_ms = res["kernel_ms"]["gelu"]
     k_bytes = res["kernel_bytes"]["gelu"]
     achieved = k_bytes / (k_ms * 1e-3) / 1e9

@@ -12,14 +12,15 @@
 // v_mfma_f32_32x32x16_f16 products summed in f32, then + bias, then + res.
 //
 // GEMM view: output time t (M) x output channel co (N), reduced over input
-// channel ci and tap k (K dimension).  A workgroup owns BT times x BC
-// channels.  Per chunk of 32 input channels it stages one window of
-// (BT-1)*stride + (K-1)*dilation + 1 input rows -- every tap's rows are
-// shifted views of it, so each input element is loaded and activated once
-// per chunk -- then runs, for every tap, the MFMAs of both 16-channel
-// halves.  A fragments (8 f16 of one row) come from LDS, B fragments (8 f16
-// of one output channel's weights) straight from the [co][k][ci] f16 weight
-// copy (L2-resident), the next tap's loaded while this tap's MFMAs run.
+// channel ci and tap k.  A workgroup owns BT times x BC channels.  It stages
+// the activated f16 input window -- (BT-1)*stride + (K-1)*dilation + 1 rows
+// of all input channels (of a chunk of them when they do not fit the
+// 160 KiB of LDS) -- once; every tap's A rows are shifted views of it, so
+// each input element is loaded and activated once per workgroup.  Then each
+// wave runs K * C_in/16 steps, each MT x NT MFMAs: A fragments (8 f16 of one
+// window row) from LDS, B fragments from the prepared weights, whose
+// fragment-major layout makes each one a contiguous KiB, read PF steps
+// ahead into a register ring so the L2 latency hides under the MFMAs.
 //
 // Fragment layout of v_mfma_f32_32x32x16_f16 (checked on the device):
 // lane l holds A[l % 32][8*(l/32) + j] and B[8*(l/32) + j][l % 32], j < 8;
@@ -33,20 +34,22 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int KC = 32;          // input channels per staged chunk
-constexpr int RS = KC + 8;      // LDS row stride in halves: 80 bytes, conflict-free 16-byte reads
-constexpr int kThreads = 256;   // 4 waves
+constexpr int kBlk = 16;              // input channels per MFMA step (the K of one MFMA)
+constexpr int kChanAlign = 32;        // input channels are padded to this
+constexpr size_t kLdsMax = 160 * 1024;
 
 struct ConvArgs {
     const char* x;              // input row (time) t of batch b at x + b*x_nb2 + t*x_nb1
-    const _Float16* w;          // [c_out_pad][k][c_in_pad]
+    const _Float16* w;          // fragment-major: [c_out_pad/32][k][c_in_pad/16][64 lanes][8]
     const float* alpha;         // snake alpha (c_in)
     const float* alpha_inv;     // snake alpha_inv (c_in)
     const float* bias;          // (c_out) or null
     const char* res;            // (c_out, t_out, B) or null
     char* y;
     int64_t x_nb1, x_nb2, y_nb1, y_nb2, r_nb1, r_nb2;
-    int32_t c_in, c_in_pad, c_out, k, t_in, t_out, stride, pad, dil, win;
+    int32_t c_in, c_in_pad, c_out, k, t_in, t_out, stride, pad, dil;
+    int32_t win;                // window rows
+    int32_t kch;                // input channels staged per chunk (a multiple of 32)
     float slope;
 };
 
@@ -67,12 +70,15 @@ __device__ __forceinline__ float prologue(float v, float a, float ai, float slop
     }
 }
 
-// WM x WN waves, each computing (MT*32 times) x (NT*32 channels).  VEC: c_in
-// % 4 == 0 and 16-byte aligned rows (one float4 per 4 channels).
-template <int PRO, int MT, int NT, int WM, int WN, bool VEC>
-__global__ __launch_bounds__(kThreads) void k_conv1d(ConvArgs a) {
-    extern __shared__ _Float16 win[];   // [a.win][RS]
-    constexpr int BT = WM * MT * 32, BC = WN * NT * 32;
+// WM x WN waves, each computing (MT*32 times) x (NT*32 output channels).
+// VEC: c_in % 4 == 0 and 16-byte aligned rows (one float4 per 4 channels).
+// PF: depth of the B fragment ring; it divides every chunk's step count, so
+// the step loop has no guard and its loads no condition, and the compiler
+// waits for exactly the fragment each step uses.
+template <int PRO, int MT, int NT, int WM, int WN, bool VEC, int PF>
+__global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
+    extern __shared__ _Float16 lds[];   // [a.win][a.kch + 8], then alpha and alpha_inv of a chunk (snake)
+    constexpr int BT = WM * MT * 32, BC = WN * NT * 32, NTH = 64 * WM * WN;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
@@ -81,6 +87,8 @@ __global__ __launch_bounds__(kThreads) void k_conv1d(ConvArgs a) {
     const char* xb = a.x + static_cast<int64_t>(blockIdx.z) * a.x_nb2;
     const int base_t = t0 * a.stride - a.pad;   // input time of window row 0
     const int lrow = lane & 31, lk = 8 * (lane >> 5);
+    const int cs = a.kch + 8;                   // LDS row stride (halves): conflict-free 16-byte reads
+    const int nblk = a.c_in_pad / kBlk;         // 16-channel blocks of the weights
 
     floatx16 acc[MT][NT];
 #pragma unroll
@@ -91,92 +99,117 @@ __global__ __launch_bounds__(kThreads) void k_conv1d(ConvArgs a) {
             for (int r = 0; r < 16; r++) acc[mt][nt][r] = 0.0f;
         }
     }
-    // this lane's weight row of each of its NT output-channel fragments
-    const _Float16* wrow[NT];
+    // fragment (co tile, k = 0, block 0) of each of the lane's NT output tiles
+    const _Float16* wf[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
-        const int co = co0 + (wn * NT + nt) * 32 + lrow;
-        wrow[nt] = a.w + static_cast<int64_t>(co) * a.k * a.c_in_pad + lk;
+        const int co_t = (co0 >> 5) + wn * NT + nt;
+        wf[nt] = a.w + static_cast<int64_t>(co_t) * a.k * nblk * 512 + lane * 8;
     }
 
-    for (int ci0 = 0; ci0 < a.c_in; ci0 += KC) {
-        __syncthreads();   // the previous chunk's fragments have been read
-        // stage pro(x) for rows [base_t, base_t + win) x channels [ci0, ci0 + 32) as f16
-        for (int e = tid; e < a.win * 8; e += kThreads) {
-            const int r = e >> 3, cg = (e & 7) * 4;
-            const int ti = base_t + r;
-            const int ci = ci0 + cg;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (ti >= 0 && ti < a.t_in) {
-                const float* src = reinterpret_cast<const float*>(xb + static_cast<int64_t>(ti) * a.x_nb1) + ci;
-                if constexpr (VEC) {
-                    if (ci < a.c_in) v = *reinterpret_cast<const float4*>(src);
-                } else {
-                    v.x = ci + 0 < a.c_in ? src[0] : 0.0f;
-                    v.y = ci + 1 < a.c_in ? src[1] : 0.0f;
-                    v.z = ci + 2 < a.c_in ? src[2] : 0.0f;
-                    v.w = ci + 3 < a.c_in ? src[3] : 0.0f;
-                }
-                if constexpr (PRO != PRO_NONE) {
-                    // padding channels (ci >= c_in) stay 0: snake(0) = leaky(0) = 0
+    for (int ci0 = 0; ci0 < a.c_in; ci0 += a.kch) {
+        const int kch = a.c_in - ci0 < a.kch ? ((a.c_in - ci0 + kChanAlign - 1) / kChanAlign) * kChanAlign : a.kch;
+        if (ci0 > 0) __syncthreads();   // the previous chunk's fragments have been read
+        // snake: this chunk's alpha and alpha_inv into LDS, so the activation
+        // below reads them without a global round trip per element
+        float* sal = reinterpret_cast<float*>(lds + a.win * cs);
+        if constexpr (PRO == PRO_SNAKE) {
+            for (int c = tid; c < kch; c += NTH) {
+                const int cc = ci0 + c < a.c_in ? ci0 + c : 0;
+                sal[c] = a.alpha[cc];
+                sal[a.kch + c] = a.alpha_inv[cc];
+            }
+            __syncthreads();
+        }
+        // stage pro(x) rows [base_t, base_t + win) x channels [ci0, ci0 + kch) as f16,
+        // kStage 4-channel groups in flight per lane
+        constexpr int kStage = 16;
+        const int gpr = kch >> 2;                 // groups per row
+        const int n_el = a.win * gpr;
+        for (int e0 = tid; e0 < n_el; e0 += kStage * NTH) {
+            float4 v[kStage];
 #pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const int c = ci + q < a.c_in ? ci + q : 0;
-                        const float al = PRO == PRO_SNAKE ? a.alpha[c] : 0.0f;
-                        const float ai = PRO == PRO_SNAKE ? a.alpha_inv[c] : 0.0f;
-                        set(v, q, prologue<PRO>(get(v, q), al, ai, a.slope));
+            for (int i = 0; i < kStage; i++) {
+                const int e = e0 + i * NTH;
+                v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (e < n_el) {
+                    const int r = e / gpr, ci = ci0 + (e - r * gpr) * 4;
+                    const int ti = base_t + r;
+                    if (ti >= 0 && ti < a.t_in) {
+                        const float* src =
+                            reinterpret_cast<const float*>(xb + static_cast<int64_t>(ti) * a.x_nb1) + ci;
+                        if constexpr (VEC) {
+                            if (ci < a.c_in) v[i] = *reinterpret_cast<const float4*>(src);
+                        } else {
+                            v[i].x = ci + 0 < a.c_in ? src[0] : 0.0f;
+                            v[i].y = ci + 1 < a.c_in ? src[1] : 0.0f;
+                            v[i].z = ci + 2 < a.c_in ? src[2] : 0.0f;
+                            v[i].w = ci + 3 < a.c_in ? src[3] : 0.0f;
+                        }
                     }
                 }
             }
-            half4 hv;
-            hv[0] = static_cast<_Float16>(v.x);
-            hv[1] = static_cast<_Float16>(v.y);
-            hv[2] = static_cast<_Float16>(v.z);
-            hv[3] = static_cast<_Float16>(v.w);
-            *reinterpret_cast<half4*>(win + r * RS + cg) = hv;
+#pragma unroll
+            for (int i = 0; i < kStage; i++) {
+                const int e = e0 + i * NTH;
+                if (e >= n_el) continue;
+                const int r = e / gpr, cg = (e - r * gpr) * 4;
+                float4 t = v[i];
+                if constexpr (PRO != PRO_NONE) {
+                    // pro(0) = 0: padding rows and channels stay 0
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float al = PRO == PRO_SNAKE ? sal[cg + q] : 0.0f;
+                        const float ai = PRO == PRO_SNAKE ? sal[a.kch + cg + q] : 0.0f;
+                        set(t, q, prologue<PRO>(get(t, q), al, ai, a.slope));
+                    }
+                }
+                half4 hv;
+                hv[0] = static_cast<_Float16>(t.x);
+                hv[1] = static_cast<_Float16>(t.y);
+                hv[2] = static_cast<_Float16>(t.z);
+                hv[3] = static_cast<_Float16>(t.w);
+                *reinterpret_cast<half4*>(lds + r * cs + cg) = hv;
+            }
         }
         __syncthreads();
 
-        half8 bcur[2][NT], bnext[2][NT];
+        // steps s = k * nb + cb over this chunk's 16-channel blocks
+        const int nb = kch / kBlk, cb0 = ci0 / kBlk;
+        const int n_steps = a.k * nb;
+        auto bfrag = [&](int nt, int s) {
+            const int k = s / nb, cb = s - k * nb;
+            return *reinterpret_cast<const half8*>(wf[nt] + (static_cast<int64_t>(k) * nblk + cb0 + cb) * 512);
+        };
+        half8 ring[PF][NT];
 #pragma unroll
-        for (int hh = 0; hh < 2; hh++) {
+        for (int p = 0; p < PF; p++) {
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                bcur[hh][nt] = *reinterpret_cast<const half8*>(wrow[nt] + ci0 + hh * 16);
-            }
+            for (int nt = 0; nt < NT; nt++) ring[p][nt] = bfrag(nt, p);
         }
-        for (int k = 0; k < a.k; k++) {
-            // next tap's weights (the last tap re-reads its own: in bounds, unused)
-            const int kn = k + 1 < a.k ? k + 1 : k;
+        for (int s0 = 0; s0 < n_steps; s0 += PF) {
 #pragma unroll
-            for (int hh = 0; hh < 2; hh++) {
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++) {
-                    bnext[hh][nt] = *reinterpret_cast<const half8*>(wrow[nt] + static_cast<int64_t>(kn) * a.c_in_pad +
-                                                                    ci0 + hh * 16);
-                }
-            }
-#pragma unroll
-            for (int hh = 0; hh < 2; hh++) {
+            for (int p = 0; p < PF; p++) {
+                const int s = s0 + p;
+                const int k = s / nb, cb = s - k * nb;
                 half8 av[MT];
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
                     const int row = ((wm * MT + mt) * 32 + lrow) * a.stride + k * a.dil;
-                    av[mt] = *reinterpret_cast<const half8*>(win + row * RS + hh * 16 + lk);
+                    av[mt] = *reinterpret_cast<const half8*>(lds + row * cs + cb * kBlk + lk);
                 }
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
 #pragma unroll
                     for (int nt = 0; nt < NT; nt++) {
-                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[mt], bcur[hh][nt], acc[mt][nt], 0, 0,
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[mt], ring[p][nt], acc[mt][nt], 0, 0,
                                                                              0);
                     }
                 }
-            }
+                // the fragment PF steps ahead (past the end: this step's again, unused)
+                const int sn = s + PF < n_steps ? s + PF : s;
 #pragma unroll
-            for (int hh = 0; hh < 2; hh++) {
-#pragma unroll
-                for (int nt = 0; nt < NT; nt++) bcur[hh][nt] = bnext[hh][nt];
+                for (int nt = 0; nt < NT; nt++) ring[p][nt] = bfrag(nt, sn);
             }
         }
     }
@@ -204,18 +237,24 @@ __global__ __launch_bounds__(kThreads) void k_conv1d(ConvArgs a) {
     }
 }
 
-// [c_out_pad][k][c_in_pad] f16 copy of a ggml (K, C_in, C_out) weight, zero
-// padded; the f16 rounding is mul_mat's conversion of its F32 operand.
+// Fragment-major f16 copy of a ggml (K, C_in, C_out) weight, zero padded:
+// fragment (co tile, k, 16-channel block) is 64 lanes x 8 halves, lane l
+// holding w[co_tile*32 + l%32][block*16 + 8*(l/32) + j][k] -- one MFMA B
+// operand, one contiguous KiB.  The f16 rounding is mul_mat's conversion of
+// its F32 operand.
 template <bool F16>
 __global__ __launch_bounds__(256) void k_conv_weights(const char* w, int64_t nb0, int64_t nb1, int64_t nb2, int32_t K,
-                                                      int32_t c_in, int32_t c_out, int32_t c_in_pad, int64_t total,
+                                                      int32_t c_in, int32_t c_out, int32_t nblk, int64_t total,
                                                       _Float16* out) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (i >= total) return;
-    const int32_t ci = static_cast<int32_t>(i % c_in_pad);
-    const int64_t q = i / c_in_pad;
+    const int64_t frag = i >> 9;
+    const int32_t lane = static_cast<int32_t>((i >> 3) & 63), j = static_cast<int32_t>(i & 7);
+    const int32_t cb = static_cast<int32_t>(frag % nblk);
+    const int64_t q = frag / nblk;
     const int32_t k = static_cast<int32_t>(q % K);
-    const int32_t co = static_cast<int32_t>(q / K);
+    const int32_t co = static_cast<int32_t>(q / K) * 32 + (lane & 31);
+    const int32_t ci = cb * 16 + 8 * (lane >> 5) + j;
     _Float16 v = static_cast<_Float16>(0.0f);
     if (ci < c_in && co < c_out) {
         const char* p = w + k * nb0 + ci * nb1 + co * nb2;
@@ -229,21 +268,44 @@ struct Tile {
     int mt, nt, wm, wn;
     int bt() const { return wm * mt * 32; }
     int bc() const { return wn * nt * 32; }
+    int threads() const { return 64 * wm * wn; }
 };
 
-template <int PRO, int MT, int NT, int WM, int WN>
-void conv_go(bool vec, dim3 grid, size_t lds, hipStream_t s, const ConvArgs& a) {
-    if (vec) hipLaunchKernelGGL((k_conv1d<PRO, MT, NT, WM, WN, true>), grid, dim3(kThreads), lds, s, a);
-    else hipLaunchKernelGGL((k_conv1d<PRO, MT, NT, WM, WN, false>), grid, dim3(kThreads), lds, s, a);
+template <typename K>
+void conv_launch(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, const ConvArgs& a) {
+    // windows past 64 KiB use the larger LDS of gfx950 (160 KiB per workgroup)
+    if (lds > 64 * 1024) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(lds));
+    }
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, a);
 }
 
-template <int PRO>
-void conv_tile(const Tile& t, bool vec, dim3 grid, size_t lds, hipStream_t s, const ConvArgs& a) {
-    if (t.wn == 2) conv_go<PRO, 2, 2, 2, 2>(vec, grid, lds, s, a);        // 128 x 128
-    else if (t.mt == 2) conv_go<PRO, 2, 2, 4, 1>(vec, grid, lds, s, a);   // 256 x 64
-    else if (t.wm == 1) conv_go<PRO, 1, 1, 1, 4>(vec, grid, lds, s, a);   // 32 x 128
-    else conv_go<PRO, 1, 1, 4, 1>(vec, grid, lds, s, a);                  // 128 x 32
+template <int PRO, int MT, int NT, int WM, int WN>
+void conv_go(bool vec, bool pf4, dim3 grid, size_t lds, hipStream_t s, const ConvArgs& a) {
+    const dim3 block(64 * WM * WN);
+    if (pf4) {
+        if (vec) conv_launch(k_conv1d<PRO, MT, NT, WM, WN, true, 4>, grid, block, lds, s, a);
+        else conv_launch(k_conv1d<PRO, MT, NT, WM, WN, false, 4>, grid, block, lds, s, a);
+    } else {
+        if (vec) conv_launch(k_conv1d<PRO, MT, NT, WM, WN, true, 2>, grid, block, lds, s, a);
+        else conv_launch(k_conv1d<PRO, MT, NT, WM, WN, false, 2>, grid, block, lds, s, a);
+    }
 }
+
+// the tile shapes below, by index
+template <int PRO>
+void conv_tile(int t, bool vec, bool pf4, dim3 grid, size_t lds, hipStream_t s, const ConvArgs& a) {
+    switch (t) {
+        case 0: conv_go<PRO, 4, 2, 2, 1>(vec, pf4, grid, lds, s, a); break;   // 256 x 64, 2 waves
+        case 1: conv_go<PRO, 4, 2, 1, 2>(vec, pf4, grid, lds, s, a); break;   // 128 x 128, 2 waves
+        case 2: conv_go<PRO, 2, 2, 1, 2>(vec, pf4, grid, lds, s, a); break;   // 64 x 128, 2 waves
+        case 3: conv_go<PRO, 2, 2, 1, 1>(vec, pf4, grid, lds, s, a); break;   // 64 x 64, 1 wave
+        default: conv_go<PRO, 4, 1, 2, 1>(vec, pf4, grid, lds, s, a); break;  // 256 x 32, 2 waves
+    }
+}
+
+constexpr Tile kTiles[5] = {{4, 2, 2, 1}, {4, 2, 1, 2}, {2, 2, 1, 2}, {2, 2, 1, 1}, {4, 1, 2, 1}};
 
 }  // namespace
 
@@ -251,25 +313,25 @@ void conv_tile(const Tile& t, bool vec, dim3 grid, size_t lds, hipStream_t s, co
 constexpr int kConvCoPad = 128;
 
 int conv1d_weights_layout(int64_t c_in, int64_t c_out, int64_t* c_in_pad, int64_t* c_out_pad) {
-    *c_in_pad = cdiv(c_in, KC) * KC;
+    *c_in_pad = cdiv(c_in, kChanAlign) * kChanAlign;
     *c_out_pad = cdiv(c_out, kConvCoPad) * kConvCoPad;
     return CBX_OK;
 }
 
 int launch_conv1d_weights(const cbx_tensor* w, _Float16* out, int64_t c_in_pad, int64_t c_out_pad, hipStream_t s) {
-    const int64_t total = c_out_pad * w->ne[0] * c_in_pad;
+    const int64_t total = c_out_pad * w->ne[0] * c_in_pad;   // = (c_out_pad/32) * K * (c_in_pad/16) * 512
     const dim3 grid(static_cast<unsigned>(cdiv(total, 256)));
     const char* p = static_cast<const char*>(w->data);
     const int64_t nb0 = static_cast<int64_t>(w->nb[0]), nb1 = static_cast<int64_t>(w->nb[1]),
                   nb2 = static_cast<int64_t>(w->nb[2]);
     const int32_t K = static_cast<int32_t>(w->ne[0]), ci = static_cast<int32_t>(w->ne[1]),
                   co = static_cast<int32_t>(w->ne[2]);
+    const int32_t nblk = static_cast<int32_t>(c_in_pad / kBlk);
     if (w->type == CBX_TYPE_F16) {
-        hipLaunchKernelGGL((k_conv_weights<true>), grid, dim3(256), 0, s, p, nb0, nb1, nb2, K, ci, co,
-                           static_cast<int32_t>(c_in_pad), total, out);
+        hipLaunchKernelGGL((k_conv_weights<true>), grid, dim3(256), 0, s, p, nb0, nb1, nb2, K, ci, co, nblk, total, out);
     } else {
-        hipLaunchKernelGGL((k_conv_weights<false>), grid, dim3(256), 0, s, p, nb0, nb1, nb2, K, ci, co,
-                           static_cast<int32_t>(c_in_pad), total, out);
+        hipLaunchKernelGGL((k_conv_weights<false>), grid, dim3(256), 0, s, p, nb0, nb1, nb2, K, ci, co, nblk, total,
+                           out);
     }
     return check_launch("conv1d_weights");
 }
@@ -302,28 +364,39 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     a.dil = dil;
     a.slope = slope;
     const int64_t batch = x->ne[2];
-    // tile: 128x128 when it gives >= 2 workgroups per CU, else 32x128 for
-    // wide outputs; 256x64 / 128x32 for narrow ones
-    const Tile big{2, 2, 2, 2}, tall{2, 2, 4, 1}, small{1, 1, 1, 4}, narrow{1, 1, 4, 1};
     auto n_wg = [&](const Tile& t) { return cdiv(a.t_out, t.bt()) * cdiv(c_out, t.bc()) * batch; };
-    Tile t = c_out <= 32 ? narrow : c_out <= 64 ? tall : (n_wg(big) >= 2 * st->n_cu ? big : small);
-    auto lds_of = [&](const Tile& tt) {
-        return static_cast<size_t>((tt.bt() - 1) * stride + (k - 1) * dil + 1) * RS * sizeof(_Float16);
-    };
-    constexpr size_t kLdsMax = 64 * 1024;
-    if (lds_of(t) > kLdsMax) t = c_out <= 32 ? narrow : small;   // strided convs: shorter windows
-    if (lds_of(t) > kLdsMax) {
-        return set_error(CBX_ERR_UNSUPPORTED, "conv1d: the input window of one tile exceeds 64 KiB of LDS");
+    auto win_of = [&](const Tile& t) { return (t.bt() - 1) * static_cast<int64_t>(stride) + (k - 1) * dil + 1; };
+    // tile: the largest per-wave work that still gives a workgroup per CU
+    int ti;
+    if (c_out <= 32) ti = 4;
+    else if (c_out <= 64) ti = n_wg(kTiles[0]) >= st->n_cu ? 0 : 3;
+    else ti = n_wg(kTiles[1]) >= st->n_cu ? 1 : n_wg(kTiles[2]) >= st->n_cu ? 2 : 3;
+    // the window of at least 32 channels must fit the LDS; strided convs fall back to 64-row tiles
+    auto fits = [&](int64_t w) { return w * (kChanAlign + 8) * 2 + 8 * kChanAlign <= static_cast<int64_t>(kLdsMax); };
+    if (!fits(win_of(kTiles[ti]))) ti = 3;
+    const int64_t win = win_of(kTiles[ti]);
+    if (!fits(win)) {
+        return set_error(CBX_ERR_UNSUPPORTED, "conv1d: one tile's input window exceeds the LDS");
     }
-    a.win = (t.bt() - 1) * stride + static_cast<int32_t>(k - 1) * dil + 1;
+    // channels per chunk: all of them when they fit, else the most that do
+    int64_t kch = (static_cast<int64_t>(kLdsMax) / (win * 2 + 8) - 8) / kChanAlign * kChanAlign;
+    kch = std::min<int64_t>(kch, c_in_pad);
+    a.win = static_cast<int32_t>(win);
+    a.kch = static_cast<int32_t>(kch);
+    const size_t lds = static_cast<size_t>(win) * static_cast<size_t>(kch + 8) * sizeof(_Float16) +
+                       (pro == PRO_SNAKE ? 2 * static_cast<size_t>(kch) * sizeof(float) : 0);
     const bool vec = a.c_in % 4 == 0 && reinterpret_cast<uintptr_t>(a.x) % 16 == 0 && a.x_nb1 % 16 == 0 &&
                      (batch <= 1 || a.x_nb2 % 16 == 0);
+    const Tile& t = kTiles[ti];
     const dim3 grid(static_cast<unsigned>(cdiv(a.t_out, t.bt())), static_cast<unsigned>(cdiv(c_out, t.bc())),
                     static_cast<unsigned>(batch));
+    // every chunk's step count (K * channels / 16) is even; a ring of 4 when all are multiples of 4
+    const int64_t last = c_in_pad - (cdiv(c_in_pad, kch) - 1) * kch;
+    const bool pf4 = (k * (kch / kBlk)) % 4 == 0 && (k * (last / kBlk)) % 4 == 0;
     switch (pro) {
-        case PRO_SNAKE: conv_tile<PRO_SNAKE>(t, vec, grid, lds_of(t), s, a); break;
-        case PRO_LEAKY: conv_tile<PRO_LEAKY>(t, vec, grid, lds_of(t), s, a); break;
-        default: conv_tile<PRO_NONE>(t, vec, grid, lds_of(t), s, a); break;
+        case PRO_SNAKE: conv_tile<PRO_SNAKE>(ti, vec, pf4, grid, lds, s, a); break;
+        case PRO_LEAKY: conv_tile<PRO_LEAKY>(ti, vec, pf4, grid, lds, s, a); break;
+        default: conv_tile<PRO_NONE>(ti, vec, pf4, grid, lds, s, a); break;
     }
     return check_launch("conv1d");
 }
