@@ -596,6 +596,32 @@ def bench_hift_conv(C, W, torch, reps=60):
             wt.close()
         out[f"{Ch}x{T}"] = res
         del x, h, y
+    # the upsamplers, leaky_relu(0.1) -> ConvTranspose1d -> crop -> + bias
+    # (hift_vocoder.cpp:680-687), on the chain from 750 mel frames:
+    # 512x750 -> 256x6000 -> 128x30000 -> 64x90000; algorithmic FLOPs
+    # 2*C_in*C_out*K*T_in
+    ups = {}
+    for (Ci, Co, s, K, T) in ((512, 256, 8, 16, 750), (256, 128, 5, 11, 6000), (128, 64, 3, 7, 30000)):
+        pad = (K - s) // 2
+        x = d(W.normal(W.seed_of(8, 1000 + Ci), (T, Ci)))
+        bias = d(W.normal(W.seed_of(8, 1001 + Ci), (Co,), 0.0, 0.1))
+        wt = C.Conv1dWeights(d(W.normal(W.seed_of(8, 1002 + Ci), (Ci, Co, K), 0.0, 1.0 / np.sqrt(Ci * K / s))),
+                             transpose_stride=s)
+        T_out = (T - 1) * s + K - 2 * pad
+        y = torch.empty((T_out, Co), dtype=torch.float32, device="cuda")
+        R = {k: C.ctypes.byref(C.desc(v)) for k, v in dict(x=x, b=bias, y=y).items()}
+        fn = lambda st: check_rc(C, L.cbx_conv_transpose1d(R["x"], wt.handle, pad, C.CONV_PRO_LEAKY_RELU, None,  # noqa: E731
+                                                           None, 0.1, R["b"], R["y"], st))
+        fn(cur_stream(torch))
+        us = per_launch_ms(torch, [fn], reps) * 1000.0
+        flops = 2.0 * Ci * Co * K * T
+        ups[f"{Ci}x{T}_to_{Co}x{T_out}"] = {
+            "us": us, "TFLOPs": flops / (us * 1e-6) / 1e12,
+            "pct_of_mfma_f16_peak": 100.0 * flops / (us * 1e-6) / 1e12 / PEAK_MFMA_F16_TFLOPS,
+            "GBps": 4.0 * (T * Ci + T_out * Co) / (us * 1e-6) / 1e9}
+        wt.close()
+        del x, y
+    out["upsample"] = ups
     return out
 
 

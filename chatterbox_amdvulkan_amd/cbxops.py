@@ -171,6 +171,8 @@ def load() -> ctypes.CDLL:
         "cbx_conv1d_weights_create": (i, [P, vp, ctypes.POINTER(vp)]),
         "cbx_conv1d_weights_destroy": (None, [vp]),
         "cbx_conv1d": (i, [P, vp, i, i, i, i, P, P, f, P, P, P, vp]),
+        "cbx_conv_transpose1d_weights_create": (i, [P, i, vp, ctypes.POINTER(vp)]),
+        "cbx_conv_transpose1d": (i, [P, vp, i, i, P, P, f, P, P, vp]),
         "cbx_run_ops": (i, [ctypes.POINTER(OpStruct), i, vp]),
         "cbx_gguf_open": (i, [ctypes.c_char_p, ctypes.POINTER(vp)]),
         "cbx_gguf_close": (None, [vp]),
@@ -530,14 +532,22 @@ CONV_PRO_NONE, CONV_PRO_SNAKE, CONV_PRO_LEAKY_RELU = 0, 1, 2
 
 class Conv1dWeights:
     """cbx_conv1d_weights: the f16 copy of a conv1d weight, torch [C_out,
-    C_in, K] (ggml ne (K, C_in, C_out)), F32 or F16."""
+    C_in, K] (ggml ne (K, C_in, C_out)), F32 or F16.  With transpose_stride
+    set: a transposed conv's weight, torch [C_in, C_out, K] (ggml ne (K,
+    C_out, C_in)), split into that many phases."""
 
-    def __init__(self, w: torch.Tensor):
+    def __init__(self, w: torch.Tensor, transpose_stride=None):
         _ready(w)
         h = ctypes.c_void_p()
-        _check(load().cbx_conv1d_weights_create(_ref(desc(w)), _stream(), ctypes.byref(h)))
+        if transpose_stride is None:
+            _check(load().cbx_conv1d_weights_create(_ref(desc(w)), _stream(), ctypes.byref(h)))
+            self.c_out, self.c_in, self.k = w.shape
+        else:
+            _check(load().cbx_conv_transpose1d_weights_create(_ref(desc(w)), transpose_stride, _stream(),
+                                                               ctypes.byref(h)))
+            self.c_in, self.c_out, self.k = w.shape
         self.handle = h
-        self.c_out, self.c_in, self.k = w.shape
+        self.stride = transpose_stride
 
     def close(self):
         if self.handle:
@@ -563,6 +573,21 @@ def conv1d(x, weights: Conv1dWeights, stride=1, pad=0, dilation=1, prologue=CONV
     opt = lambda t: _ref(desc(t)) if t is not None else None  # noqa: E731
     _check(load().cbx_conv1d(_ref(desc(x)), weights.handle, stride, pad, dilation, prologue, opt(alpha),
                              opt(alpha_inv), slope, opt(bias), opt(res), _ref(desc(out)), _stream()))
+    return out
+
+
+def conv_transpose1d(x, weights: Conv1dWeights, pad=0, prologue=CONV_PRO_NONE, alpha=None, alpha_inv=None, slope=0.0,
+                     bias=None, out=None):
+    """conv_transpose1d_CT(pro(x)) (+ bias) with `pad` cropped from both
+    ends: x torch [B, T_in, C_in] or [T_in, C_in]; weights made with
+    transpose_stride; returns [.., (T_in - 1) * stride + K - 2 pad, C_out]."""
+    _ready(x)
+    t_out = (x.shape[-2] - 1) * weights.stride + weights.k - 2 * pad
+    if out is None:
+        out = torch.empty(tuple(x.shape[:-2]) + (t_out, weights.c_out), dtype=torch.float32, device=x.device)
+    opt = lambda t: _ref(desc(t)) if t is not None else None  # noqa: E731
+    _check(load().cbx_conv_transpose1d(_ref(desc(x)), weights.handle, pad, prologue, opt(alpha), opt(alpha_inv), slope,
+                                       opt(bias), _ref(desc(out)), _stream()))
     return out
 
 

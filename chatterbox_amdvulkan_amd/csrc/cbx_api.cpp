@@ -155,8 +155,12 @@ static void yarn_cos_sin(float theta_extrap, int64_t i0, const RopeParams& p, fl
 
 struct cbx_conv1d_weights {
     int       device;
-    int64_t   k, c_in, c_out, c_in_pad, c_out_pad;
-    _Float16* data;   // [c_out_pad][k][c_in_pad]
+    int       up;       // 0: conv1d weights; >= 1: transposed conv with this stride
+    int64_t   k;        // the weight's taps
+    int64_t   taps;     // taps per phase as stored (k for conv1d)
+    int64_t   c_in, c_out, c_in_pad, c_out_pad;
+    int64_t   w_ph;     // halves per phase
+    _Float16* data;     // [phase][c_out_pad / 32][taps][c_in_pad / 16][64][8]
 };
 
 struct cbx_rope_cache {
@@ -712,40 +716,44 @@ int cbx_bias_act(int act, const cbx_tensor* x, const cbx_tensor* bias, cbx_tenso
 
 // ---- conv1d -------------------------------------------------------------------
 
-int cbx_conv1d_weights_create(const cbx_tensor* w, cbx_stream stream, cbx_conv1d_weights** out) {
-    const char* what = "cbx_conv1d_weights_create";
+static int conv_weights_create(const cbx_tensor* w, int up, cbx_stream stream, cbx_conv1d_weights** out,
+                               const char* what) {
     clear_error();
-    if (!out) return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d_weights_create: out is NULL");
+    if (!out) return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": out is NULL");
     *out = nullptr;
     int rc;
     DeviceState* st = current_state(&rc);
     if (!st) return rc;
     if ((rc = validate(w, what, "w"))) return rc;
     if (w->type != CBX_TYPE_F32 && w->type != CBX_TYPE_F16) {
-        return set_error(CBX_ERR_UNSUPPORTED, "cbx_conv1d_weights_create: w must be F32 or F16");
+        return set_error(CBX_ERR_UNSUPPORTED, std::string(what) + ": w must be F32 or F16");
     }
     if (w->ne[0] < 1 || w->ne[0] > 64 || w->ne[1] < 1 || w->ne[1] > 8192 || w->ne[2] < 1 || w->ne[2] > 8192 ||
         w->ne[3] != 1) {
-        return set_error(CBX_ERR_INVALID_ARG,
-                         "cbx_conv1d_weights_create: w must be (K <= 64, C_in <= 8192, C_out <= 8192, 1)");
+        return set_error(CBX_ERR_INVALID_ARG, std::string(what) + (up == 0 ? ": w must be (K <= 64, C_in <= 8192, C_out <= 8192, 1)"
+                                                                           : ": w must be (K <= 64, C_out <= 8192, C_in <= 8192, 1)"));
     }
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return set_error(CBX_ERR_HIP, "cbx_conv1d_weights_create: hipGetDevice failed");
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(CBX_ERR_HIP, std::string(what) + ": hipGetDevice failed");
     auto* cw = new cbx_conv1d_weights();
     cw->device = dev;
+    cw->up = up;
     cw->k = w->ne[0];
-    cw->c_in = w->ne[1];
-    cw->c_out = w->ne[2];
+    cw->taps = up == 0 ? cw->k : cdiv(cw->k, static_cast<int64_t>(up));
+    cw->c_in = up == 0 ? w->ne[1] : w->ne[2];
+    cw->c_out = up == 0 ? w->ne[2] : w->ne[1];
     conv1d_weights_layout(cw->c_in, cw->c_out, &cw->c_in_pad, &cw->c_out_pad);
-    const size_t bytes = static_cast<size_t>(cw->c_out_pad * cw->k * cw->c_in_pad) * sizeof(_Float16);
+    cw->w_ph = cw->c_out_pad * cw->taps * cw->c_in_pad;
+    const int64_t n_ph = up == 0 ? 1 : up;
+    const size_t bytes = static_cast<size_t>(n_ph * cw->w_ph) * sizeof(_Float16);
     if (hipMalloc(reinterpret_cast<void**>(&cw->data), bytes) != hipSuccess) {
         delete cw;
-        return set_error(CBX_ERR_HIP, "cbx_conv1d_weights_create: hipMalloc failed");
+        return set_error(CBX_ERR_HIP, std::string(what) + ": hipMalloc failed");
     }
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    rc = launch_conv1d_weights(w, cw->data, cw->c_in_pad, cw->c_out_pad, s);
+    rc = launch_conv1d_weights(w, up, cw->taps, cw->data, cw->c_in_pad, cw->c_out_pad, s);
     if (!rc && hipStreamSynchronize(s) != hipSuccess) {
-        rc = set_error(CBX_ERR_HIP, "cbx_conv1d_weights_create: stream synchronisation failed");
+        rc = set_error(CBX_ERR_HIP, std::string(what) + ": stream synchronisation failed");
     }
     if (rc) {
         hipFree(cw->data);
@@ -754,6 +762,20 @@ int cbx_conv1d_weights_create(const cbx_tensor* w, cbx_stream stream, cbx_conv1d
     }
     *out = cw;
     return CBX_OK;
+}
+
+int cbx_conv1d_weights_create(const cbx_tensor* w, cbx_stream stream, cbx_conv1d_weights** out) {
+    return conv_weights_create(w, 0, stream, out, "cbx_conv1d_weights_create");
+}
+
+int cbx_conv_transpose1d_weights_create(const cbx_tensor* w, int stride, cbx_stream stream,
+                                        cbx_conv1d_weights** out) {
+    if (stride < 1 || stride > 64) {
+        clear_error();
+        if (out) *out = nullptr;
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_conv_transpose1d_weights_create: stride must be 1..64");
+    }
+    return conv_weights_create(w, stride, stream, out, "cbx_conv_transpose1d_weights_create");
 }
 
 void cbx_conv1d_weights_destroy(cbx_conv1d_weights* w) {
@@ -767,6 +789,71 @@ void cbx_conv1d_weights_destroy(cbx_conv1d_weights* w) {
     delete w;
 }
 
+// Checks shared by cbx_conv1d and cbx_conv_transpose1d: the handle's device
+// and kind, x against the weights, y's shape (t_out), bias, res, the snake
+// vectors, and that y does not overlap x.  Sets *empty for an empty y.
+static int check_conv_io(const char* what, const cbx_conv1d_weights* w, bool transposed, int prologue,
+                         const cbx_tensor* x, const cbx_tensor* alpha, const cbx_tensor* alpha_inv,
+                         const cbx_tensor* bias, const cbx_tensor* res, const cbx_tensor* y, int64_t t_out,
+                         const char* t_out_rule, bool* empty) {
+    const std::string f(what);
+    int rc;
+    if (!w) return set_error(CBX_ERR_INVALID_ARG, f + ": weights are NULL");
+    if ((w->up != 0) != transposed) {
+        return set_error(CBX_ERR_INVALID_ARG, f + (transposed ? ": the weights were made for cbx_conv1d"
+                                                              : ": the weights were made for cbx_conv_transpose1d"));
+    }
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev != w->device) {
+        return set_error(CBX_ERR_INVALID_ARG, f + ": the weights belong to another device");
+    }
+    if (y->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, f + ": F32 only");
+    if (y->ne[0] != w->c_out || y->ne[1] != t_out || y->ne[2] != x->ne[2] || y->ne[3] != 1) {
+        return set_error(CBX_ERR_INVALID_ARG, f + ": y must be (C_out, T_out, B, 1), " + t_out_rule);
+    }
+    if (x->ne[1] >= (int64_t{1} << 30) || t_out >= (int64_t{1} << 30) ||
+        x->ne[2] * (transposed ? w->up : 1) >= 65536) {
+        return set_error(CBX_ERR_UNSUPPORTED, f + (transposed ? ": T must be below 2^30 and B * stride below 65536"
+                                                              : ": T must be below 2^30 and B below 65536"));
+    }
+    if (bias) {
+        if ((rc = validate(bias, what, "bias"))) return rc;
+        if (bias->type != CBX_TYPE_F32 || nelements(bias) != w->c_out || !is_contiguous(bias)) {
+            return set_error(CBX_ERR_INVALID_ARG, f + ": bias must be contiguous F32 with C_out elements");
+        }
+    }
+    if (res) {
+        if ((rc = validate(res, what, "res"))) return rc;
+        if (res->type != CBX_TYPE_F32 || !same_shape(res, y)) {
+            return set_error(CBX_ERR_INVALID_ARG, f + ": res must be F32 with y's shape");
+        }
+    }
+    if (prologue == CBX_CONV_PRO_SNAKE) {
+        for (const cbx_tensor* p : {alpha, alpha_inv}) {
+            if ((rc = validate(p, what, p == alpha ? "alpha" : "alpha_inv"))) return rc;
+            if (p->type != CBX_TYPE_F32 || nelements(p) != w->c_in || !is_contiguous(p)) {
+                return set_error(CBX_ERR_INVALID_ARG, f + ": alpha and alpha_inv must be contiguous F32 with C_in elements");
+            }
+        }
+    }
+    *empty = nelements(y) == 0;
+    if (!*empty && overlaps(x, y)) return set_error(CBX_ERR_INVALID_ARG, f + ": y must not overlap x");
+    return CBX_OK;
+}
+
+// x must be F32 (C_in, T_in, B, 1) with the weights' C_in; the prologue known.
+static int check_conv_x(const char* what, const cbx_conv1d_weights* w, const cbx_tensor* x, int prologue) {
+    const std::string f(what);
+    if (x->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, f + ": F32 only");
+    if (prologue < CBX_CONV_PRO_NONE || prologue > CBX_CONV_PRO_LEAKY_RELU) {
+        return set_error(CBX_ERR_INVALID_ARG, f + ": unknown prologue");
+    }
+    if (w && (x->ne[0] != w->c_in || x->ne[3] != 1)) {
+        return set_error(CBX_ERR_INVALID_ARG, f + ": x must be (C_in, T_in, B, 1) with the weights' C_in");
+    }
+    return CBX_OK;
+}
+
 int cbx_conv1d(const cbx_tensor* x, const cbx_conv1d_weights* w, int stride, int pad, int dilation, int prologue,
                const cbx_tensor* alpha, const cbx_tensor* alpha_inv, float slope, const cbx_tensor* bias,
                const cbx_tensor* res, cbx_tensor* y, cbx_stream stream) {
@@ -776,56 +863,55 @@ int cbx_conv1d(const cbx_tensor* x, const cbx_conv1d_weights* w, int stride, int
     DeviceState* st = current_state(&rc);
     if (!st) return rc;
     if (!w) return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: weights are NULL");
-    int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev != w->device) {
-        return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: the weights belong to another device");
-    }
     if ((rc = validate(x, what, "x")) || (rc = validate(y, what, "y"))) return rc;
-    if (x->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, "cbx_conv1d: F32 only");
+    if ((rc = check_conv_x(what, w, x, prologue))) return rc;
     if (stride < 1 || pad < 0 || dilation < 1 || stride > 64 || pad > (1 << 20) || dilation > 1024) {
         return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: stride must be 1..64, pad >= 0, dilation 1..1024");
     }
-    if (prologue < CBX_CONV_PRO_NONE || prologue > CBX_CONV_PRO_LEAKY_RELU) {
-        return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: unknown prologue");
-    }
-    if (x->ne[0] != w->c_in || x->ne[3] != 1) {
-        return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: x must be (C_in, T_in, B, 1) with the weights' C_in");
-    }
-    const int64_t t_in = x->ne[1], batch = x->ne[2];
+    const int64_t t_in = x->ne[1];
     const int64_t span = dilation * (w->k - 1) + 1;
     const int64_t t_out = t_in + 2 * pad >= span ? (t_in + 2 * pad - span) / stride + 1 : 0;
-    if (y->ne[0] != w->c_out || y->ne[1] != t_out || y->ne[2] != batch || y->ne[3] != 1) {
-        return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: y must be (C_out, T_out, B, 1), T_out = (T_in + 2 pad - "
-                                              "dilation (K - 1) - 1) / stride + 1");
+    bool empty = false;
+    if ((rc = check_conv_io(what, w, false, prologue, x, alpha, alpha_inv, bias, res, y, t_out,
+                            "T_out = (T_in + 2 pad - dilation (K - 1) - 1) / stride + 1", &empty))) {
+        return rc;
     }
-    if (t_in >= (int64_t{1} << 30) || t_out >= (int64_t{1} << 30) || batch >= 65536) {
-        return set_error(CBX_ERR_UNSUPPORTED, "cbx_conv1d: T must be below 2^30 and B below 65536");
-    }
-    if (bias) {
-        if ((rc = validate(bias, what, "bias"))) return rc;
-        if (bias->type != CBX_TYPE_F32 || nelements(bias) != w->c_out || !is_contiguous(bias)) {
-            return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: bias must be contiguous F32 with C_out elements");
-        }
-    }
-    if (res) {
-        if ((rc = validate(res, what, "res"))) return rc;
-        if (res->type != CBX_TYPE_F32 || !same_shape(res, y)) {
-            return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: res must be F32 with y's shape");
-        }
-    }
-    if (prologue == CBX_CONV_PRO_SNAKE) {
-        for (const cbx_tensor* p : {alpha, alpha_inv}) {
-            if ((rc = validate(p, what, p == alpha ? "alpha" : "alpha_inv"))) return rc;
-            if (p->type != CBX_TYPE_F32 || nelements(p) != w->c_in || !is_contiguous(p)) {
-                return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: alpha and alpha_inv must be contiguous F32 with C_in elements");
-            }
-        }
-    }
-    if (nelements(y) == 0) return CBX_OK;
-    if (overlaps(x, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: y must not overlap x");
-    return launch_conv1d(x, w->data, w->k, w->c_in_pad, w->c_out, stride, pad, dilation, prologue,
+    if (empty) return CBX_OK;
+    return launch_conv1d(x, w->data, w->k, w->c_in_pad, w->c_out, stride, pad, dilation, 1, 0, w->w_ph, prologue,
                          prologue == CBX_CONV_PRO_SNAKE ? alpha : nullptr,
                          prologue == CBX_CONV_PRO_SNAKE ? alpha_inv : nullptr, slope, bias, res, y, st,
+                         reinterpret_cast<hipStream_t>(stream));
+}
+
+int cbx_conv_transpose1d(const cbx_tensor* x, const cbx_conv1d_weights* w, int pad, int prologue,
+                         const cbx_tensor* alpha, const cbx_tensor* alpha_inv, float slope, const cbx_tensor* bias,
+                         cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_conv_transpose1d";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if (!w) return set_error(CBX_ERR_INVALID_ARG, "cbx_conv_transpose1d: weights are NULL");
+    if ((rc = validate(x, what, "x")) || (rc = validate(y, what, "y"))) return rc;
+    if ((rc = check_conv_x(what, w, x, prologue))) return rc;
+    const int64_t t_in = x->ne[1];
+    const int64_t full = t_in > 0 ? (t_in - 1) * w->up + w->k : 0;
+    if (pad < 0 || (t_in > 0 && 2 * static_cast<int64_t>(pad) >= full)) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_conv_transpose1d: pad must be >= 0 and leave T_out >= 1");
+    }
+    const int64_t t_out = t_in > 0 ? full - 2 * static_cast<int64_t>(pad) : 0;
+    bool empty = false;
+    if ((rc = check_conv_io(what, w, true, prologue, x, alpha, alpha_inv, bias, nullptr, y, t_out,
+                            "T_out = (T_in - 1) * stride + K - 2 pad", &empty))) {
+        return rc;
+    }
+    if (empty) return CBX_OK;
+    // stride 1: a single phase, i.e. a conv with the taps reversed and
+    // padding K - 1 - pad; larger strides run their phases side by side
+    const int up = w->up;
+    return launch_conv1d(x, w->data, w->taps, w->c_in_pad, w->c_out, 1, up == 1 ? static_cast<int>(w->k) - 1 - pad : 0,
+                         1, up, pad, w->w_ph, prologue, prologue == CBX_CONV_PRO_SNAKE ? alpha : nullptr,
+                         prologue == CBX_CONV_PRO_SNAKE ? alpha_inv : nullptr, slope, bias, nullptr, y, st,
                          reinterpret_cast<hipStream_t>(stream));
 }
 

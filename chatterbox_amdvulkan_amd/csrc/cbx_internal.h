@@ -99,13 +99,19 @@ int launch_bias_act(int op, const cbx_tensor* x, const cbx_tensor* bias, cbx_ten
 int launch_layer_norm_ext(const cbx_tensor* a, const cbx_tensor* a_bias, const cbx_tensor* r, const cbx_tensor* w,
                           const cbx_tensor* b, const cbx_tensor* mask, float eps, int act, cbx_tensor* s,
                           cbx_tensor* y, DeviceState* st, hipStream_t strm, const char* what);
-// conv1d (k_conv1d.hip): padded extents of the prepared f16 weights, the
-// weight conversion, and the conv itself.
+// conv1d and transposed conv1d (k_conv1d.hip): padded extents of the
+// prepared f16 weights, the weight conversion (up == 0: conv1d weight
+// (K, C_in, C_out); up >= 1: transposed weight (K, C_out, C_in) split into
+// max(up, 1) phases of `taps` taps), and the conv itself (up > 1: the
+// transposed conv's phases, crop outputs cut from each end, w_ph halves of
+// weights per phase).
 int conv1d_weights_layout(int64_t c_in, int64_t c_out, int64_t* c_in_pad, int64_t* c_out_pad);
-int launch_conv1d_weights(const cbx_tensor* w, _Float16* out, int64_t c_in_pad, int64_t c_out_pad, hipStream_t s);
+int launch_conv1d_weights(const cbx_tensor* w, int up, int64_t taps, _Float16* out, int64_t c_in_pad,
+                          int64_t c_out_pad, hipStream_t s);
 int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c_in_pad, int64_t c_out, int stride,
-                  int pad, int dil, int pro, const cbx_tensor* alpha, const cbx_tensor* alpha_inv, float slope,
-                  const cbx_tensor* bias, const cbx_tensor* res, cbx_tensor* y, DeviceState* st, hipStream_t s);
+                  int pad, int dil, int up, int crop, int64_t w_ph, int pro, const cbx_tensor* alpha,
+                  const cbx_tensor* alpha_inv, float slope, const cbx_tensor* bias, const cbx_tensor* res, cbx_tensor* y,
+                  DeviceState* st, hipStream_t s);
 int launch_snake(const cbx_tensor* x, const cbx_tensor* a, const cbx_tensor* ai, cbx_tensor* y,
                  DeviceState* st, hipStream_t s);
 

@@ -50,17 +50,52 @@ struct ConvArgs {
     int32_t c_in, c_in_pad, c_out, k, t_in, t_out, stride, pad, dil;
     int32_t win;                // window rows
     int32_t kch;                // input channels staged per chunk (a multiple of 32)
+    int32_t up;                 // transposed conv with stride up > 1: blockIdx.z = b * up + phase
+    int32_t crop;               // transposed: outputs cropped from each end
+    int64_t w_ph;               // transposed: halves of prepared weights per phase
     float slope;
 };
 
 enum { PRO_NONE = 0, PRO_SNAKE = 1, PRO_LEAKY = 2 };
 
+// Arguments of sin below this magnitude take sin_sq_small; the rest (and
+// NaN) are recomputed with the library sinf in a separate, rarely entered
+// pass, so the unrolled staging loop carries one short straight-line sin.
+constexpr float kSinSmall = 65536.0f;
+
+// sin(x)^2 for |x| < 2^16.  Cody-Waite reduction x = q*pi/2 + r with pi/2
+// split into three f32 parts P1 + P2 + P3: x - q*P1 is exact (x and q*P1
+// are multiples of the last place of P1 or finer, and the difference is
+// under 1), the q*P2 and q*P3 corrections round once each in their FMAs,
+// and the remaining q * (pi/2 - P1 - P2 - P3) is below 2^-57; then the Taylor polynomial
+// of sin r or cos r on |r| <= pi/4 (+ rounding slack): the first omitted
+// terms are r^11/11! < 2.2e-9 and r^12/12! < 1.2e-10, under half an f32 ulp
+// of the results.  sin(x)^2 = sin(r)^2 for even q, cos(r)^2 for odd q.
+__device__ __forceinline__ float sin_sq_small(float x) {
+    const float q = rintf(x * 0x1.45f306p-1f);   // x * 2/pi
+    float r = fmaf(q, -0x1.921fb6p+0f, x);
+    r = fmaf(q, 0x1.777a5cp-25f, r);
+    r = fmaf(q, 0x1.ee59dap-50f, r);
+    const float r2 = r * r;
+    float ps = fmaf(r2, 1.0f / 362880.0f, -1.0f / 5040.0f);
+    ps = fmaf(ps, r2, 1.0f / 120.0f);
+    ps = fmaf(ps, r2, -1.0f / 6.0f);
+    ps = fmaf(ps * r2, r, r);
+    float pc = fmaf(r2, -1.0f / 3628800.0f, 1.0f / 40320.0f);
+    pc = fmaf(pc, r2, -1.0f / 720.0f);
+    pc = fmaf(pc, r2, 1.0f / 24.0f);
+    pc = fmaf(pc, r2, -0.5f);
+    pc = fmaf(pc, r2, 1.0f);
+    const float s = (static_cast<int>(q) & 1) ? pc : ps;
+    return s * s;
+}
+
 template <int PRO>
 __device__ __forceinline__ float prologue(float v, float a, float ai, float slope) {
     if constexpr (PRO == PRO_SNAKE) {
+        // snake(x) = x + sin(x*a)^2 * a_inv in the reference's op order
         const float xa = v * a;
-        const float sn = sinf(xa);
-        const float s2 = sn * sn;
+        const float s2 = sin_sq_small(xa);
         const float m = s2 * ai;
         return v + m;
     } else if constexpr (PRO == PRO_LEAKY) {
@@ -84,8 +119,28 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
     const int wm = wave / WN, wn = wave % WN;
     const int t0 = blockIdx.x * BT;
     const int co0 = blockIdx.y * BC;
-    const char* xb = a.x + static_cast<int64_t>(blockIdx.z) * a.x_nb2;
-    const int base_t = t0 * a.stride - a.pad;   // input time of window row 0
+    int bz = blockIdx.z, pad = a.pad, t_out = a.t_out;
+    int64_t y_off = 0, y_step = a.y_nb1, r_off = 0, r_step = a.r_nb1;
+    const _Float16* wbase = a.w;
+    if (a.up > 1) {
+        // transposed conv, one phase ph of the full output t' = t + crop:
+        // t' = up*m + ph takes tap ph + j*up from input m - j.  Its outputs
+        // t = c1 + up*u (u = 0, 1, ..) are a stride-1 conv of the input with
+        // the phase's taps in reverse order and padding k - 1 - m(c1).
+        const int ph = bz % a.up;
+        bz /= a.up;
+        const int c1 = ((ph - a.crop) % a.up + a.up) % a.up;
+        pad = a.k - 1 - (c1 + a.crop - ph) / a.up;
+        t_out = c1 < a.t_out ? (a.t_out - c1 + a.up - 1) / a.up : 0;
+        y_off = c1 * a.y_nb1;
+        y_step = a.up * a.y_nb1;
+        r_off = c1 * a.r_nb1;
+        r_step = a.up * a.r_nb1;
+        wbase += ph * a.w_ph;
+    }
+    if (t0 >= t_out) return;   // a phase with fewer outputs than the grid covers (uniform)
+    const char* xb = a.x + static_cast<int64_t>(bz) * a.x_nb2;
+    const int base_t = t0 * a.stride - pad;     // input time of window row 0
     const int lrow = lane & 31, lk = 8 * (lane >> 5);
     const int cs = a.kch + 8;                   // LDS row stride (halves): conflict-free 16-byte reads
     const int nblk = a.c_in_pad / kBlk;         // 16-channel blocks of the weights
@@ -104,21 +159,26 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         const int co_t = (co0 >> 5) + wn * NT + nt;
-        wf[nt] = a.w + static_cast<int64_t>(co_t) * a.k * nblk * 512 + lane * 8;
+        wf[nt] = wbase + static_cast<int64_t>(co_t) * a.k * nblk * 512 + lane * 8;
     }
 
     for (int ci0 = 0; ci0 < a.c_in; ci0 += a.kch) {
         const int kch = a.c_in - ci0 < a.kch ? ((a.c_in - ci0 + kChanAlign - 1) / kChanAlign) * kChanAlign : a.kch;
         if (ci0 > 0) __syncthreads();   // the previous chunk's fragments have been read
         // snake: this chunk's alpha and alpha_inv into LDS, so the activation
-        // below reads them without a global round trip per element
+        // below reads them without a global round trip per element; a flag
+        // word after them marks a window with an argument of sin past
+        // kSinSmall
         float* sal = reinterpret_cast<float*>(lds + a.win * cs);
+        int* big_flag = reinterpret_cast<int*>(sal + 2 * a.kch);
+        bool big = false;
         if constexpr (PRO == PRO_SNAKE) {
             for (int c = tid; c < kch; c += NTH) {
                 const int cc = ci0 + c < a.c_in ? ci0 + c : 0;
                 sal[c] = a.alpha[cc];
                 sal[a.kch + c] = a.alpha_inv[cc];
             }
+            if (tid == 0) *big_flag = 0;
             __syncthreads();
         }
         // stage pro(x) rows [base_t, base_t + win) x channels [ci0, ci0 + kch) as f16,
@@ -161,6 +221,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
                     for (int q = 0; q < 4; q++) {
                         const float al = PRO == PRO_SNAKE ? sal[cg + q] : 0.0f;
                         const float ai = PRO == PRO_SNAKE ? sal[a.kch + cg + q] : 0.0f;
+                        if constexpr (PRO == PRO_SNAKE) big = big || !(fabsf(get(t, q) * al) < kSinSmall);
                         set(t, q, prologue<PRO>(get(t, q), al, ai, a.slope));
                     }
                 }
@@ -172,7 +233,29 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
                 *reinterpret_cast<half4*>(lds + r * cs + cg) = hv;
             }
         }
+        if constexpr (PRO == PRO_SNAKE) {
+            if (big) *big_flag = 1;
+        }
         __syncthreads();
+        if constexpr (PRO == PRO_SNAKE) {
+            // rare: arguments of sin at or past kSinSmall (or NaN) get the
+            // library sinf, element by element, over the staged window
+            if (*big_flag) {
+                for (int e = tid; e < a.win * kch; e += NTH) {
+                    const int r = e / kch, c = e - r * kch;
+                    const int ti = base_t + r, ci = ci0 + c;
+                    if (ti < 0 || ti >= a.t_in || ci >= a.c_in) continue;
+                    const float v = reinterpret_cast<const float*>(xb + static_cast<int64_t>(ti) * a.x_nb1)[ci];
+                    const float xa = v * sal[c];
+                    if (fabsf(xa) < kSinSmall) continue;
+                    const float sn = sinf(xa);
+                    const float s2 = sn * sn;
+                    const float m = s2 * sal[a.kch + c];
+                    lds[r * cs + c] = static_cast<_Float16>(v + m);
+                }
+                __syncthreads();
+            }
+        }
 
         // steps s = k * nb + cb over this chunk's 16-channel blocks
         const int nb = kch / kBlk, cb0 = ci0 / kBlk;
@@ -215,8 +298,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
     }
 
     // y = (sum + bias) [+ res]: ggml_add of the bias, then the residual add
-    const int64_t yb = static_cast<int64_t>(blockIdx.z) * a.y_nb2;
-    const int64_t rb = static_cast<int64_t>(blockIdx.z) * a.r_nb2;
+    const int64_t yb = static_cast<int64_t>(bz) * a.y_nb2 + y_off;
+    const int64_t rb = static_cast<int64_t>(bz) * a.r_nb2 + r_off;
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         const int co = co0 + (wn * NT + nt) * 32 + lrow;
@@ -227,39 +310,50 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int t = t0 + (wm * MT + mt) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (t >= a.t_out) continue;
+                if (t >= t_out) continue;
                 float v = acc[mt][nt][r];
                 if (a.bias) v = v + bv;
-                if (a.res) v = reinterpret_cast<const float*>(a.res + rb + static_cast<int64_t>(t) * a.r_nb1)[co] + v;
-                reinterpret_cast<float*>(a.y + yb + static_cast<int64_t>(t) * a.y_nb1)[co] = v;
+                if (a.res) v = reinterpret_cast<const float*>(a.res + rb + static_cast<int64_t>(t) * r_step)[co] + v;
+                reinterpret_cast<float*>(a.y + yb + static_cast<int64_t>(t) * y_step)[co] = v;
             }
         }
     }
 }
 
-// Fragment-major f16 copy of a ggml (K, C_in, C_out) weight, zero padded:
-// fragment (co tile, k, 16-channel block) is 64 lanes x 8 halves, lane l
-// holding w[co_tile*32 + l%32][block*16 + 8*(l/32) + j][k] -- one MFMA B
-// operand, one contiguous KiB.  The f16 rounding is mul_mat's conversion of
-// its F32 operand.
+// Fragment-major f16 copy of a conv weight, zero padded: fragment (phase,
+// co tile, tap, 16-channel block) is 64 lanes x 8 halves, lane l holding
+// w[co_tile*32 + l%32][block*16 + 8*(l/32) + j] at that tap -- one MFMA B
+// operand, one contiguous KiB.  conv1d (up == 0): ggml (K, C_in, C_out), one
+// phase, tap k.  Transposed conv with stride up: ggml (K, C_out, C_in), up
+// phases of `taps` taps, stored tap kp of phase ph being the weight's tap
+// ph + (taps - 1 - kp)*up (zero past K).  The f16 rounding is the
+// reference's conversion of an F32 weight.
+struct WPrep {
+    const char* w;
+    int64_t nb_k, nb_ci, nb_co;   // byte strides of tap, input and output channel
+    int32_t K, taps, up, c_in, c_out, nblk, co_tiles;
+    int64_t total;
+};
+
 template <bool F16>
-__global__ __launch_bounds__(256) void k_conv_weights(const char* w, int64_t nb0, int64_t nb1, int64_t nb2, int32_t K,
-                                                      int32_t c_in, int32_t c_out, int32_t nblk, int64_t total,
-                                                      _Float16* out) {
+__global__ __launch_bounds__(256) void k_conv_weights(WPrep p, _Float16* out) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= total) return;
+    if (i >= p.total) return;
     const int64_t frag = i >> 9;
     const int32_t lane = static_cast<int32_t>((i >> 3) & 63), j = static_cast<int32_t>(i & 7);
-    const int32_t cb = static_cast<int32_t>(frag % nblk);
-    const int64_t q = frag / nblk;
-    const int32_t k = static_cast<int32_t>(q % K);
-    const int32_t co = static_cast<int32_t>(q / K) * 32 + (lane & 31);
+    const int32_t cb = static_cast<int32_t>(frag % p.nblk);
+    const int64_t q = frag / p.nblk;
+    const int32_t kp = static_cast<int32_t>(q % p.taps);
+    const int64_t q2 = q / p.taps;
+    const int32_t co_t = static_cast<int32_t>(q2 % p.co_tiles), ph = static_cast<int32_t>(q2 / p.co_tiles);
+    const int32_t k = p.up == 0 ? kp : ph + (p.taps - 1 - kp) * p.up;
+    const int32_t co = co_t * 32 + (lane & 31);
     const int32_t ci = cb * 16 + 8 * (lane >> 5) + j;
     _Float16 v = static_cast<_Float16>(0.0f);
-    if (ci < c_in && co < c_out) {
-        const char* p = w + k * nb0 + ci * nb1 + co * nb2;
-        if constexpr (F16) v = __builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(p));
-        else v = static_cast<_Float16>(*reinterpret_cast<const float*>(p));
+    if (ci < p.c_in && co < p.c_out && k < p.K) {
+        const char* e = p.w + k * p.nb_k + ci * p.nb_ci + co * p.nb_co;
+        if constexpr (F16) v = __builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(e));
+        else v = static_cast<_Float16>(*reinterpret_cast<const float*>(e));
     }
     out[i] = v;
 }
@@ -318,27 +412,33 @@ int conv1d_weights_layout(int64_t c_in, int64_t c_out, int64_t* c_in_pad, int64_
     return CBX_OK;
 }
 
-int launch_conv1d_weights(const cbx_tensor* w, _Float16* out, int64_t c_in_pad, int64_t c_out_pad, hipStream_t s) {
-    const int64_t total = c_out_pad * w->ne[0] * c_in_pad;   // = (c_out_pad/32) * K * (c_in_pad/16) * 512
-    const dim3 grid(static_cast<unsigned>(cdiv(total, 256)));
-    const char* p = static_cast<const char*>(w->data);
-    const int64_t nb0 = static_cast<int64_t>(w->nb[0]), nb1 = static_cast<int64_t>(w->nb[1]),
-                  nb2 = static_cast<int64_t>(w->nb[2]);
-    const int32_t K = static_cast<int32_t>(w->ne[0]), ci = static_cast<int32_t>(w->ne[1]),
-                  co = static_cast<int32_t>(w->ne[2]);
-    const int32_t nblk = static_cast<int32_t>(c_in_pad / kBlk);
-    if (w->type == CBX_TYPE_F16) {
-        hipLaunchKernelGGL((k_conv_weights<true>), grid, dim3(256), 0, s, p, nb0, nb1, nb2, K, ci, co, nblk, total, out);
-    } else {
-        hipLaunchKernelGGL((k_conv_weights<false>), grid, dim3(256), 0, s, p, nb0, nb1, nb2, K, ci, co, nblk, total,
-                           out);
-    }
+int launch_conv1d_weights(const cbx_tensor* w, int up, int64_t taps, _Float16* out, int64_t c_in_pad,
+                          int64_t c_out_pad, hipStream_t s) {
+    WPrep p;
+    p.w = static_cast<const char*>(w->data);
+    p.nb_k = static_cast<int64_t>(w->nb[0]);
+    // conv1d: (K, C_in, C_out); transposed: (K, C_out, C_in)
+    p.nb_ci = static_cast<int64_t>(up == 0 ? w->nb[1] : w->nb[2]);
+    p.nb_co = static_cast<int64_t>(up == 0 ? w->nb[2] : w->nb[1]);
+    p.K = static_cast<int32_t>(w->ne[0]);
+    p.taps = static_cast<int32_t>(taps);
+    p.up = up;
+    p.c_in = static_cast<int32_t>(up == 0 ? w->ne[1] : w->ne[2]);
+    p.c_out = static_cast<int32_t>(up == 0 ? w->ne[2] : w->ne[1]);
+    p.nblk = static_cast<int32_t>(c_in_pad / kBlk);
+    p.co_tiles = static_cast<int32_t>(c_out_pad / 32);
+    const int64_t n_ph = up == 0 ? 1 : up;
+    p.total = n_ph * c_out_pad * taps * c_in_pad;   // = phases * co tiles * taps * blocks * 512
+    const dim3 grid(static_cast<unsigned>(cdiv(p.total, 256)));
+    if (w->type == CBX_TYPE_F16) hipLaunchKernelGGL((k_conv_weights<true>), grid, dim3(256), 0, s, p, out);
+    else hipLaunchKernelGGL((k_conv_weights<false>), grid, dim3(256), 0, s, p, out);
     return check_launch("conv1d_weights");
 }
 
 int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c_in_pad, int64_t c_out, int stride,
-                  int pad, int dil, int pro, const cbx_tensor* alpha, const cbx_tensor* alpha_inv, float slope,
-                  const cbx_tensor* bias, const cbx_tensor* res, cbx_tensor* y, DeviceState* st, hipStream_t s) {
+                  int pad, int dil, int up, int crop, int64_t w_ph, int pro, const cbx_tensor* alpha,
+                  const cbx_tensor* alpha_inv, float slope, const cbx_tensor* bias, const cbx_tensor* res, cbx_tensor* y,
+                  DeviceState* st, hipStream_t s) {
     ConvArgs a;
     a.x = static_cast<const char*>(x->data);
     a.w = w16;
@@ -362,9 +462,15 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     a.stride = stride;
     a.pad = pad;
     a.dil = dil;
+    a.up = up;
+    a.crop = crop;
+    a.w_ph = w_ph;
     a.slope = slope;
-    const int64_t batch = x->ne[2];
-    auto n_wg = [&](const Tile& t) { return cdiv(a.t_out, t.bt()) * cdiv(c_out, t.bc()) * batch; };
+    // a transposed conv with stride up > 1 runs its up output phases as
+    // stride-1 convs of ceil(T_out / up) rows each, side by side in grid z
+    const int64_t batch = x->ne[2] * (up > 1 ? up : 1);
+    const int64_t rows = up > 1 ? cdiv(a.t_out, up) : a.t_out;
+    auto n_wg = [&](const Tile& t) { return cdiv(rows, t.bt()) * cdiv(c_out, t.bc()) * batch; };
     auto win_of = [&](const Tile& t) { return (t.bt() - 1) * static_cast<int64_t>(stride) + (k - 1) * dil + 1; };
     // tile: the largest per-wave work that still gives a workgroup per CU
     int ti;
@@ -372,7 +478,7 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     else if (c_out <= 64) ti = n_wg(kTiles[0]) >= st->n_cu ? 0 : 3;
     else ti = n_wg(kTiles[1]) >= st->n_cu ? 1 : n_wg(kTiles[2]) >= st->n_cu ? 2 : 3;
     // the window of at least 32 channels must fit the LDS; strided convs fall back to 64-row tiles
-    auto fits = [&](int64_t w) { return w * (kChanAlign + 8) * 2 + 8 * kChanAlign <= static_cast<int64_t>(kLdsMax); };
+    auto fits = [&](int64_t w) { return w * (kChanAlign + 8) * 2 + 8 * kChanAlign + 16 <= static_cast<int64_t>(kLdsMax); };
     if (!fits(win_of(kTiles[ti]))) ti = 3;
     const int64_t win = win_of(kTiles[ti]);
     if (!fits(win)) {
@@ -384,11 +490,11 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     a.win = static_cast<int32_t>(win);
     a.kch = static_cast<int32_t>(kch);
     const size_t lds = static_cast<size_t>(win) * static_cast<size_t>(kch + 8) * sizeof(_Float16) +
-                       (pro == PRO_SNAKE ? 2 * static_cast<size_t>(kch) * sizeof(float) : 0);
+                       (pro == PRO_SNAKE ? (2 * static_cast<size_t>(kch) + 4) * sizeof(float) : 0);
     const bool vec = a.c_in % 4 == 0 && reinterpret_cast<uintptr_t>(a.x) % 16 == 0 && a.x_nb1 % 16 == 0 &&
-                     (batch <= 1 || a.x_nb2 % 16 == 0);
+                     (x->ne[2] <= 1 || a.x_nb2 % 16 == 0);
     const Tile& t = kTiles[ti];
-    const dim3 grid(static_cast<unsigned>(cdiv(a.t_out, t.bt())), static_cast<unsigned>(cdiv(c_out, t.bc())),
+    const dim3 grid(static_cast<unsigned>(cdiv(rows, t.bt())), static_cast<unsigned>(cdiv(c_out, t.bc())),
                     static_cast<unsigned>(batch));
     // every chunk's step count (K * channels / 16) is even; a ring of 4 when all are multiples of 4
     const int64_t last = c_in_pad - (cdiv(c_in_pad, kch) - 1) * kch;

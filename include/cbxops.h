@@ -295,6 +295,35 @@ int cbx_conv1d(const cbx_tensor* x, const cbx_conv1d_weights* w, int stride,
                const cbx_tensor* bias, const cbx_tensor* res, cbx_tensor* y,
                cbx_stream stream);
 
+/* Weights of one transposed conv1d with stride `stride` (the HiFT
+ * upsamplers' ups.i, hift_vocoder.cpp:96-115, 255-259): a ggml (K, C_out,
+ * C_in) F32/F16 weight (PyTorch ConvTranspose1d's (C_in, C_out, K) order)
+ * split into `stride` phases for the matrix cores, rounded to f16 as the
+ * reference's conv_transpose_1d rounds an F32 kernel.  Same handle type,
+ * lifetime and limits as cbx_conv1d_weights_create; stride 1..64.  A
+ * handle made here is only accepted by cbx_conv_transpose1d, and one made
+ * by cbx_conv1d_weights_create only by cbx_conv1d.                        */
+int cbx_conv_transpose1d_weights_create(const cbx_tensor* w, int stride,
+                                        cbx_stream stream,
+                                        cbx_conv1d_weights** out);
+
+/* conv_transpose1d_CT(pro(x)) (+ bias) in one kernel, on the reference's
+ * (C, T) layout (hift_vocoder.cpp:96-115, called at :686-687 right after
+ * leaky_relu, which is the prologue here):
+ *   full[i*stride + k][co] += f16(w[ci][co][k]) * f16(pro(x)[i][ci]),
+ *   y[t][co] = bias[co] + full[t + pad][co],  0 <= t < T_out,
+ * T_out = (T_in - 1) * stride + K - 2 pad -- ggml_conv_transpose_1d (p0 = 0,
+ * d0 = 1), the view that strips `pad` from both ends, then the bias add.
+ * Computed as `stride` phase convs on the matrix cores, products summed in
+ * f32 (the reference sums per-tap f16 dot products; order differs).
+ * x: F32 (C_in, T_in, B, 1); y: F32 (C_out, T_out, B, 1), not
+ * overlapping x; bias: F32 C_out or NULL; alpha, alpha_inv: snake only.   */
+int cbx_conv_transpose1d(const cbx_tensor* x, const cbx_conv1d_weights* w,
+                         int pad, int prologue, const cbx_tensor* alpha,
+                         const cbx_tensor* alpha_inv, float slope,
+                         const cbx_tensor* bias, cbx_tensor* y,
+                         cbx_stream stream);
+
 /* ---- model tables from a GGUF file ---------------------------------------- */
 
 /* The reference reads its weights with ggml's gguf reader: the header,

@@ -935,3 +935,82 @@ int cbxo_conv1d(const cbxo_tensor* x, const cbxo_tensor* w, int stride, int pad,
     free(wf);
     return 0;
 }
+
+/* conv_transpose1d_CT (hift_vocoder.cpp:96-115): ggml_conv_transpose_1d with
+ * p0 = 0, d0 = 1 converts the input and the kernel to f16 and adds, for each
+ * input time i and tap k, the f16 dot product over C_in into full[i*s + k]
+ * (f32); the reference then views [pad, pad + T_out) and adds the bias.
+ * Here the same f16 operands and every product of an output summed in f64,
+ * then the bias.  x (C_in, T_in, B); w (K, C_out, C_in) F32/F16; y (C_out,
+ * T_out, B), T_out = (T_in - 1) s + K - 2 pad.  The prologue (leaky_relu at
+ * hift_vocoder.cpp:686) is applied in f32 before the f16 rounding.        */
+int cbxo_conv_transpose1d(const cbxo_tensor* x, const cbxo_tensor* w, int stride, int pad, int prologue,
+                          const cbxo_tensor* alpha, const cbxo_tensor* alpha_inv, float slope,
+                          const cbxo_tensor* bias, cbxo_tensor* y, int nth) {
+    if (x->type != CBXO_TYPE_F32 || y->type != CBXO_TYPE_F32) return -1;
+    if (w->type != CBXO_TYPE_F32 && w->type != CBXO_TYPE_F16) return -1;
+    if (stride < 1 || pad < 0 || x->ne[3] != 1) return -1;
+    const int64_t C_in = x->ne[0], T_in = x->ne[1], B = x->ne[2];
+    const int64_t K = w->ne[0], C_out = w->ne[1];
+    if (w->ne[2] != C_in || w->ne[3] != 1 || T_in < 1) return -1;
+    const int64_t T_out = (T_in - 1) * stride + K - 2 * (int64_t)pad;
+    if (T_out < 1 || y->ne[0] != C_out || y->ne[1] != T_out || y->ne[2] != B || y->ne[3] != 1) return -1;
+    if (bias && (bias->type != CBXO_TYPE_F32 || bias->ne[0] != C_out)) return -1;
+    if (prologue == 1 && (!alpha || !alpha_inv || alpha->ne[0] != C_in || alpha_inv->ne[0] != C_in)) return -1;
+    if (prologue < 0 || prologue > 2) return -1;
+    float* h = (float*)malloc(sizeof(float) * (size_t)(C_in * T_in * B));
+    float* wf = (float*)malloc(sizeof(float) * (size_t)(C_out * K * C_in));   /* [oc][k][ic] */
+    if (!h || !wf) { free(h); free(wf); return -1; }
+    for (int64_t b = 0; b < B; b++) {
+        for (int64_t t = 0; t < T_in; t++) {
+            const float* rx = (const float*)row_ptr(x, t, b, 0);
+            for (int64_t ic = 0; ic < C_in; ic++) {
+                float v = rx[ic];
+                if (prologue == 1) {
+                    const float a = ((const float*)alpha->data)[ic];
+                    const float ai = ((const float*)alpha_inv->data)[ic];
+                    const float xa = v * a;
+                    const float sn = sinf(xa);
+                    const float s2 = sn * sn;
+                    const float m = s2 * ai;
+                    v = v + m;
+                } else if (prologue == 2) {
+                    v = op_leaky(v, slope);
+                }
+                h[(b * T_in + t) * C_in + ic] = cbxo_fp16_to_fp32(cbxo_fp32_to_fp16(v));
+            }
+        }
+    }
+    /* w element (k, oc, ic) sits in row (oc, ic) of the ggml layout */
+    for (int64_t ic = 0; ic < C_in; ic++) {
+        for (int64_t oc = 0; oc < C_out; oc++) {
+            const char* rw = row_ptr(w, oc, ic, 0);
+            for (int64_t k = 0; k < K; k++) {
+                const float v = load_elem(w, rw, k);
+                wf[(oc * K + k) * C_in + ic] = cbxo_fp16_to_fp32(cbxo_fp32_to_fp16(v));
+            }
+        }
+    }
+#pragma omp parallel for num_threads(nth) schedule(static)
+    for (int64_t bt = 0; bt < B * T_out; bt++) {
+        const int64_t b = bt / T_out, t = bt % T_out;
+        const int64_t tf = t + pad;   /* time in the uncropped output */
+        float* ry = (float*)row_ptr(y, t, b, 0);
+        for (int64_t oc = 0; oc < C_out; oc++) {
+            double acc = 0.0;
+            for (int64_t k = tf % stride; k < K; k += stride) {
+                const int64_t i = (tf - k) / stride;
+                if (tf < k || i >= T_in) continue;
+                const float* hr = h + (b * T_in + i) * C_in;
+                const float* wr = wf + (oc * K + k) * C_in;
+                for (int64_t ic = 0; ic < C_in; ic++) acc += (double)hr[ic] * (double)wr[ic];
+            }
+            float v = (float)acc;
+            if (bias) v = v + ((const float*)bias->data)[oc];
+            ry[oc] = v;
+        }
+    }
+    free(h);
+    free(wf);
+    return 0;
+}

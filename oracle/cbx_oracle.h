@@ -162,6 +162,17 @@ int cbxo_conv1d(const cbxo_tensor* x, const cbxo_tensor* w, int stride,
                 const cbxo_tensor* alpha, const cbxo_tensor* alpha_inv,
                 float slope, const cbxo_tensor* bias, const cbxo_tensor* res,
                 cbxo_tensor* y, int n_threads);
+/* conv_transpose1d_CT(pro(x)) [+ bias] (hift_vocoder.cpp:96-115):
+ * ggml_conv_transpose_1d (f16 input and kernel, p0 = 0, d0 = 1), the view
+ * that strips pad from both ends of the time axis, then the bias.  x (C_in,
+ * T_in, B) F32; w (K, C_out, C_in) F32/F16; y (C_out, T_out, B), T_out =
+ * (T_in - 1) stride + K - 2 pad.  f64 accumulation as cbxo_conv1d.        */
+int cbxo_conv_transpose1d(const cbxo_tensor* x, const cbxo_tensor* w,
+                          int stride, int pad, int prologue,
+                          const cbxo_tensor* alpha,
+                          const cbxo_tensor* alpha_inv, float slope,
+                          const cbxo_tensor* bias, cbxo_tensor* y,
+                          int n_threads);
 
 #ifdef __cplusplus
 }

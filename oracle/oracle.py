@@ -77,6 +77,7 @@ def lib():
             "cbxo_soft_max": (i, [P, P, i]),
             "cbxo_scale_diag_mask_soft_max": (i, [P, f, i, P, i]),
             "cbxo_conv1d": (i, [P, P, i, i, i, i, P, P, f, P, P, P, i]),
+            "cbxo_conv_transpose1d": (i, [P, P, i, i, i, P, P, f, P, P, i]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -363,4 +364,21 @@ def conv1d(x, w, stride=1, pad=0, dilation=1, prologue=0, alpha=None, alpha_inv=
     _check(lib().cbxo_conv1d(_ref(desc(x)), _ref(desc(np.ascontiguousarray(w))), stride, pad, dilation, prologue,
                              opt(keep[0]), opt(keep[1]), slope, opt(keep[2]), opt(keep[3]), _ref(desc(out)), nth),
            "conv1d")
+    return out
+
+
+def conv_transpose1d(x, w, stride, pad=0, prologue=0, alpha=None, alpha_inv=None, slope=0.0, bias=None, nth=1):
+    """conv_transpose1d_CT(pro(x)) (+ bias), pad cropped from both ends.  x:
+    numpy [B, T_in, C_in] or [T_in, C_in]; w: [C_in, C_out, K] (ggml ne (K,
+    C_out, C_in), the PyTorch ConvTranspose1d layout); returns [.., T_out,
+    C_out], T_out = (T_in - 1) * stride + K - 2 * pad."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    C_in, C_out, K = w.shape
+    T_out = (x.shape[-2] - 1) * stride + K - 2 * pad
+    out = np.empty(x.shape[:-2] + (T_out, C_out), dtype=np.float32)
+    opt = lambda a: _ref(desc(np.ascontiguousarray(a, dtype=np.float32))) if a is not None else None  # noqa: E731
+    keep = [np.ascontiguousarray(a, dtype=np.float32) if a is not None else None for a in (alpha, alpha_inv, bias)]
+    _check(lib().cbxo_conv_transpose1d(_ref(desc(x)), _ref(desc(np.ascontiguousarray(w))), stride, pad, prologue,
+                                       opt(keep[0]), opt(keep[1]), slope, opt(keep[2]), _ref(desc(out)), nth),
+           "conv_transpose1d")
     return out

@@ -174,3 +174,22 @@ def test_errors(cbx):
     assert L.cbx_conv1d(d(x), wts.handle, 0, 1, 1, 0, None, None, 0.0, None, None, d(y), None) == \
         cbx.ERR_INVALID_ARG
     wts.close()
+
+
+def test_snake_large_arguments(cbx, oracle):
+    """Arguments of sin at and past 2^16 (and just below) take the kernel's
+    element-wise pass with the library sinf; all stay inside f16 after the
+    prologue."""
+    C, T, K = 64, 700, 3
+    x = W.normal(70, (T, C), 0.0, 1.0)
+    alpha = np.full(C, 5.0, np.float32)
+    alpha[::3] = 0.5
+    alpha_inv = (1.0 / alpha).astype(np.float32)
+    x[::7, :] *= np.float32(3000.0)           # |x * alpha| ~ 1.5e4 .. 6e4
+    x[5, :] = np.float32(13107.2)             # x * 5 = 65536 exactly
+    x[6, :] = np.float32(13107.199)           # just below
+    x[11, ::2] = np.float32(-20000.0)         # -1e5
+    w = W.normal(71, (C, C, K), 0.0, 1.0 / np.sqrt(C * K))
+    b = W.normal(72, (C,), 0.0, 0.1)
+    got = run(cbx, x, w, 1, 1, 1, cbx.CONV_PRO_SNAKE, alpha, alpha_inv, 0.0, b, None)
+    check(oracle, got, x, w, 1, 1, 1, oracle.CONV_PRO_SNAKE, alpha, alpha_inv, 0.0, b, None, "large sin arguments")

@@ -532,3 +532,62 @@ def test_conv1d_f16_weights_equal_rounded_f32(oracle):
     x = rng.standard_normal((30, 8)).astype(np.float32)
     w = rng.standard_normal((4, 8, 3)).astype(np.float32)
     assert np.array_equal(oracle.conv1d(x, w, pad=1), oracle.conv1d(x, w.astype(np.float16), pad=1))
+
+
+# ---- conv_transpose1d (HiFT ups.i: ggml_conv_transpose_1d + crop + bias) ----------
+
+@pytest.mark.parametrize("stride,K,pad", [(8, 16, 4), (5, 11, 3), (3, 7, 2), (1, 3, 1), (3, 2, 0), (4, 9, 0)])
+def test_conv_transpose1d_matches_torch(oracle, stride, K, pad):
+    """Against torch's conv_transpose1d in float64 on the same f16-rounded
+    operands (weight [C_in, C_out, K], padding = the crop from each end):
+    the HiFT upsamplers (8, 16, 4), (5, 11, 3), (3, 7, 2), stride 1, and a
+    kernel shorter than the stride (outputs with no tap)."""
+    import torch
+    rng = np.random.default_rng(stride * 100 + K)
+    x = rng.standard_normal((2, 23, 12)).astype(np.float32)
+    w = rng.standard_normal((12, 8, K)).astype(np.float32)
+    b = rng.standard_normal(8).astype(np.float32)
+    got = oracle.conv_transpose1d(x, w, stride, pad, bias=b)
+    xh = torch.from_numpy(x.astype(np.float16).astype(np.float64)).transpose(1, 2)
+    wh = torch.from_numpy(w.astype(np.float16).astype(np.float64))
+    ref = torch.nn.functional.conv_transpose1d(xh, wh, stride=stride, padding=pad).transpose(1, 2).numpy()
+    assert got.shape == ref.shape == (2, 22 * stride + K - 2 * pad, 8)
+    # the oracle rounds the f64 sum to f32 once, then adds the bias in f32
+    assert np.array_equal(got, (ref.astype(np.float32) + b).astype(np.float32))
+
+
+@pytest.mark.parametrize("stride,K,pad", [(8, 16, 4), (5, 11, 3), (2, 5, 1)])
+def test_conv_transpose1d_is_the_adjoint_of_conv1d(oracle, stride, K, pad):
+    """<convT_w(x), y> = <x, conv_w(y)>: the transposed conv is the adjoint
+    of conv1d with the same array as its [C_out', C_in', K] weight, stride
+    and padding.  f16-exact operands, so both sides are sums of the same
+    exact products."""
+    rng = np.random.default_rng(K)
+    f16 = lambda a: a.astype(np.float16).astype(np.float32)  # noqa: E731
+    x = f16(rng.standard_normal((17, 6)))
+    w = f16(rng.standard_normal((6, 5, K)))
+    T_out = 16 * stride + K - 2 * pad
+    y = f16(rng.standard_normal((T_out, 5)))
+    lhs = np.sum(oracle.conv_transpose1d(x, w, stride, pad).astype(np.float64) * y)
+    cy = oracle.conv1d(y, w, stride, pad)
+    assert cy.shape == x.shape
+    rhs = np.sum(x.astype(np.float64) * cy)
+    assert abs(lhs - rhs) <= 1e-5 * (abs(lhs) + 1.0)
+
+
+def test_conv_transpose1d_repeat_and_prologue(oracle):
+    """K = stride with w[ci][co][k] = (ci == co): every input row repeats
+    stride times (nearest upsampling), then the crop; the leaky prologue is
+    the oracle's leaky_relu, rounded to f16; F16 weights equal rounded F32."""
+    rng = np.random.default_rng(9)
+    C, s = 8, 5
+    x = (rng.standard_normal((30, C)) * 2).astype(np.float32)
+    w = np.repeat(np.eye(C, dtype=np.float32)[:, :, None], s, axis=2)
+    f16 = lambda a: a.astype(np.float16).astype(np.float32)  # noqa: E731
+    up = np.repeat(f16(x), s, axis=0)
+    assert np.array_equal(oracle.conv_transpose1d(x, w, s, 0), up)
+    assert np.array_equal(oracle.conv_transpose1d(x, w, s, 2), up[2:-2])
+    assert np.array_equal(oracle.conv_transpose1d(x, w, s, 0, prologue=oracle.CONV_PRO_LEAKY, slope=0.1),
+                          np.repeat(f16(oracle.leaky_relu(x, 0.1)), s, axis=0))
+    w2 = rng.standard_normal((C, 4, 7)).astype(np.float32)
+    assert np.array_equal(oracle.conv_transpose1d(x, w2, 3, 2), oracle.conv_transpose1d(x, w2.astype(np.float16), 3, 2))
