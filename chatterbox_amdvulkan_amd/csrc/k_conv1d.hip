@@ -18,9 +18,18 @@
 // 160 KiB of LDS) -- once; every tap's A rows are shifted views of it, so
 // each input element is loaded and activated once per workgroup.  Then each
 // wave runs K * C_in/16 steps, each MT x NT MFMAs: A fragments (8 f16 of one
-// window row) from LDS, B fragments from the prepared weights, whose
-// fragment-major layout makes each one a contiguous KiB, read PF steps
-// ahead into a register ring so the L2 latency hides under the MFMAs.
+// window row) from LDS, read one step ahead; B fragments from the prepared
+// weights, whose fragment-major layout makes each one a contiguous KiB,
+// read PF steps ahead into a register ring so the L2 latency hides under
+// the MFMAs.  Each workgroup starts its sweep of the steps at its own
+// offset, so the workgroups sharing an L2 spread their fragment reads over
+// it instead of all reading the same KiB.  The finished tile goes through
+// LDS to row-contiguous float4 stores (with the bias and residual reads).
+//
+// The transposed conv of the upsamplers (hift_vocoder.cpp:96-115) runs on
+// the same kernel: output phase ph of stride s is a stride-1 conv of the
+// input with that phase's taps reversed, so the s phases are s such convs
+// side by side in grid z, each writing every s-th output row.
 //
 // Fragment layout of v_mfma_f32_32x32x16_f16 (checked on the device):
 // lane l holds A[l % 32][8*(l/32) + j] and B[8*(l/32) + j][l % 32], j < 8;
@@ -53,6 +62,7 @@ struct ConvArgs {
     int32_t up;                 // transposed conv with stride up > 1: blockIdx.z = b * up + phase
     int32_t crop;               // transposed: outputs cropped from each end
     int64_t w_ph;               // transposed: halves of prepared weights per phase
+    int32_t vout;               // c_out % 4 == 0 and 16-byte aligned y, res and bias: float4 stores
     float slope;
 };
 
@@ -67,8 +77,8 @@ constexpr float kSinSmall = 65536.0f;
 // split into three f32 parts P1 + P2 + P3: x - q*P1 is exact (x and q*P1
 // are multiples of the last place of P1 or finer, and the difference is
 // under 1), the q*P2 and q*P3 corrections round once each in their FMAs,
-// and the remaining q * (pi/2 - P1 - P2 - P3) is below 2^-57; then the Taylor polynomial
-// of sin r or cos r on |r| <= pi/4 (+ rounding slack): the first omitted
+// and the remaining q * (pi/2 - P1 - P2 - P3) is below 2^-57; then the
+// Taylor polynomial of sin r or cos r on |r| <= pi/4 (+ rounding slack): the first omitted
 // terms are r^11/11! < 2.2e-9 and r^12/12! < 1.2e-10, under half an f32 ulp
 // of the results.  sin(x)^2 = sin(r)^2 for even q, cos(r)^2 for odd q.
 __device__ __forceinline__ float sin_sq_small(float x) {
@@ -161,6 +171,10 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
         const int co_t = (co0 >> 5) + wn * NT + nt;
         wf[nt] = wbase + static_cast<int64_t>(co_t) * a.k * nblk * 512 + lane * 8;
     }
+    // LDS offset (halves) of the lane's A row of each tile mt at tap 0, block 0
+    int arow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) arow[mt] = ((wm * MT + mt) * 32 + lrow) * a.stride * cs + lk;
 
     for (int ci0 = 0; ci0 < a.c_in; ci0 += a.kch) {
         const int kch = a.c_in - ci0 < a.kch ? ((a.c_in - ci0 + kChanAlign - 1) / kChanAlign) * kChanAlign : a.kch;
@@ -181,57 +195,78 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
             if (tid == 0) *big_flag = 0;
             __syncthreads();
         }
-        // stage pro(x) rows [base_t, base_t + win) x channels [ci0, ci0 + kch) as f16,
-        // kStage 4-channel groups in flight per lane
-        constexpr int kStage = 16;
+        // stage pro(x) rows [base_t, base_t + win) x channels [ci0, ci0 + kch)
+        // as f16.  Element e = tid + NTH*j is window row e / gpr, 4-channel
+        // group e % gpr, both stepped incrementally (one division per chunk).
+        // Every load is issued unconditionally -- from the prepared weights
+        // (always valid) where the element lies outside x -- and zeroed
+        // afterwards, so all kStage loads of a lane are in flight together.
+        constexpr int kStage = 8;
         const int gpr = kch >> 2;                 // groups per row
         const int n_el = a.win * gpr;
+        const int dr = NTH / gpr, dg = NTH - dr * gpr;
+        const float* safe = reinterpret_cast<const float*>(a.w);
+        int r_e = tid / gpr, g_e = tid - r_e * gpr;
         for (int e0 = tid; e0 < n_el; e0 += kStage * NTH) {
             float4 v[kStage];
+            int rr = r_e, gg = g_e;
 #pragma unroll
             for (int i = 0; i < kStage; i++) {
-                const int e = e0 + i * NTH;
-                v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (e < n_el) {
-                    const int r = e / gpr, ci = ci0 + (e - r * gpr) * 4;
-                    const int ti = base_t + r;
-                    if (ti >= 0 && ti < a.t_in) {
-                        const float* src =
-                            reinterpret_cast<const float*>(xb + static_cast<int64_t>(ti) * a.x_nb1) + ci;
-                        if constexpr (VEC) {
-                            if (ci < a.c_in) v[i] = *reinterpret_cast<const float4*>(src);
-                        } else {
-                            v[i].x = ci + 0 < a.c_in ? src[0] : 0.0f;
-                            v[i].y = ci + 1 < a.c_in ? src[1] : 0.0f;
-                            v[i].z = ci + 2 < a.c_in ? src[2] : 0.0f;
-                            v[i].w = ci + 3 < a.c_in ? src[3] : 0.0f;
-                        }
-                    }
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < kStage; i++) {
-                const int e = e0 + i * NTH;
-                if (e >= n_el) continue;
-                const int r = e / gpr, cg = (e - r * gpr) * 4;
-                float4 t = v[i];
-                if constexpr (PRO != PRO_NONE) {
-                    // pro(0) = 0: padding rows and channels stay 0
+                const int ti = base_t + rr, ci = ci0 + gg * 4;
+                const bool row_ok = rr < a.win && ti >= 0 && ti < a.t_in;
+                const float* row = reinterpret_cast<const float*>(xb + static_cast<int64_t>(row_ok ? ti : 0) * a.x_nb1);
+                if constexpr (VEC) {
+                    const bool ok = row_ok && ci < a.c_in;
+                    const float4 t = *reinterpret_cast<const float4*>(ok ? row + ci : safe);
+                    v[i] = ok ? t : make_float4(0.f, 0.f, 0.f, 0.f);
+                } else {
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
-                        const float al = PRO == PRO_SNAKE ? sal[cg + q] : 0.0f;
-                        const float ai = PRO == PRO_SNAKE ? sal[a.kch + cg + q] : 0.0f;
-                        if constexpr (PRO == PRO_SNAKE) big = big || !(fabsf(get(t, q) * al) < kSinSmall);
-                        set(t, q, prologue<PRO>(get(t, q), al, ai, a.slope));
+                        const bool ok = row_ok && ci + q < a.c_in;
+                        const float t = *(ok ? row + ci + q : safe);
+                        set(v[i], q, ok ? t : 0.0f);
                     }
                 }
-                half4 hv;
-                hv[0] = static_cast<_Float16>(t.x);
-                hv[1] = static_cast<_Float16>(t.y);
-                hv[2] = static_cast<_Float16>(t.z);
-                hv[3] = static_cast<_Float16>(t.w);
-                *reinterpret_cast<half4*>(lds + r * cs + cg) = hv;
+                gg += dg;
+                rr += dr;
+                if (gg >= gpr) {
+                    gg -= gpr;
+                    rr++;
+                }
             }
+            rr = r_e;
+            gg = g_e;
+#pragma unroll
+            for (int i = 0; i < kStage; i++) {
+                if (rr < a.win) {
+                    const int cg = gg * 4;
+                    float4 t = v[i];
+                    if constexpr (PRO != PRO_NONE) {
+                        // pro(0) = 0: padding rows and channels stay 0
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const float al = PRO == PRO_SNAKE ? sal[cg + q] : 0.0f;
+                            const float ai = PRO == PRO_SNAKE ? sal[a.kch + cg + q] : 0.0f;
+                            if constexpr (PRO == PRO_SNAKE) big = big || !(fabsf(get(t, q) * al) < kSinSmall);
+                            set(t, q, prologue<PRO>(get(t, q), al, ai, a.slope));
+                        }
+                    }
+                    half4 hv;
+                    hv[0] = static_cast<_Float16>(t.x);
+                    hv[1] = static_cast<_Float16>(t.y);
+                    hv[2] = static_cast<_Float16>(t.z);
+                    hv[3] = static_cast<_Float16>(t.w);
+                    *reinterpret_cast<half4*>(lds + rr * cs + cg) = hv;
+                }
+                gg += dg;
+                rr += dr;
+                if (gg >= gpr) {
+                    gg -= gpr;
+                    rr++;
+                }
+            }
+            r_e = rr;
+            g_e = gg;
         }
         if constexpr (PRO == PRO_SNAKE) {
             if (big) *big_flag = 1;
@@ -257,62 +292,136 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
             }
         }
 
-        // steps s = k * nb + cb over this chunk's 16-channel blocks
+        // steps s = k * nb + cb over this chunk's 16-channel blocks.  A of
+        // tile mt at lds + arow[mt] + aoff, aoff = k*dil*cs + cb*16; B of tile
+        // nt at wf[nt] + boff, boff = (k*nblk + cb0 + cb)*512.  Both offsets
+        // are wave-uniform and stepped by counters (no division in the loop).
+        // Each workgroup starts its sweep at its own step and wraps around
+        // (the order of the f32 sum is free): workgroups that share an L2 do
+        // not all fetch the same weight fragment at the same time.
         const int nb = kch / kBlk, cb0 = ci0 / kBlk;
         const int n_steps = a.k * nb;
-        auto bfrag = [&](int nt, int s) {
-            const int k = s / nb, cb = s - k * nb;
-            return *reinterpret_cast<const half8*>(wf[nt] + (static_cast<int64_t>(k) * nblk + cb0 + cb) * 512);
+        const int a_wrap = a.dil * cs - nb * kBlk;            // (k, nb) -> (k + 1, 0)
+        const int64_t b_wrap = static_cast<int64_t>(nblk - nb) * 512;
+        const int64_t b_first = static_cast<int64_t>(cb0) * 512;
+        const unsigned wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+        const int s_start = static_cast<int>(((wg >> 3) * 3u) % static_cast<unsigned>(n_steps));
+        const int k_start = s_start / nb, cb_start = s_start - k_start * nb;
+        const int a_start = k_start * a.dil * cs + cb_start * kBlk;
+        const int64_t b_start = (static_cast<int64_t>(k_start) * nblk + cb0 + cb_start) * 512;
+        int k_a = k_start, cb_a = cb_start, aoff = a_start;      // A of the next step to read
+        int k_b = k_start, cb_b = cb_start;
+        int64_t boff = b_start;                                  // B of the next step to fetch
+        auto next_a = [&]() {
+            aoff += kBlk;
+            if (++cb_a == nb) {
+                cb_a = 0;
+                aoff += a_wrap;
+                if (++k_a == a.k) {
+                    k_a = 0;
+                    aoff = 0;
+                }
+            }
+        };
+        auto next_b = [&]() {
+            boff += 512;
+            if (++cb_b == nb) {
+                cb_b = 0;
+                boff += b_wrap;
+                if (++k_b == a.k) {
+                    k_b = 0;
+                    boff = b_first;
+                }
+            }
         };
         half8 ring[PF][NT];
 #pragma unroll
         for (int p = 0; p < PF; p++) {
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) ring[p][nt] = bfrag(nt, p);
+            for (int nt = 0; nt < NT; nt++) ring[p][nt] = *reinterpret_cast<const half8*>(wf[nt] + boff);
+            next_b();
         }
+        half8 av[2][MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) av[0][mt] = *reinterpret_cast<const half8*>(lds + arow[mt] + aoff);
+        next_a();
         for (int s0 = 0; s0 < n_steps; s0 += PF) {
 #pragma unroll
             for (int p = 0; p < PF; p++) {
                 const int s = s0 + p;
-                const int k = s / nb, cb = s - k * nb;
-                half8 av[MT];
+                const int cur = p & 1;   // PF is even: the parity of s
+                // A of step s + 1 (past the end: the first step's again, unused)
+                const int an = s + 1 < n_steps ? aoff : a_start;
 #pragma unroll
-                for (int mt = 0; mt < MT; mt++) {
-                    const int row = ((wm * MT + mt) * 32 + lrow) * a.stride + k * a.dil;
-                    av[mt] = *reinterpret_cast<const half8*>(lds + row * cs + cb * kBlk + lk);
-                }
+                for (int mt = 0; mt < MT; mt++) av[cur ^ 1][mt] = *reinterpret_cast<const half8*>(lds + arow[mt] + an);
+                next_a();
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
 #pragma unroll
                     for (int nt = 0; nt < NT; nt++) {
-                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[mt], ring[p][nt], acc[mt][nt], 0, 0,
-                                                                             0);
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cur][mt], ring[p][nt], acc[mt][nt], 0,
+                                                                             0, 0);
                     }
                 }
-                // the fragment PF steps ahead (past the end: this step's again, unused)
-                const int sn = s + PF < n_steps ? s + PF : s;
+                // B of step s + PF (past the end: the first step's again, unused)
+                const int64_t bn = s + PF < n_steps ? boff : b_start;
 #pragma unroll
-                for (int nt = 0; nt < NT; nt++) ring[p][nt] = bfrag(nt, sn);
+                for (int nt = 0; nt < NT; nt++) ring[p][nt] = *reinterpret_cast<const half8*>(wf[nt] + bn);
+                next_b();
             }
         }
     }
 
-    // y = (sum + bias) [+ res]: ggml_add of the bias, then the residual add
-    const int64_t yb = static_cast<int64_t>(bz) * a.y_nb2 + y_off;
-    const int64_t rb = static_cast<int64_t>(bz) * a.r_nb2 + r_off;
+    // y = (sum + bias) [+ res]: ggml_add of the bias, then the residual add.
+    // Each wave parks its tile in LDS (row-major, the window is no longer
+    // read), then writes whole rows: with vout, one float4 per lane, a row
+    // segment of NT*32 channels per NT*8 lanes.
+    __syncthreads();
+    constexpr int EPS = NT * 32 + 4;   // tile row stride in floats
+    float* ep = reinterpret_cast<float*>(lds) + wave * (MT * 32 * EPS);
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const int co = co0 + (wn * NT + nt) * 32 + lrow;
-        if (co >= a.c_out) continue;
-        const float bv = a.bias ? a.bias[co] : 0.0f;
+    for (int mt = 0; mt < MT; mt++) {
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
+        for (int nt = 0; nt < NT; nt++) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int t = t0 + (wm * MT + mt) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (t >= t_out) continue;
-                float v = acc[mt][nt][r];
-                if (a.bias) v = v + bv;
+                ep[(mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * EPS + nt * 32 + lrow] = acc[mt][nt][r];
+            }
+        }
+    }
+    __syncthreads();
+    const int64_t yb = static_cast<int64_t>(bz) * a.y_nb2 + y_off;
+    const int64_t rb = static_cast<int64_t>(bz) * a.r_nb2 + r_off;
+    const int tw = t0 + wm * MT * 32, cw = co0 + wn * NT * 32;
+    if (a.vout) {
+        constexpr int CPR = NT * 8;      // float4 per tile row
+        constexpr int RPI = 64 / CPR;    // tile rows per store instruction
+        const int c4 = (lane % CPR) * 4, co = cw + c4;
+        const bool cok = co < a.c_out;   // c_out % 4 == 0: the whole float4
+        float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (a.bias && cok) bv = *reinterpret_cast<const float4*>(a.bias + co);
+#pragma unroll 4
+        for (int rl = lane / CPR; rl < MT * 32; rl += RPI) {
+            const int t = tw + rl;
+            if (t < t_out && cok) {
+                float4 v = *reinterpret_cast<const float4*>(ep + rl * EPS + c4);
+                if (a.bias) v = make_float4(v.x + bv.x, v.y + bv.y, v.z + bv.z, v.w + bv.w);
+                if (a.res) {
+                    const float4 q = *reinterpret_cast<const float4*>(a.res + rb + static_cast<int64_t>(t) * r_step +
+                                                                      static_cast<int64_t>(co) * 4);
+                    v = make_float4(q.x + v.x, q.y + v.y, q.z + v.z, q.w + v.w);
+                }
+                *reinterpret_cast<float4*>(a.y + yb + static_cast<int64_t>(t) * y_step + static_cast<int64_t>(co) * 4) =
+                    v;
+            }
+        }
+    } else {
+        for (int i = lane; i < MT * 32 * NT * 32; i += 64) {
+            const int rl = i / (NT * 32), c = i % (NT * 32);
+            const int t = tw + rl, co = cw + c;
+            if (t < t_out && co < a.c_out) {
+                float v = ep[rl * EPS + c];
+                if (a.bias) v = v + a.bias[co];
                 if (a.res) v = reinterpret_cast<const float*>(a.res + rb + static_cast<int64_t>(t) * r_step)[co] + v;
                 reinterpret_cast<float*>(a.y + yb + static_cast<int64_t>(t) * y_step)[co] = v;
             }
@@ -489,11 +598,19 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     kch = std::min<int64_t>(kch, c_in_pad);
     a.win = static_cast<int32_t>(win);
     a.kch = static_cast<int32_t>(kch);
-    const size_t lds = static_cast<size_t>(win) * static_cast<size_t>(kch + 8) * sizeof(_Float16) +
-                       (pro == PRO_SNAKE ? (2 * static_cast<size_t>(kch) + 4) * sizeof(float) : 0);
+    const Tile& t = kTiles[ti];
+    // the window (+ snake's alpha, alpha_inv and flag), then the output tile
+    // of every wave (rows of NT*32 + 4 floats) in the same memory
+    const size_t win_bytes = static_cast<size_t>(win) * static_cast<size_t>(kch + 8) * sizeof(_Float16) +
+                             (pro == PRO_SNAKE ? (2 * static_cast<size_t>(kch) + 4) * sizeof(float) : 0);
+    const size_t out_bytes = static_cast<size_t>(t.wm * t.wn) * t.mt * 32 * (t.nt * 32 + 4) * sizeof(float);
+    const size_t lds = std::max(win_bytes, out_bytes);
     const bool vec = a.c_in % 4 == 0 && reinterpret_cast<uintptr_t>(a.x) % 16 == 0 && a.x_nb1 % 16 == 0 &&
                      (x->ne[2] <= 1 || a.x_nb2 % 16 == 0);
-    const Tile& t = kTiles[ti];
+    auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const bool one = x->ne[2] <= 1;
+    a.vout = c_out % 4 == 0 && al16(a.y) && a.y_nb1 % 16 == 0 && (one || a.y_nb2 % 16 == 0) &&
+             (!a.bias || al16(a.bias)) && (!a.res || (al16(a.res) && a.r_nb1 % 16 == 0 && (one || a.r_nb2 % 16 == 0)));
     const dim3 grid(static_cast<unsigned>(cdiv(rows, t.bt())), static_cast<unsigned>(cdiv(c_out, t.bc())),
                     static_cast<unsigned>(batch));
     // every chunk's step count (K * channels / 16) is even; a ring of 4 when all are multiples of 4
