@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="skip the secondary workloads")
+    ap.add_argument("--hift-conv", action="store_true",
+                    help="only the HiFT conv1d / transposed-conv timings, as one JSON object (for profiling)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the launches used by the FETCH_SIZE/WRITE_SIZE counter runs")
     return ap.parse_args()
@@ -557,45 +559,56 @@ def bench_hift_conv(C, W, torch, reps=60):
     shapes [1,256,6000], [1,128,48000], [1,64,120000]: snake -> conv1d
     (K 11, dilation 5) + bias, snake -> conv1d (K 3, dilation 1) + bias + x,
     and one whole sublayer (snake -> conv K 11 d 5 -> snake -> conv K 11 d 1
-    -> + x, two launches).  f16 operands, f32 accumulation on the matrix
-    cores; algorithmic FLOPs 2*C_in*C_out*K*T_out per conv."""
+    -> + x, two launches); then the three upsamplers.  f16 operands, f32
+    accumulation on the matrix cores; algorithmic FLOPs 2*C_in*C_out*K*T_out
+    per conv.  Launches rotate over buffer sets whose combined size exceeds
+    twice the Infinity Cache, so activations come from HBM."""
     d = dev_of(torch)
     L = C.load()
     out = {}
+
+    def sets_for(nbytes):
+        return max(2, math.ceil(MALL_DEFEAT_BYTES / nbytes))
+
+    def rate(flops, nbytes, us, **kw):
+        return dict({"us": us, "TFLOPs": flops / (us * 1e-6) / 1e12,
+                     "pct_of_mfma_f16_peak": 100.0 * flops / (us * 1e-6) / 1e12 / PEAK_MFMA_F16_TFLOPS,
+                     "GBps": nbytes / (us * 1e-6) / 1e9}, **kw)
+
     for (Ch, T) in ((256, 6000), (128, 48000), (64, 120000)):
-        x = d(W.normal(W.seed_of(8, Ch), (T, Ch)))
+        n_sets = sets_for(3 * 4 * T * Ch)
+        x0 = d(W.normal(W.seed_of(8, Ch), (T, Ch)))
+        bufs = [{"x": x0 if i == 0 else x0.clone(), "h": torch.empty_like(x0), "y": torch.empty_like(x0)}
+                for i in range(n_sets)]
         a, ai = (d(v) for v in W.snake_alpha(Ch, 3))
         bias = d(W.normal(W.seed_of(8, Ch + 1), (Ch,), 0.0, 0.1))
         ws = {K: C.Conv1dWeights(d(W.normal(W.seed_of(8, Ch + K), (Ch, Ch, K), 0.0, 1.0 / np.sqrt(Ch * K))))
               for K in (3, 11)}
-        h = torch.empty_like(x)
-        y = torch.empty_like(x)
-        R = {k: C.ctypes.byref(C.desc(v)) for k, v in dict(x=x, a=a, ai=ai, b=bias, h=h, y=y).items()}
-        res = {}
+        Rc = {k: C.ctypes.byref(C.desc(v)) for k, v in dict(a=a, ai=ai, b=bias).items()}
+        Rs = [{k: C.ctypes.byref(C.desc(v)) for k, v in b.items()} for b in bufs]
+        res = {"buffer_sets": n_sets}
 
-        def conv(K, dil, src, dst, residual):
+        def conv(R, K, dil, src, dst, residual):
             pad = (K - 1) // 2 * dil
-            return lambda s: check_rc(C, L.cbx_conv1d(R[src], ws[K].handle, 1, pad, dil, C.CONV_PRO_SNAKE, R["a"],
-                                                      R["ai"], 0.0, R["b"], R["x"] if residual else None, R[dst], s))
+            return lambda s: check_rc(C, L.cbx_conv1d(R[src], ws[K].handle, 1, pad, dil, C.CONV_PRO_SNAKE, Rc["a"],
+                                                      Rc["ai"], 0.0, Rc["b"], R["x"] if residual else None, R[dst],
+                                                      s))
         for name, K, dil, residual in (("k11_d5", 11, 5, False), ("k3_d1_residual", 3, 1, True)):
-            fn = conv(K, dil, "x", "y", residual)
-            fn(cur_stream(torch))
-            us = per_launch_ms(torch, [fn], reps) * 1000.0
-            flops = 2.0 * Ch * Ch * K * T
-            nbytes = 4 * T * Ch * (3 if residual else 2)
-            res[name] = {"us": us, "TFLOPs": flops / (us * 1e-6) / 1e12,
-                         "pct_of_mfma_f16_peak": 100.0 * flops / (us * 1e-6) / 1e12 / PEAK_MFMA_F16_TFLOPS,
-                         "GBps": nbytes / (us * 1e-6) / 1e9}
-        c1, c2 = conv(11, 5, "x", "h", False), conv(11, 1, "h", "y", True)
-        sub = lambda s: (c1(s), c2(s))  # noqa: E731
-        sub(cur_stream(torch))
-        us = per_launch_ms(torch, [sub], reps) * 1000.0
-        flops = 2 * 2.0 * Ch * Ch * 11 * T
-        res["sublayer_k11_d5"] = {"us": us, "TFLOPs": flops / (us * 1e-6) / 1e12, "launches": 2}
+            fns = [conv(R, K, dil, "x", "y", residual) for R in Rs]
+            fns[0](cur_stream(torch))
+            us = per_launch_ms(torch, fns, max(reps, 2 * n_sets)) * 1000.0
+            res[name] = rate(2.0 * Ch * Ch * K * T, 4 * T * Ch * (3 if residual else 2), us)
+        subs = []
+        for R in Rs:
+            c1, c2 = conv(R, 11, 5, "x", "h", False), conv(R, 11, 1, "h", "y", True)
+            subs.append(lambda s, c1=c1, c2=c2: (c1(s), c2(s)))
+        subs[0](cur_stream(torch))
+        us = per_launch_ms(torch, subs, max(reps, 2 * n_sets)) * 1000.0
+        res["sublayer_k11_d5"] = rate(2 * 2.0 * Ch * Ch * 11 * T, 4 * T * Ch * 5, us, launches=2)
         for wt in ws.values():
             wt.close()
         out[f"{Ch}x{T}"] = res
-        del x, h, y
+        del bufs, Rs, x0
     # the upsamplers, leaky_relu(0.1) -> ConvTranspose1d -> crop -> + bias
     # (hift_vocoder.cpp:680-687), on the chain from 750 mel frames:
     # 512x750 -> 256x6000 -> 128x30000 -> 64x90000; algorithmic FLOPs
@@ -603,24 +616,24 @@ def bench_hift_conv(C, W, torch, reps=60):
     ups = {}
     for (Ci, Co, s, K, T) in ((512, 256, 8, 16, 750), (256, 128, 5, 11, 6000), (128, 64, 3, 7, 30000)):
         pad = (K - s) // 2
-        x = d(W.normal(W.seed_of(8, 1000 + Ci), (T, Ci)))
+        T_out = (T - 1) * s + K - 2 * pad
+        nbytes = 4 * (T * Ci + T_out * Co)
+        n_sets = sets_for(nbytes)
+        x0 = d(W.normal(W.seed_of(8, 1000 + Ci), (T, Ci)))
+        bufs = [{"x": x0 if i == 0 else x0.clone(),
+                 "y": torch.empty((T_out, Co), dtype=torch.float32, device="cuda")} for i in range(n_sets)]
         bias = d(W.normal(W.seed_of(8, 1001 + Ci), (Co,), 0.0, 0.1))
         wt = C.Conv1dWeights(d(W.normal(W.seed_of(8, 1002 + Ci), (Ci, Co, K), 0.0, 1.0 / np.sqrt(Ci * K / s))),
                              transpose_stride=s)
-        T_out = (T - 1) * s + K - 2 * pad
-        y = torch.empty((T_out, Co), dtype=torch.float32, device="cuda")
-        R = {k: C.ctypes.byref(C.desc(v)) for k, v in dict(x=x, b=bias, y=y).items()}
-        fn = lambda st: check_rc(C, L.cbx_conv_transpose1d(R["x"], wt.handle, pad, C.CONV_PRO_LEAKY_RELU, None,  # noqa: E731
-                                                           None, 0.1, R["b"], R["y"], st))
-        fn(cur_stream(torch))
-        us = per_launch_ms(torch, [fn], reps) * 1000.0
-        flops = 2.0 * Ci * Co * K * T
-        ups[f"{Ci}x{T}_to_{Co}x{T_out}"] = {
-            "us": us, "TFLOPs": flops / (us * 1e-6) / 1e12,
-            "pct_of_mfma_f16_peak": 100.0 * flops / (us * 1e-6) / 1e12 / PEAK_MFMA_F16_TFLOPS,
-            "GBps": 4.0 * (T * Ci + T_out * Co) / (us * 1e-6) / 1e9}
+        rb = C.ctypes.byref(C.desc(bias))
+        Rs = [{k: C.ctypes.byref(C.desc(v)) for k, v in b.items()} for b in bufs]
+        fns = [lambda st, R=R: check_rc(C, L.cbx_conv_transpose1d(R["x"], wt.handle, pad, C.CONV_PRO_LEAKY_RELU,
+                                                                   None, None, 0.1, rb, R["y"], st)) for R in Rs]
+        fns[0](cur_stream(torch))
+        us = per_launch_ms(torch, fns, max(reps, 2 * n_sets)) * 1000.0
+        ups[f"{Ci}x{T}_to_{Co}x{T_out}"] = rate(2.0 * Ci * Co * K * T, nbytes, us, buffer_sets=n_sets)
         wt.close()
-        del x, y
+        del bufs, Rs, x0
     out["upsample"] = ups
     return out
 
@@ -755,6 +768,10 @@ def traffic_probe(C, W, torch):
     ac, aic = W.snake_alpha(64, 3)
     reps, el = _timed(lambda: O.conv1d(xc, wc, 1, 25, 5, O.CONV_PRO_SNAKE, ac, aic, nth=nth), seconds)
     out["hift_conv_64x2000_k11_d5_GFLOPs"] = 2.0 * 64 * 64 * 11 * 2000 * reps / el / 1e9
+    xu = W.normal(W.seed_of(8, 1100), (500, 128))
+    wu = W.normal(W.seed_of(8, 1101), (128, 64, 7), 0.0, 0.05)
+    reps, el = _timed(lambda: O.conv_transpose1d(xu, wu, 3, 2, O.CONV_PRO_LEAKY, slope=0.1, nth=nth), seconds)
+    out["hift_upsample_128x500_s3_k7_GFLOPs"] = 2.0 * 128 * 64 * 7 * 500 * reps / el / 1e9
 
     blk = W.t3_block_inputs()
     N, D, F = W.N_PREFILL, W.D_MODEL, W.D_FF
@@ -899,6 +916,9 @@ def main():
     C.init(0)
     if a.traffic_probe:
         traffic_probe(C, W, torch)
+        return 0
+    if a.hift_conv:
+        print(json.dumps({"hift_resblock_conv": bench_hift_conv(C, W, torch)}), flush=True)
         return 0
     res = bench_prefill(C, W, torch, a.steps, a.warmup)
     details = {"prefill_f32_fused": {k: v for k, v in res.items()}}
