@@ -63,6 +63,7 @@ struct ConvArgs {
     int32_t crop;               // transposed: outputs cropped from each end
     int64_t w_ph;               // transposed: halves of prepared weights per phase
     int32_t vout;               // c_out % 4 == 0 and 16-byte aligned y, res and bias: float4 stores
+    int32_t n_tt, n_ct;         // time tiles and channel tiles of the grid (work item w = (z*n_tt + t)*n_ct + c)
     float slope;
 };
 
@@ -115,21 +116,36 @@ __device__ __forceinline__ float prologue(float v, float a, float ai, float slop
     }
 }
 
-// WM x WN waves, each computing (MT*32 times) x (NT*32 output channels).
+// WM x WN x KS waves: the output tile is WM x WN wave tiles of (MT*32
+// times) x (NT*32 output channels), and KS waves share each wave tile,
+// splitting the reduction's steps between them (their partial sums are
+// added in LDS at the end, in a fixed order).
 // VEC: c_in % 4 == 0 and 16-byte aligned rows (one float4 per 4 channels).
-// PF: depth of the B fragment ring; it divides every chunk's step count, so
+// PF: depth of the B fragment ring; it divides every wave's step count, so
 // the step loop has no guard and its loads no condition, and the compiler
 // waits for exactly the fragment each step uses.
-template <int PRO, int MT, int NT, int WM, int WN, bool VEC, int PF>
-__global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
+template <int PRO, int MT, int NT, int WM, int WN, int KS, bool VEC, int PF>
+__global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_eu(KS > 1 ? 2 : 1))) void k_conv1d(
+    ConvArgs a) {
     extern __shared__ _Float16 lds[];   // [a.win][a.kch + 8], then alpha and alpha_inv of a chunk (snake)
-    constexpr int BT = WM * MT * 32, BC = WN * NT * 32, NTH = 64 * WM * WN;
+    constexpr int BT = WM * MT * 32, BC = WN * NT * 32, NTH = 64 * WM * WN * KS;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WN, wn = wave % WN;
-    const int t0 = blockIdx.x * BT;
-    const int co0 = blockIdx.y * BC;
-    int bz = blockIdx.z, pad = a.pad, t_out = a.t_out;
+    const int ks = wave / (WM * WN), wt = wave - ks * (WM * WN);
+    const int wm = wt / WN, wn = wt % WN;
+    // workgroup L of a 1-D grid runs on XCD L % 8 (round-robin dispatch);
+    // work items are numbered so that consecutive ones -- the channel tiles
+    // of one time tile, then neighbouring time tiles, which read the same or
+    // overlapping windows -- run on one XCD and meet in its L2
+    const unsigned L = blockIdx.x, n_wg = gridDim.x;
+    const unsigned q8 = n_wg >> 3, r8 = n_wg & 7, xcd = L & 7, j8 = L >> 3;
+    const unsigned w = xcd < r8 ? xcd * (q8 + 1) + j8 : r8 * (q8 + 1) + (xcd - r8) * q8 + j8;
+    const int ct = static_cast<int>(w % static_cast<unsigned>(a.n_ct));
+    const unsigned wr = w / static_cast<unsigned>(a.n_ct);
+    const int tt = static_cast<int>(wr % static_cast<unsigned>(a.n_tt));
+    const int t0 = tt * BT;
+    const int co0 = ct * BC;
+    int bz = static_cast<int>(wr / static_cast<unsigned>(a.n_tt)), pad = a.pad, t_out = a.t_out;
     int64_t y_off = 0, y_step = a.y_nb1, r_off = 0, r_step = a.r_nb1;
     const _Float16* wbase = a.w;
     if (a.up > 1) {
@@ -304,8 +320,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
         const int a_wrap = a.dil * cs - nb * kBlk;            // (k, nb) -> (k + 1, 0)
         const int64_t b_wrap = static_cast<int64_t>(nblk - nb) * 512;
         const int64_t b_first = static_cast<int64_t>(cb0) * 512;
-        const unsigned wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-        const int s_start = static_cast<int>(((wg >> 3) * 3u) % static_cast<unsigned>(n_steps));
+        // this wave's share: n_w consecutive steps (mod n_steps) from its start
+        const int n_w = n_steps / KS;
+        const int s_start = static_cast<int>((j8 * 3u + static_cast<unsigned>(ks * n_w)) % static_cast<unsigned>(n_steps));
         const int k_start = s_start / nb, cb_start = s_start - k_start * nb;
         const int a_start = k_start * a.dil * cs + cb_start * kBlk;
         const int64_t b_start = (static_cast<int64_t>(k_start) * nblk + cb0 + cb_start) * 512;
@@ -345,13 +362,13 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) av[0][mt] = *reinterpret_cast<const half8*>(lds + arow[mt] + aoff);
         next_a();
-        for (int s0 = 0; s0 < n_steps; s0 += PF) {
+        for (int s0 = 0; s0 < n_w; s0 += PF) {
 #pragma unroll
             for (int p = 0; p < PF; p++) {
                 const int s = s0 + p;
                 const int cur = p & 1;   // PF is even: the parity of s
                 // A of step s + 1 (past the end: the first step's again, unused)
-                const int an = s + 1 < n_steps ? aoff : a_start;
+                const int an = s + 1 < n_w ? aoff : a_start;
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) av[cur ^ 1][mt] = *reinterpret_cast<const half8*>(lds + arow[mt] + an);
                 next_a();
@@ -364,7 +381,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
                     }
                 }
                 // B of step s + PF (past the end: the first step's again, unused)
-                const int64_t bn = s + PF < n_steps ? boff : b_start;
+                const int64_t bn = s + PF < n_w ? boff : b_start;
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) ring[p][nt] = *reinterpret_cast<const half8*>(wf[nt] + bn);
                 next_b();
@@ -378,21 +395,31 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
     // segment of NT*32 channels per NT*8 lanes.
     __syncthreads();
     constexpr int EPS = NT * 32 + 4;   // tile row stride in floats
-    float* ep = reinterpret_cast<float*>(lds) + wave * (MT * 32 * EPS);
+    float* ep = reinterpret_cast<float*>(lds) + wt * (MT * 32 * EPS);
+    // the KS partial sums of a wave tile meet in its LDS tile: wave ks = 1
+    // writes its sum, ks = 2 .. KS-1 add theirs in turn, ks = 0 adds last
+    // (one barrier per turn; with KS = 1 wave 0 just writes)
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
+    for (int turn = 1; turn <= KS; turn++) {
+        if (ks == turn % KS) {
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
+            for (int mt = 0; mt < MT; mt++) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                ep[(mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * EPS + nt * 32 + lrow] = acc[mt][nt][r];
+                for (int nt = 0; nt < NT; nt++) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        float* e = ep + (mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * EPS + nt * 32 + lrow;
+                        *e = turn == 1 ? acc[mt][nt][r] : *e + acc[mt][nt][r];
+                    }
+                }
             }
         }
+        __syncthreads();
     }
-    __syncthreads();
     const int64_t yb = static_cast<int64_t>(bz) * a.y_nb2 + y_off;
     const int64_t rb = static_cast<int64_t>(bz) * a.r_nb2 + r_off;
     const int tw = t0 + wm * MT * 32, cw = co0 + wn * NT * 32;
+    // wave ks of the KS that share the wave tile stores every KS-th group of rows
     if (a.vout) {
         constexpr int CPR = NT * 8;      // float4 per tile row
         constexpr int RPI = 64 / CPR;    // tile rows per store instruction
@@ -401,7 +428,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
         float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
         if (a.bias && cok) bv = *reinterpret_cast<const float4*>(a.bias + co);
 #pragma unroll 4
-        for (int rl = lane / CPR; rl < MT * 32; rl += RPI) {
+        for (int rl = lane / CPR + ks * RPI; rl < MT * 32; rl += RPI * KS) {
             const int t = tw + rl;
             if (t < t_out && cok) {
                 float4 v = *reinterpret_cast<const float4*>(ep + rl * EPS + c4);
@@ -416,7 +443,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_conv1d(ConvArgs a) {
             }
         }
     } else {
-        for (int i = lane; i < MT * 32 * NT * 32; i += 64) {
+        for (int i = lane + ks * 64; i < MT * 32 * NT * 32; i += 64 * KS) {
             const int rl = i / (NT * 32), c = i % (NT * 32);
             const int t = tw + rl, co = cw + c;
             if (t < t_out && co < a.c_out) {
@@ -468,47 +495,57 @@ __global__ __launch_bounds__(256) void k_conv_weights(WPrep p, _Float16* out) {
 }
 
 struct Tile {
-    int mt, nt, wm, wn;
+    int mt, nt, wm, wn, ks;   // ks: the most waves that share a wave tile (split of the reduction)
     int bt() const { return wm * mt * 32; }
     int bc() const { return wn * nt * 32; }
-    int threads() const { return 64 * wm * wn; }
 };
 
 template <typename K>
 void conv_launch(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, const ConvArgs& a) {
-    // windows past 64 KiB use the larger LDS of gfx950 (160 KiB per workgroup)
+    // windows past 64 KiB use the larger LDS of gfx950 (160 KiB per
+    // workgroup): raise the kernel's limit once per device
     if (lds > 64 * 1024) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  static_cast<int>(lds));
+        constexpr int kDevs = 64;
+        static bool raised[kDevs] = {};
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevs || !raised[dev]) {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsMax));
+            if (dev >= 0 && dev < kDevs) raised[dev] = true;
+        }
     }
     hipLaunchKernelGGL(kernel, grid, block, lds, s, a);
 }
 
-template <int PRO, int MT, int NT, int WM, int WN>
+// (VEC, PF) in {(1, 4), (1, 2), (0, 2)}: unaligned rows take the shorter ring
+template <int PRO, int MT, int NT, int WM, int WN, int KS>
 void conv_go(bool vec, bool pf4, dim3 grid, size_t lds, hipStream_t s, const ConvArgs& a) {
-    const dim3 block(64 * WM * WN);
-    if (pf4) {
-        if (vec) conv_launch(k_conv1d<PRO, MT, NT, WM, WN, true, 4>, grid, block, lds, s, a);
-        else conv_launch(k_conv1d<PRO, MT, NT, WM, WN, false, 4>, grid, block, lds, s, a);
-    } else {
-        if (vec) conv_launch(k_conv1d<PRO, MT, NT, WM, WN, true, 2>, grid, block, lds, s, a);
-        else conv_launch(k_conv1d<PRO, MT, NT, WM, WN, false, 2>, grid, block, lds, s, a);
-    }
+    const dim3 block(64 * WM * WN * KS);
+    if (!vec) conv_launch(k_conv1d<PRO, MT, NT, WM, WN, KS, false, 2>, grid, block, lds, s, a);
+    else if (pf4) conv_launch(k_conv1d<PRO, MT, NT, WM, WN, KS, true, 4>, grid, block, lds, s, a);
+    else conv_launch(k_conv1d<PRO, MT, NT, WM, WN, KS, true, 2>, grid, block, lds, s, a);
+}
+
+template <int PRO, int MT, int NT, int WM, int WN, int KSMAX>
+void conv_ks(int ks, bool vec, bool pf4, dim3 grid, size_t lds, hipStream_t s, const ConvArgs& a) {
+    if (ks == KSMAX) conv_go<PRO, MT, NT, WM, WN, KSMAX>(vec, pf4, grid, lds, s, a);
+    else if (KSMAX == 4 && ks == 2) conv_go<PRO, MT, NT, WM, WN, (KSMAX == 4 ? 2 : 1)>(vec, pf4, grid, lds, s, a);
+    else conv_go<PRO, MT, NT, WM, WN, 1>(vec, pf4, grid, lds, s, a);
 }
 
 // the tile shapes below, by index
 template <int PRO>
-void conv_tile(int t, bool vec, bool pf4, dim3 grid, size_t lds, hipStream_t s, const ConvArgs& a) {
+void conv_tile(int t, int ks, bool vec, bool pf4, dim3 grid, size_t lds, hipStream_t s, const ConvArgs& a) {
     switch (t) {
-        case 0: conv_go<PRO, 4, 2, 2, 1>(vec, pf4, grid, lds, s, a); break;   // 256 x 64, 2 waves
-        case 1: conv_go<PRO, 4, 2, 1, 2>(vec, pf4, grid, lds, s, a); break;   // 128 x 128, 2 waves
-        case 2: conv_go<PRO, 2, 2, 1, 2>(vec, pf4, grid, lds, s, a); break;   // 64 x 128, 2 waves
-        case 3: conv_go<PRO, 2, 2, 1, 1>(vec, pf4, grid, lds, s, a); break;   // 64 x 64, 1 wave
-        default: conv_go<PRO, 4, 1, 2, 1>(vec, pf4, grid, lds, s, a); break;  // 256 x 32, 2 waves
+        case 0: conv_ks<PRO, 4, 2, 2, 1, 2>(ks, vec, pf4, grid, lds, s, a); break;   // 256 x 64
+        case 1: conv_ks<PRO, 4, 2, 1, 2, 2>(ks, vec, pf4, grid, lds, s, a); break;   // 128 x 128
+        case 2: conv_ks<PRO, 2, 2, 1, 2, 2>(ks, vec, pf4, grid, lds, s, a); break;   // 64 x 128
+        case 3: conv_ks<PRO, 2, 2, 1, 1, 4>(ks, vec, pf4, grid, lds, s, a); break;   // 64 x 64
+        default: conv_ks<PRO, 4, 1, 2, 1, 2>(ks, vec, pf4, grid, lds, s, a); break;  // 256 x 32
     }
 }
 
-constexpr Tile kTiles[5] = {{4, 2, 2, 1}, {4, 2, 1, 2}, {2, 2, 1, 2}, {2, 2, 1, 1}, {4, 1, 2, 1}};
+constexpr Tile kTiles[5] = {{4, 2, 2, 1, 2}, {4, 2, 1, 2, 2}, {2, 2, 1, 2, 2}, {2, 2, 1, 1, 4}, {4, 1, 2, 1, 2}};
 
 }  // namespace
 
@@ -599,8 +636,17 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     a.win = static_cast<int32_t>(win);
     a.kch = static_cast<int32_t>(kch);
     const Tile& t = kTiles[ti];
-    // the window (+ snake's alpha, alpha_inv and flag), then the output tile
-    // of every wave (rows of NT*32 + 4 floats) in the same memory
+    // waves per wave tile: the most (ks, ks/2, .., 1) whose share of every
+    // chunk's steps (K * channels / 16) is even -- a multiple of 4 for the
+    // 4-deep ring
+    const int64_t last = c_in_pad - (cdiv(c_in_pad, kch) - 1) * kch;
+    const int64_t n_full = k * (kch / kBlk), n_last = k * (last / kBlk);
+    auto steps_ok = [&](int ks_, int pf) { return n_full % (ks_ * pf) == 0 && n_last % (ks_ * pf) == 0; };
+    int ks = t.ks;
+    while (ks > 1 && !steps_ok(ks, 2)) ks /= 2;
+    const bool pf4 = steps_ok(ks, 4);
+    // the window (+ snake's alpha, alpha_inv and flag), then the output
+    // tile of every wave tile (rows of NT*32 + 4 floats) in the same memory
     const size_t win_bytes = static_cast<size_t>(win) * static_cast<size_t>(kch + 8) * sizeof(_Float16) +
                              (pro == PRO_SNAKE ? (2 * static_cast<size_t>(kch) + 4) * sizeof(float) : 0);
     const size_t out_bytes = static_cast<size_t>(t.wm * t.wn) * t.mt * 32 * (t.nt * 32 + 4) * sizeof(float);
@@ -611,15 +657,15 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     const bool one = x->ne[2] <= 1;
     a.vout = c_out % 4 == 0 && al16(a.y) && a.y_nb1 % 16 == 0 && (one || a.y_nb2 % 16 == 0) &&
              (!a.bias || al16(a.bias)) && (!a.res || (al16(a.res) && a.r_nb1 % 16 == 0 && (one || a.r_nb2 % 16 == 0)));
-    const dim3 grid(static_cast<unsigned>(cdiv(rows, t.bt())), static_cast<unsigned>(cdiv(c_out, t.bc())),
-                    static_cast<unsigned>(batch));
-    // every chunk's step count (K * channels / 16) is even; a ring of 4 when all are multiples of 4
-    const int64_t last = c_in_pad - (cdiv(c_in_pad, kch) - 1) * kch;
-    const bool pf4 = (k * (kch / kBlk)) % 4 == 0 && (k * (last / kBlk)) % 4 == 0;
+    a.n_tt = static_cast<int32_t>(cdiv(rows, t.bt()));
+    a.n_ct = static_cast<int32_t>(cdiv(c_out, t.bc()));
+    const int64_t n_items = static_cast<int64_t>(a.n_tt) * a.n_ct * batch;
+    if (n_items >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "conv1d: too many output tiles");
+    const dim3 grid(static_cast<unsigned>(n_items));
     switch (pro) {
-        case PRO_SNAKE: conv_tile<PRO_SNAKE>(ti, vec, pf4, grid, lds, s, a); break;
-        case PRO_LEAKY: conv_tile<PRO_LEAKY>(ti, vec, pf4, grid, lds, s, a); break;
-        default: conv_tile<PRO_NONE>(ti, vec, pf4, grid, lds, s, a); break;
+        case PRO_SNAKE: conv_tile<PRO_SNAKE>(ti, ks, vec, pf4, grid, lds, s, a); break;
+        case PRO_LEAKY: conv_tile<PRO_LEAKY>(ti, ks, vec, pf4, grid, lds, s, a); break;
+        default: conv_tile<PRO_NONE>(ti, ks, vec, pf4, grid, lds, s, a); break;
     }
     return check_launch("conv1d");
 }
