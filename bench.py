@@ -763,16 +763,6 @@ def traffic_probe(C, W, torch):
                                           r["ya"], s))
     torch.cuda.synchronize()
     cache.close()
-    xc = W.normal(W.seed_of(8, 64), (2000, 64))
-    wc = W.normal(W.seed_of(8, 75), (64, 64, 11), 0.0, 0.04)
-    ac, aic = W.snake_alpha(64, 3)
-    reps, el = _timed(lambda: O.conv1d(xc, wc, 1, 25, 5, O.CONV_PRO_SNAKE, ac, aic, nth=nth), seconds)
-    out["hift_conv_64x2000_k11_d5_GFLOPs"] = 2.0 * 64 * 64 * 11 * 2000 * reps / el / 1e9
-    xu = W.normal(W.seed_of(8, 1100), (500, 128))
-    wu = W.normal(W.seed_of(8, 1101), (128, 64, 7), 0.0, 0.05)
-    reps, el = _timed(lambda: O.conv_transpose1d(xu, wu, 3, 2, O.CONV_PRO_LEAKY, slope=0.1, nth=nth), seconds)
-    out["hift_upsample_128x500_s3_k7_GFLOPs"] = 2.0 * 128 * 64 * 7 * 500 * reps / el / 1e9
-
     blk = W.t3_block_inputs()
     N, D, F = W.N_PREFILL, W.D_MODEL, W.D_FF
     blk_sets = []
@@ -844,7 +834,7 @@ def cpu_other_workloads(W, O, nth, seconds):
     """The oracle on the other workloads' shapes (same inputs as the GPU
     legs), a bounded sample each: decode step chain (us per step), the
     64-stream f16 step, a CFM flow step, a T3 block's element-wise nodes,
-    two HiFT stages."""
+    two HiFT stages' activations, a ResBlock conv and an upsampler."""
     out = {}
     steps = [W.decode_inputs(t) for t in range(W.DECODE_STEPS)]
 
@@ -897,6 +887,15 @@ def cpu_other_workloads(W, O, nth, seconds):
         out[f"hift_snake_{B}x{Ch}x{T}_GBps"] = (8 * x.size + 8 * Ch) * reps / el / 1e9
         reps, el = _timed(lambda: O.leaky_relu(x, 0.1, nth=nth), seconds)
         out[f"hift_leaky_{B}x{Ch}x{T}_GBps"] = 8 * x.size * reps / el / 1e9
+    xc = W.normal(W.seed_of(8, 64), (2000, 64))
+    wc = W.normal(W.seed_of(8, 75), (64, 64, 11), 0.0, 0.04)
+    ac, aic = W.snake_alpha(64, 3)
+    reps, el = _timed(lambda: O.conv1d(xc, wc, 1, 25, 5, O.CONV_PRO_SNAKE, ac, aic, nth=nth), seconds)
+    out["hift_conv_64x2000_k11_d5_GFLOPs"] = 2.0 * 64 * 64 * 11 * 2000 * reps / el / 1e9
+    xu = W.normal(W.seed_of(8, 1100), (500, 128))
+    wu = W.normal(W.seed_of(8, 1101), (128, 64, 7), 0.0, 0.05)
+    reps, el = _timed(lambda: O.conv_transpose1d(xu, wu, 3, 2, O.CONV_PRO_LEAKY, slope=0.1, nth=nth), seconds)
+    out["hift_upsample_128x500_s3_k7_GFLOPs"] = 2.0 * 128 * 64 * 7 * 500 * reps / el / 1e9
     return out
 
 
