@@ -396,6 +396,19 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
     __syncthreads();
     constexpr int EPS = NT * 32 + 4;   // tile row stride in floats
     float* ep = reinterpret_cast<float*>(lds) + wt * (MT * 32 * EPS);
+    const int64_t yb = static_cast<int64_t>(bz) * a.y_nb2 + y_off;
+    const int64_t rb = static_cast<int64_t>(bz) * a.r_nb2 + r_off;
+    const int tw = t0 + wm * MT * 32, cw = co0 + wn * NT * 32;
+    // vout: wave ks of the KS that share the wave tile stores NIT row groups
+    // of RPI rows, one float4 per lane; its residual float4s are read before
+    // the last turn's barrier, all at once (the accumulators are in LDS by
+    // then), so their latency overlaps the tile exchange
+    constexpr int CPR = NT * 8;                    // float4 per tile row
+    constexpr int RPI = 64 / CPR;                  // tile rows per store instruction
+    constexpr int NIT = MT * 32 / (RPI * KS);
+    const int c4 = (lane % CPR) * 4, co4 = cw + c4, rl0 = lane / CPR + ks * RPI;
+    const bool cok = co4 < a.c_out;                // c_out % 4 == 0: the whole float4
+    float4 q[NIT];
     // the KS partial sums of a wave tile meet in its LDS tile: wave ks = 1
     // writes its sum, ks = 2 .. KS-1 add theirs in turn, ks = 0 adds last
     // (one barrier per turn; with KS = 1 wave 0 just writes)
@@ -414,31 +427,28 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
                 }
             }
         }
+        if (turn == KS && a.vout && a.res) {
+#pragma unroll
+            for (int i = 0; i < NIT; i++) {
+                const int t = tw + rl0 + i * RPI * KS;
+                const int tc = t < t_out ? t : t_out - 1;
+                q[i] = *reinterpret_cast<const float4*>(a.res + rb + static_cast<int64_t>(tc) * r_step +
+                                                        static_cast<int64_t>(cok ? co4 : 0) * 4);
+            }
+        }
         __syncthreads();
     }
-    const int64_t yb = static_cast<int64_t>(bz) * a.y_nb2 + y_off;
-    const int64_t rb = static_cast<int64_t>(bz) * a.r_nb2 + r_off;
-    const int tw = t0 + wm * MT * 32, cw = co0 + wn * NT * 32;
-    // wave ks of the KS that share the wave tile stores every KS-th group of rows
     if (a.vout) {
-        constexpr int CPR = NT * 8;      // float4 per tile row
-        constexpr int RPI = 64 / CPR;    // tile rows per store instruction
-        const int c4 = (lane % CPR) * 4, co = cw + c4;
-        const bool cok = co < a.c_out;   // c_out % 4 == 0: the whole float4
         float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (a.bias && cok) bv = *reinterpret_cast<const float4*>(a.bias + co);
-#pragma unroll 4
-        for (int rl = lane / CPR + ks * RPI; rl < MT * 32; rl += RPI * KS) {
-            const int t = tw + rl;
+        if (a.bias && cok) bv = *reinterpret_cast<const float4*>(a.bias + co4);
+#pragma unroll
+        for (int i = 0; i < NIT; i++) {
+            const int rl = rl0 + i * RPI * KS, t = tw + rl;
             if (t < t_out && cok) {
                 float4 v = *reinterpret_cast<const float4*>(ep + rl * EPS + c4);
                 if (a.bias) v = make_float4(v.x + bv.x, v.y + bv.y, v.z + bv.z, v.w + bv.w);
-                if (a.res) {
-                    const float4 q = *reinterpret_cast<const float4*>(a.res + rb + static_cast<int64_t>(t) * r_step +
-                                                                      static_cast<int64_t>(co) * 4);
-                    v = make_float4(q.x + v.x, q.y + v.y, q.z + v.z, q.w + v.w);
-                }
-                *reinterpret_cast<float4*>(a.y + yb + static_cast<int64_t>(t) * y_step + static_cast<int64_t>(co) * 4) =
+                if (a.res) v = make_float4(q[i].x + v.x, q[i].y + v.y, q[i].z + v.z, q[i].w + v.w);
+                *reinterpret_cast<float4*>(a.y + yb + static_cast<int64_t>(t) * y_step + static_cast<int64_t>(co4) * 4) =
                     v;
             }
         }
