@@ -245,6 +245,12 @@ def desc(t: torch.Tensor, ggml_type: Optional[int] = None) -> Tensor:
     if t.numel() == 0:
         t = t.contiguous()
     strides = [s * es for s in t.stride()[::-1]] or [es]
+    # a dimension of extent 1 is never stepped over: give it the stride a
+    # contiguous tensor would have (torch leaves 0 there after indexing with
+    # None or expand), as ggml does for its trivial dimensions
+    for k in range(len(shape)):
+        if shape[k] == 1:
+            strides[k] = es if k == 0 else strides[k - 1] * shape[k - 1]
     row_bytes = strides[-1] * shape[-1]
     if ggml_type == Q8_0:
         if t.dtype != torch.uint8 or t.shape[-1] % Q8_0_BLOCK or t.stride(-1) != 1:

@@ -83,3 +83,17 @@ def test_descriptor_from_torch_cpu_tensor():
     v = torch.zeros((6, 10))[:, 2:8]
     dv = C.desc(v)
     assert list(dv.ne)[:2] == [6, 6] and list(dv.nb)[:2] == [4, 40]
+
+
+def test_descriptor_of_extent_one_dims():
+    """Dimensions of extent 1 get contiguous strides whatever torch reports
+    for them (0 after None-indexing or expand): they are never stepped over,
+    and the library checks nb[0] against the element size."""
+    import torch
+
+    w = torch.eye(4)[:, :, None]              # torch strides (4, 1, 0)
+    d = C.desc(w)
+    assert list(d.ne) == [1, 4, 4, 1] and list(d.nb) == [4, 4, 16, 64]
+    b = torch.zeros(5).expand(1, 5)          # stride 0 on the leading extent-1 dim
+    db = C.desc(b)
+    assert list(db.ne) == [5, 1, 1, 1] and list(db.nb) == [4, 20, 20, 20]

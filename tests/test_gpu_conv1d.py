@@ -193,3 +193,26 @@ def test_snake_large_arguments(cbx, oracle):
     b = W.normal(72, (C,), 0.0, 0.1)
     got = run(cbx, x, w, 1, 1, 1, cbx.CONV_PRO_SNAKE, alpha, alpha_inv, 0.0, b, None)
     check(oracle, got, x, w, 1, 1, 1, oracle.CONV_PRO_SNAKE, alpha, alpha_inv, 0.0, b, None, "large sin arguments")
+
+
+def test_snake_prologue_alone(cbx, oracle):
+    """K = 1 with the identity weight: the conv returns the staged f16
+    operand itself, f16(snake(x)), so this compares the kernel's snake
+    (its own sin for |alpha x| < 2^16) with the oracle's glibc-sinf snake
+    element by element.  Both round an f32 result to f16; they may differ
+    by one f16 step where the f32 values straddle a rounding midpoint (the
+    two sins differ by an f32 ulp or two): at most 1 in 10^4 elements, and
+    never by more than one step."""
+    C, T = 128, 4000
+    x = W.normal(90, (T, C), 0.0, 2.0)
+    alpha, alpha_inv = W.snake_alpha(C, 5)
+    eye = np.eye(C, dtype=np.float32)[:, :, None]
+    got = run(cbx, x, eye, 1, 0, 1, cbx.CONV_PRO_SNAKE, alpha, alpha_inv, 0.0, None, None)
+    ref = oracle.snake(x, alpha, alpha_inv).astype(np.float16)
+    g16 = got.astype(np.float16)
+    assert np.array_equal(got, g16.astype(np.float32)), "identity conv output is not an f16 value"
+    diff = g16 != ref
+    d = np.abs(g16.astype(np.float64) - ref.astype(np.float64))
+    step = np.spacing(np.maximum(np.abs(g16), np.abs(ref))).astype(np.float64)
+    assert np.all(d[diff] <= step[diff]), "snake differs by more than one f16 step"
+    assert diff.sum() <= x.size // 10000, f"{int(diff.sum())} of {x.size} f16 values differ"
