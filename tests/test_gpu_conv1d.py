@@ -216,3 +216,13 @@ def test_snake_prologue_alone(cbx, oracle):
     step = np.spacing(np.maximum(np.abs(g16), np.abs(ref))).astype(np.float64)
     assert np.all(d[diff] <= step[diff]), "snake differs by more than one f16 step"
     assert diff.sum() <= x.size // 10000, f"{int(diff.sum())} of {x.size} f16 values differ"
+
+
+def test_input_channels_in_chunks(cbx, oracle):
+    """512 channels with K 11 dilation 15: the 64-frame tile's window (214
+    rows) holds only 352 channels in 160 KiB of LDS, so the kernel runs two
+    channel chunks (352 + 160), each staging its own snake alpha."""
+    x, w, al, ai, b, r, sl = case(oracle, 512, 700, 512, 11, 1, 75, 15, oracle.CONV_PRO_SNAKE, with_res=True,
+                                  seed=77)
+    got = run(cbx, x, w, 1, 75, 15, cbx.CONV_PRO_SNAKE, al, ai, sl, b, r)
+    check(oracle, got, x, w, 1, 75, 15, oracle.CONV_PRO_SNAKE, al, ai, sl, b, r, "C512 K11 d15, two chunks")

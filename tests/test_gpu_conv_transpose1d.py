@@ -121,3 +121,13 @@ def test_errors(cbx):
     assert L.cbx_conv_transpose1d_weights_create(d(wt), 0, None, ctypes.byref(h)) == cbx.ERR_INVALID_ARG
     wts.close()
     plain.close()
+
+
+def test_input_channels_in_chunks(cbx, oracle):
+    """2048 input channels: a 65-row window of all of them needs 267 KB, so
+    the phases run in channel chunks."""
+    x = W.normal(84, (200, 2048), 0.0, 1.0)
+    w = W.normal(85, (2048, 64, 4), 0.0, 0.02)
+    b = W.normal(86, (64,), 0.0, 0.1)
+    got = run(cbx, x, w, 2, 1, cbx.CONV_PRO_LEAKY_RELU, 0.1, b)
+    check(oracle, got, x, w, 2, 1, oracle.CONV_PRO_LEAKY, 0.1, b, "C_in 2048, s2 K4, chunked")
