@@ -125,18 +125,54 @@ __device__ __forceinline__ float4 gn_apply4(const GnArgs& a, float4 d, float sca
     return o;
 }
 
+// f64 sum of a thread's NV partials (each the sum of one float4's four
+// terms) as a tree: log-depth instead of a chain of 4*NV dependent adds.
+template <int NV>
+__device__ __forceinline__ double thread_tree_sum(double (&p)[NV]) {
+#pragma unroll
+    for (int w = 1; w < NV; w *= 2) {
+#pragma unroll
+        for (int i = 0; i + w < NV; i += 2 * w) p[i] += p[i + w];
+    }
+    return p[0];
+}
+
+// Sum over the kThreads threads: each wave's total (DPP butterfly), then
+// wave 0 adds the kThreads/64 totals with the same butterfly and leaves the
+// result in scratch[slot] for everyone.  Fixed order: every workgroup that
+// reduces the same values gets the same bits.  Two barriers; a second call
+// with another slot needs none before it.
+__device__ __forceinline__ double block_sum_tree(double v, double* scratch, int slot) {
+    constexpr int NW = kThreads / WAVE;
+    static_assert(NW <= 16, "one DPP row of wave totals");
+    v = wave_sum(v);
+    const int lane = threadIdx.x % WAVE, wid = threadIdx.x / WAVE;
+    if (lane == 0) scratch[wid] = v;
+    __syncthreads();
+    if (wid == 0) {
+        double t = lane < NW ? scratch[lane] : 0.0;
+        t += dpp_f64<0xB1>(t);
+        t += dpp_f64<0x4E>(t);
+        t += dpp_f64<0x141>(t);
+        t += dpp_f64<0x140>(t);
+        if (lane == 0) scratch[slot] = t;
+    }
+    __syncthreads();
+    return scratch[slot];
+}
+
 // Contiguous groups (ne0 % 4 == 0, ne0 x ne1 dense per channel, channels
 // adjacent, 16-byte aligned), split over n_chunks workgroups per group so a
 // few large groups still fill the chip.  Every workgroup of a group reads
 // the whole group into registers and computes the same statistics (same
 // lanes, same order: bit-identical mean and scale), then writes only its
-// chunk.  Workgroups are dealt to the 8 XCDs round-robin by index, so the
-// chunks of one group are given indices that land on one XCD: its L2 serves
-// the repeated reads of the group and HBM sees it once.  With one chunk the
-// output comes straight from registers.
+// chunk, from the registers that hold it.  Workgroups are dealt to the 8
+// XCDs round-robin by index, so the chunks of one group are given indices
+// that land on one XCD: its L2 serves the repeated reads of the group and
+// HBM sees it once.
 template <int NV, bool ACT>
 __global__ __launch_bounds__(kThreads) void k_group_norm_vec(GnArgs a, uint32_t n_chunks, uint32_t n_gi) {
-    __shared__ double red[kThreads / WAVE];
+    __shared__ double red[kThreads / WAVE + 2];
     const uint32_t b = blockIdx.x;
     const uint32_t j = b / kXcds;
     const uint32_t m = j / n_chunks;
@@ -156,61 +192,73 @@ __global__ __launch_bounds__(kThreads) void k_group_norm_vec(GnArgs a, uint32_t 
     char* yg = a.y.data + c0 * a.y.nb[2] + i3 * a.y.nb[3];
     const uint32_t per_ch = static_cast<uint32_t>(a.x.ne[0] * a.x.ne[1]);
 
-    // unconditional 16-byte loads (clamped addresses) keep all NV in flight
-    float4 v[NV];
-#pragma unroll
-    for (int k = 0; k < NV; k++) {
-        const int64_t e = (threadIdx.x + static_cast<int64_t>(k) * kThreads) * 4;
-        v[k] = *reinterpret_cast<const float4*>(xg + 4 * (e < count ? e : 0));
-    }
-    double s = 0.0;
-#pragma unroll
-    for (int k = 0; k < NV; k++) {
-        const int64_t e = (threadIdx.x + static_cast<int64_t>(k) * kThreads) * 4;
-        if (e >= count) v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int q = 0; q < 4; q++) s += static_cast<double>(get(v[k], q));
-    }
-    s = block_sum(s, red);
-    const float mean = static_cast<float>(s / static_cast<double>(count));
-    double s2 = 0.0;
-#pragma unroll
-    for (int k = 0; k < NV; k++) {
-        const int64_t e = (threadIdx.x + static_cast<int64_t>(k) * kThreads) * 4;
-        if (e < count) {   // count % 4 == 0: a vector is all in or all out
-            const float4 d = make_float4(v[k].x - mean, v[k].y - mean, v[k].z - mean, v[k].w - mean);
-            v[k] = d;
-            s2 += static_cast<double>(d.x * d.x);
-            s2 += static_cast<double>(d.y * d.y);
-            s2 += static_cast<double>(d.z * d.z);
-            s2 += static_cast<double>(d.w * d.w);
-        }
-    }
-    s2 = block_sum(s2, red);
-    const float var = static_cast<float>(s2 / static_cast<double>(count));
-    const float scale = 1.0f / sqrtf(var + a.eps);
-    if (!live) return;   // uniform across the workgroup
-
-    if (n_chunks == 1) {
-#pragma unroll
-        for (int k = 0; k < NV; k++) {
-            const int64_t e = (threadIdx.x + static_cast<int64_t>(k) * kThreads) * 4;
-            if (e >= count) continue;
-            const int64_t c = c0 + static_cast<uint32_t>(e) / per_ch;
-            *reinterpret_cast<float4*>(yg + 4 * e) = gn_apply4<ACT>(a, v[k], scale, c);
-        }
-        return;
-    }
-    // this workgroup's chunk, re-read from L2 with one vector per lane
+    // this workgroup's chunk: float4 indices [q0, q1) of the group
     const int64_t n4 = count / 4;
     const int64_t per = (n4 + n_chunks - 1) / n_chunks;
     const int64_t q0 = ci * per;
     const int64_t q1 = q0 + per < n4 ? q0 + per : n4;
-    for (int64_t q = q0 + threadIdx.x; q < q1; q += kThreads) {
-        const float4 xv = *reinterpret_cast<const float4*>(xg + 16 * q);
-        const float4 d = make_float4(xv.x - mean, xv.y - mean, xv.z - mean, xv.w - mean);
-        const int64_t c = c0 + static_cast<uint32_t>(4 * q) / per_ch;
-        Stream<float>::store4(yg + 16 * q, gn_apply4<ACT>(a, d, scale, c));
+    // unconditional 16-byte loads (clamped addresses) keep all NV in flight;
+    // up to NV = 8 the affine values of the channel of each vector this
+    // workgroup stores are loaded with them (a vector lies in one channel:
+    // ne0 % 4 == 0), past that (128 registers a thread) when it is stored
+    constexpr bool kEarly = NV <= 8;
+    float4 v[NV];
+    float wv[kEarly ? NV : 1], bv[kEarly ? NV : 1];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t qi = threadIdx.x + static_cast<int64_t>(k) * kThreads;
+        v[k] = *reinterpret_cast<const float4*>(xg + 16 * (qi < n4 ? qi : 0));
+        if constexpr (kEarly) {
+            wv[k] = 1.0f;
+            bv[k] = 0.0f;
+            if (qi >= q0 && qi < q1) {   // only the vectors this workgroup stores
+                const int64_t c = c0 + static_cast<uint32_t>(4 * qi) / per_ch;
+                if (a.w) wv[k] = a.w[c];
+                if (a.b) bv[k] = a.b[c];
+            }
+        }
+    }
+    double p[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t qi = threadIdx.x + static_cast<int64_t>(k) * kThreads;
+        if (qi >= n4) v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        p[k] = (static_cast<double>(v[k].x) + static_cast<double>(v[k].y)) +
+               (static_cast<double>(v[k].z) + static_cast<double>(v[k].w));
+    }
+    const double s = block_sum_tree(thread_tree_sum<NV>(p), red, kThreads / WAVE);
+    const float mean = static_cast<float>(s / static_cast<double>(count));
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t qi = threadIdx.x + static_cast<int64_t>(k) * kThreads;
+        const bool in = qi < n4;   // count % 4 == 0: a vector is all in or all out
+#pragma unroll
+        for (int e = 0; e < 4; e++) set(v[k], e, in ? get(v[k], e) - mean : 0.0f);
+        p[k] = (static_cast<double>(v[k].x * v[k].x) + static_cast<double>(v[k].y * v[k].y)) +
+               (static_cast<double>(v[k].z * v[k].z) + static_cast<double>(v[k].w * v[k].w));
+    }
+    const double s2 = block_sum_tree(thread_tree_sum<NV>(p), red, kThreads / WAVE + 1);
+    const float var = static_cast<float>(s2 / static_cast<double>(count));
+    const float scale = 1.0f / sqrtf(var + a.eps);
+    if (!live) return;   // uniform across the workgroup
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t qi = threadIdx.x + static_cast<int64_t>(k) * kThreads;
+        if (qi < q0 || qi >= q1) continue;
+        const int64_t c = c0 + static_cast<uint32_t>(4 * qi) / per_ch;
+        const float wk = kEarly ? wv[kEarly ? k : 0] : (a.w ? a.w[c] : 1.0f);
+        const float bk = kEarly ? bv[kEarly ? k : 0] : (a.b ? a.b[c] : 0.0f);
+        float4 o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float t = get(v[k], e) * scale;
+            if (a.w) t = t * wk;
+            if (a.b) t = t + bk;
+            if constexpr (ACT) t = apply_act(a.act, t, a.tab, 0.0f);
+            set(o, e, t);
+        }
+        if (n_chunks == 1) *reinterpret_cast<float4*>(yg + 16 * qi) = o;
+        else Stream<float>::store4(yg + 16 * qi, o);
     }
 }
 
