@@ -89,6 +89,8 @@ class GNode(ctypes.Structure):
         ("iparam", ctypes.c_int32),
         ("fparam", ctypes.c_float),
         ("rope", ctypes.c_void_p),
+        ("conv", ctypes.c_int32 * 3),
+        ("conv_w", ctypes.c_void_p),
     ]
 
 
@@ -105,11 +107,14 @@ class GLaunch(ctypes.Structure):
 
 # cbx_gop
 GOP_VIEW, GOP_GET_ROWS, GOP_ADD, GOP_MUL, GOP_SCALE, GOP_NORM, GOP_RMS_NORM, GOP_GROUP_NORM, GOP_ROPE, \
-    GOP_SOFT_MAX, GOP_DIAG_MASK_INF, GOP_UNARY, GOP_LEAKY_RELU, GOP_CPY = range(14)
+    GOP_SOFT_MAX, GOP_DIAG_MASK_INF, GOP_UNARY, GOP_LEAKY_RELU, GOP_CPY, GOP_IM2COL, GOP_MUL_MAT, \
+    GOP_CONV_TRANSPOSE_1D = range(17)
 # cbx_glaunch_kind
 GL_UNSUPPORTED, GL_VIEW, GL_GET_ROWS, GL_GET_ROWS_ADD, GL_GET_ROWS_ADD_LAYER_NORM, GL_NORM, GL_LAYER_NORM, \
     GL_LAYER_NORM_ROPE, GL_RMS_NORM, GL_GROUP_NORM, GL_SOFT_MAX, GL_SNAKE, GL_UNARY, GL_SWIGLU, GL_LEAKY_RELU, \
-    GL_ROPE, GL_CPY, GL_ADD_LAYER_NORM, GL_LAYER_NORM_MASK, GL_BIAS_ACT = range(20)
+    GL_ROPE, GL_CPY, GL_ADD_LAYER_NORM, GL_LAYER_NORM_MASK, GL_BIAS_ACT, GL_CONV1D, GL_CONV_TRANSPOSE1D = range(22)
+# conv launch flags: the prologue (bits 0-1), a bias add, the residual add
+GLF_SNAKE, GLF_LEAKY, GLF_BIAS, GLF_RESIDUAL = 1, 2, 4, 8
 
 # cbx_op_kind
 OP_LAYER_NORM, OP_RMS_NORM, OP_UNARY, OP_LEAKY_RELU, OP_SWIGLU, OP_ROPE, OP_GET_ROWS, \
@@ -744,12 +749,18 @@ class Graph:
         return len(self._descs) - 1
 
     def node(self, op: int, dst: int, src=(), iparam: int = 0, fparam: float = 0.0,
-             rope: Optional[RopeCache] = None) -> int:
+             rope: Optional[RopeCache] = None, conv=(0, 0, 0), conv_w=None) -> int:
+        """conv: (stride, padding, dilation) of an IM2COL node, (stride,) of a
+        CONV_TRANSPOSE_1D node; conv_w: Conv1dWeights on the MUL_MAT /
+        CONV_TRANSPOSE_1D node, or any non-null address when only planning."""
         s = list(src) + [-1] * (2 - len(src))
         n = GNode()
         n.op, n.dst, n.iparam, n.fparam = op, dst, iparam, fparam
         n.src[0], n.src[1] = s[0], s[1]
         n.rope = rope.handle.value if rope is not None else None
+        cv = list(conv) + [0] * (3 - len(conv))
+        n.conv[0], n.conv[1], n.conv[2] = cv[0], cv[1], cv[2]
+        n.conv_w = conv_w.handle.value if isinstance(conv_w, Conv1dWeights) else conv_w
         self.nodes.append(n)
         return dst
 

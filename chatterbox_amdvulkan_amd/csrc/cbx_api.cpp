@@ -163,6 +163,10 @@ struct cbx_conv1d_weights {
     _Float16* data;     // [phase][c_out_pad / 32][taps][c_in_pad / 16][64][8]
 };
 
+bool cbx::conv1d_weights_match(const cbx_conv1d_weights* w, int up, int64_t k, int64_t c_in, int64_t c_out) {
+    return w && w->up == up && w->k == k && w->c_in == c_in && w->c_out == c_out;
+}
+
 struct cbx_rope_cache {
     int              device;
     cbx::RopeParams  p;

@@ -13,7 +13,11 @@
 // join is add(add(mul_mat, bias), h) -> layer_norm (t3.cpp:528-532), its
 // feed-forward input add(mul_mat, bias) -> gelu (t3.cpp:535-537), and
 // causal_block1d ends layer_norm -> mish -> mul(mask) (cfm_decoder.cpp:
-// 143-148).  The planner walks
+// 143-148), and HiFT's convolutions are transpose -> cont -> im2col ->
+// mul_mat -> bias add -> transpose -> cont (conv1d_CT, hift_vocoder.cpp:
+// 77-93) or the same around conv_transpose_1d and a cropping view
+// (conv_transpose1d_CT, :96-115), after snake() or leaky_relu and, in a
+// ResBlock, before the residual add (:128-135).  The planner walks
 // the nodes in order and, at each node, takes the longest such chain whose
 // intermediate results no other node reads and the caller does not keep;
 // the chain then runs as one library call.  Because a chain is a run of
@@ -106,14 +110,137 @@ struct Planner {
                is_contiguous(&Y) && is_contiguous(&V) && is_contiguous(&R) && same_dims(r, v);
     }
 
+    // transpose (view) -> cont of x (C, T, B) at node i: the contiguous
+    // (T, C, B) copy, or -1
+    int32_t transposed_copy_at(int32_t i, int32_t x) const {
+        if (!valid_t(x) || !is(i, CBX_GOP_VIEW) || nd[i].src[0] != x || !is(i + 1, CBX_GOP_CPY)) return -1;
+        const cbx_tensor& X = t[x];
+        const int32_t v = nd[i].dst, c = nd[i + 1].dst;
+        if (!dims(v, X.ne[1], X.ne[0], X.ne[2], X.ne[3]) || t[v].data != X.data || !internal(v, 1) ||
+            nd[i + 1].src[0] != v || !same_dims(c, v) || !internal(c, 1)) {
+            return -1;
+        }
+        return c;
+    }
+
+    // [view (bias as (1, C)) -> add(y, view)] -> transpose (view) -> cont,
+    // from y (T, C, B) at node j: the node count, or 0; *fl gets bit 2 for
+    // the bias add and *out the (C, T, B) result
+    int32_t conv_tail_at(int32_t j, int32_t y, int32_t* fl, int32_t* out) const {
+        const int32_t j0 = j;
+        int32_t cur = y;
+        const int64_t C = valid_t(y) ? t[y].ne[1] : -1;
+        if (is(j, CBX_GOP_VIEW) && is(j + 1, CBX_GOP_ADD) && nd[j + 1].src[0] == cur && nd[j + 1].src[1] == nd[j].dst &&
+            valid_t(nd[j].src[0]) && nelements(&t[nd[j].src[0]]) == C && dims(nd[j].dst, 1, C, 1, 1) &&
+            internal(cur, 1) && internal(nd[j].dst, 1) && same_dims(nd[j + 1].dst, cur)) {
+            *fl |= 4;
+            cur = nd[j + 1].dst;
+            j += 2;
+        }
+        if (!valid_t(cur) || !is(j, CBX_GOP_VIEW) || nd[j].src[0] != cur || !internal(cur, 1) ||
+            !is(j + 1, CBX_GOP_CPY)) {
+            return 0;
+        }
+        const cbx_tensor& Y = t[cur];
+        const int32_t v = nd[j].dst, o = nd[j + 1].dst;
+        if (!dims(v, Y.ne[1], Y.ne[0], Y.ne[2], Y.ne[3]) || t[v].data != Y.data || !internal(v, 1) ||
+            nd[j + 1].src[0] != v || !same_dims(o, v)) {
+            return 0;
+        }
+        *out = o;
+        return j + 2 - j0;
+    }
+
+    // conv1d_CT of x (C_in, T_in, B) at node i: transpose -> cont ->
+    // im2col -> view (2-D) -> view (weight 2-D) -> mul_mat (with prepared
+    // weights) -> view (3-D) -> conv_tail [-> add(., residual)].  The node
+    // count, or 0; *fl gets bits 2 (bias) and 3 (residual).
+    int32_t conv1d_at(int32_t i, int32_t x, int32_t* fl) const {
+        const int32_t c = transposed_copy_at(i, x);
+        if (c < 0 || !is(i + 2, CBX_GOP_IM2COL) || nd[i + 2].src[1] != c) return 0;
+        const int32_t wk = nd[i + 2].src[0], col = nd[i + 2].dst;
+        if (!valid_t(wk) || !valid_t(col) || !internal(col, 1)) return 0;
+        const cbx_tensor &X = t[x], &Wk = t[wk], &Col = t[col];
+        const int64_t K = Wk.ne[0], C_in = Wk.ne[1], C_out = Wk.ne[2], B = X.ne[2], T_out = Col.ne[1];
+        if (C_in != X.ne[0] || Wk.ne[3] != 1 || Col.ne[0] != C_in * K || Col.ne[2] != B || X.ne[3] != 1) return 0;
+        if (!is(i + 3, CBX_GOP_VIEW) || nd[i + 3].src[0] != col || !is(i + 4, CBX_GOP_VIEW) ||
+            nd[i + 4].src[0] != wk || !is(i + 5, CBX_GOP_MUL_MAT)) {
+            return 0;
+        }
+        const int32_t col2 = nd[i + 3].dst, w2 = nd[i + 4].dst, mm = nd[i + 5].dst;
+        if (!dims(col2, C_in * K, T_out * B, 1, 1) || !internal(col2, 1) || !dims(w2, K * C_in, C_out, 1, 1) ||
+            !internal(w2, 1) || nd[i + 5].src[0] != col2 || nd[i + 5].src[1] != w2 || !nd[i + 5].conv_w ||
+            !dims(mm, T_out * B, C_out, 1, 1) || !internal(mm, 1) || !is(i + 6, CBX_GOP_VIEW) ||
+            nd[i + 6].src[0] != mm || !dims(nd[i + 6].dst, T_out, C_out, B, 1)) {
+            return 0;
+        }
+        int32_t out = -1;
+        const int32_t tail = conv_tail_at(i + 7, nd[i + 6].dst, fl, &out);
+        if (!tail) return 0;
+        int32_t j = i + 7 + tail;
+        if (is(j, CBX_GOP_ADD) && internal(out, 1)) {
+            const int32_t other = nd[j].src[0] == out ? nd[j].src[1] : nd[j].src[1] == out ? nd[j].src[0] : -1;
+            if (same_dims(other, out) && same_dims(nd[j].dst, out)) {
+                *fl |= 8;
+                j++;
+            }
+        }
+        return j - i;
+    }
+
+    // conv_transpose1d_CT of x (C_in, T_in, 1) at node i: transpose ->
+    // cont -> conv_transpose_1d (with prepared weights) -> view cropping
+    // pad frames at both ends -> cont -> conv_tail.  The node count, or 0.
+    int32_t convt_at(int32_t i, int32_t x, int32_t* fl) const {
+        const int32_t c = transposed_copy_at(i, x);
+        if (c < 0 || !is(i + 2, CBX_GOP_CONV_TRANSPOSE_1D) || nd[i + 2].src[1] != c || !nd[i + 2].conv_w) return 0;
+        const int32_t wk = nd[i + 2].src[0], full = nd[i + 2].dst;
+        if (!valid_t(wk) || !valid_t(full) || !internal(full, 1)) return 0;
+        const cbx_tensor &X = t[x], &Wk = t[wk], &F = t[full];
+        const int64_t K = Wk.ne[0], C_out = Wk.ne[1], s0 = nd[i + 2].conv[0];
+        if (Wk.ne[2] != X.ne[0] || X.ne[2] != 1 || X.ne[3] != 1 || s0 < 1 ||
+            !dims(full, (X.ne[1] - 1) * s0 + K, C_out, 1, 1) || F.type != CBX_TYPE_F32) {
+            return 0;
+        }
+        if (!is(i + 3, CBX_GOP_VIEW) || nd[i + 3].src[0] != full || !is(i + 4, CBX_GOP_CPY)) return 0;
+        const int32_t crop = nd[i + 3].dst, cc = nd[i + 4].dst;
+        const char* d0 = static_cast<const char*>(F.data);
+        const char* d1 = valid_t(crop) ? static_cast<const char*>(t[crop].data) : nullptr;
+        const int64_t off = d1 ? d1 - d0 : -1;
+        if (off < 0 || off % 4 || t[crop].nb[1] != F.nb[1] || !internal(crop, 1) || nd[i + 4].src[0] != crop ||
+            !same_dims(cc, crop) || !internal(cc, 1) || !dims(crop, F.ne[0] - 2 * (off / 4), C_out, 1, 1)) {
+            return 0;
+        }
+        int32_t out = -1;
+        const int32_t tail = conv_tail_at(i + 5, cc, fl, &out);
+        return tail ? 5 + tail : 0;
+    }
+
+    // A conv chain starting at node i whose input is x (the prologue's
+    // output, or the chain's own input): CONV1D / CONV_TRANSPOSE1D and its
+    // node count, or UNSUPPORTED.
+    int32_t conv_chain_at(int32_t i, int32_t x, int32_t* n, int32_t* fl) const {
+        if ((*n = conv1d_at(i, x, fl))) return CBX_GL_CONV1D;
+        if ((*n = convt_at(i, x, fl))) return CBX_GL_CONV_TRANSPOSE1D;
+        return CBX_GL_UNSUPPORTED;
+    }
+
     // The longest chain at node i: its kind, *len nodes, *flags.
     int32_t match(int32_t i, int32_t* len, int32_t* flags) const {
         const cbx_gnode& a = nd[i];
         *len = 1;
         *flags = 0;
         switch (a.op) {
-            case CBX_GOP_VIEW:
+            case CBX_GOP_VIEW: {
+                int32_t n = 0, fl = 0;
+                const int32_t k = conv_chain_at(i, a.src[0], &n, &fl);
+                if (k != CBX_GL_UNSUPPORTED) {
+                    *len = n;
+                    *flags = fl;
+                    return k;
+                }
                 return CBX_GL_VIEW;
+            }
             case CBX_GOP_GET_ROWS: {
                 int32_t g1 = a.dst;
                 const int32_t j = i + 1 + cast_after(i + 1, &g1);
@@ -231,6 +358,15 @@ struct Planner {
                     nd[i + 3].src[0] == nd[i + 2].dst && same_dims(nd[i + 3].src[1], al) && is(i + 4, CBX_GOP_ADD) &&
                     nd[i + 4].src[0] == x && nd[i + 4].src[1] == nd[i + 3].dst && internal(a.dst, 1) &&
                     internal(nd[i + 1].dst, 1) && internal(nd[i + 2].dst, 1) && internal(nd[i + 3].dst, 1)) {
+                    // snake() as the prologue of a conv: one conv launch
+                    const int32_t h = nd[i + 4].dst;
+                    int32_t n = 0, fl = 1;
+                    const int32_t k = internal(h, 1) ? conv_chain_at(i + 5, h, &n, &fl) : CBX_GL_UNSUPPORTED;
+                    if (k != CBX_GL_UNSUPPORTED) {
+                        *len = 5 + n;
+                        *flags = fl;
+                        return k;
+                    }
                     *len = 5;
                     return CBX_GL_SNAKE;
                 }
@@ -249,8 +385,16 @@ struct Planner {
                 }
                 return a.iparam >= CBX_UNARY_GELU && a.iparam <= CBX_UNARY_MISH ? CBX_GL_UNARY : CBX_GL_UNSUPPORTED;
             }
-            case CBX_GOP_LEAKY_RELU:
+            case CBX_GOP_LEAKY_RELU: {
+                int32_t n = 0, fl = 2;
+                const int32_t k = internal(a.dst, 1) ? conv_chain_at(i + 1, a.dst, &n, &fl) : CBX_GL_UNSUPPORTED;
+                if (k != CBX_GL_UNSUPPORTED) {
+                    *len = 1 + n;
+                    *flags = fl;
+                    return k;
+                }
                 return CBX_GL_LEAKY_RELU;
+            }
             case CBX_GOP_ROPE:
                 return CBX_GL_ROPE;
             case CBX_GOP_CPY:
@@ -277,6 +421,9 @@ const char* op_name(int op) {
         case CBX_GOP_UNARY: return "UNARY";
         case CBX_GOP_LEAKY_RELU: return "LEAKY_RELU";
         case CBX_GOP_CPY: return "CPY";
+        case CBX_GOP_IM2COL: return "IM2COL";
+        case CBX_GOP_MUL_MAT: return "MUL_MAT";
+        case CBX_GOP_CONV_TRANSPOSE_1D: return "CONV_TRANSPOSE_1D";
         default: return "unknown op";
     }
 }
@@ -346,8 +493,10 @@ constexpr int32_t kSpan[][2] = {
     {4, 8},  // ADD_LAYER_NORM [bias] [mish]
     {4, 7},  // LAYER_NORM_MASK [mish]
     {1, 4},  // BIAS_ACT [act | mish]
+    {9, 17}, // CONV1D [snake | leaky] [bias] [residual]
+    {7, 14}, // CONV_TRANSPOSE1D [snake | leaky] [bias]
 };
-constexpr int32_t kLastKind = CBX_GL_BIAS_ACT;
+constexpr int32_t kLastKind = CBX_GL_CONV_TRANSPOSE1D;
 static_assert(sizeof(kSpan) / sizeof(kSpan[0]) == kLastKind + 1, "one span per launch kind");
 
 // Issues the entry point a launch maps to.  A launch is only read within
@@ -463,6 +612,52 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
             if (l.n_nodes == 3) break;
             const int act = l.n_nodes == 1 ? CBX_UNARY_NONE : l.n_nodes == 4 ? CBX_UNARY_MISH : nd[f + 1].iparam;
             return cbx_bias_act(act, T(t, a.src[0]), T(t, a.src[1]), y, s);
+        }
+        case CBX_GL_CONV1D:
+        case CBX_GL_CONV_TRANSPOSE1D: {
+            // the layout the flags describe: prologue, body, bias, residual
+            const int pro = l.flags & 3;
+            const bool bias = (l.flags & 4) != 0, res = (l.flags & 8) != 0;
+            const bool tr = l.kind == CBX_GL_CONV_TRANSPOSE1D;
+            const int32_t p = pro == 1 ? 5 : pro == 2 ? 1 : 0;
+            if (pro == 3 || (tr && res) ||
+                l.n_nodes != p + (tr ? 7 : 9) + (bias ? 2 : 0) + (res ? 1 : 0)) {
+                break;
+            }
+            const int32_t b0 = f + p;   // the transpose view
+            const cbx_tensor* x = T(t, a.src[0]);
+            const cbx_tensor* al = pro == 1 ? T(t, a.src[1]) : nullptr;
+            const cbx_tensor* ai = pro == 1 ? T(t, nd[f + 3].src[1]) : nullptr;
+            const float slope = pro == 2 ? a.fparam : 0.0f;
+            const int cp = pro == 1 ? CBX_CONV_PRO_SNAKE : pro == 2 ? CBX_CONV_PRO_LEAKY_RELU : CBX_CONV_PRO_NONE;
+            const int32_t bview = b0 + (tr ? 5 : 7);   // the bias view, when there is one
+            const cbx_tensor* bt = bias ? T(t, nd[bview].src[0]) : nullptr;
+            // the prepared weights must be the node's weight tensor's
+            const cbx_gnode& wn = nd[b0 + (tr ? 2 : 5)];
+            const cbx_tensor* wk = T(t, nd[b0 + 2].src[0]);
+            if (!wk || !conv1d_weights_match(wn.conv_w, tr ? wn.conv[0] : 0, wk->ne[0], tr ? wk->ne[2] : wk->ne[1],
+                                             tr ? wk->ne[1] : wk->ne[2])) {
+                return set_error(CBX_ERR_INVALID_ARG, "cbx_graph_launch: node " + std::to_string(b0 + (tr ? 2 : 5)) +
+                                                          ": conv_w was not made from the node's weight tensor");
+            }
+            if (!tr) {
+                const cbx_gnode& ic = nd[b0 + 2];
+                const cbx_gnode& last = nd[f + l.n_nodes - 1];
+                const cbx_tensor* r = nullptr;
+                if (res) {
+                    const int32_t out = nd[f + l.n_nodes - 2].dst;
+                    r = T(t, last.src[0] == out ? last.src[1] : last.src[0]);
+                }
+                return cbx_conv1d(x, nd[b0 + 5].conv_w, ic.conv[0], ic.conv[1], ic.conv[2], cp, al, ai, slope, bt, r,
+                                  y, s);
+            }
+            // the crop: the view's offset into the full output, in frames
+            const cbx_tensor* full = T(t, nd[b0 + 2].dst);
+            const cbx_tensor* crop = T(t, nd[b0 + 3].dst);
+            if (!full || !crop) break;
+            const int64_t off = static_cast<const char*>(crop->data) - static_cast<const char*>(full->data);
+            if (off < 0 || off % 4 || off / 4 > (int64_t{1} << 30)) break;
+            return cbx_conv_transpose1d(x, nd[b0 + 2].conv_w, static_cast<int>(off / 4), cp, al, ai, slope, bt, y, s);
         }
         default:
             break;

@@ -432,7 +432,21 @@ int cbx_run_ops(const cbx_op* ops, int n_ops, cbx_stream stream);
  * Tensors are given once, in an array; nodes refer to them by index.  A
  * node reads src[] (-1 = none) and writes dst, ggml's broadcast rules
  * apply to ADD/MUL operands, and a VIEW node only re-describes its
- * source's memory (ggml's VIEW, RESHAPE, PERMUTE, TRANSPOSE: no launch).  */
+ * source's memory (ggml's VIEW, RESHAPE, PERMUTE, TRANSPOSE: no launch).
+ *
+ * The HiFT convolutions arrive as the node runs conv1d_CT and
+ * conv_transpose1d_CT emit (hift_vocoder.cpp:77-116), optionally after
+ * snake() or leaky_relu and, for conv1d, before the ResBlock's residual
+ * add (:131-135):
+ *   conv1d:  VIEW (transpose) -> CPY (cont) -> IM2COL -> VIEW (2-D) ->
+ *            VIEW (weight 2-D) -> MUL_MAT -> VIEW (3-D) [-> VIEW (bias as
+ *            (1, C_out)) -> ADD] -> VIEW (transpose) -> CPY (cont)
+ *   transposed: VIEW (transpose) -> CPY (cont) -> CONV_TRANSPOSE_1D ->
+ *            VIEW (crop) -> CPY (cont) [-> VIEW (bias) -> ADD] -> VIEW
+ *            (transpose) -> CPY (cont)
+ * and run as one cbx_conv1d / cbx_conv_transpose1d call with the weights
+ * the backend prepared at load time, given on the MUL_MAT /
+ * CONV_TRANSPOSE_1D node (conv_w).                                         */
 typedef enum cbx_gop {
     CBX_GOP_VIEW          = 0,  /* dst describes src0's memory                       */
     CBX_GOP_GET_ROWS      = 1,  /* src0 table, src1 ids I32                           */
@@ -448,6 +462,9 @@ typedef enum cbx_gop {
     CBX_GOP_UNARY         = 11, /* iparam = cbx_unary_op (GELU .. SQR)                */
     CBX_GOP_LEAKY_RELU    = 12, /* fparam = negative slope                            */
     CBX_GOP_CPY           = 13, /* ggml_cpy / ggml_cast to dst's type (F32, F16)      */
+    CBX_GOP_IM2COL        = 14, /* src0 kernel (shape), src1 data; conv = s0, p0, d0 */
+    CBX_GOP_MUL_MAT       = 15, /* src0 x src1 (only inside a conv1d chain); conv_w */
+    CBX_GOP_CONV_TRANSPOSE_1D = 16, /* src0 kernel, src1 data; conv[0] = s0; conv_w */
 } cbx_gop;
 
 typedef struct cbx_gnode {
@@ -457,6 +474,10 @@ typedef struct cbx_gnode {
     int32_t               iparam;
     float                 fparam;
     const cbx_rope_cache* rope;    /* CBX_GOP_ROPE                             */
+    int32_t               conv[3]; /* CBX_GOP_IM2COL: stride, padding, dilation;
+                                      CONV_TRANSPOSE_1D: stride (p0 0, d0 1)  */
+    const cbx_conv1d_weights* conv_w; /* MUL_MAT of a conv1d chain, CONV_TRANSPOSE_1D:
+                                      the weights prepared from its kernel   */
 } cbx_gnode;
 
 /* What one planned launch runs: nodes [first_node, first_node + n_nodes). */
@@ -481,6 +502,8 @@ typedef enum cbx_glaunch_kind {
     CBX_GL_ADD_LAYER_NORM,    /* [add(x, bias) ->] add(., r) -> norm -> mul -> add [-> mish chain] */
     CBX_GL_LAYER_NORM_MASK,   /* norm -> mul -> add [-> mish chain] -> mul(., mask (1, ne1)) */
     CBX_GL_BIAS_ACT,          /* add(x, bias) [-> unary op | -> mish chain]     */
+    CBX_GL_CONV1D,            /* [snake | leaky_relu ->] conv1d chain [-> add(x, .)] */
+    CBX_GL_CONV_TRANSPOSE1D,  /* [snake | leaky_relu ->] transposed conv chain  */
 } cbx_glaunch_kind;
 
 typedef struct cbx_glaunch {
@@ -488,7 +511,10 @@ typedef struct cbx_glaunch {
     int32_t first_node;
     int32_t n_nodes;
     int32_t flags;        /* bit 0: an intermediate the fused kernel may skip
-                             storing (the embedding sum h nobody reads)         */
+                             storing (the embedding sum h nobody reads).
+                             Conv kinds: bits 0-1 the prologue (0 none, 1
+                             snake, 2 leaky_relu), bit 2 a bias add, bit 3 the
+                             residual add.                                      */
 } cbx_glaunch;
 
 /* Splits nodes[0..n_nodes) into launches, in order, covering every node

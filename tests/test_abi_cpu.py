@@ -97,3 +97,10 @@ def test_descriptor_of_extent_one_dims():
     b = torch.zeros(5).expand(1, 5)          # stride 0 on the leading extent-1 dim
     db = C.desc(b)
     assert list(db.ne) == [5, 1, 1, 1] and list(db.nb) == [4, 20, 20, 20]
+
+
+def test_graph_node_layout_matches_header():
+    # struct cbx_gnode { int32 op, dst, src[2], iparam; float fparam; const void* rope;
+    #                    int32 conv[3]; const void* conv_w; }
+    assert C.GNode.rope.offset == 24 and C.GNode.conv.offset == 32 and C.GNode.conv_w.offset == 48
+    assert ctypes.sizeof(C.GNode) == 56

@@ -4,7 +4,9 @@ operations): T3 input embedding + first LayerNorm (t3.cpp:446-466),
 causal_block1d's LayerNorm -> Mish (cfm_decoder.cpp:143-146), snake
 (hift_vocoder.cpp:64-73), attention scores (t3.cpp:513-518), LayerNorm ->
 view -> RoPE, GroupNorm + affine + Mish, and a list of single ops.  Also
-checks how many kernel launches each list took."""
+checks how many kernel launches each list took.  The HiFT conv chains
+(a ResBlock layer, an upsampler) are checked launch by launch against the
+oracle's conv1d / conv_transpose1d."""
 import numpy as np
 import pytest
 import torch
@@ -255,3 +257,85 @@ def test_layout_error_names_the_nodes(cbx):
     with pytest.raises(cbx.CbxError) as e:
         g.compute()
     assert "nodes 0..2" in str(e.value)
+
+
+# ---- HiFT conv chains --------------------------------------------------------------
+
+def dev_new(shape, dtype=torch.float32):
+    return torch.full(shape, float("nan"), dtype=dtype, device="cuda")
+
+
+@pytest.mark.parametrize("Ch,T,K,d", [(128, 700, 11, 3), (64, 1500, 3, 5)])
+def test_resblock_sublayer_nodes(cbx, oracle, Ch, T, K, d):
+    """resblock_forward's layer as the reference's node list
+    (hift_vocoder.cpp:131-135): two conv launches, the first writing the
+    conv1d_CT result the second reads.  Each is checked against the oracle's
+    conv1d on the same input it read, within the conv tolerance
+    2^-13 sum |a b| + 2^-22 |ref| (f16 products summed in f32)."""
+    from tests._hift_graph import HiftGraph
+    from tests.test_gpu_conv1d import check
+
+    sd = W.seed_of(13, K)
+    x = W.normal(sd, (T, Ch), 0.0, 1.0)
+    arrs, p, wts = {}, {}, []
+    h = HiftGraph(dev_new)
+    tx = h.t(dev(x))
+    for k, s in enumerate(("1", "2")):
+        a, ai = W.snake_alpha(Ch, 20 + k)
+        w = W.normal(sd + 1 + k, (Ch, Ch, K), 0.0, 1.0 / np.sqrt(Ch * K))
+        b = W.normal(sd + 3 + k, (Ch,), 0.0, 0.1)
+        arrs.update({"a" + s: a, "ai" + s: ai, "w" + s: w, "b" + s: b})
+        for name, v in (("a", a), ("ai", ai), ("w", w), ("b", b)):
+            p[name + s] = h.t(dev(v))
+        wts.append(cbx.Conv1dWeights(h.at(p["w" + s])))
+    y = h.sublayer(tx, p, d, wts[0], wts[1])
+    plan = h.g.plan()
+    assert [q[0] for q in plan] == [cbx.GL_CONV1D] * 2
+    assert h.g.compute() == 2
+    mid = host(h.at(h.g.nodes[plan[0][2] - 1].dst)).reshape(T, Ch)   # the first conv1d_CT's result
+    got = host(h.at(y))
+    check(oracle, mid, x, arrs["w1"], 1, (K - 1) // 2 * d, d, oracle.CONV_PRO_SNAKE, arrs["a1"], arrs["ai1"], 0.0,
+          arrs["b1"], None, "first conv of the layer")
+    check(oracle, got, mid, arrs["w2"], 1, (K - 1) // 2, 1, oracle.CONV_PRO_SNAKE, arrs["a2"], arrs["ai2"], 0.0,
+          arrs["b2"], x, "second conv + residual")
+    for w_ in wts:
+        w_.close()
+
+
+@pytest.mark.parametrize("C_in,C_out,s,K,T", [(256, 128, 5, 11, 200), (128, 64, 3, 7, 500)])
+def test_upsampler_nodes(cbx, oracle, C_in, C_out, s, K, T):
+    """leaky_relu -> conv_transpose1d_CT (hift_vocoder.cpp:686-687) as the
+    reference's node list: one transposed-conv launch, checked against the
+    oracle's conv_transpose1d within the conv tolerance."""
+    from tests._hift_graph import HiftGraph
+    from tests.test_gpu_conv_transpose1d import check
+
+    pad = (K - s) // 2
+    sd = W.seed_of(14, s)
+    x = W.normal(sd, (T, C_in), 0.0, 1.0)
+    w = W.normal(sd + 1, (C_in, C_out, K), 0.0, 1.0 / np.sqrt(C_in * K / s))
+    b = W.normal(sd + 2, (C_out,), 0.0, 0.1)
+    h = HiftGraph(dev_new)
+    tx, tw, tb = h.t(dev(x)), h.t(dev(w)), h.t(dev(b))
+    wts = cbx.Conv1dWeights(h.at(tw), transpose_stride=s)
+    y = h.conv_transpose1d(h.leaky(tx, 0.1), tw, tb, s, pad, wts)
+    assert h.g.plan() == [(cbx.GL_CONV_TRANSPOSE1D, 0, 10, cbx.GLF_LEAKY | cbx.GLF_BIAS)]
+    assert h.g.compute() == 1
+    check(oracle, host(h.at(y)), x, w, s, pad, oracle.CONV_PRO_LEAKY, 0.1, b, "upsampler nodes")
+    wts.close()
+
+
+def test_conv_weights_of_another_shape_are_refused(cbx):
+    """A conv launch whose prepared weights were made from another weight
+    than the node's is refused before it runs."""
+    from tests._hift_graph import HiftGraph
+
+    h = HiftGraph(dev_new)
+    x = h.t(dev_new((50, 16)).zero_())
+    w = h.t(dev_new((16, 16, 3)).zero_())
+    other = cbx.Conv1dWeights(dev_new((16, 16, 5)).zero_())
+    h.conv1d(x, w, None, 1, 1, 1, other)
+    assert h.g.plan() == [(cbx.GL_CONV1D, 0, 9, 0)]
+    with pytest.raises(cbx.CbxError, match="conv_w was not made from the node's weight tensor"):
+        h.g.compute()
+    other.close()

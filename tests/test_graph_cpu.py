@@ -11,6 +11,8 @@ import torch
 
 from chatterbox_amdvulkan_amd import cbxops as C
 
+from tests._hift_graph import HiftGraph
+
 
 def f32(*shape):
     return torch.zeros(shape, dtype=torch.float32)
@@ -357,7 +359,8 @@ def test_random_lists_plan_into_an_exact_cover():
              C.GL_LAYER_NORM_ROPE: {5}, C.GL_RMS_NORM: {1, 2}, C.GL_GROUP_NORM: {1, 3, 4, 6},
              C.GL_SOFT_MAX: {1, 2, 3}, C.GL_SNAKE: {5}, C.GL_UNARY: {1, 3}, C.GL_SWIGLU: {2},
              C.GL_LEAKY_RELU: {1}, C.GL_ROPE: {1}, C.GL_CPY: {1}, C.GL_ADD_LAYER_NORM: {4, 5, 7, 8},
-             C.GL_LAYER_NORM_MASK: {4, 7}, C.GL_BIAS_ACT: {1, 2, 4}}
+             C.GL_LAYER_NORM_MASK: {4, 7}, C.GL_BIAS_ACT: {1, 2, 4}, C.GL_CONV1D: set(range(9, 18)),
+             C.GL_CONV_TRANSPOSE1D: set(range(7, 15))}
     shapes = [(4, 8), (8,), (1, 8, 1, 1), (4, 8), (4, 1)]
     for trial in range(200):
         g = C.Graph()
@@ -365,7 +368,7 @@ def test_random_lists_plan_into_an_exact_cover():
         for k in range(n_t):
             g.tensor(f32(*shapes[int(rng.integers(0, len(shapes)))]))
         for k in range(int(rng.integers(1, 25))):
-            op = int(rng.integers(0, 14))
+            op = int(rng.integers(0, 17))
             src = [int(rng.integers(-1, n_t)) for _ in range(2)]
             g.node(op, int(rng.integers(0, n_t)), src, iparam=int(rng.integers(-1, 9)),
                    fparam=float(rng.choice([1.0, 0.5, 1e-5])))
@@ -376,3 +379,130 @@ def test_random_lists_plan_into_an_exact_cover():
             assert first == at and n in spans[kind], (trial, kind, n)
             at += n
         assert at == len(g.nodes)
+
+
+# ---- HiFT conv chains (hift_vocoder.cpp) -----------------------------------------
+
+def host_new(shape, dtype=torch.float32):
+    return torch.zeros(shape, dtype=dtype)
+
+
+DUMMY_W = 0x1000   # planning reads conv_w only for being non-null
+
+
+def hift_params(h: HiftGraph, Ch=16, K=3):
+    p = {}
+    for s in ("1", "2"):
+        p["a" + s], p["ai" + s] = h.t(f32(Ch)), h.t(f32(Ch))
+        p["w" + s], p["b" + s] = h.t(torch.zeros(Ch, Ch, K, dtype=torch.float16)), h.t(f32(Ch))
+    return p
+
+
+def test_resblock_sublayer_is_two_conv_launches():
+    """resblock_forward's layer (hift_vocoder.cpp:131-135): snake -> conv1d_CT
+    -> snake -> conv1d_CT -> add(x, h): the first snake and conv1d_CT (its 9
+    nodes and the 2 of the bias add) are one launch, the second adds the
+    residual add."""
+    h = HiftGraph(host_new)
+    x = h.t(f32(40, 16))
+    h.sublayer(x, hift_params(h), 3, DUMMY_W, DUMMY_W)
+    assert h.g.plan() == [(C.GL_CONV1D, 0, 16, C.GLF_SNAKE | C.GLF_BIAS),
+                          (C.GL_CONV1D, 16, 17, C.GLF_SNAKE | C.GLF_BIAS | C.GLF_RESIDUAL)]
+
+
+def test_three_sublayers_chain():
+    """resblock_forward runs its three layers in series (hift_vocoder.cpp:128-136)."""
+    h = HiftGraph(host_new)
+    x = h.t(f32(40, 16))
+    for d in (1, 3, 5):
+        x = h.sublayer(x, hift_params(h), d, DUMMY_W, DUMMY_W)
+    plan = h.g.plan()
+    assert [p[0] for p in plan] == [C.GL_CONV1D] * 6
+    assert [p[3] & C.GLF_RESIDUAL for p in plan] == [0, 8] * 3
+    assert sum(p[2] for p in plan) == len(h.g.nodes) == 99
+
+
+def test_conv_post_and_plain_conv():
+    """conv_post (hift_vocoder.cpp:748-749): leaky_relu -> conv1d_CT; a conv
+    without prologue or bias (9 nodes) is a launch of its own."""
+    h = HiftGraph(host_new)
+    x = h.t(f32(30, 16))
+    w, b = h.t(torch.zeros(18, 16, 7, dtype=torch.float16)), h.t(f32(18))
+    y = h.conv1d(h.leaky(x, 0.01), w, b, 1, 3, 1, DUMMY_W)
+    w2 = h.t(torch.zeros(8, 18, 3))
+    h.conv1d(y, w2, None, 2, 1, 1, DUMMY_W)
+    assert h.g.plan() == [(C.GL_CONV1D, 0, 12, C.GLF_LEAKY | C.GLF_BIAS), (C.GL_CONV1D, 12, 9, 0)]
+
+
+@pytest.mark.parametrize("stride,K,pad", [(8, 16, 4), (5, 11, 3), (3, 7, 2), (1, 3, 1)])
+def test_upsampler_is_one_transposed_conv_launch(stride, K, pad):
+    """hift_vocoder.cpp:686-687: leaky_relu -> conv_transpose1d_CT (transpose,
+    cont, conv_transpose_1d, the cropping view, cont, the bias add, transpose,
+    cont)."""
+    h = HiftGraph(host_new)
+    x = h.t(f32(12, 32))
+    w, b = h.t(torch.zeros(32, 16, K, dtype=torch.float16)), h.t(f32(16))
+    h.conv_transpose1d(h.leaky(x, 0.1), w, b, stride, pad, DUMMY_W)
+    assert h.g.plan() == [(C.GL_CONV_TRANSPOSE1D, 0, 10, C.GLF_LEAKY | C.GLF_BIAS)]
+
+
+def test_conv_chains_that_do_not_fuse():
+    def sublayer_graph():
+        h = HiftGraph(host_new)
+        x = h.t(f32(40, 16))
+        return h, x, hift_params(h)
+
+    # no prepared weights on the mul_mat: ggml's own mul_mat, not a conv launch
+    h, x, p = sublayer_graph()
+    h.sublayer(x, p, 1, None, DUMMY_W)
+    plan = h.g.plan()
+    assert plan[0] == (C.GL_SNAKE, 0, 5, 0)
+    assert C.GL_UNSUPPORTED in [q[0] for q in plan]
+    assert plan[-1] == (C.GL_CONV1D, 16, 17, C.GLF_SNAKE | C.GLF_BIAS | C.GLF_RESIDUAL)
+
+    # the caller keeps the im2col columns: the chain stays apart
+    h, x, p = sublayer_graph()
+    h.sublayer(x, p, 1, DUMMY_W, DUMMY_W)
+    col = h.g.nodes[7].dst
+    assert h.g.nodes[7].op == C.GOP_IM2COL
+    assert h.g.plan(keep=[col])[0] == (C.GL_SNAKE, 0, 5, 0)
+
+    # the snake's result read elsewhere too: the snake runs alone, the conv
+    # takes no prologue
+    h, x, p = sublayer_graph()
+    s = h.snake(x, p["a1"], p["ai1"])
+    y = h.conv1d(s, p["w1"], p["b1"], 1, 1, 1, DUMMY_W)
+    h.add(s, y)
+    assert h.g.plan() == [(C.GL_SNAKE, 0, 5, 0), (C.GL_CONV1D, 5, 12, C.GLF_BIAS | C.GLF_RESIDUAL)]
+
+    # a weight whose C_in is not x's
+    h = HiftGraph(host_new)
+    x = h.t(f32(40, 16))
+    h.conv1d(x, h.t(torch.zeros(16, 8, 3)), None, 1, 1, 1, DUMMY_W)
+    assert C.GL_CONV1D not in [q[0] for q in h.g.plan()]
+
+    # a transposed conv over two batch items: not the reference's shape
+    h = HiftGraph(host_new)
+    x = h.t(f32(2, 12, 32))
+    w = h.t(torch.zeros(32, 16, 4))
+    h.conv_transpose1d(x, w, None, 2, 1, DUMMY_W)
+    assert C.GL_CONV_TRANSPOSE1D not in [q[0] for q in h.g.plan()]
+
+
+def test_hand_made_conv_launches_are_refused():
+    """A conv launch whose node count or flags do not fit the chain is
+    refused before any weights or device are touched."""
+    L = C.load()
+    h = HiftGraph(host_new)
+    x = h.t(f32(40, 16))
+    h.sublayer(x, hift_params(h), 1, DUMMY_W, DUMMY_W)
+    T, N, _ = _raw(h.g)
+    nt, nn = len(h.g._descs), len(h.g.nodes)
+    bad = [C.GLaunch(C.GL_CONV1D, 0, 16, C.GLF_SNAKE),                    # bias nodes not counted
+           C.GLaunch(C.GL_CONV1D, 0, 16, C.GLF_SNAKE | C.GLF_LEAKY | C.GLF_BIAS),
+           C.GLaunch(C.GL_CONV1D, 0, 8, 0),                               # shorter than any conv chain
+           C.GLaunch(C.GL_CONV_TRANSPOSE1D, 16, 17, C.GLF_SNAKE | C.GLF_BIAS | C.GLF_RESIDUAL),
+           C.GLaunch(C.GL_CONV1D, 20, 17, C.GLF_SNAKE | C.GLF_BIAS | C.GLF_RESIDUAL)]  # past the list
+    for l in bad:
+        assert L.cbx_graph_launch(T, nt, N, nn, ctypes.byref(l), None) == C.ERR_INVALID_ARG, \
+            (l.kind, l.first_node, l.n_nodes, l.flags)
