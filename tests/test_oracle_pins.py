@@ -311,6 +311,98 @@ def test_rope_yarn_corr_dims(oracle):
     del ctypes
 
 
+# YaRN (Peng et al. 2023, "YaRN: Efficient Context Window Extension of Large
+# Language Models"): each rotary pair mixes the extrapolated angle (the
+# position's own) with the interpolated one (freq_scale times it) by a ramp
+# that is 1 (no interpolation) for high-frequency pairs below the low
+# correction dim and 0 above the high one, linear in between, and the
+# magnitude is scaled by 1 + 0.1 ln(1 / freq_scale).  The oracle's cache is
+# checked against these properties, not against its own formula.
+
+def _corr(oracle, n_dims, n_ctx, base, beta_fast, beta_slow):
+    dims = np.zeros(2, dtype=np.float32)
+    oracle.lib().cbxo_rope_yarn_corr_dims(n_dims, n_ctx, base, beta_fast, beta_slow, dims.ctypes.data)
+    return dims
+
+
+def _angles(cache):
+    c, s = cache[0::2].astype(np.float64), cache[1::2].astype(np.float64)
+    return np.arctan2(s, c), np.hypot(c, s)
+
+
+def _theta64(p, n_dims, base):
+    return p * base ** (-2.0 * np.arange(n_dims // 2) / n_dims)
+
+
+@pytest.mark.parametrize("fs", [0.25, 0.5, 0.125])
+def test_rope_yarn_full_extrapolation_and_interpolation(oracle, fs):
+    n, base, ctx, p, attn = 64, 10000.0, 4096, 3, 1.5
+    m = attn * (1.0 + 0.1 * math.log(1.0 / fs))
+    th = _theta64(p, n, base)
+    tol = lambda t: (np.arange(n // 2) + 2) * 2.0 ** -22 * np.abs(t) + 1e-6  # noqa: E731
+    # every pair below the low correction dim: pure extrapolation
+    lo = _corr(oracle, n, ctx, base, 0.01, 0.001)
+    assert lo[0] >= n // 2
+    ang, mag = _angles(oracle.rope_cache(p, n, base, fs, 1.0, attn, ctx, 0.01, 0.001))
+    assert np.all(np.abs(ang - th) <= tol(th)) and np.allclose(mag, m, rtol=1e-6)
+    # correction dims at 0: pair 0 extrapolates, all others interpolate
+    hi = _corr(oracle, n, ctx, base, 1000.0, 1000.0)
+    assert hi[0] == 0 and hi[1] <= 0
+    ang, mag = _angles(oracle.rope_cache(p, n, base, fs, 1.0, attn, ctx, 1000.0, 1000.0))
+    exp = np.concatenate([th[:1], fs * th[1:]])
+    assert np.all(np.abs(ang - exp) <= tol(exp)) and np.allclose(mag, m, rtol=1e-6)
+    # ext_factor 0: plain interpolation, magnitude attn_factor alone
+    ang, mag = _angles(oracle.rope_cache(p, n, base, fs, 0.0, attn, ctx, 0.01, 0.001))
+    assert np.all(np.abs(ang - fs * th) <= tol(fs * th)) and np.allclose(mag, attn, rtol=1e-6)
+
+
+@pytest.mark.parametrize("ext", [1.0, 0.5])
+def test_rope_yarn_ramp_is_linear_between_correction_dims(oracle, ext):
+    n, base, ctx, p, fs = 128, 10000.0, 4096, 1, 0.25
+    bf, bs = 32.0, 1.0
+    low, high = (float(v) for v in _corr(oracle, n, ctx, base, bf, bs))
+    assert 0 < low < high < n // 2 - 1
+    ang, _ = _angles(oracle.rope_cache(p, n, base, fs, ext, 1.0, ctx, bf, bs))
+    th = _theta64(p, n, base)
+    mix = (ang - fs * th) / (th - fs * th)     # 1 = extrapolated angle, 0 = interpolated
+    i = np.arange(n // 2)
+    # mixes well resolved (angles above 1e-3 rad): the mix is ext below the
+    # low dim, 0 above the high dim, and falls linearly in between
+    ok = (th - fs * th) > 1e-3
+    assert np.allclose(mix[ok & (i <= low)], ext, atol=1e-3)
+    assert np.allclose(mix[ok & (i >= high)], 0.0, atol=1e-3)
+    mid = ok & (i > low) & (i < high)
+    assert mid.sum() >= 4
+    slope = np.diff(mix[mid])
+    assert np.all(slope < 0) and np.allclose(slope, -ext / (high - low), atol=2e-3)
+
+
+def test_rope_freq_factors_divide_the_position(oracle):
+    """A power-of-two freq factor 2^k on pair i makes that pair's angle the
+    one of position p / 2^k, exactly (the iterated f32 angle scales by 2^k
+    without rounding), with or without YaRN; so the factor divides, and
+    pair i reads factor i."""
+    n, base, p = 64, 10000.0, 96
+    k = np.array([(3 * i) % 6 for i in range(n // 2)])
+    ff = (2.0 ** k).astype(np.float32)
+    for fs, ext in ((1.0, 0.0), (0.25, 1.0)):
+        kw = dict(freq_base=base, freq_scale=fs, ext_factor=ext, n_ctx_orig=4096, beta_fast=32.0, beta_slow=1.0)
+        got = oracle.rope_cache(p, n, freq_factors=ff, **kw)
+        for i in range(n // 2):
+            plain = oracle.rope_cache(p // 2 ** int(k[i]), n, **kw)
+            assert_bitexact(got[2 * i:2 * i + 2], plain[2 * i:2 * i + 2], what=f"pair {i}, fs {fs}")
+    ones = oracle.rope_cache(p, n, freq_factors=np.ones(n // 2, np.float32), freq_base=base)
+    assert_bitexact(ones, oracle.rope_cache(p, n, freq_base=base), what="unit freq factors")
+
+
+def test_rope_attn_factor_scales_exactly(oracle):
+    x = W.normal(W.seed_of(31, 0), (5, 4, 64), 0.0, 1.0)
+    pos = np.array([0, 7, 100, 513, 2047], dtype=np.int32)
+    y1 = oracle.rope_ext(x, pos, 64, attn_factor=1.0)
+    y2 = oracle.rope_ext(x, pos, 64, attn_factor=2.0)
+    assert_bitexact(y2, 2.0 * y1, what="attn_factor 2")
+
+
 # --------------------------------------------------------------------------- #
 # activations
 # --------------------------------------------------------------------------- #
