@@ -551,11 +551,15 @@ void conv_tile(int t, int ks, bool vec, bool pf4, dim3 grid, size_t lds, hipStre
         case 1: conv_ks<PRO, 4, 2, 1, 2, 2>(ks, vec, pf4, grid, lds, s, a); break;   // 128 x 128
         case 2: conv_ks<PRO, 2, 2, 1, 2, 2>(ks, vec, pf4, grid, lds, s, a); break;   // 64 x 128
         case 3: conv_ks<PRO, 2, 2, 1, 1, 4>(ks, vec, pf4, grid, lds, s, a); break;   // 64 x 64
-        default: conv_ks<PRO, 4, 1, 2, 1, 2>(ks, vec, pf4, grid, lds, s, a); break;  // 256 x 32
+        case 4: conv_ks<PRO, 4, 1, 2, 1, 2>(ks, vec, pf4, grid, lds, s, a); break;   // 256 x 32
+        case 5: conv_ks<PRO, 3, 2, 1, 2, 2>(ks, vec, pf4, grid, lds, s, a); break;   // 96 x 128
+        case 6: conv_ks<PRO, 3, 2, 2, 1, 2>(ks, vec, pf4, grid, lds, s, a); break;   // 192 x 64
+        default: conv_ks<PRO, 3, 2, 1, 1, 4>(ks, vec, pf4, grid, lds, s, a); break;  // 96 x 64
     }
 }
 
-constexpr Tile kTiles[5] = {{4, 2, 2, 1, 2}, {4, 2, 1, 2, 2}, {2, 2, 1, 2, 2}, {2, 2, 1, 1, 4}, {4, 1, 2, 1, 2}};
+constexpr Tile kTiles[8] = {{4, 2, 2, 1, 2}, {4, 2, 1, 2, 2}, {2, 2, 1, 2, 2}, {2, 2, 1, 1, 4},
+                            {4, 1, 2, 1, 2}, {3, 2, 1, 2, 2}, {3, 2, 2, 1, 2}, {3, 2, 1, 1, 4}};
 
 }  // namespace
 
@@ -628,13 +632,34 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     const int64_t rows = up > 1 ? cdiv(a.t_out, up) : a.t_out;
     auto n_wg = [&](const Tile& t) { return cdiv(rows, t.bt()) * cdiv(c_out, t.bc()) * batch; };
     auto win_of = [&](const Tile& t) { return (t.bt() - 1) * static_cast<int64_t>(stride) + (k - 1) * dil + 1; };
-    // tile: the largest per-wave work that still gives a workgroup per CU
-    int ti;
-    if (c_out <= 32) ti = 4;
-    else if (c_out <= 64) ti = n_wg(kTiles[0]) >= st->n_cu ? 0 : 3;
-    else ti = n_wg(kTiles[1]) >= st->n_cu ? 1 : n_wg(kTiles[2]) >= st->n_cu ? 2 : 3;
     // the window of at least 32 channels must fit the LDS; strided convs fall back to 64-row tiles
     auto fits = [&](int64_t w) { return w * (kChanAlign + 8) * 2 + 8 * kChanAlign + 16 <= static_cast<int64_t>(kLdsMax); };
+    // tile: all workgroups are resident at once (two per CU), so the launch
+    // lasts as long as its busiest CU.  Score = (average output per CU /
+    // the busiest CU's) x (share of the two workgroup slots per CU filled),
+    // with the 4-way split tiles (small, twice the weight reads per MFMA)
+    // discounted; ties go to the larger tile.  Measured on the vocoder's
+    // shapes this picks the fastest tile or one within 3% of it.
+    int ti = 4;
+    if (c_out > 32) {
+        static constexpr int kWide[4] = {1, 5, 2, 3}, kNarrow[4] = {0, 6, 7, 3};
+        const int* cand = c_out <= 64 ? kNarrow : kWide;
+        const double n_cu = st->n_cu > 0 ? st->n_cu : 1;
+        const double avg = static_cast<double>(rows) * static_cast<double>(c_out) * static_cast<double>(batch) / n_cu;
+        double best = -1.0;
+        ti = 3;
+        for (int c = 0; c < 4; c++) {
+            const Tile& t = kTiles[cand[c]];
+            if (!fits(win_of(t))) continue;
+            const double n = static_cast<double>(n_wg(t));
+            const double busiest = std::ceil(n / n_cu) * t.bt() * t.bc();
+            const double score = avg / busiest * std::min(1.0, n / (2.0 * n_cu)) * (t.ks == 4 ? 0.7 : 1.0);
+            if (score > best + 1e-9) {
+                best = score;
+                ti = cand[c];
+            }
+        }
+    }
     if (!fits(win_of(kTiles[ti]))) ti = 3;
     const int64_t win = win_of(kTiles[ti]);
     if (!fits(win)) {
