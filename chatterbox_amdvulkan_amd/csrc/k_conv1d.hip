@@ -79,9 +79,9 @@ constexpr float kSinSmall = 65536.0f;
 // are multiples of the last place of P1 or finer, and the difference is
 // under 1), the q*P2 and q*P3 corrections round once each in their FMAs,
 // and the remaining q * (pi/2 - P1 - P2 - P3) is below 2^-57; then the
-// Taylor polynomial of sin r or cos r on |r| <= pi/4 (+ rounding slack): the first omitted
-// terms are r^11/11! < 2.2e-9 and r^12/12! < 1.2e-10, under half an f32 ulp
-// of the results.  sin(x)^2 = sin(r)^2 for even q, cos(r)^2 for odd q.
+// Taylor polynomial of sin r on |r| <= pi/4 (+ rounding slack): the first
+// omitted term is r^11/11! < 2.2e-9, under half an f32 ulp of the result.
+// sin(x)^2 = sin(r)^2 for even q, cos(r)^2 = 1 - sin(r)^2 for odd q.
 __device__ __forceinline__ float sin_sq_small(float x) {
     const float q = rintf(x * 0x1.45f306p-1f);   // x * 2/pi
     float r = fmaf(q, -0x1.921fb6p+0f, x);
@@ -92,28 +92,9 @@ __device__ __forceinline__ float sin_sq_small(float x) {
     ps = fmaf(ps, r2, 1.0f / 120.0f);
     ps = fmaf(ps, r2, -1.0f / 6.0f);
     ps = fmaf(ps * r2, r, r);
-    float pc = fmaf(r2, -1.0f / 3628800.0f, 1.0f / 40320.0f);
-    pc = fmaf(pc, r2, -1.0f / 720.0f);
-    pc = fmaf(pc, r2, 1.0f / 24.0f);
-    pc = fmaf(pc, r2, -0.5f);
-    pc = fmaf(pc, r2, 1.0f);
-    const float s = (static_cast<int>(q) & 1) ? pc : ps;
-    return s * s;
-}
-
-template <int PRO>
-__device__ __forceinline__ float prologue(float v, float a, float ai, float slope) {
-    if constexpr (PRO == PRO_SNAKE) {
-        // snake(x) = x + sin(x*a)^2 * a_inv in the reference's op order
-        const float xa = v * a;
-        const float s2 = sin_sq_small(xa);
-        const float m = s2 * ai;
-        return v + m;
-    } else if constexpr (PRO == PRO_LEAKY) {
-        return act_leaky(v, slope);
-    } else {
-        return v;
-    }
+    // cos(r)^2 = 1 - sin(r)^2 in one rounding; it is >= 1/2 on |r| <= pi/4,
+    // so nothing cancels
+    return (static_cast<int>(q) & 1) ? fmaf(-ps, ps, 1.0f) : ps * ps;
 }
 
 // WM x WN x KS waves: the output tile is WM x WN wave tiles of (MT*32
@@ -201,7 +182,6 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
         // kSinSmall
         float* sal = reinterpret_cast<float*>(lds + a.win * cs);
         int* big_flag = reinterpret_cast<int*>(sal + 2 * a.kch);
-        bool big = false;
         if constexpr (PRO == PRO_SNAKE) {
             for (int c = tid; c < kch; c += NTH) {
                 const int cc = ci0 + c < a.c_in ? ci0 + c : 0;
@@ -212,24 +192,33 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
             __syncthreads();
         }
         // stage pro(x) rows [base_t, base_t + win) x channels [ci0, ci0 + kch)
-        // as f16.  Element e = tid + NTH*j is window row e / gpr, 4-channel
-        // group e % gpr, both stepped incrementally (one division per chunk).
-        // Every load is issued unconditionally -- from the prepared weights
+        // as f16.  Thread tid owns the 4-channel group g = tid % gpr in rows
+        // tid / gpr + dr * j: dr = NTH / gpr rows per pass (the host keeps
+        // kch <= 4 * NTH); threads past dr * gpr repeat another thread's
+        // group and rows and write the same values.  Batches of kStage
+        // passes that end inside the window run without a row guard.  Every
+        // load is issued unconditionally -- from the prepared weights
         // (always valid) where the element lies outside x -- and zeroed
         // afterwards, so all kStage loads of a lane are in flight together.
         constexpr int kStage = 8;
         const int gpr = kch >> 2;                 // groups per row
-        const int n_el = a.win * gpr;
-        const int dr = NTH / gpr, dg = NTH - dr * gpr;
+        const int dr = NTH / gpr;
+        const int tq = tid < dr * gpr ? tid : tid - dr * gpr;
+        const int r0 = tq / gpr, cg = 4 * (tq - r0 * gpr), ci = ci0 + cg;
         const float* safe = reinterpret_cast<const float*>(a.w);
-        int r_e = tid / gpr, g_e = tid - r_e * gpr;
-        for (int e0 = tid; e0 < n_el; e0 += kStage * NTH) {
+        float4 al4 = make_float4(0.f, 0.f, 0.f, 0.f), ai4 = al4;   // snake: the group's alpha, alpha_inv
+        if constexpr (PRO == PRO_SNAKE) {
+            al4 = *reinterpret_cast<const float4*>(sal + cg);
+            ai4 = *reinterpret_cast<const float4*>(sal + a.kch + cg);
+        }
+        float mx = 0.0f;   // snake: the largest |x * alpha| staged (NaN needs no fix-up: both sins give NaN)
+        auto stage_batch = [&](int p0, auto guarded) {
+            constexpr bool G = decltype(guarded)::value;
             float4 v[kStage];
-            int rr = r_e, gg = g_e;
 #pragma unroll
             for (int i = 0; i < kStage; i++) {
-                const int ti = base_t + rr, ci = ci0 + gg * 4;
-                const bool row_ok = rr < a.win && ti >= 0 && ti < a.t_in;
+                const int rr = r0 + (p0 + i) * dr, ti = base_t + rr;
+                const bool row_ok = (!G || rr < a.win) && ti >= 0 && ti < a.t_in;
                 const float* row = reinterpret_cast<const float*>(xb + static_cast<int64_t>(row_ok ? ti : 0) * a.x_nb1);
                 if constexpr (VEC) {
                     const bool ok = row_ok && ci < a.c_in;
@@ -243,28 +232,22 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
                         set(v[i], q, ok ? t : 0.0f);
                     }
                 }
-                gg += dg;
-                rr += dr;
-                if (gg >= gpr) {
-                    gg -= gpr;
-                    rr++;
-                }
             }
-            rr = r_e;
-            gg = g_e;
 #pragma unroll
             for (int i = 0; i < kStage; i++) {
-                if (rr < a.win) {
-                    const int cg = gg * 4;
+                const int rr = r0 + (p0 + i) * dr;
+                if (!G || rr < a.win) {
                     float4 t = v[i];
-                    if constexpr (PRO != PRO_NONE) {
-                        // pro(0) = 0: padding rows and channels stay 0
+                    // pro(0) = 0: padding rows and channels stay 0
 #pragma unroll
-                        for (int q = 0; q < 4; q++) {
-                            const float al = PRO == PRO_SNAKE ? sal[cg + q] : 0.0f;
-                            const float ai = PRO == PRO_SNAKE ? sal[a.kch + cg + q] : 0.0f;
-                            if constexpr (PRO == PRO_SNAKE) big = big || !(fabsf(get(t, q) * al) < kSinSmall);
-                            set(t, q, prologue<PRO>(get(t, q), al, ai, a.slope));
+                    for (int q = 0; q < 4; q++) {
+                        if constexpr (PRO == PRO_SNAKE) {
+                            // snake(x) = x + sin(x*a)^2 * a_inv in the reference's op order
+                            const float xv = get(t, q), xa = xv * get(al4, q);
+                            mx = fmaxf(mx, fabsf(xa));
+                            set(t, q, xv + sin_sq_small(xa) * get(ai4, q));
+                        } else if constexpr (PRO == PRO_LEAKY) {
+                            set(t, q, act_leaky(get(t, q), a.slope));
                         }
                     }
                     half4 hv;
@@ -274,18 +257,13 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
                     hv[3] = static_cast<_Float16>(t.w);
                     *reinterpret_cast<half4*>(lds + rr * cs + cg) = hv;
                 }
-                gg += dg;
-                rr += dr;
-                if (gg >= gpr) {
-                    gg -= gpr;
-                    rr++;
-                }
             }
-            r_e = rr;
-            g_e = gg;
-        }
+        };
+        int p0 = 0;
+        for (; (p0 + kStage) * dr <= a.win; p0 += kStage) stage_batch(p0, std::false_type{});
+        if (p0 * dr < a.win) stage_batch(p0, std::true_type{});
         if constexpr (PRO == PRO_SNAKE) {
-            if (big) *big_flag = 1;
+            if (!(mx < kSinSmall)) *big_flag = 1;
         }
         __syncthreads();
         if constexpr (PRO == PRO_SNAKE) {
@@ -665,21 +643,29 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     if (!fits(win)) {
         return set_error(CBX_ERR_UNSUPPORTED, "conv1d: one tile's input window exceeds the LDS");
     }
-    // channels per chunk: all of them when they fit, else the most that do
-    int64_t kch = (static_cast<int64_t>(kLdsMax) / (win * 2 + 8) - 8) / kChanAlign * kChanAlign;
-    kch = std::min<int64_t>(kch, c_in_pad);
-    a.win = static_cast<int32_t>(win);
-    a.kch = static_cast<int32_t>(kch);
+    // channels per chunk: all of them when they fit the LDS, else the most
+    // that do, and at most 4 per thread of the workgroup (a thread stages
+    // one 4-channel group of a window row per pass)
+    const int64_t kch_lds = std::min<int64_t>(
+        (static_cast<int64_t>(kLdsMax) / (win * 2 + 8) - 8) / kChanAlign * kChanAlign, c_in_pad);
     const Tile& t = kTiles[ti];
     // waves per wave tile: the most (ks, ks/2, .., 1) whose share of every
     // chunk's steps (K * channels / 16) is even -- a multiple of 4 for the
-    // 4-deep ring
-    const int64_t last = c_in_pad - (cdiv(c_in_pad, kch) - 1) * kch;
-    const int64_t n_full = k * (kch / kBlk), n_last = k * (last / kBlk);
+    // 4-deep ring (with ks = 1 it always is: chunks are multiples of 32)
+    int64_t kch = 0, n_full = 0, n_last = 0;
+    auto plan_chunks = [&](int ks_) {
+        kch = std::min<int64_t>(kch_lds, 4 * 64 * t.wm * t.wn * ks_);
+        const int64_t last = c_in_pad - (cdiv(c_in_pad, kch) - 1) * kch;
+        n_full = k * (kch / kBlk);
+        n_last = k * (last / kBlk);
+    };
     auto steps_ok = [&](int ks_, int pf) { return n_full % (ks_ * pf) == 0 && n_last % (ks_ * pf) == 0; };
     int ks = t.ks;
-    while (ks > 1 && !steps_ok(ks, 2)) ks /= 2;
+    plan_chunks(ks);
+    while (ks > 1 && !steps_ok(ks, 2)) plan_chunks(ks /= 2);
     const bool pf4 = steps_ok(ks, 4);
+    a.win = static_cast<int32_t>(win);
+    a.kch = static_cast<int32_t>(kch);
     // the window (+ snake's alpha, alpha_inv and flag), then the output
     // tile of every wave tile (rows of NT*32 + 4 floats) in the same memory
     const size_t win_bytes = static_cast<size_t>(win) * static_cast<size_t>(kch + 8) * sizeof(_Float16) +
