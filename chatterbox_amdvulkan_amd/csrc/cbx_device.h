@@ -253,6 +253,48 @@ __device__ __forceinline__ float act_leaky(float x, float ns) {
     return ((x > 0.f) ? x : 0.f) + ns * ((x < 0.0f) ? x : 0.f);
 }
 
+// Arguments of sin below this magnitude take sin_sq_small; larger ones (and
+// NaN) take the library sinf.
+constexpr float kSinSmall = 65536.0f;
+
+// sin(x)^2 for |x| < 2^16.  Cody-Waite reduction x = q*pi/2 + r with pi/2
+// split into three f32 parts P1 + P2 + P3: x - q*P1 is exact (x and q*P1
+// are multiples of the last place of P1 or finer, and the difference is
+// under 1), the q*P2 and q*P3 corrections round once each in their FMAs,
+// and the remaining q * (pi/2 - P1 - P2 - P3) is below 2^-57; then the
+// Taylor polynomial of sin r on |r| <= pi/4 (+ rounding slack): the first
+// omitted term is r^11/11! < 2.2e-9, under half an f32 ulp of the result.
+// sin(x)^2 = sin(r)^2 for even q, cos(r)^2 = 1 - sin(r)^2 for odd q (in one
+// rounding; it is >= 1/2 on |r| <= pi/4, so nothing cancels).
+__device__ __forceinline__ float sin_sq_small(float x) {
+    const float q = rintf(x * 0x1.45f306p-1f);   // x * 2/pi
+    float r = fmaf(q, -0x1.921fb6p+0f, x);
+    r = fmaf(q, 0x1.777a5cp-25f, r);
+    r = fmaf(q, 0x1.ee59dap-50f, r);
+    const float r2 = r * r;
+    float ps = fmaf(r2, 1.0f / 362880.0f, -1.0f / 5040.0f);
+    ps = fmaf(ps, r2, 1.0f / 120.0f);
+    ps = fmaf(ps, r2, -1.0f / 6.0f);
+    ps = fmaf(ps * r2, r, r);
+    return (static_cast<int>(q) & 1) ? fmaf(-ps, ps, 1.0f) : ps * ps;
+}
+
+// snake(x) = x + sin(x*a)^2 * a_inv in the order of the five ggml ops of
+// snake() (mul, sin, sqr, mul, add), sin^2 from sin_sq_small below 2^16
+// and from the library sinf (a rarely taken branch) above.
+__device__ __forceinline__ float snake_elem(float xv, float a, float ai) {
+    const float xa = xv * a;
+    float s2;
+    if (fabsf(xa) < kSinSmall) {
+        s2 = sin_sq_small(xa);
+    } else {
+        const float sn = sinf(xa);
+        s2 = sn * sn;
+    }
+    const float m = s2 * ai;
+    return xv + m;
+}
+
 // Runtime-selected activation for epilogues (op is uniform per launch).
 __device__ __forceinline__ float apply_act(int op, float x, const uint16_t* tab, float param) {
     switch (op) {

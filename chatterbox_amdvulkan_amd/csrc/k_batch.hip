@@ -136,13 +136,7 @@ __device__ __forceinline__ void b_swiglu_t(const BOp& op, uint32_t lb) {
     }
 }
 
-__device__ __forceinline__ float b_snake1(float xv, float a, float ai) {
-    const float xa = xv * a;
-    const float sn = sinf(xa);
-    const float s2 = sn * sn;
-    const float m = s2 * ai;
-    return xv + m;
-}
+__device__ __forceinline__ float b_snake1(float xv, float a, float ai) { return snake_elem(xv, a, ai); }
 
 __device__ __forceinline__ void b_snake(const BOp& op, uint32_t lb) {
     const uint32_t i = lb * kThreads + threadIdx.x;

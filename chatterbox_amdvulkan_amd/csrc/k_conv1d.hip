@@ -69,33 +69,10 @@ struct ConvArgs {
 
 enum { PRO_NONE = 0, PRO_SNAKE = 1, PRO_LEAKY = 2 };
 
-// Arguments of sin below this magnitude take sin_sq_small; the rest (and
-// NaN) are recomputed with the library sinf in a separate, rarely entered
-// pass, so the unrolled staging loop carries one short straight-line sin.
-constexpr float kSinSmall = 65536.0f;
-
-// sin(x)^2 for |x| < 2^16.  Cody-Waite reduction x = q*pi/2 + r with pi/2
-// split into three f32 parts P1 + P2 + P3: x - q*P1 is exact (x and q*P1
-// are multiples of the last place of P1 or finer, and the difference is
-// under 1), the q*P2 and q*P3 corrections round once each in their FMAs,
-// and the remaining q * (pi/2 - P1 - P2 - P3) is below 2^-57; then the
-// Taylor polynomial of sin r on |r| <= pi/4 (+ rounding slack): the first
-// omitted term is r^11/11! < 2.2e-9, under half an f32 ulp of the result.
-// sin(x)^2 = sin(r)^2 for even q, cos(r)^2 = 1 - sin(r)^2 for odd q.
-__device__ __forceinline__ float sin_sq_small(float x) {
-    const float q = rintf(x * 0x1.45f306p-1f);   // x * 2/pi
-    float r = fmaf(q, -0x1.921fb6p+0f, x);
-    r = fmaf(q, 0x1.777a5cp-25f, r);
-    r = fmaf(q, 0x1.ee59dap-50f, r);
-    const float r2 = r * r;
-    float ps = fmaf(r2, 1.0f / 362880.0f, -1.0f / 5040.0f);
-    ps = fmaf(ps, r2, 1.0f / 120.0f);
-    ps = fmaf(ps, r2, -1.0f / 6.0f);
-    ps = fmaf(ps * r2, r, r);
-    // cos(r)^2 = 1 - sin(r)^2 in one rounding; it is >= 1/2 on |r| <= pi/4,
-    // so nothing cancels
-    return (static_cast<int>(q) & 1) ? fmaf(-ps, ps, 1.0f) : ps * ps;
-}
+// Snake's sin^2 is sin_sq_small (cbx_device.h) for arguments below
+// kSinSmall; windows holding a larger argument are fixed up element by
+// element with the library sinf in a separate, rarely entered pass, so the
+// unrolled staging loop carries one short straight-line sin.
 
 // WM x WN x KS waves: the output tile is WM x WN wave tiles of (MT*32
 // times) x (NT*32 output channels), and KS waves share each wave tile,
@@ -267,8 +244,8 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
         }
         __syncthreads();
         if constexpr (PRO == PRO_SNAKE) {
-            // rare: arguments of sin at or past kSinSmall (or NaN) get the
-            // library sinf, element by element, over the staged window
+            // rare: arguments of sin at or past kSinSmall get the library
+            // sinf, element by element, over the staged window
             if (*big_flag) {
                 for (int e = tid; e < a.win * kch; e += NTH) {
                     const int r = e / kch, c = e - r * kch;

@@ -12,7 +12,8 @@
 // Each op body is ggml-cpu's scalar expression, compiled without FMA
 // contraction.  GELU reproduces the fp16 table exactly (act_gelu_fast).
 // Other transcendentals (expf, logf, tanhf, erff, sinf) are the device's
-// libm and may differ from the CPU result in the last bit.
+// libm and may differ from the CPU result in the last bit; Snake's sin^2 is
+// the compact sin_sq_small below 2^16 (an ulp or two from the CPU's).
 #include "cbx_device.h"
 
 namespace cbx {
@@ -127,16 +128,10 @@ __global__ __launch_bounds__(kThreads) void k_swiglu_rows(View g, View u, View y
 }
 
 // ---- snake --------------------------------------------------------------------
-// y = x + sin(x*a)^2 * ainv, each step rounded to f32 as the five ggml ops
-// of snake() (mul, sin, sqr, mul, add) round it.
+// y = x + sin(x*a)^2 * ainv (snake_elem: the five ggml ops of snake() in
+// their order).
 
-__device__ __forceinline__ float snake1(float xv, float a, float ai) {
-    const float xa = xv * a;
-    const float sn = sinf(xa);
-    const float s2 = sn * sn;
-    const float m = s2 * ai;
-    return xv + m;
-}
+__device__ __forceinline__ float snake1(float xv, float a, float ai) { return snake_elem(xv, a, ai); }
 
 // Contiguous x/y.  INNER: alpha per element of ne[0] (the reference's (C, T)
 // layout, C % 4 == 0), channel = element % C.  Otherwise alpha per row of
