@@ -128,6 +128,28 @@ def test_snake_zero_and_specials(cbx, oracle):
     assert_close(got, oracle.snake(x, a, ai), x=x, what="snake batch")
 
 
+def test_snake_argument_range(cbx, oracle):
+    """Snake's sin^2 across magnitudes from 2^-30 to 2^30 (the compact
+    reduction below 2^16, the library sinf above), next to multiples of
+    pi/2 (where sin^2 and cos^2 = 1 - sin^2 take turns), and at 0, +-Inf and
+    NaN, against the oracle (glibc sinf)."""
+    rng = np.random.default_rng(57)
+    mag = np.exp2(rng.uniform(-30, 30, 20000))
+    k = rng.integers(-40000, 40000, 20000)
+    near = k * (np.pi / 2) + rng.uniform(-1e-3, 1e-3, 20000)
+    x = np.concatenate([mag * rng.choice([-1.0, 1.0], 20000), near, [0.0, -0.0, np.inf, -np.inf, np.nan, 65535.9,
+                        65536.0, -65536.0, 1e30, -3e38]]).astype(np.float32)
+    x = x[: x.size // 64 * 64].reshape(-1, 64)
+    a = W.uniform_range(58, (64,), 0.5, 1.5)
+    ai = (1.0 / (a + np.float32(1e-9))).astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        exp = oracle.snake(x, a, ai)
+    got = host(cbx.snake(dev(x), dev(a), dev(ai)))
+    fin = np.isfinite(x)
+    assert_close(np.where(fin, got, 0), np.where(fin, exp, 0), x=np.where(fin, x, 0), what="snake range")
+    assert np.array_equal(np.isnan(got), np.isnan(exp))
+
+
 def test_non_contiguous_rows(cbx, oracle):
     big = W.normal(56, (50, 300))
     view = big[:, 7:263]
