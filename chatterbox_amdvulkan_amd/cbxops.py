@@ -178,6 +178,7 @@ def load() -> ctypes.CDLL:
         "cbx_conv1d": (i, [P, vp, i, i, i, i, P, P, f, P, P, P, vp]),
         "cbx_conv_transpose1d_weights_create": (i, [P, i, vp, ctypes.POINTER(vp)]),
         "cbx_conv_transpose1d": (i, [P, vp, i, i, P, P, f, P, P, vp]),
+        "cbx_causal_conv1d": (i, [P, vp, P, P, P, vp]),
         "cbx_run_ops": (i, [ctypes.POINTER(OpStruct), i, vp]),
         "cbx_gguf_open": (i, [ctypes.c_char_p, ctypes.POINTER(vp)]),
         "cbx_gguf_close": (None, [vp]),
@@ -599,6 +600,18 @@ def conv_transpose1d(x, weights: Conv1dWeights, pad=0, prologue=CONV_PRO_NONE, a
     opt = lambda t: _ref(desc(t)) if t is not None else None  # noqa: E731
     _check(load().cbx_conv_transpose1d(_ref(desc(x)), weights.handle, pad, prologue, opt(alpha), opt(alpha_inv), slope,
                                        opt(bias), _ref(desc(out)), _stream()))
+    return out
+
+
+def causal_conv1d(x, weights: Conv1dWeights, mask=None, bias=None, out=None):
+    """CausalConv1d(mask * x) (+ bias): K - 1 zero frames on the left, stride
+    1, T_out = T_in.  x torch [B, T, C_in] or [T, C_in]; mask T floats (the
+    reference's (1, T)) or None; returns [.., T, C_out]."""
+    _ready(x)
+    if out is None:
+        out = torch.empty(tuple(x.shape[:-1]) + (weights.c_out,), dtype=torch.float32, device=x.device)
+    opt = lambda t: _ref(desc(t)) if t is not None else None  # noqa: E731
+    _check(load().cbx_causal_conv1d(_ref(desc(x)), weights.handle, opt(mask), opt(bias), _ref(desc(out)), _stream()))
     return out
 
 

@@ -919,6 +919,35 @@ int cbx_conv_transpose1d(const cbx_tensor* x, const cbx_conv1d_weights* w, int p
                          reinterpret_cast<hipStream_t>(stream));
 }
 
+int cbx_causal_conv1d(const cbx_tensor* x, const cbx_conv1d_weights* w, const cbx_tensor* mask,
+                      const cbx_tensor* bias, cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_causal_conv1d";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if (!w) return set_error(CBX_ERR_INVALID_ARG, "cbx_causal_conv1d: weights are NULL");
+    if ((rc = validate(x, what, "x")) || (rc = validate(y, what, "y"))) return rc;
+    if ((rc = check_conv_x(what, w, x, CBX_CONV_PRO_NONE))) return rc;
+    if (mask) {
+        if ((rc = validate(mask, what, "mask"))) return rc;
+        if (mask->type != CBX_TYPE_F32 || nelements(mask) != x->ne[1] || !is_contiguous(mask)) {
+            return set_error(CBX_ERR_INVALID_ARG, "cbx_causal_conv1d: mask must be contiguous F32 with T elements");
+        }
+    }
+    bool empty = false;
+    if ((rc = check_conv_io(what, w, false, CBX_CONV_PRO_NONE, x, nullptr, nullptr, bias, nullptr, y, x->ne[1],
+                            "T_out = T_in (left padding K - 1)", &empty))) {
+        return rc;
+    }
+    if (empty) return CBX_OK;
+    // a stride-1 conv with K - 1 zero frames on the left; y's length (T_in)
+    // ends the window, so no frame past T_in - 1 is read
+    return launch_conv1d(x, w->data, w->k, w->c_in_pad, w->c_out, 1, static_cast<int>(w->k) - 1, 1, 1, 0, w->w_ph,
+                         mask ? kConvProMask : CBX_CONV_PRO_NONE, mask, nullptr, 0.0f, bias, nullptr, y, st,
+                         reinterpret_cast<hipStream_t>(stream));
+}
+
 int cbx_snake(const cbx_tensor* x, const cbx_tensor* alpha, const cbx_tensor* alpha_inv, cbx_tensor* y,
               cbx_stream stream) {
     const char* what = "cbx_snake";

@@ -99,6 +99,9 @@ int launch_bias_act(int op, const cbx_tensor* x, const cbx_tensor* bias, cbx_ten
 int launch_layer_norm_ext(const cbx_tensor* a, const cbx_tensor* a_bias, const cbx_tensor* r, const cbx_tensor* w,
                           const cbx_tensor* b, const cbx_tensor* mask, float eps, int act, cbx_tensor* s,
                           cbx_tensor* y, DeviceState* st, hipStream_t strm, const char* what);
+// launch_conv1d's prologue past the public ones: x times a per-frame mask
+// (passed as alpha, t_in floats)
+constexpr int kConvProMask = 3;
 // conv1d and transposed conv1d (k_conv1d.hip): padded extents of the
 // prepared f16 weights, the weight conversion (up == 0: conv1d weight
 // (K, C_in, C_out); up >= 1: transposed weight (K, C_out, C_in) split into

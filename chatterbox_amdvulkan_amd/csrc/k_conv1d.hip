@@ -50,7 +50,7 @@ constexpr size_t kLdsMax = 160 * 1024;
 struct ConvArgs {
     const char* x;              // input row (time) t of batch b at x + b*x_nb2 + t*x_nb1
     const _Float16* w;          // fragment-major: [c_out_pad/32][k][c_in_pad/16][64 lanes][8]
-    const float* alpha;         // snake alpha (c_in)
+    const float* alpha;         // snake alpha (c_in); the frame mask (t_in values) for PRO_MASK
     const float* alpha_inv;     // snake alpha_inv (c_in)
     const float* bias;          // (c_out) or null
     const char* res;            // (c_out, t_out, B) or null
@@ -67,7 +67,8 @@ struct ConvArgs {
     float slope;
 };
 
-enum { PRO_NONE = 0, PRO_SNAKE = 1, PRO_LEAKY = 2 };
+// PRO_MASK: x times a per-frame mask (the CFM causal block's pre-mask)
+enum { PRO_NONE = 0, PRO_SNAKE = 1, PRO_LEAKY = 2, PRO_MASK = 3 };
 
 // Snake's sin^2 is sin_sq_small (cbx_device.h) for arguments below
 // kSinSmall; windows holding a larger argument are fixed up element by
@@ -192,11 +193,16 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
         auto stage_batch = [&](int p0, auto guarded) {
             constexpr bool G = decltype(guarded)::value;
             float4 v[kStage];
+            float mv[kStage];   // PRO_MASK: the row's mask value
 #pragma unroll
             for (int i = 0; i < kStage; i++) {
                 const int rr = r0 + (p0 + i) * dr, ti = base_t + rr;
                 const bool row_ok = (!G || rr < a.win) && ti >= 0 && ti < a.t_in;
                 const float* row = reinterpret_cast<const float*>(xb + static_cast<int64_t>(row_ok ? ti : 0) * a.x_nb1);
+                if constexpr (PRO == PRO_MASK) {
+                    const float m = *(row_ok ? a.alpha + ti : safe);
+                    mv[i] = row_ok ? m : 0.0f;
+                }
                 if constexpr (VEC) {
                     const bool ok = row_ok && ci < a.c_in;
                     const float4 t = *reinterpret_cast<const float4*>(ok ? row + ci : safe);
@@ -225,6 +231,8 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
                             set(t, q, xv + sin_sq_small(xa) * get(ai4, q));
                         } else if constexpr (PRO == PRO_LEAKY) {
                             set(t, q, act_leaky(get(t, q), a.slope));
+                        } else if constexpr (PRO == PRO_MASK) {
+                            set(t, q, get(t, q) * mv[i]);
                         }
                     }
                     half4 hv;
@@ -663,6 +671,7 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     switch (pro) {
         case PRO_SNAKE: conv_tile<PRO_SNAKE>(ti, ks, vec, pf4, grid, lds, s, a); break;
         case PRO_LEAKY: conv_tile<PRO_LEAKY>(ti, ks, vec, pf4, grid, lds, s, a); break;
+        case PRO_MASK: conv_tile<PRO_MASK>(ti, ks, vec, pf4, grid, lds, s, a); break;
         default: conv_tile<PRO_NONE>(ti, ks, vec, pf4, grid, lds, s, a); break;
     }
     return check_launch("conv1d");

@@ -324,6 +324,21 @@ int cbx_conv_transpose1d(const cbx_tensor* x, const cbx_conv1d_weights* w,
                          const cbx_tensor* bias, cbx_tensor* y,
                          cbx_stream stream);
 
+/* The CFM decoder's CausalConv1d with causal_block1d's pre-mask in one
+ * kernel (cfm_decoder.cpp:89-120, called at :139-142 after
+ * h = ggml_mul(x, mask)): transpose -> cont -> left pad of K - 1 zero
+ * frames (left_pad_TC, :66-77) -> im2col (F16) -> mul_mat (PREC_F32) ->
+ * + bias -> transpose -> cont.
+ *   y[t][co] = bias[co] + sum_{ci,k} f16(w[co][ci][k]) *
+ *              f16(x[t + k - (K - 1)][ci] * mask[t + k - (K - 1)])
+ * with zero frames before t = 0.  Weights from cbx_conv1d_weights_create.
+ * x: F32 (C_in, T, B, 1); y: F32 (C_out, T, B, 1), not overlapping x;
+ * mask: F32 with T contiguous elements (ggml (1, T)) or NULL; bias: F32
+ * C_out or NULL.                                                           */
+int cbx_causal_conv1d(const cbx_tensor* x, const cbx_conv1d_weights* w,
+                      const cbx_tensor* mask, const cbx_tensor* bias,
+                      cbx_tensor* y, cbx_stream stream);
+
 /* ---- model tables from a GGUF file ---------------------------------------- */
 
 /* The reference reads its weights with ggml's gguf reader: the header,

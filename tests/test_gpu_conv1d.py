@@ -160,6 +160,50 @@ def test_tile_shapes(cbx, oracle, C, C_out, T, B):
     check(oracle, got, x, w, 1, 1, 1, oracle.CONV_PRO_SNAKE, al, ai, sl, b, r, f"{B}x{C}x{T} -> {C_out}")
 
 
+@pytest.mark.parametrize("C_in,C_out,T,B,with_mask", [(256, 256, 500, 1, True), (512, 256, 500, 1, True),
+                                                      (80, 256, 377, 2, False), (256, 80, 500, 1, True)])
+def test_cfm_causal_conv(cbx, oracle, C_in, C_out, T, B, with_mask):
+    """CausalConv1d (cfm_decoder.cpp:89-120) after causal_block1d's pre-mask
+    (:139): the oracle's conv1d of mask * x padded by K - 1 = 2 frames on
+    both sides, first T outputs (output t reads inputs t - 2 .. t), within
+    the conv tolerance."""
+    K = 3
+    sd = W.seed_of(15, C_in + C_out + T)
+    shape = (T, C_in) if B == 1 else (B, T, C_in)
+    x = W.normal(sd, shape)
+    w = W.normal(sd + 1, (C_out, C_in, K), 0.0, 1.0 / np.sqrt(C_in * K))
+    b = W.normal(sd + 2, (C_out,), 0.0, 0.1)
+    mask = np.ones(T, dtype=np.float32)
+    mask[T - T // 5:] = 0.0
+    xm = (x * mask[:, None]).astype(np.float32) if with_mask else x
+    ref = oracle.conv1d(xm, w, 1, K - 1, 1, oracle.CONV_PRO_NONE, None, None, 0.0, b, None, nth=8)[..., :T, :]
+    mag = oracle.conv1d(np.abs(xm), np.abs(w), 1, K - 1, 1, nth=8)[..., :T, :].astype(np.float64)
+    wts = cbx.Conv1dWeights(dev(w))
+    got = host(cbx.causal_conv1d(dev(x), wts, dev(mask) if with_mask else None, dev(b)))
+    wts.close()
+    d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    bound = 2.0 ** -13 * mag + 2.0 ** -22 * np.abs(ref)
+    assert got.shape == ref.shape
+    assert not (d > bound).any(), f"{int((d > bound).sum())} outside the bound"
+
+
+def test_causal_conv_errors(cbx):
+    L = cbx.load()
+    d = lambda t: ctypes.byref(cbx.desc(t))  # noqa: E731
+    wts = cbx.Conv1dWeights(torch.zeros((16, 32, 3), device="cuda"))
+    x, y = torch.zeros((100, 32), device="cuda"), torch.zeros((100, 16), device="cuda")
+    assert L.cbx_causal_conv1d(d(x), wts.handle, None, None, d(y), None) == cbx.OK, cbx.last_error()
+    bad_mask = torch.ones(99, device="cuda")
+    assert L.cbx_causal_conv1d(d(x), wts.handle, d(bad_mask), None, d(y), None) == cbx.ERR_INVALID_ARG
+    assert "mask" in cbx.last_error()
+    y_short = torch.zeros((98, 16), device="cuda")
+    assert L.cbx_causal_conv1d(d(x), wts.handle, None, None, d(y_short), None) == cbx.ERR_INVALID_ARG
+    up = cbx.Conv1dWeights(torch.zeros((32, 16, 4), device="cuda"), transpose_stride=2)
+    assert L.cbx_causal_conv1d(d(x), up.handle, None, None, d(y), None) == cbx.ERR_INVALID_ARG
+    wts.close()
+    up.close()
+
+
 def test_errors(cbx):
     L = cbx.load()
     w = torch.zeros((16, 32, 3), device="cuda")
