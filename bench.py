@@ -635,6 +635,28 @@ def bench_hift_conv(C, W, torch, reps=60):
         wt.close()
         del bufs, Rs, x0
     out["upsample"] = ups
+    # the CFM decoder's causal_block1d conv: mul(x, mask) -> CausalConv1d K 3
+    # (+ bias), cfm_decoder.cpp:89-120,139-142, on [2, C_in, 500] frames
+    # (the CFG pair); algorithmic FLOPs 2*C_in*C_out*3*T*B
+    cfm = {}
+    for (Ci, Co, T, B) in ((256, 256, 500, 2), (512, 256, 500, 2)):
+        nbytes = 4 * B * T * (Ci + Co)
+        n_sets = sets_for(nbytes)
+        x0 = d(W.normal(W.seed_of(8, 2000 + Ci), (B, T, Ci)))
+        bufs = [{"x": x0 if i == 0 else x0.clone(), "y": torch.empty((B, T, Co), dtype=torch.float32, device="cuda")}
+                for i in range(n_sets)]
+        mask = torch.ones(T, dtype=torch.float32, device="cuda")
+        bias = d(W.normal(W.seed_of(8, 2001 + Ci), (Co,), 0.0, 0.1))
+        wt = C.Conv1dWeights(d(W.normal(W.seed_of(8, 2002 + Ci), (Co, Ci, 3), 0.0, 1.0 / np.sqrt(Ci * 3))))
+        rm, rb = C.ctypes.byref(C.desc(mask)), C.ctypes.byref(C.desc(bias))
+        Rs = [{k: C.ctypes.byref(C.desc(v)) for k, v in b.items()} for b in bufs]
+        fns = [lambda st, R=R: check_rc(C, L.cbx_causal_conv1d(R["x"], wt.handle, rm, rb, R["y"], st)) for R in Rs]
+        fns[0](cur_stream(torch))
+        us = per_launch_ms(torch, fns, max(reps, 2 * n_sets)) * 1000.0
+        cfm[f"{B}x{Ci}x{T}_to_{Co}"] = rate(2.0 * Ci * Co * 3 * T * B, nbytes, us, buffer_sets=n_sets)
+        wt.close()
+        del bufs, Rs, x0
+    out["cfm_causal_conv"] = cfm
     return out
 
 

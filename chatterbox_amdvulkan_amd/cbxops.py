@@ -108,13 +108,14 @@ class GLaunch(ctypes.Structure):
 # cbx_gop
 GOP_VIEW, GOP_GET_ROWS, GOP_ADD, GOP_MUL, GOP_SCALE, GOP_NORM, GOP_RMS_NORM, GOP_GROUP_NORM, GOP_ROPE, \
     GOP_SOFT_MAX, GOP_DIAG_MASK_INF, GOP_UNARY, GOP_LEAKY_RELU, GOP_CPY, GOP_IM2COL, GOP_MUL_MAT, \
-    GOP_CONV_TRANSPOSE_1D = range(17)
+    GOP_CONV_TRANSPOSE_1D, GOP_CONCAT = range(18)
 # cbx_glaunch_kind
 GL_UNSUPPORTED, GL_VIEW, GL_GET_ROWS, GL_GET_ROWS_ADD, GL_GET_ROWS_ADD_LAYER_NORM, GL_NORM, GL_LAYER_NORM, \
     GL_LAYER_NORM_ROPE, GL_RMS_NORM, GL_GROUP_NORM, GL_SOFT_MAX, GL_SNAKE, GL_UNARY, GL_SWIGLU, GL_LEAKY_RELU, \
-    GL_ROPE, GL_CPY, GL_ADD_LAYER_NORM, GL_LAYER_NORM_MASK, GL_BIAS_ACT, GL_CONV1D, GL_CONV_TRANSPOSE1D = range(22)
+    GL_ROPE, GL_CPY, GL_ADD_LAYER_NORM, GL_LAYER_NORM_MASK, GL_BIAS_ACT, GL_CONV1D, GL_CONV_TRANSPOSE1D, \
+    GL_CAUSAL_CONV1D = range(23)
 # conv launch flags: the prologue (bits 0-1), a bias add, the residual add
-GLF_SNAKE, GLF_LEAKY, GLF_BIAS, GLF_RESIDUAL = 1, 2, 4, 8
+GLF_SNAKE, GLF_LEAKY, GLF_MASK, GLF_BIAS, GLF_RESIDUAL = 1, 2, 3, 4, 8
 
 # cbx_op_kind
 OP_LAYER_NORM, OP_RMS_NORM, OP_UNARY, OP_LEAKY_RELU, OP_SWIGLU, OP_ROPE, OP_GET_ROWS, \

@@ -17,7 +17,10 @@
 // mul_mat -> bias add -> transpose -> cont (conv1d_CT, hift_vocoder.cpp:
 // 77-93) or the same around conv_transpose_1d and a cropping view
 // (conv_transpose1d_CT, :96-115), after snake() or leaky_relu and, in a
-// ResBlock, before the residual add (:128-135).  The planner walks
+// ResBlock, before the residual add (:128-135); the CFM decoder's
+// causal_conv1d pads K-1 zero frames on the left with a zero-scaled view
+// and a concat before its im2col (cfm_decoder.cpp:66-120), after
+// causal_block1d's mul(x, mask) (:139).  The planner walks
 // the nodes in order and, at each node, takes the longest such chain whose
 // intermediate results no other node reads and the caller does not keep;
 // the chain then runs as one library call.  Because a chain is a run of
@@ -216,6 +219,59 @@ struct Planner {
         return tail ? 5 + tail : 0;
     }
 
+    // causal_conv1d of x (C_in, T, 1) at node i (cfm_decoder.cpp:89-120):
+    // transpose -> cont (read twice) -> view of its first K-1 frames ->
+    // cont -> scale(0) -> concat(zeros, cont, dim 0) -> im2col (stride 1,
+    // padding 0, dilation 1) -> view (2-D) -> view (weight 2-D) -> mul_mat
+    // (with prepared weights) -> conv_tail.  The node count, or 0; *fl gets
+    // bit 2 for the bias add.
+    int32_t causal_at(int32_t i, int32_t x, int32_t* fl) const {
+        if (!valid_t(x) || !is(i, CBX_GOP_VIEW) || nd[i].src[0] != x || !is(i + 1, CBX_GOP_CPY)) return 0;
+        const cbx_tensor& X = t[x];
+        const int32_t v = nd[i].dst, c = nd[i + 1].dst;
+        if (X.ne[2] != 1 || X.ne[3] != 1 || !dims(v, X.ne[1], X.ne[0], 1, 1) || t[v].data != X.data ||
+            !internal(v, 1) || nd[i + 1].src[0] != v || !same_dims(c, v) || !internal(c, 2)) {
+            return 0;
+        }
+        if (!is(i + 2, CBX_GOP_VIEW) || nd[i + 2].src[0] != c || !is(i + 3, CBX_GOP_CPY) ||
+            !is(i + 4, CBX_GOP_SCALE) || !is(i + 5, CBX_GOP_CONCAT)) {
+            return 0;
+        }
+        const int32_t zv = nd[i + 2].dst, zc = nd[i + 3].dst, zs = nd[i + 4].dst, pd = nd[i + 5].dst;
+        if (!valid_t(zv)) return 0;
+        const int64_t pad = t[zv].ne[0];
+        if (pad < 1 || !dims(zv, pad, X.ne[0], 1, 1) || t[zv].data != t[c].data || t[zv].nb[1] != t[c].nb[1] ||
+            !internal(zv, 1) || nd[i + 3].src[0] != zv || !same_dims(zc, zv) || !internal(zc, 1) ||
+            nd[i + 4].src[0] != zc || nd[i + 4].fparam != 0.0f || !same_dims(zs, zv) || !internal(zs, 1) ||
+            nd[i + 5].src[0] != zs || nd[i + 5].src[1] != c || nd[i + 5].iparam != 0 ||
+            !dims(pd, X.ne[1] + pad, X.ne[0], 1, 1) || !internal(pd, 1)) {
+            return 0;
+        }
+        if (!is(i + 6, CBX_GOP_IM2COL) || nd[i + 6].src[1] != pd) return 0;
+        const cbx_gnode& ic = nd[i + 6];
+        const int32_t wk = ic.src[0], col = ic.dst;
+        if (!valid_t(wk) || !valid_t(col) || !internal(col, 1)) return 0;
+        const cbx_tensor& Wk = t[wk];
+        const int64_t K = Wk.ne[0], C_in = Wk.ne[1], C_out = Wk.ne[2], T = X.ne[1];
+        if (C_in != X.ne[0] || Wk.ne[3] != 1 || K - 1 != pad || ic.conv[0] != 1 || ic.conv[1] != 0 ||
+            ic.conv[2] != 1 || !dims(col, C_in * K, T, 1, 1)) {
+            return 0;
+        }
+        if (!is(i + 7, CBX_GOP_VIEW) || nd[i + 7].src[0] != col || !is(i + 8, CBX_GOP_VIEW) ||
+            nd[i + 8].src[0] != wk || !is(i + 9, CBX_GOP_MUL_MAT)) {
+            return 0;
+        }
+        const int32_t col2 = nd[i + 7].dst, w2 = nd[i + 8].dst, mm = nd[i + 9].dst;
+        if (!dims(col2, C_in * K, T, 1, 1) || !internal(col2, 1) || !dims(w2, K * C_in, C_out, 1, 1) ||
+            !internal(w2, 1) || nd[i + 9].src[0] != col2 || nd[i + 9].src[1] != w2 || !nd[i + 9].conv_w ||
+            !dims(mm, T, C_out, 1, 1) || !internal(mm, 1)) {
+            return 0;
+        }
+        int32_t out = -1;
+        const int32_t tail = conv_tail_at(i + 10, mm, fl, &out);
+        return tail ? 10 + tail : 0;
+    }
+
     // A conv chain starting at node i whose input is x (the prologue's
     // output, or the chain's own input): CONV1D / CONV_TRANSPOSE1D and its
     // node count, or UNSUPPORTED.
@@ -238,6 +294,11 @@ struct Planner {
                     *len = n;
                     *flags = fl;
                     return k;
+                }
+                if ((n = causal_at(i, a.src[0], &fl))) {
+                    *len = n;
+                    *flags = fl;
+                    return CBX_GL_CAUSAL_CONV1D;
                 }
                 return CBX_GL_VIEW;
             }
@@ -370,6 +431,16 @@ struct Planner {
                     *len = 5;
                     return CBX_GL_SNAKE;
                 }
+                // causal_block1d's mul(x, mask (1, T)) before a causal conv
+                if (valid_t(x) && dims(al, 1, t[x].ne[1], 1, 1) && internal(a.dst, 1)) {
+                    int32_t fl = 3;
+                    const int32_t n = causal_at(i + 1, a.dst, &fl);
+                    if (n) {
+                        *len = 1 + n;
+                        *flags = fl;
+                        return CBX_GL_CAUSAL_CONV1D;
+                    }
+                }
                 return CBX_GL_UNSUPPORTED;
             }
             case CBX_GOP_UNARY: {
@@ -424,6 +495,7 @@ const char* op_name(int op) {
         case CBX_GOP_IM2COL: return "IM2COL";
         case CBX_GOP_MUL_MAT: return "MUL_MAT";
         case CBX_GOP_CONV_TRANSPOSE_1D: return "CONV_TRANSPOSE_1D";
+        case CBX_GOP_CONCAT: return "CONCAT";
         default: return "unknown op";
     }
 }
@@ -495,8 +567,9 @@ constexpr int32_t kSpan[][2] = {
     {1, 4},  // BIAS_ACT [act | mish]
     {9, 17}, // CONV1D [snake | leaky] [bias] [residual]
     {7, 14}, // CONV_TRANSPOSE1D [snake | leaky] [bias]
+    {12, 15}, // CAUSAL_CONV1D [mask] [bias]
 };
-constexpr int32_t kLastKind = CBX_GL_CONV_TRANSPOSE1D;
+constexpr int32_t kLastKind = CBX_GL_CAUSAL_CONV1D;
 static_assert(sizeof(kSpan) / sizeof(kSpan[0]) == kLastKind + 1, "one span per launch kind");
 
 // Issues the entry point a launch maps to.  A launch is only read within
@@ -658,6 +731,23 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
             const int64_t off = static_cast<const char*>(crop->data) - static_cast<const char*>(full->data);
             if (off < 0 || off % 4 || off / 4 > (int64_t{1} << 30)) break;
             return cbx_conv_transpose1d(x, nd[b0 + 2].conv_w, static_cast<int>(off / 4), cp, al, ai, slope, bt, y, s);
+        }
+        case CBX_GL_CAUSAL_CONV1D: {
+            // [mask ->] 12 nodes [+ bias 2]
+            const bool masked = (l.flags & 3) == 3, bias = (l.flags & 4) != 0;
+            if (((l.flags & 3) != 0 && !masked) || (l.flags & 8) ||
+                l.n_nodes != (masked ? 1 : 0) + 12 + (bias ? 2 : 0)) {
+                break;
+            }
+            const int32_t b0 = f + (masked ? 1 : 0);   // the transpose view
+            const cbx_gnode& wn = nd[b0 + 9];
+            const cbx_tensor* wk = T(t, nd[b0 + 6].src[0]);
+            if (!wk || !conv1d_weights_match(wn.conv_w, 0, wk->ne[0], wk->ne[1], wk->ne[2])) {
+                return set_error(CBX_ERR_INVALID_ARG, "cbx_graph_launch: node " + std::to_string(b0 + 9) +
+                                                          ": conv_w was not made from the node's weight tensor");
+            }
+            return cbx_causal_conv1d(T(t, a.src[0]), wn.conv_w, masked ? T(t, a.src[1]) : nullptr,
+                                     bias ? T(t, nd[b0 + 10].src[0]) : nullptr, y, s);
         }
         default:
             break;

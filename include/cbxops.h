@@ -461,7 +461,13 @@ int cbx_run_ops(const cbx_op* ops, int n_ops, cbx_stream stream);
  *            (transpose) -> CPY (cont)
  * and run as one cbx_conv1d / cbx_conv_transpose1d call with the weights
  * the backend prepared at load time, given on the MUL_MAT /
- * CONV_TRANSPOSE_1D node (conv_w).                                         */
+ * CONV_TRANSPOSE_1D node (conv_w).  The CFM decoder's causal_conv1d
+ * (cfm_decoder.cpp:89-120), optionally after causal_block1d's
+ * MUL(x, mask), runs as one cbx_causal_conv1d call:
+ *   VIEW (transpose) -> CPY (cont) -> VIEW (its first K-1 frames) -> CPY
+ *   -> SCALE (0) -> CONCAT (zeros, cont; dim 0) -> IM2COL (1, 0, 1) ->
+ *   VIEW (2-D) -> VIEW (weight 2-D) -> MUL_MAT [-> VIEW (bias) -> ADD] ->
+ *   VIEW (transpose) -> CPY (cont)                                          */
 typedef enum cbx_gop {
     CBX_GOP_VIEW          = 0,  /* dst describes src0's memory                       */
     CBX_GOP_GET_ROWS      = 1,  /* src0 table, src1 ids I32                           */
@@ -480,6 +486,7 @@ typedef enum cbx_gop {
     CBX_GOP_IM2COL        = 14, /* src0 kernel (shape), src1 data; conv = s0, p0, d0 */
     CBX_GOP_MUL_MAT       = 15, /* src0 x src1 (only inside a conv1d chain); conv_w */
     CBX_GOP_CONV_TRANSPOSE_1D = 16, /* src0 kernel, src1 data; conv[0] = s0; conv_w */
+    CBX_GOP_CONCAT        = 17, /* src0 then src1 along dim iparam              */
 } cbx_gop;
 
 typedef struct cbx_gnode {
@@ -519,6 +526,7 @@ typedef enum cbx_glaunch_kind {
     CBX_GL_BIAS_ACT,          /* add(x, bias) [-> unary op | -> mish chain]     */
     CBX_GL_CONV1D,            /* [snake | leaky_relu ->] conv1d chain [-> add(x, .)] */
     CBX_GL_CONV_TRANSPOSE1D,  /* [snake | leaky_relu ->] transposed conv chain  */
+    CBX_GL_CAUSAL_CONV1D,     /* [mul(x, mask (1, T)) ->] causal conv chain     */
 } cbx_glaunch_kind;
 
 typedef struct cbx_glaunch {
@@ -528,8 +536,8 @@ typedef struct cbx_glaunch {
     int32_t flags;        /* bit 0: an intermediate the fused kernel may skip
                              storing (the embedding sum h nobody reads).
                              Conv kinds: bits 0-1 the prologue (0 none, 1
-                             snake, 2 leaky_relu), bit 2 a bias add, bit 3 the
-                             residual add.                                      */
+                             snake, 2 leaky_relu, 3 the frame mask), bit 2 a
+                             bias add, bit 3 the residual add.                  */
 } cbx_glaunch;
 
 /* Splits nodes[0..n_nodes) into launches, in order, covering every node

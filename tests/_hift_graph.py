@@ -4,7 +4,9 @@ im2col to F16, mul_mat and a reshape, the bias add, between two
 transposes; conv_1d_f32 at :46-58), conv_transpose1d_CT (:96-116:
 conv_transpose_1d, a cropping view and cont, the bias add, between two
 transposes), composed as resblock_forward's sublayer (:119-138), conv_post
-(:748-749) and an upsampler (:685-687).
+(:748-749) and an upsampler (:685-687); and the CFM decoder's
+causal_conv1d (cfm_decoder.cpp:89-120, its left padding from left_pad_TC at
+:66-77) after causal_block1d's mul(x, mask) (:139).
 
 Tensors are torch tensors laid out as ggml's (torch shape = reversed ne);
 views share their source's storage, so the planner sees what the ggml graph
@@ -99,3 +101,36 @@ class HiftGraph:
         h = self.snake(h, p["a2"], p["ai2"])
         h = self.conv1d(h, p["w2"], p["b2"], 1, (K - 1) // 2, 1, conv_w2)
         return self.add(x, h)
+
+    def causal_conv1d(self, x: int, w: int, b, conv_w) -> int:
+        """causal_conv1d of x (ggml (C_in, T)); w torch [C_out, C_in, K]: K - 1
+        zero frames from a zero-scaled view of the first frames, concatenated
+        in front, then im2col (stride 1, no padding) and mul_mat."""
+        C_out, C_in, K = self.at(w).shape
+        T = self.at(x).shape[-2]
+        xt = self.transposed_copy(x)
+        zv = self.node_view(self.at(xt)[:, :K - 1], xt)
+        zc = self.node_new(C.GOP_CPY, (C_in, K - 1), (zv,))
+        zs = self.node_new(C.GOP_SCALE, (C_in, K - 1), (zc,), fparam=0.0)
+        pd = self.node_new(C.GOP_CONCAT, (C_in, T + K - 1), (zs, xt), iparam=0)
+        col = self.node_new(C.GOP_IM2COL, (1, T, C_in * K), (w, pd), dtype=torch.float16, conv=(1, 0, 1))
+        col2 = self.node_view(self.at(col).reshape(T, C_in * K), col)
+        w2 = self.node_view(self.at(w).reshape(C_out, C_in * K), w)
+        mm = self.node_new(C.GOP_MUL_MAT, (C_out, T), (col2, w2), conv_w=conv_w)
+        return self.tail(mm, b)
+
+    def mul(self, a: int, b: int) -> int:
+        return self.node_new(C.GOP_MUL, tuple(self.at(a).shape), (a, b))
+
+    def causal_block(self, x: int, mask: int, w: int, b: int, ln_w: int, ln_b: int, conv_w, eps=1e-5) -> int:
+        """causal_block1d (cfm_decoder.cpp:133-149): mul(x, mask) -> causal
+        conv (+ bias) -> layer_norm -> mish -> mul(., mask)."""
+        h = self.causal_conv1d(self.mul(x, mask), w, b, conv_w)
+        sh = tuple(self.at(h).shape)
+        n = self.node_new(C.GOP_NORM, sh, (h,), fparam=eps)
+        m = self.node_new(C.GOP_MUL, sh, (n, ln_w))
+        y = self.node_new(C.GOP_ADD, sh, (m, ln_b))
+        sp = self.node_new(C.GOP_UNARY, sh, (y,), iparam=C.SOFTPLUS)
+        th = self.node_new(C.GOP_UNARY, sh, (sp,), iparam=C.TANH)
+        mi = self.node_new(C.GOP_MUL, sh, (y, th))
+        return self.mul(mi, mask)

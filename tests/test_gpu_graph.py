@@ -339,3 +339,39 @@ def test_conv_weights_of_another_shape_are_refused(cbx):
     with pytest.raises(cbx.CbxError, match="conv_w was not made from the node's weight tensor"):
         h.g.compute()
     other.close()
+
+
+def test_cfm_causal_block_nodes(cbx, oracle):
+    """causal_block1d (cfm_decoder.cpp:133-149) as the reference's node list:
+    mul(x, mask) -> causal_conv1d (+ bias) in one launch, layer_norm -> mish
+    -> mul(mask) in another.  The conv output is checked against the oracle's
+    conv of mask * x (K - 1 zero frames in front) within the conv
+    tolerance; the tail against the oracle's nodes on that output."""
+    from tests._hift_graph import HiftGraph
+
+    T, C_in, C_out, K = 500, 256, 256, 3
+    sd = W.seed_of(16, 0)
+    x = W.normal(sd, (T, C_in))
+    mask = np.ones((T, 1), dtype=np.float32)
+    mask[T - 60:] = 0.0
+    w = W.normal(sd + 1, (C_out, C_in, K), 0.0, 1.0 / np.sqrt(C_in * K))
+    b = W.normal(sd + 2, (C_out,), 0.0, 0.1)
+    lw = W.normal(sd + 3, (C_out,), 1.0, 0.02)
+    lb = W.normal(sd + 4, (C_out,), 0.0, 0.02)
+    h = HiftGraph(dev_new)
+    tx, tm, tw, tb, tlw, tlb = (h.t(dev(v)) for v in (x, mask, w, b, lw, lb))
+    wts = cbx.Conv1dWeights(h.at(tw))
+    y = h.causal_block(tx, tm, tw, tb, tlw, tlb, wts)
+    plan = h.g.plan()
+    assert plan == [(cbx.GL_CAUSAL_CONV1D, 0, 15, cbx.GLF_MASK | cbx.GLF_BIAS), (cbx.GL_LAYER_NORM_MASK, 15, 7, 0)]
+    assert h.g.compute() == 2
+    conv = host(h.at(h.g.nodes[14].dst))
+    xm = oracle.mul(x, mask)
+    ref = oracle.conv1d(xm, w, 1, K - 1, 1, oracle.CONV_PRO_NONE, None, None, 0.0, b, None, nth=8)[:T]
+    mag = oracle.conv1d(np.abs(xm), np.abs(w), 1, K - 1, 1, nth=8)[:T].astype(np.float64)
+    d = np.abs(conv.astype(np.float64) - ref.astype(np.float64))
+    assert not (d > 2.0 ** -13 * mag + 2.0 ** -22 * np.abs(ref)).any()
+    ln = oracle.add(oracle.mul(oracle.norm(conv, 1e-5), lw), lb)
+    exp = oracle.mul(oracle.mul(ln, oracle.unary(oracle.TANH, oracle.unary(oracle.SOFTPLUS, ln))), mask)
+    assert_close(host(h.at(y)), exp, x=ln, what="causal block tail")
+    wts.close()

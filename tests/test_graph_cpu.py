@@ -360,7 +360,7 @@ def test_random_lists_plan_into_an_exact_cover():
              C.GL_SOFT_MAX: {1, 2, 3}, C.GL_SNAKE: {5}, C.GL_UNARY: {1, 3}, C.GL_SWIGLU: {2},
              C.GL_LEAKY_RELU: {1}, C.GL_ROPE: {1}, C.GL_CPY: {1}, C.GL_ADD_LAYER_NORM: {4, 5, 7, 8},
              C.GL_LAYER_NORM_MASK: {4, 7}, C.GL_BIAS_ACT: {1, 2, 4}, C.GL_CONV1D: set(range(9, 18)),
-             C.GL_CONV_TRANSPOSE1D: set(range(7, 15))}
+             C.GL_CONV_TRANSPOSE1D: set(range(7, 15)), C.GL_CAUSAL_CONV1D: set(range(12, 16))}
     shapes = [(4, 8), (8,), (1, 8, 1, 1), (4, 8), (4, 1)]
     for trial in range(200):
         g = C.Graph()
@@ -368,7 +368,7 @@ def test_random_lists_plan_into_an_exact_cover():
         for k in range(n_t):
             g.tensor(f32(*shapes[int(rng.integers(0, len(shapes)))]))
         for k in range(int(rng.integers(1, 25))):
-            op = int(rng.integers(0, 17))
+            op = int(rng.integers(0, 18))
             src = [int(rng.integers(-1, n_t)) for _ in range(2)]
             g.node(op, int(rng.integers(0, n_t)), src, iparam=int(rng.integers(-1, 9)),
                    fparam=float(rng.choice([1.0, 0.5, 1e-5])))
@@ -506,3 +506,51 @@ def test_hand_made_conv_launches_are_refused():
     for l in bad:
         assert L.cbx_graph_launch(T, nt, N, nn, ctypes.byref(l), None) == C.ERR_INVALID_ARG, \
             (l.kind, l.first_node, l.n_nodes, l.flags)
+
+
+def test_cfm_causal_block():
+    """causal_block1d (cfm_decoder.cpp:133-149): mul(x, mask) and the causal
+    conv's 14 nodes (with its bias add) are one causal-conv launch, then
+    layer_norm -> mish -> mul(mask) one more."""
+    h = HiftGraph(host_new)
+    x, mask = h.t(f32(50, 32)), h.t(f32(50, 1))
+    w, b = h.t(torch.zeros(64, 32, 3, dtype=torch.float16)), h.t(f32(64))
+    lw, lb = h.t(f32(64)), h.t(f32(64))
+    h.causal_block(x, mask, w, b, lw, lb, DUMMY_W)
+    assert h.g.plan() == [(C.GL_CAUSAL_CONV1D, 0, 15, C.GLF_MASK | C.GLF_BIAS), (C.GL_LAYER_NORM_MASK, 15, 7, 0)]
+    # hand-made launches whose flags do not fit the 15 nodes are refused before any weights are read
+    L = C.load()
+    T_, N_, _ = _raw(h.g)
+    for l in (C.GLaunch(C.GL_CAUSAL_CONV1D, 0, 15, C.GLF_BIAS), C.GLaunch(C.GL_CAUSAL_CONV1D, 0, 15, C.GLF_SNAKE),
+              C.GLaunch(C.GL_CAUSAL_CONV1D, 0, 15, C.GLF_MASK | C.GLF_BIAS | C.GLF_RESIDUAL),
+              C.GLaunch(C.GL_CAUSAL_CONV1D, 0, 11, 0)):
+        assert L.cbx_graph_launch(T_, len(h.g._descs), N_, len(h.g.nodes), ctypes.byref(l), None) == C.ERR_INVALID_ARG
+
+
+def test_causal_conv_forms():
+    # no mask, no bias: 12 nodes
+    h = HiftGraph(host_new)
+    x = h.t(f32(40, 16))
+    h.causal_conv1d(x, h.t(torch.zeros(24, 16, 4)), None, DUMMY_W)
+    assert h.g.plan() == [(C.GL_CAUSAL_CONV1D, 0, 12, 0)]
+    # the caller keeps the transposed copy: not fused
+    x_tc = h.g.nodes[1].dst
+    assert C.GL_CAUSAL_CONV1D not in [q[0] for q in h.g.plan(keep=[x_tc])]
+    # a padding of K - 2 frames is not a causal conv of this weight
+    h = HiftGraph(host_new)
+    x = h.t(f32(40, 16))
+    h.causal_conv1d(x, h.t(torch.zeros(24, 16, 4)), None, DUMMY_W)
+    zv = h.g.nodes[2].dst
+    h.g._descs[zv] = C.desc(h.at(h.g.nodes[1].dst)[:, :2])
+    assert C.GL_CAUSAL_CONV1D not in [q[0] for q in h.g.plan()]
+    # no prepared weights: the mul_mat stays the caller's
+    h = HiftGraph(host_new)
+    x = h.t(f32(40, 16))
+    h.causal_conv1d(x, h.t(torch.zeros(24, 16, 3)), None, None)
+    assert C.GL_CAUSAL_CONV1D not in [q[0] for q in h.g.plan()]
+    # a mask that is not one value per frame is a plain multiply
+    h = HiftGraph(host_new)
+    x = h.t(f32(40, 16))
+    m = h.t(f32(40, 16))
+    h.causal_conv1d(h.mul(x, m), h.t(torch.zeros(24, 16, 3)), None, DUMMY_W)
+    assert h.g.plan()[:2] == [(C.GL_UNSUPPORTED, 0, 1, 0), (C.GL_CAUSAL_CONV1D, 1, 12, 0)]
