@@ -517,12 +517,13 @@ void conv_tile(int t, int ks, bool vec, bool pf4, dim3 grid, size_t lds, hipStre
         case 4: conv_ks<PRO, 4, 1, 2, 1, 2>(ks, vec, pf4, grid, lds, s, a); break;   // 256 x 32
         case 5: conv_ks<PRO, 3, 2, 1, 2, 2>(ks, vec, pf4, grid, lds, s, a); break;   // 96 x 128
         case 6: conv_ks<PRO, 3, 2, 2, 1, 2>(ks, vec, pf4, grid, lds, s, a); break;   // 192 x 64
-        default: conv_ks<PRO, 3, 2, 1, 1, 4>(ks, vec, pf4, grid, lds, s, a); break;  // 96 x 64
+        case 7: conv_ks<PRO, 3, 2, 1, 1, 4>(ks, vec, pf4, grid, lds, s, a); break;   // 96 x 64
+        default: conv_ks<PRO, 1, 2, 1, 1, 4>(ks, vec, pf4, grid, lds, s, a); break;  // 32 x 64
     }
 }
 
-constexpr Tile kTiles[8] = {{4, 2, 2, 1, 2}, {4, 2, 1, 2, 2}, {2, 2, 1, 2, 2}, {2, 2, 1, 1, 4},
-                            {4, 1, 2, 1, 2}, {3, 2, 1, 2, 2}, {3, 2, 2, 1, 2}, {3, 2, 1, 1, 4}};
+constexpr Tile kTiles[9] = {{4, 2, 2, 1, 2}, {4, 2, 1, 2, 2}, {2, 2, 1, 2, 2}, {2, 2, 1, 1, 4}, {4, 1, 2, 1, 2},
+                            {3, 2, 1, 2, 2}, {3, 2, 2, 1, 2}, {3, 2, 1, 1, 4}, {1, 2, 1, 1, 4}};
 
 }  // namespace
 
@@ -602,16 +603,17 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     // the busiest CU's) x (share of the two workgroup slots per CU filled),
     // with the 4-way split tiles (small, twice the weight reads per MFMA)
     // discounted; ties go to the larger tile.  Measured on the vocoder's
-    // shapes this picks the fastest tile or one within 3% of it.
+    // and the CFM decoder's shapes this picks the fastest tile or one within
+    // 3% of it.
     int ti = 4;
     if (c_out > 32) {
-        static constexpr int kWide[4] = {1, 5, 2, 3}, kNarrow[4] = {0, 6, 7, 3};
+        static constexpr int kWide[5] = {1, 5, 2, 3, 8}, kNarrow[5] = {0, 6, 7, 3, 8};
         const int* cand = c_out <= 64 ? kNarrow : kWide;
         const double n_cu = st->n_cu > 0 ? st->n_cu : 1;
         const double avg = static_cast<double>(rows) * static_cast<double>(c_out) * static_cast<double>(batch) / n_cu;
         double best = -1.0;
         ti = 3;
-        for (int c = 0; c < 4; c++) {
+        for (int c = 0; c < 5; c++) {
             const Tile& t = kTiles[cand[c]];
             if (!fits(win_of(t))) continue;
             const double n = static_cast<double>(n_wg(t));

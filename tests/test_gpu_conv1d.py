@@ -149,11 +149,14 @@ def test_hift_stage_shape(cbx, oracle):
     check(oracle, got, x, w, 1, 25, 5, oracle.CONV_PRO_SNAKE, al, ai, sl, b, r, "64x24000 K11 d5")
 
 
-@pytest.mark.parametrize("C,C_out,T,B", [(64, 512, 685, 16), (64, 64, 5050, 16), (64, 64, 3013, 16)])
+@pytest.mark.parametrize("C,C_out,T,B", [(64, 64, 14362, 8), (64, 128, 3983, 16), (64, 128, 26196, 1),
+                                         (64, 64, 8154, 4), (64, 512, 685, 16), (64, 64, 5050, 16),
+                                         (64, 64, 3013, 16), (64, 64, 2000, 1)])
 def test_tile_shapes(cbx, oracle, C, C_out, T, B):
-    """Batched convs whose output counts pick the 96-frame tiles on a
-    256-CU device (96 x 128 with KS 2, 192 x 64, 96 x 64 with KS 4), Snake
-    prologue, bias and residual."""
+    """Convs whose output counts pick each tile shape on a 256-CU device
+    (256 x 64, 128 x 128, 64 x 128, 64 x 64 with KS 4, 96 x 128, 192 x 64,
+    96 x 64 with KS 4, 32 x 64 with KS 4), Snake prologue, bias and
+    residual."""
     x, w, al, ai, b, r, sl = case(oracle, C, T, C_out, 3, 1, 1, 1, oracle.CONV_PRO_SNAKE, with_res=True, B=B,
                                   seed=70 + C_out + T)
     got = run(cbx, x, w, 1, 1, 1, cbx.CONV_PRO_SNAKE, al, ai, sl, b, r)
