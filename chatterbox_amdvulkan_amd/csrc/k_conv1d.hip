@@ -2,8 +2,9 @@
 // (channel innermost) as an implicit GEMM on the matrix cores, with the
 // activation that precedes the conv applied while the input is staged:
 // Snake in the ResBlocks (hift_vocoder.cpp:119-138), LeakyReLU before
-// conv_post (:748-749).  Bias and the ResBlock's residual add are fused into
-// the store.
+// conv_post (:748-749), and for the CFM decoder's causal conv the frame mask
+// of causal_block1d (cfm_decoder.cpp:89-120,139; K-1 frames of left
+// padding).  Bias and the ResBlock's residual add are fused into the store.
 //
 // Arithmetic class of the reference (conv_1d_f32, hift_vocoder.cpp:46-59):
 // im2col rounds the conv input to f16, mul_mat rounds the weights to f16 and
