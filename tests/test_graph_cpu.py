@@ -554,3 +554,50 @@ def test_causal_conv_forms():
     m = h.t(f32(40, 16))
     h.causal_conv1d(h.mul(x, m), h.t(torch.zeros(24, 16, 3)), None, DUMMY_W)
     assert h.g.plan()[:2] == [(C.GL_UNSUPPORTED, 0, 1, 0), (C.GL_CAUSAL_CONV1D, 1, 12, 0)]
+
+
+def test_mutated_conv_chains_plan_into_an_exact_cover():
+    """The reference's conv chains (a ResBlock layer, an upsampler, a causal
+    block) with one node field changed at random -- an operand, the op, a
+    parameter, the prepared weights -- still plan into an exact cover of the
+    list, each launch within its kind's span (no chain is misread past its
+    nodes, nothing runs off the list)."""
+    spans = {C.GL_CONV1D: range(9, 18), C.GL_CONV_TRANSPOSE1D: range(7, 15), C.GL_CAUSAL_CONV1D: range(12, 16)}
+    rng = np.random.default_rng(11)
+
+    def lists():
+        h = HiftGraph(host_new)
+        h.sublayer(h.t(f32(40, 16)), hift_params(h), 3, DUMMY_W, DUMMY_W)
+        yield h
+        h = HiftGraph(host_new)
+        h.conv_transpose1d(h.leaky(h.t(f32(12, 32)), 0.1), h.t(torch.zeros(32, 16, 8)), h.t(f32(16)), 4, 2, DUMMY_W)
+        yield h
+        h = HiftGraph(host_new)
+        h.causal_block(h.t(f32(50, 32)), h.t(f32(50, 1)), h.t(torch.zeros(64, 32, 3)), h.t(f32(64)), h.t(f32(64)),
+                       h.t(f32(64)), DUMMY_W)
+        yield h
+
+    for trial in range(300):
+        for h in lists():
+            g = h.g
+            n = g.nodes[int(rng.integers(0, len(g.nodes)))]
+            field = int(rng.integers(0, 6))
+            if field == 0:
+                n.src[0] = int(rng.integers(-1, len(g._descs)))
+            elif field == 1:
+                n.src[1] = int(rng.integers(-1, len(g._descs)))
+            elif field == 2:
+                n.op = int(rng.integers(0, 18))
+            elif field == 3:
+                n.dst = int(rng.integers(0, len(g._descs)))
+            elif field == 4:
+                n.conv[int(rng.integers(0, 3))] = int(rng.integers(-1, 4))
+            else:
+                n.conv_w = None if n.conv_w else DUMMY_W
+            at = 0
+            for kind, first, cnt, flags in g.plan():
+                assert first == at, (trial, kind)
+                if kind in spans:
+                    assert cnt in spans[kind], (trial, kind, cnt)
+                at += cnt
+            assert at == len(g.nodes)
