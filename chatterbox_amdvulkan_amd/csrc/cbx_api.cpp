@@ -941,6 +941,7 @@ int cbx_causal_conv1d(const cbx_tensor* x, const cbx_conv1d_weights* w, const cb
         return rc;
     }
     if (empty) return CBX_OK;
+    if (mask && overlaps(mask, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_causal_conv1d: y must not overlap mask");
     // a stride-1 conv with K - 1 zero frames on the left; y's length (T_in)
     // ends the window, so no frame past T_in - 1 is read
     return launch_conv1d(x, w->data, w->k, w->c_in_pad, w->c_out, 1, static_cast<int>(w->k) - 1, 1, 1, 0, w->w_ph,

@@ -201,6 +201,10 @@ def test_causal_conv_errors(cbx):
     assert "mask" in cbx.last_error()
     y_short = torch.zeros((98, 16), device="cuda")
     assert L.cbx_causal_conv1d(d(x), wts.handle, None, None, d(y_short), None) == cbx.ERR_INVALID_ARG
+    buf = torch.zeros(1600, device="cuda")           # the mask is y's last 100 floats
+    yv, mv = buf.view(100, 16), buf[1500:]
+    assert L.cbx_causal_conv1d(d(x), wts.handle, d(mv), None, d(yv), None) == cbx.ERR_INVALID_ARG
+    assert "overlap" in cbx.last_error()
     up = cbx.Conv1dWeights(torch.zeros((32, 16, 4), device="cuda"), transpose_stride=2)
     assert L.cbx_causal_conv1d(d(x), up.handle, None, None, d(y), None) == cbx.ERR_INVALID_ARG
     wts.close()
