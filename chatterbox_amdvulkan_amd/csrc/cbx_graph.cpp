@@ -164,8 +164,13 @@ struct Planner {
         const int32_t wk = nd[i + 2].src[0], col = nd[i + 2].dst;
         if (!valid_t(wk) || !valid_t(col) || !internal(col, 1)) return 0;
         const cbx_tensor &X = t[x], &Wk = t[wk], &Col = t[col];
+        // one batch item only: for N > 1 the graph's reshape of the (OL*N,
+        // OC) product to (OL, OC, N) does not separate the items, so the
+        // nodes would not compute a batched conv
         const int64_t K = Wk.ne[0], C_in = Wk.ne[1], C_out = Wk.ne[2], B = X.ne[2], T_out = Col.ne[1];
-        if (C_in != X.ne[0] || Wk.ne[3] != 1 || Col.ne[0] != C_in * K || Col.ne[2] != B || X.ne[3] != 1) return 0;
+        if (C_in != X.ne[0] || Wk.ne[3] != 1 || Col.ne[0] != C_in * K || Col.ne[2] != B || B != 1 || X.ne[3] != 1) {
+            return 0;
+        }
         if (!is(i + 3, CBX_GOP_VIEW) || nd[i + 3].src[0] != col || !is(i + 4, CBX_GOP_VIEW) ||
             nd[i + 4].src[0] != wk || !is(i + 5, CBX_GOP_MUL_MAT)) {
             return 0;

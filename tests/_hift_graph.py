@@ -68,14 +68,15 @@ class HiftGraph:
         """conv1d_CT of x (ggml (C_in, T)); w torch [C_out, C_in, K]."""
         C_out, C_in, K = self.at(w).shape
         T_in = self.at(x).shape[-2]
+        B = self.at(x).shape[0] if self.at(x).dim() == 3 else 1
         T_out = (T_in + 2 * pad - dil * (K - 1) - 1) // stride + 1
         xt = self.transposed_copy(x)
-        col = self.node_new(C.GOP_IM2COL, (1, T_out, C_in * K), (w, xt), dtype=torch.float16,
+        col = self.node_new(C.GOP_IM2COL, (B, T_out, C_in * K), (w, xt), dtype=torch.float16,
                             conv=(stride, pad, dil))
-        col2 = self.node_view(self.at(col).reshape(T_out, C_in * K), col)
+        col2 = self.node_view(self.at(col).reshape(B * T_out, C_in * K), col)
         w2 = self.node_view(self.at(w).reshape(C_out, C_in * K), w)
-        mm = self.node_new(C.GOP_MUL_MAT, (C_out, T_out), (col2, w2), conv_w=conv_w)
-        y3 = self.node_view(self.at(mm).reshape(1, C_out, T_out), mm)
+        mm = self.node_new(C.GOP_MUL_MAT, (C_out, B * T_out), (col2, w2), conv_w=conv_w)
+        y3 = self.node_view(self.at(mm).reshape(B, C_out, T_out), mm)
         return self.tail(y3, b)
 
     def conv_transpose1d(self, x: int, w: int, b, stride: int, pad: int, conv_w) -> int:

@@ -481,6 +481,13 @@ def test_conv_chains_that_do_not_fuse():
     h.conv1d(x, h.t(torch.zeros(16, 8, 3)), None, 1, 1, 1, DUMMY_W)
     assert C.GL_CONV1D not in [q[0] for q in h.g.plan()]
 
+    # conv1d_CT over two batch items: the graph's (OL*N, OC) -> (OL, OC, N)
+    # reshape mixes the items, so the chain is not a batched conv
+    h = HiftGraph(host_new)
+    x = h.t(f32(2, 40, 16))
+    h.conv1d(x, h.t(torch.zeros(16, 16, 3)), None, 1, 1, 1, DUMMY_W)
+    assert C.GL_CONV1D not in [q[0] for q in h.g.plan()]
+
     # a transposed conv over two batch items: not the reference's shape
     h = HiftGraph(host_new)
     x = h.t(f32(2, 12, 32))
