@@ -302,6 +302,30 @@ def test_resblock_sublayer_nodes(cbx, oracle, Ch, T, K, d):
         w_.close()
 
 
+def test_conv_pre_nodes(cbx, oracle):
+    """conv_pre (hift_vocoder.cpp:673): conv1d_CT with no prologue, K 7,
+    padding 3, bias, 80 mel channels in -> 512 out, as the reference's nine
+    nodes plus the bias add: one conv launch, checked against the oracle's
+    conv1d within the conv tolerance."""
+    from tests._hift_graph import HiftGraph
+    from tests.test_gpu_conv1d import check
+
+    T, C_in, C_out, K = 300, 80, 512, 7
+    sd = W.seed_of(17, 0)
+    x = W.normal(sd, (T, C_in))
+    w = W.normal(sd + 1, (C_out, C_in, K), 0.0, 1.0 / np.sqrt(C_in * K))
+    b = W.normal(sd + 2, (C_out,), 0.0, 0.1)
+    h = HiftGraph(dev_new)
+    tx, tw, tb = h.t(dev(x)), h.t(dev(w)), h.t(dev(b))
+    wts = cbx.Conv1dWeights(h.at(tw))
+    y = h.conv1d(tx, tw, tb, 1, 3, 1, wts)
+    assert h.g.plan() == [(cbx.GL_CONV1D, 0, 11, cbx.GLF_BIAS)]
+    assert h.g.compute() == 1
+    check(oracle, host(h.at(y)).reshape(T, C_out), x, w, 1, 3, 1, oracle.CONV_PRO_NONE, None, None, 0.0, b, None,
+          "conv_pre nodes")
+    wts.close()
+
+
 @pytest.mark.parametrize("C_in,C_out,s,K,T", [(256, 128, 5, 11, 200), (128, 64, 3, 7, 500)])
 def test_upsampler_nodes(cbx, oracle, C_in, C_out, s, K, T):
     """leaky_relu -> conv_transpose1d_CT (hift_vocoder.cpp:686-687) as the
