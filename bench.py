@@ -130,19 +130,44 @@ def capture(torch, fn):
     return g
 
 
-def time_graph_steps(torch, graphs_all, graphs_one, n_sets, steps):
-    """Replay exactly `steps` steps: whole rotations, then single-set graphs."""
-    full, rem = divmod(steps, n_sets)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(full):
-        graphs_all.replay()
-    for i in range(rem):
-        graphs_one[i].replay()
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1)
+class StepGraphs:
+    """HIP graphs that replay exactly `steps` steps over the buffer sets in
+    order: whole rotations (one graph holding a step per set), then a graph
+    of the first `steps mod n_sets` sets.  Every graph is replayed before
+    anything is timed: a graph's first replay uploads it and costs several
+    times a later one."""
+
+    def __init__(self, torch, step_fns, steps):
+        self.torch = torch
+        self.full, rem = divmod(steps, len(step_fns))
+        self.g_all = capture(torch, lambda s: [f(s) for f in step_fns]) if self.full else None
+        self.g_rem = capture(torch, lambda s: [f(s) for f in step_fns[:rem]]) if rem else None
+
+    def replay(self):
+        for _ in range(self.full):
+            self.g_all.replay()
+        if self.g_rem is not None:
+            self.g_rem.replay()
+
+    def warm(self, warmup_steps, n_sets):
+        """At least `warmup_steps` untimed steps, every graph replayed."""
+        if self.g_all is not None:
+            for _ in range(max(1, math.ceil(warmup_steps / n_sets))):
+                self.g_all.replay()
+        if self.g_rem is not None:
+            self.g_rem.replay()
+        self.torch.cuda.synchronize()
+
+    def time_ms(self):
+        """Milliseconds for the steps, events on the launch stream."""
+        torch = self.torch
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        self.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
 
 
 def per_launch_ms(torch, fns, reps):
@@ -203,11 +228,9 @@ def bench_prefill(C, W, torch, steps, warmup, f16_table=False, fused=True, one_l
         for k in ("h", "ln", "g"):
             st.t[k].zero_()
 
-    g_all = capture(torch, lambda s: [step(st)(s) for st in sets])
-    g_one = [capture(torch, step(st)) for st in sets]
-    time_graph_steps(torch, g_all, g_one, n_sets, warmup)
-    ms = time_graph_steps(torch, g_all, g_one, n_sets, steps)
-    torch.cuda.synchronize()
+    graphs = StepGraphs(torch, [step(st) for st in sets], steps)
+    graphs.warm(warmup, n_sets)
+    ms = graphs.time_ms()
     for k, v in eager.items():
         if not same_bits(sets[0].t[k].cpu().numpy(), v):
             raise SystemExit(f"bench: graph replay result {k} differs from the eager launch")
@@ -222,7 +245,7 @@ def bench_prefill(C, W, torch, steps, warmup, f16_table=False, fused=True, one_l
         k_ms = {"gather_pos": per_launch_ms(torch, [st.gather for st in sets], reps),
                 "layer_norm": per_launch_ms(torch, [st.layer_norm for st in sets], reps),
                 "gelu": per_launch_ms(torch, [st.gelu for st in sets], reps)}
-    del g_all, g_one, sets
+    del graphs, sets
     return {"ms_per_step": ms / steps, "bytes_per_step": per_step, "n_sets": n_sets,
             "kernel_ms": k_ms, "kernel_bytes": nbytes}
 

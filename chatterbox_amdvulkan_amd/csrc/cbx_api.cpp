@@ -841,7 +841,21 @@ static int check_conv_io(const char* what, const cbx_conv1d_weights* w, bool tra
         }
     }
     *empty = nelements(y) == 0;
-    if (!*empty && overlaps(x, y)) return set_error(CBX_ERR_INVALID_ARG, f + ": y must not overlap x");
+    if (*empty) return CBX_OK;
+    if (overlaps(x, y)) return set_error(CBX_ERR_INVALID_ARG, f + ": y must not overlap x");
+    // Other workgroups' tile stores would race with this workgroup's reads
+    // of bias / alpha (staging) and res (epilogue): none may share y's bytes,
+    // except res being exactly y (same data and strides: each output is read
+    // and then written by the one thread that owns it).
+    if (bias && overlaps(bias, y)) return set_error(CBX_ERR_INVALID_ARG, f + ": bias must not overlap y");
+    if (prologue == CBX_CONV_PRO_SNAKE && (overlaps(alpha, y) || overlaps(alpha_inv, y))) {
+        return set_error(CBX_ERR_INVALID_ARG, f + ": alpha and alpha_inv must not overlap y");
+    }
+    if (res && overlaps(res, y)) {
+        bool same = res->data == y->data;
+        for (int i = 0; i < 4; i++) same = same && res->nb[i] == y->nb[i];
+        if (!same) return set_error(CBX_ERR_INVALID_ARG, f + ": res must be y itself or not overlap it");
+    }
     return CBX_OK;
 }
 

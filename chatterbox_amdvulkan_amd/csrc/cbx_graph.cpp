@@ -424,10 +424,15 @@ struct Planner {
                     nd[i + 3].src[0] == nd[i + 2].dst && same_dims(nd[i + 3].src[1], al) && is(i + 4, CBX_GOP_ADD) &&
                     nd[i + 4].src[0] == x && nd[i + 4].src[1] == nd[i + 3].dst && internal(a.dst, 1) &&
                     internal(nd[i + 1].dst, 1) && internal(nd[i + 2].dst, 1) && internal(nd[i + 3].dst, 1)) {
-                    // snake() as the prologue of a conv: one conv launch
+                    // snake() as the prologue of a conv: one conv launch.
+                    // The conv's prologue reads alpha per input channel,
+                    // i.e. along ne0 of the (C, T) input: a (1, T) alpha
+                    // (one value per frame) is a snake of its own.
                     const int32_t h = nd[i + 4].dst;
+                    const bool per_channel = row_vec(al, x) && row_vec(nd[i + 3].src[1], x);
                     int32_t n = 0, fl = 1;
-                    const int32_t k = internal(h, 1) ? conv_chain_at(i + 5, h, &n, &fl) : CBX_GL_UNSUPPORTED;
+                    const int32_t k = per_channel && internal(h, 1) ? conv_chain_at(i + 5, h, &n, &fl)
+                                                                    : CBX_GL_UNSUPPORTED;
                     if (k != CBX_GL_UNSUPPORTED) {
                         *len = 5 + n;
                         *flags = fl;

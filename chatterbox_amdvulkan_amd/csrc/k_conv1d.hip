@@ -35,6 +35,10 @@
 // Fragment layout of v_mfma_f32_32x32x16_f16 (checked on the device):
 // lane l holds A[l % 32][8*(l/32) + j] and B[8*(l/32) + j][l % 32], j < 8;
 // accumulator register r of lane l is D[8*(r/4) + 4*(l/32) + r%4][l % 32].
+#include <mutex>
+#include <set>
+#include <utility>
+
 #include "cbx_device.h"
 
 namespace cbx {
@@ -477,15 +481,20 @@ struct Tile {
 template <typename K>
 void conv_launch(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, const ConvArgs& a) {
     // windows past 64 KiB use the larger LDS of gfx950 (160 KiB per
-    // workgroup): raise the kernel's limit once per device
+    // workgroup): raise the limit of each kernel once per device (every
+    // instantiation has the same function type, so the record is keyed on
+    // the kernel's address)
     if (lds > 64 * 1024) {
-        constexpr int kDevs = 64;
-        static bool raised[kDevs] = {};
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevs || !raised[dev]) {
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsMax));
-            if (dev >= 0 && dev < kDevs) raised[dev] = true;
+        static std::mutex mu;
+        static std::set<std::pair<int, const void*>> raised;
+        const void* fn = reinterpret_cast<const void*>(kernel);
+        int dev = -1;
+        (void)hipGetDevice(&dev);
+        std::lock_guard<std::mutex> lock(mu);
+        if (raised.count({dev, fn}) == 0 &&
+            hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsMax)) ==
+                hipSuccess) {
+            raised.insert({dev, fn});
         }
     }
     hipLaunchKernelGGL(kernel, grid, block, lds, s, a);

@@ -235,6 +235,27 @@ def test_errors(cbx):
     assert L.cbx_conv1d(d(x), None, 1, 1, 1, 0, None, None, 0.0, None, None, d(y), None) == cbx.ERR_INVALID_ARG
     assert L.cbx_conv1d(d(x), wts.handle, 0, 1, 1, 0, None, None, 0.0, None, None, d(y), None) == \
         cbx.ERR_INVALID_ARG
+    # bias, alpha, alpha_inv overlapping y; res overlapping y other than as y
+    # itself (other workgroups' tile stores would race with their reads)
+    buf = torch.zeros(1700, device="cuda")
+    yb = buf[:1600].view(100, 16)
+    assert L.cbx_conv1d(d(x), wts.handle, 1, 1, 1, 0, None, None, 0.0, d(buf[1584:1600]), None, d(yb), None) == \
+        cbx.ERR_INVALID_ARG
+    assert "bias" in cbx.last_error()
+    a32 = torch.ones(32, device="cuda")
+    snake_y = torch.zeros(3300, device="cuda")
+    ys = snake_y[:1600].view(100, 16)
+    for al, ai in ((snake_y[:32], a32), (a32, snake_y[1590:1622])):
+        assert L.cbx_conv1d(d(x), wts.handle, 1, 1, 1, cbx.CONV_PRO_SNAKE, d(al), d(ai), 0.0, None, None, d(ys),
+                            None) == cbx.ERR_INVALID_ARG
+        assert "alpha" in cbx.last_error()
+    shifted = buf[16:1616].view(100, 16)
+    assert L.cbx_conv1d(d(x), wts.handle, 1, 1, 1, 0, None, None, 0.0, None, d(shifted), d(yb), None) == \
+        cbx.ERR_INVALID_ARG
+    assert "res" in cbx.last_error()
+    # res == y (same memory, same strides) is the documented in-place residual
+    assert L.cbx_conv1d(d(x), wts.handle, 1, 1, 1, 0, None, None, 0.0, None, d(yb), d(yb), None) == cbx.OK
+    torch.cuda.synchronize()
     wts.close()
 
 

@@ -475,6 +475,17 @@ def test_conv_chains_that_do_not_fuse():
     h.add(s, y)
     assert h.g.plan() == [(C.GL_SNAKE, 0, 5, 0), (C.GL_CONV1D, 5, 12, C.GLF_BIAS | C.GLF_RESIDUAL)]
 
+    # alpha with one value per frame ((1, T), legal for a standalone snake)
+    # is not the conv prologue's per-channel alpha, even when T == C_in: the
+    # snake runs alone and the conv takes no prologue
+    for T in (16, 40):
+        h = HiftGraph(host_new)
+        x = h.t(f32(T, 16))
+        a, ai = h.t(f32(T, 1)), h.t(f32(T, 1))
+        w, b = h.t(torch.zeros(16, 16, 3, dtype=torch.float16)), h.t(f32(16))
+        h.conv1d(h.snake(x, a, ai), w, b, 1, 1, 1, DUMMY_W)
+        assert h.g.plan() == [(C.GL_SNAKE, 0, 5, 0), (C.GL_CONV1D, 5, 11, C.GLF_BIAS)], T
+
     # a weight whose C_in is not x's
     h = HiftGraph(host_new)
     x = h.t(f32(40, 16))
