@@ -48,6 +48,9 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="skip the secondary workloads")
     ap.add_argument("--hift-conv", action="store_true",
                     help="only the HiFT conv1d / transposed-conv timings, as one JSON object (for profiling)")
+    ap.add_argument("--only", choices=["decode", "serving", "cfm", "hift", "softmax", "t3_block", "hift_conv",
+                                       "copy"],
+                    help="run one secondary workload alone and print its JSON (no headline line)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the launches used by the FETCH_SIZE/WRITE_SIZE counter runs")
     return ap.parse_args()
@@ -417,7 +420,17 @@ def bench_cfm(C, W, torch, reps=400):
         ro = C.ctypes.byref(C.desc(t["ya_rope"].view(2, W.CFM_T, W.CFM_HEADS, W.HEAD_DIM)))
         sets.append((t, r, ra, ro))
 
+    ws = C.GroupNormWorkspace()
+
     def gn(key):
+        """GroupNorm+affine+Mish with the statistics split over chunk
+        workgroups (cbx_group_norm_ws; one workspace, stream-ordered)."""
+        return lambda st: (lambda s: check_rc(C, L.cbx_group_norm_ws(st[1]["x" + key], W.CFM_GROUPS, 1e-5,
+                                                                     st[1]["w" + key], st[1]["b" + key], C.MISH,
+                                                                     st[1]["y" + key], ws.handle, s)))
+
+    def gn_whole(key):
+        """The same op with every workgroup reducing its whole group (cbx_group_norm)."""
         return lambda st: (lambda s: check_rc(C, L.cbx_group_norm(st[1]["x" + key], W.CFM_GROUPS, 1e-5,
                                                                   st[1]["w" + key], st[1]["b" + key], C.MISH,
                                                                   st[1]["y" + key], s)))
@@ -436,6 +449,8 @@ def bench_cfm(C, W, torch, reps=400):
 
     out = {}
     for name, mk in (("group_norm_mish_256", gn("256")), ("group_norm_mish_512", gn("512")),
+                     ("group_norm_mish_256_whole_group_per_workgroup", gn_whole("256")),
+                     ("group_norm_mish_512_whole_group_per_workgroup", gn_whole("512")),
                      ("layer_norm_1024x512", ln), ("rope_2x500x8x64", rope), ("layer_norm_rope_fused", ln_rope)):
         fns = [mk(st) for st in sets]
         for f in fns:
@@ -455,11 +470,24 @@ def bench_cfm(C, W, torch, reps=400):
                                     "layer_norm_rope [2,500,512]"}
     for k in ("group_norm_mish_256", "group_norm_mish_512"):
         out[k]["GBps"] = nb[k] / (out[k]["us"] * 1e-6) / 1e9
+        out[k + "_whole_group_per_workgroup"]["GBps"] = nb[k] / (out[k + "_whole_group_per_workgroup"]["us"] *
+                                                                 1e-6) / 1e9
+    # the split must reproduce the whole-group kernel bit for bit
+    t0 = sets[0][0]
+    for key in ("256", "512"):
+        gn(key)(sets[0])(cur_stream(torch))
+        torch.cuda.synchronize()
+        split = t0["y" + key].cpu().numpy()
+        gn_whole(key)(sets[0])(cur_stream(torch))
+        torch.cuda.synchronize()
+        if not same_bits(split, t0["y" + key].cpu().numpy()):
+            raise SystemExit(f"bench: split GroupNorm [2,{key},500] differs from the whole-group kernel")
     out["layer_norm_rope_fused"]["GBps"] = nb["layer_norm_rope"] / (out["layer_norm_rope_fused"]["us"] * 1e-6) / 1e9
     lr = out["layer_norm_1024x512"]["us"] + out["rope_2x500x8x64"]["us"]
     out["layer_norm_then_rope_GBps_vs_fused_bytes"] = nb["layer_norm_rope"] / (lr * 1e-6) / 1e9
     out["flow_step"]["GBps"] = per_step / (out["flow_step"]["us"] * 1e-6) / 1e9
     cache.close()
+    ws.close()
     return dict(out, bytes_per_flow_step=per_step, bytes=nb, buffer_sets=n_sets)
 
 
@@ -964,6 +992,19 @@ def main():
     if a.hift_conv:
         print(json.dumps({"hift_resblock_conv": bench_hift_conv(C, W, torch)}), flush=True)
         return 0
+    if a.only:
+        nb = W.prefill_bytes()
+        fn = {"decode": lambda: bench_decode(C, W, torch), "serving": lambda: bench_serving(C, W, torch),
+              "cfm": lambda: bench_cfm(C, W, torch), "hift": lambda: bench_hift(C, W, torch),
+              "softmax": lambda: bench_softmax(C, W, torch), "t3_block": lambda: bench_t3_block(C, W, torch),
+              "hift_conv": lambda: bench_hift_conv(C, W, torch),
+              "copy": lambda: bench_copy_ceiling(C, torch, {"gelu_bytes": nb["gelu"],
+                                                            "embed_layer_norm_bytes": nb["embed_layer_norm"],
+                                                            "chain_bytes": sum(nb.values()),
+                                                            "group_norm_256_bytes": W.cfm_bytes()["group_norm_mish_256"],
+                                                            "group_norm_512_bytes": W.cfm_bytes()["group_norm_mish_512"]})}
+        print(json.dumps({a.only: fn[a.only]()}), flush=True)
+        return 0
     res = bench_prefill(C, W, torch, a.steps, a.warmup)
     details = {"prefill_f32_fused": {k: v for k, v in res.items()}}
     if not a.quick:
@@ -979,9 +1020,12 @@ def main():
         rr = bench_prefill(C, W, torch, max(200, a.steps // 4), 20, resident=True)
         details["prefill_f32_fused_cache_resident"] = dict(rr, GBps=gbps(rr))
         nb = W.prefill_bytes()
+        cb = W.cfm_bytes()
         details["copy_ceiling"] = bench_copy_ceiling(C, torch, {"gelu_bytes": nb["gelu"],
                                                                 "embed_layer_norm_bytes": nb["embed_layer_norm"],
-                                                                "chain_bytes": sum(nb.values())})
+                                                                "chain_bytes": sum(nb.values()),
+                                                                "group_norm_256_bytes": cb["group_norm_mish_256"],
+                                                                "group_norm_512_bytes": cb["group_norm_mish_512"]})
         log("decode")
         details["t3_decode"] = bench_decode(C, W, torch)
         log("serving")

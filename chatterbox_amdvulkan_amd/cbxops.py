@@ -158,6 +158,10 @@ def load() -> ctypes.CDLL:
         "cbx_rms_norm": (i, [P, f, P, vp]),
         "cbx_rms_norm_mul": (i, [P, P, f, P, vp]),
         "cbx_group_norm": (i, [P, i, f, P, P, i, P, vp]),
+        "cbx_group_norm_workspace_create": (i, [ctypes.POINTER(vp)]),
+        "cbx_group_norm_workspace_destroy": (None, [vp]),
+        "cbx_group_norm_workspace_tune": (i, [vp, ctypes.c_uint32, ctypes.c_int32]),
+        "cbx_group_norm_ws": (i, [P, i, f, P, P, i, P, vp, vp]),
         "cbx_rope_cache_create": (i, [i, i, i, f, f, f, f, f, f, vp, ctypes.c_int32, ctypes.POINTER(vp)]),
         "cbx_rope_cache_destroy": (None, [vp]),
         "cbx_rope_ext": (i, [P, P, vp, P, vp]),
@@ -381,6 +385,45 @@ def group_norm(x, n_groups, eps, w=None, b=None, act=UNARY_NONE, out=None):
     out = _out_like(x, out)
     _check(load().cbx_group_norm(_ref(desc(x)), n_groups, eps, _ref(desc(w)) if w is not None else None,
                                  _ref(desc(b)) if b is not None else None, act, _ref(desc(out)), _stream()))
+    return out
+
+
+class GroupNormWorkspace:
+    """cbx_group_norm_workspace: partial sums and arrival counters of the
+    split-reduction GroupNorm (one call at a time per workspace)."""
+
+    def __init__(self, device: Optional[int] = None, max_wait_us: Optional[int] = None, n_chunks: int = 0):
+        dev = torch.cuda.current_device() if device is None else int(device)
+        init(dev)
+        h = ctypes.c_void_p()
+        with torch.cuda.device(dev):
+            _check(load().cbx_group_norm_workspace_create(ctypes.byref(h)))
+        self.handle = h
+        if max_wait_us is not None or n_chunks:
+            self.tune(2000 if max_wait_us is None else max_wait_us, n_chunks)
+
+    def tune(self, max_wait_us: int, n_chunks: int = 0):
+        _check(load().cbx_group_norm_workspace_tune(self.handle, max_wait_us, n_chunks))
+
+    def close(self):
+        if self.handle:
+            load().cbx_group_norm_workspace_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def group_norm_ws(x, n_groups, eps, ws: GroupNormWorkspace, w=None, b=None, act=UNARY_NONE, out=None):
+    """group_norm with the statistics split over many workgroups (same results)."""
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_group_norm_ws(_ref(desc(x)), n_groups, eps, _ref(desc(w)) if w is not None else None,
+                                    _ref(desc(b)) if b is not None else None, act, _ref(desc(out)), ws.handle,
+                                    _stream()))
     return out
 
 

@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -467,29 +468,123 @@ int cbx_layer_norm_mask(const cbx_tensor* x, const cbx_tensor* w, const cbx_tens
                                  reinterpret_cast<hipStream_t>(stream), what);
 }
 
-int cbx_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
-                   int act, cbx_tensor* y, cbx_stream stream) {
-    const char* what = "cbx_group_norm";
-    clear_error();
+static int check_group_norm(const char* what, const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w,
+                            const cbx_tensor* b, int act, const cbx_tensor* y) {
+    const std::string f(what);
     int rc;
-    DeviceState* st = current_state(&rc);
-    if (!st) return rc;
     if ((rc = validate(x, what, "x")) || (rc = validate(y, what, "y"))) return rc;
-    if (x->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, "cbx_group_norm: F32 only");
-    if (!same_shape(x, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_group_norm: x and y shapes differ");
-    if (n_groups <= 0) return set_error(CBX_ERR_INVALID_ARG, "cbx_group_norm: n_groups must be > 0");
-    if (!(eps >= 0.0f)) return set_error(CBX_ERR_INVALID_ARG, "cbx_group_norm: eps must be >= 0");
+    if (x->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, f + ": F32 only");
+    if (!same_shape(x, y)) return set_error(CBX_ERR_INVALID_ARG, f + ": x and y shapes differ");
+    if (n_groups <= 0) return set_error(CBX_ERR_INVALID_ARG, f + ": n_groups must be > 0");
+    if (!(eps >= 0.0f)) return set_error(CBX_ERR_INVALID_ARG, f + ": eps must be >= 0");
     if ((rc = check_act(act, what))) return rc;
     for (const cbx_tensor* p : {w, b}) {
         if (!p) continue;
         if ((rc = validate(p, what, p == w ? "w" : "b"))) return rc;
         if (p->type != CBX_TYPE_F32 || p->ne[0] != 1 || p->ne[1] != 1 || p->ne[2] != x->ne[2] || p->ne[3] != 1 ||
             (p->ne[2] > 1 && p->nb[2] != sizeof(float))) {
-            return set_error(CBX_ERR_UNSUPPORTED, "cbx_group_norm: w/b must be contiguous F32 with ne = (1, 1, x.ne2, 1)");
+            return set_error(CBX_ERR_UNSUPPORTED, f + ": w/b must be contiguous F32 with ne = (1, 1, x.ne2, 1)");
         }
     }
+    // in place means y is x (same memory and strides); any other overlap of
+    // y with x, w or b would have other workgroups' stores race with reads
+    if (nelements(x) > 0 && overlaps(x, y)) {
+        bool same = x->data == y->data;
+        for (int i = 0; i < 4; i++) same = same && x->nb[i] == y->nb[i];
+        if (!same) return set_error(CBX_ERR_INVALID_ARG, f + ": y must be x itself or not overlap it");
+    }
+    if ((w && overlaps(w, y)) || (b && overlaps(b, y))) {
+        return set_error(CBX_ERR_INVALID_ARG, f + ": w and b must not overlap y");
+    }
+    return CBX_OK;
+}
+
+int cbx_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
+                   int act, cbx_tensor* y, cbx_stream stream) {
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = check_group_norm("cbx_group_norm", x, n_groups, eps, w, b, act, y))) return rc;
     if (nelements(x) == 0) return CBX_OK;
     return launch_group_norm(x, n_groups, eps, w, b, act, y, st, reinterpret_cast<hipStream_t>(stream));
+}
+
+struct cbx_group_norm_workspace {
+    int      device;
+    void*    mem;          // partial sums and arrival counters, zeroed
+    uint64_t wait_ticks;   // 100 MHz real-time counter ticks
+    int32_t  n_chunks;     // 0: automatic
+};
+
+// The longest a chunk workgroup waits for the others before computing the
+// group's statistics itself: 2 ms, far past the few microseconds a resident
+// grid takes.
+static constexpr uint64_t kGnDefaultWaitTicks = 200000;
+
+int cbx_group_norm_workspace_create(cbx_group_norm_workspace** out) {
+    clear_error();
+    if (!out) return set_error(CBX_ERR_INVALID_ARG, "cbx_group_norm_workspace_create: out is NULL");
+    *out = nullptr;
+    int rc;
+    if (!current_state(&rc)) return rc;
+    auto* ws = new (std::nothrow) cbx_group_norm_workspace();
+    if (!ws) return set_error(CBX_ERR_HIP, "cbx_group_norm_workspace_create: out of host memory");
+    hipGetDevice(&ws->device);
+    ws->wait_ticks = kGnDefaultWaitTicks;
+    ws->n_chunks = 0;
+    const size_t bytes = group_norm_workspace_bytes();
+    if (hipMalloc(&ws->mem, bytes) != hipSuccess) {
+        delete ws;
+        return set_error(CBX_ERR_HIP, "cbx_group_norm_workspace_create: hipMalloc failed");
+    }
+    if (hipMemset(ws->mem, 0, bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        hipFree(ws->mem);
+        delete ws;
+        return set_error(CBX_ERR_HIP, "cbx_group_norm_workspace_create: clearing failed");
+    }
+    *out = ws;
+    return CBX_OK;
+}
+
+void cbx_group_norm_workspace_destroy(cbx_group_norm_workspace* ws) {
+    if (!ws) return;
+    int prev = 0;
+    hipGetDevice(&prev);
+    hipSetDevice(ws->device);
+    hipDeviceSynchronize();
+    hipFree(ws->mem);
+    hipSetDevice(prev);
+    delete ws;
+}
+
+int cbx_group_norm_workspace_tune(cbx_group_norm_workspace* ws, uint32_t max_wait_us, int32_t n_chunks) {
+    clear_error();
+    if (!ws) return set_error(CBX_ERR_INVALID_ARG, "cbx_group_norm_workspace_tune: ws is NULL");
+    if (n_chunks < 0 || n_chunks > 32) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_group_norm_workspace_tune: n_chunks must be 0 (automatic) .. 32");
+    }
+    ws->wait_ticks = static_cast<uint64_t>(max_wait_us) * 100;
+    ws->n_chunks = n_chunks;
+    return CBX_OK;
+}
+
+int cbx_group_norm_ws(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
+                      int act, cbx_tensor* y, cbx_group_norm_workspace* ws, cbx_stream stream) {
+    const char* what = "cbx_group_norm_ws";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if (!ws) return set_error(CBX_ERR_INVALID_ARG, "cbx_group_norm_ws: ws is NULL");
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev != ws->device) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_group_norm_ws: the workspace belongs to another device");
+    }
+    if ((rc = check_group_norm(what, x, n_groups, eps, w, b, act, y))) return rc;
+    if (nelements(x) == 0) return CBX_OK;
+    return launch_group_norm_split(x, n_groups, eps, w, b, act, y, ws->mem, ws->wait_ticks, ws->n_chunks, st,
+                                   reinterpret_cast<hipStream_t>(stream));
 }
 
 // ---- rope --------------------------------------------------------------------

@@ -164,10 +164,20 @@ __device__ __forceinline__ float act_silu(float x) { return x / (1.0f + expf(-x)
 __device__ __forceinline__ float act_softplus(float x) {
     return (x > 20.0f) ? x : logf(1.0f + expf(x));
 }
+// mish() = x * tanh(softplus(x)) (cfm_decoder.cpp:36-38).  ggml's softplus
+// is log(t) with t = 1 + e^x rounded to f32 (x <= 20), and
+// tanh(log t) = (t^2 - 1) / (t^2 + 1) = n / (n + 2) with n = u (u + 2),
+// u = t - 1 (exact: t is in [1, 2^29]).  Evaluating that instead of logf and
+// tanhf keeps the one rounding that dominates the composition (of t, which
+// decides the result for x < -9) and costs one expf and a reciprocal; the
+// other roundings of logf and tanhf are an ulp or two each.  Past 20
+// softplus is x and tanhf(x) is 1: the result is x.
 __device__ __forceinline__ float act_mish(float x) {
-    const float sp = act_softplus(x);
-    const float t = tanhf(sp);
-    return x * t;
+    if (x > 20.0f) return x;
+    const float t = 1.0f + expf(x);
+    const float u = t - 1.0f;
+    const float n = u * (u + 2.0f);
+    return x * (n * __builtin_amdgcn_rcpf(n + 2.0f));
 }
 __device__ __forceinline__ float act_gelu_erf(float x) {
     return 0.5f * x * (1.0f + erff(x * CBX_SQRT_2_INV));
@@ -309,6 +319,37 @@ __device__ __forceinline__ float apply_act(int op, float x, const uint16_t* tab,
         case UNARY_LEAKY:        return act_leaky(x, param);
         default:                 return x;
     }
+}
+
+// The activation over every element a thread holds, the switch taken once:
+// per element (apply_act in a loop) the branches around each case keep the
+// compiler from interleaving independent elements, and a transcendental's
+// latency is then paid element after element.
+template <int NV>
+__device__ __forceinline__ void apply_act_vec(int op, float4 (&v)[NV], const uint16_t* tab, float param) {
+#define CBX_ACT_ALL(expr)                                         \
+    _Pragma("unroll") for (int k = 0; k < NV; k++) {              \
+        _Pragma("unroll") for (int e = 0; e < 4; e++) {           \
+            const float x = get(v[k], e);                         \
+            set(v[k], e, (expr));                                 \
+        }                                                         \
+    }
+    switch (op) {
+        case CBX_UNARY_GELU:
+#pragma unroll
+            for (int k = 0; k < NV; k++) v[k] = act_gelu_fast4(tab, v[k]);
+            break;
+        case CBX_UNARY_GELU_ERF: CBX_ACT_ALL(act_gelu_erf(x)); break;
+        case CBX_UNARY_SILU:     CBX_ACT_ALL(act_silu(x)); break;
+        case CBX_UNARY_TANH:     CBX_ACT_ALL(tanhf(x)); break;
+        case CBX_UNARY_SOFTPLUS: CBX_ACT_ALL(act_softplus(x)); break;
+        case CBX_UNARY_SIN:      CBX_ACT_ALL(sinf(x)); break;
+        case CBX_UNARY_SQR:      CBX_ACT_ALL(x * x); break;
+        case CBX_UNARY_MISH:     CBX_ACT_ALL(act_mish(x)); break;
+        case UNARY_LEAKY:        CBX_ACT_ALL(act_leaky(x, param)); break;
+        default: break;
+    }
+#undef CBX_ACT_ALL
 }
 
 }  // namespace cbx

@@ -54,7 +54,10 @@ struct DeviceState {
 };
 
 // Device error bits.
-enum : uint32_t { DEV_ERR_ROW_INDEX = 1u };
+enum : uint32_t {
+    DEV_ERR_ROW_INDEX = 1u,   // a get_rows index was out of range (row zeroed)
+    DEV_ERR_GN_WAIT   = 2u,   // an in-place split GroupNorm workgroup stopped waiting for the others
+};
 
 // ---- host helpers implemented in cbx_api.cpp ----------------------------
 int  set_error(int code, const std::string& msg);
@@ -88,6 +91,15 @@ int launch_embed_norm(const cbx_tensor* src, const cbx_tensor* ids, const cbx_te
 int launch_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w,
                       const cbx_tensor* b, int act, cbx_tensor* y, DeviceState* st,
                       hipStream_t s);
+// The split-reduction GroupNorm over a workspace of
+// group_norm_workspace_bytes() (zeroed once, left zeroed by every launch);
+// layouts it does not cover go to launch_group_norm.  wait_ticks: the
+// longest wait of a workgroup for the others, in 100 MHz ticks (0: never
+// wait); n_chunks_req: chunks per group, 0 = automatic.
+size_t group_norm_workspace_bytes();
+int launch_group_norm_split(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
+                            int act, cbx_tensor* y, void* workspace, uint64_t wait_ticks, int n_chunks_req,
+                            DeviceState* st, hipStream_t s);
 int launch_unary(int op, float param, const cbx_tensor* x, cbx_tensor* y, DeviceState* st,
                  hipStream_t s);
 int launch_swiglu(const cbx_tensor* g, const cbx_tensor* u, cbx_tensor* y, DeviceState* st,

@@ -142,8 +142,9 @@ __device__ __forceinline__ double thread_tree_sum(double (&p)[NV]) {
 // result in scratch[slot] for everyone.  Fixed order: every workgroup that
 // reduces the same values gets the same bits.  Two barriers; a second call
 // with another slot needs none before it.
+template <int THREADS = kThreads>
 __device__ __forceinline__ double block_sum_tree(double v, double* scratch, int slot) {
-    constexpr int NW = kThreads / WAVE;
+    constexpr int NW = THREADS / WAVE;
     static_assert(NW <= 16, "one DPP row of wave totals");
     v = wave_sum(v);
     const int lane = threadIdx.x % WAVE, wid = threadIdx.x / WAVE;
@@ -161,6 +162,25 @@ __device__ __forceinline__ double block_sum_tree(double v, double* scratch, int 
     return scratch[slot];
 }
 
+// The same sum with one barrier: each wave's total (DPP butterfly) to LDS,
+// then every thread adds the wave totals in index order (the same bits in
+// every thread and every workgroup that reduces the same values).  Calls
+// alternate between two LDS areas by the parity of `slot`; a call may reuse
+// an area once a barrier has passed since its last reads (every caller
+// here has one in between).
+template <int THREADS>
+__device__ __forceinline__ double block_sum_1b(double v, double* scratch, int slot) {
+    constexpr int NW = THREADS / WAVE;
+    v = wave_sum(v);
+    double* sc = scratch + NW * (slot & 1);
+    if (threadIdx.x % WAVE == 0) sc[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    double t = sc[0];
+#pragma unroll
+    for (int i = 1; i < NW; i++) t += sc[i];
+    return t;
+}
+
 // Contiguous groups (ne0 % 4 == 0, ne0 x ne1 dense per channel, channels
 // adjacent, 16-byte aligned), split over n_chunks workgroups per group so a
 // few large groups still fill the chip.  Every workgroup of a group reads
@@ -172,7 +192,7 @@ __device__ __forceinline__ double block_sum_tree(double v, double* scratch, int 
 // HBM sees it once.
 template <int NV, bool ACT>
 __global__ __launch_bounds__(kThreads) void k_group_norm_vec(GnArgs a, uint32_t n_chunks, uint32_t n_gi) {
-    __shared__ double red[kThreads / WAVE + 2];
+    __shared__ double red[2 * (kThreads / WAVE)];
     const uint32_t b = blockIdx.x;
     const uint32_t j = b / kXcds;
     const uint32_t m = j / n_chunks;
@@ -226,7 +246,7 @@ __global__ __launch_bounds__(kThreads) void k_group_norm_vec(GnArgs a, uint32_t 
         p[k] = (static_cast<double>(v[k].x) + static_cast<double>(v[k].y)) +
                (static_cast<double>(v[k].z) + static_cast<double>(v[k].w));
     }
-    const double s = block_sum_tree(thread_tree_sum<NV>(p), red, kThreads / WAVE);
+    const double s = block_sum_1b<kThreads>(thread_tree_sum<NV>(p), red, 0);
     const float mean = static_cast<float>(s / static_cast<double>(count));
 #pragma unroll
     for (int k = 0; k < NV; k++) {
@@ -237,7 +257,7 @@ __global__ __launch_bounds__(kThreads) void k_group_norm_vec(GnArgs a, uint32_t 
         p[k] = (static_cast<double>(v[k].x * v[k].x) + static_cast<double>(v[k].y * v[k].y)) +
                (static_cast<double>(v[k].z * v[k].z) + static_cast<double>(v[k].w * v[k].w));
     }
-    const double s2 = block_sum_tree(thread_tree_sum<NV>(p), red, kThreads / WAVE + 1);
+    const double s2 = block_sum_1b<kThreads>(thread_tree_sum<NV>(p), red, 1);
     const float var = static_cast<float>(s2 / static_cast<double>(count));
     const float scale = 1.0f / sqrtf(var + a.eps);
     if (!live) return;   // uniform across the workgroup
@@ -248,17 +268,244 @@ __global__ __launch_bounds__(kThreads) void k_group_norm_vec(GnArgs a, uint32_t 
         const int64_t c = c0 + static_cast<uint32_t>(4 * qi) / per_ch;
         const float wk = kEarly ? wv[kEarly ? k : 0] : (a.w ? a.w[c] : 1.0f);
         const float bk = kEarly ? bv[kEarly ? k : 0] : (a.b ? a.b[c] : 0.0f);
-        float4 o;
+        float4 o[1];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             float t = get(v[k], e) * scale;
             if (a.w) t = t * wk;
             if (a.b) t = t + bk;
-            if constexpr (ACT) t = apply_act(a.act, t, a.tab, 0.0f);
-            set(o, e, t);
+            set(o[0], e, t);
         }
-        if (n_chunks == 1) *reinterpret_cast<float4*>(yg + 16 * qi) = o;
-        else Stream<float>::store4(yg + 16 * qi, o);
+        // a thread stores only the vectors of its workgroup's chunk (one or
+        // two of the NV it holds): the activation's switch once per vector
+        if constexpr (ACT) apply_act_vec<1>(a.act, o, a.tab, 0.0f);
+        if (n_chunks == 1) *reinterpret_cast<float4*>(yg + 16 * qi) = o[0];
+        else Stream<float>::store4(yg + 16 * qi, o[0]);
+    }
+}
+
+// ---- split reduction --------------------------------------------------------
+// A few large groups (the CFM's 2 x 8) spread over many workgroups: each
+// chunk workgroup holds only its chunk of the group in registers and
+// reduces it; the chunks' f64 partial sums meet in a workspace, once for
+// the mean and once for the variance.  Each element is read once and every
+// workgroup's VALU work is its own chunk, not the whole group.
+//
+// A partial travels as two 64-bit words (its low and high halves), each
+// tagged in its upper 32 bits with the launch's tag: the dispatch's packet
+// index on its queue mixed with the queue's address, shifted left and made
+// odd (never the 0 of fresh memory; packets of one queue within 2^31 of
+// each other get different tags).  A word is written whole and read whole, so a reader
+// that finds this launch's tag in both words of a slot has that chunk's
+// partial; words left by earlier launches carry other tags and nothing is
+// ever cleared.  Wave 0 polls the group's 2n words, a lane a word, with
+// agent-scope loads.  The words are written with plain stores, which reach
+// the L2 the workgroups of one group share (their indices put them on one
+// XCD: dispatch deals workgroups to the 8 XCDs round-robin), except in
+// place, where agent-scope stores make them visible on any XCD.
+//
+// Waits are bounded: after GnSplit::wait_ticks of the 100 MHz real-time
+// counter a workgroup stops waiting and computes every chunk's partial
+// itself from x, with the same lanes and order as that chunk's own
+// workgroup, so the statistics are the same bits either way and a
+// workgroup that never gets a CU while the others run delays nothing.  (In
+// place, a workgroup that stops waiting may read chunks already
+// overwritten: it raises DEV_ERR_GN_WAIT.)  wait_ticks == 0: never wait.
+constexpr int kSplitThreads = 512;
+constexpr int kSplitMaxChunks = 32;
+constexpr uint32_t kSplitMaxSlots = 1024;   // group instances x chunks per launch
+
+struct GnSplit {
+    uint64_t* word;        // [2 stages][kSplitMaxSlots][2 words]
+    uint32_t* err;
+    uint32_t  n_chunks;
+    uint32_t  n_gi;
+    uint64_t  wait_ticks;
+    uint32_t  in_place;
+};
+
+// The dispatch's 64-bit packet index on its queue (llvm.amdgcn.dispatch.id;
+// clang has no builtin for it).
+extern "C" __device__ uint64_t cbx_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+
+__device__ __forceinline__ uint32_t launch_tag() {
+    const uint64_t id = cbx_dispatch_id();
+    const uint64_t q = reinterpret_cast<uintptr_t>(__builtin_amdgcn_queue_ptr());
+    const uint32_t qmix = static_cast<uint32_t>(((q >> 6) * 0x9E3779B97F4A7C15ull) >> 32);
+    // consecutive packets on one queue get distinct tags for 2^31 launches
+    return ((static_cast<uint32_t>(id) ^ qmix) << 1) | 1u;
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(v & 0xffffffffu), lane);
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(v >> 32), lane);
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// One chunk's partial of stage 0 (Σx) or 1 (Σ(x - mean)^2, the f32
+// difference and square summed in f64): thread t holds float4 indices
+// q0 + t + k * kSplitThreads below q1.  The same function serves the chunk's
+// own workgroup and a workgroup that computes it on the chunk's behalf.
+// `area`: which of the two LDS areas of block_sum_1b (its parity).
+template <int NV>
+__device__ __forceinline__ double chunk_partial(const float4 (&v)[NV], const bool (&ok)[NV], int stage, float mean,
+                                                double* red, int area) {
+    double p[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        if (stage == 0) {
+            p[k] = ok[k] ? (static_cast<double>(v[k].x) + static_cast<double>(v[k].y)) +
+                               (static_cast<double>(v[k].z) + static_cast<double>(v[k].w))
+                         : 0.0;
+        } else {
+            const float d0 = v[k].x - mean, d1 = v[k].y - mean, d2 = v[k].z - mean, d3 = v[k].w - mean;
+            p[k] = ok[k] ? (static_cast<double>(d0 * d0) + static_cast<double>(d1 * d1)) +
+                               (static_cast<double>(d2 * d2) + static_cast<double>(d3 * d3))
+                         : 0.0;
+        }
+    }
+    return block_sum_1b<kSplitThreads>(thread_tree_sum<NV>(p), red, area);
+}
+
+template <int NV>
+__device__ __forceinline__ void chunk_load(const char* xg, int64_t q0, int64_t q1, float4 (&v)[NV], bool (&ok)[NV]) {
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t qi = q0 + threadIdx.x + static_cast<int64_t>(k) * kSplitThreads;
+        ok[k] = qi < q1;
+        // lanes past the chunk (a chunk may be empty) load the group's first
+        // vector: an address inside the group
+        v[k] = *reinterpret_cast<const float4*>(xg + 16 * (ok[k] ? qi : 0));
+    }
+}
+
+// Publishes this chunk's partial, waits (bounded) for the group's other
+// chunks and returns the partials' sum in chunk order, or computes every
+// chunk's partial itself when the wait runs out.
+template <int NV>
+__device__ __forceinline__ double split_combine(const GnSplit& sp, uint32_t tag, uint32_t gi, uint32_t ci,
+                                                int stage, double mine, float mean, const char* xg, int64_t n4,
+                                                int64_t per, double* red, int slot) {
+    __shared__ int waited_out;
+    const uint32_t n = sp.n_chunks;
+    uint64_t* wd = sp.word + 2 * (stage * kSplitMaxSlots + gi * n);
+    if (threadIdx.x < WAVE) {
+        const uint32_t lane = threadIdx.x;
+        const uint64_t bits = __builtin_bit_cast(uint64_t, mine);
+        const uint64_t tg = static_cast<uint64_t>(tag) << 32;
+        // lanes 0 and 1 publish the low and high halves
+        const uint64_t own = tg | (lane == 0 ? bits & 0xffffffffu : bits >> 32);
+        if (lane < 2) {
+            if (sp.in_place) __hip_atomic_store(&wd[2 * ci + lane], own, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else __hip_atomic_store(&wd[2 * ci + lane], own, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        bool ok = false;
+        uint64_t mv = tg;
+        if (sp.wait_ticks) {
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            while (true) {
+                if (lane < 2 * n && lane / 2 != ci) {
+                    mv = __hip_atomic_load(&wd[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                if (__all((mv >> 32) == tag)) {
+                    ok = true;
+                    break;
+                }
+                if (__builtin_amdgcn_s_memrealtime() - t0 > sp.wait_ticks) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        if (ok) {
+            double t = 0.0;
+            for (uint32_t c = 0; c < n; c++) {
+                const uint64_t b = c == ci ? bits
+                                           : (readlane_u64(mv, 2 * c) & 0xffffffffu) |
+                                                 (readlane_u64(mv, 2 * c + 1) << 32);
+                t += __builtin_bit_cast(double, b);
+            }
+            if (lane == 0) red[slot] = t;
+        }
+        if (lane == 0) waited_out = ok ? 0 : 1;
+    }
+    __syncthreads();
+    if (waited_out) {
+        // every chunk's partial, as its own workgroup computes it
+        if (sp.in_place && threadIdx.x == 0) atomicOr(sp.err, DEV_ERR_GN_WAIT);
+        double t = 0.0;
+        for (uint32_t c = 0; c < n; c++) {
+            float4 v[NV];
+            bool ok[NV];
+            const int64_t q0 = static_cast<int64_t>(c) * per;
+            chunk_load<NV>(xg, q0, q0 + per < n4 ? q0 + per : n4, v, ok);
+            // areas alternate by iteration (c = 0 takes the one the
+            // caller's last sum did not)
+            t += chunk_partial<NV>(v, ok, stage, mean, red, 1 + static_cast<int>(c));
+        }
+        return t;   // the same in every thread
+    }
+    return red[slot];
+}
+
+template <int NV, bool ACT>
+__global__ __launch_bounds__(kSplitThreads) void k_group_norm_split(GnArgs a, GnSplit sp) {
+    // two areas of wave totals for block_sum_1b, then the broadcast slot
+    __shared__ double red[2 * (kSplitThreads / WAVE) + 1];
+    constexpr int kSlot = 2 * (kSplitThreads / WAVE);
+    const uint32_t b = blockIdx.x;
+    const uint32_t j = b / kXcds;
+    const uint32_t m = j / sp.n_chunks;
+    const uint32_t ci = j - m * sp.n_chunks;
+    const uint32_t gi = b % kXcds + kXcds * m;
+    const int64_t C = a.x.ne[2];
+    const int64_t g = gi % a.n_groups, i3 = gi / a.n_groups;
+    const int64_t c0 = g * a.cpg;
+    // past the last group, or an empty group (past C): every workgroup of it
+    // leaves here, so nobody counts on its counter
+    if (gi >= sp.n_gi || c0 >= C) return;
+    const int64_t c1 = c0 + a.cpg < C ? c0 + a.cpg : C;
+    const int64_t count = a.x.ne[0] * a.x.ne[1] * (c1 - c0);
+    const char* xg = a.x.data + c0 * a.x.nb[2] + i3 * a.x.nb[3];
+    char* yg = a.y.data + c0 * a.y.nb[2] + i3 * a.y.nb[3];
+    const uint32_t per_ch = static_cast<uint32_t>(a.x.ne[0] * a.x.ne[1]);
+    const int64_t n4 = count / 4;
+    const int64_t per = (n4 + sp.n_chunks - 1) / sp.n_chunks;
+    const int64_t q0 = static_cast<int64_t>(ci) * per;
+    const int64_t q1 = q0 + per < n4 ? q0 + per : n4;
+
+    float4 v[NV];
+    bool ok[NV];
+    chunk_load<NV>(xg, q0, q1, v, ok);
+    float wv[NV], bv[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t qi = q0 + threadIdx.x + static_cast<int64_t>(k) * kSplitThreads;
+        const int64_t c = c0 + static_cast<uint32_t>(4 * (ok[k] ? qi : 0)) / per_ch;
+        wv[k] = a.w ? a.w[c] : 1.0f;
+        bv[k] = a.b ? a.b[c] : 0.0f;
+    }
+    const uint32_t tag = launch_tag();
+    const double s0 = chunk_partial<NV>(v, ok, 0, 0.0f, red, 0);
+    const double s = split_combine<NV>(sp, tag, gi, ci, 0, s0, 0.0f, xg, n4, per, red, kSlot);
+    const float mean = static_cast<float>(s / static_cast<double>(count));
+    const double s1 = chunk_partial<NV>(v, ok, 1, mean, red, 0);
+    const double s2 = split_combine<NV>(sp, tag, gi, ci, 1, s1, mean, xg, n4, per, red, kSlot);
+    const float var = static_cast<float>(s2 / static_cast<double>(count));
+    const float scale = 1.0f / sqrtf(var + a.eps);
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float t = (get(v[k], e) - mean) * scale;
+            if (a.w) t = t * wv[k];
+            if (a.b) t = t + bv[k];
+            set(v[k], e, t);
+        }
+    }
+    if constexpr (ACT) apply_act_vec<NV>(a.act, v, a.tab, 0.0f);
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int64_t qi = q0 + threadIdx.x + static_cast<int64_t>(k) * kSplitThreads;
+        if (ok[k]) Stream<float>::store4(yg + 16 * qi, v[k]);
     }
 }
 
@@ -323,10 +570,32 @@ void gn_vec(const GnArgs& a, int nv, uint32_t n_chunks, uint32_t n_gi, hipStream
     }
 }
 
-}  // namespace
+template <bool ACT>
+void gn_split(const GnArgs& a, const GnSplit& sp, int nv, hipStream_t s) {
+    const dim3 grid(kXcds * ((sp.n_gi + kXcds - 1) / kXcds) * sp.n_chunks);
+    switch (nv) {
+        case 1: hipLaunchKernelGGL((k_group_norm_split<1, ACT>), grid, dim3(kSplitThreads), 0, s, a, sp); break;
+        case 2: hipLaunchKernelGGL((k_group_norm_split<2, ACT>), grid, dim3(kSplitThreads), 0, s, a, sp); break;
+        case 4: hipLaunchKernelGGL((k_group_norm_split<4, ACT>), grid, dim3(kSplitThreads), 0, s, a, sp); break;
+        default: hipLaunchKernelGGL((k_group_norm_split<8, ACT>), grid, dim3(kSplitThreads), 0, s, a, sp); break;
+    }
+}
 
-int launch_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
-                      int act, cbx_tensor* y, DeviceState* st, hipStream_t s) {
+// The vectorised layout: every group a contiguous run of floats (ne0, ne1
+// dense within a channel, channels adjacent), 16-byte aligned, ne0 % 4 == 0.
+bool gn_vec_layout(const cbx_tensor* x, const cbx_tensor* y) {
+    bool vec = x->ne[0] % 4 == 0;
+    for (const cbx_tensor* t : {x, y}) {
+        const size_t row = 4 * static_cast<size_t>(t->ne[0]);
+        if (t->ne[1] > 1 && t->nb[1] != row) vec = false;
+        if (t->ne[2] > 1 && t->nb[2] != row * static_cast<size_t>(t->ne[1])) vec = false;
+        if (reinterpret_cast<uintptr_t>(t->data) % 16 || t->nb[2] % 16 || t->nb[3] % 16) vec = false;
+    }
+    return vec;
+}
+
+GnArgs gn_args(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b, int act,
+               cbx_tensor* y, DeviceState* st) {
     GnArgs a;
     a.x = view_of(x);
     a.y = view_of(y);
@@ -337,15 +606,54 @@ int launch_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_te
     a.eps = eps;
     a.act = act;
     a.tab = st->gelu_table;
-    // VEC: every group is a contiguous run of floats (ne0, ne1 dense within a
-    // channel, channels adjacent), 16-byte aligned, ne0 % 4 == 0.
-    bool vec = x->ne[0] % 4 == 0;
-    for (const cbx_tensor* t : {x, static_cast<const cbx_tensor*>(y)}) {
-        const size_t row = 4 * static_cast<size_t>(t->ne[0]);
-        if (t->ne[1] > 1 && t->nb[1] != row) vec = false;
-        if (t->ne[2] > 1 && t->nb[2] != row * static_cast<size_t>(t->ne[1])) vec = false;
-        if (reinterpret_cast<uintptr_t>(t->data) % 16 || t->nb[2] % 16 || t->nb[3] % 16) vec = false;
+    return a;
+}
+
+}  // namespace
+
+size_t group_norm_workspace_bytes() {
+    return 2 * kSplitMaxSlots * 2 * sizeof(uint64_t);
+}
+
+int launch_group_norm_split(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
+                            int act, cbx_tensor* y, void* workspace, uint64_t wait_ticks, int n_chunks_req,
+                            DeviceState* st, hipStream_t s) {
+    const int64_t cpg = cdiv(x->ne[2], n_groups);
+    const int64_t count = x->ne[0] * x->ne[1] * std::min<int64_t>(cpg, x->ne[2]);
+    const int64_t n_gi = int64_t{n_groups} * x->ne[3];
+    const int64_t n4 = count / 4;
+    // about one 512-lane workgroup per two CUs (measured best on the CFM
+    // shapes: more chunks add dispatch skew to every exchange, fewer leave
+    // the activation and stores to too few SIMDs); at most 8 vectors a lane
+    int64_t n_chunks = n_chunks_req > 0 ? n_chunks_req : cdiv(st->n_cu, int64_t{2} * n_gi);
+    n_chunks = std::min<int64_t>({n_chunks, kSplitMaxChunks, n4});
+    n_chunks = std::max<int64_t>(n_chunks, cdiv(n4, 8 * kSplitThreads));
+    const int64_t padded_gi = int64_t{kXcds} * cdiv(n_gi, kXcds);
+    // the split applies when the groups are few (n_chunks >= 2) and the
+    // whole grid is resident at once (at most 2 workgroups of 512 lanes a CU)
+    if (!gn_vec_layout(x, y) || n_chunks < 2 || n_chunks > kSplitMaxChunks || n_gi * n_chunks > kSplitMaxSlots ||
+        padded_gi * n_chunks > int64_t{2} * st->n_cu) {
+        return launch_group_norm(x, n_groups, eps, w, b, act, y, st, s);
     }
+    const int64_t per = cdiv(n4, n_chunks);
+    const int nv = per <= kSplitThreads ? 1 : per <= 2 * kSplitThreads ? 2 : per <= 4 * kSplitThreads ? 4 : 8;
+    GnArgs a = gn_args(x, n_groups, eps, w, b, act, y, st);
+    GnSplit sp;
+    sp.word = static_cast<uint64_t*>(workspace);
+    sp.err = st->err_word;
+    sp.n_chunks = static_cast<uint32_t>(n_chunks);
+    sp.n_gi = static_cast<uint32_t>(n_gi);
+    sp.wait_ticks = wait_ticks;
+    sp.in_place = x->data == y->data;
+    if (act != CBX_UNARY_NONE) gn_split<true>(a, sp, nv, s);
+    else gn_split<false>(a, sp, nv, s);
+    return check_launch("group_norm");
+}
+
+int launch_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
+                      int act, cbx_tensor* y, DeviceState* st, hipStream_t s) {
+    GnArgs a = gn_args(x, n_groups, eps, w, b, act, y, st);
+    const bool vec = gn_vec_layout(x, y);
     const int64_t count = x->ne[0] * x->ne[1] * std::min<int64_t>(a.cpg, x->ne[2]);
     const int64_t need = cdiv(count, int64_t{kThreads} * 4);
     const int nv = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : need <= 16 ? 16 : 0;

@@ -82,7 +82,11 @@ const char* cbx_last_error(void);
 const char* cbx_version(void);
 /* Reads (and with clear != 0 resets) the device error word of `device`,
  * synchronising the device first.  Bit 0: a get_rows index was out of
- * range (ggml aborts there; this library writes zeros to that row).       */
+ * range (ggml aborts there; this library writes zeros to that row).
+ * Bit 1: an in-place cbx_group_norm_ws workgroup stopped waiting for the
+ * group's other chunks and read chunks that may already have been
+ * overwritten (a grid not resident at once; not seen with the default
+ * wait).                                                                    */
 int  cbx_device_errors(int device, uint32_t* flags_out, int clear);
 
 /* ---- gather and conversion ---------------------------------------------- */
@@ -145,6 +149,35 @@ int cbx_rms_norm_mul(const cbx_tensor* x, const cbx_tensor* g, float eps,
 int cbx_group_norm(const cbx_tensor* x, int n_groups, float eps,
                    const cbx_tensor* w, const cbx_tensor* b, int act,
                    cbx_tensor* y, cbx_stream stream);
+
+/* cbx_group_norm with the statistics split over many workgroups.  A few
+ * large groups (the CFM decoder's two CFG items x 8 groups) run as chunks:
+ * each workgroup reads and reduces only its chunk, and the chunks' f64
+ * partial sums meet in the workspace -- one HBM read of x, no workgroup
+ * reducing a whole group.  Same results as cbx_group_norm, bit for bit.
+ * Layouts the split does not cover (strided groups, many small groups)
+ * run as cbx_group_norm.  A workspace serves one call at a time: calls
+ * that share one must not overlap in time (one stream, or streams ordered
+ * by events); give concurrent streams a workspace each.
+ *
+ * The workspace (32 KiB of device memory on the current device, zeroed once;
+ * nothing in it needs clearing between calls) has no counterpart in ggml, whose CPU group
+ * norm reduces each group on one thread; cbx_group_norm_workspace_create /
+ * _destroy are the explicit init/destroy pair of the op.                  */
+typedef struct cbx_group_norm_workspace cbx_group_norm_workspace;
+int  cbx_group_norm_workspace_create(cbx_group_norm_workspace** out);
+void cbx_group_norm_workspace_destroy(cbx_group_norm_workspace* ws);
+/* A chunk workgroup waits at most max_wait_us for the group's other
+ * chunks (default 2000), then computes every chunk's partial itself; 0:
+ * never wait (each workgroup reduces the whole group, as cbx_group_norm
+ * does).  n_chunks: chunks per group, 0 (default) = automatic, else 2..32.
+ * The results do not depend on either.  For tests and tuning.             */
+int  cbx_group_norm_workspace_tune(cbx_group_norm_workspace* ws,
+                                   uint32_t max_wait_us, int32_t n_chunks);
+int  cbx_group_norm_ws(const cbx_tensor* x, int n_groups, float eps,
+                       const cbx_tensor* w, const cbx_tensor* b, int act,
+                       cbx_tensor* y, cbx_group_norm_workspace* ws,
+                       cbx_stream stream);
 
 /* The residual join and the LayerNorm that reads it, in one pass:
  *   s = ggml_add(ggml_add(a, a_bias), r)     (a_bias NULL: ggml_add(a, r))
