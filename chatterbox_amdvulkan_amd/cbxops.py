@@ -162,6 +162,7 @@ def load() -> ctypes.CDLL:
         "cbx_group_norm_workspace_destroy": (None, [vp]),
         "cbx_group_norm_workspace_tune": (i, [vp, ctypes.c_uint32, ctypes.c_int32]),
         "cbx_group_norm_ws": (i, [P, i, f, P, P, i, P, vp, vp]),
+        "cbx_group_norm_noalloc": (i, [P, i, f, P, P, i, P, vp]),
         "cbx_rope_cache_create": (i, [i, i, i, f, f, f, f, f, f, vp, ctypes.c_int32, ctypes.POINTER(vp)]),
         "cbx_rope_cache_destroy": (None, [vp]),
         "cbx_rope_ext": (i, [P, P, vp, P, vp]),
@@ -424,6 +425,15 @@ def group_norm_ws(x, n_groups, eps, ws: GroupNormWorkspace, w=None, b=None, act=
     _check(load().cbx_group_norm_ws(_ref(desc(x)), n_groups, eps, _ref(desc(w)) if w is not None else None,
                                     _ref(desc(b)) if b is not None else None, act, _ref(desc(out)), ws.handle,
                                     _stream()))
+    return out
+
+
+def group_norm_noalloc(x, n_groups, eps, w=None, b=None, act=UNARY_NONE, out=None):
+    """group_norm_ws over the library's static scratch (allocates nothing)."""
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_group_norm_noalloc(_ref(desc(x)), n_groups, eps, _ref(desc(w)) if w is not None else None,
+                                         _ref(desc(b)) if b is not None else None, act, _ref(desc(out)), _stream()))
     return out
 
 

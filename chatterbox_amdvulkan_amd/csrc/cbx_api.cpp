@@ -213,6 +213,7 @@ int cbx_init(int device) {
                hipDeviceSynchronize() != hipSuccess) {
         rc = set_error(CBX_ERR_HIP, "cbx_init: upload failed");
     }
+    if (rc == CBX_OK) rc = group_norm_scratch_setup(&st.gn_scratch);
     if (rc != CBX_OK) {
         if (st.gelu_table) hipFree(st.gelu_table);
         if (st.err_word) hipFree(st.err_word);
@@ -584,6 +585,25 @@ int cbx_group_norm_ws(const cbx_tensor* x, int n_groups, float eps, const cbx_te
     if ((rc = check_group_norm(what, x, n_groups, eps, w, b, act, y))) return rc;
     if (nelements(x) == 0) return CBX_OK;
     return launch_group_norm_split(x, n_groups, eps, w, b, act, y, ws->mem, ws->wait_ticks, ws->n_chunks, st,
+                                   reinterpret_cast<hipStream_t>(stream));
+}
+
+int cbx_group_norm_noalloc(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
+                           int act, cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_group_norm_noalloc";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = check_group_norm(what, x, n_groups, eps, w, b, act, y))) return rc;
+    const int64_t n_gi = int64_t{n_groups} * x->ne[3];
+    if (n_gi > static_cast<int64_t>(group_norm_scratch_slots())) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_group_norm_noalloc: n_groups x ne[3] = " + std::to_string(n_gi) +
+                                                  " exceeds the " + std::to_string(group_norm_scratch_slots()) +
+                                                  " group instances of the library's static scratch");
+    }
+    if (nelements(x) == 0) return CBX_OK;
+    return launch_group_norm_split(x, n_groups, eps, w, b, act, y, st->gn_scratch, kGnDefaultWaitTicks, 0, st,
                                    reinterpret_cast<hipStream_t>(stream));
 }
 

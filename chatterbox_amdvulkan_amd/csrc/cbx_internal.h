@@ -51,6 +51,7 @@ struct DeviceState {
     int       n_cu = 0;
     uint16_t* gelu_table = nullptr;   // 65536 fp16 codes
     uint32_t* err_word = nullptr;     // sticky device error bits
+    void*     gn_scratch = nullptr;   // this device's address of the static group norm scratch
 };
 
 // Device error bits.
@@ -97,6 +98,12 @@ int launch_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_te
 // longest wait of a workgroup for the others, in 100 MHz ticks (0: never
 // wait); n_chunks_req: chunks per group, 0 = automatic.
 size_t group_norm_workspace_bytes();
+// The current device's address of the library's static split-GroupNorm
+// scratch (group_norm_workspace_bytes() of it), for cbx_group_norm_noalloc;
+// called once per device by cbx_init.  The split handles up to
+// group_norm_scratch_slots() group instances x chunks.
+int group_norm_scratch_setup(void** out);
+size_t group_norm_scratch_slots();
 int launch_group_norm_split(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
                             int act, cbx_tensor* y, void* workspace, uint64_t wait_ticks, int n_chunks_req,
                             DeviceState* st, hipStream_t s);

@@ -11,6 +11,7 @@
 // Groups of up to 64K elements stay in registers between the two
 // reductions; larger ones take three passes over memory.
 #include <algorithm>
+#include <string>
 
 #include "cbx_device.h"
 
@@ -139,27 +140,27 @@ __device__ __forceinline__ double thread_tree_sum(double (&p)[NV]) {
 
 // Sum over the kThreads threads: each wave's total (DPP butterfly), then
 // wave 0 adds the kThreads/64 totals with the same butterfly and leaves the
-// result in scratch[slot] for everyone.  Fixed order: every workgroup that
+// result in lds[slot] for everyone.  Fixed order: every workgroup that
 // reduces the same values gets the same bits.  Two barriers; a second call
 // with another slot needs none before it.
 template <int THREADS = kThreads>
-__device__ __forceinline__ double block_sum_tree(double v, double* scratch, int slot) {
+__device__ __forceinline__ double block_sum_tree(double v, double* lds, int slot) {
     constexpr int NW = THREADS / WAVE;
     static_assert(NW <= 16, "one DPP row of wave totals");
     v = wave_sum(v);
     const int lane = threadIdx.x % WAVE, wid = threadIdx.x / WAVE;
-    if (lane == 0) scratch[wid] = v;
+    if (lane == 0) lds[wid] = v;
     __syncthreads();
     if (wid == 0) {
-        double t = lane < NW ? scratch[lane] : 0.0;
+        double t = lane < NW ? lds[lane] : 0.0;
         t += dpp_f64<0xB1>(t);
         t += dpp_f64<0x4E>(t);
         t += dpp_f64<0x141>(t);
         t += dpp_f64<0x140>(t);
-        if (lane == 0) scratch[slot] = t;
+        if (lane == 0) lds[slot] = t;
     }
     __syncthreads();
-    return scratch[slot];
+    return lds[slot];
 }
 
 // The same sum with one barrier: each wave's total (DPP butterfly) to LDS,
@@ -169,10 +170,10 @@ __device__ __forceinline__ double block_sum_tree(double v, double* scratch, int 
 // an area once a barrier has passed since its last reads (every caller
 // here has one in between).
 template <int THREADS>
-__device__ __forceinline__ double block_sum_1b(double v, double* scratch, int slot) {
+__device__ __forceinline__ double block_sum_1b(double v, double* lds, int slot) {
     constexpr int NW = THREADS / WAVE;
     v = wave_sum(v);
-    double* sc = scratch + NW * (slot & 1);
+    double* sc = lds + NW * (slot & 1);
     if (threadIdx.x % WAVE == 0) sc[threadIdx.x / WAVE] = v;
     __syncthreads();
     double t = sc[0];
@@ -609,7 +610,30 @@ GnArgs gn_args(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w
     return a;
 }
 
+// Scratch of cbx_group_norm_noalloc, for callers that cannot allocate: the
+// split reduction's exchange words for kSplitMaxSlots chunk slots (32 KiB)
+// in the library's own device memory, one copy per GPU, held until the
+// process ends.  Zero at load; the launch tags mean nothing in it ever needs
+// clearing.  Host code must not pass `scratch` itself to a kernel (on the
+// host it names a stand-in, not device memory): group_norm_scratch_setup
+// looks up each device's address once, at cbx_init, and launches use that.
+static __device__ __align__(256) uint64_t scratch[2 * kSplitMaxSlots * 2];
+
 }  // namespace
+
+int group_norm_scratch_setup(void** out) {
+    *out = nullptr;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        return set_error(CBX_ERR_HIP, std::string("cbx_init: hipGetSymbolAddress of the group norm scratch failed: ") +
+                                          hipGetErrorString(e));
+    }
+    *out = p;
+    return CBX_OK;
+}
+
+size_t group_norm_scratch_slots() { return kSplitMaxSlots; }
 
 size_t group_norm_workspace_bytes() {
     return 2 * kSplitMaxSlots * 2 * sizeof(uint64_t);

@@ -179,6 +179,19 @@ int  cbx_group_norm_ws(const cbx_tensor* x, int n_groups, float eps,
                        cbx_tensor* y, cbx_group_norm_workspace* ws,
                        cbx_stream stream);
 
+/* cbx_group_norm_ws without a workspace: the same kernels and results, the
+ * exchange words in the library's own static device memory (32 KiB per GPU,
+ * set up by cbx_init, held until the process ends).  No counterpart in the
+ * reference: for callers that cannot allocate device memory at all -- code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  The call allocates nothing.  n_groups x x.ne[3] is limited to
+ * 1024 group instances (larger: CBX_ERR_UNSUPPORTED).  Every call on a GPU
+ * shares that GPU's scratch: calls that overlap in time on one GPU race
+ * (keep them on one stream, or ordered by events).                        */
+int  cbx_group_norm_noalloc(const cbx_tensor* x, int n_groups, float eps,
+                            const cbx_tensor* w, const cbx_tensor* b, int act,
+                            cbx_tensor* y, cbx_stream stream);
+
 /* The residual join and the LayerNorm that reads it, in one pass:
  *   s = ggml_add(ggml_add(a, a_bias), r)     (a_bias NULL: ggml_add(a, r))
  *   y = act(layer_norm(s, w, b, eps))
