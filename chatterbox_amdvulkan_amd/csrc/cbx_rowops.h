@@ -79,6 +79,63 @@ __device__ __forceinline__ float wave_row_scale(float4 (&v)[NV], int lane, int64
     }
 }
 
+// W waves of one workgroup cooperating on one row: wave w holds float4s
+// [w*64*NV, (w+1)*64*NV) of it, so the helpers here, written for a lane's
+// vectors lane4 + 64k, take lane4 = w*64*NV + lane (lane4 = lane for one
+// wave a row).  Each reduction: the wave's total by the DPP butterfly, the
+// W totals through LDS (one barrier), added in wave order by every thread
+// -- a fixed order, like the one-wave form.  lds: 2*W doubles.
+template <int NV, int KIND, int W>
+__device__ __forceinline__ float row_scale_w(float4 (&v)[NV], int lane4, int64_t ne0, float eps, double* lds) {
+    if constexpr (W == 1) {
+        return wave_row_scale<NV, KIND>(v, lane4, ne0, eps);
+    } else {
+        const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+        double s = 0.0;
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float t = get(v[k], e);
+                if constexpr (KIND == NORM_LN) s += static_cast<double>(t);
+                else s += static_cast<double>(t * t);
+            }
+        }
+        s = wave_sum(s);
+        if (lane == 0) lds[wid] = s;
+        __syncthreads();
+        s = lds[0];
+#pragma unroll
+        for (int i = 1; i < W; i++) s += lds[i];
+        if constexpr (KIND == NORM_LN) {
+            const float mean = static_cast<float>(s) / static_cast<float>(ne0);
+            double s2 = 0.0;
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                if ((lane4 + 64 * k) * 4 < ne0) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float d = get(v[k], e) - mean;
+                        set(v[k], e, d);
+                        s2 += static_cast<double>(d * d);
+                    }
+                }
+            }
+            s2 = wave_sum(s2);
+            if (lane == 0) lds[W + wid] = s2;
+            __syncthreads();
+            s2 = lds[W];
+#pragma unroll
+            for (int i = 1; i < W; i++) s2 += lds[W + i];
+            const float var = static_cast<float>(s2 / static_cast<double>(ne0));
+            return 1.0f / sqrtf(var + eps);
+        } else {
+            const float ms = static_cast<float>(s / static_cast<double>(ne0));
+            return 1.0f / sqrtf(ms + eps);
+        }
+    }
+}
+
 // Affine vectors for the lane's elements, loaded up front (uniform branches:
 // the loads overlap the row loads instead of stalling the epilogue).
 template <int NV>
@@ -113,6 +170,10 @@ struct Affine {
     }
 };
 
+// Output rows are written with streaming (nontemporal) stores: left dirty
+// in the L2 instead, the rows were written back at the kernel's end, which
+// measured 0.2 us longer per launch for the 8 MB of the T3 prefill's
+// embedding + LayerNorm.
 template <typename TO, int NV, bool ACT>
 __device__ __forceinline__ void wave_row_store(const float4 (&v)[NV], int lane, int64_t ne0, float scale,
                                                const Affine<NV>& af, bool hw, bool hb, int act,
@@ -130,7 +191,7 @@ __device__ __forceinline__ void wave_row_store(const float4 (&v)[NV], int lane, 
                 if constexpr (ACT) t = apply_act(act, t, tab, 0.0f);
                 set(o, e, t);
             }
-            Elt<TO>::store4(yr + j * Elt<TO>::size, o);
+            Stream<TO>::store4(yr + j * Elt<TO>::size, o);
         }
     }
 }
@@ -171,10 +232,10 @@ __device__ __forceinline__ void embed_bad_row(char* hr, char* yr, int64_t ne0, i
 // an id was out of range -- the caller passed row 0 in its place, and the
 // row's outputs are zeroed instead, after the loads, so no branch precedes
 // them.
-template <int TYPE, int TYPE2, int NV>
+template <int TYPE, int TYPE2, int NV, int W = 1>
 __device__ __forceinline__ void embed_ln_row(const char* s1, const char* s2, const Affine<NV>& af, bool hw, bool hb,
                                              char* hr, char* yr, int64_t ne0, float eps, int lane, bool bad,
-                                             uint32_t* err) {
+                                             uint32_t* err, double* lds = nullptr) {
     float4 p[NV], q[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
@@ -182,8 +243,8 @@ __device__ __forceinline__ void embed_ln_row(const char* s1, const char* s2, con
         p[k] = load_table4<TYPE>(s1, j < ne0 ? j : 0);
         q[k] = load_table4<TYPE2>(s2, j < ne0 ? j : 0);
     }
-    if (bad) {
-        embed_bad_row(hr, yr, ne0, lane, err);
+    if (bad) {   // uniform over the workgroup: every wave of the row leaves
+        if (lane < 64) embed_bad_row(hr, yr, ne0, lane, err);
         return;
     }
     float4 v[NV];
@@ -192,12 +253,12 @@ __device__ __forceinline__ void embed_ln_row(const char* s1, const char* s2, con
         const int64_t j = (lane + 64 * k) * 4;
         if (j < ne0) {
             v[k] = make_float4(p[k].x + q[k].x, p[k].y + q[k].y, p[k].z + q[k].z, p[k].w + q[k].w);
-            if (hr) *reinterpret_cast<float4*>(hr + j * 4) = v[k];
+            if (hr) Stream<float>::store4(hr + j * 4, v[k]);
         } else {
             v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
     }
-    const float scale = wave_row_scale<NV, NORM_LN>(v, lane, ne0, eps);
+    const float scale = row_scale_w<NV, NORM_LN, W>(v, lane, ne0, eps, lds);
     wave_row_store<float, NV, false>(v, lane, ne0, scale, af, hw, hb, CBX_UNARY_NONE, nullptr, yr);
 }
 

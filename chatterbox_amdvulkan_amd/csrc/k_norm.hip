@@ -138,12 +138,16 @@ struct EmbedFlat {
     uint32_t* err;
 };
 
-// One wave per workgroup and exactly n_tok workgroups: no bounds check and
-// no read of the launch's block size, so nothing waits before the argument
-// loads and the id loads are issued.
-template <int TYPE, int TYPE2, int NV>
-__global__ __launch_bounds__(64) void k_embed_norm_flat(EmbedFlat a) {
-    const int lane = threadIdx.x;
+// One workgroup per token, exactly n_tok workgroups: no bounds check and no
+// read of the launch's block size, so nothing waits before the argument
+// loads and the id loads are issued.  W waves share the token's row (wave w
+// holds float4s [w*64*NV, (w+1)*64*NV)): with few tokens (a 512-token
+// prefill on 256 CUs) one wave a row leaves most SIMDs idle while each
+// wave walks its chain of dependent loads and reductions.
+template <int TYPE, int TYPE2, int NV, int W>
+__global__ __launch_bounds__(64 * W) void k_embed_norm_flat(EmbedFlat a) {
+    __shared__ double lds[2 * W];
+    const int lane = (threadIdx.x >> 6) * 64 * NV + (threadIdx.x & 63);   // the lane's first float4
     const int t = static_cast<int>(blockIdx.x);
     const int32_t id = __builtin_amdgcn_readfirstlane(a.ids[t]);
     const int32_t id2 = __builtin_amdgcn_readfirstlane(a.ids2[t]);
@@ -155,8 +159,8 @@ __global__ __launch_bounds__(64) void k_embed_norm_flat(EmbedFlat a) {
     // an out-of-range id reads row 0 and zeroes the outputs after the loads
     const bool bad = id < 0 || id >= a.src_rows || id2 < 0 || id2 >= a.src2_rows;
     const int64_t r1 = bad ? 0 : id, r2 = bad ? 0 : id2;
-    embed_ln_row<TYPE, TYPE2, NV>(a.src + r1 * a.src_nb1, a.src2 + r2 * a.src2_nb1, af, a.w != nullptr,
-                                  a.b != nullptr, hr, yr, ne0, a.eps, lane, bad, a.err);
+    embed_ln_row<TYPE, TYPE2, NV, W>(a.src + r1 * a.src_nb1, a.src2 + r2 * a.src2_nb1, af, a.w != nullptr,
+                                     a.b != nullptr, hr, yr, ne0, a.eps, lane, bad, a.err, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -461,21 +465,25 @@ void embed_nv(const EmbedArgs& a, int nv, dim3 grid, dim3 block, hipStream_t s) 
     }
 }
 
+// nv: vectors a lane for one wave a row; w: waves a row (nv % w == 0)
 template <int TYPE, int TYPE2>
-void embed_flat_nv(const EmbedFlat& a, int nv, hipStream_t s) {
-    const dim3 grid(static_cast<unsigned>(a.n_tok)), block(64);
-    switch (nv) {
-        case 1: hipLaunchKernelGGL((k_embed_norm_flat<TYPE, TYPE2, 1>), grid, block, 0, s, a); break;
-        case 2: hipLaunchKernelGGL((k_embed_norm_flat<TYPE, TYPE2, 2>), grid, block, 0, s, a); break;
-        default: hipLaunchKernelGGL((k_embed_norm_flat<TYPE, TYPE2, 4>), grid, block, 0, s, a); break;
+void embed_flat_nv(const EmbedFlat& a, int nv, int w, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(a.n_tok)), block(64 * w);
+    switch (nv * 8 + w) {
+        case 1 * 8 + 1: hipLaunchKernelGGL((k_embed_norm_flat<TYPE, TYPE2, 1, 1>), grid, block, 0, s, a); break;
+        case 2 * 8 + 1: hipLaunchKernelGGL((k_embed_norm_flat<TYPE, TYPE2, 2, 1>), grid, block, 0, s, a); break;
+        case 2 * 8 + 2: hipLaunchKernelGGL((k_embed_norm_flat<TYPE, TYPE2, 1, 2>), grid, block, 0, s, a); break;
+        case 4 * 8 + 1: hipLaunchKernelGGL((k_embed_norm_flat<TYPE, TYPE2, 4, 1>), grid, block, 0, s, a); break;
+        case 4 * 8 + 2: hipLaunchKernelGGL((k_embed_norm_flat<TYPE, TYPE2, 2, 2>), grid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL((k_embed_norm_flat<TYPE, TYPE2, 1, 4>), grid, block, 0, s, a); break;
     }
 }
 
 template <int TYPE>
-void embed_flat_t2(int t2, const EmbedFlat& a, int nv, hipStream_t s) {
-    if (t2 == CBX_TYPE_F32) embed_flat_nv<TYPE, CBX_TYPE_F32>(a, nv, s);
-    else if (t2 == CBX_TYPE_F16) embed_flat_nv<TYPE, CBX_TYPE_F16>(a, nv, s);
-    else embed_flat_nv<TYPE, CBX_TYPE_Q8_0>(a, nv, s);
+void embed_flat_t2(int t2, const EmbedFlat& a, int nv, int w, hipStream_t s) {
+    if (t2 == CBX_TYPE_F32) embed_flat_nv<TYPE, CBX_TYPE_F32>(a, nv, w, s);
+    else if (t2 == CBX_TYPE_F16) embed_flat_nv<TYPE, CBX_TYPE_F16>(a, nv, w, s);
+    else embed_flat_nv<TYPE, CBX_TYPE_Q8_0>(a, nv, w, s);
 }
 
 template <int TYPE>
@@ -533,10 +541,14 @@ int launch_embed_norm(const cbx_tensor* src, const cbx_tensor* ids, const cbx_te
         f.ne0 = static_cast<int32_t>(ne0);
         f.eps = eps;
         f.err = st->err_word;
+        // waves a row: enough waves for about eight a CU, at most 4 and at
+        // most one per vector a lane (the row split into whole float4 runs)
+        int wr = 1;
+        while (wr < 4 && wr < nv && n_tok * wr < int64_t{8} * st->n_cu) wr *= 2;
         switch (src->type) {
-            case CBX_TYPE_F32: embed_flat_t2<CBX_TYPE_F32>(src2->type, f, nv, s); break;
-            case CBX_TYPE_F16: embed_flat_t2<CBX_TYPE_F16>(src2->type, f, nv, s); break;
-            default: embed_flat_t2<CBX_TYPE_Q8_0>(src2->type, f, nv, s); break;
+            case CBX_TYPE_F32: embed_flat_t2<CBX_TYPE_F32>(src2->type, f, nv, wr, s); break;
+            case CBX_TYPE_F16: embed_flat_t2<CBX_TYPE_F16>(src2->type, f, nv, wr, s); break;
+            default: embed_flat_t2<CBX_TYPE_Q8_0>(src2->type, f, nv, wr, s); break;
         }
         return check_launch("get_rows_add_layer_norm");
     }

@@ -45,9 +45,14 @@ __device__ __forceinline__ int64_t row_off(const RowMap& m, uint32_t r) {
     else return row_at(m, r);
 }
 
-template <int NV, bool ACT, int PRO, bool MASK, int WPB, bool FLAT>
-__global__ __launch_bounds__(64 * WPB) void k_ln_ext(LnExtArgs p) {
-    const int lane = threadIdx.x & 63;
+// WPB rows a workgroup (one wave each), or, with WPR > 1, one row shared by
+// WPR waves (wave w holds float4s [w*64*NV, (w+1)*64*NV) of it): few rows
+// (a 512-token prefill on 256 CUs) leave most SIMDs idle at one wave a row.
+template <int NV, bool ACT, int PRO, bool MASK, int WPB, bool FLAT, int WPR = 1>
+__global__ __launch_bounds__(64 * WPB * WPR) void k_ln_ext(LnExtArgs p) {
+    static_assert(WPB == 1 || WPR == 1, "rows a workgroup or waves a row, not both");
+    __shared__ double lds[2 * WPR];
+    const int lane = WPR > 1 ? (threadIdx.x >> 6) * 64 * NV + (threadIdx.x & 63) : (threadIdx.x & 63);
     uint32_t row = blockIdx.x;
     if constexpr (WPB > 1) {
         row = row * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -97,27 +102,30 @@ __global__ __launch_bounds__(64 * WPB) void k_ln_ext(LnExtArgs p) {
 #pragma unroll
             for (int k = 0; k < NV; k++) {
                 const int64_t j = (lane + 64 * k) * 4;
-                if (j < ne0) *reinterpret_cast<float4*>(sr + j * 4) = v[k];
+                if (j < ne0) Stream<float>::store4(sr + j * 4, v[k]);
             }
         }
     }
-    const float scale = wave_row_scale<NV, NORM_LN>(v, lane, ne0, p.eps);
+    const float scale = row_scale_w<NV, NORM_LN, WPR>(v, lane, ne0, p.eps, lds);
     const bool hw = p.w != nullptr, hb = p.b != nullptr;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float t = get(v[k], e) * scale;
+            if (hw) t = t * get(af.w[k], e);
+            if (hb) t = t + get(af.b[k], e);
+            set(v[k], e, t);
+        }
+    }
+    if constexpr (ACT) apply_act_vec<NV>(p.act, v, p.tab, 0.0f);
 #pragma unroll
     for (int k = 0; k < NV; k++) {
         const int64_t j = (lane + 64 * k) * 4;
         if (j < ne0) {
-            float4 o;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float t = get(v[k], e) * scale;
-                if (hw) t = t * get(af.w[k], e);
-                if (hb) t = t + get(af.b[k], e);
-                if constexpr (ACT) t = apply_act(p.act, t, p.tab, 0.0f);
-                if constexpr (MASK) t = t * m;
-                set(o, e, t);
-            }
-            *reinterpret_cast<float4*>(yr + j * 4) = o;
+            float4 o = v[k];
+            if constexpr (MASK) o = make_float4(o.x * m, o.y * m, o.z * m, o.w * m);
+            Stream<float>::store4(yr + j * 4, o);
         }
     }
 }
@@ -134,10 +142,33 @@ void go_nv(const LnExtArgs& a, int nv, dim3 grid, hipStream_t s) {
     }
 }
 
+// One row a workgroup shared by wpr waves (nv: vectors a lane for one wave
+// a row; each wave then holds nv / wpr).
+template <bool ACT, int PRO, bool MASK>
+void go_wpr(const LnExtArgs& a, int nv, int wpr, dim3 grid, hipStream_t s) {
+    const dim3 block(64 * wpr);
+    switch (nv * 8 + wpr) {
+        case 2 * 8 + 2: hipLaunchKernelGGL((k_ln_ext<1, ACT, PRO, MASK, 1, true, 2>), grid, block, 0, s, a); break;
+        case 4 * 8 + 2: hipLaunchKernelGGL((k_ln_ext<2, ACT, PRO, MASK, 1, true, 2>), grid, block, 0, s, a); break;
+        case 4 * 8 + 4: hipLaunchKernelGGL((k_ln_ext<1, ACT, PRO, MASK, 1, true, 4>), grid, block, 0, s, a); break;
+        case 8 * 8 + 2: hipLaunchKernelGGL((k_ln_ext<4, ACT, PRO, MASK, 1, true, 2>), grid, block, 0, s, a); break;
+        case 8 * 8 + 4: hipLaunchKernelGGL((k_ln_ext<2, ACT, PRO, MASK, 1, true, 4>), grid, block, 0, s, a); break;
+        case 16 * 8 + 2: hipLaunchKernelGGL((k_ln_ext<8, ACT, PRO, MASK, 1, true, 2>), grid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL((k_ln_ext<4, ACT, PRO, MASK, 1, true, 4>), grid, block, 0, s, a); break;   // 16, 4
+    }
+}
+
 // Uniformly strided tensors take the FLAT kernels (four rows per workgroup
-// past 2048 rows); any other layout the general row map, one row each.
+// past 2048 rows, one row shared by wpr waves when the rows are few); any
+// other layout the general row map, one row each.
 template <int PRO, bool MASK>
-void go_pro(const LnExtArgs& a, bool act, int nv, int wpb, bool flat, int64_t nr, hipStream_t s) {
+void go_pro(const LnExtArgs& a, bool act, int nv, int wpb, int wpr, bool flat, int64_t nr, hipStream_t s) {
+    if (flat && wpr > 1) {
+        const dim3 grid(static_cast<unsigned>(nr));
+        if (act) go_wpr<true, PRO, MASK>(a, nv, wpr, grid, s);
+        else go_wpr<false, PRO, MASK>(a, nv, wpr, grid, s);
+        return;
+    }
     if (!flat) {
         const dim3 grid(static_cast<unsigned>(nr));
         if (act) go_nv<true, PRO, MASK, 1, false>(a, nv, grid, s);
@@ -197,11 +228,15 @@ int launch_layer_norm_ext(const cbx_tensor* a, const cbx_tensor* a_bias, const c
     p.act = act;
     const int nv = ne0 <= 256 ? 1 : ne0 <= 512 ? 2 : ne0 <= 1024 ? 4 : ne0 <= 2048 ? 8 : 16;
     const int wpb = nr >= int64_t{8} * st->n_cu ? 4 : 1;
+    // waves a row: enough for about eight waves a CU, at most 4 and at most
+    // one per vector a lane
+    int wpr = 1;
+    while (wpr < 4 && wpr < nv && nr * wpr < int64_t{8} * st->n_cu) wpr *= 2;
     const bool has_act = act != CBX_UNARY_NONE;
     const bool flat = p.ma.flat && p.my.flat && (!r || p.mr.flat) && (!s || p.ms.flat);
-    if (mask) go_pro<PRO_NONE, true>(p, has_act, nv, wpb, flat, nr, strm);
-    else if (a_bias) go_pro<PRO_BIAS_RESID, false>(p, has_act, nv, wpb, flat, nr, strm);
-    else go_pro<PRO_RESID, false>(p, has_act, nv, wpb, flat, nr, strm);
+    if (mask) go_pro<PRO_NONE, true>(p, has_act, nv, wpb, wpr, flat, nr, strm);
+    else if (a_bias) go_pro<PRO_BIAS_RESID, false>(p, has_act, nv, wpb, wpr, flat, nr, strm);
+    else go_pro<PRO_RESID, false>(p, has_act, nv, wpb, wpr, flat, nr, strm);
     return check_launch(what);
 }
 

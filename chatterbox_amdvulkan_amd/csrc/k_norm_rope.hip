@@ -154,7 +154,7 @@ __global__ __launch_bounds__(64) void k_layer_norm_rope(NormRopeArgs a) {
                 }
             }
         }
-        Elt<float>::store4(yr + j * 4, o);
+        Stream<float>::store4(yr + j * 4, o);
     }
 }
 
