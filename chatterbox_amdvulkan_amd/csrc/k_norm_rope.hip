@@ -35,6 +35,7 @@ struct NormRopeArgs {
     uint32_t n_tok;        // x.ne1: tokens per batch item (the position index)
     int32_t n_pos;
     float eps;
+    int32_t vec_cs;        // the table is 16-byte aligned with n_dims % 4 == 0: 16-byte cos/sin loads
     RopeParams rp;
 };
 
@@ -46,12 +47,35 @@ __device__ __forceinline__ int pair_of(int i, int nd, int half) {
     return i >> 1;
 }
 
+// cos/sin of the 4 elements of a vector starting at head-local element i0
+// (a multiple of 4) from the table row tr, when all 4 are rotated: NEOX's
+// pairs are i0 .. i0 + 3 (or those less half), four consecutive float2 --
+// two 16-byte loads; NORMAL's are i0/2, i0/2 (+1 twice) -- one.
+template <int MODE>
+__device__ __forceinline__ void cos_sin4(const float2* tr, int i0, int half, float2 (&cs)[4]) {
+    if constexpr (MODE == 2) {
+        const int m = i0 < half ? i0 : i0 - half;
+        const float4 a = *reinterpret_cast<const float4*>(tr + m);
+        const float4 b = *reinterpret_cast<const float4*>(tr + m + 2);
+        cs[0] = make_float2(a.x, a.y);
+        cs[1] = make_float2(a.z, a.w);
+        cs[2] = make_float2(b.x, b.y);
+        cs[3] = make_float2(b.z, b.w);
+    } else {
+        const float4 a = *reinterpret_cast<const float4*>(tr + (i0 >> 1));
+        cs[0] = cs[1] = make_float2(a.x, a.y);
+        cs[2] = cs[3] = make_float2(a.z, a.w);
+    }
+}
+
 // FLAT: x and y rows at one stride each (no test of the row map before the
-// loads are issued).
-template <int NV, int MODE, bool FLAT>
-__global__ __launch_bounds__(64) void k_layer_norm_rope(NormRopeArgs a) {
+// loads are issued).  W waves share a row (wave w holds float4s
+// [w*64*NV, (w+1)*64*NV) of it) when the rows are few.
+template <int NV, int MODE, bool FLAT, int W = 1>
+__global__ __launch_bounds__(64 * W) void k_layer_norm_rope(NormRopeArgs a) {
     __shared__ float row[kRowMax];
-    const int lane = threadIdx.x;
+    __shared__ double lds[2 * W];
+    const int lane = (threadIdx.x >> 6) * 64 * NV + (threadIdx.x & 63);   // the lane's first float4
     const uint32_t r = blockIdx.x;                // token row over ne1 * ne2
     const int64_t ne0 = a.ne0;
     const char* xr = a.x + (FLAT ? static_cast<int64_t>(r) * a.mx.nb1 : row_at(a.mx, r));
@@ -84,10 +108,14 @@ __global__ __launch_bounds__(64) void k_layer_norm_rope(NormRopeArgs a) {
         const float2* tr = a.table + static_cast<int64_t>(p) * half;
 #pragma unroll
         for (int k = 0; k < NV; k++) {
+            if (a.vec_cs && i0[k] + 4 <= nd) {
+                cos_sin4<MODE>(tr, i0[k], half, cs[k]);
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int m = pair_of<MODE>(i0[k] + e, nd, half);
-                cs[k][e] = m >= 0 ? tr[m] : make_float2(0.f, 0.f);
+                for (int e = 0; e < 4; e++) {
+                    const int m = pair_of<MODE>(i0[k] + e, nd, half);
+                    cs[k][e] = m >= 0 ? tr[m] : make_float2(0.f, 0.f);
+                }
             }
         }
     } else {   // positions past the table: the device recurrence
@@ -105,7 +133,7 @@ __global__ __launch_bounds__(64) void k_layer_norm_rope(NormRopeArgs a) {
     for (int k = 0; k < NV; k++) {
         if ((lane + 64 * k) * 4 >= ne0) v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    const float scale = wave_row_scale<NV, NORM_LN>(v, lane, ne0, a.eps);
+    const float scale = row_scale_w<NV, NORM_LN, W>(v, lane, ne0, a.eps, lds);
     const bool hw = a.w != nullptr, hb = a.b != nullptr;
 #pragma unroll
     for (int k = 0; k < NV; k++) {
@@ -159,7 +187,16 @@ __global__ __launch_bounds__(64) void k_layer_norm_rope(NormRopeArgs a) {
 }
 
 template <int MODE, bool FLAT>
-void go(const NormRopeArgs& a, int nv, dim3 grid, hipStream_t s) {
+void go(const NormRopeArgs& a, int nv, int w, dim3 grid, hipStream_t s) {
+    if (FLAT && w > 1) {
+        const dim3 block(64 * w);
+        switch (nv * 8 + w) {
+            case 2 * 8 + 2: hipLaunchKernelGGL((k_layer_norm_rope<1, MODE, FLAT, 2>), grid, block, 0, s, a); break;
+            case 4 * 8 + 2: hipLaunchKernelGGL((k_layer_norm_rope<2, MODE, FLAT, 2>), grid, block, 0, s, a); break;
+            default: hipLaunchKernelGGL((k_layer_norm_rope<1, MODE, FLAT, 4>), grid, block, 0, s, a); break;   // 4, 4
+        }
+        return;
+    }
     switch (nv) {
         case 1: hipLaunchKernelGGL((k_layer_norm_rope<1, MODE, FLAT>), grid, dim3(64), 0, s, a); break;
         case 2: hipLaunchKernelGGL((k_layer_norm_rope<2, MODE, FLAT>), grid, dim3(64), 0, s, a); break;
@@ -172,7 +209,6 @@ void go(const NormRopeArgs& a, int nv, dim3 grid, hipStream_t s) {
 int launch_layer_norm_rope(const cbx_tensor* x, const cbx_tensor* w, const cbx_tensor* b, float eps, int64_t head_dim,
                            const cbx_tensor* pos, const RopeParams& p, const float2* table, int32_t n_pos,
                            const float* ff, cbx_tensor* y, DeviceState* st, hipStream_t s) {
-    (void)st;
     NormRopeArgs a;
     a.x = static_cast<const char*>(x->data);
     a.y = static_cast<char*>(y->data);
@@ -192,15 +228,21 @@ int launch_layer_norm_rope(const cbx_tensor* x, const cbx_tensor* w, const cbx_t
     a.rp = p;
     const int64_t rows = x->ne[1] * x->ne[2] * x->ne[3];
     if (rows >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "layer_norm_rope: too many rows");
+    a.vec_cs = (reinterpret_cast<uintptr_t>(table) % 16 == 0 && p.n_dims % 4 == 0) ? 1 : 0;
     const int nv = x->ne[0] <= 256 ? 1 : x->ne[0] <= 512 ? 2 : 4;
+    // waves a row: enough for about eight waves a CU, at most 4 and at most
+    // one per vector a lane (the rotation reads partners from the LDS row
+    // after a workgroup barrier, so a wave's share need not be whole heads)
+    int wr = 1;
+    while (wr < 4 && wr < nv && rows * wr < int64_t{8} * st->n_cu) wr *= 2;
     const dim3 grid(static_cast<unsigned>(rows));
     const bool flat = a.mx.flat && a.my.flat;
     if (p.mode == 2) {
-        if (flat) go<2, true>(a, nv, grid, s);
-        else go<2, false>(a, nv, grid, s);
+        if (flat) go<2, true>(a, nv, wr, grid, s);
+        else go<2, false>(a, nv, 1, grid, s);
     } else {
-        if (flat) go<0, true>(a, nv, grid, s);
-        else go<0, false>(a, nv, grid, s);
+        if (flat) go<0, true>(a, nv, wr, grid, s);
+        else go<0, false>(a, nv, 1, grid, s);
     }
     return check_launch("layer_norm_rope");
 }
