@@ -393,6 +393,19 @@ def bench_serving(C, W, torch, reps=400):
             raise SystemExit(f"bench: serving plan {name} differs from one kernel per op")
         us = per_launch_ms(torch, fns, reps) * 1000.0
         out[name] = {"us_per_step": us, "GBps": per_step / (us * 1e-6) / 1e9}
+    # which op sets the one-launch time: each op alone as a one-op launch of
+    # the same batch kernel (same bodies, same workgroup mapping)
+    names = ("rms_norm_mul", "rope_q", "rope_k", "swiglu", "get_rows_q8_0")
+    alone = {}
+    for k, nm in enumerate(names):
+        singles = []
+        for t, _, one in sets:
+            b1 = C.OpBatch([one.ops[k]])
+            singles.append(b1)
+        fns = [(lambda b1: lambda s: check_rc(C, L.cbx_run_ops(b1.arr, b1.n, s)))(b1) for b1 in singles]
+        fns[0](cur_stream(torch))
+        alone[nm] = per_launch_ms(torch, fns, reps) * 1000.0
+    out["one_op_launch_us"] = alone
     cache.close()
     return dict(out, bytes_per_step=per_step, bytes=nb, buffer_sets=n_sets)
 

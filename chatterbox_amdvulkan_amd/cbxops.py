@@ -716,6 +716,7 @@ class OpBatch:
         if not ops or len(ops) > MAX_OPS:
             raise CbxError(ERR_INVALID_ARG, f"1..{MAX_OPS} ops per launch")
         self._keep: list = []
+        self.ops = list(ops)
         self.n = len(ops)
         self.arr = (OpStruct * self.n)(*[op.struct(self._keep) for op in ops])
 

@@ -1177,7 +1177,11 @@ int build_op(int i, const cbx_op& o, BOp& b, DeviceState* st, int64_t* nblk) {
             b.t[1] = bten(w, 0);
             b.t[2] = bten(bb, 0);
             b.t[6] = bten(y, static_cast<int64_t>(y->nb[1]));
-            *nblk = cdiv(b.rows, 4);
+            // rows of 513..1024 and few of them (a decode step's 1..64
+            // streams): one row a workgroup, shared by its 4 waves (aux3 = 4)
+            // instead of 4 rows a workgroup, one wave each (aux3 = 1)
+            b.aux3 = b.nv == 4 && b.rows <= int64_t{4} * st->n_cu ? 4 : 1;
+            *nblk = b.aux3 == 4 ? b.rows : cdiv(b.rows, 4);
             return CBX_OK;
         }
         case CBX_OP_UNARY:
@@ -1235,6 +1239,16 @@ int build_op(int i, const cbx_op& o, BOp& b, DeviceState* st, int64_t* nblk) {
             b.ff = c->freq_factors;
             b.n_pos = c->n_pos;
             b.rp = c->p;
+            // nv = 1: four pairs a lane with 4-element vector loads of x and
+            // y and 16-byte cos/sin loads (n_dims % 8 == 0, rows aligned to
+            // the vector size, the table to 16 bytes); 0: a pair a lane
+            {
+                const size_t vb = 4 * type_size(x->type);
+                const bool al = reinterpret_cast<uintptr_t>(x->data) % vb == 0 &&
+                                reinterpret_cast<uintptr_t>(y->data) % vb == 0 && x->nb[1] % vb == 0 &&
+                                y->nb[1] % vb == 0 && reinterpret_cast<uintptr_t>(c->table) % 16 == 0;
+                b.nv = al && c->p.n_dims % 8 == 0 ? 1 : 0;
+            }
             *nblk = nelements(x) ? b.rows : 0;
             return CBX_OK;
         }

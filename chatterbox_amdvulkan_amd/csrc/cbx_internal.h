@@ -166,9 +166,11 @@ struct BTen {
 };
 
 // One op of a batch, in kernel-argument memory.  Field use by kind:
-//   norms:     t0 x, t1 w, t2 b, t6 y; ne0, rows; nv vectors per lane; t_x type
+//   norms:     t0 x, t1 w, t2 b, t6 y; ne0, rows; nv vectors per lane; t_x type;
+//              aux3 waves a row (1: four rows a workgroup; 4: one row)
 //   unary/leaky/swiglu: t0 (t1) -> t6; n elements in `rows`; t_x type
-//   rope:      t0 x, t1 pos, t6 y; ne0 head_dim, aux heads, aux2 ne2, rows tokens
+//   rope:      t0 x, t1 pos, t6 y; ne0 head_dim, aux heads, aux2 ne2, rows tokens;
+//              nv 1: four pairs a lane with vector loads, 0: one pair a lane
 //   get_rows(+add)(+LN): t0 table, t1 ids, t2 table2, t3 ids2, t4 w, t5 b,
 //              t6 dst (h), t7 y; t_x/t_x2 table types; aux/aux2 table rows
 //   snake:     t0 x, t1 a, t2 ai, t6 y; act 1 = alpha along ne0; aux C,

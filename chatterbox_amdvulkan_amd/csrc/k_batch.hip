@@ -24,8 +24,11 @@ __device__ __forceinline__ void b_norm_row(const BOp& op, int64_t row, int lane,
     char* yr = op.t[6].p + row * op.t[6].nb1;
     const float* w = reinterpret_cast<const float*>(op.t[1].p);
     const float* b = reinterpret_cast<const float*>(op.t[2].p);
+    // branch-free affine loads (a missing w or b reads the GELU table, 64K
+    // floats, instead): with `if (w)` the compiler sinks them past the
+    // reduction, adding their latency to the row's chain
     Affine<NV> af;
-    af.load(w, b, lane, ne0);
+    af.load_sel(w, b, reinterpret_cast<const float*>(tab), lane, ne0);
     float4 v[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
@@ -53,11 +56,47 @@ __device__ __forceinline__ void b_norm_nv(const BOp& op, int64_t row, int lane, 
     }
 }
 
-__device__ __forceinline__ void b_norm(const BOp& op, uint32_t lb, const uint16_t* tab) {
+// One row a workgroup, its 4 waves holding a quarter of it each (rows of
+// 1024 = 4 x 64 lanes x one float4): few rows then still give the SIMDs
+// work, where one wave a row left a 64-row step on 16 workgroups.
+template <typename T, int KIND>
+__device__ __forceinline__ void b_norm_row4(const BOp& op, int64_t row, const uint16_t* tab, double* lds) {
+    const int64_t ne0 = op.ne0;
+    const int lane4 = threadIdx.x;   // wave w: float4s [64w, 64w + 64)
+    const char* xr = op.t[0].p + row * op.t[0].nb1;
+    char* yr = op.t[6].p + row * op.t[6].nb1;
+    const float* w = reinterpret_cast<const float*>(op.t[1].p);
+    const float* b = reinterpret_cast<const float*>(op.t[2].p);
+    Affine<1> af;
+    af.load_sel(w, b, reinterpret_cast<const float*>(tab), lane4, ne0);
+    float4 v[1];
+    const int64_t j = lane4 * 4;
+    v[0] = Elt<T>::load4(xr + (j < ne0 ? j : 0) * Elt<T>::size);
+    if (j >= ne0) v[0] = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float scale = row_scale_w<1, KIND, 4>(v, lane4, ne0, op.eps, lds);
+    if (op.act != CBX_UNARY_NONE) {
+        wave_row_store<T, 1, true>(v, lane4, ne0, scale, af, w != nullptr, b != nullptr, op.act, tab, yr);
+    } else {
+        wave_row_store<T, 1, false>(v, lane4, ne0, scale, af, w != nullptr, b != nullptr, op.act, tab, yr);
+    }
+}
+
+__device__ __forceinline__ void b_norm(const BOp& op, uint32_t lb, const uint16_t* tab, double* lds) {
+    const bool f16 = op.t_x == CBX_TYPE_F16;
+    if (op.aux3 == 4) {   // one row a workgroup (rows <= 1024 elements, nv == 4)
+        const int64_t row = lb;
+        if (op.kind == CBX_OP_LAYER_NORM) {
+            if (f16) b_norm_row4<uint16_t, NORM_LN>(op, row, tab, lds);
+            else b_norm_row4<float, NORM_LN>(op, row, tab, lds);
+        } else {
+            if (f16) b_norm_row4<uint16_t, NORM_RMS>(op, row, tab, lds);
+            else b_norm_row4<float, NORM_RMS>(op, row, tab, lds);
+        }
+        return;
+    }
     const int lane = threadIdx.x & 63;
     const int64_t row = static_cast<int64_t>(lb) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (row >= op.rows) return;   // uniform per wave
-    const bool f16 = op.t_x == CBX_TYPE_F16;
     if (op.kind == CBX_OP_LAYER_NORM) {
         if (f16) b_norm_nv<uint16_t, NORM_LN>(op, row, lane, tab);
         else b_norm_nv<float, NORM_LN>(op, row, lane, tab);
@@ -168,8 +207,74 @@ __device__ __forceinline__ void b_snake(const BOp& op, uint32_t lb) {
 }
 
 // ---- rope: one token per workgroup ------------------------------------------------
+// Four rotation pairs a lane: NEOX pairs m..m+3 are two 4-element vectors of
+// the head (at m and m + n_dims/2), NORMAL pairs m..m+3 the 8 elements from
+// 2m; their cos/sin are two 16-byte loads from the table row of the
+// token's position (no staging: the row is in L2 after the first lane).
+// Same products and roundings as the one-pair-a-lane form below.
+template <typename T>
+__device__ __forceinline__ void b_rope_vec(const BOp& op, uint32_t t) {
+    const uint32_t half = static_cast<uint32_t>(op.rp.n_dims / 2);
+    const uint32_t heads = static_cast<uint32_t>(op.aux), ne2 = static_cast<uint32_t>(op.aux2);
+    const uint32_t n_tail = static_cast<uint32_t>(op.ne0 - op.rp.n_dims);
+    const int32_t p = *reinterpret_cast<const int32_t*>(op.t[1].p + (t % ne2) * op.t[1].nb1);
+    const bool in_tab = p >= 0 && p < op.n_pos;
+    const float2* tr = reinterpret_cast<const float2*>(op.table) + static_cast<int64_t>(in_tab ? p : 0) * half;
+    constexpr int es = Elt<T>::size;
+    const char* xt = op.t[0].p + static_cast<int64_t>(t) * heads * op.t[0].nb1;
+    char* yt = op.t[6].p + static_cast<int64_t>(t) * heads * op.t[6].nb1;
+    const uint32_t per_head = half / 4;
+    const bool neox = op.rp.mode == 2;
+    for (uint32_t q = threadIdx.x; q < heads * per_head; q += kThreads) {
+        const uint32_t h = q / per_head;
+        const uint32_t m = (q - h * per_head) * 4;
+        const char* xr = xt + h * op.t[0].nb1;
+        char* yr = yt + h * op.t[6].nb1;
+        const uint32_t ia = neox ? m : 2 * m, ib = neox ? m + half : 2 * m + 4;
+        const float4 xa = Elt<T>::load4(xr + ia * es);
+        const float4 xb = Elt<T>::load4(xr + ib * es);
+        float2 c[4];
+        if (in_tab) {
+            const float4 c01 = *reinterpret_cast<const float4*>(tr + m);
+            const float4 c23 = *reinterpret_cast<const float4*>(tr + m + 2);
+            c[0] = make_float2(c01.x, c01.y);
+            c[1] = make_float2(c01.z, c01.w);
+            c[2] = make_float2(c23.x, c23.y);
+            c[3] = make_float2(c23.z, c23.w);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) rope_cos_sin_dev(p, static_cast<int>(m) + e, op.rp, op.ff, &c[e].x, &c[e].y);
+        }
+        float4 ya, yb;
+        if (neox) {   // y[i] = x0 cos - x1 sin, y[i + half] = x0 sin + x1 cos
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float x0 = get(xa, e), x1 = get(xb, e);
+                set(ya, e, x0 * c[e].x - x1 * c[e].y);
+                set(yb, e, x0 * c[e].y + x1 * c[e].x);
+            }
+        } else {      // pairs (2k, 2k + 1)
+            ya = make_float4(xa.x * c[0].x - xa.y * c[0].y, xa.x * c[0].y + xa.y * c[0].x,
+                             xa.z * c[1].x - xa.w * c[1].y, xa.z * c[1].y + xa.w * c[1].x);
+            yb = make_float4(xb.x * c[2].x - xb.y * c[2].y, xb.x * c[2].y + xb.y * c[2].x,
+                             xb.z * c[3].x - xb.w * c[3].y, xb.z * c[3].y + xb.w * c[3].x);
+        }
+        Elt<T>::store4(yr + ia * es, ya);
+        Elt<T>::store4(yr + ib * es, yb);
+    }
+    for (uint32_t q = threadIdx.x; q < heads * n_tail; q += kThreads) {
+        const uint32_t h = q / n_tail;
+        const uint32_t j = static_cast<uint32_t>(op.rp.n_dims) + (q - h * n_tail);
+        *reinterpret_cast<T*>(yt + h * op.t[6].nb1 + j * es) = *reinterpret_cast<const T*>(xt + h * op.t[0].nb1 + j * es);
+    }
+}
+
 template <typename T>
 __device__ __forceinline__ void b_rope_t(const BOp& op, uint32_t lb, float2* cs) {
+    if (op.nv == 1) {
+        b_rope_vec<T>(op, lb);
+        return;
+    }
     const uint32_t t = lb;                        // token index over ne2 * ne3
     const uint32_t half = static_cast<uint32_t>(op.rp.n_dims / 2);
     const uint32_t heads = static_cast<uint32_t>(op.aux), ne2 = static_cast<uint32_t>(op.aux2);
@@ -256,7 +361,7 @@ __device__ __forceinline__ void b_embed_ln_t(const BOp& op, uint32_t lb, uint32_
     const float* w = reinterpret_cast<const float*>(op.t[4].p);
     const float* b = reinterpret_cast<const float*>(op.t[5].p);
     Affine<NV> af;
-    af.load(w, b, lane, ne0);
+    af.load_sel(w, b, reinterpret_cast<const float*>(op.table), lane, ne0);
     const bool bad = id < 0 || id >= op.aux || id2 < 0 || id2 >= op.aux2;
     const int64_t r1 = bad ? 0 : id, r2 = bad ? 0 : id2;
     embed_ln_row<TYPE, TYPE2, NV>(op.t[0].p + r1 * op.t[0].nb1, op.t[2].p + r2 * op.t[2].nb1, af, w != nullptr,
@@ -294,6 +399,7 @@ __device__ __forceinline__ void b_embed_1(const BOp& op, uint32_t lb, uint32_t* 
 __global__ __launch_bounds__(kThreads) void k_batch(BatchArgs args) {
     (void)args;
     __shared__ float2 cs[kRopeMaxHalf];
+    __shared__ double lds[8];
     const BatchArgs* a = (const BatchArgs*)(const void*)__builtin_amdgcn_kernarg_segment_ptr();
     const uint32_t b = blockIdx.x;
     const int n = a->n;
@@ -308,14 +414,18 @@ __global__ __launch_bounds__(kThreads) void k_batch(BatchArgs args) {
             base = a->blk0[k];
         }
     }
-    const BOp& op = a->op[i];
+    // the op's fields, copied before any branch on them: the copy's scalar
+    // loads issue together, where reads under each branch (kind, layout,
+    // type) came as dependent rounds of argument loads before the first
+    // load of data
+    const BOp op = a->op[i];
     const uint32_t lb = b - base;
     uint32_t* err = a->err;
     const uint16_t* tab = reinterpret_cast<const uint16_t*>(op.table);
     switch (op.kind) {
         case CBX_OP_LAYER_NORM:
         case CBX_OP_RMS_NORM:
-            b_norm(op, lb, tab);
+            b_norm(op, lb, tab, lds);
             break;
         case CBX_OP_UNARY:
         case CBX_OP_LEAKY_RELU:

@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from chatterbox_amdvulkan_amd import workloads as W
-from tests._util import assert_bitexact, assert_close
+from tests._util import RTOL_F16, assert_bitexact, assert_close
 
 pytestmark = pytest.mark.gpu
 
@@ -171,3 +171,48 @@ def test_gelu_all_codes_in_batch(cbx, oracle):
     cbx.run_ops([cbx.Op(cbx.OP_UNARY, [a], [ya], act=cbx.GELU), cbx.Op(cbx.OP_UNARY, [b], [yb], act=cbx.GELU)])
     assert_bitexact(host(ya), oracle.unary(oracle.GELU, x32), "batched gelu f32")
     assert_bitexact(host(yb), oracle.unary(oracle.GELU, codes), "batched gelu f16")
+
+
+@pytest.mark.parametrize("mode,n_dims", [(2, 64), (0, 64), (2, 32), (0, 32), (2, 20), (0, 20)])
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_batched_rope_forms(cbx, oracle, mode, n_dims, dtype):
+    """RoPE in the batch kernel, both pairings, full and partial rotation
+    (n_dims % 8 != 0 takes the pair-a-lane form), positions inside and past
+    the table (the device recurrence): the same bits as cbx_rope_ext, and the
+    oracle's bits inside the table."""
+    cache = cbx.RopeCache(n_dims, mode=mode, n_ctx_orig=2048, n_pos=48)
+    x = W.normal(85 + n_dims + mode, (40, 12, 64)).astype(dtype)       # (n_tok, n_head, head_dim)
+    pos = np.concatenate([np.arange(0, 40, 2), np.arange(44, 64)]).astype(np.int32)   # 20 past the table
+    xd, pd = dev(x), dev(pos)
+    y = torch.empty_like(xd)
+    cbx.run_ops([cbx.Op(cbx.OP_ROPE, [xd, pd], [y], rope=cache)])
+    single = host(cbx.rope_ext(xd, pd, cache))
+    got = host(y)
+    assert_bitexact(got, single, "batched rope = single op")
+    inside = pos < 48
+    exp = oracle.rope_ext(x, pos, n_dims, mode=mode)
+    assert_bitexact(got[inside], exp[inside], "batched rope in the table")
+    rtol = 1e-5 if dtype == np.float32 else RTOL_F16
+    assert_close(got[~inside].astype(np.float32), exp[~inside].astype(np.float32), rtol=rtol, atol_x=2 ** -20,
+                 x=x[~inside].astype(np.float32), what="batched rope past the table")
+    cache.close()
+
+
+@pytest.mark.parametrize("rows", [1, 64, 1500])
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_batched_norm_row_forms(cbx, oracle, rows, dtype):
+    """RMSNorm and LayerNorm of 1024-wide rows in the batch kernel: few rows
+    (one row a workgroup over four waves) and many (four rows a workgroup):
+    the same bits as the single-op entry points and the oracle."""
+    x = W.normal(90 + rows, (rows, 1024)).astype(dtype)
+    g = W.normal(91, (1024,), 1.0, 0.02)
+    b = W.normal(92, (1024,), 0.0, 0.02)
+    xd, gd, bd = dev(x), dev(g), dev(b)
+    yr, yl = torch.empty_like(xd), torch.empty_like(xd)
+    cbx.run_ops([cbx.Op(cbx.OP_RMS_NORM, [xd, gd], [yr], eps=1e-5),
+                 cbx.Op(cbx.OP_LAYER_NORM, [xd, gd, bd], [yl], eps=1e-5)])
+    assert_bitexact(host(yr), host(cbx.rms_norm_mul(xd, gd, 1e-5)), "batched rms = single op")
+    assert_bitexact(host(yl), host(cbx.layer_norm(xd, gd, bd, 1e-5)), "batched ln = single op")
+    if dtype == np.float32:
+        assert_bitexact(host(yr), oracle.rms_norm_mul(x, g, 1e-5, nth=8), "batched rms")
+        assert_bitexact(host(yl), oracle.layer_norm(x, g, b, 1e-5, nth=8), "batched ln")
