@@ -113,7 +113,7 @@ GOP_VIEW, GOP_GET_ROWS, GOP_ADD, GOP_MUL, GOP_SCALE, GOP_NORM, GOP_RMS_NORM, GOP
 GL_UNSUPPORTED, GL_VIEW, GL_GET_ROWS, GL_GET_ROWS_ADD, GL_GET_ROWS_ADD_LAYER_NORM, GL_NORM, GL_LAYER_NORM, \
     GL_LAYER_NORM_ROPE, GL_RMS_NORM, GL_GROUP_NORM, GL_SOFT_MAX, GL_SNAKE, GL_UNARY, GL_SWIGLU, GL_LEAKY_RELU, \
     GL_ROPE, GL_CPY, GL_ADD_LAYER_NORM, GL_LAYER_NORM_MASK, GL_BIAS_ACT, GL_CONV1D, GL_CONV_TRANSPOSE1D, \
-    GL_CAUSAL_CONV1D = range(23)
+    GL_CAUSAL_CONV1D, GL_GET_ROWS_CONCAT_ADD_LAYER_NORM = range(24)
 # conv launch flags: the prologue (bits 0-1), a bias add, the residual add
 GLF_SNAKE, GLF_LEAKY, GLF_MASK, GLF_BIAS, GLF_RESIDUAL = 1, 2, 3, 4, 8
 
@@ -152,6 +152,7 @@ def load() -> ctypes.CDLL:
         "cbx_get_rows": (i, [P, P, P, vp]),
         "cbx_get_rows_add": (i, [P, P, P, P, P, vp]),
         "cbx_get_rows_add_layer_norm": (i, [P, P, P, P, P, P, f, P, P, vp]),
+        "cbx_get_rows_concat_add_layer_norm": (i, [P, P, P, P, P, P, P, P, P, f, P, P, vp]),
         "cbx_cpy": (i, [P, P, vp]),
         "cbx_norm": (i, [P, f, P, vp]),
         "cbx_layer_norm": (i, [P, P, P, f, i, P, vp]),
@@ -316,6 +317,26 @@ def get_rows_add(table, ids, table2, ids2, out=None, q8_0=False, q8_0_2=False):
                                    _ref(desc(table2, Q8_0 if q8_0_2 else None)), _ref(desc(ids2)),
                                    _ref(desc(out)), _stream()))
     return out
+
+
+def get_rows_concat_add_layer_norm(prefix, table_a, ids_a, table_b, ids_b, table2, ids2, w, b, eps, h=None,
+                                   out=None, store_h=True, q8=()):
+    """The T3 input with the conditioning prefix (t3.cpp:432-466): rows of
+    concat(prefix, get_rows(table_a, ids_a), get_rows(table_b, ids_b)) plus
+    get_rows(table2, ids2), then LayerNorm; returns (h, y).  prefix and
+    table_a/ids_a may be None; q8 names the tables ("a", "b", "2") stored as Q8_0."""
+    _ready(table_b)
+    ne0 = table_b.shape[-1] // Q8_0_BLOCK * QK8_0 if "b" in q8 else table_b.shape[-1]
+    n = (prefix.shape[0] if prefix is not None else 0) + (ids_a.numel() if ids_a is not None else 0) + ids_b.numel()
+    if out is None:
+        out = torch.empty((n, ne0), dtype=torch.float32, device=table_b.device)
+    if h is None and store_h:
+        h = torch.empty((n, ne0), dtype=torch.float32, device=table_b.device)
+    opt = lambda t, k=None: _ref(desc(t, Q8_0 if k in q8 else None)) if t is not None else None  # noqa: E731
+    _check(load().cbx_get_rows_concat_add_layer_norm(
+        opt(prefix), opt(table_a, "a"), opt(ids_a), opt(table_b, "b"), opt(ids_b), opt(table2, "2"), opt(ids2),
+        opt(w), opt(b), eps, opt(h), _ref(desc(out)), _stream()))
+    return h, out
 
 
 def get_rows_add_layer_norm(table, ids, table2, ids2, w, b, eps, h=None, out=None, q8_0=False, q8_0_2=False,

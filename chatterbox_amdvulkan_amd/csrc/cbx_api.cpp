@@ -310,6 +310,7 @@ int cbx_get_rows_add(const cbx_tensor* src, const cbx_tensor* ids, const cbx_ten
 }
 
 static int check_row_param(const cbx_tensor* p, const cbx_tensor* x, const char* what, const char* name);
+static bool overlaps(const cbx_tensor* a, const cbx_tensor* b);
 
 int cbx_get_rows_add_layer_norm(const cbx_tensor* src, const cbx_tensor* ids, const cbx_tensor* src2,
                                 const cbx_tensor* ids2, const cbx_tensor* w, const cbx_tensor* b, float eps,
@@ -330,6 +331,74 @@ int cbx_get_rows_add_layer_norm(const cbx_tensor* src, const cbx_tensor* ids, co
     if ((rc = check_row_param(w, y, what, "w")) || (rc = check_row_param(b, y, what, "b"))) return rc;
     if (nelements(y) == 0) return CBX_OK;
     return launch_embed_norm(src, ids, src2, ids2, w, b, eps, h, y, st, reinterpret_cast<hipStream_t>(stream));
+}
+
+int cbx_get_rows_concat_add_layer_norm(const cbx_tensor* prefix, const cbx_tensor* src_a, const cbx_tensor* ids_a,
+                                       const cbx_tensor* src_b, const cbx_tensor* ids_b, const cbx_tensor* src2,
+                                       const cbx_tensor* ids2, const cbx_tensor* w, const cbx_tensor* b, float eps,
+                                       cbx_tensor* h, cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_get_rows_concat_add_layer_norm";
+    const std::string f(what);
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(y, what, "y"))) return rc;
+    if (y->type != CBX_TYPE_F32 || y->ne[2] != 1 || y->ne[3] != 1) {
+        return set_error(CBX_ERR_INVALID_ARG, f + ": y must be F32 (D, N, 1, 1)");
+    }
+    const int64_t D = y->ne[0];
+    // a gathered segment: a 2-D table of D-wide rows and 1-D contiguous I32 ids
+    auto seg = [&](const cbx_tensor* src, const cbx_tensor* ids, const char* ns, const char* ni) -> int {
+        int r;
+        if ((r = validate(src, what, ns)) || (r = validate(ids, what, ni))) return r;
+        if (src->type != CBX_TYPE_F32 && src->type != CBX_TYPE_F16 && src->type != CBX_TYPE_Q8_0) {
+            return set_error(CBX_ERR_UNSUPPORTED, f + ": tables must be F32, F16 or Q8_0");
+        }
+        if (src->ne[0] != D || src->ne[2] != 1 || src->ne[3] != 1 || src->ne[1] == 0 || src->ne[1] >= (int64_t{1} << 31)) {
+            return set_error(CBX_ERR_INVALID_ARG, f + ": tables must be 2-D with ne0 = y.ne0 and 1..2^31-1 rows");
+        }
+        if (ids->type != CBX_TYPE_I32 || ids->ne[1] != 1 || ids->ne[2] != 1 || ids->ne[3] != 1 ||
+            (ids->ne[0] > 1 && ids->nb[0] != sizeof(int32_t))) {
+            return set_error(CBX_ERR_INVALID_ARG, f + ": ids must be contiguous 1-D I32");
+        }
+        return CBX_OK;
+    };
+    if (!src_b || !ids_b || !src2 || !ids2) {
+        return set_error(CBX_ERR_INVALID_ARG, f + ": src_b, ids_b, src2 and ids2 are required");
+    }
+    if ((src_a == nullptr) != (ids_a == nullptr)) return set_error(CBX_ERR_INVALID_ARG, f + ": src_a and ids_a go together");
+    if ((rc = seg(src_b, ids_b, "src_b", "ids_b")) || (rc = seg(src2, ids2, "src2", "ids2"))) return rc;
+    if (src_a && (rc = seg(src_a, ids_a, "src_a", "ids_a"))) return rc;
+    int64_t n_pre = 0;
+    if (prefix) {
+        if ((rc = validate(prefix, what, "prefix"))) return rc;
+        if (prefix->type != CBX_TYPE_F32 || prefix->ne[0] != D || prefix->ne[2] != 1 || prefix->ne[3] != 1) {
+            return set_error(CBX_ERR_INVALID_ARG, f + ": prefix must be F32 (y.ne0, n_prefix, 1, 1)");
+        }
+        n_pre = prefix->ne[1];
+    }
+    const int64_t n_tok = n_pre + (ids_a ? ids_a->ne[0] : 0) + ids_b->ne[0];
+    if (y->ne[1] != n_tok || ids2->ne[0] != n_tok) {
+        return set_error(CBX_ERR_INVALID_ARG, f + ": y.ne1 and ids2 must count the prefix rows plus both ids");
+    }
+    if (n_tok >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, f + ": too many rows");
+    if (h) {
+        if ((rc = validate(h, what, "h"))) return rc;
+        if (h->type != CBX_TYPE_F32 || !same_shape(h, y)) return set_error(CBX_ERR_INVALID_ARG, f + ": h must be F32 with y's shape");
+    }
+    if (!(eps >= 0.0f)) return set_error(CBX_ERR_INVALID_ARG, f + ": eps must be >= 0");
+    if ((rc = check_row_param(w, y, what, "w")) || (rc = check_row_param(b, y, what, "b"))) return rc;
+    if (n_tok == 0 || D == 0) return CBX_OK;
+    // outputs written by other workgroups must not alias what rows are read from
+    for (const cbx_tensor* in : {prefix, src_a, ids_a, src_b, ids_b, src2, ids2, w, b}) {
+        if (in && (overlaps(in, y) || (h && overlaps(in, h)))) {
+            return set_error(CBX_ERR_INVALID_ARG, f + ": h and y must not overlap the inputs");
+        }
+    }
+    if (h && overlaps(h, y)) return set_error(CBX_ERR_INVALID_ARG, f + ": h and y overlap");
+    return launch_embed_concat_norm(prefix, src_a, ids_a, src_b, ids_b, src2, ids2, w, b, eps, h, y, st,
+                                    reinterpret_cast<hipStream_t>(stream));
 }
 
 int cbx_cpy(const cbx_tensor* src, cbx_tensor* dst, cbx_stream stream) {

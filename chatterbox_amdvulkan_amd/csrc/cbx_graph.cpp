@@ -39,6 +39,83 @@ using namespace cbx;
 
 namespace {
 
+// The T3 input chain with the conditioning prefix, as t3.cpp:432-466 builds
+// it (in graph order):
+//   [get_rows(src_a, ids_a) [-> cast] -> concat(prefix, ., 1) ->]
+//   get_rows(src_b, ids_b) [-> cast] -> concat(seq, ., 1) ->
+//   get_rows(src2, ids2) [-> cast] -> add(seq, .) -> norm -> mul -> add
+// where the first concat's src0 is the prefix rows (the conditioning
+// encoder's output).  Without the prompt segment the text gather's concat
+// is the first one.  Parsed from node i on structure alone (ops, operand
+// links, concat along dim 1).
+struct ConcatT3 {
+    int32_t g_a = -1, g_b = -1, g_pos = -1;   // gather nodes (g_a -1: no prompt segment)
+    int32_t prefix = -1;                      // tensor holding the prefix rows
+    int32_t add = -1;                         // seq + positions; the LayerNorm is add + 1 .. add + 3
+    int32_t n_nodes = 0;
+    int32_t inner[8];                         // intermediates: each has exactly one reader in the chain
+    int32_t n_inner = 0;
+    int32_t cast[3];                          // the cast nodes (each must make F32)
+    int32_t n_cast = 0;
+};
+
+bool parse_concat_t3(const cbx_gnode* nd, int32_t n, int32_t i, ConcatT3* c) {
+    auto is = [&](int32_t k, int op) { return k >= 0 && k < n && nd[k].op == op; };
+    // a gather at k with an optional cast: the node after it, its value in *v
+    auto gather = [&](int32_t k, int32_t* v) -> int32_t {
+        if (!is(k, CBX_GOP_GET_ROWS)) return -1;
+        *v = nd[k].dst;
+        if (is(k + 1, CBX_GOP_CPY) && nd[k + 1].src[0] == *v) {
+            c->inner[c->n_inner++] = *v;
+            c->cast[c->n_cast++] = k + 1;
+            *v = nd[k + 1].dst;
+            return k + 2;
+        }
+        return k + 1;
+    };
+    auto concat_of = [&](int32_t k, int32_t src1) {
+        return is(k, CBX_GOP_CONCAT) && nd[k].src[1] == src1 && nd[k].iparam == 1;
+    };
+    c->n_inner = 0;
+    c->n_cast = 0;
+    int32_t v1 = -1;
+    const int32_t k1 = gather(i, &v1);
+    if (k1 < 0 || !concat_of(k1, v1)) return false;
+    c->prefix = nd[k1].src[0];
+    c->inner[c->n_inner++] = v1;
+    int32_t seq = nd[k1].dst;
+    int32_t v2 = -1;
+    const int32_t k2 = gather(k1 + 1, &v2);
+    if (k2 < 0) return false;
+    int32_t add, vpos;
+    if (concat_of(k2, v2) && nd[k2].src[0] == seq) {   // prompt, then text
+        c->g_a = i;
+        c->g_b = k1 + 1;
+        c->inner[c->n_inner++] = seq;
+        c->inner[c->n_inner++] = v2;
+        seq = nd[k2].dst;
+        c->g_pos = k2 + 1;
+        add = gather(k2 + 1, &vpos);
+    } else {                                          // text only
+        c->g_a = -1;
+        c->g_b = i;
+        c->g_pos = k1 + 1;
+        vpos = v2;
+        add = k2;
+    }
+    if (add < 0 || !is(add, CBX_GOP_ADD) || nd[add].src[0] != seq || nd[add].src[1] != vpos) return false;
+    c->inner[c->n_inner++] = seq;
+    c->inner[c->n_inner++] = vpos;
+    const int32_t h = nd[add].dst;
+    if (!is(add + 1, CBX_GOP_NORM) || nd[add + 1].src[0] != h || !is(add + 2, CBX_GOP_MUL) ||
+        nd[add + 2].src[0] != nd[add + 1].dst || !is(add + 3, CBX_GOP_ADD) || nd[add + 3].src[0] != nd[add + 2].dst) {
+        return false;
+    }
+    c->add = add;
+    c->n_nodes = add + 4 - i;
+    return true;
+}
+
 struct Planner {
     const cbx_tensor* t;
     int32_t n_t;
@@ -308,6 +385,22 @@ struct Planner {
                 return CBX_GL_VIEW;
             }
             case CBX_GOP_GET_ROWS: {
+                ConcatT3 c;
+                if (parse_concat_t3(nd, n, i, &c)) {
+                    bool ok = true;
+                    for (int32_t q = 0; q < c.n_inner; q++) ok = ok && internal(c.inner[q], 1);
+                    for (int32_t q = 0; q < c.n_cast; q++) ok = ok && t[nd[c.cast[q]].dst].type == CBX_TYPE_F32;
+                    const int32_t h = nd[c.add].dst, nn = nd[c.add + 1].dst, mm = nd[c.add + 2].dst;
+                    const int32_t P = c.prefix;
+                    ok = ok && internal(nn, 1) && internal(mm, 1) && valid_t(P) && valid_t(h) &&
+                         t[P].type == CBX_TYPE_F32 && t[P].ne[0] == t[h].ne[0] && t[P].ne[2] == 1 && t[P].ne[3] == 1 &&
+                         row_vec(nd[c.add + 2].src[1], h) && row_vec(nd[c.add + 3].src[1], h);
+                    if (ok) {
+                        if (internal(h, 1)) *flags = 1;   // h read only by the norm: not stored
+                        *len = c.n_nodes;
+                        return CBX_GL_GET_ROWS_CONCAT_ADD_LAYER_NORM;
+                    }
+                }
                 int32_t g1 = a.dst;
                 const int32_t j = i + 1 + cast_after(i + 1, &g1);
                 if (is(j, CBX_GOP_GET_ROWS)) {
@@ -578,8 +671,9 @@ constexpr int32_t kSpan[][2] = {
     {9, 17}, // CONV1D [snake | leaky] [bias] [residual]
     {7, 14}, // CONV_TRANSPOSE1D [snake | leaky] [bias]
     {12, 15}, // CAUSAL_CONV1D [mask] [bias]
+    {7, 12},  // GET_ROWS_CONCAT_ADD_LAYER_NORM [prompt gather, concat] [casts]
 };
-constexpr int32_t kLastKind = CBX_GL_CAUSAL_CONV1D;
+constexpr int32_t kLastKind = CBX_GL_GET_ROWS_CONCAT_ADD_LAYER_NORM;
 static_assert(sizeof(kSpan) / sizeof(kSpan[0]) == kLastKind + 1, "one span per launch kind");
 
 // Issues the entry point a launch maps to.  A launch is only read within
@@ -612,6 +706,19 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
             return cbx_get_rows_add_layer_norm(T(t, a.src[0]), T(t, a.src[1]), T(t, b.src[0]), T(t, b.src[1]),
                                                T(t, nd[k_add + 2].src[1]), T(t, nd[k_add + 3].src[1]),
                                                nd[k_add + 1].fparam, h, y, s);
+        }
+        case CBX_GL_GET_ROWS_CONCAT_ADD_LAYER_NORM: {
+            ConcatT3 c;
+            if (!parse_concat_t3(nd, n_nodes, f, &c) || c.n_nodes != l.n_nodes) break;
+            bool f32_casts = true;
+            for (int32_t q = 0; q < c.n_cast; q++) f32_casts = f32_casts && t[nd[c.cast[q]].dst].type == CBX_TYPE_F32;
+            if (!f32_casts) break;
+            const cbx_gnode &ga = nd[c.g_a < 0 ? c.g_b : c.g_a], &gb = nd[c.g_b], &gp = nd[c.g_pos];
+            cbx_tensor* h = (l.flags & 1) ? nullptr : const_cast<cbx_tensor*>(&t[nd[c.add].dst]);
+            return cbx_get_rows_concat_add_layer_norm(
+                T(t, c.prefix), c.g_a < 0 ? nullptr : T(t, ga.src[0]), c.g_a < 0 ? nullptr : T(t, ga.src[1]),
+                T(t, gb.src[0]), T(t, gb.src[1]), T(t, gp.src[0]), T(t, gp.src[1]), T(t, nd[c.add + 2].src[1]),
+                T(t, nd[c.add + 3].src[1]), nd[c.add + 1].fparam, h, y, s);
         }
         case CBX_GL_NORM:
             return cbx_norm(T(t, a.src[0]), a.fparam, y, s);

@@ -89,6 +89,13 @@ int launch_row_norm(int kind, const cbx_tensor* x, const cbx_tensor* w, const cb
 int launch_embed_norm(const cbx_tensor* src, const cbx_tensor* ids, const cbx_tensor* src2, const cbx_tensor* ids2,
                       const cbx_tensor* w, const cbx_tensor* b, float eps, cbx_tensor* h, cbx_tensor* y,
                       DeviceState* st, hipStream_t s);
+// The T3 input with the conditioning prefix: rows of concat(prefix,
+// get_rows(src_a, ids_a), get_rows(src_b, ids_b)) + get_rows(src2, ids2),
+// then LayerNorm (prefix and src_a/ids_a may be null).
+int launch_embed_concat_norm(const cbx_tensor* prefix, const cbx_tensor* src_a, const cbx_tensor* ids_a,
+                             const cbx_tensor* src_b, const cbx_tensor* ids_b, const cbx_tensor* src2,
+                             const cbx_tensor* ids2, const cbx_tensor* w, const cbx_tensor* b, float eps,
+                             cbx_tensor* h, cbx_tensor* y, DeviceState* st, hipStream_t s);
 int launch_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w,
                       const cbx_tensor* b, int act, cbx_tensor* y, DeviceState* st,
                       hipStream_t s);

@@ -178,21 +178,23 @@ template <typename TO, int NV, bool ACT>
 __device__ __forceinline__ void wave_row_store(const float4 (&v)[NV], int lane, int64_t ne0, float scale,
                                                const Affine<NV>& af, bool hw, bool hb, int act,
                                                const uint16_t* __restrict__ tab, char* yr) {
+    float4 o[NV];
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float t = get(v[k], e) * scale;
+            if (hw) t = t * get(af.w[k], e);
+            if (hb) t = t + get(af.b[k], e);
+            set(o[k], e, t);
+        }
+    }
+    // the activation's switch once for all of the lane's elements
+    if constexpr (ACT) apply_act_vec<NV>(act, o, tab, 0.0f);
 #pragma unroll
     for (int k = 0; k < NV; k++) {
         const int64_t j = (lane + 64 * k) * 4;
-        if (j < ne0) {
-            float4 o;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float t = get(v[k], e) * scale;
-                if (hw) t = t * get(af.w[k], e);
-                if (hb) t = t + get(af.b[k], e);
-                if constexpr (ACT) t = apply_act(act, t, tab, 0.0f);
-                set(o, e, t);
-            }
-            Stream<TO>::store4(yr + j * Elt<TO>::size, o);
-        }
+        if (j < ne0) Stream<TO>::store4(yr + j * Elt<TO>::size, o[k]);
     }
 }
 

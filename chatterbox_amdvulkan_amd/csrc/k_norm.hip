@@ -164,6 +164,78 @@ __global__ __launch_bounds__(64 * W) void k_embed_norm_flat(EmbedFlat a) {
 }
 
 // ---------------------------------------------------------------------------
+// The T3 input with the conditioning prefix (t3.cpp:432-466):
+//   seq = concat(prefix, cast(get_rows(src_a, ids_a)), cast(get_rows(src_b,
+//         ids_b))) along ne1; h = seq + cast(get_rows(src2, ids2)); LN(h).
+// Token t's first row comes from the segment that holds it: a prefix row
+// (F32, as the conditioning encoder wrote it), or a gathered table row;
+// then the embedding kernel's row body.  One workgroup per token, W waves.
+// ---------------------------------------------------------------------------
+
+struct ConcatSeg {
+    const char* base;      // table (gathered) or prefix rows
+    const int32_t* ids;    // nullptr: the prefix (row t - start of the segment)
+    int64_t nb1;
+    int32_t rows;          // table rows (id bound)
+    int32_t type;
+};
+
+struct EmbedConcat {
+    ConcatSeg seg[3];
+    int32_t end0, end1;    // the segments hold tokens [0, end0), [end0, end1), [end1, n_tok)
+    const char* src2;
+    const int32_t* ids2;
+    int64_t src2_nb1;
+    int32_t src2_rows;
+    const float* w;
+    const float* b;
+    char* h;
+    char* y;
+    int64_t h_nb1, y_nb1;
+    int32_t ne0;
+    float eps;
+    const uint16_t* tab;
+    uint32_t* err;
+};
+
+template <int TYPE, int TYPE2, int NV, int W>
+__device__ __forceinline__ void concat_row(const EmbedConcat& a, const char* s1, bool bad, const Affine<NV>& af,
+                                           char* hr, char* yr, int lane, double* lds) {
+    const int t = static_cast<int>(blockIdx.x);
+    const int32_t id2 = __builtin_amdgcn_readfirstlane(a.ids2[t]);
+    const bool bad2 = bad || id2 < 0 || id2 >= a.src2_rows;
+    const char* s2 = a.src2 + static_cast<int64_t>(bad2 ? 0 : id2) * a.src2_nb1;
+    embed_ln_row<TYPE, TYPE2, NV, W>(s1, s2, af, a.w != nullptr, a.b != nullptr, hr, yr, a.ne0, a.eps, lane, bad2,
+                                     a.err, lds);
+}
+
+template <int TYPE2, int NV, int W>
+__global__ __launch_bounds__(64 * W) void k_embed_concat_norm(EmbedConcat a) {
+    __shared__ double lds[2 * W];
+    const int lane = (threadIdx.x >> 6) * 64 * NV + (threadIdx.x & 63);
+    const int t = static_cast<int>(blockIdx.x);
+    const int k = t < a.end0 ? 0 : t < a.end1 ? 1 : 2;            // uniform
+    const ConcatSeg& sg = a.seg[k];
+    const int local = t - (k == 0 ? 0 : k == 1 ? a.end0 : a.end1);
+    int32_t row = local;
+    bool bad = false;
+    if (sg.ids) {
+        row = __builtin_amdgcn_readfirstlane(sg.ids[local]);
+        bad = row < 0 || row >= sg.rows;
+    }
+    const char* s1 = sg.base + static_cast<int64_t>(bad ? 0 : row) * sg.nb1;
+    char* yr = a.y + t * a.y_nb1;
+    char* hr = a.h ? a.h + t * a.h_nb1 : nullptr;
+    Affine<NV> af;
+    af.load_sel(a.w, a.b, reinterpret_cast<const float*>(a.tab), lane, a.ne0);
+    switch (sg.type) {   // uniform
+        case CBX_TYPE_F32: concat_row<CBX_TYPE_F32, TYPE2, NV, W>(a, s1, bad, af, hr, yr, lane, lds); break;
+        case CBX_TYPE_F16: concat_row<CBX_TYPE_F16, TYPE2, NV, W>(a, s1, bad, af, hr, yr, lane, lds); break;
+        default: concat_row<CBX_TYPE_Q8_0, TYPE2, NV, W>(a, s1, bad, af, hr, yr, lane, lds); break;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // workgroup-per-row fallback (ragged or unaligned rows, up to 8192 elements)
 // ---------------------------------------------------------------------------
 
@@ -500,6 +572,81 @@ bool table_vec_ok(const cbx_tensor* t) {
 }
 
 }  // namespace
+
+namespace {
+
+template <int TYPE2>
+void concat_go(const EmbedConcat& a, int n_tok, int nv, int w, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(n_tok)), block(64 * w);
+    switch (nv * 8 + w) {
+        case 1 * 8 + 1: hipLaunchKernelGGL((k_embed_concat_norm<TYPE2, 1, 1>), grid, block, 0, s, a); break;
+        case 2 * 8 + 1: hipLaunchKernelGGL((k_embed_concat_norm<TYPE2, 2, 1>), grid, block, 0, s, a); break;
+        case 2 * 8 + 2: hipLaunchKernelGGL((k_embed_concat_norm<TYPE2, 1, 2>), grid, block, 0, s, a); break;
+        case 4 * 8 + 1: hipLaunchKernelGGL((k_embed_concat_norm<TYPE2, 4, 1>), grid, block, 0, s, a); break;
+        case 4 * 8 + 2: hipLaunchKernelGGL((k_embed_concat_norm<TYPE2, 2, 2>), grid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL((k_embed_concat_norm<TYPE2, 1, 4>), grid, block, 0, s, a); break;
+    }
+}
+
+ConcatSeg concat_seg(const cbx_tensor* src, const cbx_tensor* ids, const cbx_tensor* fallback) {
+    ConcatSeg g;
+    const cbx_tensor* t = src ? src : fallback;
+    g.base = static_cast<const char*>(t->data);
+    g.ids = ids ? static_cast<const int32_t*>(ids->data) : nullptr;
+    g.nb1 = static_cast<int64_t>(t->nb[1]);
+    g.rows = static_cast<int32_t>(t->ne[1]);
+    g.type = src ? src->type : CBX_TYPE_F32;
+    return g;
+}
+
+}  // namespace
+
+int launch_embed_concat_norm(const cbx_tensor* prefix, const cbx_tensor* src_a, const cbx_tensor* ids_a,
+                             const cbx_tensor* src_b, const cbx_tensor* ids_b, const cbx_tensor* src2,
+                             const cbx_tensor* ids2, const cbx_tensor* w, const cbx_tensor* b, float eps,
+                             cbx_tensor* h, cbx_tensor* y, DeviceState* st, hipStream_t s) {
+    const int64_t ne0 = y->ne[0];
+    if (ne0 % 4 != 0 || ne0 > 1024 || !table_vec_ok(src_b) || (src_a && !table_vec_ok(src_a)) ||
+        !table_vec_ok(src2) || (prefix && !rows_aligned(prefix, 16)) || !rows_aligned(y, 16) ||
+        (h && !rows_aligned(h, 16)) || (w && reinterpret_cast<uintptr_t>(w->data) % 16) ||
+        (b && reinterpret_cast<uintptr_t>(b->data) % 16)) {
+        return set_error(CBX_ERR_UNSUPPORTED,
+                         "get_rows_concat_add_layer_norm: needs ne0 % 4 == 0, ne0 <= 1024, 16-byte aligned rows, w, "
+                         "b (Q8_0 tables: an even address)");
+    }
+    EmbedConcat a;
+    const int64_t n_pre = prefix ? prefix->ne[1] : 0, n_a = ids_a ? ids_a->ne[0] : 0, n_b = ids_b->ne[0];
+    const int64_t n_tok = n_pre + n_a + n_b;
+    a.seg[0] = concat_seg(prefix, nullptr, src_b);
+    a.seg[0].rows = static_cast<int32_t>(n_pre);
+    a.seg[1] = concat_seg(src_a, ids_a, src_b);
+    a.seg[2] = concat_seg(src_b, ids_b, src_b);
+    a.end0 = static_cast<int32_t>(n_pre);
+    a.end1 = static_cast<int32_t>(n_pre + n_a);
+    a.src2 = static_cast<const char*>(src2->data);
+    a.ids2 = static_cast<const int32_t*>(ids2->data);
+    a.src2_nb1 = static_cast<int64_t>(src2->nb[1]);
+    a.src2_rows = static_cast<int32_t>(src2->ne[1]);
+    a.w = w ? static_cast<const float*>(w->data) : nullptr;
+    a.b = b ? static_cast<const float*>(b->data) : nullptr;
+    a.h = h ? static_cast<char*>(h->data) : nullptr;
+    a.y = static_cast<char*>(y->data);
+    a.h_nb1 = h ? static_cast<int64_t>(h->nb[1]) : 0;
+    a.y_nb1 = static_cast<int64_t>(y->nb[1]);
+    a.ne0 = static_cast<int32_t>(ne0);
+    a.eps = eps;
+    a.tab = st->gelu_table;
+    a.err = st->err_word;
+    const int nv = pow2_nv(cdiv(ne0, 256));
+    int wr = 1;
+    while (wr < 4 && wr < nv && n_tok * wr < int64_t{8} * st->n_cu) wr *= 2;
+    switch (src2->type) {
+        case CBX_TYPE_F32: concat_go<CBX_TYPE_F32>(a, static_cast<int>(n_tok), nv, wr, s); break;
+        case CBX_TYPE_F16: concat_go<CBX_TYPE_F16>(a, static_cast<int>(n_tok), nv, wr, s); break;
+        default: concat_go<CBX_TYPE_Q8_0>(a, static_cast<int>(n_tok), nv, wr, s); break;
+    }
+    return check_launch("get_rows_concat_add_layer_norm");
+}
 
 int launch_embed_norm(const cbx_tensor* src, const cbx_tensor* ids, const cbx_tensor* src2, const cbx_tensor* ids2,
                       const cbx_tensor* w, const cbx_tensor* b, float eps, cbx_tensor* h, cbx_tensor* y,

@@ -115,6 +115,28 @@ int cbx_get_rows_add_layer_norm(const cbx_tensor* src, const cbx_tensor* ids,
                                 float eps, cbx_tensor* h, cbx_tensor* y,
                                 cbx_stream stream);
 
+/* The T3 input when the sequence starts with the conditioning prefix
+ * (t3.cpp:432-466), in one pass:
+ *   seq = ggml_concat(ggml_concat(prefix, cast(get_rows(src_a, ids_a)), 1),
+ *                     cast(get_rows(src_b, ids_b)), 1)
+ *   h   = ggml_add(seq, cast(get_rows(src2, ids2)))
+ *   y   = layer_norm(h, w, b, eps)
+ * prefix: F32 (D, n_prefix, 1, 1) rows already computed (the conditioning
+ * encoder's output, t3.cpp:434-436), or NULL; src_a/ids_a (the prompt's
+ * speech tokens, t3.cpp:439-442) may be NULL; src_b/ids_b (the text tokens,
+ * t3.cpp:445-448) and src2/ids2 (positions, :452-454) are required.
+ * Tables: 2-D F32/F16/Q8_0 with ne0 = D; ids: contiguous 1-D I32; y (and h,
+ * stored when non-NULL): F32 (D, N, 1, 1) with N = n_prefix + len(ids_a) +
+ * len(ids_b) = len(ids2).  D % 4 == 0, D <= 1024, 16-byte aligned rows.
+ * Out-of-range ids: as cbx_get_rows_add_layer_norm.                        */
+int cbx_get_rows_concat_add_layer_norm(const cbx_tensor* prefix,
+                                       const cbx_tensor* src_a, const cbx_tensor* ids_a,
+                                       const cbx_tensor* src_b, const cbx_tensor* ids_b,
+                                       const cbx_tensor* src2, const cbx_tensor* ids2,
+                                       const cbx_tensor* w, const cbx_tensor* b,
+                                       float eps, cbx_tensor* h, cbx_tensor* y,
+                                       cbx_stream stream);
+
 /* ggml_cpy / ggml_cast between F32 and F16 (round to nearest even), same
  * shape (t3.cpp:441,447,454).                                              */
 int cbx_cpy(const cbx_tensor* src, cbx_tensor* dst, cbx_stream stream);
@@ -513,7 +535,13 @@ int cbx_run_ops(const cbx_op* ops, int n_ops, cbx_stream stream);
  *   VIEW (transpose) -> CPY (cont) -> VIEW (its first K-1 frames) -> CPY
  *   -> SCALE (0) -> CONCAT (zeros, cont; dim 0) -> IM2COL (1, 0, 1) ->
  *   VIEW (2-D) -> VIEW (weight 2-D) -> MUL_MAT [-> VIEW (bias) -> ADD] ->
- *   VIEW (transpose) -> CPY (cont)                                          */
+ *   VIEW (transpose) -> CPY (cont)
+ * The T3 input with the conditioning prefix (t3.cpp:432-466) runs as one
+ * cbx_get_rows_concat_add_layer_norm call:
+ *   [GET_ROWS (prompt) [-> CPY] -> CONCAT (prefix, ., dim 1) ->] GET_ROWS
+ *   (text) [-> CPY] -> CONCAT (., ., dim 1) -> GET_ROWS (positions)
+ *   [-> CPY] -> ADD -> NORM -> MUL -> ADD
+ * (without the prompt segment the text gather's CONCAT takes the prefix).  */
 typedef enum cbx_gop {
     CBX_GOP_VIEW          = 0,  /* dst describes src0's memory                       */
     CBX_GOP_GET_ROWS      = 1,  /* src0 table, src1 ids I32                           */
@@ -573,6 +601,9 @@ typedef enum cbx_glaunch_kind {
     CBX_GL_CONV1D,            /* [snake | leaky_relu ->] conv1d chain [-> add(x, .)] */
     CBX_GL_CONV_TRANSPOSE1D,  /* [snake | leaky_relu ->] transposed conv chain  */
     CBX_GL_CAUSAL_CONV1D,     /* [mul(x, mask (1, T)) ->] causal conv chain     */
+    CBX_GL_GET_ROWS_CONCAT_ADD_LAYER_NORM, /* [get_rows [-> cast] -> concat(prefix, .) ->]
+                                 get_rows [-> cast] -> concat -> get_rows [-> cast]
+                                 -> add -> norm -> mul -> add (t3.cpp:432-466)   */
 } cbx_glaunch_kind;
 
 typedef struct cbx_glaunch {

@@ -68,6 +68,90 @@ def test_t3_input_embedding(cbx, oracle, keep_h):
         assert np.isnan(host(buf[4])).all(), "h was not asked for and stays unwritten"
 
 
+@pytest.mark.parametrize("prompt,text_q8,keep_h", [(True, False, True), (True, True, False), (False, False, True)])
+def test_t3_input_with_conditioning_prefix(cbx, oracle, prompt, text_q8, keep_h):
+    """t3.cpp:432-466: the conditioning row (the encoder's output, given),
+    the prompt's speech-token rows and the text-token rows concatenated,
+    plus the position rows, then LN-1 -- the reference's node list, one
+    launch, against the oracle evaluating every node (concat is a copy)."""
+    D, Lp, Lt = 1024, 150, 40
+    n = 1 + (Lp if prompt else 0) + Lt
+    cond = W.normal(W.seed_of(7, 10), (1, D), 0.0, 0.5)
+    speech = W.normal(W.seed_of(7, 11), (900, D), 0.0, 0.02).astype(np.float16)
+    text = W.normal(W.seed_of(7, 12), (2000, D), 0.0, 0.02)
+    text_dev = W.quantize_q8_0(text) if text_q8 else text.astype(np.float16)
+    posT = W.normal(W.seed_of(7, 13), (600, D), 0.0, 0.02).astype(np.float16)
+    prompt_ids = W.randint(W.seed_of(7, 14), (Lp,), 0, 900)
+    toks = W.randint(W.seed_of(7, 15), (Lt,), 0, 2000)
+    positions = np.arange(n, dtype=np.int32)
+    w = W.normal(W.seed_of(7, 16), (D,), 1.0, 0.02)
+    b = W.normal(W.seed_of(7, 17), (D,), 0.0, 0.02)
+
+    g = cbx.Graph()
+    tc = g.tensor(dev(cond))
+    tsp, ttx = g.tensor(dev(speech)), g.tensor(dev(text_dev), cbx.Q8_0 if text_q8 else None)
+    tps = g.tensor(dev(posT))
+    tpi, ttk, tpo = g.tensor(dev(prompt_ids)), g.tensor(dev(toks)), g.tensor(dev(positions))
+    tw, tb = g.tensor(dev(w)), g.tensor(dev(b))
+    outs = {}
+
+    def node(op, shape, src, **kw):
+        buf = empty(*shape)
+        t = g.tensor(buf)
+        outs[t] = buf
+        g.node(op, t, src, **kw)
+        return t
+
+    seq = tc
+    if prompt:
+        gp = node(cbx.GOP_GET_ROWS, (Lp, D), (tsp, tpi))
+        cp = node(cbx.GOP_CPY, (Lp, D), (gp,))
+        seq = node(cbx.GOP_CONCAT, (1 + Lp, D), (seq, cp), iparam=1)
+    gt = node(cbx.GOP_GET_ROWS, (Lt, D), (ttx, ttk))
+    ct = node(cbx.GOP_CPY, (Lt, D), (gt,))
+    seq = node(cbx.GOP_CONCAT, (n, D), (seq, ct), iparam=1)
+    gq = node(cbx.GOP_GET_ROWS, (n, D), (tps, tpo))
+    cq = node(cbx.GOP_CPY, (n, D), (gq,))
+    h = node(cbx.GOP_ADD, (n, D), (seq, cq))
+    nn = node(cbx.GOP_NORM, (n, D), (h,), fparam=1e-5)
+    mm = node(cbx.GOP_MUL, (n, D), (nn, tw))
+    y = node(cbx.GOP_ADD, (n, D), (mm, tb))
+    keep = [h, y] if keep_h else [y]
+    assert g.compute(keep) == 1
+    assert g.plan(keep)[0][0] == cbx.GL_GET_ROWS_CONCAT_ADD_LAYER_NORM
+
+    parts = [cond]
+    if prompt:
+        parts.append(oracle.cpy(oracle.get_rows(speech, prompt_ids), np.float32))
+    parts.append(oracle.cpy(oracle.get_rows(text_dev, toks, q8_0=text_q8), np.float32))
+    h_ref = oracle.add(np.concatenate(parts, axis=0), oracle.cpy(oracle.get_rows(posT, positions), np.float32))
+    y_ref = oracle.add(oracle.mul(oracle.norm(h_ref, 1e-5), w), b)
+    assert_bitexact(host(outs[y]), y_ref, "LN(concat + pos)")
+    if keep_h:
+        assert_bitexact(host(outs[h]), h_ref, "h kept")
+    else:
+        assert np.isnan(host(outs[h])).all(), "h was not asked for and stays unwritten"
+
+
+def test_t3_input_with_prefix_bad_id(cbx):
+    """An out-of-range text id zeroes that row and raises the device error
+    bit; the other rows are unaffected."""
+    import ctypes
+    D = 256
+    cond = dev(W.normal(3, (2, D)))
+    text = dev(W.normal(4, (50, D)))
+    posT = dev(W.normal(5, (60, D)))
+    toks = dev(np.array([1, 2, 77, 3], dtype=np.int32))
+    pos = dev(np.arange(6, dtype=np.int32))
+    h, y = cbx.get_rows_concat_add_layer_norm(cond, None, None, text, toks, posT, pos, None, None, 1e-5)
+    flags = ctypes.c_uint32(0)
+    assert cbx.load().cbx_device_errors(0, ctypes.byref(flags), 1) == cbx.OK
+    assert flags.value & 1
+    yh = host(y)
+    assert not yh[4].any() and not host(h)[4].any()
+    assert np.abs(yh[[0, 1, 2, 3, 5]]).sum() > 0
+
+
 def test_causal_block_layer_norm_mish(cbx, oracle):
     T, Ch = 300, 256
     x = W.normal(W.seed_of(8, 0), (T, Ch), 0.1, 1.5)

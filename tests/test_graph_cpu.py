@@ -48,6 +48,95 @@ def test_t3_input_chain_is_one_launch():
     assert plan[1] == (C.GL_UNSUPPORTED, 8, 1, 0)               # a plain residual add is not this library's
 
 
+def t3_input_concat(g: C.Graph, prompt=True, casts=True, D=64, n_pre=1, n_a=5, n_b=7, cast_type=torch.float32,
+                    dim=1):
+    """t3.cpp:432-466 with the conditioning prefix: [get_rows(speech, prompt)
+    -> cast -> concat(prefix, ., 1) ->] get_rows(text, tokens) -> cast ->
+    concat -> get_rows(pos) -> cast -> add -> norm -> mul -> add, then a
+    node that reads h again (the block's residual).  Returns the tensors."""
+    n = n_pre + (n_a if prompt else 0) + n_b
+    pre = g.tensor(f32(n_pre, D))
+    sp, tx, ps = g.tensor(f32(30, D)), g.tensor(f32(40, D)), g.tensor(f32(50, D))
+    ia = g.tensor(torch.zeros(n_a, dtype=torch.int32))
+    ib = g.tensor(torch.zeros(n_b, dtype=torch.int32))
+    ip = g.tensor(torch.zeros(n, dtype=torch.int32))
+    w, b = g.tensor(f32(D)), g.tensor(f32(D))
+
+    def gather(table, ids, rows):
+        v = g.tensor(f32(rows, D))
+        g.node(C.GOP_GET_ROWS, v, (table, ids))
+        if casts:
+            c = g.tensor(torch.zeros(rows, D, dtype=cast_type))
+            g.node(C.GOP_CPY, c, (v,))
+            v = c
+        return v
+
+    seq, rows = pre, n_pre
+    if prompt:
+        v = gather(sp, ia, n_a)
+        rows += n_a
+        cat = g.tensor(f32(rows, D))
+        g.node(C.GOP_CONCAT, cat, (seq, v), iparam=dim)
+        seq = cat
+    v = gather(tx, ib, n_b)
+    rows += n_b
+    cat = g.tensor(f32(rows, D))
+    g.node(C.GOP_CONCAT, cat, (seq, v), iparam=dim)
+    seq = cat
+    pv = gather(ps, ip, n)
+    t = [g.tensor(f32(n, D)) for _ in range(5)]
+    g.node(C.GOP_ADD, t[0], (seq, pv))              # h
+    g.node(C.GOP_NORM, t[1], (t[0],), fparam=1e-5)
+    g.node(C.GOP_MUL, t[2], (t[1], w))
+    g.node(C.GOP_ADD, t[3], (t[2], b))
+    g.node(C.GOP_ADD, t[4], (t[3], t[0]))          # stands for the residual read of h
+    return t
+
+
+@pytest.mark.parametrize("prompt,casts,n_nodes", [(True, True, 12), (True, False, 9), (False, True, 9),
+                                                  (False, False, 7)])
+def test_t3_input_with_conditioning_prefix_is_one_launch(prompt, casts, n_nodes):
+    g = C.Graph()
+    t3_input_concat(g, prompt=prompt, casts=casts)
+    plan = g.plan()
+    assert plan[0] == (C.GL_GET_ROWS_CONCAT_ADD_LAYER_NORM, 0, n_nodes, 0)   # h is read later: stored
+    assert plan[1] == (C.GL_UNSUPPORTED, n_nodes, 1, 0)                      # the plain residual add
+
+
+def test_t3_input_with_prefix_unread_sum_and_refusals():
+    # h read only by the norm: not stored (flag 1)
+    g = C.Graph()
+    t = t3_input_concat(g)
+    g.nodes.pop()
+    assert g.plan() == [(C.GL_GET_ROWS_CONCAT_ADD_LAYER_NORM, 0, 12, 1)]
+    # a cast to F16 rounds: not this chain
+    g = C.Graph()
+    t3_input_concat(g, cast_type=torch.float16)
+    assert g.plan()[0][0] != C.GL_GET_ROWS_CONCAT_ADD_LAYER_NORM
+    # concat along another dimension: not this chain
+    g = C.Graph()
+    t3_input_concat(g, dim=0)
+    assert g.plan()[0][0] != C.GL_GET_ROWS_CONCAT_ADD_LAYER_NORM
+    # an intermediate kept by the caller: not fused
+    g = C.Graph()
+    t = t3_input_concat(g)
+    concat_out = g.nodes[2].dst
+    assert g.nodes[2].op == C.GOP_CONCAT
+    assert g.plan(keep=[concat_out])[0][0] != C.GL_GET_ROWS_CONCAT_ADD_LAYER_NORM
+
+
+def test_t3_input_with_prefix_hand_made_launch_is_refused():
+    """A launch of this kind whose node count does not match the chain is
+    refused before anything runs (no device needed)."""
+    g = C.Graph()
+    t3_input_concat(g)
+    Tn, Nn, _ = g._arrays([])
+    bad = C.GLaunch(C.GL_GET_ROWS_CONCAT_ADD_LAYER_NORM, 0, 11, 0)
+    L = C.load()
+    assert L.cbx_graph_launch(Tn, len(g._descs), Nn, len(g.nodes), ctypes.byref(bad), None) == C.ERR_INVALID_ARG
+    assert "does not fit" in C.last_error()
+
+
 def test_t3_input_unread_sum_is_not_stored():
     g = C.Graph()
     t3_input(g, residual_read=False)
