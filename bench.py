@@ -51,6 +51,10 @@ def parse():
     ap.add_argument("--only", choices=["decode", "serving", "cfm", "hift", "softmax", "t3_block", "hift_conv",
                                        "copy"],
                     help="run one secondary workload alone and print its JSON (no headline line)")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print the markdown summary of two --pmc runs over --traffic-probe (no GPU)")
+    ap.add_argument("--stats-summary", nargs=3, metavar=("STATS_DIR", "TITLE", "COMMAND"),
+                    help="print the markdown summary of a --kernel-trace --stats run (no GPU)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the launches used by the FETCH_SIZE/WRITE_SIZE counter runs")
     return ap.parse_args()
@@ -794,7 +798,7 @@ def bench_copy_ceiling(C, torch, sizes, reps=400):
     return out
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_fused_layer_ops.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_per_kernel_all_workloads.md")
 
 
 def recorded_traffic(key):
@@ -810,70 +814,241 @@ def recorded_traffic(key):
     return None
 
 
+COPY_PROBE_ELEMS = 16 << 20   # the calibration copy: 64 MiB in, 64 MiB out
+
+
+STATS_FILE = os.path.join(ROOT, "profiles", "prefill_chain_gelu_embedln_kernel_stats.md")
+
+
+def recorded_kernel_avg_us(kernel):
+    """A kernel's average duration (us) in the committed rocprofv3 kernel
+    stats of the headline workload, or None."""
+    try:
+        with open(STATS_FILE) as f:
+            for line in f:
+                if line.startswith(f"| `{kernel}` |"):
+                    return float(line.split("|")[3])
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
+
+
+def traffic_groups(W):
+    """The counter probe's launch groups in launch order: (label, algorithmic
+    bytes per launch, launches).  Each group runs on its own buffer sets
+    (one per launch; two for the 983 MB vocoder shape)."""
+    nb, cb, bb, sb = W.prefill_bytes(), W.cfm_bytes(), W.t3_block_bytes(), W.serving_bytes()
+    hift = {}
+    for (B, Ch, T) in (W.HIFT_SHAPES[0], W.HIFT_SHAPES[-1]):
+        hift[(B, Ch, T)] = 8 * B * Ch * T
+    (s0, s1) = W.HIFT_SHAPES[0], W.HIFT_SHAPES[-1]
+    return [
+        ("copy_64MiB", 2 * 4 * COPY_PROBE_ELEMS, 4),
+        ("copy_4KiB", 2 * 4096, 8),
+        ("gelu_512x4096", nb["gelu"], 8),
+        ("embed_layer_norm_512x1024", nb["embed_layer_norm"], 8),
+        ("group_norm_mish_2x256x500", cb["group_norm_mish_256"], 8),
+        ("group_norm_mish_2x512x500", cb["group_norm_mish_512"], 8),
+        ("layer_norm_rope_2x500x512", cb["layer_norm_rope"], 8),
+        ("residual_join_layer_norm_512x1024", bb["residual_ln2"], 8),
+        ("bias_gelu_512x4096", bb["fc_bias_gelu"], 8),
+        ("snake_1x256x6000", hift[s0] + 8 * s0[1], 8),
+        ("leaky_relu_1x256x6000", hift[s0], 8),
+        ("snake_16x64x120000", hift[s1] + 8 * s1[1], 2),
+        ("leaky_relu_16x64x120000", hift[s1], 2),
+        ("rms_norm_64x1024_f16", sb["rms_norm_mul"], 8),
+        ("rope_64x16x64_f16", sb["rope_qk"] // 2, 8),
+        ("swiglu_64x4096_f16", sb["swiglu"], 8),
+        ("get_rows_q8_0_64x1024", sb["get_rows_q8_0"], 8),
+        ("serving_step_one_launch", sum(sb.values()), 8),
+        ("causal_conv1d_2x256x500", 4 * 2 * 500 * (256 + 256) + 2 * 256 * 256 * 3 + 4 * 256 + 4 * 500, 8),
+    ]
+
+
 def traffic_probe(C, W, torch):
-    """A few launches for counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE):
-    a plain f32 copy of 64 MiB (the calibration kernel of known size), then
-    GELU [512,4096], the fused embedding + LayerNorm, GroupNorm+Mish
-    [2,512,500], LayerNorm+RoPE [2,500,512], the residual join + LayerNorm
-    [512,1024] and bias + GELU [512,4096], each on 8 rotating buffer sets.
-    Prints the algorithmic bytes of each."""
-    x = torch.empty(16 << 20, dtype=torch.float32, device="cuda").uniform_()
-    ys = [torch.empty_like(x) for _ in range(4)]
+    """The launches of the FETCH_SIZE / WRITE_SIZE counter runs: every buffer
+    is made first, then the groups of traffic_groups() run in order, each
+    kernel on its own buffer sets, with a device synchronisation between
+    groups (so the profiler's dispatch order is the groups' order)."""
     L = C.load()
-    s = cur_stream(torch)
-    dx = C.ctypes.byref(C.desc(x))
-    for y in ys:
-        check_rc(C, L.cbx_cpy(dx, C.ctypes.byref(C.desc(y)), s))
-    torch.cuda.synchronize()
-    inp = W.prefill_inputs()
-    sets = [PrefillSet(C, W, torch, inp) for _ in range(8)]
-    for st in sets:
-        check_rc(C, st.gelu(s))
-    torch.cuda.synchronize()
-    for st in sets:
-        check_rc(C, st.embed_layer_norm(s))
-    torch.cuda.synchronize()
     d = dev_of(torch)
+    s = cur_stream(torch)
+    R = lambda t, ty=None: C.ctypes.byref(C.desc(t, ty))  # noqa: E731
+    groups = {}
+    x = torch.empty(COPY_PROBE_ELEMS, dtype=torch.float32, device="cuda").uniform_()
+    ys = [torch.empty_like(x) for _ in range(4)]
+    groups["copy_64MiB"] = [(lambda y: lambda: L.cbx_cpy(R(x), R(y), s))(y) for y in ys]
+    small = [(torch.empty(1024, dtype=torch.float32, device="cuda").uniform_(),
+              torch.empty(1024, dtype=torch.float32, device="cuda")) for _ in range(8)]
+    groups["copy_4KiB"] = [(lambda a_, b_: lambda: L.cbx_cpy(R(a_), R(b_), s))(a_, b_) for a_, b_ in small]
+    inp = W.prefill_inputs()
+    pre = [PrefillSet(C, W, torch, inp) for _ in range(8)]
+    groups["gelu_512x4096"] = [(lambda st_: lambda: st_.gelu(s))(st_) for st_ in pre]
+    groups["embed_layer_norm_512x1024"] = [(lambda st_: lambda: st_.embed_layer_norm(s))(st_) for st_ in pre]
     cfm = W.cfm_inputs()
     cache = C.RopeCache(W.HEAD_DIM, mode=2, n_ctx_orig=2048, n_pos=2048)
-    cfm_sets = []
+    ws = C.GroupNormWorkspace()
+    cs = []
     for _ in range(8):
         t = {k: d(v) for k, v in cfm.items()}
-        t["y512"], t["ya"] = torch.empty_like(t["x512"]), torch.empty_like(t["xa"])
-        cfm_sets.append((t, {k: C.ctypes.byref(C.desc(v)) for k, v in t.items()}))
-    for _, r in cfm_sets:
-        check_rc(C, L.cbx_group_norm(r["x512"], W.CFM_GROUPS, 1e-5, r["w512"], r["b512"], C.MISH, r["y512"], s))
-    torch.cuda.synchronize()
-    for _, r in cfm_sets:
-        check_rc(C, L.cbx_layer_norm_rope(r["xa"], r["wa"], r["ba"], 1e-5, W.HEAD_DIM, r["pos"], cache.handle,
-                                          r["ya"], s))
-    torch.cuda.synchronize()
-    cache.close()
+        for k in ("x256", "x512", "xa"):
+            t["y" + k[1:]] = torch.empty_like(t[k])
+        cs.append({k: R(v) for k, v in t.items()} | {"_t": t})
+    for key in ("256", "512"):
+        groups[f"group_norm_mish_2x{key}x500"] = [
+            (lambda r, key=key: lambda: L.cbx_group_norm_ws(r["x" + key], W.CFM_GROUPS, 1e-5, r["w" + key],
+                                                            r["b" + key], C.MISH, r["y" + key], ws.handle, s))(r)
+            for r in cs]
+    groups["layer_norm_rope_2x500x512"] = [
+        (lambda r: lambda: L.cbx_layer_norm_rope(r["xa"], r["wa"], r["ba"], 1e-5, W.HEAD_DIM, r["pos"], cache.handle,
+                                                 r["ya"], s))(r) for r in cs]
     blk = W.t3_block_inputs()
     N, D, F = W.N_PREFILL, W.D_MODEL, W.D_FF
-    blk_sets = []
+    bs = []
     for _ in range(8):
         t = {k: d(blk[k]) for k in ("attn_mm", "h", "out_b", "ln2_w", "ln2_b", "fc_mm", "fc_b")}
         t["res"], t["ln2"] = torch.empty((N, D), device="cuda"), torch.empty((N, D), device="cuda")
         t["gelu"] = torch.empty((N, F), device="cuda")
-        blk_sets.append({k: C.ctypes.byref(C.desc(v)) for k, v in t.items()})
-    for r in blk_sets:
-        check_rc(C, L.cbx_add_layer_norm(r["attn_mm"], r["out_b"], r["h"], r["ln2_w"], r["ln2_b"], 1e-5, -1,
-                                         r["res"], r["ln2"], s))
+        bs.append({k: R(v) for k, v in t.items()} | {"_t": t})
+    groups["residual_join_layer_norm_512x1024"] = [
+        (lambda r: lambda: L.cbx_add_layer_norm(r["attn_mm"], r["out_b"], r["h"], r["ln2_w"], r["ln2_b"], 1e-5, -1,
+                                                r["res"], r["ln2"], s))(r) for r in bs]
+    groups["bias_gelu_512x4096"] = [(lambda r: lambda: L.cbx_bias_act(C.GELU, r["fc_mm"], r["fc_b"], r["gelu"], s))(r)
+                                    for r in bs]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(W.seed_of(4, 0))
+    hb = []
+    for (B, Ch, T), n_sets in ((W.HIFT_SHAPES[0], 8), (W.HIFT_SHAPES[-1], 2)):
+        a, ai = (d(v) for v in W.snake_alpha(Ch))
+        sets_ = []
+        for _ in range(n_sets):
+            xx = torch.empty((B, T, Ch), dtype=torch.float32, device="cuda").normal_(generator=gen)
+            sets_.append((xx, torch.empty_like(xx)))
+        hb.append((a, ai, sets_))
+        tag = f"{B}x{Ch}x{T}"
+        groups[f"snake_{tag}"] = [(lambda xx, yy, a=a, ai=ai: lambda: L.cbx_snake(R(xx), R(a), R(ai), R(yy), s))(xx, yy)
+                                  for xx, yy in sets_]
+        groups[f"leaky_relu_{tag}"] = [(lambda xx, yy: lambda: L.cbx_leaky_relu(R(xx), 0.1, R(yy), s))(xx, yy)
+                                       for xx, yy in sets_]
+    sv_base = {k: d(v) for k, v in W.serving_inputs().items()}
+    sv = []
+    for _ in range(8):
+        t = {k: v.clone() for k, v in sv_base.items()}
+        t["y"], t["qo"], t["ko"] = torch.empty_like(t["x"]), torch.empty_like(t["q"]), torch.empty_like(t["k"])
+        t["h"] = torch.empty_like(t["gate"])
+        t["emb"] = torch.empty((W.N_STREAMS, W.D_MODEL), dtype=torch.float32, device="cuda")
+        r = {k: R(v, C.Q8_0 if k == "tab" else None) for k, v in t.items()}
+        one = C.OpBatch([C.Op(C.OP_RMS_NORM, [t["x"], t["g"]], [t["y"]], eps=1e-5),
+                         C.Op(C.OP_ROPE, [t["q"], t["pos"]], [t["qo"]], rope=cache),
+                         C.Op(C.OP_ROPE, [t["k"], t["pos"]], [t["ko"]], rope=cache),
+                         C.Op(C.OP_SWIGLU, [t["gate"], t["up"]], [t["h"]]),
+                         C.Op(C.OP_GET_ROWS, [t["tab"], t["ids"]], [t["emb"]], q8=[0])])
+        sv.append((t, r, one))
+    groups["rms_norm_64x1024_f16"] = [(lambda r: lambda: L.cbx_rms_norm_mul(r["x"], r["g"], 1e-5, r["y"], s))(r)
+                                      for _, r, _ in sv]
+    groups["rope_64x16x64_f16"] = [(lambda r: lambda: L.cbx_rope_ext(r["q"], r["pos"], cache.handle, r["qo"], s))(r)
+                                   for _, r, _ in sv]
+    groups["swiglu_64x4096_f16"] = [(lambda r: lambda: L.cbx_swiglu(r["gate"], r["up"], r["h"], s))(r) for _, r, _ in sv]
+    groups["get_rows_q8_0_64x1024"] = [(lambda r: lambda: L.cbx_get_rows(r["tab"], r["ids"], r["emb"], s))(r)
+                                       for _, r, _ in sv]
+    groups["serving_step_one_launch"] = [(lambda one: lambda: L.cbx_run_ops(one.arr, one.n, s))(one) for _, _, one in sv]
+    cc = []
+    wt = C.Conv1dWeights(d(W.normal(W.seed_of(8, 2002 + 256), (256, 256, 3), 0.0, 1.0 / np.sqrt(256 * 3))))
+    mask = torch.ones(500, dtype=torch.float32, device="cuda")
+    bias = d(W.normal(W.seed_of(8, 2001 + 256), (256,), 0.0, 0.1))
+    for _ in range(8):
+        xx = d(W.normal(W.seed_of(8, 2000 + 256), (2, 500, 256)))
+        cc.append((xx, torch.empty_like(xx)))
+    groups["causal_conv1d_2x256x500"] = [
+        (lambda xx, yy: lambda: L.cbx_causal_conv1d(R(xx), wt.handle, R(mask), R(bias), R(yy), s))(xx, yy)
+        for xx, yy in cc]
     torch.cuda.synchronize()
-    for r in blk_sets:
-        check_rc(C, L.cbx_bias_act(C.GELU, r["fc_mm"], r["fc_b"], r["gelu"], s))
-    torch.cuda.synchronize()
-    nb = W.prefill_bytes()
-    cb = W.cfm_bytes()
-    bb = W.t3_block_bytes()
-    print(json.dumps({"copy_bytes_read": x.numel() * 4, "copy_bytes_written": x.numel() * 4,
-                      "gelu_bytes_read": nb["gelu"] // 2, "gelu_bytes_written": nb["gelu"] // 2,
-                      "embed_layer_norm_bytes": nb["embed_layer_norm"],
-                      "group_norm_mish_512_bytes": cb["group_norm_mish_512"],
-                      "layer_norm_rope_bytes": cb["layer_norm_rope"],
-                      "residual_join_layer_norm_bytes": bb["residual_ln2"],
-                      "bias_gelu_bytes": bb["fc_bias_gelu"]}), flush=True)
+    for label, nbytes, n in traffic_groups(W):
+        fns = groups[label]
+        assert len(fns) == n, label
+        for fn in fns:
+            check_rc(C, fn())
+        torch.cuda.synchronize()
+        log(f"traffic probe: {label} x{n}")
+    cache.close()
+    ws.close()
+    wt.close()
+    print(json.dumps({"groups": [[lb, nbytes, n] for lb, nbytes, n in traffic_groups(W)]}), flush=True)
+
+
+def _pmc_rows(d):
+    """(kernel name, counter value) of every dispatch of a rocprofv3 --pmc
+    csv run, in dispatch order."""
+    import csv
+    import glob
+    f = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))[0]
+    rows = list(csv.DictReader(open(f)))
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    return [(r["Kernel_Name"], float(r["Counter_Value"])) for r in rows if "cbx::" in r["Kernel_Name"]]
+
+
+def short_kernel(name):
+    import re
+    n = re.sub(r"\(anonymous namespace\)::", "", name)
+    n = re.sub(r"^void ", "", n)
+    return re.sub(r"\((cbx::|float const|char const|unsigned|cbx|long).*$", "", n)
+
+
+def traffic_summary(W, fetch_dir, write_dir):
+    """Markdown of two counter runs over --traffic-probe: each group's
+    dispatches (our kernels, in dispatch order) matched to traffic_groups(),
+    FETCH_SIZE and WRITE_SIZE scaled by what they read for the copy of known
+    size."""
+    F, Wr = _pmc_rows(fetch_dir), _pmc_rows(write_dir)
+    groups = traffic_groups(W)
+    total = sum(n for _, _, n in groups)
+    if len(F) != total or len(Wr) != total:
+        raise SystemExit(f"traffic summary: {len(F)} / {len(Wr)} dispatches of ours, {total} expected")
+    per, i = [], 0
+    for label, nbytes, n in groups:
+        fs = sorted(v for _, v in F[i:i + n])
+        ws_ = sorted(v for _, v in Wr[i:i + n])
+        per.append((label, nbytes, n, short_kernel(F[i][0]), fs[len(fs) // 2], ws_[len(ws_) // 2]))
+        i += n
+    copy_kib = 4 * COPY_PROBE_ELEMS / 1024
+    f_scale, w_scale = copy_kib / per[0][4], copy_kib / per[0][5]
+    out = ["# HBM traffic per launch of every configuration's kernels (FETCH_SIZE, WRITE_SIZE)", "",
+           "Two `rocprofv3 --pmc` passes on one MI355X over the same probe (a 64 MiB f32 copy of known size, then",
+           "each kernel's launches on their own buffer sets; the groups are `traffic_groups()` in bench.py):", "",
+           "```", "cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT",
+           "timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch -o run -- "
+           "python -u bench.py --traffic-probe",
+           "timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write -o run -- "
+           "python -u bench.py --traffic-probe",
+           "python bench.py --traffic-summary gpurun_out/pmc_fetch gpurun_out/pmc_write", "```", "",
+           f"Calibration: the copy moves {copy_kib:.0f} KiB each way; FETCH_SIZE reads {per[0][4]:.1f} KiB for it "
+           f"and WRITE_SIZE {per[0][5]:.1f}, so reads are scaled by {f_scale:.4f} and writes by {w_scale:.4f}.", "",
+           "| workload | kernel | launches | FETCH_SIZE KiB | WRITE_SIZE KiB | algorithmic bytes | traffic bytes | ratio |",
+           "|---|---|---|---|---|---|---|---|"]
+    tail = []
+    for label, nbytes, n, kern, fv, wv in per[1:]:
+        traffic = (fv * f_scale + wv * w_scale) * 1024
+        out.append(f"| {label} | `{kern}` | {n} | {fv:.1f} | {wv:.1f} | {nbytes} | {traffic:.0f} | "
+                   f"{traffic / nbytes:.3f} |")
+        tail.append(f"traffic_bytes_per_launch {label}: {traffic:.0f}")
+    return "\n".join(out + [""] + tail) + "\n"
+
+
+def stats_summary(stats_dir, title, command):
+    """Markdown of a rocprofv3 --kernel-trace --stats run: our kernels'
+    calls and durations."""
+    import csv
+    import glob
+    f = sorted(glob.glob(os.path.join(stats_dir, "**", "*kernel_stats.csv"), recursive=True))[0]
+    rows = [r for r in csv.DictReader(open(f)) if "cbx::" in r["Name"]]
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    out = [f"# {title}", "", "Command (one MI355X):", "", "```", "cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT",
+           command, "```", "", "Kernels of libcbxops (rocprofv3 kernel stats; durations in microseconds):", "",
+           "| kernel | calls | average | min | max |", "|---|---|---|---|---|"]
+    for r in rows:
+        out.append(f"| `{short_kernel(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.3f} | "
+                   f"{float(r['MinNs']) / 1e3:.3f} | {float(r['MaxNs']) / 1e3:.3f} |")
+    return "\n".join(out) + "\n"
 
 
 def cpu_baseline(W, seconds):
@@ -992,10 +1167,17 @@ def main():
         print("bench.py measures one GPU: this op path has no cross-GPU exchange and runs on one "
               "device; --gpus above 1 is not supported.", file=sys.stderr)
         return 2
+    from chatterbox_amdvulkan_amd import workloads as W
+
+    if a.traffic_summary:
+        print(traffic_summary(W, *a.traffic_summary), end="")
+        return 0
+    if a.stats_summary:
+        print(stats_summary(*a.stats_summary), end="")
+        return 0
     import torch
 
     from chatterbox_amdvulkan_amd import cbxops as C
-    from chatterbox_amdvulkan_amd import workloads as W
 
     torch.cuda.set_device(0)
     C.init(0)
@@ -1055,6 +1237,7 @@ def main():
         details["hift_resblock_conv"] = bench_hift_conv(C, W, torch)
     k_ms = res["kernel_ms"]["gelu"]
     k_bytes = res["kernel_bytes"]["gelu"]
+    rp_us = recorded_kernel_avg_us("cbx::k_unary<float, 0>")
     achieved = k_bytes / (k_ms * 1e-3) / 1e9
     value = res["bytes_per_step"] / (res["ms_per_step"] * 1e-3) / 1e9
     out = {
@@ -1080,7 +1263,10 @@ def main():
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": recorded_traffic("gelu_512x4096"),
                      "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT),
-                     "launch_ms": k_ms, "algorithmic_bytes": k_bytes},
+                     "launch_ms": k_ms, "algorithmic_bytes": k_bytes,
+                     "rocprof_avg_us": rp_us,
+                     "frac_from_rocprof_avg": round(k_bytes / (rp_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4) if rp_us else None,
+                     "rocprof_source": os.path.relpath(STATS_FILE, ROOT)},
     }
     if "t3_decode" in details:
         dd = details["t3_decode"]
