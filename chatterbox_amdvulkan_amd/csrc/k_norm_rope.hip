@@ -70,8 +70,12 @@ __device__ __forceinline__ void cos_sin4(const float2* tr, int i0, int half, flo
 
 // FLAT: x and y rows at one stride each (no test of the row map before the
 // loads are issued).  W waves share a row (wave w holds float4s
-// [w*64*NV, (w+1)*64*NV) of it) when the rows are few.
-template <int NV, int MODE, bool FLAT, int W = 1>
+// [w*64*NV, (w+1)*64*NV) of it) when the rows are few.  XS: the rotation
+// partners come from other lanes' registers instead of the LDS row: NORMAL
+// pairs (2k, 2k+1) lie in one 4-vector; a NEOX pair is half/4 vectors
+// apart, which is lane ^ (half/4) when hd/4 divides 64 and half/4 is a
+// power of two (the head's vectors sit on consecutive lanes of one wave).
+template <int NV, int MODE, bool FLAT, int W = 1, bool XS = false>
 __global__ __launch_bounds__(64 * W) void k_layer_norm_rope(NormRopeArgs a) {
     __shared__ float row[kRowMax];
     __shared__ double lds[2 * W];
@@ -148,8 +152,39 @@ __global__ __launch_bounds__(64 * W) void k_layer_norm_rope(NormRopeArgs a) {
                 set(o, e, t);
             }
             v[k] = o;
-            *reinterpret_cast<float4*>(&row[j]) = o;
+            if constexpr (!XS) *reinterpret_cast<float4*>(&row[j]) = o;
         }
+    }
+    if constexpr (XS) {
+        const int dq = half >> 2;   // partner distance in vectors (NEOX)
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            float4 pv = v[k];
+            if constexpr (MODE == 2) {   // every lane takes part in the shuffles
+                pv.x = __shfl_xor(v[k].x, dq);
+                pv.y = __shfl_xor(v[k].y, dq);
+                pv.z = __shfl_xor(v[k].z, dq);
+                pv.w = __shfl_xor(v[k].w, dq);
+            }
+            const int64_t j = (lane + 64 * k) * 4;
+            if (j >= ne0) continue;
+            float4 o = v[k];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int i = i0[k] + e;
+                if (i >= nd) continue;            // past n_dims: copied
+                const float2 c = cs[k][e];
+                if constexpr (MODE == 2) {
+                    if (i < half) set(o, e, get(v[k], e) * c.x - get(pv, e) * c.y);
+                    else set(o, e, get(pv, e) * c.y + get(v[k], e) * c.x);
+                } else {
+                    if ((i & 1) == 0) set(o, e, get(v[k], e) * c.x - get(v[k], e + 1) * c.y);
+                    else set(o, e, get(v[k], e - 1) * c.y + get(v[k], e) * c.x);
+                }
+            }
+            Stream<float>::store4(yr + j * 4, o);
+        }
+        return;
     }
     __syncthreads();
 
@@ -186,21 +221,21 @@ __global__ __launch_bounds__(64 * W) void k_layer_norm_rope(NormRopeArgs a) {
     }
 }
 
-template <int MODE, bool FLAT>
+template <int MODE, bool FLAT, bool XS>
 void go(const NormRopeArgs& a, int nv, int w, dim3 grid, hipStream_t s) {
     if (FLAT && w > 1) {
         const dim3 block(64 * w);
         switch (nv * 8 + w) {
-            case 2 * 8 + 2: hipLaunchKernelGGL((k_layer_norm_rope<1, MODE, FLAT, 2>), grid, block, 0, s, a); break;
-            case 4 * 8 + 2: hipLaunchKernelGGL((k_layer_norm_rope<2, MODE, FLAT, 2>), grid, block, 0, s, a); break;
-            default: hipLaunchKernelGGL((k_layer_norm_rope<1, MODE, FLAT, 4>), grid, block, 0, s, a); break;   // 4, 4
+            case 2 * 8 + 2: hipLaunchKernelGGL((k_layer_norm_rope<1, MODE, FLAT, 2, XS>), grid, block, 0, s, a); break;
+            case 4 * 8 + 2: hipLaunchKernelGGL((k_layer_norm_rope<2, MODE, FLAT, 2, XS>), grid, block, 0, s, a); break;
+            default: hipLaunchKernelGGL((k_layer_norm_rope<1, MODE, FLAT, 4, XS>), grid, block, 0, s, a); break;   // 4, 4
         }
         return;
     }
     switch (nv) {
-        case 1: hipLaunchKernelGGL((k_layer_norm_rope<1, MODE, FLAT>), grid, dim3(64), 0, s, a); break;
-        case 2: hipLaunchKernelGGL((k_layer_norm_rope<2, MODE, FLAT>), grid, dim3(64), 0, s, a); break;
-        default: hipLaunchKernelGGL((k_layer_norm_rope<4, MODE, FLAT>), grid, dim3(64), 0, s, a); break;
+        case 1: hipLaunchKernelGGL((k_layer_norm_rope<1, MODE, FLAT, 1, XS>), grid, dim3(64), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((k_layer_norm_rope<2, MODE, FLAT, 1, XS>), grid, dim3(64), 0, s, a); break;
+        default: hipLaunchKernelGGL((k_layer_norm_rope<4, MODE, FLAT, 1, XS>), grid, dim3(64), 0, s, a); break;
     }
 }
 
@@ -237,12 +272,20 @@ int launch_layer_norm_rope(const cbx_tensor* x, const cbx_tensor* w, const cbx_t
     while (wr < 4 && wr < nv && rows * wr < int64_t{8} * st->n_cu) wr *= 2;
     const dim3 grid(static_cast<unsigned>(rows));
     const bool flat = a.mx.flat && a.my.flat;
+    // partners in registers: the head's vectors on consecutive lanes of one
+    // wave (hd/4 divides 64), whole 4-vectors rotated or copied (n_dims % 4
+    // == 0; NEOX: half/4 a power of two, so the partner is lane ^ (half/4))
+    const int64_t hq = head_dim / 4, dq = p.n_dims / 8;
+    const bool xs = flat && a.vec_cs && 64 % hq == 0 && p.n_dims % 4 == 0 &&
+                    (p.mode != 2 || (p.n_dims % 8 == 0 && dq > 0 && (dq & (dq - 1)) == 0));
     if (p.mode == 2) {
-        if (flat) go<2, true>(a, nv, wr, grid, s);
-        else go<2, false>(a, nv, 1, grid, s);
+        if (xs) go<2, true, true>(a, nv, wr, grid, s);
+        else if (flat) go<2, true, false>(a, nv, wr, grid, s);
+        else go<2, false, false>(a, nv, 1, grid, s);
     } else {
-        if (flat) go<0, true>(a, nv, wr, grid, s);
-        else go<0, false>(a, nv, 1, grid, s);
+        if (xs) go<0, true, true>(a, nv, wr, grid, s);
+        else if (flat) go<0, true, false>(a, nv, wr, grid, s);
+        else go<0, false, false>(a, nv, 1, grid, s);
     }
     return check_launch("layer_norm_rope");
 }

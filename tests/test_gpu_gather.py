@@ -119,3 +119,50 @@ def test_cpy(cbx, oracle, src_t, dst_t):
     out2 = torch.empty(xs.shape, dtype=out.dtype, device="cuda")
     got2 = host(cbx.cpy(dev(x)[:, 3:1003], out2))
     assert_bitexact(got2, oracle.cpy(np.ascontiguousarray(xs), dst_t), "cpy strided")
+
+
+@pytest.mark.parametrize("ne0", [256, 1024, 2560])
+def test_q8_0_long_rows(cbx, oracle, ne0):
+    """Q8_0 rows of 16-byte aligned length (ne0 % 256 == 0) over several
+    workgroup passes (2560 = 2.5 x 1024 elements): alone, with a second
+    Q8_0 table, with an f32 or f16 table added, first/last rows; bit-exact."""
+    n_rows = 19
+    q = oracle.quantize_q8_0(W.normal(240 + ne0, (n_rows, ne0), 0.0, 0.05))
+    q2 = oracle.quantize_q8_0(W.normal(241 + ne0, (n_rows, ne0), 0.0, 0.05))
+    f = W.normal(242 + ne0, (n_rows, ne0))
+    h = W.normal(243 + ne0, (n_rows, ne0)).astype(np.float16)
+    ids = np.concatenate([[0, n_rows - 1], W.randint(244, (21,), 0, n_rows)]).astype(np.int32)
+    ids2 = W.randint(245, (ids.size,), 0, n_rows)
+    gq = oracle.get_rows(q, ids, q8_0=True)
+    assert_bitexact(host(cbx.get_rows(dev(q), dev(ids), q8_0=True)), gq, "q8 long rows")
+    got = cbx.get_rows_add(dev(q), dev(ids), dev(q2), dev(ids2), q8_0=True, q8_0_2=True)
+    assert_bitexact(host(got), oracle.add(gq, oracle.get_rows(q2, ids2, q8_0=True)), "q8 + q8")
+    got = cbx.get_rows_add(dev(q), dev(ids), dev(f), dev(ids2), q8_0=True)
+    assert_bitexact(host(got), oracle.add(gq, oracle.get_rows(f, ids2)), "q8 + f32")
+    got = cbx.get_rows_add(dev(h), dev(ids2), dev(q), dev(ids), q8_0_2=True)
+    assert_bitexact(host(got), oracle.add(oracle.get_rows(h, ids2), gq), "f16 + q8")
+
+
+def test_q8_0_in_op_batch(cbx, oracle):
+    """The one-launch gather with Q8_0 tables: ne0 = 2048 (two passes of the
+    workgroup) and ne0 = 160 (a ragged pass), and an out-of-range id zeroing
+    its row and raising the device error bit."""
+    qa = oracle.quantize_q8_0(W.normal(250, (11, 2048), 0.0, 0.05))
+    qb = oracle.quantize_q8_0(W.normal(251, (11, 160), 0.0, 0.05))
+    ia = W.randint(252, (9,), 0, 11)
+    ib = W.randint(253, (9,), 0, 11)
+    ic = np.array([3, 11, 0], dtype=np.int32)
+    ya = torch.empty((9, 2048), dtype=torch.float32, device="cuda")
+    yb = torch.empty((9, 160), dtype=torch.float32, device="cuda")
+    yc = torch.empty((3, 2048), dtype=torch.float32, device="cuda")
+    ta, tb = dev(qa), dev(qb)
+    cbx.device_errors(clear=True)
+    cbx.run_ops([cbx.Op(cbx.OP_GET_ROWS, [ta, dev(ia)], [ya], q8=[0]),
+                 cbx.Op(cbx.OP_GET_ROWS, [tb, dev(ib)], [yb], q8=[0]),
+                 cbx.Op(cbx.OP_GET_ROWS, [ta, dev(ic)], [yc], q8=[0])])
+    assert_bitexact(host(ya), oracle.get_rows(qa, ia, q8_0=True), "batch q8 2048")
+    assert_bitexact(host(yb), oracle.get_rows(qb, ib, q8_0=True), "batch q8 160")
+    out = host(yc)
+    assert cbx.device_errors(clear=True) & 1
+    assert not out[1].any()
+    assert_bitexact(out[[0, 2]], oracle.get_rows(qa, ic[[0, 2]], q8_0=True), "batch q8 good rows")

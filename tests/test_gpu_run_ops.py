@@ -216,3 +216,24 @@ def test_batched_norm_row_forms(cbx, oracle, rows, dtype):
     if dtype == np.float32:
         assert_bitexact(host(yr), oracle.rms_norm_mul(x, g, 1e-5, nth=8), "batched rms")
         assert_bitexact(host(yl), oracle.layer_norm(x, g, b, 1e-5, nth=8), "batched ln")
+
+
+@pytest.mark.parametrize("n,offset", [(4096 * 8, 0), (1003, 0), (4096, 4)])
+def test_batched_f16_elementwise_forms(cbx, oracle, n, offset):
+    """f16 element-wise ops in the batch over a long aligned run, a ragged
+    length (the tail lane) and operands only 8-byte aligned (offset 4
+    elements); each equals its single-op entry point and the oracle."""
+    x = W.normal(90, (n + offset,), 0.0, 3.0).astype(np.float16)
+    u = W.normal(91, (n + offset,), 0.0, 1.0).astype(np.float16)
+    tx, tu = dev(x)[offset:], dev(u)[offset:]
+    xs, us = x[offset:], u[offset:]
+    ys = [torch.empty_like(tx) for _ in range(4)]
+    cbx.run_ops([cbx.Op(cbx.OP_UNARY, [tx], [ys[0]], act=cbx.SILU),
+                 cbx.Op(cbx.OP_LEAKY_RELU, [tx], [ys[1]], param=0.1),
+                 cbx.Op(cbx.OP_SWIGLU, [tx, tu], [ys[2]]),
+                 cbx.Op(cbx.OP_UNARY, [tu], [ys[3]], act=cbx.GELU)])
+    assert_bitexact(host(ys[0]), host(cbx.silu(tx)), "silu = single op")
+    assert_close(host(ys[0]), oracle.unary(oracle.SILU, xs), x=xs, what="silu f16", rtol=RTOL_F16)
+    assert_bitexact(host(ys[1]), oracle.leaky_relu(xs, 0.1), "leaky f16")
+    assert_bitexact(host(ys[2]), host(cbx.swiglu(tx, tu)), "swiglu = single op")
+    assert_bitexact(host(ys[3]), oracle.unary(oracle.GELU, us), "gelu f16")
