@@ -13,6 +13,8 @@
 // and the device's cosf/sinf.
 #include "cbx_rowops.h"
 
+#include <algorithm>
+
 namespace cbx {
 namespace {
 
@@ -114,6 +116,70 @@ __global__ __launch_bounds__(kRopeThreads) void k_rope(RopeArgs a) {
     }
 }
 
+// Four pairs a lane, no LDS: NEOX pairs m..m+3 of a head are two 4-element
+// vectors (at m and m + n_dims/2), NORMAL pairs m..m+3 the 8 elements from
+// 2m; their cos/sin are two 16-byte loads from the table row of the token's
+// position.  One workgroup per token, the token's ne1 * n_dims/8 pair
+// groups over its lanes (a loop past the block).  Needs n_dims % 8 == 0, a
+// 16-byte aligned table, and x / y head rows aligned for 4-element loads.
+// The products and roundings are those of k_rope.
+template <typename T, int MODE>
+__global__ __launch_bounds__(kRopeThreads) void k_rope_vec(RopeArgs a) {
+    const RopeParams& rp = a.rp;
+    const uint32_t half = static_cast<uint32_t>(rp.n_dims / 2);
+    const uint32_t per_head = half / 4;
+    const uint32_t t = blockIdx.x;
+    const uint32_t i2 = t % a.ne2, i3 = t / a.ne2;
+    const int32_t p = *reinterpret_cast<const int32_t*>(a.pos + i2 * a.pos_nb0);
+    const bool in_tab = p >= 0 && p < a.n_pos;
+    const float2* tr = a.table + static_cast<int64_t>(in_tab ? p : 0) * half;
+    constexpr int es = Elt<T>::size;
+    const char* xt = a.x + i2 * a.xnb2 + i3 * a.xnb3;
+    char* yt = a.y + i2 * a.ynb2 + i3 * a.ynb3;
+    for (uint32_t q = threadIdx.x; q < a.ne1 * per_head; q += blockDim.x) {
+        const uint32_t h = q / per_head;
+        const uint32_t m = (q - h * per_head) * 4;
+        const char* xr = xt + h * a.xnb1;
+        char* yr = yt + h * a.ynb1;
+        const uint32_t ia = MODE == 2 ? m : 2 * m, ib = MODE == 2 ? m + half : 2 * m + 4;
+        const float4 xa = Elt<T>::load4(xr + ia * es);
+        const float4 xb = Elt<T>::load4(xr + ib * es);
+        float2 c[4];
+        if (in_tab) {
+            const float4 c01 = *reinterpret_cast<const float4*>(tr + m);
+            const float4 c23 = *reinterpret_cast<const float4*>(tr + m + 2);
+            c[0] = make_float2(c01.x, c01.y);
+            c[1] = make_float2(c01.z, c01.w);
+            c[2] = make_float2(c23.x, c23.y);
+            c[3] = make_float2(c23.z, c23.w);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) rope_cos_sin_dev(p, static_cast<int>(m) + e, rp, a.ff, &c[e].x, &c[e].y);
+        }
+        float4 ya, yb;
+        if constexpr (MODE == 2) {   // y[i] = x0 cos - x1 sin, y[i + half] = x0 sin + x1 cos
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float x0 = get(xa, e), x1 = get(xb, e);
+                set(ya, e, x0 * c[e].x - x1 * c[e].y);
+                set(yb, e, x0 * c[e].y + x1 * c[e].x);
+            }
+        } else {                     // pairs (2k, 2k + 1)
+            ya = make_float4(xa.x * c[0].x - xa.y * c[0].y, xa.x * c[0].y + xa.y * c[0].x,
+                             xa.z * c[1].x - xa.w * c[1].y, xa.z * c[1].y + xa.w * c[1].x);
+            yb = make_float4(xb.x * c[2].x - xb.y * c[2].y, xb.x * c[2].y + xb.y * c[2].x,
+                             xb.z * c[3].x - xb.w * c[3].y, xb.z * c[3].y + xb.w * c[3].x);
+        }
+        Elt<T>::store4(yr + ia * es, ya);
+        Elt<T>::store4(yr + ib * es, yb);
+    }
+    for (uint32_t q = threadIdx.x; q < a.ne1 * a.n_tail; q += blockDim.x) {
+        const uint32_t h = q / a.n_tail;
+        const uint32_t j = static_cast<uint32_t>(rp.n_dims) + (q - h * a.n_tail);
+        *reinterpret_cast<T*>(yt + h * a.ynb1 + j * es) = *reinterpret_cast<const T*>(xt + h * a.xnb1 + j * es);
+    }
+}
+
 template <typename T, int MODE>
 void rope_it(int it, dim3 grid, dim3 block, size_t lds, hipStream_t s, const RopeArgs& a) {
     switch (it) {
@@ -153,6 +219,26 @@ int launch_rope(const cbx_tensor* x, const cbx_tensor* pos, const RopeParams& p,
     a.n_tail = static_cast<uint32_t>(x->ne[0] - p.n_dims);
     a.n_pos = n_pos;
     a.rp = p;
+    // four pairs a lane with vector loads: the block just covers the
+    // token's pair groups (a multiple of 64 lanes, at most kRopeThreads)
+    const int64_t al = x->type == CBX_TYPE_F32 ? 16 : 8;
+    bool vec = p.n_dims % 8 == 0 && p.n_dims > 0 && reinterpret_cast<uintptr_t>(table) % 16 == 0;
+    for (const cbx_tensor* t : {x, static_cast<const cbx_tensor*>(y)}) {
+        if (reinterpret_cast<uintptr_t>(t->data) % al) vec = false;
+        for (int k = 1; k < 4; k++) if (t->ne[k] > 1 && static_cast<int64_t>(t->nb[k]) % al) vec = false;
+    }
+    if (vec) {
+        const int64_t groups = x->ne[1] * (p.n_dims / 8);
+        const dim3 vblock(static_cast<unsigned>(std::min<int64_t>(kRopeThreads, cdiv(groups, 64) * 64)));
+        if (x->type == CBX_TYPE_F32) {
+            if (p.mode == 2) hipLaunchKernelGGL((k_rope_vec<float, 2>), grid, vblock, 0, s, a);
+            else hipLaunchKernelGGL((k_rope_vec<float, 0>), grid, vblock, 0, s, a);
+        } else {
+            if (p.mode == 2) hipLaunchKernelGGL((k_rope_vec<uint16_t, 2>), grid, vblock, 0, s, a);
+            else hipLaunchKernelGGL((k_rope_vec<uint16_t, 0>), grid, vblock, 0, s, a);
+        }
+        return check_launch("rope_ext");
+    }
     // pairs per token over the workgroup: 1, 2 or 4 per lane preload their x
     const int64_t per_lane = cdiv(x->ne[1] * (p.n_dims / 2), kRopeThreads);
     const int it = per_lane <= 1 ? 1 : per_lane <= 2 ? 2 : per_lane <= 4 ? 4 : 0;

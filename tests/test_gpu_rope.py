@@ -115,3 +115,31 @@ def test_in_place(cbx, oracle, cache64):
     t = dev(x)
     cbx.rope_ext(t, dev(pos), cache64, out=t)
     assert_bitexact(host(t), oracle.rope_ext(x, pos, 64), "in place")
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+@pytest.mark.parametrize("mode", [0, 2])
+@pytest.mark.parametrize("ne0,n_dims", [(64, 64), (66, 64), (64, 20), (128, 40)])
+def test_vector_and_scalar_forms(cbx, oracle, dtype, mode, ne0, n_dims):
+    """Four pairs a lane with vector loads (n_dims % 8 == 0, aligned head
+    rows) and the pair-a-lane form (ne0 = 66: head rows off the vector
+    alignment; n_dims 20 and 40: n_dims % 8 != 0), both pairings, f32 and
+    f16, positions in and past the table: each as the oracle."""
+    x = W.normal(46 + ne0 + n_dims, (19, 12, ne0)).astype(dtype)
+    pos = np.concatenate([W.randint(47, (17,), 0, 200), [250, 400]]).astype(np.int32)
+    c = cbx.RopeCache(n_dims, mode=mode, n_ctx_orig=2048, n_pos=200)
+    got = host(cbx.rope_ext(dev(x), dev(pos), c))
+    exp = oracle.rope_ext(x, pos, n_dims, mode=mode)
+    assert_bitexact(got[:17], exp[:17], f"rope in table mode {mode} ne0 {ne0} n_dims {n_dims}")
+    x32 = x.astype(np.float32)
+    half = n_dims // 2
+    if mode == 2:
+        pr = np.hypot(x32[..., :half], x32[..., half:n_dims])
+        pair = np.concatenate([pr, pr, np.abs(x32[..., n_dims:])], axis=-1)
+    else:
+        pr = np.repeat(np.hypot(x32[..., 0:n_dims:2], x32[..., 1:n_dims:2]), 2, axis=-1)
+        pair = np.concatenate([pr, np.abs(x32[..., n_dims:])], axis=-1)
+    rt = 2.0 ** -10 if dtype == np.float16 else 1e-5
+    assert_close(got[17:].astype(np.float32), exp[17:].astype(np.float32), x=pair[17:], rtol=rt,
+                 atol_x=2.0 ** -10 if dtype == np.float16 else 2.0 ** -20, what="rope past the table")
+    c.close()
