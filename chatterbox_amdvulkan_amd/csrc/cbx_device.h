@@ -191,24 +191,26 @@ __device__ __forceinline__ float act_gelu_tab(const uint16_t* __restrict__ tab, 
 }
 
 // The same function with the table read only where it is needed.  For
-// |x| < 10 the result is a function of h = f16(x) alone.  With
-// E = 2^(xf (K1 + K2 xf^2)) = e^(2a), a = sqrt(2/pi) xf (1 + 0.044715 xf^2)
-// (the inner polynomial with one fused multiply-add),
-// the table's 0.5 xf (1 + tanh a) equals xf (1 - 1/(E + 1)); that is
-// evaluated with the hardware exp2 and reciprocal (q = 1 - r is within
-// ~2 ulps of 1 absolute, i.e. ~2/q ulps of g relative, plus ~8 ulps from
-// the rounding of the exponent), and the f16 rounding of g is kept when g
-// lies more than 8 + 16/q f32 ulps from an f16 rounding midpoint.  Otherwise
-// (q < 1/128, f16-subnormal g, or too close to a midpoint) the exact table
-// entry is used; lanes that do not need it all read entry 0, so the load
-// touches a single cache line in the common case.  Because the result
-// depends on h only, running every f16 code through this function checks it
-// for every input.
+// |x| < 10 the result is a function of h = f16(x) alone.  The table's
+// 0.5 xf (1 + tanh a), a = sqrt(2/pi) xf (1 + 0.044715 xf^2), equals
+// g = xf q with q = 1 / (1 + e), e = 2^-w, w = xf (K1 + K2 xf^2) (the inner
+// polynomial with one fused multiply-add), evaluated with the hardware exp2
+// and reciprocal: q carries the reciprocal's and the addition's roundings
+// and what the rounding of w does to e (ln 2 |dw| relative; it grows with
+// |w| only where e is large).  The table's own f32 evaluation loses up to
+// ~1/(2q) ulps in 1 + tanh a (a cancellation for a < 0).  The f16 rounding
+// of g is kept when g lies more than 8 + 16/q = 24 + 16 e f32 ulps from an
+// f16 rounding midpoint (its low 13 bits); otherwise (f16-subnormal g, or
+// too close to a midpoint) the exact table entry is used.  x <= -10 reads
+// entry 0 (GELU(+0) = +0, ggml's result there); lanes that need no entry
+// all read entry 0 too, so the load touches a single cache line in the
+// common case.  Because the result depends on h only, running every f16
+// code through this function checks it for every input.
 #define CBX_GELU_K1 2.3022081983f          // 2 sqrt(2/pi) log2(e)
 #define CBX_GELU_K2 0.10294324967f         // K1 * 0.044715
 
 struct GeluPart {
-    uint32_t idx;   // table entry to read: h, or 0 when g's rounding is sure
+    uint32_t idx;   // table entry to read: h, or 0 when g's rounding is sure or x <= -10
     float    g;
     bool     sure;
 };
@@ -217,20 +219,21 @@ __device__ __forceinline__ GeluPart gelu_part(float x) {
     const uint32_t h = f2h(x);
     const float xf = h2f(static_cast<uint16_t>(h));
     const float w = xf * __builtin_fmaf(CBX_GELU_K2, xf * xf, CBX_GELU_K1);
-    const float r = __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(w) + 1.0f);
-    const float q = 1.0f - r;
+    const float e = __builtin_amdgcn_exp2f(-w);   // 1/q - 1
+    const float q = __builtin_amdgcn_rcpf(e + 1.0f);
     const float g = xf * q;
-    const uint32_t gb = __builtin_bit_cast(uint32_t, g) & 0x7fffffffu;
-    const float dist = __builtin_fabsf(static_cast<float>(static_cast<int32_t>(gb & 0x1fffu) - 0x1000));
+    const int32_t d = static_cast<int32_t>(__builtin_bit_cast(uint32_t, g) & 0x1fffu) - 0x1000;
+    // x <= -10 gives xf <= -10, w < -125.9 and an infinite margin: never sure
+    const float margin = __builtin_fmaf(e, 16.0f, 24.0f);
+    const bool neg10 = x <= -10.0f;
     // bitwise & keeps this branch-free, so the table loads of several
     // elements issue together
-    const bool sure = (q >= 0.0078125f) & (gb >= 0x38800000u) & ((dist - 8.0f) * q > 16.0f);
-    return GeluPart{sure ? 0u : h, g, sure};
+    const bool sure = (__builtin_fabsf(static_cast<float>(d)) > margin) & (__builtin_fabsf(g) >= 0x1p-14f);
+    return GeluPart{(sure | neg10) ? 0u : h, g, sure};
 }
 
 __device__ __forceinline__ float gelu_finish(float x, const GeluPart& p, uint16_t tv) {
-    float r = h2f(p.sure ? static_cast<uint16_t>(f2h(p.g)) : tv);
-    r = x <= -10.0f ? 0.0f : r;
+    const float r = h2f(p.sure ? static_cast<uint16_t>(f2h(p.g)) : tv);
     return x >= 10.0f ? x : r;
 }
 
