@@ -287,42 +287,62 @@ __global__ __launch_bounds__(kThreads) void k_group_norm_vec(GnArgs a, uint32_t 
 
 // ---- split reduction --------------------------------------------------------
 // A few large groups (the CFM's 2 x 8) spread over many workgroups: each
-// chunk workgroup holds only its chunk of the group in registers and
-// reduces it; the chunks' f64 partial sums meet in a workspace, once for
-// the mean and once for the variance.  Each element is read once and every
-// workgroup's VALU work is its own chunk, not the whole group.
+// chunk workgroup holds only its chunk of the group in registers, and the
+// f64 partial sums of its waves meet those of the group's other chunks in a
+// workspace, once for the mean and once for the variance.  Each element is
+// read once and every workgroup's VALU work is its own chunk.
+//
+// Every wave publishes its own partial and every wave collects the group's
+// partials itself: no barrier and no LDS anywhere, so a wave goes from its
+// loads to its exchange and from the exchange to its stores without waiting
+// for the other waves of its workgroup.  The group's P = n_chunks x 4
+// partials (slot ci * 4 + wave) are added in slot order -- lane l adds
+// slots l, l + 64, .. starting from +0, then the lanes by the DPP
+// butterfly -- the same bits in every wave of the group.
 //
 // A partial travels as two 64-bit words (its low and high halves), each
 // tagged in its upper 32 bits with the launch's tag: the dispatch's packet
 // index on its queue mixed with the queue's address, shifted left and made
 // odd (never the 0 of fresh memory; packets of one queue within 2^31 of
-// each other get different tags).  A word is written whole and read whole, so a reader
-// that finds this launch's tag in both words of a slot has that chunk's
-// partial; words left by earlier launches carry other tags and nothing is
-// ever cleared.  Wave 0 polls the group's 2n words, a lane a word, with
-// agent-scope loads.  The words are written with plain stores, which reach
-// the L2 the workgroups of one group share (their indices put them on one
-// XCD: dispatch deals workgroups to the 8 XCDs round-robin), except in
-// place, where agent-scope stores make them visible on any XCD.
+// each other get different tags).  A word is written whole and read whole,
+// so a reader that finds this launch's tag in both words of a slot has that
+// wave's partial; words left by earlier launches carry other tags and
+// nothing is ever cleared.  The words are written with plain stores, which
+// reach the L2 the workgroups of one group share (their indices put them on
+// one XCD: dispatch deals workgroups to the 8 XCDs round-robin), except in
+// place, where agent-scope stores make them visible on any XCD; they are
+// read with agent-scope loads.
 //
 // Waits are bounded: after GnSplit::wait_ticks of the 100 MHz real-time
-// counter a workgroup stops waiting and computes every chunk's partial
-// itself from x, with the same lanes and order as that chunk's own
-// workgroup, so the statistics are the same bits either way and a
-// workgroup that never gets a CU while the others run delays nothing.  (In
-// place, a workgroup that stops waiting may read chunks already
-// overwritten: it raises DEV_ERR_GN_WAIT.)  wait_ticks == 0: never wait.
-constexpr int kSplitThreads = 512;
+// counter a wave stops waiting and computes every slot's partial itself
+// from x, with the same lanes and order as the wave that owns the slot, so
+// the statistics are the same bits either way and a workgroup that never
+// gets a CU while the others run delays nothing.  (In place, a wave that
+// stops waiting may read chunks already overwritten: it raises
+// DEV_ERR_GN_WAIT.)  wait_ticks == 0: never wait.
+constexpr int kSplitThreads = 256;
+constexpr int kSplitWaves = kSplitThreads / WAVE;
 constexpr int kSplitMaxChunks = 32;
+constexpr int kSplitLaneSlots = kSplitMaxChunks * kSplitWaves / WAVE;   // partial slots a lane collects
 constexpr uint32_t kSplitMaxSlots = 1024;   // group instances x chunks per launch
+constexpr uint32_t kSplitStageWords = 2 * kSplitMaxSlots * kSplitWaves;
 
+// Compact arguments: every field arrives in the kernel's first round of
+// scalar loads, and the index arithmetic before the first load is 32-bit.
 struct GnSplit {
-    uint64_t* word;        // [2 stages][kSplitMaxSlots][2 words]
+    const char* x;
+    char* y;
+    const float* w;
+    const float* b;
+    uint64_t* word;          // [2 stages][kSplitMaxSlots * kSplitWaves][2 words]
     uint32_t* err;
-    uint32_t  n_chunks;
-    uint32_t  n_gi;
-    uint64_t  wait_ticks;
-    uint32_t  in_place;
+    const uint16_t* tab;
+    int64_t x_nb3, y_nb3;    // batch strides (bytes)
+    uint64_t wait_ticks;
+    uint32_t n_chunks, n_gi, n_groups, per_ch, cpg, C;   // per_ch = ne0 * ne1
+    float eps;
+    int32_t act;
+    uint32_t in_place;
 };
 
 // The dispatch's 64-bit packet index on its queue (llvm.amdgcn.dispatch.id;
@@ -337,20 +357,10 @@ __device__ __forceinline__ uint32_t launch_tag() {
     return ((static_cast<uint32_t>(id) ^ qmix) << 1) | 1u;
 }
 
-__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
-    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(v & 0xffffffffu), lane);
-    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(v >> 32), lane);
-    return (static_cast<uint64_t>(hi) << 32) | lo;
-}
-
-// One chunk's partial of stage 0 (Σx) or 1 (Σ(x - mean)^2, the f32
-// difference and square summed in f64): thread t holds float4 indices
-// q0 + t + k * kSplitThreads below q1.  The same function serves the chunk's
-// own workgroup and a workgroup that computes it on the chunk's behalf.
-// `area`: which of the two LDS areas of block_sum_1b (its parity).
+// A lane's partial of stage 0 (Σx) or 1 (Σ(x - mean)^2, the f32
+// difference and square summed in f64) over its NV vectors.
 template <int NV>
-__device__ __forceinline__ double chunk_partial(const float4 (&v)[NV], const bool (&ok)[NV], int stage, float mean,
-                                                double* red, int area) {
+__device__ __forceinline__ double lane_partial(const float4 (&v)[NV], const bool (&ok)[NV], int stage, float mean) {
     double p[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
@@ -365,132 +375,151 @@ __device__ __forceinline__ double chunk_partial(const float4 (&v)[NV], const boo
                          : 0.0;
         }
     }
-    return block_sum_1b<kSplitThreads>(thread_tree_sum<NV>(p), red, area);
+    return thread_tree_sum<NV>(p);
 }
 
+// The NV vectors that wave `wv` of the chunk [q0, q1) holds in lane `lane`
+// (float4 indices q0 + wv*64 + lane + k*kSplitThreads); lanes past the chunk
+// (a chunk may be empty) load the group's first vector, an address inside
+// the group.
 template <int NV>
-__device__ __forceinline__ void chunk_load(const char* xg, int64_t q0, int64_t q1, float4 (&v)[NV], bool (&ok)[NV]) {
+__device__ __forceinline__ void wave_chunk_load(const char* xg, uint32_t q0, uint32_t q1, uint32_t wv, uint32_t lane,
+                                                float4 (&v)[NV], bool (&ok)[NV]) {
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        const int64_t qi = q0 + threadIdx.x + static_cast<int64_t>(k) * kSplitThreads;
+        const uint32_t qi = q0 + wv * WAVE + lane + static_cast<uint32_t>(k) * kSplitThreads;
         ok[k] = qi < q1;
-        // lanes past the chunk (a chunk may be empty) load the group's first
-        // vector: an address inside the group
-        v[k] = *reinterpret_cast<const float4*>(xg + 16 * (ok[k] ? qi : 0));
+        v[k] = *reinterpret_cast<const float4*>(xg + 16 * static_cast<uint64_t>(ok[k] ? qi : 0));
     }
 }
 
-// Publishes this chunk's partial, waits (bounded) for the group's other
-// chunks and returns the partials' sum in chunk order, or computes every
-// chunk's partial itself when the wait runs out.
+// Publishes this wave's partial of `stage`, waits (bounded) for the group's
+// other partials and returns the group's sum (the same bits in every wave
+// of the group), or computes every slot's partial itself when the wait
+// runs out.
 template <int NV>
-__device__ __forceinline__ double split_combine(const GnSplit& sp, uint32_t tag, uint32_t gi, uint32_t ci,
-                                                int stage, double mine, float mean, const char* xg, int64_t n4,
-                                                int64_t per, double* red, int slot) {
-    __shared__ int waited_out;
-    const uint32_t n = sp.n_chunks;
-    uint64_t* wd = sp.word + 2 * (stage * kSplitMaxSlots + gi * n);
-    if (threadIdx.x < WAVE) {
-        const uint32_t lane = threadIdx.x;
-        const uint64_t bits = __builtin_bit_cast(uint64_t, mine);
-        const uint64_t tg = static_cast<uint64_t>(tag) << 32;
+__device__ __forceinline__ double split_exchange(const GnSplit& a, uint32_t tag, uint32_t gi, uint32_t ci, int stage,
+                                                 double mine, float mean, const char* xg, uint32_t n4, uint32_t per) {
+    const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const uint32_t P = a.n_chunks * kSplitWaves;
+    uint64_t* wd = a.word + static_cast<uint64_t>(stage) * kSplitStageWords + 2 * static_cast<uint64_t>(gi) * P;
+    const uint64_t bits = __builtin_bit_cast(uint64_t, mine);
+    const uint64_t tg = static_cast<uint64_t>(tag) << 32;
+    const uint32_t own = ci * kSplitWaves + wave;
+    if (lane < 2) {
         // lanes 0 and 1 publish the low and high halves
-        const uint64_t own = tg | (lane == 0 ? bits & 0xffffffffu : bits >> 32);
-        if (lane < 2) {
-            if (sp.in_place) __hip_atomic_store(&wd[2 * ci + lane], own, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            else __hip_atomic_store(&wd[2 * ci + lane], own, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
-        bool ok = false;
-        uint64_t mv = tg;
-        if (sp.wait_ticks) {
-            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-            while (true) {
-                if (lane < 2 * n && lane / 2 != ci) {
-                    mv = __hip_atomic_load(&wd[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-                if (__all((mv >> 32) == tag)) {
-                    ok = true;
-                    break;
-                }
-                if (__builtin_amdgcn_s_memrealtime() - t0 > sp.wait_ticks) break;
-                __builtin_amdgcn_s_sleep(1);
-            }
-        }
-        if (ok) {
-            double t = 0.0;
-            for (uint32_t c = 0; c < n; c++) {
-                const uint64_t b = c == ci ? bits
-                                           : (readlane_u64(mv, 2 * c) & 0xffffffffu) |
-                                                 (readlane_u64(mv, 2 * c + 1) << 32);
-                t += __builtin_bit_cast(double, b);
-            }
-            if (lane == 0) red[slot] = t;
-        }
-        if (lane == 0) waited_out = ok ? 0 : 1;
+        const uint64_t word = tg | (lane == 0 ? bits & 0xffffffffu : bits >> 32);
+        if (a.in_place) __hip_atomic_store(&wd[2 * own + lane], word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else __hip_atomic_store(&wd[2 * own + lane], word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    __syncthreads();
-    if (waited_out) {
-        // every chunk's partial, as its own workgroup computes it
-        if (sp.in_place && threadIdx.x == 0) atomicOr(sp.err, DEV_ERR_GN_WAIT);
-        double t = 0.0;
-        for (uint32_t c = 0; c < n; c++) {
+    double val[kSplitLaneSlots];
+    bool ok = false;
+    if (a.wait_ticks) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (true) {
+            bool have = true;
+#pragma unroll
+            for (int r = 0; r < kSplitLaneSlots; r++) {
+                const uint32_t sl = lane + WAVE * r;
+                val[r] = 0.0;
+                if (sl < P) {
+                    if (sl == own) {
+                        val[r] = mine;
+                    } else {
+                        const uint64_t lo = __hip_atomic_load(&wd[2 * sl], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        const uint64_t hi =
+                            __hip_atomic_load(&wd[2 * sl + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        have = have && (lo >> 32) == tag && (hi >> 32) == tag;
+                        val[r] = __builtin_bit_cast(double, (lo & 0xffffffffu) | (hi << 32));
+                    }
+                }
+            }
+            if (__all(have)) {
+                ok = true;
+                break;
+            }
+            if (__builtin_amdgcn_s_memrealtime() - t0 > a.wait_ticks) break;
+        }
+    }
+    if (!ok) {
+        // every slot's partial, as the wave that owns it computes it
+        if (a.in_place && lane == 0) atomicOr(a.err, DEV_ERR_GN_WAIT);
+#pragma unroll
+        for (int r = 0; r < kSplitLaneSlots; r++) val[r] = 0.0;
+        for (uint32_t sl = 0; sl < P; sl++) {
+            const uint32_t c = sl / kSplitWaves, wv = sl - c * kSplitWaves;
+            const uint32_t q0 = c * per, q1 = q0 + per < n4 ? q0 + per : n4;
             float4 v[NV];
-            bool ok[NV];
-            const int64_t q0 = static_cast<int64_t>(c) * per;
-            chunk_load<NV>(xg, q0, q0 + per < n4 ? q0 + per : n4, v, ok);
-            // areas alternate by iteration (c = 0 takes the one the
-            // caller's last sum did not)
-            t += chunk_partial<NV>(v, ok, stage, mean, red, 1 + static_cast<int>(c));
+            bool okv[NV];
+            wave_chunk_load<NV>(xg, q0, q1, wv, lane, v, okv);
+            const double ps = wave_sum(lane_partial<NV>(v, okv, stage, mean));
+#pragma unroll
+            for (int r = 0; r < kSplitLaneSlots; r++) {
+                if (sl == lane + WAVE * r) val[r] = ps;
+            }
         }
-        return t;   // the same in every thread
     }
-    return red[slot];
+    double t = 0.0;
+#pragma unroll
+    for (int r = 0; r < kSplitLaneSlots; r++) t += val[r];
+    return wave_sum(t);
 }
 
-template <int NV, bool ACT>
-__global__ __launch_bounds__(kSplitThreads) void k_group_norm_split(GnArgs a, GnSplit sp) {
-    // two areas of wave totals for block_sum_1b, then the broadcast slot
-    __shared__ double red[2 * (kSplitThreads / WAVE) + 1];
-    constexpr int kSlot = 2 * (kSplitThreads / WAVE);
-    const uint32_t b = blockIdx.x;
-    const uint32_t j = b / kXcds;
-    const uint32_t m = j / sp.n_chunks;
-    const uint32_t ci = j - m * sp.n_chunks;
+// ACT: 0 none, 1 the activation chosen at run time, 2 Mish (the CFM
+// decoder's GroupNorm -> Mish) compiled in, without the switch's branches.
+template <int NV, int ACT>
+__global__ __launch_bounds__(kSplitThreads) void k_group_norm_split(GnSplit a) {
+    arg_now(a.x);
+    arg_now(a.y);
+    arg_now(a.w);
+    arg_now(a.b);
+    arg_now(a.word);
+    arg_now(reinterpret_cast<const void*>(a.x_nb3));
+    arg_now(reinterpret_cast<const void*>(a.y_nb3));
+    arg_now(a.per_ch);
+    arg_now(a.cpg);
+    arg_now(a.C);
+    // workgroup b: XCD b % 8, and its chunks on that XCD
+    const uint32_t b = blockIdx.x, j = b / kXcds;
+    const uint32_t m = j / a.n_chunks, ci = j - m * a.n_chunks;
     const uint32_t gi = b % kXcds + kXcds * m;
-    const int64_t C = a.x.ne[2];
-    const int64_t g = gi % a.n_groups, i3 = gi / a.n_groups;
-    const int64_t c0 = g * a.cpg;
+    const uint32_t i3 = gi / a.n_groups, g = gi - i3 * a.n_groups;
+    const uint32_t c0 = g * a.cpg;
     // past the last group, or an empty group (past C): every workgroup of it
-    // leaves here, so nobody counts on its counter
-    if (gi >= sp.n_gi || c0 >= C) return;
-    const int64_t c1 = c0 + a.cpg < C ? c0 + a.cpg : C;
-    const int64_t count = a.x.ne[0] * a.x.ne[1] * (c1 - c0);
-    const char* xg = a.x.data + c0 * a.x.nb[2] + i3 * a.x.nb[3];
-    char* yg = a.y.data + c0 * a.y.nb[2] + i3 * a.y.nb[3];
-    const uint32_t per_ch = static_cast<uint32_t>(a.x.ne[0] * a.x.ne[1]);
-    const int64_t n4 = count / 4;
-    const int64_t per = (n4 + sp.n_chunks - 1) / sp.n_chunks;
-    const int64_t q0 = static_cast<int64_t>(ci) * per;
-    const int64_t q1 = q0 + per < n4 ? q0 + per : n4;
+    // leaves here, so nobody counts on its partials
+    if (gi >= a.n_gi || c0 >= a.C) return;
+    const uint32_t c1 = c0 + a.cpg < a.C ? c0 + a.cpg : a.C;
+    const uint32_t n4 = (a.per_ch * (c1 - c0)) / 4;
+    const uint32_t per = (n4 + a.n_chunks - 1) / a.n_chunks;
+    const uint32_t q0 = ci * per, q1 = q0 + per < n4 ? q0 + per : n4;
+    const uint64_t gofs = static_cast<uint64_t>(c0) * a.per_ch * 4;
+    const char* xg = a.x + gofs + static_cast<int64_t>(i3) * a.x_nb3;
+    char* yg = a.y + gofs + static_cast<int64_t>(i3) * a.y_nb3;
+    const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
 
     float4 v[NV];
     bool ok[NV];
-    chunk_load<NV>(xg, q0, q1, v, ok);
+    wave_chunk_load<NV>(xg, q0, q1, wave, lane, v, ok);
+    // the affine values of each vector's channel (a vector lies in one
+    // channel: ne0 % 4 == 0), read from x where there are none
     float wv[NV], bv[NV];
+    const float* wq = a.w ? a.w : reinterpret_cast<const float*>(xg);
+    const float* bq = a.b ? a.b : reinterpret_cast<const float*>(xg);
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        const int64_t qi = q0 + threadIdx.x + static_cast<int64_t>(k) * kSplitThreads;
-        const int64_t c = c0 + static_cast<uint32_t>(4 * (ok[k] ? qi : 0)) / per_ch;
-        wv[k] = a.w ? a.w[c] : 1.0f;
-        bv[k] = a.b ? a.b[c] : 0.0f;
+        const uint32_t qi = q0 + threadIdx.x + static_cast<uint32_t>(k) * kSplitThreads;
+        const uint32_t c = c0 + (4 * (ok[k] ? qi : q0)) / a.per_ch;
+        wv[k] = wq[a.w ? c : 0];
+        bv[k] = bq[a.b ? c : 0];
     }
     const uint32_t tag = launch_tag();
-    const double s0 = chunk_partial<NV>(v, ok, 0, 0.0f, red, 0);
-    const double s = split_combine<NV>(sp, tag, gi, ci, 0, s0, 0.0f, xg, n4, per, red, kSlot);
-    const float mean = static_cast<float>(s / static_cast<double>(count));
-    const double s1 = chunk_partial<NV>(v, ok, 1, mean, red, 0);
-    const double s2 = split_combine<NV>(sp, tag, gi, ci, 1, s1, mean, xg, n4, per, red, kSlot);
-    const float var = static_cast<float>(s2 / static_cast<double>(count));
+    const double count = static_cast<double>(4 * n4);
+    const double s =
+        split_exchange<NV>(a, tag, gi, ci, 0, wave_sum(lane_partial<NV>(v, ok, 0, 0.0f)), 0.0f, xg, n4, per);
+    const float mean = static_cast<float>(s / count);
+    const double s2 =
+        split_exchange<NV>(a, tag, gi, ci, 1, wave_sum(lane_partial<NV>(v, ok, 1, mean)), mean, xg, n4, per);
+    const float var = static_cast<float>(s2 / count);
     const float scale = 1.0f / sqrtf(var + a.eps);
 #pragma unroll
     for (int k = 0; k < NV; k++) {
@@ -499,14 +528,15 @@ __global__ __launch_bounds__(kSplitThreads) void k_group_norm_split(GnArgs a, Gn
             float t = (get(v[k], e) - mean) * scale;
             if (a.w) t = t * wv[k];
             if (a.b) t = t + bv[k];
+            if constexpr (ACT == 2) t = act_mish(t);
             set(v[k], e, t);
         }
     }
-    if constexpr (ACT) apply_act_vec<NV>(a.act, v, a.tab, 0.0f);
+    if constexpr (ACT == 1) apply_act_vec<NV>(a.act, v, a.tab, 0.0f);
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        const int64_t qi = q0 + threadIdx.x + static_cast<int64_t>(k) * kSplitThreads;
-        if (ok[k]) Stream<float>::store4(yg + 16 * qi, v[k]);
+        const uint32_t qi = q0 + threadIdx.x + static_cast<uint32_t>(k) * kSplitThreads;
+        if (ok[k]) Stream<float>::store4(yg + 16 * static_cast<uint64_t>(qi), v[k]);
     }
 }
 
@@ -571,14 +601,14 @@ void gn_vec(const GnArgs& a, int nv, uint32_t n_chunks, uint32_t n_gi, hipStream
     }
 }
 
-template <bool ACT>
-void gn_split(const GnArgs& a, const GnSplit& sp, int nv, hipStream_t s) {
-    const dim3 grid(kXcds * ((sp.n_gi + kXcds - 1) / kXcds) * sp.n_chunks);
+template <int ACT>
+void gn_split(const GnSplit& sp, uint32_t n_slots, int nv, hipStream_t s) {
+    const dim3 grid(n_slots);
     switch (nv) {
-        case 1: hipLaunchKernelGGL((k_group_norm_split<1, ACT>), grid, dim3(kSplitThreads), 0, s, a, sp); break;
-        case 2: hipLaunchKernelGGL((k_group_norm_split<2, ACT>), grid, dim3(kSplitThreads), 0, s, a, sp); break;
-        case 4: hipLaunchKernelGGL((k_group_norm_split<4, ACT>), grid, dim3(kSplitThreads), 0, s, a, sp); break;
-        default: hipLaunchKernelGGL((k_group_norm_split<8, ACT>), grid, dim3(kSplitThreads), 0, s, a, sp); break;
+        case 1: hipLaunchKernelGGL((k_group_norm_split<1, ACT>), grid, dim3(kSplitThreads), 0, s, sp); break;
+        case 2: hipLaunchKernelGGL((k_group_norm_split<2, ACT>), grid, dim3(kSplitThreads), 0, s, sp); break;
+        case 4: hipLaunchKernelGGL((k_group_norm_split<4, ACT>), grid, dim3(kSplitThreads), 0, s, sp); break;
+        default: hipLaunchKernelGGL((k_group_norm_split<8, ACT>), grid, dim3(kSplitThreads), 0, s, sp); break;
     }
 }
 
@@ -611,13 +641,13 @@ GnArgs gn_args(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w
 }
 
 // Scratch of cbx_group_norm_noalloc, for callers that cannot allocate: the
-// split reduction's exchange words for kSplitMaxSlots chunk slots (32 KiB)
+// split reduction's exchange words for kSplitMaxSlots chunk slots (128 KiB)
 // in the library's own device memory, one copy per GPU, held until the
 // process ends.  Zero at load; the launch tags mean nothing in it ever needs
 // clearing.  Host code must not pass `scratch` itself to a kernel (on the
 // host it names a stand-in, not device memory): group_norm_scratch_setup
 // looks up each device's address once, at cbx_init, and launches use that.
-static __device__ __align__(256) uint64_t scratch[2 * kSplitMaxSlots * 2];
+static __device__ __align__(256) uint64_t scratch[2 * kSplitStageWords];
 
 }  // namespace
 
@@ -636,7 +666,7 @@ int group_norm_scratch_setup(void** out) {
 size_t group_norm_scratch_slots() { return kSplitMaxSlots; }
 
 size_t group_norm_workspace_bytes() {
-    return 2 * kSplitMaxSlots * 2 * sizeof(uint64_t);
+    return 2 * static_cast<size_t>(kSplitStageWords) * sizeof(uint64_t);
 }
 
 int launch_group_norm_split(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
@@ -646,31 +676,46 @@ int launch_group_norm_split(const cbx_tensor* x, int n_groups, float eps, const 
     const int64_t count = x->ne[0] * x->ne[1] * std::min<int64_t>(cpg, x->ne[2]);
     const int64_t n_gi = int64_t{n_groups} * x->ne[3];
     const int64_t n4 = count / 4;
-    // about one 512-lane workgroup per two CUs (measured best on the CFM
-    // shapes: more chunks add dispatch skew to every exchange, fewer leave
-    // the activation and stores to too few SIMDs); at most 8 vectors a lane
-    int64_t n_chunks = n_chunks_req > 0 ? n_chunks_req : cdiv(st->n_cu, int64_t{2} * n_gi);
+    // one 256-lane workgroup per CU (measured best on the CFM shapes against
+    // 8 to 32 chunks of 256 to 1024 lanes: more chunks add participants and
+    // dispatch skew to every exchange, fewer leave the activation and stores
+    // to too few SIMDs); at most 8 vectors a lane
+    int64_t n_chunks = n_chunks_req > 0 ? n_chunks_req : cdiv(st->n_cu, n_gi);
     n_chunks = std::min<int64_t>({n_chunks, kSplitMaxChunks, n4});
     n_chunks = std::max<int64_t>(n_chunks, cdiv(n4, 8 * kSplitThreads));
     const int64_t padded_gi = int64_t{kXcds} * cdiv(n_gi, kXcds);
     // the split applies when the groups are few (n_chunks >= 2) and the
-    // whole grid is resident at once (at most 2 workgroups of 512 lanes a CU)
+    // whole grid is resident at once (at most 2 workgroups a CU)
     if (!gn_vec_layout(x, y) || n_chunks < 2 || n_chunks > kSplitMaxChunks || n_gi * n_chunks > kSplitMaxSlots ||
-        padded_gi * n_chunks > int64_t{2} * st->n_cu) {
+        padded_gi * n_chunks > int64_t{2} * st->n_cu || x->ne[0] * x->ne[1] * cpg >= (int64_t{1} << 30)) {
         return launch_group_norm(x, n_groups, eps, w, b, act, y, st, s);
     }
     const int64_t per = cdiv(n4, n_chunks);
     const int nv = per <= kSplitThreads ? 1 : per <= 2 * kSplitThreads ? 2 : per <= 4 * kSplitThreads ? 4 : 8;
-    GnArgs a = gn_args(x, n_groups, eps, w, b, act, y, st);
     GnSplit sp;
+    sp.x = static_cast<const char*>(x->data);
+    sp.y = static_cast<char*>(y->data);
+    sp.w = w ? static_cast<const float*>(w->data) : nullptr;
+    sp.b = b ? static_cast<const float*>(b->data) : nullptr;
     sp.word = static_cast<uint64_t*>(workspace);
     sp.err = st->err_word;
+    sp.tab = st->gelu_table;
+    sp.x_nb3 = static_cast<int64_t>(x->nb[3]);
+    sp.y_nb3 = static_cast<int64_t>(y->nb[3]);
+    sp.wait_ticks = wait_ticks;
     sp.n_chunks = static_cast<uint32_t>(n_chunks);
     sp.n_gi = static_cast<uint32_t>(n_gi);
-    sp.wait_ticks = wait_ticks;
+    sp.n_groups = static_cast<uint32_t>(n_groups);
+    sp.per_ch = static_cast<uint32_t>(x->ne[0] * x->ne[1]);
+    sp.cpg = static_cast<uint32_t>(cpg);
+    sp.C = static_cast<uint32_t>(x->ne[2]);
+    sp.eps = eps;
+    sp.act = act;
     sp.in_place = x->data == y->data;
-    if (act != CBX_UNARY_NONE) gn_split<true>(a, sp, nv, s);
-    else gn_split<false>(a, sp, nv, s);
+    const uint32_t n_slots = static_cast<uint32_t>(padded_gi * n_chunks);
+    if (act == CBX_UNARY_MISH) gn_split<2>(sp, n_slots, nv, s);
+    else if (act != CBX_UNARY_NONE) gn_split<1>(sp, n_slots, nv, s);
+    else gn_split<0>(sp, n_slots, nv, s);
     return check_launch("group_norm");
 }
 
