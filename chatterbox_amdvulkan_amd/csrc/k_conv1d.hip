@@ -434,6 +434,309 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
     }
 }
 
+// ---- pipelined form ---------------------------------------------------------
+// Long stride-1 convs (the vocoder's ResBlock convs on 48000-frame stages):
+// in k_conv1d every workgroup of the launch is resident at once, so all of
+// them stage their windows together (HBM busy, matrix cores idle), then run
+// the MFMA loop together (HBM idle), then store together.  Here one
+// workgroup per CU owns one output tile of BT = WM*MT*32 frames x BC =
+// WN*NT*32 channels with 8 waves: waves 0-3 run the MFMA loop (one wave
+// tile each), waves 4-7 stage the activated input window of the next
+// 64-channel chunk into the other of two LDS buffers meanwhile, one
+// barrier per chunk; so staging overlaps the matrix cores for all chunks
+// but the first (which all 8 waves stage).  The B fragments stream from
+// global memory through a register ring PF steps deep that runs on across
+// chunk boundaries (the weights do not wait for the staging).  The staging
+// waves read the residual while the last chunk runs, then store the tile
+// (parked in LDS by the MFMA waves) as row-contiguous float4 with the bias
+// and residual added.  The arithmetic per output is k_conv1d's (f16
+// operands, f32 sums), in another order of the reduction's steps.
+constexpr int kPipeKch = 64;          // input channels per chunk
+constexpr int kPipeThreads = 512;     // 4 MFMA waves + 4 staging waves
+constexpr int kPipeCs = kPipeKch + 8; // LDS row stride of a window buffer (halves)
+
+template <int PRO, int MT, int NT, int WM, int WN, int PF>
+__global__ __launch_bounds__(kPipeThreads) void k_conv1d_pipe(ConvArgs a) {
+    static_assert(WM * WN == 4, "four MFMA waves");
+    constexpr int NB = kPipeKch / kBlk;   // 16-channel blocks per chunk
+    constexpr int BT = WM * MT * 32, BC = WN * NT * 32;
+    constexpr int NPT = kPipeThreads / 2;  // staging threads
+    constexpr int cs = kPipeCs;
+    extern __shared__ _Float16 lds[];      // two window buffers of a.win rows; then the output tile
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool stager = wave >= 4;
+    // work item w of the launch, numbered as in k_conv1d (consecutive items
+    // on one XCD)
+    const unsigned L = blockIdx.x, n_wg = gridDim.x;
+    const unsigned q8 = n_wg >> 3, r8 = n_wg & 7, xcd = L & 7, j8 = L >> 3;
+    const unsigned w = xcd < r8 ? xcd * (q8 + 1) + j8 : r8 * (q8 + 1) + (xcd - r8) * q8 + j8;
+    const int ct = static_cast<int>(w % static_cast<unsigned>(a.n_ct));
+    const unsigned wr = w / static_cast<unsigned>(a.n_ct);
+    const int tt = static_cast<int>(wr % static_cast<unsigned>(a.n_tt));
+    const int bz = static_cast<int>(wr / static_cast<unsigned>(a.n_tt));
+    const int t0 = tt * BT, co0 = ct * BC;
+    const char* xb = a.x + static_cast<int64_t>(bz) * a.x_nb2;
+    const int base_t = t0 - a.pad;           // input time of window row 0 (stride 1)
+    const int buf_h = a.win * cs;            // halves per window buffer
+    const int nchunks = a.c_in / kPipeKch;   // the host keeps c_in % 64 == 0
+    const int nblk = a.c_in_pad / kBlk;
+
+    // stage chunk c -- rows [base_t, base_t + win) x channels [64c, 64c + 64)
+    // of pro(x) as f16 -- into buffer c & 1, with NTH threads from thread
+    // tb: thread pt owns the 4-channel group cg of rows pt / 16 + (NTH/16) j.
+    // The loads of a batch of KST rows are all issued before any is used
+    // (rows outside x read the prepared weights, a valid address, and are
+    // zeroed); a batch covers a 192-frame tile's window of a K 11 d 5 conv.
+    // (the lambda captures copies of the fields it reads: a reference to the
+    // by-value kernel argument would put the argument block in scratch)
+    _Float16* const lds0 = lds;
+    const float* const alpha = a.alpha;
+    const float* const alpha_inv = a.alpha_inv;
+    const float* const safe = reinterpret_cast<const float*>(a.w);
+    const int win = a.win, t_in = a.t_in;
+    const int64_t x_nb1 = a.x_nb1;
+    const float slope = a.slope;
+    auto stage = [=](int c, int tb, auto nth_c, auto kst_c) {
+        constexpr int NTH = decltype(nth_c)::value, KST = decltype(kst_c)::value;
+        _Float16* buf = lds0 + (c & 1) * buf_h;
+        constexpr int gpr = kPipeKch / 4;    // 4-channel groups per row
+        constexpr int dr = NTH / gpr;        // rows per pass
+        const int pt = tid - tb;
+        const int r0 = pt / gpr, cg = 4 * (pt % gpr), ci = c * kPipeKch + cg;
+        float al[4] = {0.f, 0.f, 0.f, 0.f}, ai[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (PRO == PRO_SNAKE) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                al[q] = alpha[ci + q];
+                ai[q] = alpha_inv[ci + q];
+            }
+        }
+        float mx = 0.0f;   // snake: the largest |x * alpha| staged (NaN needs no fix-up: both sins give NaN)
+        for (int p0 = 0; p0 * dr < win; p0 += KST) {
+            float4 v[KST];
+#pragma unroll
+            for (int i = 0; i < KST; i++) {
+                const int rr = r0 + (p0 + i) * dr, ti = base_t + rr;
+                const bool ok = rr < win && ti >= 0 && ti < t_in;
+                const float* row = reinterpret_cast<const float*>(xb + static_cast<int64_t>(ok ? ti : 0) * x_nb1);
+                const float4 t = *reinterpret_cast<const float4*>(ok ? row + ci : safe);
+                v[i] = ok ? t : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int i = 0; i < KST; i++) {
+                const int rr = r0 + (p0 + i) * dr;
+                if (rr < win) {
+                    float4 t = v[i];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        if constexpr (PRO == PRO_SNAKE) {
+                            // snake(x) = x + sin(x*a)^2 * a_inv in the reference's op order
+                            const float xv = get(t, q), xa = xv * al[q];
+                            mx = fmaxf(mx, fabsf(xa));
+                            set(t, q, xv + sin_sq_small(xa) * ai[q]);
+                        } else if constexpr (PRO == PRO_LEAKY) {
+                            set(t, q, act_leaky(get(t, q), slope));
+                        }
+                    }
+                    half4 hv;
+                    hv[0] = static_cast<_Float16>(t.x);
+                    hv[1] = static_cast<_Float16>(t.y);
+                    hv[2] = static_cast<_Float16>(t.z);
+                    hv[3] = static_cast<_Float16>(t.w);
+                    *reinterpret_cast<half4*>(buf + rr * cs + cg) = hv;
+                }
+            }
+        }
+        if constexpr (PRO == PRO_SNAKE) {
+            // rare: this thread's elements with an argument of sin at or past
+            // kSinSmall get the library sinf (only this thread wrote them)
+            if (!(mx < kSinSmall)) {
+                for (int rr = r0; rr < win; rr += dr) {
+                    const int ti = base_t + rr;
+                    if (ti < 0 || ti >= t_in) continue;
+                    const float* row = reinterpret_cast<const float*>(xb + static_cast<int64_t>(ti) * x_nb1);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float xv = row[ci + q], xa = xv * al[q];
+                        if (fabsf(xa) < kSinSmall) continue;
+                        const float sn = sinf(xa);
+                        const float s2 = sn * sn;
+                        const float m = s2 * ai[q];
+                        buf[rr * cs + cg + q] = static_cast<_Float16>(xv + m);
+                    }
+                }
+            }
+        }
+    };
+
+    // The two kinds of wave run separate loops with the same barriers (one
+    // after chunk 0 is staged -- by all eight waves --, one per chunk, one
+    // after the tile is parked), so the accumulators and the B ring are
+    // live only in the MFMA waves' code and the staging and epilogue
+    // registers only in the staging waves'.  The staging waves read the
+    // residual while the last chunk runs on the matrix cores, and store the
+    // tile.
+    constexpr int EPS = BC + 4;                     // parked tile row stride (floats)
+    constexpr int C4 = BC / 4;                      // float4 per tile row
+    constexpr int NIT = BT * C4 / NPT;              // float4 of the tile per staging thread
+    static_assert(NPT % C4 == 0 && (BT * C4) % NPT == 0, "staging threads cover whole rows");
+    float* ep = reinterpret_cast<float*>(lds);      // over the window buffers, no longer read
+    if (stager) {
+        stage(0, 0, std::integral_constant<int, kPipeThreads>{}, std::integral_constant<int, 8>{});
+        __syncthreads();
+        const int pt = tid - NPT;
+        const int c4 = 4 * (pt % C4), co = co0 + c4, rl0 = pt / C4;
+        const int64_t yb = static_cast<int64_t>(bz) * a.y_nb2, rb = static_cast<int64_t>(bz) * a.r_nb2;
+        for (int c = 0; c + 1 < nchunks; c++) {
+            stage(c + 1, NPT, std::integral_constant<int, NPT>{}, std::integral_constant<int, 16>{});
+            __syncthreads();
+        }
+        // the last chunk's turn: nothing to stage, the residual is read
+        float4 q[NIT];
+        if (a.res) {
+#pragma unroll
+            for (int i = 0; i < NIT; i++) {
+                const int t = t0 + rl0 + i * (NPT / C4);
+                const int tc = t < a.t_out ? t : a.t_out - 1;
+                q[i] = *reinterpret_cast<const float4*>(a.res + rb + static_cast<int64_t>(tc) * a.r_nb1 +
+                                                        static_cast<int64_t>(co) * 4);
+            }
+        }
+        __syncthreads();
+        __syncthreads();
+        // y = (sum + bias) [+ res]: ggml_add of the bias, then the residual add
+        const float4 bv = a.bias ? *reinterpret_cast<const float4*>(a.bias + co) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < NIT; i++) {
+            const int rl = rl0 + i * (NPT / C4), t = t0 + rl;
+            if (t < a.t_out) {
+                float4 v = *reinterpret_cast<const float4*>(ep + rl * EPS + c4);
+                if (a.bias) v = make_float4(v.x + bv.x, v.y + bv.y, v.z + bv.z, v.w + bv.w);
+                if (a.res) v = make_float4(q[i].x + v.x, q[i].y + v.y, q[i].z + v.z, q[i].w + v.w);
+                *reinterpret_cast<float4*>(a.y + yb + static_cast<int64_t>(t) * a.y_nb1 +
+                                           static_cast<int64_t>(co) * 4) = v;
+            }
+        }
+    } else {
+        floatx16 acc[MT][NT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[mt][nt][r] = 0.0f;
+            }
+        }
+        const int wm = wave / WN, wn = wave % WN;
+        const int lrow = lane & 31, lk = 8 * (lane >> 5);
+        const _Float16* wf[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int co_t = (co0 >> 5) + wn * NT + nt;
+            wf[nt] = a.w + static_cast<int64_t>(co_t) * a.k * nblk * 512 + lane * 8;
+        }
+        int arow[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) arow[mt] = ((wm * MT + mt) * 32 + lrow) * cs + lk;
+        // The steps in order: g = (c * K + k) * NB + blk over the chunks c,
+        // taps k (from the workgroup's first tap k0, cyclically: the
+        // workgroups that share an L2 start on different taps) and 16-channel
+        // blocks blk; B of a step at (k * nblk + c * NB + blk) * 512.  B of
+        // step g sits in ring slot g % PF, read PF steps ahead across chunk
+        // boundaries (the weights do not wait for the staging); A is read
+        // from LDS one step ahead within a chunk, the first step of a chunk
+        // after the chunk's barrier.
+        half8 ring[PF][NT];
+        const int k0 = static_cast<int>(j8 % static_cast<unsigned>(a.k));
+        int cB = 0, iB = 0, kB = k0, bB = 0;   // the step whose B is read next (tap kB, its iB-th)
+        auto b_next = [&](int slot) {
+            const int64_t off = (static_cast<int64_t>(kB) * nblk + cB * NB + bB) * 512;
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) ring[slot][nt] = *reinterpret_cast<const half8*>(wf[nt] + off);
+            if (++bB == NB) {
+                bB = 0;
+                kB = kB + 1 == a.k ? 0 : kB + 1;
+                if (++iB == a.k) {
+                    iB = 0;
+                    if (++cB == nchunks) cB = 0;   // past the last step: the first steps' again (unused)
+                }
+            }
+        };
+#pragma unroll
+        for (int q = 0; q < PF; q++) b_next(q);
+        stage(0, 0, std::integral_constant<int, kPipeThreads>{}, std::integral_constant<int, 8>{});
+        __syncthreads();
+        const _Float16* buf = lds;
+        half8 av[2][MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            av[0][mt] = *reinterpret_cast<const half8*>(buf + arow[mt] + k0 * a.dil * cs);
+        }
+        int cA = 0, iA = 0, kA = k0, bA = 0;   // the step whose A is in av[p & 1]
+        const int total = nchunks * a.k * NB;  // a multiple of PF (the host's choice)
+        for (int g0 = 0; g0 < total; g0 += PF) {
+#pragma unroll
+            for (int p = 0; p < PF; p++) {
+                const int cur = p & 1;
+                int bN = bA + 1, kN = kA, iN = iA, cN = cA;
+                if (bN == NB) {
+                    bN = 0;
+                    kN = kN + 1 == a.k ? 0 : kN + 1;
+                    if (++iN == a.k) {
+                        iN = 0;
+                        ++cN;
+                    }
+                }
+                const bool same = cN == cA;
+                if (same) {
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) {
+                        av[cur ^ 1][mt] = *reinterpret_cast<const half8*>(buf + arow[mt] + kN * a.dil * cs + bN * kBlk);
+                    }
+                }
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++) {
+                        acc[mt][nt] =
+                            __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cur][mt], ring[p][nt], acc[mt][nt], 0, 0, 0);
+                    }
+                }
+                b_next(p);
+                if (!same && cN < nchunks) {
+                    // chunk cN begins: its window has been staged once every
+                    // wave is here
+                    __syncthreads();
+                    buf = lds + (cN & 1) * buf_h;
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) {
+                        av[cur ^ 1][mt] = *reinterpret_cast<const half8*>(buf + arow[mt] + k0 * a.dil * cs);
+                    }
+                }
+                cA = cN;
+                iA = iN;
+                kA = kN;
+                bA = bN;
+            }
+        }
+        __syncthreads();
+        // the tile to LDS: rows of BC + 4 floats
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = (wm * MT + mt) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    ep[row * EPS + (wn * NT + nt) * 32 + lrow] = acc[mt][nt][r];
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // Fragment-major f16 copy of a conv weight, zero padded: fragment (phase,
 // co tile, tap, 16-channel block) is 64 lanes x 8 halves, lane l holding
 // w[co_tile*32 + l%32][block*16 + 8*(l/32) + j] at that tap -- one MFMA B
@@ -600,6 +903,52 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     a.crop = crop;
     a.w_ph = w_ph;
     a.slope = slope;
+    // long stride-1 convs with K >= 5, C_in % 64 == 0 and C_out % 128 == 0
+    // take the pipelined kernel when its 192 x 128 tiles fill the CUs evenly
+    // (one workgroup a CU at a time: at least 3/4 of the CU slots of every
+    // round busy, and at least half the CUs); with K 3 the matrix-core phase
+    // is too short to hide staging behind and k_conv1d is as fast
+    if (up == 1 && stride == 1 && k >= 5 && (pro == PRO_NONE || pro == PRO_SNAKE || pro == PRO_LEAKY) &&
+        a.c_in % kPipeKch == 0 && c_out % 128 == 0) {
+        auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+        const bool one = x->ne[2] <= 1;
+        const bool vec_in = al16(a.x) && a.x_nb1 % 16 == 0 && (one || a.x_nb2 % 16 == 0);
+        const bool vec_out = al16(a.y) && a.y_nb1 % 16 == 0 && (one || a.y_nb2 % 16 == 0) && (!a.bias || al16(a.bias)) &&
+                             (!a.res || (al16(a.res) && a.r_nb1 % 16 == 0 && (one || a.r_nb2 % 16 == 0)));
+        constexpr int PBT = 192, PBC = 128;
+        const int64_t n_cu = st->n_cu > 0 ? st->n_cu : 1;
+        const int64_t items = cdiv(static_cast<int64_t>(a.t_out), int64_t{PBT}) * (c_out / PBC) * x->ne[2];
+        const int64_t rounds = cdiv(items, n_cu);
+        const int64_t pwin = PBT + (k - 1) * static_cast<int64_t>(dil);
+        const size_t plds = std::max<size_t>(2 * static_cast<size_t>(pwin) * kPipeCs * sizeof(_Float16),
+                                             static_cast<size_t>(PBT) * (PBC + 4) * sizeof(float));
+        if (vec_in && vec_out && plds <= kLdsMax && 2 * items >= n_cu && 4 * items >= 3 * rounds * n_cu &&
+            items < (int64_t{1} << 31)) {
+            a.win = static_cast<int32_t>(pwin);
+            a.kch = kPipeKch;
+            a.vout = 1;
+            a.n_tt = static_cast<int32_t>(cdiv(static_cast<int64_t>(a.t_out), int64_t{PBT}));
+            a.n_ct = static_cast<int32_t>(c_out / PBC);
+            const dim3 grid(static_cast<unsigned>(items)), block(kPipeThreads);
+            // the B ring 8 steps (two taps) deep when the step count allows
+            const bool pf8 = (a.c_in / kPipeKch) * k % 2 == 0;
+            switch (pro) {
+                case PRO_SNAKE:
+                    if (pf8) conv_launch(k_conv1d_pipe<PRO_SNAKE, 3, 2, 2, 2, 8>, grid, block, plds, s, a);
+                    else conv_launch(k_conv1d_pipe<PRO_SNAKE, 3, 2, 2, 2, 4>, grid, block, plds, s, a);
+                    break;
+                case PRO_LEAKY:
+                    if (pf8) conv_launch(k_conv1d_pipe<PRO_LEAKY, 3, 2, 2, 2, 8>, grid, block, plds, s, a);
+                    else conv_launch(k_conv1d_pipe<PRO_LEAKY, 3, 2, 2, 2, 4>, grid, block, plds, s, a);
+                    break;
+                default:
+                    if (pf8) conv_launch(k_conv1d_pipe<PRO_NONE, 3, 2, 2, 2, 8>, grid, block, plds, s, a);
+                    else conv_launch(k_conv1d_pipe<PRO_NONE, 3, 2, 2, 2, 4>, grid, block, plds, s, a);
+                    break;
+            }
+            return check_launch("conv1d");
+        }
+    }
     // a transposed conv with stride up > 1 runs its up output phases as
     // stride-1 convs of ceil(T_out / up) rows each, side by side in grid z
     const int64_t batch = x->ne[2] * (up > 1 ? up : 1);

@@ -309,3 +309,58 @@ def test_input_channels_in_chunks(cbx, oracle):
                                   seed=77)
     got = run(cbx, x, w, 1, 75, 15, cbx.CONV_PRO_SNAKE, al, ai, sl, b, r)
     check(oracle, got, x, w, 1, 75, 15, oracle.CONV_PRO_SNAKE, al, ai, sl, b, r, "C512 K11 d15, two chunks")
+
+
+def pipelined_tiles(C_in, C_out, T_out, B, K):
+    """The launch runs k_conv1d_pipe (192 x 128 tiles, one workgroup a CU)
+    when K >= 5, C_in % 64 == 0, C_out % 128 == 0 and its tiles fill the
+    CUs: at least half of them, and 3/4 of every round's slots."""
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    items = -(-T_out // 192) * (C_out // 128) * (B or 1)
+    rounds = -(-items // n_cu)
+    return (K >= 5 and C_in % 64 == 0 and C_out % 128 == 0 and 2 * items >= n_cu and
+            4 * items >= 3 * rounds * n_cu)
+
+
+PIPE = [  # (C_in, C_out, T, B, K, dilation, prologue, residual)
+    (128, 128, 48000, None, 11, 5, "SNAKE", False),   # the 128-channel stage's ResBlock conv 1, full length
+    (128, 128, 48000, None, 11, 1, "SNAKE", True),    # a conv 2 with the residual, full length
+    (64, 128, 300, 96, 11, 5, "LEAKY", False),        # one 64-channel chunk (the 4-deep ring), a short last tile
+    (256, 128, 400, 64, 7, 3, "NONE", True),          # four chunks, no prologue
+    (128, 128, 400, 64, 5, 2, "SNAKE", False),        # the smallest K taken
+]
+
+
+@pytest.mark.parametrize("C,C_out,T,B,K,dil,pro,residual", PIPE)
+def test_pipelined_kernel(cbx, oracle, C, C_out, T, B, K, dil, pro, residual):
+    """Shapes that take the pipelined kernel (input channels staged in
+    64-channel chunks by four waves while four others run the matrix
+    cores): the ResBlock convs of the 48000-frame stage at full length,
+    batches, one and four chunks, each prologue, bias and residual.  Snake
+    inputs include arguments past 2^16 (the per-thread library-sinf pass)."""
+    pad = (K - 1) // 2 * dil
+    if not pipelined_tiles(C, C_out, T, B, K):
+        pytest.skip("this device's CU count does not route the shape to the pipelined kernel")
+    opro = getattr(oracle, f"CONV_PRO_{pro}")
+    x, w, al, ai, b, r, sl = case(oracle, C, T, C_out, K, 1, pad, dil, opro, with_res=residual, B=B, seed=K + dil)
+    if pro == "SNAKE":
+        x[..., T // 3:T // 3 + 3, 5:9] = np.float32(30000.0)   # |x * alpha| in [15000, 45000]: the compact sin
+        x[..., T // 2, :] = np.float32(-60000.0)              # past 2^16 where alpha > 1.09: the library sinf
+    cpro = cbx.CONV_PRO_LEAKY_RELU if pro == "LEAKY" else getattr(cbx, f"CONV_PRO_{pro}")
+    got = run(cbx, x, w, 1, pad, dil, cpro, al, ai, sl, b, r)
+    check(oracle, got, x, w, 1, pad, dil, opro, al, ai, sl, b, r, f"pipelined C{C}->{C_out} T{T} B{B} K{K} d{dil}")
+
+
+def test_pipelined_in_place_residual(cbx, oracle):
+    """y == res on the pipelined kernel: each output is read and written by
+    the thread that owns it."""
+    C, T, B, K = 128, 400, 64, 7
+    if not pipelined_tiles(C, C, T, B, K):
+        pytest.skip("this device's CU count does not route the shape to the pipelined kernel")
+    x, w, al, ai, b, r, sl = case(oracle, C, T, C, K, 1, 3, 1, oracle.CONV_PRO_SNAKE, with_res=True, B=B, seed=91)
+    wts = cbx.Conv1dWeights(dev(w))
+    rd = dev(r)
+    y = cbx.conv1d(dev(x), wts, 1, 3, 1, cbx.CONV_PRO_SNAKE, dev(al), dev(ai), sl, dev(b), rd, out=rd)
+    assert y is rd
+    check(oracle, host(rd), x, w, 1, 3, 1, oracle.CONV_PRO_SNAKE, al, ai, sl, b, r, "pipelined y == res")
+    wts.close()
