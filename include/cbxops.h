@@ -182,7 +182,7 @@ int cbx_group_norm(const cbx_tensor* x, int n_groups, float eps,
  * that share one must not overlap in time (one stream, or streams ordered
  * by events); give concurrent streams a workspace each.
  *
- * The workspace (32 KiB of device memory on the current device, zeroed once;
+ * The workspace (128 KiB of device memory on the current device, zeroed once;
  * nothing in it needs clearing between calls) has no counterpart in ggml, whose CPU group
  * norm reduces each group on one thread; cbx_group_norm_workspace_create /
  * _destroy are the explicit init/destroy pair of the op.                  */
@@ -191,8 +191,8 @@ int  cbx_group_norm_workspace_create(cbx_group_norm_workspace** out);
 void cbx_group_norm_workspace_destroy(cbx_group_norm_workspace* ws);
 /* A chunk workgroup waits at most max_wait_us for the group's other
  * chunks (default 2000), then computes every chunk's partial itself; 0:
- * never wait (each workgroup reduces the whole group, as cbx_group_norm
- * does).  n_chunks: chunks per group, 0 (default) = automatic, else 2..32.
+ * never wait (each wave reduces the whole group itself from x).
+ * n_chunks: chunks per group, 0 (default) = automatic, else 2..32.
  * The results do not depend on either.  For tests and tuning.             */
 int  cbx_group_norm_workspace_tune(cbx_group_norm_workspace* ws,
                                    uint32_t max_wait_us, int32_t n_chunks);
@@ -202,7 +202,7 @@ int  cbx_group_norm_ws(const cbx_tensor* x, int n_groups, float eps,
                        cbx_stream stream);
 
 /* cbx_group_norm_ws without a workspace: the same kernels and results, the
- * exchange words in the library's own static device memory (32 KiB per GPU,
+ * exchange words in the library's own static device memory (128 KiB per GPU,
  * set up by cbx_init, held until the process ends).  No counterpart in the
  * reference: for callers that cannot allocate device memory at all -- code
  * under HIP graph capture, tight serving loops, harnesses that forbid
