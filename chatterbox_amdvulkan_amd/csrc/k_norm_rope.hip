@@ -88,8 +88,13 @@ __global__ __launch_bounds__(64 * W) void k_layer_norm_rope(NormRopeArgs a) {
 
     // position of the token (ne1 index of x); the row and affine loads go
     // out first, then the cos/sin of each of the lane's elements (table rows
-    // are L2-resident), so the table latency hides under the row loads
+    // are L2-resident), so the table latency hides under the row loads.  The
+    // cos/sin are read for the position the token would have in a sequence
+    // numbered 0, 1, 2, .. (the CFM and S3 transformers' positions) while
+    // its position is still being read, and read again only when it
+    // differs: no second round trip in the common case.
     const uint32_t tok = r % a.n_tok;
+    const int32_t ps = static_cast<int32_t>(tok);
     const int32_t p = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const int32_t*>(a.pos + tok * a.pos_nb0));
     Affine<NV> af;
     af.load_sel(a.w, a.b, reinterpret_cast<const float*>(yr), lane, ne0);
@@ -108,8 +113,8 @@ __global__ __launch_bounds__(64 * W) void k_layer_norm_rope(NormRopeArgs a) {
         // hd % 4 == 0: the vector sits in one head (32-bit: jc < 1024)
         i0[k] = static_cast<int>(static_cast<uint32_t>(jc) % static_cast<uint32_t>(a.hd));
     }
-    if (p >= 0 && p < a.n_pos) {   // uniform
-        const float2* tr = a.table + static_cast<int64_t>(p) * half;
+    auto table_row = [&](int32_t q) {
+        const float2* tr = a.table + static_cast<int64_t>(q) * half;
 #pragma unroll
         for (int k = 0; k < NV; k++) {
             if (a.vec_cs && i0[k] + 4 <= nd) {
@@ -122,6 +127,11 @@ __global__ __launch_bounds__(64 * W) void k_layer_norm_rope(NormRopeArgs a) {
                 }
             }
         }
+    };
+    if (a.n_pos > 0) table_row(ps < a.n_pos ? ps : 0);   // speculative: row ps (row 0 past the table)
+    if (p == ps && p < a.n_pos) {                         // uniform: the speculative row is the token's
+    } else if (p >= 0 && p < a.n_pos) {
+        table_row(p);
     } else {   // positions past the table: the device recurrence
 #pragma unroll
         for (int k = 0; k < NV; k++) {

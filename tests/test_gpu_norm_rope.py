@@ -73,6 +73,29 @@ def test_no_affine_in_place_and_positions_past_table(cbx, oracle):
     cache.close()
 
 
+@pytest.mark.parametrize("n_pos", [0, 1, 45, 2048])
+def test_positions_in_order_and_table_ends(cbx, oracle, n_pos):
+    """Positions 0, 1, .. T-1 (the kernel reads the cos/sin row of position
+    t for token t before the position itself arrives) against tables that
+    end before, inside and after the sequence, and an empty one (no row to
+    read ahead: every position takes the device recurrence); then the same
+    tokens at positions 5, 6, .. (every speculative row is the wrong one)."""
+    B, T = 2, 90
+    x = W.normal(95, (B, T, 512))
+    w = W.normal(96, (512,), 1.0, 0.02)
+    b = W.normal(97, (512,), 0.0, 0.02)
+    cache = cbx.RopeCache(64, mode=2, n_ctx_orig=2048, n_pos=n_pos)
+    for off in (0, 5):
+        pos = np.arange(off, off + T, dtype=np.int32)
+        got = host(cbx.layer_norm_rope(dev(x), dev(w), dev(b), 1e-5, 64, dev(pos), cache))
+        two = cbx.rope_ext(cbx.layer_norm(dev(x), dev(w), dev(b), 1e-5).view(B, T, 8, 64), dev(pos), cache)
+        assert_bitexact(got, host(two).reshape(x.shape), f"n_pos {n_pos}, positions from {off}")
+        ln = oracle.layer_norm(x, w, b, 1e-5)
+        exp = oracle.rope_ext(ln.reshape(B, T, 8, 64), pos, 64, mode=2).reshape(x.shape)
+        assert_close(got, exp, x=ln, what=f"n_pos {n_pos}, positions from {off} vs oracle")
+    cache.close()
+
+
 def test_rejects_bad_shapes(cbx):
     x = dev(W.normal(95, (2, 8, 256)))
     pos = dev(np.arange(8, dtype=np.int32))
