@@ -536,6 +536,60 @@ def bench_softmax(C, W, torch, reps=200):
     return out
 
 
+def graph_exec_costs(C, torch, base, n_blocks, s, calls=100):
+    """Host and device microseconds per call of cbx_graph_compute and of
+    cbx_graph_exec_launch on `n_blocks` T3 blocks' element-wise node lists
+    (3 launches each), each block writing its own intermediates."""
+    import ctypes
+
+    L = C.load()
+    N, D = base["h"].shape
+    F = base["fc_mm"].shape[1]
+    g = C.Graph()
+    T = {k: g.tensor(v) for k, v in base.items()}
+    keep = []
+    for _ in range(n_blocks):
+        t = {k: g.tensor(torch.empty((N, D), dtype=torch.float32, device="cuda"))
+             for k in ("cur", "res", "n", "m", "ln2", "pcur", "h2", "n2", "m2", "ln1")}
+        t.update({k: g.tensor(torch.empty((N, F), dtype=torch.float32, device="cuda")) for k in ("fcb", "gelu")})
+        g.node(C.GOP_ADD, t["cur"], (T["attn_mm"], T["out_b"]))
+        g.node(C.GOP_ADD, t["res"], (t["cur"], T["h"]))
+        g.node(C.GOP_NORM, t["n"], (t["res"],), fparam=1e-5)
+        g.node(C.GOP_MUL, t["m"], (t["n"], T["ln2_w"]))
+        g.node(C.GOP_ADD, t["ln2"], (t["m"], T["ln2_b"]))
+        g.node(C.GOP_ADD, t["fcb"], (T["fc_mm"], T["fc_b"]))
+        g.node(C.GOP_UNARY, t["gelu"], (t["fcb"],), iparam=C.GELU)
+        g.node(C.GOP_ADD, t["pcur"], (T["proj_mm"], T["proj_b"]))
+        g.node(C.GOP_ADD, t["h2"], (t["pcur"], t["res"]))
+        g.node(C.GOP_NORM, t["n2"], (t["h2"],), fparam=1e-5)
+        g.node(C.GOP_MUL, t["m2"], (t["n2"], T["ln1_w"]))
+        g.node(C.GOP_ADD, t["ln1"], (t["m2"], T["ln1_b"]))
+        keep += [t["ln2"], t["gelu"], t["h2"], t["ln1"]]
+    Tn, Nn, Kn = g._arrays(keep)
+    n = ctypes.c_int32(0)
+    ex = g.capture(keep)
+
+    def compute():
+        check_rc(C, L.cbx_graph_compute(Tn, len(g._descs), Nn, len(g.nodes), Kn, len(keep), s, ctypes.byref(n)))
+
+    res = {"launches": ex.n_launches}
+    for name, f in (("compute", compute), ("exec", lambda: ex.launch(s))):
+        for _ in range(5):
+            f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        tm = time.perf_counter()
+        e0.record()
+        for _ in range(calls):
+            f()
+        host = (time.perf_counter() - tm) / calls * 1e6
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = {"host_us": host, "device_us": e0.elapsed_time(e1) * 1000.0 / calls}
+    ex.close()
+    return res
+
+
 def bench_t3_block(C, W, torch, reps=300):
     """One T3 block's element-wise nodes at prefill size [512,1024] /
     [512,4096] (t3.cpp:526-546; the matmul outputs given): the residual join
@@ -616,6 +670,12 @@ def bench_t3_block(C, W, torch, reps=300):
     host_us = (time.perf_counter() - tm) / 200 * 1e6
     torch.cuda.synchronize()
     out["graph_compute_host_us_per_call"] = host_us
+    # host cost per call of cbx_graph_compute (plans and launches every
+    # call) against cbx_graph_exec_launch (the list captured once into a HIP
+    # graph), for the block's list and for 16 blocks' lists in one (48
+    # launches; the blocks share the inputs), with the device time per call
+    # of the same back-to-back calls (inputs cache-resident)
+    out["graph_exec"] = {f"{nb}_blocks": graph_exec_costs(C, torch, base, nb, s) for nb in (1, 16)}
     return dict(out, buffer_sets=n_sets)
 
 

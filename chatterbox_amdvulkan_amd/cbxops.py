@@ -203,6 +203,11 @@ def load() -> ctypes.CDLL:
         "cbx_graph_compute": (i, [P, ctypes.c_int32, ctypes.POINTER(GNode), ctypes.c_int32,
                                   ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, vp,
                                   ctypes.POINTER(ctypes.c_int32)]),
+        "cbx_graph_exec_create": (i, [P, ctypes.c_int32, ctypes.POINTER(GNode), ctypes.c_int32,
+                                      ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, ctypes.POINTER(vp),
+                                      ctypes.POINTER(ctypes.c_int32)]),
+        "cbx_graph_exec_launch": (i, [vp, vp]),
+        "cbx_graph_exec_destroy": (None, [vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -880,3 +885,42 @@ class Graph:
         _check(load().cbx_graph_compute(T, len(self._descs), N, len(self.nodes), K, len(keep), _stream(),
                                         ctypes.byref(n)))
         return n.value
+
+    def capture(self, keep=()) -> "GraphExec":
+        """The node list recorded once into a HIP graph (cbx_graph_exec_create)
+        for replays over the same buffers."""
+        return GraphExec(self, keep)
+
+
+class GraphExec:
+    """cbx_graph_exec: a Graph's launches captured into a HIP graph; launch()
+    replays them on torch's current stream.  The graph holds the tensors'
+    addresses: keep the Graph (and its tensors) alive while this is used."""
+
+    def __init__(self, g: Graph, keep=()):
+        for t in g._torch:
+            if t.is_cuda:
+                _ready(t)
+                break
+        T, N, K = g._arrays(keep)
+        h = ctypes.c_void_p()
+        n = ctypes.c_int32(0)
+        _check(load().cbx_graph_exec_create(T, len(g._descs), N, len(g.nodes), K, len(keep), ctypes.byref(h),
+                                            ctypes.byref(n)))
+        self.handle = h
+        self.n_launches = n.value
+        self._graph = g
+
+    def launch(self, stream=None):
+        _check(load().cbx_graph_exec_launch(self.handle, _stream() if stream is None else stream))
+
+    def close(self):
+        if self.handle:
+            load().cbx_graph_exec_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -30,6 +30,7 @@
 // layouts as they do for any caller.
 #include <hip/hip_runtime.h>
 
+#include <new>
 #include <string>
 #include <vector>
 
@@ -899,6 +900,114 @@ int cbx_graph_launch(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gno
     if (rc) return rc;
     if (!launch) return set_error(CBX_ERR_INVALID_ARG, "cbx_graph_launch: launch is NULL");
     return run(tensors, nodes, n_nodes, *launch, stream);
+}
+
+// A planned node list recorded into a HIP graph.  The graph holds the
+// kernels' arguments as they were when it was captured (the tensors'
+// addresses and shapes, the nodes' parameters); a replay runs the same
+// launches on whatever those buffers hold then.
+struct cbx_graph_exec {
+    int device;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    int32_t n_launches;
+};
+
+int cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes,
+                          const int32_t* keep, int32_t n_keep, cbx_graph_exec** out, int32_t* n_launches) {
+    clear_error();
+    static const char* f = "cbx_graph_exec_create";
+    if (n_launches) *n_launches = 0;
+    if (!out) return set_error(CBX_ERR_INVALID_ARG, std::string(f) + ": out is NULL");
+    *out = nullptr;
+    int rc = CBX_OK;
+    if (!current_state(&rc)) return rc;
+    std::vector<cbx_glaunch> ls;
+    rc = plan(tensors, n_tensors, nodes, n_nodes, keep, n_keep, &ls, f);
+    if (rc) return rc;
+    for (const cbx_glaunch& l : ls) {
+        if (l.kind == CBX_GL_UNSUPPORTED) {
+            return set_error(CBX_ERR_UNSUPPORTED, std::string(f) + ": node " + std::to_string(l.first_node) + " (" +
+                                                      op_name(nodes[l.first_node].op) +
+                                                      ") starts no chain the library runs");
+        }
+    }
+    // the launches are recorded on a stream of our own, so nothing else the
+    // caller has queued ends up in the graph
+    hipStream_t cs = nullptr;
+    if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) {
+        return set_error(CBX_ERR_HIP, std::string(f) + ": stream creation failed");
+    }
+    if (hipStreamBeginCapture(cs, hipStreamCaptureModeRelaxed) != hipSuccess) {
+        hipStreamDestroy(cs);
+        return set_error(CBX_ERR_HIP, std::string(f) + ": stream capture failed to start");
+    }
+    int32_t issued = 0;
+    std::string inner;
+    for (const cbx_glaunch& l : ls) {
+        rc = run(tensors, nodes, n_nodes, l, cs);
+        if (rc) {
+            inner = "nodes " + std::to_string(l.first_node) + ".." + std::to_string(l.first_node + l.n_nodes - 1) +
+                    ": " + cbx_last_error();
+            break;
+        }
+        if (l.kind != CBX_GL_VIEW) issued++;
+    }
+    hipGraph_t g = nullptr;
+    const hipError_t ec = hipStreamEndCapture(cs, &g);
+    hipStreamDestroy(cs);
+    if (rc || ec != hipSuccess || !g) {
+        if (g) hipGraphDestroy(g);
+        if (rc) return set_error(rc, std::string(f) + ": " + inner);
+        return set_error(CBX_ERR_HIP, std::string(f) + ": stream capture failed: " + hipGetErrorString(ec));
+    }
+    hipGraphExec_t ge = nullptr;
+    if (hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess || !ge) {
+        hipGraphDestroy(g);
+        return set_error(CBX_ERR_HIP, std::string(f) + ": graph instantiation failed");
+    }
+    auto* x = new (std::nothrow) cbx_graph_exec();
+    if (!x) {
+        hipGraphExecDestroy(ge);
+        hipGraphDestroy(g);
+        return set_error(CBX_ERR_HIP, std::string(f) + ": out of host memory");
+    }
+    hipGetDevice(&x->device);
+    x->graph = g;
+    x->exec = ge;
+    x->n_launches = issued;
+    *out = x;
+    if (n_launches) *n_launches = issued;
+    return CBX_OK;
+}
+
+int cbx_graph_exec_launch(cbx_graph_exec* exec, cbx_stream stream) {
+    clear_error();
+    if (!exec) return set_error(CBX_ERR_INVALID_ARG, "cbx_graph_exec_launch: exec is NULL");
+    int dev = -1;
+    hipGetDevice(&dev);
+    if (dev != exec->device) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_graph_exec_launch: the graph was captured on device " +
+                                                  std::to_string(exec->device) + ", the current device is " +
+                                                  std::to_string(dev));
+    }
+    const hipError_t e = hipGraphLaunch(exec->exec, reinterpret_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+        return set_error(CBX_ERR_HIP, std::string("cbx_graph_exec_launch: ") + hipGetErrorString(e));
+    }
+    return CBX_OK;
+}
+
+void cbx_graph_exec_destroy(cbx_graph_exec* exec) {
+    if (!exec) return;
+    int prev = 0;
+    hipGetDevice(&prev);
+    hipSetDevice(exec->device);
+    hipDeviceSynchronize();   // no replay still in flight
+    hipGraphExecDestroy(exec->exec);
+    hipGraphDestroy(exec->graph);
+    hipSetDevice(prev);
+    delete exec;
 }
 
 int cbx_graph_compute(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes,

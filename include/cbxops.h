@@ -644,6 +644,26 @@ int cbx_graph_compute(const cbx_tensor* tensors, int32_t n_tensors,
                       const int32_t* keep, int32_t n_keep,
                       cbx_stream stream, int32_t* n_launches);
 
+/* The same node list planned once and recorded into a HIP graph, for a
+ * caller that runs one list again and again over the same buffers (a
+ * decode or sampling loop: each step's graph_compute in
+ * t3.cpp:604, cfm_decoder.cpp:596, hift_vocoder.cpp:765 rebuilds and
+ * re-runs an identical node list).  The graph holds the tensors' addresses
+ * and shapes and the nodes' parameters as they are at creation; each
+ * cbx_graph_exec_launch replays every launch on `stream` (one host call,
+ * whatever the launch count) over whatever the buffers hold then.  A
+ * change of address, shape or parameter needs a new exec.  Launch on the
+ * device current at creation.  Unsupported nodes: CBX_ERR_UNSUPPORTED as in
+ * cbx_graph_compute.  *n_launches (may be NULL) gets the kernel launch
+ * count of one replay.  Destroy waits for the device to be idle.          */
+typedef struct cbx_graph_exec cbx_graph_exec;
+int  cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors,
+                           const cbx_gnode* nodes, int32_t n_nodes,
+                           const int32_t* keep, int32_t n_keep,
+                           cbx_graph_exec** out, int32_t* n_launches);
+int  cbx_graph_exec_launch(cbx_graph_exec* exec, cbx_stream stream);
+void cbx_graph_exec_destroy(cbx_graph_exec* exec);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,203 @@
+"""cbx_graph_exec: a node list planned once, recorded into a HIP graph and
+replayed, as a decode or sampling loop would run the same list step after
+step (t3.cpp:604, cfm_decoder.cpp:596, hift_vocoder.cpp:765 call
+graph_compute on an identical node list every step).  Every replay must
+give the bits cbx_graph_compute gives on the same buffers: replays are
+interleaved with the program's own eager work (outputs overwritten with
+NaN, inputs rewritten in place) and synchronisations, and each replay is
+checked.  Node lists: one T3 block's element-wise nodes (three launches),
+LayerNorm -> view -> RoPE, GroupNorm -> affine -> Mish, a HiFT ResBlock
+layer (two conv launches) and the CFM causal block (conv, then LayerNorm
+-> Mish -> mask)."""
+import numpy as np
+import pytest
+import torch
+
+from chatterbox_amdvulkan_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def empty(*shape, dtype=torch.float32):
+    return torch.full(shape, float("nan"), dtype=dtype, device="cuda")
+
+
+def new(shape, dtype=torch.float32):
+    """HiftGraph's allocator: new(shape, dtype)."""
+    return empty(*shape, dtype=dtype)
+
+
+def bits(t):
+    return t.view(torch.int32) if t.dtype == torch.float32 else t.view(torch.int16)
+
+
+def check_replays(g, keep, outs, inputs, n_launches, replays=3):
+    """Two rounds (the inputs as given, then rewritten in place): the eager
+    result of the round, then `replays` replays each checked bit for bit
+    against it, every replay after the outputs are overwritten with NaN."""
+    ex = g.capture(keep)
+    assert ex.n_launches == n_launches
+    try:
+        for rnd in range(2):
+            if rnd:
+                for t in inputs:
+                    t.copy_(t * 0.75 + 0.125)     # new inputs in the same buffers
+            for o in outs:
+                o.fill_(float("nan"))
+            assert g.compute(keep) == n_launches
+            torch.cuda.synchronize()
+            exp = [bits(o).clone() for o in outs]
+            for o in exp:
+                assert o.numel() > 0
+            for r in range(replays):
+                for o in outs:
+                    o.fill_(float("nan"))
+                torch.cuda.synchronize()
+                ex.launch()
+                torch.cuda.synchronize()
+                for k, (o, e) in enumerate(zip(outs, exp)):
+                    assert torch.equal(bits(o), e), f"round {rnd}, replay {r}: output {k} differs from eager"
+        # many replays in flight back to back, then one check
+        for o in outs:
+            o.fill_(float("nan"))
+        for _ in range(20):
+            ex.launch()
+        torch.cuda.synchronize()
+        for k, (o, e) in enumerate(zip(outs, exp)):
+            assert torch.equal(bits(o), e), f"after 20 replays: output {k} differs from eager"
+    finally:
+        ex.close()
+
+
+def test_t3_block_elementwise(cbx):
+    """The residual join + LN2, fc bias + GELU, and the projection's residual
+    join + next LN1 (t3.cpp:526-546, matmul outputs given): 12 nodes, three
+    launches, four kept outputs."""
+    t = {k: dev(v) for k, v in W.t3_block_inputs().items()}
+    N, D, F = W.N_PREFILL, W.D_MODEL, W.D_FF
+    for k in ("cur", "res", "n", "m", "ln2", "pcur", "h2", "n2", "m2", "ln1"):
+        t[k] = empty(N, D)
+    for k in ("fcb", "gelu"):
+        t[k] = empty(N, F)
+    g = cbx.Graph()
+    T = {k: g.tensor(v) for k, v in t.items()}
+    g.node(cbx.GOP_ADD, T["cur"], (T["attn_mm"], T["out_b"]))
+    g.node(cbx.GOP_ADD, T["res"], (T["cur"], T["h"]))
+    g.node(cbx.GOP_NORM, T["n"], (T["res"],), fparam=1e-5)
+    g.node(cbx.GOP_MUL, T["m"], (T["n"], T["ln2_w"]))
+    g.node(cbx.GOP_ADD, T["ln2"], (T["m"], T["ln2_b"]))
+    g.node(cbx.GOP_ADD, T["fcb"], (T["fc_mm"], T["fc_b"]))
+    g.node(cbx.GOP_UNARY, T["gelu"], (T["fcb"],), iparam=cbx.GELU)
+    g.node(cbx.GOP_ADD, T["pcur"], (T["proj_mm"], T["proj_b"]))
+    g.node(cbx.GOP_ADD, T["h2"], (T["pcur"], T["res"]))
+    g.node(cbx.GOP_NORM, T["n2"], (T["h2"],), fparam=1e-5)
+    g.node(cbx.GOP_MUL, T["m2"], (T["n2"], T["ln1_w"]))
+    g.node(cbx.GOP_ADD, T["ln1"], (T["m2"], T["ln1_b"]))
+    keep = [T["ln2"], T["gelu"], T["h2"], T["ln1"]]
+    check_replays(g, keep, [t["ln2"], t["gelu"], t["h2"], t["ln1"]],
+                  [t["attn_mm"], t["h"], t["fc_mm"], t["proj_mm"]], 3)
+
+
+def test_layer_norm_view_rope(cbx):
+    B, T, H, hd = 2, 100, 8, 64
+    x = dev(W.normal(W.seed_of(11, 0), (B, T, H * hd), 0.2, 1.0))
+    w = W.normal(W.seed_of(11, 1), (H * hd,), 1.0, 0.02)
+    b = W.normal(W.seed_of(11, 2), (H * hd,), 0.0, 0.02)
+    pos = np.arange(T, dtype=np.int32)
+    cache = cbx.RopeCache(hd, mode=2, n_ctx_orig=2048, n_pos=2048)
+    g = cbx.Graph()
+    tx, tw, tb, tp = g.tensor(x), g.tensor(dev(w)), g.tensor(dev(b)), g.tensor(dev(pos))
+    n_, m_, y_ = (g.tensor(empty(B, T, H * hd)) for _ in range(3))
+    v_ = g.tensor(g._torch[y_].view(B, T, H, hd))
+    out = empty(B, T, H, hd)
+    r_ = g.tensor(out)
+    g.node(cbx.GOP_NORM, n_, (tx,), fparam=1e-5)
+    g.node(cbx.GOP_MUL, m_, (n_, tw))
+    g.node(cbx.GOP_ADD, y_, (m_, tb))
+    g.node(cbx.GOP_VIEW, v_, (y_,))
+    g.node(cbx.GOP_ROPE, r_, (v_, tp), rope=cache)
+    check_replays(g, [], [out], [x], 1)
+    cache.close()
+
+
+def test_group_norm_affine_mish(cbx):
+    inp = W.cfm_inputs()
+    x = dev(inp["x256"])
+    g = cbx.Graph()
+    tx, tw, tb = g.tensor(x), g.tensor(dev(inp["w256"])), g.tensor(dev(inp["b256"]))
+    buf = [empty(*x.shape) for _ in range(6)]
+    t = [g.tensor(v) for v in buf]
+    g.node(cbx.GOP_GROUP_NORM, t[0], (tx,), iparam=8, fparam=1e-5)
+    g.node(cbx.GOP_MUL, t[1], (t[0], tw))
+    g.node(cbx.GOP_ADD, t[2], (t[1], tb))
+    g.node(cbx.GOP_UNARY, t[3], (t[2],), iparam=cbx.SOFTPLUS)
+    g.node(cbx.GOP_UNARY, t[4], (t[3],), iparam=cbx.TANH)
+    g.node(cbx.GOP_MUL, t[5], (t[2], t[4]))
+    check_replays(g, [], [buf[5]], [x], 1)
+
+
+def test_resblock_layer(cbx):
+    """resblock_forward's layer (hift_vocoder.cpp:131-135): two conv
+    launches, the second reading what the first wrote."""
+    from tests._hift_graph import HiftGraph
+
+    Ch, T, K, d = 128, 700, 11, 3
+    sd = W.seed_of(13, K)
+    h = HiftGraph(new)
+    x = dev(W.normal(sd, (T, Ch), 0.0, 1.0))
+    tx = h.t(x)
+    p, wts = {}, []
+    for k, s in enumerate(("1", "2")):
+        a, ai = W.snake_alpha(Ch, 20 + k)
+        w = W.normal(sd + 1 + k, (Ch, Ch, K), 0.0, 1.0 / np.sqrt(Ch * K))
+        b = W.normal(sd + 3 + k, (Ch,), 0.0, 0.1)
+        for name, v in (("a", a), ("ai", ai), ("w", w), ("b", b)):
+            p[name + s] = h.t(dev(v))
+        wts.append(cbx.Conv1dWeights(h.at(p["w" + s])))
+    y = h.sublayer(tx, p, d, wts[0], wts[1])
+    plan = h.g.plan()
+    assert [q[0] for q in plan] == [cbx.GL_CONV1D] * 2
+    mid = h.at(h.g.nodes[plan[0][2] - 1].dst)
+    check_replays(h.g, [], [mid, h.at(y)], [x], 2)
+    for w_ in wts:
+        w_.close()
+
+
+def test_cfm_causal_block(cbx):
+    """causal_block1d (cfm_decoder.cpp:133-149): mul(x, mask) -> causal
+    conv + bias, then layer_norm -> mish -> mul(mask)."""
+    from tests._hift_graph import HiftGraph
+
+    T, C_in, C_out, K = 500, 256, 256, 3
+    sd = W.seed_of(16, 0)
+    mask = np.ones((T, 1), dtype=np.float32)
+    mask[T - 60:] = 0.0
+    h = HiftGraph(new)
+    x = dev(W.normal(sd, (T, C_in)))
+    w = W.normal(sd + 1, (C_out, C_in, K), 0.0, 1.0 / np.sqrt(C_in * K))
+    vals = (mask, w, W.normal(sd + 2, (C_out,), 0.0, 0.1), W.normal(sd + 3, (C_out,), 1.0, 0.02),
+            W.normal(sd + 4, (C_out,), 0.0, 0.02))
+    tx = h.t(x)
+    tm, tw, tb, tlw, tlb = (h.t(dev(v)) for v in vals)
+    wts = cbx.Conv1dWeights(h.at(tw))
+    y = h.causal_block(tx, tm, tw, tb, tlw, tlb, wts)
+    assert [q[0] for q in h.g.plan()] == [cbx.GL_CAUSAL_CONV1D, cbx.GL_LAYER_NORM_MASK]
+    check_replays(h.g, [], [h.at(h.g.nodes[14].dst), h.at(y)], [x], 2)
+    wts.close()
+
+
+def test_unsupported_node_is_refused(cbx):
+    """A node that starts no chain the library runs: no exec is made."""
+    n, D = 16, 64
+    g = cbx.Graph()
+    a, b, c = g.tensor(dev(np.ones((n, D), np.float32))), g.tensor(dev(np.ones((n, D), np.float32))), \
+        g.tensor(empty(n, D))
+    g.node(cbx.GOP_ADD, c, (a, b))         # a plain add of two activations
+    with pytest.raises(cbx.CbxError) as e:
+        g.capture()
+    assert e.value.status == cbx.ERR_UNSUPPORTED
+    assert "node 0 (ADD)" in str(e.value)

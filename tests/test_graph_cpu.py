@@ -421,6 +421,22 @@ def test_compute_refuses_unsupported_before_any_launch():
     assert "node 8 (ADD)" in C.last_error()
 
 
+def test_graph_exec_argument_errors():
+    """cbx_graph_exec_*: a NULL out or exec is refused before the device is
+    touched, and destroying NULL does nothing (this runs without a GPU)."""
+    L = C.load()
+    g = C.Graph()
+    t3_input(g)
+    T, N, K = _raw(g)
+    n = ctypes.c_int32(-1)
+    rc = L.cbx_graph_exec_create(T, len(g._descs), N, len(g.nodes), K, 0, None, ctypes.byref(n))
+    assert rc == C.ERR_INVALID_ARG and n.value == 0
+    assert "out is NULL" in C.last_error()
+    assert L.cbx_graph_exec_launch(None, None) == C.ERR_INVALID_ARG
+    assert "exec is NULL" in C.last_error()
+    L.cbx_graph_exec_destroy(None)
+
+
 def test_hand_made_launches_stay_inside_the_list():
     L = C.load()
     g = C.Graph()
