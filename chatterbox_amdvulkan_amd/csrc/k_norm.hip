@@ -151,6 +151,13 @@ __global__ __launch_bounds__(64 * W) void k_embed_norm_flat(EmbedFlat a) {
     const int t = static_cast<int>(blockIdx.x);
     const int32_t id = __builtin_amdgcn_readfirstlane(a.ids[t]);
     const int32_t id2 = __builtin_amdgcn_readfirstlane(a.ids2[t]);
+    // the other fields by the time the ids arrive (left alone, the compiler
+    // loads the row strides only after the ids: one more scalar round trip
+    // before the row loads); after the id loads, which stay scalar loads
+    arg_now(a.src); arg_now(a.src2); arg_now(a.w); arg_now(a.b); arg_now(a.h); arg_now(a.y);
+    arg_now(reinterpret_cast<const void*>(a.src_nb1)); arg_now(reinterpret_cast<const void*>(a.src2_nb1));
+    arg_now(reinterpret_cast<const void*>(a.h_nb1)); arg_now(reinterpret_cast<const void*>(a.y_nb1));
+    arg_now(static_cast<uint32_t>(a.src_rows)); arg_now(static_cast<uint32_t>(a.src2_rows));
     const int64_t ne0 = a.ne0;
     char* yr = a.y + t * a.y_nb1;
     char* hr = a.h ? a.h + t * a.h_nb1 : nullptr;
