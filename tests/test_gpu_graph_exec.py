@@ -201,3 +201,20 @@ def test_unsupported_node_is_refused(cbx):
         g.capture()
     assert e.value.status == cbx.ERR_UNSUPPORTED
     assert "node 0 (ADD)" in str(e.value)
+
+
+def test_views_only_list(cbx):
+    """A list of VIEW nodes launches nothing: the exec holds an empty graph
+    and its replays do nothing."""
+    g = cbx.Graph()
+    x = torch.arange(64, dtype=torch.float32, device="cuda")
+    a = g.tensor(x)
+    v = g.tensor(x.view(8, 8))
+    g.node(cbx.GOP_VIEW, v, (a,))
+    ex = g.capture()
+    assert ex.n_launches == 0
+    ex.launch()
+    ex.launch()
+    torch.cuda.synchronize()
+    assert torch.equal(x, torch.arange(64, dtype=torch.float32, device="cuda"))
+    ex.close()
