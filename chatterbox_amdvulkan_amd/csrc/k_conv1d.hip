@@ -455,8 +455,10 @@ constexpr int kPipeKch = 64;          // input channels per chunk
 constexpr int kPipeThreads = 512;     // 4 MFMA waves + 4 staging waves
 constexpr int kPipeCs = kPipeKch + 8; // LDS row stride of a window buffer (halves)
 
-template <int PRO, int MT, int NT, int WM, int WN, int PF>
-__global__ __launch_bounds__(kPipeThreads) void k_conv1d_pipe(ConvArgs a) {
+// OCC: waves per SIMD the register budget is sized for (2: one workgroup a
+// CU; 4: two, whose phases then also overlap each other's)
+template <int PRO, int MT, int NT, int WM, int WN, int PF, int OCC>
+__global__ __launch_bounds__(kPipeThreads) __attribute__((amdgpu_waves_per_eu(OCC))) void k_conv1d_pipe(ConvArgs a) {
     static_assert(WM * WN == 4, "four MFMA waves");
     constexpr int NB = kPipeKch / kBlk;   // 16-channel blocks per chunk
     constexpr int BT = WM * MT * 32, BC = WN * NT * 32;
@@ -904,10 +906,12 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     a.w_ph = w_ph;
     a.slope = slope;
     // long stride-1 convs with K >= 5, C_in % 64 == 0 and C_out % 128 == 0
-    // take the pipelined kernel when its 192 x 128 tiles fill the CUs evenly
-    // (one workgroup a CU at a time: at least 3/4 of the CU slots of every
-    // round busy, and at least half the CUs); with K 3 the matrix-core phase
-    // is too short to hide staging behind and k_conv1d is as fast
+    // take the pipelined kernel: 96 x 128 tiles, two workgroups a CU, when
+    // they fill the CUs' two slots evenly (at least 3/4 of the slots of every
+    // round busy, and a workgroup on every CU); else 192 x 128 tiles, one a
+    // CU, on the same terms for one slot (and at least half the CUs).  With
+    // K 3 the matrix-core phase is too short to hide staging behind and
+    // k_conv1d is as fast
     if (up == 1 && stride == 1 && k >= 5 && (pro == PRO_NONE || pro == PRO_SNAKE || pro == PRO_LEAKY) &&
         a.c_in % kPipeKch == 0 && c_out % 128 == 0) {
         auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
@@ -915,37 +919,44 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
         const bool vec_in = al16(a.x) && a.x_nb1 % 16 == 0 && (one || a.x_nb2 % 16 == 0);
         const bool vec_out = al16(a.y) && a.y_nb1 % 16 == 0 && (one || a.y_nb2 % 16 == 0) && (!a.bias || al16(a.bias)) &&
                              (!a.res || (al16(a.res) && a.r_nb1 % 16 == 0 && (one || a.r_nb2 % 16 == 0)));
-        constexpr int PBT = 192, PBC = 128;
+        constexpr int PBC = 128;
         const int64_t n_cu = st->n_cu > 0 ? st->n_cu : 1;
-        const int64_t items = cdiv(static_cast<int64_t>(a.t_out), int64_t{PBT}) * (c_out / PBC) * x->ne[2];
-        const int64_t rounds = cdiv(items, n_cu);
-        const int64_t pwin = PBT + (k - 1) * static_cast<int64_t>(dil);
-        const size_t plds = std::max<size_t>(2 * static_cast<size_t>(pwin) * kPipeCs * sizeof(_Float16),
-                                             static_cast<size_t>(PBT) * (PBC + 4) * sizeof(float));
-        if (vec_in && vec_out && plds <= kLdsMax && 2 * items >= n_cu && 4 * items >= 3 * rounds * n_cu &&
-            items < (int64_t{1} << 31)) {
-            a.win = static_cast<int32_t>(pwin);
+        auto items_of = [&](int64_t bt) { return cdiv(static_cast<int64_t>(a.t_out), bt) * (c_out / PBC) * x->ne[2]; };
+        auto lds_of = [&](int64_t bt) {
+            const int64_t pwin = bt + (k - 1) * static_cast<int64_t>(dil);
+            return std::max<size_t>(2 * static_cast<size_t>(pwin) * kPipeCs * sizeof(_Float16),
+                                    static_cast<size_t>(bt) * (PBC + 4) * sizeof(float));
+        };
+        // at least `need` workgroups, and every round fills 3/4 of the slots
+        auto fills = [&](int64_t items, int64_t slots, int64_t need) {
+            return items >= need && 4 * items >= 3 * cdiv(items, slots) * slots && items < (int64_t{1} << 31);
+        };
+        const int64_t i96 = items_of(96), i192 = items_of(192);
+        const bool two = 2 * lds_of(96) <= kLdsMax && fills(i96, 2 * n_cu, n_cu);
+        const int64_t PBT = two ? 96 : 192, items = two ? i96 : i192;
+        const size_t plds = lds_of(PBT);
+        if (vec_in && vec_out && plds <= kLdsMax && (two || fills(i192, n_cu, (n_cu + 1) / 2))) {
+            a.win = static_cast<int32_t>(PBT + (k - 1) * static_cast<int64_t>(dil));
             a.kch = kPipeKch;
             a.vout = 1;
-            a.n_tt = static_cast<int32_t>(cdiv(static_cast<int64_t>(a.t_out), int64_t{PBT}));
+            a.n_tt = static_cast<int32_t>(cdiv(static_cast<int64_t>(a.t_out), PBT));
             a.n_ct = static_cast<int32_t>(c_out / PBC);
             const dim3 grid(static_cast<unsigned>(items)), block(kPipeThreads);
             // the B ring 8 steps (two taps) deep when the step count allows
             const bool pf8 = (a.c_in / kPipeKch) * k % 2 == 0;
+#define CBX_PIPE(P)                                                                                       \
+    do {                                                                                                  \
+        if (two && pf8) conv_launch(k_conv1d_pipe<P, 3, 1, 1, 4, 8, 4>, grid, block, plds, s, a);        \
+        else if (two) conv_launch(k_conv1d_pipe<P, 3, 1, 1, 4, 4, 4>, grid, block, plds, s, a);          \
+        else if (pf8) conv_launch(k_conv1d_pipe<P, 3, 2, 2, 2, 8, 2>, grid, block, plds, s, a);          \
+        else conv_launch(k_conv1d_pipe<P, 3, 2, 2, 2, 4, 2>, grid, block, plds, s, a);                   \
+    } while (0)
             switch (pro) {
-                case PRO_SNAKE:
-                    if (pf8) conv_launch(k_conv1d_pipe<PRO_SNAKE, 3, 2, 2, 2, 8>, grid, block, plds, s, a);
-                    else conv_launch(k_conv1d_pipe<PRO_SNAKE, 3, 2, 2, 2, 4>, grid, block, plds, s, a);
-                    break;
-                case PRO_LEAKY:
-                    if (pf8) conv_launch(k_conv1d_pipe<PRO_LEAKY, 3, 2, 2, 2, 8>, grid, block, plds, s, a);
-                    else conv_launch(k_conv1d_pipe<PRO_LEAKY, 3, 2, 2, 2, 4>, grid, block, plds, s, a);
-                    break;
-                default:
-                    if (pf8) conv_launch(k_conv1d_pipe<PRO_NONE, 3, 2, 2, 2, 8>, grid, block, plds, s, a);
-                    else conv_launch(k_conv1d_pipe<PRO_NONE, 3, 2, 2, 2, 4>, grid, block, plds, s, a);
-                    break;
+                case PRO_SNAKE: CBX_PIPE(PRO_SNAKE); break;
+                case PRO_LEAKY: CBX_PIPE(PRO_LEAKY); break;
+                default: CBX_PIPE(PRO_NONE); break;
             }
+#undef CBX_PIPE
             return check_launch("conv1d");
         }
     }

@@ -312,20 +312,26 @@ def test_input_channels_in_chunks(cbx, oracle):
 
 
 def pipelined_tiles(C_in, C_out, T_out, B, K):
-    """The launch runs k_conv1d_pipe (192 x 128 tiles, one workgroup a CU)
-    when K >= 5, C_in % 64 == 0, C_out % 128 == 0 and its tiles fill the
-    CUs: at least half of them, and 3/4 of every round's slots."""
+    """The launch runs k_conv1d_pipe when K >= 5, C_in % 64 == 0, C_out %
+    128 == 0 and its tiles fill the CUs: 96 x 128 tiles two a CU (a
+    workgroup on every CU, 3/4 of every round's slots), else 192 x 128
+    tiles one a CU (at least half the CUs, 3/4 of every round's slots)."""
+    if not (K >= 5 and C_in % 64 == 0 and C_out % 128 == 0):
+        return False
     n_cu = torch.cuda.get_device_properties(0).multi_processor_count
-    items = -(-T_out // 192) * (C_out // 128) * (B or 1)
-    rounds = -(-items // n_cu)
-    return (K >= 5 and C_in % 64 == 0 and C_out % 128 == 0 and 2 * items >= n_cu and
-            4 * items >= 3 * rounds * n_cu)
+
+    def fills(bt, slots, need):
+        items = -(-T_out // bt) * (C_out // 128) * (B or 1)
+        return items >= need and 4 * items >= 3 * -(-items // slots) * slots
+
+    return fills(96, 2 * n_cu, n_cu) or fills(192, n_cu, (n_cu + 1) // 2)
 
 
 PIPE = [  # (C_in, C_out, T, B, K, dilation, prologue, residual)
     (128, 128, 48000, None, 11, 5, "SNAKE", False),   # the 128-channel stage's ResBlock conv 1, full length
     (128, 128, 48000, None, 11, 1, "SNAKE", True),    # a conv 2 with the residual, full length
-    (64, 128, 300, 96, 11, 5, "LEAKY", False),        # one 64-channel chunk (the 4-deep ring), a short last tile
+    (64, 128, 300, 96, 11, 5, "LEAKY", False),        # one 64-channel chunk (the 4-deep ring), 96-row tiles
+    (64, 128, 400, 64, 11, 5, "SNAKE", False),        # the same on 192-row tiles, a short last tile
     (256, 128, 400, 64, 7, 3, "NONE", True),          # four chunks, no prologue
     (128, 128, 400, 64, 5, 2, "SNAKE", False),        # the smallest K taken
 ]
