@@ -913,13 +913,14 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     // K 3 the matrix-core phase is too short to hide staging behind and
     // k_conv1d is as fast
     if (up == 1 && stride == 1 && k >= 5 && (pro == PRO_NONE || pro == PRO_SNAKE || pro == PRO_LEAKY) &&
-        a.c_in % kPipeKch == 0 && c_out % 128 == 0) {
+        a.c_in % kPipeKch == 0 && c_out % 64 == 0) {
         auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
         const bool one = x->ne[2] <= 1;
         const bool vec_in = al16(a.x) && a.x_nb1 % 16 == 0 && (one || a.x_nb2 % 16 == 0);
         const bool vec_out = al16(a.y) && a.y_nb1 % 16 == 0 && (one || a.y_nb2 % 16 == 0) && (!a.bias || al16(a.bias)) &&
                              (!a.res || (al16(a.res) && a.r_nb1 % 16 == 0 && (one || a.r_nb2 % 16 == 0)));
-        constexpr int PBC = 128;
+        const bool narrow = c_out % 128 != 0;   // 64-channel output tiles: 128 x 64, two a CU
+        const int64_t PBC = narrow ? 64 : 128;
         const int64_t n_cu = st->n_cu > 0 ? st->n_cu : 1;
         auto items_of = [&](int64_t bt) { return cdiv(static_cast<int64_t>(a.t_out), bt) * (c_out / PBC) * x->ne[2]; };
         auto lds_of = [&](int64_t bt) {
@@ -931,11 +932,12 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
         auto fills = [&](int64_t items, int64_t slots, int64_t need) {
             return items >= need && 4 * items >= 3 * cdiv(items, slots) * slots && items < (int64_t{1} << 31);
         };
-        const int64_t i96 = items_of(96), i192 = items_of(192);
-        const bool two = 2 * lds_of(96) <= kLdsMax && fills(i96, 2 * n_cu, n_cu);
-        const int64_t PBT = two ? 96 : 192, items = two ? i96 : i192;
+        const int64_t t2 = narrow ? 128 : 96;   // rows of the two-a-CU tile
+        const int64_t i2 = items_of(t2), i192 = items_of(192);
+        const bool two = 2 * lds_of(t2) <= kLdsMax && fills(i2, 2 * n_cu, n_cu);
+        const int64_t PBT = two ? t2 : 192, items = two ? i2 : i192;
         const size_t plds = lds_of(PBT);
-        if (vec_in && vec_out && plds <= kLdsMax && (two || fills(i192, n_cu, (n_cu + 1) / 2))) {
+        if (vec_in && vec_out && plds <= kLdsMax && (two || (!narrow && fills(i192, n_cu, (n_cu + 1) / 2)))) {
             a.win = static_cast<int32_t>(PBT + (k - 1) * static_cast<int64_t>(dil));
             a.kch = kPipeKch;
             a.vout = 1;
@@ -946,7 +948,9 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
             const bool pf8 = (a.c_in / kPipeKch) * k % 2 == 0;
 #define CBX_PIPE(P)                                                                                       \
     do {                                                                                                  \
-        if (two && pf8) conv_launch(k_conv1d_pipe<P, 3, 1, 1, 4, 8, 4>, grid, block, plds, s, a);        \
+        if (narrow && pf8) conv_launch(k_conv1d_pipe<P, 2, 1, 2, 2, 8, 4>, grid, block, plds, s, a);     \
+        else if (narrow) conv_launch(k_conv1d_pipe<P, 2, 1, 2, 2, 4, 4>, grid, block, plds, s, a);       \
+        else if (two && pf8) conv_launch(k_conv1d_pipe<P, 3, 1, 1, 4, 8, 4>, grid, block, plds, s, a);   \
         else if (two) conv_launch(k_conv1d_pipe<P, 3, 1, 1, 4, 4, 4>, grid, block, plds, s, a);          \
         else if (pf8) conv_launch(k_conv1d_pipe<P, 3, 2, 2, 2, 8, 2>, grid, block, plds, s, a);          \
         else conv_launch(k_conv1d_pipe<P, 3, 2, 2, 2, 4, 2>, grid, block, plds, s, a);                   \

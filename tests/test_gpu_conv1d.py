@@ -313,17 +313,21 @@ def test_input_channels_in_chunks(cbx, oracle):
 
 def pipelined_tiles(C_in, C_out, T_out, B, K):
     """The launch runs k_conv1d_pipe when K >= 5, C_in % 64 == 0, C_out %
-    128 == 0 and its tiles fill the CUs: 96 x 128 tiles two a CU (a
-    workgroup on every CU, 3/4 of every round's slots), else 192 x 128
-    tiles one a CU (at least half the CUs, 3/4 of every round's slots)."""
-    if not (K >= 5 and C_in % 64 == 0 and C_out % 128 == 0):
+    64 == 0 and its tiles fill the CUs: C_out a multiple of 128 on 96 x 128
+    tiles two a CU (a workgroup on every CU, 3/4 of every round's slots),
+    else 192 x 128 tiles one a CU (at least half the CUs, 3/4 of every
+    round's slots); other C_out on 128 x 64 tiles two a CU."""
+    if not (K >= 5 and C_in % 64 == 0 and C_out % 64 == 0):
         return False
     n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    bc = 64 if C_out % 128 else 128
 
     def fills(bt, slots, need):
-        items = -(-T_out // bt) * (C_out // 128) * (B or 1)
+        items = -(-T_out // bt) * (C_out // bc) * (B or 1)
         return items >= need and 4 * items >= 3 * -(-items // slots) * slots
 
+    if bc == 64:   # 128 x 64 tiles, two a CU, or k_conv1d
+        return fills(128, 2 * n_cu, n_cu)
     return fills(96, 2 * n_cu, n_cu) or fills(192, n_cu, (n_cu + 1) // 2)
 
 
@@ -333,6 +337,8 @@ PIPE = [  # (C_in, C_out, T, B, K, dilation, prologue, residual)
     (64, 128, 300, 96, 11, 5, "LEAKY", False),        # one 64-channel chunk (the 4-deep ring), 96-row tiles
     (64, 128, 400, 64, 11, 5, "SNAKE", False),        # the same on 192-row tiles, a short last tile
     (256, 128, 400, 64, 7, 3, "NONE", True),          # four chunks, no prologue
+    (64, 64, 120000, None, 11, 5, "SNAKE", False),    # the 64-channel stage's ResBlock conv 1, full length
+    (64, 64, 120000, None, 11, 1, "SNAKE", True),     # its conv 2 with the residual
     (128, 128, 400, 64, 5, 2, "SNAKE", False),        # the smallest K taken
 ]
 
