@@ -905,14 +905,15 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     a.crop = crop;
     a.w_ph = w_ph;
     a.slope = slope;
-    // long stride-1 convs with K >= 5, C_in % 64 == 0 and C_out % 128 == 0
-    // take the pipelined kernel: 96 x 128 tiles, two workgroups a CU, when
-    // they fill the CUs' two slots evenly (at least 3/4 of the slots of every
-    // round busy, and a workgroup on every CU); else 192 x 128 tiles, one a
-    // CU, on the same terms for one slot (and at least half the CUs).  With
-    // K 3 the matrix-core phase is too short to hide staging behind and
-    // k_conv1d is as fast
-    if (up == 1 && stride == 1 && k >= 5 && (pro == PRO_NONE || pro == PRO_SNAKE || pro == PRO_LEAKY) &&
+    // long stride-1 convs with K >= 3, C_in % 64 == 0 and C_out % 64 == 0
+    // take the pipelined kernel: 96 x 128 tiles (128 x 64 when C_out is not a
+    // multiple of 128), two workgroups a CU, when they fill the CUs' two
+    // slots evenly (at least 3/4 of the slots of every round busy, and a
+    // workgroup on every CU); else, with K >= 5 and C_out % 128 == 0,
+    // 192 x 128 tiles one a CU on the same terms for one slot (and at least
+    // half the CUs).  One workgroup a CU has too short a matrix-core phase
+    // at K 3 to hide staging behind; two a CU overlap each other's
+    if (up == 1 && stride == 1 && k >= 3 && (pro == PRO_NONE || pro == PRO_SNAKE || pro == PRO_LEAKY) &&
         a.c_in % kPipeKch == 0 && c_out % 64 == 0) {
         auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
         const bool one = x->ne[2] <= 1;
@@ -937,7 +938,7 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
         const bool two = 2 * lds_of(t2) <= kLdsMax && fills(i2, 2 * n_cu, n_cu);
         const int64_t PBT = two ? t2 : 192, items = two ? i2 : i192;
         const size_t plds = lds_of(PBT);
-        if (vec_in && vec_out && plds <= kLdsMax && (two || (!narrow && fills(i192, n_cu, (n_cu + 1) / 2)))) {
+        if (vec_in && vec_out && plds <= kLdsMax && (two || (!narrow && k >= 5 && fills(i192, n_cu, (n_cu + 1) / 2)))) {
             a.win = static_cast<int32_t>(PBT + (k - 1) * static_cast<int64_t>(dil));
             a.kch = kPipeKch;
             a.vout = 1;

@@ -312,12 +312,12 @@ def test_input_channels_in_chunks(cbx, oracle):
 
 
 def pipelined_tiles(C_in, C_out, T_out, B, K):
-    """The launch runs k_conv1d_pipe when K >= 5, C_in % 64 == 0, C_out %
+    """The launch runs k_conv1d_pipe when K >= 3, C_in % 64 == 0, C_out %
     64 == 0 and its tiles fill the CUs: C_out a multiple of 128 on 96 x 128
     tiles two a CU (a workgroup on every CU, 3/4 of every round's slots),
-    else 192 x 128 tiles one a CU (at least half the CUs, 3/4 of every
-    round's slots); other C_out on 128 x 64 tiles two a CU."""
-    if not (K >= 5 and C_in % 64 == 0 and C_out % 64 == 0):
+    else, with K >= 5, 192 x 128 tiles one a CU (at least half the CUs, 3/4
+    of every round's slots); other C_out on 128 x 64 tiles two a CU."""
+    if not (K >= 3 and C_in % 64 == 0 and C_out % 64 == 0):
         return False
     n_cu = torch.cuda.get_device_properties(0).multi_processor_count
     bc = 64 if C_out % 128 else 128
@@ -328,7 +328,7 @@ def pipelined_tiles(C_in, C_out, T_out, B, K):
 
     if bc == 64:   # 128 x 64 tiles, two a CU, or k_conv1d
         return fills(128, 2 * n_cu, n_cu)
-    return fills(96, 2 * n_cu, n_cu) or fills(192, n_cu, (n_cu + 1) // 2)
+    return fills(96, 2 * n_cu, n_cu) or (K >= 5 and fills(192, n_cu, (n_cu + 1) // 2))
 
 
 PIPE = [  # (C_in, C_out, T, B, K, dilation, prologue, residual)
@@ -339,6 +339,8 @@ PIPE = [  # (C_in, C_out, T, B, K, dilation, prologue, residual)
     (256, 128, 400, 64, 7, 3, "NONE", True),          # four chunks, no prologue
     (64, 64, 120000, None, 11, 5, "SNAKE", False),    # the 64-channel stage's ResBlock conv 1, full length
     (64, 64, 120000, None, 11, 1, "SNAKE", True),     # its conv 2 with the residual
+    (128, 128, 48000, None, 3, 1, "SNAKE", True),     # a K 3 conv with the residual, full length
+    (64, 64, 120000, None, 3, 5, "LEAKY", False),     # a K 3 conv on the 128 x 64 tiles
     (128, 128, 400, 64, 5, 2, "SNAKE", False),        # the smallest K taken
 ]
 
