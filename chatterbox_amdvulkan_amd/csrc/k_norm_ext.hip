@@ -52,6 +52,13 @@ template <int NV, bool ACT, int PRO, bool MASK, int WPB, bool FLAT, int WPR = 1>
 __global__ __launch_bounds__(64 * WPB * WPR) void k_ln_ext(LnExtArgs p) {
     static_assert(WPB == 1 || WPR == 1, "rows a workgroup or waves a row, not both");
     __shared__ double lds[2 * WPR];
+    // the rows' addresses in the first batch of argument loads (left alone,
+    // the compiler loads the affine pointers first and the row pointers and
+    // strides in a second scalar round trip before the row loads)
+    arg_now(p.a); arg_now(p.r); arg_now(p.ab); arg_now(p.w); arg_now(p.b); arg_now(p.s); arg_now(p.y);
+    arg_now(reinterpret_cast<const void*>(p.ma.nb1)); arg_now(reinterpret_cast<const void*>(p.mr.nb1));
+    arg_now(reinterpret_cast<const void*>(p.ms.nb1)); arg_now(reinterpret_cast<const void*>(p.my.nb1));
+    arg_now(static_cast<uint32_t>(p.ne0));
     const int lane = WPR > 1 ? (threadIdx.x >> 6) * 64 * NV + (threadIdx.x & 63) : (threadIdx.x & 63);
     uint32_t row = blockIdx.x;
     if constexpr (WPB > 1) {

@@ -32,6 +32,7 @@ struct RopeArgs {
     uint32_t ne1, ne2, n_tail;
     int32_t n_pos;
     RopeParams rp;
+    uint32_t nth;   // k_rope_vec: its block size (a multiple of 64 up to kRopeThreads)
 };
 
 // IT > 0: every pair of the token is one of the lane's first IT (ne1 *
@@ -131,12 +132,23 @@ __global__ __launch_bounds__(kRopeThreads) void k_rope_vec(RopeArgs a) {
     const uint32_t t = blockIdx.x;
     const uint32_t i2 = t % a.ne2, i3 = t / a.ne2;
     const int32_t p = *reinterpret_cast<const int32_t*>(a.pos + i2 * a.pos_nb0);
+    // the fields used once the position is known, in the argument loads that
+    // go out with the position's (left alone, the compiler loads some of them
+    // only after the position has arrived: one more scalar round trip before
+    // the table and row loads); after the position load, which stays scalar
+    arg_now(a.x); arg_now(a.y); arg_now(a.table);
+    arg_now(reinterpret_cast<const void*>(a.xnb1)); arg_now(reinterpret_cast<const void*>(a.xnb2));
+    arg_now(reinterpret_cast<const void*>(a.xnb3)); arg_now(reinterpret_cast<const void*>(a.ynb1));
+    arg_now(reinterpret_cast<const void*>(a.ynb2)); arg_now(reinterpret_cast<const void*>(a.ynb3));
+    arg_now(a.ne1); arg_now(static_cast<uint32_t>(a.n_pos)); arg_now(static_cast<uint32_t>(rp.n_dims));
+    arg_now(a.nth);
+    const uint32_t nth = a.nth;   // the block size (read with the other fields, not from the dispatch packet)
     const bool in_tab = p >= 0 && p < a.n_pos;
     const float2* tr = a.table + static_cast<int64_t>(in_tab ? p : 0) * half;
     constexpr int es = Elt<T>::size;
     const char* xt = a.x + i2 * a.xnb2 + i3 * a.xnb3;
     char* yt = a.y + i2 * a.ynb2 + i3 * a.ynb3;
-    for (uint32_t q = threadIdx.x; q < a.ne1 * per_head; q += blockDim.x) {
+    for (uint32_t q = threadIdx.x; q < a.ne1 * per_head; q += nth) {
         const uint32_t h = q / per_head;
         const uint32_t m = (q - h * per_head) * 4;
         const char* xr = xt + h * a.xnb1;
@@ -173,7 +185,7 @@ __global__ __launch_bounds__(kRopeThreads) void k_rope_vec(RopeArgs a) {
         Elt<T>::store4(yr + ia * es, ya);
         Elt<T>::store4(yr + ib * es, yb);
     }
-    for (uint32_t q = threadIdx.x; q < a.ne1 * a.n_tail; q += blockDim.x) {
+    for (uint32_t q = threadIdx.x; q < a.ne1 * a.n_tail; q += nth) {
         const uint32_t h = q / a.n_tail;
         const uint32_t j = static_cast<uint32_t>(rp.n_dims) + (q - h * a.n_tail);
         *reinterpret_cast<T*>(yt + h * a.ynb1 + j * es) = *reinterpret_cast<const T*>(xt + h * a.xnb1 + j * es);
@@ -230,6 +242,7 @@ int launch_rope(const cbx_tensor* x, const cbx_tensor* pos, const RopeParams& p,
     if (vec) {
         const int64_t groups = x->ne[1] * (p.n_dims / 8);
         const dim3 vblock(static_cast<unsigned>(std::min<int64_t>(kRopeThreads, cdiv(groups, 64) * 64)));
+        a.nth = vblock.x;
         if (x->type == CBX_TYPE_F32) {
             if (p.mode == 2) hipLaunchKernelGGL((k_rope_vec<float, 2>), grid, vblock, 0, s, a);
             else hipLaunchKernelGGL((k_rope_vec<float, 0>), grid, vblock, 0, s, a);

@@ -78,6 +78,19 @@ __global__ __launch_bounds__(kGatherThreads) void k_get_rows(GatherArgs a) {
         id2 = *reinterpret_cast<const int32_t*>(a.ids2.p + i10 * a.ids2.nb0 + i11 * a.ids2.nb1 + i12 * a.ids2.nb2);
         ok = ok && id2 >= 0 && id2 < a.src2.rows;
     }
+    // the table and output fields in the argument loads that go out with
+    // the ids' (left alone, the compiler loads some only after the ids have
+    // arrived: one more scalar round trip before the row loads)
+    arg_now(a.src.p); arg_now(reinterpret_cast<const void*>(a.src.nb1));
+    arg_now(reinterpret_cast<const void*>(a.src.nb2)); arg_now(reinterpret_cast<const void*>(a.src.nb3));
+    arg_now(reinterpret_cast<const void*>(a.src.rows)); arg_now(a.dst);
+    arg_now(reinterpret_cast<const void*>(a.dnb1)); arg_now(reinterpret_cast<const void*>(a.dnb2));
+    arg_now(reinterpret_cast<const void*>(a.dnb3)); arg_now(static_cast<uint32_t>(a.ne0));
+    if constexpr (TYPE2 >= 0) {
+        arg_now(a.src2.p); arg_now(reinterpret_cast<const void*>(a.src2.nb1));
+        arg_now(reinterpret_cast<const void*>(a.src2.nb2)); arg_now(reinterpret_cast<const void*>(a.src2.nb3));
+        arg_now(reinterpret_cast<const void*>(a.src2.rows));
+    }
     char* d = a.dst + i10 * a.dnb1 + i11 * a.dnb2 + i12 * a.dnb3;
     // ggml aborts on an out-of-range index; here the row is zeroed and the
     // sticky device error bit is raised for the host to read.  A bad id

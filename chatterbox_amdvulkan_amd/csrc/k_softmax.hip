@@ -46,6 +46,12 @@ struct SoftMaxArgs {
 // FLAT: rows at one stride each, so the row map's flag is not tested either.
 template <int NV, int WPB, bool FLAT>
 __global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
+    // every field in the first batch of argument loads (left alone, the
+    // compiler loads the row count first and the rest after its test: a
+    // second scalar round trip before the row loads)
+    arg_now(a.x); arg_now(a.y); arg_now(reinterpret_cast<const void*>(a.mx.nb1));
+    arg_now(reinterpret_cast<const void*>(a.my.nb1)); arg_now(reinterpret_cast<const void*>(a.n_past));
+    arg_now(static_cast<uint32_t>(a.ne0)); arg_now(static_cast<uint32_t>(a.nr)); arg_now(a.n_q);
     const int lane = threadIdx.x & 63;
     uint32_t r = blockIdx.x;
     if constexpr (WPB > 1) {
