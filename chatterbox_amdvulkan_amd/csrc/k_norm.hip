@@ -45,6 +45,17 @@ struct WaveNormArgs {
 // and nothing tests an argument before the loads are issued.
 template <typename T, int NV, int KIND, bool ACT, int WPB, bool FLAT>
 __global__ __launch_bounds__(64 * WPB) void k_row_norm_wave(WaveNormArgs a) {
+    // every field the loads need in the first batch of argument loads (left
+    // alone, the compiler loads the row count first and the rest after the
+    // bounds test, or the row maps after the affine pointers)
+    arg_now(a.x); arg_now(a.y); arg_now(a.w); arg_now(a.b); arg_now(a.tab);
+    arg_now(reinterpret_cast<const void*>(a.mx.nb1)); arg_now(reinterpret_cast<const void*>(a.my.nb1));
+    arg_now(static_cast<uint32_t>(a.ne0)); arg_now(static_cast<uint32_t>(a.nr));
+    if constexpr (!FLAT) {
+        arg_now(reinterpret_cast<const void*>(a.mx.nb2)); arg_now(reinterpret_cast<const void*>(a.mx.nb3));
+        arg_now(reinterpret_cast<const void*>(a.my.nb2)); arg_now(reinterpret_cast<const void*>(a.my.nb3));
+        arg_now(a.mx.ne1); arg_now(a.mx.ne2); arg_now(a.my.ne1); arg_now(a.my.ne2); arg_now(a.mx.flat); arg_now(a.my.flat);
+    }
     const int lane = threadIdx.x & 63;
     uint32_t r = blockIdx.x;
     if constexpr (WPB > 1) {

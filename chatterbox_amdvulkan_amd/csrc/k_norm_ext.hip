@@ -58,7 +58,17 @@ __global__ __launch_bounds__(64 * WPB * WPR) void k_ln_ext(LnExtArgs p) {
     arg_now(p.a); arg_now(p.r); arg_now(p.ab); arg_now(p.w); arg_now(p.b); arg_now(p.s); arg_now(p.y);
     arg_now(reinterpret_cast<const void*>(p.ma.nb1)); arg_now(reinterpret_cast<const void*>(p.mr.nb1));
     arg_now(reinterpret_cast<const void*>(p.ms.nb1)); arg_now(reinterpret_cast<const void*>(p.my.nb1));
-    arg_now(static_cast<uint32_t>(p.ne0));
+    arg_now(static_cast<uint32_t>(p.ne0)); arg_now(static_cast<uint32_t>(p.nr));
+    if constexpr (MASK) {
+        arg_now(p.mask);
+        arg_now(p.ma.ne1);
+    }
+    if constexpr (!FLAT) {
+        for (const RowMap* m : {&p.ma, &p.mr, &p.ms, &p.my}) {
+            arg_now(reinterpret_cast<const void*>(m->nb2)); arg_now(reinterpret_cast<const void*>(m->nb3));
+            arg_now(m->ne1); arg_now(m->ne2); arg_now(m->flat);
+        }
+    }
     const int lane = WPR > 1 ? (threadIdx.x >> 6) * 64 * NV + (threadIdx.x & 63) : (threadIdx.x & 63);
     uint32_t row = blockIdx.x;
     if constexpr (WPB > 1) {
