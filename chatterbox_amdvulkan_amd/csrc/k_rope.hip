@@ -231,6 +231,7 @@ int launch_rope(const cbx_tensor* x, const cbx_tensor* pos, const RopeParams& p,
     a.n_tail = static_cast<uint32_t>(x->ne[0] - p.n_dims);
     a.n_pos = n_pos;
     a.rp = p;
+    a.nth = kRopeThreads;
     // four pairs a lane with vector loads: the block just covers the
     // token's pair groups (a multiple of 64 lanes, at most kRopeThreads)
     const int64_t al = x->type == CBX_TYPE_F32 ? 16 : 8;
