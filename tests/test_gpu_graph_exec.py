@@ -7,8 +7,9 @@ interleaved with the program's own eager work (outputs overwritten with
 NaN, inputs rewritten in place) and synchronisations, and each replay is
 checked.  Node lists: one T3 block's element-wise nodes (three launches),
 LayerNorm -> view -> RoPE, GroupNorm -> affine -> Mish, a HiFT ResBlock
-layer (two conv launches) and the CFM causal block (conv, then LayerNorm
--> Mish -> mask)."""
+layer (two conv launches), the CFM causal block (conv, then LayerNorm
+-> Mish -> mask), and a decode step whose position changes between
+replays."""
 import numpy as np
 import pytest
 import torch
@@ -218,3 +219,53 @@ def test_views_only_list(cbx):
     torch.cuda.synchronize()
     assert torch.equal(x, torch.arange(64, dtype=torch.float32, device="cuda"))
     ex.close()
+
+
+def test_decode_step_with_new_positions(cbx):
+    """A T3-style decode step (RMSNorm * gain, RoPE of q and k at the
+    token's position, SiLU-gate) replayed as the position and the inputs
+    change from step to step in the same buffers -- positions inside the
+    cos/sin table, at its last row and past it (computed, not read): every
+    replay matches cbx_graph_compute on the same buffers bit for bit."""
+    D, H, hd, F = 1024, 16, 64, 4096
+    x = dev(W.normal(W.seed_of(21, 0), (1, D)))
+    gain = dev(W.normal(W.seed_of(21, 1), (D,), 1.0, 0.05))
+    q = dev(W.normal(W.seed_of(21, 2), (1, H, hd)))
+    k = dev(W.normal(W.seed_of(21, 3), (1, H, hd)))
+    gt = dev(W.normal(W.seed_of(21, 4), (1, F)))
+    up = dev(W.normal(W.seed_of(21, 5), (1, F)))
+    pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+    cache = cbx.RopeCache(hd, mode=2, n_ctx_orig=2048, n_pos=2048)
+    g = cbx.Graph()
+    tx, tg_, tq, tk, tgt, tup, tp = (g.tensor(v) for v in (x, gain, q, k, gt, up, pos))
+    rn, y, qo, ko, s, o = empty(1, D), empty(1, D), empty(1, H, hd), empty(1, H, hd), empty(1, F), empty(1, F)
+    trn, ty, tqo, tko, ts, to = (g.tensor(v) for v in (rn, y, qo, ko, s, o))
+    g.node(cbx.GOP_RMS_NORM, trn, (tx,), fparam=1e-5)
+    g.node(cbx.GOP_MUL, ty, (trn, tg_))
+    g.node(cbx.GOP_ROPE, tqo, (tq, tp), rope=cache)
+    g.node(cbx.GOP_ROPE, tko, (tk, tp), rope=cache)
+    g.node(cbx.GOP_UNARY, ts, (tgt,), iparam=cbx.SILU)
+    g.node(cbx.GOP_MUL, to, (ts, tup))
+    outs = [y, qo, ko, o]
+    ex = g.capture()
+    assert ex.n_launches == 4
+    try:
+        for step, p in enumerate((0, 1, 7, 29, 2047, 3000, 5)):
+            pos.fill_(p)
+            for t in (x, q, k, gt, up):
+                t.copy_(t * 0.875 + 0.0625 * step)
+            for t in outs:
+                t.fill_(float("nan"))
+            assert g.compute() == 4
+            torch.cuda.synchronize()
+            exp = [bits(t).clone() for t in outs]
+            for t in outs:
+                t.fill_(float("nan"))
+            torch.cuda.synchronize()
+            ex.launch()
+            torch.cuda.synchronize()
+            for n, (t, e) in enumerate(zip(outs, exp)):
+                assert torch.equal(bits(t), e), f"position {p}: output {n} differs from eager"
+    finally:
+        ex.close()
+        cache.close()
