@@ -586,6 +586,27 @@ def graph_exec_costs(C, torch, base, n_blocks, s, calls=100):
         e1.record()
         torch.cuda.synchronize()
         res[name] = {"host_us": host, "device_us": e0.elapsed_time(e1) * 1000.0 / calls}
+    # re-pointing the exec at the list (the next step of a loop; here the same
+    # buffers, so the same launches: taken in place) against capturing anew
+    ip = ctypes.c_int32(0)
+    upd = new = 0.0
+    reps = max(1, calls // 5)
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        tm = time.perf_counter()
+        check_rc(C, L.cbx_graph_exec_update(ex.handle, Tn, len(g._descs), Nn, len(g.nodes), Kn, len(keep),
+                                            ctypes.byref(n), ctypes.byref(ip)))
+        upd += time.perf_counter() - tm
+        ex.launch(s)
+        h2 = ctypes.c_void_p()
+        tm = time.perf_counter()
+        check_rc(C, L.cbx_graph_exec_create(Tn, len(g._descs), Nn, len(g.nodes), Kn, len(keep), ctypes.byref(h2),
+                                            ctypes.byref(n)))
+        new += time.perf_counter() - tm
+        L.cbx_graph_exec_destroy(h2)
+    res["update_host_us"] = upd / reps * 1e6
+    res["update_in_place"] = bool(ip.value)
+    res["create_host_us"] = new / reps * 1e6
     ex.close()
     return res
 

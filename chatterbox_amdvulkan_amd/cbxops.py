@@ -207,6 +207,9 @@ def load() -> ctypes.CDLL:
                                       ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, ctypes.POINTER(vp),
                                       ctypes.POINTER(ctypes.c_int32)]),
         "cbx_graph_exec_launch": (i, [vp, vp]),
+        "cbx_graph_exec_update": (i, [vp, P, ctypes.c_int32, ctypes.POINTER(GNode), ctypes.c_int32,
+                                      ctypes.POINTER(ctypes.c_int32), ctypes.c_int32,
+                                      ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]),
         "cbx_graph_exec_destroy": (None, [vp]),
     }
     for name, (res, args) in sigs.items():
@@ -842,6 +845,12 @@ class Graph:
         self._torch.append(t)
         return len(self._descs) - 1
 
+    def rebind(self, i: int, t: torch.Tensor, ggml_type: Optional[int] = None) -> None:
+        """Tensor i of the list becomes t (another buffer, or a view of
+        another length: the next step of a loop)."""
+        self._descs[i] = desc(t, ggml_type)
+        self._torch[i] = t
+
     def node(self, op: int, dst: int, src=(), iparam: int = 0, fparam: float = 0.0,
              rope: Optional[RopeCache] = None, conv=(0, 0, 0), conv_w=None) -> int:
         """conv: (stride, padding, dilation) of an IM2COL node, (stride,) of a
@@ -913,6 +922,25 @@ class GraphExec:
 
     def launch(self, stream=None):
         _check(load().cbx_graph_exec_launch(self.handle, _stream() if stream is None else stream))
+
+    def update(self, g: Graph = None, keep=()) -> bool:
+        """cbx_graph_exec_update: the exec re-pointed at `g` (default: the
+        Graph it was captured from, as it is now -- its tensors re-bound or its
+        nodes' parameters changed).  True when the instantiated graph took the
+        new arguments in place, False when it was re-instantiated."""
+        g = self._graph if g is None else g
+        for t in g._torch:
+            if t.is_cuda:
+                _ready(t)
+                break
+        T, N, K = g._arrays(keep)
+        n = ctypes.c_int32(0)
+        ip = ctypes.c_int32(0)
+        _check(load().cbx_graph_exec_update(self.handle, T, len(g._descs), N, len(g.nodes), K, len(keep),
+                                            ctypes.byref(n), ctypes.byref(ip)))
+        self.n_launches = n.value
+        self._graph = g
+        return bool(ip.value)
 
     def close(self):
         if self.handle:

@@ -913,17 +913,14 @@ struct cbx_graph_exec {
     int32_t n_launches;
 };
 
-int cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes,
-                          const int32_t* keep, int32_t n_keep, cbx_graph_exec** out, int32_t* n_launches) {
-    clear_error();
-    static const char* f = "cbx_graph_exec_create";
-    if (n_launches) *n_launches = 0;
-    if (!out) return set_error(CBX_ERR_INVALID_ARG, std::string(f) + ": out is NULL");
+// Plans the list and records its launches into a new HIP graph (*out);
+// *issued gets the kernel launch count.  f names the caller in errors.
+static int capture_list(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes,
+                        const int32_t* keep, int32_t n_keep, hipGraph_t* out, int32_t* issued, const char* f) {
     *out = nullptr;
-    int rc = CBX_OK;
-    if (!current_state(&rc)) return rc;
+    *issued = 0;
     std::vector<cbx_glaunch> ls;
-    rc = plan(tensors, n_tensors, nodes, n_nodes, keep, n_keep, &ls, f);
+    int rc = plan(tensors, n_tensors, nodes, n_nodes, keep, n_keep, &ls, f);
     if (rc) return rc;
     for (const cbx_glaunch& l : ls) {
         if (l.kind == CBX_GL_UNSUPPORTED) {
@@ -942,7 +939,7 @@ int cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors, const cb
         hipStreamDestroy(cs);
         return set_error(CBX_ERR_HIP, std::string(f) + ": stream capture failed to start");
     }
-    int32_t issued = 0;
+    int32_t n = 0;
     std::string inner;
     for (const cbx_glaunch& l : ls) {
         rc = run(tensors, nodes, n_nodes, l, cs);
@@ -951,7 +948,7 @@ int cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors, const cb
                     ": " + cbx_last_error();
             break;
         }
-        if (l.kind != CBX_GL_VIEW) issued++;
+        if (l.kind != CBX_GL_VIEW) n++;
     }
     hipGraph_t g = nullptr;
     const hipError_t ec = hipStreamEndCapture(cs, &g);
@@ -961,6 +958,24 @@ int cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors, const cb
         if (rc) return set_error(rc, std::string(f) + ": " + inner);
         return set_error(CBX_ERR_HIP, std::string(f) + ": stream capture failed: " + hipGetErrorString(ec));
     }
+    *out = g;
+    *issued = n;
+    return CBX_OK;
+}
+
+int cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes,
+                          const int32_t* keep, int32_t n_keep, cbx_graph_exec** out, int32_t* n_launches) {
+    clear_error();
+    static const char* f = "cbx_graph_exec_create";
+    if (n_launches) *n_launches = 0;
+    if (!out) return set_error(CBX_ERR_INVALID_ARG, std::string(f) + ": out is NULL");
+    *out = nullptr;
+    int rc = CBX_OK;
+    if (!current_state(&rc)) return rc;
+    hipGraph_t g = nullptr;
+    int32_t issued = 0;
+    rc = capture_list(tensors, n_tensors, nodes, n_nodes, keep, n_keep, &g, &issued, f);
+    if (rc) return rc;
     hipGraphExec_t ge = nullptr;
     if (hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess || !ge) {
         hipGraphDestroy(g);
@@ -977,6 +992,63 @@ int cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors, const cb
     x->exec = ge;
     x->n_launches = issued;
     *out = x;
+    if (n_launches) *n_launches = issued;
+    return CBX_OK;
+}
+
+int cbx_graph_exec_update(cbx_graph_exec* exec, const cbx_tensor* tensors, int32_t n_tensors,
+                          const cbx_gnode* nodes, int32_t n_nodes, const int32_t* keep, int32_t n_keep,
+                          int32_t* n_launches, int32_t* in_place) {
+    clear_error();
+    static const char* f = "cbx_graph_exec_update";
+    if (n_launches) *n_launches = 0;
+    if (in_place) *in_place = 0;
+    if (!exec) return set_error(CBX_ERR_INVALID_ARG, std::string(f) + ": exec is NULL");
+    int dev = -1;
+    hipGetDevice(&dev);
+    if (dev != exec->device) {
+        return set_error(CBX_ERR_INVALID_ARG, std::string(f) + ": the graph was captured on device " +
+                                                  std::to_string(exec->device) + ", the current device is " +
+                                                  std::to_string(dev));
+    }
+    int rc = CBX_OK;
+    if (!current_state(&rc)) return rc;
+    hipGraph_t g = nullptr;
+    int32_t issued = 0;
+    rc = capture_list(tensors, n_tensors, nodes, n_nodes, keep, n_keep, &g, &issued, f);
+    if (rc) return rc;   // exec is left as it was
+    // the replays queued so far run with the arguments they were queued
+    // with: nothing is changed before the device has finished them (an event
+    // recorded behind every replay instead cost 4.4 us of device time a
+    // replay of three launches)
+    if (hipDeviceSynchronize() != hipSuccess) {
+        hipGraphDestroy(g);
+        return set_error(CBX_ERR_HIP, std::string(f) + ": waiting for the device failed");
+    }
+    // the same launches with other arguments: the instantiated graph takes
+    // the new arguments in place
+    hipGraphNode_t bad_node = nullptr;
+    hipGraphExecUpdateResult res = hipGraphExecUpdateError;
+    if (issued == exec->n_launches && hipGraphExecUpdate(exec->exec, g, &bad_node, &res) == hipSuccess &&
+        res == hipGraphExecUpdateSuccess) {
+        hipGraphDestroy(exec->graph);
+        exec->graph = g;
+        if (n_launches) *n_launches = issued;
+        if (in_place) *in_place = 1;
+        return CBX_OK;
+    }
+    (void)hipGetLastError();   // a refused update leaves nothing to report
+    // another set of launches: a new instantiation replaces the old one
+    hipGraphExec_t ge = nullptr;
+    if (hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess || !ge) {
+        hipGraphDestroy(g);
+        return set_error(CBX_ERR_HIP, std::string(f) + ": graph instantiation failed");
+    }
+    hipGraphExecDestroy(exec->exec);
+    hipGraphDestroy(exec->graph);
+    exec->exec = ge;
+    exec->graph = g;
+    exec->n_launches = issued;
     if (n_launches) *n_launches = issued;
     return CBX_OK;
 }

@@ -652,7 +652,7 @@ int cbx_graph_compute(const cbx_tensor* tensors, int32_t n_tensors,
  * and shapes and the nodes' parameters as they are at creation; each
  * cbx_graph_exec_launch replays every launch on `stream` (one host call,
  * whatever the launch count) over whatever the buffers hold then.  A
- * change of address, shape or parameter needs a new exec.  Launch on the
+ * change of address, shape or parameter needs cbx_graph_exec_update.  Launch on the
  * device current at creation.  Unsupported nodes: CBX_ERR_UNSUPPORTED as in
  * cbx_graph_compute.  *n_launches (may be NULL) gets the kernel launch
  * count of one replay.  Destroy waits for the device to be idle.          */
@@ -663,6 +663,22 @@ int  cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors,
                            cbx_graph_exec** out, int32_t* n_launches);
 int  cbx_graph_exec_launch(cbx_graph_exec* exec, cbx_stream stream);
 void cbx_graph_exec_destroy(cbx_graph_exec* exec);
+
+/* The exec re-pointed at the list as it is now (the next step of the same
+ * loop: t3.cpp:604's decode graph with the position and the KV views of the
+ * next token).  The list is planned and recorded again; when it gives the
+ * same launches with other arguments (addresses, shapes, positions), the
+ * instantiated graph takes them in place (*in_place = 1), otherwise it is
+ * re-instantiated (*in_place = 0).  Waits first for the device to finish
+ * the work queued on it (hipDeviceSynchronize), so the replays queued so far
+ * run with the arguments they were queued with.  On error
+ * `exec` is left as it was.  Same device as at creation.  *n_launches and
+ * *in_place may be NULL.                                                   */
+int  cbx_graph_exec_update(cbx_graph_exec* exec,
+                           const cbx_tensor* tensors, int32_t n_tensors,
+                           const cbx_gnode* nodes, int32_t n_nodes,
+                           const int32_t* keep, int32_t n_keep,
+                           int32_t* n_launches, int32_t* in_place);
 
 #ifdef __cplusplus
 }

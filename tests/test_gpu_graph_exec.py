@@ -269,3 +269,174 @@ def test_decode_step_with_new_positions(cbx):
     finally:
         ex.close()
         cache.close()
+
+
+def decode_list(cbx, cache, bufs):
+    """The decode step's six nodes over one buffer set (a dict of tensors)."""
+    g = cbx.Graph()
+    ids = {n: g.tensor(bufs[n]) for n in ("x", "gain", "q", "k", "gt", "up", "pos", "rn", "y", "qo", "ko", "s", "o")}
+    g.node(cbx.GOP_RMS_NORM, ids["rn"], (ids["x"],), fparam=1e-5)
+    g.node(cbx.GOP_MUL, ids["y"], (ids["rn"], ids["gain"]))
+    g.node(cbx.GOP_ROPE, ids["qo"], (ids["q"], ids["pos"]), rope=cache)
+    g.node(cbx.GOP_ROPE, ids["ko"], (ids["k"], ids["pos"]), rope=cache)
+    g.node(cbx.GOP_UNARY, ids["s"], (ids["gt"],), iparam=cbx.SILU)
+    g.node(cbx.GOP_MUL, ids["o"], (ids["s"], ids["up"]))
+    return g, ids
+
+
+def decode_bufs(seed, p):
+    D, H, hd, F = 1024, 16, 64, 4096
+    b = {"x": dev(W.normal(W.seed_of(seed, 0), (1, D))), "gain": dev(W.normal(W.seed_of(seed, 1), (D,), 1.0, 0.05)),
+         "q": dev(W.normal(W.seed_of(seed, 2), (1, H, hd))), "k": dev(W.normal(W.seed_of(seed, 3), (1, H, hd))),
+         "gt": dev(W.normal(W.seed_of(seed, 4), (1, F))), "up": dev(W.normal(W.seed_of(seed, 5), (1, F))),
+         "pos": torch.full((1,), p, dtype=torch.int32, device="cuda")}
+    for n, shape in (("rn", (1, D)), ("y", (1, D)), ("qo", (1, H, hd)), ("ko", (1, H, hd)), ("s", (1, F)),
+                     ("o", (1, F))):
+        b[n] = empty(*shape)
+    return b
+
+
+def test_update_to_other_buffers_in_place(cbx):
+    """cbx_graph_exec_update: each step's decode list over its own buffer set
+    and position (the same launches with other addresses and values) is taken
+    by the instantiated graph in place; a replay queued before the update
+    keeps its own arguments (replays and updates alternate with no
+    synchronisation of the test's own before the end; every set is then
+    checked against cbx_graph_compute)."""
+    cache = cbx.RopeCache(64, mode=2, n_ctx_orig=2048, n_pos=2048)
+    sets = [decode_bufs(31 + i, p) for i, p in enumerate((3, 700, 2047, 2500))]
+    outs = ("y", "qo", "ko", "o")
+    exp = []
+    for b in sets:
+        g, _ = decode_list(cbx, cache, b)
+        assert g.compute() == 4
+        torch.cuda.synchronize()
+        exp.append([bits(b[n]).clone() for n in outs])
+        for n in outs:
+            b[n].fill_(float("nan"))
+    torch.cuda.synchronize()
+    g, ids = decode_list(cbx, cache, sets[0])
+    ex = g.capture()
+    try:
+        ex.launch()                                   # set 0, still queued
+        for i in range(1, len(sets)):
+            for n, t in ids.items():
+                g.rebind(t, sets[i][n])
+            assert ex.update() is True, f"set {i}: not updated in place"
+            assert ex.n_launches == 4
+            ex.launch()                               # no synchronisation in between
+        torch.cuda.synchronize()
+        for i, b in enumerate(sets):
+            for n, e in zip(outs, exp[i]):
+                assert torch.equal(bits(b[n]), e), f"set {i}: {n} differs from eager"
+    finally:
+        ex.close()
+        cache.close()
+
+
+def test_update_to_other_lengths(cbx):
+    """LayerNorm -> view -> RoPE over views of T = 100, 37, 512 and 1 tokens of
+    one buffer (a sequence whose length changes between steps, as the KV
+    views of a decode loop do): every replay after an update matches
+    cbx_graph_compute on the same views, whether the graph took the new
+    grid in place or was instantiated again."""
+    B, H, hd, Tmax = 1, 8, 64, 512
+    xa = dev(W.normal(W.seed_of(33, 0), (B, Tmax, H * hd), 0.2, 1.0))
+    w = dev(W.normal(W.seed_of(33, 1), (H * hd,), 1.0, 0.02))
+    b = dev(W.normal(W.seed_of(33, 2), (H * hd,), 0.0, 0.02))
+    posa = torch.arange(Tmax, dtype=torch.int32, device="cuda")
+    bufs = [empty(B, Tmax, H * hd) for _ in range(3)]
+    outa = empty(B, Tmax, H, hd)
+    cache = cbx.RopeCache(hd, mode=2, n_ctx_orig=2048, n_pos=2048)
+
+    def views(T):
+        return ([xa[:, :T], w, b, posa[:T]] + [t[:, :T] for t in bufs] +
+                [bufs[2][:, :T].view(B, T, H, hd), outa[:, :T]])
+
+    g = cbx.Graph()
+    tid = [g.tensor(v) for v in views(100)]
+    tx, tw, tb, tp, n_, m_, y_, v_, r_ = tid
+    g.node(cbx.GOP_NORM, n_, (tx,), fparam=1e-5)
+    g.node(cbx.GOP_MUL, m_, (n_, tw))
+    g.node(cbx.GOP_ADD, y_, (m_, tb))
+    g.node(cbx.GOP_VIEW, v_, (y_,))
+    g.node(cbx.GOP_ROPE, r_, (v_, tp), rope=cache)
+    ex = g.capture()
+    try:
+        for T in (100, 37, 512, 1):
+            for i, v in zip(tid, views(T)):
+                g.rebind(i, v)
+            outa.fill_(float("nan"))
+            assert g.compute() == 1
+            torch.cuda.synchronize()
+            e = bits(outa).clone()
+            outa.fill_(float("nan"))
+            torch.cuda.synchronize()
+            ex.update()
+            assert ex.n_launches == 1
+            ex.launch()
+            torch.cuda.synchronize()
+            assert torch.equal(bits(outa), e), f"T = {T}: differs from eager"
+            assert not torch.isnan(outa[:, :T]).any()
+    finally:
+        ex.close()
+        cache.close()
+
+
+def test_update_to_another_list(cbx):
+    """An update to a list with other launches (the decode step's four, then
+    GroupNorm -> affine -> Mish's one) re-instantiates the graph; an update to
+    a list with an unsupported node fails and leaves the exec as it was."""
+    cache = cbx.RopeCache(64, mode=2, n_ctx_orig=2048, n_pos=2048)
+    b0 = decode_bufs(41, 9)
+    g, _ = decode_list(cbx, cache, b0)
+    assert g.compute() == 4
+    torch.cuda.synchronize()
+    exp0 = [bits(b0[n]).clone() for n in ("y", "qo", "ko", "o")]
+    inp = W.cfm_inputs()
+    x = dev(inp["x256"])
+    g2 = cbx.Graph()
+    tx, tw, tb = g2.tensor(x), g2.tensor(dev(inp["w256"])), g2.tensor(dev(inp["b256"]))
+    buf = [empty(*x.shape) for _ in range(6)]
+    t = [g2.tensor(v) for v in buf]
+    g2.node(cbx.GOP_GROUP_NORM, t[0], (tx,), iparam=8, fparam=1e-5)
+    g2.node(cbx.GOP_MUL, t[1], (t[0], tw))
+    g2.node(cbx.GOP_ADD, t[2], (t[1], tb))
+    g2.node(cbx.GOP_UNARY, t[3], (t[2],), iparam=cbx.SOFTPLUS)
+    g2.node(cbx.GOP_UNARY, t[4], (t[3],), iparam=cbx.TANH)
+    g2.node(cbx.GOP_MUL, t[5], (t[2], t[4]))
+    assert g2.compute() == 1
+    torch.cuda.synchronize()
+    exp2 = bits(buf[5]).clone()
+    g3 = cbx.Graph()
+    a3, b3, c3 = g3.tensor(dev(np.ones((4, 64), np.float32))), g3.tensor(dev(np.ones((4, 64), np.float32))), \
+        g3.tensor(empty(4, 64))
+    g3.node(cbx.GOP_ADD, c3, (a3, b3))
+    ex = g.capture()
+    try:
+        buf[5].fill_(float("nan"))
+        torch.cuda.synchronize()
+        assert ex.update(g2) is False
+        assert ex.n_launches == 1
+        ex.launch()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(buf[5]), exp2)
+        with pytest.raises(cbx.CbxError) as e:
+            ex.update(g3)
+        assert e.value.status == cbx.ERR_UNSUPPORTED
+        buf[5].fill_(float("nan"))
+        torch.cuda.synchronize()
+        ex.launch()                                  # still the GroupNorm list
+        torch.cuda.synchronize()
+        assert torch.equal(bits(buf[5]), exp2)
+        for n in ("y", "qo", "ko", "o"):
+            b0[n].fill_(float("nan"))
+        assert ex.update(g) is False                 # back to the decode list
+        assert ex.n_launches == 4
+        ex.launch()
+        torch.cuda.synchronize()
+        for n, e0 in zip(("y", "qo", "ko", "o"), exp0):
+            assert torch.equal(bits(b0[n]), e0), n
+    finally:
+        ex.close()
+        cache.close()

@@ -434,6 +434,11 @@ def test_graph_exec_argument_errors():
     assert "out is NULL" in C.last_error()
     assert L.cbx_graph_exec_launch(None, None) == C.ERR_INVALID_ARG
     assert "exec is NULL" in C.last_error()
+    ip = ctypes.c_int32(-1)
+    n = ctypes.c_int32(-1)
+    rc = L.cbx_graph_exec_update(None, T, len(g._descs), N, len(g.nodes), K, 0, ctypes.byref(n), ctypes.byref(ip))
+    assert rc == C.ERR_INVALID_ARG and n.value == 0 and ip.value == 0
+    assert "cbx_graph_exec_update: exec is NULL" in C.last_error()
     L.cbx_graph_exec_destroy(None)
 
 
