@@ -337,9 +337,9 @@ def test_update_to_other_buffers_in_place(cbx):
 def test_update_to_other_lengths(cbx):
     """LayerNorm -> view -> RoPE over views of T = 100, 37, 512 and 1 tokens of
     one buffer (a sequence whose length changes between steps, as the KV
-    views of a decode loop do): every replay after an update matches
-    cbx_graph_compute on the same views, whether the graph took the new
-    grid in place or was instantiated again."""
+    views of a decode loop do): every update is taken in place (new grids,
+    and kernel variants where the row count picks another) and every replay
+    after it matches cbx_graph_compute on the same views."""
     B, H, hd, Tmax = 1, 8, 64, 512
     xa = dev(W.normal(W.seed_of(33, 0), (B, Tmax, H * hd), 0.2, 1.0))
     w = dev(W.normal(W.seed_of(33, 1), (H * hd,), 1.0, 0.02))
@@ -362,6 +362,7 @@ def test_update_to_other_lengths(cbx):
     g.node(cbx.GOP_VIEW, v_, (y_,))
     g.node(cbx.GOP_ROPE, r_, (v_, tp), rope=cache)
     ex = g.capture()
+    flags = []
     try:
         for T in (100, 37, 512, 1):
             for i, v in zip(tid, views(T)):
@@ -372,15 +373,56 @@ def test_update_to_other_lengths(cbx):
             e = bits(outa).clone()
             outa.fill_(float("nan"))
             torch.cuda.synchronize()
-            ex.update()
+            flags.append(ex.update())
             assert ex.n_launches == 1
             ex.launch()
             torch.cuda.synchronize()
             assert torch.equal(bits(outa), e), f"T = {T}: differs from eager"
             assert not torch.isnan(outa[:, :T]).any()
+        assert flags == [True] * 4, f"in place per length: {flags}"
     finally:
         ex.close()
         cache.close()
+
+
+def test_update_resblock_to_another_input(cbx):
+    """The HiFT ResBlock layer's two conv launches re-pointed at another
+    input buffer of the same shape (the next utterance's activations): the
+    update goes in place and the replay matches cbx_graph_compute."""
+    from tests._hift_graph import HiftGraph
+
+    Ch, T, K, d = 128, 700, 11, 3
+    sd = W.seed_of(14, K)
+    h = HiftGraph(new)
+    x0 = dev(W.normal(sd, (T, Ch), 0.0, 1.0))
+    x1 = dev(W.normal(sd + 9, (T, Ch), 0.0, 1.0))
+    tx = h.t(x0)
+    p, wts = {}, []
+    for k, s in enumerate(("1", "2")):
+        a, ai = W.snake_alpha(Ch, 30 + k)
+        w = W.normal(sd + 1 + k, (Ch, Ch, K), 0.0, 1.0 / np.sqrt(Ch * K))
+        b = W.normal(sd + 3 + k, (Ch,), 0.0, 0.1)
+        for name, v in (("a", a), ("ai", ai), ("w", w), ("b", b)):
+            p[name + s] = h.t(dev(v))
+        wts.append(cbx.Conv1dWeights(h.at(p["w" + s])))
+    y = h.at(h.sublayer(tx, p, d, wts[0], wts[1]))
+    ex = h.g.capture()
+    try:
+        h.g.rebind(tx, x1)
+        y.fill_(float("nan"))
+        assert h.g.compute() == 2
+        torch.cuda.synchronize()
+        e = bits(y).clone()
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        assert ex.update() is True
+        ex.launch()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(y), e)
+    finally:
+        ex.close()
+        for w_ in wts:
+            w_.close()
 
 
 def test_update_to_another_list(cbx):
