@@ -908,15 +908,19 @@ int cbx_graph_launch(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gno
 // launches on whatever those buffers hold then.
 struct cbx_graph_exec {
     int device;
+    hipStream_t cs;   // the stream its captures are recorded on
     hipGraph_t graph;
     hipGraphExec_t exec;
     int32_t n_launches;
 };
 
-// Plans the list and records its launches into a new HIP graph (*out);
-// *issued gets the kernel launch count.  f names the caller in errors.
+// Plans the list and records its launches on cs (a stream of the exec's
+// own, so nothing else the caller has queued ends up in the graph) into a
+// new HIP graph (*out); *issued gets the kernel launch count.  f names the
+// caller in errors.
 static int capture_list(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes,
-                        const int32_t* keep, int32_t n_keep, hipGraph_t* out, int32_t* issued, const char* f) {
+                        const int32_t* keep, int32_t n_keep, hipStream_t cs, hipGraph_t* out, int32_t* issued,
+                        const char* f) {
     *out = nullptr;
     *issued = 0;
     std::vector<cbx_glaunch> ls;
@@ -929,14 +933,7 @@ static int capture_list(const cbx_tensor* tensors, int32_t n_tensors, const cbx_
                                                       ") starts no chain the library runs");
         }
     }
-    // the launches are recorded on a stream of our own, so nothing else the
-    // caller has queued ends up in the graph
-    hipStream_t cs = nullptr;
-    if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) {
-        return set_error(CBX_ERR_HIP, std::string(f) + ": stream creation failed");
-    }
     if (hipStreamBeginCapture(cs, hipStreamCaptureModeRelaxed) != hipSuccess) {
-        hipStreamDestroy(cs);
         return set_error(CBX_ERR_HIP, std::string(f) + ": stream capture failed to start");
     }
     int32_t n = 0;
@@ -952,7 +949,6 @@ static int capture_list(const cbx_tensor* tensors, int32_t n_tensors, const cbx_
     }
     hipGraph_t g = nullptr;
     const hipError_t ec = hipStreamEndCapture(cs, &g);
-    hipStreamDestroy(cs);
     if (rc || ec != hipSuccess || !g) {
         if (g) hipGraphDestroy(g);
         if (rc) return set_error(rc, std::string(f) + ": " + inner);
@@ -972,22 +968,32 @@ int cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors, const cb
     *out = nullptr;
     int rc = CBX_OK;
     if (!current_state(&rc)) return rc;
+    hipStream_t cs = nullptr;
+    if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) {
+        return set_error(CBX_ERR_HIP, std::string(f) + ": stream creation failed");
+    }
     hipGraph_t g = nullptr;
     int32_t issued = 0;
-    rc = capture_list(tensors, n_tensors, nodes, n_nodes, keep, n_keep, &g, &issued, f);
-    if (rc) return rc;
+    rc = capture_list(tensors, n_tensors, nodes, n_nodes, keep, n_keep, cs, &g, &issued, f);
+    if (rc) {
+        hipStreamDestroy(cs);
+        return rc;
+    }
     hipGraphExec_t ge = nullptr;
     if (hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess || !ge) {
         hipGraphDestroy(g);
+        hipStreamDestroy(cs);
         return set_error(CBX_ERR_HIP, std::string(f) + ": graph instantiation failed");
     }
     auto* x = new (std::nothrow) cbx_graph_exec();
     if (!x) {
         hipGraphExecDestroy(ge);
         hipGraphDestroy(g);
+        hipStreamDestroy(cs);
         return set_error(CBX_ERR_HIP, std::string(f) + ": out of host memory");
     }
     hipGetDevice(&x->device);
+    x->cs = cs;
     x->graph = g;
     x->exec = ge;
     x->n_launches = issued;
@@ -1015,7 +1021,7 @@ int cbx_graph_exec_update(cbx_graph_exec* exec, const cbx_tensor* tensors, int32
     if (!current_state(&rc)) return rc;
     hipGraph_t g = nullptr;
     int32_t issued = 0;
-    rc = capture_list(tensors, n_tensors, nodes, n_nodes, keep, n_keep, &g, &issued, f);
+    rc = capture_list(tensors, n_tensors, nodes, n_nodes, keep, n_keep, exec->cs, &g, &issued, f);
     if (rc) return rc;   // exec is left as it was
     // the replays queued so far run with the arguments they were queued
     // with: nothing is changed before the device has finished them (an event
@@ -1078,6 +1084,7 @@ void cbx_graph_exec_destroy(cbx_graph_exec* exec) {
     hipDeviceSynchronize();   // no replay still in flight
     hipGraphExecDestroy(exec->exec);
     hipGraphDestroy(exec->graph);
+    hipStreamDestroy(exec->cs);
     hipSetDevice(prev);
     delete exec;
 }

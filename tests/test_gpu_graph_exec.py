@@ -9,7 +9,8 @@ checked.  Node lists: one T3 block's element-wise nodes (three launches),
 LayerNorm -> view -> RoPE, GroupNorm -> affine -> Mish, a HiFT ResBlock
 layer (two conv launches), the CFM causal block (conv, then LayerNorm
 -> Mish -> mask), and a decode step whose position changes between
-replays."""
+replays; then cbx_graph_exec_update re-pointing an exec at other buffers,
+other sequence lengths and other lists."""
 import numpy as np
 import pytest
 import torch
