@@ -655,7 +655,9 @@ int cbx_graph_compute(const cbx_tensor* tensors, int32_t n_tensors,
  * change of address, shape or parameter needs cbx_graph_exec_update.  Launch on the
  * device current at creation.  Unsupported nodes: CBX_ERR_UNSUPPORTED as in
  * cbx_graph_compute.  *n_launches (may be NULL) gets the kernel launch
- * count of one replay.  Destroy waits for the device to be idle.          */
+ * count of one replay.  Each exec holds a HIP stream of its own, which its
+ * captures are recorded on (nothing runs on it), until it is destroyed.
+ * Destroy waits for the device to be idle.                                */
 typedef struct cbx_graph_exec cbx_graph_exec;
 int  cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors,
                            const cbx_gnode* nodes, int32_t n_nodes,
