@@ -673,8 +673,10 @@ void cbx_graph_exec_destroy(cbx_graph_exec* exec);
  * instantiated graph takes them in place (*in_place = 1), otherwise it is
  * re-instantiated (*in_place = 0).  Waits first for the device to finish
  * the work queued on it (hipDeviceSynchronize), so the replays queued so far
- * run with the arguments they were queued with.  On error
- * `exec` is left as it was.  Same device as at creation.  *n_launches and
+ * run with the arguments they were queued with.  On an error of planning
+ * or recording (an unsupported node, a bad layout)
+ * `exec` is left as it was; after CBX_ERR_HIP (the new graph could not be
+ * instantiated) destroy it.  Same device as at creation.  *n_launches and
  * *in_place may be NULL.                                                   */
 int  cbx_graph_exec_update(cbx_graph_exec* exec,
                            const cbx_tensor* tensors, int32_t n_tensors,
