@@ -35,7 +35,7 @@ struct NormRopeArgs {
     uint32_t n_tok;        // x.ne1: tokens per batch item (the position index)
     int32_t n_pos;
     float eps;
-    int32_t vec_cs;        // the table is 16-byte aligned with n_dims % 4 == 0: 16-byte cos/sin loads
+    int32_t vec_cs;        // 16-byte cos/sin loads: table 16-byte aligned, n_dims % 4 (NEOX: % 8) == 0
     RopeParams rp;
 };
 
@@ -273,7 +273,13 @@ int launch_layer_norm_rope(const cbx_tensor* x, const cbx_tensor* w, const cbx_t
     a.rp = p;
     const int64_t rows = x->ne[1] * x->ne[2] * x->ne[3];
     if (rows >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "layer_norm_rope: too many rows");
-    a.vec_cs = (reinterpret_cast<uintptr_t>(table) % 16 == 0 && p.n_dims % 4 == 0) ? 1 : 0;
+    // 16-byte cos/sin loads: NORMAL needs n_dims % 4 == 0 (a vector's two
+    // pairs are one float4 of the row); NEOX needs n_dims % 8 == 0, so that
+    // half % 4 == 0 and no vector straddles the half boundary (with
+    // n_dims % 8 == 4 a vector at i0 < half < i0 + 4 would take pairs
+    // half, half + 1 of the next table row for its upper elements)
+    const int vec_mod = p.mode == 2 ? 8 : 4;
+    a.vec_cs = (reinterpret_cast<uintptr_t>(table) % 16 == 0 && p.n_dims % vec_mod == 0) ? 1 : 0;
     const int nv = x->ne[0] <= 256 ? 1 : x->ne[0] <= 512 ? 2 : 4;
     // waves a row: enough for about eight waves a CU, at most 4 and at most
     // one per vector a lane (the rotation reads partners from the LDS row

@@ -37,13 +37,17 @@ def test_cfm_shape(cbx, oracle):
 @pytest.mark.parametrize("C,hd,n_dims,mode", [(256, 64, 64, 2), (1024, 128, 96, 2), (512, 64, 32, 0),
                                               (192, 64, 64, 0), (64, 32, 16, 2), (1000, 40, 40, 2),
                                               (1024, 256, 256, 2), (512, 128, 64, 2), (1024, 128, 128, 0),
-                                              (96, 16, 8, 2)])
+                                              (96, 16, 8, 2), (48, 12, 12, 2), (96, 24, 20, 2),
+                                              (240, 24, 20, 0)])
 def test_shapes_modes_partial_dims(cbx, oracle, C, hd, n_dims, mode):
     """Row widths for every vector count, NORMAL and NEOX pairs, rotation of
     only the first n_dims of each head (the rest copied), ragged C; NEOX
     partners 2 to 32 lanes apart (taken from other lanes' registers) and
     heads that do not tile a wave (hd = 40) or whose half is not a power of
-    two in vectors (n_dims = 96), which take the partners from LDS."""
+    two in vectors (n_dims = 96), which take the partners from LDS; NEOX
+    with n_dims % 8 == 4 (half not a multiple of 4, so one 4-vector of each
+    head straddles the half boundary and its cos/sin are read pair by
+    pair)."""
     T, B = 37, 2
     x = W.normal(90 + C, (B, T, C), 0.3, 2.0)
     w = W.normal(91, (C,), 1.0, 0.05)
