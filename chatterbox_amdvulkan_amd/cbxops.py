@@ -164,6 +164,7 @@ def load() -> ctypes.CDLL:
         "cbx_group_norm_workspace_tune": (i, [vp, ctypes.c_uint32, ctypes.c_int32]),
         "cbx_group_norm_ws": (i, [P, i, f, P, P, i, P, vp, vp]),
         "cbx_group_norm_noalloc": (i, [P, i, f, P, P, i, P, vp]),
+        "cbx_group_norm_split_enabled": (i, [i]),
         "cbx_rope_cache_create": (i, [i, i, i, f, f, f, f, f, f, vp, ctypes.c_int32, ctypes.POINTER(vp)]),
         "cbx_rope_cache_destroy": (None, [vp]),
         "cbx_rope_ext": (i, [P, P, vp, P, vp]),
@@ -418,8 +419,21 @@ def group_norm(x, n_groups, eps, w=None, b=None, act=UNARY_NONE, out=None):
     return out
 
 
+GN_WAIT_AUTO = 0xFFFFFFFF   # CBX_GN_WAIT_AUTO
+
+
+def group_norm_split_enabled(device: Optional[int] = None) -> bool:
+    """cbx_group_norm_split_enabled: whether cbx_init's probe let the split
+    reduction run on the device."""
+    dev = torch.cuda.current_device() if device is None else int(device)
+    init(dev)
+    r = load().cbx_group_norm_split_enabled(dev)
+    _check(min(r, 0))
+    return r == 1
+
+
 class GroupNormWorkspace:
-    """cbx_group_norm_workspace: partial sums and arrival counters of the
+    """cbx_group_norm_workspace: the tagged partial sums of the
     split-reduction GroupNorm (one call at a time per workspace)."""
 
     def __init__(self, device: Optional[int] = None, max_wait_us: Optional[int] = None, n_chunks: int = 0):
@@ -430,7 +444,7 @@ class GroupNormWorkspace:
             _check(load().cbx_group_norm_workspace_create(ctypes.byref(h)))
         self.handle = h
         if max_wait_us is not None or n_chunks:
-            self.tune(2000 if max_wait_us is None else max_wait_us, n_chunks)
+            self.tune(GN_WAIT_AUTO if max_wait_us is None else max_wait_us, n_chunks)
 
     def tune(self, max_wait_us: int, n_chunks: int = 0):
         _check(load().cbx_group_norm_workspace_tune(self.handle, max_wait_us, n_chunks))

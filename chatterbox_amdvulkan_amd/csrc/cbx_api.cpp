@@ -214,6 +214,7 @@ int cbx_init(int device) {
         rc = set_error(CBX_ERR_HIP, "cbx_init: upload failed");
     }
     if (rc == CBX_OK) rc = group_norm_scratch_setup(&st.gn_scratch);
+    if (rc == CBX_OK) rc = group_norm_probe_xcd(&st.gn_split_ok);
     if (rc != CBX_OK) {
         if (st.gelu_table) hipFree(st.gelu_table);
         if (st.err_word) hipFree(st.err_word);
@@ -577,20 +578,23 @@ int cbx_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_tenso
     if (!st) return rc;
     if ((rc = check_group_norm("cbx_group_norm", x, n_groups, eps, w, b, act, y))) return rc;
     if (nelements(x) == 0) return CBX_OK;
-    return launch_group_norm(x, n_groups, eps, w, b, act, y, st, reinterpret_cast<hipStream_t>(stream));
+    // a few large groups out of place: the split reduction over the
+    // library's scratch set for this stream (the split itself sends in-place
+    // calls and the layouts it does not cover to launch_group_norm)
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (int64_t{n_groups} * x->ne[3] <= static_cast<int64_t>(group_norm_scratch_slots())) {
+        return launch_group_norm_split(x, n_groups, eps, w, b, act, y, group_norm_scratch_for(st, s), kGnWaitAuto, 0,
+                                       st, s);
+    }
+    return launch_group_norm(x, n_groups, eps, w, b, act, y, st, s);
 }
 
 struct cbx_group_norm_workspace {
     int      device;
-    void*    mem;          // partial sums and arrival counters, zeroed
-    uint64_t wait_ticks;   // 100 MHz real-time counter ticks
+    void*    mem;          // the partials' tagged exchange words, zeroed once
+    uint64_t wait_ticks;   // 100 MHz real-time counter ticks; kGnWaitAuto: from the launch's size
     int32_t  n_chunks;     // 0: automatic
 };
-
-// The longest a chunk workgroup waits for the others before computing the
-// group's statistics itself: 2 ms, far past the few microseconds a resident
-// grid takes.
-static constexpr uint64_t kGnDefaultWaitTicks = 200000;
 
 int cbx_group_norm_workspace_create(cbx_group_norm_workspace** out) {
     clear_error();
@@ -601,7 +605,7 @@ int cbx_group_norm_workspace_create(cbx_group_norm_workspace** out) {
     auto* ws = new (std::nothrow) cbx_group_norm_workspace();
     if (!ws) return set_error(CBX_ERR_HIP, "cbx_group_norm_workspace_create: out of host memory");
     hipGetDevice(&ws->device);
-    ws->wait_ticks = kGnDefaultWaitTicks;
+    ws->wait_ticks = kGnWaitAuto;
     ws->n_chunks = 0;
     const size_t bytes = group_norm_workspace_bytes();
     if (hipMalloc(&ws->mem, bytes) != hipSuccess) {
@@ -634,9 +638,22 @@ int cbx_group_norm_workspace_tune(cbx_group_norm_workspace* ws, uint32_t max_wai
     if (n_chunks < 0 || n_chunks > 32) {
         return set_error(CBX_ERR_INVALID_ARG, "cbx_group_norm_workspace_tune: n_chunks must be 0 (automatic) .. 32");
     }
-    ws->wait_ticks = static_cast<uint64_t>(max_wait_us) * 100;
+    ws->wait_ticks = max_wait_us == CBX_GN_WAIT_AUTO ? kGnWaitAuto : static_cast<uint64_t>(max_wait_us) * 100;
     ws->n_chunks = n_chunks;
     return CBX_OK;
+}
+
+int cbx_group_norm_split_enabled(int device) {
+    clear_error();
+    if (device < 0 || device >= kMaxDevices) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_group_norm_split_enabled: device out of range");
+    }
+    const DeviceState& st = g_dev[device];
+    if (!st.ready) {
+        return set_error(CBX_ERR_NOT_INITIALIZED,
+                         "cbx_init() has not been called for device " + std::to_string(device));
+    }
+    return st.gn_split_ok ? 1 : 0;
 }
 
 int cbx_group_norm_ws(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
@@ -672,8 +689,9 @@ int cbx_group_norm_noalloc(const cbx_tensor* x, int n_groups, float eps, const c
                                                   " group instances of the library's static scratch");
     }
     if (nelements(x) == 0) return CBX_OK;
-    return launch_group_norm_split(x, n_groups, eps, w, b, act, y, st->gn_scratch, kGnDefaultWaitTicks, 0, st,
-                                   reinterpret_cast<hipStream_t>(stream));
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    return launch_group_norm_split(x, n_groups, eps, w, b, act, y, group_norm_scratch_for(st, s), kGnWaitAuto, 0, st,
+                                   s);
 }
 
 // ---- rope --------------------------------------------------------------------

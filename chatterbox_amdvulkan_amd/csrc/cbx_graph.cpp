@@ -906,13 +906,61 @@ int cbx_graph_launch(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gno
 // kernels' arguments as they were when it was captured (the tensors'
 // addresses and shapes, the nodes' parameters); a replay runs the same
 // launches on whatever those buffers hold then.
+//
+// Two instantiations of it take turns: launches replay inst[cur]; an update
+// re-points the other one, inst[1 - cur], and makes it current.  So an
+// update never changes the arguments of the instantiation whose replays may
+// still be queued: it waits only for the other one's replays, all issued
+// before the previous update.  Events recorded by each update, on every
+// stream the exec was launched on since the one before, mark them (one
+// event a stream per update, none per replay).
+struct GraphInst {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int32_t n_launches = 0;
+};
+
 struct cbx_graph_exec {
     int device;
-    hipStream_t cs;   // the stream its captures are recorded on
-    hipGraph_t graph;
-    hipGraphExec_t exec;
-    int32_t n_launches;
+    hipStream_t cs;                       // the stream its captures are recorded on
+    GraphInst inst[2];
+    int cur;                              // the instantiation launches replay
+    std::vector<hipStream_t> launched;    // streams launched on since the last update
+    std::vector<hipEvent_t> marks;        // recorded at the last update: inst[1 - cur]'s replays
+    std::vector<hipEvent_t> spare;        // events free for reuse
 };
+
+// Waits for the events of the last update (the replays of inst[1 - cur]).
+static int wait_marks(cbx_graph_exec* x, const char* f) {
+    bool ok = true;
+    for (hipEvent_t e : x->marks) {
+        ok = hipEventSynchronize(e) == hipSuccess && ok;
+        x->spare.push_back(e);
+    }
+    x->marks.clear();
+    return ok ? CBX_OK : set_error(CBX_ERR_HIP, std::string(f) + ": waiting for earlier replays failed");
+}
+
+// Records an event on every stream launched on since the last update (they
+// follow every replay of inst[cur] issued so far) into x->marks.
+static int mark_launches(cbx_graph_exec* x, const char* f) {
+    for (hipStream_t st : x->launched) {
+        hipEvent_t e = nullptr;
+        if (!x->spare.empty()) {
+            e = x->spare.back();
+            x->spare.pop_back();
+        } else if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+            return set_error(CBX_ERR_HIP, std::string(f) + ": event creation failed");
+        }
+        if (hipEventRecord(e, st) != hipSuccess) {
+            x->spare.push_back(e);
+            return set_error(CBX_ERR_HIP, std::string(f) + ": recording an event behind the replays failed");
+        }
+        x->marks.push_back(e);
+    }
+    x->launched.clear();
+    return CBX_OK;
+}
 
 // Plans the list and records its launches on cs (a stream of the exec's
 // own, so nothing else the caller has queued ends up in the graph) into a
@@ -972,31 +1020,32 @@ int cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors, const cb
     if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) {
         return set_error(CBX_ERR_HIP, std::string(f) + ": stream creation failed");
     }
-    hipGraph_t g = nullptr;
+    hipGraph_t g[2] = {nullptr, nullptr};
     int32_t issued = 0;
-    rc = capture_list(tensors, n_tensors, nodes, n_nodes, keep, n_keep, cs, &g, &issued, f);
-    if (rc) {
-        hipStreamDestroy(cs);
+    rc = capture_list(tensors, n_tensors, nodes, n_nodes, keep, n_keep, cs, &g[0], &issued, f);
+    if (rc == CBX_OK && hipGraphClone(&g[1], g[0]) != hipSuccess) {
+        rc = set_error(CBX_ERR_HIP, std::string(f) + ": graph clone failed");
+    }
+    hipGraphExec_t ge[2] = {nullptr, nullptr};
+    for (int k = 0; k < 2 && rc == CBX_OK; k++) {
+        if (hipGraphInstantiate(&ge[k], g[k], nullptr, nullptr, 0) != hipSuccess || !ge[k]) {
+            rc = set_error(CBX_ERR_HIP, std::string(f) + ": graph instantiation failed");
+        }
+    }
+    auto* x = rc == CBX_OK ? new (std::nothrow) cbx_graph_exec() : nullptr;
+    if (rc == CBX_OK && !x) rc = set_error(CBX_ERR_HIP, std::string(f) + ": out of host memory");
+    if (rc != CBX_OK) {
+        for (int k = 0; k < 2; k++) {
+            if (ge[k]) (void)hipGraphExecDestroy(ge[k]);
+            if (g[k]) (void)hipGraphDestroy(g[k]);
+        }
+        (void)hipStreamDestroy(cs);
         return rc;
     }
-    hipGraphExec_t ge = nullptr;
-    if (hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess || !ge) {
-        hipGraphDestroy(g);
-        hipStreamDestroy(cs);
-        return set_error(CBX_ERR_HIP, std::string(f) + ": graph instantiation failed");
-    }
-    auto* x = new (std::nothrow) cbx_graph_exec();
-    if (!x) {
-        hipGraphExecDestroy(ge);
-        hipGraphDestroy(g);
-        hipStreamDestroy(cs);
-        return set_error(CBX_ERR_HIP, std::string(f) + ": out of host memory");
-    }
-    hipGetDevice(&x->device);
+    (void)hipGetDevice(&x->device);
     x->cs = cs;
-    x->graph = g;
-    x->exec = ge;
-    x->n_launches = issued;
+    for (int k = 0; k < 2; k++) x->inst[k] = GraphInst{g[k], ge[k], issued};
+    x->cur = 0;
     *out = x;
     if (n_launches) *n_launches = issued;
     return CBX_OK;
@@ -1011,7 +1060,7 @@ int cbx_graph_exec_update(cbx_graph_exec* exec, const cbx_tensor* tensors, int32
     if (in_place) *in_place = 0;
     if (!exec) return set_error(CBX_ERR_INVALID_ARG, std::string(f) + ": exec is NULL");
     int dev = -1;
-    hipGetDevice(&dev);
+    (void)hipGetDevice(&dev);
     if (dev != exec->device) {
         return set_error(CBX_ERR_INVALID_ARG, std::string(f) + ": the graph was captured on device " +
                                                   std::to_string(exec->device) + ", the current device is " +
@@ -1023,22 +1072,23 @@ int cbx_graph_exec_update(cbx_graph_exec* exec, const cbx_tensor* tensors, int32
     int32_t issued = 0;
     rc = capture_list(tensors, n_tensors, nodes, n_nodes, keep, n_keep, exec->cs, &g, &issued, f);
     if (rc) return rc;   // exec is left as it was
-    // the replays queued so far run with the arguments they were queued
-    // with: nothing is changed before the device has finished them (an event
-    // recorded behind every replay instead cost 4.4 us of device time a
-    // replay of three launches)
-    if (hipDeviceSynchronize() != hipSuccess) {
-        hipGraphDestroy(g);
-        return set_error(CBX_ERR_HIP, std::string(f) + ": waiting for the device failed");
+    // the instantiation to re-point is the one not replayed since the last
+    // update: wait for its replays (issued before that update), then mark
+    // the current one's
+    if ((rc = wait_marks(exec, f)) || (rc = mark_launches(exec, f))) {
+        (void)hipGraphDestroy(g);
+        return rc;
     }
+    GraphInst& t = exec->inst[1 - exec->cur];
     // the same launches with other arguments: the instantiated graph takes
     // the new arguments in place
     hipGraphNode_t bad_node = nullptr;
     hipGraphExecUpdateResult res = hipGraphExecUpdateError;
-    if (issued == exec->n_launches && hipGraphExecUpdate(exec->exec, g, &bad_node, &res) == hipSuccess &&
+    if (issued == t.n_launches && hipGraphExecUpdate(t.exec, g, &bad_node, &res) == hipSuccess &&
         res == hipGraphExecUpdateSuccess) {
-        hipGraphDestroy(exec->graph);
-        exec->graph = g;
+        (void)hipGraphDestroy(t.graph);
+        t.graph = g;
+        exec->cur = 1 - exec->cur;
         if (n_launches) *n_launches = issued;
         if (in_place) *in_place = 1;
         return CBX_OK;
@@ -1047,14 +1097,13 @@ int cbx_graph_exec_update(cbx_graph_exec* exec, const cbx_tensor* tensors, int32
     // another set of launches: a new instantiation replaces the old one
     hipGraphExec_t ge = nullptr;
     if (hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess || !ge) {
-        hipGraphDestroy(g);
+        (void)hipGraphDestroy(g);
         return set_error(CBX_ERR_HIP, std::string(f) + ": graph instantiation failed");
     }
-    hipGraphExecDestroy(exec->exec);
-    hipGraphDestroy(exec->graph);
-    exec->exec = ge;
-    exec->graph = g;
-    exec->n_launches = issued;
+    (void)hipGraphExecDestroy(t.exec);
+    (void)hipGraphDestroy(t.graph);
+    t = GraphInst{g, ge, issued};
+    exec->cur = 1 - exec->cur;
     if (n_launches) *n_launches = issued;
     return CBX_OK;
 }
@@ -1063,29 +1112,40 @@ int cbx_graph_exec_launch(cbx_graph_exec* exec, cbx_stream stream) {
     clear_error();
     if (!exec) return set_error(CBX_ERR_INVALID_ARG, "cbx_graph_exec_launch: exec is NULL");
     int dev = -1;
-    hipGetDevice(&dev);
+    (void)hipGetDevice(&dev);
     if (dev != exec->device) {
         return set_error(CBX_ERR_INVALID_ARG, "cbx_graph_exec_launch: the graph was captured on device " +
                                                   std::to_string(exec->device) + ", the current device is " +
                                                   std::to_string(dev));
     }
-    const hipError_t e = hipGraphLaunch(exec->exec, reinterpret_cast<hipStream_t>(stream));
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const hipError_t e = hipGraphLaunch(exec->inst[exec->cur].exec, s);
     if (e != hipSuccess) {
         return set_error(CBX_ERR_HIP, std::string("cbx_graph_exec_launch: ") + hipGetErrorString(e));
     }
+    bool seen = false;
+    for (hipStream_t t : exec->launched) seen = seen || t == s;
+    if (!seen) exec->launched.push_back(s);
     return CBX_OK;
 }
 
 void cbx_graph_exec_destroy(cbx_graph_exec* exec) {
     if (!exec) return;
     int prev = 0;
-    hipGetDevice(&prev);
-    hipSetDevice(exec->device);
-    hipDeviceSynchronize();   // no replay still in flight
-    hipGraphExecDestroy(exec->exec);
-    hipGraphDestroy(exec->graph);
-    hipStreamDestroy(exec->cs);
-    hipSetDevice(prev);
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(exec->device);
+    // no replay of either instantiation still in flight
+    static const char* f = "cbx_graph_exec_destroy";
+    if (wait_marks(exec, f) != CBX_OK || mark_launches(exec, f) != CBX_OK || wait_marks(exec, f) != CBX_OK) {
+        (void)hipDeviceSynchronize();
+    }
+    for (hipEvent_t e : exec->spare) (void)hipEventDestroy(e);
+    for (GraphInst& t : exec->inst) {
+        (void)hipGraphExecDestroy(t.exec);
+        (void)hipGraphDestroy(t.graph);
+    }
+    (void)hipStreamDestroy(exec->cs);
+    (void)hipSetDevice(prev);
     delete exec;
 }
 

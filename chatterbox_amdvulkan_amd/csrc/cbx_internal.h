@@ -52,12 +52,13 @@ struct DeviceState {
     uint16_t* gelu_table = nullptr;   // 65536 fp16 codes
     uint32_t* err_word = nullptr;     // sticky device error bits
     void*     gn_scratch = nullptr;   // this device's address of the static group norm scratch
+    bool      gn_split_ok = false;    // dispatch deals workgroups to XCDs by index mod 8 (probed)
 };
 
 // Device error bits.
 enum : uint32_t {
     DEV_ERR_ROW_INDEX = 1u,   // a get_rows index was out of range (row zeroed)
-    DEV_ERR_GN_WAIT   = 2u,   // an in-place split GroupNorm workgroup stopped waiting for the others
+    DEV_ERR_RESERVED1 = 2u,   // no longer raised (in-place GroupNorm never takes the split)
 };
 
 // ---- host helpers implemented in cbx_api.cpp ----------------------------
@@ -100,17 +101,24 @@ int launch_group_norm(const cbx_tensor* x, int n_groups, float eps, const cbx_te
                       const cbx_tensor* b, int act, cbx_tensor* y, DeviceState* st,
                       hipStream_t s);
 // The split-reduction GroupNorm over a workspace of
-// group_norm_workspace_bytes() (zeroed once, left zeroed by every launch);
-// layouts it does not cover go to launch_group_norm.  wait_ticks: the
-// longest wait of a workgroup for the others, in 100 MHz ticks (0: never
-// wait); n_chunks_req: chunks per group, 0 = automatic.
+// group_norm_workspace_bytes() (zeroed once; never needs clearing again);
+// in-place calls and layouts it does not cover go to launch_group_norm.
+// wait_ticks: the longest wait of a workgroup for the others, in 100 MHz
+// ticks (0: never wait; kGnWaitAuto: from the launch's size);
+// n_chunks_req: chunks per group, 0 = automatic.
+constexpr uint64_t kGnWaitAuto = ~uint64_t{0};
 size_t group_norm_workspace_bytes();
 // The current device's address of the library's static split-GroupNorm
-// scratch (group_norm_workspace_bytes() of it), for cbx_group_norm_noalloc;
-// called once per device by cbx_init.  The split handles up to
-// group_norm_scratch_slots() group instances x chunks.
+// scratch (sets of group_norm_workspace_bytes()), for cbx_group_norm and
+// cbx_group_norm_noalloc; called once per device by cbx_init.  The split
+// handles up to group_norm_scratch_slots() group instances x chunks.
 int group_norm_scratch_setup(void** out);
 size_t group_norm_scratch_slots();
+// The scratch set a call on stream s uses.
+void* group_norm_scratch_for(const DeviceState* st, hipStream_t s);
+// Launches a probe on the current device and sets *ok when workgroups with
+// equal index mod 8 ran on one XCD (the split's assumption).
+int group_norm_probe_xcd(bool* ok);
 int launch_group_norm_split(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
                             int act, cbx_tensor* y, void* workspace, uint64_t wait_ticks, int n_chunks_req,
                             DeviceState* st, hipStream_t s);

@@ -290,7 +290,10 @@ __global__ __launch_bounds__(kThreads) void k_group_norm_vec(GnArgs a, uint32_t 
 // chunk workgroup holds only its chunk of the group in registers, and the
 // f64 partial sums of its waves meet those of the group's other chunks in a
 // workspace, once for the mean and once for the variance.  Each element is
-// read once and every workgroup's VALU work is its own chunk.
+// read once and every workgroup's VALU work is its own chunk.  Out of place
+// only: the host sends a y that overlaps x to the one-workgroup-per-group
+// kernels, because a wave that stops waiting (below) re-reads the whole
+// group from x, which must then still hold the input.
 //
 // Every wave publishes its own partial and every wave collects the group's
 // partials itself: no barrier and no LDS anywhere, so a wave goes from its
@@ -300,26 +303,28 @@ __global__ __launch_bounds__(kThreads) void k_group_norm_vec(GnArgs a, uint32_t 
 // slots l, l + 64, .. starting from +0, then the lanes by the DPP
 // butterfly -- the same bits in every wave of the group.
 //
-// A partial travels as two 64-bit words (its low and high halves), each
-// tagged in its upper 32 bits with the launch's tag: the dispatch's packet
-// index on its queue mixed with the queue's address, shifted left and made
-// odd (never the 0 of fresh memory; packets of one queue within 2^31 of
-// each other get different tags).  A word is written whole and read whole,
-// so a reader that finds this launch's tag in both words of a slot has that
-// wave's partial; words left by earlier launches carry other tags and
-// nothing is ever cleared.  The words are written with plain stores, which
-// reach the L2 the workgroups of one group share (their indices put them on
-// one XCD: dispatch deals workgroups to the 8 XCDs round-robin), except in
-// place, where agent-scope stores make them visible on any XCD; they are
-// read with agent-scope loads.
+// A partial travels as two 64-bit words (its low and high halves); the
+// upper 32 bits of the first carry the low half of the launch's 64-bit tag,
+// those of the second its high half.  The tag is an odd multiple of the
+// dispatch's 64-bit packet index on its queue plus a hash of the queue and
+// kernel-argument addresses (a bijection of the packet index: launches on
+// one queue never share a tag), never 0 (fresh memory).  A word is written
+// whole and read whole, so a reader that finds all 64 tag bits in a slot has
+// that wave's partial; words left by earlier launches, or by a launch on
+// another stream that shares the workspace, carry other tags, and nothing
+// is ever cleared.  The words are written with plain stores, which reach
+// the L2 that the workgroups of one group share (their indices put them on
+// one XCD: dispatch deals workgroups to the 8 XCDs round-robin, which the
+// host checks once per device before it uses this kernel), and read with
+// agent-scope loads.
 //
 // Waits are bounded: after GnSplit::wait_ticks of the 100 MHz real-time
 // counter a wave stops waiting and computes every slot's partial itself
 // from x, with the same lanes and order as the wave that owns the slot, so
-// the statistics are the same bits either way and a workgroup that never
-// gets a CU while the others run delays nothing.  (In place, a wave that
-// stops waiting may read chunks already overwritten: it raises
-// DEV_ERR_GN_WAIT.)  wait_ticks == 0: never wait.
+// the statistics are the same bits either way, and a workgroup that never
+// gets a CU while the others run (another stream's kernel holding the CUs,
+// or a launch on another stream writing the same workspace) delays them by
+// the wait, never changes a result.  wait_ticks == 0: never wait.
 constexpr int kSplitThreads = 256;
 constexpr int kSplitWaves = kSplitThreads / WAVE;
 constexpr int kSplitMaxChunks = 32;
@@ -335,26 +340,25 @@ struct GnSplit {
     const float* w;
     const float* b;
     uint64_t* word;          // [2 stages][kSplitMaxSlots * kSplitWaves][2 words]
-    uint32_t* err;
     const uint16_t* tab;
     int64_t x_nb3, y_nb3;    // batch strides (bytes)
     uint64_t wait_ticks;
     uint32_t n_chunks, n_gi, n_groups, per_ch, cpg, C;   // per_ch = ne0 * ne1
     float eps;
     int32_t act;
-    uint32_t in_place;
 };
 
 // The dispatch's 64-bit packet index on its queue (llvm.amdgcn.dispatch.id;
 // clang has no builtin for it).
 extern "C" __device__ uint64_t cbx_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
 
-__device__ __forceinline__ uint32_t launch_tag() {
+__device__ __forceinline__ uint64_t launch_tag() {
     const uint64_t id = cbx_dispatch_id();
     const uint64_t q = reinterpret_cast<uintptr_t>(__builtin_amdgcn_queue_ptr());
-    const uint32_t qmix = static_cast<uint32_t>(((q >> 6) * 0x9E3779B97F4A7C15ull) >> 32);
-    // consecutive packets on one queue get distinct tags for 2^31 launches
-    return ((static_cast<uint32_t>(id) ^ qmix) << 1) | 1u;
+    const uint64_t ka = reinterpret_cast<uintptr_t>(__builtin_amdgcn_kernarg_segment_ptr());
+    const uint64_t mix = ((q >> 6) * 0xC2B2AE3D27D4EB4Full) ^ ((ka >> 4) * 0x165667B19E3779F9ull);
+    const uint64_t t = id * 0x9E3779B97F4A7C15ull + mix;   // odd multiplier: one tag per packet index
+    return t ? t : 1;
 }
 
 // A lane's partial of stage 0 (Σx) or 1 (Σ(x - mean)^2, the f32
@@ -398,19 +402,18 @@ __device__ __forceinline__ void wave_chunk_load(const char* xg, uint32_t q0, uin
 // of the group), or computes every slot's partial itself when the wait
 // runs out.
 template <int NV>
-__device__ __forceinline__ double split_exchange(const GnSplit& a, uint32_t tag, uint32_t gi, uint32_t ci, int stage,
+__device__ __forceinline__ double split_exchange(const GnSplit& a, uint64_t tag, uint32_t gi, uint32_t ci, int stage,
                                                  double mine, float mean, const char* xg, uint32_t n4, uint32_t per) {
     const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
     const uint32_t P = a.n_chunks * kSplitWaves;
     uint64_t* wd = a.word + static_cast<uint64_t>(stage) * kSplitStageWords + 2 * static_cast<uint64_t>(gi) * P;
     const uint64_t bits = __builtin_bit_cast(uint64_t, mine);
-    const uint64_t tg = static_cast<uint64_t>(tag) << 32;
+    const uint64_t tag_lo = tag << 32, tag_hi = tag & 0xffffffff00000000ull;
     const uint32_t own = ci * kSplitWaves + wave;
     if (lane < 2) {
         // lanes 0 and 1 publish the low and high halves
-        const uint64_t word = tg | (lane == 0 ? bits & 0xffffffffu : bits >> 32);
-        if (a.in_place) __hip_atomic_store(&wd[2 * own + lane], word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else __hip_atomic_store(&wd[2 * own + lane], word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const uint64_t word = lane == 0 ? tag_lo | (bits & 0xffffffffu) : tag_hi | (bits >> 32);
+        __hip_atomic_store(&wd[2 * own + lane], word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
     double val[kSplitLaneSlots];
     bool ok = false;
@@ -429,7 +432,8 @@ __device__ __forceinline__ double split_exchange(const GnSplit& a, uint32_t tag,
                         const uint64_t lo = __hip_atomic_load(&wd[2 * sl], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         const uint64_t hi =
                             __hip_atomic_load(&wd[2 * sl + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        have = have && (lo >> 32) == tag && (hi >> 32) == tag;
+                        have = have && (lo & 0xffffffff00000000ull) == tag_lo &&
+                               (hi & 0xffffffff00000000ull) == tag_hi;
                         val[r] = __builtin_bit_cast(double, (lo & 0xffffffffu) | (hi << 32));
                     }
                 }
@@ -442,8 +446,8 @@ __device__ __forceinline__ double split_exchange(const GnSplit& a, uint32_t tag,
         }
     }
     if (!ok) {
-        // every slot's partial, as the wave that owns it computes it
-        if (a.in_place && lane == 0) atomicOr(a.err, DEV_ERR_GN_WAIT);
+        // every slot's partial, as the wave that owns it computes it (x is
+        // still the input: the split runs out of place only)
 #pragma unroll
         for (int r = 0; r < kSplitLaneSlots; r++) val[r] = 0.0;
         for (uint32_t sl = 0; sl < P; sl++) {
@@ -512,7 +516,7 @@ __global__ __launch_bounds__(kSplitThreads) void k_group_norm_split(GnSplit a) {
         wv[k] = wq[a.w ? c : 0];
         bv[k] = bq[a.b ? c : 0];
     }
-    const uint32_t tag = launch_tag();
+    const uint64_t tag = launch_tag();
     const double count = static_cast<double>(4 * n4);
     const double s =
         split_exchange<NV>(a, tag, gi, ci, 0, wave_sum(lane_partial<NV>(v, ok, 0, 0.0f)), 0.0f, xg, n4, per);
@@ -640,14 +644,28 @@ GnArgs gn_args(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w
     return a;
 }
 
-// Scratch of cbx_group_norm_noalloc, for callers that cannot allocate: the
-// split reduction's exchange words for kSplitMaxSlots chunk slots (128 KiB)
+// Scratch of cbx_group_norm_noalloc and cbx_group_norm, for callers that
+// cannot allocate: kScratchSets sets of the split reduction's exchange
+// words, each for kSplitMaxSlots chunk slots (128 KiB a set, 1 MiB in all),
 // in the library's own device memory, one copy per GPU, held until the
-// process ends.  Zero at load; the launch tags mean nothing in it ever needs
-// clearing.  Host code must not pass `scratch` itself to a kernel (on the
-// host it names a stand-in, not device memory): group_norm_scratch_setup
-// looks up each device's address once, at cbx_init, and launches use that.
-static __device__ __align__(256) uint64_t scratch[2 * kSplitStageWords];
+// process ends.  A call takes the set its stream hashes to, so calls on
+// different streams rarely share one (and when they do, the launch tags
+// keep the results exact; only the waits run out).  Zero at load; the launch
+// tags mean nothing in it ever needs clearing.  Host code must not pass
+// `scratch` itself to a kernel (on the host it names a stand-in, not device
+// memory): group_norm_scratch_setup looks up each device's address once, at
+// cbx_init, and launches use that.
+constexpr uint32_t kScratchSets = 8;
+static __device__ __align__(256) uint64_t scratch[kScratchSets * 2 * kSplitStageWords];
+
+// Which XCD (its XCC_ID hardware register) runs each workgroup.
+__global__ __launch_bounds__(kSplitThreads) void k_xcc_probe(uint32_t* out) {
+    if (threadIdx.x == 0) {
+        uint32_t id;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(id));
+        out[blockIdx.x] = id;
+    }
+}
 
 }  // namespace
 
@@ -665,8 +683,35 @@ int group_norm_scratch_setup(void** out) {
 
 size_t group_norm_scratch_slots() { return kSplitMaxSlots; }
 
+void* group_norm_scratch_for(const DeviceState* st, hipStream_t s) {
+    const uint64_t h = (static_cast<uint64_t>(reinterpret_cast<uintptr_t>(s)) >> 4) * 0x9E3779B97F4A7C15ull;
+    const uint32_t set = static_cast<uint32_t>(h >> 61) % kScratchSets;
+    return static_cast<char*>(st->gn_scratch) + set * group_norm_workspace_bytes();
+}
+
 size_t group_norm_workspace_bytes() {
     return 2 * static_cast<size_t>(kSplitStageWords) * sizeof(uint64_t);
+}
+
+int group_norm_probe_xcd(bool* ok) {
+    *ok = false;
+    constexpr uint32_t kBlocks = 2048;
+    uint32_t* d = nullptr;
+    if (hipMalloc(reinterpret_cast<void**>(&d), kBlocks * sizeof(uint32_t)) != hipSuccess) {
+        return set_error(CBX_ERR_HIP, "cbx_init: hipMalloc of the XCD probe failed");
+    }
+    hipLaunchKernelGGL(k_xcc_probe, dim3(kBlocks), dim3(kSplitThreads), 0, nullptr, d);
+    uint32_t h[kBlocks];
+    const bool good = hipGetLastError() == hipSuccess &&
+                      hipMemcpy(h, d, sizeof(h), hipMemcpyDeviceToHost) == hipSuccess;
+    (void)hipFree(d);
+    if (!good) return set_error(CBX_ERR_HIP, "cbx_init: the XCD probe failed");
+    // the split's chunks of one group are workgroups b with one b % 8: they
+    // must share an XCD (and so an L2)
+    bool same = true;
+    for (uint32_t b = kXcds; b < kBlocks; b++) same = same && h[b] == h[b % kXcds];
+    *ok = same;
+    return CBX_OK;
 }
 
 int launch_group_norm_split(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
@@ -684,11 +729,25 @@ int launch_group_norm_split(const cbx_tensor* x, int n_groups, float eps, const 
     n_chunks = std::min<int64_t>({n_chunks, kSplitMaxChunks, n4});
     n_chunks = std::max<int64_t>(n_chunks, cdiv(n4, 8 * kSplitThreads));
     const int64_t padded_gi = int64_t{kXcds} * cdiv(n_gi, kXcds);
-    // the split applies when the groups are few (n_chunks >= 2) and the
-    // whole grid is resident at once (at most 2 workgroups a CU)
-    if (!gn_vec_layout(x, y) || n_chunks < 2 || n_chunks > kSplitMaxChunks || n_gi * n_chunks > kSplitMaxSlots ||
-        padded_gi * n_chunks > int64_t{2} * st->n_cu || x->ne[0] * x->ne[1] * cpg >= (int64_t{1} << 30)) {
+    // the split applies out of place (a wave that stops waiting re-reads x),
+    // on a device whose dispatch was seen to deal workgroups to XCDs by
+    // index mod 8, when the groups are few (n_chunks >= 2) and the whole
+    // grid is resident at once (at most 2 workgroups a CU)
+    const uintptr_t xl = reinterpret_cast<uintptr_t>(x->data), yl = reinterpret_cast<uintptr_t>(y->data);
+    const size_t span = static_cast<size_t>(x->ne[3]) * x->nb[3];
+    const bool overlap = xl < yl + span && yl < xl + span;
+    if (overlap || !st->gn_split_ok || !gn_vec_layout(x, y) || n_chunks < 2 || n_chunks > kSplitMaxChunks ||
+        n_gi * n_chunks > kSplitMaxSlots || padded_gi * n_chunks > int64_t{2} * st->n_cu ||
+        x->ne[0] * x->ne[1] * cpg >= (int64_t{1} << 30)) {
         return launch_group_norm(x, n_groups, eps, w, b, act, y, st, s);
+    }
+    if (wait_ticks == kGnWaitAuto) {
+        // ten times what the launch should take (a few microseconds plus its
+        // bytes at 2 TB/s), at least 20 us: long past a resident grid's
+        // arrival skew, short against the fallback's cost of a stall
+        const double bytes = 8.0 * static_cast<double>(count) * static_cast<double>(n_gi);
+        const double us = std::max(20.0, 10.0 * (3.0 + bytes / 2.0e6));
+        wait_ticks = static_cast<uint64_t>(us * 100.0);
     }
     const int64_t per = cdiv(n4, n_chunks);
     const int nv = per <= kSplitThreads ? 1 : per <= 2 * kSplitThreads ? 2 : per <= 4 * kSplitThreads ? 4 : 8;
@@ -698,7 +757,6 @@ int launch_group_norm_split(const cbx_tensor* x, int n_groups, float eps, const 
     sp.w = w ? static_cast<const float*>(w->data) : nullptr;
     sp.b = b ? static_cast<const float*>(b->data) : nullptr;
     sp.word = static_cast<uint64_t*>(workspace);
-    sp.err = st->err_word;
     sp.tab = st->gelu_table;
     sp.x_nb3 = static_cast<int64_t>(x->nb[3]);
     sp.y_nb3 = static_cast<int64_t>(y->nb[3]);
@@ -711,7 +769,6 @@ int launch_group_norm_split(const cbx_tensor* x, int n_groups, float eps, const 
     sp.C = static_cast<uint32_t>(x->ne[2]);
     sp.eps = eps;
     sp.act = act;
-    sp.in_place = x->data == y->data;
     const uint32_t n_slots = static_cast<uint32_t>(padded_gi * n_chunks);
     if (act == CBX_UNARY_MISH) gn_split<2>(sp, n_slots, nv, s);
     else if (act != CBX_UNARY_NONE) gn_split<1>(sp, n_slots, nv, s);

@@ -83,10 +83,8 @@ const char* cbx_version(void);
 /* Reads (and with clear != 0 resets) the device error word of `device`,
  * synchronising the device first.  Bit 0: a get_rows index was out of
  * range (ggml aborts there; this library writes zeros to that row).
- * Bit 1: an in-place cbx_group_norm_ws workgroup stopped waiting for the
- * group's other chunks and read chunks that may already have been
- * overwritten (a grid not resident at once; not seen with the default
- * wait).                                                                    */
+ * Bit 1: reserved, never raised (in-place GroupNorm calls do not take the
+ * split reduction, the only path that raised it).                          */
 int  cbx_device_errors(int device, uint32_t* flags_out, int clear);
 
 /* ---- gather and conversion ---------------------------------------------- */
@@ -167,7 +165,13 @@ int cbx_rms_norm_mul(const cbx_tensor* x, const cbx_tensor* g, float eps,
 
 /* ggml_group_norm(x, n_groups, eps) [-> mul(w) -> add(b)] [-> act] in one
  * pass.  Channels are ne[2] (ggml's convention), F32.  w, b: F32 with ne =
- * (1,1,ne2,1), or NULL.  act: CBX_UNARY_NONE or an activation.             */
+ * (1,1,ne2,1), or NULL.  act: CBX_UNARY_NONE or an activation.  y may be x.
+ * A few large groups out of place (the CFM decoder's) run as the split
+ * reduction of cbx_group_norm_ws over the library's own scratch (the set
+ * the stream hashes to; see cbx_group_norm_noalloc), when cbx_init found
+ * the device's dispatch compatible with it (cbx_group_norm_split_enabled);
+ * everything else, in place included, one workgroup reduces each group.
+ * The results are the same bits either way.                               */
 int cbx_group_norm(const cbx_tensor* x, int n_groups, float eps,
                    const cbx_tensor* w, const cbx_tensor* b, int act,
                    cbx_tensor* y, cbx_stream stream);
@@ -177,10 +181,13 @@ int cbx_group_norm(const cbx_tensor* x, int n_groups, float eps,
  * each workgroup reads and reduces only its chunk, and the chunks' f64
  * partial sums meet in the workspace -- one HBM read of x, no workgroup
  * reducing a whole group.  Same results as cbx_group_norm, bit for bit.
- * Layouts the split does not cover (strided groups, many small groups)
- * run as cbx_group_norm.  A workspace serves one call at a time: calls
- * that share one must not overlap in time (one stream, or streams ordered
- * by events); give concurrent streams a workspace each.
+ * In-place calls (y overlapping x) and layouts the split does not cover
+ * (strided groups, many small groups) run as one workgroup per group.
+ * A workspace serves one call at a time at full speed: calls that overlap
+ * in time on one workspace still give exact results (every partial carries
+ * its launch's 64-bit tag), but their chunks stop waiting for each other's
+ * partials and each recomputes the group, so give concurrent streams a
+ * workspace each.
  *
  * The workspace (128 KiB of device memory on the current device, zeroed once;
  * nothing in it needs clearing between calls) has no counterpart in ggml, whose CPU group
@@ -190,26 +197,37 @@ typedef struct cbx_group_norm_workspace cbx_group_norm_workspace;
 int  cbx_group_norm_workspace_create(cbx_group_norm_workspace** out);
 void cbx_group_norm_workspace_destroy(cbx_group_norm_workspace* ws);
 /* A chunk workgroup waits at most max_wait_us for the group's other
- * chunks (default 2000), then computes every chunk's partial itself; 0:
- * never wait (each wave reduces the whole group itself from x).
- * n_chunks: chunks per group, 0 (default) = automatic, else 2..32.
- * The results do not depend on either.  For tests and tuning.             */
+ * chunks, then computes every chunk's partial itself from x (which the
+ * split never overwrites: it runs out of place only); 0: never wait (each
+ * wave reduces the whole group itself); CBX_GN_WAIT_AUTO (the default):
+ * ten times the launch's expected length, at least 20 us.  n_chunks: chunks
+ * per group, 0 (default) = automatic, else 2..32.  The results do not
+ * depend on either.  For tests and tuning.                                */
+#define CBX_GN_WAIT_AUTO 0xFFFFFFFFu
 int  cbx_group_norm_workspace_tune(cbx_group_norm_workspace* ws,
                                    uint32_t max_wait_us, int32_t n_chunks);
+/* 1 when cbx_init found that the device deals workgroups to its XCDs by
+ * index mod 8 (checked with a probe kernel), so the split runs; 0 when it
+ * did not (every GroupNorm then reduces a group in one workgroup); or a
+ * negative cbx_status.                                                    */
+int  cbx_group_norm_split_enabled(int device);
 int  cbx_group_norm_ws(const cbx_tensor* x, int n_groups, float eps,
                        const cbx_tensor* w, const cbx_tensor* b, int act,
                        cbx_tensor* y, cbx_group_norm_workspace* ws,
                        cbx_stream stream);
 
 /* cbx_group_norm_ws without a workspace: the same kernels and results, the
- * exchange words in the library's own static device memory (128 KiB per GPU,
- * set up by cbx_init, held until the process ends).  No counterpart in the
- * reference: for callers that cannot allocate device memory at all -- code
- * under HIP graph capture, tight serving loops, harnesses that forbid
+ * exchange words in the library's own static device memory (8 sets of
+ * 128 KiB, 1 MiB per GPU, set up by cbx_init, held until the process ends;
+ * a call uses the set its stream's handle hashes to).  No counterpart in
+ * the reference: for callers that cannot allocate device memory at all --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc.  The call allocates nothing.  n_groups x x.ne[3] is limited to
- * 1024 group instances (larger: CBX_ERR_UNSUPPORTED).  Every call on a GPU
- * shares that GPU's scratch: calls that overlap in time on one GPU race
- * (keep them on one stream, or ordered by events).                        */
+ * 1024 group instances (larger: CBX_ERR_UNSUPPORTED).  Calls that overlap
+ * in time on one GPU race for a set when their streams hash to the same
+ * one: their results stay exact (tagged partials, and a chunk that stops
+ * waiting recomputes the group from x), but they lose the split's speed;
+ * keep such calls on one stream, or ordered by events.                     */
 int  cbx_group_norm_noalloc(const cbx_tensor* x, int n_groups, float eps,
                             const cbx_tensor* w, const cbx_tensor* b, int act,
                             cbx_tensor* y, cbx_stream stream);
@@ -656,8 +674,10 @@ int cbx_graph_compute(const cbx_tensor* tensors, int32_t n_tensors,
  * device current at creation.  Unsupported nodes: CBX_ERR_UNSUPPORTED as in
  * cbx_graph_compute.  *n_launches (may be NULL) gets the kernel launch
  * count of one replay.  Each exec holds a HIP stream of its own, which its
- * captures are recorded on (nothing runs on it), until it is destroyed.
- * Destroy waits for the device to be idle.                                */
+ * captures are recorded on (nothing runs on it), and two instantiations of
+ * the graph, which take turns (cbx_graph_exec_update), until it is
+ * destroyed.  Destroy waits for the exec's own replays (not for other work
+ * on the device); every stream it was launched on must still exist then. */
 typedef struct cbx_graph_exec cbx_graph_exec;
 int  cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors,
                            const cbx_gnode* nodes, int32_t n_nodes,
@@ -671,13 +691,18 @@ void cbx_graph_exec_destroy(cbx_graph_exec* exec);
  * next token).  The list is planned and recorded again; when it gives the
  * same launches with other arguments (addresses, shapes, positions), the
  * instantiated graph takes them in place (*in_place = 1), otherwise it is
- * re-instantiated (*in_place = 0).  Waits first for the device to finish
- * the work queued on it (hipDeviceSynchronize), so the replays queued so far
- * run with the arguments they were queued with.  On an error of planning
- * or recording (an unsupported node, a bad layout)
- * `exec` is left as it was; after CBX_ERR_HIP (the new graph could not be
- * instantiated) destroy it.  Same device as at creation.  *n_launches and
- * *in_place may be NULL.                                                   */
+ * re-instantiated (*in_place = 0).  Stream-ordered: the exec's two
+ * instantiations take turns, and an update re-points the one not replayed
+ * since the previous update, after waiting (on events recorded by that
+ * update) for its replays -- all issued before the previous update -- and
+ * for nothing else.  So replays queued so far keep the arguments they were
+ * queued with, the replay launched just before this update may still run
+ * while the host updates (a per-step loop keeps the device busy), and other
+ * streams' work is never waited for.  Every stream the exec was launched on
+ * since the previous update must still exist.  On an error of planning or
+ * recording (an unsupported node, a bad layout) `exec` is left as it was;
+ * after CBX_ERR_HIP (the new graph could not be instantiated) destroy it.
+ * Same device as at creation.  *n_launches and *in_place may be NULL.      */
 int  cbx_graph_exec_update(cbx_graph_exec* exec,
                            const cbx_tensor* tensors, int32_t n_tensors,
                            const cbx_gnode* nodes, int32_t n_nodes,

@@ -335,6 +335,92 @@ def test_update_to_other_buffers_in_place(cbx):
         cache.close()
 
 
+def long_work_on(stream):
+    """Enqueues ~0.05-1 s of bounded device work on `stream` (a spin kernel
+    that ends after a fixed cycle count) and returns an event behind it."""
+    done = torch.cuda.Event()
+    with torch.cuda.stream(stream):
+        torch.cuda._sleep(120_000_000)
+        done.record()
+    return done
+
+
+def test_update_leaves_other_streams_running(cbx):
+    """An update waits for its own exec's replays only: work queued on
+    another stream is still running when cbx_graph_exec_update returns (a
+    device-wide wait would have waited for it), and the updated replay gives
+    cbx_graph_compute's bits."""
+    cache = cbx.RopeCache(64, mode=2, n_ctx_orig=2048, n_pos=2048)
+    sets = [decode_bufs(41 + i, p) for i, p in enumerate((5, 900, 17))]
+    outs = ("y", "qo", "ko", "o")
+    exp = []
+    for b in sets:
+        g, _ = decode_list(cbx, cache, b)
+        assert g.compute() == 4
+        torch.cuda.synchronize()
+        exp.append([bits(b[n]).clone() for n in outs])
+        for n in outs:
+            b[n].fill_(float("nan"))
+    torch.cuda.synchronize()
+    g, ids = decode_list(cbx, cache, sets[0])
+    ex = g.capture()
+    other = torch.cuda.Stream()
+    try:
+        ex.launch()
+        for i in (1, 2):
+            done = long_work_on(other)
+            for n, t in ids.items():
+                g.rebind(t, sets[i][n])
+            assert ex.update() is True
+            running = not done.query()
+            ex.launch()
+            torch.cuda.synchronize()
+            assert running, f"update {i} waited for another stream's work"
+        for i, b in enumerate(sets):
+            for n, e in zip(outs, exp[i]):
+                assert torch.equal(bits(b[n]), e), f"set {i}: {n} differs from eager"
+    finally:
+        ex.close()
+        cache.close()
+
+
+def test_update_while_the_last_replay_runs(cbx):
+    """A per-step loop: update, launch, update, launch ... with no
+    synchronisation, each step over its own buffers and position, the
+    replay before each update still queued behind long work on the same
+    stream (the update must not change the arguments it was queued with):
+    every step's outputs equal cbx_graph_compute's."""
+    cache = cbx.RopeCache(64, mode=2, n_ctx_orig=2048, n_pos=2048)
+    sets = [decode_bufs(51 + i, p) for i, p in enumerate((0, 1, 2, 3, 2047, 2048, 9, 10))]
+    outs = ("y", "qo", "ko", "o")
+    exp = []
+    for b in sets:
+        g, _ = decode_list(cbx, cache, b)
+        assert g.compute() == 4
+        torch.cuda.synchronize()
+        exp.append([bits(b[n]).clone() for n in outs])
+        for n in outs:
+            b[n].fill_(float("nan"))
+    torch.cuda.synchronize()
+    g, ids = decode_list(cbx, cache, sets[0])
+    ex = g.capture()
+    try:
+        long_work_on(torch.cuda.current_stream())     # the replays queue behind it
+        ex.launch()
+        for i in range(1, len(sets)):
+            for n, t in ids.items():
+                g.rebind(t, sets[i][n])
+            assert ex.update() is True
+            ex.launch()
+        torch.cuda.synchronize()
+        for i, b in enumerate(sets):
+            for n, e in zip(outs, exp[i]):
+                assert torch.equal(bits(b[n]), e), f"step {i}: {n} differs from eager"
+    finally:
+        ex.close()
+        cache.close()
+
+
 def test_update_to_other_lengths(cbx):
     """LayerNorm -> view -> RoPE over views of T = 100, 37, 512 and 1 tokens of
     one buffer (a sequence whose length changes between steps, as the KV
@@ -429,7 +515,10 @@ def test_update_resblock_to_another_input(cbx):
 def test_update_to_another_list(cbx):
     """An update to a list with other launches (the decode step's four, then
     GroupNorm -> affine -> Mish's one) re-instantiates the graph; an update to
-    a list with an unsupported node fails and leaves the exec as it was."""
+    a list with an unsupported node fails and leaves the exec as it was.
+    The exec's two instantiations take turns, so going back to the decode
+    list re-points the one that still holds it (in place), and a third list
+    re-instantiates again."""
     cache = cbx.RopeCache(64, mode=2, n_ctx_orig=2048, n_pos=2048)
     b0 = decode_bufs(41, 9)
     g, _ = decode_list(cbx, cache, b0)
@@ -474,12 +563,17 @@ def test_update_to_another_list(cbx):
         assert torch.equal(bits(buf[5]), exp2)
         for n in ("y", "qo", "ko", "o"):
             b0[n].fill_(float("nan"))
-        assert ex.update(g) is False                 # back to the decode list
+        assert ex.update(g) is True                  # back to the decode list: the other instantiation
         assert ex.n_launches == 4
         ex.launch()
         torch.cuda.synchronize()
         for n, e0 in zip(("y", "qo", "ko", "o"), exp0):
             assert torch.equal(bits(b0[n]), e0), n
+        buf[5].fill_(float("nan"))
+        assert ex.update(g2) is True                 # and the GroupNorm list's is still there
+        ex.launch()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(buf[5]), exp2)
     finally:
         ex.close()
         cache.close()

@@ -2,8 +2,9 @@
 workgroups that meet in a workspace.  Same bits as cbx_group_norm and the
 oracle for every chunk count, whether a workgroup waits for the others or
 computes every chunk's partial itself (a wait of 0: forced from the host),
-in place, and on consecutive calls over one workspace (the counters must
-come back to zero)."""
+in place (with and without the wait), on consecutive calls over one
+workspace (the words of earlier launches carry other tags), and when two
+streams run calls over one workspace at the same time."""
 import ctypes
 
 import numpy as np
@@ -104,12 +105,59 @@ def test_consecutive_calls_reuse_the_workspace(cbx, oracle):
     ws.close()
 
 
-def test_in_place(cbx, oracle):
-    x, w, b = cfm(512)
-    ws = cbx.GroupNormWorkspace()
+@pytest.mark.parametrize("max_wait_us", [None, 0, 1])
+@pytest.mark.parametrize("C", [256, 512])
+def test_in_place(cbx, oracle, C, max_wait_us):
+    """y == x with the default wait, with no wait at all and with a 1 us
+    wait (every or nearly every wave would stop waiting and re-read the
+    group from x while other chunks store over it, if in-place calls took
+    the split): the oracle's bits, with and without Mish, and no error bit."""
+    x, w, b = cfm(C)
+    ws = cbx.GroupNormWorkspace(max_wait_us=max_wait_us)
+    gn = oracle.group_norm_affine(x, 8, 1e-5, w, b, False, nth=8)
     t = dev(x)
     cbx.group_norm_ws(t, 8, 1e-5, ws, dev(w), dev(b), out=t)
-    assert_bitexact(host(t), oracle.group_norm_affine(x, 8, 1e-5, w, b, False, nth=8), "in place")
+    assert_bitexact(host(t), gn, f"in place, wait {max_wait_us}")
+    t = dev(x)
+    cbx.group_norm_ws(t, 8, 1e-5, ws, dev(w), dev(b), act=cbx.MISH, out=t)
+    ref = cbx.group_norm_ws(dev(x), 8, 1e-5, ws, dev(w), dev(b), act=cbx.MISH)
+    assert_bitexact(host(t), host(ref), f"in place + mish, wait {max_wait_us}")
+    t = dev(x)
+    cbx.group_norm_noalloc(t, 8, 1e-5, dev(w), dev(b), out=t)
+    assert_bitexact(host(t), gn, "noalloc in place")
+    t = dev(x)
+    cbx.group_norm(t, 8, 1e-5, dev(w), dev(b), out=t)
+    assert_bitexact(host(t), gn, "group_norm in place")
+    no_device_errors(cbx)
+    ws.close()
+
+
+def test_split_enabled_on_this_device(cbx):
+    """cbx_init's probe found workgroups with one index mod 8 on one XCD
+    (MI355X deals them round-robin), so the split runs."""
+    assert cbx.group_norm_split_enabled(0)
+
+
+def test_two_streams_share_one_workspace(cbx, oracle):
+    """Calls on two streams over one workspace, free to overlap in time
+    (each writes partials the other's waves read past by tag): every result
+    keeps the oracle's bits; a short wait keeps any stall brief."""
+    ws = cbx.GroupNormWorkspace(max_wait_us=50)
+    cases = []
+    for C in (256, 512):
+        x, w, b = cfm(C)
+        cases.append((dev(x), dev(w), dev(b), oracle.group_norm_affine(x, 8, 1e-5, w, b, False, nth=8)))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    outs = []
+    for i in range(24):
+        k = i % 2
+        with torch.cuda.stream(streams[k]):
+            xd, wd, bd, _ = cases[k]
+            outs.append((k, cbx.group_norm_ws(xd, 8, 1e-5, ws, wd, bd)))
+    torch.cuda.synchronize()
+    for i, (k, o) in enumerate(outs):
+        assert_bitexact(host(o), cases[k][3], f"call {i} on stream {k}")
     no_device_errors(cbx)
     ws.close()
 
