@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="skip the secondary workloads")
     ap.add_argument("--hift-conv", action="store_true",
                     help="only the HiFT conv1d / transposed-conv timings, as one JSON object (for profiling)")
-    ap.add_argument("--only", choices=["decode", "serving", "cfm", "hift", "softmax", "t3_block", "hift_conv",
+    ap.add_argument("--only", choices=["decode", "serving", "cfm", "hift", "softmax", "t3_block", "t3_token", "hift_conv",
                                        "copy"],
                     help="run one secondary workload alone and print its JSON (no headline line)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -700,6 +700,75 @@ def bench_t3_block(C, W, torch, reps=300):
     return dict(out, buffer_sets=n_sets)
 
 
+def bench_t3_token(C, W, torch, reps=200, tokens=64):
+    """One T3 decode step's element-wise nodes at N_new = 1 (t3.cpp:446-546:
+    the input embedding, 24 blocks' LN-1, qkv bias, score softmax, residual
+    joins with LN-2 and the next LN-1, fc bias + GELU, the final LN; the
+    matmul outputs given), planned into 121 launches by the node-list
+    executor.  Device time per token from back-to-back replays of the list
+    captured into a HIP graph (cbx_graph_exec); the same list planned and
+    launched every token (cbx_graph_compute); and a decode loop of `tokens`
+    consecutive tokens, each re-pointed with cbx_graph_exec_update (the
+    scores one column longer, the mask's n_past), its token and position
+    written, then replayed -- wall time per token, host time of the update."""
+    from chatterbox_amdvulkan_amd import t3_decode as T
+
+    inp = W.t3_token_inputs()
+    dev = T.upload(inp)
+    n0 = 255
+    st = T.T3DecodeStep(dev, n0)
+    st.set_token(17, n0)
+    ex = st.graph.capture(st.keep)
+    s = cur_stream(torch)
+    out = {"launches": ex.n_launches, "blocks": st.n_blocks, "n_past": n0,
+           "bytes_per_token": W.t3_token_bytes(st.n_blocks, n0)}
+    for _ in range(10):
+        ex.launch(s)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        ex.launch(s)
+    e1.record()
+    torch.cuda.synchronize()
+    dev_us = e0.elapsed_time(e1) * 1000.0 / reps
+    out["exec_replay_us_per_token"] = dev_us
+    out["exec_replay_us_per_launch"] = dev_us / ex.n_launches
+    # plan + launch every token (no graph)
+    for _ in range(3):
+        st.graph.compute(st.keep)
+    torch.cuda.synchronize()
+    n_c = max(20, reps // 4)
+    tm = time.perf_counter()
+    e0.record()
+    for _ in range(n_c):
+        st.graph.compute(st.keep)
+    host = (time.perf_counter() - tm) / n_c * 1e6
+    e1.record()
+    torch.cuda.synchronize()
+    out["graph_compute_us_per_token"] = {"host_us": host, "device_us": e0.elapsed_time(e1) * 1000.0 / n_c}
+    # a decode loop: update + token write + replay per token, no sync inside
+    upd = 0.0
+    torch.cuda.synchronize()
+    t_loop = time.perf_counter()
+    for t in range(tokens):
+        n_past = n0 + 1 + t
+        st.retarget(n_past)
+        tm = time.perf_counter()
+        ok = ex.update(st.graph, st.keep)
+        upd += time.perf_counter() - tm
+        if not ok:
+            raise SystemExit("bench: the T3 token list was not updated in place")
+        st.set_token((17 * t) % W.T3_SPEECH_VOCAB, n_past)
+        ex.launch(s)
+    torch.cuda.synchronize()
+    out["decode_loop_us_per_token"] = (time.perf_counter() - t_loop) / tokens * 1e6
+    out["update_host_us_per_token"] = upd / tokens * 1e6
+    out["decode_loop_tokens"] = tokens
+    ex.close()
+    return out
+
+
 PEAK_MFMA_F16_TFLOPS = 2500.0
 
 
@@ -1176,7 +1245,9 @@ def cpu_other_workloads(W, O, nth, seconds):
     """The oracle on the other workloads' shapes (same inputs as the GPU
     legs), a bounded sample each: decode step chain (us per step), the
     64-stream f16 step, a CFM flow step, a T3 block's element-wise nodes,
-    two HiFT stages' activations, a ResBlock conv and an upsampler."""
+    one T3 decode token's element-wise nodes (24 blocks at N_new = 1, one
+    thread: every op is one row), two HiFT stages' activations, a ResBlock
+    conv and an upsampler."""
     out = {}
     steps = [W.decode_inputs(t) for t in range(W.DECODE_STEPS)]
 
@@ -1221,6 +1292,10 @@ def cpu_other_workloads(W, O, nth, seconds):
     reps, el = _timed(t3_block, seconds)
     bb = W.t3_block_bytes()
     out["t3_block_elementwise_GBps"] = (bb["residual_ln2"] + bb["fc_bias_gelu"] + bb["residual_next_ln1"]) * reps / el / 1e9
+
+    tok = O.T3TokenStep(W.t3_token_inputs(), 255)
+    reps, el = _timed(lambda: tok.run(17, 255), seconds)
+    out["t3_token_elementwise_us_per_token_1thread"] = el / reps * 1e6
 
     for (B, Ch, T) in W.HIFT_SHAPES[:3:2]:
         x = W.normal(W.seed_of(4, 2), (B, T, Ch))
@@ -1273,6 +1348,7 @@ def main():
         fn = {"decode": lambda: bench_decode(C, W, torch), "serving": lambda: bench_serving(C, W, torch),
               "cfm": lambda: bench_cfm(C, W, torch), "hift": lambda: bench_hift(C, W, torch),
               "softmax": lambda: bench_softmax(C, W, torch), "t3_block": lambda: bench_t3_block(C, W, torch),
+              "t3_token": lambda: bench_t3_token(C, W, torch),
               "hift_conv": lambda: bench_hift_conv(C, W, torch),
               "copy": lambda: bench_copy_ceiling(C, torch, {"gelu_bytes": nb["gelu"],
                                                             "embed_layer_norm_bytes": nb["embed_layer_norm"],
@@ -1314,6 +1390,8 @@ def main():
         details["attention_softmax"] = bench_softmax(C, W, torch)
         log("t3 block")
         details["t3_block_elementwise"] = bench_t3_block(C, W, torch)
+        log("t3 token")
+        details["t3_token_elementwise"] = bench_t3_token(C, W, torch)
         log("hift conv")
         details["hift_resblock_conv"] = bench_hift_conv(C, W, torch)
     k_ms = res["kernel_ms"]["gelu"]
@@ -1353,6 +1431,12 @@ def main():
         dd = details["t3_decode"]
         out["t3_decode_us_per_step_chain"] = {k: round(dd[k]["us_per_step"], 3)
                                               for k in ("per_op_4_launches", "qk_merged_3_launches", "one_launch")}
+    if "t3_token_elementwise" in details:
+        tt = details["t3_token_elementwise"]
+        out["t3_per_token_us"] = {"reference_sequence": "t3.cpp:446-546 at N_new = 1, 24 blocks, "
+                                                        f"{tt['launches']} launches, n_past {tt['n_past']}",
+                                  "exec_replay": round(tt["exec_replay_us_per_token"], 2),
+                                  "decode_loop_with_update": round(tt["decode_loop_us_per_token"], 2)}
     out["details"] = details
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(W, a.cpu_seconds)

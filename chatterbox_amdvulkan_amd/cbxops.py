@@ -853,8 +853,10 @@ class Graph:
         self._descs: list = []
         self._torch: list = []
         self.nodes: list = []
+        self._bound = None
 
     def tensor(self, t: torch.Tensor, ggml_type: Optional[int] = None) -> int:
+        self._bound = None
         self._descs.append(desc(t, ggml_type))
         self._torch.append(t)
         return len(self._descs) - 1
@@ -862,8 +864,23 @@ class Graph:
     def rebind(self, i: int, t: torch.Tensor, ggml_type: Optional[int] = None) -> None:
         """Tensor i of the list becomes t (another buffer, or a view of
         another length: the next step of a loop)."""
-        self._descs[i] = desc(t, ggml_type)
+        if self._bound is not None:
+            self._bound[0][i] = desc(t, ggml_type)   # copied into the array _descs[i] views
+        else:
+            self._descs[i] = desc(t, ggml_type)
         self._torch[i] = t
+
+    def bind_arrays(self, keep=()):
+        """Builds the arrays the C calls take once and makes the list's
+        descriptors and nodes views of them, so a loop that changes a few
+        descriptors (rebind, or their fields set in place) or node
+        parameters between calls passes the same arrays again without
+        rebuilding them.  Adding a tensor or a node unbinds."""
+        T, N, K = self._arrays(keep)
+        self._descs = [T[i] for i in range(len(self._descs))]
+        self.nodes = [N[i] for i in range(len(self.nodes))]
+        self._bound = (T, N, K, tuple(keep))
+        return T, N, K
 
     def node(self, op: int, dst: int, src=(), iparam: int = 0, fparam: float = 0.0,
              rope: Optional[RopeCache] = None, conv=(0, 0, 0), conv_w=None) -> int:
@@ -878,10 +895,13 @@ class Graph:
         cv = list(conv) + [0] * (3 - len(conv))
         n.conv[0], n.conv[1], n.conv[2] = cv[0], cv[1], cv[2]
         n.conv_w = conv_w.handle.value if isinstance(conv_w, Conv1dWeights) else conv_w
+        self._bound = None
         self.nodes.append(n)
         return dst
 
     def _arrays(self, keep):
+        if self._bound is not None and self._bound[3] == tuple(keep):
+            return self._bound[:3]
         T = (Tensor * max(1, len(self._descs)))(*self._descs)
         N = (GNode * max(1, len(self.nodes)))(*self.nodes)
         K = (ctypes.c_int32 * max(1, len(keep)))(*keep)

@@ -10,8 +10,9 @@
 //
 // Rows up to 4096 with ne0 % 4 == 0: one wave per row, the row in
 // registers (one read, one write), the max by a butterfly of lane shuffles
-// (exact in any order), the sum by the f64 DPP butterfly.  Other rows: a
-// workgroup per row, three passes.
+// (exact in any order), the sum by the f64 DPP butterfly.  Few rows up to
+// 4096 (a decode step's): a workgroup per row, the row in registers, one
+// kernel for every length.  Other rows: a workgroup per row, three passes.
 #include "cbx_rowops.h"
 
 namespace cbx {
@@ -105,6 +106,57 @@ __global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
     }
 }
 
+// Few rows of up to 4096 scores at any alignment (the decode step's H
+// rows of n_past + 1 columns): one 256-lane workgroup a row, the row in
+// registers (16 columns a lane, loads issued together), the max and the
+// f64 sum over the workgroup.  One kernel for every length up to 4096, so a
+// decode loop whose rows grow by one column a token launches the same
+// kernel each token and a captured graph takes the new length in place.
+__global__ __launch_bounds__(kThreads) void k_soft_max_row(View x, View y, float s, int64_t n_past, bool fx, bool fy) {
+    constexpr int K = kWaveMaxRow / kThreads;
+    __shared__ double red[kThreads / WAVE];
+    __shared__ float redf[kThreads / WAVE];
+    const int64_t r = blockIdx.x;
+    const int64_t ne0 = x.ne[0];
+    const float* xr = reinterpret_cast<const float*>(x.data + row_offset(x, r, fx));
+    float* yr = reinterpret_cast<float*>(y.data + row_offset(y, r, fy));
+    const int64_t j = r % x.ne[1];
+    const int64_t lim = n_past >= 0 ? (n_past + j < ne0 - 1 ? n_past + j : ne0 - 1) : ne0 - 1;
+    float v[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int64_t c = threadIdx.x + static_cast<int64_t>(k) * kThreads;
+        v[k] = xr[c < ne0 ? c : 0];
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int64_t c = threadIdx.x + static_cast<int64_t>(k) * kThreads;
+        v[k] = c < ne0 ? masked(v[k], s, c, lim) : -INFINITY;
+        m = fmaxf(m, v[k]);
+    }
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) redf[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kThreads / WAVE; w++) m = fmaxf(m, redf[w]);
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int64_t c = threadIdx.x + static_cast<int64_t>(k) * kThreads;
+        v[k] = c < ne0 ? expf(v[k] - m) : 0.0f;
+        sum += static_cast<double>(v[k]);
+    }
+    sum = block_sum(sum, red);
+    const float inv = static_cast<float>(1.0 / sum);
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int64_t c = threadIdx.x + static_cast<int64_t>(k) * kThreads;
+        if (c < ne0) yr[c] = v[k] * inv;
+    }
+}
+
 // Any row length: max, then the f64 sum of exponentials, then the output,
 // each pass over the row (the exponentials are recomputed identically).
 __global__ __launch_bounds__(kThreads) void k_soft_max_loop(View x, View y, float s, int64_t n_past, bool fx,
@@ -156,7 +208,11 @@ int launch_soft_max(const cbx_tensor* x, float s, int64_t n_past, cbx_tensor* y,
                      (x->ne[2] <= 1 || x->nb[2] % 16 == 0) && (x->ne[3] <= 1 || x->nb[3] % 16 == 0) &&
                      (y->ne[2] <= 1 || y->nb[2] % 16 == 0) && (y->ne[3] <= 1 || y->nb[3] % 16 == 0);
     if (nr >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "soft_max: too many rows");
-    if (vec) {
+    if (ne0 <= kWaveMaxRow && nr < int64_t{4} * st->n_cu) {
+        // few rows (a decode step's heads): one kernel whatever the length
+        hipLaunchKernelGGL(k_soft_max_row, dim3(static_cast<unsigned>(nr)), dim3(kThreads), 0, strm, vx, vy, s, n_past,
+                           fx, fy);
+    } else if (vec) {
         const int64_t need = cdiv(ne0, 256);
         const int nv = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : 16;
         SoftMaxArgs a;

@@ -253,3 +253,52 @@ def t3_block_bytes() -> dict:
     bias_gelu = 2 * N * F * 4 + F * 4
     return {"residual_ln2": join, "fc_bias_gelu": bias_gelu, "residual_next_ln1": join,
             "ggml_nodes": 2 * 11 * act + 4 * N * F * 4}
+
+
+# ---- workload 6: the T3 decode step's element-wise nodes, one token -------------
+# Chatterbox-Turbo's T3 (t3.h): 24 blocks, width 1024, 16 heads of 64, FFN
+# 4096; the speech-token table (6563 rows) and the learned position table
+# (8196 rows) are F16 in the shipped GGUF (convert_chatterbox_to_gguf.py:277-290).
+T3_LAYERS = 24
+T3_HEADS = 16
+T3_SPEECH_VOCAB = 6563
+T3_POS_ROWS = 8196
+T3_MAX_CTX = 1024
+
+
+def t3_token_inputs(n_layers: int = T3_LAYERS, max_ctx: int = T3_MAX_CTX) -> dict:
+    """Tables, per-block parameters and per-block matmul outputs of one T3
+    decode step at N_new = 1 (t3.cpp:446-546); per-block arrays are stacked
+    [n_layers, width].  kq holds H x max_ctx scores a block: the step with
+    n_past uses its first H x (n_past + 1) floats as (H, 1, n_past + 1), the
+    contiguous output of mul_mat(K, Q)."""
+    w = 6
+    L, D, F, H = n_layers, D_MODEL, D_FF, T3_HEADS
+    return {
+        "speech_emb": normal(seed_of(w, 0), (T3_SPEECH_VOCAB, D), 0.0, 0.02).astype(np.float16),
+        "pos_embd": normal(seed_of(w, 1), (T3_POS_ROWS, D), 0.0, 0.02).astype(np.float16),
+        "ln1_w": normal(seed_of(w, 2), (L, D), 1.0, 0.02), "ln1_b": normal(seed_of(w, 3), (L, D), 0.0, 0.02),
+        "qkv_b": normal(seed_of(w, 4), (L, 3 * D), 0.0, 0.02), "out_b": normal(seed_of(w, 5), (L, D), 0.0, 0.02),
+        "ln2_w": normal(seed_of(w, 6), (L, D), 1.0, 0.02), "ln2_b": normal(seed_of(w, 7), (L, D), 0.0, 0.02),
+        "fc_b": normal(seed_of(w, 8), (L, F), 0.0, 0.02), "proj_b": normal(seed_of(w, 9), (L, D), 0.0, 0.02),
+        "qkv_mm": normal(seed_of(w, 10), (L, 3 * D)), "kq": normal(seed_of(w, 11), (L, H * max_ctx), 0.0, 3.0),
+        "out_mm": normal(seed_of(w, 12), (L, D), 0.0, 0.5), "fc_mm": normal(seed_of(w, 13), (L, F)),
+        "proj_mm": normal(seed_of(w, 14), (L, D), 0.0, 0.5),
+        "out_w": normal(seed_of(w, 15), (D,), 1.0, 0.02), "out_b_final": normal(seed_of(9, 0), (D,), 0.0, 0.02),
+    }
+
+
+def t3_token_bytes(n_layers: int = T3_LAYERS, n_past: int = 0) -> int:
+    """Algorithmic bytes of one token's element-wise launches: every input
+    read once and every output written once (embedding: two F16 rows in, h
+    and LN-1 out; per block: the qkv bias add, the scores, the residual
+    joins with their LayerNorms, the fc bias + GELU; vectors counted once)."""
+    D, F, H = D_MODEL, D_FF, T3_HEADS
+    n_kv = n_past + 1
+    emb = 2 * D * 2 + 2 * D * 4 + 2 * D * 4
+    per = (3 * D * 4 * 3                      # qkv_mm + qkv_b in, qkv out
+           + 2 * H * n_kv * 4                 # scores in, probabilities out
+           + (3 * D * 4 + 3 * D * 4 + 2 * D * 4)   # out_mm, h in, out_b; attn_res, ln2 out; ln2 w, b
+           + 3 * F * 4                        # fc_mm + fc_b in, gelu out
+           + (3 * D * 4 + 3 * D * 4 + 2 * D * 4))  # proj_mm, attn_res, proj_b; h, ln out; ln w, b
+    return emb + n_layers * per

@@ -1014,3 +1014,83 @@ int cbxo_conv_transpose1d(const cbxo_tensor* x, const cbxo_tensor* w, int stride
     free(wf);
     return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* the T3 decode step's element-wise nodes (t3.cpp:446-546, N_new = 1)       */
+/* ------------------------------------------------------------------------ */
+
+static cbxo_tensor f32_2d(const float* p, int64_t ne0, int64_t ne1) {
+    cbxo_tensor t;
+    memset(&t, 0, sizeof(t));
+    t.data = (void*)p;
+    t.type = CBXO_TYPE_F32;
+    t.ne[0] = ne0;
+    t.ne[1] = ne1;
+    t.ne[2] = 1;
+    t.ne[3] = 1;
+    t.nb[0] = 4;
+    t.nb[1] = 4 * (size_t)ne0;
+    t.nb[2] = t.nb[1] * (size_t)ne1;
+    t.nb[3] = t.nb[2];
+    return t;
+}
+
+int cbxo_t3_token_step(const cbxo_tensor* tok_table, int32_t token, const cbxo_tensor* pos_table,
+                       int32_t position, int64_t d_ff, int64_t n_head, int32_t n_past, float eps,
+                       const cbxo_t3_block* blocks, int32_t n_blocks, const float* out_w, const float* out_b,
+                       float* h0, float* y) {
+    const int64_t D = tok_table->ne[0];
+    if (pos_table->ne[0] != D || n_head <= 0 || D % n_head || n_past < 0 || n_blocks < 0) return -1;
+    const int64_t n_kv = (int64_t)n_past + 1;
+    /* the reference's score scale, 1/sqrt(head size) in f32 (t3.cpp:513) */
+    const float kq_scale = 1.0f / sqrtf((float)(D / n_head));
+    float* tmp = (float*)malloc(sizeof(float) * (size_t)(2 * D + d_ff));
+    if (!tmp) return -1;
+    float* t0 = tmp;          /* (D) a row before its next add / norm */
+    float* t1 = tmp + D;      /* (D) */
+    int rc = 0;
+    /* the input embedding: get_rows -> cast(F32), twice, then add */
+    const int32_t ids[2] = {token, position};
+    cbxo_tensor tid = f32_2d(NULL, 1, 1), pid = f32_2d(NULL, 1, 1);
+    tid.data = (void*)&ids[0];
+    tid.type = CBXO_TYPE_I32;
+    pid.data = (void*)&ids[1];
+    pid.type = CBXO_TYPE_I32;
+    cbxo_tensor r0 = f32_2d(t0, D, 1), r1 = f32_2d(t1, D, 1), th = f32_2d(h0, D, 1);
+    rc = cbxo_get_rows(tok_table, &tid, &r0, 1);
+    if (!rc) rc = cbxo_get_rows(pos_table, &pid, &r1, 1);
+    if (!rc) rc = cbxo_add(&r0, &r1, &th, 1);
+    const float* h = h0;
+    for (int32_t il = 0; il < n_blocks && !rc; il++) {
+        const cbxo_t3_block* B = &blocks[il];
+        cbxo_tensor hin = f32_2d(h, D, 1);
+        cbxo_tensor w1 = f32_2d(B->ln1_w, D, 1), b1 = f32_2d(B->ln1_b, D, 1), l1 = f32_2d(B->ln1, D, 1);
+        rc = cbxo_layer_norm(&hin, &w1, &b1, eps, &l1, 1);
+        cbxo_tensor qm = f32_2d(B->qkv_mm, 3 * D, 1), qb = f32_2d(B->qkv_b, 3 * D, 1), qo = f32_2d(B->qkv, 3 * D, 1);
+        if (!rc) rc = cbxo_add(&qm, &qb, &qo, 1);
+        cbxo_tensor kq = f32_2d(B->kq, n_kv, n_head), pr = f32_2d(B->probs, n_kv, n_head);
+        if (!rc) rc = cbxo_scale_diag_mask_soft_max(&kq, kq_scale, n_past, &pr, 1);
+        /* attn_residual = add(add(out_mm, out_b), h) */
+        cbxo_tensor om = f32_2d(B->out_mm, D, 1), ob = f32_2d(B->out_b, D, 1), ar = f32_2d(B->attn_res, D, 1);
+        if (!rc) rc = cbxo_add(&om, &ob, &r0, 1);
+        if (!rc) rc = cbxo_add(&r0, &hin, &ar, 1);
+        cbxo_tensor w2 = f32_2d(B->ln2_w, D, 1), b2 = f32_2d(B->ln2_b, D, 1), l2 = f32_2d(B->ln2, D, 1);
+        if (!rc) rc = cbxo_layer_norm(&ar, &w2, &b2, eps, &l2, 1);
+        /* gelu(add(fc_mm, fc_b)) */
+        cbxo_tensor fm = f32_2d(B->fc_mm, d_ff, 1), fb = f32_2d(B->fc_b, d_ff, 1), fs = f32_2d(tmp + 2 * D, d_ff, 1);
+        cbxo_tensor go = f32_2d(B->gelu, d_ff, 1);
+        if (!rc) rc = cbxo_add(&fm, &fb, &fs, 1);
+        if (!rc) rc = cbxo_unary(CBXO_UNARY_GELU, &fs, &go, 1);
+        /* h = add(add(proj_mm, proj_b), attn_residual) */
+        cbxo_tensor pm = f32_2d(B->proj_mm, D, 1), pb = f32_2d(B->proj_b, D, 1), ho = f32_2d(B->h, D, 1);
+        if (!rc) rc = cbxo_add(&pm, &pb, &r0, 1);
+        if (!rc) rc = cbxo_add(&r0, &ar, &ho, 1);
+        h = B->h;
+    }
+    if (!rc) {
+        cbxo_tensor hin = f32_2d(h, D, 1), w = f32_2d(out_w, D, 1), b = f32_2d(out_b, D, 1), yo = f32_2d(y, D, 1);
+        rc = cbxo_layer_norm(&hin, &w, &b, eps, &yo, 1);
+    }
+    free(tmp);
+    return rc;
+}

@@ -174,6 +174,48 @@ int cbxo_conv_transpose1d(const cbxo_tensor* x, const cbxo_tensor* w,
                           const cbxo_tensor* bias, cbxo_tensor* y,
                           int n_threads);
 
+/* ---- the T3 decode step's element-wise nodes --------------------------- */
+/* One T3 block at N_new = 1 (t3.cpp:460-542) with its matmul outputs given:
+ * the parameters it adds or scales by, those outputs, and where each of its
+ * element-wise results goes.  F32, contiguous.  D = model width, F = FFN
+ * width, H = heads, n_kv = n_past + 1 attention columns a head.            */
+typedef struct cbxo_t3_block {
+    const float *ln1_w, *ln1_b;  /* (D) LN-1 (t3.cpp:465-466)               */
+    const float *qkv_b;          /* (3D) (t3.cpp:470)                       */
+    const float *out_b;          /* (D) (t3.cpp:526)                        */
+    const float *ln2_w, *ln2_b;  /* (D) LN-2 (t3.cpp:531-532)               */
+    const float *fc_b;           /* (F) (t3.cpp:536)                        */
+    const float *proj_b;         /* (D) (t3.cpp:540)                        */
+    const float *qkv_mm;         /* (3D) mul_mat(qkv_w, ln1)                */
+    const float *kq;             /* (H, n_kv) mul_mat(K, Q)                 */
+    const float *out_mm;         /* (D) mul_mat(out_w, attention)           */
+    const float *fc_mm;          /* (F) mul_mat(fc_w, ln2)                  */
+    const float *proj_mm;        /* (D) mul_mat(proj_w, gelu)               */
+    float *ln1;                  /* (D) LN-1 of the block's input h         */
+    float *qkv;                  /* (3D) qkv_mm + qkv_b                     */
+    float *probs;                /* (H, n_kv) soft_max(mask(scale(kq)))     */
+    float *attn_res;             /* (D) (out_mm + out_b) + h                */
+    float *ln2;                  /* (D) LN-2 of attn_res                    */
+    float *gelu;                 /* (F) gelu(fc_mm + fc_b)                  */
+    float *h;                    /* (D) (proj_mm + proj_b) + attn_res       */
+} cbxo_t3_block;
+
+/* The element-wise nodes of one T3 decode step at N_new = 1 in the order
+ * the reference builds them (t3.cpp:446-455 the input embedding of
+ * `token` at `position`: get_rows -> cast, twice, then add; then per
+ * block LN-1, the qkv bias, scale(1/sqrt(D/H)) -> diag_mask_inf(n_past)
+ * -> soft_max, the output bias and residual, LN-2, the fc bias and GELU,
+ * the projection bias and residual; t3.cpp:545-546 the final LN into y).
+ * tok_table, pos_table: F32 or F16 (D wide).  h0 (D) gets the embedding
+ * sum.  One thread: at N_new = 1 every op is one row.  Returns 0, or a
+ * negative value on invalid input.                                        */
+int cbxo_t3_token_step(const cbxo_tensor* tok_table, int32_t token,
+                       const cbxo_tensor* pos_table, int32_t position,
+                       int64_t d_ff, int64_t n_head, int32_t n_past,
+                       float eps, const cbxo_t3_block* blocks,
+                       int32_t n_blocks, const float* out_w,
+                       const float* out_b, float* h0, float* y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,6 +78,9 @@ def lib():
             "cbxo_scale_diag_mask_soft_max": (i, [P, f, i, P, i]),
             "cbxo_conv1d": (i, [P, P, i, i, i, i, P, P, f, P, P, P, i]),
             "cbxo_conv_transpose1d": (i, [P, P, i, i, i, P, P, f, P, P, i]),
+            "cbxo_t3_token_step": (i, [P, ctypes.c_int32, P, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64,
+                                       ctypes.c_int32, f, ctypes.POINTER(T3Block), ctypes.c_int32, vp, vp, vp,
+                                       vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -382,3 +385,53 @@ def conv_transpose1d(x, w, stride, pad=0, prologue=0, alpha=None, alpha_inv=None
                                        opt(keep[0]), opt(keep[1]), slope, opt(keep[2]), _ref(desc(out)), nth),
            "conv_transpose1d")
     return out
+
+
+# ---- the T3 decode step's element-wise nodes (t3.cpp:446-546, N_new = 1) ----
+
+T3_BLOCK_IN = ("ln1_w", "ln1_b", "qkv_b", "out_b", "ln2_w", "ln2_b", "fc_b", "proj_b",
+               "qkv_mm", "kq", "out_mm", "fc_mm", "proj_mm")
+T3_BLOCK_OUT = ("ln1", "qkv", "probs", "attn_res", "ln2", "gelu", "h")
+
+
+class T3Block(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in T3_BLOCK_IN + T3_BLOCK_OUT]
+
+
+class T3TokenStep:
+    """cbxo_t3_token_step over the arrays of workloads.t3_token_inputs: one
+    token's element-wise nodes in the reference's order, one thread.  The
+    block table is built once per n_past, so run() is one C call (the CPU
+    baseline times it).  Outputs: h0, y and per block the T3_BLOCK_OUT
+    arrays (probs as (H, n_past + 1))."""
+
+    def __init__(self, inp: dict, n_past: int, n_head: int = 16, eps: float = 1e-5):
+        self.inp, self.n_past, self.n_head, self.eps = inp, int(n_past), int(n_head), float(eps)
+        L, D = inp["ln1_w"].shape
+        F = inp["fc_b"].shape[1]
+        n_kv = self.n_past + 1
+        self.d_ff = F
+        self.kq = [np.ascontiguousarray(inp["kq"][il, :n_head * n_kv].reshape(n_head, n_kv)) for il in range(L)]
+        self.out = {"h0": np.empty((1, D), np.float32), "y": np.empty((1, D), np.float32)}
+        shapes = {"ln1": (L, D), "qkv": (L, 3 * D), "probs": (L, n_head, n_kv), "attn_res": (L, D),
+                  "ln2": (L, D), "gelu": (L, F), "h": (L, D)}
+        for k, shp in shapes.items():
+            self.out[k] = np.full(shp, np.nan, np.float32)
+        self.blocks = (T3Block * L)()
+        for il in range(L):
+            b = self.blocks[il]
+            for k in T3_BLOCK_IN:
+                a = self.kq[il] if k == "kq" else inp[k][il]
+                assert a.dtype == np.float32 and a.flags.c_contiguous
+                setattr(b, k, a.ctypes.data)
+            for k in T3_BLOCK_OUT:
+                setattr(b, k, self.out[k][il].ctypes.data)
+        self._tok = desc(inp["speech_emb"])
+        self._pos = desc(inp["pos_embd"])
+
+    def run(self, token: int, position: int) -> dict:
+        _check(lib().cbxo_t3_token_step(_ref(self._tok), int(token), _ref(self._pos), int(position), self.d_ff,
+                                         self.n_head, self.n_past, self.eps, self.blocks, len(self.blocks),
+                                         self.inp["out_w"].ctypes.data, self.inp["out_b_final"].ctypes.data,
+                                         self.out["h0"].ctypes.data, self.out["y"].ctypes.data), "t3_token_step")
+        return self.out
