@@ -5,6 +5,7 @@
 // evaluated with one rounding per operation, as ggml-cpu's scalar code is.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -155,6 +156,7 @@ static void yarn_cos_sin(float theta_extrap, int64_t i0, const RopeParams& p, fl
 }  // namespace cbx
 
 struct cbx_conv1d_weights {
+    uint64_t  serial;   // distinct for every handle this process creates
     int       device;
     int       up;       // 0: conv1d weights; >= 1: transposed conv with this stride
     int64_t   k;        // the weight's taps
@@ -169,12 +171,20 @@ bool cbx::conv1d_weights_match(const cbx_conv1d_weights* w, int up, int64_t k, i
 }
 
 struct cbx_rope_cache {
+    uint64_t         serial;       // distinct for every handle this process creates
     int              device;
     cbx::RopeParams  p;
     int32_t          n_pos;
     float2*          table;        // [n_pos][n_dims/2] (cos, sin)
     float*           freq_factors; // device copy or nullptr
 };
+
+// Serial numbers of the handles: a graph exec compares them to tell a
+// handle from a new one at the same address.
+static std::atomic<uint64_t> g_handle_serial{1};
+
+uint64_t cbx::rope_cache_serial(const cbx_rope_cache* c) { return c ? c->serial : 0; }
+uint64_t cbx::conv1d_weights_serial(const cbx_conv1d_weights* w) { return w ? w->serial : 0; }
 
 using namespace cbx;
 
@@ -736,6 +746,7 @@ int cbx_rope_cache_create(int n_dims, int mode, int n_ctx_orig, float freq_base,
         }
     }
     auto* cache = new cbx_rope_cache();
+    cache->serial = g_handle_serial.fetch_add(1);
     cache->device = dev;
     cache->p = p;
     cache->n_pos = n_pos;
@@ -942,6 +953,7 @@ static int conv_weights_create(const cbx_tensor* w, int up, cbx_stream stream, c
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return set_error(CBX_ERR_HIP, std::string(what) + ": hipGetDevice failed");
     auto* cw = new cbx_conv1d_weights();
+    cw->serial = g_handle_serial.fetch_add(1);
     cw->device = dev;
     cw->up = up;
     cw->k = w->ne[0];

@@ -30,6 +30,8 @@
 // layouts as they do for any caller.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cstring>
 #include <new>
 #include <string>
 #include <vector>
@@ -914,10 +916,24 @@ int cbx_graph_launch(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gno
 // before the previous update.  Events recorded by each update, on every
 // stream the exec was launched on since the one before, mark them (one
 // event a stream per update, none per replay).
+//
+// Each instantiation remembers the plan it holds, each launch's signature
+// (every value its kernels are built from) and which of its graph's kernel
+// nodes each launch issued.  An update whose plan has the same launches
+// re-records only the launches whose signature changed and sets their
+// kernel nodes' arguments in the instantiated graph (a decode loop's next
+// token changes a few launches of many); anything else records the whole
+// list and updates or re-instantiates the graph.
 struct GraphInst {
-    hipGraph_t graph = nullptr;
+    hipGraph_t graph = nullptr;            // the graph `exec` was instantiated from
     hipGraphExec_t exec = nullptr;
-    int32_t n_launches = 0;
+    int32_t n_launches = 0;                // kernel launches of one replay
+    bool indexed = false;                  // the fields below describe `exec`
+    std::vector<hipGraphNode_t> knodes;    // graph's kernel nodes in launch order
+    std::vector<cbx_glaunch> ls;           // the plan it holds
+    std::vector<int32_t> k0, kn;           // per launch: first kernel node, kernel count
+    std::vector<uint64_t> sig;             // the launches' signatures, back to back
+    std::vector<size_t> sig_at;            // launch i's signature: [sig_at[i], sig_at[i + 1])
 };
 
 struct cbx_graph_exec {
@@ -962,18 +978,73 @@ static int mark_launches(cbx_graph_exec* x, const char* f) {
     return CBX_OK;
 }
 
-// Plans the list and records its launches on cs (a stream of the exec's
-// own, so nothing else the caller has queued ends up in the graph) into a
-// new HIP graph (*out); *issued gets the kernel launch count.  f names the
-// caller in errors.
-static int capture_list(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes,
-                        const int32_t* keep, int32_t n_keep, hipStream_t cs, hipGraph_t* out, int32_t* issued,
-                        const char* f) {
-    *out = nullptr;
-    *issued = 0;
-    std::vector<cbx_glaunch> ls;
-    int rc = plan(tensors, n_tensors, nodes, n_nodes, keep, n_keep, &ls, f);
-    if (rc) return rc;
+// Every value a launch's kernels are built from: its place and kind, every
+// field of its nodes, every field of the tensors they name, and the serial
+// numbers of the RoPE cache and conv weights they use (a new handle at a
+// freed one's address differs).  Equal signatures issue equal kernels with
+// equal arguments.
+static void launch_signature(const cbx_tensor* t, const cbx_gnode* nd, const cbx_glaunch& l,
+                             std::vector<uint64_t>* sig) {
+    auto u = [](auto v) { return static_cast<uint64_t>(v); };
+    sig->insert(sig->end(), {u(l.kind), u(l.first_node), u(l.n_nodes), u(l.flags)});
+    for (int32_t i = l.first_node; i < l.first_node + l.n_nodes; i++) {
+        const cbx_gnode& n = nd[i];
+        uint32_t fb;
+        std::memcpy(&fb, &n.fparam, 4);
+        sig->insert(sig->end(), {u(n.op), u(n.dst), u(n.src[0]), u(n.src[1]), u(n.iparam), u(fb),
+                                 u(reinterpret_cast<uintptr_t>(n.rope)), rope_cache_serial(n.rope), u(n.conv[0]),
+                                 u(n.conv[1]), u(n.conv[2]), u(reinterpret_cast<uintptr_t>(n.conv_w)),
+                                 conv1d_weights_serial(n.conv_w)});
+        for (int32_t k : {n.dst, n.src[0], n.src[1]}) {
+            if (k < 0) {
+                sig->push_back(~uint64_t{0});
+                continue;
+            }
+            const cbx_tensor& x = t[k];
+            sig->insert(sig->end(), {u(reinterpret_cast<uintptr_t>(x.data)), u(x.type), u(x.reserved), u(x.ne[0]),
+                                     u(x.ne[1]), u(x.ne[2]), u(x.ne[3]), u(x.nb[0]), u(x.nb[1]), u(x.nb[2]),
+                                     u(x.nb[3])});
+        }
+    }
+}
+
+static void signatures(const cbx_tensor* t, const cbx_gnode* nd, const std::vector<cbx_glaunch>& ls,
+                       std::vector<uint64_t>* sig, std::vector<size_t>* at) {
+    sig->clear();
+    at->assign(1, 0);
+    for (const cbx_glaunch& l : ls) {
+        launch_signature(t, nd, l, sig);
+        at->push_back(sig->size());
+    }
+}
+
+// The kernel nodes of a graph recorded from one stream, in order: a chain
+// from its one root.  False when the graph is not such a chain of kernel
+// nodes.
+static bool kernel_chain(hipGraph_t g, std::vector<hipGraphNode_t>* out) {
+    out->clear();
+    size_t n = 0;
+    if (hipGraphGetNodes(g, nullptr, &n) != hipSuccess) return false;
+    if (n == 0) return true;
+    size_t nr = 1;
+    hipGraphNode_t node = nullptr;
+    if (hipGraphGetRootNodes(g, &node, &nr) != hipSuccess || nr != 1) return false;
+    out->reserve(n);
+    while (node) {
+        hipGraphNodeType ty;
+        if (hipGraphNodeGetType(node, &ty) != hipSuccess || ty != hipGraphNodeTypeKernel) return false;
+        out->push_back(node);
+        size_t nd = 0;
+        if (hipGraphNodeGetDependentNodes(node, nullptr, &nd) != hipSuccess || nd > 1) return false;
+        hipGraphNode_t next = nullptr;
+        if (nd == 1 && hipGraphNodeGetDependentNodes(node, &next, &nd) != hipSuccess) return false;
+        node = nd == 1 ? next : nullptr;
+    }
+    return out->size() == n;
+}
+
+// The unsupported-node check every recording makes first.
+static int refuse_unsupported(const cbx_gnode* nodes, const std::vector<cbx_glaunch>& ls, const char* f) {
     for (const cbx_glaunch& l : ls) {
         if (l.kind == CBX_GL_UNSUPPORTED) {
             return set_error(CBX_ERR_UNSUPPORTED, std::string(f) + ": node " + std::to_string(l.first_node) + " (" +
@@ -981,12 +1052,31 @@ static int capture_list(const cbx_tensor* tensors, int32_t n_tensors, const cbx_
                                                       ") starts no chain the library runs");
         }
     }
+    return CBX_OK;
+}
+
+// Records launches ls[which[0]], ls[which[1]], .. (every launch when which
+// is NULL) on cs (a stream of the exec's own, so nothing else the caller has
+// queued ends up in the graph) into a new HIP graph (*out); kcount[j] gets
+// the kernel nodes launch j of the recording added (-1 when that could not
+// be read) and *issued the kernel launch count.  f names the caller in
+// errors.
+static int record(const cbx_tensor* tensors, const cbx_gnode* nodes, int32_t n_nodes,
+                  const std::vector<cbx_glaunch>& ls, const std::vector<int32_t>* which, hipStream_t cs,
+                  hipGraph_t* out, std::vector<int32_t>* kcount, int32_t* issued, const char* f) {
+    *out = nullptr;
+    *issued = 0;
+    kcount->clear();
     if (hipStreamBeginCapture(cs, hipStreamCaptureModeRelaxed) != hipSuccess) {
         return set_error(CBX_ERR_HIP, std::string(f) + ": stream capture failed to start");
     }
+    int rc = CBX_OK;
     int32_t n = 0;
+    size_t before = 0;
     std::string inner;
-    for (const cbx_glaunch& l : ls) {
+    const size_t count = which ? which->size() : ls.size();
+    for (size_t j = 0; j < count; j++) {
+        const cbx_glaunch& l = ls[which ? static_cast<size_t>((*which)[j]) : j];
         rc = run(tensors, nodes, n_nodes, l, cs);
         if (rc) {
             inner = "nodes " + std::to_string(l.first_node) + ".." + std::to_string(l.first_node + l.n_nodes - 1) +
@@ -994,17 +1084,49 @@ static int capture_list(const cbx_tensor* tensors, int32_t n_tensors, const cbx_
             break;
         }
         if (l.kind != CBX_GL_VIEW) n++;
+        // the nodes the capture holds now, less those before this launch
+        hipStreamCaptureStatus cst;
+        hipGraph_t cg = nullptr;
+        size_t now = 0;
+        if (hipStreamGetCaptureInfo_v2(cs, &cst, nullptr, &cg, nullptr, nullptr) == hipSuccess && cg &&
+            hipGraphGetNodes(cg, nullptr, &now) == hipSuccess && now >= before) {
+            kcount->push_back(static_cast<int32_t>(now - before));
+            before = now;
+        } else {
+            kcount->push_back(-1);
+        }
     }
     hipGraph_t g = nullptr;
     const hipError_t ec = hipStreamEndCapture(cs, &g);
     if (rc || ec != hipSuccess || !g) {
-        if (g) hipGraphDestroy(g);
+        if (g) (void)hipGraphDestroy(g);
         if (rc) return set_error(rc, std::string(f) + ": " + inner);
         return set_error(CBX_ERR_HIP, std::string(f) + ": stream capture failed: " + hipGetErrorString(ec));
     }
     *out = g;
     *issued = n;
     return CBX_OK;
+}
+
+// Fills an instantiation's bookkeeping for the plan it now holds, recorded
+// with per-launch kernel counts kcount; indexed stays false when the
+// graph's kernel nodes cannot be matched to the launches.
+static void index_inst(GraphInst* t, const cbx_tensor* tensors, const cbx_gnode* nodes,
+                       const std::vector<cbx_glaunch>& ls, const std::vector<int32_t>& kcount, bool keep_nodes) {
+    t->indexed = false;
+    t->ls = ls;
+    signatures(tensors, nodes, ls, &t->sig, &t->sig_at);
+    t->k0.assign(ls.size(), 0);
+    t->kn.assign(ls.size(), 0);
+    int32_t at = 0;
+    for (size_t i = 0; i < ls.size(); i++) {
+        if (i >= kcount.size() || kcount[i] < 0) return;
+        t->k0[i] = at;
+        t->kn[i] = kcount[i];
+        at += kcount[i];
+    }
+    if (!keep_nodes && !kernel_chain(t->graph, &t->knodes)) return;
+    t->indexed = static_cast<int32_t>(t->knodes.size()) == at;
 }
 
 int cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes,
@@ -1016,13 +1138,19 @@ int cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors, const cb
     *out = nullptr;
     int rc = CBX_OK;
     if (!current_state(&rc)) return rc;
+    std::vector<cbx_glaunch> ls;
+    if ((rc = plan(tensors, n_tensors, nodes, n_nodes, keep, n_keep, &ls, f)) ||
+        (rc = refuse_unsupported(nodes, ls, f))) {
+        return rc;
+    }
     hipStream_t cs = nullptr;
     if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) {
         return set_error(CBX_ERR_HIP, std::string(f) + ": stream creation failed");
     }
     hipGraph_t g[2] = {nullptr, nullptr};
     int32_t issued = 0;
-    rc = capture_list(tensors, n_tensors, nodes, n_nodes, keep, n_keep, cs, &g[0], &issued, f);
+    std::vector<int32_t> kcount;
+    rc = record(tensors, nodes, n_nodes, ls, nullptr, cs, &g[0], &kcount, &issued, f);
     if (rc == CBX_OK && hipGraphClone(&g[1], g[0]) != hipSuccess) {
         rc = set_error(CBX_ERR_HIP, std::string(f) + ": graph clone failed");
     }
@@ -1044,10 +1172,71 @@ int cbx_graph_exec_create(const cbx_tensor* tensors, int32_t n_tensors, const cb
     }
     (void)hipGetDevice(&x->device);
     x->cs = cs;
-    for (int k = 0; k < 2; k++) x->inst[k] = GraphInst{g[k], ge[k], issued};
+    for (int k = 0; k < 2; k++) {
+        GraphInst& t = x->inst[k];
+        t.graph = g[k];
+        t.exec = ge[k];
+        t.n_launches = issued;
+        index_inst(&t, tensors, nodes, ls, kcount, false);
+    }
     x->cur = 0;
     *out = x;
     if (n_launches) *n_launches = issued;
+    return CBX_OK;
+}
+
+// The targeted update: the launches whose signature changed, recorded
+// alone, their kernels' arguments set on t's kernel nodes.  *done = false
+// (and nothing fatal) when the update has to take the whole-list path.
+static int update_changed(cbx_graph_exec* x, GraphInst& t, const cbx_tensor* tensors, const cbx_gnode* nodes,
+                          int32_t n_nodes, const std::vector<cbx_glaunch>& ls, const std::vector<uint64_t>& sig,
+                          const std::vector<size_t>& sig_at, bool* done, const char* f) {
+    *done = false;
+    std::vector<int32_t> changed;
+    for (size_t i = 0; i < ls.size(); i++) {
+        const size_t a = sig_at[i], b = sig_at[i + 1];
+        if (b - a != t.sig_at[i + 1] - t.sig_at[i] ||
+            !std::equal(sig.begin() + static_cast<std::ptrdiff_t>(a), sig.begin() + static_cast<std::ptrdiff_t>(b),
+                        t.sig.begin() + static_cast<std::ptrdiff_t>(t.sig_at[i]))) {
+            changed.push_back(static_cast<int32_t>(i));
+        }
+    }
+    if (!changed.empty()) {
+        hipGraph_t g = nullptr;
+        std::vector<int32_t> kcount;
+        int32_t issued = 0;
+        int rc = record(tensors, nodes, n_nodes, ls, &changed, x->cs, &g, &kcount, &issued, f);
+        if (rc) return rc;   // t untouched
+        std::vector<hipGraphNode_t> gn;
+        bool ok = kernel_chain(g, &gn);
+        size_t want = 0;
+        for (size_t j = 0; ok && j < changed.size(); j++) {
+            ok = kcount[j] == t.kn[static_cast<size_t>(changed[j])];
+            want += static_cast<size_t>(kcount[j] > 0 ? kcount[j] : 0);
+        }
+        ok = ok && gn.size() == want;
+        // each changed launch's kernels, in order, onto the nodes it issued
+        size_t p = 0;
+        for (size_t j = 0; ok && j < changed.size(); j++) {
+            const size_t i = static_cast<size_t>(changed[j]);
+            for (int32_t q = 0; ok && q < t.kn[i]; q++, p++) {
+                hipKernelNodeParams kp;
+                ok = hipGraphKernelNodeGetParams(gn[p], &kp) == hipSuccess &&
+                     hipGraphExecKernelNodeSetParams(t.exec, t.knodes[static_cast<size_t>(t.k0[i] + q)], &kp) ==
+                         hipSuccess;
+            }
+        }
+        (void)hipGraphDestroy(g);
+        if (!ok) {
+            (void)hipGetLastError();
+            t.indexed = false;   // possibly half set: the whole-list path rewrites every node
+            return CBX_OK;
+        }
+    }
+    t.ls = ls;
+    t.sig = sig;
+    t.sig_at = sig_at;
+    *done = true;
     return CBX_OK;
 }
 
@@ -1068,26 +1257,51 @@ int cbx_graph_exec_update(cbx_graph_exec* exec, const cbx_tensor* tensors, int32
     }
     int rc = CBX_OK;
     if (!current_state(&rc)) return rc;
+    std::vector<cbx_glaunch> ls;
+    if ((rc = plan(tensors, n_tensors, nodes, n_nodes, keep, n_keep, &ls, f)) ||
+        (rc = refuse_unsupported(nodes, ls, f))) {
+        return rc;   // exec is left as it was
+    }
+    GraphInst& t = exec->inst[1 - exec->cur];
+    bool same_plan = t.indexed && ls.size() == t.ls.size();
+    for (size_t i = 0; same_plan && i < ls.size(); i++) {
+        same_plan = ls[i].kind == t.ls[i].kind && ls[i].first_node == t.ls[i].first_node &&
+                    ls[i].n_nodes == t.ls[i].n_nodes && ls[i].flags == t.ls[i].flags;
+    }
+    if (same_plan) {
+        std::vector<uint64_t> sig;
+        std::vector<size_t> sig_at;
+        signatures(tensors, nodes, ls, &sig, &sig_at);
+        // the instantiation to re-point is the one not replayed since the
+        // last update: wait for its replays (issued before that update),
+        // then mark the current one's
+        if ((rc = wait_marks(exec, f)) || (rc = mark_launches(exec, f))) return rc;
+        bool done = false;
+        if ((rc = update_changed(exec, t, tensors, nodes, n_nodes, ls, sig, sig_at, &done, f))) return rc;
+        if (done) {
+            exec->cur = 1 - exec->cur;
+            if (n_launches) *n_launches = t.n_launches;
+            if (in_place) *in_place = 1;
+            return CBX_OK;
+        }
+    }
     hipGraph_t g = nullptr;
     int32_t issued = 0;
-    rc = capture_list(tensors, n_tensors, nodes, n_nodes, keep, n_keep, exec->cs, &g, &issued, f);
+    std::vector<int32_t> kcount;
+    rc = record(tensors, nodes, n_nodes, ls, nullptr, exec->cs, &g, &kcount, &issued, f);
     if (rc) return rc;   // exec is left as it was
-    // the instantiation to re-point is the one not replayed since the last
-    // update: wait for its replays (issued before that update), then mark
-    // the current one's
-    if ((rc = wait_marks(exec, f)) || (rc = mark_launches(exec, f))) {
+    if (!same_plan && ((rc = wait_marks(exec, f)) || (rc = mark_launches(exec, f)))) {
         (void)hipGraphDestroy(g);
         return rc;
     }
-    GraphInst& t = exec->inst[1 - exec->cur];
     // the same launches with other arguments: the instantiated graph takes
-    // the new arguments in place
+    // the new arguments in place (its kernel nodes stay those of t.graph)
     hipGraphNode_t bad_node = nullptr;
     hipGraphExecUpdateResult res = hipGraphExecUpdateError;
     if (issued == t.n_launches && hipGraphExecUpdate(t.exec, g, &bad_node, &res) == hipSuccess &&
         res == hipGraphExecUpdateSuccess) {
-        (void)hipGraphDestroy(t.graph);
-        t.graph = g;
+        (void)hipGraphDestroy(g);
+        index_inst(&t, tensors, nodes, ls, kcount, true);
         exec->cur = 1 - exec->cur;
         if (n_launches) *n_launches = issued;
         if (in_place) *in_place = 1;
@@ -1102,7 +1316,10 @@ int cbx_graph_exec_update(cbx_graph_exec* exec, const cbx_tensor* tensors, int32
     }
     (void)hipGraphExecDestroy(t.exec);
     (void)hipGraphDestroy(t.graph);
-    t = GraphInst{g, ge, issued};
+    t.graph = g;
+    t.exec = ge;
+    t.n_launches = issued;
+    index_inst(&t, tensors, nodes, ls, kcount, false);
     exec->cur = 1 - exec->cur;
     if (n_launches) *n_launches = issued;
     return CBX_OK;

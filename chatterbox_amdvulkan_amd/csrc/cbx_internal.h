@@ -153,6 +153,9 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
 // conv1d weight (K, C_in, C_out) when up == 0, else a transposed weight
 // (K, C_out, C_in) split for stride up.
 bool conv1d_weights_match(const cbx_conv1d_weights* w, int up, int64_t k, int64_t c_in, int64_t c_out);
+// Serial numbers distinct for every handle the process creates (0 for NULL).
+uint64_t rope_cache_serial(const cbx_rope_cache* c);
+uint64_t conv1d_weights_serial(const cbx_conv1d_weights* w);
 int launch_snake(const cbx_tensor* x, const cbx_tensor* a, const cbx_tensor* ai, cbx_tensor* y,
                  DeviceState* st, hipStream_t s);
 
