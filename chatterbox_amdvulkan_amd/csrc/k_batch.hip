@@ -17,7 +17,7 @@ constexpr int kThreads = 256;
 constexpr int kRopeMaxHalf = 256;
 
 // ---- norms: wave per row ----------------------------------------------------
-template <typename T, int NV, int KIND>
+template <typename T, int NV, int KIND, bool ACT>
 __device__ __forceinline__ void b_norm_row(const BOp& op, int64_t row, int lane, const uint16_t* tab) {
     const int64_t ne0 = op.ne0;
     const char* xr = op.t[0].p + row * op.t[0].nb1;
@@ -40,26 +40,26 @@ __device__ __forceinline__ void b_norm_row(const BOp& op, int64_t row, int lane,
         if ((lane + 64 * k) * 4 >= ne0) v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     const float scale = wave_row_scale<NV, KIND>(v, lane, ne0, op.eps);
-    if (op.act != CBX_UNARY_NONE) {
+    if (ACT && op.act != CBX_UNARY_NONE) {
         wave_row_store<T, NV, true>(v, lane, ne0, scale, af, w != nullptr, b != nullptr, op.act, tab, yr);
     } else {
         wave_row_store<T, NV, false>(v, lane, ne0, scale, af, w != nullptr, b != nullptr, op.act, tab, yr);
     }
 }
 
-template <typename T, int KIND>
+template <typename T, int KIND, bool ACT>
 __device__ __forceinline__ void b_norm_nv(const BOp& op, int64_t row, int lane, const uint16_t* tab) {
     switch (op.nv) {
-        case 1: b_norm_row<T, 1, KIND>(op, row, lane, tab); break;
-        case 2: b_norm_row<T, 2, KIND>(op, row, lane, tab); break;
-        default: b_norm_row<T, 4, KIND>(op, row, lane, tab); break;
+        case 1: b_norm_row<T, 1, KIND, ACT>(op, row, lane, tab); break;
+        case 2: b_norm_row<T, 2, KIND, ACT>(op, row, lane, tab); break;
+        default: b_norm_row<T, 4, KIND, ACT>(op, row, lane, tab); break;
     }
 }
 
 // One row a workgroup, its 4 waves holding a quarter of it each (rows of
 // 1024 = 4 x 64 lanes x one float4): few rows then still give the SIMDs
 // work, where one wave a row left a 64-row step on 16 workgroups.
-template <typename T, int KIND>
+template <typename T, int KIND, bool ACT>
 __device__ __forceinline__ void b_norm_row4(const BOp& op, int64_t row, const uint16_t* tab, double* lds) {
     const int64_t ne0 = op.ne0;
     const int lane4 = threadIdx.x;   // wave w: float4s [64w, 64w + 64)
@@ -74,36 +74,51 @@ __device__ __forceinline__ void b_norm_row4(const BOp& op, int64_t row, const ui
     v[0] = Elt<T>::load4(xr + (j < ne0 ? j : 0) * Elt<T>::size);
     if (j >= ne0) v[0] = make_float4(0.f, 0.f, 0.f, 0.f);
     const float scale = row_scale_w<1, KIND, 4>(v, lane4, ne0, op.eps, lds);
-    if (op.act != CBX_UNARY_NONE) {
+    if (ACT && op.act != CBX_UNARY_NONE) {
         wave_row_store<T, 1, true>(v, lane4, ne0, scale, af, w != nullptr, b != nullptr, op.act, tab, yr);
     } else {
         wave_row_store<T, 1, false>(v, lane4, ne0, scale, af, w != nullptr, b != nullptr, op.act, tab, yr);
     }
 }
 
+// T: the element type of a norm body (one of the two when the kernel has
+// only that one compiled in, else chosen by the op).
+template <bool F32, bool F16, typename Body>
+__device__ __forceinline__ void by_type(bool f16, Body body) {
+    if constexpr (F16) {
+        if (f16 || !F32) {
+            body(uint16_t{});
+            return;
+        }
+    }
+    if constexpr (F32) body(float{});
+}
+
+// NB: which of the f32 (bit 0) and f16 (bit 1) norms, and (bit 2) the
+// activation epilogue (without it the kernel holds no activation code and
+// the host sends no norm with an activation)
+template <uint32_t NB>
 __device__ __forceinline__ void b_norm(const BOp& op, uint32_t lb, const uint16_t* tab, double* lds) {
+    constexpr bool F32 = (NB & 1u) != 0, F16 = (NB & 2u) != 0, ACT = (NB & 4u) != 0;
     const bool f16 = op.t_x == CBX_TYPE_F16;
+    const bool ln = op.kind == CBX_OP_LAYER_NORM;
     if (op.aux3 == 4) {   // one row a workgroup (rows <= 1024 elements, nv == 4)
         const int64_t row = lb;
-        if (op.kind == CBX_OP_LAYER_NORM) {
-            if (f16) b_norm_row4<uint16_t, NORM_LN>(op, row, tab, lds);
-            else b_norm_row4<float, NORM_LN>(op, row, tab, lds);
-        } else {
-            if (f16) b_norm_row4<uint16_t, NORM_RMS>(op, row, tab, lds);
-            else b_norm_row4<float, NORM_RMS>(op, row, tab, lds);
-        }
+        by_type<F32, F16>(f16, [&](auto t) {
+            using T = decltype(t);
+            if (ln) b_norm_row4<T, NORM_LN, ACT>(op, row, tab, lds);
+            else b_norm_row4<T, NORM_RMS, ACT>(op, row, tab, lds);
+        });
         return;
     }
     const int lane = threadIdx.x & 63;
     const int64_t row = static_cast<int64_t>(lb) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (row >= op.rows) return;   // uniform per wave
-    if (op.kind == CBX_OP_LAYER_NORM) {
-        if (f16) b_norm_nv<uint16_t, NORM_LN>(op, row, lane, tab);
-        else b_norm_nv<float, NORM_LN>(op, row, lane, tab);
-    } else {
-        if (f16) b_norm_nv<uint16_t, NORM_RMS>(op, row, lane, tab);
-        else b_norm_nv<float, NORM_RMS>(op, row, lane, tab);
-    }
+    by_type<F32, F16>(f16, [&](auto t) {
+        using T = decltype(t);
+        if (ln) b_norm_nv<T, NORM_LN, ACT>(op, row, lane, tab);
+        else b_norm_nv<T, NORM_RMS, ACT>(op, row, lane, tab);
+    });
 }
 
 // ---- element-wise: one 4-vector per lane --------------------------------------
@@ -393,12 +408,34 @@ __device__ __forceinline__ void b_embed_1(const BOp& op, uint32_t lb, uint32_t* 
 }
 
 // ---- the batch kernel ------------------------------------------------------------------
+// Which op bodies a kernel compiles in (by kind and element type): the
+// kernel's registers are those of its heaviest body, so each launch takes
+// the smallest instantiation that covers its ops (a decode step's norms,
+// RoPE, SiLU-gate and gathers fit in far fewer than the fused embedding +
+// LayerNorm with its three table types).
+enum : uint32_t {
+    KB_NORM_F32 = 1u << 0,
+    KB_NORM_F16 = 1u << 1,
+    KB_UNARY_F32 = 1u << 2,
+    KB_UNARY_F16 = 1u << 3,
+    KB_SWIGLU_F32 = 1u << 4,
+    KB_SWIGLU_F16 = 1u << 5,
+    KB_ROPE_F32 = 1u << 6,
+    KB_ROPE_F16 = 1u << 7,
+    KB_GATHER = 1u << 8,
+    KB_EMBED = 1u << 9,
+    KB_SNAKE = 1u << 10,
+    KB_NORM_ACT = 1u << 11,   // a norm with an activation epilogue
+    KB_ALL = (1u << 12) - 1,
+};
+
 // The op list is read in place from the kernel-argument segment (the
 // pointer's origin lets the compiler use scalar constant loads); indexing the
 // by-value parameter with a run-time index would copy all of it to scratch.
+template <uint32_t KS>
 __global__ __launch_bounds__(kThreads) void k_batch(BatchArgs args) {
     (void)args;
-    __shared__ float2 cs[kRopeMaxHalf];
+    __shared__ float2 cs[(KS & (KB_ROPE_F32 | KB_ROPE_F16)) ? kRopeMaxHalf : 1];
     __shared__ double lds[8];
     const BatchArgs* a = (const BatchArgs*)(const void*)__builtin_amdgcn_kernarg_segment_ptr();
     const uint32_t b = blockIdx.x;
@@ -422,46 +459,112 @@ __global__ __launch_bounds__(kThreads) void k_batch(BatchArgs args) {
     const uint32_t lb = b - base;
     uint32_t* err = a->err;
     const uint16_t* tab = reinterpret_cast<const uint16_t*>(op.table);
+    const bool f16 = op.t_x == CBX_TYPE_F16;
     switch (op.kind) {
         case CBX_OP_LAYER_NORM:
         case CBX_OP_RMS_NORM:
-            b_norm(op, lb, tab, lds);
+            if constexpr ((KS & (KB_NORM_F32 | KB_NORM_F16)) != 0) {
+                b_norm<(KS & (KB_NORM_F32 | KB_NORM_F16)) | ((KS & KB_NORM_ACT) ? 4u : 0u)>(op, lb, tab, lds);
+            }
             break;
         case CBX_OP_UNARY:
         case CBX_OP_LEAKY_RELU:
-            if (op.t_x == CBX_TYPE_F16) b_unary_t<uint16_t>(op, lb, tab);
-            else b_unary_t<float>(op, lb, tab);
+            if constexpr ((KS & KB_UNARY_F16) != 0) {
+                if (f16) {
+                    b_unary_t<uint16_t>(op, lb, tab);
+                    break;
+                }
+            }
+            if constexpr ((KS & KB_UNARY_F32) != 0) {
+                if (!f16) b_unary_t<float>(op, lb, tab);
+            }
             break;
         case CBX_OP_SWIGLU:
-            if (op.t_x == CBX_TYPE_F16) b_swiglu_t<uint16_t>(op, lb);
-            else b_swiglu_t<float>(op, lb);
+            if constexpr ((KS & KB_SWIGLU_F16) != 0) {
+                if (f16) {
+                    b_swiglu_t<uint16_t>(op, lb);
+                    break;
+                }
+            }
+            if constexpr ((KS & KB_SWIGLU_F32) != 0) {
+                if (!f16) b_swiglu_t<float>(op, lb);
+            }
             break;
         case CBX_OP_ROPE:
-            if (op.t_x == CBX_TYPE_F16) b_rope_t<uint16_t>(op, lb, cs);
-            else b_rope_t<float>(op, lb, cs);
+            if constexpr ((KS & KB_ROPE_F16) != 0) {
+                if (f16) {
+                    b_rope_t<uint16_t>(op, lb, cs);
+                    break;
+                }
+            }
+            if constexpr ((KS & KB_ROPE_F32) != 0) {
+                if (!f16) b_rope_t<float>(op, lb, cs);
+            }
             break;
         case CBX_OP_GET_ROWS:
-            if (op.t_x == CBX_TYPE_F32) b_gather_1<CBX_TYPE_F32>(op, lb, err);
-            else if (op.t_x == CBX_TYPE_F16) b_gather_1<CBX_TYPE_F16>(op, lb, err);
-            else b_gather_1<CBX_TYPE_Q8_0>(op, lb, err);
+            if constexpr ((KS & KB_GATHER) != 0) {
+                if (op.t_x == CBX_TYPE_F32) b_gather_1<CBX_TYPE_F32>(op, lb, err);
+                else if (op.t_x == CBX_TYPE_F16) b_gather_1<CBX_TYPE_F16>(op, lb, err);
+                else b_gather_1<CBX_TYPE_Q8_0>(op, lb, err);
+            }
             break;
         case CBX_OP_GET_ROWS_ADD_LAYER_NORM:
-            if (op.t_x == CBX_TYPE_F32) b_embed_1<CBX_TYPE_F32>(op, lb, err);
-            else if (op.t_x == CBX_TYPE_F16) b_embed_1<CBX_TYPE_F16>(op, lb, err);
-            else b_embed_1<CBX_TYPE_Q8_0>(op, lb, err);
+            if constexpr ((KS & KB_EMBED) != 0) {
+                if (op.t_x == CBX_TYPE_F32) b_embed_1<CBX_TYPE_F32>(op, lb, err);
+                else if (op.t_x == CBX_TYPE_F16) b_embed_1<CBX_TYPE_F16>(op, lb, err);
+                else b_embed_1<CBX_TYPE_Q8_0>(op, lb, err);
+            }
             break;
         case CBX_OP_SNAKE:
-            b_snake(op, lb);
+            if constexpr ((KS & KB_SNAKE) != 0) b_snake(op, lb);
             break;
         default:
             break;
     }
 }
 
+// The bodies an op needs.
+uint32_t op_bits(const BOp& op) {
+    const bool f16 = op.t_x == CBX_TYPE_F16;
+    switch (op.kind) {
+        case CBX_OP_LAYER_NORM:
+        case CBX_OP_RMS_NORM: return (f16 ? KB_NORM_F16 : KB_NORM_F32) | (op.act != CBX_UNARY_NONE ? KB_NORM_ACT : 0u);
+        case CBX_OP_UNARY:
+        case CBX_OP_LEAKY_RELU: return f16 ? KB_UNARY_F16 : KB_UNARY_F32;
+        case CBX_OP_SWIGLU: return f16 ? KB_SWIGLU_F16 : KB_SWIGLU_F32;
+        case CBX_OP_ROPE: return f16 ? KB_ROPE_F16 : KB_ROPE_F32;
+        case CBX_OP_GET_ROWS: return KB_GATHER;
+        case CBX_OP_GET_ROWS_ADD_LAYER_NORM: return KB_EMBED;
+        case CBX_OP_SNAKE: return KB_SNAKE;
+        default: return KB_ALL;
+    }
+}
+
+// The instantiations, smallest first: the decode step in f32 (norm, RoPE,
+// SiLU-gate, gather), the 64-stream f16 step (the same in f16 with the Q8_0
+// gather), the prefill's embedding + LayerNorm with GELU, every op alone,
+// and everything.
+template <uint32_t KS>
+void go(const BatchArgs& a, uint32_t total_blocks, hipStream_t s) {
+    hipLaunchKernelGGL(k_batch<KS>, dim3(total_blocks), dim3(kThreads), 0, s, a);
+}
+
+constexpr uint32_t kDecodeF32 = KB_NORM_F32 | KB_ROPE_F32 | KB_SWIGLU_F32 | KB_GATHER;
+constexpr uint32_t kDecodeF16 = KB_NORM_F16 | KB_ROPE_F16 | KB_SWIGLU_F16 | KB_GATHER;
+constexpr uint32_t kPrefill = KB_EMBED | KB_UNARY_F32;
+
 }  // namespace
 
 int launch_batch(const BatchArgs& a, uint32_t total_blocks, hipStream_t s) {
-    hipLaunchKernelGGL(k_batch, dim3(total_blocks), dim3(kThreads), 0, s, a);
+    uint32_t need = 0;
+    for (int i = 0; i < a.n; i++) need |= op_bits(a.op[i]);
+    auto covers = [need](uint32_t ks) { return (need & ~ks) == 0; };
+    if (covers(kDecodeF32)) go<kDecodeF32>(a, total_blocks, s);
+    else if (covers(kDecodeF16)) go<kDecodeF16>(a, total_blocks, s);
+    else if (covers(kPrefill)) go<kPrefill>(a, total_blocks, s);
+    else if (covers(KB_UNARY_F32 | KB_UNARY_F16)) go<KB_UNARY_F32 | KB_UNARY_F16>(a, total_blocks, s);
+    else if (covers(KB_SNAKE)) go<KB_SNAKE>(a, total_blocks, s);
+    else go<KB_ALL>(a, total_blocks, s);
     return check_launch("run_ops");
 }
 
