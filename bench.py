@@ -446,11 +446,23 @@ def bench_cfm(C, W, torch, reps=400):
                                                                      st[1]["w" + key], st[1]["b" + key], C.MISH,
                                                                      st[1]["y" + key], ws.handle, s)))
 
-    def gn_whole(key):
-        """The same op with every workgroup reducing its whole group (cbx_group_norm)."""
+    def gn_entry(key):
+        """The same op through cbx_group_norm (the split over the library's
+        scratch set for the stream)."""
         return lambda st: (lambda s: check_rc(C, L.cbx_group_norm(st[1]["x" + key], W.CFM_GROUPS, 1e-5,
                                                                   st[1]["w" + key], st[1]["b" + key], C.MISH,
                                                                   st[1]["y" + key], s)))
+
+    def flow_batch(st):
+        """The flow step's three ops in one launch (cbx_run_ops)."""
+        t = st[0]
+        b = C.OpBatch([C.Op(C.OP_GROUP_NORM, [t["x256"], t["w256"], t["b256"]], [t["y256"]], act=C.MISH, eps=1e-5,
+                            iparam=W.CFM_GROUPS),
+                       C.Op(C.OP_GROUP_NORM, [t["x512"], t["w512"], t["b512"]], [t["y512"]], act=C.MISH, eps=1e-5,
+                            iparam=W.CFM_GROUPS),
+                       C.Op(C.OP_LAYER_NORM_ROPE, [t["xa"], t["wa"], t["ba"], t["pos"]], [t["ya_rope"]], eps=1e-5,
+                            rope=cache, iparam=W.HEAD_DIM)])
+        return lambda s: b.launch(s)
 
     def ln(st):
         r = st[1]
@@ -466,8 +478,8 @@ def bench_cfm(C, W, torch, reps=400):
 
     out = {}
     for name, mk in (("group_norm_mish_256", gn("256")), ("group_norm_mish_512", gn("512")),
-                     ("group_norm_mish_256_whole_group_per_workgroup", gn_whole("256")),
-                     ("group_norm_mish_512_whole_group_per_workgroup", gn_whole("512")),
+                     ("group_norm_mish_256_entry_point", gn_entry("256")),
+                     ("group_norm_mish_512_entry_point", gn_entry("512")),
                      ("layer_norm_1024x512", ln), ("rope_2x500x8x64", rope), ("layer_norm_rope_fused", ln_rope)):
         fns = [mk(st) for st in sets]
         for f in fns:
@@ -485,24 +497,38 @@ def bench_cfm(C, W, torch, reps=400):
     out["flow_step"] = {"us": per_launch_ms(torch, [step(st) for st in sets], reps) * 1000.0,
                         "launches": "group_norm+mish [2,256,500], group_norm+mish [2,512,500], "
                                     "layer_norm_rope [2,500,512]"}
+    # the three ops in one launch must give the three launches' bits
+    t0 = sets[0][0]
+    step(sets[0])(cur_stream(torch))
+    torch.cuda.synchronize()
+    three = [t0[k].cpu().numpy() for k in ("y256", "y512", "ya_rope")]
+    for k in ("y256", "y512", "ya_rope"):
+        t0[k].fill_(float("nan"))
+    flows = [flow_batch(st) for st in sets]
+    flows[0](cur_stream(torch))
+    torch.cuda.synchronize()
+    for k, ref in zip(("y256", "y512", "ya_rope"), three):
+        if not same_bits(ref, t0[k].cpu().numpy()):
+            raise SystemExit(f"bench: the one-launch flow step's {k} differs from the three launches'")
+    out["flow_step_one_launch"] = {"us": per_launch_ms(torch, flows, reps) * 1000.0,
+                                   "launches": "cbx_run_ops: both group norms (split) + layer_norm_rope"}
     for k in ("group_norm_mish_256", "group_norm_mish_512"):
         out[k]["GBps"] = nb[k] / (out[k]["us"] * 1e-6) / 1e9
-        out[k + "_whole_group_per_workgroup"]["GBps"] = nb[k] / (out[k + "_whole_group_per_workgroup"]["us"] *
-                                                                 1e-6) / 1e9
-    # the split must reproduce the whole-group kernel bit for bit
-    t0 = sets[0][0]
+        out[k + "_entry_point"]["GBps"] = nb[k] / (out[k + "_entry_point"]["us"] * 1e-6) / 1e9
+    # the workspace form and the entry point must give the same bits
     for key in ("256", "512"):
         gn(key)(sets[0])(cur_stream(torch))
         torch.cuda.synchronize()
         split = t0["y" + key].cpu().numpy()
-        gn_whole(key)(sets[0])(cur_stream(torch))
+        gn_entry(key)(sets[0])(cur_stream(torch))
         torch.cuda.synchronize()
         if not same_bits(split, t0["y" + key].cpu().numpy()):
-            raise SystemExit(f"bench: split GroupNorm [2,{key},500] differs from the whole-group kernel")
+            raise SystemExit(f"bench: GroupNorm [2,{key},500] differs between cbx_group_norm_ws and cbx_group_norm")
     out["layer_norm_rope_fused"]["GBps"] = nb["layer_norm_rope"] / (out["layer_norm_rope_fused"]["us"] * 1e-6) / 1e9
     lr = out["layer_norm_1024x512"]["us"] + out["rope_2x500x8x64"]["us"]
     out["layer_norm_then_rope_GBps_vs_fused_bytes"] = nb["layer_norm_rope"] / (lr * 1e-6) / 1e9
     out["flow_step"]["GBps"] = per_step / (out["flow_step"]["us"] * 1e-6) / 1e9
+    out["flow_step_one_launch"]["GBps"] = per_step / (out["flow_step_one_launch"]["us"] * 1e-6) / 1e9
     cache.close()
     ws.close()
     return dict(out, bytes_per_flow_step=per_step, bytes=nb, buffer_sets=n_sets)

@@ -63,6 +63,8 @@ class OpStruct(ctypes.Structure):
         ("src", ctypes.POINTER(Tensor) * 6),
         ("dst", ctypes.POINTER(Tensor) * 2),
         ("rope", ctypes.c_void_p),
+        ("iparam", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 
@@ -119,7 +121,7 @@ GLF_SNAKE, GLF_LEAKY, GLF_MASK, GLF_BIAS, GLF_RESIDUAL = 1, 2, 3, 4, 8
 
 # cbx_op_kind
 OP_LAYER_NORM, OP_RMS_NORM, OP_UNARY, OP_LEAKY_RELU, OP_SWIGLU, OP_ROPE, OP_GET_ROWS, \
-    OP_GET_ROWS_ADD_LAYER_NORM, OP_SNAKE = range(1, 10)
+    OP_GET_ROWS_ADD_LAYER_NORM, OP_SNAKE, OP_GROUP_NORM, OP_LAYER_NORM_ROPE = range(1, 12)
 MAX_OPS = 12
 
 _lib = None
@@ -725,12 +727,14 @@ def snake(x, alpha, alpha_inv, out=None):
 
 class Op:
     """One entry of run_ops: kind (OP_*), source and destination tensors
-    (None for absent optional operands), activation, eps, param, rope table.
-    q8 lists the source indices that are Q8_0 tables (uint8 blocks)."""
+    (None for absent optional operands), activation, eps, param, rope table,
+    iparam (GroupNorm's n_groups, LayerNorm+RoPE's head_dim).  q8 lists the
+    source indices that are Q8_0 tables (uint8 blocks)."""
 
     def __init__(self, kind, src=(), dst=(), act=UNARY_NONE, eps=0.0, param=0.0, rope: Optional[RopeCache] = None,
-                 q8=()):
+                 q8=(), iparam=0):
         self.kind, self.act, self.eps, self.param, self.rope = kind, act, eps, param, rope
+        self.iparam = iparam
         self.src = list(src) + [None] * (6 - len(src))
         self.dst = list(dst) + [None] * (2 - len(dst))
         self.q8 = set(q8)
@@ -749,6 +753,7 @@ class Op:
                 keep.append(d)
                 o.dst[k] = ctypes.pointer(d)
         o.rope = self.rope.handle.value if self.rope is not None else None
+        o.iparam = self.iparam
         return o
 
 

@@ -1239,7 +1239,8 @@ int batch_fail(int i, int code, const std::string& msg) {
 }
 
 // Fills b from o (validated) and returns the op's workgroup count in *nblk.
-int build_op(int i, const cbx_op& o, BOp& b, DeviceState* st, int64_t* nblk) {
+// GroupNorm ops take chunk slots of the stream's scratch set from *gn_slot on.
+int build_op(int i, const cbx_op& o, BOp& b, DeviceState* st, hipStream_t strm, uint32_t* gn_slot, int64_t* nblk) {
     const char* what = "cbx_run_ops";
     int rc;
     b.kind = o.kind;
@@ -1434,6 +1435,82 @@ int build_op(int i, const cbx_op& o, BOp& b, DeviceState* st, int64_t* nblk) {
             *nblk = cdiv(n / 4, 256);
             return CBX_OK;
         }
+        case CBX_OP_GROUP_NORM: {
+            const cbx_tensor *x = o.src[0], *w = o.src[1], *bb = o.src[2], *y = o.dst[0];
+            if ((rc = check_group_norm(what, x, o.iparam, o.eps, w, bb, o.act, y))) return rc;
+            if (o.act != CBX_UNARY_NONE && o.act != CBX_UNARY_MISH) {
+                return batch_fail(i, CBX_ERR_UNSUPPORTED, "group norm takes no activation or Mish");
+            }
+            if (nelements(x) == 0) return CBX_OK;
+            GnSplit sp;
+            uint32_t n_slots = 0, used = 0;
+            int nv = 1;
+            const char* why = nullptr;
+            if (!group_norm_split_args(x, o.iparam, o.eps, w, bb, o.act, y, group_norm_scratch_for(st, strm), *gn_slot,
+                                       kGnWaitAuto, 0, st, &sp, &n_slots, &nv, &used, &why)) {
+                return batch_fail(i, CBX_ERR_UNSUPPORTED, std::string("group norm does not take the split reduction: ") +
+                                                              why);
+            }
+            if (nv > 4) return batch_fail(i, CBX_ERR_UNSUPPORTED, "group norm chunks of more than 4 vectors a lane");
+            b.gn = sp;
+            b.nv = nv;
+            b.aux = o.act == CBX_UNARY_MISH ? 2 : 0;
+            *gn_slot += used;
+            *nblk = n_slots;
+            return CBX_OK;
+        }
+        case CBX_OP_LAYER_NORM_ROPE: {
+            const cbx_tensor *x = o.src[0], *w = o.src[1], *bb = o.src[2], *pos = o.src[3], *y = o.dst[0];
+            const cbx_rope_cache* c = o.rope;
+            if (!c) return batch_fail(i, CBX_ERR_INVALID_ARG, "rope is NULL");
+            int dev = 0;
+            if (hipGetDevice(&dev) != hipSuccess || dev != c->device) {
+                return batch_fail(i, CBX_ERR_INVALID_ARG, "rope table belongs to another device");
+            }
+            if ((rc = validate(x, what, "x")) || (rc = validate(y, what, "y")) || (rc = validate(pos, what, "pos"))) return rc;
+            if (x->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32) return batch_fail(i, CBX_ERR_UNSUPPORTED, "F32 only");
+            if (!same_shape(x, y)) return batch_fail(i, CBX_ERR_INVALID_ARG, "x and y shapes differ");
+            if (!(o.eps >= 0.0f)) return batch_fail(i, CBX_ERR_INVALID_ARG, "eps must be >= 0");
+            if ((rc = check_row_param(w, x, what, "w")) || (rc = check_row_param(bb, x, what, "b"))) return rc;
+            const int64_t hd = o.iparam;
+            if (hd <= 0 || hd % 4 || x->ne[0] % hd) {
+                return batch_fail(i, CBX_ERR_INVALID_ARG, "head_dim must divide x.ne0 and be a multiple of 4");
+            }
+            if (c->p.n_dims > hd) return batch_fail(i, CBX_ERR_INVALID_ARG, "n_dims > head_dim");
+            if (x->ne[3] != 1) return batch_fail(i, CBX_ERR_INVALID_ARG, "x must be at most 3-D (C, n_tok, batch)");
+            if (pos->type != CBX_TYPE_I32 || pos->ne[0] != x->ne[1] || pos->ne[1] != 1 || pos->ne[2] != 1 ||
+                pos->ne[3] != 1) {
+                return batch_fail(i, CBX_ERR_INVALID_ARG, "pos must be I32 with ne = (x.ne1, 1, 1, 1)");
+            }
+            const int64_t hq = hd / 4, dq = c->p.n_dims / 8;
+            const bool neox = c->p.mode == 2;
+            const bool xs = flat_rows(x) && flat_rows(y) && rows_aligned_to(x, 16) && rows_aligned_to(y, 16) &&
+                            reinterpret_cast<uintptr_t>(c->table) % 16 == 0 && 64 % hq == 0 &&
+                            (neox ? c->p.n_dims % 8 == 0 && dq > 0 && (dq & (dq - 1)) == 0 : c->p.n_dims % 4 == 0);
+            if (x->ne[0] > 1024 || !xs || (w && reinterpret_cast<uintptr_t>(w->data) % 16) ||
+                (bb && reinterpret_cast<uintptr_t>(bb->data) % 16) || x->ne[1] * x->ne[2] >= (int64_t{1} << 31)) {
+                return batch_fail(i, CBX_ERR_UNSUPPORTED,
+                                  "layer norm + rope needs rows <= 1024 at one 16-byte aligned stride and a head's "
+                                  "rotation partners in one wave");
+            }
+            b.t_x = CBX_TYPE_F32;
+            b.ne0 = x->ne[0];
+            b.aux = hd;
+            b.aux2 = x->ne[1];
+            b.rows = x->ne[1] * x->ne[2];
+            b.t[0] = bten(x, static_cast<int64_t>(x->nb[1]));
+            b.t[1] = bten(pos, static_cast<int64_t>(pos->nb[0]));
+            b.t[2] = bten(w, 0);
+            b.t[3] = bten(bb, 0);
+            b.t[6] = bten(y, static_cast<int64_t>(y->nb[1]));
+            b.table = c->table;
+            b.ff = c->freq_factors;
+            b.n_pos = c->n_pos;
+            b.rp = c->p;
+            b.nv = x->ne[0] <= 256 ? 1 : x->ne[0] <= 512 ? 2 : 4;
+            *nblk = nelements(x) ? cdiv(b.rows, 4) : 0;
+            return CBX_OK;
+        }
         default:
             return batch_fail(i, CBX_ERR_INVALID_ARG, "unknown op kind " + std::to_string(o.kind));
     }
@@ -1452,13 +1529,32 @@ extern "C" int cbx_run_ops(const cbx_op* ops, int n_ops, cbx_stream stream) {
     BatchArgs a{};
     a.n = n_ops;
     a.err = st->err_word;
-    int64_t total = 0;
-    for (int i = 0; i < n_ops; i++) {
+    const hipStream_t strm = reinterpret_cast<hipStream_t>(stream);
+    // GroupNorm ops first: their block ranges then start at multiples of 8
+    // (each takes a multiple of 8 workgroups) and their chunk workgroups are
+    // dispatched before any other op's, so a group's chunks are resident
+    // together
+    int order[CBX_MAX_OPS];
+    int n_order = 0;
+    for (int pass = 0; pass < 2; pass++) {
+        for (int i = 0; i < n_ops; i++) {
+            if ((ops[i].kind == CBX_OP_GROUP_NORM) == (pass == 0)) order[n_order++] = i;
+        }
+    }
+    int64_t total = 0, gn_blocks = 0;
+    uint32_t gn_slot = 0;
+    for (int k = 0; k < n_ops; k++) {
+        const int i = order[k];
+        if (ops[i].reserved != 0) return batch_fail(i, CBX_ERR_INVALID_ARG, "reserved must be 0");
         int64_t nb = 0;
-        a.blk0[i] = static_cast<uint32_t>(total);
-        if ((rc = build_op(i, ops[i], a.op[i], st, &nb))) return rc;
+        a.blk0[k] = static_cast<uint32_t>(total);
+        if ((rc = build_op(i, ops[i], a.op[k], st, strm, &gn_slot, &nb))) return rc;
+        if (ops[i].kind == CBX_OP_GROUP_NORM) gn_blocks += nb;
         total += nb;
         if (total >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "cbx_run_ops: too many workgroups");
+    }
+    if (gn_blocks > int64_t{2} * st->n_cu) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_run_ops: the group norms' chunk workgroups are more than 2 a CU");
     }
     // independence: no op writes what another op reads or writes
     for (int i = 0; i < n_ops; i++) {

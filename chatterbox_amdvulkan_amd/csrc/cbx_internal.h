@@ -183,6 +183,36 @@ struct BTen {
     int64_t nb1;
 };
 
+// The split-reduction GroupNorm's arguments (its standalone kernel and the
+// op batch's GroupNorm): the group instances' chunk workgroups, the
+// workspace of tagged exchange words ([2 stages][slots x 4 waves][2 words],
+// a stage kSplitStageWords long), the wait bound in 100 MHz ticks.
+struct GnSplit {
+    const char* x;
+    char* y;
+    const float* w;
+    const float* b;
+    uint64_t* word;
+    const uint16_t* tab;
+    int64_t x_nb3, y_nb3;    // batch strides (bytes)
+    uint64_t wait_ticks;
+    uint32_t n_chunks, n_gi, n_groups, per_ch, cpg, C;   // per_ch = ne0 * ne1
+    float eps;
+    int32_t act;
+};
+
+// The split GroupNorm of x (chunks per group automatic, or n_chunks_req)
+// over workspace words from chunk slot first_slot on: fills *sp, the grid
+// (*n_slots workgroups, a multiple of 8), the vectors a lane holds (*nv) and
+// the chunk slots it uses (*slots_used), or returns false with *why when
+// the split does not apply (in place, strided groups, too many or too few
+// chunks, a grid not resident at once, a device whose dispatch was not seen
+// to deal workgroups to XCDs by index mod 8).
+bool group_norm_split_args(const cbx_tensor* x, int n_groups, float eps, const cbx_tensor* w, const cbx_tensor* b,
+                           int act, const cbx_tensor* y, void* workspace, uint32_t first_slot, uint64_t wait_ticks,
+                           int n_chunks_req, const DeviceState* st, GnSplit* sp, uint32_t* n_slots, int* nv,
+                           uint32_t* slots_used, const char** why);
+
 // One op of a batch, in kernel-argument memory.  Field use by kind:
 //   norms:     t0 x, t1 w, t2 b, t6 y; ne0, rows; nv vectors per lane; t_x type;
 //              aux3 waves a row (1: four rows a workgroup; 4: one row)
@@ -193,6 +223,10 @@ struct BTen {
 //              t6 dst (h), t7 y; t_x/t_x2 table types; aux/aux2 table rows
 //   snake:     t0 x, t1 a, t2 ai, t6 y; act 1 = alpha along ne0; aux C,
 //              aux2 cmask, aux3 ne0/4
+//   group norm (split): gn; nv vectors per lane; aux 0 no activation, 2 Mish
+//   layer norm + rope: t0 x, t1 pos, t2 w, t3 b, t6 y; ne0 row length,
+//              aux head size, aux2 tokens (x.ne1), rows; nv vectors per lane;
+//              table/ff/n_pos/rp the cache's
 struct BOp {
     int32_t     kind;
     int32_t     act;
@@ -200,13 +234,17 @@ struct BOp {
     int32_t     t_x, t_x2;
     float       eps, param;
     int64_t     ne0, rows, aux, aux2, aux3;
-    BTen        t[8];
+    union {
+        BTen    t[8];
+        GnSplit gn;
+    };
     const void* table;       // rope cos/sin table or the GELU table
     const float* ff;         // rope freq factors (device) or nullptr
     int32_t     n_pos;
     RopeParams  rp;
 };
 
+static_assert(sizeof(GnSplit) <= sizeof(BTen) * 8, "the split GroupNorm's arguments share the tensor slots");
 constexpr int kBatchMaxOps = CBX_MAX_OPS;
 
 struct BatchArgs {

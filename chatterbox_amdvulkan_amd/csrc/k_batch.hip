@@ -8,6 +8,8 @@
 // with the token's cos/sin row in LDS (one token per workgroup), row gathers
 // (one row per workgroup) and the fused embedding + LayerNorm (4 tokens per
 // workgroup).  Launching them together pays the fixed dispatch cost once.
+#include "cbx_gnsplit.h"
+#include "cbx_normrope.h"
 #include "cbx_rowops.h"
 
 namespace cbx {
@@ -407,6 +409,74 @@ __device__ __forceinline__ void b_embed_1(const BOp& op, uint32_t lb, uint32_t* 
     else b_embed_nv<TYPE, CBX_TYPE_Q8_0>(op, lb, err);
 }
 
+// ---- GroupNorm (split reduction): one chunk a workgroup -------------------------------
+// The op's block range starts at a multiple of 8 (GroupNorm ops come first in
+// a launch), so the body's index mod 8 is the XCD's, as in its own kernel.
+// gn is read where it lies in the argument segment: it shares its bytes with
+// the tensor slots of the workgroup's copy of the op, and reading one copy
+// through both views would keep that copy in memory.
+__device__ __forceinline__ void b_group_norm(const GnSplit& gn, int nv, int64_t act, uint32_t lb) {
+    if (act == 2) {   // Mish
+        switch (nv) {
+            case 1: gn_split_body<1, 2>(gn, lb); break;
+            case 2: gn_split_body<2, 2>(gn, lb); break;
+            default: gn_split_body<4, 2>(gn, lb); break;
+        }
+    } else {
+        switch (nv) {
+            case 1: gn_split_body<1, 0>(gn, lb); break;
+            case 2: gn_split_body<2, 0>(gn, lb); break;
+            default: gn_split_body<4, 0>(gn, lb); break;
+        }
+    }
+}
+
+// ---- LayerNorm + RoPE: one wave a token row, four rows a workgroup --------------------
+// The rotation partners come from other lanes of the row's wave (the host
+// admits only such layouts), so no LDS and no barrier.
+template <int MODE, int NV>
+__device__ __forceinline__ void b_ln_rope_nv(const BOp& op, uint32_t lb) {
+    const uint32_t r = lb * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (r >= static_cast<uint32_t>(op.rows)) return;   // uniform per wave
+    NormRopeArgs a;
+    a.x = op.t[0].p;
+    a.y = op.t[6].p;
+    a.w = reinterpret_cast<const float*>(op.t[2].p);
+    a.b = reinterpret_cast<const float*>(op.t[3].p);
+    a.pos = op.t[1].p;
+    a.pos_nb0 = op.t[1].nb1;
+    a.table = reinterpret_cast<const float2*>(op.table);
+    a.ff = op.ff;
+    a.mx.nb1 = op.t[0].nb1;
+    a.mx.flat = 1;
+    a.my.nb1 = op.t[6].nb1;
+    a.my.flat = 1;
+    a.ne0 = static_cast<int32_t>(op.ne0);
+    a.hd = static_cast<int32_t>(op.aux);
+    a.n_tok = static_cast<uint32_t>(op.aux2);
+    a.n_pos = op.n_pos;
+    a.eps = op.eps;
+    a.vec_cs = 1;
+    a.rp = op.rp;
+    ln_rope_row<NV, MODE, true, 1, true>(a, r, static_cast<int>(threadIdx.x & 63), nullptr, nullptr);
+}
+
+__device__ __forceinline__ void b_ln_rope(const BOp& op, uint32_t lb) {
+    if (op.rp.mode == 2) {
+        switch (op.nv) {
+            case 1: b_ln_rope_nv<2, 1>(op, lb); break;
+            case 2: b_ln_rope_nv<2, 2>(op, lb); break;
+            default: b_ln_rope_nv<2, 4>(op, lb); break;
+        }
+    } else {
+        switch (op.nv) {
+            case 1: b_ln_rope_nv<0, 1>(op, lb); break;
+            case 2: b_ln_rope_nv<0, 2>(op, lb); break;
+            default: b_ln_rope_nv<0, 4>(op, lb); break;
+        }
+    }
+}
+
 // ---- the batch kernel ------------------------------------------------------------------
 // Which op bodies a kernel compiles in (by kind and element type): the
 // kernel's registers are those of its heaviest body, so each launch takes
@@ -426,7 +496,9 @@ enum : uint32_t {
     KB_EMBED = 1u << 9,
     KB_SNAKE = 1u << 10,
     KB_NORM_ACT = 1u << 11,   // a norm with an activation epilogue
-    KB_ALL = (1u << 12) - 1,
+    KB_GROUP_NORM = 1u << 12,
+    KB_LN_ROPE = 1u << 13,
+    KB_ALL = (1u << 14) - 1,
 };
 
 // The op list is read in place from the kernel-argument segment (the
@@ -518,6 +590,12 @@ __global__ __launch_bounds__(kThreads) void k_batch(BatchArgs args) {
         case CBX_OP_SNAKE:
             if constexpr ((KS & KB_SNAKE) != 0) b_snake(op, lb);
             break;
+        case CBX_OP_GROUP_NORM:
+            if constexpr ((KS & KB_GROUP_NORM) != 0) b_group_norm(a->op[i].gn, op.nv, op.aux, lb);
+            break;
+        case CBX_OP_LAYER_NORM_ROPE:
+            if constexpr ((KS & KB_LN_ROPE) != 0) b_ln_rope(op, lb);
+            break;
         default:
             break;
     }
@@ -536,14 +614,17 @@ uint32_t op_bits(const BOp& op) {
         case CBX_OP_GET_ROWS: return KB_GATHER;
         case CBX_OP_GET_ROWS_ADD_LAYER_NORM: return KB_EMBED;
         case CBX_OP_SNAKE: return KB_SNAKE;
+        case CBX_OP_GROUP_NORM: return KB_GROUP_NORM;
+        case CBX_OP_LAYER_NORM_ROPE: return KB_LN_ROPE;
         default: return KB_ALL;
     }
 }
 
 // The instantiations, smallest first: the decode step in f32 (norm, RoPE,
 // SiLU-gate, gather), the 64-stream f16 step (the same in f16 with the Q8_0
-// gather), the prefill's embedding + LayerNorm with GELU, every op alone,
-// and everything.
+// gather), the prefill's embedding + LayerNorm with GELU, the CFM flow
+// step's GroupNorms with LayerNorm + RoPE, the element-wise ops, snake, and
+// everything.
 template <uint32_t KS>
 void go(const BatchArgs& a, uint32_t total_blocks, hipStream_t s) {
     hipLaunchKernelGGL(k_batch<KS>, dim3(total_blocks), dim3(kThreads), 0, s, a);
@@ -552,6 +633,7 @@ void go(const BatchArgs& a, uint32_t total_blocks, hipStream_t s) {
 constexpr uint32_t kDecodeF32 = KB_NORM_F32 | KB_ROPE_F32 | KB_SWIGLU_F32 | KB_GATHER;
 constexpr uint32_t kDecodeF16 = KB_NORM_F16 | KB_ROPE_F16 | KB_SWIGLU_F16 | KB_GATHER;
 constexpr uint32_t kPrefill = KB_EMBED | KB_UNARY_F32;
+constexpr uint32_t kFlow = KB_GROUP_NORM | KB_LN_ROPE;
 
 }  // namespace
 
@@ -562,6 +644,9 @@ int launch_batch(const BatchArgs& a, uint32_t total_blocks, hipStream_t s) {
     if (covers(kDecodeF32)) go<kDecodeF32>(a, total_blocks, s);
     else if (covers(kDecodeF16)) go<kDecodeF16>(a, total_blocks, s);
     else if (covers(kPrefill)) go<kPrefill>(a, total_blocks, s);
+    else if (covers(KB_GROUP_NORM)) go<KB_GROUP_NORM>(a, total_blocks, s);
+    else if (covers(KB_LN_ROPE)) go<KB_LN_ROPE>(a, total_blocks, s);
+    else if (covers(kFlow)) go<kFlow>(a, total_blocks, s);
     else if (covers(KB_UNARY_F32 | KB_UNARY_F16)) go<KB_UNARY_F32 | KB_UNARY_F16>(a, total_blocks, s);
     else if (covers(KB_SNAKE)) go<KB_SNAKE>(a, total_blocks, s);
     else go<KB_ALL>(a, total_blocks, s);

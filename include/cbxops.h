@@ -487,16 +487,23 @@ typedef enum cbx_op_kind {
     CBX_OP_GET_ROWS                = 7, /* src0 table, src1 ids [, src2 table2, src3 ids2: added] -> dst0 */
     CBX_OP_GET_ROWS_ADD_LAYER_NORM = 8, /* src0..3 as GET_ROWS, src4 w, src5 b -> dst0 h|NULL, dst1 y; eps */
     CBX_OP_SNAKE                   = 9, /* src0 x, src1 alpha, src2 alpha_inv -> dst0 y                   */
+    CBX_OP_GROUP_NORM              = 10, /* src0 x, src1 w|NULL, src2 b|NULL -> dst0 y; iparam n_groups,
+                                            eps, act (NONE or MISH): the split reduction, out of place   */
+    CBX_OP_LAYER_NORM_ROPE         = 11, /* src0 x, src1 w|NULL, src2 b|NULL, src3 pos -> dst0 y;
+                                            iparam head_dim, eps, rope = table                           */
 } cbx_op_kind;
 
 typedef struct cbx_op {
     int32_t               kind;    /* cbx_op_kind */
-    int32_t               act;     /* cbx_unary_op (CBX_OP_UNARY, CBX_OP_LAYER_NORM epilogue) */
+    int32_t               act;     /* cbx_unary_op (CBX_OP_UNARY, CBX_OP_LAYER_NORM epilogue,
+                                      CBX_OP_GROUP_NORM) */
     float                 eps;
     float                 param;
     const cbx_tensor*     src[6];
     cbx_tensor*           dst[2];
     const cbx_rope_cache* rope;
+    int32_t               iparam;  /* CBX_OP_GROUP_NORM: n_groups; CBX_OP_LAYER_NORM_ROPE: head_dim */
+    int32_t               reserved; /* must be 0 */
 } cbx_op;
 
 #define CBX_MAX_OPS 12
@@ -514,7 +521,20 @@ typedef struct cbx_op {
  *   - ROPE: n_dims <= 512 (columns n_dims..ne0 are copied, as ggml does);
  *   - gathers: 1-D ids, 2-D tables, ne0 % 4 == 0 (<= 1024 with LayerNorm),
  *     F32 destination rows 16-byte aligned;
- *   - SNAKE: F32, contiguous, 16-byte aligned, ne0 % 4 == 0.              */
+ *   - SNAKE: F32, contiguous, 16-byte aligned, ne0 % 4 == 0;
+ *   - GROUP_NORM: the layouts and sizes cbx_group_norm runs as the split
+ *     reduction (contiguous groups, out of place, a few large groups; no
+ *     activation or Mish; at most 4 vectors a lane), its chunk workgroups
+ *     resident at once with every other GROUP_NORM of the call (at most 2
+ *     a CU in all, 1024 chunk slots in all); the exchange words in the
+ *     library's scratch set for `stream`, as cbx_group_norm_noalloc's;
+ *   - LAYER_NORM_ROPE: cbx_layer_norm_rope's operands with F32 rows at one
+ *     stride, the rotation partners of a head in one wave (head_dim / 4
+ *     divides 64; NEOX: n_dims % 8 == 0 and n_dims / 8 a power of two;
+ *     NORMAL: n_dims % 4 == 0) and a 16-byte aligned table.
+ * GROUP_NORM ops run first in the launch (their workgroups get the CUs
+ * first, so all of a group's chunks are resident); the results do not
+ * depend on the order.                                                    */
 int cbx_run_ops(const cbx_op* ops, int n_ops, cbx_stream stream);
 
 /* ---- ggml-style node lists ------------------------------------------------ */

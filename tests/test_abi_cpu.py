@@ -50,9 +50,10 @@ def test_ops_before_init_fail_cleanly():
 
 
 def test_op_struct_layout_matches_header():
-    # struct cbx_op { int32 kind, act; float eps, param; cbx_tensor* src[6], dst[2]; void* rope; }
+    # struct cbx_op { int32 kind, act; float eps, param; cbx_tensor* src[6], dst[2]; void* rope;
+    #                  int32 iparam, reserved; }
     assert C.OpStruct.src.offset == 16 and C.OpStruct.dst.offset == 64 and C.OpStruct.rope.offset == 80
-    assert ctypes.sizeof(C.OpStruct) == 88
+    assert C.OpStruct.iparam.offset == 88 and ctypes.sizeof(C.OpStruct) == 96
     with pytest.raises(C.CbxError):
         C.OpBatch([C.Op(C.OP_UNARY)] * (C.MAX_OPS + 1))
 

@@ -1,5 +1,7 @@
 """cbx_run_ops: several independent ops in one launch must give exactly what
 the single-op entry points give (and hence the oracle's results)."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -237,3 +239,92 @@ def test_batched_f16_elementwise_forms(cbx, oracle, n, offset):
     assert_bitexact(host(ys[1]), oracle.leaky_relu(xs, 0.1), "leaky f16")
     assert_bitexact(host(ys[2]), host(cbx.swiglu(tx, tu)), "swiglu = single op")
     assert_bitexact(host(ys[3]), oracle.unary(oracle.GELU, us), "gelu f16")
+
+
+def cfm_flow_ops(cbx, rope64, order="gn_first", act=None):
+    """The CFM flow step's three ops (GroupNorm(8)+affine+Mish on [2,256,500]
+    and [2,512,500], LayerNorm+RoPE on [2,500,8x64]) as one op list."""
+    act = cbx.MISH if act is None else act
+    inp = W.cfm_inputs()
+    t = {k: dev(v) for k, v in inp.items()}
+    y256, y512, ya = (torch.full_like(t[k], float("nan")) for k in ("x256", "x512", "xa"))
+    gn = [cbx.Op(cbx.OP_GROUP_NORM, [t["x256"], t["w256"], t["b256"]], [y256], act=act, eps=1e-5,
+                 iparam=W.CFM_GROUPS),
+          cbx.Op(cbx.OP_GROUP_NORM, [t["x512"], t["w512"], t["b512"]], [y512], act=act, eps=1e-5,
+                 iparam=W.CFM_GROUPS)]
+    lr = [cbx.Op(cbx.OP_LAYER_NORM_ROPE, [t["xa"], t["wa"], t["ba"], t["pos"]], [ya], eps=1e-5, rope=rope64,
+                 iparam=W.HEAD_DIM)]
+    ops = gn + lr if order == "gn_first" else lr + gn[::-1]
+    return inp, t, (y256, y512, ya), ops
+
+
+@pytest.mark.parametrize("order", ["gn_first", "ln_rope_first"])
+@pytest.mark.parametrize("mish", [True, False])
+def test_cfm_flow_step_one_launch(cbx, oracle, rope64, order, mish):
+    """Both GroupNorms (split reduction) and LayerNorm+RoPE in one launch,
+    listed in either order: the single-op entry points' bits (GroupNorm
+    without Mish: the oracle's bits), LayerNorm+RoPE the oracle's bits."""
+    act = cbx.MISH if mish else cbx.UNARY_NONE
+    inp, t, (y256, y512, ya), ops = cfm_flow_ops(cbx, rope64, order, act)
+    cbx.run_ops(ops)
+    for x, w, b, y, C in ((t["x256"], t["w256"], t["b256"], y256, 256), (t["x512"], t["w512"], t["b512"], y512, 512)):
+        ref = cbx.group_norm(x, W.CFM_GROUPS, 1e-5, w, b, act=act)
+        assert_bitexact(host(y), host(ref), f"group norm {C} = cbx_group_norm")
+        if not mish:
+            exp = oracle.group_norm_affine(inp[f"x{C}"], W.CFM_GROUPS, 1e-5, inp[f"w{C}"], inp[f"b{C}"], False, nth=8)
+            assert_bitexact(host(y), exp, f"group norm {C} vs oracle")
+    ln = oracle.layer_norm(inp["xa"], inp["wa"], inp["ba"], 1e-5, nth=8)
+    exp = oracle.rope_ext(ln.reshape(2, W.CFM_T, W.CFM_HEADS, W.HEAD_DIM), inp["pos"], W.HEAD_DIM, mode=2,
+                          nth=8).reshape(inp["xa"].shape)
+    assert_bitexact(host(ya), exp, "layer norm + rope vs oracle")
+    f = ctypes.c_uint32(0)
+    assert cbx.load().cbx_device_errors(0, ctypes.byref(f), 1) == cbx.OK and f.value == 0
+
+
+def test_flow_step_repeated_and_with_other_ops(cbx, oracle, rope64):
+    """The same list launched 20 times back to back (the exchange words of
+    each launch carry its own tag) and once more beside a GELU op (the
+    all-kinds kernel): same bits every time."""
+    inp, t, outs, ops = cfm_flow_ops(cbx, rope64)
+    batch = cbx.OpBatch(ops)
+    batch.launch()
+    ref = [host(o).copy() for o in outs]
+    for o in outs:
+        o.fill_(float("nan"))
+    for _ in range(20):
+        batch.launch()
+    for o, r in zip(outs, ref):
+        assert_bitexact(host(o), r, "after 20 launches")
+    g = dev(W.normal(99, (4096,)))
+    gy = torch.empty_like(g)
+    for o in outs:
+        o.fill_(float("nan"))
+    cbx.run_ops(ops + [cbx.Op(cbx.OP_UNARY, [g], [gy], act=cbx.GELU)])
+    for o, r in zip(outs, ref):
+        assert_bitexact(host(o), r, "beside a GELU op")
+    assert_bitexact(host(gy), host(cbx.gelu(g)), "gelu in the same launch")
+
+
+def test_flow_ops_refused_layouts(cbx, rope64):
+    """In-place GroupNorm (the split is out of place only), a GroupNorm of
+    many small groups (no split), a head size whose partners span waves, and
+    a non-zero reserved field are refused before anything launches."""
+    x = dev(W.normal(5, (2, 256, 1, 500)))
+    with pytest.raises(cbx.CbxError, match="in place"):
+        cbx.run_ops([cbx.Op(cbx.OP_GROUP_NORM, [x], [x], eps=1e-5, iparam=8)])
+    small = dev(W.normal(6, (64, 32, 1, 8)))
+    with pytest.raises(cbx.CbxError, match="split"):
+        cbx.run_ops([cbx.Op(cbx.OP_GROUP_NORM, [small], [torch.empty_like(small)], eps=1e-5, iparam=8)])
+    xa = dev(W.normal(7, (2, 10, 320)))
+    pos = dev(np.arange(10, dtype=np.int32))
+    c40 = cbx.RopeCache(40, mode=2, n_pos=64)
+    with pytest.raises(cbx.CbxError, match="partners"):
+        cbx.run_ops([cbx.Op(cbx.OP_LAYER_NORM_ROPE, [xa, None, None, pos], [torch.empty_like(xa)], eps=1e-5,
+                            rope=c40, iparam=40)])
+    c40.close()
+    op = cbx.Op(cbx.OP_LAYER_NORM_ROPE, [xa, None, None, pos], [torch.empty_like(xa)], eps=1e-5, rope=rope64,
+                iparam=64)
+    b = cbx.OpBatch([op])
+    b.arr[0].reserved = 1
+    with pytest.raises(cbx.CbxError, match="reserved"):
+        b.launch()
