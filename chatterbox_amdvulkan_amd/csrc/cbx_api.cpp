@@ -1541,17 +1541,34 @@ extern "C" int cbx_run_ops(const cbx_op* ops, int n_ops, cbx_stream stream) {
             if ((ops[i].kind == CBX_OP_GROUP_NORM) == (pass == 0)) order[n_order++] = i;
         }
     }
-    int64_t total = 0, gn_blocks = 0;
+    int64_t total = 0, gn_blocks = 0, nbk[CBX_MAX_OPS];
     uint32_t gn_slot = 0;
     for (int k = 0; k < n_ops; k++) {
         const int i = order[k];
         if (ops[i].reserved != 0) return batch_fail(i, CBX_ERR_INVALID_ARG, "reserved must be 0");
-        int64_t nb = 0;
-        a.blk0[k] = static_cast<uint32_t>(total);
-        if ((rc = build_op(i, ops[i], a.op[k], st, strm, &gn_slot, &nb))) return rc;
-        if (ops[i].kind == CBX_OP_GROUP_NORM) gn_blocks += nb;
-        total += nb;
+        if ((rc = build_op(i, ops[i], a.op[k], st, strm, &gn_slot, &nbk[k]))) return rc;
+        if (ops[i].kind == CBX_OP_GROUP_NORM) gn_blocks += nbk[k];
+        total += nbk[k];
         if (total >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "cbx_run_ops: too many workgroups");
+    }
+    // a launch of more workgroups than about 6 a CU takes two rounds: its
+    // f32 element-wise ops then take two vectors a lane (half the
+    // workgroups), the rest stay as they are
+    if (total > int64_t{6} * st->n_cu) {
+        for (int k = 0; k < n_ops; k++) {
+            BOp& b = a.op[k];
+            if ((b.kind == CBX_OP_UNARY || b.kind == CBX_OP_LEAKY_RELU) && b.t_x == CBX_TYPE_F32 && nbk[k] > 0) {
+                total -= nbk[k];
+                b.aux3 = 2;
+                nbk[k] = cdiv(b.rows / 4 + 1, 512);
+                total += nbk[k];
+            }
+        }
+    }
+    total = 0;
+    for (int k = 0; k < n_ops; k++) {
+        a.blk0[k] = static_cast<uint32_t>(total);
+        total += nbk[k];
     }
     if (gn_blocks > int64_t{2} * st->n_cu) {
         return set_error(CBX_ERR_UNSUPPORTED, "cbx_run_ops: the group norms' chunk workgroups are more than 2 a CU");

@@ -129,8 +129,48 @@ __device__ __forceinline__ float b_unary1(int op, float x, const uint16_t* tab, 
     return apply_act(op, x, tab, param);
 }
 
+// Two 4-vectors a lane (aux3 == 2; f32, not the f16 table path): half the
+// workgroups, so that a large element-wise op fits the CUs in one round
+// beside the other ops of its launch.  Both loads issue first; the same
+// arithmetic per element as one vector a lane.
+__device__ __forceinline__ void b_unary_f32_x2(const BOp& op, uint32_t lb, const uint16_t* tab) {
+    const int64_t i0 = static_cast<int64_t>(lb) * (2 * kThreads) + threadIdx.x;
+    const int64_t i1 = i0 + kThreads;
+    const int64_t n = op.rows, n4 = n >> 2;
+    const int fn = op.kind == CBX_OP_LEAKY_RELU ? UNARY_LEAKY : op.act;
+    const char* x = op.t[0].p;
+    char* y = op.t[6].p;
+    const float4 v0 = Stream<float>::load4(x + (i0 < n4 ? i0 : 0) * 16);
+    const float4 v1 = Stream<float>::load4(x + (i1 < n4 ? i1 : 0) * 16);
+    float4 o0, o1;
+    if (fn == CBX_UNARY_GELU) {
+        o0 = act_gelu_fast4(tab, v0);
+        o1 = act_gelu_fast4(tab, v1);
+    } else {
+        o0 = make_float4(b_unary1(fn, v0.x, tab, op.param), b_unary1(fn, v0.y, tab, op.param),
+                         b_unary1(fn, v0.z, tab, op.param), b_unary1(fn, v0.w, tab, op.param));
+        o1 = make_float4(b_unary1(fn, v1.x, tab, op.param), b_unary1(fn, v1.y, tab, op.param),
+                         b_unary1(fn, v1.z, tab, op.param), b_unary1(fn, v1.w, tab, op.param));
+    }
+    if (i0 < n4) Stream<float>::store4(y + i0 * 16, o0);
+    if (i1 < n4) Stream<float>::store4(y + i1 * 16, o1);
+    for (int64_t i : {i0, i1}) {
+        if (i == n4) {
+            for (int64_t j = n4 * 4; j < n; j++) {
+                Elt<float>::store1(y + j * 4, b_unary1(fn, Elt<float>::load1(x + j * 4), tab, op.param));
+            }
+        }
+    }
+}
+
 template <typename T>
 __device__ __forceinline__ void b_unary_t(const BOp& op, uint32_t lb, const uint16_t* tab) {
+    if constexpr (std::is_same<T, float>::value) {
+        if (op.aux3 == 2) {
+            b_unary_f32_x2(op, lb, tab);
+            return;
+        }
+    }
     const int64_t i = static_cast<int64_t>(lb) * kThreads + threadIdx.x;
     const int64_t n = op.rows, n4 = n >> 2;
     const int fn = op.kind == CBX_OP_LEAKY_RELU ? UNARY_LEAKY : op.act;

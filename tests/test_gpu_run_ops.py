@@ -100,6 +100,25 @@ def test_prefill_chain_one_launch(cbx, oracle):
     assert_bitexact(host(g), oracle.unary(oracle.GELU, inp["ffn"], nth=8), "gelu")
 
 
+@pytest.mark.parametrize("n", [2 * 1024 * 1024, 2 * 1024 * 1024 - 3, 1700001])
+def test_large_launch_two_vectors_a_lane(cbx, oracle, n):
+    """A launch of more workgroups than about 6 a CU gives its f32
+    element-wise ops two vectors a lane: GELU and LeakyReLU over lengths
+    with and without a tail (n % 4 != 0), next to a norm, match the
+    single-op entry points bit for bit."""
+    x = W.normal(140 + n % 7, (n,), 0.0, 3.0)
+    xd = dev(x)
+    g, lk = torch.empty_like(xd), torch.empty_like(xd)
+    r = dev(W.normal(141, (64, 1024)))
+    ry = torch.empty_like(r)
+    cbx.run_ops([cbx.Op(cbx.OP_LAYER_NORM, [r], [ry], eps=1e-5),
+                 cbx.Op(cbx.OP_UNARY, [xd], [g], act=cbx.GELU),
+                 cbx.Op(cbx.OP_LEAKY_RELU, [xd], [lk], param=0.1)])
+    assert_bitexact(host(g), oracle.unary(oracle.GELU, x, nth=8), "gelu")
+    assert_bitexact(host(lk), oracle.leaky_relu(x, 0.1, nth=8), "leaky")
+    assert_bitexact(host(ry), host(cbx.layer_norm(r, None, None, 1e-5)), "norm")
+
+
 def test_vocoder_ops_and_tails(cbx, oracle):
     """Snake (both alpha layouts), LeakyReLU, LayerNorm+Mish, unary with a
     ragged length, gather + add -- together."""
