@@ -122,11 +122,16 @@ __global__ __launch_bounds__(kThreads) void k_soft_max_row(View x, View y, float
     float* yr = reinterpret_cast<float*>(y.data + row_offset(y, r, fy));
     const int64_t j = r % x.ne[1];
     const int64_t lim = n_past >= 0 ? (n_past + j < ne0 - 1 ? n_past + j : ne0 - 1) : ne0 - 1;
+    // the columns a lane holds: k < nk (uniform); the loads of those issue
+    // together, the others are skipped (a decode row of 256 scores reads
+    // one column a lane, not 16)
+    const int nk = static_cast<int>((ne0 + kThreads - 1) / kThreads);
     float v[K];
 #pragma unroll
     for (int k = 0; k < K; k++) {
         const int64_t c = threadIdx.x + static_cast<int64_t>(k) * kThreads;
-        v[k] = xr[c < ne0 ? c : 0];
+        v[k] = -INFINITY;
+        if (k < nk) v[k] = xr[c < ne0 ? c : 0];
     }
     float m = -INFINITY;
 #pragma unroll
@@ -144,16 +149,18 @@ __global__ __launch_bounds__(kThreads) void k_soft_max_row(View x, View y, float
     double sum = 0.0;
 #pragma unroll
     for (int k = 0; k < K; k++) {
-        const int64_t c = threadIdx.x + static_cast<int64_t>(k) * kThreads;
-        v[k] = c < ne0 ? expf(v[k] - m) : 0.0f;
-        sum += static_cast<double>(v[k]);
+        if (k < nk) {
+            const int64_t c = threadIdx.x + static_cast<int64_t>(k) * kThreads;
+            v[k] = c < ne0 ? expf(v[k] - m) : 0.0f;
+            sum += static_cast<double>(v[k]);
+        }
     }
     sum = block_sum(sum, red);
     const float inv = static_cast<float>(1.0 / sum);
 #pragma unroll
     for (int k = 0; k < K; k++) {
         const int64_t c = threadIdx.x + static_cast<int64_t>(k) * kThreads;
-        if (c < ne0) yr[c] = v[k] * inv;
+        if (k < nk && c < ne0) yr[c] = v[k] * inv;
     }
 }
 
