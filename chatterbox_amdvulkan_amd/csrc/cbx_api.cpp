@@ -1396,7 +1396,11 @@ int build_op(int i, const cbx_op& o, BOp& b, DeviceState* st, hipStream_t strm, 
                 b.t[6] = bten(h, h ? static_cast<int64_t>(h->nb[1]) : 0);
                 b.t[7] = bten(y, static_cast<int64_t>(y->nb[1]));
                 b.nv = y->ne[0] <= 256 ? 1 : y->ne[0] <= 512 ? 2 : 4;
-                *nblk = cdiv(b.rows, 4);
+                // rows of 513..1024 and few tokens against the CUs: one
+                // token a workgroup over its 4 waves (aux3 = 4) instead of
+                // four tokens a workgroup, one wave each
+                b.aux3 = b.nv == 4 && b.rows <= int64_t{4} * st->n_cu ? 4 : 1;
+                *nblk = b.aux3 == 4 ? b.rows : cdiv(b.rows, 4);
             } else {
                 b.t[6] = bten(y, static_cast<int64_t>(y->nb[1]));
                 *nblk = b.rows;
@@ -1550,6 +1554,19 @@ extern "C" int cbx_run_ops(const cbx_op* ops, int n_ops, cbx_stream stream) {
         if (ops[i].kind == CBX_OP_GROUP_NORM) gn_blocks += nbk[k];
         total += nbk[k];
         if (total >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "cbx_run_ops: too many workgroups");
+    }
+    // an embedding + LayerNorm beside more than 2 other workgroups a CU
+    // takes one wave a token (four tokens a workgroup): its four-wave form's
+    // longer-lived workgroups would hold the CUs the other ops need (the
+    // prefill chain with GELU: 6.93 against 6.54 us a launch)
+    for (int k = 0; k < n_ops; k++) {
+        BOp& b = a.op[k];
+        if (b.kind == CBX_OP_GET_ROWS_ADD_LAYER_NORM && b.aux3 == 4 && total - nbk[k] > int64_t{2} * st->n_cu) {
+            total -= nbk[k];
+            b.aux3 = 1;
+            nbk[k] = cdiv(b.rows, 4);
+            total += nbk[k];
+        }
     }
     // a launch of more workgroups than about 6 a CU takes two rounds: its
     // f32 element-wise ops then take two vectors a lane (half the

@@ -433,8 +433,35 @@ __device__ __forceinline__ void b_gather_1(const BOp& op, uint32_t lb, uint32_t*
     else b_gather_t<TYPE, CBX_TYPE_Q8_0>(op, lb, err);
 }
 
+// One token a workgroup, its 4 waves holding a quarter of the row each
+// (rows of 513..1024 elements, aux3 == 4): the standalone kernel's few-row
+// form, for launches whose tokens are few against the CUs (a 512-token
+// prefill), where one wave a token walks the whole row's chain alone.
 template <int TYPE, int TYPE2>
-__device__ __forceinline__ void b_embed_nv(const BOp& op, uint32_t lb, uint32_t* err) {
+__device__ __forceinline__ void b_embed_ln_w4(const BOp& op, uint32_t lb, uint32_t* err, double* lds) {
+    const int lane = threadIdx.x;   // wave w: float4s [64w, 64w + 64)
+    const int64_t t = lb;
+    const int64_t ne0 = op.ne0;
+    const int32_t id = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const int32_t*>(op.t[1].p + t * op.t[1].nb1));
+    const int32_t id2 = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const int32_t*>(op.t[3].p + t * op.t[3].nb1));
+    char* yr = op.t[7].p + t * op.t[7].nb1;
+    char* hr = op.t[6].p ? op.t[6].p + t * op.t[6].nb1 : nullptr;
+    const float* w = reinterpret_cast<const float*>(op.t[4].p);
+    const float* b = reinterpret_cast<const float*>(op.t[5].p);
+    Affine<1> af;
+    af.load_sel(w, b, reinterpret_cast<const float*>(op.table), lane, ne0);
+    const bool bad = id < 0 || id >= op.aux || id2 < 0 || id2 >= op.aux2;
+    const int64_t r1 = bad ? 0 : id, r2 = bad ? 0 : id2;
+    embed_ln_row<TYPE, TYPE2, 1, 4>(op.t[0].p + r1 * op.t[0].nb1, op.t[2].p + r2 * op.t[2].nb1, af, w != nullptr,
+                                    b != nullptr, hr, yr, ne0, op.eps, lane, bad, err, lds);
+}
+
+template <int TYPE, int TYPE2>
+__device__ __forceinline__ void b_embed_nv(const BOp& op, uint32_t lb, uint32_t* err, double* lds) {
+    if (op.aux3 == 4) {
+        b_embed_ln_w4<TYPE, TYPE2>(op, lb, err, lds);
+        return;
+    }
     switch (op.nv) {
         case 1: b_embed_ln_t<TYPE, TYPE2, 1>(op, lb, err); break;
         case 2: b_embed_ln_t<TYPE, TYPE2, 2>(op, lb, err); break;
@@ -443,10 +470,10 @@ __device__ __forceinline__ void b_embed_nv(const BOp& op, uint32_t lb, uint32_t*
 }
 
 template <int TYPE>
-__device__ __forceinline__ void b_embed_1(const BOp& op, uint32_t lb, uint32_t* err) {
-    if (op.t_x2 == CBX_TYPE_F32) b_embed_nv<TYPE, CBX_TYPE_F32>(op, lb, err);
-    else if (op.t_x2 == CBX_TYPE_F16) b_embed_nv<TYPE, CBX_TYPE_F16>(op, lb, err);
-    else b_embed_nv<TYPE, CBX_TYPE_Q8_0>(op, lb, err);
+__device__ __forceinline__ void b_embed_1(const BOp& op, uint32_t lb, uint32_t* err, double* lds) {
+    if (op.t_x2 == CBX_TYPE_F32) b_embed_nv<TYPE, CBX_TYPE_F32>(op, lb, err, lds);
+    else if (op.t_x2 == CBX_TYPE_F16) b_embed_nv<TYPE, CBX_TYPE_F16>(op, lb, err, lds);
+    else b_embed_nv<TYPE, CBX_TYPE_Q8_0>(op, lb, err, lds);
 }
 
 // ---- GroupNorm (split reduction): one chunk a workgroup -------------------------------
@@ -622,9 +649,9 @@ __global__ __launch_bounds__(kThreads) void k_batch(BatchArgs args) {
             break;
         case CBX_OP_GET_ROWS_ADD_LAYER_NORM:
             if constexpr ((KS & KB_EMBED) != 0) {
-                if (op.t_x == CBX_TYPE_F32) b_embed_1<CBX_TYPE_F32>(op, lb, err);
-                else if (op.t_x == CBX_TYPE_F16) b_embed_1<CBX_TYPE_F16>(op, lb, err);
-                else b_embed_1<CBX_TYPE_Q8_0>(op, lb, err);
+                if (op.t_x == CBX_TYPE_F32) b_embed_1<CBX_TYPE_F32>(op, lb, err, lds);
+                else if (op.t_x == CBX_TYPE_F16) b_embed_1<CBX_TYPE_F16>(op, lb, err, lds);
+                else b_embed_1<CBX_TYPE_Q8_0>(op, lb, err, lds);
             }
             break;
         case CBX_OP_SNAKE:
