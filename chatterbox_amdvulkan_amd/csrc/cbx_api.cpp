@@ -1583,9 +1583,10 @@ extern "C" int cbx_run_ops(const cbx_op* ops, int n_ops, cbx_stream stream) {
         }
     }
     total = 0;
-    for (int k = 0; k < n_ops; k++) {
-        a.blk0[k] = static_cast<uint32_t>(total);
-        total += nbk[k];
+    for (int k = 0; k < kBatchMaxOps; k++) {
+        // past the last op: an offset no workgroup reaches
+        a.blk0[k] = k < n_ops ? static_cast<uint32_t>(total) : UINT32_MAX;
+        if (k < n_ops) total += nbk[k];
     }
     if (gn_blocks > int64_t{2} * st->n_cu) {
         return set_error(CBX_ERR_UNSUPPORTED, "cbx_run_ops: the group norms' chunk workgroups are more than 2 a CU");

@@ -578,17 +578,20 @@ __global__ __launch_bounds__(kThreads) void k_batch(BatchArgs args) {
     __shared__ double lds[8];
     const BatchArgs* a = (const BatchArgs*)(const void*)__builtin_amdgcn_kernarg_segment_ptr();
     const uint32_t b = blockIdx.x;
-    const int n = a->n;
-    // the op owning this workgroup: all first-block offsets are read at once
-    // (independent scalar loads), not one dependent load per op
+    // the op owning this workgroup: every first-block offset is read, in one
+    // round of scalar loads (the host fills the entries past the last op
+    // with UINT32_MAX, so no test of the op count stands between them: with
+    // one, the compiler loaded the offsets one dependent round at a time)
+    uint32_t blk[kBatchMaxOps];
+#pragma unroll
+    for (int k = 0; k < kBatchMaxOps; k++) blk[k] = a->blk0[k];
     int i = 0;
     uint32_t base = 0;   // blk0[0] == 0
 #pragma unroll
     for (int k = 1; k < kBatchMaxOps; k++) {
-        if (k < n && b >= a->blk0[k]) {
-            i = k;
-            base = a->blk0[k];
-        }
+        const bool in = b >= blk[k];
+        i = in ? k : i;
+        base = in ? blk[k] : base;
     }
     // the op's fields, copied before any branch on them: the copy's scalar
     // loads issue together, where reads under each branch (kind, layout,
