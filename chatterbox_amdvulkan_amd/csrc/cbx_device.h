@@ -108,6 +108,19 @@ __device__ __forceinline__ void set(float4& v, int k, float x) {
 __device__ __forceinline__ void arg_now(const void* p) { asm volatile("" ::"s"(p)); }
 __device__ __forceinline__ void arg_now(uint32_t v) { asm volatile("" ::"s"(v)); }
 
+// ---- early stores ------------------------------------------------------------
+// A row kernel that stores one output (the embedding sum, the residual sum)
+// before its reductions: if some loads may still be pending when that store
+// issues (loads the compiler sank into a conditional block, the affine
+// vectors), the compiler waits for them at their first use after the store
+// with vmcnt(0) -- and on this GPU family vmcnt counts stores as well, so
+// the arithmetic after the reductions waits for the early store's write
+// acknowledgement.  Waiting for every vector memory operation just before
+// the early store (an s_waitcnt the compiler's wait placement accounts for)
+// leaves only the store pending.  Call it where every lane passes (not
+// inside the store's own condition).
+__device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
+
 // ---- reductions ----------------------------------------------------------
 // DPP move of a double (two 32-bit halves) inside each 16-lane row.
 template <int CTRL>

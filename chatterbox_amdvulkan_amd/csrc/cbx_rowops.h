@@ -238,6 +238,11 @@ template <int TYPE, int TYPE2, int NV, int W = 1>
 __device__ __forceinline__ void embed_ln_row(const char* s1, const char* s2, const Affine<NV>& af, bool hw, bool hb,
                                              char* hr, char* yr, int64_t ne0, float eps, int lane, bool bad,
                                              uint32_t* err, double* lds = nullptr) {
+    // several waves a row: the caller's w and b loads stay ahead of the row
+    // loads (the standalone [512,1024] kernel, four waves a token: 3.85
+    // against 3.99 us with the rows first); one wave a row: the compiler's
+    // order (the op batch's prefill launch: 6.00 against 6.14 us)
+    if constexpr (W > 1) __builtin_amdgcn_sched_barrier(0);
     float4 p[NV], q[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
@@ -249,15 +254,22 @@ __device__ __forceinline__ void embed_ln_row(const char* s1, const char* s2, con
         if (lane < 64) embed_bad_row(hr, yr, ne0, lane, err);
         return;
     }
+    // h by a select, not a branch (a branch would take the row loads into
+    // its block), then h stored with nothing else pending: the prefill
+    // launch's embedding + LayerNorm beside GELU, 6.00 against 6.47 us
     float4 v[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        const int64_t j = (lane + 64 * k) * 4;
-        if (j < ne0) {
-            v[k] = make_float4(p[k].x + q[k].x, p[k].y + q[k].y, p[k].z + q[k].z, p[k].w + q[k].w);
-            if (hr) Stream<float>::store4(hr + j * 4, v[k]);
-        } else {
-            v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        const bool in = (lane + 64 * k) * 4 < ne0;
+        v[k] = make_float4(in ? p[k].x + q[k].x : 0.f, in ? p[k].y + q[k].y : 0.f, in ? p[k].z + q[k].z : 0.f,
+                           in ? p[k].w + q[k].w : 0.f);
+    }
+    wait_vector_memory();
+    if (hr) {
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int64_t j = (lane + 64 * k) * 4;
+            if (j < ne0) Stream<float>::store4(hr + j * 4, v[k]);
         }
     }
     const float scale = row_scale_w<NV, NORM_LN, W>(v, lane, ne0, eps, lds);

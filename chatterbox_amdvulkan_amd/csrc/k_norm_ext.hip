@@ -81,6 +81,9 @@ __global__ __launch_bounds__(64 * WPB * WPR) void k_ln_ext(LnExtArgs p) {
     char* sr = p.s + row_off<FLAT>(p.ms, row);   // only stored through when p.s is set
     Affine<NV> af;
     af.load_sel(p.w, p.b, reinterpret_cast<const float*>(p.tab), lane, ne0);
+    // several waves a row: w and b issue ahead of the row loads, as in the
+    // embedding's LayerNorm
+    if constexpr (WPR > 1) __builtin_amdgcn_sched_barrier(0);
     float m = 1.0f;
     if constexpr (MASK) m = p.mask[row % p.ma.ne1];
     // every load is unconditional (clamped address) so all are in flight
@@ -101,20 +104,18 @@ __global__ __launch_bounds__(64 * WPB * WPR) void k_ln_ext(LnExtArgs p) {
             q[k] = *reinterpret_cast<const float4*>(rr + (j < ne0 ? j : 0) * 4);
         }
     }
+    // the sums by selects, not a branch (a branch would take the loads into
+    // its block); the sum, when stored, with nothing else pending
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        if ((lane + 64 * k) * 4 >= ne0) {
-            v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-            continue;
-        }
-        if constexpr (PRO == PRO_BIAS_RESID) {
-            v[k] = make_float4(v[k].x + c[k].x, v[k].y + c[k].y, v[k].z + c[k].z, v[k].w + c[k].w);
-        }
-        if constexpr (PRO != PRO_NONE) {
-            v[k] = make_float4(v[k].x + q[k].x, v[k].y + q[k].y, v[k].z + q[k].z, v[k].w + q[k].w);
-        }
+        const bool in = (lane + 64 * k) * 4 < ne0;
+        float4 t = v[k];
+        if constexpr (PRO == PRO_BIAS_RESID) t = make_float4(t.x + c[k].x, t.y + c[k].y, t.z + c[k].z, t.w + c[k].w);
+        if constexpr (PRO != PRO_NONE) t = make_float4(t.x + q[k].x, t.y + q[k].y, t.z + q[k].z, t.w + q[k].w);
+        v[k] = make_float4(in ? t.x : 0.f, in ? t.y : 0.f, in ? t.z : 0.f, in ? t.w : 0.f);
     }
     if constexpr (PRO != PRO_NONE) {
+        wait_vector_memory();
         if (p.s) {
 #pragma unroll
             for (int k = 0; k < NV; k++) {

@@ -76,11 +76,13 @@ int launch_layer_norm_rope(const cbx_tensor* x, const cbx_tensor* w, const cbx_t
     const int vec_mod = p.mode == 2 ? 8 : 4;
     a.vec_cs = (reinterpret_cast<uintptr_t>(table) % 16 == 0 && p.n_dims % vec_mod == 0) ? 1 : 0;
     const int nv = x->ne[0] <= 256 ? 1 : x->ne[0] <= 512 ? 2 : 4;
-    // waves a row: enough for about eight waves a CU, at most 4 and at most
-    // one per vector a lane (the rotation reads partners from the LDS row
-    // after a workgroup barrier, so a wave's share need not be whole heads)
+    // waves a row: one, unless the launch would have fewer than about two
+    // waves a CU; then up to 4, at most one per vector a lane (the rotation
+    // reads partners from the LDS row after a workgroup barrier, so a wave's
+    // share need not be whole heads).  [2,500,512]: one wave a row, 3.30
+    // against 3.41 us with two (the second reduction's barrier)
     int wr = 1;
-    while (wr < 4 && wr < nv && rows * wr < int64_t{8} * st->n_cu) wr *= 2;
+    while (wr < 4 && wr < nv && rows * wr < int64_t{2} * st->n_cu) wr *= 2;
     const dim3 grid(static_cast<unsigned>(rows));
     const bool flat = a.mx.flat && a.my.flat;
     // partners in registers: the head's vectors on consecutive lanes of one

@@ -61,6 +61,25 @@ def test_shapes_modes_partial_dims(cbx, oracle, C, hd, n_dims, mode):
     cache.close()
 
 
+@pytest.mark.parametrize("C,hd,n_dims,mode", [(1024, 128, 96, 2), (1000, 40, 40, 2), (768, 64, 64, 0),
+                                              (512, 128, 64, 2), (1024, 256, 256, 2)])
+def test_many_rows_one_wave_a_row(cbx, oracle, C, hd, n_dims, mode):
+    """600 rows: every width takes one wave a row (the launch holds at least
+    two waves a CU), with partners from registers (hd = 64) or from LDS."""
+    T, B = 300, 2
+    x = W.normal(190 + C, (B, T, C), 0.1, 1.5)
+    w = W.normal(191, (C,), 1.0, 0.05)
+    b = W.normal(192, (C,), 0.0, 0.05)
+    pos = W.randint(193, (T,), 0, 4096)
+    cache = cbx.RopeCache(n_dims, mode=mode, n_ctx_orig=4096, freq_base=10000.0, n_pos=4096)
+    got = host(cbx.layer_norm_rope(dev(x), dev(w), dev(b), 1e-5, hd, dev(pos), cache))
+    ln = oracle.layer_norm(x, w, b, 1e-5, nth=8)
+    exp = oracle.rope_ext(ln.reshape(B, T, C // hd, hd), pos, n_dims, mode=mode, n_ctx_orig=4096,
+                          nth=8).reshape(x.shape)
+    assert_bitexact(got, exp, f"ln+rope C={C} hd={hd} n_dims={n_dims} mode={mode}, 600 rows")
+    cache.close()
+
+
 def test_no_affine_in_place_and_positions_past_table(cbx, oracle):
     """w = b = NULL; y == x; positions beyond the table's rows use the device
     recurrence exactly as cbx_rope_ext does."""
