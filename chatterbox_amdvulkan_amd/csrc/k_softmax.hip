@@ -21,10 +21,36 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaveMaxRow = 4096;
 
+// Max over the 64 lanes of a wave, in every lane (a max is exact in any
+// order).  wave_max: a butterfly of lane shuffles (LDS permutes).
+// wave_max_dpp: the f64 sum's butterfly inside each 16-lane row (DPP moves,
+// no LDS round trip), then the four row maxima read from lanes 0/16/32/48;
+// all 64 lanes must be active.  The few-row decode kernel takes the DPP
+// form (0.25 us a launch less: the T3 decode token, 24 softmax launches,
+// 247-249 against 253-255 us); the wave-per-row kernel keeps the shuffles
+// (DPP there: T3 prefill scores 8.0 against 8.15 us, CFM scores 8.4
+// against 8.2 us).
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
     return v;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));    // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f32<0x4E>(v));    // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f32<0x141>(v));   // row_half_mirror
+    v = fmaxf(v, dpp_f32<0x140>(v));   // row_mirror
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 // score after scale and mask; columns past the row end read as -inf
@@ -112,54 +138,75 @@ __global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
 // f64 sum over the workgroup.  One kernel for every length up to 4096, so a
 // decode loop whose rows grow by one column a token launches the same
 // kernel each token and a captured graph takes the new length in place.
-__global__ __launch_bounds__(kThreads) void k_soft_max_row(View x, View y, float s, int64_t n_past, bool fx, bool fy) {
+// The row's address and query index come from the compact arguments with
+// 32-bit index arithmetic, every field in the first batch of argument
+// loads: a View's 64-bit divisions and the dependent argument loads they
+// waited on put about 900 instructions before the first score load.
+template <bool FLAT>
+__global__ __launch_bounds__(kThreads) void k_soft_max_row(SoftMaxArgs a) {
     constexpr int K = kWaveMaxRow / kThreads;
-    __shared__ double red[kThreads / WAVE];
-    __shared__ float redf[kThreads / WAVE];
-    const int64_t r = blockIdx.x;
-    const int64_t ne0 = x.ne[0];
-    const float* xr = reinterpret_cast<const float*>(x.data + row_offset(x, r, fx));
-    float* yr = reinterpret_cast<float*>(y.data + row_offset(y, r, fy));
-    const int64_t j = r % x.ne[1];
-    const int64_t lim = n_past >= 0 ? (n_past + j < ne0 - 1 ? n_past + j : ne0 - 1) : ne0 - 1;
+    constexpr int NW = kThreads / WAVE;
+    __shared__ float redf[NW];
+    __shared__ double red[NW];
+    arg_now(a.x); arg_now(a.y); arg_now(reinterpret_cast<const void*>(a.mx.nb1));
+    arg_now(reinterpret_cast<const void*>(a.my.nb1)); arg_now(reinterpret_cast<const void*>(a.n_past));
+    arg_now(static_cast<uint32_t>(a.ne0)); arg_now(a.n_q);
+    if constexpr (!FLAT) {
+        for (const RowMap* m : {&a.mx, &a.my}) {
+            arg_now(reinterpret_cast<const void*>(m->nb2)); arg_now(reinterpret_cast<const void*>(m->nb3));
+            arg_now(m->ne1); arg_now(m->ne2);
+        }
+    }
+    const uint32_t r = blockIdx.x;
+    const int ne0 = a.ne0;
+    const float* xr = reinterpret_cast<const float*>(a.x + (FLAT ? r * a.mx.nb1 : row_at(a.mx, r)));
+    float* yr = reinterpret_cast<float*>(a.y + (FLAT ? r * a.my.nb1 : row_at(a.my, r)));
+    const int64_t j = r % a.n_q;
+    const int64_t lim = a.n_past >= 0 ? (a.n_past + j < ne0 - 1 ? a.n_past + j : ne0 - 1) : ne0 - 1;
     // the columns a lane holds: k < nk (uniform); the loads of those issue
     // together, the others are skipped (a decode row of 256 scores reads
     // one column a lane, not 16)
-    const int nk = static_cast<int>((ne0 + kThreads - 1) / kThreads);
+    const int nk = (ne0 + kThreads - 1) / kThreads;
     float v[K];
 #pragma unroll
     for (int k = 0; k < K; k++) {
-        const int64_t c = threadIdx.x + static_cast<int64_t>(k) * kThreads;
+        const int c = threadIdx.x + k * kThreads;
         v[k] = -INFINITY;
         if (k < nk) v[k] = xr[c < ne0 ? c : 0];
     }
     float m = -INFINITY;
 #pragma unroll
     for (int k = 0; k < K; k++) {
-        const int64_t c = threadIdx.x + static_cast<int64_t>(k) * kThreads;
-        v[k] = c < ne0 ? masked(v[k], s, c, lim) : -INFINITY;
+        const int c = threadIdx.x + k * kThreads;
+        v[k] = c < ne0 ? masked(v[k], a.s, c, lim) : -INFINITY;
         m = fmaxf(m, v[k]);
     }
-    m = wave_max(m);
+    m = wave_max_dpp(m);
     if ((threadIdx.x & 63) == 0) redf[threadIdx.x >> 6] = m;
     __syncthreads();
     m = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kThreads / WAVE; w++) m = fmaxf(m, redf[w]);
+    for (int w = 0; w < NW; w++) m = fmaxf(m, redf[w]);
     double sum = 0.0;
 #pragma unroll
     for (int k = 0; k < K; k++) {
         if (k < nk) {
-            const int64_t c = threadIdx.x + static_cast<int64_t>(k) * kThreads;
+            const int c = threadIdx.x + k * kThreads;
             v[k] = c < ne0 ? expf(v[k] - m) : 0.0f;
             sum += static_cast<double>(v[k]);
         }
     }
-    sum = block_sum(sum, red);
+    // the wave totals in index order (one barrier; the area is not the max's)
+    sum = wave_sum(sum);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    sum = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) sum += red[w];
     const float inv = static_cast<float>(1.0 / sum);
 #pragma unroll
     for (int k = 0; k < K; k++) {
-        const int64_t c = threadIdx.x + static_cast<int64_t>(k) * kThreads;
+        const int c = threadIdx.x + k * kThreads;
         if (k < nk && c < ne0) yr[c] = v[k] * inv;
     }
 }
@@ -190,6 +237,20 @@ __global__ __launch_bounds__(kThreads) void k_soft_max_loop(View x, View y, floa
     for (int64_t c = threadIdx.x; c < ne0; c += kThreads) yr[c] = expf(masked(xr[c], s, c, lim) - m) * inv;
 }
 
+SoftMaxArgs sm_args(const cbx_tensor* x, cbx_tensor* y, float s, int64_t n_past, int64_t nr) {
+    SoftMaxArgs a;
+    a.x = static_cast<const char*>(x->data);
+    a.y = static_cast<char*>(y->data);
+    a.mx = row_map(x);
+    a.my = row_map(y);
+    a.n_past = n_past;
+    a.ne0 = static_cast<int32_t>(x->ne[0]);
+    a.nr = static_cast<int32_t>(nr);
+    a.n_q = static_cast<uint32_t>(x->ne[1] > 0 ? x->ne[1] : 1);
+    a.s = s;
+    return a;
+}
+
 int waves_for(int64_t rows, const DeviceState* st) { return rows >= int64_t{8} * st->n_cu ? 4 : 1; }
 
 template <int WPB, bool FLAT>
@@ -217,21 +278,13 @@ int launch_soft_max(const cbx_tensor* x, float s, int64_t n_past, cbx_tensor* y,
     if (nr >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "soft_max: too many rows");
     if (ne0 <= kWaveMaxRow && nr < int64_t{4} * st->n_cu) {
         // few rows (a decode step's heads): one kernel whatever the length
-        hipLaunchKernelGGL(k_soft_max_row, dim3(static_cast<unsigned>(nr)), dim3(kThreads), 0, strm, vx, vy, s, n_past,
-                           fx, fy);
+        SoftMaxArgs a = sm_args(x, y, s, n_past, nr);
+        if (a.mx.flat && a.my.flat) hipLaunchKernelGGL(k_soft_max_row<true>, dim3(static_cast<unsigned>(nr)), dim3(kThreads), 0, strm, a);
+        else hipLaunchKernelGGL(k_soft_max_row<false>, dim3(static_cast<unsigned>(nr)), dim3(kThreads), 0, strm, a);
     } else if (vec) {
         const int64_t need = cdiv(ne0, 256);
         const int nv = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : 16;
-        SoftMaxArgs a;
-        a.x = static_cast<const char*>(x->data);
-        a.y = static_cast<char*>(y->data);
-        a.mx = row_map(x);
-        a.my = row_map(y);
-        a.n_past = n_past;
-        a.ne0 = static_cast<int32_t>(ne0);
-        a.nr = static_cast<int32_t>(nr);
-        a.n_q = static_cast<uint32_t>(x->ne[1]);
-        a.s = s;
+        SoftMaxArgs a = sm_args(x, y, s, n_past, nr);
         // strided-plane layouts take one row per workgroup through the row map
         if (!(a.mx.flat && a.my.flat)) sm_wave<1, false>(nv, a, strm);
         else if (waves_for(nr, st) == 1) sm_wave<1, true>(nv, a, strm);
