@@ -211,6 +211,63 @@ __global__ __launch_bounds__(kThreads) void k_soft_max_row(SoftMaxArgs a) {
     }
 }
 
+// Few rows of up to 1024 scores at any alignment (the T3 decode step's 16
+// rows of n_past + 1 columns, n_past < 1024): one wave a row, up to 16
+// columns a lane (column lane + 64 k), the max and the f64 sum by DPP
+// butterflies -- no LDS and no barrier.  One kernel for every length up to
+// 1024, like k_soft_max_row.
+template <bool FLAT>
+__global__ __launch_bounds__(WAVE) void k_soft_max_row_w(SoftMaxArgs a) {
+    constexpr int K = 1024 / WAVE;
+    arg_now(a.x); arg_now(a.y); arg_now(reinterpret_cast<const void*>(a.mx.nb1));
+    arg_now(reinterpret_cast<const void*>(a.my.nb1)); arg_now(reinterpret_cast<const void*>(a.n_past));
+    arg_now(static_cast<uint32_t>(a.ne0)); arg_now(a.n_q);
+    if constexpr (!FLAT) {
+        for (const RowMap* m : {&a.mx, &a.my}) {
+            arg_now(reinterpret_cast<const void*>(m->nb2)); arg_now(reinterpret_cast<const void*>(m->nb3));
+            arg_now(m->ne1); arg_now(m->ne2);
+        }
+    }
+    const uint32_t r = blockIdx.x;
+    const int ne0 = a.ne0, lane = threadIdx.x;
+    const float* xr = reinterpret_cast<const float*>(a.x + (FLAT ? r * a.mx.nb1 : row_at(a.mx, r)));
+    float* yr = reinterpret_cast<float*>(a.y + (FLAT ? r * a.my.nb1 : row_at(a.my, r)));
+    const int64_t j = r % a.n_q;
+    const int64_t lim = a.n_past >= 0 ? (a.n_past + j < ne0 - 1 ? a.n_past + j : ne0 - 1) : ne0 - 1;
+    const int nk = (ne0 + WAVE - 1) / WAVE;   // uniform: the loads of k < nk issue together
+    float v[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int c = lane + k * WAVE;
+        v[k] = -INFINITY;
+        if (k < nk) v[k] = xr[c < ne0 ? c : 0];
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int c = lane + k * WAVE;
+        v[k] = c < ne0 ? masked(v[k], a.s, c, lim) : -INFINITY;
+        m = fmaxf(m, v[k]);
+    }
+    m = wave_max_dpp(m);
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        if (k < nk) {
+            const int c = lane + k * WAVE;
+            v[k] = c < ne0 ? expf(v[k] - m) : 0.0f;
+            sum += static_cast<double>(v[k]);
+        }
+    }
+    sum = wave_sum(sum);
+    const float inv = static_cast<float>(1.0 / sum);
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int c = lane + k * WAVE;
+        if (k < nk && c < ne0) yr[c] = v[k] * inv;
+    }
+}
+
 // Any row length: max, then the f64 sum of exponentials, then the output,
 // each pass over the row (the exponentials are recomputed identically).
 __global__ __launch_bounds__(kThreads) void k_soft_max_loop(View x, View y, float s, int64_t n_past, bool fx,
@@ -279,8 +336,16 @@ int launch_soft_max(const cbx_tensor* x, float s, int64_t n_past, cbx_tensor* y,
     if (ne0 <= kWaveMaxRow && nr < int64_t{4} * st->n_cu) {
         // few rows (a decode step's heads): one kernel whatever the length
         SoftMaxArgs a = sm_args(x, y, s, n_past, nr);
-        if (a.mx.flat && a.my.flat) hipLaunchKernelGGL(k_soft_max_row<true>, dim3(static_cast<unsigned>(nr)), dim3(kThreads), 0, strm, a);
-        else hipLaunchKernelGGL(k_soft_max_row<false>, dim3(static_cast<unsigned>(nr)), dim3(kThreads), 0, strm, a);
+        const dim3 grid(static_cast<unsigned>(nr));
+        const bool flat = a.mx.flat && a.my.flat;
+        if (ne0 <= 1024) {
+            if (flat) hipLaunchKernelGGL(k_soft_max_row_w<true>, grid, dim3(WAVE), 0, strm, a);
+            else hipLaunchKernelGGL(k_soft_max_row_w<false>, grid, dim3(WAVE), 0, strm, a);
+        } else if (flat) {
+            hipLaunchKernelGGL(k_soft_max_row<true>, grid, dim3(kThreads), 0, strm, a);
+        } else {
+            hipLaunchKernelGGL(k_soft_max_row<false>, grid, dim3(kThreads), 0, strm, a);
+        }
     } else if (vec) {
         const int64_t need = cdiv(ne0, 256);
         const int nv = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : 16;

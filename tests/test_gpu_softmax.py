@@ -74,6 +74,18 @@ def test_row_lengths_in_place_and_constant_rows(cbx, oracle, n):
     assert_bitexact(got[0], np.full(n, np.float32(1.0 / n)), "constant row")
 
 
+@pytest.mark.parametrize("n", [300, 2000])
+def test_few_rows_planes_not_at_one_stride(cbx, oracle, n):
+    """Few rows whose planes are not one row stride apart (a slice of the
+    rows and columns of a 3-D tensor): the decode kernels' row map, one wave
+    a row up to 1024 columns and a workgroup a row past that."""
+    base = W.normal(135 + n, (2, 5, n + 12), 0.0, 9.0)
+    v = dev(base)[:, 1:4, 6:6 + n]
+    exp = oracle.scale_diag_mask_soft_max(np.ascontiguousarray(base[:, 1:4, 6:6 + n]), 0.5, n - 3)
+    got = host(cbx.scale_diag_mask_soft_max(v, 0.5, n - 3))
+    check(got, exp, f"planes apart, n={n}", mask_of((2, 3, n), n - 3))
+
+
 def test_strided_rows_and_extremes(cbx, oracle):
     """A column-sliced view (rows at a stride, loop path) and large score gaps."""
     base = W.normal(134, (6, 300), 0.0, 30.0)
