@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--hift-conv", action="store_true",
                     help="only the HiFT conv1d / transposed-conv timings, as one JSON object (for profiling)")
     ap.add_argument("--only", choices=["decode", "serving", "cfm", "hift", "softmax", "t3_block", "t3_token", "hift_conv",
-                                       "copy"],
+                                       "cfm_estimator", "copy"],
                     help="run one secondary workload alone and print its JSON (no headline line)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the markdown summary of two --pmc runs over --traffic-probe (no GPU)")
@@ -797,6 +797,84 @@ def bench_t3_token(C, W, torch, reps=200, tokens=64):
     return out
 
 
+def estimator_bytes(C, e, plan):
+    """Bytes one estimator call's launches move: per launch, every tensor it
+    reads from outside the launch once (a causal conv's weights as their
+    prepared f16 copy) and every tensor it stores."""
+    nd, at = e.graph.nodes, e.b.at
+    total = 0
+    for kind, f, n, flags in plan:
+        if kind == C.GL_VIEW:
+            continue
+        made = {nd[j].dst for j in range(f, f + n)}
+        reads = {s for j in range(f, f + n) for s in nd[j].src if s >= 0} - made
+        if kind == C.GL_CAUSAL_CONV1D:
+            w = nd[f + 7].src[0]          # the weight tensor of the im2col node
+            reads.discard(w)
+            total += at(w).numel() * 2
+        total += sum(at(s).numel() * at(s).element_size() for s in reads)
+        y = at(nd[f + n - 1].dst)
+        total += y.numel() * y.element_size()
+        if kind == C.GL_ADD_LAYER_NORM and not flags & 1:
+            total += y.numel() * y.element_size()   # the residual sum, stored too
+    return total
+
+
+def bench_cfm_estimator(C, torch, T=500, reps=20):
+    """One CFM estimator call's element-wise nodes (cfm_decoder.cpp:395-565:
+    14 resnet blocks with their 29 causal blocks, 56 transformer blocks; the
+    matmul outputs given, the causal convs on the library's conv kernel) at
+    the reference's sizes over T frames, planned into one list of launches
+    (chatterbox_amdvulkan_amd/cfm_estimator.py).  Device time per call from
+    back-to-back replays of the list captured into a HIP graph
+    (cbx_graph_exec), and the same list planned and launched each call
+    (cbx_graph_compute)."""
+    from chatterbox_amdvulkan_amd.cfm_estimator import CFMEstimator
+
+    e = CFMEstimator(T, seed=5)
+    try:
+        plan = e.plan()
+        ex = e.graph.capture(e.keep)
+        s = cur_stream(torch)
+        nbytes = estimator_bytes(C, e, plan)
+        kinds = {}
+        names = {v: k[3:].lower() for k, v in vars(C).items() if k.startswith("GL_") and isinstance(v, int)}
+        for p in plan:
+            if p[0] != C.GL_VIEW:
+                kinds[names[p[0]]] = kinds.get(names[p[0]], 0) + 1
+        out = {"reference_sequence": f"cfm_decoder.cpp:395-565, T_mel {T}, 14 resnet blocks, 56 transformer blocks",
+               "launches": ex.n_launches, "launches_by_kind": kinds, "bytes_per_call": nbytes}
+        for _ in range(3):
+            ex.launch(s)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            ex.launch(s)
+        e1.record()
+        torch.cuda.synchronize()
+        dev_us = e0.elapsed_time(e1) * 1000.0 / reps
+        out["exec_replay_us_per_call"] = dev_us
+        out["exec_replay_us_per_launch"] = dev_us / ex.n_launches
+        out["GBps"] = nbytes / (dev_us * 1e-6) / 1e9
+        ex.close()
+        for _ in range(2):
+            e.graph.compute(e.keep)
+        torch.cuda.synchronize()
+        n_c = max(5, reps // 4)
+        tm = time.perf_counter()
+        e0.record()
+        for _ in range(n_c):
+            e.graph.compute(e.keep)
+        host = (time.perf_counter() - tm) / n_c * 1e6
+        e1.record()
+        torch.cuda.synchronize()
+        out["graph_compute_us_per_call"] = {"host_us": host, "device_us": e0.elapsed_time(e1) * 1000.0 / n_c}
+        return out
+    finally:
+        e.close()
+
+
 PEAK_MFMA_F16_TFLOPS = 2500.0
 
 
@@ -1490,6 +1568,7 @@ def main():
               "cfm": lambda: bench_cfm(C, W, torch), "hift": lambda: bench_hift(C, W, torch),
               "softmax": lambda: bench_softmax(C, W, torch), "t3_block": lambda: bench_t3_block(C, W, torch),
               "t3_token": lambda: bench_t3_token(C, W, torch),
+              "cfm_estimator": lambda: bench_cfm_estimator(C, torch),
               "hift_conv": lambda: bench_hift_conv(C, W, torch),
               "copy": lambda: bench_copy_ceiling(C, torch, {"gelu_bytes": nb["gelu"],
                                                             "embed_layer_norm_bytes": nb["embed_layer_norm"],
@@ -1536,6 +1615,8 @@ def main():
         details["t3_block_elementwise"] = bench_t3_block(C, W, torch)
         log("t3 token")
         details["t3_token_elementwise"] = bench_t3_token(C, W, torch)
+        log("cfm estimator")
+        details["cfm_estimator_elementwise"] = bench_cfm_estimator(C, torch)
         log("hift conv")
         details["hift_resblock_conv"] = bench_hift_conv(C, W, torch)
     k_ms = res["kernel_ms"]["run_ops"]
@@ -1589,6 +1670,11 @@ def main():
                                                         f"{tt['launches']} launches, n_past {tt['n_past']}",
                                   "exec_replay": round(tt["exec_replay_us_per_token"], 2),
                                   "decode_loop_with_update": round(tt["decode_loop_us_per_token"], 2)}
+    if "cfm_estimator_elementwise" in details:
+        ce = details["cfm_estimator_elementwise"]
+        out["cfm_estimator_us_per_call"] = {"reference_sequence": ce["reference_sequence"] +
+                                            f", {ce['launches']} launches",
+                                            "exec_replay": round(ce["exec_replay_us_per_call"], 2)}
     out["details"] = details
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(W, a.cpu_seconds)

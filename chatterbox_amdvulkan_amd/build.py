@@ -38,6 +38,7 @@ SOURCES = [
     "k_conv1d.hip",
     "k_eltwise.hip",
     "k_batch.hip",
+    "k_binary.hip",
 ]
 HEADERS = ["cbx_internal.h", "cbx_device.h", "cbx_rowops.h", os.path.join("..", "..", "include", "cbxops.h")]
 

@@ -115,7 +115,7 @@ GOP_VIEW, GOP_GET_ROWS, GOP_ADD, GOP_MUL, GOP_SCALE, GOP_NORM, GOP_RMS_NORM, GOP
 GL_UNSUPPORTED, GL_VIEW, GL_GET_ROWS, GL_GET_ROWS_ADD, GL_GET_ROWS_ADD_LAYER_NORM, GL_NORM, GL_LAYER_NORM, \
     GL_LAYER_NORM_ROPE, GL_RMS_NORM, GL_GROUP_NORM, GL_SOFT_MAX, GL_SNAKE, GL_UNARY, GL_SWIGLU, GL_LEAKY_RELU, \
     GL_ROPE, GL_CPY, GL_ADD_LAYER_NORM, GL_LAYER_NORM_MASK, GL_BIAS_ACT, GL_CONV1D, GL_CONV_TRANSPOSE1D, \
-    GL_CAUSAL_CONV1D, GL_GET_ROWS_CONCAT_ADD_LAYER_NORM = range(24)
+    GL_CAUSAL_CONV1D, GL_GET_ROWS_CONCAT_ADD_LAYER_NORM, GL_BINARY, GL_CONCAT = range(26)
 # conv launch flags: the prologue (bits 0-1), a bias add, the residual add
 GLF_SNAKE, GLF_LEAKY, GLF_MASK, GLF_BIAS, GLF_RESIDUAL = 1, 2, 3, 4, 8
 
@@ -183,6 +183,8 @@ def load() -> ctypes.CDLL:
         "cbx_add_layer_norm": (i, [P, P, P, P, P, f, i, P, P, vp]),
         "cbx_layer_norm_mask": (i, [P, P, P, f, i, P, P, vp]),
         "cbx_bias_act": (i, [i, P, P, P, vp]),
+        "cbx_binary": (i, [i, P, P, P, vp]),
+        "cbx_concat": (i, [P, P, i, P, vp]),
         "cbx_conv1d_weights_create": (i, [P, vp, ctypes.POINTER(vp)]),
         "cbx_conv1d_weights_destroy": (None, [vp]),
         "cbx_conv1d": (i, [P, vp, i, i, i, i, P, P, f, P, P, P, vp]),
@@ -634,6 +636,32 @@ def bias_act(act, x, bias, out=None):
     _ready(x)
     out = _out_like(x, out)
     _check(load().cbx_bias_act(act, _ref(desc(x)), _ref(desc(bias)), _ref(desc(out)), _stream()))
+    return out
+
+
+# cbx_binary_op
+BINARY_ADD, BINARY_MUL = 0, 1
+
+
+def binary(op, a, b, out=None):
+    """ggml_add / ggml_mul(a, b) with b repeated to a's shape (torch shapes are
+    ggml's ne reversed: a mask of one value per frame of a (T, C) tensor is
+    (T, 1))."""
+    _ready(a)
+    out = _out_like(a, out)
+    _check(load().cbx_binary(op, _ref(desc(a)), _ref(desc(b)), _ref(desc(out)), _stream()))
+    return out
+
+
+def concat(a, b, dim, out=None):
+    """ggml_concat(a, b, dim), dim a ggml axis (0: the last torch axis)."""
+    _ready(a)
+    if out is None:
+        shape = list(a.shape)
+        ax = a.dim() - 1 - dim
+        shape[ax] = a.shape[ax] + b.shape[ax]
+        out = torch.empty(shape, dtype=a.dtype, device=a.device)
+    _check(load().cbx_concat(_ref(desc(a)), _ref(desc(b)), dim, _ref(desc(out)), _stream()))
     return out
 
 

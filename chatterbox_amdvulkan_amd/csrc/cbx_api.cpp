@@ -1613,3 +1613,63 @@ extern "C" int cbx_run_ops(const cbx_op* ops, int n_ops, cbx_stream stream) {
     if (total == 0) return CBX_OK;
     return launch_batch(a, static_cast<uint32_t>(total), reinterpret_cast<hipStream_t>(stream));
 }
+
+// ---- ggml_add / ggml_mul with repeat, ggml_concat ------------------------------
+
+namespace {
+
+bool same_view(const cbx_tensor* a, const cbx_tensor* b) {
+    if (a->data != b->data || !same_shape(a, b)) return false;
+    for (int k = 0; k < 4; k++) if (a->ne[k] > 1 && a->nb[k] != b->nb[k]) return false;
+    return true;
+}
+
+}  // namespace
+
+extern "C" int cbx_binary(int op, const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_binary";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(a, what, "a")) || (rc = validate(b, what, "b")) || (rc = validate(y, what, "y"))) return rc;
+    if (op != CBX_BINARY_ADD && op != CBX_BINARY_MUL) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_binary: unknown op " + std::to_string(op));
+    }
+    if (a->type != CBX_TYPE_F32 || b->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_binary: F32 only");
+    }
+    if (!same_shape(a, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_binary: a and y shapes differ");
+    if (nelements(a) == 0) return CBX_OK;
+    for (int k = 0; k < 4; k++) {
+        if (b->ne[k] < 1 || a->ne[k] % b->ne[k] != 0) {
+            return set_error(CBX_ERR_INVALID_ARG, "cbx_binary: b must repeat to a's shape (every a.ne[i] a multiple of b.ne[i])");
+        }
+    }
+    if (overlaps(y, b) || (overlaps(y, a) && !same_view(y, a))) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_binary: y overlaps b, or a other than as a itself");
+    }
+    return launch_binary(op, a, b, y, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int cbx_concat(const cbx_tensor* a, const cbx_tensor* b, int dim, cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_concat";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(a, what, "a")) || (rc = validate(b, what, "b")) || (rc = validate(y, what, "y"))) return rc;
+    if (dim < 0 || dim > 3) return set_error(CBX_ERR_INVALID_ARG, "cbx_concat: dim must be 0..3");
+    if ((a->type != CBX_TYPE_F32 && a->type != CBX_TYPE_F16) || b->type != a->type || y->type != a->type) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_concat: a, b and y must all be F32 or all F16");
+    }
+    for (int k = 0; k < 4; k++) {
+        const bool ok = k == dim ? y->ne[k] == a->ne[k] + b->ne[k] : (a->ne[k] == y->ne[k] && b->ne[k] == y->ne[k]);
+        if (!ok) {
+            return set_error(CBX_ERR_INVALID_ARG, "cbx_concat: y.ne[dim] must be a.ne[dim] + b.ne[dim] and the other dims equal");
+        }
+    }
+    if (overlaps(y, a) || overlaps(y, b)) return set_error(CBX_ERR_INVALID_ARG, "cbx_concat: y overlaps a or b");
+    if (nelements(y) == 0) return CBX_OK;
+    return launch_concat(a, b, dim, y, reinterpret_cast<hipStream_t>(stream));
+}

@@ -171,6 +171,14 @@ struct Planner {
     }
 
     bool col_vec(int32_t p, int32_t x) const { return valid_t(x) && dims(p, 1, t[x].ne[1], 1, 1); }
+    // b repeats to x's shape (ggml_can_repeat): every x.ne[k] a multiple of b.ne[k]
+    bool repeats(int32_t b, int32_t x) const {
+        if (!valid_t(b) || !valid_t(x)) return false;
+        for (int k = 0; k < 4; k++) {
+            if (t[b].ne[k] < 1 || t[x].ne[k] % t[b].ne[k] != 0) return false;
+        }
+        return true;
+    }
 
     // layer_norm at node i reading `in`, optionally followed by a mish
     // chain: the node count (3 or 6), or 0
@@ -464,10 +472,16 @@ struct Planner {
                         *len = 1 + l;
                         return CBX_GL_ADD_LAYER_NORM;
                     }
-                    if (!bias) return CBX_GL_UNSUPPORTED;   // (a one-row x is also a bias add)
+                    if (!bias) {   // (a one-row x is also a bias add)
+                        *flags = CBX_BINARY_ADD;
+                        return CBX_GL_BINARY;
+                    }
                 }
                 // bias add [-> activation]
-                if (!bias && !col_vec(a.src[1], x)) return CBX_GL_UNSUPPORTED;
+                if (!bias && !col_vec(a.src[1], x)) {
+                    *flags = CBX_BINARY_ADD;
+                    return repeats(a.src[1], x) ? CBX_GL_BINARY : CBX_GL_UNSUPPORTED;
+                }
                 if (is_unary(i + 1, CBX_UNARY_SOFTPLUS) && mish_at(i + 1, t1) && internal(t1, 2)) {
                     *len = 4;
                 } else if (is(i + 1, CBX_GOP_UNARY) && nd[i + 1].src[0] == t1 && internal(t1, 1) &&
@@ -547,7 +561,8 @@ struct Planner {
                         return CBX_GL_CAUSAL_CONV1D;
                     }
                 }
-                return CBX_GL_UNSUPPORTED;
+                *flags = CBX_BINARY_MUL;
+                return repeats(al, x) ? CBX_GL_BINARY : CBX_GL_UNSUPPORTED;
             }
             case CBX_GOP_UNARY: {
                 const int32_t x = a.src[0];
@@ -576,6 +591,8 @@ struct Planner {
                 return CBX_GL_ROPE;
             case CBX_GOP_CPY:
                 return CBX_GL_CPY;
+            case CBX_GOP_CONCAT:
+                return CBX_GL_CONCAT;
             default:
                 return CBX_GL_UNSUPPORTED;
         }
@@ -675,8 +692,10 @@ constexpr int32_t kSpan[][2] = {
     {7, 14}, // CONV_TRANSPOSE1D [snake | leaky] [bias]
     {12, 15}, // CAUSAL_CONV1D [mask] [bias]
     {7, 12},  // GET_ROWS_CONCAT_ADD_LAYER_NORM [prompt gather, concat] [casts]
+    {1, 1},  // BINARY
+    {1, 1},  // CONCAT
 };
-constexpr int32_t kLastKind = CBX_GL_GET_ROWS_CONCAT_ADD_LAYER_NORM;
+constexpr int32_t kLastKind = CBX_GL_CONCAT;
 static_assert(sizeof(kSpan) / sizeof(kSpan[0]) == kLastKind + 1, "one span per launch kind");
 
 // Issues the entry point a launch maps to.  A launch is only read within
@@ -784,6 +803,11 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
             return cbx_rope_ext(T(t, a.src[0]), T(t, a.src[1]), a.rope, y, s);
         case CBX_GL_CPY:
             return cbx_cpy(T(t, a.src[0]), y, s);
+        case CBX_GL_BINARY:
+            if (a.op != (l.flags == CBX_BINARY_MUL ? CBX_GOP_MUL : CBX_GOP_ADD)) break;
+            return cbx_binary(l.flags, T(t, a.src[0]), T(t, a.src[1]), y, s);
+        case CBX_GL_CONCAT:
+            return cbx_concat(T(t, a.src[0]), T(t, a.src[1]), a.iparam, y, s);
         case CBX_GL_ADD_LAYER_NORM: {
             if (l.n_nodes == 6) break;
             const bool bias = l.n_nodes == 5 || l.n_nodes == 8;

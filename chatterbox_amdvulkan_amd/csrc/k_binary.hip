@@ -1,0 +1,162 @@
+// k_binary.hip -- ggml_add / ggml_mul with the second operand repeated to
+// the first's shape, and ggml_concat.
+//
+// Binary: y[i0,i1,i2,i3] = a[i0,i1,i2,i3] op b[i0 % b.ne0, i1 % b.ne1,
+// i2 % b.ne2, i3 % b.ne3] (ggml_can_repeat(b, a)), one f32 rounding -- the
+// CFM decoder's mul(x, mask) of every (C, T) tensor by its per-frame mask
+// (cfm_decoder.cpp:139,148,182,554-557) and the residual joins that no
+// LayerNorm follows (cfm_decoder.cpp:183,287).  Contiguous tensors with b
+// the same shape, a repeated row of ne0 values, or one value per row take
+// one 4-element vector per lane over a grid that covers a once; other
+// layouts take a workgroup per row.
+//
+// Concat: y = ggml_concat(a, b, dim) -- the decoder's channel packing and
+// skip join (cfm_decoder.cpp:486-492,536).  A workgroup per output row.
+#include <type_traits>
+
+#include "cbx_internal.h"
+#include "cbx_device.h"
+
+namespace cbx {
+namespace {
+
+constexpr int kThreads = 256;
+
+enum { BIN_SAME = 0, BIN_ROW = 1, BIN_COL = 2 };
+
+template <int OP>
+__device__ __forceinline__ float bin(float x, float y) {
+    if constexpr (OP == CBX_BINARY_ADD) return x + y;
+    else return x * y;
+}
+
+// MODE BIN_SAME: b[i]; BIN_ROW: b[i % ne0] (ne0 % 4 == 0); BIN_COL: b[row
+// % nbr], one value a row of ne0 elements.
+template <int OP, int MODE>
+__global__ __launch_bounds__(kThreads) void k_binary_flat(const float* __restrict__ a, const float* __restrict__ b,
+                                                          float* __restrict__ y, uint32_t n4, uint32_t ne0_4,
+                                                          uint32_t nbr) {
+    arg_now(a);
+    arg_now(b);
+    arg_now(y);
+    // lanes past the end load the last vector and store nothing (n4 >= 1)
+    const uint32_t iu = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t i = iu < n4 ? iu : n4 - 1;
+    float4 bv;
+    if constexpr (MODE == BIN_SAME) {
+        bv = *reinterpret_cast<const float4*>(b + 4ull * i);
+    } else if constexpr (MODE == BIN_ROW) {
+        bv = *reinterpret_cast<const float4*>(b + 4u * (i % ne0_4));
+    } else {
+        const float s = b[(i / ne0_4) % nbr];
+        bv = make_float4(s, s, s, s);
+    }
+    const float4 v = *reinterpret_cast<const float4*>(a + 4ull * i);
+    const float4 o = make_float4(bin<OP>(v.x, bv.x), bin<OP>(v.y, bv.y), bin<OP>(v.z, bv.z), bin<OP>(v.w, bv.w));
+    if (iu < n4) *reinterpret_cast<float4*>(y + 4ull * i) = o;
+}
+
+// Any strides: rows of a (and y) enumerate ne1, ne2, ne3; b's row is the
+// repeat of the same indices.
+template <int OP>
+__global__ __launch_bounds__(kThreads) void k_binary_rows(View a, View b, View y, int64_t nr) {
+    for (int64_t r = blockIdx.x; r < nr; r += gridDim.x) {
+        const int64_t i1 = r % a.ne[1], q = r / a.ne[1];
+        const int64_t i2 = q % a.ne[2], i3 = q / a.ne[2];
+        const char* ar = a.data + i1 * a.nb[1] + i2 * a.nb[2] + i3 * a.nb[3];
+        char* yr = y.data + i1 * y.nb[1] + i2 * y.nb[2] + i3 * y.nb[3];
+        const char* br = b.data + (i1 % b.ne[1]) * b.nb[1] + (i2 % b.ne[2]) * b.nb[2] + (i3 % b.ne[3]) * b.nb[3];
+        for (int64_t j = threadIdx.x; j < a.ne[0]; j += kThreads) {
+            const float x = *reinterpret_cast<const float*>(ar + j * a.nb[0]);
+            const float v = *reinterpret_cast<const float*>(br + (j % b.ne[0]) * b.nb[0]);
+            *reinterpret_cast<float*>(yr + j * y.nb[0]) = bin<OP>(x, v);
+        }
+    }
+}
+
+// A workgroup per row of y: along dim 0 the row is a's row then b's; along
+// dim d > 0 the row is a's when its index along d is below a.ne[d], else
+// b's at that index minus a.ne[d].  ES: the element size (4 or 2).
+template <int ES>
+__global__ __launch_bounds__(kThreads) void k_concat(View a, View b, View y, int dim, int64_t nr) {
+    using E = typename std::conditional<ES == 4, uint32_t, uint16_t>::type;
+    for (int64_t r = blockIdx.x; r < nr; r += gridDim.x) {
+        int64_t idx[4];
+        idx[1] = r % y.ne[1];
+        const int64_t q = r / y.ne[1];
+        idx[2] = q % y.ne[2];
+        idx[3] = q / y.ne[2];
+        char* yr = y.data + idx[1] * y.nb[1] + idx[2] * y.nb[2] + idx[3] * y.nb[3];
+        if (dim == 0) {
+            const char* ar = a.data + idx[1] * a.nb[1] + idx[2] * a.nb[2] + idx[3] * a.nb[3];
+            const char* br = b.data + idx[1] * b.nb[1] + idx[2] * b.nb[2] + idx[3] * b.nb[3];
+            for (int64_t j = threadIdx.x; j < y.ne[0]; j += kThreads) {
+                const E v = j < a.ne[0] ? *reinterpret_cast<const E*>(ar + j * a.nb[0])
+                                        : *reinterpret_cast<const E*>(br + (j - a.ne[0]) * b.nb[0]);
+                *reinterpret_cast<E*>(yr + j * y.nb[0]) = v;
+            }
+        } else {
+            // the source's fields by value (a reference to a kernel argument
+            // would put the argument block in scratch)
+            const bool from_a = idx[dim] < a.ne[dim];
+            if (!from_a) idx[dim] -= a.ne[dim];
+            const char* sd = from_a ? a.data : b.data;
+            const int64_t s0 = from_a ? a.nb[0] : b.nb[0], s1 = from_a ? a.nb[1] : b.nb[1];
+            const int64_t s2 = from_a ? a.nb[2] : b.nb[2], s3 = from_a ? a.nb[3] : b.nb[3];
+            const char* sr = sd + idx[1] * s1 + idx[2] * s2 + idx[3] * s3;
+            for (int64_t j = threadIdx.x; j < y.ne[0]; j += kThreads) {
+                *reinterpret_cast<E*>(yr + j * y.nb[0]) = *reinterpret_cast<const E*>(sr + j * s0);
+            }
+        }
+    }
+}
+
+bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+template <int OP>
+void binary_go(const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y, hipStream_t s) {
+    const int64_t n = nelements(a);
+    const bool same = same_shape(a, b) && is_contiguous(b) && al16(b->data);
+    const bool row = b->ne[0] == a->ne[0] && b->ne[1] == 1 && b->ne[2] == 1 && b->ne[3] == 1 && is_contiguous(b) &&
+                     al16(b->data);
+    const bool col = b->ne[0] == 1 && b->ne[1] == a->ne[1] && b->ne[2] == 1 && b->ne[3] == 1 &&
+                     (b->ne[1] == 1 || b->nb[1] == sizeof(float));
+    const bool flat = is_contiguous(a) && is_contiguous(y) && al16(a->data) && al16(y->data) && a->ne[0] % 4 == 0 &&
+                      n / 4 < (int64_t{1} << 31) && (same || row || col);
+    if (flat) {
+        const uint32_t n4 = static_cast<uint32_t>(n / 4), ne0_4 = static_cast<uint32_t>(a->ne[0] / 4);
+        const uint32_t nbr = static_cast<uint32_t>(b->ne[1]);
+        const dim3 grid(static_cast<unsigned>(cdiv(n4, kThreads)));
+        const float* ap = static_cast<const float*>(a->data);
+        const float* bp = static_cast<const float*>(b->data);
+        float* yp = static_cast<float*>(y->data);
+        if (same) hipLaunchKernelGGL((k_binary_flat<OP, BIN_SAME>), grid, dim3(kThreads), 0, s, ap, bp, yp, n4, ne0_4, nbr);
+        else if (row) hipLaunchKernelGGL((k_binary_flat<OP, BIN_ROW>), grid, dim3(kThreads), 0, s, ap, bp, yp, n4, ne0_4, nbr);
+        else hipLaunchKernelGGL((k_binary_flat<OP, BIN_COL>), grid, dim3(kThreads), 0, s, ap, bp, yp, n4, ne0_4, nbr);
+        return;
+    }
+    const int64_t nr = nrows(a);
+    hipLaunchKernelGGL((k_binary_rows<OP>), dim3(static_cast<unsigned>(std::min<int64_t>(nr, int64_t{1} << 20))),
+                       dim3(kThreads), 0, s, view_of(a), view_of(b), view_of(y), nr);
+}
+
+}  // namespace
+
+int launch_binary(int op, const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y, hipStream_t s) {
+    if (op == CBX_BINARY_ADD) binary_go<CBX_BINARY_ADD>(a, b, y, s);
+    else binary_go<CBX_BINARY_MUL>(a, b, y, s);
+    return check_launch(op == CBX_BINARY_ADD ? "binary add" : "binary mul");
+}
+
+int launch_concat(const cbx_tensor* a, const cbx_tensor* b, int dim, cbx_tensor* y, hipStream_t s) {
+    const int64_t nr = nrows(y);
+    const dim3 grid(static_cast<unsigned>(std::min<int64_t>(nr, int64_t{1} << 20)));
+    if (y->type == CBX_TYPE_F32) {
+        hipLaunchKernelGGL((k_concat<4>), grid, dim3(kThreads), 0, s, view_of(a), view_of(b), view_of(y), dim, nr);
+    } else {
+        hipLaunchKernelGGL((k_concat<2>), grid, dim3(kThreads), 0, s, view_of(a), view_of(b), view_of(y), dim, nr);
+    }
+    return check_launch("concat");
+}
+
+}  // namespace cbx

@@ -332,6 +332,28 @@ int cbx_leaky_relu(const cbx_tensor* x, float slope, cbx_tensor* y,
 int cbx_bias_act(int act, const cbx_tensor* x, const cbx_tensor* bias,
                  cbx_tensor* y, cbx_stream stream);
 
+/* ggml_add(a, b) / ggml_mul(a, b) with b repeated to a's shape
+ * (ggml_can_repeat(b, a): every a.ne[i] a multiple of b.ne[i]): y = a + b or
+ * a * b, one f32 rounding.  The CFM decoder's mul(x, mask (1, T)) before its
+ * 1x1 convs and after final_proj (cfm_decoder.cpp:182,554-557) and the
+ * residual joins no LayerNorm follows (:183,287).  F32; a, y the same shape,
+ * any strides (nb[0] the element size); y may be a itself, and must not
+ * overlap b.                                                              */
+typedef enum {
+    CBX_BINARY_ADD = 0,
+    CBX_BINARY_MUL = 1,
+} cbx_binary_op;
+int cbx_binary(int op, const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y,
+               cbx_stream stream);
+
+/* ggml_concat(a, b, dim): y.ne[dim] = a.ne[dim] + b.ne[dim], the other
+ * dims equal to a's and b's; a's elements first (cfm_decoder.cpp:486-492
+ * packing x, mu, spks, cond along the channels; :536 the skip join).  F32
+ * or F16 (all three the same type), any strides; y must not overlap a or b.
+ * dim 0..3.                                                               */
+int cbx_concat(const cbx_tensor* a, const cbx_tensor* b, int dim, cbx_tensor* y,
+               cbx_stream stream);
+
 /* ggml_swiglu_split(g, u) = silu(g) * u, F32 or F16. */
 int cbx_swiglu(const cbx_tensor* g, const cbx_tensor* u, cbx_tensor* y,
                cbx_stream stream);
@@ -642,6 +664,10 @@ typedef enum cbx_glaunch_kind {
     CBX_GL_GET_ROWS_CONCAT_ADD_LAYER_NORM, /* [get_rows [-> cast] -> concat(prefix, .) ->]
                                  get_rows [-> cast] -> concat -> get_rows [-> cast]
                                  -> add -> norm -> mul -> add (t3.cpp:432-466)   */
+    CBX_GL_BINARY,            /* one add or mul whose second operand repeats to the
+                                 first's shape (cbx_binary): a per-frame mask, a
+                                 residual join no norm follows. flags: the op   */
+    CBX_GL_CONCAT,            /* one concat (cbx_concat)                        */
 } cbx_glaunch_kind;
 
 typedef struct cbx_glaunch {

@@ -1,0 +1,98 @@
+"""cbx_binary (ggml_add / ggml_mul with the second operand repeated) and
+cbx_concat (ggml_concat) against the oracle's add / mul (ggml's repeat by
+index) and numpy's concatenate: one f32 rounding per element, so bit-exact;
+a concat is a copy."""
+import numpy as np
+import pytest
+import torch
+
+from chatterbox_amdvulkan_amd import workloads as W
+from tests._util import assert_bitexact
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+# torch shapes (ggml ne reversed): a, then b repeating into it
+SHAPES = [
+    ((500, 256), (500, 256)),     # residual join, same shape
+    ((500, 256), (256,)),         # a bias along the channels
+    ((500, 256), (500, 1)),       # the per-frame mask of a (C, T) tensor
+    ((500, 320), (500, 1)),
+    ((3, 40, 12), (40, 1)),       # mask repeated over a batch
+    ((2, 6, 10), (1, 3, 5)),      # repeats along every axis
+    ((7, 13), (1, 13)),           # odd widths (the row path)
+    ((5, 6, 7, 8), (1, 1, 7, 1)),
+    ((1024,), (1024,)),           # vectors (the time embedding)
+]
+
+
+@pytest.mark.parametrize("op", [0, 1])
+@pytest.mark.parametrize("sa,sb", SHAPES)
+def test_binary_repeat_shapes(cbx, oracle, op, sa, sb):
+    a = W.normal(W.seed_of(40, len(sa)), sa, 0.0, 2.0)
+    b = W.normal(W.seed_of(41, len(sb)), sb, 0.5, 1.5)
+    got = host(cbx.binary(op, dev(a), dev(b)))
+    exp = oracle.add(a, b) if op == cbx.BINARY_ADD else oracle.mul(a, b)
+    assert_bitexact(got, exp, f"op {op} {sa} by {sb}")
+
+
+def test_binary_views_and_in_place(cbx, oracle):
+    """Strided a, b and y (column slices of wider buffers), and y == a."""
+    base = W.normal(W.seed_of(42, 0), (60, 50), 0.0, 1.0)
+    bb = W.normal(W.seed_of(42, 1), (60, 9), 0.0, 1.0)
+    a = dev(base)[:, 3:43]
+    m = dev(bb)[:, 2:3]                # (60, 1), rows 36 bytes apart
+    yb = torch.full((60, 64), float("nan"), device="cuda")
+    y = yb[:, 8:48]
+    cbx.binary(cbx.BINARY_MUL, a, m, out=y)
+    exp = oracle.mul(np.ascontiguousarray(base[:, 3:43]), np.ascontiguousarray(bb[:, 2:3]))
+    assert_bitexact(host(y), exp, "strided mul")
+    assert np.isnan(host(yb)[:, :8]).all() and np.isnan(host(yb)[:, 48:]).all(), "only y's columns written"
+    t = dev(base)
+    r = dev(W.normal(W.seed_of(42, 2), (60, 50), 0.0, 1.0))
+    cbx.binary(cbx.BINARY_ADD, t, r, out=t)
+    assert_bitexact(host(t), oracle.add(base, host(r)), "in place")
+
+
+def test_binary_refusals(cbx):
+    a = torch.zeros((6, 10), device="cuda")
+    with pytest.raises(cbx.CbxError):
+        cbx.binary(cbx.BINARY_ADD, a, torch.zeros((6, 3), device="cuda"))      # 10 % 3 != 0
+    with pytest.raises(cbx.CbxError):
+        cbx.binary(7, a, torch.zeros((10,), device="cuda"))                     # no such op
+    with pytest.raises(cbx.CbxError):
+        cbx.binary(cbx.BINARY_ADD, a, a[:, :5], out=a)                          # y overlaps b
+    with pytest.raises(cbx.CbxError):
+        cbx.binary(cbx.BINARY_ADD, a.half(), torch.zeros((10,), device="cuda").half())   # F32 only
+
+
+@pytest.mark.parametrize("dim", [0, 1, 2, 3])
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_concat_dims(cbx, dim, dtype):
+    sa = [2, 3, 4, 5]
+    sb = list(sa)
+    ax = 3 - dim
+    sb[ax] = 2 + dim
+    a = W.normal(W.seed_of(43, dim), tuple(sa), 0.0, 1.0).astype(dtype)
+    b = W.normal(W.seed_of(44, dim), tuple(sb), 0.0, 1.0).astype(dtype)
+    got = host(cbx.concat(dev(a), dev(b), dim))
+    assert_bitexact(got, np.concatenate((a, b), axis=ax), f"concat dim {dim} {np.dtype(dtype).name}")
+
+
+def test_concat_channels_of_views(cbx):
+    """The decoder's channel packing on (T, C) tensors, one operand a view."""
+    x = W.normal(W.seed_of(45, 0), (500, 80), 0.0, 1.0)
+    wide = W.normal(W.seed_of(45, 1), (500, 100), 0.0, 1.0)
+    got = host(cbx.concat(dev(x), dev(wide)[:, 10:90], 0))
+    assert_bitexact(got, np.concatenate((x, wide[:, 10:90]), axis=1), "pack")
+    with pytest.raises(cbx.CbxError):
+        cbx.concat(dev(x), dev(x[:10]), 0)                                      # other dims differ

@@ -198,11 +198,12 @@ def test_unsupported_node_is_refused(cbx):
     g = cbx.Graph()
     a, b, c = g.tensor(dev(np.ones((n, D), np.float32))), g.tensor(dev(np.ones((n, D), np.float32))), \
         g.tensor(empty(n, D))
-    g.node(cbx.GOP_ADD, c, (a, b))         # a plain add of two activations
+    g.node(cbx.GOP_ADD, c, (a, b))         # a plain add of two activations: a binary launch
+    g.node(cbx.GOP_UNARY, g.tensor(empty(n, D)), (c,), iparam=42)   # no such activation
     with pytest.raises(cbx.CbxError) as e:
         g.capture()
     assert e.value.status == cbx.ERR_UNSUPPORTED
-    assert "node 0 (ADD)" in str(e.value)
+    assert "node 1 (UNARY)" in str(e.value)
 
 
 def test_views_only_list(cbx):
@@ -544,6 +545,7 @@ def test_update_to_another_list(cbx):
     a3, b3, c3 = g3.tensor(dev(np.ones((4, 64), np.float32))), g3.tensor(dev(np.ones((4, 64), np.float32))), \
         g3.tensor(empty(4, 64))
     g3.node(cbx.GOP_ADD, c3, (a3, b3))
+    g3.node(cbx.GOP_UNARY, g3.tensor(empty(4, 64)), (c3,), iparam=42)   # no such activation
     ex = g.capture()
     try:
         buf[5].fill_(float("nan"))

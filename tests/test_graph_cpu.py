@@ -45,7 +45,7 @@ def test_t3_input_chain_is_one_launch():
     t3_input(g)
     plan = g.plan()
     assert plan[0] == (C.GL_GET_ROWS_ADD_LAYER_NORM, 0, 8, 0)   # h is read again: stored
-    assert plan[1] == (C.GL_UNSUPPORTED, 8, 1, 0)               # a plain residual add is not this library's
+    assert plan[1] == (C.GL_BINARY, 8, 1, C.BINARY_ADD)         # a plain residual add: cbx_binary
 
 
 def t3_input_concat(g: C.Graph, prompt=True, casts=True, D=64, n_pre=1, n_a=5, n_b=7, cast_type=torch.float32,
@@ -100,7 +100,7 @@ def test_t3_input_with_conditioning_prefix_is_one_launch(prompt, casts, n_nodes)
     t3_input_concat(g, prompt=prompt, casts=casts)
     plan = g.plan()
     assert plan[0] == (C.GL_GET_ROWS_CONCAT_ADD_LAYER_NORM, 0, n_nodes, 0)   # h is read later: stored
-    assert plan[1] == (C.GL_UNSUPPORTED, n_nodes, 1, 0)                      # the plain residual add
+    assert plan[1] == (C.GL_BINARY, n_nodes, 1, C.BINARY_ADD)                # the plain residual add
 
 
 def test_t3_input_with_prefix_unread_sum_and_refusals():
@@ -176,11 +176,11 @@ def test_layer_norm_mish_mask():
     g = C.Graph()
     causal_block_tail(g)
     assert g.plan() == [(C.GL_LAYER_NORM_MASK, 0, 7, 0)]
-    # a mask that is not one value per frame is a plain multiply: not this library's
+    # a mask that is not one value per frame is a plain multiply of its own
     g2 = C.Graph()
     t = causal_block_tail(g2)
     g2._descs[3] = C.desc(f32(20, 32))
-    assert g2.plan() == [(C.GL_LAYER_NORM, 0, 6, 0), (C.GL_UNSUPPORTED, 6, 1, 0)]
+    assert g2.plan() == [(C.GL_LAYER_NORM, 0, 6, 0), (C.GL_BINARY, 6, 1, C.BINARY_MUL)]
 
 
 def t3_block_tail(g: C.Graph, N=5, D=64, F=256):
@@ -216,7 +216,7 @@ def test_t3_block_tail():
                         (C.GL_BIAS_ACT, 6, 2, 0),
                         (C.GL_UNSUPPORTED, 8, 1, 0),
                         (C.GL_BIAS_ACT, 9, 1, 0),         # proj bias add alone
-                        (C.GL_UNSUPPORTED, 10, 1, 0)]     # a residual add with no norm after it
+                        (C.GL_BINARY, 10, 1, C.BINARY_ADD)]   # a residual add with no norm after it
 
 
 def test_residual_join_without_bias_and_unread_sum():
@@ -248,13 +248,13 @@ def test_bias_add_forms():
     full = g.tensor(f32(6, 40))
     g.node(C.GOP_ADD, g.tensor(f32(6, 40)), (x, full))
     assert g.plan() == [(C.GL_BIAS_ACT, 0, 2, 0), (C.GL_BIAS_ACT, 2, 4, 0), (C.GL_BIAS_ACT, 6, 2, 0),
-                        (C.GL_UNSUPPORTED, 8, 1, 0)]
+                        (C.GL_BINARY, 8, 1, C.BINARY_ADD)]   # the full-shape add
 
 
 def test_layer_norm_output_read_elsewhere_keeps_mish_separate():
     g = C.Graph()
     causal_block_tail(g, extra_reader=True)
-    assert g.plan() == [(C.GL_LAYER_NORM, 0, 3, 0), (C.GL_UNARY, 3, 3, 0), (C.GL_UNSUPPORTED, 6, 1, 0),
+    assert g.plan() == [(C.GL_LAYER_NORM, 0, 3, 0), (C.GL_UNARY, 3, 3, 0), (C.GL_BINARY, 6, 1, C.BINARY_MUL),
                         (C.GL_UNARY, 7, 1, 0)]
 
 
@@ -267,8 +267,8 @@ def test_shape_mismatch_is_not_a_layer_norm():
     g.node(C.GOP_NORM, n, (x,), fparam=1e-5)
     g.node(C.GOP_MUL, m, (n, w))
     g.node(C.GOP_ADD, y, (m, b))
-    # the norm alone, the full-shape multiply not this library's, the bias add alone
-    assert [p[0] for p in g.plan()] == [C.GL_NORM, C.GL_UNSUPPORTED, C.GL_BIAS_ACT]
+    # the norm alone, the full-shape multiply alone, the bias add alone
+    assert [p[0] for p in g.plan()] == [C.GL_NORM, C.GL_BINARY, C.GL_BIAS_ACT]
 
 
 def test_snake_chain():
@@ -283,9 +283,9 @@ def test_snake_chain():
     g.node(C.GOP_MUL, t[3], (t[2], ai))
     g.node(C.GOP_ADD, t[4], (x, t[3]))
     assert g.plan() == [(C.GL_SNAKE, 0, 5, 0)]
-    # the same nodes with the sin result kept: five separate nodes, two of them not runnable alone
-    assert [p[0] for p in g.plan(keep=[t[1]])] == [C.GL_UNSUPPORTED, C.GL_UNARY, C.GL_UNARY, C.GL_UNSUPPORTED,
-                                                    C.GL_UNSUPPORTED]
+    # the same nodes with the sin result kept: five separate launches
+    assert [p[0] for p in g.plan(keep=[t[1]])] == [C.GL_BINARY, C.GL_UNARY, C.GL_UNARY, C.GL_BINARY,
+                                                    C.GL_BINARY]
 
 
 @pytest.mark.parametrize("with_mask", [True, False])
@@ -413,12 +413,13 @@ def test_compute_refuses_unsupported_before_any_launch():
     the call before the device is touched (this runs without a GPU)."""
     L = C.load()
     g = C.Graph()
-    t3_input(g)
+    t = t3_input(g)
+    g.node(99, g.tensor(f32(6, 64)), (t[8],))     # a matmul (op 99 stands in): not this library's
     T, N, K = _raw(g)
     n = ctypes.c_int32(-1)
     rc = L.cbx_graph_compute(T, len(g._descs), N, len(g.nodes), K, 0, None, ctypes.byref(n))
     assert rc == C.ERR_UNSUPPORTED and n.value == 0
-    assert "node 8 (ADD)" in C.last_error()
+    assert "node 9 (unknown op)" in C.last_error()
 
 
 def test_graph_exec_argument_errors():
@@ -470,7 +471,8 @@ def test_random_lists_plan_into_an_exact_cover():
              C.GL_SOFT_MAX: {1, 2, 3}, C.GL_SNAKE: {5}, C.GL_UNARY: {1, 3}, C.GL_SWIGLU: {2},
              C.GL_LEAKY_RELU: {1}, C.GL_ROPE: {1}, C.GL_CPY: {1}, C.GL_ADD_LAYER_NORM: {4, 5, 7, 8},
              C.GL_LAYER_NORM_MASK: {4, 7}, C.GL_BIAS_ACT: {1, 2, 4}, C.GL_CONV1D: set(range(9, 18)),
-             C.GL_CONV_TRANSPOSE1D: set(range(7, 15)), C.GL_CAUSAL_CONV1D: set(range(12, 16))}
+             C.GL_CONV_TRANSPOSE1D: set(range(7, 15)), C.GL_CAUSAL_CONV1D: set(range(12, 16)),
+             C.GL_BINARY: {1}, C.GL_CONCAT: {1}}
     shapes = [(4, 8), (8,), (1, 8, 1, 1), (4, 8), (4, 1)]
     for trial in range(200):
         g = C.Graph()
@@ -681,7 +683,7 @@ def test_causal_conv_forms():
     x = h.t(f32(40, 16))
     m = h.t(f32(40, 16))
     h.causal_conv1d(h.mul(x, m), h.t(torch.zeros(24, 16, 3)), None, DUMMY_W)
-    assert h.g.plan()[:2] == [(C.GL_UNSUPPORTED, 0, 1, 0), (C.GL_CAUSAL_CONV1D, 1, 12, 0)]
+    assert h.g.plan()[:2] == [(C.GL_BINARY, 0, 1, C.BINARY_MUL), (C.GL_CAUSAL_CONV1D, 1, 12, 0)]
 
 
 def test_mutated_conv_chains_plan_into_an_exact_cover():
