@@ -821,7 +821,7 @@ def estimator_bytes(C, e, plan):
 
 
 def bench_cfm_estimator(C, torch, T=500, reps=20):
-    """One CFM estimator call's element-wise nodes (cfm_decoder.cpp:395-565:
+    """One CFM estimator call's element-wise nodes (cfm_decoder.cpp:395-558:
     14 resnet blocks with their 29 causal blocks, 56 transformer blocks; the
     matmul outputs given, the causal convs on the library's conv kernel) at
     the reference's sizes over T frames, planned into one list of launches
@@ -842,7 +842,7 @@ def bench_cfm_estimator(C, torch, T=500, reps=20):
         for p in plan:
             if p[0] != C.GL_VIEW:
                 kinds[names[p[0]]] = kinds.get(names[p[0]], 0) + 1
-        out = {"reference_sequence": f"cfm_decoder.cpp:395-565, T_mel {T}, 14 resnet blocks, 56 transformer blocks",
+        out = {"reference_sequence": f"cfm_decoder.cpp:395-558, T_mel {T}, 14 resnet blocks, 56 transformer blocks",
                "launches": ex.n_launches, "launches_by_kind": kinds, "bytes_per_call": nbytes}
         for _ in range(3):
             ex.launch(s)

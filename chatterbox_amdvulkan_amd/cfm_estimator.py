@@ -1,6 +1,6 @@
 """The element-wise nodes of one CFM estimator call -- the flow decoder's
 U-Net, CFMDecoder::estimator_forward_with_stages
-(chatterbox-cpp/src/cfm_decoder.cpp:395-565) -- as that builder emits them,
+(chatterbox-cpp/src/cfm_decoder.cpp:395-558) -- as that builder emits them,
 each matmul's output given as a device tensor and the causal convs run by
 the library: the caller-side list that libcbxops' node-list executor
 (cbx_graph_*) plans and runs, once per flow step.
@@ -8,25 +8,25 @@ the library: the caller-side list that libcbxops' node-list executor
 Per call the reference builds (ggml node order; matmuls left out, [..] the
 given outputs):
   time embedding, for t and r: [l1] add(b) -> silu, [l2] add(b); concat
-    (the mixer's input)                                        (:452-464)
-  pack: concat(x, mu), concat(., spks), concat(., cond)        (:486-492)
+    (the mixer's input)                                        (:463-477)
+  pack: concat(x, mu), concat(., spks), concat(., cond)        (:480-491)
   down: resnet 320 -> 256, n_tr transformers, mul(h, mask) -> causal conv
-                                                               (:497-516)
-  mid, n_mid times: resnet 256 -> 256, n_tr transformers       (:519-530)
+                                                               (:494-513)
+  mid, n_mid times: resnet 256 -> 256, n_tr transformers       (:515-526)
   up: concat(h, skip), resnet 512 -> 256, n_tr transformers, mul(h, mask)
-    -> causal conv                                             (:534-553)
+    -> causal conv                                             (:528-544)
   final: causal_block1d, mul(h, mask) -> [final_proj] add(b) -> mul(mask)
-                                                               (:556-565)
-  resnet (causal_resnet_block1d, :152-182): causal_block1d, mish(t_mix) ->
+                                                               (:546-557)
+  resnet (causal_resnet_block1d, :152-179): causal_block1d, mish(t_mix) ->
     [mlp] add(b) -> add(h, .), causal_block1d, mul(x, mask) -> [res_conv]
     add(b) -> add(h, .)
-  transformer (basic_transformer_block, :194-263): layer_norm -> [q, k, v,
+  transformer (basic_transformer_block, :190-245): layer_norm -> [q, k, v,
     scores] scale -> soft_max -> [attn, to_out] add(b) -> add(x, .) ->
     layer_norm -> [ff.0] add(b) -> gelu_erf -> [ff.2] add(b) -> add(x, .)
   causal_block1d (:133-149): mul(x, mask) -> causal conv (+ bias) ->
     layer_norm -> mish -> mul(mask)
 
-The repeat of spks over the frames (ggml_repeat, :482-484) is given: the
+The repeat of spks over the frames (ggml_repeat, :482-485) is given: the
 library has no repeat.  With the reference's sizes (n_mid 12, n_tr 4) a
 call holds 14 resnet blocks (29 causal_block1d with the final block) and 56
 transformer blocks (112 LayerNorms, 56 bias + gelu_erf).

@@ -3,15 +3,15 @@
 //
 // Binary: y[i0,i1,i2,i3] = a[i0,i1,i2,i3] op b[i0 % b.ne0, i1 % b.ne1,
 // i2 % b.ne2, i3 % b.ne3] (ggml_can_repeat(b, a)), one f32 rounding -- the
-// CFM decoder's mul(x, mask) of every (C, T) tensor by its per-frame mask
-// (cfm_decoder.cpp:139,148,182,554-557) and the residual joins that no
-// LayerNorm follows (cfm_decoder.cpp:183,287).  Contiguous tensors with b
+// CFM decoder's mul(x, mask) of a (C, T) tensor by its per-frame mask
+// before the 1x1 convs and around final_proj (cfm_decoder.cpp:176,553,555)
+// and the residual join that ends a transformer stack (:244).  Contiguous tensors with b
 // the same shape, a repeated row of ne0 values, or one value per row take
 // one 4-element vector per lane over a grid that covers a once; other
 // layouts take a workgroup per row.
 //
 // Concat: y = ggml_concat(a, b, dim) -- the decoder's channel packing and
-// skip join (cfm_decoder.cpp:486-492,536).  A workgroup per output row.
+// skip join (cfm_decoder.cpp:489-491,530), the time embeddings (:476).  A workgroup per output row.
 #include <type_traits>
 
 #include "cbx_internal.h"

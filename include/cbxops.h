@@ -335,8 +335,8 @@ int cbx_bias_act(int act, const cbx_tensor* x, const cbx_tensor* bias,
 /* ggml_add(a, b) / ggml_mul(a, b) with b repeated to a's shape
  * (ggml_can_repeat(b, a): every a.ne[i] a multiple of b.ne[i]): y = a + b or
  * a * b, one f32 rounding.  The CFM decoder's mul(x, mask (1, T)) before its
- * 1x1 convs and after final_proj (cfm_decoder.cpp:182,554-557) and the
- * residual joins no LayerNorm follows (:183,287).  F32; a, y the same shape,
+ * 1x1 convs and around final_proj (cfm_decoder.cpp:176,553,555) and the
+ * residual join that ends a transformer stack (:244).  F32; a, y the same shape,
  * any strides (nb[0] the element size); y may be a itself, and must not
  * overlap b.                                                              */
 typedef enum {
@@ -347,8 +347,9 @@ int cbx_binary(int op, const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y,
                cbx_stream stream);
 
 /* ggml_concat(a, b, dim): y.ne[dim] = a.ne[dim] + b.ne[dim], the other
- * dims equal to a's and b's; a's elements first (cfm_decoder.cpp:486-492
- * packing x, mu, spks, cond along the channels; :536 the skip join).  F32
+ * dims equal to a's and b's; a's elements first (cfm_decoder.cpp:489-491
+ * packing x, mu, spks, cond along the channels; :530 the skip join; :476
+ * the time embeddings).  F32
  * or F16 (all three the same type), any strides; y must not overlap a or b.
  * dim 0..3.                                                               */
 int cbx_concat(const cbx_tensor* a, const cbx_tensor* b, int dim, cbx_tensor* y,

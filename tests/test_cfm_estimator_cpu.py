@@ -1,4 +1,4 @@
-"""The CFM estimator's node list (cfm_decoder.cpp:395-565, matmul outputs
+"""The CFM estimator's node list (cfm_decoder.cpp:395-558, matmul outputs
 given) planned on the host: every node claimed, and the launches the
 reference's structure implies for n_mid mid blocks and n_tr transformers a
 stage."""

@@ -1,4 +1,4 @@
-"""One CFM estimator call's element-wise node list (cfm_decoder.cpp:395-565,
+"""One CFM estimator call's element-wise node list (cfm_decoder.cpp:395-558,
 matmul outputs given; chatterbox_amdvulkan_amd/cfm_estimator.py) run launch
 by launch, each launch checked against the oracle on the inputs it read
 from the device: bit-exact for the adds, muls, concats and LayerNorms; the
