@@ -833,12 +833,13 @@ void conv_tile(int t, int ks, bool vec, bool pf4, dim3 grid, size_t lds, hipStre
         case 5: conv_ks<PRO, 3, 2, 1, 2, 2>(ks, vec, pf4, grid, lds, s, a); break;   // 96 x 128
         case 6: conv_ks<PRO, 3, 2, 2, 1, 2>(ks, vec, pf4, grid, lds, s, a); break;   // 192 x 64
         case 7: conv_ks<PRO, 3, 2, 1, 1, 4>(ks, vec, pf4, grid, lds, s, a); break;   // 96 x 64
-        default: conv_ks<PRO, 1, 2, 1, 1, 4>(ks, vec, pf4, grid, lds, s, a); break;  // 32 x 64
+        case 8: conv_ks<PRO, 1, 2, 1, 1, 4>(ks, vec, pf4, grid, lds, s, a); break;   // 32 x 64
+        default: conv_ks<PRO, 1, 1, 1, 1, 4>(ks, vec, pf4, grid, lds, s, a); break;  // 32 x 32
     }
 }
 
-constexpr Tile kTiles[9] = {{4, 2, 2, 1, 2}, {4, 2, 1, 2, 2}, {2, 2, 1, 2, 2}, {2, 2, 1, 1, 4}, {4, 1, 2, 1, 2},
-                            {3, 2, 1, 2, 2}, {3, 2, 2, 1, 2}, {3, 2, 1, 1, 4}, {1, 2, 1, 1, 4}};
+constexpr Tile kTiles[10] = {{4, 2, 2, 1, 2}, {4, 2, 1, 2, 2}, {2, 2, 1, 2, 2}, {2, 2, 1, 1, 4}, {4, 1, 2, 1, 2},
+                             {3, 2, 1, 2, 2}, {3, 2, 2, 1, 2}, {3, 2, 1, 1, 4}, {1, 2, 1, 1, 4}, {1, 1, 1, 1, 4}};
 
 }  // namespace
 
@@ -1000,6 +1001,12 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
             }
         }
     }
+    // 32 x 64 tiles that leave CUs without a workgroup (the CFM decoder's
+    // causal convs on 500 frames: 64 or 128 of them) split each tile's
+    // channels in two: [2,256,500] -> 256 6.86 against 7.6 us, [2,512,500]
+    // 9.35 against 10.3 us; where 32 x 64 tiles fill the CUs the narrower
+    // ones are slower (256 x 6000 K11 45 against 27.5 us)
+    if (ti == 8 && n_wg(kTiles[8]) < st->n_cu) ti = 9;
     if (!fits(win_of(kTiles[ti]))) ti = 3;
     const int64_t win = win_of(kTiles[ti]);
     if (!fits(win)) {
