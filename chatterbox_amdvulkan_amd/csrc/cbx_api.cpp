@@ -1652,6 +1652,36 @@ extern "C" int cbx_binary(int op, const cbx_tensor* a, const cbx_tensor* b, cbx_
     return launch_binary(op, a, b, y, reinterpret_cast<hipStream_t>(stream));
 }
 
+extern "C" int cbx_bias_residual(const cbx_tensor* x, const cbx_tensor* bias, const cbx_tensor* r, cbx_tensor* y,
+                                 cbx_stream stream) {
+    const char* what = "cbx_bias_residual";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(x, what, "x")) || (rc = validate(bias, what, "bias")) || (rc = validate(r, what, "r")) ||
+        (rc = validate(y, what, "y"))) {
+        return rc;
+    }
+    if (x->type != CBX_TYPE_F32 || bias->type != CBX_TYPE_F32 || r->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32) {
+        return set_error(CBX_ERR_UNSUPPORTED, "cbx_bias_residual: F32 only");
+    }
+    if (!same_shape(r, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_bias_residual: r and y shapes differ");
+    if (nelements(r) == 0) return CBX_OK;
+    for (int k = 0; k < 4; k++) {
+        if (x->ne[k] < 1 || r->ne[k] % x->ne[k] != 0 || bias->ne[k] < 1 || x->ne[k] % bias->ne[k] != 0) {
+            return set_error(CBX_ERR_INVALID_ARG,
+                             "cbx_bias_residual: bias must repeat to x's shape and x to r's (every ne[i] a multiple)");
+        }
+    }
+    if (overlaps(y, bias) || (overlaps(y, r) && !same_view(y, r)) ||
+        (overlaps(y, x) && !(same_shape(x, r) && same_view(y, x)))) {
+        return set_error(CBX_ERR_INVALID_ARG,
+                         "cbx_bias_residual: y overlaps bias, r other than as r itself, or x other than as x itself");
+    }
+    return launch_bias_residual(x, bias, r, y, reinterpret_cast<hipStream_t>(stream));
+}
+
 extern "C" int cbx_concat(const cbx_tensor* a, const cbx_tensor* b, int dim, cbx_tensor* y, cbx_stream stream) {
     const char* what = "cbx_concat";
     clear_error();

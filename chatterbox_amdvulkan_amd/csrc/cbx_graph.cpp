@@ -180,6 +180,28 @@ struct Planner {
         return true;
     }
 
+    // v views the whole of p unchanged: same data, dims and (contiguous) layout
+    bool alias(int32_t v, int32_t p) const {
+        return same_dims(v, p) && t[v].data == t[p].data && t[v].type == t[p].type && is_contiguous(&t[v]) &&
+               is_contiguous(&t[p]);
+    }
+
+    // add(x, bias) [-> view (an alias of the sum)] -> add(r, .) at node i,
+    // bias repeating to x and x to r: the node count (2 or 3), or 0
+    int32_t bias_residual_at(int32_t i) const {
+        if (!is(i, CBX_GOP_ADD)) return 0;
+        const int32_t x = nd[i].src[0], t1 = nd[i].dst;
+        if (!repeats(nd[i].src[1], x) || !same_dims(t1, x) || !internal(t1, 1)) return 0;
+        int32_t k = i + 1, sum = t1;
+        if (is(k, CBX_GOP_VIEW) && nd[k].src[0] == t1) {
+            if (!alias(nd[k].dst, t1) || !internal(nd[k].dst, 1)) return 0;
+            sum = nd[k++].dst;
+        }
+        if (!is(k, CBX_GOP_ADD)) return 0;
+        const int32_t r = nd[k].src[0] == sum ? nd[k].src[1] : nd[k].src[1] == sum ? nd[k].src[0] : -1;
+        return r >= 0 && r != sum && repeats(sum, r) && same_dims(nd[k].dst, r) ? k + 1 - i : 0;
+    }
+
     // layer_norm at node i reading `in`, optionally followed by a mish
     // chain: the node count (3 or 6), or 0
     int32_t layer_norm_mish_at(int32_t i, int32_t in) const {
@@ -464,6 +486,11 @@ struct Planner {
                         return CBX_GL_ADD_LAYER_NORM;
                     }
                 }
+                // bias add [-> view] -> residual add with no norm after it
+                if (const int32_t l = bias_residual_at(i)) {
+                    *len = l;
+                    return CBX_GL_BIAS_RESIDUAL;
+                }
                 // residual add -> layer_norm [-> mish]
                 if (same_dims(a.src[1], x)) {
                     const int32_t l = layer_norm_mish_at(i + 1, t1);
@@ -694,8 +721,9 @@ constexpr int32_t kSpan[][2] = {
     {7, 12},  // GET_ROWS_CONCAT_ADD_LAYER_NORM [prompt gather, concat] [casts]
     {1, 1},  // BINARY
     {1, 1},  // CONCAT
+    {2, 3},  // BIAS_RESIDUAL [view]
 };
-constexpr int32_t kLastKind = CBX_GL_CONCAT;
+constexpr int32_t kLastKind = CBX_GL_BIAS_RESIDUAL;
 static_assert(sizeof(kSpan) / sizeof(kSpan[0]) == kLastKind + 1, "one span per launch kind");
 
 // Issues the entry point a launch maps to.  A launch is only read within
@@ -806,6 +834,22 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
         case CBX_GL_BINARY:
             if (a.op != (l.flags == CBX_BINARY_MUL ? CBX_GOP_MUL : CBX_GOP_ADD)) break;
             return cbx_binary(l.flags, T(t, a.src[0]), T(t, a.src[1]), y, s);
+        case CBX_GL_BIAS_RESIDUAL: {
+            const cbx_gnode& last = nd[f + l.n_nodes - 1];
+            int32_t sum = a.dst;
+            if (l.n_nodes == 3) {
+                const cbx_gnode& v = nd[f + 1];
+                if (v.op != CBX_GOP_VIEW || v.src[0] != a.dst || v.dst < 0 || a.dst < 0 ||
+                    t[v.dst].data != t[a.dst].data || !same_shape(&t[v.dst], &t[a.dst]) ||
+                    !is_contiguous(&t[v.dst]) || !is_contiguous(&t[a.dst])) {
+                    break;
+                }
+                sum = v.dst;
+            }
+            const int32_t r = last.src[0] == sum ? last.src[1] : last.src[1] == sum ? last.src[0] : -1;
+            if (a.op != CBX_GOP_ADD || last.op != CBX_GOP_ADD || r < 0) break;
+            return cbx_bias_residual(T(t, a.src[0]), T(t, a.src[1]), T(t, r), y, s);
+        }
         case CBX_GL_CONCAT:
             return cbx_concat(T(t, a.src[0]), T(t, a.src[1]), a.iparam, y, s);
         case CBX_GL_ADD_LAYER_NORM: {

@@ -10,6 +10,11 @@
 // one 4-element vector per lane over a grid that covers a once; other
 // layouts take a workgroup per row.
 //
+// Bias + residual: y = r + (x + bias), the inner add rounded first -- a
+// projection's bias add joined to the residual it feeds when no norm
+// follows (cfm_decoder.cpp:162-165 the time MLP broadcast over the frames,
+// :242-244 a stack's last ff.2).  Same two forms as the binary ops.
+//
 // Concat: y = ggml_concat(a, b, dim) -- the decoder's channel packing and
 // skip join (cfm_decoder.cpp:489-491,530), the time embeddings (:476).  A workgroup per output row.
 #include <type_traits>
@@ -70,6 +75,53 @@ __global__ __launch_bounds__(kThreads) void k_binary_rows(View a, View b, View y
             const float x = *reinterpret_cast<const float*>(ar + j * a.nb[0]);
             const float v = *reinterpret_cast<const float*>(br + (j % b.ne[0]) * b.nb[0]);
             *reinterpret_cast<float*>(yr + j * y.nb[0]) = bin<OP>(x, v);
+        }
+    }
+}
+
+// one 4-element vector of an operand with r's shape (BIN_SAME) or of one
+// repeated row of ne0 values (BIN_ROW)
+template <int MODE>
+__device__ __forceinline__ float4 load_rep(const float* __restrict__ p, uint32_t i, uint32_t ne0_4) {
+    if constexpr (MODE == BIN_SAME) return *reinterpret_cast<const float4*>(p + 4ull * i);
+    else return *reinterpret_cast<const float4*>(p + 4u * (i % ne0_4));
+}
+
+// y = r + (x + bias) over contiguous r and y; XM, BM: the modes of x and bias
+template <int XM, int BM>
+__global__ __launch_bounds__(kThreads) void k_bias_residual_flat(const float* __restrict__ x,
+                                                                 const float* __restrict__ b,
+                                                                 const float* __restrict__ r, float* __restrict__ y,
+                                                                 uint32_t n4, uint32_t ne0_4) {
+    arg_now(x);
+    arg_now(b);
+    arg_now(r);
+    arg_now(y);
+    const uint32_t iu = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t i = iu < n4 ? iu : n4 - 1;
+    const float4 xv = load_rep<XM>(x, i, ne0_4), bv = load_rep<BM>(b, i, ne0_4);
+    const float4 rv = *reinterpret_cast<const float4*>(r + 4ull * i);
+    const float4 o = make_float4(rv.x + (xv.x + bv.x), rv.y + (xv.y + bv.y), rv.z + (xv.z + bv.z),
+                                 rv.w + (xv.w + bv.w));
+    if (iu < n4) *reinterpret_cast<float4*>(y + 4ull * i) = o;
+}
+
+// Any strides: rows of r (and y) enumerate ne1, ne2, ne3; x's and bias's
+// rows are the repeats of the same indices (bias repeats to x and x to r,
+// so i mod bias.ne = (i mod x.ne) mod bias.ne)
+__global__ __launch_bounds__(kThreads) void k_bias_residual_rows(View x, View b, View r, View y, int64_t nr) {
+    for (int64_t q = blockIdx.x; q < nr; q += gridDim.x) {
+        const int64_t i1 = q % r.ne[1], u = q / r.ne[1];
+        const int64_t i2 = u % r.ne[2], i3 = u / r.ne[2];
+        const char* rr = r.data + i1 * r.nb[1] + i2 * r.nb[2] + i3 * r.nb[3];
+        char* yr = y.data + i1 * y.nb[1] + i2 * y.nb[2] + i3 * y.nb[3];
+        const char* xr = x.data + (i1 % x.ne[1]) * x.nb[1] + (i2 % x.ne[2]) * x.nb[2] + (i3 % x.ne[3]) * x.nb[3];
+        const char* br = b.data + (i1 % b.ne[1]) * b.nb[1] + (i2 % b.ne[2]) * b.nb[2] + (i3 % b.ne[3]) * b.nb[3];
+        for (int64_t j = threadIdx.x; j < r.ne[0]; j += kThreads) {
+            const float xv = *reinterpret_cast<const float*>(xr + (j % x.ne[0]) * x.nb[0]);
+            const float bv = *reinterpret_cast<const float*>(br + (j % b.ne[0]) * b.nb[0]);
+            const float rv = *reinterpret_cast<const float*>(rr + j * r.nb[0]);
+            *reinterpret_cast<float*>(yr + j * y.nb[0]) = rv + (xv + bv);
         }
     }
 }
@@ -140,7 +192,45 @@ void binary_go(const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y, hipStrea
                        dim3(kThreads), 0, s, view_of(a), view_of(b), view_of(y), nr);
 }
 
+// x or bias as a flat operand of r's shape: 0 the same shape, 1 one row, -1 neither
+int flat_mode(const cbx_tensor* p, const cbx_tensor* r) {
+    if (!is_contiguous(p) || !al16(p->data)) return -1;
+    if (same_shape(p, r)) return BIN_SAME;
+    if (p->ne[0] == r->ne[0] && p->ne[1] == 1 && p->ne[2] == 1 && p->ne[3] == 1) return BIN_ROW;
+    return -1;
+}
+
 }  // namespace
+
+int launch_bias_residual(const cbx_tensor* x, const cbx_tensor* bias, const cbx_tensor* r, cbx_tensor* y,
+                         hipStream_t s) {
+    const int64_t n = nelements(r);
+    const int xm = flat_mode(x, r), bm = flat_mode(bias, r);
+    if (xm >= 0 && bm >= 0 && is_contiguous(r) && is_contiguous(y) && al16(r->data) && al16(y->data) &&
+        r->ne[0] % 4 == 0 && n / 4 < (int64_t{1} << 31)) {
+        const uint32_t n4 = static_cast<uint32_t>(n / 4), ne0_4 = static_cast<uint32_t>(r->ne[0] / 4);
+        const dim3 grid(static_cast<unsigned>(cdiv(n4, kThreads)));
+        const float* xp = static_cast<const float*>(x->data);
+        const float* bp = static_cast<const float*>(bias->data);
+        const float* rp = static_cast<const float*>(r->data);
+        float* yp = static_cast<float*>(y->data);
+        if (xm == BIN_SAME && bm == BIN_SAME) {
+            hipLaunchKernelGGL((k_bias_residual_flat<BIN_SAME, BIN_SAME>), grid, dim3(kThreads), 0, s, xp, bp, rp, yp,
+                               n4, ne0_4);
+        } else if (xm == BIN_SAME) {
+            hipLaunchKernelGGL((k_bias_residual_flat<BIN_SAME, BIN_ROW>), grid, dim3(kThreads), 0, s, xp, bp, rp, yp,
+                               n4, ne0_4);
+        } else {   // x one row: bias, repeating to it, is one row too
+            hipLaunchKernelGGL((k_bias_residual_flat<BIN_ROW, BIN_ROW>), grid, dim3(kThreads), 0, s, xp, bp, rp, yp,
+                               n4, ne0_4);
+        }
+    } else {
+        const int64_t nr = nrows(r);
+        hipLaunchKernelGGL(k_bias_residual_rows, dim3(static_cast<unsigned>(std::min<int64_t>(nr, int64_t{1} << 20))),
+                           dim3(kThreads), 0, s, view_of(x), view_of(bias), view_of(r), view_of(y), nr);
+    }
+    return check_launch("bias residual");
+}
 
 int launch_binary(int op, const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y, hipStream_t s) {
     if (op == CBX_BINARY_ADD) binary_go<CBX_BINARY_ADD>(a, b, y, s);

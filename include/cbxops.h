@@ -346,6 +346,17 @@ typedef enum {
 int cbx_binary(int op, const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y,
                cbx_stream stream);
 
+/* ggml_add(r, ggml_add(x, bias)) in one pass: y = r + (x + bias), each add
+ * one f32 rounding, the inner one first.  bias repeats to x's shape and x
+ * to r's (ggml_can_repeat).  The projections whose biased output joins a
+ * residual with no norm between: a transformer stack's last ff.2
+ * (cfm_decoder.cpp:242-244) and a resnet's time MLP, its (C_out) output
+ * broadcast over the frames (:162-165).  F32, any strides (nb[0] the
+ * element size); y the shape of r and may be r itself (or x, when x has
+ * r's shape); y must not overlap bias.                                    */
+int cbx_bias_residual(const cbx_tensor* x, const cbx_tensor* bias, const cbx_tensor* r,
+                      cbx_tensor* y, cbx_stream stream);
+
 /* ggml_concat(a, b, dim): y.ne[dim] = a.ne[dim] + b.ne[dim], the other
  * dims equal to a's and b's; a's elements first (cfm_decoder.cpp:489-491
  * packing x, mu, spks, cond along the channels; :530 the skip join; :476
@@ -669,6 +680,8 @@ typedef enum cbx_glaunch_kind {
                                  first's shape (cbx_binary): a per-frame mask, a
                                  residual join no norm follows. flags: the op   */
     CBX_GL_CONCAT,            /* one concat (cbx_concat)                        */
+    CBX_GL_BIAS_RESIDUAL,     /* add(x, bias) [-> view (same dims)] -> add(r, .)
+                                 with no norm after it (cbx_bias_residual)      */
 } cbx_glaunch_kind;
 
 typedef struct cbx_glaunch {

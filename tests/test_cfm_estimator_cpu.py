@@ -23,16 +23,17 @@ def test_plan_counts(T, n_mid, n_tr):
         "GL_LAYER_NORM_MASK": 2 * n_res + 1,    # the causal blocks' LN -> Mish -> mask
         "GL_SOFT_MAX": n_t,                     # scale -> soft_max
         "GL_ADD_LAYER_NORM": 2 * n_t,           # every transformer LayerNorm, joined to its residual
-        # gelu_erf per transformer; t and r time MLPs (bias + silu, bias); the
-        # mlp bias and its broadcast add a resnet; the last ff.2 bias of a
-        # stack (no norm follows); final_proj's bias
-        "GL_BIAS_ACT": n_t + 4 + 2 * n_res + n_res + 1,
-        # mul(x, mask) before each res_conv; the residual a stack ends with;
-        # mul(h, mask) before final_proj and after it
-        "GL_BINARY": n_res + n_res + 2,
+        # gelu_erf per transformer; t and r time MLPs (bias + silu, bias);
+        # final_proj's bias
+        "GL_BIAS_ACT": n_t + 4 + 1,
+        # mul(x, mask) before each res_conv; mul(h, mask) before final_proj
+        # and after it
+        "GL_BINARY": n_res + 2,
+        # a resnet's mlp bias -> (C, 1) view -> add over the frames; a
+        # stack's last ff.2 bias -> residual add (no norm follows)
+        "GL_BIAS_RESIDUAL": 2 * n_res,
         "GL_UNARY": n_res,                      # mish(t_mix) in every resnet
         "GL_CONCAT": 5,                         # t|r, the three packing concats, the skip join
-        "GL_VIEW": n_res,                       # the mlp output reshaped to (C, 1)
     }
     assert dict(got) == exp
     assert sum(p[2] for p in plan) == len(e.graph.nodes)
@@ -40,3 +41,8 @@ def test_plan_counts(T, n_mid, n_tr):
         if kind == C.GL_BINARY:
             op = e.graph.nodes[first].op
             assert flags == (C.BINARY_MUL if op == C.GOP_MUL else C.BINARY_ADD)
+        if kind == C.GL_BIAS_RESIDUAL:
+            assert n == (3 if e.graph.nodes[first + 1].op == C.GOP_VIEW else 2)
+    # the kernel launches at the reference's sizes
+    if (T, n_mid, n_tr) == (500, 12, 4):
+        assert sum(1 for p in plan if p[0] != C.GL_VIEW) == 352

@@ -1,5 +1,6 @@
-"""cbx_binary (ggml_add / ggml_mul with the second operand repeated) and
-cbx_concat (ggml_concat) against the oracle's add / mul (ggml's repeat by
+"""cbx_binary (ggml_add / ggml_mul with the second operand repeated),
+cbx_bias_residual (two ggml_adds in one pass) and cbx_concat (ggml_concat)
+against the oracle's add / mul (ggml's repeat by
 index) and numpy's concatenate: one f32 rounding per element, so bit-exact;
 a concat is a copy."""
 import numpy as np
@@ -73,6 +74,67 @@ def test_binary_refusals(cbx):
         cbx.binary(cbx.BINARY_ADD, a, a[:, :5], out=a)                          # y overlaps b
     with pytest.raises(cbx.CbxError):
         cbx.binary(cbx.BINARY_ADD, a.half(), torch.zeros((10,), device="cuda").half())   # F32 only
+
+
+# torch shapes: r, x repeating into r, bias repeating into x
+BIAS_RESIDUAL = [
+    ((500, 256), (500, 256), (256,)),     # a stack's last ff.2 output, its bias, the residual stream
+    ((500, 256), (256,), (256,)),         # the time MLP's output broadcast over the frames
+    ((500, 256), (1, 256), (256,)),
+    ((2, 40, 12), (40, 12), (12,)),       # repeated over a batch
+    ((7, 13), (7, 13), (1, 13)),          # odd widths (the row path)
+    ((6, 12), (12,), (4,)),               # a bias shorter than x's row
+    ((3, 8, 16), (1, 8, 1), (1, 1, 1)),
+]
+
+
+@pytest.mark.parametrize("sr,sx,sb", BIAS_RESIDUAL)
+def test_bias_residual_shapes(cbx, oracle, sr, sx, sb):
+    """r + (x + bias), the inner add rounded first: the two ggml adds the
+    oracle runs one after the other."""
+    r = W.normal(W.seed_of(46, len(sr)), sr, 0.0, 4.0)
+    x = W.normal(W.seed_of(47, len(sx)), sx, 0.0, 3.0)
+    b = W.normal(W.seed_of(48, len(sb)), sb, 0.5, 1.0)
+    got = host(cbx.bias_residual(dev(x), dev(b), dev(r)))
+    assert_bitexact(got, oracle.add(r, oracle.add(x, b)), f"{sr} {sx} {sb}")
+
+
+def test_bias_residual_views_and_in_place(cbx, oracle):
+    """Strided operands, y == r and y == x."""
+    rb = W.normal(W.seed_of(49, 0), (60, 50), 0.0, 2.0)
+    xb = W.normal(W.seed_of(49, 1), (60, 44), 0.0, 2.0)
+    b = W.normal(W.seed_of(49, 2), (40,), 0.0, 1.0)
+    yb = torch.full((60, 64), float("nan"), device="cuda")
+    y = yb[:, 8:48]
+    cbx.bias_residual(dev(xb)[:, 2:42], dev(b), dev(rb)[:, 5:45], out=y)
+    exp = oracle.add(np.ascontiguousarray(rb[:, 5:45]), oracle.add(np.ascontiguousarray(xb[:, 2:42]), b))
+    assert_bitexact(host(y), exp, "strided")
+    assert np.isnan(host(yb)[:, :8]).all() and np.isnan(host(yb)[:, 48:]).all(), "only y's columns written"
+    r = W.normal(W.seed_of(49, 3), (64, 40), 0.0, 2.0)
+    x = W.normal(W.seed_of(49, 4), (64, 40), 0.0, 2.0)
+    exp = oracle.add(r, oracle.add(x, b))
+    t = dev(r)
+    cbx.bias_residual(dev(x), dev(b), t, out=t)
+    assert_bitexact(host(t), exp, "y is r")
+    t = dev(x)
+    cbx.bias_residual(t, dev(b), dev(r), out=t)
+    assert_bitexact(host(t), exp, "y is x")
+
+
+def test_bias_residual_refusals(cbx):
+    r = torch.zeros((6, 12), device="cuda")
+    b = torch.zeros((12,), device="cuda")
+    with pytest.raises(cbx.CbxError):
+        cbx.bias_residual(torch.zeros((6, 5), device="cuda"), torch.zeros((5,), device="cuda"), r)   # 12 % 5
+    with pytest.raises(cbx.CbxError):
+        cbx.bias_residual(torch.zeros((12,), device="cuda"), torch.zeros((6, 12), device="cuda"), r)  # bias into x
+    with pytest.raises(cbx.CbxError):
+        cbx.bias_residual(r, r[0], r, out=r)                                      # y overlaps bias
+    x = torch.zeros((12,), device="cuda")
+    with pytest.raises(cbx.CbxError):
+        cbx.bias_residual(x, b, r, out=torch.zeros((6, 10), device="cuda"))       # y not r's shape
+    with pytest.raises(cbx.CbxError):
+        cbx.bias_residual(x.half(), b.half(), r.half())                           # F32 only
 
 
 @pytest.mark.parametrize("dim", [0, 1, 2, 3])

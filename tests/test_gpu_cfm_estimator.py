@@ -54,6 +54,12 @@ def check_launch(e, oracle, launch, k):
         a, b = H(nd[f].src[0]), H(nd[f].src[1])
         exp = oracle.mul(a, b) if flags == C.BINARY_MUL else oracle.add(a, b)
         assert_bitexact(H(y), exp, what)
+    elif kind == C.GL_BIAS_RESIDUAL:
+        last = nd[f + n - 1]
+        s = nd[f + n - 2].dst                     # the bias sum, or its (C, 1) view
+        r = last.src[1] if last.src[0] == s else last.src[0]
+        exp = oracle.add(H(r), oracle.add(H(nd[f].src[0]), H(nd[f].src[1])))
+        assert_bitexact(H(y), exp, what)
     elif kind == C.GL_CONCAT:
         a, b = H(nd[f].src[0]), H(nd[f].src[1])
         assert_bitexact(H(y), np.concatenate((a, b), axis=a.ndim - 1 - nd[f].iparam), what)
@@ -131,7 +137,7 @@ def test_estimator_launch_by_launch(cbx, oracle, T, n_mid, n_tr, tail):
 
 def test_estimator_full_size_runs(cbx):
     """The reference's sizes (500 frames, 12 mid blocks, 4 transformers a
-    stage: 380 launches) through one captured graph: finite output, masked
+    stage: 352 launches) through one captured graph: finite output, masked
     frames zero."""
     e = CFMEstimator(500, seed=3, mask_tail=40)
     try:

@@ -215,8 +215,7 @@ def test_t3_block_tail():
                         (C.GL_UNSUPPORTED, 5, 1, 0),
                         (C.GL_BIAS_ACT, 6, 2, 0),
                         (C.GL_UNSUPPORTED, 8, 1, 0),
-                        (C.GL_BIAS_ACT, 9, 1, 0),         # proj bias add alone
-                        (C.GL_BINARY, 10, 1, C.BINARY_ADD)]   # a residual add with no norm after it
+                        (C.GL_BIAS_RESIDUAL, 9, 2, 0)]    # proj bias add -> residual add, no norm after it
 
 
 def test_residual_join_without_bias_and_unread_sum():
@@ -461,6 +460,46 @@ def test_hand_made_launches_stay_inside_the_list():
     assert L.cbx_graph_launch(T, 2, N, 2, ctypes.byref(C.GLaunch(C.GL_VIEW, 1, 1, 0)), None) == C.OK
 
 
+def test_bias_residual_chains():
+    """add(x, bias) [-> view] -> add(r, .) with no norm after it: one
+    launch (cfm_decoder.cpp:162-165 the time MLP over the frames, :242-244 a
+    stack's last ff.2); not when the sum is read again or kept, when the view
+    is not the sum itself, or when a norm follows (that is the
+    residual + LayerNorm launch)."""
+    def time_mlp(view_of_other=False, keep_sum=False):
+        g = C.Graph()
+        h = g.tensor(f32(10, 16))
+        mlp, b = g.tensor(f32(16)), g.tensor(f32(16))
+        s_t = f32(16)
+        s = g.tensor(s_t)
+        v = g.tensor(f32(1, 16) if view_of_other else s_t.view(1, 16))
+        g.node(C.GOP_ADD, s, (mlp, b))
+        g.node(C.GOP_VIEW, v, (s,))
+        g.node(C.GOP_ADD, g.tensor(f32(10, 16)), (h, v))
+        return g.plan(keep=[s] if keep_sum else [])
+
+    assert time_mlp() == [(C.GL_BIAS_RESIDUAL, 0, 3, 0)]
+    assert [p[0] for p in time_mlp(view_of_other=True)] == [C.GL_BIAS_ACT, C.GL_VIEW, C.GL_BIAS_ACT]
+    assert [p[0] for p in time_mlp(keep_sum=True)] == [C.GL_BIAS_ACT, C.GL_VIEW, C.GL_BIAS_ACT]
+
+    def ff2(read_twice=False, norm_after=False):
+        g = C.Graph()
+        x, mm, b = g.tensor(f32(10, 16)), g.tensor(f32(10, 16)), g.tensor(f32(16))
+        t = g.node(C.GOP_ADD, g.tensor(f32(10, 16)), (mm, b))
+        y = g.node(C.GOP_ADD, g.tensor(f32(10, 16)), (x, t))
+        if read_twice:
+            g.node(C.GOP_UNARY, g.tensor(f32(10, 16)), (t,), iparam=C.SILU)
+        if norm_after:
+            n = g.node(C.GOP_NORM, g.tensor(f32(10, 16)), (y,), fparam=1e-5)
+            m = g.node(C.GOP_MUL, g.tensor(f32(10, 16)), (n, g.tensor(f32(16))))
+            g.node(C.GOP_ADD, g.tensor(f32(10, 16)), (m, g.tensor(f32(16))))
+        return g.plan()
+
+    assert ff2() == [(C.GL_BIAS_RESIDUAL, 0, 2, 0)]
+    assert [p[0] for p in ff2(read_twice=True)] == [C.GL_BIAS_ACT, C.GL_BINARY, C.GL_UNARY]
+    assert [p[0] for p in ff2(norm_after=True)] == [C.GL_ADD_LAYER_NORM]
+
+
 def test_random_lists_plan_into_an_exact_cover():
     """Random node lists over random operands: the plan covers every node
     exactly once, in order, each launch within its kind's span."""
@@ -472,7 +511,7 @@ def test_random_lists_plan_into_an_exact_cover():
              C.GL_LEAKY_RELU: {1}, C.GL_ROPE: {1}, C.GL_CPY: {1}, C.GL_ADD_LAYER_NORM: {4, 5, 7, 8},
              C.GL_LAYER_NORM_MASK: {4, 7}, C.GL_BIAS_ACT: {1, 2, 4}, C.GL_CONV1D: set(range(9, 18)),
              C.GL_CONV_TRANSPOSE1D: set(range(7, 15)), C.GL_CAUSAL_CONV1D: set(range(12, 16)),
-             C.GL_BINARY: {1}, C.GL_CONCAT: {1}}
+             C.GL_BINARY: {1}, C.GL_CONCAT: {1}, C.GL_BIAS_RESIDUAL: {2, 3}}
     shapes = [(4, 8), (8,), (1, 8, 1, 1), (4, 8), (4, 1)]
     for trial in range(200):
         g = C.Graph()
