@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--hift-conv", action="store_true",
                     help="only the HiFT conv1d / transposed-conv timings, as one JSON object (for profiling)")
     ap.add_argument("--only", choices=["decode", "serving", "cfm", "hift", "softmax", "t3_block", "t3_token", "hift_conv",
-                                       "cfm_estimator", "copy"],
+                                       "cfm_estimator", "hift_decode", "copy"],
                     help="run one secondary workload alone and print its JSON (no headline line)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the markdown summary of two --pmc runs over --traffic-probe (no GPU)")
@@ -875,6 +875,62 @@ def bench_cfm_estimator(C, torch, T=500, reps=20):
         e.close()
 
 
+def bench_hift_decode(C, torch, T_mel=500, reps=10):
+    """One HiFT vocoder decode (hift_vocoder.cpp:613-749: conv_pre, the three
+    upsampling stages with their source convs and resblocks, conv_post; the
+    host STFT of the source and the iSTFT left out) over T_mel mel frames,
+    planned into one list of launches (chatterbox_amdvulkan_amd/
+    hift_decode.py).  Device time per decode from back-to-back replays of
+    the list captured into a HIP graph (cbx_graph_exec), the convs'
+    arithmetic rate against the f16 MFMA peak, and the same list planned and
+    launched each decode (cbx_graph_compute)."""
+    from chatterbox_amdvulkan_amd.hift_decode import HiFTDecode
+
+    e = HiFTDecode(T_mel, seed=5)
+    try:
+        plan = e.plan()
+        ex = e.graph.capture(e.keep)
+        s = cur_stream(torch)
+        flops = e.flops()
+        kinds = {}
+        names = {v: k[3:].lower() for k, v in vars(C).items() if k.startswith("GL_") and isinstance(v, int)}
+        for p in plan:
+            if p[0] != C.GL_VIEW:
+                kinds[names[p[0]]] = kinds.get(names[p[0]], 0) + 1
+        out = {"reference_sequence": f"hift_vocoder.cpp:613-749, T_mel {T_mel} "
+                                     f"(stages of {e.stage_frames[0]}, {e.stage_frames[1]}, {e.stage_frames[2]} frames)",
+               "launches": ex.n_launches, "launches_by_kind": kinds, "conv_flop_per_decode": flops}
+        for _ in range(2):
+            ex.launch(s)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            ex.launch(s)
+        e1.record()
+        torch.cuda.synchronize()
+        dev_us = e0.elapsed_time(e1) * 1000.0 / reps
+        out["exec_replay_us_per_decode"] = dev_us
+        out["conv_TFLOPs"] = flops / (dev_us * 1e-6) / 1e12
+        out["pct_of_f16_mfma_peak"] = 100.0 * out["conv_TFLOPs"] / PEAK_MFMA_F16_TFLOPS
+        out["audio_seconds_per_decode"] = T_mel * 480 / 24000
+        ex.close()
+        e.graph.compute(e.keep)
+        torch.cuda.synchronize()
+        n_c = max(3, reps // 2)
+        tm = time.perf_counter()
+        e0.record()
+        for _ in range(n_c):
+            e.graph.compute(e.keep)
+        host = (time.perf_counter() - tm) / n_c * 1e6
+        e1.record()
+        torch.cuda.synchronize()
+        out["graph_compute_us_per_decode"] = {"host_us": host, "device_us": e0.elapsed_time(e1) * 1000.0 / n_c}
+        return out
+    finally:
+        e.close()
+
+
 PEAK_MFMA_F16_TFLOPS = 2500.0
 
 
@@ -1569,6 +1625,7 @@ def main():
               "softmax": lambda: bench_softmax(C, W, torch), "t3_block": lambda: bench_t3_block(C, W, torch),
               "t3_token": lambda: bench_t3_token(C, W, torch),
               "cfm_estimator": lambda: bench_cfm_estimator(C, torch),
+              "hift_decode": lambda: bench_hift_decode(C, torch),
               "hift_conv": lambda: bench_hift_conv(C, W, torch),
               "copy": lambda: bench_copy_ceiling(C, torch, {"gelu_bytes": nb["gelu"],
                                                             "embed_layer_norm_bytes": nb["embed_layer_norm"],
@@ -1617,6 +1674,8 @@ def main():
         details["t3_token_elementwise"] = bench_t3_token(C, W, torch)
         log("cfm estimator")
         details["cfm_estimator_elementwise"] = bench_cfm_estimator(C, torch)
+        log("hift decode")
+        details["hift_decode"] = bench_hift_decode(C, torch)
         log("hift conv")
         details["hift_resblock_conv"] = bench_hift_conv(C, W, torch)
     k_ms = res["kernel_ms"]["run_ops"]
@@ -1675,6 +1734,12 @@ def main():
         out["cfm_estimator_us_per_call"] = {"reference_sequence": ce["reference_sequence"] +
                                             f", {ce['launches']} launches",
                                             "exec_replay": round(ce["exec_replay_us_per_call"], 2)}
+    if "hift_decode" in details:
+        hd = details["hift_decode"]
+        out["hift_decode_us_per_call"] = {"reference_sequence": hd["reference_sequence"] +
+                                          f", {hd['launches']} launches",
+                                          "exec_replay": round(hd["exec_replay_us_per_decode"], 2),
+                                          "conv_TFLOPs": round(hd["conv_TFLOPs"], 1)}
     out["details"] = details
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(W, a.cpu_seconds)

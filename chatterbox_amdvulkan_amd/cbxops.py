@@ -116,7 +116,7 @@ GL_UNSUPPORTED, GL_VIEW, GL_GET_ROWS, GL_GET_ROWS_ADD, GL_GET_ROWS_ADD_LAYER_NOR
     GL_LAYER_NORM_ROPE, GL_RMS_NORM, GL_GROUP_NORM, GL_SOFT_MAX, GL_SNAKE, GL_UNARY, GL_SWIGLU, GL_LEAKY_RELU, \
     GL_ROPE, GL_CPY, GL_ADD_LAYER_NORM, GL_LAYER_NORM_MASK, GL_BIAS_ACT, GL_CONV1D, GL_CONV_TRANSPOSE1D, \
     GL_CAUSAL_CONV1D, GL_GET_ROWS_CONCAT_ADD_LAYER_NORM, GL_BINARY, GL_CONCAT, \
-    GL_BIAS_RESIDUAL = range(27)
+    GL_BIAS_RESIDUAL, GL_SCALE = range(28)
 # conv launch flags: the prologue (bits 0-1), a bias add, the residual add
 GLF_SNAKE, GLF_LEAKY, GLF_MASK, GLF_BIAS, GLF_RESIDUAL = 1, 2, 3, 4, 8
 
@@ -187,6 +187,7 @@ def load() -> ctypes.CDLL:
         "cbx_binary": (i, [i, P, P, P, vp]),
         "cbx_concat": (i, [P, P, i, P, vp]),
         "cbx_bias_residual": (i, [P, P, P, P, vp]),
+        "cbx_scale": (i, [P, f, P, vp]),
         "cbx_conv1d_weights_create": (i, [P, vp, ctypes.POINTER(vp)]),
         "cbx_conv1d_weights_destroy": (None, [vp]),
         "cbx_conv1d": (i, [P, vp, i, i, i, i, P, P, f, P, P, P, vp]),
@@ -661,6 +662,14 @@ def bias_residual(x, bias, r, out=None):
     _ready(r)
     out = _out_like(r, out)
     _check(load().cbx_bias_residual(_ref(desc(x)), _ref(desc(bias)), _ref(desc(r)), _ref(desc(out)), _stream()))
+    return out
+
+
+def scale(x, s, out=None):
+    """ggml_scale(x, s): x * s, one f32 rounding."""
+    _ready(x)
+    out = _out_like(x, out)
+    _check(load().cbx_scale(_ref(desc(x)), float(s), _ref(desc(out)), _stream()))
     return out
 
 

@@ -1682,6 +1682,20 @@ extern "C" int cbx_bias_residual(const cbx_tensor* x, const cbx_tensor* bias, co
     return launch_bias_residual(x, bias, r, y, reinterpret_cast<hipStream_t>(stream));
 }
 
+extern "C" int cbx_scale(const cbx_tensor* x, float sc, cbx_tensor* y, cbx_stream stream) {
+    const char* what = "cbx_scale";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(x, what, "x")) || (rc = validate(y, what, "y"))) return rc;
+    if (x->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, "cbx_scale: F32 only");
+    if (!same_shape(x, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_scale: x and y shapes differ");
+    if (overlaps(y, x) && !same_view(y, x)) return set_error(CBX_ERR_INVALID_ARG, "cbx_scale: y overlaps x other than as x itself");
+    if (nelements(x) == 0) return CBX_OK;
+    return launch_scale(x, sc, y, reinterpret_cast<hipStream_t>(stream));
+}
+
 extern "C" int cbx_concat(const cbx_tensor* a, const cbx_tensor* b, int dim, cbx_tensor* y, cbx_stream stream) {
     const char* what = "cbx_concat";
     clear_error();

@@ -539,17 +539,19 @@ struct Planner {
                 // scale and the mask only fuse into a plain soft_max: a
                 // soft_max with its own scale would round twice
                 int32_t j = i, prev = a.src[0];
+                bool chain = true;
                 if (is(j, CBX_GOP_SCALE)) prev = nd[j++].dst;
                 if (is(j, CBX_GOP_DIAG_MASK_INF) && (j == i || (nd[j].src[0] == prev && internal(prev, 1)))) {
-                    if (nd[j].iparam < 0) return CBX_GL_UNSUPPORTED;
-                    prev = nd[j++].dst;
+                    if (nd[j].iparam < 0) chain = false;
+                    else prev = nd[j++].dst;
                 }
-                if (is(j, CBX_GOP_SOFT_MAX) && nd[j].src[0] == prev && internal(prev, 1) && nd[j].src[1] < 0 &&
-                    nd[j].fparam == 1.0f) {
+                if (chain && is(j, CBX_GOP_SOFT_MAX) && nd[j].src[0] == prev && internal(prev, 1) &&
+                    nd[j].src[1] < 0 && nd[j].fparam == 1.0f) {
                     *len = j + 1 - i;
                     return CBX_GL_SOFT_MAX;
                 }
-                return CBX_GL_UNSUPPORTED;
+                // a scale on its own (the mean of a HiFT stage's resblocks)
+                return a.op == CBX_GOP_SCALE ? CBX_GL_SCALE : CBX_GL_UNSUPPORTED;
             }
             case CBX_GOP_SOFT_MAX:
                 return a.src[1] < 0 ? CBX_GL_SOFT_MAX : CBX_GL_UNSUPPORTED;
@@ -722,8 +724,9 @@ constexpr int32_t kSpan[][2] = {
     {1, 1},  // BINARY
     {1, 1},  // CONCAT
     {2, 3},  // BIAS_RESIDUAL [view]
+    {1, 1},  // SCALE
 };
-constexpr int32_t kLastKind = CBX_GL_BIAS_RESIDUAL;
+constexpr int32_t kLastKind = CBX_GL_SCALE;
 static_assert(sizeof(kSpan) / sizeof(kSpan[0]) == kLastKind + 1, "one span per launch kind");
 
 // Issues the entry point a launch maps to.  A launch is only read within
@@ -850,6 +853,9 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
             if (a.op != CBX_GOP_ADD || last.op != CBX_GOP_ADD || r < 0) break;
             return cbx_bias_residual(T(t, a.src[0]), T(t, a.src[1]), T(t, r), y, s);
         }
+        case CBX_GL_SCALE:
+            if (a.op != CBX_GOP_SCALE) break;
+            return cbx_scale(T(t, a.src[0]), a.fparam, y, s);
         case CBX_GL_CONCAT:
             return cbx_concat(T(t, a.src[0]), T(t, a.src[1]), a.iparam, y, s);
         case CBX_GL_ADD_LAYER_NORM: {

@@ -15,6 +15,9 @@
 // follows (cfm_decoder.cpp:162-165 the time MLP broadcast over the frames,
 // :242-244 a stack's last ff.2).  Same two forms as the binary ops.
 //
+// Scale: y = x * s (ggml_scale) -- the mean of a HiFT stage's three
+// resblocks (hift_vocoder.cpp:736), the same two forms.
+//
 // Concat: y = ggml_concat(a, b, dim) -- the decoder's channel packing and
 // skip join (cfm_decoder.cpp:489-491,530), the time embeddings (:476).  A workgroup per output row.
 #include <type_traits>
@@ -126,6 +129,30 @@ __global__ __launch_bounds__(kThreads) void k_bias_residual_rows(View x, View b,
     }
 }
 
+// y = x * s over contiguous x and y
+__global__ __launch_bounds__(kThreads) void k_scale_flat(const float* __restrict__ x, float* __restrict__ y, float s,
+                                                         uint32_t n4) {
+    arg_now(x);
+    arg_now(y);
+    const uint32_t iu = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t i = iu < n4 ? iu : n4 - 1;
+    const float4 v = *reinterpret_cast<const float4*>(x + 4ull * i);
+    if (iu < n4) *reinterpret_cast<float4*>(y + 4ull * i) = make_float4(v.x * s, v.y * s, v.z * s, v.w * s);
+}
+
+// any strides: a workgroup per row
+__global__ __launch_bounds__(kThreads) void k_scale_rows(View x, View y, float s, int64_t nr) {
+    for (int64_t q = blockIdx.x; q < nr; q += gridDim.x) {
+        const int64_t i1 = q % x.ne[1], u = q / x.ne[1];
+        const int64_t i2 = u % x.ne[2], i3 = u / x.ne[2];
+        const char* xr = x.data + i1 * x.nb[1] + i2 * x.nb[2] + i3 * x.nb[3];
+        char* yr = y.data + i1 * y.nb[1] + i2 * y.nb[2] + i3 * y.nb[3];
+        for (int64_t j = threadIdx.x; j < x.ne[0]; j += kThreads) {
+            *reinterpret_cast<float*>(yr + j * y.nb[0]) = *reinterpret_cast<const float*>(xr + j * x.nb[0]) * s;
+        }
+    }
+}
+
 // A workgroup per row of y: along dim 0 the row is a's row then b's; along
 // dim d > 0 the row is a's when its index along d is below a.ne[d], else
 // b's at that index minus a.ne[d].  ES: the element size (4 or 2).
@@ -230,6 +257,21 @@ int launch_bias_residual(const cbx_tensor* x, const cbx_tensor* bias, const cbx_
                            dim3(kThreads), 0, s, view_of(x), view_of(bias), view_of(r), view_of(y), nr);
     }
     return check_launch("bias residual");
+}
+
+int launch_scale(const cbx_tensor* x, float s, cbx_tensor* y, hipStream_t strm) {
+    const int64_t n = nelements(x);
+    if (is_contiguous(x) && is_contiguous(y) && al16(x->data) && al16(y->data) && n % 4 == 0 &&
+        n / 4 < (int64_t{1} << 31)) {
+        const uint32_t n4 = static_cast<uint32_t>(n / 4);
+        hipLaunchKernelGGL(k_scale_flat, dim3(static_cast<unsigned>(cdiv(n4, kThreads))), dim3(kThreads), 0, strm,
+                           static_cast<const float*>(x->data), static_cast<float*>(y->data), s, n4);
+    } else {
+        const int64_t nr = nrows(x);
+        hipLaunchKernelGGL(k_scale_rows, dim3(static_cast<unsigned>(std::min<int64_t>(nr, int64_t{1} << 20))),
+                           dim3(kThreads), 0, strm, view_of(x), view_of(y), s, nr);
+    }
+    return check_launch("scale");
 }
 
 int launch_binary(int op, const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y, hipStream_t s) {

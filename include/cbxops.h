@@ -357,6 +357,12 @@ int cbx_binary(int op, const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y,
 int cbx_bias_residual(const cbx_tensor* x, const cbx_tensor* bias, const cbx_tensor* r,
                       cbx_tensor* y, cbx_stream stream);
 
+/* ggml_scale(x, s): y = x * s, one f32 rounding.  The mean of a HiFT
+ * stage's three resblocks, scale(sum, 1/3) (hift_vocoder.cpp:736).  F32,
+ * any strides (nb[0] the element size); y x's shape, and may be x itself
+ * (no other overlap).                                                     */
+int cbx_scale(const cbx_tensor* x, float s, cbx_tensor* y, cbx_stream stream);
+
 /* ggml_concat(a, b, dim): y.ne[dim] = a.ne[dim] + b.ne[dim], the other
  * dims equal to a's and b's; a's elements first (cfm_decoder.cpp:489-491
  * packing x, mu, spks, cond along the channels; :530 the skip join; :476
@@ -619,7 +625,7 @@ typedef enum cbx_gop {
     CBX_GOP_GET_ROWS      = 1,  /* src0 table, src1 ids I32                           */
     CBX_GOP_ADD           = 2,  /* src0 + src1 (a bias add, or inside a chain)        */
     CBX_GOP_MUL           = 3,  /* src0 * src1 (only inside a chain)                  */
-    CBX_GOP_SCALE         = 4,  /* src0 * fparam (only before SOFT_MAX)               */
+    CBX_GOP_SCALE         = 4,  /* src0 * fparam                                      */
     CBX_GOP_NORM          = 5,  /* fparam = eps                                       */
     CBX_GOP_RMS_NORM      = 6,  /* fparam = eps                                       */
     CBX_GOP_GROUP_NORM    = 7,  /* iparam = n_groups, fparam = eps                    */
@@ -682,6 +688,7 @@ typedef enum cbx_glaunch_kind {
     CBX_GL_CONCAT,            /* one concat (cbx_concat)                        */
     CBX_GL_BIAS_RESIDUAL,     /* add(x, bias) [-> view (same dims)] -> add(r, .)
                                  with no norm after it (cbx_bias_residual)      */
+    CBX_GL_SCALE,             /* one scale no soft_max follows (cbx_scale)      */
 } cbx_glaunch_kind;
 
 typedef struct cbx_glaunch {

@@ -1,5 +1,6 @@
 """cbx_binary (ggml_add / ggml_mul with the second operand repeated),
-cbx_bias_residual (two ggml_adds in one pass) and cbx_concat (ggml_concat)
+cbx_bias_residual (two ggml_adds in one pass), cbx_scale (ggml_scale) and
+cbx_concat (ggml_concat)
 against the oracle's add / mul (ggml's repeat by
 index) and numpy's concatenate: one f32 rounding per element, so bit-exact;
 a concat is a copy."""
@@ -135,6 +136,31 @@ def test_bias_residual_refusals(cbx):
         cbx.bias_residual(x, b, r, out=torch.zeros((6, 10), device="cuda"))       # y not r's shape
     with pytest.raises(cbx.CbxError):
         cbx.bias_residual(x.half(), b.half(), r.half())                           # F32 only
+
+
+@pytest.mark.parametrize("shape", [(601, 64), (40, 256), (7, 13), (3, 5, 6, 2)])
+def test_scale(cbx, shape):
+    """ggml_scale: one f32 product per element, so numpy's f32 multiply is
+    the whole reference; the resblock mean's 1/3 and a power of two."""
+    x = W.normal(W.seed_of(50, len(shape)), shape, 0.0, 3.0)
+    for s in (np.float32(1.0 / 3.0), np.float32(0.25), np.float32(-7.5)):
+        assert_bitexact(host(cbx.scale(dev(x), float(s))), x * s, f"scale {shape} by {s}")
+
+
+def test_scale_views_in_place_and_refusals(cbx):
+    base = W.normal(W.seed_of(51, 0), (60, 50), 0.0, 1.0)
+    yb = torch.full((60, 64), float("nan"), device="cuda")
+    y = yb[:, 8:48]
+    cbx.scale(dev(base)[:, 3:43], 1.0 / 3.0, out=y)
+    assert_bitexact(host(y), base[:, 3:43] * np.float32(1.0 / 3.0), "strided")
+    assert np.isnan(host(yb)[:, :8]).all() and np.isnan(host(yb)[:, 48:]).all(), "only y's columns written"
+    t = dev(base)
+    cbx.scale(t, 0.5, out=t)
+    assert_bitexact(host(t), base * np.float32(0.5), "in place")
+    with pytest.raises(cbx.CbxError):
+        cbx.scale(t, 2.0, out=t[1:])                                          # y overlaps x otherwise
+    with pytest.raises(cbx.CbxError):
+        cbx.scale(t.half(), 2.0)                                              # F32 only
 
 
 @pytest.mark.parametrize("dim", [0, 1, 2, 3])

@@ -309,7 +309,19 @@ def test_soft_max_with_own_scale_does_not_absorb_scale():
     s, y = g.tensor(f32(4, 8)), g.tensor(f32(4, 8))
     g.node(C.GOP_SCALE, s, (kq,), fparam=0.5)
     g.node(C.GOP_SOFT_MAX, y, (s,), fparam=2.0)
-    assert g.plan() == [(C.GL_UNSUPPORTED, 0, 1, 0), (C.GL_SOFT_MAX, 1, 1, 0)]
+    # the scale stays a launch of its own: folded in, it would round once
+    # where ggml rounds twice
+    assert g.plan() == [(C.GL_SCALE, 0, 1, 0), (C.GL_SOFT_MAX, 1, 1, 0)]
+
+
+def test_lone_scale_and_mask():
+    """A scale no soft_max follows is a cbx_scale launch; a lone
+    diag_mask_inf is not a chain the library runs."""
+    g = C.Graph()
+    x = g.tensor(f32(4, 8))
+    s = g.node(C.GOP_SCALE, g.tensor(f32(4, 8)), (x,), fparam=1.0 / 3.0)
+    g.node(C.GOP_DIAG_MASK_INF, g.tensor(f32(4, 8)), (s,), iparam=1)
+    assert g.plan() == [(C.GL_SCALE, 0, 1, 0), (C.GL_UNSUPPORTED, 1, 1, 0)]
 
 
 def test_soft_max_with_mask_operand_is_unsupported():
@@ -511,7 +523,7 @@ def test_random_lists_plan_into_an_exact_cover():
              C.GL_LEAKY_RELU: {1}, C.GL_ROPE: {1}, C.GL_CPY: {1}, C.GL_ADD_LAYER_NORM: {4, 5, 7, 8},
              C.GL_LAYER_NORM_MASK: {4, 7}, C.GL_BIAS_ACT: {1, 2, 4}, C.GL_CONV1D: set(range(9, 18)),
              C.GL_CONV_TRANSPOSE1D: set(range(7, 15)), C.GL_CAUSAL_CONV1D: set(range(12, 16)),
-             C.GL_BINARY: {1}, C.GL_CONCAT: {1}, C.GL_BIAS_RESIDUAL: {2, 3}}
+             C.GL_BINARY: {1}, C.GL_CONCAT: {1}, C.GL_BIAS_RESIDUAL: {2, 3}, C.GL_SCALE: {1}}
     shapes = [(4, 8), (8,), (1, 8, 1, 1), (4, 8), (4, 1)]
     for trial in range(200):
         g = C.Graph()
