@@ -19,7 +19,11 @@
 // resblocks (hift_vocoder.cpp:736), the same two forms.
 //
 // Concat: y = ggml_concat(a, b, dim) -- the decoder's channel packing and
-// skip join (cfm_decoder.cpp:489-491,530), the time embeddings (:476).  A workgroup per output row.
+// skip join (cfm_decoder.cpp:489-491,530), the time embeddings (:476), the
+// HiFT vocoder's one-frame reflection pad (hift_vocoder.cpp:694-707).
+// Contiguous tensors take one vector a lane over a grid that covers y once
+// (each of y's blocks a's block then b's); other layouts a workgroup per
+// output row.
 #include <type_traits>
 
 #include "cbx_internal.h"
@@ -190,6 +194,21 @@ __global__ __launch_bounds__(kThreads) void k_concat(View a, View b, View y, int
     }
 }
 
+// Contiguous a, b and y: y is `outer` blocks, each a's block of na vectors
+// then b's of nb (na, nb: the elements up to and including the concat dim,
+// in units of V).  One vector a lane over a grid that covers y once.
+template <typename V>
+__global__ __launch_bounds__(kThreads) void k_concat_flat(const V* __restrict__ a, const V* __restrict__ b,
+                                                          V* __restrict__ y, uint32_t na, uint32_t nb, uint32_t n) {
+    arg_now(a);
+    arg_now(b);
+    arg_now(y);
+    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t blk = i / (na + nb), r = i - blk * (na + nb);
+    y[i] = r < na ? a[blk * na + r] : b[blk * nb + (r - na)];
+}
+
 bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 template <int OP>
@@ -281,6 +300,32 @@ int launch_binary(int op, const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* 
 }
 
 int launch_concat(const cbx_tensor* a, const cbx_tensor* b, int dim, cbx_tensor* y, hipStream_t s) {
+    if (is_contiguous(a) && is_contiguous(b) && is_contiguous(y) && nelements(y) < (int64_t{1} << 32)) {
+        int64_t ia = 1, ib = 1;
+        for (int k = 0; k <= dim; k++) {
+            ia *= a->ne[k];
+            ib *= b->ne[k];
+        }
+        const int64_t es = y->type == CBX_TYPE_F32 ? 4 : 2;
+        const bool v16 = (ia * es) % 16 == 0 && (ib * es) % 16 == 0 && al16(a->data) && al16(b->data) && al16(y->data);
+        const int64_t vb = v16 ? 16 : es;
+        const uint32_t na = static_cast<uint32_t>(ia * es / vb), nb = static_cast<uint32_t>(ib * es / vb);
+        const uint32_t n = static_cast<uint32_t>(nelements(y) * es / vb);
+        const dim3 grid(static_cast<unsigned>(cdiv(n, kThreads)));
+        if (v16) {
+            hipLaunchKernelGGL(k_concat_flat<uint4>, grid, dim3(kThreads), 0, s, static_cast<const uint4*>(a->data),
+                               static_cast<const uint4*>(b->data), static_cast<uint4*>(y->data), na, nb, n);
+        } else if (es == 4) {
+            hipLaunchKernelGGL(k_concat_flat<uint32_t>, grid, dim3(kThreads), 0, s,
+                               static_cast<const uint32_t*>(a->data), static_cast<const uint32_t*>(b->data),
+                               static_cast<uint32_t*>(y->data), na, nb, n);
+        } else {
+            hipLaunchKernelGGL(k_concat_flat<uint16_t>, grid, dim3(kThreads), 0, s,
+                               static_cast<const uint16_t*>(a->data), static_cast<const uint16_t*>(b->data),
+                               static_cast<uint16_t*>(y->data), na, nb, n);
+        }
+        return check_launch("concat");
+    }
     const int64_t nr = nrows(y);
     const dim3 grid(static_cast<unsigned>(std::min<int64_t>(nr, int64_t{1} << 20)));
     if (y->type == CBX_TYPE_F32) {

@@ -176,6 +176,22 @@ def test_concat_dims(cbx, dim, dtype):
     assert_bitexact(got, np.concatenate((a, b), axis=ax), f"concat dim {dim} {np.dtype(dtype).name}")
 
 
+@pytest.mark.parametrize("sa,sb,dim", [((1, 64), (60000, 64), 1),      # the vocoder's one-frame pad
+                                        ((500, 80), (500, 80), 0),      # the decoder's channel packing
+                                        ((500, 256), (500, 256), 0),    # the skip join
+                                        ((3, 7, 12), (3, 5, 12), 1),
+                                        ((2, 3, 4, 8), (1, 3, 4, 8), 3)])
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_concat_contiguous(cbx, sa, sb, dim, dtype):
+    """Contiguous operands take the flat kernel, 16-byte vectors when every
+    block is a multiple of 16 bytes, elements otherwise."""
+    a = W.normal(W.seed_of(52, len(sa)), sa, 0.0, 1.0).astype(dtype)
+    b = W.normal(W.seed_of(53, len(sb)), sb, 0.0, 1.0).astype(dtype)
+    ax = a.ndim - 1 - dim
+    got = host(cbx.concat(dev(a), dev(b), dim))
+    assert_bitexact(got, np.concatenate((a, b), axis=ax), f"concat {sa} {sb} dim {dim} {np.dtype(dtype).name}")
+
+
 def test_concat_channels_of_views(cbx):
     """The decoder's channel packing on (T, C) tensors, one operand a view."""
     x = W.normal(W.seed_of(45, 0), (500, 80), 0.0, 1.0)
