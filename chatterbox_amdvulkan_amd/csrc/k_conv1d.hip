@@ -921,25 +921,37 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
         const bool vec_in = al16(a.x) && a.x_nb1 % 16 == 0 && (one || a.x_nb2 % 16 == 0);
         const bool vec_out = al16(a.y) && a.y_nb1 % 16 == 0 && (one || a.y_nb2 % 16 == 0) && (!a.bias || al16(a.bias)) &&
                              (!a.res || (al16(a.res) && a.r_nb1 % 16 == 0 && (one || a.r_nb2 % 16 == 0)));
-        const bool narrow = c_out % 128 != 0;   // 64-channel output tiles: 128 x 64, two a CU
-        const int64_t PBC = narrow ? 64 : 128;
+        bool narrow = c_out % 128 != 0;   // 64-channel output tiles: 128 x 64, two a CU
         const int64_t n_cu = st->n_cu > 0 ? st->n_cu : 1;
-        auto items_of = [&](int64_t bt) { return cdiv(static_cast<int64_t>(a.t_out), bt) * (c_out / PBC) * x->ne[2]; };
-        auto lds_of = [&](int64_t bt) {
+        auto items_of = [&](int64_t bt, int64_t bc) {
+            return cdiv(static_cast<int64_t>(a.t_out), bt) * (c_out / bc) * x->ne[2];
+        };
+        auto lds_of = [&](int64_t bt, int64_t bc) {
             const int64_t pwin = bt + (k - 1) * static_cast<int64_t>(dil);
             return std::max<size_t>(2 * static_cast<size_t>(pwin) * kPipeCs * sizeof(_Float16),
-                                    static_cast<size_t>(bt) * (PBC + 4) * sizeof(float));
+                                    static_cast<size_t>(bt) * (bc + 4) * sizeof(float));
         };
         // at least `need` workgroups, and every round fills 3/4 of the slots
         auto fills = [&](int64_t items, int64_t slots, int64_t need) {
             return items >= need && 4 * items >= 3 * cdiv(items, slots) * slots && items < (int64_t{1} << 31);
         };
         const int64_t t2 = narrow ? 128 : 96;   // rows of the two-a-CU tile
-        const int64_t i2 = items_of(t2), i192 = items_of(192);
-        const bool two = 2 * lds_of(t2) <= kLdsMax && fills(i2, 2 * n_cu, n_cu);
-        const int64_t PBT = two ? t2 : 192, items = two ? i2 : i192;
-        const size_t plds = lds_of(PBT);
-        if (vec_in && vec_out && plds <= kLdsMax && (two || (!narrow && k >= 5 && fills(i192, n_cu, (n_cu + 1) / 2)))) {
+        const int64_t i2 = items_of(t2, narrow ? 64 : 128), i192 = items_of(192, 128);
+        bool two = 2 * lds_of(t2, narrow ? 64 : 128) <= kLdsMax && fills(i2, 2 * n_cu, n_cu);
+        const bool one192 = !two && !narrow && k >= 5 && fills(i192, n_cu, (n_cu + 1) / 2);
+        // neither, with 128-channel multiples: 128 x 64 tiles two a CU when
+        // they give every CU a workgroup, however unevenly they fill the
+        // second slots (the 128 x 20000 stage of a 500-frame decode, 314
+        // workgroups: K 11 24.1 -> 20.3 us, K 7 18.3 -> 17.2, K 3 14.4 ->
+        // 13.7 against k_conv1d's 32 x 64 tiles)
+        if (!two && !one192 && !narrow) {
+            const int64_t in = items_of(128, 64);
+            if (in >= n_cu && in < (int64_t{1} << 31) && 2 * lds_of(128, 64) <= kLdsMax) narrow = two = true;
+        }
+        const int64_t PBC = narrow ? 64 : 128;
+        const int64_t PBT = two ? (narrow ? 128 : 96) : 192, items = items_of(PBT, PBC);
+        const size_t plds = lds_of(PBT, PBC);
+        if (vec_in && vec_out && plds <= kLdsMax && (two || one192)) {
             a.win = static_cast<int32_t>(PBT + (k - 1) * static_cast<int64_t>(dil));
             a.kch = kPipeKch;
             a.vout = 1;

@@ -316,7 +316,8 @@ def pipelined_tiles(C_in, C_out, T_out, B, K):
     64 == 0 and its tiles fill the CUs: C_out a multiple of 128 on 96 x 128
     tiles two a CU (a workgroup on every CU, 3/4 of every round's slots),
     else, with K >= 5, 192 x 128 tiles one a CU (at least half the CUs, 3/4
-    of every round's slots); other C_out on 128 x 64 tiles two a CU."""
+    of every round's slots), else 128 x 64 tiles two a CU when they give
+    every CU a workgroup; other C_out on 128 x 64 tiles two a CU."""
     if not (K >= 3 and C_in % 64 == 0 and C_out % 64 == 0):
         return False
     n_cu = torch.cuda.get_device_properties(0).multi_processor_count
@@ -328,7 +329,9 @@ def pipelined_tiles(C_in, C_out, T_out, B, K):
 
     if bc == 64:   # 128 x 64 tiles, two a CU, or k_conv1d
         return fills(128, 2 * n_cu, n_cu)
-    return fills(96, 2 * n_cu, n_cu) or (K >= 5 and fills(192, n_cu, (n_cu + 1) // 2))
+    if fills(96, 2 * n_cu, n_cu) or (K >= 5 and fills(192, n_cu, (n_cu + 1) // 2)):
+        return True
+    return -(-T_out // 128) * (C_out // 64) * (B or 1) >= n_cu   # 128 x 64 tiles on every CU
 
 
 PIPE = [  # (C_in, C_out, T, B, K, dilation, prologue, residual)
@@ -342,6 +345,8 @@ PIPE = [  # (C_in, C_out, T, B, K, dilation, prologue, residual)
     (128, 128, 48000, None, 3, 1, "SNAKE", True),     # a K 3 conv with the residual, full length
     (64, 64, 120000, None, 3, 5, "LEAKY", False),     # a K 3 conv on the 128 x 64 tiles
     (128, 128, 400, 64, 5, 2, "SNAKE", False),        # the smallest K taken
+    (128, 128, 20000, None, 11, 5, "SNAKE", False),   # 128 x 64 tiles for 128 channels (a 500-frame decode's stage)
+    (128, 128, 20000, None, 3, 1, "SNAKE", True),     # the same at K 3 with the residual
 ]
 
 
