@@ -118,7 +118,7 @@ GL_UNSUPPORTED, GL_VIEW, GL_GET_ROWS, GL_GET_ROWS_ADD, GL_GET_ROWS_ADD_LAYER_NOR
     GL_CAUSAL_CONV1D, GL_GET_ROWS_CONCAT_ADD_LAYER_NORM, GL_BINARY, GL_CONCAT, \
     GL_BIAS_RESIDUAL, GL_SCALE = range(28)
 # conv launch flags: the prologue (bits 0-1), a bias add, the residual add
-GLF_SNAKE, GLF_LEAKY, GLF_MASK, GLF_BIAS, GLF_RESIDUAL = 1, 2, 3, 4, 8
+GLF_SNAKE, GLF_LEAKY, GLF_MASK, GLF_BIAS, GLF_RESIDUAL, GLF_SUM, GLF_SCALE = 1, 2, 3, 4, 8, 16, 32
 
 # cbx_op_kind
 OP_LAYER_NORM, OP_RMS_NORM, OP_UNARY, OP_LEAKY_RELU, OP_SWIGLU, OP_ROPE, OP_GET_ROWS, \
@@ -191,6 +191,7 @@ def load() -> ctypes.CDLL:
         "cbx_conv1d_weights_create": (i, [P, vp, ctypes.POINTER(vp)]),
         "cbx_conv1d_weights_destroy": (None, [vp]),
         "cbx_conv1d": (i, [P, vp, i, i, i, i, P, P, f, P, P, P, vp]),
+        "cbx_conv1d_sum": (i, [P, vp, i, i, i, i, P, P, f, P, P, P, f, P, vp]),
         "cbx_conv_transpose1d_weights_create": (i, [P, i, vp, ctypes.POINTER(vp)]),
         "cbx_conv_transpose1d": (i, [P, vp, i, i, P, P, f, P, P, vp]),
         "cbx_causal_conv1d": (i, [P, vp, P, P, P, vp]),
@@ -732,6 +733,21 @@ def conv1d(x, weights: Conv1dWeights, stride=1, pad=0, dilation=1, prologue=CONV
     opt = lambda t: _ref(desc(t)) if t is not None else None  # noqa: E731
     _check(load().cbx_conv1d(_ref(desc(x)), weights.handle, stride, pad, dilation, prologue, opt(alpha),
                              opt(alpha_inv), slope, opt(bias), opt(res), _ref(desc(out)), _stream()))
+    return out
+
+
+def conv1d_sum(x, weights: Conv1dWeights, stride, pad, dilation, prologue, alpha, alpha_inv, slope, bias, res, acc,
+               scale=1.0, out=None):
+    """(acc + conv1d(...)) * scale in one kernel: a HiFT stage's ResBlock sum
+    and mean folded into the resblock's last conv."""
+    _ready(x)
+    t_out = (x.shape[-2] + 2 * pad - dilation * (weights.k - 1) - 1) // stride + 1
+    if out is None:
+        out = torch.empty(tuple(x.shape[:-2]) + (t_out, weights.c_out), dtype=torch.float32, device=x.device)
+    opt = lambda t: _ref(desc(t)) if t is not None else None  # noqa: E731
+    _check(load().cbx_conv1d_sum(_ref(desc(x)), weights.handle, stride, pad, dilation, prologue, opt(alpha),
+                                 opt(alpha_inv), slope, opt(bias), opt(res), opt(acc), float(scale),
+                                 _ref(desc(out)), _stream()))
     return out
 
 

@@ -1086,19 +1086,43 @@ static int check_conv_x(const char* what, const cbx_conv1d_weights* w, const cbx
     return CBX_OK;
 }
 
+// cbx_conv1d and cbx_conv1d_sum: acc (with its scale) only from the latter
+static int conv1d_common(const char* what, const cbx_tensor* x, const cbx_conv1d_weights* w, int stride, int pad,
+                         int dilation, int prologue, const cbx_tensor* alpha, const cbx_tensor* alpha_inv, float slope,
+                         const cbx_tensor* bias, const cbx_tensor* res, const cbx_tensor* acc, float scale,
+                         cbx_tensor* y, cbx_stream stream);
+
 int cbx_conv1d(const cbx_tensor* x, const cbx_conv1d_weights* w, int stride, int pad, int dilation, int prologue,
                const cbx_tensor* alpha, const cbx_tensor* alpha_inv, float slope, const cbx_tensor* bias,
                const cbx_tensor* res, cbx_tensor* y, cbx_stream stream) {
-    const char* what = "cbx_conv1d";
+    return conv1d_common("cbx_conv1d", x, w, stride, pad, dilation, prologue, alpha, alpha_inv, slope, bias, res,
+                         nullptr, 1.0f, y, stream);
+}
+
+int cbx_conv1d_sum(const cbx_tensor* x, const cbx_conv1d_weights* w, int stride, int pad, int dilation, int prologue,
+                   const cbx_tensor* alpha, const cbx_tensor* alpha_inv, float slope, const cbx_tensor* bias,
+                   const cbx_tensor* res, const cbx_tensor* acc, float scale, cbx_tensor* y, cbx_stream stream) {
+    if (!acc) {
+        clear_error();
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d_sum: acc is NULL (cbx_conv1d has no sum)");
+    }
+    return conv1d_common("cbx_conv1d_sum", x, w, stride, pad, dilation, prologue, alpha, alpha_inv, slope, bias, res,
+                         acc, scale, y, stream);
+}
+
+static int conv1d_common(const char* what, const cbx_tensor* x, const cbx_conv1d_weights* w, int stride, int pad,
+                         int dilation, int prologue, const cbx_tensor* alpha, const cbx_tensor* alpha_inv, float slope,
+                         const cbx_tensor* bias, const cbx_tensor* res, const cbx_tensor* acc, float scale,
+                         cbx_tensor* y, cbx_stream stream) {
     clear_error();
     int rc;
     DeviceState* st = current_state(&rc);
     if (!st) return rc;
-    if (!w) return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: weights are NULL");
+    if (!w) return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": weights are NULL");
     if ((rc = validate(x, what, "x")) || (rc = validate(y, what, "y"))) return rc;
     if ((rc = check_conv_x(what, w, x, prologue))) return rc;
     if (stride < 1 || pad < 0 || dilation < 1 || stride > 64 || pad > (1 << 20) || dilation > 1024) {
-        return set_error(CBX_ERR_INVALID_ARG, "cbx_conv1d: stride must be 1..64, pad >= 0, dilation 1..1024");
+        return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": stride must be 1..64, pad >= 0, dilation 1..1024");
     }
     const int64_t t_in = x->ne[1];
     const int64_t span = dilation * (w->k - 1) + 1;
@@ -1109,10 +1133,18 @@ int cbx_conv1d(const cbx_tensor* x, const cbx_conv1d_weights* w, int stride, int
         return rc;
     }
     if (empty) return CBX_OK;
+    if (acc) {
+        if ((rc = validate(acc, what, "acc"))) return rc;
+        if (acc->type != CBX_TYPE_F32 || !same_shape(acc, y)) {
+            return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": acc must be F32 with y's shape");
+        }
+        // read in the epilogue while other workgroups store their tiles
+        if (overlaps(acc, y)) return set_error(CBX_ERR_INVALID_ARG, std::string(what) + ": acc must not overlap y");
+    }
     return launch_conv1d(x, w->data, w->k, w->c_in_pad, w->c_out, stride, pad, dilation, 1, 0, w->w_ph, prologue,
                          prologue == CBX_CONV_PRO_SNAKE ? alpha : nullptr,
                          prologue == CBX_CONV_PRO_SNAKE ? alpha_inv : nullptr, slope, bias, res, y, st,
-                         reinterpret_cast<hipStream_t>(stream));
+                         reinterpret_cast<hipStream_t>(stream), acc, scale);
 }
 
 int cbx_conv_transpose1d(const cbx_tensor* x, const cbx_conv1d_weights* w, int pad, int prologue,

@@ -301,6 +301,21 @@ struct Planner {
             if (same_dims(other, out) && same_dims(nd[j].dst, out)) {
                 *fl |= 8;
                 j++;
+                // the ResBlock sum: add(sum, r) of the residual's result r,
+                // then [scale] (hift_vocoder.cpp:731-736)
+                const int32_t r = nd[j - 1].dst;
+                if (is(j, CBX_GOP_ADD) && internal(r, 1)) {
+                    const int32_t acc = nd[j].src[0] == r ? nd[j].src[1] : nd[j].src[1] == r ? nd[j].src[0] : -1;
+                    if (acc != r && same_dims(acc, r) && same_dims(nd[j].dst, r)) {
+                        *fl |= 16;
+                        j++;
+                        const int32_t sum = nd[j - 1].dst;
+                        if (is(j, CBX_GOP_SCALE) && nd[j].src[0] == sum && internal(sum, 1) && same_dims(nd[j].dst, r)) {
+                            *fl |= 32;
+                            j++;
+                        }
+                    }
+                }
             }
         }
         return j - i;
@@ -717,7 +732,7 @@ constexpr int32_t kSpan[][2] = {
     {4, 8},  // ADD_LAYER_NORM [bias] [mish]
     {4, 7},  // LAYER_NORM_MASK [mish]
     {1, 4},  // BIAS_ACT [act | mish]
-    {9, 17}, // CONV1D [snake | leaky] [bias] [residual]
+    {9, 19}, // CONV1D [snake | leaky] [bias] [residual [sum [scale]]]
     {7, 14}, // CONV_TRANSPOSE1D [snake | leaky] [bias]
     {12, 15}, // CAUSAL_CONV1D [mask] [bias]
     {7, 12},  // GET_ROWS_CONCAT_ADD_LAYER_NORM [prompt gather, concat] [casts]
@@ -883,12 +898,15 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
         case CBX_GL_CONV1D:
         case CBX_GL_CONV_TRANSPOSE1D: {
             // the layout the flags describe: prologue, body, bias, residual
+            // [, the sum [, its scale]]
             const int pro = l.flags & 3;
             const bool bias = (l.flags & 4) != 0, res = (l.flags & 8) != 0;
+            const bool sum = (l.flags & 16) != 0, scl = (l.flags & 32) != 0;
             const bool tr = l.kind == CBX_GL_CONV_TRANSPOSE1D;
             const int32_t p = pro == 1 ? 5 : pro == 2 ? 1 : 0;
-            if (pro == 3 || (tr && res) ||
-                l.n_nodes != p + (tr ? 7 : 9) + (bias ? 2 : 0) + (res ? 1 : 0)) {
+            const int32_t n_res = p + (tr ? 7 : 9) + (bias ? 2 : 0) + (res ? 1 : 0);   // nodes up to the residual add
+            if (pro == 3 || (tr && (res || sum)) || (sum && !res) || (scl && !sum) ||
+                l.n_nodes != n_res + (sum ? 1 : 0) + (scl ? 1 : 0)) {
                 break;
             }
             const int32_t b0 = f + p;   // the transpose view
@@ -909,14 +927,28 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
             }
             if (!tr) {
                 const cbx_gnode& ic = nd[b0 + 2];
-                const cbx_gnode& last = nd[f + l.n_nodes - 1];
                 const cbx_tensor* r = nullptr;
                 if (res) {
-                    const int32_t out = nd[f + l.n_nodes - 2].dst;
-                    r = T(t, last.src[0] == out ? last.src[1] : last.src[0]);
+                    const cbx_gnode& ra = nd[f + n_res - 1];   // add(residual, conv out)
+                    const int32_t out = nd[f + n_res - 2].dst;
+                    r = T(t, ra.src[0] == out ? ra.src[1] : ra.src[0]);
                 }
-                return cbx_conv1d(x, nd[b0 + 5].conv_w, ic.conv[0], ic.conv[1], ic.conv[2], cp, al, ai, slope, bt, r,
-                                  y, s);
+                if (!sum) {
+                    return cbx_conv1d(x, nd[b0 + 5].conv_w, ic.conv[0], ic.conv[1], ic.conv[2], cp, al, ai, slope, bt,
+                                      r, y, s);
+                }
+                const cbx_gnode& sa = nd[f + n_res];          // add(acc, residual's result)
+                const int32_t rr = nd[f + n_res - 1].dst;
+                if (sa.op != CBX_GOP_ADD || (sa.src[0] != rr && sa.src[1] != rr)) break;
+                const cbx_tensor* acc = T(t, sa.src[0] == rr ? sa.src[1] : sa.src[0]);
+                float sc = 1.0f;
+                if (scl) {
+                    const cbx_gnode& sn = nd[f + n_res + 1];
+                    if (sn.op != CBX_GOP_SCALE || sn.src[0] != sa.dst) break;
+                    sc = sn.fparam;
+                }
+                return cbx_conv1d_sum(x, nd[b0 + 5].conv_w, ic.conv[0], ic.conv[1], ic.conv[2], cp, al, ai, slope, bt,
+                                      r, acc, sc, y, s);
             }
             // the crop: the view's offset into the full output, in frames
             const cbx_tensor* full = T(t, nd[b0 + 2].dst);

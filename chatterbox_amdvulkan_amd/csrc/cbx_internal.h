@@ -154,7 +154,7 @@ int launch_conv1d_weights(const cbx_tensor* w, int up, int64_t taps, _Float16* o
 int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c_in_pad, int64_t c_out, int stride,
                   int pad, int dil, int up, int crop, int64_t w_ph, int pro, const cbx_tensor* alpha,
                   const cbx_tensor* alpha_inv, float slope, const cbx_tensor* bias, const cbx_tensor* res, cbx_tensor* y,
-                  DeviceState* st, hipStream_t s);
+                  DeviceState* st, hipStream_t s, const cbx_tensor* acc = nullptr, float oscale = 1.0f);
 // Whether prepared weights were made from a weight of these extents: a
 // conv1d weight (K, C_in, C_out) when up == 0, else a transposed weight
 // (K, C_out, C_in) split for stride up.

@@ -70,7 +70,26 @@ struct ConvArgs {
     int32_t vout;               // c_out % 4 == 0 and 16-byte aligned y, res and bias: float4 stores
     int32_t n_tt, n_ct;         // time tiles and channel tiles of the grid (work item w = (z*n_tt + t)*n_ct + c)
     float slope;
+    const char* acc;            // (c_out, t_out, B) added after the residual, or null (stride-1 convs only)
+    int64_t a_nb1, a_nb2;
+    float oscale;               // the sum times oscale when scaled
+    int32_t scaled;
 };
+
+// The ResBlock sum after the residual add (hift_vocoder.cpp:731-736):
+// acc + v, then times oscale when scaled -- ggml_add(sum, r) and
+// ggml_scale, each one f32 rounding, in that order.  acc has y's (t, co)
+// layout; vector form (co % 4 == 0, 16-byte aligned rows).  The fields
+// come by value (a reference to the kernel argument would put the argument
+// block in scratch).
+__device__ __forceinline__ float4 sum_scale(float4 v, const char* acc, int64_t a_nb1, int64_t a_nb2, float oscale,
+                                            int32_t scaled, int bz, int t, int co) {
+    const float4 s4 = *reinterpret_cast<const float4*>(acc + static_cast<int64_t>(bz) * a_nb2 +
+                                                       static_cast<int64_t>(t) * a_nb1 + static_cast<int64_t>(co) * 4);
+    v = make_float4(s4.x + v.x, s4.y + v.y, s4.z + v.z, s4.w + v.w);
+    if (scaled) v = make_float4(v.x * oscale, v.y * oscale, v.z * oscale, v.w * oscale);
+    return v;
+}
 
 // PRO_MASK: x times a per-frame mask (the CFM causal block's pre-mask)
 enum { PRO_NONE = 0, PRO_SNAKE = 1, PRO_LEAKY = 2, PRO_MASK = 3 };
@@ -416,6 +435,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
                 float4 v = *reinterpret_cast<const float4*>(ep + rl * EPS + c4);
                 if (a.bias) v = make_float4(v.x + bv.x, v.y + bv.y, v.z + bv.z, v.w + bv.w);
                 if (a.res) v = make_float4(q[i].x + v.x, q[i].y + v.y, q[i].z + v.z, q[i].w + v.w);
+                if (a.acc) v = sum_scale(v, a.acc, a.a_nb1, a.a_nb2, a.oscale, a.scaled, bz, t, co4);
                 *reinterpret_cast<float4*>(a.y + yb + static_cast<int64_t>(t) * y_step + static_cast<int64_t>(co4) * 4) =
                     v;
             }
@@ -428,6 +448,11 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
                 float v = ep[rl * EPS + c];
                 if (a.bias) v = v + a.bias[co];
                 if (a.res) v = reinterpret_cast<const float*>(a.res + rb + static_cast<int64_t>(t) * r_step)[co] + v;
+                if (a.acc) {
+                    v = reinterpret_cast<const float*>(a.acc + static_cast<int64_t>(bz) * a.a_nb2 +
+                                                       static_cast<int64_t>(t) * a.a_nb1)[co] + v;
+                    if (a.scaled) v = v * a.oscale;
+                }
                 reinterpret_cast<float*>(a.y + yb + static_cast<int64_t>(t) * y_step)[co] = v;
             }
         }
@@ -616,6 +641,7 @@ __global__ __launch_bounds__(kPipeThreads) __attribute__((amdgpu_waves_per_eu(OC
                 float4 v = *reinterpret_cast<const float4*>(ep + rl * EPS + c4);
                 if (a.bias) v = make_float4(v.x + bv.x, v.y + bv.y, v.z + bv.z, v.w + bv.w);
                 if (a.res) v = make_float4(q[i].x + v.x, q[i].y + v.y, q[i].z + v.z, q[i].w + v.w);
+                if (a.acc) v = sum_scale(v, a.acc, a.a_nb1, a.a_nb2, a.oscale, a.scaled, bz, t, co);
                 *reinterpret_cast<float4*>(a.y + yb + static_cast<int64_t>(t) * a.y_nb1 +
                                            static_cast<int64_t>(co) * 4) = v;
             }
@@ -878,7 +904,7 @@ int launch_conv1d_weights(const cbx_tensor* w, int up, int64_t taps, _Float16* o
 int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c_in_pad, int64_t c_out, int stride,
                   int pad, int dil, int up, int crop, int64_t w_ph, int pro, const cbx_tensor* alpha,
                   const cbx_tensor* alpha_inv, float slope, const cbx_tensor* bias, const cbx_tensor* res, cbx_tensor* y,
-                  DeviceState* st, hipStream_t s) {
+                  DeviceState* st, hipStream_t s, const cbx_tensor* acc, float oscale) {
     ConvArgs a;
     a.x = static_cast<const char*>(x->data);
     a.w = w16;
@@ -893,6 +919,11 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     a.y_nb2 = static_cast<int64_t>(y->nb[2]);
     a.r_nb1 = res ? static_cast<int64_t>(res->nb[1]) : 0;
     a.r_nb2 = res ? static_cast<int64_t>(res->nb[2]) : 0;
+    a.acc = acc ? static_cast<const char*>(acc->data) : nullptr;
+    a.a_nb1 = acc ? static_cast<int64_t>(acc->nb[1]) : 0;
+    a.a_nb2 = acc ? static_cast<int64_t>(acc->nb[2]) : 0;
+    a.oscale = oscale;
+    a.scaled = acc && oscale != 1.0f;
     a.c_in = static_cast<int32_t>(x->ne[0]);
     a.c_in_pad = static_cast<int32_t>(c_in_pad);
     a.c_out = static_cast<int32_t>(c_out);
@@ -920,7 +951,8 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
         const bool one = x->ne[2] <= 1;
         const bool vec_in = al16(a.x) && a.x_nb1 % 16 == 0 && (one || a.x_nb2 % 16 == 0);
         const bool vec_out = al16(a.y) && a.y_nb1 % 16 == 0 && (one || a.y_nb2 % 16 == 0) && (!a.bias || al16(a.bias)) &&
-                             (!a.res || (al16(a.res) && a.r_nb1 % 16 == 0 && (one || a.r_nb2 % 16 == 0)));
+                             (!a.res || (al16(a.res) && a.r_nb1 % 16 == 0 && (one || a.r_nb2 % 16 == 0))) &&
+                             (!a.acc || (al16(a.acc) && a.a_nb1 % 16 == 0 && (one || a.a_nb2 % 16 == 0)));
         bool narrow = c_out % 128 != 0;   // 64-channel output tiles: 128 x 64, two a CU
         const int64_t n_cu = st->n_cu > 0 ? st->n_cu : 1;
         auto items_of = [&](int64_t bt, int64_t bc) {
@@ -1058,7 +1090,8 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     const bool one = x->ne[2] <= 1;
     a.vout = c_out % 4 == 0 && al16(a.y) && a.y_nb1 % 16 == 0 && (one || a.y_nb2 % 16 == 0) &&
-             (!a.bias || al16(a.bias)) && (!a.res || (al16(a.res) && a.r_nb1 % 16 == 0 && (one || a.r_nb2 % 16 == 0)));
+             (!a.bias || al16(a.bias)) && (!a.res || (al16(a.res) && a.r_nb1 % 16 == 0 && (one || a.r_nb2 % 16 == 0))) &&
+             (!a.acc || (al16(a.acc) && a.a_nb1 % 16 == 0 && (one || a.a_nb2 % 16 == 0)));
     a.n_tt = static_cast<int32_t>(cdiv(rows, t.bt()));
     a.n_ct = static_cast<int32_t>(cdiv(c_out, t.bc()));
     const int64_t n_items = static_cast<int64_t>(a.n_tt) * a.n_ct * batch;

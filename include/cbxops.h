@@ -421,6 +421,20 @@ int cbx_conv1d(const cbx_tensor* x, const cbx_conv1d_weights* w, int stride,
                const cbx_tensor* bias, const cbx_tensor* res, cbx_tensor* y,
                cbx_stream stream);
 
+/* cbx_conv1d with a HiFT stage's ResBlock sum folded into it
+ * (hift_vocoder.cpp:731-736: sum = ggml_add(sum, r), then x =
+ * ggml_scale(sum, 1/3) after the last resblock):
+ *   y = (acc + r) * scale,  r = cbx_conv1d's output (res required for the
+ * ResBlock's last conv; may be NULL)
+ * each step one f32 rounding in that order; scale 1.0f multiplies by
+ * nothing.  acc: F32 with y's shape, not overlapping y.                    */
+int cbx_conv1d_sum(const cbx_tensor* x, const cbx_conv1d_weights* w, int stride,
+                   int pad, int dilation, int prologue, const cbx_tensor* alpha,
+                   const cbx_tensor* alpha_inv, float slope,
+                   const cbx_tensor* bias, const cbx_tensor* res,
+                   const cbx_tensor* acc, float scale, cbx_tensor* y,
+                   cbx_stream stream);
+
 /* Weights of one transposed conv1d with stride `stride` (the HiFT
  * upsamplers' ups.i, hift_vocoder.cpp:96-115, 255-259): a ggml (K, C_out,
  * C_in) F32/F16 weight (PyTorch ConvTranspose1d's (C_in, C_out, K) order)
@@ -699,7 +713,10 @@ typedef struct cbx_glaunch {
                              storing (the embedding sum h nobody reads).
                              Conv kinds: bits 0-1 the prologue (0 none, 1
                              snake, 2 leaky_relu, 3 the frame mask), bit 2 a
-                             bias add, bit 3 the residual add.                  */
+                             bias add, bit 3 the residual add; CONV1D also
+                             bit 4 an add of another tensor after the
+                             residual add and bit 5 a scale after that (the
+                             ResBlock sum and mean, cbx_conv1d_sum).          */
 } cbx_glaunch;
 
 /* Splits nodes[0..n_nodes) into launches, in order, covering every node

@@ -48,6 +48,28 @@ def check(oracle, got, x, w, stride, pad, dil, pro, alpha, alpha_inv, slope, bia
                            f"{float((d - bound).max()):.3g} (d {float(d.max()):.3g})")
 
 
+def check_sum(oracle, got, x, w, stride, pad, dil, pro, alpha, alpha_inv, slope, bias, res, acc, scale, what):
+    """(acc + r) * scale against the oracle's conv r: the conv bound on r,
+    scaled, plus the two f32 roundings of the sum and the scale
+    (2^-22 |exp| covers both, one ulp of |exp| on each side)."""
+    ref = oracle.conv1d(x, w, stride, pad, dil, pro, alpha, alpha_inv, slope, bias, res, nth=8)
+    s = np.float32(scale)
+    exp = oracle.add(acc, ref) * s if scale != 1.0 else oracle.add(acc, ref)
+    if pro == oracle.CONV_PRO_SNAKE:
+        h = oracle.snake(x, alpha, alpha_inv)
+    elif pro == oracle.CONV_PRO_LEAKY:
+        h = oracle.leaky_relu(x, slope)
+    else:
+        h = x
+    mag = oracle.conv1d(np.abs(h), np.abs(w), stride, pad, dil, nth=8).astype(np.float64)
+    d = np.abs(got.astype(np.float64) - exp.astype(np.float64))
+    bound = abs(float(s)) * (2.0 ** -13 * mag + 2.0 ** -22 * np.abs(ref)) + 2.0 ** -22 * np.abs(exp)
+    assert got.shape == exp.shape, what
+    bad = d > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {got.size} outside the bound; worst excess "
+                           f"{float((d - bound).max()):.3g}")
+
+
 def case(oracle, C, T, C_out, K, stride, pad, dil, pro, with_bias=True, with_res=False, B=None, seed=0, w_f16=False,
          slope=0.1):
     sd = W.seed_of(11, seed)
@@ -382,4 +404,43 @@ def test_pipelined_in_place_residual(cbx, oracle):
     y = cbx.conv1d(dev(x), wts, 1, 3, 1, cbx.CONV_PRO_SNAKE, dev(al), dev(ai), sl, dev(b), rd, out=rd)
     assert y is rd
     check(oracle, host(rd), x, w, 1, 3, 1, oracle.CONV_PRO_SNAKE, al, ai, sl, b, r, "pipelined y == res")
+    wts.close()
+
+
+SUM = [  # (C_in, C_out, T, B, K, dilation, scale): the conv kernels the sum rides on
+    (256, 256, 400, None, 3, 1, 1.0 / 3.0),          # k_conv1d, float4 epilogue
+    (128, 128, 48000, None, 11, 1, 1.0),             # k_conv1d_pipe (96 x 128 tiles), the sum alone
+    (64, 128, 300, 96, 11, 5, 1.0 / 3.0),            # k_conv1d_pipe on a batch
+    (64, 18, 500, None, 7, 1, 1.0 / 3.0),            # 18 channels out: the scalar epilogue
+]
+
+
+@pytest.mark.parametrize("C,C_out,T,B,K,dil,scale", SUM)
+def test_conv1d_sum(cbx, oracle, C, C_out, T, B, K, dil, scale):
+    """cbx_conv1d_sum: a ResBlock's last conv with the stage's sum and mean
+    folded in, (acc + (res + conv)) * scale, against the oracle's conv, add
+    and f32 scale."""
+    pad = (K - 1) // 2 * dil
+    x, w, al, ai, b, r, sl = case(oracle, C, T, C_out, K, 1, pad, dil, oracle.CONV_PRO_SNAKE, with_res=True, B=B,
+                                  seed=K + 7)
+    acc = W.normal(W.seed_of(12, K), r.shape, 0.0, 2.0)
+    wts = cbx.Conv1dWeights(dev(w))
+    got = host(cbx.conv1d_sum(dev(x), wts, 1, pad, dil, cbx.CONV_PRO_SNAKE, dev(al), dev(ai), 0.0, dev(b), dev(r),
+                              dev(acc), scale))
+    wts.close()
+    check_sum(oracle, got, x, w, 1, pad, dil, oracle.CONV_PRO_SNAKE, al, ai, sl, b, r, acc, scale,
+              f"sum C{C}->{C_out} T{T} B{B} K{K} d{dil} scale {scale}")
+
+
+def test_conv1d_sum_refusals(cbx):
+    x = dev(np.zeros((50, 16), np.float32))
+    wts = cbx.Conv1dWeights(dev(np.zeros((16, 16, 3), np.float32)))
+    y = torch.zeros((50, 16), device="cuda")
+    with pytest.raises(cbx.CbxError, match="acc is NULL"):
+        cbx.conv1d_sum(x, wts, 1, 1, 1, cbx.CONV_PRO_NONE, None, None, 0.0, None, None, None, 1.0, out=y)
+    with pytest.raises(cbx.CbxError, match="acc must not overlap y"):
+        cbx.conv1d_sum(x, wts, 1, 1, 1, cbx.CONV_PRO_NONE, None, None, 0.0, None, None, y, 1.0, out=y)
+    with pytest.raises(cbx.CbxError, match="acc must be F32 with y's shape"):
+        cbx.conv1d_sum(x, wts, 1, 1, 1, cbx.CONV_PRO_NONE, None, None, 0.0, None, None,
+                       torch.zeros((49, 16), device="cuda"), 1.0, out=y)
     wts.close()

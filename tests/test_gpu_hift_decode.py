@@ -2,9 +2,10 @@
 host STFT and iSTFT; chatterbox_amdvulkan_amd/hift_decode.py) run launch by
 launch, each launch checked against the oracle on the inputs it read from
 the device: the conv bar for the 77 conv1d_CT and 3 conv_transpose1d_CT
-launches (f16 operands, f32 sums: |d| <= 2^-13 sum |a b| + 2^-22 |ref|),
-bit-exact for the adds, the resblock mean's scale, the pad's copy and its
-concat.  Then the whole list through cbx_graph_compute and a captured
+launches (f16 operands, f32 sums: |d| <= 2^-13 sum |a b| + 2^-22 |ref|;
+with the resblock sum and mean folded into a conv, that bound scaled plus
+the two f32 roundings), bit-exact for the source joins, the pad's copy and
+its concat.  Then the whole list through cbx_graph_compute and a captured
 cbx_graph_exec: the same output bits."""
 import numpy as np
 import pytest
@@ -14,6 +15,7 @@ from chatterbox_amdvulkan_amd import cbxops as C
 from chatterbox_amdvulkan_amd.hift_decode import HiFTDecode
 from tests._util import assert_bitexact
 from tests.test_gpu_conv1d import check as check_conv
+from tests.test_gpu_conv1d import check_sum
 from tests.test_gpu_conv_transpose1d import check as check_convt
 
 pytestmark = pytest.mark.gpu
@@ -40,13 +42,21 @@ def check_launch(e, oracle, launch, k):
     got = H(y)
     assert np.isfinite(got).all(), what
     if kind == C.GL_CONV1D:
-        r = e.conv_ref[y]
+        extra = (1 if flags & C.GLF_SUM else 0) + (1 if flags & C.GLF_SCALE else 0)
+        rout = nd[f + n - 1 - extra].dst           # the residual add's result: the recorded chain's end
+        r = e.conv_ref[rout]
         x = H2(r["x"])
         pro = {"snake": oracle.CONV_PRO_SNAKE, "leaky": oracle.CONV_PRO_LEAKY, None: oracle.CONV_PRO_NONE}[r["pro"]]
         a, ai = (H(r["alpha"][0]), H(r["alpha"][1])) if r["pro"] == "snake" else (None, None)
         res = H2(r["res"]) if r["res"] is not None else None
-        check_conv(oracle, got.reshape(-1, got.shape[-1]), x, H(r["w"]), r["stride"], r["pad"], r["dil"], pro, a, ai,
-                   r["slope"], H(r["bias"]), res, what)
+        args = (x, H(r["w"]), r["stride"], r["pad"], r["dil"], pro, a, ai, r["slope"], H(r["bias"]), res)
+        if not extra:
+            check_conv(oracle, got.reshape(-1, got.shape[-1]), *args, what)
+        else:
+            sa = nd[f + n - extra]                 # add(sum so far, r)
+            acc = H2(sa.src[0] if sa.src[1] == rout else sa.src[1])
+            scale = nd[f + n - 1].fparam if flags & C.GLF_SCALE else 1.0
+            check_sum(oracle, got.reshape(-1, got.shape[-1]), *args, acc, scale, what + " (with the resblock sum)")
     elif kind == C.GL_CONV_TRANSPOSE1D:
         r = e.conv_ref[y]
         check_convt(oracle, got.reshape(-1, got.shape[-1]), H2(r["x"]), H(r["w"]), r["stride"], r["pad"],

@@ -21,9 +21,7 @@ def test_plan_counts(T_mel):
         # 3 x 6 resblock convs; conv_post -- 72 of them behind a snake
         "GL_CONV1D": 1 + 3 * (1 + 6 + 18) + 1,
         "GL_CONV_TRANSPOSE1D": 3,            # leaky_relu -> ups[i] + bias
-        # per stage add(x, source) and the two adds of the resblock sum
-        "GL_BINARY": 3 * 3,
-        "GL_SCALE": 3,                       # the resblock mean
+        "GL_BINARY": 3,                      # per stage add(x, source)
         "GL_VIEW": 1, "GL_CPY": 1, "GL_CONCAT": 1,   # stage 2's reflection pad
     }
     assert sum(p[2] for p in plan) == len(e.graph.nodes)
@@ -31,10 +29,16 @@ def test_plan_counts(T_mel):
     assert sum(1 for fl in flags if fl & 3 == C.GLF_SNAKE) == 72
     assert sum(1 for fl in flags if fl & C.GLF_RESIDUAL) == 36      # every layer's second conv
     assert all(fl & C.GLF_BIAS for fl in flags)
+    # the resblock sums ride on the last conv of resblocks 1 and 2 of each
+    # stage, the mean (scale 1/3) on resblock 2's
+    assert sum(1 for fl in flags if fl & C.GLF_SUM) == 6
+    assert sum(1 for fl in flags if fl & C.GLF_SCALE) == 3
+    assert all(fl & C.GLF_RESIDUAL for fl in flags if fl & C.GLF_SUM)
     assert all(p[3] == C.GLF_LEAKY | C.GLF_BIAS for p in plan if p[0] == C.GL_CONV_TRANSPOSE1D)
     # every conv launch ends in a tensor whose chain was recorded
     nd = e.graph.nodes
-    ends = {nd[f + n - 1].dst for k, f, n, _ in plan if k in (C.GL_CONV1D, C.GL_CONV_TRANSPOSE1D)}
+    extra = lambda fl: (1 if fl & C.GLF_SUM else 0) + (1 if fl & C.GLF_SCALE else 0)  # noqa: E731
+    ends = {nd[f + n - 1 - extra(fl)].dst for k, f, n, fl in plan if k in (C.GL_CONV1D, C.GL_CONV_TRANSPOSE1D)}
     assert ends == set(e.conv_ref)
 
 
