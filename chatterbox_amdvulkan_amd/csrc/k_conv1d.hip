@@ -77,15 +77,10 @@ struct ConvArgs {
 };
 
 // The ResBlock sum after the residual add (hift_vocoder.cpp:731-736):
-// acc + v, then times oscale when scaled -- ggml_add(sum, r) and
-// ggml_scale, each one f32 rounding, in that order.  acc has y's (t, co)
-// layout; vector form (co % 4 == 0, 16-byte aligned rows).  The fields
-// come by value (a reference to the kernel argument would put the argument
-// block in scratch).
-__device__ __forceinline__ float4 sum_scale(float4 v, const char* acc, int64_t a_nb1, int64_t a_nb2, float oscale,
-                                            int32_t scaled, int bz, int t, int co) {
-    const float4 s4 = *reinterpret_cast<const float4*>(acc + static_cast<int64_t>(bz) * a_nb2 +
-                                                       static_cast<int64_t>(t) * a_nb1 + static_cast<int64_t>(co) * 4);
+// s4 (acc's float4, read with the residual's) + v, then times oscale when
+// scaled -- ggml_add(sum, r) and ggml_scale, each one f32 rounding, in
+// that order.  acc has y's (t, co) layout.
+__device__ __forceinline__ float4 sum_scale(float4 v, float4 s4, float oscale, int32_t scaled) {
     v = make_float4(s4.x + v.x, s4.y + v.y, s4.z + v.z, s4.w + v.w);
     if (scaled) v = make_float4(v.x * oscale, v.y * oscale, v.z * oscale, v.w * oscale);
     return v;
@@ -423,6 +418,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
                                                         static_cast<int64_t>(cok ? co4 : 0) * 4);
             }
         }
+
         __syncthreads();
     }
     if (a.vout) {
@@ -435,7 +431,16 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
                 float4 v = *reinterpret_cast<const float4*>(ep + rl * EPS + c4);
                 if (a.bias) v = make_float4(v.x + bv.x, v.y + bv.y, v.z + bv.z, v.w + bv.w);
                 if (a.res) v = make_float4(q[i].x + v.x, q[i].y + v.y, q[i].z + v.z, q[i].w + v.w);
-                if (a.acc) v = sum_scale(v, a.acc, a.a_nb1, a.a_nb2, a.oscale, a.scaled, bz, t, co4);
+                // the ResBlock sum so far (stride-1 convs: y's rows), read here:
+                // held from before the barrier like q it would cost the large
+                // tiles an occupancy step, sum or not
+                if (a.acc) {
+                    v = sum_scale(v,
+                                  *reinterpret_cast<const float4*>(a.acc + static_cast<int64_t>(bz) * a.a_nb2 +
+                                                                   static_cast<int64_t>(t) * a.a_nb1 +
+                                                                   static_cast<int64_t>(co4) * 4),
+                                  a.oscale, a.scaled);
+                }
                 *reinterpret_cast<float4*>(a.y + yb + static_cast<int64_t>(t) * y_step + static_cast<int64_t>(co4) * 4) =
                     v;
             }
@@ -620,7 +625,7 @@ __global__ __launch_bounds__(kPipeThreads) __attribute__((amdgpu_waves_per_eu(OC
             __syncthreads();
         }
         // the last chunk's turn: nothing to stage, the residual is read
-        float4 q[NIT];
+        float4 q[NIT], q2[NIT];
         if (a.res) {
 #pragma unroll
             for (int i = 0; i < NIT; i++) {
@@ -628,6 +633,15 @@ __global__ __launch_bounds__(kPipeThreads) __attribute__((amdgpu_waves_per_eu(OC
                 const int tc = t < a.t_out ? t : a.t_out - 1;
                 q[i] = *reinterpret_cast<const float4*>(a.res + rb + static_cast<int64_t>(tc) * a.r_nb1 +
                                                         static_cast<int64_t>(co) * 4);
+            }
+        }
+        if (a.acc) {   // the ResBlock sum so far, read with the residual
+#pragma unroll
+            for (int i = 0; i < NIT; i++) {
+                const int t = t0 + rl0 + i * (NPT / C4);
+                const int tc = t < a.t_out ? t : a.t_out - 1;
+                q2[i] = *reinterpret_cast<const float4*>(a.acc + static_cast<int64_t>(bz) * a.a_nb2 +
+                                                         static_cast<int64_t>(tc) * a.a_nb1 + static_cast<int64_t>(co) * 4);
             }
         }
         __syncthreads();
@@ -641,7 +655,7 @@ __global__ __launch_bounds__(kPipeThreads) __attribute__((amdgpu_waves_per_eu(OC
                 float4 v = *reinterpret_cast<const float4*>(ep + rl * EPS + c4);
                 if (a.bias) v = make_float4(v.x + bv.x, v.y + bv.y, v.z + bv.z, v.w + bv.w);
                 if (a.res) v = make_float4(q[i].x + v.x, q[i].y + v.y, q[i].z + v.z, q[i].w + v.w);
-                if (a.acc) v = sum_scale(v, a.acc, a.a_nb1, a.a_nb2, a.oscale, a.scaled, bz, t, co);
+                if (a.acc) v = sum_scale(v, q2[i], a.oscale, a.scaled);
                 *reinterpret_cast<float4*>(a.y + yb + static_cast<int64_t>(t) * a.y_nb1 +
                                            static_cast<int64_t>(co) * 4) = v;
             }
