@@ -1040,14 +1040,20 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     // and the CFM decoder's shapes this picks the fastest tile or one within
     // 3% of it.
     int ti = 4;
-    if (c_out > 32) {
-        static constexpr int kWide[5] = {1, 5, 2, 3, 8}, kNarrow[5] = {0, 6, 7, 3, 8};
-        const int* cand = c_out <= 64 ? kNarrow : kWide;
+    {
+        // outputs of up to 32 channels: 256 x 32 or 32 x 32 tiles (conv_post,
+        // 64 -> 18 channels: 12.1 against 16.0 us on 60001 frames, 7.8
+        // against 15.3 us on 2000, on 32 x 32).  (256 x 32 tiles for the 64-
+        // channel upsampler: 18.1 against 21.0 us on 20000 frames in, 27.8
+        // against 21.8 us on 30000 -- two uneven rounds -- not taken.)
+        static constexpr int kWide[5] = {1, 5, 2, 3, 8}, kNarrow[5] = {0, 6, 7, 3, 8}, kOne[2] = {4, 9};
+        const int* cand = c_out <= 32 ? kOne : c_out <= 64 ? kNarrow : kWide;
+        const int n_cand = c_out <= 32 ? 2 : 5;
         const double n_cu = st->n_cu > 0 ? st->n_cu : 1;
         const double avg = static_cast<double>(rows) * static_cast<double>(c_out) * static_cast<double>(batch) / n_cu;
         double best = -1.0;
-        ti = 3;
-        for (int c = 0; c < 5; c++) {
+        ti = c_out <= 32 ? 4 : 3;
+        for (int c = 0; c < n_cand; c++) {
             const Tile& t = kTiles[cand[c]];
             if (!fits(win_of(t))) continue;
             const double n = static_cast<double>(n_wg(t));
