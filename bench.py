@@ -1352,7 +1352,7 @@ def counters_summary(W, title, command, *dirs):
         g = _group_medians(W, d)
         per = g if per is None else [(a[0], a[1], a[2], a[3], {**a[4], **b[4]}) for a, b in zip(per, g)]
     names = sorted({c for p in per for c in p[4]})
-    out = [f"# {title}", "", "Command (one MI355X):", "", "```", "cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT",
+    out = [f"# {title}", "", "Command (one MI355X):", "", "```", f"cd /tmp && export TMPDIR=/tmp && cd {ROOT}",
            command, "```", "", "Median over each group's launches (one launch per buffer set; groups as "
            "`traffic_groups()` in bench.py).", "",
            "| workload | kernel | " + " | ".join(names) + " |", "|---|---|" + "---|" * len(names)]
@@ -1437,12 +1437,12 @@ def traffic_summary(W, fetch_dir, write_dir):
     out = ["# HBM traffic per launch of every configuration's kernels (FETCH_SIZE, WRITE_SIZE)", "",
            "Two `rocprofv3 --pmc` passes on one MI355X over the same probe (a 64 MiB f32 copy of known size, then",
            "each kernel's launches on their own buffer sets; the groups are `traffic_groups()` in bench.py):", "",
-           "```", "cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT",
-           "timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch -o run -- "
+           "```", f"cd /tmp && export TMPDIR=/tmp && cd {ROOT}",
+           f"timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE --output-format csv -d {fetch_dir} -o run -- "
            "python -u bench.py --traffic-probe",
-           "timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write -o run -- "
+           f"timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE --output-format csv -d {write_dir} -o run -- "
            "python -u bench.py --traffic-probe",
-           "python bench.py --traffic-summary gpurun_out/pmc_fetch gpurun_out/pmc_write", "```", "",
+           f"python bench.py --traffic-summary {fetch_dir} {write_dir}", "```", "",
            f"Calibration: the copy moves {copy_kib:.0f} KiB each way; FETCH_SIZE reads {per[0][4]:.1f} KiB for it "
            f"and WRITE_SIZE {per[0][5]:.1f}, so reads are scaled by {f_scale:.4f} and writes by {w_scale:.4f}.", "",
            "| workload | kernel | launches | FETCH_SIZE KiB | WRITE_SIZE KiB | algorithmic bytes | traffic bytes | ratio |",
@@ -1464,7 +1464,7 @@ def stats_summary(stats_dir, title, command):
     f = sorted(glob.glob(os.path.join(stats_dir, "**", "*kernel_stats.csv"), recursive=True))[0]
     rows = [r for r in csv.DictReader(open(f)) if "cbx::" in r["Name"]]
     rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
-    out = [f"# {title}", "", "Command (one MI355X):", "", "```", "cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT",
+    out = [f"# {title}", "", "Command (one MI355X):", "", "```", f"cd /tmp && export TMPDIR=/tmp && cd {ROOT}",
            command, "```", "", "Kernels of libcbxops (rocprofv3 kernel stats; durations in microseconds):", "",
            "| kernel | calls | average | min | max |", "|---|---|---|---|---|"]
     for r in rows:

@@ -4,8 +4,9 @@ configurations' shapes and over every f16-representable input: the maximum
 relative error, the share of bit-identical results, and how many elements
 need the absolute floor 2^-22 |x| of the test bar because their error
 exceeds 1e-5 |exp|.  Each measurement is printed (pytest -s shows the table)
-and held to the bar of tests/_util.py; the relative part alone (north_star's
-1e-5) is asserted for every op whose formula does not cancel."""
+and held to the bar of tests/_util.py; the relative part alone (1e-5, the
+f32 tolerance of the path) is asserted for every op whose formula does not
+cancel."""
 import numpy as np
 import pytest
 import torch
