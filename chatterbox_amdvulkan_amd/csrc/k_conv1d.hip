@@ -302,9 +302,13 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
         const int a_wrap = a.dil * cs - nb * kBlk;            // (k, nb) -> (k + 1, 0)
         const int64_t b_wrap = static_cast<int64_t>(nblk - nb) * 512;
         const int64_t b_first = static_cast<int64_t>(cb0) * 512;
-        // this wave's share: n_w consecutive steps (mod n_steps) from its start
-        const int n_w = n_steps / KS;
-        const int s_start = static_cast<int>((j8 * 3u + static_cast<unsigned>(ks * n_w)) % static_cast<unsigned>(n_steps));
+        // this wave's share: n_w consecutive steps (mod n_steps) from its
+        // start -- steps [s_lo, s_lo + n_w) of the chunk's, the KS shares as
+        // even as the count allows (they differ by at most one; an odd share
+        // runs its last step after the paired ones, PF 2 only)
+        const int s_lo = ks * n_steps / KS;
+        const int n_w = (ks + 1) * n_steps / KS - s_lo;
+        const int s_start = static_cast<int>((j8 * 3u + static_cast<unsigned>(s_lo)) % static_cast<unsigned>(n_steps));
         const int k_start = s_start / nb, cb_start = s_start - k_start * nb;
         const int a_start = k_start * a.dil * cs + cb_start * kBlk;
         const int64_t b_start = (static_cast<int64_t>(k_start) * nblk + cb0 + cb_start) * 512;
@@ -344,7 +348,8 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) av[0][mt] = *reinterpret_cast<const half8*>(lds + arow[mt] + aoff);
         next_a();
-        for (int s0 = 0; s0 < n_w; s0 += PF) {
+        const int n_pair = n_w - n_w % PF;   // the steps the ring runs in whole groups
+        for (int s0 = 0; s0 < n_pair; s0 += PF) {
 #pragma unroll
             for (int p = 0; p < PF; p++) {
                 const int s = s0 + p;
@@ -367,6 +372,20 @@ __global__ __launch_bounds__(64 * WM * WN * KS) __attribute__((amdgpu_waves_per_
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) ring[p][nt] = *reinterpret_cast<const half8*>(wf[nt] + bn);
                 next_b();
+            }
+        }
+        if constexpr (PF == 2) {
+            // an odd share's last step: its A came in av[0] and its B in
+            // ring[0] with the last pair (n_w is wave-uniform)
+            if (n_w & 1) {
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++) {
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[0][mt], ring[0][nt], acc[mt][nt], 0,
+                                                                             0, 0);
+                    }
+                }
             }
         }
     }
@@ -1082,9 +1101,7 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
     const int64_t kch_lds = std::min<int64_t>(
         (static_cast<int64_t>(kLdsMax) / (win * 2 + 8) - 8) / kChanAlign * kChanAlign, c_in_pad);
     const Tile& t = kTiles[ti];
-    // waves per wave tile: the most (ks, ks/2, .., 1) whose share of every
-    // chunk's steps (K * channels / 16) is even -- a multiple of 4 for the
-    // 4-deep ring (with ks = 1 it always is: chunks are multiples of 32)
+    // waves per wave tile (ks) and the chunks' steps (K * channels / 16)
     int64_t kch = 0, n_full = 0, n_last = 0;
     auto plan_chunks = [&](int ks_) {
         kch = std::min<int64_t>(kch_lds, 4 * 64 * t.wm * t.wn * ks_);
@@ -1093,9 +1110,19 @@ int launch_conv1d(const cbx_tensor* x, const _Float16* w16, int64_t k, int64_t c
         n_last = k * (last / kBlk);
     };
     auto steps_ok = [&](int ks_, int pf) { return n_full % (ks_ * pf) == 0 && n_last % (ks_ * pf) == 0; };
+    // fewer waves while a chunk's steps split unevenly into shares under 8:
+    // the shares may be uneven (differ by one) on the 2-deep ring, and are
+    // equal multiples of 4 on the 4-deep one.  Long uneven shares keep the
+    // waves (conv_pre, 80 input channels, 42 steps: 11.5 -> 6.7 us on four
+    // waves against one; the CFM decoder's 320-channel causal conv, 60: 10.6
+    // -> 7.6 us against two); short ones do not pay for the partial-sum
+    // exchange (conv_post, 28 steps: 12.4 us on two waves, 14.2 on four)
     int ks = t.ks;
     plan_chunks(ks);
-    while (ks > 1 && !steps_ok(ks, 2)) plan_chunks(ks /= 2);
+    while (ks > 1 && (std::min(n_full, n_last) < 2 * ks ||
+                      (!steps_ok(ks, 2) && std::min(n_full, n_last) < 8 * ks))) {
+        plan_chunks(ks /= 2);
+    }
     const bool pf4 = steps_ok(ks, 4);
     a.win = static_cast<int32_t>(win);
     a.kch = static_cast<int32_t>(kch);
