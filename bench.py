@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--hift-conv", action="store_true",
                     help="only the HiFT conv1d / transposed-conv timings, as one JSON object (for profiling)")
     ap.add_argument("--only", choices=["decode", "serving", "cfm", "hift", "softmax", "t3_block", "t3_token", "hift_conv",
-                                       "cfm_estimator", "hift_decode", "copy"],
+                                       "cfm_estimator", "hift_decode", "s3_encoder", "copy"],
                     help="run one secondary workload alone and print its JSON (no headline line)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the markdown summary of two --pmc runs over --traffic-probe (no GPU)")
@@ -875,6 +875,61 @@ def bench_cfm_estimator(C, torch, T=500, reps=20):
         e.close()
 
 
+def bench_s3_encoder(C, torch, T_mel=1000, reps=20):
+    """One S3 speech-tokenizer encoder call's element-wise nodes
+    (s3enc.cpp:124-290: the front convs' bias + GELU-erf, 6 layers' LayerNorms,
+    q / k RoPE, FSMN join, score softmax, bias + residual joins, bias +
+    GELU-erf; matmul, conv and FSMN outputs given) over T_mel mel frames,
+    planned into one list of launches (chatterbox_amdvulkan_amd/
+    s3_encoder.py).  Device time per call from back-to-back replays of the
+    list captured into a HIP graph (cbx_graph_exec), and the same list
+    planned and launched each call (cbx_graph_compute)."""
+    from chatterbox_amdvulkan_amd.s3_encoder import S3EncoderCall
+
+    e = S3EncoderCall(T_mel, seed=5)
+    try:
+        plan = e.plan()
+        ex = e.graph.capture(e.keep)
+        s = cur_stream(torch)
+        nbytes = estimator_bytes(C, e, plan)
+        kinds = {}
+        names = {v: k[3:].lower() for k, v in vars(C).items() if k.startswith("GL_") and isinstance(v, int)}
+        for p in plan:
+            if p[0] != C.GL_VIEW:
+                kinds[names[p[0]]] = kinds.get(names[p[0]], 0) + 1
+        out = {"reference_sequence": f"s3enc.cpp:124-290, T_mel {T_mel} ({e.T_tok} tokens), {e.n_layer} layers",
+               "launches": ex.n_launches, "launches_by_kind": kinds, "bytes_per_call": nbytes}
+        for _ in range(3):
+            ex.launch(s)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            ex.launch(s)
+        e1.record()
+        torch.cuda.synchronize()
+        dev_us = e0.elapsed_time(e1) * 1000.0 / reps
+        out["exec_replay_us_per_call"] = dev_us
+        out["exec_replay_us_per_launch"] = dev_us / ex.n_launches
+        out["GBps"] = nbytes / (dev_us * 1e-6) / 1e9
+        ex.close()
+        for _ in range(2):
+            e.graph.compute(e.keep)
+        torch.cuda.synchronize()
+        n_c = max(5, reps // 4)
+        tm = time.perf_counter()
+        e0.record()
+        for _ in range(n_c):
+            e.graph.compute(e.keep)
+        host = (time.perf_counter() - tm) / n_c * 1e6
+        e1.record()
+        torch.cuda.synchronize()
+        out["graph_compute_us_per_call"] = {"host_us": host, "device_us": e0.elapsed_time(e1) * 1000.0 / n_c}
+        return out
+    finally:
+        e.close()
+
+
 def bench_hift_decode(C, torch, T_mel=500, reps=10):
     """One HiFT vocoder decode (hift_vocoder.cpp:613-749: conv_pre, the three
     upsampling stages with their source convs and resblocks, conv_post; the
@@ -1626,6 +1681,7 @@ def main():
               "t3_token": lambda: bench_t3_token(C, W, torch),
               "cfm_estimator": lambda: bench_cfm_estimator(C, torch),
               "hift_decode": lambda: bench_hift_decode(C, torch),
+              "s3_encoder": lambda: bench_s3_encoder(C, torch),
               "hift_conv": lambda: bench_hift_conv(C, W, torch),
               "copy": lambda: bench_copy_ceiling(C, torch, {"gelu_bytes": nb["gelu"],
                                                             "embed_layer_norm_bytes": nb["embed_layer_norm"],
@@ -1676,6 +1732,8 @@ def main():
         details["cfm_estimator_elementwise"] = bench_cfm_estimator(C, torch)
         log("hift decode")
         details["hift_decode"] = bench_hift_decode(C, torch)
+        log("s3 encoder")
+        details["s3_encoder_elementwise"] = bench_s3_encoder(C, torch)
         log("hift conv")
         details["hift_resblock_conv"] = bench_hift_conv(C, W, torch)
     k_ms = res["kernel_ms"]["run_ops"]
@@ -1734,6 +1792,11 @@ def main():
         out["cfm_estimator_us_per_call"] = {"reference_sequence": ce["reference_sequence"] +
                                             f", {ce['launches']} launches",
                                             "exec_replay": round(ce["exec_replay_us_per_call"], 2)}
+    if "s3_encoder_elementwise" in details:
+        se = details["s3_encoder_elementwise"]
+        out["s3_encoder_us_per_call"] = {"reference_sequence": se["reference_sequence"] +
+                                         f", {se['launches']} launches",
+                                         "exec_replay": round(se["exec_replay_us_per_call"], 2)}
     if "hift_decode" in details:
         hd = details["hift_decode"]
         out["hift_decode_us_per_call"] = {"reference_sequence": hd["reference_sequence"] +
