@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--hift-conv", action="store_true",
                     help="only the HiFT conv1d / transposed-conv timings, as one JSON object (for profiling)")
     ap.add_argument("--only", choices=["decode", "serving", "cfm", "hift", "softmax", "t3_block", "t3_token", "hift_conv",
-                                       "cfm_estimator", "hift_decode", "s3_encoder", "copy"],
+                                       "cfm_estimator", "hift_decode", "s3_encoder", "flow_encoder", "copy"],
                     help="run one secondary workload alone and print its JSON (no headline line)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the markdown summary of two --pmc runs over --traffic-probe (no GPU)")
@@ -798,9 +798,10 @@ def bench_t3_token(C, W, torch, reps=200, tokens=64):
 
 
 def estimator_bytes(C, e, plan):
-    """Bytes one estimator call's launches move: per launch, every tensor it
+    """Bytes one node-list call's launches move: per launch, every tensor it
     reads from outside the launch once (a causal conv's weights as their
-    prepared f16 copy) and every tensor it stores."""
+    prepared f16 copy, a gather's table as the rows it gathers) and every
+    tensor it stores."""
     nd, at = e.graph.nodes, e.b.at
     total = 0
     for kind, f, n, flags in plan:
@@ -812,6 +813,9 @@ def estimator_bytes(C, e, plan):
             w = nd[f + 7].src[0]          # the weight tensor of the im2col node
             reads.discard(w)
             total += at(w).numel() * 2
+        if kind == C.GL_GET_ROWS:         # the gathered rows, not the whole table
+            reads.discard(nd[f].src[0])
+            total += at(nd[f].dst).numel() * at(nd[f].dst).element_size()
         total += sum(at(s).numel() * at(s).element_size() for s in reads)
         y = at(nd[f + n - 1].dst)
         total += y.numel() * y.element_size()
@@ -875,59 +879,81 @@ def bench_cfm_estimator(C, torch, T=500, reps=20):
         e.close()
 
 
+def bench_node_list(C, torch, e, ref, reps):
+    """Device time per call of a reference-sequence node list e (its graph,
+    keep list and plan) from back-to-back replays of the list captured into
+    a HIP graph (cbx_graph_exec), and the same list planned and launched each
+    call (cbx_graph_compute)."""
+    plan = e.plan()
+    ex = e.graph.capture(e.keep)
+    s = cur_stream(torch)
+    nbytes = estimator_bytes(C, e, plan)
+    kinds = {}
+    names = {v: k[3:].lower() for k, v in vars(C).items() if k.startswith("GL_") and isinstance(v, int)}
+    for p in plan:
+        if p[0] != C.GL_VIEW:
+            kinds[names[p[0]]] = kinds.get(names[p[0]], 0) + 1
+    out = {"reference_sequence": ref, "launches": ex.n_launches, "launches_by_kind": kinds,
+           "bytes_per_call": nbytes}
+    for _ in range(3):
+        ex.launch(s)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        ex.launch(s)
+    e1.record()
+    torch.cuda.synchronize()
+    dev_us = e0.elapsed_time(e1) * 1000.0 / reps
+    out["exec_replay_us_per_call"] = dev_us
+    out["exec_replay_us_per_launch"] = dev_us / ex.n_launches
+    out["GBps"] = nbytes / (dev_us * 1e-6) / 1e9
+    ex.close()
+    for _ in range(2):
+        e.graph.compute(e.keep)
+    torch.cuda.synchronize()
+    n_c = max(5, reps // 4)
+    tm = time.perf_counter()
+    e0.record()
+    for _ in range(n_c):
+        e.graph.compute(e.keep)
+    host = (time.perf_counter() - tm) / n_c * 1e6
+    e1.record()
+    torch.cuda.synchronize()
+    out["graph_compute_us_per_call"] = {"host_us": host, "device_us": e0.elapsed_time(e1) * 1000.0 / n_c}
+    return out
+
+
 def bench_s3_encoder(C, torch, T_mel=1000, reps=20):
     """One S3 speech-tokenizer encoder call's element-wise nodes
     (s3enc.cpp:124-290: the front convs' bias + GELU-erf, 6 layers' LayerNorms,
     q / k RoPE, FSMN join, score softmax, bias + residual joins, bias +
     GELU-erf; matmul, conv and FSMN outputs given) over T_mel mel frames,
     planned into one list of launches (chatterbox_amdvulkan_amd/
-    s3_encoder.py).  Device time per call from back-to-back replays of the
-    list captured into a HIP graph (cbx_graph_exec), and the same list
-    planned and launched each call (cbx_graph_compute)."""
+    s3_encoder.py)."""
     from chatterbox_amdvulkan_amd.s3_encoder import S3EncoderCall
 
     e = S3EncoderCall(T_mel, seed=5)
     try:
-        plan = e.plan()
-        ex = e.graph.capture(e.keep)
-        s = cur_stream(torch)
-        nbytes = estimator_bytes(C, e, plan)
-        kinds = {}
-        names = {v: k[3:].lower() for k, v in vars(C).items() if k.startswith("GL_") and isinstance(v, int)}
-        for p in plan:
-            if p[0] != C.GL_VIEW:
-                kinds[names[p[0]]] = kinds.get(names[p[0]], 0) + 1
-        out = {"reference_sequence": f"s3enc.cpp:124-290, T_mel {T_mel} ({e.T_tok} tokens), {e.n_layer} layers",
-               "launches": ex.n_launches, "launches_by_kind": kinds, "bytes_per_call": nbytes}
-        for _ in range(3):
-            ex.launch(s)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            ex.launch(s)
-        e1.record()
-        torch.cuda.synchronize()
-        dev_us = e0.elapsed_time(e1) * 1000.0 / reps
-        out["exec_replay_us_per_call"] = dev_us
-        out["exec_replay_us_per_launch"] = dev_us / ex.n_launches
-        out["GBps"] = nbytes / (dev_us * 1e-6) / 1e9
-        ex.close()
-        for _ in range(2):
-            e.graph.compute(e.keep)
-        torch.cuda.synchronize()
-        n_c = max(5, reps // 4)
-        tm = time.perf_counter()
-        e0.record()
-        for _ in range(n_c):
-            e.graph.compute(e.keep)
-        host = (time.perf_counter() - tm) / n_c * 1e6
-        e1.record()
-        torch.cuda.synchronize()
-        out["graph_compute_us_per_call"] = {"host_us": host, "device_us": e0.elapsed_time(e1) * 1000.0 / n_c}
-        return out
+        return bench_node_list(C, torch, e, f"s3enc.cpp:124-290, T_mel {T_mel} ({e.T_tok} tokens), "
+                               f"{e.n_layer} layers", reps)
     finally:
         e.close()
+
+
+def bench_flow_encoder(C, torch, T=250, reps=20):
+    """One flow-encoder call's element-wise nodes (flow_encoder.cpp:537-700:
+    the speech-token gather, the embed linears' bias + LayerNorm + scale, the
+    pre-lookahead's bias + LeakyReLU and residual, 6 + 4 conformer blocks'
+    bias adds, pos_bias adds, score softmax, bias + residual + LayerNorm
+    joins and bias + SiLU, after_norm, encoder_proj's bias; matmul, conv and
+    layout outputs given) over T speech tokens, planned into one list of
+    launches (chatterbox_amdvulkan_amd/flow_encoder.py)."""
+    from chatterbox_amdvulkan_amd.flow_encoder import FlowEncoderCall
+
+    e = FlowEncoderCall(T, seed=6)
+    return bench_node_list(C, torch, e, f"flow_encoder.cpp:537-700, {T} tokens ({2 * T} frames), "
+                           f"{e.n_blocks} + {e.n_up_blocks} blocks", reps)
 
 
 def bench_hift_decode(C, torch, T_mel=500, reps=10):
@@ -1682,6 +1708,7 @@ def main():
               "cfm_estimator": lambda: bench_cfm_estimator(C, torch),
               "hift_decode": lambda: bench_hift_decode(C, torch),
               "s3_encoder": lambda: bench_s3_encoder(C, torch),
+              "flow_encoder": lambda: bench_flow_encoder(C, torch),
               "hift_conv": lambda: bench_hift_conv(C, W, torch),
               "copy": lambda: bench_copy_ceiling(C, torch, {"gelu_bytes": nb["gelu"],
                                                             "embed_layer_norm_bytes": nb["embed_layer_norm"],
@@ -1734,6 +1761,8 @@ def main():
         details["hift_decode"] = bench_hift_decode(C, torch)
         log("s3 encoder")
         details["s3_encoder_elementwise"] = bench_s3_encoder(C, torch)
+        log("flow encoder")
+        details["flow_encoder_elementwise"] = bench_flow_encoder(C, torch)
         log("hift conv")
         details["hift_resblock_conv"] = bench_hift_conv(C, W, torch)
     k_ms = res["kernel_ms"]["run_ops"]
@@ -1797,6 +1826,11 @@ def main():
         out["s3_encoder_us_per_call"] = {"reference_sequence": se["reference_sequence"] +
                                          f", {se['launches']} launches",
                                          "exec_replay": round(se["exec_replay_us_per_call"], 2)}
+    if "flow_encoder_elementwise" in details:
+        fe = details["flow_encoder_elementwise"]
+        out["flow_encoder_us_per_call"] = {"reference_sequence": fe["reference_sequence"] +
+                                           f", {fe['launches']} launches",
+                                           "exec_replay": round(fe["exec_replay_us_per_call"], 2)}
     if "hift_decode" in details:
         hd = details["hift_decode"]
         out["hift_decode_us_per_call"] = {"reference_sequence": hd["reference_sequence"] +

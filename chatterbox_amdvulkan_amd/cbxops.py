@@ -173,6 +173,7 @@ def load() -> ctypes.CDLL:
         "cbx_rope_ext": (i, [P, P, vp, P, vp]),
         "cbx_layer_norm_rope": (i, [P, P, P, f, ctypes.c_int64, P, vp, P, vp]),
         "cbx_scale_diag_mask_soft_max": (i, [P, f, ctypes.c_int32, P, vp]),
+        "cbx_add_scale_diag_mask_soft_max": (i, [P, P, f, ctypes.c_int32, P, vp]),
         "cbx_unary": (i, [i, P, P, vp]),
         "cbx_gelu": (i, [P, P, vp]),
         "cbx_gelu_erf": (i, [P, P, vp]),
@@ -550,6 +551,18 @@ def scale_diag_mask_soft_max(x, scale=1.0, n_past=-1, out=None):
     _ready(x)
     out = _out_like(x, out)
     _check(load().cbx_scale_diag_mask_soft_max(_ref(desc(x)), scale, n_past, _ref(desc(out)), _stream()))
+    return out
+
+
+def add_scale_diag_mask_soft_max(a, b, scale=1.0, n_past=-1, out=None):
+    """soft_max(diag_mask_inf(scale(a + b), n_past)) over the last dim, a and b
+    of one shape (the relative-position attention's content and shifted
+    position scores); n_past < 0: no mask."""
+    _ready(a)
+    _ready(b)
+    out = _out_like(a, out)
+    _check(load().cbx_add_scale_diag_mask_soft_max(_ref(desc(a)), _ref(desc(b)), scale, n_past, _ref(desc(out)),
+                                                    _stream()))
     return out
 
 

@@ -862,7 +862,32 @@ int cbx_scale_diag_mask_soft_max(const cbx_tensor* x, float scale, int32_t n_pas
     }
     if (!same_shape(x, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_scale_diag_mask_soft_max: x and y shapes differ");
     if (nelements(x) == 0) return CBX_OK;
-    return launch_soft_max(x, scale, n_past, y, st, reinterpret_cast<hipStream_t>(stream));
+    return launch_soft_max(x, nullptr, scale, n_past, y, st, reinterpret_cast<hipStream_t>(stream));
+}
+
+int cbx_add_scale_diag_mask_soft_max(const cbx_tensor* a, const cbx_tensor* b, float scale, int32_t n_past,
+                                     cbx_tensor* y, cbx_stream stream) {
+    const std::string f = "cbx_add_scale_diag_mask_soft_max";
+    const char* what = f.c_str();
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(a, what, "a")) || (rc = validate(b, what, "b")) || (rc = validate(y, what, "y"))) return rc;
+    if (a->type != CBX_TYPE_F32 || b->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32) {
+        return set_error(CBX_ERR_UNSUPPORTED, f + ": F32 only");
+    }
+    if (!same_shape(a, b) || !same_shape(a, y)) return set_error(CBX_ERR_INVALID_ARG, f + ": a, b and y shapes differ");
+    if (nelements(a) == 0) return CBX_OK;
+    // each row is read whole before it is stored: y may be a or b itself,
+    // any other overlap would race with other rows' reads
+    for (const cbx_tensor* p : {a, b}) {
+        if (!overlaps(p, y)) continue;
+        bool same = p->data == y->data;
+        for (int i = 0; i < 4; i++) same = same && p->nb[i] == y->nb[i];
+        if (!same) return set_error(CBX_ERR_INVALID_ARG, f + ": y must be a or b itself or overlap neither");
+    }
+    return launch_soft_max(a, b, scale, n_past, y, st, reinterpret_cast<hipStream_t>(stream));
 }
 
 // ---- activations -------------------------------------------------------------

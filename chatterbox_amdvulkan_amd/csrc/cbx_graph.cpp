@@ -186,6 +186,26 @@ struct Planner {
                is_contiguous(&t[p]);
     }
 
+    // add(a, b) of two F32 tensors of one shape at node i, then [scale ->]
+    // [diag_mask_inf ->] soft_max reading the sum alone: the node count, or 0
+    int32_t add_soft_max_at(int32_t i) const {
+        const cbx_gnode& a = nd[i];
+        const int32_t x = a.src[0];
+        if (!same_dims(a.src[1], x) || !same_dims(a.dst, x) || t[x].type != CBX_TYPE_F32 ||
+            t[a.src[1]].type != CBX_TYPE_F32) {
+            return 0;
+        }
+        int32_t j = i + 1, prev = a.dst;
+        if (is(j, CBX_GOP_SCALE) && nd[j].src[0] == prev && internal(prev, 1)) prev = nd[j++].dst;
+        if (is(j, CBX_GOP_DIAG_MASK_INF) && nd[j].src[0] == prev && internal(prev, 1)) {
+            if (nd[j].iparam < 0) return 0;
+            prev = nd[j++].dst;
+        }
+        const bool sm = is(j, CBX_GOP_SOFT_MAX) && nd[j].src[0] == prev && internal(prev, 1) && nd[j].src[1] < 0 &&
+                        nd[j].fparam == 1.0f;
+        return sm ? j + 1 - i : 0;
+    }
+
     // add(x, bias) [-> view (an alias of the sum)] -> add(r, .) at node i,
     // bias repeating to x and x to r: the node count (2 or 3), or 0
     int32_t bias_residual_at(int32_t i) const {
@@ -506,6 +526,11 @@ struct Planner {
                     *len = l;
                     return CBX_GL_BIAS_RESIDUAL;
                 }
+                // score terms' add -> [scale] [mask] -> soft_max
+                if (const int32_t l = add_soft_max_at(i)) {
+                    *len = l;
+                    return CBX_GL_SOFT_MAX;
+                }
                 // residual add -> layer_norm [-> mish]
                 if (same_dims(a.src[1], x)) {
                     const int32_t l = layer_norm_mish_at(i + 1, t1);
@@ -722,7 +747,7 @@ constexpr int32_t kSpan[][2] = {
     {5, 5},  // LAYER_NORM_ROPE
     {1, 2},  // RMS_NORM [mul]
     {1, 6},  // GROUP_NORM [affine] [mish]
-    {1, 3},  // SOFT_MAX [scale] [mask]
+    {1, 4},  // SOFT_MAX [add] [scale] [mask]
     {5, 5},  // SNAKE
     {1, 3},  // UNARY / mish
     {2, 2},  // SWIGLU
@@ -821,10 +846,14 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
                                   s);
         }
         case CBX_GL_SOFT_MAX: {
-            if (l.n_nodes == 1) return cbx_scale_diag_mask_soft_max(T(t, a.src[0]), a.fparam, -1, y, s);
+            if (l.n_nodes == 1) {
+                if (a.op != CBX_GOP_SOFT_MAX) break;
+                return cbx_scale_diag_mask_soft_max(T(t, a.src[0]), a.fparam, -1, y, s);
+            }
+            const bool add = a.op == CBX_GOP_ADD;
             float scale = 1.0f;
             int32_t n_past = -1;
-            for (int32_t k = f; k < f + l.n_nodes - 1; k++) {
+            for (int32_t k = add ? f + 1 : f; k < f + l.n_nodes - 1; k++) {
                 if (nd[k].op == CBX_GOP_SCALE) scale = nd[k].fparam;
                 if (nd[k].op == CBX_GOP_DIAG_MASK_INF) {
                     if (nd[k].iparam < 0) {
@@ -833,6 +862,7 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
                     n_past = nd[k].iparam;
                 }
             }
+            if (add) return cbx_add_scale_diag_mask_soft_max(T(t, a.src[0]), T(t, a.src[1]), scale, n_past, y, s);
             return cbx_scale_diag_mask_soft_max(T(t, a.src[0]), scale, n_past, y, s);
         }
         case CBX_GL_SNAKE:

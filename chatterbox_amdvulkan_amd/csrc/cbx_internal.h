@@ -176,7 +176,9 @@ struct RopeParams {
 int launch_rope(const cbx_tensor* x, const cbx_tensor* pos, const RopeParams& p,
                 const float2* table, int32_t n_pos, const float* freq_factors_dev,
                 cbx_tensor* y, DeviceState* st, hipStream_t s);
-int launch_soft_max(const cbx_tensor* x, float s, int64_t n_past, cbx_tensor* y, DeviceState* st, hipStream_t strm);
+// b: the second score term added in front (x's shape), or null
+int launch_soft_max(const cbx_tensor* x, const cbx_tensor* b, float s, int64_t n_past, cbx_tensor* y,
+                    DeviceState* st, hipStream_t strm);
 int launch_layer_norm_rope(const cbx_tensor* x, const cbx_tensor* w, const cbx_tensor* b, float eps, int64_t head_dim,
                            const cbx_tensor* pos, const RopeParams& p, const float2* table, int32_t n_pos,
                            const float* ff, cbx_tensor* y, DeviceState* st, hipStream_t s);

@@ -3,10 +3,13 @@
 //   y = ggml_soft_max(ggml_diag_mask_inf(ggml_scale(x, s), n_past))
 //
 // (t3.cpp:513-518; without the mask, n_past < 0: cfm_decoder.cpp:218-220,
-// flow_encoder.cpp:371-372, s3enc.cpp:260-262).  Per row of ne0 scores:
-// t = x*s (one f32 multiply), t = -inf where column i > n_past + j (j = the
-// row's ne1 index), m = max t, e = expf(t - m), sum of e in f64,
-// y = e * (float)(1.0 / sum) -- ggml-cpu's scalar order of operations.
+// flow_encoder.cpp:371-372, s3enc.cpp:260-262), and with the two score
+// terms' sum in front, x = ggml_add(a, b) (flow_encoder.cpp:369-372: the
+// content and the shifted position scores).  Per row of ne0 scores:
+// [x = a + b (one f32 add),] t = x*s (one f32 multiply), t = -inf where
+// column i > n_past + j (j = the row's ne1 index), m = max t,
+// e = expf(t - m), sum of e in f64, y = e * (float)(1.0 / sum) --
+// ggml-cpu's scalar order of operations.
 //
 // Rows up to 4096 with ne0 % 4 == 0: one wave per row, the row in
 // registers (one read, one write), the max by a butterfly of lane shuffles
@@ -60,8 +63,9 @@ __device__ __forceinline__ float masked(float x, float s, int64_t col, int64_t l
 
 struct SoftMaxArgs {
     const char* x;
+    const char* b;         // the second score term (ADD), x's shape
     char* y;
-    RowMap mx, my;
+    RowMap mx, mb, my;
     int64_t n_past;
     int32_t ne0, nr;
     uint32_t n_q;          // x.ne1: the query index of a row is r % n_q
@@ -71,7 +75,7 @@ struct SoftMaxArgs {
 // WPB rows per workgroup; with one, the grid is exactly one workgroup per
 // row and nothing waits (bounds check, block size) before the loads issue.
 // FLAT: rows at one stride each, so the row map's flag is not tested either.
-template <int NV, int WPB, bool FLAT>
+template <int NV, int WPB, bool FLAT, bool ADD>
 __global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
     // every field in the first batch of argument loads (left alone, the
     // compiler loads the row count first and the rest after its test: a
@@ -79,6 +83,9 @@ __global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
     arg_now(a.x); arg_now(a.y); arg_now(reinterpret_cast<const void*>(a.mx.nb1));
     arg_now(reinterpret_cast<const void*>(a.my.nb1)); arg_now(reinterpret_cast<const void*>(a.n_past));
     arg_now(static_cast<uint32_t>(a.ne0)); arg_now(static_cast<uint32_t>(a.nr)); arg_now(a.n_q);
+    if constexpr (ADD) {
+        arg_now(a.b); arg_now(reinterpret_cast<const void*>(a.mb.nb1));
+    }
     const int lane = threadIdx.x & 63;
     uint32_t r = blockIdx.x;
     if constexpr (WPB > 1) {
@@ -90,14 +97,16 @@ __global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
     const int64_t n_past = a.n_past;
     const char* xr = a.x + (FLAT ? static_cast<int64_t>(r) * a.mx.nb1 : row_at(a.mx, r));
     char* yr = a.y + (FLAT ? static_cast<int64_t>(r) * a.my.nb1 : row_at(a.my, r));
+    const char* br = ADD ? a.b + (FLAT ? static_cast<int64_t>(r) * a.mb.nb1 : row_at(a.mb, r)) : nullptr;
     // last unmasked column of this row
     const int64_t j = r % a.n_q;
     const int64_t lim = n_past >= 0 ? (n_past + j < ne0 - 1 ? n_past + j : ne0 - 1) : ne0 - 1;
-    float4 v[NV];
+    float4 v[NV], w[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
         const int64_t c = (lane + 64 * k) * 4;
         v[k] = Elt<float>::load4(xr + (c < ne0 ? c : 0) * 4);
+        if constexpr (ADD) w[k] = Elt<float>::load4(br + (c < ne0 ? c : 0) * 4);
     }
     float m = -INFINITY;
 #pragma unroll
@@ -105,7 +114,8 @@ __global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
         const int64_t c = (lane + 64 * k) * 4;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const float t = masked(get(v[k], e), s, c + e, lim);
+            const float x = ADD ? get(v[k], e) + get(w[k], e) : get(v[k], e);
+            const float t = masked(x, s, c + e, lim);
             set(v[k], e, t);
             m = fmaxf(m, t);
         }
@@ -142,7 +152,7 @@ __global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
 // 32-bit index arithmetic, every field in the first batch of argument
 // loads: a View's 64-bit divisions and the dependent argument loads they
 // waited on put about 900 instructions before the first score load.
-template <bool FLAT>
+template <bool FLAT, bool ADD>
 __global__ __launch_bounds__(kThreads) void k_soft_max_row(SoftMaxArgs a) {
     constexpr int K = kWaveMaxRow / kThreads;
     constexpr int NW = kThreads / WAVE;
@@ -151,6 +161,9 @@ __global__ __launch_bounds__(kThreads) void k_soft_max_row(SoftMaxArgs a) {
     arg_now(a.x); arg_now(a.y); arg_now(reinterpret_cast<const void*>(a.mx.nb1));
     arg_now(reinterpret_cast<const void*>(a.my.nb1)); arg_now(reinterpret_cast<const void*>(a.n_past));
     arg_now(static_cast<uint32_t>(a.ne0)); arg_now(a.n_q);
+    if constexpr (ADD) {
+        arg_now(a.b); arg_now(reinterpret_cast<const void*>(a.mb.nb1));
+    }
     if constexpr (!FLAT) {
         for (const RowMap* m : {&a.mx, &a.my}) {
             arg_now(reinterpret_cast<const void*>(m->nb2)); arg_now(reinterpret_cast<const void*>(m->nb3));
@@ -161,6 +174,7 @@ __global__ __launch_bounds__(kThreads) void k_soft_max_row(SoftMaxArgs a) {
     const int ne0 = a.ne0;
     const float* xr = reinterpret_cast<const float*>(a.x + (FLAT ? r * a.mx.nb1 : row_at(a.mx, r)));
     float* yr = reinterpret_cast<float*>(a.y + (FLAT ? r * a.my.nb1 : row_at(a.my, r)));
+    const float* bq = ADD ? reinterpret_cast<const float*>(a.b + (FLAT ? r * a.mb.nb1 : row_at(a.mb, r))) : nullptr;
     const int64_t j = r % a.n_q;
     const int64_t lim = a.n_past >= 0 ? (a.n_past + j < ne0 - 1 ? a.n_past + j : ne0 - 1) : ne0 - 1;
     // the columns a lane holds: k < nk (uniform); the loads of those issue
@@ -172,7 +186,7 @@ __global__ __launch_bounds__(kThreads) void k_soft_max_row(SoftMaxArgs a) {
     for (int k = 0; k < K; k++) {
         const int c = threadIdx.x + k * kThreads;
         v[k] = -INFINITY;
-        if (k < nk) v[k] = xr[c < ne0 ? c : 0];
+        if (k < nk) v[k] = ADD ? xr[c < ne0 ? c : 0] + bq[c < ne0 ? c : 0] : xr[c < ne0 ? c : 0];
     }
     float m = -INFINITY;
 #pragma unroll
@@ -216,12 +230,15 @@ __global__ __launch_bounds__(kThreads) void k_soft_max_row(SoftMaxArgs a) {
 // columns a lane (column lane + 64 k), the max and the f64 sum by DPP
 // butterflies -- no LDS and no barrier.  One kernel for every length up to
 // 1024, like k_soft_max_row.
-template <bool FLAT>
+template <bool FLAT, bool ADD>
 __global__ __launch_bounds__(WAVE) void k_soft_max_row_w(SoftMaxArgs a) {
     constexpr int K = 1024 / WAVE;
     arg_now(a.x); arg_now(a.y); arg_now(reinterpret_cast<const void*>(a.mx.nb1));
     arg_now(reinterpret_cast<const void*>(a.my.nb1)); arg_now(reinterpret_cast<const void*>(a.n_past));
     arg_now(static_cast<uint32_t>(a.ne0)); arg_now(a.n_q);
+    if constexpr (ADD) {
+        arg_now(a.b); arg_now(reinterpret_cast<const void*>(a.mb.nb1));
+    }
     if constexpr (!FLAT) {
         for (const RowMap* m : {&a.mx, &a.my}) {
             arg_now(reinterpret_cast<const void*>(m->nb2)); arg_now(reinterpret_cast<const void*>(m->nb3));
@@ -232,6 +249,7 @@ __global__ __launch_bounds__(WAVE) void k_soft_max_row_w(SoftMaxArgs a) {
     const int ne0 = a.ne0, lane = threadIdx.x;
     const float* xr = reinterpret_cast<const float*>(a.x + (FLAT ? r * a.mx.nb1 : row_at(a.mx, r)));
     float* yr = reinterpret_cast<float*>(a.y + (FLAT ? r * a.my.nb1 : row_at(a.my, r)));
+    const float* bq = ADD ? reinterpret_cast<const float*>(a.b + (FLAT ? r * a.mb.nb1 : row_at(a.mb, r))) : nullptr;
     const int64_t j = r % a.n_q;
     const int64_t lim = a.n_past >= 0 ? (a.n_past + j < ne0 - 1 ? a.n_past + j : ne0 - 1) : ne0 - 1;
     const int nk = (ne0 + WAVE - 1) / WAVE;   // uniform: the loads of k < nk issue together
@@ -240,7 +258,7 @@ __global__ __launch_bounds__(WAVE) void k_soft_max_row_w(SoftMaxArgs a) {
     for (int k = 0; k < K; k++) {
         const int c = lane + k * WAVE;
         v[k] = -INFINITY;
-        if (k < nk) v[k] = xr[c < ne0 ? c : 0];
+        if (k < nk) v[k] = ADD ? xr[c < ne0 ? c : 0] + bq[c < ne0 ? c : 0] : xr[c < ne0 ? c : 0];
     }
     float m = -INFINITY;
 #pragma unroll
@@ -270,35 +288,40 @@ __global__ __launch_bounds__(WAVE) void k_soft_max_row_w(SoftMaxArgs a) {
 
 // Any row length: max, then the f64 sum of exponentials, then the output,
 // each pass over the row (the exponentials are recomputed identically).
-__global__ __launch_bounds__(kThreads) void k_soft_max_loop(View x, View y, float s, int64_t n_past, bool fx,
-                                                            bool fy) {
+__global__ __launch_bounds__(kThreads) void k_soft_max_loop(View x, View b, View y, float s, int64_t n_past,
+                                                            bool fx, bool fb, bool fy) {
     __shared__ double red[kThreads / WAVE];
     __shared__ float redf[kThreads / WAVE];
     const int64_t r = blockIdx.x;
     const int64_t ne0 = x.ne[0];
     const float* xr = reinterpret_cast<const float*>(x.data + row_offset(x, r, fx));
     float* yr = reinterpret_cast<float*>(y.data + row_offset(y, r, fy));
+    // b.data null: no second term
+    const float* br = b.data ? reinterpret_cast<const float*>(b.data + row_offset(b, r, fb)) : nullptr;
+    const auto at = [&](int64_t c) { return br ? xr[c] + br[c] : xr[c]; };
     const int64_t j = r % x.ne[1];
     const int64_t lim = n_past >= 0 ? (n_past + j < ne0 - 1 ? n_past + j : ne0 - 1) : ne0 - 1;
     float m = -INFINITY;
-    for (int64_t c = threadIdx.x; c < ne0; c += kThreads) m = fmaxf(m, masked(xr[c], s, c, lim));
+    for (int64_t c = threadIdx.x; c < ne0; c += kThreads) m = fmaxf(m, masked(at(c), s, c, lim));
     m = wave_max(m);
     if ((threadIdx.x & 63) == 0) redf[threadIdx.x >> 6] = m;
     __syncthreads();
     m = -INFINITY;
     for (int w = 0; w < kThreads / WAVE; w++) m = fmaxf(m, redf[w]);
     double sum = 0.0;
-    for (int64_t c = threadIdx.x; c < ne0; c += kThreads) sum += static_cast<double>(expf(masked(xr[c], s, c, lim) - m));
+    for (int64_t c = threadIdx.x; c < ne0; c += kThreads) sum += static_cast<double>(expf(masked(at(c), s, c, lim) - m));
     sum = block_sum(sum, red);
     const float inv = static_cast<float>(1.0 / sum);
-    for (int64_t c = threadIdx.x; c < ne0; c += kThreads) yr[c] = expf(masked(xr[c], s, c, lim) - m) * inv;
+    for (int64_t c = threadIdx.x; c < ne0; c += kThreads) yr[c] = expf(masked(at(c), s, c, lim) - m) * inv;
 }
 
-SoftMaxArgs sm_args(const cbx_tensor* x, cbx_tensor* y, float s, int64_t n_past, int64_t nr) {
+SoftMaxArgs sm_args(const cbx_tensor* x, const cbx_tensor* b, cbx_tensor* y, float s, int64_t n_past, int64_t nr) {
     SoftMaxArgs a;
     a.x = static_cast<const char*>(x->data);
+    a.b = b ? static_cast<const char*>(b->data) : nullptr;
     a.y = static_cast<char*>(y->data);
     a.mx = row_map(x);
+    a.mb = row_map(b ? b : x);
     a.my = row_map(y);
     a.n_past = n_past;
     a.ne0 = static_cast<int32_t>(x->ne[0]);
@@ -310,53 +333,66 @@ SoftMaxArgs sm_args(const cbx_tensor* x, cbx_tensor* y, float s, int64_t n_past,
 
 int waves_for(int64_t rows, const DeviceState* st) { return rows >= int64_t{8} * st->n_cu ? 4 : 1; }
 
-template <int WPB, bool FLAT>
+template <int WPB, bool FLAT, bool ADD>
 void sm_wave(int nv, const SoftMaxArgs& a, hipStream_t strm) {
     const dim3 grid(static_cast<unsigned>(cdiv(a.nr, WPB))), block(64 * WPB);
     switch (nv) {
-        case 1: hipLaunchKernelGGL((k_soft_max_wave<1, WPB, FLAT>), grid, block, 0, strm, a); break;
-        case 2: hipLaunchKernelGGL((k_soft_max_wave<2, WPB, FLAT>), grid, block, 0, strm, a); break;
-        case 4: hipLaunchKernelGGL((k_soft_max_wave<4, WPB, FLAT>), grid, block, 0, strm, a); break;
-        case 8: hipLaunchKernelGGL((k_soft_max_wave<8, WPB, FLAT>), grid, block, 0, strm, a); break;
-        default: hipLaunchKernelGGL((k_soft_max_wave<16, WPB, FLAT>), grid, block, 0, strm, a); break;
+        case 1: hipLaunchKernelGGL((k_soft_max_wave<1, WPB, FLAT, ADD>), grid, block, 0, strm, a); break;
+        case 2: hipLaunchKernelGGL((k_soft_max_wave<2, WPB, FLAT, ADD>), grid, block, 0, strm, a); break;
+        case 4: hipLaunchKernelGGL((k_soft_max_wave<4, WPB, FLAT, ADD>), grid, block, 0, strm, a); break;
+        case 8: hipLaunchKernelGGL((k_soft_max_wave<8, WPB, FLAT, ADD>), grid, block, 0, strm, a); break;
+        default: hipLaunchKernelGGL((k_soft_max_wave<16, WPB, FLAT, ADD>), grid, block, 0, strm, a); break;
     }
 }
 
-}  // namespace
-
-int launch_soft_max(const cbx_tensor* x, float s, int64_t n_past, cbx_tensor* y, DeviceState* st, hipStream_t strm) {
-    const View vx = view_of(x), vy = view_of(y);
-    const bool fx = flat_rows(x), fy = flat_rows(y);
-    const int64_t nr = nrows(x), ne0 = x->ne[0];
-    const bool vec = ne0 <= kWaveMaxRow && ne0 % 4 == 0 && reinterpret_cast<uintptr_t>(x->data) % 16 == 0 &&
-                     reinterpret_cast<uintptr_t>(y->data) % 16 == 0 && x->nb[1] % 16 == 0 && y->nb[1] % 16 == 0 &&
-                     (x->ne[2] <= 1 || x->nb[2] % 16 == 0) && (x->ne[3] <= 1 || x->nb[3] % 16 == 0) &&
-                     (y->ne[2] <= 1 || y->nb[2] % 16 == 0) && (y->ne[3] <= 1 || y->nb[3] % 16 == 0);
-    if (nr >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "soft_max: too many rows");
+template <bool ADD>
+void sm_launch(const SoftMaxArgs& a, int64_t ne0, bool vec, const View& vx, const View& vb, const View& vy,
+               bool fx, bool fb, bool fy, const DeviceState* st, hipStream_t strm) {
+    const int64_t nr = a.nr;
     if (ne0 <= kWaveMaxRow && nr < int64_t{4} * st->n_cu) {
         // few rows (a decode step's heads): one kernel whatever the length
-        SoftMaxArgs a = sm_args(x, y, s, n_past, nr);
         const dim3 grid(static_cast<unsigned>(nr));
-        const bool flat = a.mx.flat && a.my.flat;
+        const bool flat = a.mx.flat && a.my.flat && (!ADD || a.mb.flat);
         if (ne0 <= 1024) {
-            if (flat) hipLaunchKernelGGL(k_soft_max_row_w<true>, grid, dim3(WAVE), 0, strm, a);
-            else hipLaunchKernelGGL(k_soft_max_row_w<false>, grid, dim3(WAVE), 0, strm, a);
+            if (flat) hipLaunchKernelGGL((k_soft_max_row_w<true, ADD>), grid, dim3(WAVE), 0, strm, a);
+            else hipLaunchKernelGGL((k_soft_max_row_w<false, ADD>), grid, dim3(WAVE), 0, strm, a);
         } else if (flat) {
-            hipLaunchKernelGGL(k_soft_max_row<true>, grid, dim3(kThreads), 0, strm, a);
+            hipLaunchKernelGGL((k_soft_max_row<true, ADD>), grid, dim3(kThreads), 0, strm, a);
         } else {
-            hipLaunchKernelGGL(k_soft_max_row<false>, grid, dim3(kThreads), 0, strm, a);
+            hipLaunchKernelGGL((k_soft_max_row<false, ADD>), grid, dim3(kThreads), 0, strm, a);
         }
     } else if (vec) {
         const int64_t need = cdiv(ne0, 256);
         const int nv = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : 16;
-        SoftMaxArgs a = sm_args(x, y, s, n_past, nr);
         // strided-plane layouts take one row per workgroup through the row map
-        if (!(a.mx.flat && a.my.flat)) sm_wave<1, false>(nv, a, strm);
-        else if (waves_for(nr, st) == 1) sm_wave<1, true>(nv, a, strm);
-        else sm_wave<4, true>(nv, a, strm);
+        if (!(a.mx.flat && a.my.flat && (!ADD || a.mb.flat))) sm_wave<1, false, ADD>(nv, a, strm);
+        else if (waves_for(nr, st) == 1) sm_wave<1, true, ADD>(nv, a, strm);
+        else sm_wave<4, true, ADD>(nv, a, strm);
     } else {
-        hipLaunchKernelGGL(k_soft_max_loop, dim3(static_cast<unsigned>(nr)), dim3(kThreads), 0, strm, vx, vy, s, n_past,
-                           fx, fy);
+        hipLaunchKernelGGL(k_soft_max_loop, dim3(static_cast<unsigned>(nr)), dim3(kThreads), 0, strm, vx, vb, vy, a.s,
+                           a.n_past, fx, fb, fy);
+    }
+}
+
+bool vec_rows(const cbx_tensor* t) {
+    return reinterpret_cast<uintptr_t>(t->data) % 16 == 0 && t->nb[1] % 16 == 0 && (t->ne[2] <= 1 || t->nb[2] % 16 == 0) &&
+           (t->ne[3] <= 1 || t->nb[3] % 16 == 0);
+}
+
+}  // namespace
+
+int launch_soft_max(const cbx_tensor* x, const cbx_tensor* b, float s, int64_t n_past, cbx_tensor* y,
+                    DeviceState* st, hipStream_t strm) {
+    const int64_t nr = nrows(x), ne0 = x->ne[0];
+    if (nr >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "soft_max: too many rows");
+    const bool vec = ne0 <= kWaveMaxRow && ne0 % 4 == 0 && vec_rows(x) && vec_rows(y) && (!b || vec_rows(b));
+    View vb{};
+    if (b) vb = view_of(b);
+    const SoftMaxArgs a = sm_args(x, b, y, s, n_past, nr);
+    if (b) {
+        sm_launch<true>(a, ne0, vec, view_of(x), vb, view_of(y), flat_rows(x), flat_rows(b), flat_rows(y), st, strm);
+    } else {
+        sm_launch<false>(a, ne0, vec, view_of(x), vb, view_of(y), flat_rows(x), false, flat_rows(y), st, strm);
     }
     return check_launch("soft_max");
 }

@@ -308,6 +308,16 @@ int cbx_scale_diag_mask_soft_max(const cbx_tensor* x, float scale,
                                  int32_t n_past, cbx_tensor* y,
                                  cbx_stream stream);
 
+/* The same with the two score terms' sum in front:
+ * ggml_soft_max(ggml_scale(ggml_add(a, b), scale)) (flow_encoder.cpp:
+ * 369-372: the content scores AC and the shifted position scores BD of the
+ * relative-position attention), a + b rounded to f32 before the scale, the
+ * mask as above when n_past >= 0.  a, b, y: F32 with the same shape; y may
+ * be a or b itself and must not overlap them otherwise.                     */
+int cbx_add_scale_diag_mask_soft_max(const cbx_tensor* a, const cbx_tensor* b,
+                                     float scale, int32_t n_past,
+                                     cbx_tensor* y, cbx_stream stream);
+
 /* ---- activations -------------------------------------------------------- */
 
 /* One ggml unary op (cbx_unary_op), F32 or F16, x and y same shape. */

@@ -1,0 +1,43 @@
+"""One flow-encoder call's node list (flow_encoder.cpp:537-700; matmul,
+conv and layout outputs given) planned on the host: every node claimed,
+and the launches the reference's structure implies for n_blocks blocks over
+T tokens and n_up blocks over 2T frames."""
+import collections
+
+import pytest
+
+from chatterbox_amdvulkan_amd import cbxops as C
+from chatterbox_amdvulkan_amd.flow_encoder import FlowEncoderCall
+
+
+@pytest.mark.parametrize("T,n_blocks,n_up", [(250, 6, 4), (7, 2, 1), (2, 1, 1)])
+def test_plan_counts(T, n_blocks, n_up):
+    e = FlowEncoderCall(T, n_blocks=n_blocks, n_up_blocks=n_up, device=False)
+    plan = e.plan()
+    names = {v: k for k, v in vars(C).items() if k.startswith("GL_") and isinstance(v, int)}
+    got = collections.Counter(names[p[0]] for p in plan)
+    L = n_blocks + n_up
+    assert dict(got) == {
+        "GL_GET_ROWS": 1,                     # the speech-token embedding
+        # per block the q, k, v bias adds and the w1 bias + silu; the two
+        # embed linears' bias, the two pre-lookahead convs' and the up conv's
+        # bias (as (1, C)), the encoder_proj bias
+        "GL_BIAS_ACT": 4 * L + 6,
+        # per block q as heads and pos_bias_u, pos_bias_v as (64, 8, 1); the
+        # three conv biases as (1, C)
+        "GL_VIEW": 3 * L + 3,
+        "GL_BINARY": 2 * L,                   # q + pos_bias_u, q + pos_bias_v
+        "GL_SOFT_MAX": L,                     # AC + BD -> scale(1/8) -> soft_max
+        # per block x + (out + b) -> LN; w2 bias + residual -> the next LN
+        # (the up stack's last: after_norm); the pre-lookahead's residual ->
+        # the first block's LN
+        "GL_ADD_LAYER_NORM": 2 * L,
+        "GL_BIAS_RESIDUAL": 1,                # the 25 Hz stack's last w2 bias + residual
+        # the two embed LNs; the 50 Hz stack's first LN (after the scale)
+        "GL_LAYER_NORM": 3,
+        "GL_SCALE": 2,                        # x sqrt(512) after each embed LN
+        "GL_LEAKY_RELU": 1,                   # the pre-lookahead's conv1
+    }
+    assert sum(p[2] for p in plan) == len(e.graph.nodes)
+    assert all(p[2] == 3 for p in plan if p[0] == C.GL_SOFT_MAX)
+    assert e.graph.nodes[-1].dst == e.out and tuple(e.b.shape(e.out)) == (2 * T, 80)

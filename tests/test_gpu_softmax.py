@@ -93,3 +93,45 @@ def test_strided_rows_and_extremes(cbx, oracle):
     got = host(cbx.scale_diag_mask_soft_max(v, 2.0, 3))
     check(got, oracle.scale_diag_mask_soft_max(np.ascontiguousarray(base[:, 10:266]), 2.0, 3), "strided",
           mask_of((6, 256), 3))
+
+
+@pytest.mark.parametrize("shape,n_past", [((8, 500, 500), -1), ((8, 40, 40), -1), ((2, 3, 2000), 1990),
+                                          ((6, 5000), 4000), ((1100, 37), 5), ((1, 8, 250, 252), -1)])
+def test_add_scale_soft_max(cbx, oracle, shape, n_past):
+    """cbx_add_scale_diag_mask_soft_max: the flow encoder's AC + BD scores
+    ([8 heads, 2T, 2T] at T 250), few rows (one wave a row; a workgroup a
+    row past 1024), rows past 4096 and rows of 37 (the three-pass kernel).
+    The same bits as the plain epilogue over the sum rounded on the device,
+    and within the f32 bar of the oracle's add -> scale -> soft_max."""
+    a = W.normal(140 + shape[-1], shape, 0.0, 3.0)
+    b = W.normal(141 + shape[-1], shape, 0.0, 3.0)
+    ta, tb = dev(a), dev(b)
+    got = host(cbx.add_scale_diag_mask_soft_max(ta, tb, 0.125, n_past))
+    assert_bitexact(got, host(cbx.scale_diag_mask_soft_max(ta + tb, 0.125, n_past)), f"{shape}: fused vs sum")
+    exp = oracle.scale_diag_mask_soft_max(oracle.add(a, b), 0.125, n_past, nth=8)
+    check(got, exp, f"{shape}", mask_of(shape, n_past) if n_past >= 0 else None)
+
+
+def test_add_scale_soft_max_in_place_and_strided(cbx, oracle):
+    """y = a, y = b, and b a column slice of a wider tensor (rows at a
+    stride, the row map)."""
+    a = W.normal(150, (4, 64, 128), 0.0, 5.0)
+    wide = W.normal(151, (4, 64, 160), 0.0, 5.0)
+    b = np.ascontiguousarray(wide[..., 16:144])
+    exp = oracle.scale_diag_mask_soft_max(oracle.add(a, b), 0.5, -1, nth=8)
+    ta, tb = dev(a), dev(wide)[..., 16:144]
+    check(host(cbx.add_scale_diag_mask_soft_max(ta, tb, 0.5)), exp, "strided b")
+    cbx.add_scale_diag_mask_soft_max(ta, tb, 0.5, out=ta)
+    check(host(ta), exp, "y = a")
+    ta, tb = dev(a), dev(b)
+    cbx.add_scale_diag_mask_soft_max(ta, tb, 0.5, out=tb)
+    check(host(tb), exp, "y = b")
+
+
+def test_add_scale_soft_max_refusals(cbx):
+    a = torch.zeros(4, 64, device="cuda")
+    with pytest.raises(cbx.CbxError, match="shapes differ"):
+        cbx.add_scale_diag_mask_soft_max(a, torch.zeros(4, 32, device="cuda"))
+    big = torch.zeros(5, 64, device="cuda")
+    with pytest.raises(cbx.CbxError, match="overlap"):
+        cbx.add_scale_diag_mask_soft_max(a, big[:4], out=big[1:])

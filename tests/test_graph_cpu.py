@@ -303,6 +303,40 @@ def test_attention_scores(with_mask):
     assert g.plan() == [(C.GL_SOFT_MAX, 0, 3 if with_mask else 2, 0)]
 
 
+@pytest.mark.parametrize("with_scale,with_mask", [(True, False), (True, True), (False, False)])
+def test_score_terms_add_joins_the_soft_max(with_scale, with_mask):
+    """flow_encoder.cpp:369-372: add(AC, BD_shift) -> scale -> soft_max is one
+    launch; the sum kept by the caller, a broadcast or F16 operand, or a
+    soft_max with its own scale leave the add a launch of its own."""
+    def build(keep_sum=False, b_shape=(4, 7, 9), b_dtype=torch.float32, sm_scale=1.0):
+        g = C.Graph()
+        ac = g.tensor(f32(4, 7, 9))
+        bd = g.tensor(torch.zeros(b_shape, dtype=b_dtype))
+        t = [g.tensor(f32(4, 7, 9)) for _ in range(4)]
+        g.node(C.GOP_ADD, t[0], (ac, bd))
+        src = t[0]
+        if with_scale:
+            g.node(C.GOP_SCALE, t[1], (src,), fparam=0.125)
+            src = t[1]
+        if with_mask:
+            g.node(C.GOP_DIAG_MASK_INF, t[2], (src,), iparam=2)
+            src = t[2]
+        g.node(C.GOP_SOFT_MAX, t[3], (src,), fparam=sm_scale)
+        return g, g.plan(keep=[t[0]] if keep_sum else [])
+
+    n = 2 + with_scale + with_mask
+    g, plan = build()
+    assert plan == [(C.GL_SOFT_MAX, 0, n, 0)]
+    _, plan = build(keep_sum=True)
+    assert plan == [(C.GL_BINARY, 0, 1, C.BINARY_ADD), (C.GL_SOFT_MAX, 1, n - 1, 0)]
+    _, plan = build(b_shape=(1, 7, 9))
+    assert plan[0] == (C.GL_BINARY, 0, 1, C.BINARY_ADD)
+    _, plan = build(b_dtype=torch.float16)
+    assert plan[0][0] != C.GL_SOFT_MAX
+    _, plan = build(sm_scale=2.0)
+    assert plan[0][0] != C.GL_SOFT_MAX and plan[-1] == (C.GL_SOFT_MAX, n - 1, 1, 0)
+
+
 def test_soft_max_with_own_scale_does_not_absorb_scale():
     g = C.Graph()
     kq = g.tensor(f32(4, 8))
@@ -519,7 +553,7 @@ def test_random_lists_plan_into_an_exact_cover():
     spans = {C.GL_UNSUPPORTED: {1}, C.GL_VIEW: {1}, C.GL_GET_ROWS: {1, 2}, C.GL_GET_ROWS_ADD: {3, 4, 5},
              C.GL_GET_ROWS_ADD_LAYER_NORM: {6, 7, 8}, C.GL_NORM: {1}, C.GL_LAYER_NORM: {3, 6},
              C.GL_LAYER_NORM_ROPE: {5}, C.GL_RMS_NORM: {1, 2}, C.GL_GROUP_NORM: {1, 3, 4, 6},
-             C.GL_SOFT_MAX: {1, 2, 3}, C.GL_SNAKE: {5}, C.GL_UNARY: {1, 3}, C.GL_SWIGLU: {2},
+             C.GL_SOFT_MAX: {1, 2, 3, 4}, C.GL_SNAKE: {5}, C.GL_UNARY: {1, 3}, C.GL_SWIGLU: {2},
              C.GL_LEAKY_RELU: {1}, C.GL_ROPE: {1}, C.GL_CPY: {1}, C.GL_ADD_LAYER_NORM: {4, 5, 7, 8},
              C.GL_LAYER_NORM_MASK: {4, 7}, C.GL_BIAS_ACT: {1, 2, 4}, C.GL_CONV1D: set(range(9, 18)),
              C.GL_CONV_TRANSPOSE1D: set(range(7, 15)), C.GL_CAUSAL_CONV1D: set(range(12, 16)),
