@@ -42,8 +42,10 @@ __device__ __forceinline__ float bin(float x, float y) {
     else return x * y;
 }
 
-// MODE BIN_SAME: b[i]; BIN_ROW: b[i % ne0] (ne0 % 4 == 0); BIN_COL: b[row
-// % nbr], one value a row of ne0 elements.
+// MODE BIN_SAME: b[i]; BIN_ROW: b[i % (4 ne0_4)], b one period of a's
+// leading dims (a row, or a (ne0, ne1) plane repeated over ne2: the flow
+// encoder's (64, 8, 1) pos_bias over (64, 8, T) query heads); BIN_COL:
+// b[row % nbr], one value a row of ne0 elements.
 template <int OP, int MODE>
 __global__ __launch_bounds__(kThreads) void k_binary_flat(const float* __restrict__ a, const float* __restrict__ b,
                                                           float* __restrict__ y, uint32_t n4, uint32_t ne0_4,
@@ -215,14 +217,21 @@ template <int OP>
 void binary_go(const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y, hipStream_t s) {
     const int64_t n = nelements(a);
     const bool same = same_shape(a, b) && is_contiguous(b) && al16(b->data);
-    const bool row = b->ne[0] == a->ne[0] && b->ne[1] == 1 && b->ne[2] == 1 && b->ne[3] == 1 && is_contiguous(b) &&
-                     al16(b->data);
+    // b's dims equal a's below k and are 1 from k on: b repeats every
+    // `period` elements of a contiguous a
+    int k = 0;
+    int64_t period = 1;
+    while (k < 4 && b->ne[k] == a->ne[k]) period *= a->ne[k++];
+    bool lead = k >= 1 && is_contiguous(b) && al16(b->data) && period / 4 < (int64_t{1} << 31);
+    for (int j = k; j < 4; j++) lead = lead && b->ne[j] == 1;
+    const bool row = !same && lead;
     const bool col = b->ne[0] == 1 && b->ne[1] == a->ne[1] && b->ne[2] == 1 && b->ne[3] == 1 &&
                      (b->ne[1] == 1 || b->nb[1] == sizeof(float));
     const bool flat = is_contiguous(a) && is_contiguous(y) && al16(a->data) && al16(y->data) && a->ne[0] % 4 == 0 &&
                       n / 4 < (int64_t{1} << 31) && (same || row || col);
     if (flat) {
-        const uint32_t n4 = static_cast<uint32_t>(n / 4), ne0_4 = static_cast<uint32_t>(a->ne[0] / 4);
+        const uint32_t n4 = static_cast<uint32_t>(n / 4);
+        const uint32_t ne0_4 = static_cast<uint32_t>((row ? period : a->ne[0]) / 4);
         const uint32_t nbr = static_cast<uint32_t>(b->ne[1]);
         const dim3 grid(static_cast<unsigned>(cdiv(n4, kThreads)));
         const float* ap = static_cast<const float*>(a->data);

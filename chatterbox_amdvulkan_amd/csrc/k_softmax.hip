@@ -14,8 +14,10 @@
 // Rows up to 4096 with ne0 % 4 == 0: one wave per row, the row in
 // registers (one read, one write), the max by a butterfly of lane shuffles
 // (exact in any order), the sum by the f64 DPP butterfly.  Few rows up to
-// 4096 (a decode step's): a workgroup per row, the row in registers, one
-// kernel for every length.  Other rows: a workgroup per row, three passes.
+// 4096 (a decode step's): a workgroup per row (a wave up to 1024), the row
+// in registers, one kernel for every length.  Rows up to 1024 not a
+// multiple of 4: a wave per row, the same kernel.  Other rows: a workgroup
+// per row, three passes.
 #include "cbx_rowops.h"
 
 namespace cbx {
@@ -225,8 +227,9 @@ __global__ __launch_bounds__(kThreads) void k_soft_max_row(SoftMaxArgs a) {
     }
 }
 
-// Few rows of up to 1024 scores at any alignment (the T3 decode step's 16
-// rows of n_past + 1 columns, n_past < 1024): one wave a row, up to 16
+// Rows of up to 1024 scores at any alignment (the T3 decode step's 16 rows
+// of n_past + 1 columns, n_past < 1024; the 25 Hz conformer blocks' 250
+// keys, flow_encoder.cpp:369-372, s3enc.cpp:260-262): one wave a row, up to 16
 // columns a lane (column lane + 64 k), the max and the f64 sum by DPP
 // butterflies -- no LDS and no barrier.  One kernel for every length up to
 // 1024, like k_soft_max_row.
@@ -360,6 +363,15 @@ void sm_launch(const SoftMaxArgs& a, int64_t ne0, bool vec, const View& vx, cons
             hipLaunchKernelGGL((k_soft_max_row<true, ADD>), grid, dim3(kThreads), 0, strm, a);
         } else {
             hipLaunchKernelGGL((k_soft_max_row<false, ADD>), grid, dim3(kThreads), 0, strm, a);
+        }
+    } else if (!vec && ne0 <= 1024) {
+        // many unaligned rows up to 1024 (the 25 Hz conformer blocks' 250
+        // keys): one wave a row, as for few rows, not three passes
+        const dim3 grid(static_cast<unsigned>(nr));
+        if (a.mx.flat && a.my.flat && (!ADD || a.mb.flat)) {
+            hipLaunchKernelGGL((k_soft_max_row_w<true, ADD>), grid, dim3(WAVE), 0, strm, a);
+        } else {
+            hipLaunchKernelGGL((k_soft_max_row_w<false, ADD>), grid, dim3(WAVE), 0, strm, a);
         }
     } else if (vec) {
         const int64_t need = cdiv(ne0, 256);

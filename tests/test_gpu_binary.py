@@ -34,6 +34,10 @@ SHAPES = [
     ((7, 13), (1, 13)),           # odd widths (the row path)
     ((5, 6, 7, 8), (1, 1, 7, 1)),
     ((1024,), (1024,)),           # vectors (the time embedding)
+    ((250, 8, 64), (1, 8, 64)),   # pos_bias over the query heads (a flat period of 512)
+    ((3, 5, 8, 12), (1, 1, 8, 12)),
+    ((3, 5, 8, 12), (1, 5, 8, 12)),
+    ((6, 8, 12), (1, 8, 1)),      # a leading-dim period with a 1 inside: the row map
 ]
 
 

@@ -86,6 +86,27 @@ def test_few_rows_planes_not_at_one_stride(cbx, oracle, n):
     check(got, exp, f"planes apart, n={n}", mask_of((2, 3, n), n - 3))
 
 
+@pytest.mark.parametrize("shape,n_past", [((8, 250, 250), -1), ((1500, 1023), 600), ((2, 700, 1021), 0),
+                                          ((1100, 1025), 3)])
+def test_many_unaligned_rows(cbx, oracle, shape, n_past):
+    """Many rows whose length is not a multiple of 4: a wave a row up to
+    1024 columns (the 25 Hz conformer blocks' 250 keys), three passes past
+    that."""
+    x = W.normal(160 + shape[-1], shape, 0.0, 6.0)
+    got = host(cbx.scale_diag_mask_soft_max(dev(x), 0.125, n_past))
+    check(got, oracle.scale_diag_mask_soft_max(x, 0.125, n_past, nth=8), f"{shape}",
+          mask_of(shape, n_past) if n_past >= 0 else None)
+
+
+def test_many_unaligned_rows_planes_apart(cbx, oracle):
+    """The same over a slice of a 3-D tensor (planes not one row stride
+    apart): the row map."""
+    base = W.normal(170, (4, 300, 260), 0.0, 6.0)
+    v = dev(base)[:, 10:290, 3:253]
+    exp = oracle.scale_diag_mask_soft_max(np.ascontiguousarray(base[:, 10:290, 3:253]), 0.5, 7, nth=8)
+    check(host(cbx.scale_diag_mask_soft_max(v, 0.5, 7)), exp, "planes apart", mask_of((4, 280, 250), 7))
+
+
 def test_strided_rows_and_extremes(cbx, oracle):
     """A column-sliced view (rows at a stride, loop path) and large score gaps."""
     base = W.normal(134, (6, 300), 0.0, 30.0)
@@ -95,8 +116,9 @@ def test_strided_rows_and_extremes(cbx, oracle):
           mask_of((6, 256), 3))
 
 
-@pytest.mark.parametrize("shape,n_past", [((8, 500, 500), -1), ((8, 40, 40), -1), ((2, 3, 2000), 1990),
-                                          ((6, 5000), 4000), ((1100, 37), 5), ((1, 8, 250, 252), -1)])
+@pytest.mark.parametrize("shape,n_past", [((8, 500, 500), -1), ((8, 250, 250), -1), ((8, 40, 40), -1),
+                                          ((2, 3, 2000), 1990), ((6, 5000), 4000), ((1100, 37), 5),
+                                          ((1, 8, 250, 252), -1)])
 def test_add_scale_soft_max(cbx, oracle, shape, n_past):
     """cbx_add_scale_diag_mask_soft_max: the flow encoder's AC + BD scores
     ([8 heads, 2T, 2T] at T 250), few rows (one wave a row; a workgroup a
