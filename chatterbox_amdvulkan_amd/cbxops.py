@@ -116,7 +116,7 @@ GL_UNSUPPORTED, GL_VIEW, GL_GET_ROWS, GL_GET_ROWS_ADD, GL_GET_ROWS_ADD_LAYER_NOR
     GL_LAYER_NORM_ROPE, GL_RMS_NORM, GL_GROUP_NORM, GL_SOFT_MAX, GL_SNAKE, GL_UNARY, GL_SWIGLU, GL_LEAKY_RELU, \
     GL_ROPE, GL_CPY, GL_ADD_LAYER_NORM, GL_LAYER_NORM_MASK, GL_BIAS_ACT, GL_CONV1D, GL_CONV_TRANSPOSE1D, \
     GL_CAUSAL_CONV1D, GL_GET_ROWS_CONCAT_ADD_LAYER_NORM, GL_BINARY, GL_CONCAT, \
-    GL_BIAS_RESIDUAL, GL_SCALE = range(28)
+    GL_BIAS_RESIDUAL, GL_SCALE, GL_BIAS_ADD_PAIR = range(29)
 # conv launch flags: the prologue (bits 0-1), a bias add, the residual add
 GLF_SNAKE, GLF_LEAKY, GLF_MASK, GLF_BIAS, GLF_RESIDUAL, GLF_SUM, GLF_SCALE = 1, 2, 3, 4, 8, 16, 32
 
@@ -188,6 +188,7 @@ def load() -> ctypes.CDLL:
         "cbx_binary": (i, [i, P, P, P, vp]),
         "cbx_concat": (i, [P, P, i, P, vp]),
         "cbx_bias_residual": (i, [P, P, P, P, vp]),
+        "cbx_bias_add_pair": (i, [P, P, P, P, P, P, vp]),
         "cbx_scale": (i, [P, f, P, vp]),
         "cbx_conv1d_weights_create": (i, [P, vp, ctypes.POINTER(vp)]),
         "cbx_conv1d_weights_destroy": (None, [vp]),
@@ -677,6 +678,17 @@ def bias_residual(x, bias, r, out=None):
     out = _out_like(r, out)
     _check(load().cbx_bias_residual(_ref(desc(x)), _ref(desc(bias)), _ref(desc(r)), _ref(desc(out)), _stream()))
     return out
+
+
+def bias_add_pair(x, bias, u, v, out_u=None, out_v=None):
+    """(x + bias) + u and (x + bias) + v in one pass, the sum not stored:
+    bias, u and v repeat to x's shape; each add one f32 rounding."""
+    _ready(x)
+    out_u = _out_like(x, out_u)
+    out_v = _out_like(x, out_v)
+    _check(load().cbx_bias_add_pair(_ref(desc(x)), _ref(desc(bias)), _ref(desc(u)), _ref(desc(v)), _ref(desc(out_u)),
+                                    _ref(desc(out_v)), _stream()))
+    return out_u, out_v
 
 
 def scale(x, s, out=None):

@@ -1739,6 +1739,41 @@ extern "C" int cbx_bias_residual(const cbx_tensor* x, const cbx_tensor* bias, co
     return launch_bias_residual(x, bias, r, y, reinterpret_cast<hipStream_t>(stream));
 }
 
+extern "C" int cbx_bias_add_pair(const cbx_tensor* x, const cbx_tensor* bias, const cbx_tensor* u,
+                                 const cbx_tensor* v, cbx_tensor* yu, cbx_tensor* yv, cbx_stream stream) {
+    const char* what = "cbx_bias_add_pair";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    if ((rc = validate(x, what, "x")) || (rc = validate(bias, what, "bias")) || (rc = validate(u, what, "u")) ||
+        (rc = validate(v, what, "v")) || (rc = validate(yu, what, "yu")) || (rc = validate(yv, what, "yv"))) {
+        return rc;
+    }
+    for (const cbx_tensor* p : {x, bias, u, v, static_cast<const cbx_tensor*>(yu), static_cast<const cbx_tensor*>(yv)}) {
+        if (p->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, "cbx_bias_add_pair: F32 only");
+    }
+    if (!same_shape(x, yu) || !same_shape(x, yv)) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_bias_add_pair: yu and yv must have x's shape");
+    }
+    if (nelements(x) == 0) return CBX_OK;
+    for (const cbx_tensor* p : {bias, u, v}) {
+        for (int k = 0; k < 4; k++) {
+            if (p->ne[k] < 1 || x->ne[k] % p->ne[k] != 0) {
+                return set_error(CBX_ERR_INVALID_ARG,
+                                 "cbx_bias_add_pair: bias, u and v must repeat to x's shape (every ne[i] a multiple)");
+            }
+        }
+    }
+    for (const cbx_tensor* p : {x, bias, u, v}) {
+        if (overlaps(yu, p) || overlaps(yv, p)) {
+            return set_error(CBX_ERR_INVALID_ARG, "cbx_bias_add_pair: yu or yv overlaps an input");
+        }
+    }
+    if (overlaps(yu, yv)) return set_error(CBX_ERR_INVALID_ARG, "cbx_bias_add_pair: yu and yv overlap");
+    return launch_bias_add_pair(x, bias, u, v, yu, yv, reinterpret_cast<hipStream_t>(stream));
+}
+
 extern "C" int cbx_scale(const cbx_tensor* x, float sc, cbx_tensor* y, cbx_stream stream) {
     const char* what = "cbx_scale";
     clear_error();

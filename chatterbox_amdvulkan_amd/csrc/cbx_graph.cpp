@@ -119,6 +119,18 @@ bool parse_concat_t3(const cbx_gnode* nd, int32_t n, int32_t i, ConcatT3* c) {
     return true;
 }
 
+// The number of leading dims of v whose sizes multiply to n (a vector of n
+// values re-described as one period of v's shape), or -1
+int lead_dims(const cbx_tensor& v, int64_t n) {
+    int64_t p = 1;
+    for (int k = 0; k < 4; k++) {
+        p *= v.ne[k];
+        if (p == n) return k + 1;
+        if (p > n) return -1;
+    }
+    return -1;
+}
+
 struct Planner {
     const cbx_tensor* t;
     int32_t n_t;
@@ -204,6 +216,39 @@ struct Planner {
         const bool sm = is(j, CBX_GOP_SOFT_MAX) && nd[j].src[0] == prev && internal(prev, 1) && nd[j].src[1] < 0 &&
                         nd[j].fparam == 1.0f;
         return sm ? j + 1 - i : 0;
+    }
+
+    // add(x, bias) -> view (a contiguous reshape of the sum) -> add(view, u),
+    // add(view, v) at node i, the sum and the view read by nothing else
+    // (flow_encoder.cpp:320, 341-345: q's bias, then pos_bias_u and
+    // pos_bias_v over the query heads); up to two views of other tensors
+    // (u's and v's reshapes) may stand among the adds, a view running
+    // nothing: the node count (4 to 6), or 0
+    int32_t bias_pair_at(int32_t i) const {
+        const cbx_gnode& a = nd[i];
+        const int32_t x = a.src[0], bias = a.src[1], s = a.dst;
+        if (!row_vec(bias, x) || !same_dims(s, x) || !is(i + 1, CBX_GOP_VIEW) || nd[i + 1].src[0] != s ||
+            !internal(s, 1)) {
+            return 0;
+        }
+        const int32_t vw = nd[i + 1].dst;
+        if (!valid_t(vw) || !internal(vw, 2)) return 0;
+        const cbx_tensor &X = t[x], &B = t[bias], &S = t[s], &V = t[vw];
+        if (X.type != CBX_TYPE_F32 || B.type != CBX_TYPE_F32 || S.type != CBX_TYPE_F32 || V.type != CBX_TYPE_F32 ||
+            !is_contiguous(&X) || !is_contiguous(&B) || !is_contiguous(&S) || !is_contiguous(&V) ||
+            V.data != S.data || nelements(&V) != nelements(&S) || lead_dims(V, X.ne[0]) < 0) {
+            return 0;
+        }
+        int32_t j = i + 2, n_add = 0;
+        for (; n_add < 2 && j < i + 6; j++) {
+            if (is(j, CBX_GOP_VIEW) && nd[j].src[0] != s && nd[j].src[0] != vw) continue;
+            if (!is(j, CBX_GOP_ADD) || nd[j].src[0] != vw || !repeats(nd[j].src[1], vw) ||
+                t[nd[j].src[1]].type != CBX_TYPE_F32 || !same_dims(nd[j].dst, vw)) {
+                return 0;
+            }
+            n_add++;
+        }
+        return n_add == 2 ? j - i : 0;
     }
 
     // add(x, bias) [-> view (an alias of the sum)] -> add(r, .) at node i,
@@ -521,6 +566,11 @@ struct Planner {
                         return CBX_GL_ADD_LAYER_NORM;
                     }
                 }
+                // bias add -> heads view -> two broadcast adds
+                if (const int32_t l = bias_pair_at(i)) {
+                    *len = l;
+                    return CBX_GL_BIAS_ADD_PAIR;
+                }
                 // bias add [-> view] -> residual add with no norm after it
                 if (const int32_t l = bias_residual_at(i)) {
                     *len = l;
@@ -765,8 +815,9 @@ constexpr int32_t kSpan[][2] = {
     {1, 1},  // CONCAT
     {2, 3},  // BIAS_RESIDUAL [view]
     {1, 1},  // SCALE
+    {4, 6},  // BIAS_ADD_PAIR [views of u, v]
 };
-constexpr int32_t kLastKind = CBX_GL_SCALE;
+constexpr int32_t kLastKind = CBX_GL_BIAS_ADD_PAIR;
 static_assert(sizeof(kSpan) / sizeof(kSpan[0]) == kLastKind + 1, "one span per launch kind");
 
 // Issues the entry point a launch maps to.  A launch is only read within
@@ -882,6 +933,36 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
         case CBX_GL_BINARY:
             if (a.op != (l.flags == CBX_BINARY_MUL ? CBX_GOP_MUL : CBX_GOP_ADD)) break;
             return cbx_binary(l.flags, T(t, a.src[0]), T(t, a.src[1]), y, s);
+        case CBX_GL_BIAS_ADD_PAIR: {
+            // the heads view, then views of other tensors and the two adds
+            const cbx_gnode& v = nd[f + 1];
+            if (a.op != CBX_GOP_ADD || v.op != CBX_GOP_VIEW || v.src[0] != a.dst) break;
+            int32_t k_add[2], n_add = 0;
+            for (int32_t k = f + 2; k < f + l.n_nodes; k++) {
+                if (nd[k].op == CBX_GOP_ADD && nd[k].src[0] == v.dst && n_add < 2) k_add[n_add++] = k;
+                else if (nd[k].op != CBX_GOP_VIEW || nd[k].src[0] == a.dst || nd[k].src[0] == v.dst) n_add = 3;
+            }
+            if (n_add != 2 || k_add[1] != f + l.n_nodes - 1) break;
+            const cbx_gnode &pu = nd[k_add[0]], &pv = nd[k_add[1]];
+            const cbx_tensor *X = T(t, a.src[0]), *B = T(t, a.src[1]), *S = T(t, a.dst), *V = T(t, v.dst);
+            if (!X || !B || !S || !V) break;
+            const int kb = lead_dims(*V, X->ne[0]);
+            if (!is_contiguous(X) || !is_contiguous(B) || !is_contiguous(S) || !is_contiguous(V) || V->data != S->data ||
+                nelements(V) != nelements(X) || !same_shape(S, X) || B->ne[0] != X->ne[0] ||
+                nelements(B) != B->ne[0] || kb < 0) {
+                return set_error(CBX_ERR_INVALID_ARG, "cbx_graph_launch: node " + std::to_string(f + 1) +
+                                                          ": the view is not a contiguous reshape of the biased sum");
+            }
+            // x and the bias re-described over the view's dims (the sum is
+            // never stored, the two adds read it through the view)
+            cbx_tensor xv = *V, bv = *V;
+            xv.data = X->data;
+            bv.data = B->data;
+            for (int k = kb; k < 4; k++) bv.ne[k] = 1;
+            for (int k = 1; k < 4; k++) bv.nb[k] = bv.nb[k - 1] * static_cast<size_t>(bv.ne[k - 1]);
+            return cbx_bias_add_pair(&xv, &bv, T(t, pu.src[1]), T(t, pv.src[1]),
+                                     const_cast<cbx_tensor*>(&t[pu.dst]), y, s);
+        }
         case CBX_GL_BIAS_RESIDUAL: {
             const cbx_gnode& last = nd[f + l.n_nodes - 1];
             int32_t sum = a.dst;

@@ -131,6 +131,8 @@ int launch_bias_act(int op, const cbx_tensor* x, const cbx_tensor* bias, cbx_ten
 // cbx_binary and cbx_concat (k_binary.hip), arguments checked by the caller.
 int launch_binary(int op, const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y, hipStream_t s);
 int launch_scale(const cbx_tensor* x, float s, cbx_tensor* y, hipStream_t strm);
+int launch_bias_add_pair(const cbx_tensor* x, const cbx_tensor* bias, const cbx_tensor* u, const cbx_tensor* v,
+                         cbx_tensor* yu, cbx_tensor* yv, hipStream_t s);
 int launch_bias_residual(const cbx_tensor* x, const cbx_tensor* bias, const cbx_tensor* r, cbx_tensor* y,
                          hipStream_t s);
 int launch_concat(const cbx_tensor* a, const cbx_tensor* b, int dim, cbx_tensor* y, hipStream_t s);

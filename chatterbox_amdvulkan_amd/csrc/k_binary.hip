@@ -115,6 +115,60 @@ __global__ __launch_bounds__(kThreads) void k_bias_residual_flat(const float* __
     if (iu < n4) *reinterpret_cast<float4*>(y + 4ull * i) = o;
 }
 
+// yu = (x + bias) + u, yv = (x + bias) + v over contiguous x, yu, yv;
+// bias, u and v each one period of x's leading dims (pb, pu, pv float4s)
+__global__ __launch_bounds__(kThreads) void k_bias_add_pair_flat(const float* __restrict__ x,
+                                                                 const float* __restrict__ b,
+                                                                 const float* __restrict__ u,
+                                                                 const float* __restrict__ v, float* __restrict__ yu,
+                                                                 float* __restrict__ yv, uint32_t n4, uint32_t pb,
+                                                                 uint32_t pu, uint32_t pv) {
+    arg_now(x);
+    arg_now(b);
+    arg_now(u);
+    arg_now(v);
+    arg_now(yu);
+    arg_now(yv);
+    const uint32_t iu = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t i = iu < n4 ? iu : n4 - 1;
+    const float4 xv = *reinterpret_cast<const float4*>(x + 4ull * i);
+    const float4 bv = *reinterpret_cast<const float4*>(b + 4u * (i % pb));
+    const float4 uv = *reinterpret_cast<const float4*>(u + 4u * (i % pu));
+    const float4 vv = *reinterpret_cast<const float4*>(v + 4u * (i % pv));
+    const float4 sv = make_float4(xv.x + bv.x, xv.y + bv.y, xv.z + bv.z, xv.w + bv.w);
+    if (iu < n4) {
+        *reinterpret_cast<float4*>(yu + 4ull * i) = make_float4(sv.x + uv.x, sv.y + uv.y, sv.z + uv.z, sv.w + uv.w);
+        *reinterpret_cast<float4*>(yv + 4ull * i) = make_float4(sv.x + vv.x, sv.y + vv.y, sv.z + vv.z, sv.w + vv.w);
+    }
+}
+
+__device__ __forceinline__ const char* rep_row(const View& p, int64_t i1, int64_t i2, int64_t i3) {
+    return p.data + (i1 % p.ne[1]) * p.nb[1] + (i2 % p.ne[2]) * p.nb[2] + (i3 % p.ne[3]) * p.nb[3];
+}
+
+__device__ __forceinline__ float rep_at(const char* row, const View& p, int64_t j) {
+    return *reinterpret_cast<const float*>(row + (j % p.ne[0]) * p.nb[0]);
+}
+
+// Any strides: rows of x (and yu, yv) enumerate ne1, ne2, ne3; bias, u and
+// v repeat to x by index
+__global__ __launch_bounds__(kThreads) void k_bias_add_pair_rows(View x, View b, View u, View v, View yu, View yv,
+                                                                 int64_t nr) {
+    for (int64_t q = blockIdx.x; q < nr; q += gridDim.x) {
+        const int64_t i1 = q % x.ne[1], w = q / x.ne[1];
+        const int64_t i2 = w % x.ne[2], i3 = w / x.ne[2];
+        const char* xr = x.data + i1 * x.nb[1] + i2 * x.nb[2] + i3 * x.nb[3];
+        char* ur = yu.data + i1 * yu.nb[1] + i2 * yu.nb[2] + i3 * yu.nb[3];
+        char* vr = yv.data + i1 * yv.nb[1] + i2 * yv.nb[2] + i3 * yv.nb[3];
+        const char *br = rep_row(b, i1, i2, i3), *pur = rep_row(u, i1, i2, i3), *pvr = rep_row(v, i1, i2, i3);
+        for (int64_t j = threadIdx.x; j < x.ne[0]; j += kThreads) {
+            const float sv = *reinterpret_cast<const float*>(xr + j * x.nb[0]) + rep_at(br, b, j);
+            *reinterpret_cast<float*>(ur + j * yu.nb[0]) = sv + rep_at(pur, u, j);
+            *reinterpret_cast<float*>(vr + j * yv.nb[0]) = sv + rep_at(pvr, v, j);
+        }
+    }
+}
+
 // Any strides: rows of r (and y) enumerate ne1, ne2, ne3; x's and bias's
 // rows are the repeats of the same indices (bias repeats to x and x to r,
 // so i mod bias.ne = (i mod x.ne) mod bias.ne)
@@ -213,25 +267,33 @@ __global__ __launch_bounds__(kThreads) void k_concat_flat(const V* __restrict__ 
 
 bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+// An operand p of r's leading dims (p.ne[k] == r.ne[k] below some k >= 1,
+// 1 from k on), contiguous and 16-byte aligned: the float4s of one period
+// of it in r's elements, or 0 when p is not such an operand.
+uint32_t period4(const cbx_tensor* p, const cbx_tensor* r) {
+    if (!is_contiguous(p) || !al16(p->data)) return 0;
+    int k = 0;
+    int64_t per = 1;
+    while (k < 4 && p->ne[k] == r->ne[k]) per *= r->ne[k++];
+    for (int j = k; j < 4; j++) {
+        if (p->ne[j] != 1) return 0;
+    }
+    return k >= 1 && per % 4 == 0 && per / 4 < (int64_t{1} << 31) ? static_cast<uint32_t>(per / 4) : 0;
+}
+
 template <int OP>
 void binary_go(const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y, hipStream_t s) {
     const int64_t n = nelements(a);
     const bool same = same_shape(a, b) && is_contiguous(b) && al16(b->data);
-    // b's dims equal a's below k and are 1 from k on: b repeats every
-    // `period` elements of a contiguous a
-    int k = 0;
-    int64_t period = 1;
-    while (k < 4 && b->ne[k] == a->ne[k]) period *= a->ne[k++];
-    bool lead = k >= 1 && is_contiguous(b) && al16(b->data) && period / 4 < (int64_t{1} << 31);
-    for (int j = k; j < 4; j++) lead = lead && b->ne[j] == 1;
-    const bool row = !same && lead;
+    const uint32_t per4 = period4(b, a);
+    const bool row = !same && per4 > 0;
     const bool col = b->ne[0] == 1 && b->ne[1] == a->ne[1] && b->ne[2] == 1 && b->ne[3] == 1 &&
                      (b->ne[1] == 1 || b->nb[1] == sizeof(float));
     const bool flat = is_contiguous(a) && is_contiguous(y) && al16(a->data) && al16(y->data) && a->ne[0] % 4 == 0 &&
                       n / 4 < (int64_t{1} << 31) && (same || row || col);
     if (flat) {
         const uint32_t n4 = static_cast<uint32_t>(n / 4);
-        const uint32_t ne0_4 = static_cast<uint32_t>((row ? period : a->ne[0]) / 4);
+        const uint32_t ne0_4 = row ? per4 : static_cast<uint32_t>(a->ne[0] / 4);
         const uint32_t nbr = static_cast<uint32_t>(b->ne[1]);
         const dim3 grid(static_cast<unsigned>(cdiv(n4, kThreads)));
         const float* ap = static_cast<const float*>(a->data);
@@ -285,6 +347,26 @@ int launch_bias_residual(const cbx_tensor* x, const cbx_tensor* bias, const cbx_
                            dim3(kThreads), 0, s, view_of(x), view_of(bias), view_of(r), view_of(y), nr);
     }
     return check_launch("bias residual");
+}
+
+int launch_bias_add_pair(const cbx_tensor* x, const cbx_tensor* bias, const cbx_tensor* u, const cbx_tensor* v,
+                         cbx_tensor* yu, cbx_tensor* yv, hipStream_t s) {
+    const int64_t n = nelements(x);
+    const uint32_t pb = period4(bias, x), pu = period4(u, x), pv = period4(v, x);
+    if (pb && pu && pv && is_contiguous(x) && is_contiguous(yu) && is_contiguous(yv) && al16(x->data) &&
+        al16(yu->data) && al16(yv->data) && n / 4 < (int64_t{1} << 31)) {   // pb > 0: n a multiple of 4
+        const uint32_t n4 = static_cast<uint32_t>(n / 4);
+        hipLaunchKernelGGL(k_bias_add_pair_flat, dim3(static_cast<unsigned>(cdiv(n4, kThreads))), dim3(kThreads), 0, s,
+                           static_cast<const float*>(x->data), static_cast<const float*>(bias->data),
+                           static_cast<const float*>(u->data), static_cast<const float*>(v->data),
+                           static_cast<float*>(yu->data), static_cast<float*>(yv->data), n4, pb, pu, pv);
+    } else {
+        const int64_t nr = nrows(x);
+        hipLaunchKernelGGL(k_bias_add_pair_rows, dim3(static_cast<unsigned>(std::min<int64_t>(nr, int64_t{1} << 20))),
+                           dim3(kThreads), 0, s, view_of(x), view_of(bias), view_of(u), view_of(v), view_of(yu),
+                           view_of(yv), nr);
+    }
+    return check_launch("bias add pair");
 }
 
 int launch_scale(const cbx_tensor* x, float s, cbx_tensor* y, hipStream_t strm) {

@@ -13,10 +13,13 @@ Per call the reference builds (ggml node order; [..] the given outputs):
   pre_lookahead (:435-477): [conv1] add(b as (1, C)) -> leaky_relu(0.01),
     [pad, conv2] add(b as (1, C)), [transposed] add(., x)
   6 conformer blocks over T tokens (:306-406): layer_norm (eps 1e-12) ->
-    [q, k, v] add(b) each; q viewed as (64, 8, T) -> add(pos_bias_u as
-    (64, 8, 1)), add(pos_bias_v); [AC, BD shifted] add -> scale(1/8) ->
-    soft_max; [attn, out] add(b) -> add(x, .) -> layer_norm -> [w1] add(b)
-    -> silu -> [w2] add(b) -> add(x, .)
+    [v] add(b), [k] add(b), [q] add(b) -> viewed as (64, 8, T) -> add(.,
+    pos_bias_u as (64, 8, 1)), add(., pos_bias_v); [AC, BD shifted] add ->
+    scale(1/8) -> soft_max; [attn, out] add(b) -> add(x, .) -> layer_norm ->
+    [w1] add(b) -> silu -> [w2] add(b) -> add(x, .)
+    (v, k, q: the order ggml's depth-first graph build visits them in, from
+    the attention product V_trans x scores, whose scores read k's and q's
+    products)
   up_layer (:487-535): [nearest x2, pad, conv] add(b as (1, C)) [transposed]
   linear_no_subsample again, 4 conformer blocks over 2T, layer_norm
   (after_norm, eps 1e-5), [encoder_proj] add(b)                 (:632-660)
@@ -111,9 +114,9 @@ class FlowEncoderCall:
         LayerNorm, which the caller adds to the list (after the add before
         it, so the two join)."""
         b = self.b
-        q = b.add(self._given(f"{name}.q", (T, D)), self._bias(D))
-        self._keep(b.add(self._given(f"{name}.k", (T, D)), self._bias(D)))
         self._keep(b.add(self._given(f"{name}.v", (T, D)), self._bias(D)))
+        self._keep(b.add(self._given(f"{name}.k", (T, D)), self._bias(D)))
+        q = b.add(self._given(f"{name}.q", (T, D)), self._bias(D))
         qh = b.node_view(b.at(q).view(T, N_HEAD, HEAD_DIM), q)
         for pb in ("u", "v"):
             bias = self._rand((N_HEAD, HEAD_DIM), 0.0, 0.1)

@@ -367,6 +367,17 @@ int cbx_binary(int op, const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y,
 int cbx_bias_residual(const cbx_tensor* x, const cbx_tensor* bias, const cbx_tensor* r,
                       cbx_tensor* y, cbx_stream stream);
 
+/* ggml_add(s, u) and ggml_add(s, v) of one s = ggml_add(x, bias), s not
+ * stored: yu = (x + bias) + u, yv = (x + bias) + v, each add one f32
+ * rounding.  The relative-position attention's query terms: q's bias, then
+ * pos_bias_u and pos_bias_v over the (64, 8, T) query heads
+ * (flow_encoder.cpp:320, 341-345).  bias, u and v repeat to x's shape
+ * (ggml_can_repeat); yu and yv have x's shape.  F32, any strides (nb[0]
+ * the element size); yu and yv overlap neither each other nor an input.   */
+int cbx_bias_add_pair(const cbx_tensor* x, const cbx_tensor* bias, const cbx_tensor* u,
+                      const cbx_tensor* v, cbx_tensor* yu, cbx_tensor* yv,
+                      cbx_stream stream);
+
 /* ggml_scale(x, s): y = x * s, one f32 rounding.  The mean of a HiFT
  * stage's three resblocks, scale(sum, 1/3) (hift_vocoder.cpp:736).  F32,
  * any strides (nb[0] the element size); y x's shape, and may be x itself
@@ -713,6 +724,8 @@ typedef enum cbx_glaunch_kind {
     CBX_GL_BIAS_RESIDUAL,     /* add(x, bias) [-> view (same dims)] -> add(r, .)
                                  with no norm after it (cbx_bias_residual)      */
     CBX_GL_SCALE,             /* one scale no soft_max follows (cbx_scale)      */
+    CBX_GL_BIAS_ADD_PAIR,     /* add(x, bias) -> view (a contiguous reshape) ->
+                                 add(., u), add(., v) (cbx_bias_add_pair)       */
 } cbx_glaunch_kind;
 
 typedef struct cbx_glaunch {

@@ -19,14 +19,14 @@ def test_plan_counts(T, n_blocks, n_up):
     L = n_blocks + n_up
     assert dict(got) == {
         "GL_GET_ROWS": 1,                     # the speech-token embedding
-        # per block the q, k, v bias adds and the w1 bias + silu; the two
+        # per block the k and v bias adds and the w1 bias + silu; the two
         # embed linears' bias, the two pre-lookahead convs' and the up conv's
         # bias (as (1, C)), the encoder_proj bias
-        "GL_BIAS_ACT": 4 * L + 6,
-        # per block q as heads and pos_bias_u, pos_bias_v as (64, 8, 1); the
-        # three conv biases as (1, C)
-        "GL_VIEW": 3 * L + 3,
-        "GL_BINARY": 2 * L,                   # q + pos_bias_u, q + pos_bias_v
+        "GL_BIAS_ACT": 3 * L + 6,
+        # per block q's bias, then q + pos_bias_u and q + pos_bias_v (with
+        # q's view as heads and pos_bias_u, pos_bias_v's as (64, 8, 1))
+        "GL_BIAS_ADD_PAIR": L,
+        "GL_VIEW": 3,                         # the three conv biases as (1, C)
         "GL_SOFT_MAX": L,                     # AC + BD -> scale(1/8) -> soft_max
         # per block x + (out + b) -> LN; w2 bias + residual -> the next LN
         # (the up stack's last: after_norm); the pre-lookahead's residual ->
@@ -40,4 +40,5 @@ def test_plan_counts(T, n_blocks, n_up):
     }
     assert sum(p[2] for p in plan) == len(e.graph.nodes)
     assert all(p[2] == 3 for p in plan if p[0] == C.GL_SOFT_MAX)
+    assert all(p[2] == 6 for p in plan if p[0] == C.GL_BIAS_ADD_PAIR)
     assert e.graph.nodes[-1].dst == e.out and tuple(e.b.shape(e.out)) == (2 * T, 80)

@@ -51,6 +51,46 @@ def test_binary_repeat_shapes(cbx, oracle, op, sa, sb):
     assert_bitexact(got, exp, f"op {op} {sa} by {sb}")
 
 
+@pytest.mark.parametrize("sx,sb,su", [
+    ((250, 8, 64), (1, 8, 64), (1, 8, 64)),    # q's bias (re-described over the heads), pos_bias_u / v
+    ((500, 8, 64), (1, 1, 64), (1, 8, 64)),
+    ((7, 3, 10), (1, 3, 10), (1, 1, 10)),      # rows of 10: the row map
+    ((4, 6, 8), (4, 1, 8), (1, 6, 1)),         # repeats inside: the row map
+])
+def test_bias_add_pair(cbx, oracle, sx, sb, su):
+    """cbx_bias_add_pair: (x + bias) + u and (x + bias) + v, bit-exact to the
+    oracle's two adds in ggml's order."""
+    x = W.normal(W.seed_of(44, sx[0]), sx, 0.0, 2.0)
+    b = W.normal(W.seed_of(45, sx[0]), sb, 0.0, 0.5)
+    u = W.normal(W.seed_of(46, sx[0]), su, 0.0, 0.5)
+    v = W.normal(W.seed_of(47, sx[0]), su, 0.0, 0.5)
+    yu, yv = cbx.bias_add_pair(dev(x), dev(b), dev(u), dev(v))
+    s = oracle.add(x, b)
+    assert_bitexact(host(yu), oracle.add(s, u), f"{sx} + u")
+    assert_bitexact(host(yv), oracle.add(s, v), f"{sx} + v")
+
+
+def test_bias_add_pair_strided_and_refusals(cbx, oracle):
+    """x a column slice of a wider buffer (the row map), and the refusals:
+    outputs that overlap an input or each other, operands that do not
+    repeat."""
+    base = W.normal(W.seed_of(48, 0), (30, 80), 0.0, 1.0)
+    b, u, v = (W.normal(W.seed_of(48, k), (64,), 0.0, 1.0) for k in (1, 2, 3))
+    x = dev(base)[:, 8:72]
+    yu, yv = cbx.bias_add_pair(x, dev(b), dev(u), dev(v))
+    s = oracle.add(np.ascontiguousarray(base[:, 8:72]), b)
+    assert_bitexact(host(yu), oracle.add(s, u), "strided + u")
+    assert_bitexact(host(yv), oracle.add(s, v), "strided + v")
+    xt, bt, ut, vt = dev(base[:, :64]), dev(b), dev(u), dev(v)
+    with pytest.raises(cbx.CbxError, match="overlaps an input"):
+        cbx.bias_add_pair(xt, bt, ut, vt, out_u=xt)
+    y = torch.zeros(30, 64, device="cuda")
+    with pytest.raises(cbx.CbxError, match="yu and yv overlap"):
+        cbx.bias_add_pair(xt, bt, ut, vt, out_u=y, out_v=y)
+    with pytest.raises(cbx.CbxError, match="repeat"):
+        cbx.bias_add_pair(xt, dev(np.zeros(48, np.float32)), ut, vt)
+
+
 def test_binary_views_and_in_place(cbx, oracle):
     """Strided a, b and y (column slices of wider buffers), and y == a."""
     base = W.normal(W.seed_of(42, 0), (60, 50), 0.0, 1.0)

@@ -337,6 +337,53 @@ def test_score_terms_add_joins_the_soft_max(with_scale, with_mask):
     assert plan[0][0] != C.GL_SOFT_MAX and plan[-1] == (C.GL_SOFT_MAX, n - 1, 1, 0)
 
 
+def test_query_bias_and_pos_bias_pair():
+    """flow_encoder.cpp:320, 341-345: add(q_mm, q_b) -> reshape to (64, 8, T)
+    heads -> add(., pos_bias_u), add(., pos_bias_v) is one launch; the sum
+    or the heads read elsewhere, or a view that is not a contiguous reshape,
+    leave the bias add and the two adds apart."""
+    def build(T=10, keep_sum=False, keep_heads=False, sliced=False, third_reader=False):
+        g = C.Graph()
+        q_mm, q_b = g.tensor(f32(T, 512)), g.tensor(f32(512))
+        s_t = f32(T, 512)
+        s = g.tensor(s_t)
+        g.node(C.GOP_ADD, s, (q_mm, q_b))
+        heads = s_t[:, :256].view(T, 4, 64) if sliced else s_t.view(T, 8, 64)
+        vw = g.tensor(heads)
+        g.node(C.GOP_VIEW, vw, (s,))
+        shp = tuple(heads.shape)
+        u, v = g.tensor(f32(1, *shp[1:])), g.tensor(f32(1, *shp[1:]))
+        g.node(C.GOP_ADD, g.tensor(f32(*shp)), (vw, u))
+        g.node(C.GOP_ADD, g.tensor(f32(*shp)), (vw, v))
+        if third_reader:
+            g.node(C.GOP_ADD, g.tensor(f32(*shp)), (vw, u))
+        keep = ([s] if keep_sum else []) + ([vw] if keep_heads else [])
+        return g.plan(keep=keep)
+
+    assert build() == [(C.GL_BIAS_ADD_PAIR, 0, 4, 0)]
+    assert build(T=1) == [(C.GL_BIAS_ADD_PAIR, 0, 4, 0)]
+    # the (8, 64) weights reshaped to (64, 8, 1) by views among the adds
+    g = C.Graph()
+    q_mm, q_b = g.tensor(f32(10, 512)), g.tensor(f32(512))
+    s_t = f32(10, 512)
+    s = g.tensor(s_t)
+    g.node(C.GOP_ADD, s, (q_mm, q_b))
+    vw = g.tensor(s_t.view(10, 8, 64))
+    g.node(C.GOP_VIEW, vw, (s,))
+    for _ in range(2):
+        w = f32(8, 64)
+        w3 = g.tensor(w.view(1, 8, 64))
+        g.node(C.GOP_VIEW, w3, (g.tensor(w),))
+        g.node(C.GOP_ADD, g.tensor(f32(10, 8, 64)), (vw, w3))
+    assert g.plan() == [(C.GL_BIAS_ADD_PAIR, 0, 6, 0)]
+    apart = [(C.GL_BIAS_ACT, 0, 1, 0), (C.GL_VIEW, 1, 1, 0), (C.GL_BINARY, 2, 1, C.BINARY_ADD),
+             (C.GL_BINARY, 3, 1, C.BINARY_ADD)]
+    assert build(keep_sum=True) == apart
+    assert build(keep_heads=True) == apart
+    assert build(third_reader=True)[:4] == apart
+    assert build(sliced=True)[0] != (C.GL_BIAS_ADD_PAIR, 0, 4, 0)
+
+
 def test_soft_max_with_own_scale_does_not_absorb_scale():
     g = C.Graph()
     kq = g.tensor(f32(4, 8))
@@ -557,7 +604,8 @@ def test_random_lists_plan_into_an_exact_cover():
              C.GL_LEAKY_RELU: {1}, C.GL_ROPE: {1}, C.GL_CPY: {1}, C.GL_ADD_LAYER_NORM: {4, 5, 7, 8},
              C.GL_LAYER_NORM_MASK: {4, 7}, C.GL_BIAS_ACT: {1, 2, 4}, C.GL_CONV1D: set(range(9, 18)),
              C.GL_CONV_TRANSPOSE1D: set(range(7, 15)), C.GL_CAUSAL_CONV1D: set(range(12, 16)),
-             C.GL_BINARY: {1}, C.GL_CONCAT: {1}, C.GL_BIAS_RESIDUAL: {2, 3}, C.GL_SCALE: {1}}
+             C.GL_BINARY: {1}, C.GL_CONCAT: {1}, C.GL_BIAS_RESIDUAL: {2, 3}, C.GL_SCALE: {1},
+             C.GL_BIAS_ADD_PAIR: {4, 5, 6}}
     shapes = [(4, 8), (8,), (1, 8, 1, 1), (4, 8), (4, 1)]
     for trial in range(200):
         g = C.Graph()
