@@ -13,11 +13,12 @@
 //
 // Rows up to 4096 with ne0 % 4 == 0: one wave per row, the row in
 // registers (one read, one write), the max by a butterfly of lane shuffles
-// (exact in any order), the sum by the f64 DPP butterfly.  Few rows up to
-// 4096 (a decode step's): a workgroup per row (a wave up to 1024), the row
-// in registers, one kernel for every length.  Rows up to 1024 not a
-// multiple of 4: a wave per row, the same kernel.  Other rows: a workgroup
-// per row, three passes.
+// (exact in any order), the sum by the f64 DPP butterfly; rows up to 2048
+// with ne0 % 2 == 0 at 8-byte steps the same in float2s (the 25 Hz
+// conformer blocks' 250 keys).  Few rows up to 4096 (a decode step's): a
+// workgroup per row (a wave up to 1024), the row in registers, one kernel
+// for every length.  Other rows up to 1024: a wave per row, the same
+// kernel.  Longer ones: a workgroup per row, three passes.
 #include "cbx_rowops.h"
 
 namespace cbx {
@@ -74,10 +75,29 @@ struct SoftMaxArgs {
     float s;
 };
 
+// VW consecutive scores a lane per load: 4 (float4) for rows at 16-byte
+// steps, 2 (float2) for rows at 8-byte steps (the 25 Hz conformer blocks'
+// 250 keys, rows 1000 bytes apart)
+template <int VW>
+__device__ __forceinline__ float4 load_v(const char* p) {
+    if constexpr (VW == 4) {
+        return Elt<float>::load4(p);
+    } else {
+        const float2 t = *reinterpret_cast<const float2*>(p);
+        return make_float4(t.x, t.y, 0.0f, 0.0f);
+    }
+}
+
+template <int VW>
+__device__ __forceinline__ void store_v(char* p, float4 v) {
+    if constexpr (VW == 4) Elt<float>::store4(p, v);
+    else *reinterpret_cast<float2*>(p) = make_float2(v.x, v.y);
+}
+
 // WPB rows per workgroup; with one, the grid is exactly one workgroup per
 // row and nothing waits (bounds check, block size) before the loads issue.
 // FLAT: rows at one stride each, so the row map's flag is not tested either.
-template <int NV, int WPB, bool FLAT, bool ADD>
+template <int NV, int WPB, bool FLAT, bool ADD, int VW>
 __global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
     // every field in the first batch of argument loads (left alone, the
     // compiler loads the row count first and the rest after its test: a
@@ -106,16 +126,16 @@ __global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
     float4 v[NV], w[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        const int64_t c = (lane + 64 * k) * 4;
-        v[k] = Elt<float>::load4(xr + (c < ne0 ? c : 0) * 4);
-        if constexpr (ADD) w[k] = Elt<float>::load4(br + (c < ne0 ? c : 0) * 4);
+        const int64_t c = (lane + 64 * k) * VW;
+        v[k] = load_v<VW>(xr + (c < ne0 ? c : 0) * 4);
+        if constexpr (ADD) w[k] = load_v<VW>(br + (c < ne0 ? c : 0) * 4);
     }
     float m = -INFINITY;
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        const int64_t c = (lane + 64 * k) * 4;
+        const int64_t c = (lane + 64 * k) * VW;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
+        for (int e = 0; e < VW; e++) {
             const float x = ADD ? get(v[k], e) + get(w[k], e) : get(v[k], e);
             const float t = masked(x, s, c + e, lim);
             set(v[k], e, t);
@@ -127,7 +147,7 @@ __global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
 #pragma unroll
     for (int k = 0; k < NV; k++) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
+        for (int e = 0; e < VW; e++) {
             const float ev = expf(get(v[k], e) - m);
             set(v[k], e, ev);
             sum += static_cast<double>(ev);
@@ -137,9 +157,9 @@ __global__ __launch_bounds__(64 * WPB) void k_soft_max_wave(SoftMaxArgs a) {
     const float inv = static_cast<float>(1.0 / sum);
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-        const int64_t c = (lane + 64 * k) * 4;
-        if (c < ne0) {   // ne0 % 4 == 0: whole vectors
-            Elt<float>::store4(yr + c * 4, make_float4(v[k].x * inv, v[k].y * inv, v[k].z * inv, v[k].w * inv));
+        const int64_t c = (lane + 64 * k) * VW;
+        if (c < ne0) {   // ne0 % VW == 0: whole vectors
+            store_v<VW>(yr + c * 4, make_float4(v[k].x * inv, v[k].y * inv, v[k].z * inv, v[k].w * inv));
         }
     }
 }
@@ -228,8 +248,8 @@ __global__ __launch_bounds__(kThreads) void k_soft_max_row(SoftMaxArgs a) {
 }
 
 // Rows of up to 1024 scores at any alignment (the T3 decode step's 16 rows
-// of n_past + 1 columns, n_past < 1024; the 25 Hz conformer blocks' 250
-// keys, flow_encoder.cpp:369-372, s3enc.cpp:260-262): one wave a row, up to 16
+// of n_past + 1 columns, n_past < 1024; many rows of odd length): one wave
+// a row, up to 16
 // columns a lane (column lane + 64 k), the max and the f64 sum by DPP
 // butterflies -- no LDS and no barrier.  One kernel for every length up to
 // 1024, like k_soft_max_row.
@@ -336,21 +356,32 @@ SoftMaxArgs sm_args(const cbx_tensor* x, const cbx_tensor* b, cbx_tensor* y, flo
 
 int waves_for(int64_t rows, const DeviceState* st) { return rows >= int64_t{8} * st->n_cu ? 4 : 1; }
 
-template <int WPB, bool FLAT, bool ADD>
+template <int WPB, bool FLAT, bool ADD, int VW>
 void sm_wave(int nv, const SoftMaxArgs& a, hipStream_t strm) {
     const dim3 grid(static_cast<unsigned>(cdiv(a.nr, WPB))), block(64 * WPB);
     switch (nv) {
-        case 1: hipLaunchKernelGGL((k_soft_max_wave<1, WPB, FLAT, ADD>), grid, block, 0, strm, a); break;
-        case 2: hipLaunchKernelGGL((k_soft_max_wave<2, WPB, FLAT, ADD>), grid, block, 0, strm, a); break;
-        case 4: hipLaunchKernelGGL((k_soft_max_wave<4, WPB, FLAT, ADD>), grid, block, 0, strm, a); break;
-        case 8: hipLaunchKernelGGL((k_soft_max_wave<8, WPB, FLAT, ADD>), grid, block, 0, strm, a); break;
-        default: hipLaunchKernelGGL((k_soft_max_wave<16, WPB, FLAT, ADD>), grid, block, 0, strm, a); break;
+        case 1: hipLaunchKernelGGL((k_soft_max_wave<1, WPB, FLAT, ADD, VW>), grid, block, 0, strm, a); break;
+        case 2: hipLaunchKernelGGL((k_soft_max_wave<2, WPB, FLAT, ADD, VW>), grid, block, 0, strm, a); break;
+        case 4: hipLaunchKernelGGL((k_soft_max_wave<4, WPB, FLAT, ADD, VW>), grid, block, 0, strm, a); break;
+        case 8: hipLaunchKernelGGL((k_soft_max_wave<8, WPB, FLAT, ADD, VW>), grid, block, 0, strm, a); break;
+        default: hipLaunchKernelGGL((k_soft_max_wave<16, WPB, FLAT, ADD, VW>), grid, block, 0, strm, a); break;
     }
 }
 
+// the wave-per-row kernel for rows of VW-float vectors (NV of them a lane)
+template <bool ADD, int VW>
+void sm_waves(const SoftMaxArgs& a, int64_t ne0, const DeviceState* st, hipStream_t strm) {
+    const int64_t need = cdiv(ne0, 64 * VW);
+    const int nv = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : 16;
+    // strided-plane layouts take one row per workgroup through the row map
+    if (!(a.mx.flat && a.my.flat && (!ADD || a.mb.flat))) sm_wave<1, false, ADD, VW>(nv, a, strm);
+    else if (waves_for(a.nr, st) == 1) sm_wave<1, true, ADD, VW>(nv, a, strm);
+    else sm_wave<4, true, ADD, VW>(nv, a, strm);
+}
+
 template <bool ADD>
-void sm_launch(const SoftMaxArgs& a, int64_t ne0, bool vec, const View& vx, const View& vb, const View& vy,
-               bool fx, bool fb, bool fy, const DeviceState* st, hipStream_t strm) {
+void sm_launch(const SoftMaxArgs& a, int64_t ne0, bool vec, bool vec2, const View& vx, const View& vb,
+               const View& vy, bool fx, bool fb, bool fy, const DeviceState* st, hipStream_t strm) {
     const int64_t nr = a.nr;
     if (ne0 <= kWaveMaxRow && nr < int64_t{4} * st->n_cu) {
         // few rows (a decode step's heads): one kernel whatever the length
@@ -364,31 +395,29 @@ void sm_launch(const SoftMaxArgs& a, int64_t ne0, bool vec, const View& vx, cons
         } else {
             hipLaunchKernelGGL((k_soft_max_row<false, ADD>), grid, dim3(kThreads), 0, strm, a);
         }
-    } else if (!vec && ne0 <= 1024) {
-        // many unaligned rows up to 1024 (the 25 Hz conformer blocks' 250
-        // keys): one wave a row, as for few rows, not three passes
+    } else if (vec) {
+        sm_waves<ADD, 4>(a, ne0, st, strm);
+    } else if (vec2) {
+        sm_waves<ADD, 2>(a, ne0, st, strm);
+    } else if (ne0 <= 1024) {
+        // many rows of odd length up to 1024: one wave a row, as for few
+        // rows, not three passes
         const dim3 grid(static_cast<unsigned>(nr));
         if (a.mx.flat && a.my.flat && (!ADD || a.mb.flat)) {
             hipLaunchKernelGGL((k_soft_max_row_w<true, ADD>), grid, dim3(WAVE), 0, strm, a);
         } else {
             hipLaunchKernelGGL((k_soft_max_row_w<false, ADD>), grid, dim3(WAVE), 0, strm, a);
         }
-    } else if (vec) {
-        const int64_t need = cdiv(ne0, 256);
-        const int nv = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : need <= 8 ? 8 : 16;
-        // strided-plane layouts take one row per workgroup through the row map
-        if (!(a.mx.flat && a.my.flat && (!ADD || a.mb.flat))) sm_wave<1, false, ADD>(nv, a, strm);
-        else if (waves_for(nr, st) == 1) sm_wave<1, true, ADD>(nv, a, strm);
-        else sm_wave<4, true, ADD>(nv, a, strm);
     } else {
         hipLaunchKernelGGL(k_soft_max_loop, dim3(static_cast<unsigned>(nr)), dim3(kThreads), 0, strm, vx, vb, vy, a.s,
                            a.n_past, fx, fb, fy);
     }
 }
 
-bool vec_rows(const cbx_tensor* t) {
-    return reinterpret_cast<uintptr_t>(t->data) % 16 == 0 && t->nb[1] % 16 == 0 && (t->ne[2] <= 1 || t->nb[2] % 16 == 0) &&
-           (t->ne[3] <= 1 || t->nb[3] % 16 == 0);
+// every row of t starts at a multiple of `al` bytes
+bool vec_rows(const cbx_tensor* t, size_t al) {
+    return reinterpret_cast<uintptr_t>(t->data) % al == 0 && t->nb[1] % al == 0 && (t->ne[2] <= 1 || t->nb[2] % al == 0) &&
+           (t->ne[3] <= 1 || t->nb[3] % al == 0);
 }
 
 }  // namespace
@@ -397,14 +426,16 @@ int launch_soft_max(const cbx_tensor* x, const cbx_tensor* b, float s, int64_t n
                     DeviceState* st, hipStream_t strm) {
     const int64_t nr = nrows(x), ne0 = x->ne[0];
     if (nr >= (int64_t{1} << 31)) return set_error(CBX_ERR_UNSUPPORTED, "soft_max: too many rows");
-    const bool vec = ne0 <= kWaveMaxRow && ne0 % 4 == 0 && vec_rows(x) && vec_rows(y) && (!b || vec_rows(b));
+    const bool vec = ne0 <= kWaveMaxRow && ne0 % 4 == 0 && vec_rows(x, 16) && vec_rows(y, 16) && (!b || vec_rows(b, 16));
+    const bool vec2 = ne0 <= kWaveMaxRow / 2 && ne0 % 2 == 0 && vec_rows(x, 8) && vec_rows(y, 8) && (!b || vec_rows(b, 8));
     View vb{};
     if (b) vb = view_of(b);
     const SoftMaxArgs a = sm_args(x, b, y, s, n_past, nr);
     if (b) {
-        sm_launch<true>(a, ne0, vec, view_of(x), vb, view_of(y), flat_rows(x), flat_rows(b), flat_rows(y), st, strm);
+        sm_launch<true>(a, ne0, vec, vec2, view_of(x), vb, view_of(y), flat_rows(x), flat_rows(b), flat_rows(y), st,
+                        strm);
     } else {
-        sm_launch<false>(a, ne0, vec, view_of(x), vb, view_of(y), flat_rows(x), false, flat_rows(y), st, strm);
+        sm_launch<false>(a, ne0, vec, vec2, view_of(x), vb, view_of(y), flat_rows(x), false, flat_rows(y), st, strm);
     }
     return check_launch("soft_max");
 }

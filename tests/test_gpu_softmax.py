@@ -86,8 +86,9 @@ def test_few_rows_planes_not_at_one_stride(cbx, oracle, n):
     check(got, exp, f"planes apart, n={n}", mask_of((2, 3, n), n - 3))
 
 
-@pytest.mark.parametrize("shape,n_past", [((8, 250, 250), -1), ((1500, 1023), 600), ((2, 700, 1021), 0),
-                                          ((1100, 1025), 3)])
+@pytest.mark.parametrize("shape,n_past", [((8, 250, 250), -1), ((20, 250, 250), 100), ((1500, 1023), 600),
+                                          ((2, 700, 1021), 0), ((1100, 1025), 3), ((1100, 2046), 1000),
+                                          ((1100, 2050), -1)])
 def test_many_unaligned_rows(cbx, oracle, shape, n_past):
     """Many rows whose length is not a multiple of 4: a wave a row up to
     1024 columns (the 25 Hz conformer blocks' 250 keys), three passes past
@@ -98,13 +99,19 @@ def test_many_unaligned_rows(cbx, oracle, shape, n_past):
           mask_of(shape, n_past) if n_past >= 0 else None)
 
 
-def test_many_unaligned_rows_planes_apart(cbx, oracle):
+@pytest.mark.parametrize("c0", [2, 3])
+def test_many_unaligned_rows_planes_apart(cbx, oracle, c0):
     """The same over a slice of a 3-D tensor (planes not one row stride
-    apart): the row map."""
+    apart): the row map, with rows at 8-byte steps (float2 loads, c0 2) or
+    at 4-byte ones (c0 3)."""
     base = W.normal(170, (4, 300, 260), 0.0, 6.0)
-    v = dev(base)[:, 10:290, 3:253]
-    exp = oracle.scale_diag_mask_soft_max(np.ascontiguousarray(base[:, 10:290, 3:253]), 0.5, 7, nth=8)
+    v = dev(base)[:, 10:290, c0:c0 + 250]
+    exp = oracle.scale_diag_mask_soft_max(np.ascontiguousarray(base[:, 10:290, c0:c0 + 250]), 0.5, 7, nth=8)
     check(host(cbx.scale_diag_mask_soft_max(v, 0.5, 7)), exp, "planes apart", mask_of((4, 280, 250), 7))
+    b = W.normal(171, (4, 280, 250), 0.0, 2.0)
+    exp = oracle.scale_diag_mask_soft_max(oracle.add(np.ascontiguousarray(base[:, 10:290, c0:c0 + 250]), b), 0.5, -1,
+                                          nth=8)
+    check(host(cbx.add_scale_diag_mask_soft_max(v, dev(b), 0.5)), exp, "planes apart, with the added row")
 
 
 def test_strided_rows_and_extremes(cbx, oracle):
