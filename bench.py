@@ -801,7 +801,8 @@ def estimator_bytes(C, e, plan):
     """Bytes one node-list call's launches move: per launch, every tensor it
     reads from outside the launch once (a causal conv's weights as their
     prepared f16 copy, a gather's table as the rows it gathers) and every
-    tensor it stores."""
+    tensor it stores (the last node's, the stored residual sum, the first
+    of two outputs)."""
     nd, at = e.graph.nodes, e.b.at
     total = 0
     for kind, f, n, flags in plan:
@@ -821,6 +822,9 @@ def estimator_bytes(C, e, plan):
         total += y.numel() * y.element_size()
         if kind == C.GL_ADD_LAYER_NORM and not flags & 1:
             total += y.numel() * y.element_size()   # the residual sum, stored too
+        if kind in (C.GL_BIAS_ADD_TWO, C.GL_BIAS_ADD_PAIR):   # two outputs: the other one
+            k = f if kind == C.GL_BIAS_ADD_TWO else next(j for j in range(f + 2, f + n) if nd[j].op == C.GOP_ADD)
+            total += at(nd[k].dst).numel() * at(nd[k].dst).element_size()
     return total
 
 

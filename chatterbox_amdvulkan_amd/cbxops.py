@@ -116,7 +116,7 @@ GL_UNSUPPORTED, GL_VIEW, GL_GET_ROWS, GL_GET_ROWS_ADD, GL_GET_ROWS_ADD_LAYER_NOR
     GL_LAYER_NORM_ROPE, GL_RMS_NORM, GL_GROUP_NORM, GL_SOFT_MAX, GL_SNAKE, GL_UNARY, GL_SWIGLU, GL_LEAKY_RELU, \
     GL_ROPE, GL_CPY, GL_ADD_LAYER_NORM, GL_LAYER_NORM_MASK, GL_BIAS_ACT, GL_CONV1D, GL_CONV_TRANSPOSE1D, \
     GL_CAUSAL_CONV1D, GL_GET_ROWS_CONCAT_ADD_LAYER_NORM, GL_BINARY, GL_CONCAT, \
-    GL_BIAS_RESIDUAL, GL_SCALE, GL_BIAS_ADD_PAIR = range(29)
+    GL_BIAS_RESIDUAL, GL_SCALE, GL_BIAS_ADD_PAIR, GL_BIAS_ADD_TWO = range(30)
 # conv launch flags: the prologue (bits 0-1), a bias add, the residual add
 GLF_SNAKE, GLF_LEAKY, GLF_MASK, GLF_BIAS, GLF_RESIDUAL, GLF_SUM, GLF_SCALE = 1, 2, 3, 4, 8, 16, 32
 
@@ -189,6 +189,7 @@ def load() -> ctypes.CDLL:
         "cbx_concat": (i, [P, P, i, P, vp]),
         "cbx_bias_residual": (i, [P, P, P, P, vp]),
         "cbx_bias_add_pair": (i, [P, P, P, P, P, P, vp]),
+        "cbx_bias_add_two": (i, [P, P, P, P, P, P, vp]),
         "cbx_scale": (i, [P, f, P, vp]),
         "cbx_conv1d_weights_create": (i, [P, vp, ctypes.POINTER(vp)]),
         "cbx_conv1d_weights_destroy": (None, [vp]),
@@ -689,6 +690,17 @@ def bias_add_pair(x, bias, u, v, out_u=None, out_v=None):
     _check(load().cbx_bias_add_pair(_ref(desc(x)), _ref(desc(bias)), _ref(desc(u)), _ref(desc(v)), _ref(desc(out_u)),
                                     _ref(desc(out_v)), _stream()))
     return out_u, out_v
+
+
+def bias_add_two(x0, b0, x1, b1, out0=None, out1=None):
+    """x0 + b0 and x1 + b1, two independent bias adds in one launch."""
+    _ready(x0)
+    _ready(x1)
+    out0 = _out_like(x0, out0)
+    out1 = _out_like(x1, out1)
+    _check(load().cbx_bias_add_two(_ref(desc(x0)), _ref(desc(b0)), _ref(desc(out0)), _ref(desc(x1)), _ref(desc(b1)),
+                                   _ref(desc(out1)), _stream()))
+    return out0, out1
 
 
 def scale(x, s, out=None):

@@ -153,6 +153,16 @@ static void yarn_cos_sin(float theta_extrap, int64_t i0, const RopeParams& p, fl
     *s = sinf(theta) * mscale;
 }
 
+bool bytes_overlap(const cbx_tensor* a, const cbx_tensor* b) {
+    auto span = [](const cbx_tensor* t) {
+        size_t hi = type_size(t->type);
+        for (int i = 0; i < 4; i++) hi += static_cast<size_t>(t->ne[i] > 0 ? t->ne[i] - 1 : 0) * t->nb[i];
+        return hi;
+    };
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a->data), b0 = reinterpret_cast<uintptr_t>(b->data);
+    return a0 < b0 + span(b) && b0 < a0 + span(a);
+}
+
 }  // namespace cbx
 
 struct cbx_conv1d_weights {
@@ -497,15 +507,7 @@ static int check_f32_like(const cbx_tensor* t, const cbx_tensor* x, const char* 
 }
 
 // Byte ranges of two tensors' rows overlap.
-static bool overlaps(const cbx_tensor* a, const cbx_tensor* b) {
-    auto span = [](const cbx_tensor* t) {
-        size_t hi = type_size(t->type);
-        for (int i = 0; i < 4; i++) hi += static_cast<size_t>(t->ne[i] > 0 ? t->ne[i] - 1 : 0) * t->nb[i];
-        return hi;
-    };
-    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a->data), b0 = reinterpret_cast<uintptr_t>(b->data);
-    return a0 < b0 + span(b) && b0 < a0 + span(a);
-}
+static bool overlaps(const cbx_tensor* a, const cbx_tensor* b) { return bytes_overlap(a, b); }
 
 int cbx_add_layer_norm(const cbx_tensor* a, const cbx_tensor* a_bias, const cbx_tensor* r, const cbx_tensor* w,
                        const cbx_tensor* b, float eps, int act, cbx_tensor* s, cbx_tensor* y, cbx_stream stream) {
@@ -954,6 +956,41 @@ int cbx_bias_act(int act, const cbx_tensor* x, const cbx_tensor* bias, cbx_tenso
     if (!is_contiguous(bias)) return set_error(CBX_ERR_UNSUPPORTED, "cbx_bias_act: bias must be contiguous");
     if (nelements(x) == 0) return CBX_OK;
     return launch_bias_act(act, x, bias, y, st, reinterpret_cast<hipStream_t>(stream));
+}
+
+int cbx_bias_add_two(const cbx_tensor* x0, const cbx_tensor* b0, cbx_tensor* y0, const cbx_tensor* x1,
+                     const cbx_tensor* b1, cbx_tensor* y1, cbx_stream stream) {
+    const char* what = "cbx_bias_add_two";
+    clear_error();
+    int rc;
+    DeviceState* st = current_state(&rc);
+    if (!st) return rc;
+    const cbx_tensor* xs[2] = {x0, x1};
+    const cbx_tensor* bs[2] = {b0, b1};
+    const cbx_tensor* ys[2] = {y0, y1};
+    for (int k = 0; k < 2; k++) {
+        if ((rc = validate(xs[k], what, k ? "x1" : "x0")) || (rc = validate(bs[k], what, k ? "b1" : "b0")) ||
+            (rc = validate(ys[k], what, k ? "y1" : "y0"))) {
+            return rc;
+        }
+        const cbx_tensor *x = xs[k], *b = bs[k], *y = ys[k];
+        if (x->type != CBX_TYPE_F32 || b->type != CBX_TYPE_F32 || y->type != CBX_TYPE_F32) {
+            return set_error(CBX_ERR_UNSUPPORTED, "cbx_bias_add_two: F32 only");
+        }
+        if (!same_shape(x, y)) return set_error(CBX_ERR_INVALID_ARG, "cbx_bias_add_two: an x and its y differ in shape");
+        const bool inner = b->ne[0] == x->ne[0] && b->ne[1] == 1 && b->ne[2] == 1 && b->ne[3] == 1;
+        const bool outer = b->ne[0] == 1 && b->ne[1] == x->ne[1] && b->ne[2] == 1 && b->ne[3] == 1;
+        if ((!inner && !outer) || !is_contiguous(b)) {
+            return set_error(CBX_ERR_UNSUPPORTED,
+                             "cbx_bias_add_two: each bias contiguous with ne = (x.ne0,1,1,1) or (1,x.ne1,1,1)");
+        }
+    }
+    // the two adds run side by side: neither output may meet the other
+    // add's operands or output
+    if (overlaps(y0, x1) || overlaps(y0, b1) || overlaps(y0, y1) || overlaps(y1, x0) || overlaps(y1, b0)) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_bias_add_two: an output overlaps the other add's tensors");
+    }
+    return launch_bias_add_two(x0, b0, y0, x1, b1, y1, st, reinterpret_cast<hipStream_t>(stream));
 }
 
 // ---- conv1d -------------------------------------------------------------------

@@ -742,6 +742,25 @@ const char* op_name(int op) {
     }
 }
 
+// The bias adds at nodes i and i + 1 neither read nor write what the other
+// writes (by tensor and by bytes), and each bias is a row of its x: the two
+// may run side by side in one launch.
+bool independent_adds(const cbx_tensor* t, const cbx_gnode* nd, int32_t i) {
+    const cbx_gnode &a = nd[i], &b = nd[i + 1];
+    if (a.op != CBX_GOP_ADD || b.op != CBX_GOP_ADD) return false;
+    for (const cbx_gnode* g : {&a, &b}) {
+        if (g->src[0] < 0 || g->src[1] < 0) return false;
+        const cbx_tensor &x = t[g->src[0]], &bias = t[g->src[1]], &y = t[g->dst];
+        if (x.type != CBX_TYPE_F32 || bias.type != CBX_TYPE_F32 || y.type != CBX_TYPE_F32 || !same_shape(&x, &y) ||
+            !is_contiguous(&bias) || bias.ne[0] != x.ne[0] || nelements(&bias) != bias.ne[0]) {
+            return false;
+        }
+    }
+    const cbx_tensor *ya = &t[a.dst], *yb = &t[b.dst];
+    return !bytes_overlap(ya, &t[b.src[0]]) && !bytes_overlap(ya, &t[b.src[1]]) && !bytes_overlap(ya, yb) &&
+           !bytes_overlap(yb, &t[a.src[0]]) && !bytes_overlap(yb, &t[a.src[1]]);
+}
+
 int check_lists(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes,
                 const char* what) {
     if ((!tensors && n_tensors) || n_tensors < 0 || (!nodes && n_nodes) || n_nodes < 0) {
@@ -777,6 +796,14 @@ int plan(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, i
     for (int32_t i = 0; i < n_nodes;) {
         int32_t len = 1, flags = 0;
         const int32_t kind = p.match(i, &len, &flags);
+        // two lone bias adds in a row that do not read each other (the
+        // projections of v and k, flow_encoder.cpp:320-322): one launch
+        if (kind == CBX_GL_BIAS_ACT && len == 1 && !out->empty() && out->back().kind == CBX_GL_BIAS_ACT &&
+            out->back().n_nodes == 1 && out->back().first_node == i - 1 && independent_adds(tensors, nodes, i - 1)) {
+            out->back() = cbx_glaunch{CBX_GL_BIAS_ADD_TWO, i - 1, 2, 0};
+            i += 1;
+            continue;
+        }
         out->push_back(cbx_glaunch{kind, i, kind == CBX_GL_UNSUPPORTED ? 1 : len, flags});
         i += out->back().n_nodes;
     }
@@ -816,8 +843,9 @@ constexpr int32_t kSpan[][2] = {
     {2, 3},  // BIAS_RESIDUAL [view]
     {1, 1},  // SCALE
     {4, 6},  // BIAS_ADD_PAIR [views of u, v]
+    {2, 2},  // BIAS_ADD_TWO
 };
-constexpr int32_t kLastKind = CBX_GL_BIAS_ADD_PAIR;
+constexpr int32_t kLastKind = CBX_GL_BIAS_ADD_TWO;
 static_assert(sizeof(kSpan) / sizeof(kSpan[0]) == kLastKind + 1, "one span per launch kind");
 
 // Issues the entry point a launch maps to.  A launch is only read within
@@ -933,6 +961,12 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
         case CBX_GL_BINARY:
             if (a.op != (l.flags == CBX_BINARY_MUL ? CBX_GOP_MUL : CBX_GOP_ADD)) break;
             return cbx_binary(l.flags, T(t, a.src[0]), T(t, a.src[1]), y, s);
+        case CBX_GL_BIAS_ADD_TWO: {
+            const cbx_gnode& b = nd[f + 1];
+            if (a.op != CBX_GOP_ADD || b.op != CBX_GOP_ADD) break;
+            return cbx_bias_add_two(T(t, a.src[0]), T(t, a.src[1]), const_cast<cbx_tensor*>(&t[a.dst]),
+                                    T(t, b.src[0]), T(t, b.src[1]), y, s);
+        }
         case CBX_GL_BIAS_ADD_PAIR: {
             // the heads view, then views of other tensors and the two adds
             const cbx_gnode& v = nd[f + 1];

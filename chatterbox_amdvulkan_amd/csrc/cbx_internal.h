@@ -75,6 +75,7 @@ size_t  type_size(int type);
 bool    is_contiguous(const cbx_tensor* t);
 bool    rows_contiguous(const cbx_tensor* t);   // nb[0] == element size
 bool    same_shape(const cbx_tensor* a, const cbx_tensor* b);
+bool    bytes_overlap(const cbx_tensor* a, const cbx_tensor* b);   // the byte ranges of the two tensors meet
 // Validates pointer, type, non-negative sizes and nb[0] for a float/int
 // tensor.  Returns 0 or a negative status with the error recorded.
 int validate(const cbx_tensor* t, const char* what, const char* name);
@@ -131,6 +132,8 @@ int launch_bias_act(int op, const cbx_tensor* x, const cbx_tensor* bias, cbx_ten
 // cbx_binary and cbx_concat (k_binary.hip), arguments checked by the caller.
 int launch_binary(int op, const cbx_tensor* a, const cbx_tensor* b, cbx_tensor* y, hipStream_t s);
 int launch_scale(const cbx_tensor* x, float s, cbx_tensor* y, hipStream_t strm);
+int launch_bias_add_two(const cbx_tensor* x0, const cbx_tensor* b0, cbx_tensor* y0, const cbx_tensor* x1,
+                        const cbx_tensor* b1, cbx_tensor* y1, DeviceState* st, hipStream_t s);
 int launch_bias_add_pair(const cbx_tensor* x, const cbx_tensor* bias, const cbx_tensor* u, const cbx_tensor* v,
                          cbx_tensor* yu, cbx_tensor* yv, hipStream_t s);
 int launch_bias_residual(const cbx_tensor* x, const cbx_tensor* bias, const cbx_tensor* r, cbx_tensor* y,

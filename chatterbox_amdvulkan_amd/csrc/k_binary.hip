@@ -142,6 +142,28 @@ __global__ __launch_bounds__(kThreads) void k_bias_add_pair_flat(const float* __
     }
 }
 
+// y0 = x0 + b0 and y1 = x1 + b1, two independent bias adds over contiguous
+// tensors, each bias one period of its x's leading dims (p0, p1 float4s):
+// the first g0 workgroups take the first add's n0 float4s, the rest the
+// second's n1 (which add is uniform per workgroup)
+__global__ __launch_bounds__(kThreads) void k_bias_add_two_flat(const float* __restrict__ x0,
+                                                                const float* __restrict__ b0, float* __restrict__ y0,
+                                                                uint32_t n0, uint32_t p0, uint32_t g0,
+                                                                const float* __restrict__ x1,
+                                                                const float* __restrict__ b1, float* __restrict__ y1,
+                                                                uint32_t n1, uint32_t p1) {
+    const bool second = blockIdx.x >= g0;
+    const uint32_t i = (second ? blockIdx.x - g0 : blockIdx.x) * kThreads + threadIdx.x;
+    const float* x = second ? x1 : x0;
+    const float* b = second ? b1 : b0;
+    float* y = second ? y1 : y0;
+    const uint32_t n = second ? n1 : n0, p = second ? p1 : p0;
+    if (i >= n) return;
+    const float4 xv = *reinterpret_cast<const float4*>(x + 4ull * i);
+    const float4 bv = *reinterpret_cast<const float4*>(b + 4u * (i % p));
+    *reinterpret_cast<float4*>(y + 4ull * i) = make_float4(xv.x + bv.x, xv.y + bv.y, xv.z + bv.z, xv.w + bv.w);
+}
+
 __device__ __forceinline__ const char* rep_row(const View& p, int64_t i1, int64_t i2, int64_t i3) {
     return p.data + (i1 % p.ne[1]) * p.nb[1] + (i2 % p.ne[2]) * p.nb[2] + (i3 % p.ne[3]) * p.nb[3];
 }
@@ -347,6 +369,28 @@ int launch_bias_residual(const cbx_tensor* x, const cbx_tensor* bias, const cbx_
                            dim3(kThreads), 0, s, view_of(x), view_of(bias), view_of(r), view_of(y), nr);
     }
     return check_launch("bias residual");
+}
+
+int launch_bias_add_two(const cbx_tensor* x0, const cbx_tensor* b0, cbx_tensor* y0, const cbx_tensor* x1,
+                        const cbx_tensor* b1, cbx_tensor* y1, DeviceState* st, hipStream_t s) {
+    const int64_t m0 = nelements(x0), m1 = nelements(x1);
+    auto flat = [](const cbx_tensor* x, const cbx_tensor* b, const cbx_tensor* y) {
+        return period4(b, x) > 0 && is_contiguous(x) && is_contiguous(y) && al16(x->data) && al16(y->data);
+    };
+    const int64_t g0 = cdiv(m0 / 4, kThreads), g1 = cdiv(m1 / 4, kThreads);
+    if (m0 > 0 && m1 > 0 && flat(x0, b0, y0) && flat(x1, b1, y1) && g0 + g1 < (int64_t{1} << 31)) {
+        hipLaunchKernelGGL(k_bias_add_two_flat, dim3(static_cast<unsigned>(g0 + g1)), dim3(kThreads), 0, s,
+                           static_cast<const float*>(x0->data), static_cast<const float*>(b0->data),
+                           static_cast<float*>(y0->data), static_cast<uint32_t>(m0 / 4), period4(b0, x0),
+                           static_cast<uint32_t>(g0), static_cast<const float*>(x1->data),
+                           static_cast<const float*>(b1->data), static_cast<float*>(y1->data),
+                           static_cast<uint32_t>(m1 / 4), period4(b1, x1));
+        return check_launch("bias add two");
+    }
+    // other layouts: the two bias adds one after the other
+    int rc = m0 > 0 ? launch_bias_act(CBX_UNARY_NONE, x0, b0, y0, st, s) : CBX_OK;
+    if (rc == CBX_OK && m1 > 0) rc = launch_bias_act(CBX_UNARY_NONE, x1, b1, y1, st, s);
+    return rc;
 }
 
 int launch_bias_add_pair(const cbx_tensor* x, const cbx_tensor* bias, const cbx_tensor* u, const cbx_tensor* v,

@@ -378,6 +378,17 @@ int cbx_bias_add_pair(const cbx_tensor* x, const cbx_tensor* bias, const cbx_ten
                       const cbx_tensor* v, cbx_tensor* yu, cbx_tensor* yv,
                       cbx_stream stream);
 
+/* Two independent ggml_add(x, bias) in one launch: y0 = x0 + b0 and
+ * y1 = x1 + b1, each one f32 rounding, as cbx_bias_act with no activation.
+ * Two adjacent bias adds that do not read each other: the projections of v
+ * and k (flow_encoder.cpp:320-322), of q and v (s3enc.cpp:205-207).  Each
+ * bias contiguous with ne = (x.ne0,1,1,1) or (1,x.ne1,1,1); each y has its
+ * x's shape and may be that x itself; neither y may overlap the other
+ * add's tensors.                                                            */
+int cbx_bias_add_two(const cbx_tensor* x0, const cbx_tensor* b0, cbx_tensor* y0,
+                     const cbx_tensor* x1, const cbx_tensor* b1, cbx_tensor* y1,
+                     cbx_stream stream);
+
 /* ggml_scale(x, s): y = x * s, one f32 rounding.  The mean of a HiFT
  * stage's three resblocks, scale(sum, 1/3) (hift_vocoder.cpp:736).  F32,
  * any strides (nb[0] the element size); y x's shape, and may be x itself
@@ -725,7 +736,10 @@ typedef enum cbx_glaunch_kind {
                                  with no norm after it (cbx_bias_residual)      */
     CBX_GL_SCALE,             /* one scale no soft_max follows (cbx_scale)      */
     CBX_GL_BIAS_ADD_PAIR,     /* add(x, bias) -> view (a contiguous reshape) ->
-                                 add(., u), add(., v) (cbx_bias_add_pair)       */
+                                 [views of other tensors] add(., u), add(., v)
+                                 (cbx_bias_add_pair)                            */
+    CBX_GL_BIAS_ADD_TWO,      /* two lone bias adds in a row, independent of
+                                 each other (cbx_bias_add_two)                  */
 } cbx_glaunch_kind;
 
 typedef struct cbx_glaunch {

@@ -74,6 +74,9 @@ def run_and_check(graph, at, keep, oracle, launch, k, rope=None):
             assert n == 2 and nd[f].op == C.GOP_SCALE
             x, sc = H(nd[f].src[0]), nd[f].fparam
         softmax_close(got, oracle.scale_diag_mask_soft_max(x, sc, -1, nth=8), what)
+    elif kind == C.GL_BIAS_ADD_TWO:
+        for k in (f, f + 1):
+            assert_bitexact(H(nd[k].dst), oracle.add(H(nd[k].src[0]), H(nd[k].src[1])), f"{what} (node {k})")
     elif kind == C.GL_BIAS_ADD_PAIR:     # add -> heads view -> [views] two adds
         s = oracle.add(H(nd[f].src[0]), H(nd[f].src[1])).reshape(at(nd[f + 1].dst).shape)
         adds = [k for k in range(f + 2, f + n) if nd[k].op == C.GOP_ADD]

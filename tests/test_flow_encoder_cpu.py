@@ -19,10 +19,11 @@ def test_plan_counts(T, n_blocks, n_up):
     L = n_blocks + n_up
     assert dict(got) == {
         "GL_GET_ROWS": 1,                     # the speech-token embedding
-        # per block the k and v bias adds and the w1 bias + silu; the two
-        # embed linears' bias, the two pre-lookahead convs' and the up conv's
-        # bias (as (1, C)), the encoder_proj bias
-        "GL_BIAS_ACT": 3 * L + 6,
+        # per block the w1 bias + silu; the two embed linears' bias, the two
+        # pre-lookahead convs' and the up conv's bias (as (1, C)), the
+        # encoder_proj bias
+        "GL_BIAS_ACT": L + 6,
+        "GL_BIAS_ADD_TWO": L,                 # per block the v and k bias adds side by side
         # per block q's bias, then q + pos_bias_u and q + pos_bias_v (with
         # q's view as heads and pos_bias_u, pos_bias_v's as (64, 8, 1))
         "GL_BIAS_ADD_PAIR": L,

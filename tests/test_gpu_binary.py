@@ -244,3 +244,32 @@ def test_concat_channels_of_views(cbx):
     assert_bitexact(got, np.concatenate((x, wide[:, 10:90]), axis=1), "pack")
     with pytest.raises(cbx.CbxError):
         cbx.concat(dev(x), dev(x[:10]), 0)                                      # other dims differ
+
+
+@pytest.mark.parametrize("s0,s1,col", [((250, 512), (250, 512), False), ((500, 512), (37, 64), False),
+                                       ((20, 30), (250, 512), False), ((40, 64), (12, 64), True)])
+def test_bias_add_two(cbx, oracle, s0, s1, col):
+    """cbx_bias_add_two: two independent bias adds in one launch, each
+    bit-exact to the oracle's add; rows of 30 floats and a per-row bias
+    (1, ne1) take the two-launch fallback."""
+    x0 = W.normal(W.seed_of(50, s0[0]), s0, 0.0, 2.0)
+    x1 = W.normal(W.seed_of(51, s1[0]), s1, 0.0, 2.0)
+    b0 = W.normal(W.seed_of(52, s0[1]), (s0[1],), 0.0, 0.5)
+    b1 = W.normal(W.seed_of(53, s1[1]), (s1[0], 1) if col else (s1[1],), 0.0, 0.5)
+    y0, y1 = cbx.bias_add_two(dev(x0), dev(b0), dev(x1), dev(b1))
+    assert_bitexact(host(y0), oracle.add(x0, b0), f"{s0}")
+    assert_bitexact(host(y1), oracle.add(x1, b1), f"{s1}")
+
+
+def test_bias_add_two_in_place_and_refusals(cbx, oracle):
+    x0 = W.normal(W.seed_of(54, 0), (64, 128), 0.0, 1.0)
+    x1 = W.normal(W.seed_of(54, 1), (64, 128), 0.0, 1.0)
+    b = W.normal(W.seed_of(54, 2), (128,), 0.0, 1.0)
+    t0, t1, tb = dev(x0), dev(x1), dev(b)
+    cbx.bias_add_two(t0, tb, t1, tb, out0=t0, out1=t1)
+    assert_bitexact(host(t0), oracle.add(x0, b), "y0 = x0")
+    assert_bitexact(host(t1), oracle.add(x1, b), "y1 = x1")
+    with pytest.raises(cbx.CbxError, match="overlaps the other"):
+        cbx.bias_add_two(t0, tb, t1, tb, out0=t1)
+    with pytest.raises(cbx.CbxError, match="ne = "):
+        cbx.bias_add_two(t0, dev(np.zeros(64, np.float32)), t1, tb)

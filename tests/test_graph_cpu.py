@@ -337,6 +337,33 @@ def test_score_terms_add_joins_the_soft_max(with_scale, with_mask):
     assert plan[0][0] != C.GL_SOFT_MAX and plan[-1] == (C.GL_SOFT_MAX, n - 1, 1, 0)
 
 
+def test_two_lone_bias_adds_share_a_launch():
+    """Adjacent bias adds that neither read nor overlap each other's output
+    (v's and k's projections) are one launch; an add reading the first's
+    sum, one whose output overlaps the other's input, a column bias, or a
+    bias add that starts a longer chain stay apart."""
+    def build(dep=False, alias=False, col=False, act=False, rows=(10, 10)):
+        g = C.Graph()
+        v_mm, v_b = g.tensor(f32(rows[0], 64)), g.tensor(f32(64))
+        k_mm = g.tensor(f32(rows[1], 64))
+        k_b = g.tensor(f32(rows[1], 1) if col else f32(64))
+        v_t = f32(rows[0], 64)
+        v = g.tensor(v_t)
+        g.node(C.GOP_ADD, v, (v_mm, v_b))
+        k = g.tensor(v_t if alias else f32(rows[1], 64))
+        g.node(C.GOP_ADD, k, (v if dep else k_mm, k_b))
+        if act:
+            g.node(C.GOP_UNARY, g.tensor(f32(rows[1], 64)), (k,), iparam=C.SILU)
+        return g.plan(keep=[v] if act else [v, k])
+
+    assert build() == [(C.GL_BIAS_ADD_TWO, 0, 2, 0)]
+    assert build(rows=(10, 30)) == [(C.GL_BIAS_ADD_TWO, 0, 2, 0)]
+    assert build(dep=True) == [(C.GL_BIAS_ACT, 0, 1, 0), (C.GL_BIAS_ACT, 1, 1, 0)]
+    assert build(alias=True) == [(C.GL_BIAS_ACT, 0, 1, 0), (C.GL_BIAS_ACT, 1, 1, 0)]
+    assert build(col=True) == [(C.GL_BIAS_ACT, 0, 1, 0), (C.GL_BIAS_ACT, 1, 1, 0)]
+    assert build(act=True) == [(C.GL_BIAS_ACT, 0, 1, 0), (C.GL_BIAS_ACT, 1, 2, 0)]
+
+
 def test_query_bias_and_pos_bias_pair():
     """flow_encoder.cpp:320, 341-345: add(q_mm, q_b) -> reshape to (64, 8, T)
     heads -> add(., pos_bias_u), add(., pos_bias_v) is one launch; the sum
@@ -605,7 +632,7 @@ def test_random_lists_plan_into_an_exact_cover():
              C.GL_LAYER_NORM_MASK: {4, 7}, C.GL_BIAS_ACT: {1, 2, 4}, C.GL_CONV1D: set(range(9, 18)),
              C.GL_CONV_TRANSPOSE1D: set(range(7, 15)), C.GL_CAUSAL_CONV1D: set(range(12, 16)),
              C.GL_BINARY: {1}, C.GL_CONCAT: {1}, C.GL_BIAS_RESIDUAL: {2, 3}, C.GL_SCALE: {1},
-             C.GL_BIAS_ADD_PAIR: {4, 5, 6}}
+             C.GL_BIAS_ADD_PAIR: {4, 5, 6}, C.GL_BIAS_ADD_TWO: {2}}
     shapes = [(4, 8), (8,), (1, 8, 1, 1), (4, 8), (4, 1)]
     for trial in range(200):
         g = C.Graph()

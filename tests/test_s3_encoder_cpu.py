@@ -17,9 +17,10 @@ def test_plan_counts(T_mel, n_layer):
     got = collections.Counter(names[p[0]] for p in plan)
     L = n_layer
     assert dict(got) == {
-        # the two front convs' bias (as (1, C)) + gelu_erf; per layer the q and
-        # v bias adds and the fc bias + gelu_erf
-        "GL_BIAS_ACT": 2 + 3 * L,
+        # the two front convs' bias (as (1, C)) + gelu_erf; per layer the fc
+        # bias + gelu_erf
+        "GL_BIAS_ACT": 2 + L,
+        "GL_BIAS_ADD_TWO": L,                 # the q and v bias adds side by side
         "GL_VIEW": 2 + 2 * L,                 # the front biases as (1, C); q and k as heads
         "GL_ROPE": 2 * L,                     # q and k
         "GL_BINARY": L,                       # add(fsmn, v)
