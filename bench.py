@@ -822,8 +822,8 @@ def estimator_bytes(C, e, plan):
         total += y.numel() * y.element_size()
         if kind == C.GL_ADD_LAYER_NORM and not flags & 1:
             total += y.numel() * y.element_size()   # the residual sum, stored too
-        if kind in (C.GL_BIAS_ADD_TWO, C.GL_BIAS_ADD_PAIR):   # two outputs: the other one
-            k = f if kind == C.GL_BIAS_ADD_TWO else next(j for j in range(f + 2, f + n) if nd[j].op == C.GOP_ADD)
+        if kind in (C.GL_BIAS_ADD_TWO, C.GL_ROPE_TWO, C.GL_BIAS_ADD_PAIR):   # two outputs: the other one
+            k = f if kind != C.GL_BIAS_ADD_PAIR else next(j for j in range(f + 2, f + n) if nd[j].op == C.GOP_ADD)
             total += at(nd[k].dst).numel() * at(nd[k].dst).element_size()
     return total
 

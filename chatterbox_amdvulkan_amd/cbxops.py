@@ -116,7 +116,7 @@ GL_UNSUPPORTED, GL_VIEW, GL_GET_ROWS, GL_GET_ROWS_ADD, GL_GET_ROWS_ADD_LAYER_NOR
     GL_LAYER_NORM_ROPE, GL_RMS_NORM, GL_GROUP_NORM, GL_SOFT_MAX, GL_SNAKE, GL_UNARY, GL_SWIGLU, GL_LEAKY_RELU, \
     GL_ROPE, GL_CPY, GL_ADD_LAYER_NORM, GL_LAYER_NORM_MASK, GL_BIAS_ACT, GL_CONV1D, GL_CONV_TRANSPOSE1D, \
     GL_CAUSAL_CONV1D, GL_GET_ROWS_CONCAT_ADD_LAYER_NORM, GL_BINARY, GL_CONCAT, \
-    GL_BIAS_RESIDUAL, GL_SCALE, GL_BIAS_ADD_PAIR, GL_BIAS_ADD_TWO = range(30)
+    GL_BIAS_RESIDUAL, GL_SCALE, GL_BIAS_ADD_PAIR, GL_BIAS_ADD_TWO, GL_ROPE_TWO = range(31)
 # conv launch flags: the prologue (bits 0-1), a bias add, the residual add
 GLF_SNAKE, GLF_LEAKY, GLF_MASK, GLF_BIAS, GLF_RESIDUAL, GLF_SUM, GLF_SCALE = 1, 2, 3, 4, 8, 16, 32
 

@@ -761,6 +761,21 @@ bool independent_adds(const cbx_tensor* t, const cbx_gnode* nd, int32_t i) {
            !bytes_overlap(yb, &t[a.src[0]]) && !bytes_overlap(yb, &t[a.src[1]]);
 }
 
+// Nodes i and i + 1 neither read nor write what the other writes, by
+// tensor bytes: they may run side by side in one launch.
+bool independent_nodes(const cbx_tensor* t, const cbx_gnode* nd, int32_t i) {
+    const cbx_gnode &a = nd[i], &b = nd[i + 1];
+    const cbx_tensor *ya = &t[a.dst], *yb = &t[b.dst];
+    if (bytes_overlap(ya, yb)) return false;
+    for (int32_t s : b.src) {
+        if (s >= 0 && bytes_overlap(ya, &t[s])) return false;
+    }
+    for (int32_t s : a.src) {
+        if (s >= 0 && bytes_overlap(yb, &t[s])) return false;
+    }
+    return true;
+}
+
 int check_lists(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, int32_t n_nodes,
                 const char* what) {
     if ((!tensors && n_tensors) || n_tensors < 0 || (!nodes && n_nodes) || n_nodes < 0) {
@@ -804,6 +819,13 @@ int plan(const cbx_tensor* tensors, int32_t n_tensors, const cbx_gnode* nodes, i
             i += 1;
             continue;
         }
+        // two RoPEs in a row on separate tensors (q and k, s3enc.cpp:215-229)
+        if (kind == CBX_GL_ROPE && !out->empty() && out->back().kind == CBX_GL_ROPE &&
+            out->back().first_node == i - 1 && independent_nodes(tensors, nodes, i - 1)) {
+            out->back() = cbx_glaunch{CBX_GL_ROPE_TWO, i - 1, 2, 0};
+            i += 1;
+            continue;
+        }
         out->push_back(cbx_glaunch{kind, i, kind == CBX_GL_UNSUPPORTED ? 1 : len, flags});
         i += out->back().n_nodes;
     }
@@ -844,8 +866,9 @@ constexpr int32_t kSpan[][2] = {
     {1, 1},  // SCALE
     {4, 6},  // BIAS_ADD_PAIR [views of u, v]
     {2, 2},  // BIAS_ADD_TWO
+    {2, 2},  // ROPE_TWO
 };
-constexpr int32_t kLastKind = CBX_GL_BIAS_ADD_TWO;
+constexpr int32_t kLastKind = CBX_GL_ROPE_TWO;
 static_assert(sizeof(kSpan) / sizeof(kSpan[0]) == kLastKind + 1, "one span per launch kind");
 
 // Issues the entry point a launch maps to.  A launch is only read within
@@ -956,6 +979,25 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
             return cbx_leaky_relu(T(t, a.src[0]), a.fparam, y, s);
         case CBX_GL_ROPE:
             return cbx_rope_ext(T(t, a.src[0]), T(t, a.src[1]), a.rope, y, s);
+        case CBX_GL_ROPE_TWO: {
+            const cbx_gnode& b = nd[f + 1];
+            if (a.op != CBX_GOP_ROPE || b.op != CBX_GOP_ROPE) break;
+            cbx_op ops[2] = {};
+            for (int k = 0; k < 2; k++) {
+                const cbx_gnode& g = nd[f + k];
+                ops[k].kind = CBX_OP_ROPE;
+                ops[k].src[0] = T(t, g.src[0]);
+                ops[k].src[1] = T(t, g.src[1]);
+                ops[k].dst[0] = const_cast<cbx_tensor*>(&t[g.dst]);
+                ops[k].rope = g.rope;
+            }
+            const int rc = cbx_run_ops(ops, 2, s);
+            if (rc != CBX_ERR_UNSUPPORTED) return rc;
+            // a layout the one-launch kernel does not take (nothing was
+            // launched): the two RoPEs one after the other
+            const int r0 = cbx_rope_ext(T(t, a.src[0]), T(t, a.src[1]), a.rope, const_cast<cbx_tensor*>(&t[a.dst]), s);
+            return r0 ? r0 : cbx_rope_ext(T(t, b.src[0]), T(t, b.src[1]), b.rope, y, s);
+        }
         case CBX_GL_CPY:
             return cbx_cpy(T(t, a.src[0]), y, s);
         case CBX_GL_BINARY:

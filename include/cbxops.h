@@ -740,6 +740,9 @@ typedef enum cbx_glaunch_kind {
                                  (cbx_bias_add_pair)                            */
     CBX_GL_BIAS_ADD_TWO,      /* two lone bias adds in a row, independent of
                                  each other (cbx_bias_add_two)                  */
+    CBX_GL_ROPE_TWO,          /* two rope nodes in a row on separate tensors
+                                 (cbx_run_ops; the two cbx_rope_ext calls for
+                                 layouts it does not take)                      */
 } cbx_glaunch_kind;
 
 typedef struct cbx_glaunch {

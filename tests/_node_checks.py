@@ -59,10 +59,11 @@ def run_and_check(graph, at, keep, oracle, launch, k, rope=None):
         assert_bitexact(got, H(nd[f].src[0]) * np.float32(nd[f].fparam), what)
     elif kind == C.GL_LEAKY_RELU:
         assert_bitexact(got, oracle.leaky_relu(H(nd[f].src[0]), nd[f].fparam), what)
-    elif kind == C.GL_ROPE:
+    elif kind in (C.GL_ROPE, C.GL_ROPE_TWO):
         assert rope is not None, what
-        exp = oracle.rope_ext(H(nd[f].src[0]), H(nd[f].src[1]), **rope)
-        assert_bitexact(got, exp, what)
+        for k in range(f, f + n):
+            exp = oracle.rope_ext(H(nd[k].src[0]), H(nd[k].src[1]), **rope)
+            assert_bitexact(H(nd[k].dst), exp, f"{what} (node {k})")
     elif kind == C.GL_BINARY:
         a, b = H(nd[f].src[0]), H(nd[f].src[1])
         assert_bitexact(got, oracle.mul(a, b) if flags == C.BINARY_MUL else oracle.add(a, b), what)

@@ -364,6 +364,26 @@ def test_two_lone_bias_adds_share_a_launch():
     assert build(act=True) == [(C.GL_BIAS_ACT, 0, 1, 0), (C.GL_BIAS_ACT, 1, 2, 0)]
 
 
+def test_two_ropes_share_a_launch():
+    """q's and k's RoPE in a row (s3enc.cpp:215-229) are one launch; a RoPE
+    of the first's output, or one writing over the other's input, is not."""
+    def build(chain=False, clobber=False, in_place=False):
+        g = C.Graph()
+        pos = g.tensor(torch.zeros(6, dtype=torch.int32))
+        q, k = g.tensor(f32(6, 4, 64)), g.tensor(f32(6, 4, 64))
+        qr_t = f32(6, 4, 64)
+        qr = g.tensor(qr_t)
+        g.node(C.GOP_ROPE, qr, (q, pos))
+        kr = g.tensor(g._torch[q] if clobber else g._torch[k] if in_place else f32(6, 4, 64))
+        g.node(C.GOP_ROPE, kr, (qr if chain else k, pos))
+        return g.plan(keep=[qr, kr])
+
+    assert build() == [(C.GL_ROPE_TWO, 0, 2, 0)]
+    assert build(in_place=True) == [(C.GL_ROPE_TWO, 0, 2, 0)]     # k's RoPE over k itself
+    assert build(chain=True) == [(C.GL_ROPE, 0, 1, 0), (C.GL_ROPE, 1, 1, 0)]
+    assert build(clobber=True) == [(C.GL_ROPE, 0, 1, 0), (C.GL_ROPE, 1, 1, 0)]   # k's output over q
+
+
 def test_query_bias_and_pos_bias_pair():
     """flow_encoder.cpp:320, 341-345: add(q_mm, q_b) -> reshape to (64, 8, T)
     heads -> add(., pos_bias_u), add(., pos_bias_v) is one launch; the sum
@@ -632,7 +652,8 @@ def test_random_lists_plan_into_an_exact_cover():
              C.GL_LAYER_NORM_MASK: {4, 7}, C.GL_BIAS_ACT: {1, 2, 4}, C.GL_CONV1D: set(range(9, 18)),
              C.GL_CONV_TRANSPOSE1D: set(range(7, 15)), C.GL_CAUSAL_CONV1D: set(range(12, 16)),
              C.GL_BINARY: {1}, C.GL_CONCAT: {1}, C.GL_BIAS_RESIDUAL: {2, 3}, C.GL_SCALE: {1},
-             C.GL_BIAS_ADD_PAIR: {4, 5, 6}, C.GL_BIAS_ADD_TWO: {2}}
+             C.GL_BIAS_ADD_PAIR: {4, 5, 6}, C.GL_BIAS_ADD_TWO: {2},
+             C.GL_ROPE_TWO: {2}}
     shapes = [(4, 8), (8,), (1, 8, 1, 1), (4, 8), (4, 1)]
     for trial in range(200):
         g = C.Graph()

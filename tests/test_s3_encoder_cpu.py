@@ -22,7 +22,7 @@ def test_plan_counts(T_mel, n_layer):
         "GL_BIAS_ACT": 2 + L,
         "GL_BIAS_ADD_TWO": L,                 # the q and v bias adds side by side
         "GL_VIEW": 2 + 2 * L,                 # the front biases as (1, C); q and k as heads
-        "GL_ROPE": 2 * L,                     # q and k
+        "GL_ROPE_TWO": L,                     # q and k side by side
         "GL_BINARY": L,                       # add(fsmn, v)
         "GL_SOFT_MAX": L,                     # scale -> soft_max
         # out bias + the FSMN join; the last layer's proj bias + residual
