@@ -955,6 +955,11 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
             const bool add = a.op == CBX_GOP_ADD;
             float scale = 1.0f;
             int32_t n_past = -1;
+            bool chain = nd[f + l.n_nodes - 1].op == CBX_GOP_SOFT_MAX;
+            for (int32_t k = add ? f + 1 : f; k < f + l.n_nodes - 1; k++) {
+                chain = chain && (nd[k].op == CBX_GOP_SCALE || nd[k].op == CBX_GOP_DIAG_MASK_INF);
+            }
+            if (!chain) break;
             for (int32_t k = add ? f + 1 : f; k < f + l.n_nodes - 1; k++) {
                 if (nd[k].op == CBX_GOP_SCALE) scale = nd[k].fparam;
                 if (nd[k].op == CBX_GOP_DIAG_MASK_INF) {

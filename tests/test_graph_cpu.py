@@ -600,6 +600,26 @@ def test_hand_made_launches_stay_inside_the_list():
     assert L.cbx_graph_launch(T, 2, N, 2, ctypes.byref(C.GLaunch(C.GL_VIEW, 1, 1, 0)), None) == C.OK
 
 
+def test_hand_made_launches_of_the_paired_kinds_are_refused():
+    """The two-output and paired launch kinds, and the softmax chain, on
+    nodes that are not their chains: refused before any entry point runs."""
+    L = C.load()
+    g = C.Graph()
+    ts = [g.tensor(f32(2, 8)) for _ in range(7)]
+    for k in range(6):
+        if k % 2:
+            g.node(C.GOP_VIEW, ts[k + 1], (ts[k],))
+        else:
+            g.node(C.GOP_NORM, ts[k + 1], (ts[k],), fparam=1e-5)
+    T, N, _ = _raw(g)
+    for l in [C.GLaunch(C.GL_BIAS_ADD_PAIR, 0, 4, 0), C.GLaunch(C.GL_BIAS_ADD_PAIR, 0, 6, 0),
+              C.GLaunch(C.GL_BIAS_ADD_TWO, 0, 2, 0), C.GLaunch(C.GL_ROPE_TWO, 0, 2, 0),
+              C.GLaunch(C.GL_SOFT_MAX, 0, 1, 0), C.GLaunch(C.GL_SOFT_MAX, 0, 3, 0),
+              C.GLaunch(C.GL_SOFT_MAX, 0, 4, 0), C.GLaunch(C.GL_BIAS_ADD_TWO, 0, 3, 0)]:
+        assert L.cbx_graph_launch(T, 7, N, 6, ctypes.byref(l), None) == C.ERR_INVALID_ARG, (l.kind, l.n_nodes)
+        assert "does not fit" in C.last_error()
+
+
 def test_bias_residual_chains():
     """add(x, bias) [-> view] -> add(r, .) with no norm after it: one
     launch (cfm_decoder.cpp:162-165 the time MLP over the frames, :242-244 a
