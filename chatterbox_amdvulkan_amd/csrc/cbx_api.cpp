@@ -986,9 +986,12 @@ int cbx_bias_add_two(const cbx_tensor* x0, const cbx_tensor* b0, cbx_tensor* y0,
         }
     }
     // the two adds run side by side: neither output may meet the other
-    // add's operands or output
+    // add's operands or output, nor its own bias (read by every row)
     if (overlaps(y0, x1) || overlaps(y0, b1) || overlaps(y0, y1) || overlaps(y1, x0) || overlaps(y1, b0)) {
         return set_error(CBX_ERR_INVALID_ARG, "cbx_bias_add_two: an output overlaps the other add's tensors");
+    }
+    if (overlaps(y0, b0) || overlaps(y1, b1)) {
+        return set_error(CBX_ERR_INVALID_ARG, "cbx_bias_add_two: an output overlaps its bias");
     }
     return launch_bias_add_two(x0, b0, y0, x1, b1, y1, st, reinterpret_cast<hipStream_t>(stream));
 }

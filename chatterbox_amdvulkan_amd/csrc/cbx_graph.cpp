@@ -743,8 +743,8 @@ const char* op_name(int op) {
 }
 
 // The bias adds at nodes i and i + 1 neither read nor write what the other
-// writes (by tensor and by bytes), and each bias is a row of its x: the two
-// may run side by side in one launch.
+// writes (by bytes), neither output meets its own bias, and each bias is a
+// row of its x: the two may run side by side in one launch.
 bool independent_adds(const cbx_tensor* t, const cbx_gnode* nd, int32_t i) {
     const cbx_gnode &a = nd[i], &b = nd[i + 1];
     if (a.op != CBX_GOP_ADD || b.op != CBX_GOP_ADD) return false;
@@ -758,7 +758,8 @@ bool independent_adds(const cbx_tensor* t, const cbx_gnode* nd, int32_t i) {
     }
     const cbx_tensor *ya = &t[a.dst], *yb = &t[b.dst];
     return !bytes_overlap(ya, &t[b.src[0]]) && !bytes_overlap(ya, &t[b.src[1]]) && !bytes_overlap(ya, yb) &&
-           !bytes_overlap(yb, &t[a.src[0]]) && !bytes_overlap(yb, &t[a.src[1]]);
+           !bytes_overlap(yb, &t[a.src[0]]) && !bytes_overlap(yb, &t[a.src[1]]) && !bytes_overlap(ya, &t[a.src[1]]) &&
+           !bytes_overlap(yb, &t[b.src[1]]);
 }
 
 // Nodes i and i + 1 neither read nor write what the other writes, by

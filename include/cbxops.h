@@ -383,8 +383,8 @@ int cbx_bias_add_pair(const cbx_tensor* x, const cbx_tensor* bias, const cbx_ten
  * Two adjacent bias adds that do not read each other: the projections of v
  * and k (flow_encoder.cpp:320-322), of q and v (s3enc.cpp:205-207).  Each
  * bias contiguous with ne = (x.ne0,1,1,1) or (1,x.ne1,1,1); each y has its
- * x's shape and may be that x itself; neither y may overlap the other
- * add's tensors.                                                            */
+ * x's shape and may be that x itself; neither y may overlap its bias or
+ * the other add's tensors.                                                  */
 int cbx_bias_add_two(const cbx_tensor* x0, const cbx_tensor* b0, cbx_tensor* y0,
                      const cbx_tensor* x1, const cbx_tensor* b1, cbx_tensor* y1,
                      cbx_stream stream);
