@@ -275,4 +275,4 @@ def test_bias_add_two_in_place_and_refusals(cbx, oracle):
         cbx.bias_add_two(t0, dev(np.zeros(64, np.float32)), t1, tb)
     wide = torch.zeros(65, 128, device="cuda")
     with pytest.raises(cbx.CbxError, match="its bias"):
-        cbx.bias_add_two(t0, wide[64], t1, tb, out0=wide[:64])
+        cbx.bias_add_two(t0, wide[63], t1, tb, out0=wide[:64])
