@@ -1588,6 +1588,31 @@ def cpu_baseline(W, seconds):
             "nproc": os.cpu_count(), "cpu_model": model, "details": details}
 
 
+def cpu_node_list(C, e):
+    """A node-list builder's nodes as oracle.run_node_list takes them, the
+    tensors' shapes, and seeded leaf values (normal f32; int32 leaves, the
+    token ids and positions, 0, 1, 2, ...)."""
+    import torch
+
+    names = {C.GOP_VIEW: "view", C.GOP_GET_ROWS: "get_rows", C.GOP_ADD: "add", C.GOP_MUL: "mul",
+             C.GOP_SCALE: "scale", C.GOP_NORM: "norm", C.GOP_SOFT_MAX: "soft_max", C.GOP_UNARY: "unary",
+             C.GOP_LEAKY_RELU: "leaky_relu", C.GOP_ROPE: "rope"}
+    nodes = [(names[n.op], n.dst, n.src[0], n.src[1], n.iparam, n.fparam) for n in e.graph.nodes]
+    made = {n.dst for n in e.graph.nodes}
+    n_t = len(e.graph._descs)
+    shapes = {i: tuple(e.b.at(i).shape) for i in range(n_t)}
+    rng = np.random.default_rng(7)
+    leaves = {}
+    for i in range(n_t):
+        if i in made:
+            continue
+        if e.b.at(i).dtype == torch.int32:
+            leaves[i] = (np.arange(int(np.prod(shapes[i]))) % 1000).astype(np.int32).reshape(shapes[i])
+        else:
+            leaves[i] = rng.standard_normal(shapes[i]).astype(np.float32)
+    return nodes, shapes, leaves
+
+
 def _timed(fn, seconds):
     reps, t0 = 0, time.perf_counter()
     while True:
@@ -1653,6 +1678,18 @@ def cpu_other_workloads(W, O, nth, seconds):
     tok = O.T3TokenStep(W.t3_token_inputs(), 255)
     reps, el = _timed(lambda: tok.run(17, 255), seconds)
     out["t3_token_elementwise_us_per_token_1thread"] = el / reps * 1e6
+
+    # the encoder calls' node lists run node by node on the oracle, as
+    # ggml-cpu runs a graph (same lists and sizes as the GPU legs)
+    from chatterbox_amdvulkan_amd import cbxops as C
+    from chatterbox_amdvulkan_amd.flow_encoder import FlowEncoderCall
+    from chatterbox_amdvulkan_amd.s3_encoder import HEAD_DIM, ROPE_BASE, ROPE_MAX, S3EncoderCall
+
+    rope = dict(n_dims=HEAD_DIM, mode=2, n_ctx_orig=ROPE_MAX, freq_base=ROPE_BASE)
+    for name, e in (("flow_encoder", FlowEncoderCall(250, device=False)), ("s3_encoder", S3EncoderCall(1000, device=False))):
+        nodes, shapes, leaves = cpu_node_list(C, e)
+        reps, el = _timed(lambda: O.run_node_list(nodes, shapes, dict(leaves), rope=rope, nth=nth), seconds)
+        out[f"{name}_call_us"] = el / reps * 1e6
 
     for (B, Ch, T) in W.HIFT_SHAPES[:3:2]:
         x = W.normal(W.seed_of(4, 2), (B, T, Ch))

@@ -435,3 +435,42 @@ class T3TokenStep:
                                          self.inp["out_w"].ctypes.data, self.inp["out_b_final"].ctypes.data,
                                          self.out["h0"].ctypes.data, self.out["y"].ctypes.data), "t3_token_step")
         return self.out
+
+
+def run_node_list(nodes, shapes, values, rope=None, nth=1):
+    """Runs a ggml-style node list node by node, as ggml-cpu's graph compute
+    does (chatterbox-cpp/src/backend.cpp:108-122 on the CPU backend).
+
+    nodes: (op, dst, src0, src1, iparam, fparam) tuples, op one of "view",
+    "get_rows", "add", "mul", "scale", "norm", "soft_max", "unary",
+    "leaky_relu", "rope"; shapes[i]: the numpy shape of tensor i; values: a
+    dict holding the leaf arrays by index, filled with every node's output.
+    A view is a reshape of its contiguous source.  rope: rope_ext's keyword
+    arguments (n_dims first) for the rope nodes.  Returns values."""
+    for op, d, s0, s1, ip, fp in nodes:
+        a = values[s0] if s0 >= 0 else None
+        b = values[s1] if s1 >= 0 else None
+        if op == "view":
+            out = a.reshape(shapes[d])
+        elif op == "get_rows":
+            out = get_rows(a, b, nth=nth)
+        elif op == "add":
+            out = add(a, b, nth=nth)
+        elif op == "mul":
+            out = mul(a, b, nth=nth)
+        elif op == "scale":
+            out = scale(a, fp, nth=nth)
+        elif op == "norm":
+            out = norm(a, fp, nth=nth)
+        elif op == "soft_max":
+            out = scale_diag_mask_soft_max(a, fp, -1, nth=nth)
+        elif op == "unary":
+            out = unary(ip, a, nth=nth)
+        elif op == "leaky_relu":
+            out = leaky_relu(a, fp, nth=nth)
+        elif op == "rope":
+            out = rope_ext(a, b, **rope, nth=nth)
+        else:
+            raise ValueError(f"run_node_list: no oracle op for {op!r}")
+        values[d] = out
+    return values
