@@ -625,7 +625,8 @@ def swiglu(g, u, out=None):
 
 
 def add_layer_norm(a, r, w, b, eps, a_bias=None, act=UNARY_NONE, s=None, out=None, store_sum=True):
-    """Residual join + LayerNorm: s = (a [+ a_bias]) + r, y = act(LN(s)*w + b).
+    """Residual join + LayerNorm: s = (a [+ a_bias]) [+ r], y = act(LN(s)*w + b)
+    (r None: a linear's bias, then its LayerNorm; a_bias required).
     Returns (s, y); s is None when store_sum is False."""
     _ready(a)
     out = _out_like(a, out)
@@ -634,7 +635,7 @@ def add_layer_norm(a, r, w, b, eps, a_bias=None, act=UNARY_NONE, s=None, out=Non
     if not store_sum:
         s = None
     _check(load().cbx_add_layer_norm(_ref(desc(a)), _ref(desc(a_bias) if a_bias is not None else None),
-                                     _ref(desc(r)), _ref(desc(w) if w is not None else None),
+                                     _ref(desc(r) if r is not None else None), _ref(desc(w) if w is not None else None),
                                      _ref(desc(b) if b is not None else None), eps, act,
                                      _ref(desc(s) if s is not None else None), _ref(desc(out)), _stream()))
     return s, out

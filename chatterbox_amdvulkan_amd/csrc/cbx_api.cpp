@@ -518,7 +518,8 @@ int cbx_add_layer_norm(const cbx_tensor* a, const cbx_tensor* a_bias, const cbx_
     if (!st) return rc;
     if ((rc = validate(a, what, "a"))) return rc;
     if (a->type != CBX_TYPE_F32) return set_error(CBX_ERR_UNSUPPORTED, "cbx_add_layer_norm: a must be F32");
-    if ((rc = check_f32_like(r, a, what, "r")) || (rc = check_f32_like(y, a, what, "y")) ||
+    if (!r && !a_bias) return set_error(CBX_ERR_INVALID_ARG, "cbx_add_layer_norm: r may be NULL only with a_bias");
+    if ((r && (rc = check_f32_like(r, a, what, "r"))) || (rc = check_f32_like(y, a, what, "y")) ||
         (s && (rc = check_f32_like(s, a, what, "s")))) return rc;
     if ((rc = check_row_param(a_bias, a, what, "a_bias")) || (rc = check_row_param(w, a, what, "w")) ||
         (rc = check_row_param(b, a, what, "b")) || (rc = check_act(act, what))) return rc;

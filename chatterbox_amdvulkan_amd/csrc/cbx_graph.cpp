@@ -269,6 +269,18 @@ struct Planner {
 
     // layer_norm at node i reading `in`, optionally followed by a mish
     // chain: the node count (3 or 6), or 0
+    // a tensor in a layout the fused LayerNorm kernel takes: ne0 % 4 == 0,
+    // ne0 <= 4096, 16-byte aligned data and row steps
+    bool ln_ext_fits(int32_t p) const {
+        if (!valid_t(p) || t[p].ne[0] % 4 != 0 || t[p].ne[0] > 4096 || reinterpret_cast<uintptr_t>(t[p].data) % 16) {
+            return false;
+        }
+        for (int k = 1; k < 4; k++) {
+            if (t[p].nb[k] % 16) return false;
+        }
+        return true;
+    }
+
     int32_t layer_norm_mish_at(int32_t i, int32_t in) const {
         if (!layer_norm_at(i) || nd[i].src[0] != in) return 0;
         const int32_t y = nd[i + 2].dst;
@@ -598,6 +610,19 @@ struct Planner {
                 if (!bias && !col_vec(a.src[1], x)) {
                     *flags = CBX_BINARY_ADD;
                     return repeats(a.src[1], x) ? CBX_GL_BINARY : CBX_GL_UNSUPPORTED;
+                }
+                // bias add -> layer_norm [-> mish] (a linear's bias, then its
+                // LayerNorm: flow_encoder.cpp:414-415), in the layouts the
+                // fused kernel takes (else the two launches as before)
+                if (const int32_t l = bias ? layer_norm_mish_at(i + 1, t1) : 0) {
+                    const bool fits = ln_ext_fits(x) && ln_ext_fits(a.src[1]) && ln_ext_fits(nd[i + 2].src[1]) &&
+                                      ln_ext_fits(nd[i + 3].src[1]) && ln_ext_fits(nd[i + l].dst) &&
+                                      (internal(t1, 1) || ln_ext_fits(t1));
+                    if (fits) {
+                        if (internal(t1, 1)) *flags = 1;
+                        *len = 1 + l;
+                        return CBX_GL_ADD_LAYER_NORM;
+                    }
                 }
                 if (is_unary(i + 1, CBX_UNARY_SOFTPLUS) && mish_at(i + 1, t1) && internal(t1, 2)) {
                     *len = 4;
@@ -1069,6 +1094,15 @@ int run(const cbx_tensor* t, const cbx_gnode* nd, int32_t n_nodes, const cbx_gla
         case CBX_GL_ADD_LAYER_NORM: {
             if (l.n_nodes == 6) break;
             const bool bias = l.n_nodes == 5 || l.n_nodes == 8;
+            // 4 or 7 nodes: add(a, r) of one shape, or add(a, bias) with no
+            // residual (bias a row of a)
+            const cbx_tensor *a0 = T(t, a.src[0]), *a1 = T(t, a.src[1]);
+            if (!bias && a0 && a1 && !same_shape(a0, a1) && a1->ne[0] == a0->ne[0] && nelements(a1) == a1->ne[0]) {
+                const int32_t ln = f + 1;
+                cbx_tensor* sum = (l.flags & 1) ? nullptr : const_cast<cbx_tensor*>(&t[a.dst]);
+                return cbx_add_layer_norm(a0, a1, nullptr, T(t, nd[ln + 1].src[1]), T(t, nd[ln + 2].src[1]),
+                                          nd[ln].fparam, l.n_nodes == 7 ? CBX_UNARY_MISH : CBX_UNARY_NONE, sum, y, s);
+            }
             const int32_t k = bias ? f + 1 : f;        // the residual add
             const int32_t ln = k + 1;                  // the norm
             const cbx_gnode& r = nd[k];

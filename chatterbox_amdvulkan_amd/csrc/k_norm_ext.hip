@@ -19,7 +19,8 @@
 namespace cbx {
 namespace {
 
-enum { PRO_NONE = 0, PRO_RESID = 1, PRO_BIAS_RESID = 2 };
+// the prologue: none, s = a + r, s = (a + bias) + r, s = a + bias
+enum { PRO_NONE = 0, PRO_RESID = 1, PRO_BIAS_RESID = 2, PRO_BIAS = 3 };
 
 struct LnExtArgs {
     const char* a;
@@ -94,9 +95,9 @@ __global__ __launch_bounds__(64 * WPB * WPR) void k_ln_ext(LnExtArgs p) {
         const int64_t j = (lane + 64 * k) * 4;
         const int64_t jc = j < ne0 ? j : 0;
         v[k] = *reinterpret_cast<const float4*>(ar + jc * 4);
-        if constexpr (PRO == PRO_BIAS_RESID) c[k] = *reinterpret_cast<const float4*>(p.ab + jc);
+        if constexpr (PRO == PRO_BIAS_RESID || PRO == PRO_BIAS) c[k] = *reinterpret_cast<const float4*>(p.ab + jc);
     }
-    if constexpr (PRO != PRO_NONE) {
+    if constexpr (PRO == PRO_RESID || PRO == PRO_BIAS_RESID) {
         const char* rr = p.r + row_off<FLAT>(p.mr, row);
 #pragma unroll
         for (int k = 0; k < NV; k++) {
@@ -110,8 +111,12 @@ __global__ __launch_bounds__(64 * WPB * WPR) void k_ln_ext(LnExtArgs p) {
     for (int k = 0; k < NV; k++) {
         const bool in = (lane + 64 * k) * 4 < ne0;
         float4 t = v[k];
-        if constexpr (PRO == PRO_BIAS_RESID) t = make_float4(t.x + c[k].x, t.y + c[k].y, t.z + c[k].z, t.w + c[k].w);
-        if constexpr (PRO != PRO_NONE) t = make_float4(t.x + q[k].x, t.y + q[k].y, t.z + q[k].z, t.w + q[k].w);
+        if constexpr (PRO == PRO_BIAS_RESID || PRO == PRO_BIAS) {
+            t = make_float4(t.x + c[k].x, t.y + c[k].y, t.z + c[k].z, t.w + c[k].w);
+        }
+        if constexpr (PRO == PRO_RESID || PRO == PRO_BIAS_RESID) {
+            t = make_float4(t.x + q[k].x, t.y + q[k].y, t.z + q[k].z, t.w + q[k].w);
+        }
         v[k] = make_float4(in ? t.x : 0.f, in ? t.y : 0.f, in ? t.z : 0.f, in ? t.w : 0.f);
     }
     if constexpr (PRO != PRO_NONE) {
@@ -253,6 +258,7 @@ int launch_layer_norm_ext(const cbx_tensor* a, const cbx_tensor* a_bias, const c
     const bool has_act = act != CBX_UNARY_NONE;
     const bool flat = p.ma.flat && p.my.flat && (!r || p.mr.flat) && (!s || p.ms.flat);
     if (mask) go_pro<PRO_NONE, true>(p, has_act, nv, wpb, wpr, flat, nr, strm);
+    else if (a_bias && !r) go_pro<PRO_BIAS, false>(p, has_act, nv, wpb, wpr, flat, nr, strm);
     else if (a_bias) go_pro<PRO_BIAS_RESID, false>(p, has_act, nv, wpb, wpr, flat, nr, strm);
     else go_pro<PRO_RESID, false>(p, has_act, nv, wpb, wpr, flat, nr, strm);
     return check_launch(what);

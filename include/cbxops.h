@@ -233,11 +233,14 @@ int  cbx_group_norm_noalloc(const cbx_tensor* x, int n_groups, float eps,
                             cbx_tensor* y, cbx_stream stream);
 
 /* The residual join and the LayerNorm that reads it, in one pass:
- *   s = ggml_add(ggml_add(a, a_bias), r)     (a_bias NULL: ggml_add(a, r))
+ *   s = ggml_add(ggml_add(a, a_bias), r)     (a_bias NULL: ggml_add(a, r);
+ *                                             r NULL: ggml_add(a, a_bias))
  *   y = act(layer_norm(s, w, b, eps))
  * (t3.cpp:528-532: attn_residual = add(add(mul_mat, out_b), h), then the
  * pre-FFN LayerNorm; t3.cpp:539-541 with the next block's :465-466 or the
- * final LayerNorm :545-546; s3enc.cpp:273-276; flow_encoder.cpp:395-399).
+ * final LayerNorm :545-546; s3enc.cpp:273-276; flow_encoder.cpp:395-399;
+ * with no residual, a linear's bias and the LayerNorm after it,
+ * flow_encoder.cpp:414-415).  r may be NULL only when a_bias is not.
  * a, r, s, y: F32, one shape, ne0 % 4 == 0, ne0 <= 4096, 16-byte aligned
  * rows; a_bias, w, b: F32 (x.ne0,1,1,1), 16-byte aligned, or NULL.  s (the
  * residual stream) is stored when non-NULL; it may be a or r but must not

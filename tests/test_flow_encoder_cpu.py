@@ -19,10 +19,9 @@ def test_plan_counts(T, n_blocks, n_up):
     L = n_blocks + n_up
     assert dict(got) == {
         "GL_GET_ROWS": 1,                     # the speech-token embedding
-        # per block the w1 bias + silu; the two embed linears' bias, the two
-        # pre-lookahead convs' and the up conv's bias (as (1, C)), the
-        # encoder_proj bias
-        "GL_BIAS_ACT": L + 6,
+        # per block the w1 bias + silu; the two pre-lookahead convs' and the
+        # up conv's bias (as (1, C)), the encoder_proj bias
+        "GL_BIAS_ACT": L + 4,
         "GL_BIAS_ADD_TWO": L,                 # per block the v and k bias adds side by side
         # per block q's bias, then q + pos_bias_u and q + pos_bias_v (with
         # q's view as heads and pos_bias_u, pos_bias_v's as (64, 8, 1))
@@ -31,11 +30,10 @@ def test_plan_counts(T, n_blocks, n_up):
         "GL_SOFT_MAX": L,                     # AC + BD -> scale(1/8) -> soft_max
         # per block x + (out + b) -> LN; w2 bias + residual -> the next LN
         # (the up stack's last: after_norm); the pre-lookahead's residual ->
-        # the first block's LN
-        "GL_ADD_LAYER_NORM": 2 * L,
+        # the first block's LN; the two embed linears' bias -> their LN
+        "GL_ADD_LAYER_NORM": 2 * L + 2,
         "GL_BIAS_RESIDUAL": 1,                # the 25 Hz stack's last w2 bias + residual
-        # the two embed LNs; the 50 Hz stack's first LN (after the scale)
-        "GL_LAYER_NORM": 3,
+        "GL_LAYER_NORM": 1,                   # the 50 Hz stack's first LN (after the scale)
         "GL_SCALE": 2,                        # x sqrt(512) after each embed LN
         "GL_LEAKY_RELU": 1,                   # the pre-lookahead's conv1
     }

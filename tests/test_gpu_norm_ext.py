@@ -46,6 +46,26 @@ def test_add_layer_norm(cbx, oracle, rows, D, with_bias):
     assert_bitexact(host(y), ln_ref(oracle, s_ref, w, b, 1e-5), f"LN(sum) {rows}x{D}")
 
 
+@pytest.mark.parametrize("rows,D", [(250, 512), (500, 512), (7, 1024), (3000, 256)])
+@pytest.mark.parametrize("store_sum", [True, False])
+def test_bias_layer_norm(cbx, oracle, rows, D, store_sum):
+    """r NULL: s = a + bias, y = LN(s)*w + b (the flow encoder's embed
+    linears, flow_encoder.cpp:414-415), both bit-exact; r and a_bias both
+    NULL is refused."""
+    sd = W.seed_of(25, rows + D)
+    a = W.normal(sd, (rows, D), 0.0, 1.0)
+    ab = W.normal(sd + 1, (D,), 0.0, 0.1)
+    w = W.normal(sd + 2, (D,), 1.0, 0.05)
+    b = W.normal(sd + 3, (D,), 0.0, 0.05)
+    s, y = cbx.add_layer_norm(dev(a), None, dev(w), dev(b), 1e-5, a_bias=dev(ab), store_sum=store_sum)
+    s_ref = oracle.add(a, ab)
+    if store_sum:
+        assert_bitexact(host(s), s_ref, f"sum {rows}x{D}")
+    assert_bitexact(host(y), ln_ref(oracle, s_ref, w, b, 1e-5), f"LN(a + bias) {rows}x{D}")
+    with pytest.raises(cbx.CbxError, match="r may be NULL only"):
+        cbx.add_layer_norm(dev(a), None, dev(w), dev(b), 1e-5)
+
+
 @pytest.mark.parametrize("act", ["GELU", "MISH", "SILU"])
 def test_add_layer_norm_activation(cbx, oracle, act):
     a = W.normal(21, (64, 512))

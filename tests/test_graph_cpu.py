@@ -337,6 +337,35 @@ def test_score_terms_add_joins_the_soft_max(with_scale, with_mask):
     assert plan[0][0] != C.GL_SOFT_MAX and plan[-1] == (C.GL_SOFT_MAX, n - 1, 1, 0)
 
 
+def test_bias_add_then_layer_norm():
+    """flow_encoder.cpp:414-415: a linear's bias add, then its LayerNorm, is
+    one launch when the fused kernel takes the layout (rows of 512); rows
+    of 4100 floats or a kept sum that is not 16-byte stepped leave the two
+    launches."""
+    def build(D=512, keep_sum=False, mish=False):
+        g = C.Graph()
+        x, bias = g.tensor(f32(10, D)), g.tensor(f32(D))
+        w, b = g.tensor(f32(D)), g.tensor(f32(D))
+        s = g.tensor(f32(10, D))
+        g.node(C.GOP_ADD, s, (x, bias))
+        n, m, y = g.tensor(f32(10, D)), g.tensor(f32(10, D)), g.tensor(f32(10, D))
+        g.node(C.GOP_NORM, n, (s,), fparam=1e-5)
+        g.node(C.GOP_MUL, m, (n, w))
+        g.node(C.GOP_ADD, y, (m, b))
+        if mish:
+            sp, th = g.tensor(f32(10, D)), g.tensor(f32(10, D))
+            g.node(C.GOP_UNARY, sp, (y,), iparam=C.SOFTPLUS)
+            g.node(C.GOP_UNARY, th, (sp,), iparam=C.TANH)
+            g.node(C.GOP_MUL, g.tensor(f32(10, D)), (y, th))
+        return g.plan(keep=[s] if keep_sum else [])
+
+    assert build() == [(C.GL_ADD_LAYER_NORM, 0, 4, 1)]
+    assert build(keep_sum=True) == [(C.GL_ADD_LAYER_NORM, 0, 4, 0)]
+    assert build(mish=True) == [(C.GL_ADD_LAYER_NORM, 0, 7, 1)]
+    assert build(D=4100) == [(C.GL_BIAS_ACT, 0, 1, 0), (C.GL_LAYER_NORM, 1, 3, 0)]
+    assert build(D=510) == [(C.GL_BIAS_ACT, 0, 1, 0), (C.GL_LAYER_NORM, 1, 3, 0)]
+
+
 def test_two_lone_bias_adds_share_a_launch():
     """Adjacent bias adds that neither read nor overlap each other's output
     (v's and k's projections) are one launch; an add reading the first's
